@@ -1,0 +1,191 @@
+"""Block-level pinning of the oracle: the composed Anima and MOSS blocks against float64 numpy restatements of the
+reference's own torch blocks (moss/moss_ref.py:56-67 `block`; the Anima block's site order from
+hexagon/mega/blk.c:149-176 and export_block.py's FullBlock call), and structural invariants (zero gates leave x
+unchanged, stop-after-stage semantics of meta[M_STOP], masked joint-attention keys have no influence)."""
+import numpy as np
+import pytest
+
+from oracle import hxo
+
+
+def f16(a):
+    return np.asarray(a).astype(np.float16)
+
+
+def _ln(x):
+    mu = x.mean(-1, keepdims=True)
+    return (x - mu) / np.sqrt((x * x).mean(-1, keepdims=True) - mu * mu + 1e-6)
+
+
+def _rms(x, w):
+    return x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6) * w
+
+
+def _rope(x, cos, sin):
+    # moss_ref.py:37-39 rotate: x*cos + cat(-b, a)*sin over halves of 128, cos/sin duplicated to 128
+    a, b = x[..., :64], x[..., 64:]
+    c, s = cos[:, None, :], sin[:, None, :]
+    return np.concatenate([a * c - b * s, b * c + a * s], -1)
+
+
+def _attn(q, k, v, nvalid=None):
+    T, D = q.shape
+    H = D // 128
+    nv = k.shape[0] if nvalid is None else nvalid
+    qh, kh, vh = q.reshape(T, H, 128), k[:nv].reshape(nv, H, 128), v[:nv].reshape(nv, H, 128)
+    S = np.einsum("thd,shd->hts", qh, kh)
+    P = np.exp(S - S.max(-1, keepdims=True))
+    P /= P.sum(-1, keepdims=True)
+    return np.einsum("hts,shd->thd", P, vh).reshape(T, D)
+
+
+def _gelu_tanh(x):
+    return 0.5 * x * (1 + np.tanh(np.sqrt(2 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
+def anima_block_f64(x, ctx, mod9, cos, sin, w, H):
+    """float64 restatement of the Anima block (no fp16 storage rounding)."""
+    d = lambda k: w[k].astype(np.float64)
+    g = w["gain"].astype(np.float64).reshape(4, 128)
+    T, D = x.shape
+    m = mod9.astype(np.float64).reshape(9, D)
+    x = x.astype(np.float64).copy()
+    ctxd = ctx.astype(np.float64)
+    # site 0
+    h = _ln(x) * (1 + m[1]) + m[0]
+    q = _rope(_rms((h @ d("wq").T).reshape(T, H, 128), g[0]), cos, sin).reshape(T, D)
+    k = _rope(_rms((h @ d("wk").T).reshape(T, H, 128), g[1]), cos, sin).reshape(T, D)
+    v = h @ d("wv").T
+    x = x + m[2] * (_attn(q, k, v) @ d("wo").T)
+    # site 1
+    h = _ln(x) * (1 + m[4]) + m[3]
+    q = _rms((h @ d("wcq").T).reshape(T, H, 128), g[2]).reshape(T, D)
+    ck = _rms((ctxd @ d("wck").T).reshape(len(ctxd), H, 128), g[3]).reshape(len(ctxd), D)
+    cv = ctxd @ d("wcv").T
+    x = x + m[5] * (_attn(q, ck, cv) @ d("wco").T)
+    # site 2
+    h = _ln(x) * (1 + m[7]) + m[6]
+    x = x + m[8] * (_gelu_tanh(h @ d("w1").T) @ d("w2").T)
+    return x
+
+
+def make_anima(T=128, D=256, H=2, C=64, DC=128, F=512, seed=0, gh=8):
+    rng = np.random.default_rng(seed)
+    w = {}
+    for k, (n, kk) in {"wq": (D, D), "wk": (D, D), "wv": (D, D), "wo": (D, D), "wcq": (D, D), "wck": (D, DC),
+                       "wcv": (D, DC), "wco": (D, D), "w1": (F, D), "w2": (D, F)}.items():
+        w[k] = f16(rng.standard_normal((n, kk)) * 0.02 * np.sqrt(2048 / kk))
+    w["gain"] = np.concatenate([rng.uniform(0.5, 1.5, 128) / np.sqrt(128), rng.uniform(0.5, 1.5, 128),
+                                rng.uniform(0.5, 1.5, 128) / np.sqrt(128), rng.uniform(0.5, 1.5, 128)]).astype(np.float32)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    ctx = f16(rng.standard_normal((C, DC)))
+    mod9 = (rng.standard_normal((9, D)) * 0.3).astype(np.float32)
+    cos, sin = hxo.rope_anima(gh, T // gh)
+    return x, ctx, mod9, cos, sin, w
+
+
+def test_anima_block_vs_float64_restatement():
+    x, ctx, mod9, cos, sin, w = make_anima()
+    ref = anima_block_f64(x, ctx, mod9, cos, sin, w, H=2)
+    for mode in (0, 1):
+        out, buf, n = hxo.anima_block(x, ctx, mod9, cos, sin, w, H=2, F=512, gelu=1, attn_mode=mode)
+        assert n == 13
+        dl = ref - x
+        rel = np.linalg.norm(out - ref) / np.linalg.norm(dl)
+        cos_d = np.dot((out - x).ravel(), dl.ravel()) / np.linalg.norm(out - x) / np.linalg.norm(dl)
+        assert rel < 5e-3, rel
+        assert cos_d > 0.99998, cos_d
+
+
+def test_anima_zero_gates_and_stop_semantics():
+    x, ctx, mod9, cos, sin, w = make_anima(seed=1)
+    m = mod9.copy()
+    m[[2, 5, 8]] = 0.0
+    out, _, n = hxo.anima_block(x, ctx, m, cos, sin, w, H=2, F=512)
+    assert n == 13 and np.array_equal(out, x)
+    # stop after stage 5 (site 0 finished) == a block whose sites 1, 2 have zero gates
+    out5, buf5, n5 = hxo.anima_block(x, ctx, mod9, cos, sin, w, H=2, F=512, stop=5)
+    m2 = mod9.copy()
+    m2[[5, 8]] = 0.0
+    full, buf, _ = hxo.anima_block(x, ctx, m2, cos, sin, w, H=2, F=512)
+    assert n5 == 5 and np.array_equal(out5, full)
+    # stop after stage 1: only h written, x untouched
+    out1, buf1, n1 = hxo.anima_block(x, ctx, mod9, cos, sin, w, H=2, F=512, stop=1)
+    assert n1 == 1 and np.array_equal(out1, x)
+    assert np.array_equal(buf1["h"], hxo.lnmod(x, mod9[0], mod9[1]))
+    assert not buf1["q"].any()
+    # stop after stage 2: q is the raw projection, stage 3 applies RMS + RoPE in place
+    _, b2, _ = hxo.anima_block(x, ctx, mod9, cos, sin, w, H=2, F=512, stop=2)
+    _, b3, _ = hxo.anima_block(x, ctx, mod9, cos, sin, w, H=2, F=512, stop=3)
+    assert np.array_equal(b3["q"], hxo.rmsrope(b2["q"], w["gain"][:128], cos, sin))
+
+
+def test_anima_gelu_modes_differ_only_in_mlp():
+    x, ctx, mod9, cos, sin, w = make_anima(seed=2)
+    a, ba, _ = hxo.anima_block(x, ctx, mod9, cos, sin, w, H=2, F=512, gelu=0)
+    b, bb, _ = hxo.anima_block(x, ctx, mod9, cos, sin, w, H=2, F=512, gelu=1)
+    assert np.array_equal(ba["o"], bb["o"])  # sites 0/1 identical
+    assert not np.array_equal(ba["mid"], bb["mid"])
+    assert np.linalg.norm(a - b) / np.linalg.norm(b - x) < 5e-2  # erf vs tanh GELU are close
+
+
+def moss_block_f64(x, mod6, cos, sin, w, nvalid):
+    """float64 restatement of moss_ref.py:56-67 block (no LoRA), attention over the valid tokens only."""
+    d = lambda k: w[k].astype(np.float64)
+    T, D = x.shape
+    H = D // 128
+    sa, ca, ga, sf, cf, gf = mod6.astype(np.float64).reshape(6, D)
+    x = x.astype(np.float64).copy()
+    y = _rms(x, w["n1"]) * (1 + ca) + sa
+    q = _rope(_rms((y @ d("wq").T).reshape(T, H, 128), w["gq"]), cos, sin).reshape(T, D)
+    k = _rope(_rms((y @ d("wk").T).reshape(T, H, 128), w["gk"]), cos, sin).reshape(T, D)
+    v = y @ d("wv").T
+    x = x + (_attn(q, k, v, nvalid) @ d("wo").T) * ga
+    y = _rms(x, w["n2"]) * (1 + cf) + sf
+    up, gt = y @ d("wup").T, y @ d("wgate").T
+    mid = (4.0 * np.tanh(gt / 4.0) / (1 + np.exp(-gt))) * (25.0 * np.tanh(up / 25.0))
+    return x + (mid @ d("wdown").T) * gf
+
+
+def make_moss(T=160, nvalid=150, D=256, F=512, seed=0):
+    rng = np.random.default_rng(seed)
+    w = {k: f16(rng.standard_normal((n, kk)) * 0.02 * np.sqrt(3072 / kk)) for k, (n, kk) in
+         {"wq": (D, D), "wk": (D, D), "wv": (D, D), "wo": (D, D), "wup": (F, D), "wgate": (F, D), "wdown": (D, F)}.items()}
+    w["gq"] = (rng.uniform(0.5, 1.5, 128) / np.sqrt(128)).astype(np.float32)
+    w["gk"] = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    w["n1"] = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    w["n2"] = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    x = (rng.standard_normal((T, D)) * 4).astype(np.float32)
+    mod6 = (rng.standard_normal((6, D)) * 0.3).astype(np.float32)
+    bands = (1.0 / 10000.0 ** (np.arange(16) / 16)).astype(np.float32)
+    cos, sin = hxo.rope_moss(10, 12, 30, bands)  # 120 image + 30 text = 150 valid tokens
+    cos = np.concatenate([cos, np.ones((T - len(cos), 64), np.float32)])
+    sin = np.concatenate([sin, np.zeros((T - len(sin), 64), np.float32)])
+    return x, mod6, cos, sin, w
+
+
+def test_moss_block_vs_float64_restatement():
+    x, mod6, cos, sin, w = make_moss()
+    nv = 150
+    ref = moss_block_f64(x, mod6, cos, sin, w, nv)
+    out, buf, n = hxo.moss_block(x, mod6, cos, sin, w, H=2, F=512, nvalid=nv)
+    assert n == 8
+    dl = (ref - x)[:nv]
+    rel = np.linalg.norm((out - ref)[:nv]) / np.linalg.norm(dl)
+    assert rel < 6e-3, rel
+    # padded rows never influence valid rows
+    x2 = x.copy()
+    x2[nv:] = 123.0
+    out2, _, _ = hxo.moss_block(x2, mod6, cos, sin, w, H=2, F=512, nvalid=nv)
+    assert np.array_equal(out2[:nv], out[:nv])
+
+
+@pytest.mark.parametrize("stop", [1, 4, 5, 8])
+def test_moss_stop(stop):
+    x, mod6, cos, sin, w = make_moss(seed=3)
+    out, buf, n = hxo.moss_block(x, mod6, cos, sin, w, H=2, F=512, nvalid=150, stop=stop)
+    assert n == stop
+    if stop < 5:
+        assert np.array_equal(out, x)
+    else:
+        assert not np.array_equal(out, x)
