@@ -1,0 +1,413 @@
+// DiT runner: the layer directly above the block boundary. It owns every weight of a synthetic DiT in HBM
+// (GPU block packs + glue), and runs one flow-matching Euler step entirely on the device:
+//   timestep sinusoid -> t-embedding -> per-block adaLN modulation (megarun.cpp:156-171 role; animad.cpp:424-431)
+//   patchify + x_embedder (animad.cpp:447-452) [MOSS: + text projection, joint token layout]
+//   blocks 0..n-1 (hxa_block_run)
+//   final adaLN + linear + unpatchify (animad.cpp:474-492) fused with the Euler update x += (s' - s) v
+// A step is captured once into a HIP graph and replayed; sigma values are read from device memory so one graph
+// serves every step.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "../../include/hexanima_hip.h"
+#include "hxa_common.h"
+#include "kernels.h"
+
+namespace {
+
+struct Dit {
+  hxa_dit_cfg cfg{};
+  hxa_block_dims bd{};
+  int Timg = 0, Ttot = 0, ntxt = 0;
+  hipStream_t st = nullptr;
+  std::vector<void *> packs;
+  long pack_bytes = 0;
+  std::vector<hxa_h *> modw;  // Anima: per block [6D][D]; MOSS: one shared [6D][D]
+  hxa_h *glue = nullptr;      // x_embed [D][4C] | t_embed [D][temb] | final_mod [2D][D] | final_lin [4C][D] | text_proj
+  long glue_elems = 0;
+  hxa_h *Wemb = nullptr, *L1 = nullptr, *Lf = nullptr, *Wfin = nullptr, *Wtxt = nullptr;
+  float *lat = nullptr, *vel = nullptr, *tok = nullptr, *x = nullptr, *sinus = nullptr, *cvec = nullptr;
+  float *mods = nullptr, *fmod = nullptr, *sig = nullptr, *cosT = nullptr, *sinT = nullptr, *ones = nullptr;
+  hxa_h *ctx16 = nullptr;  // Anima: [B*C][DC]; MOSS: text [B*ntxt][ntxt_in]
+  void *ws = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph = nullptr;
+  float *sig_host = nullptr;  // pinned
+};
+
+thread_local char g_derr[256];
+int dfail(int code, const char *m) {
+  snprintf(g_derr, sizeof g_derr, "%s", m);
+  return code;
+}
+#define DHIP(x)                                  \
+  do {                                           \
+    if ((x) != hipSuccess) return dfail(HXA_E_HIP, #x); \
+  } while (0)
+#define DTRY(x)                     \
+  do {                              \
+    int r__ = (x);                  \
+    if (r__ != HXA_OK) return r__;  \
+  } while (0)
+
+long align256(long x) { return (x + 255) & ~255L; }
+
+// megarun.cpp:77-90: 3-axis split-half table over hd = 128 (22 zero t-angles, 21 h, 21 w; theta 10000)
+void rope_anima(int gh, int gw, std::vector<float> &c, std::vector<float> &s) {
+  const int dim_h = 128 / 6 * 2, dim_t = 128 - 2 * dim_h, nt = dim_t / 2, nh = dim_h / 2;
+  std::vector<double> fh(nh);
+  for (int i = 0; i < nh; i++) fh[i] = 1.0 / pow(10000.0, (2.0 * i) / dim_h);
+  c.assign((size_t)gh * gw * 64, 0.0f);
+  s.assign((size_t)gh * gw * 64, 0.0f);
+  for (int tk = 0; tk < gh * gw; tk++) {
+    const int hh = tk / gw, ww = tk % gw;
+    for (int d = 0; d < 64; d++) {
+      const double ang = d < nt ? 0.0 : d < nt + nh ? hh * fh[d - nt] : ww * fh[d - nt - nh];
+      c[(size_t)tk * 64 + d] = (float)cos(ang);
+      s[(size_t)tk * 64 + d] = (float)sin(ang);
+    }
+  }
+}
+// moss_ref.py:27-35: 4 axes x 16 bands; image (0, ntxt, h-(H-1)/2, w-(W-1)/2), text (0, i, 0, 0);
+// synthetic bands 10000^(-i/16); padding rows get the identity rotation
+void rope_moss(int H, int W, int ntxt, int Ttot, std::vector<float> &c, std::vector<float> &s) {
+  c.assign((size_t)Ttot * 64, 1.0f);
+  s.assign((size_t)Ttot * 64, 0.0f);
+  const int nimg = H * W;
+  for (int tk = 0; tk < nimg + ntxt; tk++) {
+    double pos[4];
+    if (tk < nimg) {
+      pos[0] = 0;
+      pos[1] = ntxt;
+      pos[2] = (tk / W) - (H - 1) / 2.0;
+      pos[3] = (tk % W) - (W - 1) / 2.0;
+    } else {
+      pos[0] = 0;
+      pos[1] = tk - nimg;
+      pos[2] = pos[3] = 0;
+    }
+    for (int d = 0; d < 64; d++) {
+      const double band = (double)(float)(1.0 / pow(10000.0, (d % 16) / 16.0));
+      const double ph = pos[d / 16] * band;
+      c[(size_t)tk * 64 + d] = (float)cos(ph);
+      s[(size_t)tk * 64 + d] = (float)sin(ph);
+    }
+  }
+}
+
+
+uint16_t f2h_host(float f) {
+  // round-to-nearest-even fp32 -> fp16 (inputs are finite and in range)
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sgn = (x >> 16) & 0x8000u;
+  x &= 0x7fffffffu;
+  if (x >= 0x477ff000u) return (uint16_t)(sgn | 0x7c00u);
+  if (x >= 0x38800000u) {
+    uint32_t h = (((x >> 23) - 112u) << 10) | ((x & 0x7fffffu) >> 13);
+    const uint32_t rem = x & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sgn | h);
+  }
+  const float a = fabsf(f) * 16777216.0f;  // subnormal: units of 2^-24
+  return (uint16_t)(sgn | (uint32_t)nearbyintf(a));
+}
+
+int init_pack(Dit &d, void *pack, uint64_t seed, float *tmp32) {
+  const hxa_block_dims &b = d.bd;
+  int N[8], K[8], fmt[8];
+  const int n = hxa_pack_mats(b.kind, b.D, b.F, b.DC, b.fmt_attn, b.fmt_mlp, N, K, fmt);
+  long offs[32];
+  hxa_pack_layout(b.kind, b.D, b.F, b.DC, b.fmt_attn, b.fmt_mlp, offs, 32);
+  char *base = (char *)pack;
+  for (int i = 0; i < n; i++) {
+    const size_t elems = (size_t)N[i] * K[i];
+    if (fmt[i] == HXA_W_F16) {
+      DTRY(hxa_fill_normal_launch(base + offs[3 * i], 1, elems, seed * 131 + i, 0.0f, 0.02f, d.st));
+    } else {
+      DTRY(hxa_fill_normal_launch(tmp32, 0, elems, seed * 131 + i, 0.0f, 0.02f, d.st));
+      DTRY(hxa_quantize_launch(tmp32, N[i], K[i], fmt[i], base + offs[3 * i], (hxa_h *)(base + offs[3 * i + 1]), d.st));
+    }
+  }
+  float *vec = (float *)(base + offs[3 * n]);
+  const float qg = 1.0f / sqrtf(128.0f);
+  if (b.kind == 0) {  // q/k norm gains 1; the q gains carry 1/sqrt(128) (export_all.py:31-32)
+    DTRY(hxa_fill_const_launch(vec, 0, 128, qg, d.st));
+    DTRY(hxa_fill_const_launch(vec + 128, 0, 128, 1.0f, d.st));
+    DTRY(hxa_fill_const_launch(vec + 256, 0, 128, qg, d.st));
+    DTRY(hxa_fill_const_launch(vec + 384, 0, 128, 1.0f, d.st));
+  } else {
+    DTRY(hxa_fill_const_launch(vec, 0, 128, qg, d.st));
+    DTRY(hxa_fill_const_launch(vec + 128, 0, 128 + 2 * b.D, 1.0f, d.st));
+  }
+  return HXA_OK;
+}
+
+enum { MODE_EULER = 0, MODE_VELOCITY = 1 };
+
+int record_step(Dit &d, int mode) {
+  const hxa_block_dims &b = d.bd;
+  const int B = b.batch, D = b.D, C4 = 4 * d.cfg.lat_c, temb = d.cfg.temb, nb = d.cfg.nblocks;
+  hipStream_t st = d.st;
+  // timestep embedding and modulation
+  DTRY(hxa_sinusoid_launch(d.sig, 1, temb, d.sinus, st));
+  DTRY(hxa_linear_f32_launch(d.sinus, temb, 1, temb, d.L1, D, d.cvec, D, 0, nullptr, 0, 0, st));
+  if (b.kind == 0) {
+    for (int k = 0; k < nb; k++)  // rows 0-2 -> site 0, rows 3-5 -> site 2 (site 1 keeps identity modulation)
+      DTRY(hxa_linear_f32_launch(d.cvec, D, 1, D, d.modw[k], 6 * D, d.mods + (long)k * 9 * D, 0, 1, nullptr, 3 * D, 3 * D, st));
+  } else {
+    DTRY(hxa_linear_f32_launch(d.cvec, D, 1, D, d.modw[0], 6 * D, d.mods, 0, 1, nullptr, 0, 0, st));
+  }
+  DTRY(hxa_linear_f32_launch(d.cvec, D, 1, D, d.Lf, 2 * D, d.fmod, 0, 1, nullptr, 0, 0, st));
+  // patch embed (+ MOSS text tokens)
+  DTRY(hxa_patchify_launch(d.lat, B, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w, d.tok, st));
+  for (int i = 0; i < B; i++) {
+    DTRY(hxa_linear_f32_launch(d.tok + (long)i * d.Timg * C4, C4, d.Timg, C4, d.Wemb, D, d.x + (long)i * d.Ttot * D, D, 0,
+                               nullptr, 0, 0, st));
+    if (b.kind == 1) {
+      float *xt = d.x + ((long)i * d.Ttot + d.Timg) * D;
+      DTRY(hxa_fill_const_launch(xt, 0, (size_t)(d.Ttot - d.Timg) * D, 0.0f, st));
+      HxaWeight wt{HXA_W_F16, D, d.cfg.ntxt_in, d.Wtxt, nullptr, nullptr};
+      HxaGemm g{};
+      g.A = d.ctx16 + (long)i * d.ntxt * d.cfg.ntxt_in;
+      g.lda = d.cfg.ntxt_in;
+      g.M = d.ntxt;
+      g.w = &wt;
+      g.ksplit = 1;
+      g.epi = HXA_EPI_RESADD;  // text projection x += 1 * f16(text W^T) (moss blk.c MODE 2)
+      g.x = xt;
+      g.ldx = D;
+      g.gate = d.ones;
+      DTRY(hxa_gemm_launch(g, st));
+    }
+  }
+  // blocks
+  for (int k = 0; k < nb; k++) {
+    const float *mod = b.kind == 0 ? d.mods + (long)k * 9 * D : d.mods;
+    DTRY(hxa_block_run(&d.bd, d.packs[k], d.x, b.kind == 0 ? d.ctx16 : nullptr, mod, d.cosT, d.sinT, d.ws, 0, nullptr, 0, st));
+  }
+  // final layer (+ Euler update)
+  DTRY(hxa_final_launch(d.x, B, d.Timg, d.Ttot, D, d.fmod, d.fmod + D, d.Wfin, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w,
+                        mode == MODE_EULER ? d.lat : d.vel, mode == MODE_EULER ? d.sig + 2 : nullptr, st));
+  return HXA_OK;
+}
+
+int set_sigma(Dit &d, float s0, float s1) {
+  float h[4] = {s0, s1, s1 - s0, 0.0f};  // pageable source: staged before the call returns
+  DHIP(hipMemcpyAsync(d.sig, h, sizeof h, hipMemcpyHostToDevice, d.st));
+  return HXA_OK;
+}
+
+}  // namespace
+
+extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out) {
+  if (!cfg || !out) return dfail(HXA_E_ARG, "null");
+  *out = nullptr;
+  Dit *dp = new Dit();
+  Dit &d = *dp;
+  d.cfg = *cfg;
+  d.bd = cfg->blk;
+  hxa_block_dims &b = d.bd;
+  const int D = b.D, B = b.batch, C4 = 4 * cfg->lat_c;
+  if (cfg->lat_h % 2 || cfg->lat_w % 2 || C4 > 256 || 256 % C4 || cfg->temb % 2 || cfg->nblocks < 1) {
+    delete dp;
+    return dfail(HXA_E_ARG, "dit: latent / embedding shape");
+  }
+  d.Timg = (cfg->lat_h / 2) * (cfg->lat_w / 2);
+  if (b.kind == 0) {
+    b.T = d.Ttot = d.Timg;
+    b.nvalid = b.T;
+  } else {
+    d.ntxt = b.C;
+    d.Ttot = (d.Timg + d.ntxt + 31) / 32 * 32;
+    b.T = d.Ttot;
+    b.nvalid = d.Timg + d.ntxt;
+    b.C = 0;
+    b.DC = 0;
+    if (cfg->ntxt_in <= 0 || cfg->ntxt_in % 64) {
+      delete dp;
+      return dfail(HXA_E_ARG, "dit: MOSS text width");
+    }
+  }
+  if (b.kind == 0 && d.Timg % 32) {
+    delete dp;
+    return dfail(HXA_E_ARG, "dit: token count must be a multiple of 32");
+  }
+  int rc = HXA_OK;
+  auto M = [&](void **p, size_t bytes) {
+    if (rc == HXA_OK && hipMalloc(p, bytes) != hipSuccess) rc = dfail(HXA_E_RESOURCE, "dit: out of device memory");
+  };
+  if (hipStreamCreateWithFlags(&d.st, hipStreamNonBlocking) != hipSuccess) {
+    delete dp;
+    return dfail(HXA_E_RESOURCE, "dit: stream");
+  }
+  d.pack_bytes = hxa_pack_layout(b.kind, D, b.F, b.DC, b.fmt_attn, b.fmt_mlp, nullptr, 0);
+  d.packs.assign(cfg->nblocks, nullptr);
+  for (auto &p : d.packs) M(&p, d.pack_bytes);
+  d.modw.assign(b.kind == 0 ? cfg->nblocks : 1, nullptr);
+  for (auto &p : d.modw) M((void **)&p, 2L * 6 * D * D);
+  d.glue_elems = (long)D * C4 + (long)D * cfg->temb + 2L * D * D + (long)C4 * D + (b.kind == 1 ? (long)D * cfg->ntxt_in : 0);
+  M((void **)&d.glue, 2 * d.glue_elems);
+  const long latn = (long)B * cfg->lat_c * cfg->lat_h * cfg->lat_w;
+  M((void **)&d.lat, 4 * latn);
+  M((void **)&d.vel, 4 * latn);
+  M((void **)&d.tok, 4L * B * d.Timg * C4);
+  M((void **)&d.x, 4L * B * d.Ttot * D);
+  M((void **)&d.sinus, 4L * cfg->temb);
+  M((void **)&d.cvec, 4L * D);
+  M((void **)&d.mods, 4L * (b.kind == 0 ? cfg->nblocks * 9L : 6L) * D);
+  M((void **)&d.fmod, 4L * 2 * D);
+  M((void **)&d.sig, 16);
+  M((void **)&d.cosT, 4L * d.Ttot * 64);
+  M((void **)&d.sinT, 4L * d.Ttot * 64);
+  M((void **)&d.ones, 4L * D);
+  M((void **)&d.ctx16, b.kind == 0 ? 2L * B * b.C * b.DC : 2L * B * d.ntxt * cfg->ntxt_in);
+  M(&d.ws, hxa_block_ws_bytes(&b));
+  if (rc != HXA_OK) {
+    hxa_dit_destroy(dp);
+    return rc;
+  }
+  // weights: N(0, 0.02), quantised after generation for q8 / q4 formats
+  long maxmat = 0;
+  {
+    int N[8], K[8], f[8];
+    const int n = hxa_pack_mats(b.kind, D, b.F, b.DC, b.fmt_attn, b.fmt_mlp, N, K, f);
+    for (int i = 0; i < n; i++) maxmat = std::max(maxmat, (long)N[i] * K[i]);
+  }
+  float *tmp = nullptr;
+  if (b.fmt_attn != HXA_W_F16 || b.fmt_mlp != HXA_W_F16) M((void **)&tmp, 4 * maxmat);
+  for (int k = 0; k < cfg->nblocks && rc == HXA_OK; k++) rc = init_pack(d, d.packs[k], seed * 1000003ull + k, tmp);
+  for (size_t k = 0; k < d.modw.size() && rc == HXA_OK; k++)
+    rc = hxa_fill_normal_launch(d.modw[k], 1, 6L * D * D, seed * 7919ull + 100000 + k, 0.0f, 0.02f, d.st);
+  if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.glue, 1, d.glue_elems, seed * 7919ull + 99999, 0.0f, 0.02f, d.st);
+  d.Wemb = d.glue;
+  d.L1 = d.Wemb + (long)D * C4;
+  d.Lf = d.L1 + (long)D * cfg->temb;
+  d.Wfin = d.Lf + 2L * D * D;
+  d.Wtxt = b.kind == 1 ? d.Wfin + (long)C4 * D : nullptr;
+  if (rc == HXA_OK) rc = hxa_fill_const_launch(d.ones, 0, D, 1.0f, d.st);
+  if (rc == HXA_OK && b.kind == 0) {  // site-1 rows of every block: shift 0, scale 0, gate 1
+    for (int k = 0; k < cfg->nblocks && rc == HXA_OK; k++) {
+      rc = hxa_fill_const_launch(d.mods + (long)k * 9 * D + 3L * D, 0, 2L * D, 0.0f, d.st);
+      if (rc == HXA_OK) rc = hxa_fill_const_launch(d.mods + (long)k * 9 * D + 5L * D, 0, D, 1.0f, d.st);
+    }
+  }
+  if (rc == HXA_OK && hipMemsetAsync(d.x, 0, 4L * B * d.Ttot * D, d.st) != hipSuccess) rc = dfail(HXA_E_HIP, "memset");
+  std::vector<float> c, s;
+  if (b.kind == 0) {
+    // token (gy, gx) of a gh x gw grid, gh = H/2 rows (megarun's gh, gw arguments)
+    rope_anima(cfg->lat_h / 2, cfg->lat_w / 2, c, s);
+  } else {
+    rope_moss(cfg->lat_h / 2, cfg->lat_w / 2, d.ntxt, d.Ttot, c, s);
+  }
+  if (rc == HXA_OK && (hipMemcpyAsync(d.cosT, c.data(), 4 * c.size(), hipMemcpyHostToDevice, d.st) != hipSuccess ||
+                       hipMemcpyAsync(d.sinT, s.data(), 4 * s.size(), hipMemcpyHostToDevice, d.st) != hipSuccess))
+    rc = dfail(HXA_E_HIP, "rope upload");
+  if (rc == HXA_OK && hipStreamSynchronize(d.st) != hipSuccess) rc = dfail(HXA_E_HIP, "init sync");
+  if (tmp) (void)hipFree(tmp);
+  if (rc != HXA_OK) {
+    hxa_dit_destroy(dp);
+    return rc;
+  }
+  *out = dp;
+  return HXA_OK;
+}
+
+extern "C" int hxa_dit_destroy(void *p) {
+  Dit *d = (Dit *)p;
+  if (!d) return HXA_OK;
+  if (d->st) (void)hipStreamSynchronize(d->st);
+  if (d->exec) (void)hipGraphExecDestroy(d->exec);
+  if (d->graph) (void)hipGraphDestroy(d->graph);
+  for (void *q : d->packs) if (q) (void)hipFree(q);
+  for (void *q : d->modw) if (q) (void)hipFree(q);
+  void *bufs[] = {d->glue, d->lat, d->vel, d->tok, d->x, d->sinus, d->cvec, d->mods, d->fmod, d->sig, d->cosT, d->sinT, d->ones, d->ctx16, d->ws};
+  for (void *q : bufs) if (q) (void)hipFree(q);
+  if (d->st) (void)hipStreamDestroy(d->st);
+  delete d;
+  return HXA_OK;
+}
+
+extern "C" int hxa_dit_set_inputs(void *p, const float *lat, const float *ctx) {
+  Dit &d = *(Dit *)p;
+  const hxa_block_dims &b = d.bd;
+  const long latn = (long)b.batch * d.cfg.lat_c * d.cfg.lat_h * d.cfg.lat_w;
+  if (lat) DHIP(hipMemcpyAsync(d.lat, lat, 4 * latn, hipMemcpyHostToDevice, d.st));
+  if (ctx) {
+    const long n = b.kind == 0 ? (long)b.batch * b.C * b.DC : (long)b.batch * d.ntxt * d.cfg.ntxt_in;
+    std::vector<uint16_t> h(n);
+    for (long i = 0; i < n; i++) h[i] = f2h_host(ctx[i]);
+    DHIP(hipMemcpyAsync(d.ctx16, h.data(), 2 * n, hipMemcpyHostToDevice, d.st));
+  }
+  DHIP(hipStreamSynchronize(d.st));
+  return HXA_OK;
+}
+
+extern "C" int hxa_dit_get_latent(void *p, float *lat) {
+  Dit &d = *(Dit *)p;
+  const long latn = (long)d.bd.batch * d.cfg.lat_c * d.cfg.lat_h * d.cfg.lat_w;
+  DHIP(hipMemcpyAsync(lat, d.lat, 4 * latn, hipMemcpyDeviceToHost, d.st));
+  DHIP(hipStreamSynchronize(d.st));
+  return HXA_OK;
+}
+
+extern "C" int hxa_dit_step(void *p, float sigma, float sigma_next, int use_graph) {
+  Dit &d = *(Dit *)p;
+  DTRY(set_sigma(d, sigma, sigma_next));
+  if (!use_graph) return record_step(d, MODE_EULER);
+  if (!d.exec) {
+    DHIP(hipStreamBeginCapture(d.st, hipStreamCaptureModeRelaxed));
+    const int r = record_step(d, MODE_EULER);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(d.st, &g);
+    if (r != HXA_OK) {
+      if (g) (void)hipGraphDestroy(g);
+      return r;
+    }
+    if (e != hipSuccess) return dfail(HXA_E_HIP, "graph capture");
+    d.graph = g;
+    DHIP(hipGraphInstantiate(&d.exec, d.graph, nullptr, nullptr, 0));
+  }
+  DHIP(hipGraphLaunch(d.exec, d.st));
+  return HXA_OK;
+}
+
+extern "C" int hxa_dit_velocity(void *p, float sigma, float *v) {
+  Dit &d = *(Dit *)p;
+  DTRY(set_sigma(d, sigma, sigma));
+  DTRY(record_step(d, MODE_VELOCITY));
+  const long latn = (long)d.bd.batch * d.cfg.lat_c * d.cfg.lat_h * d.cfg.lat_w;
+  DHIP(hipMemcpyAsync(v, d.vel, 4 * latn, hipMemcpyDeviceToHost, d.st));
+  DHIP(hipStreamSynchronize(d.st));
+  return HXA_OK;
+}
+
+extern "C" long hxa_dit_export(void *p, int which, void *host, size_t bytes) {
+  Dit &d = *(Dit *)p;
+  const int nb = d.cfg.nblocks;
+  const void *src = nullptr;
+  long n = 0;
+  if (which >= 0 && which < nb) {
+    src = d.packs[which];
+    n = d.pack_bytes;
+  } else if (which >= nb && which < nb + (int)d.modw.size()) {
+    src = d.modw[which - nb];
+    n = 2L * 6 * d.bd.D * d.bd.D;
+  } else if (which == 2 * nb) {
+    src = d.glue;
+    n = 2 * d.glue_elems;
+  } else {
+    return dfail(HXA_E_ARG, "dit export index");
+  }
+  if (!host) return n;
+  if ((long)bytes < n) return dfail(HXA_E_ARG, "dit export buffer too small");
+  if (hipStreamSynchronize(d.st) != hipSuccess || hipMemcpy(host, src, n, hipMemcpyDeviceToHost) != hipSuccess)
+    return dfail(HXA_E_HIP, "dit export copy");
+  return n;
+}
+
+extern "C" void *hxa_dit_stream(void *p) { return p ? (void *)((Dit *)p)->st : nullptr; }

@@ -1,0 +1,490 @@
+// Bandwidth-bound kernels of the DiT block runner for gfx950: modulated LayerNorm / RMSNorm, per-head
+// RMSNorm + RoPE, the split-K gated residual, the reference crouton-layout conversions used at the C-ABI
+// boundary, synthetic-data fills and the caller-side glue (patch embed, timestep sinusoid, final layer + Euler).
+//
+// Row kernels use one 64-lane wave per row with 16-byte vector loads (fully coalesced); reductions stay inside
+// the wave (no LDS, no barriers).
+#include "hxa_common.h"
+#include "kernels.h"
+
+namespace {
+
+HXA_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// modulated norm (kern.c:31-65 LN-mod; moss kern.c:345-375 RMS-mod)
+// ---------------------------------------------------------------------------------------------------------------
+template <int VPL>
+__global__ __launch_bounds__(256) void normmod_kernel(const float *__restrict__ x, long ldx, int T, int D,
+                                                      const float *__restrict__ shift, const float *__restrict__ scale,
+                                                      const float *__restrict__ w, float eps, hxa_h *__restrict__ h,
+                                                      long ldh) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= T) return;
+  const float4_t *xr = (const float4_t *)(x + (long)row * ldx);
+  float4_t v[VPL];
+  float s = 0.0f, q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPL; i++) {
+    v[i] = xr[lane + 64 * i];
+    s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+    q += (v[i][0] * v[i][0] + v[i][1] * v[i][1]) + (v[i][2] * v[i][2] + v[i][3] * v[i][3]);
+  }
+  s = wave_sum(s);
+  q = wave_sum(q);
+  const float inv = 1.0f / (float)D;
+  float mu, r;
+  if (w == nullptr) {
+    mu = s * inv;
+    r = rsqrtf(q * inv - mu * mu + eps);  // var = E[x^2] - mu^2 (kern.c:52-53)
+  } else {
+    mu = 0.0f;
+    r = rsqrtf(q * inv + eps);
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; i++) {
+    const int c = (lane + 64 * i) * 4;
+    const float4_t sc = *(const float4_t *)(scale + c), sh = *(const float4_t *)(shift + c);
+    float4_t mul = sc + 1.0f;
+    if (w != nullptr) mul *= *(const float4_t *)(w + c);  // k_rms_prep: M = (1 + scale) * w
+    half4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] = (hxa_h)((v[i][e] - mu) * r * mul[e] + sh[e]);
+    *(half4_t *)(h + (long)row * ldh + c) = o;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// per-head RMSNorm * gain + split-half RoPE (kern.c:163-197); one wave per (token, head): lane l owns d = l, l+64
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rmsrope_kernel(hxa_h *q0, hxa_h *q1, const float *g0, const float *g1, long ldq,
+                                                      int T, int H, const float *__restrict__ cosT,
+                                                      const float *__restrict__ sinT, int ttab) {
+  const long wid = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (wid >= (long)T * H) return;
+  const int t = (int)(wid / H), hd = (int)(wid % H);
+  hxa_h *q = blockIdx.y ? q1 : q0;
+  const float *g = blockIdx.y ? g1 : g0;
+  hxa_h *p = q + (long)t * ldq + hd * 128;
+  float a = (float)p[lane], b = (float)p[lane + 64];
+  const float ss = wave_sum(a * a + b * b);
+  const float r = rsqrtf(ss * (1.0f / 128.0f) + 1e-6f);
+  a = a * r * g[lane];
+  b = b * r * g[lane + 64];
+  if (cosT != nullptr) {
+    const int tt = t % ttab;
+    const float c = cosT[(long)tt * 64 + lane], s = sinT[(long)tt * 64 + lane];
+    const float na = a * c - b * s, nb = a * s + b * c;
+    a = na;
+    b = nb;
+  }
+  p[lane] = (hxa_h)a;
+  p[lane + 64] = (hxa_h)b;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// x += gate * (t1 + t2)   (kern.c:330-339, split-K down projection)
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void resadd2_kernel(float *x, long ldx, const hxa_h *__restrict__ t1,
+                                                      const hxa_h *__restrict__ t2, long ldt, int T, int D,
+                                                      const float *__restrict__ gate) {
+  const long i4 = (long)blockIdx.x * 256 + threadIdx.x;
+  const int per_row = D / 4;
+  if (i4 >= (long)T * per_row) return;
+  const int row = (int)(i4 / per_row), c = (int)(i4 % per_row) * 4;
+  float4_t *xp = (float4_t *)(x + (long)row * ldx + c);
+  const half4_t a = *(const half4_t *)(t1 + (long)row * ldt + c), b = *(const half4_t *)(t2 + (long)row * ldt + c);
+  const float4_t g = *(const float4_t *)(gate + c);
+  float4_t xv = *xp;
+#pragma unroll
+  for (int e = 0; e < 4; e++) xv[e] = fmaf(g[e], (float)a[e] + (float)b[e], xv[e]);
+  *xp = xv;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// crouton layout conversions (kern.h:5-8): x32 float(r,c) = r*32+c; h16 halfword(r,c) = (r/2)*64 + c*2 + (r&1)
+// ---------------------------------------------------------------------------------------------------------------
+__global__ void x32_to_rows_kernel(const float *tiles, float *x, int R, int C) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)R * C) return;
+  const int r = (int)(i / C), c = (int)(i % C);
+  x[i] = tiles[((long)(r >> 5) * (C >> 5) + (c >> 5)) * 1024 + (r & 31) * 32 + (c & 31)];
+}
+__global__ void rows_to_x32_kernel(const float *x, float *tiles, int R, int C) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)R * C) return;
+  const int r = (int)(i / C), c = (int)(i % C);
+  tiles[((long)(r >> 5) * (C >> 5) + (c >> 5)) * 1024 + (r & 31) * 32 + (c & 31)] = x[i];
+}
+__global__ void h16_to_rows_kernel(const hxa_h *tiles, hxa_h *a, long lda, int R, int C) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)R * C) return;
+  const int r = (int)(i / C), c = (int)(i % C);
+  a[(long)r * lda + c] = tiles[((long)(r >> 5) * (C >> 5) + (c >> 5)) * 1024 + ((r & 31) >> 1) * 64 + (c & 31) * 2 + (r & 1)];
+}
+__global__ void rows_to_h16_kernel(const hxa_h *a, long lda, hxa_h *tiles, int R, int C, int transposed) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)R * C) return;
+  const int r = (int)(i / C), c = (int)(i % C);
+  const hxa_h v = transposed ? a[(long)c * lda + r] : a[(long)r * lda + c];
+  tiles[((long)(r >> 5) * (C >> 5) + (c >> 5)) * 1024 + ((r & 31) >> 1) * 64 + (c & 31) * 2 + (r & 1)] = v;
+}
+__global__ void cs_to_rows_kernel(const float *tiles, float *rows, int T) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)T * 64) return;
+  const int tk = (int)(i / 64), d = (int)(i % 64);
+  rows[i] = tiles[((long)(tk >> 5) * 2 + (d >> 5)) * 1024 + (tk & 31) * 32 + (d & 31)];
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// synthetic data: counter-based hash (splitmix64 finaliser) -> uniform / Box-Muller normal
+// ---------------------------------------------------------------------------------------------------------------
+HXA_DEV uint64_t mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__global__ void fill_normal_kernel(void *dst, int dtype, size_t n, uint64_t seed, float mean, float std) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t h = mix64(seed * 0xD1B54A32D192ED03ull + i);
+  const float u1 = ((float)(h >> 40) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+  const float u2 = (float)((h >> 16) & 0xFFFFFFull) * (1.0f / 16777216.0f);
+  const float z = sqrtf(-2.0f * __logf(u1)) * __cosf(6.283185307179586f * u2);
+  const float v = mean + std * z;
+  if (dtype == 0) ((float *)dst)[i] = v;
+  else ((hxa_h *)dst)[i] = (hxa_h)v;
+}
+__global__ void fill_uniform_int_kernel(void *dst, int bits, size_t n, uint64_t seed, int lo, int hi) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t h = mix64(seed * 0xD1B54A32D192ED03ull + i);
+  const uint32_t span = (uint32_t)(hi - lo + 1);
+  if (bits == 8) {
+    ((int8_t *)dst)[i] = (int8_t)(lo + (int)((h >> 32) % span));
+  } else {  // one byte = two int4 nibbles (value + 8)
+    const int a = lo + (int)((h >> 32) % span) + 8, b = lo + (int)((h & 0xFFFFFFFFull) % span) + 8;
+    ((uint8_t *)dst)[i] = (uint8_t)(a | (b << 4));
+  }
+}
+__global__ void fill_const_kernel(void *dst, int dtype, size_t n, float v) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  if (dtype == 0) ((float *)dst)[i] = v;
+  else ((hxa_h *)dst)[i] = (hxa_h)v;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// caller-side glue (phone/animad.cpp)
+// ---------------------------------------------------------------------------------------------------------------
+// patchify (animad.cpp:447-450): lat [B][C][H][W] -> tok [B*T][C*4], feature (c, ph, pw)
+__global__ void patchify_kernel(const float *lat, int B, int Cc, int H, int W, float *tok) {
+  const int gh = H / 2, gw = W / 2, F = Cc * 4;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)B * gh * gw * F) return;
+  const int f = (int)(i % F);
+  const long tkb = i / F;
+  const int tk = (int)(tkb % (gh * gw)), b = (int)(tkb / (gh * gw));
+  const int gy = tk / gw, gx = tk % gw, c = f / 4, a = (f / 2) & 1, bb = f & 1;
+  tok[i] = lat[(((long)b * Cc + c) * H + gy * 2 + a) * W + gx * 2 + bb];
+}
+
+// y[m][n] = act(sum_k x[m][k] * W[n][k] (+ bias[n])); act 0 none, 1 SiLU on the input (x -> x sigmoid(x)).
+// One wave per output feature n, lanes stride K (coalesced weight reads), up to 8 input rows.
+__global__ __launch_bounds__(256) void gemv_kernel(const float *__restrict__ x, long ldx, int M, int K,
+                                                   const hxa_h *__restrict__ W, int N, float *__restrict__ y, long ldy,
+                                                   int act, const float *__restrict__ bias, int split, int gap) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (n >= N) return;
+  float accm[8];
+#pragma unroll
+  for (int m = 0; m < 8; m++) accm[m] = 0.0f;
+  const hxa_h *wr = W + (long)n * K;
+  for (int k = lane * 2; k < K; k += 128) {
+    const half2_t wv = *(const half2_t *)(wr + k);
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+      if (m < M) {
+        float x0 = x[(long)m * ldx + k], x1 = x[(long)m * ldx + k + 1];
+        if (act == 1) {
+          x0 = x0 / (1.0f + __expf(-x0));
+          x1 = x1 / (1.0f + __expf(-x1));
+        }
+        accm[m] = fmaf(x0, (float)wv[0], fmaf(x1, (float)wv[1], accm[m]));
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 8; m++) {
+    if (m < M) {
+      const float v = wave_sum(accm[m]);
+      if (lane == 0) y[(long)m * ldy + n + (n >= split ? gap : 0)] = v + (bias ? bias[n] : 0.0f);
+    }
+  }
+}
+
+// x[m][n] = sum_k tok[m][k] * W[n][k], K <= 256 (patch embed). A 64-row x 64-col tile per workgroup; tok rows and
+// the weight tile are staged in LDS as fp32.
+__global__ __launch_bounds__(256) void linear_smallk_kernel(const float *__restrict__ x, long ldx, int M, int K,
+                                                            const hxa_h *__restrict__ W, int N, float *__restrict__ y,
+                                                            long ldy) {
+  __shared__ float xs[64][65];
+  __shared__ float ws[64][65];
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64, tid = threadIdx.x;
+  for (int i = tid; i < 64 * K; i += 256) {
+    const int r = i / K, k = i % K;
+    xs[r][k] = m0 + r < M ? x[(long)(m0 + r) * ldx + k] : 0.0f;
+    ws[r][k] = n0 + r < N ? (float)W[(long)(n0 + r) * K + k] : 0.0f;
+  }
+  __syncthreads();
+  const int tr = tid / 16, tc = tid % 16;  // 4x4 outputs per thread
+  float acc[4][4] = {};
+  for (int k = 0; k < K; k++) {
+    float a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) a[i] = xs[tr * 4 + i][k];
+#pragma unroll
+    for (int j = 0; j < 4; j++) b[j] = ws[tc + 16 * j][k];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int m = m0 + tr * 4 + i, n = n0 + tc + 16 * j;
+      if (m < M && n < N) y[(long)m * ldy + n] = acc[i][j];
+    }
+}
+
+// timestep sinusoid (animad.cpp:425): out[i] = cos(t w_i), out[half+i] = sin(t w_i), w_i = 10000^(-i/half)
+__global__ void sinusoid_kernel(const float *t, int n, int dim, float *out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int half = dim / 2;
+  if (i >= n * half) return;
+  const int b = i / half, j = i % half;
+  const float a = t[b] * expf(-logf(10000.0f) * (float)j / (float)half);
+  out[(long)b * dim + j] = cosf(a);
+  out[(long)b * dim + half + j] = sinf(a);
+}
+
+// final layer (animad.cpp:474-492): per token LN (eps 1e-6, two-pass) * (1 + scale) + shift, linear D -> 4C,
+// unpatchify (ph, pw, c) into lat; when dt != 0 the Euler update lat += dt * v is applied instead of storing v.
+__global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ x, int T, int xrows, int D,
+                                                    const float *__restrict__ shift, const float *__restrict__ scale,
+                                                    const hxa_h *__restrict__ Wf, int Cc, int H, int W, float *lat,
+                                                    const float *__restrict__ dtp) {
+  extern __shared__ float xn[];  // D floats + 256 scratch
+  float *red = xn + D;
+  const long tok = blockIdx.x;
+  const int b = (int)(tok / T), tk = (int)(tok % T), tid = threadIdx.x;
+  const float *xr = x + ((long)b * xrows + tk) * D;
+  float s = 0.0f;
+  for (int c = tid; c < D; c += 256) s += xr[c];
+  s = wave_sum(s);
+  if ((tid & 63) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  const float mu = (red[0] + red[1] + red[2] + red[3]) / (float)D;
+  __syncthreads();
+  float q = 0.0f;
+  for (int c = tid; c < D; c += 256) {
+    const float d = xr[c] - mu;
+    q += d * d;
+  }
+  q = wave_sum(q);
+  if ((tid & 63) == 0) red[tid >> 6] = q;
+  __syncthreads();
+  const float rs = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)D + 1e-6f);
+  for (int c = tid; c < D; c += 256) xn[c] = (xr[c] - mu) * rs * (1.0f + scale[c]) + shift[c];
+  __syncthreads();
+  // 4C outputs, 256/(4C) threads each
+  const int NO = 4 * Cc, per = 256 / NO;
+  const int o = tid / per, part = tid % per;
+  float acc = 0.0f;
+  if (o < NO) {
+    const hxa_h *wr = Wf + (long)o * D;
+    for (int c = part; c < D; c += per) acc = fmaf(xn[c], (float)wr[c], acc);
+  }
+  __syncthreads();
+  red[tid] = acc;
+  __syncthreads();
+  if (tid < NO) {
+    float v = 0.0f;
+    for (int j = 0; j < per; j++) v += red[tid * per + j];
+    const int gw = W / 2, gy = tk / gw, gx = tk % gw;
+    const int ab = tid / Cc, c = tid % Cc, a = ab >> 1, bb = ab & 1;
+    float *dst = lat + (((long)b * Cc + c) * H + gy * 2 + a) * W + gx * 2 + bb;
+    if (dtp != nullptr) *dst += *dtp * v;
+    else *dst = v;
+  }
+}
+
+// q8 / q4 quantisation of W[N][K] fp32, one thread per (column n, 32-group g): amax of the fp16-rounded weights,
+// s = f16(max(amax / qmax, 6.2e-5)), q = clip(rint(f16(w) / s)) (export_all.py:10-18, moss/export_all_q8.py:13)
+__global__ void quantize_kernel(const float *W, int N, int K, int fmt, void *q, hxa_h *s) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const int G = K / 32;
+  if (i >= (long)N * G) return;
+  const int n = (int)(i / G), g = (int)(i % G);
+  const float *wr = W + (long)n * K + g * 32;
+  float a[32], amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; j++) {
+    a[j] = (float)(hxa_h)wr[j];
+    amax = fmaxf(amax, fabsf(a[j]));
+  }
+  const float qmax = fmt == HXA_W_Q8 ? 127.0f : 7.0f, qmin = fmt == HXA_W_Q8 ? -127.0f : -8.0f;
+  float sc = amax / qmax;
+  if (sc < 6.2e-5f) sc = 6.2e-5f;
+  const hxa_h sh = (hxa_h)sc;
+  const float sf = (float)sh;
+  s[(long)g * N + n] = sh;
+  if (fmt == HXA_W_Q8) {
+    int8_t *qr = (int8_t *)q + (long)n * K + g * 32;
+#pragma unroll
+    for (int j = 0; j < 32; j++) qr[j] = (int8_t)fminf(fmaxf(rintf(a[j] / sf), qmin), qmax);
+  } else {
+    uint32_t *qw = (uint32_t *)((uint8_t *)q + (long)n * (K / 2) + g * 16);
+#pragma unroll
+    for (int w8 = 0; w8 < 4; w8++) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int v = (int)fminf(fmaxf(rintf(a[w8 * 8 + j] / sf), qmin), qmax) + 8;
+        word |= (uint32_t)v << ((j & 1) ? 16 + 4 * (j >> 1) : 4 * (j >> 1));
+      }
+      qw[w8] = word;
+    }
+  }
+}
+
+inline unsigned nblk(long n, int per = 256) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+#define LAUNCH_OK() (hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP)
+
+int hxa_norm_mod_launch(const float *x, long ldx, int T, int D, const float *shift, const float *scale, const float *w,
+                        float eps, hxa_h *h, long ldh, hipStream_t st) {
+  if (T <= 0 || D % 256 != 0 || ldx % 4 || ldh % 4) return HXA_E_ARG;
+  const int vpl = D / 256;
+  dim3 g(nblk(T, 4)), b(256);
+  switch (vpl) {
+    case 1: hipLaunchKernelGGL(normmod_kernel<1>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
+    case 2: hipLaunchKernelGGL(normmod_kernel<2>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
+    case 4: hipLaunchKernelGGL(normmod_kernel<4>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
+    case 8: hipLaunchKernelGGL(normmod_kernel<8>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
+    case 10: hipLaunchKernelGGL(normmod_kernel<10>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
+    case 12: hipLaunchKernelGGL(normmod_kernel<12>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
+    case 16: hipLaunchKernelGGL(normmod_kernel<16>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
+    default: return HXA_E_ARG;
+  }
+  return LAUNCH_OK();
+}
+
+int hxa_rmsrope_launch(hxa_h *q0, hxa_h *q1, const float *g0, const float *g1, long ldq, int T, int H, const float *cosT,
+                       const float *sinT, int ttab, hipStream_t st) {
+  if (T <= 0 || H <= 0 || (cosT && ttab <= 0)) return HXA_E_ARG;
+  dim3 g(nblk((long)T * H, 4), q1 ? 2 : 1);
+  hipLaunchKernelGGL(rmsrope_kernel, g, dim3(256), 0, st, q0, q1, g0, g1, ldq, T, H, cosT, sinT, ttab > 0 ? ttab : 1);
+  return LAUNCH_OK();
+}
+
+int hxa_resadd2_launch(float *x, long ldx, const hxa_h *t1, const hxa_h *t2, long ldt, int T, int D, const float *gate,
+                       hipStream_t st) {
+  if (D % 4 || ldx % 4 || ldt % 4) return HXA_E_ARG;
+  hipLaunchKernelGGL(resadd2_kernel, dim3(nblk((long)T * D / 4)), dim3(256), 0, st, x, ldx, t1, t2, ldt, T, D, gate);
+  return LAUNCH_OK();
+}
+
+int hxa_x32_to_rows_launch(const float *tiles, float *x, int R, int C, hipStream_t st) {
+  if (R % 32 || C % 32) return HXA_E_ARG;
+  hipLaunchKernelGGL(x32_to_rows_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, tiles, x, R, C);
+  return LAUNCH_OK();
+}
+int hxa_rows_to_x32_launch(const float *x, float *tiles, int R, int C, hipStream_t st) {
+  if (R % 32 || C % 32) return HXA_E_ARG;
+  hipLaunchKernelGGL(rows_to_x32_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, x, tiles, R, C);
+  return LAUNCH_OK();
+}
+int hxa_h16_to_rows_launch(const hxa_h *tiles, hxa_h *a, long lda, int R, int C, hipStream_t st) {
+  if (R % 32 || C % 32) return HXA_E_ARG;
+  hipLaunchKernelGGL(h16_to_rows_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, tiles, a, lda, R, C);
+  return LAUNCH_OK();
+}
+int hxa_rows_to_h16_launch(const hxa_h *a, long lda, hxa_h *tiles, int R, int C, int transposed, hipStream_t st) {
+  if (R % 32 || C % 32) return HXA_E_ARG;
+  hipLaunchKernelGGL(rows_to_h16_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, a, lda, tiles, R, C, transposed);
+  return LAUNCH_OK();
+}
+int hxa_cs_to_rows_launch(const float *tiles, float *rows, int T, hipStream_t st) {
+  if (T % 32) return HXA_E_ARG;
+  hipLaunchKernelGGL(cs_to_rows_kernel, dim3(nblk((long)T * 64)), dim3(256), 0, st, tiles, rows, T);
+  return LAUNCH_OK();
+}
+
+int hxa_fill_normal_launch(void *dst, int dtype, size_t n, uint64_t seed, float mean, float std, hipStream_t st) {
+  if (n == 0) return HXA_OK;
+  hipLaunchKernelGGL(fill_normal_kernel, dim3(nblk((long)n)), dim3(256), 0, st, dst, dtype, n, seed, mean, std);
+  return LAUNCH_OK();
+}
+int hxa_fill_uniform_int_launch(void *dst, int bits, size_t n, uint64_t seed, int lo, int hi, hipStream_t st) {
+  if (n == 0) return HXA_OK;
+  if (hi < lo || (bits != 8 && bits != 4)) return HXA_E_ARG;
+  hipLaunchKernelGGL(fill_uniform_int_kernel, dim3(nblk((long)n)), dim3(256), 0, st, dst, bits, n, seed, lo, hi);
+  return LAUNCH_OK();
+}
+int hxa_fill_const_launch(void *dst, int dtype, size_t n, float v, hipStream_t st) {
+  if (n == 0) return HXA_OK;
+  hipLaunchKernelGGL(fill_const_kernel, dim3(nblk((long)n)), dim3(256), 0, st, dst, dtype, n, v);
+  return LAUNCH_OK();
+}
+
+int hxa_patchify_launch(const float *lat, int B, int Cc, int H, int W, float *tok, hipStream_t st) {
+  if (H % 2 || W % 2) return HXA_E_ARG;
+  hipLaunchKernelGGL(patchify_kernel, dim3(nblk((long)B * Cc * H * W)), dim3(256), 0, st, lat, B, Cc, H, W, tok);
+  return LAUNCH_OK();
+}
+
+int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W, int N, float *y, long ldy, int act,
+                          const float *bias, int split, int gap, hipStream_t st) {
+  if (M <= 0 || K <= 0 || N <= 0) return HXA_E_ARG;
+  if (M <= 8) {
+    if (K % 2) return HXA_E_ARG;
+    hipLaunchKernelGGL(gemv_kernel, dim3(nblk(N, 4)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy, act, bias,
+                       split > 0 ? split : N, gap);
+  } else {
+    if (K > 64 || act != 0 || bias != nullptr || split > 0) return HXA_E_ARG;
+    hipLaunchKernelGGL(linear_smallk_kernel, dim3(nblk(N, 64), nblk(M, 64)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy);
+  }
+  return LAUNCH_OK();
+}
+
+int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale,
+                     const hxa_h *Wf, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st) {
+  const int NO = 4 * Cc;
+  if (NO > 256 || 256 % NO || (H / 2) * (W / 2) != T || xrows < T) return HXA_E_ARG;
+  const size_t lds = sizeof(float) * (size_t)(D + 256);
+  hipLaunchKernelGGL(final_kernel, dim3(B * T), dim3(256), lds, st, x, T, xrows, D, shift, scale, Wf, Cc, H, W, lat, dtp);
+  return LAUNCH_OK();
+}
+
+
+
+int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t st) {
+  hipLaunchKernelGGL(sinusoid_kernel, dim3(nblk((long)n * dim / 2)), dim3(256), 0, st, t, n, dim, out);
+  return LAUNCH_OK();
+}
+int hxa_quantize_launch(const float *W, int N, int K, int fmt, void *q, hxa_h *s, hipStream_t st) {
+  if (K % 32 || (fmt != HXA_W_Q8 && fmt != HXA_W_Q4)) return HXA_E_ARG;
+  hipLaunchKernelGGL(quantize_kernel, dim3(nblk((long)N * (K / 32))), dim3(256), 0, st, W, N, K, fmt, q, s);
+  return LAUNCH_OK();
+}

@@ -1,0 +1,390 @@
+// Weight-only-quantised / fp16 GEMM for gfx950: O[M][N] = A[M][K] . W[N][K]^T with fused epilogues.
+//
+// Replaces the reference's HMX GEMM engine (hexagon/mega/gemm2.c:96-137, gemm_run_geo) including its q8 tile
+// dequantisation (gemm2.c:19-35 dq_tile), the MOSS q4a dequantisation (moss/hexagon/mega/gemm2.c:39-56) and the
+// flush epilogues (gemm2.c:58-82: gated residual, GELU, split-K residual partial; moss mode 5 SiTU).
+//
+// Design (CDNA4, 64-wide waves):
+//  * 256 threads = 4 waves in a 2x2 grid; each wave owns a (BM/2)x(BN/2) sub-tile computed with
+//    v_mfma_f32_32x32x16_f16 (fp32 accumulate).
+//  * K is consumed in BK=64 steps; A and W tiles are staged in LDS (double buffered, rows padded to 144 B so the
+//    16-byte fragment reads of 32 consecutive rows fall in distinct banks). Global loads for step k+1 are issued
+//    before the MFMAs of step k.
+//  * int8 / int4 weights are dequantised on their way into LDS with the fp16 exponent-bias trick: a byte u placed
+//    under the exponent 0x64 is the fp16 value 1024+u, so (1024+u) - 1152 = q exactly, then one fp16 multiply by
+//    the group scale gives f16(q*s) -- the reference's exact dequantised value (gemm2.c:19-22).
+//  * The block index is remapped so each of the 8 XCDs (own L2) works on a contiguous range of output tiles.
+#include "hxa_common.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int BK = 64;
+constexpr int LDS_ROW = BK + 8;  // halves
+
+struct GemmParams {
+  const hxa_h *A;
+  long lda;
+  const void *W;
+  const hxa_h *S, *Z;
+  long ldw;  // elements per W row (fp16/int8: K; int4: bytes per row = K/2)
+  int M, N, Kslice, Ktot;
+  int epi;
+  hxa_h *out;
+  long ldo, out_zstride;
+  float *x;
+  long ldx;
+  const float *gate;
+  hxa_h *out_t;  // columns >= split_col go transposed to out_t[n - split_col][m]
+  long ldo_t;
+  int split_col;
+  int tiles_m, tiles_n;
+};
+
+HXA_DEV half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+HXA_DEV uint32_t as_u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// 4 int8 (two's complement, k-consecutive) -> 2 x half2 of f16(q*s)
+HXA_DEV void dq8_word(uint32_t d, half2_t s2, uint32_t &o0, uint32_t &o1) {
+  const uint32_t x = d ^ 0x80808080u;                         // offset binary u = q + 128
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);  // (0x64|u0, 0x64|u1) = 1024+u
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
+  const half2_t c = {(hxa_h)1152.0f, (hxa_h)1152.0f};
+  o0 = as_u((as_h2(lo) - c) * s2);
+  o1 = as_u((as_h2(hi) - c) * s2);
+}
+
+// 8 int4 of one 32-bit word -> 4 x half2
+template <bool ASYM>
+HXA_DEV void dq4_word(uint32_t d, half2_t s2, half2_t z2, uint32_t *o) {
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t v = ((d >> (4 * j)) & 0x000F000Fu) | 0x64006400u;  // (1024+n_{2j}, 1024+n_{2j+1})
+    if (ASYM) {
+      const half2_t c = {(hxa_h)1024.0f, (hxa_h)1024.0f};
+      o[j] = as_u(__builtin_elementwise_fma(as_h2(v) - c, s2, z2));
+    } else {
+      const half2_t c = {(hxa_h)1032.0f, (hxa_h)1032.0f};
+      o[j] = as_u((as_h2(v) - c) * s2);
+    }
+  }
+}
+
+HXA_DEV float gelu_tanh_f(float t) {
+  const float u = 0.7978845608028654f * (t + 0.044715f * t * t * t);
+  return 0.5f * t * (1.0f + tanhf(u));
+}
+HXA_DEV float gelu_erf_f(float t) {
+  // kern.c:248-260: f16(max(t,0) - T2(|t|)), T2 = f16(|t| * 0.5 * erfc(|t|/sqrt 2))
+  const float a = fabsf(t);
+  const float t2 = (float)(hxa_h)(a * 0.5f * erfcf(a * 0.7071067811865476f));
+  return fmaxf(t, 0.0f) - t2;
+}
+HXA_DEV float situ_f(float u, float g) {
+  // moss kern.c:376-405: f16(f16(25 tanh(u/25)) * f16(4 tanh(g/4) sigmoid(g)))
+  const float tu = (float)(hxa_h)(25.0f * tanhf(u * 0.04f));
+  const float gs = (float)(hxa_h)(4.0f * tanhf(g * 0.25f) / (1.0f + __expf(-g)));
+  return tu * gs;
+}
+
+template <int BM, int BN, int FMT, bool ASYM>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
+  constexpr int WTM = BM / 2, WTN = BN / 2, MI = WTM / 32, NI = WTN / 32;
+  constexpr int CA = BM / 32;                                   // 16-byte A chunks per thread per stage
+  constexpr int CB = FMT == HXA_W_F16 ? BN / 32 : FMT == HXA_W_Q8 ? BN / 64 : BN / 128;
+  static_assert(CB >= 1, "tile too narrow for this weight format");
+  extern __shared__ __attribute__((aligned(16))) hxa_h lds[];
+  hxa_h *const As0 = lds, *const Bs0 = lds + BM * LDS_ROW;
+  constexpr int STAGE = (BM + BN) * LDS_ROW;
+
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int bid = blockIdx.x;
+  const int tile = (ntiles % 8 == 0) ? (bid % 8) * (ntiles / 8) + bid / 8 : bid;
+  const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int z = blockIdx.z;
+  const int kbase = z * p.Kslice;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+
+  float16_t acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < NI; j++) acc[i][j] = (float16_t){};
+
+  uint4_t ra[CA];
+  uint4_t rb[CB];
+  hxa_h rs[CB], rz[CB];
+
+  auto load = [&](int kt) {
+    const int k0 = kbase + kt * BK;
+#pragma unroll
+    for (int i = 0; i < CA; i++) {
+      const int c = tid + i * 256, r = c >> 3, cc = c & 7;
+      const int m = m0 + r;
+      ra[i] = m < p.M ? *(const uint4_t *)(p.A + (long)m * p.lda + k0 + cc * 8) : (uint4_t){0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < CB; i++) {
+      const int c = tid + i * 256;
+      if (FMT == HXA_W_F16) {
+        const int r = c >> 3, cc = c & 7, n = n0 + r;
+        rb[i] = n < p.N ? *(const uint4_t *)((const hxa_h *)p.W + (long)n * p.ldw + k0 + cc * 8) : (uint4_t){0, 0, 0, 0};
+      } else if (FMT == HXA_W_Q8) {
+        const int r = c >> 2, cc = c & 3, n = n0 + r;
+        const int kk = k0 + cc * 16;
+        rb[i] = n < p.N ? *(const uint4_t *)((const int8_t *)p.W + (long)n * p.ldw + kk) : (uint4_t){0, 0, 0, 0};
+        rs[i] = n < p.N ? p.S[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
+      } else {
+        const int r = c >> 1, cc = c & 1, n = n0 + r;
+        const int kk = k0 + cc * 32;
+        rb[i] = n < p.N ? *(const uint4_t *)((const uint8_t *)p.W + (long)n * p.ldw + (kk >> 1)) : (uint4_t){0, 0, 0, 0};
+        rs[i] = n < p.N ? p.S[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
+        if (ASYM) rz[i] = n < p.N ? p.Z[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
+      }
+    }
+  };
+  auto store = [&](int buf) {
+    hxa_h *As = As0 + buf * STAGE, *Bs = Bs0 + buf * STAGE;
+#pragma unroll
+    for (int i = 0; i < CA; i++) {
+      const int c = tid + i * 256, r = c >> 3, cc = c & 7;
+      *(uint4_t *)(As + r * LDS_ROW + cc * 8) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < CB; i++) {
+      const int c = tid + i * 256;
+      if (FMT == HXA_W_F16) {
+        const int r = c >> 3, cc = c & 7;
+        *(uint4_t *)(Bs + r * LDS_ROW + cc * 8) = rb[i];
+      } else if (FMT == HXA_W_Q8) {
+        const int r = c >> 2, cc = c & 3;
+        const half2_t s2 = {rs[i], rs[i]};
+        uint32_t o[8];
+        dq8_word(rb[i].x, s2, o[0], o[1]);
+        dq8_word(rb[i].y, s2, o[2], o[3]);
+        dq8_word(rb[i].z, s2, o[4], o[5]);
+        dq8_word(rb[i].w, s2, o[6], o[7]);
+        *(uint4_t *)(Bs + r * LDS_ROW + cc * 16) = (uint4_t){o[0], o[1], o[2], o[3]};
+        *(uint4_t *)(Bs + r * LDS_ROW + cc * 16 + 8) = (uint4_t){o[4], o[5], o[6], o[7]};
+      } else {
+        const int r = c >> 1, cc = c & 1;
+        const half2_t s2 = {rs[i], rs[i]};
+        const half2_t z2 = ASYM ? (half2_t){rz[i], rz[i]} : (half2_t){};
+        uint32_t o[16];
+        dq4_word<ASYM>(rb[i].x, s2, z2, o + 0);
+        dq4_word<ASYM>(rb[i].y, s2, z2, o + 4);
+        dq4_word<ASYM>(rb[i].z, s2, z2, o + 8);
+        dq4_word<ASYM>(rb[i].w, s2, z2, o + 12);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          *(uint4_t *)(Bs + r * LDS_ROW + cc * 32 + q * 8) = (uint4_t){o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+      }
+    }
+  };
+  auto compute = [&](int buf) {
+    const hxa_h *As = As0 + buf * STAGE, *Bs = Bs0 + buf * STAGE;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ks++) {
+      half8_t a[MI], b[NI];
+      const int col = ks * 16 + (lane >> 5) * 8;
+#pragma unroll
+      for (int i = 0; i < MI; i++) a[i] = *(const half8_t *)(As + (wm * WTM + i * 32 + (lane & 31)) * LDS_ROW + col);
+#pragma unroll
+      for (int j = 0; j < NI; j++) b[j] = *(const half8_t *)(Bs + (wn * WTN + j * 32 + (lane & 31)) * LDS_ROW + col);
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NI; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int nk = p.Kslice / BK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt++) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) load(kt + 1);
+    compute(cur);
+    if (kt + 1 < nk) store(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + (r%4) of each 32x32 block ----
+  const int rbase = m0 + wm * WTM + 4 * (lane >> 5);
+  const int cbase = n0 + wn * WTN + (lane & 31);
+  if (p.epi == HXA_EPI_SITU) {
+    // wave columns [n0 + wn*WTN, +WTN) hold NI/2 (up, gate) block pairs
+    const int pair0 = (n0 + wn * WTN) / 64;
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+      for (int jp = 0; jp < NI / 2; jp++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int row = rbase + i * 32 + 8 * (r >> 2) + (r & 3);
+          const int col = (pair0 + jp) * 32 + (lane & 31);
+          if (row < p.M && col * 2 < p.N) {
+            const float u = (float)(hxa_h)acc[i][2 * jp][r], g = (float)(hxa_h)acc[i][2 * jp + 1][r];
+            p.out[(long)row * p.ldo + col] = (hxa_h)situ_f(u, g);
+          }
+        }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < NI; j++) {
+      const int col = cbase + j * 32;
+      if (col >= p.N) continue;
+      if (p.out_t != nullptr && col >= p.split_col) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; r4++) {
+          const int row = rbase + i * 32 + 8 * r4;
+          hxa_h *dst = p.out_t + (long)(col - p.split_col) * p.ldo_t + row;
+          if (row + 3 < p.M) {
+            const half4_t v = {(hxa_h)acc[i][j][4 * r4], (hxa_h)acc[i][j][4 * r4 + 1], (hxa_h)acc[i][j][4 * r4 + 2], (hxa_h)acc[i][j][4 * r4 + 3]};
+            *(half4_t *)dst = v;
+          } else {
+            for (int e = 0; e < 4; e++)
+              if (row + e < p.M) dst[e] = (hxa_h)acc[i][j][4 * r4 + e];
+          }
+        }
+        continue;
+      }
+      const float g = p.epi == HXA_EPI_RESADD ? p.gate[col] : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = rbase + i * 32 + 8 * (r >> 2) + (r & 3);
+        if (row >= p.M) continue;
+        const hxa_h t = (hxa_h)acc[i][j][r];
+        switch (p.epi) {
+          case HXA_EPI_STORE: p.out[(long)row * p.ldo + col] = t; break;
+          case HXA_EPI_GELU_TANH: p.out[(long)row * p.ldo + col] = (hxa_h)gelu_tanh_f((float)t); break;
+          case HXA_EPI_GELU_ERF: p.out[(long)row * p.ldo + col] = (hxa_h)gelu_erf_f((float)t); break;
+          case HXA_EPI_RESADD: {
+            float *xp = p.x + (long)row * p.ldx + col;
+            *xp = fmaf(g, (float)t, *xp);
+          } break;
+          case HXA_EPI_PARTIAL: p.out[(long)z * p.out_zstride + (long)row * p.ldo + col] = t; break;
+          default: break;
+        }
+      }
+    }
+}
+
+struct TileCfg {
+  int bm, bn;
+};
+constexpr TileCfg kCfgs[] = {{256, 128}, {128, 256}, {128, 128}, {64, 128}, {128, 64}};
+
+template <int BM, int BN, int FMT, bool ASYM>
+hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
+  auto kern = gemm_kernel<BM, BN, FMT, ASYM>;
+  const int lds = 2 * (BM + BN) * LDS_ROW * (int)sizeof(hxa_h);
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  dim3 grid(p.tiles_m * p.tiles_n, 1, ksplit);
+  hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, p);
+  return hipGetLastError();
+}
+
+template <int FMT, bool ASYM>
+hipError_t launch_fmt(int bm, int bn, const GemmParams &p, int ksplit, hipStream_t st) {
+  if (bm == 256 && bn == 128) return launch_t<256, 128, FMT, ASYM>(p, ksplit, st);
+  if (bm == 128 && bn == 256) return launch_t<128, 256, FMT, ASYM>(p, ksplit, st);
+  if (bm == 128 && bn == 128) return launch_t<128, 128, FMT, ASYM>(p, ksplit, st);
+  if (bm == 64 && bn == 128) return launch_t<64, 128, FMT, ASYM>(p, ksplit, st);
+  if constexpr (FMT != HXA_W_Q4) {
+    if (bm == 128 && bn == 64) return launch_t<128, 64, FMT, ASYM>(p, ksplit, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+int g_num_cu = 0;
+
+}  // namespace
+
+// Choose a tile shape: best wave-quantisation efficiency over the GPU's CUs, ties to the larger tile.
+static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int *bm, int *bn) {
+  if (g_num_cu == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    hipDeviceProp_t prop;
+    g_num_cu = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 256;
+  }
+  double best = -1.0;
+  for (const TileCfg &c : kCfgs) {
+    if (fmt == HXA_W_Q4 && c.bn < 128) continue;
+    if (epi == HXA_EPI_SITU && c.bn < 128) continue;
+    const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ksplit;
+    const long waves = (tiles + g_num_cu - 1) / g_num_cu;
+    const double useful = (double)M * N / ((double)((M + c.bm - 1) / c.bm) * c.bm * ((N + c.bn - 1) / c.bn) * c.bn);
+    const double eff = useful * (double)tiles / (double)(waves * g_num_cu) * (c.bm * c.bn >= 128 * 128 ? 1.0 : 0.8);
+    if (eff > best + 1e-9) {
+      best = eff;
+      *bm = c.bm;
+      *bn = c.bn;
+    }
+  }
+}
+
+int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
+  const HxaWeight &w = *g.w;
+  if (g.M <= 0 || w.N <= 0 || w.K <= 0 || g.ksplit < 1) return HXA_E_ARG;
+  if (w.K % (BK * g.ksplit) != 0) return HXA_E_ARG;
+  if (w.fmt != HXA_W_F16 && w.s == nullptr) return HXA_E_ARG;
+  if (g.epi == HXA_EPI_SITU && (w.N % 64) != 0) return HXA_E_ARG;
+  if ((g.lda % 8) != 0 || ((uintptr_t)g.A % 16) != 0 || ((uintptr_t)w.w % 16) != 0) return HXA_E_ARG;
+  GemmParams p{};
+  if (g.epi == HXA_EPI_STORE_T) {  // all columns transposed
+    p.out_t = g.out;
+    p.ldo_t = g.ldo;
+    p.split_col = 0;
+  } else if (g.epi == HXA_EPI_STORE && g.out_t != nullptr) {  // fused projections: the tail columns transposed
+    if (g.split_col % 32 != 0 || g.split_col < 0 || g.split_col > w.N) return HXA_E_ARG;
+    p.out_t = g.out_t;
+    p.ldo_t = g.ldo_t;
+    p.split_col = g.split_col;
+  }
+  if (p.out_t != nullptr && ((p.ldo_t % 4) != 0 || ((uintptr_t)p.out_t % 8) != 0)) return HXA_E_ARG;
+  p.A = g.A;
+  p.lda = g.lda;
+  p.W = w.w;
+  p.S = w.s;
+  p.Z = w.z;
+  p.ldw = w.fmt == HXA_W_Q4 ? w.K / 2 : w.K;
+  p.M = g.M;
+  p.N = w.N;
+  p.Ktot = w.K;
+  p.Kslice = w.K / g.ksplit;
+  p.epi = g.epi;
+  p.out = g.epi == HXA_EPI_STORE_T ? nullptr : g.out;
+  p.ldo = g.ldo;
+  p.out_zstride = g.out_zstride;
+  p.x = g.x;
+  p.ldx = g.ldx;
+  p.gate = g.gate;
+  int bm = 128, bn = 128;
+  pick_tile(g.M, w.N, g.ksplit, w.fmt, g.epi, &bm, &bn);
+  if (g.force_bm) {
+    bm = g.force_bm;
+    bn = g.force_bn;
+    if ((g.epi == HXA_EPI_SITU || w.fmt == HXA_W_Q4) && bn < 128) return HXA_E_ARG;  // needs >= 2 column blocks per wave
+  }
+  p.tiles_m = (g.M + bm - 1) / bm;
+  p.tiles_n = (w.N + bn - 1) / bn;
+  hipError_t e;
+  if (w.fmt == HXA_W_F16) e = launch_fmt<HXA_W_F16, false>(bm, bn, p, g.ksplit, st);
+  else if (w.fmt == HXA_W_Q8) e = launch_fmt<HXA_W_Q8, false>(bm, bn, p, g.ksplit, st);
+  else if (w.z) e = launch_fmt<HXA_W_Q4, true>(bm, bn, p, g.ksplit, st);
+  else e = launch_fmt<HXA_W_Q4, false>(bm, bn, p, g.ksplit, st);
+  return e == hipSuccess ? HXA_OK : HXA_E_HIP;
+}

@@ -1,0 +1,70 @@
+// Internal launch interface of the HIP kernels (device pointers; not part of the public C-ABI).
+#pragma once
+#include "hxa_common.h"
+
+struct HxaGemm {
+  const hxa_h *A;     // [M][lda] fp16
+  long lda;
+  int M;
+  const HxaWeight *w; // W[N][K] in one of the HXA_W_* formats
+  int ksplit;         // split-K slices (HXA_EPI_PARTIAL only)
+  int epi;            // HXA_EPI_*
+  hxa_h *out;         // STORE / GELU / PARTIAL / SITU: [M][ldo]; STORE_T: [N][ldo]; QKV: q/k part
+  long ldo, out_zstride;
+  float *x;           // RESADD: x[M][ldx] fp32
+  long ldx;
+  const float *gate;  // RESADD: gate[N]
+  hxa_h *out_t;       // QKV/KV split: columns >= split_col are written transposed to out_t[n - split_col][m]
+  long ldo_t;
+  int split_col;
+  int force_bm, force_bn;  // 0 = automatic tile choice
+};
+int hxa_gemm_launch(const HxaGemm &g, hipStream_t st);
+
+struct HxaAttn {
+  const hxa_h *q, *k, *vt;  // q [T][ldq], k [NKV][ldk] (head h at column h*128); vt [H*128][ldvt] (keys contiguous)
+  long ldq, ldk, ldvt;
+  hxa_h *o;                 // [T][ldo]
+  long ldo;
+  int T, NKV, nvalid, H, batch;
+  long q_bstride, k_bstride, vt_bstride, o_bstride;  // per-image offsets (elements)
+};
+int hxa_attn_launch(const HxaAttn &p, hipStream_t st);
+
+// h[t][:] = f16(norm(x[t][:]) * mul + add); LN: (x-mu)*rsqrt(E[x^2]-mu^2+eps), RMS (w != NULL): x*rsqrt(E[x^2]+eps)
+// with mul = (1 + scale) (LN) or (1 + scale) * w (RMS), add = shift.
+int hxa_norm_mod_launch(const float *x, long ldx, int T, int D, const float *shift, const float *scale, const float *w,
+                        float eps, hxa_h *h, long ldh, hipStream_t st);
+// per-head RMSNorm * gain (+ RoPE on pairs (d, d+64)) in place for ntens tensors sharing a layout
+int hxa_rmsrope_launch(hxa_h *q0, hxa_h *q1, const float *g0, const float *g1, long ldq, int T, int H, const float *cosT,
+                       const float *sinT, int ttab, hipStream_t st);
+// x[t][c] += gate[c] * (t1 + t2)
+int hxa_resadd2_launch(float *x, long ldx, const hxa_h *t1, const hxa_h *t2, long ldt, int T, int D, const float *gate,
+                       hipStream_t st);
+
+// layout conversions between the reference's crouton tiles and row-major device buffers
+int hxa_x32_to_rows_launch(const float *tiles, float *x, int R, int C, hipStream_t st);
+int hxa_rows_to_x32_launch(const float *x, float *tiles, int R, int C, hipStream_t st);
+int hxa_h16_to_rows_launch(const hxa_h *tiles, hxa_h *a, long lda, int R, int C, hipStream_t st);
+int hxa_rows_to_h16_launch(const hxa_h *a, long lda, hxa_h *tiles, int R, int C, int transposed, hipStream_t st);
+int hxa_cs_to_rows_launch(const float *tiles, float *rows, int T, hipStream_t st);  // [slab][2][32][32] -> [T][64]
+
+// synthetic data (counter-based hash RNG; deterministic for a seed)
+int hxa_fill_normal_launch(void *dst, int dtype, size_t n, uint64_t seed, float mean, float std, hipStream_t st);
+int hxa_fill_uniform_int_launch(void *dst, int bits, size_t n, uint64_t seed, int lo, int hi, hipStream_t st);
+int hxa_fill_const_launch(void *dst, int dtype, size_t n, float v, hipStream_t st);
+
+// caller-side glue (phone/animad.cpp)
+int hxa_patchify_launch(const float *lat, int B, int Cc, int H, int W, float *tok, hipStream_t st);
+// M <= 8: GEMV (one wave per output; output index n -> n + gap for n >= split); M > 8: K <= 64 (patch embed)
+int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W, int N, float *y, long ldy, int act,
+                          const float *bias, int split, int gap, hipStream_t st);
+// final layer over B images of T image tokens (image b's rows start at b*xrows); dtp == NULL: lat = v,
+// else lat += (*dtp) * v (Euler step)
+int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale,
+                     const hxa_h *Wf, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st);
+int hxa_quantize_launch(const float *W, int N, int K, int fmt, void *q, hxa_h *s, hipStream_t st);
+int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t st);
+
+// matrix shapes of a GPU block pack (see hxa_pack_layout); returns the matrix count
+int hxa_pack_mats(int kind, int D, int F, int DC, int fa, int fm, int *N, int *K, int *fmt);

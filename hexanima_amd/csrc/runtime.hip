@@ -1,0 +1,842 @@
+// Host runtime of libhexanima_hip.so: device helpers, the kernel entry points of the C-ABI, GPU block packs,
+// the block orchestrator (hexagon/mega/blk.c:109-183 / moss/hexagon/mega/blk.c:234-259 restated for HIP),
+// the reference block ABI (mega_open / mega_block / mega_close + buffer registration) and the DiT runner.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/hexanima_hip.h"
+#include "hxa_common.h"
+#include "kernels.h"
+
+// ---------------------------------------------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------------------------------------------
+static thread_local char g_err[512];
+static int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+#define HIPC(x)                                                                                  \
+  do {                                                                                           \
+    hipError_t e__ = (x);                                                                        \
+    if (e__ != hipSuccess) return fail(HXA_E_HIP, "%s: %s (%s:%d)", #x, hipGetErrorString(e__), __FILE__, __LINE__); \
+  } while (0)
+#define TRY(x)                    \
+  do {                            \
+    int r__ = (x);                \
+    if (r__ != HXA_OK) {          \
+      if (!g_err[0]) fail(r__, "%s failed (%d)", #x, r__); \
+      return r__;                 \
+    }                             \
+  } while (0)
+
+static inline hipStream_t S(void *s) { return (hipStream_t)s; }
+static inline long al256(long x) { return (x + 255) & ~255L; }
+
+extern "C" const char *hxa_last_error(void) { return g_err; }
+extern "C" const char *hxa_version(void) { return "hexanima_hip 0.1 gfx950"; }
+
+// ---------------------------------------------------------------------------------------------------------------
+// device runtime
+// ---------------------------------------------------------------------------------------------------------------
+extern "C" int hxa_init(int device) {
+  g_err[0] = 0;
+  int n = 0;
+  HIPC(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(HXA_E_ARG, "device %d of %d", device, n);
+  HIPC(hipSetDevice(device));
+  HIPC(hipFree(nullptr));
+  return HXA_OK;
+}
+extern "C" int hxa_malloc(void **p, size_t bytes) {
+  *p = nullptr;
+  if (bytes == 0) return HXA_OK;
+  HIPC(hipMalloc(p, bytes));
+  return HXA_OK;
+}
+extern "C" int hxa_free(void *p) {
+  if (p) HIPC(hipFree(p));
+  return HXA_OK;
+}
+extern "C" int hxa_h2d(void *dst, const void *src, size_t bytes) {
+  HIPC(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return HXA_OK;
+}
+extern "C" int hxa_d2h(void *dst, const void *src, size_t bytes) {
+  HIPC(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return HXA_OK;
+}
+extern "C" int hxa_d2d(void *dst, const void *src, size_t bytes) {
+  HIPC(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+  return HXA_OK;
+}
+extern "C" int hxa_memset(void *p, int value, size_t bytes) {
+  HIPC(hipMemset(p, value, bytes));
+  return HXA_OK;
+}
+extern "C" int hxa_sync(void) {
+  HIPC(hipDeviceSynchronize());
+  return HXA_OK;
+}
+extern "C" int hxa_stream_create(void **stream) {
+  hipStream_t s;
+  HIPC(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *stream = s;
+  return HXA_OK;
+}
+extern "C" int hxa_stream_destroy(void *stream) {
+  HIPC(hipStreamDestroy(S(stream)));
+  return HXA_OK;
+}
+extern "C" int hxa_stream_sync(void *stream) {
+  HIPC(hipStreamSynchronize(S(stream)));
+  return HXA_OK;
+}
+extern "C" int hxa_event_create(void **ev) {
+  hipEvent_t e;
+  HIPC(hipEventCreate(&e));
+  *ev = e;
+  return HXA_OK;
+}
+extern "C" int hxa_event_destroy(void *ev) {
+  HIPC(hipEventDestroy((hipEvent_t)ev));
+  return HXA_OK;
+}
+extern "C" int hxa_event_record(void *ev, void *stream) {
+  HIPC(hipEventRecord((hipEvent_t)ev, S(stream)));
+  return HXA_OK;
+}
+extern "C" int hxa_event_elapsed_ms(void *a, void *b, float *ms) {
+  HIPC(hipEventSynchronize((hipEvent_t)b));
+  HIPC(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+  return HXA_OK;
+}
+extern "C" int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, char *name, int name_len) {
+  int dev = 0;
+  HIPC(hipGetDevice(&dev));
+  hipDeviceProp_t p;
+  HIPC(hipGetDeviceProperties(&p, dev));
+  if (num_cu) *num_cu = p.multiProcessorCount;
+  if (clock_khz) *clock_khz = p.clockRate;
+  if (mem_bytes) *mem_bytes = p.totalGlobalMem;
+  if (name && name_len > 0) snprintf(name, name_len, "%s %s", p.name, p.gcnArchName);
+  return HXA_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// kernel entry points
+// ---------------------------------------------------------------------------------------------------------------
+static int gemm_common(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
+                       int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx,
+                       const float *gate, void *out_t, long ldo_t, int split_col, int bm, int bn, void *stream) {
+  if (!A || !w) return fail(HXA_E_ARG, "gemm: null operand");
+  if (fmt < HXA_W_F16 || fmt > HXA_W_Q4) return fail(HXA_E_MODE, "gemm: format %d", fmt);
+  if (epi == HXA_EPI_RESADD ? (!x || !gate) : !out) return fail(HXA_E_ARG, "gemm: null output");
+  HxaWeight wt{fmt, N, K, w, (const hxa_h *)s, (const hxa_h *)z};
+  HxaGemm g{};
+  g.A = (const hxa_h *)A;
+  g.lda = lda;
+  g.M = M;
+  g.w = &wt;
+  g.ksplit = ksplit < 1 ? 1 : ksplit;
+  g.epi = epi;
+  g.out = (hxa_h *)out;
+  g.ldo = ldo;
+  g.out_zstride = out_zstride;
+  g.x = x;
+  g.ldx = ldx;
+  g.gate = gate;
+  g.out_t = (hxa_h *)out_t;
+  g.ldo_t = ldo_t;
+  g.split_col = split_col;
+  g.force_bm = bm;
+  g.force_bn = bn;
+  const int r = hxa_gemm_launch(g, S(stream));
+  if (r != HXA_OK) return fail(r, "gemm M=%d N=%d K=%d fmt=%d epi=%d ksplit=%d rejected (%d)", M, N, K, fmt, epi, ksplit, r);
+  return HXA_OK;
+}
+extern "C" int hxa_gemm(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
+                        int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
+                        void *out_t, long ldo_t, int split_col, void *stream) {
+  return gemm_common(A, lda, M, fmt, w, s, z, N, K, ksplit, epi, out, ldo, out_zstride, x, ldx, gate, out_t, ldo_t,
+                     split_col, 0, 0, stream);
+}
+extern "C" int hxa_gemm_tile(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N,
+                             int K, int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx,
+                             const float *gate, int bm, int bn, void *stream) {
+  return gemm_common(A, lda, M, fmt, w, s, z, N, K, ksplit, epi, out, ldo, out_zstride, x, ldx, gate, nullptr, 0, 0, bm,
+                     bn, stream);
+}
+extern "C" int hxa_attention(const void *q, long ldq, const void *k, long ldk, const void *vt, long ldvt, void *o, long ldo,
+                             int T, int NKV, int nvalid, int H, int batch, long qb, long kb, long vb, long ob,
+                             void *stream) {
+  HxaAttn p{(const hxa_h *)q, (const hxa_h *)k, (const hxa_h *)vt, ldq, ldk, ldvt, (hxa_h *)o, ldo, T, NKV, nvalid, H,
+            batch, qb, kb, vb, ob};
+  const int r = hxa_attn_launch(p, S(stream));
+  if (r != HXA_OK) return fail(r, "attention T=%d NKV=%d nvalid=%d H=%d rejected", T, NKV, nvalid, H);
+  return HXA_OK;
+}
+extern "C" int hxa_norm_mod(const float *x, long ldx, int T, int D, const float *shift, const float *scale,
+                            const float *w, float eps, void *h, long ldh, void *stream) {
+  const int r = hxa_norm_mod_launch(x, ldx, T, D, shift, scale, w, eps, (hxa_h *)h, ldh, S(stream));
+  if (r != HXA_OK) return fail(r, "norm_mod T=%d D=%d rejected", T, D);
+  return HXA_OK;
+}
+extern "C" int hxa_rmsrope(void *q0, void *q1, const float *g0, const float *g1, long ldq, int T, int H,
+                           const float *cosT, const float *sinT, int ttab, void *stream) {
+  const int r = hxa_rmsrope_launch((hxa_h *)q0, (hxa_h *)q1, g0, g1, ldq, T, H, cosT, sinT, ttab, S(stream));
+  if (r != HXA_OK) return fail(r, "rmsrope rejected");
+  return HXA_OK;
+}
+extern "C" int hxa_resadd2(float *x, long ldx, const void *t1, const void *t2, long ldt, int T, int D, const float *gate,
+                           void *stream) {
+  const int r = hxa_resadd2_launch(x, ldx, (const hxa_h *)t1, (const hxa_h *)t2, ldt, T, D, gate, S(stream));
+  if (r != HXA_OK) return fail(r, "resadd2 rejected");
+  return HXA_OK;
+}
+extern "C" int hxa_fill_normal(void *dst, int dtype, size_t n, uint64_t seed, float mean, float std, void *stream) {
+  return hxa_fill_normal_launch(dst, dtype, n, seed, mean, std, S(stream));
+}
+extern "C" int hxa_fill_uniform_int(void *dst, int bits, size_t n, uint64_t seed, int lo, int hi, void *stream) {
+  return hxa_fill_uniform_int_launch(dst, bits, n, seed, lo, hi, S(stream));
+}
+extern "C" int hxa_fill_const(void *dst, int dtype, size_t n, float v, void *stream) {
+  return hxa_fill_const_launch(dst, dtype, n, v, S(stream));
+}
+extern "C" int hxa_quantize(const float *W, int N, int K, int fmt, void *q, void *s, void *stream) {
+  const int r = hxa_quantize_launch(W, N, K, fmt, q, (hxa_h *)s, S(stream));
+  if (r != HXA_OK) return fail(r, "quantize rejected");
+  return HXA_OK;
+}
+extern "C" int hxa_x32_to_rows(const float *tiles, float *x, int R, int C, void *stream) {
+  return hxa_x32_to_rows_launch(tiles, x, R, C, S(stream));
+}
+extern "C" int hxa_rows_to_x32(const float *x, float *tiles, int R, int C, void *stream) {
+  return hxa_rows_to_x32_launch(x, tiles, R, C, S(stream));
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// GPU block packs
+// ---------------------------------------------------------------------------------------------------------------
+struct MatSpec {
+  int N, K, fmt;
+};
+static void pack_mats(int kind, int D, int F, int DC, int fa, int fm, std::vector<MatSpec> &m) {
+  m.clear();
+  if (kind == 0) m = {{3 * D, D, fa}, {D, D, fa}, {D, D, fa}, {2 * D, DC, fa}, {D, D, fa}, {F, D, fm}, {D, F, fm}};
+  else m = {{3 * D, D, fa}, {D, D, fa}, {2 * F, D, fm}, {D, F, fm}};
+}
+int hxa_pack_mats(int kind, int D, int F, int DC, int fa, int fm, int *N, int *K, int *fmt) {
+  std::vector<MatSpec> m;
+  pack_mats(kind, D, F, DC, fa, fm, m);
+  for (size_t i = 0; i < m.size(); i++) {
+    N[i] = m[i].N;
+    K[i] = m[i].K;
+    fmt[i] = m[i].fmt;
+  }
+  return (int)m.size();
+}
+static long wbytes(const MatSpec &m) {
+  return m.fmt == HXA_W_F16 ? 2L * m.N * m.K : m.fmt == HXA_W_Q8 ? (long)m.N * m.K : (long)m.N * m.K / 2;
+}
+extern "C" long hxa_pack_layout(int kind, int D, int F, int DC, int fa, int fm, long *offs, int noffs) {
+  std::vector<MatSpec> mats;
+  pack_mats(kind, D, F, DC, fa, fm, mats);
+  long off = 0;
+  int o = 0;
+  auto put = [&](long v) {
+    if (offs && o < noffs) offs[o] = v;
+    o++;
+  };
+  for (const MatSpec &m : mats) {
+    put(off);
+    off += al256(wbytes(m));
+    if (m.fmt != HXA_W_F16) {
+      put(off);
+      off += al256(2L * (m.K / 32) * m.N);
+    } else {
+      put(-1);
+    }
+    put(-1);
+  }
+  put(off);
+  off += al256(kind == 0 ? 4L * 4 * 128 : 4L * (256 + 2 * D));
+  return off;
+}
+struct PackView {
+  HxaWeight w[7];
+  int nmat;
+  const float *vec;
+};
+static PackView pack_view(const hxa_block_dims *d, const void *pack) {
+  std::vector<MatSpec> mats;
+  pack_mats(d->kind, d->D, d->F, d->DC, d->fmt_attn, d->fmt_mlp, mats);
+  long offs[32];
+  hxa_pack_layout(d->kind, d->D, d->F, d->DC, d->fmt_attn, d->fmt_mlp, offs, 32);
+  PackView v{};
+  v.nmat = (int)mats.size();
+  const char *b = (const char *)pack;
+  for (int i = 0; i < v.nmat; i++) {
+    v.w[i] = HxaWeight{mats[i].fmt, mats[i].N, mats[i].K, b + offs[3 * i],
+                       offs[3 * i + 1] >= 0 ? (const hxa_h *)(b + offs[3 * i + 1]) : nullptr, nullptr};
+  }
+  v.vec = (const float *)(b + offs[3 * v.nmat]);
+  return v;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// block workspace + orchestrator
+// ---------------------------------------------------------------------------------------------------------------
+enum { WS_H, WS_Q, WS_K, WS_VT, WS_O, WS_T1, WS_MID, WS_CK, WS_CVT, WS_T2, WS_N };
+struct WsLayout {
+  long off[WS_N];
+  long ld[WS_N];
+  long total;
+};
+static WsLayout ws_layout(const hxa_block_dims *d) {
+  const long BT = (long)d->batch * d->T, BC = (long)d->batch * d->C, D = d->D;
+  WsLayout L{};
+  long off = 0;
+  auto put = [&](int id, long bytes, long ld) {
+    L.off[id] = off;
+    L.ld[id] = ld;
+    off += al256(bytes);
+  };
+  put(WS_H, 2 * BT * D, D);
+  put(WS_Q, 2 * BT * 2 * D, 2 * D);  // q | k interleaved per row
+  L.off[WS_K] = L.off[WS_Q] + 2 * D;  // byte offset of k inside the q|k rows
+  L.ld[WS_K] = 2 * D;
+  put(WS_VT, 2 * D * BT, BT);
+  put(WS_O, 2 * BT * D, D);
+  put(WS_T1, 2 * 2 * BT * D, D);  // two split-K partials
+  L.off[WS_T2] = L.off[WS_T1] + 2 * BT * D;
+  L.ld[WS_T2] = D;
+  put(WS_MID, 2 * BT * (long)d->F, d->F);
+  if (d->kind == 0) {
+    put(WS_CK, 2 * BC * D, D);
+    put(WS_CVT, 2 * D * BC, BC);
+  } else {
+    L.off[WS_CK] = L.off[WS_CVT] = 0;
+    L.ld[WS_CK] = L.ld[WS_CVT] = 0;
+  }
+  L.total = off;
+  return L;
+}
+extern "C" long hxa_block_ws_bytes(const hxa_block_dims *d) { return ws_layout(d).total; }
+extern "C" void *hxa_block_ws_buf(const hxa_block_dims *d, void *ws, int which, long *ld) {
+  if (which < 0 || which >= WS_N) return nullptr;
+  const WsLayout L = ws_layout(d);
+  if (ld) *ld = L.ld[which];
+  return (char *)ws + L.off[which];
+}
+
+static int check_dims(const hxa_block_dims *d) {
+  if (d->kind != 0 && d->kind != 1) return fail(HXA_E_MODE, "block kind %d", d->kind);
+  if (d->D % 256 || d->H * 128 != d->D || d->T <= 0 || d->T % 32 || d->batch < 1 || d->F % 128)
+    return fail(HXA_E_ARG, "block dims D=%d H=%d F=%d T=%d batch=%d", d->D, d->H, d->F, d->T, d->batch);
+  if (d->kind == 0 && (d->C <= 0 || d->C % 32 || d->DC % 64)) return fail(HXA_E_ARG, "context C=%d DC=%d", d->C, d->DC);
+  if (d->kind == 1 && (d->nvalid < 1 || d->nvalid > d->T)) return fail(HXA_E_ARG, "nvalid %d", d->nvalid);
+  return HXA_OK;
+}
+
+struct StageTimer {
+  int *us;
+  int n;
+  hipStream_t st;
+  std::vector<hipEvent_t> ev;
+  int count = 0;
+  StageTimer(int *u, int nn, hipStream_t s) : us(u), n(nn), st(s) {
+    if (us) {
+      ev.resize(n + 1);
+      for (auto &e : ev) (void)hipEventCreate(&e);
+      (void)hipEventRecord(ev[0], st);
+    }
+  }
+  void tick() {
+    count++;
+    if (us && count <= n) (void)hipEventRecord(ev[count], st);
+  }
+  ~StageTimer() {
+    if (!us) return;
+    (void)hipStreamSynchronize(st);
+    for (int i = 0; i < n; i++) {
+      float ms = 0.0f;
+      if (i < count && hipEventElapsedTime(&ms, ev[i], ev[i + 1]) == hipSuccess) us[i] = (int)lrintf(ms * 1000.0f);
+      else us[i] = 0;
+    }
+    for (auto &e : ev) (void)hipEventDestroy(e);
+  }
+};
+
+// One block; stage numbering follows the reference TICK() order (blk.c:136).
+extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
+                             const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
+                             void *stream) {
+  g_err[0] = 0;
+  TRY(check_dims(d));
+  if (!pack || !x || !mod || !ws || (d->kind == 0 && !ctx)) return fail(HXA_E_ARG, "block: null pointer");
+  hipStream_t st = S(stream);
+  const PackView pv = pack_view(d, pack);
+  const WsLayout L = ws_layout(d);
+  char *w8 = (char *)ws;
+  hxa_h *h = (hxa_h *)(w8 + L.off[WS_H]), *qk = (hxa_h *)(w8 + L.off[WS_Q]), *k = (hxa_h *)(w8 + L.off[WS_K]);
+  hxa_h *vT = (hxa_h *)(w8 + L.off[WS_VT]), *o = (hxa_h *)(w8 + L.off[WS_O]), *t1 = (hxa_h *)(w8 + L.off[WS_T1]);
+  hxa_h *t2 = (hxa_h *)(w8 + L.off[WS_T2]), *mid = (hxa_h *)(w8 + L.off[WS_MID]);
+  const int D = d->D, H = d->H, T = d->T, B = d->batch, F = d->F;
+  const int BT = B * T;
+  const long ldqk = 2L * D;
+  StageTimer tm(stage_us, nstage, st);
+  int stage = 0;
+#define STAGE_DONE()                              \
+  do {                                            \
+    tm.tick();                                    \
+    if (stop && ++stage >= stop) return HXA_OK;   \
+    if (!stop) ++stage;                           \
+  } while (0)
+  auto gemm = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
+                  const float *gate, hxa_h *out_t, long ldo_t, int split, int ksplit, long zstride) -> int {
+    HxaGemm g{};
+    g.A = A;
+    g.lda = lda;
+    g.M = M;
+    g.w = &w;
+    g.ksplit = ksplit;
+    g.epi = epi;
+    g.out = out;
+    g.ldo = ldo;
+    g.out_zstride = zstride;
+    g.x = xx;
+    g.ldx = D;
+    g.gate = gate;
+    g.out_t = out_t;
+    g.ldo_t = ldo_t;
+    g.split_col = split;
+    const int r = hxa_gemm_launch(g, st);
+    if (r != HXA_OK) return fail(r, "block gemm N=%d K=%d epi=%d rejected", w.N, w.K, epi);
+    return HXA_OK;
+  };
+  auto attn = [&](const hxa_h *q, const hxa_h *kk, long ldk, const hxa_h *vt, long ldvt, int NKV, int nvalid, long kb,
+                  long vb) -> int {
+    HxaAttn p{q, kk, vt, ldqk, ldk, ldvt, o, D, T, NKV, nvalid, H, B, (long)T * ldqk, kb, vb, (long)T * D};
+    const int r = hxa_attn_launch(p, st);
+    if (r != HXA_OK) return fail(r, "block attention rejected");
+    return HXA_OK;
+  };
+
+  if (d->kind == 0) {
+    const float *gain = pv.vec;
+    const HxaWeight &Wqkv = pv.w[0], &Wo = pv.w[1], &Wcq = pv.w[2], &Wckv = pv.w[3], &Wco = pv.w[4], &W1 = pv.w[5],
+                    &W2 = pv.w[6];
+    const int BC = B * d->C;
+    hxa_h *ck = (hxa_h *)(w8 + L.off[WS_CK]), *cvT = (hxa_h *)(w8 + L.off[WS_CVT]);
+    // site 0: self-attention (blk.c:157-162)
+    TRY(hxa_norm_mod_launch(x, D, BT, D, mod, mod + D, nullptr, 1e-6f, h, D, st));
+    STAGE_DONE();
+    TRY(gemm(h, D, BT, Wqkv, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
+    STAGE_DONE();
+    TRY(hxa_rmsrope_launch(qk, k, gain, gain + 128, ldqk, BT, H, cosT, sinT, T, st));
+    STAGE_DONE();
+    TRY(attn(qk, k, ldqk, vT, BT, T, T, (long)T * ldqk, T));
+    STAGE_DONE();
+    TRY(gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
+    STAGE_DONE();
+    // site 1: cross-attention (blk.c:163-169)
+    TRY(hxa_norm_mod_launch(x, D, BT, D, mod + 3 * D, mod + 4 * D, nullptr, 1e-6f, h, D, st));
+    STAGE_DONE();
+    TRY(gemm(h, D, BT, Wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    TRY(gemm((const hxa_h *)ctx, d->DC, BC, Wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0));
+    STAGE_DONE();
+    TRY(hxa_rmsrope_launch(qk, nullptr, gain + 256, nullptr, ldqk, BT, H, nullptr, nullptr, 0, st));
+    TRY(hxa_rmsrope_launch(ck, nullptr, gain + 384, nullptr, D, BC, H, nullptr, nullptr, 0, st));
+    STAGE_DONE();
+    TRY(attn(qk, ck, D, cvT, BC, d->C, d->C, (long)d->C * D, d->C));
+    STAGE_DONE();
+    TRY(gemm(o, D, BT, Wco, HXA_EPI_RESADD, nullptr, 0, x, mod + 5 * D, nullptr, 0, 0, 1, 0));
+    STAGE_DONE();
+    // site 2: MLP (blk.c:170-174)
+    TRY(hxa_norm_mod_launch(x, D, BT, D, mod + 6 * D, mod + 7 * D, nullptr, 1e-6f, h, D, st));
+    STAGE_DONE();
+    TRY(gemm(h, D, BT, W1, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    STAGE_DONE();
+    TRY(gemm(mid, F, BT, W2, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
+    TRY(hxa_resadd2_launch(x, D, t1, t2, D, BT, D, mod + 8 * D, st));
+    STAGE_DONE();
+  } else {
+    const float *gq = pv.vec, *gk = pv.vec + 128, *n1 = pv.vec + 256, *n2 = pv.vec + 256 + D;
+    const HxaWeight &Wqkv = pv.w[0], &Wo = pv.w[1], &Wug = pv.w[2], &Wdn = pv.w[3];
+    // attention half (moss blk.c:234-247)
+    TRY(hxa_norm_mod_launch(x, D, BT, D, mod, mod + D, n1, 1e-6f, h, D, st));
+    STAGE_DONE();
+    STAGE_DONE();  // the reference's LoRA-A GEMM stage (no LoRA)
+    TRY(gemm(h, D, BT, Wqkv, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
+    TRY(hxa_rmsrope_launch(qk, k, gq, gk, ldqk, BT, H, cosT, sinT, T, st));
+    STAGE_DONE();
+    TRY(attn(qk, k, ldqk, vT, BT, T, d->nvalid, (long)T * ldqk, T));
+    STAGE_DONE();
+    TRY(gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
+    STAGE_DONE();
+    // FFN half (moss blk.c:248-259)
+    TRY(hxa_norm_mod_launch(x, D, BT, D, mod + 3 * D, mod + 4 * D, n2, 1e-6f, h, D, st));
+    STAGE_DONE();
+    TRY(gemm(h, D, BT, Wug, HXA_EPI_SITU, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    STAGE_DONE();
+    TRY(gemm(mid, F, BT, Wdn, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
+    TRY(hxa_resadd2_launch(x, D, t1, t2, D, BT, D, mod + 5 * D, st));
+    STAGE_DONE();
+  }
+#undef STAGE_DONE
+  return HXA_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// reference ABI: mega_open / mega_block / mega_close and buffer registration
+// ---------------------------------------------------------------------------------------------------------------
+namespace {
+// hexagon/mega/blk_meta.h:3-4
+enum { M_X = 0, M_CTX, M_MOD, M_GAIN, M_COS, M_SIN, M_WSQ, M_WSK, M_WSV, M_WSO, M_WCQ, M_WCK, M_WCV, M_WCO, M_WM1, M_WM2,
+       M_H, M_Q, M_K, M_V, M_O, M_T, M_MID, M_CK, M_CV, M_NTOK, M_NCTX, M_STOP, M_NW, M_REL, M_FIRST, M_Q8, M_NMETA };
+// moss/hexagon/mega/blk_meta.h:3-4 (prefix MM_)
+enum { MM_X = 0, MM_COS, MM_SIN, MM_H, MM_Q, MM_K, MM_V, MM_O, MM_T, MM_MID, MM_LQ, MM_LO, MM_LU, MM_LD, MM_NTOK,
+       MM_NVALID, MM_STOP, MM_NW, MM_REL, MM_FIRST, MM_MODE, MM_NCB, MM_FMT, MM_ROWS, MM_CS, MM_WOFF, MM_NMETA };
+constexpr int ANIMA_D = 2048, ANIMA_F = 8192, ANIMA_DC = 1024, TMAX = 6144;
+
+struct HostBuf {
+  void *ptr;
+  size_t bytes;
+  int kind;
+};
+struct DevBlock {  // a registered block's weights converted to a GPU pack
+  void *pack = nullptr;
+  hxa_block_dims dims{};
+  std::vector<int> key;  // meta offsets used for the conversion
+};
+struct Ctx {
+  hipStream_t st = nullptr;
+  std::map<int, HostBuf> bufs;
+  std::map<int, DevBlock> blocks;
+  // device-resident activations of the current run of blocks
+  float *x = nullptr, *cosr = nullptr, *sinr = nullptr, *mod = nullptr, *stage = nullptr;
+  hxa_h *ctx = nullptr;
+  void *ws = nullptr;
+  size_t x_bytes = 0, ctx_bytes = 0, cs_bytes = 0, sn_bytes = 0, mod_bytes = 0, ws_bytes = 0, stage_bytes = 0;
+  int cur_T = 0, cur_C = 0;
+};
+std::mutex g_ctx_mu;
+
+int ensure(void **p, size_t *have, size_t need) {
+  if (*have >= need && *p) return HXA_OK;
+  if (*p) (void)hipFree(*p);
+  *p = nullptr;
+  *have = 0;
+  HIPC(hipMalloc(p, need));
+  *have = need;
+  return HXA_OK;
+}
+
+// fp16 crouton weight tiles of matrix [K][N] ([nb][kb], tile rows = k) -> W[N][K] (export_all.py:7-8)
+void crouton_to_nk(const uint16_t *tiles, int N, int K, uint16_t *w) {
+  const int kb = K / 32;
+  for (int n = 0; n < N; n++)
+    for (int k = 0; k < K; k++) {
+      const int r = k & 31, c = n & 31;
+      w[(size_t)n * K + k] = tiles[((size_t)(n >> 5) * kb + (k >> 5)) * 1024 + (r >> 1) * 64 + c * 2 + (r & 1)];
+    }
+}
+// q8 records (export_all.py:10-18) -> int8 q[N][K] + s[K/32][N]; rows kofs.. of a record matrix with kbt k-blocks
+void q8rec_to_native(const uint8_t *rec, int N, int K, int kbt, uint8_t *q, uint16_t *s, int ncol_stride) {
+  const int kb = K / 32;
+  for (int jb = 0; jb < N / 32; jb++)
+    for (int ib = 0; ib < kb; ib++) {
+      const uint8_t *R = rec + ((size_t)jb * kbt + ib) * 1152;
+      const uint16_t *sv = (const uint16_t *)R;
+      for (int c = 0; c < 32; c++) {
+        const int n = jb * 32 + c;
+        s[(size_t)ib * ncol_stride + n] = sv[2 * c];
+        for (int r = 0; r < 32; r++) q[(size_t)n * K + ib * 32 + r] = (uint8_t)(R[128 + (r >> 1) * 64 + c * 2 + (r & 1)] ^ 0x80);
+      }
+    }
+}
+
+// Convert one registered Anima blkNN.bin (fixed D=2048 layout, blk_wlayout.h) into a GPU pack.
+int build_anima_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
+  const int D = ANIMA_D, F = ANIMA_F, DC = ANIMA_DC;
+  const bool q8 = meta[M_Q8] != 0;
+  const int fmt = q8 ? HXA_W_Q8 : HXA_W_F16;
+  db.dims = hxa_block_dims{0, D, D / 128, F, 0, DC, 0, 1, 0, fmt, fmt, 0};
+  long offs[32];
+  const long bytes = hxa_pack_layout(0, D, F, DC, fmt, fmt, offs, 32);
+  std::vector<uint8_t> host(bytes, 0);
+  // pack matrix order: qkv (q,k,v rows), o, cq, ckv (k,v rows), co, w1, w2
+  struct Src {
+    int meta_id, N, K, mat, row0;
+  };
+  const Src srcs[] = {{M_WSQ, D, D, 0, 0},     {M_WSK, D, D, 0, D},   {M_WSV, D, D, 0, 2 * D}, {M_WSO, D, D, 1, 0},
+                      {M_WCQ, D, D, 2, 0},     {M_WCK, D, DC, 3, 0},  {M_WCV, D, DC, 3, D},    {M_WCO, D, D, 4, 0},
+                      {M_WM1, F, D, 5, 0},     {M_WM2, D, F, 6, 0}};
+  const int matN[7] = {3 * D, D, D, 2 * D, D, F, D};
+  for (const Src &s : srcs) {
+    const size_t elems = (size_t)s.N * s.K;
+    const size_t need = q8 ? elems / 1024 * 1152 : elems * 2;
+    if (meta[s.meta_id] < 0 || (size_t)meta[s.meta_id] + need > hb.bytes) return fail(HXA_E_WEIGHTS, "weight offset out of range");
+    const uint8_t *src = (const uint8_t *)hb.ptr + meta[s.meta_id];
+    uint8_t *wdst = host.data() + offs[3 * s.mat];
+    if (!q8) {
+      crouton_to_nk((const uint16_t *)src, s.N, s.K, (uint16_t *)wdst + (size_t)s.row0 * s.K);
+    } else {
+      q8rec_to_native(src, s.N, s.K, s.K / 32, wdst + (size_t)s.row0 * s.K, (uint16_t *)(host.data() + offs[3 * s.mat + 1]) + s.row0,
+                      matN[s.mat]);
+    }
+  }
+  if (meta[M_GAIN] < 0 || (size_t)meta[M_GAIN] + 2048 > hb.bytes) return fail(HXA_E_WEIGHTS, "gain offset out of range");
+  memcpy(host.data() + offs[21], (const uint8_t *)hb.ptr + meta[M_GAIN], 2048);
+  void *dev = nullptr;
+  HIPC(hipMalloc(&dev, bytes));
+  HIPC(hipMemcpy(dev, host.data(), bytes, hipMemcpyHostToDevice));
+  db.pack = dev;
+  (void)c;
+  return HXA_OK;
+}
+
+// MOSS blkNN.bin (moss/export_moss.py:14-41, offsets moss blk_meta.h:6-17): q,k,v,o [3072+128][3072], up_gate
+// [3072+128][16384] (32-column blocks interleaved up/gate), down [8192+128][3072], LoRA A matrices, gains.
+// The LoRA rows are dropped (a pack without LoRA); gains: gq, gk, n1, n2.
+int build_moss_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
+  const int D = meta[MM_NCB] ? meta[MM_NCB] * 32 : 3072, F = 8192, fmt = HXA_W_Q8;
+  if (D != 3072) return fail(HXA_E_MODE, "moss pack: only the 3072-wide layout is defined");
+  const size_t W_Q = 0, W_K = 11059200, W_V = 22118400, W_O = 33177600, W_UG = 44236800, W_DN = 103219200,
+               W_GAIN = 135364608, W_TOTAL = 135397376;
+  const size_t base = (size_t)meta[MM_WOFF];
+  if (base + W_TOTAL > hb.bytes) return fail(HXA_E_WEIGHTS, "moss weights shorter than a block pack");
+  const uint8_t *b = (const uint8_t *)hb.ptr + base;
+  db.dims = hxa_block_dims{1, D, D / 128, F, 0, 0, 0, 1, 0, fmt, fmt, 0};
+  long offs[32];
+  const long bytes = hxa_pack_layout(1, D, F, 0, fmt, fmt, offs, 32);
+  std::vector<uint8_t> host(bytes, 0);
+  const int kbt = D / 32 + 4;  // LoRA B rows appended as 4 extra k blocks
+  q8rec_to_native(b + W_Q, D, D, kbt, host.data() + offs[0], (uint16_t *)(host.data() + offs[1]), 3 * D);
+  q8rec_to_native(b + W_K, D, D, kbt, host.data() + offs[0] + (size_t)D * D, (uint16_t *)(host.data() + offs[1]) + D, 3 * D);
+  q8rec_to_native(b + W_V, D, D, kbt, host.data() + offs[0] + (size_t)2 * D * D, (uint16_t *)(host.data() + offs[1]) + 2 * D, 3 * D);
+  q8rec_to_native(b + W_O, D, D, kbt, host.data() + offs[3], (uint16_t *)(host.data() + offs[4]), D);
+  q8rec_to_native(b + W_UG, 2 * F, D, kbt, host.data() + offs[6], (uint16_t *)(host.data() + offs[7]), 2 * F);
+  q8rec_to_native(b + W_DN, D, F, F / 32 + 4, host.data() + offs[9], (uint16_t *)(host.data() + offs[10]), D);
+  // gains: q/sqrt(128) [128], k [128], norm1 [3072], norm2 [3072] (export_moss.py gain vector)
+  memcpy(host.data() + offs[12], b + W_GAIN, 4L * (256 + 2 * D));
+  void *dev = nullptr;
+  HIPC(hipMalloc(&dev, bytes));
+  HIPC(hipMemcpy(dev, host.data(), bytes, hipMemcpyHostToDevice));
+  db.pack = dev;
+  (void)c;
+  return HXA_OK;
+}
+
+Ctx *ctx_of(remote_handle64 h) { return (Ctx *)(uintptr_t)h; }
+
+int blob_range(const HostBuf &b, long off, size_t bytes) { return off >= 0 && (size_t)off + bytes <= b.bytes; }
+}  // namespace
+
+extern "C" int mega_open(const char *uri, remote_handle64 *h) {
+  (void)uri;
+  g_err[0] = 0;
+  if (!h) return fail(HXA_E_ARG, "mega_open: null handle");
+  Ctx *c = new Ctx();
+  if (hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return fail(HXA_E_RESOURCE, "mega_open: no HIP device");
+  }
+  *h = (remote_handle64)(uintptr_t)c;
+  return HXA_OK;
+}
+
+extern "C" int mega_close(remote_handle64 h) {
+  Ctx *c = ctx_of(h);
+  if (!c) return HXA_OK;
+  (void)hipStreamSynchronize(c->st);
+  for (auto &kv : c->blocks) (void)hipFree(kv.second.pack);
+  for (void *p : {(void *)c->x, (void *)c->cosr, (void *)c->sinr, (void *)c->mod, (void *)c->ctx, c->ws, (void *)c->stage})
+    if (p) (void)hipFree(p);
+  (void)hipStreamDestroy(c->st);
+  delete c;
+  return HXA_OK;
+}
+
+extern "C" int hxa_register(remote_handle64 h, int fd, void *host_ptr, size_t bytes, int kind) {
+  Ctx *c = ctx_of(h);
+  if (!c || !host_ptr || bytes == 0) return fail(HXA_E_ARG, "hxa_register: bad arguments");
+  if (kind < 0 || kind > 2) return fail(HXA_E_MODE, "hxa_register: kind %d", kind);
+  auto it = c->blocks.find(fd);
+  if (it != c->blocks.end()) {  // re-registration invalidates the converted copy
+    (void)hipFree(it->second.pack);
+    c->blocks.erase(it);
+  }
+  c->bufs[fd] = HostBuf{host_ptr, bytes, kind};
+  return HXA_OK;
+}
+extern "C" int hxa_unregister(remote_handle64 h, int fd) {
+  Ctx *c = ctx_of(h);
+  if (!c) return fail(HXA_E_ARG, "hxa_unregister: bad handle");
+  (void)hipStreamSynchronize(c->st);
+  auto it = c->blocks.find(fd);
+  if (it != c->blocks.end()) {
+    (void)hipFree(it->second.pack);
+    c->blocks.erase(it);
+  }
+  c->bufs.erase(fd);
+  return HXA_OK;
+}
+
+// shared part of mega_block / mega_moss_block after the meta has been decoded
+namespace {
+struct BlockCall {
+  int kind, T, C, nvalid, stop, first, rel;
+  long off_x, off_ctx, off_cos, off_sin;
+  long off_stage[9];  // h, q, k, v, o, t, mid, ck, cv (blob byte offsets, -1 = none)
+};
+
+int run_ref_block(Ctx *c, const BlockCall &bc, const DevBlock &db, const HostBuf &blob, const float *modh, int modlen,
+                  int *times, int ntimes) {
+  const auto t_entry = std::chrono::steady_clock::now();
+  hipStream_t st = c->st;
+  hxa_block_dims d = db.dims;
+  d.T = bc.T;
+  d.C = bc.C;
+  d.batch = 1;
+  d.nvalid = bc.nvalid;
+  d.gelu = 0;  // the reference block uses the erf GELU table (kern.c:248-260)
+  const int D = d.D;
+  const size_t xb = (size_t)bc.T * D * 4;
+  if (!blob_range(blob, bc.off_x, xb) || !blob_range(blob, bc.off_cos, (size_t)bc.T * 256) ||
+      !blob_range(blob, bc.off_sin, (size_t)bc.T * 256))
+    return fail(HXA_E_META, "meta offsets outside the blob");
+  if (d.kind == 0 && !blob_range(blob, bc.off_ctx, (size_t)bc.C * d.DC * 2)) return fail(HXA_E_META, "ctx outside the blob");
+  if (modlen < (d.kind == 0 ? 9 : 6) * D * 4) return fail(HXA_E_META, "modlen %d too short", modlen);
+  TRY(ensure((void **)&c->x, &c->x_bytes, xb));
+  TRY(ensure((void **)&c->cosr, &c->cs_bytes, (size_t)bc.T * 64 * 4));
+  TRY(ensure((void **)&c->sinr, &c->sn_bytes, (size_t)bc.T * 64 * 4));
+  TRY(ensure((void **)&c->mod, &c->mod_bytes, (size_t)9 * D * 4));
+  if (d.kind == 0) TRY(ensure((void **)&c->ctx, &c->ctx_bytes, (size_t)bc.C * d.DC * 2));
+  TRY(ensure(&c->ws, &c->ws_bytes, (size_t)hxa_block_ws_bytes(&d)));
+  // staging for every host<->device copy of this call: x32 tiles, cos/sin tiles, ctx tiles, stage buffers
+  const size_t stage_need = std::max({xb, (size_t)bc.T * d.F * 2, (size_t)bc.T * 256, (size_t)bc.C * d.DC * 2,
+                                      (size_t)bc.C * D * 2});
+  TRY(ensure((void **)&c->stage, &c->stage_bytes, stage_need));
+  if (bc.first || c->cur_T != bc.T || c->cur_C != bc.C) {
+    // x32 tiles -> rows; ctx16 tiles -> rows; cos/sin tiles -> rows (megarun.cpp:59-90 layouts)
+    HIPC(hipMemcpyAsync(c->stage, (const char *)blob.ptr + bc.off_x, xb, hipMemcpyHostToDevice, st));
+    TRY(hxa_x32_to_rows_launch(c->stage, c->x, bc.T, D, st));
+    HIPC(hipMemcpyAsync(c->stage, (const char *)blob.ptr + bc.off_cos, (size_t)bc.T * 256, hipMemcpyHostToDevice, st));
+    TRY(hxa_cs_to_rows_launch(c->stage, c->cosr, bc.T, st));
+    HIPC(hipMemcpyAsync(c->stage, (const char *)blob.ptr + bc.off_sin, (size_t)bc.T * 256, hipMemcpyHostToDevice, st));
+    TRY(hxa_cs_to_rows_launch(c->stage, c->sinr, bc.T, st));
+    if (d.kind == 0) {
+      HIPC(hipMemcpyAsync(c->stage, (const char *)blob.ptr + bc.off_ctx, (size_t)bc.C * d.DC * 2, hipMemcpyHostToDevice, st));
+      TRY(hxa_h16_to_rows_launch((const hxa_h *)c->stage, c->ctx, d.DC, bc.C, d.DC, st));
+    }
+    c->cur_T = bc.T;
+    c->cur_C = bc.C;
+  }
+  HIPC(hipMemcpyAsync(c->mod, modh, (size_t)(d.kind == 0 ? 9 : 6) * D * 4, hipMemcpyHostToDevice, st));
+  int us[16] = {0};
+  const int nst = d.kind == 0 ? 13 : 8;
+  const auto t_work = std::chrono::steady_clock::now();
+  TRY(hxa_block_run(&d, db.pack, c->x, c->ctx, c->mod, c->cosr, c->sinr, c->ws, bc.stop, times ? us : nullptr, nst, st));
+  if (bc.stop) {  // stage buffers back to the blob as h16 tiles (what cmp_blk.py reads)
+    const WsLayout L = ws_layout(&d);
+    const int which[9] = {WS_H, WS_Q, WS_K, WS_VT, WS_O, WS_T1, WS_MID, WS_CK, WS_CVT};
+    for (int i = 0; i < 9; i++) {
+      if (bc.off_stage[i] < 0) continue;
+      if (d.kind == 1 && i >= 7) continue;
+      const int R = i >= 7 ? bc.C : bc.T, Cc = i == 6 ? d.F : D;
+      const size_t bytes = (size_t)R * Cc * 2;
+      if (!blob_range(blob, bc.off_stage[i], bytes)) continue;
+      const bool tr = i == 3 || i == 8;
+      TRY(hxa_rows_to_h16_launch((const hxa_h *)((char *)c->ws + L.off[which[i]]), L.ld[which[i]], (hxa_h *)c->stage, R, Cc,
+                                 tr ? 1 : 0, st));
+      HIPC(hipMemcpyAsync((char *)blob.ptr + bc.off_stage[i], c->stage, bytes, hipMemcpyDeviceToHost, st));
+      HIPC(hipStreamSynchronize(st));
+    }
+  }
+  if (bc.rel) {  // result visible to the caller (blk.c:193)
+    TRY(hxa_rows_to_x32_launch(c->x, c->stage, bc.T, D, st));
+    HIPC(hipMemcpyAsync((char *)blob.ptr + bc.off_x, c->stage, xb, hipMemcpyDeviceToHost, st));
+  }
+  HIPC(hipStreamSynchronize(st));
+  if (times) {
+    for (int i = 0; i < ntimes; i++) times[i] = 0;
+    for (int i = 0; i < nst && i < ntimes && i < 17; i++) times[i] = us[i];
+    if (ntimes > 24) times[24] = (int)std::chrono::duration_cast<std::chrono::microseconds>(t_work - t_entry).count();
+  }
+  return HXA_OK;
+}
+}  // namespace
+
+extern "C" int mega_block(remote_handle64 h, const int *meta, int nmeta, int wfd, int bfd, const uint8_t *mod, int modlen,
+                          int *times, int ntimes, int *rc) {
+  g_err[0] = 0;
+  int dummy = 0;
+  if (!rc) rc = &dummy;
+  *rc = 0;
+  Ctx *c = ctx_of(h);
+  if (!c) return *rc = HXA_E_ARG, 0;
+  auto bit = c->bufs.find(bfd);
+  if (bit == c->bufs.end() || bit->second.kind != HXA_KIND_BLOB) { *rc = HXA_E_BLOB; fail(*rc, "blob fd %d not registered", bfd); return 0; }
+  auto wit = c->bufs.find(wfd);
+  if (wit == c->bufs.end() || wit->second.kind != HXA_KIND_WEIGHTS_ANIMA) { *rc = HXA_E_WEIGHTS; fail(*rc, "weight fd %d not registered", wfd); return 0; }
+  if (!meta || nmeta < M_NMETA || !mod) { *rc = HXA_E_META; fail(*rc, "meta too short"); return 0; }
+  if (meta[M_STOP] == 99) return 0;  // blk.c:115: return after mapping
+  const int T = meta[M_NTOK], C = meta[M_NCTX];
+  if (T <= 0 || T % 32 || T > TMAX || C <= 0 || C % 32) { *rc = HXA_E_META; fail(*rc, "ntok %d / nctx %d", T, C); return 0; }
+  if (meta[M_STOP] >= 90) { *rc = HXA_E_MODE; fail(*rc, "DSP experiment stop code %d", meta[M_STOP]); return 0; }
+  auto dit = c->blocks.find(wfd);
+  if (dit == c->blocks.end()) {
+    DevBlock db;
+    const int r = build_anima_pack(*c, wit->second, meta, db);
+    if (r != HXA_OK) { *rc = r; return 0; }
+    dit = c->blocks.emplace(wfd, db).first;
+  }
+  BlockCall bc{0, T, C, T, meta[M_STOP], meta[M_FIRST], meta[M_REL], meta[M_X], meta[M_CTX], meta[M_COS], meta[M_SIN],
+               {meta[M_H], meta[M_Q], meta[M_K], meta[M_V], meta[M_O], meta[M_T], meta[M_MID], meta[M_CK], meta[M_CV]}};
+  *rc = run_ref_block(c, bc, dit->second, bit->second, (const float *)mod, modlen, times, ntimes);
+  return 0;
+}
+
+extern "C" int mega_moss_block(remote_handle64 h, const int *meta, int nmeta, int wfd, int bfd, const uint8_t *mod,
+                               int modlen, int *times, int ntimes, int *rc) {
+  g_err[0] = 0;
+  int dummy = 0;
+  if (!rc) rc = &dummy;
+  *rc = 0;
+  Ctx *c = ctx_of(h);
+  if (!c) return *rc = HXA_E_ARG, 0;
+  auto bit = c->bufs.find(bfd);
+  if (bit == c->bufs.end() || bit->second.kind != HXA_KIND_BLOB) { *rc = HXA_E_BLOB; fail(*rc, "blob fd %d not registered", bfd); return 0; }
+  auto wit = c->bufs.find(wfd);
+  if (wit == c->bufs.end() || wit->second.kind != HXA_KIND_WEIGHTS_MOSS) { *rc = HXA_E_WEIGHTS; fail(*rc, "weight fd %d not registered", wfd); return 0; }
+  if (!meta || nmeta < MM_NMETA || !mod) { *rc = HXA_E_META; fail(*rc, "meta too short"); return 0; }
+  if (meta[MM_MODE] != 0) { *rc = HXA_E_MODE; fail(*rc, "moss mode %d (only the DiT block, mode 0)", meta[MM_MODE]); return 0; }
+  const int T = meta[MM_NTOK], nv = meta[MM_NVALID] ? meta[MM_NVALID] : T;
+  if (T <= 0 || T % 32 || T > 8192 || nv < 1 || nv > T) { *rc = HXA_E_META; fail(*rc, "ntok %d nvalid %d", T, nv); return 0; }
+  auto dit = c->blocks.find(wfd);
+  if (dit == c->blocks.end()) {
+    DevBlock db;
+    const int r = build_moss_pack(*c, wit->second, meta, db);
+    if (r != HXA_OK) { *rc = r; return 0; }
+    dit = c->blocks.emplace(wfd, db).first;
+  }
+  BlockCall bc{1, T, 0, nv, meta[MM_STOP], meta[MM_FIRST], meta[MM_REL], meta[MM_X], -1, meta[MM_COS], meta[MM_SIN],
+               {meta[MM_H], meta[MM_Q], meta[MM_K], meta[MM_V], meta[MM_O], meta[MM_T], meta[MM_MID], -1, -1}};
+  *rc = run_ref_block(c, bc, dit->second, bit->second, (const float *)mod, modlen, times, ntimes);
+  return 0;
+}

@@ -1,0 +1,206 @@
+/* hexanima_hip.h -- C-ABI of the MI355X (gfx950) DiT block runner, libhexanima_hip.so.
+ *
+ * The first section is the drop-in boundary: the same three symbols and C signatures as the reference's FastRPC
+ * block interface, so a megarun/mossrun-style caller links against this library instead of the DSP stub.
+ * Everything else is the device-level interface used by the runner, the benchmark and the parity tests
+ * (plain device pointers and sizes; no framework types).
+ *
+ * All functions return 0 on success or a negative status (see HXA_E_*); hxa_last_error() describes the last one.
+ * A handle / stream is not thread-safe: calls on one handle must be serialised by the caller, as the reference's
+ * single caller thread does (megarun.cpp:176-184).
+ */
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint64_t remote_handle64; /* the reference's remote handle type (remote.idl) */
+
+/* status codes; -1/-2/-5/-6/-7 keep the reference's *rc meanings (blk.c:110-127, :188) */
+#define HXA_OK 0
+#define HXA_E_RESOURCE (-1) /* device resources could not be acquired (VTCM/HMX acquire in the reference) */
+#define HXA_E_LOCK (-2)
+#define HXA_E_WEIGHTS (-5)  /* weight buffer not registered / unreadable (HAP_mmap_get(wfd) failure) */
+#define HXA_E_NOBLOB (-6)
+#define HXA_E_BLOB (-7)     /* blob not registered (HAP_mmap_get(bfd) failure) */
+#define HXA_E_META (-10)    /* bad meta[]: ntok % 32 != 0, ntok > TMAX, offsets outside the registered buffers */
+#define HXA_E_MODE (-11)    /* unsupported mode / format */
+#define HXA_E_ARG (-12)     /* invalid argument (shape, alignment, null pointer) */
+#define HXA_E_HIP (-13)     /* HIP runtime error */
+
+/* ============================================================================================================
+ * 1. Reference block-execution ABI
+ * ============================================================================================================ */
+
+/* replaces mega_open (hexagon/mega/mega_imp.c:16): creates a context on the current HIP device. uri is ignored. */
+int mega_open(const char *uri, remote_handle64 *h);
+/* replaces mega_close (mega_imp.c:18): releases every device buffer of the handle. */
+int mega_close(remote_handle64 h);
+/* replaces mega_block (hexagon/mega/blk.c:186, IDL mega.idl:10): runs one Anima DiT block.
+ *   meta[]   : the reference enum of blk_meta.h:3-4 (byte offsets into the blob / weight buffer + params)
+ *   wfd, bfd : keys of buffers registered with hxa_register (the reference's rpcmem fds)
+ *   mod      : 9 x 2048 fp32 (shift, scale, gate per site), modlen = 73728
+ *   times    : per-stage microseconds (TICK order of blk.c:136), times[24] = entry overhead
+ *   *rc      : 0 or a status code; the return value is 0 as in the reference.
+ * meta[M_FIRST] uploads x / ctx / cos / sin from the blob to device-resident copies; meta[M_REL] writes x back
+ * to the blob (x32 tiles). Weights are converted to the GPU layout and uploaded on first use, then stay resident.
+ * meta[M_STOP] = n stops after n stages and writes the stage buffers (h,q,k,v,o,t,mid,ck,cv) back to the blob. */
+int mega_block(remote_handle64 h, const int *meta, int nmeta, int wfd, int bfd, const uint8_t *mod, int modlen, int *times,
+               int ntimes, int *rc);
+/* the MOSS build of the same entry (moss/hexagon/mega/blk.c:262-274) with the MOSS meta enum
+ * (moss/hexagon/mega/blk_meta.h:3-4); MODE 0 (DiT block) only; mod = 6 x DIM fp32. */
+int mega_moss_block(remote_handle64 h, const int *meta, int nmeta, int wfd, int bfd, const uint8_t *mod, int modlen,
+                    int *times, int ntimes, int *rc);
+
+/* buffer registration: replaces rpcmem_alloc + fastrpc_mmap of the caller (megarun.cpp:100-119, :141-148).
+ * kind: HXA_KIND_* below. The host memory must stay valid until hxa_unregister / mega_close. */
+#define HXA_KIND_WEIGHTS_ANIMA 0 /* blkNN.bin of hexagon/mega/export_all.py (fp16 crouton or q8 records) */
+#define HXA_KIND_BLOB 1          /* activation blob (offsets in meta[]) */
+#define HXA_KIND_WEIGHTS_MOSS 2  /* blkNN.bin of moss/export_moss.py (q8 records, LoRA rows appended) */
+int hxa_register(remote_handle64 h, int fd, void *host_ptr, size_t bytes, int kind);
+int hxa_unregister(remote_handle64 h, int fd);
+
+/* ============================================================================================================
+ * 2. Device runtime
+ * ============================================================================================================ */
+const char *hxa_last_error(void);
+const char *hxa_version(void);
+int hxa_init(int device);
+int hxa_malloc(void **p, size_t bytes);
+int hxa_free(void *p);
+int hxa_h2d(void *dst, const void *src, size_t bytes);
+int hxa_d2h(void *dst, const void *src, size_t bytes);
+int hxa_d2d(void *dst, const void *src, size_t bytes);
+int hxa_memset(void *p, int value, size_t bytes);
+int hxa_sync(void);
+int hxa_stream_create(void **stream);
+int hxa_stream_destroy(void *stream);
+int hxa_stream_sync(void *stream);
+int hxa_event_create(void **ev);
+int hxa_event_destroy(void *ev);
+int hxa_event_record(void *ev, void *stream);
+int hxa_event_elapsed_ms(void *start, void *stop, float *ms);
+int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, char *name, int name_len);
+
+/* ============================================================================================================
+ * 3. Kernels (device pointers; stream NULL = the null stream)
+ * ============================================================================================================ */
+#define HXA_W_F16 0 /* w [N][K] fp16 */
+#define HXA_W_Q8 1  /* q [N][K] int8, s [K/32][N] fp16; value f16(q*s) */
+#define HXA_W_Q4 2  /* q [N][K/2] (k0+2j at bits 4j, k0+2j+1 at bits 16+4j of each 32-bit word; nibble = q+8),
+                       s [K/32][N] fp16, optional z [K/32][N]: value f16(nibble*s + z), z NULL: f16((nibble-8)*s) */
+#define HXA_EPI_STORE 0
+#define HXA_EPI_GELU_TANH 1
+#define HXA_EPI_GELU_ERF 2
+#define HXA_EPI_RESADD 3
+#define HXA_EPI_STORE_T 4
+#define HXA_EPI_SITU 5
+#define HXA_EPI_PARTIAL 6
+
+/* out = epi(A[M][K] . W[N][K]^T); replaces gemm_run_ex / gemm_run_geo (hexagon/mega/gemm2.c:96-141).
+ * STORE: out[m][n] (ldo); with out_t != NULL the columns n >= split_col go to out_t[n - split_col][m] (ldo_t).
+ * STORE_T: out[n][m]. GELU_*: out = f16(gelu(f16(acc))). RESADD: x[m][n] += gate[n] f16(acc) (x fp32, ldx).
+ * SITU: W rows interleaved per 32 (up_j, gate_j), out[m][j*32+c] (moss gemm2.c mode 5).
+ * PARTIAL: ksplit slices, out[z*out_zstride + m*ldo + n] = f16(partial z) (blk.c:172-174). */
+int hxa_gemm(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
+             int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
+             void *out_t, long ldo_t, int split_col, void *stream);
+/* same, with an explicit tile shape (tests / tuning); bm x bn in {256x128, 128x256, 128x128, 64x128, 128x64} */
+int hxa_gemm_tile(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
+                  int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
+                  int bm, int bn, void *stream);
+/* attention over heads of 128 (blk.c:54-91): q [T][ldq], k [NKV][ldk], vt [H*128][ldvt] (V transposed),
+ * o [T][ldo]; keys >= nvalid masked; batch images at element strides qb/kb/vb/ob. */
+int hxa_attention(const void *q, long ldq, const void *k, long ldk, const void *vt, long ldvt, void *o, long ldo, int T,
+                  int NKV, int nvalid, int H, int batch, long qb, long kb, long vb, long ob, void *stream);
+/* h = f16(norm(x) * (1 + scale) [* w] + shift); LN when w == NULL (kern.c:38-65), RMS otherwise (moss kern.c:353) */
+int hxa_norm_mod(const float *x, long ldx, int T, int D, const float *shift, const float *scale, const float *w,
+                 float eps, void *h, long ldh, void *stream);
+/* per-head RMSNorm * gain (+ RoPE when cosT != NULL) in place on q0 (and q1 when not NULL) (kern.c:163-197);
+ * cos/sin [ttab][64], row t % ttab */
+int hxa_rmsrope(void *q0, void *q1, const float *g0, const float *g1, long ldq, int T, int H, const float *cosT,
+                const float *sinT, int ttab, void *stream);
+/* x += gate * (t1 + t2) (kern.c:330-339) */
+int hxa_resadd2(float *x, long ldx, const void *t1, const void *t2, long ldt, int T, int D, const float *gate,
+                void *stream);
+/* synthetic data: dtype 0 fp32, 1 fp16 */
+int hxa_fill_normal(void *dst, int dtype, size_t n, uint64_t seed, float mean, float std, void *stream);
+int hxa_fill_uniform_int(void *dst, int bits, size_t n, uint64_t seed, int lo, int hi, void *stream);
+int hxa_fill_const(void *dst, int dtype, size_t n, float v, void *stream);
+/* q8 / q4 quantisation of fp32 W[N][K] (export_all.py:10-18 semantics, group 32, fp16 scales) */
+int hxa_quantize(const float *W, int N, int K, int fmt, void *q, void *s, void *stream);
+/* crouton <-> row-major conversions (kern.h:5-8) */
+int hxa_x32_to_rows(const float *tiles, float *x, int R, int C, void *stream);
+int hxa_rows_to_x32(const float *x, float *tiles, int R, int C, void *stream);
+
+/* ============================================================================================================
+ * 4. GPU block packs and the device-level block (weights resident in HBM)
+ * ============================================================================================================ */
+/* A pack is one device allocation holding every weight of one block in the GPU layouts above, at offsets
+ * given by hxa_pack_layout (each matrix: w, then s, then z, 256-byte aligned).
+ * kind 0 (Anima structure): matrices qkv [3D][D], o [D][D], cq [D][D], ckv [2D][DC], co [D][D], w1 [F][D],
+ *   w2 [D][F], then gain fp32 [4][128] (q/sqrt(128), k, cross q/sqrt(128), cross k).
+ * kind 1 (MOSS structure): qkv [3D][D], o [D][D], ug [2F][D] (rows interleaved per 32: up_j, gate_j),
+ *   down [D][F], then fp32 gq[128], gk[128], n1[D], n2[D].
+ * fmt_attn applies to the attention matrices, fmt_mlp to the MLP ones (asym q4 not used in packs).
+ * offs receives 3 offsets (w, s, z; -1 when absent) per matrix followed by the vector offset; returns bytes. */
+long hxa_pack_layout(int kind, int D, int F, int DC, int fmt_attn, int fmt_mlp, long *offs, int noffs);
+
+typedef struct {
+  int kind;      /* 0 Anima, 1 MOSS */
+  int D, H, F;   /* width, heads (x128), MLP width (MOSS: up and gate each F) */
+  int C, DC;     /* context tokens per image and context width (Anima) */
+  int T, batch;  /* tokens per image (padded to 32), images */
+  int nvalid;    /* MOSS: valid tokens per image (joint attention key mask) */
+  int fmt_attn, fmt_mlp;
+  int gelu;      /* Anima MLP activation: 0 erf (reference block), 1 tanh */
+} hxa_block_dims;
+/* bytes of the activation workspace of hxa_block_run */
+long hxa_block_ws_bytes(const hxa_block_dims *d);
+/* One block, everything on the device:
+ *   x    [batch*T][D] fp32 residual stream, updated in place
+ *   ctx  [batch*C][DC] fp16 (Anima; NULL for MOSS)
+ *   mod  Anima: 9 x D fp32 (site s: shift 3s, scale 3s+1, gate 3s+2); MOSS: 6 x D (shift_a, scale_a, gate_a,
+ *        shift_f, scale_f, gate_f)
+ *   cos, sin [T][64] fp32 (NULL: no RoPE)
+ *   stop: stop after this many stages (0 = all); stage_us: per-stage microseconds (NULL: not timed). */
+int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod, const float *cosT,
+                  const float *sinT, void *ws, int stop, int *stage_us, int nstage, void *stream);
+/* stage buffers of the workspace: which 0 h, 1 q, 2 k, 3 vT ([D][batch*T]), 4 o, 5 t1, 6 mid, 7 ck, 8 cvT, 9 t2;
+ * returns the device pointer and its row stride in elements */
+void *hxa_block_ws_buf(const hxa_block_dims *d, void *ws, int which, long *ld);
+
+/* ============================================================================================================
+ * 5. DiT runner (the process above the boundary: patch embed, timestep modulation, blocks, final layer, Euler)
+ * ============================================================================================================ */
+typedef struct {
+  hxa_block_dims blk;   /* per-block shape (T = gh*gw tokens per image) */
+  int nblocks;
+  int lat_c, lat_h, lat_w; /* latent [C][H][W]; patch 2 */
+  int temb;             /* sinusoid width of the timestep embedding (256) */
+  int ntxt_in;          /* MOSS: text width before projection (0 = none) */
+} hxa_dit_cfg;
+int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **dit);
+int hxa_dit_destroy(void *dit);
+/* set latents [batch][C][H][W] fp32 and the context [batch][C][DC] fp32 (host pointers) */
+int hxa_dit_set_inputs(void *dit, const float *lat, const float *ctx);
+int hxa_dit_get_latent(void *dit, float *lat);
+/* one Euler step x <- x + (sigma_next - sigma) v(x, sigma); use_graph 1 replays a captured HIP graph */
+int hxa_dit_step(void *dit, float sigma, float sigma_next, int use_graph);
+/* the velocity v(x, sigma) of the current latent into v [batch][C][H][W] (host), without updating x */
+int hxa_dit_velocity(void *dit, float sigma, float *v);
+/* copies of the device weights for checking (host may be NULL to query the size; returns bytes):
+ *   which in [0, nblocks): block pack `which`
+ *   which in [nblocks, 2 nblocks): modulation weights of block which-nblocks, fp16 [6D][D]
+ *     (MOSS: one shared [6D][D] matrix, which == nblocks)
+ *   which == 2 nblocks: glue, fp16, concatenated: x_embed [D][4C], t_embed [D][temb], final_mod [2D][D],
+ *     final_linear [4C][D], then (MOSS only) text_proj [D][ntxt_in] */
+long hxa_dit_export(void *dit, int which, void *host, size_t bytes);
+void *hxa_dit_stream(void *dit);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,95 @@
+"""Shared helpers of the parity tests: comparison metrics (the reference's own: hexagon/mega/cmp_block.py:5-6
+rel err on the block delta + cosine; moss/cmp_blk.py:9 per-stage rel err), GPU-pack <-> oracle-weight conversion
+and an oracle-composed DiT step (the caller-side glue of phone/animad.cpp:424-492 around the oracle blocks)."""
+import numpy as np
+
+from oracle import hxo
+
+
+def f16(a):
+    return np.asarray(a).astype(np.float16)
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / (np.linalg.norm(b) + 1e-30))
+
+
+def delta_metrics(out, ref, x0):
+    """cmp_block.py:5-6: rel err on the block delta and cosine of the deltas."""
+    out, ref, x0 = (np.asarray(v, np.float64) for v in (out, ref, x0))
+    dl = ref - x0
+    do = out - x0
+    r = float(np.linalg.norm(out - ref) / np.linalg.norm(dl))
+    c = float(do.ravel() @ dl.ravel() / (np.linalg.norm(do) * np.linalg.norm(dl)))
+    return r, c
+
+
+def ulp_diff(a16, b16):
+    """max distance in fp16 ulps between two fp16 arrays (same sign assumed)."""
+    a = np.asarray(a16).view(np.uint16).astype(np.int32)
+    b = np.asarray(b16).view(np.uint16).astype(np.int32)
+    sa = np.where(a & 0x8000, -(a & 0x7FFF), a)
+    sb = np.where(b & 0x8000, -(b & 0x7FFF), b)
+    return np.abs(sa - sb)
+
+
+def unpack_weights(pack: np.ndarray, kind: int, D: int, F: int, DC: int, fmt_attn: int, fmt_mlp: int, layout):
+    """GPU pack image -> dict of fp16 (uint16) W[N][K] matrices (dequantised) and the fp32 vector section."""
+    total, offs, voff = layout
+    shapes = ([(3 * D, D), (D, D), (D, D), (2 * D, DC), (D, D), (F, D), (D, F)] if kind == 0
+              else [(3 * D, D), (D, D), (2 * F, D), (D, F)])
+    mats = []
+    for i, ((N, K), (wo, so)) in enumerate(zip(shapes, offs)):
+        fmt = fmt_attn if i < (5 if kind == 0 else 2) else fmt_mlp
+        if fmt == 0:
+            mats.append(pack[wo:wo + N * K * 2].view(np.uint16).reshape(N, K).copy())
+        else:
+            s = pack[so:so + (K // 32) * N * 2].view(np.uint16).reshape(K // 32, N).copy()
+            if fmt == 1:
+                q = pack[wo:wo + N * K].view(np.int8).reshape(N, K).copy()
+                mats.append(hxo.q8_dequant(q, s))
+            else:
+                q = pack[wo:wo + N * K // 2].reshape(N, K // 2).copy()
+                mats.append(hxo.q4_dequant(q, s))
+    if kind == 0:
+        qkv, wo_, wcq, ckv, wco, w1, w2 = mats
+        vec = pack[voff:voff + 4 * 512].view(np.float32).copy()
+        return {"wq": qkv[:D], "wk": qkv[D:2 * D], "wv": qkv[2 * D:], "wo": wo_, "wcq": wcq, "wck": ckv[:D],
+                "wcv": ckv[D:], "wco": wco, "w1": w1, "w2": w2, "gain": vec}
+    qkv, wo_, ug, dn = mats
+    vec = pack[voff:voff + 4 * (256 + 2 * D)].view(np.float32).copy()
+    ugr = ug.reshape(F // 32, 2, 32, D)
+    return {"wq": qkv[:D], "wk": qkv[D:2 * D], "wv": qkv[2 * D:], "wo": wo_,
+            "wup": np.ascontiguousarray(ugr[:, 0].reshape(F, D)), "wgate": np.ascontiguousarray(ugr[:, 1].reshape(F, D)),
+            "wdown": dn, "gq": vec[:128], "gk": vec[128:256], "n1": vec[256:256 + D], "n2": vec[256 + D:]}
+
+
+def silu(v):
+    v = np.asarray(v, np.float64)
+    return (v / (1.0 + np.exp(-v))).astype(np.float32)
+
+
+def oracle_anima_velocity(lat, ctx16, sigma, blocks, modws, glue, *, D, H, F, C4, temb, gelu=1, attn_mode=0):
+    """v(x, sigma) of the Anima-structure DiT, image by image, from the oracle primitives.
+    glue = (Wemb [D][C4], L1 [D][temb], Lf [2D][D], Wfin [C4][D]) fp16; modws[k] [6D][D] fp16."""
+    Wemb, L1, Lf, Wfin = glue
+    B, Cc, Hl, Wl = lat.shape
+    s = hxo.sinusoid(sigma, temb)
+    c = hxo.linear_f32(s[None, :], L1)
+    sc = silu(c)
+    mods = []
+    for mw in modws:
+        m6 = hxo.linear_f32(sc, mw)[0].reshape(6, D)
+        mods.append(np.concatenate([m6[:3], np.zeros((2, D), np.float32), np.ones((1, D), np.float32), m6[3:]]))
+    fm = hxo.linear_f32(sc, Lf)[0]
+    cos, sin = hxo.rope_anima(Hl // 2, Wl // 2)
+    out = np.zeros_like(lat)
+    for b in range(B):
+        x = hxo.linear_f32(hxo.patchify(lat[b]), Wemb)
+        for w, m9 in zip(blocks, mods):
+            x, _, _ = hxo.anima_block(x, ctx16[b], m9, cos, sin, w, H=H, F=F, gelu=gelu, attn_mode=attn_mode)
+        xn = hxo.final_norm(x, fm[:D], fm[D:])
+        out[b] = hxo.unpatchify(hxo.linear_f32(xn, Wfin), Cc, Hl, Wl)
+    return out

@@ -1,0 +1,67 @@
+"""CPU-side checks of the C-ABI library: it loads, exports every function include/hexanima_hip.h declares, and its
+host-only layout functions agree with the reference's byte layouts. No compute is launched here."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hexanima_hip.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    return set(re.findall(r"^\s*(?:int|long|void\s*\*|const char\s*\*)\s*\**\s*(\w+)\s*\(", src, re.M))
+
+
+@pytest.fixture(scope="module")
+def hip():
+    from hexanima_amd import hip as h
+    h.lib()
+    return h
+
+
+def test_library_exports_every_declared_symbol(hip):
+    out = subprocess.run(["nm", "-D", "--defined-only", hip.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    syms = {l.split()[-1] for l in out.splitlines() if l.strip()}
+    decl = _declared()
+    assert len(decl) >= 40
+    assert decl <= syms, sorted(decl - syms)
+    # the reference's three block-interface symbols (mega.idl:3-11, mega_imp.c:16-18, blk.c:186)
+    assert {"mega_open", "mega_block", "mega_close"} <= syms
+    # and the Python binding covers exactly the declared set
+    assert set(hip.exported_symbols()) == decl
+
+
+def test_pack_layout_matches_reference_matrix_bytes(hip):
+    # an fp16 Anima pack holds the same ten matrices as blkNN.bin: 125829120 bytes before the gains (blk_wlayout.h:18)
+    total, mats, voff = hip.pack_layout(0, 2048, 8192, 1024, 0, 0)
+    assert voff == 125829120
+    assert all(o % 256 == 0 for o, _ in mats) and voff % 256 == 0
+    # q8: one int8 per weight + one fp16 scale per (32-row group, column) = 17/16 byte per weight (the reference
+    # record stores each scale twice: 1152 B per 32x32 tile, export_all.py:10-18)
+    t8, m8, v8 = hip.pack_layout(0, 2048, 8192, 1024, 1, 1)
+    assert v8 == 125829120 // 2 * 17 // 16
+    t4, m4, v4 = hip.pack_layout(1, 3072, 12288, 0, 1, 2)
+    assert all(s >= 0 for _, s in m4)
+
+
+def test_ws_bytes_and_init_without_gpu(hip):
+    d = hip.BlockDims(0, 2048, 16, 8192, 256, 1024, 1536, 1, 1536, 0, 0, 1)
+    # h, q|k, v^T, o, two split-K partials (fp16, 7 x [T][D] in total) + the MLP hidden [T][F] + cross k / v^T
+    assert hip.lib().hxa_block_ws_bytes(C.byref(d)) >= 1536 * (14 * 2048 + 2 * 8192) + 4 * 256 * 2048
+    if not os.path.exists("/dev/kfd"):
+        rc = hip.lib().hxa_init(0)
+        assert rc == -13 and "device" in hip.last_error()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    import importlib
+    from hexanima_amd import hip as h
+    monkeypatch.setattr(h, "LIB_PATH", str(tmp_path / "absent.so"))
+    monkeypatch.setattr(h, "_lib", None)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        h.lib()

@@ -1,0 +1,349 @@
+"""GPU parity of whole blocks, the reference block ABI (mega_block) and the DiT runner against the CPU oracle.
+
+Metrics are the reference's own (hexagon/mega/cmp_block.py:5-6 rel err on the block delta + cosine;
+moss/cmp_blk.py:9 per-stage rel err). Tolerances, stated per test: block delta rel err <= 5e-3 and cosine
+>= 0.99999 against the oracle in reference-rounding mode; per-stage fp16 buffers rel err <= 2e-3 before
+attention and <= 1e-2 after it (the oracle keeps the reference's fp16 S/P/rowsum rounding, the GPU an fp32 online
+softmax)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import hxo
+from tests._helpers import delta_metrics, f16, oracle_anima_velocity, rel, unpack_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _hip():
+    from hexanima_amd import hip
+    hip.init()
+    return hip
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def cfg0_mod9(D, rng, t=0.75):
+    """config-0 modulation: Linear(256->D) . SiLU . Linear(D->6D) of sinusoid_256(t), weights N(0,0.02),
+    expanded to 9 rows (cross-attention site: shift 0, scale 0, gate 1)."""
+    L1 = f16(rng.standard_normal((D, 256)) * 0.02)
+    L2 = f16(rng.standard_normal((6 * D, D)) * 0.02)
+    c = hxo.linear_f32(hxo.sinusoid(t, 256)[None], L1)
+    m6 = hxo.linear_f32((c / (1 + np.exp(-c.astype(np.float64)))).astype(np.float32), L2)[0].reshape(6, D)
+    return np.concatenate([m6[:3], np.zeros((2, D), np.float32), np.ones((1, D), np.float32), m6[3:]]).astype(np.float32)
+
+
+def make_anima_pack(hip, rng, D, F, DC, fmt):
+    H = D // 128
+    shapes = hip.pack_shapes(0, D, F, DC)
+    mats = []
+    for (N, K) in shapes:
+        W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        mats.append(f16(W) if fmt == 0 else (hxo.q8_quantize(W) if fmt == 1 else hxo.q4_quantize(W)))
+    gain = np.concatenate([np.full(128, 1 / np.sqrt(128)), np.ones(128), np.full(128, 1 / np.sqrt(128)), np.ones(128)])
+    img = hip.build_pack(0, D, F, DC, fmt, fmt, mats, gain.astype(np.float32))
+    w = unpack_weights(img, 0, D, F, DC, fmt, fmt, hip.pack_layout(0, D, F, DC, fmt, fmt))
+    return img, w, H
+
+
+def run_block_gpu(hip, d, img, x, ctx, mod, cos, sin, stop=0):
+    dpack = hip.DeviceArray.from_numpy(img)
+    dx = hip.DeviceArray.from_numpy(x)
+    dctx = hip.DeviceArray.from_numpy(f16(ctx)) if ctx is not None else None
+    dmod = hip.DeviceArray.from_numpy(mod)
+    dc, ds = hip.DeviceArray.from_numpy(cos), hip.DeviceArray.from_numpy(sin)
+    ws = hip.block_ws(d)
+    us = (C.c_int * 16)()
+    hip.check(hip.lib().hxa_block_run(C.byref(d), dpack.ptr, dx.ptr, dctx.ptr if dctx else None, dmod.ptr, dc.ptr, ds.ptr,
+                                      ws.ptr, stop, us, 16, None), "block_run")
+    hip.sync()
+    return dx.numpy(), ws, list(us)
+
+
+@pytest.mark.parametrize("fmt,D,F,label", [(0, 2048, 8192, "cfg0 2B fp16 block"), (1, 2560, 10240, "cfg3 2.9B q8 block")])
+def test_anima_block_full_size(fmt, D, F, label):
+    """Config 0 (and the config-3 q8 block): 1536 image tokens, 256 text tokens of width 1024, tanh GELU."""
+    hip = _hip()
+    say(f"{label}: T=1536 D={D} F={F} fmt={fmt}")
+    rng = np.random.default_rng(100 + fmt)
+    T, C_, DC = 1536, 256, 1024
+    img, w, H = make_anima_pack(hip, rng, D, F, DC, fmt)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    ctx = f16(rng.standard_normal((C_, DC)))
+    mod9 = cfg0_mod9(D, rng)
+    cos, sin = hxo.rope_anima(48, 32)
+    d = hip.BlockDims(0, D, H, F, C_, DC, T, 1, T, fmt, fmt, 1)
+    got, ws, us = run_block_gpu(hip, d, img, x, ctx, mod9, cos, sin)
+    print("stage us:", us[:13], flush=True)
+    ref, buf, n = hxo.anima_block(x, ctx, mod9, cos, sin, w, H=H, F=F, gelu=1, attn_mode=0)
+    r, c = delta_metrics(got, ref, x)
+    print(f"rel err on delta {r:.2e} cos {c:.7f}", flush=True)
+    assert r < 5e-3 and c > 0.99999
+    # per-stage (cmp_blk.py style) from the last site's buffers: MLP hidden
+    mid = hip.read_ws(d, ws, hip.WS_MID, T, F)
+    assert rel(mid.astype(np.float32), buf["mid"].view(np.float16).astype(np.float32)) < 1e-2
+
+
+def test_anima_block_stages_and_batch():
+    hip = _hip()
+    say("anima block per-stage (M_STOP) + batch 2")
+    rng = np.random.default_rng(7)
+    D, F, DC, T, C_ = 512, 1024, 256, 256, 64
+    img, w, H = make_anima_pack(hip, rng, D, F, DC, 0)
+    x = rng.standard_normal((2 * T, D)).astype(np.float32)
+    ctx = f16(rng.standard_normal((2 * C_, DC)))
+    mod9 = cfg0_mod9(D, rng)
+    cos, sin = hxo.rope_anima(16, 16)
+    d = hip.BlockDims(0, D, H, F, C_, DC, T, 2, T, 0, 0, 1)
+    for stop, keys in ((1, ["h"]), (2, ["q", "k", "v"]), (3, ["q", "k"]), (4, ["o"]), (13, [])):
+        got, ws, _ = run_block_gpu(hip, d, img, x, ctx, mod9, cos, sin, stop=stop)
+        for b in range(2):
+            ref, buf, n = hxo.anima_block(x[b * T:(b + 1) * T], ctx[b * C_:(b + 1) * C_], mod9, cos, sin, w, H=H, F=F,
+                                          gelu=1, stop=stop)
+            assert n == stop
+            gx = got[b * T:(b + 1) * T]
+            if stop < 5:
+                assert np.array_equal(gx, x[b * T:(b + 1) * T])
+            else:
+                r, c = delta_metrics(gx, ref, x[b * T:(b + 1) * T])
+                assert r < 5e-3 and c > 0.99999
+            for k in keys:
+                which = {"h": hip.WS_H, "q": hip.WS_Q, "k": hip.WS_K, "v": hip.WS_VT, "o": hip.WS_O}[k]
+                if k == "v":
+                    g = hip.read_ws(d, ws, which, D, 2 * T)[:, b * T:(b + 1) * T].T
+                else:
+                    g = hip.read_ws(d, ws, which, 2 * T, D)[b * T:(b + 1) * T]
+                tol = 1e-2 if k == "o" else 2e-3
+                assert rel(g.astype(np.float32), buf[k].view(np.float16).astype(np.float32)) < tol, (stop, k)
+
+
+def test_moss_block_joint_attention_q8_q4():
+    """MOSS-class block (joint attention with a key mask, RMS-mod, SiTU, int8 attention / int4 MLP weights)."""
+    hip = _hip()
+    say("moss block T=544 nvalid=520 D=3072 F=4096 q8/q4")
+    rng = np.random.default_rng(11)
+    D, F, T, nv = 3072, 4096, 544, 520
+    H = D // 128
+    shapes = hip.pack_shapes(1, D, F, 0)
+    mats = []
+    for i, (N, K) in enumerate(shapes):
+        W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        mats.append(hxo.q8_quantize(W) if i < 2 else hxo.q4_quantize(W))
+    vec = np.concatenate([np.full(128, 1 / np.sqrt(128)), np.ones(128), rng.uniform(0.5, 1.5, 2 * D)]).astype(np.float32)
+    img = hip.build_pack(1, D, F, 0, 1, 2, mats, vec)
+    w = unpack_weights(img, 1, D, F, 0, 1, 2, hip.pack_layout(1, D, F, 0, 1, 2))
+    x = (rng.standard_normal((T, D)) * 2).astype(np.float32)
+    x[nv:] = 0
+    mod6 = (rng.standard_normal((6, D)) * 0.2).astype(np.float32)
+    bands = (1.0 / 10000.0 ** (np.arange(16) / 16)).astype(np.float32)
+    cs, sn = hxo.rope_moss(20, 24, 40, bands)  # 480 image + 40 text tokens
+    cos = np.concatenate([cs, np.ones((T - nv, 64), np.float32)])
+    sin = np.concatenate([sn, np.zeros((T - nv, 64), np.float32)])
+    d = hip.BlockDims(1, D, H, F, 0, 0, T, 1, nv, 1, 2, 0)
+    got, ws, us = run_block_gpu(hip, d, img, x, None, mod6, cos, sin)
+    ref, buf, n = hxo.moss_block(x, mod6, cos, sin, w, H=H, F=F, nvalid=nv)
+    r, c = delta_metrics(got[:nv], ref[:nv], x[:nv])
+    print(f"moss rel err on delta {r:.2e} cos {c:.7f}", flush=True)
+    assert r < 5e-3 and c > 0.99999
+
+
+# ------------------------------------------------------------------------------------------------ reference ABI
+def _megarun_layout(T, nctx):
+    """megarun.cpp:42-57 layout(): blob offsets (4 KiB aligned) of x, ctx, mod, cos, sin, h, q, k, v, o, t, mid, ck, cv."""
+    D = 2048
+    up = lambda v: (v + 4095) & ~4095
+    sz = {"X": T * D * 4, "CTX": nctx * 1024 * 2, "MOD": 9 * D * 4, "COS": (T // 32) * 2 * 1024 * 4,
+          "SIN": (T // 32) * 2 * 1024 * 4}
+    for k in ("H", "Q", "K", "V", "O", "T"):
+        sz[k] = T * D * 2
+    sz["MID"] = T * 8192 * 2
+    sz["CK"] = sz["CV"] = nctx * D * 2
+    offs, off = {}, 0
+    for k in ("X", "CTX", "MOD", "COS", "SIN", "H", "Q", "K", "V", "O", "T", "MID", "CK", "CV"):
+        offs[k] = off
+        off += up(sz[k])
+    return offs, off
+
+
+META = ["X", "CTX", "MOD", "GAIN", "COS", "SIN", "WSQ", "WSK", "WSV", "WSO", "WCQ", "WCK", "WCV", "WCO", "WM1", "WM2",
+        "H", "Q", "K", "V", "O", "T", "MID", "CK", "CV", "NTOK", "NCTX", "STOP", "NW", "REL", "FIRST", "Q8"]
+W_OFFS = {"WSQ": 0, "WSK": 8388608, "WSV": 16777216, "WSO": 25165824, "WCQ": 33554432, "WCK": 41943040,
+          "WCV": 46137344, "WCO": 50331648, "WM1": 58720256, "WM2": 92274688, "GAIN": 125829120}  # blk_wlayout.h
+
+
+def _blk_file(rng, q8):
+    """A synthetic blkNN.bin (export_all.py:29-36): 10 matrices as fp16 crouton tiles or q8 records, gains."""
+    D, F, DC = 2048, 8192, 1024
+    mats = {"WSQ": (D, D), "WSK": (D, D), "WSV": (D, D), "WSO": (D, D), "WCQ": (D, D), "WCK": (D, DC), "WCV": (D, DC),
+            "WCO": (D, D), "WM1": (F, D), "WM2": (D, F)}
+    total = 138416128 if not q8 else 125829120 // 2048 * 1152 + 4096 + (138416128 - 125833216)
+    buf = np.zeros(total, np.uint8)
+    w = {}
+    for k, (N, K) in mats.items():
+        W = f16(rng.standard_normal((N, K)) * 0.02)
+        off = W_OFFS[k] if not q8 else W_OFFS[k] // 2048 * 1152
+        if q8:
+            rec = hxo.q8rec_pack(W, floor_mode=0)
+            buf[off:off + rec.size] = rec
+            W = hxo.q8rec_unpack(rec, N, K)
+        else:
+            t = hxo.wt16_pack(W).view(np.uint8)
+            buf[off:off + t.size] = t
+        w[k] = W
+    gain = np.concatenate([np.full(128, 1 / np.sqrt(128)), np.ones(128), np.full(128, 1 / np.sqrt(128)), np.ones(128)]).astype(np.float32)
+    goff = W_OFFS["GAIN"] if not q8 else W_OFFS["GAIN"] // 2048 * 1152
+    buf[goff:goff + 2048] = gain.view(np.uint8)
+    ow = {"wq": w["WSQ"], "wk": w["WSK"], "wv": w["WSV"], "wo": w["WSO"], "wcq": w["WCQ"], "wck": w["WCK"],
+          "wcv": w["WCV"], "wco": w["WCO"], "w1": w["WM1"], "w2": w["WM2"], "gain": gain}
+    return buf, ow
+
+
+@pytest.mark.parametrize("q8", [False, True])
+def test_mega_block_reference_abi(q8):
+    """Two blocks through mega_block exactly as megarun drives them (FIRST on the first, REL on the last)."""
+    hip = _hip()
+    say(f"mega_block ABI q8={q8}")
+    lib = hip.lib()
+    rng = np.random.default_rng(21 + q8)
+    D, T, NCTX = 2048, 256, 256
+    gh, gw = 16, 16
+    offs, total = _megarun_layout(T, NCTX)
+    blob = np.zeros(total, np.uint8)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    ctx = f16(rng.standard_normal((NCTX, 1024)))
+    cos, sin = hxo.rope_anima(gh, gw)
+    blob[offs["X"]:offs["X"] + T * D * 4] = hxo.x32_tile(x).view(np.uint8)
+    blob[offs["CTX"]:offs["CTX"] + NCTX * 1024 * 2] = hxo.h16_tile(ctx).view(np.uint8)
+    for nm, tab in (("COS", cos), ("SIN", sin)):  # [slab][j][32][32], angle index d = 32 j + col
+        t = np.ascontiguousarray(tab.reshape(T // 32, 32, 2, 32).transpose(0, 2, 1, 3)).astype(np.float32)
+        blob[offs[nm]:offs[nm] + t.nbytes] = t.view(np.uint8).reshape(-1)
+    blocks = [_blk_file(rng, q8) for _ in range(2)]
+    mods = [cfg0_mod9(D, rng) for _ in range(2)]
+    h = C.c_uint64()
+    hip.check(lib.mega_open(b"file:///libmega_skel.so?mega_skel_handle_invoke&_modver=1.0&_dom=cdsp", C.byref(h)), "mega_open")
+    try:
+        hip.check(lib.hxa_register(h, 100, blob.ctypes.data, blob.nbytes, hip.KIND_BLOB), "register blob")
+        for i, (wb, _) in enumerate(blocks):
+            hip.check(lib.hxa_register(h, 200 + i, wb.ctypes.data, wb.nbytes, hip.KIND_WEIGHTS_ANIMA), "register w")
+        meta = np.zeros(32, np.int32)
+        for k, v in offs.items():
+            meta[META.index(k)] = v
+        for k, v in W_OFFS.items():
+            meta[META.index(k)] = v if not q8 else v // 2048 * 1152
+        meta[META.index("NTOK")], meta[META.index("NCTX")], meta[META.index("Q8")] = T, NCTX, int(q8)
+        times = np.zeros(32, np.int32)
+        rc = C.c_int(0)
+        for i in range(2):
+            meta[META.index("FIRST")], meta[META.index("REL")] = int(i == 0), int(i == 1)
+            r = lib.mega_block(h, meta.ctypes.data, 32, 200 + i, 100, mods[i].ctypes.data, mods[i].nbytes,
+                               times.ctypes.data, 32, C.byref(rc))
+            assert r == 0 and rc.value == 0, hip.last_error()
+            if i == 0:  # x stays on the device until REL
+                assert np.array_equal(blob[offs["X"]:offs["X"] + T * D * 4].view(np.float32), hxo.x32_tile(x))
+        print("times (us):", times[:13].tolist(), flush=True)
+        got = hxo.x32_untile(blob[offs["X"]:offs["X"] + T * D * 4].view(np.float32).copy(), T, D)
+        ref = x
+        for (wb, ow), m in zip(blocks, mods):
+            ref, _, _ = hxo.anima_block(ref, ctx, m, cos, sin, ow, H=16, F=8192, gelu=0)
+        r, c = delta_metrics(got, ref, x)
+        print(f"ABI rel err on delta {r:.2e} cos {c:.7f}", flush=True)
+        assert r < 5e-3 and c > 0.99999
+        # error paths (blk.c:110-127, :188 codes)
+        r = lib.mega_block(h, meta.ctypes.data, 32, 200, 999, mods[0].ctypes.data, mods[0].nbytes, None, 0, C.byref(rc))
+        assert r == 0 and rc.value == -7
+        r = lib.mega_block(h, meta.ctypes.data, 32, 999, 100, mods[0].ctypes.data, mods[0].nbytes, None, 0, C.byref(rc))
+        assert r == 0 and rc.value == -5
+        bad = meta.copy()
+        bad[META.index("NTOK")] = 250
+        r = lib.mega_block(h, bad.ctypes.data, 32, 200, 100, mods[0].ctypes.data, mods[0].nbytes, None, 0, C.byref(rc))
+        assert r == 0 and rc.value == -10
+    finally:
+        lib.mega_close(h)
+
+
+# ------------------------------------------------------------------------------------------------ DiT runner
+def _small_dit(hip, batch=2, nblocks=2, fmt=0):
+    bd = hip.BlockDims(0, 256, 2, 1024, 32, 128, 0, batch, 0, fmt, fmt, 1)
+    cfg = hip.DitCfg(bd, nblocks, 16, 16, 16, 256, 0)
+    p = C.c_void_p()
+    hip.check(hip.lib().hxa_dit_create(C.byref(cfg), 1234, C.byref(p)), "dit_create")
+    return p, cfg
+
+
+def _export(hip, p, which):
+    n = hip.lib().hxa_dit_export(p, which, None, 0)
+    buf = np.zeros(n, np.uint8)
+    assert hip.lib().hxa_dit_export(p, which, buf.ctypes.data, n) == n
+    return buf
+
+
+def test_dit_small_denoise_vs_oracle():
+    """4-step Euler denoise (sigmas 1, .75, .5, .25 -> 0) of a 2-block DiT, batch 2, against the oracle DiT."""
+    hip = _hip()
+    say("dit small 2 blocks batch 2 4-step denoise")
+    lib = hip.lib()
+    p, cfg = _small_dit(hip)
+    try:
+        rng = np.random.default_rng(5)
+        lat = rng.standard_normal((2, 16, 16, 16)).astype(np.float32)
+        ctx = rng.standard_normal((2, 32, 128)).astype(np.float32)
+        hip.check(lib.hxa_dit_set_inputs(p, lat.ctypes.data, ctx.ctypes.data), "set_inputs")
+        D, C4 = 256, 64
+        layout = hip.pack_layout(0, 256, 1024, 128, 0, 0)
+        blocks = [unpack_weights(_export(hip, p, k), 0, 256, 1024, 128, 0, 0, layout) for k in range(2)]
+        modws = [_export(hip, p, 2 + k).view(np.uint16).reshape(6 * D, D) for k in range(2)]
+        g = _export(hip, p, 4).view(np.uint16)
+        o = 0
+        glue = []
+        for (n, k) in ((D, C4), (D, 256), (2 * D, D), (C4, D)):
+            glue.append(g[o:o + n * k].reshape(n, k))
+            o += n * k
+        sig = [1.0, 0.75, 0.5, 0.25, 0.0]
+        ctx16 = f16(ctx)
+        v_gpu = np.zeros_like(lat)
+        hip.check(lib.hxa_dit_velocity(p, 1.0, v_gpu.ctypes.data), "velocity")
+        v_ref = oracle_anima_velocity(lat, ctx16, 1.0, blocks, modws, glue, D=D, H=2, F=1024, C4=C4, temb=256)
+        print("velocity rel err", rel(v_gpu, v_ref), flush=True)
+        assert rel(v_gpu, v_ref) < 5e-3
+        ref = lat.copy()
+        for i in range(4):
+            hip.check(lib.hxa_dit_step(p, sig[i], sig[i + 1], 1), "step")
+            ref = ref + (sig[i + 1] - sig[i]) * oracle_anima_velocity(ref, ctx16, sig[i], blocks, modws, glue, D=D, H=2,
+                                                                        F=1024, C4=C4, temb=256)
+        got = np.zeros_like(lat)
+        hip.check(lib.hxa_dit_get_latent(p, got.ctypes.data), "get_latent")
+        r, c = delta_metrics(got, ref, lat)
+        print(f"denoise rel err on delta {r:.2e} cos {c:.7f}", flush=True)
+        assert r < 5e-3 and c > 0.99999
+    finally:
+        lib.hxa_dit_destroy(p)
+
+
+def test_dit_graph_replay_matches_eager():
+    """The captured step graph replayed several times (with eager work and syncs between replays) equals the
+    eagerly launched step, bit for bit."""
+    hip = _hip()
+    say("dit graph replay vs eager")
+    lib = hip.lib()
+    rng = np.random.default_rng(6)
+    lat = rng.standard_normal((2, 16, 16, 16)).astype(np.float32)
+    ctx = rng.standard_normal((2, 32, 128)).astype(np.float32)
+    outs = []
+    for use_graph in (0, 1):
+        p, cfg = _small_dit(hip)
+        try:
+            hip.check(lib.hxa_dit_set_inputs(p, lat.ctypes.data, ctx.ctypes.data), "set_inputs")
+            res = []
+            for i, (s0, s1) in enumerate(((1.0, 0.75), (0.75, 0.5), (0.5, 0.25), (0.25, 0.0))):
+                hip.check(lib.hxa_dit_step(p, s0, s1, use_graph), "step")
+                cur = np.zeros_like(lat)
+                hip.check(lib.hxa_dit_get_latent(p, cur.ctypes.data), "get")
+                res.append(cur)
+            outs.append(res)
+        finally:
+            lib.hxa_dit_destroy(p)
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)

@@ -1,0 +1,282 @@
+"""GPU parity of the individual HIP kernels against the CPU oracle, through the C-ABI (hexanima_amd/hip.py).
+
+Tolerances (fp16 storage): GEMM / norm outputs may differ from the oracle's correctly rounded value by the fp32
+accumulation order only -> at most 1 fp16 ulp, almost all bit-identical. Attention uses an fp32 online softmax,
+so it is compared with the oracle's exact-softmax mode (max abs 4e-3, rel-l2 2e-3) and with the reference-rounding
+mode (rel-l2 1e-2, the reference's own fp16 S/P rounding noise)."""
+import numpy as np
+import pytest
+
+from oracle import hxo
+from tests._helpers import f16, rel, ulp_diff
+
+pytestmark = pytest.mark.gpu
+
+
+def _hip():
+    from hexanima_amd import hip
+    hip.init()
+    return hip
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+# ------------------------------------------------------------------------------------------------ GEMM
+def _run_gemm(hip, A, fmt, w, s, N, K, epi=0, ksplit=1, tile=None, x=None, gate=None):
+    M = A.shape[0]
+    dA = hip.DeviceArray.from_numpy(f16(A))
+    dW = hip.DeviceArray.from_numpy(w)
+    dS = hip.DeviceArray.from_numpy(s) if s is not None else None
+    if epi == hip.EPI_RESADD:
+        dx = hip.DeviceArray.from_numpy(x.astype(np.float32))
+        dg = hip.DeviceArray.from_numpy(gate.astype(np.float32))
+        out = None
+    elif epi == hip.EPI_PARTIAL:
+        out = hip.DeviceArray((ksplit, M, N), np.float16)
+    elif epi == hip.EPI_STORE_T:
+        out = hip.DeviceArray((N, M), np.float16)
+    elif epi == hip.EPI_SITU:
+        out = hip.DeviceArray((M, N // 2), np.float16)
+    else:
+        out = hip.DeviceArray((M, N), np.float16)
+    ldo = {hip.EPI_STORE_T: M, hip.EPI_SITU: N // 2}.get(epi, N)
+    args = (dA.ptr, K, M, fmt, dW.ptr, dS.ptr if dS else None, None, N, K, ksplit, epi, out.ptr if out else None, ldo,
+            M * N, dx.ptr if epi == hip.EPI_RESADD else None, N, dg.ptr if epi == hip.EPI_RESADD else None)
+    if tile:
+        hip.check(hip.lib().hxa_gemm_tile(*args, tile[0], tile[1], None), "gemm_tile")
+    else:
+        hip.check(hip.lib().hxa_gemm(*args, None, 0, 0, None), "gemm")
+    hip.sync()
+    return dx.numpy() if epi == hip.EPI_RESADD else out.numpy()
+
+
+@pytest.mark.parametrize("tile", [None, (256, 128), (128, 256), (128, 128), (64, 128), (128, 64)])
+def test_gemm_f16_tiles(tile):
+    hip = _hip()
+    say(f"gemm f16 tile={tile}")
+    rng = np.random.default_rng(0)
+    M, N, K = 320, 384, 512  # ragged in M for every tile shape
+    A = rng.standard_normal((M, K))
+    W = f16(rng.standard_normal((N, K)) * 0.05)
+    got = _run_gemm(hip, A, 0, W, None, N, K, tile=tile)
+    ref = f16(hxo.gemm(f16(A), W))
+    assert ulp_diff(got, ref).max() <= 1
+    assert np.mean(got.view(np.uint16) == ref.view(np.uint16)) > 0.98
+
+
+@pytest.mark.parametrize("N,K", [(6144, 2048), (2048, 2048), (8192, 2048), (2048, 8192)])
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_gemm_w8a16_w4a16_config1(N, K, fmt):
+    """The W8A16 / W4A16 microbench shapes (M = 1536): dequantised-fp16 GEMM is the reference."""
+    hip = _hip()
+    say(f"gemm fmt={fmt} M=1536 N={N} K={K}")
+    rng = np.random.default_rng(N + K + fmt)
+    M = 1536
+    A = f16(rng.standard_normal((M, K)))
+    s = np.full((K // 32, N), np.float16(0.02 / 127)).view(np.uint16)
+    if fmt == 1:
+        q = rng.integers(-127, 128, (N, K)).astype(np.int8)
+        wdq = hxo.q8_dequant(q, s)
+    else:
+        qv = rng.integers(-8, 8, (N, K))
+        q = np.zeros((N, K // 8), np.uint32)
+        for j in range(8):
+            sh = 16 + 4 * (j // 2) if j % 2 else 4 * (j // 2)
+            q |= ((qv[:, j::8] + 8).astype(np.uint32) << sh)
+        q = q.view(np.uint8).reshape(N, K // 2)
+        wdq = hxo.q4_dequant(q, s)
+        assert np.array_equal(wdq.view(np.float16).astype(np.float32), (qv * np.float32(np.float16(0.02 / 127))).astype(np.float16).astype(np.float32))
+    got = _run_gemm(hip, A, fmt, q, s, N, K)
+    ref = f16(hxo.gemm(A, wdq))
+    d = ulp_diff(got, ref)
+    assert d.max() <= 1, d.max()
+    assert np.mean(d == 0) > 0.98
+
+
+def test_gemm_epilogues():
+    hip = _hip()
+    rng = np.random.default_rng(3)
+    M, N, K = 256, 512, 256
+    A = f16(rng.standard_normal((M, K)))
+    W = f16(rng.standard_normal((N, K)) * 0.1)
+    t = f16(hxo.gemm(A, W))
+    say("gemm epi gelu tanh / erf")
+    for epi, mode in ((1, 1), (2, 0)):
+        got = _run_gemm(hip, A, 0, W, None, N, K, epi=epi)
+        ref = hxo.gelu(t, mode).view(np.float16)
+        assert ulp_diff(got, ref).max() <= 2
+    say("gemm epi store_t")
+    got = _run_gemm(hip, A, 0, W, None, N, K, epi=4)
+    assert ulp_diff(got.T, t).max() <= 1
+    say("gemm epi resadd")
+    x = rng.standard_normal((M, N)).astype(np.float32)
+    g = rng.standard_normal(N).astype(np.float32)
+    got = _run_gemm(hip, A, 0, W, None, N, K, epi=3, x=x, gate=g)
+    # x + g * f16(acc); the f16(acc) may differ by one ulp from the oracle's rounding
+    assert np.allclose(got, hxo.resadd(x, t, g), atol=np.abs(g).max() * 2e-3 * np.abs(t.astype(np.float32)).max())
+    say("gemm epi partial (split-K 2)")
+    got = _run_gemm(hip, A, 0, W, None, N, K, epi=6, ksplit=2)
+    r0 = f16(hxo.gemm(np.ascontiguousarray(A[:, :K // 2]), np.ascontiguousarray(W[:, :K // 2])))
+    r1 = f16(hxo.gemm(np.ascontiguousarray(A[:, K // 2:]), np.ascontiguousarray(W[:, K // 2:])))
+    assert ulp_diff(got[0], r0).max() <= 1 and ulp_diff(got[1], r1).max() <= 1
+    say("gemm epi situ (interleaved up/gate)")
+    F = N // 2
+    up = np.ascontiguousarray(W.reshape(F // 32, 2, 32, K)[:, 0].reshape(F, K))
+    gt = np.ascontiguousarray(W.reshape(F // 32, 2, 32, K)[:, 1].reshape(F, K))
+    got = _run_gemm(hip, A, 0, W, None, N, K, epi=5)
+    ref = hxo.situ(f16(hxo.gemm(A, up)), f16(hxo.gemm(A, gt))).view(np.float16)
+    assert ulp_diff(got, ref).max() <= 2
+
+
+def test_gemm_fused_qkv_split_transposed():
+    hip = _hip()
+    say("gemm fused qkv with transposed v")
+    rng = np.random.default_rng(4)
+    M, D = 256, 256
+    A = f16(rng.standard_normal((M, D)))
+    W = f16(rng.standard_normal((3 * D, D)) * 0.05)
+    dA, dW = hip.DeviceArray.from_numpy(A), hip.DeviceArray.from_numpy(W)
+    qk = hip.DeviceArray((M, 2 * D), np.float16)
+    vt = hip.DeviceArray((D, M), np.float16)
+    hip.check(hip.lib().hxa_gemm(dA.ptr, D, M, 0, dW.ptr, None, None, 3 * D, D, 1, 0, qk.ptr, 2 * D, 0, None, 0, None,
+                                 vt.ptr, M, 2 * D, None), "qkv")
+    hip.sync()
+    ref = f16(hxo.gemm(A, W))
+    assert ulp_diff(qk.numpy(), ref[:, :2 * D]).max() <= 1
+    assert ulp_diff(vt.numpy().T, ref[:, 2 * D:]).max() <= 1
+
+
+def test_gemm_rejects_bad_shapes():
+    hip = _hip()
+    say("gemm argument checks")
+    dA = hip.DeviceArray((64, 96), np.float16, zero=True)
+    dW = hip.DeviceArray((64, 96), np.float16, zero=True)
+    out = hip.DeviceArray((64, 64), np.float16)
+    rc = hip.lib().hxa_gemm(dA.ptr, 96, 64, 0, dW.ptr, None, None, 64, 96, 1, 0, out.ptr, 64, 0, None, 0, None, None, 0, 0, None)
+    assert rc == -12  # K % 64 != 0
+    rc = hip.lib().hxa_gemm(dA.ptr, 96, 64, 1, dW.ptr, None, None, 64, 64, 1, 0, out.ptr, 64, 0, None, 0, None, None, 0, 0, None)
+    assert rc == -12  # q8 without scales
+
+
+# ------------------------------------------------------------------------------------------------ attention
+def _attn(hip, q, k, v, nvalid=None, batch=1):
+    T, D = q.shape[0] // batch, q.shape[1]
+    NKV = k.shape[0] // batch
+    H = D // 128
+    dq, dk = hip.DeviceArray.from_numpy(f16(q)), hip.DeviceArray.from_numpy(f16(k))
+    vt = np.ascontiguousarray(f16(v).T)  # [D][batch*NKV]
+    dv = hip.DeviceArray.from_numpy(vt)
+    do = hip.DeviceArray((batch * T, D), np.float16)
+    hip.check(hip.lib().hxa_attention(dq.ptr, D, dk.ptr, D, dv.ptr, batch * NKV, do.ptr, D, T, NKV,
+                                      NKV if nvalid is None else nvalid, H, batch, T * D, NKV * D, NKV, T * D, None), "attn")
+    hip.sync()
+    return do.numpy()
+
+
+@pytest.mark.parametrize("T,NKV,nvalid,H", [(1536, 1536, 1536, 16), (1536, 256, 256, 16), (448, 448, 430, 4), (96, 64, 64, 2)])
+def test_attention_vs_oracle(T, NKV, nvalid, H):
+    hip = _hip()
+    say(f"attention T={T} NKV={NKV} nvalid={nvalid} H={H}")
+    rng = np.random.default_rng(T + NKV)
+    D = 128 * H
+    # unit-RMS q/k heads with the 1/sqrt(128) gain folded into q, as after the RMS+RoPE stage
+    q = f16(rng.standard_normal((T, D)) / np.sqrt(128) * 2.0)
+    k = f16(rng.standard_normal((NKV, D)))
+    v = f16(rng.standard_normal((NKV, D)))
+    got = _attn(hip, q, k, v, nvalid).astype(np.float64)
+    exact = hxo.attention(q, k, v, nvalid, mode=1).view(np.float16).astype(np.float64)
+    refr = hxo.attention(q, k, v, nvalid, mode=0).view(np.float16).astype(np.float64)
+    assert np.max(np.abs(got - exact)) < 4e-3
+    assert rel(got, exact) < 2e-3
+    assert rel(got, refr) < 1e-2
+
+
+def test_attention_batched_images_are_independent():
+    hip = _hip()
+    say("attention batch=3")
+    rng = np.random.default_rng(9)
+    T, NKV, D = 128, 96, 256
+    q = f16(rng.standard_normal((3 * T, D)) * 0.2)
+    k = f16(rng.standard_normal((3 * NKV, D)))
+    v = f16(rng.standard_normal((3 * NKV, D)))
+    got = _attn(hip, q, k, v, batch=3)
+    for b in range(3):
+        one = _attn(hip, q[b * T:(b + 1) * T], k[b * NKV:(b + 1) * NKV], v[b * NKV:(b + 1) * NKV])
+        assert np.array_equal(got[b * T:(b + 1) * T], one)
+
+
+# ------------------------------------------------------------------------------------------------ elementwise
+@pytest.mark.parametrize("D", [2048, 2560, 3072])
+@pytest.mark.parametrize("rms", [False, True])
+def test_norm_mod(D, rms):
+    hip = _hip()
+    say(f"norm_mod D={D} rms={rms}")
+    rng = np.random.default_rng(D)
+    T = 96
+    x = (rng.standard_normal((T, D)) * 3 + 0.5).astype(np.float32)
+    sh, sc, w = (rng.standard_normal(D).astype(np.float32) * 0.3 for _ in range(3))
+    dx, dsh, dsc, dw = (hip.DeviceArray.from_numpy(a) for a in (x, sh, sc, w))
+    h = hip.DeviceArray((T, D), np.float16)
+    hip.check(hip.lib().hxa_norm_mod(dx.ptr, D, T, D, dsh.ptr, dsc.ptr, dw.ptr if rms else None, 1e-6, h.ptr, D, None), "norm")
+    hip.sync()
+    ref = hxo.rmsmod(x, w, sh, sc) if rms else hxo.lnmod(x, sh, sc)
+    assert ulp_diff(h.numpy(), ref.view(np.float16)).max() <= 1
+
+
+@pytest.mark.parametrize("rope", [False, True])
+def test_rmsrope(rope):
+    hip = _hip()
+    say(f"rmsrope rope={rope}")
+    rng = np.random.default_rng(11)
+    T, D = 256, 512
+    q = f16(rng.standard_normal((T, D)) * 2)
+    g = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    cos, sin = hxo.rope_anima(16, 16)
+    dq = hip.DeviceArray.from_numpy(q)
+    dg = hip.DeviceArray.from_numpy(g)
+    dc, ds = hip.DeviceArray.from_numpy(cos), hip.DeviceArray.from_numpy(sin)
+    hip.check(hip.lib().hxa_rmsrope(dq.ptr, None, dg.ptr, None, D, T, D // 128, dc.ptr if rope else None,
+                                    ds.ptr if rope else None, T, None), "rmsrope")
+    hip.sync()
+    ref = hxo.rmsrope(q, g, cos if rope else None, sin if rope else None).view(np.float16)
+    assert ulp_diff(dq.numpy(), ref).max() <= 1
+
+
+def test_resadd2_and_tile_conversions():
+    hip = _hip()
+    say("resadd2 + x32 conversions")
+    rng = np.random.default_rng(12)
+    T, D = 64, 256
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    t1, t2 = f16(rng.standard_normal((T, D))), f16(rng.standard_normal((T, D)))
+    g = rng.standard_normal(D).astype(np.float32)
+    dx, d1, d2, dg = (hip.DeviceArray.from_numpy(a) for a in (x, t1, t2, g))
+    hip.check(hip.lib().hxa_resadd2(dx.ptr, D, d1.ptr, d2.ptr, D, T, D, dg.ptr, None), "resadd2")
+    hip.sync()
+    assert np.array_equal(dx.numpy(), hxo.resadd2(x, t1, t2, g))
+    tiles = hxo.x32_tile(x)
+    dt = hip.DeviceArray.from_numpy(tiles)
+    rows = hip.DeviceArray((T, D), np.float32)
+    hip.check(hip.lib().hxa_x32_to_rows(dt.ptr, rows.ptr, T, D, None), "x32_to_rows")
+    back = hip.DeviceArray((T * D,), np.float32)
+    hip.check(hip.lib().hxa_rows_to_x32(rows.ptr, back.ptr, T, D, None), "rows_to_x32")
+    hip.sync()
+    assert np.array_equal(rows.numpy(), x) and np.array_equal(back.numpy(), tiles)
+
+
+def test_quantize_matches_oracle():
+    hip = _hip()
+    say("quantize q8 / q4")
+    rng = np.random.default_rng(13)
+    N, K = 96, 256
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    W[5, :32] = 0
+    dW = hip.DeviceArray.from_numpy(W)
+    for fmt, (qo, so) in ((1, hxo.q8_quantize(W)), (2, hxo.q4_quantize(W))):
+        q = hip.DeviceArray(qo.shape, qo.dtype)
+        s = hip.DeviceArray(so.shape, np.uint16)
+        hip.check(hip.lib().hxa_quantize(dW.ptr, N, K, fmt, q.ptr, s.ptr, None), "quantize")
+        hip.sync()
+        assert np.array_equal(s.numpy(), so) and np.array_equal(q.numpy(), qo)
