@@ -71,8 +71,9 @@ HXA_DEV void dq4_word(uint32_t d, half2_t s2, half2_t z2, uint32_t *o) {
 }
 
 HXA_DEV float gelu_tanh_f(float t) {
+  // 0.5 t (1 + tanh u) written as t / (1 + exp(-2u)) (kern.c:116-132): no cancellation for negative t
   const float u = 0.7978845608028654f * (t + 0.044715f * t * t * t);
-  return 0.5f * t * (1.0f + tanhf(u));
+  return t / (1.0f + __expf(-2.0f * u));
 }
 HXA_DEV float gelu_erf_f(float t) {
   // kern.c:248-260: f16(max(t,0) - T2(|t|)), T2 = f16(|t| * 0.5 * erfc(|t|/sqrt 2))
@@ -90,12 +91,16 @@ HXA_DEV float situ_f(float u, float g) {
 template <int BM, int BN, int FMT, bool ASYM>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   constexpr int WTM = BM / 2, WTN = BN / 2, MI = WTM / 32, NI = WTN / 32;
-  constexpr int CA = BM / 32;                                   // 16-byte A chunks per thread per stage
-  constexpr int CB = FMT == HXA_W_F16 ? BN / 32 : FMT == HXA_W_Q8 ? BN / 64 : BN / 128;
-  static_assert(CB >= 1, "tile too narrow for this weight format");
+  constexpr int CA = BM * 8 / 256;                                   // 16-byte A chunks per thread per stage
+  constexpr int CPR = FMT == HXA_W_F16 ? 8 : FMT == HXA_W_Q8 ? 4 : 2;  // 16-byte W chunks per row per stage
+  constexpr int NCB = BN * CPR;                                      // W chunks per stage
+  constexpr int CB = (NCB + 255) / 256;
+  constexpr int STAGE = (BM + BN) * LDS_ROW;
+  constexpr int CROW = BN + 8;                                       // epilogue C tile row (halves)
+  static_assert(BM * 8 % 256 == 0, "A tile must split evenly over 256 threads");
+  static_assert(BM * CROW <= 2 * STAGE, "C tile must fit in the main-loop LDS");
   extern __shared__ __attribute__((aligned(16))) hxa_h lds[];
   hxa_h *const As0 = lds, *const Bs0 = lds + BM * LDS_ROW;
-  constexpr int STAGE = (BM + BN) * LDS_ROW;
 
   const int ntiles = p.tiles_m * p.tiles_n;
   const int bid = blockIdx.x;
@@ -108,11 +113,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
 
-  float16_t acc[MI][NI];
+  // acc[j][i]: 32x32 block of output columns j (A operand of the MFMA = W rows) and rows i (B operand = A rows)
+  float16_t acc[NI][MI];
 #pragma unroll
-  for (int i = 0; i < MI; i++)
+  for (int j = 0; j < NI; j++)
 #pragma unroll
-    for (int j = 0; j < NI; j++) acc[i][j] = (float16_t){};
+    for (int i = 0; i < MI; i++) acc[j][i] = (float16_t){};
 
   uint4_t ra[CA];
   uint4_t rb[CB];
@@ -129,20 +135,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < CB; i++) {
       const int c = tid + i * 256;
-      if (FMT == HXA_W_F16) {
-        const int r = c >> 3, cc = c & 7, n = n0 + r;
-        rb[i] = n < p.N ? *(const uint4_t *)((const hxa_h *)p.W + (long)n * p.ldw + k0 + cc * 8) : (uint4_t){0, 0, 0, 0};
-      } else if (FMT == HXA_W_Q8) {
-        const int r = c >> 2, cc = c & 3, n = n0 + r;
-        const int kk = k0 + cc * 16;
-        rb[i] = n < p.N ? *(const uint4_t *)((const int8_t *)p.W + (long)n * p.ldw + kk) : (uint4_t){0, 0, 0, 0};
-        rs[i] = n < p.N ? p.S[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
-      } else {
-        const int r = c >> 1, cc = c & 1, n = n0 + r;
-        const int kk = k0 + cc * 32;
-        rb[i] = n < p.N ? *(const uint4_t *)((const uint8_t *)p.W + (long)n * p.ldw + (kk >> 1)) : (uint4_t){0, 0, 0, 0};
-        rs[i] = n < p.N ? p.S[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
-        if (ASYM) rz[i] = n < p.N ? p.Z[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
+      if (NCB % 256 == 0 || c < NCB) {
+        if (FMT == HXA_W_F16) {
+          const int r = c >> 3, cc = c & 7, n = n0 + r;
+          rb[i] = n < p.N ? *(const uint4_t *)((const hxa_h *)p.W + (long)n * p.ldw + k0 + cc * 8) : (uint4_t){0, 0, 0, 0};
+        } else if (FMT == HXA_W_Q8) {
+          const int r = c >> 2, cc = c & 3, n = n0 + r;
+          const int kk = k0 + cc * 16;
+          rb[i] = n < p.N ? *(const uint4_t *)((const int8_t *)p.W + (long)n * p.ldw + kk) : (uint4_t){0, 0, 0, 0};
+          rs[i] = n < p.N ? p.S[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
+        } else {
+          const int r = c >> 1, cc = c & 1, n = n0 + r;
+          const int kk = k0 + cc * 32;
+          rb[i] = n < p.N ? *(const uint4_t *)((const uint8_t *)p.W + (long)n * p.ldw + (kk >> 1)) : (uint4_t){0, 0, 0, 0};
+          rs[i] = n < p.N ? p.S[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
+          if (ASYM) rz[i] = n < p.N ? p.Z[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
+        }
       }
     }
   };
@@ -156,31 +164,33 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < CB; i++) {
       const int c = tid + i * 256;
-      if (FMT == HXA_W_F16) {
-        const int r = c >> 3, cc = c & 7;
-        *(uint4_t *)(Bs + r * LDS_ROW + cc * 8) = rb[i];
-      } else if (FMT == HXA_W_Q8) {
-        const int r = c >> 2, cc = c & 3;
-        const half2_t s2 = {rs[i], rs[i]};
-        uint32_t o[8];
-        dq8_word(rb[i].x, s2, o[0], o[1]);
-        dq8_word(rb[i].y, s2, o[2], o[3]);
-        dq8_word(rb[i].z, s2, o[4], o[5]);
-        dq8_word(rb[i].w, s2, o[6], o[7]);
-        *(uint4_t *)(Bs + r * LDS_ROW + cc * 16) = (uint4_t){o[0], o[1], o[2], o[3]};
-        *(uint4_t *)(Bs + r * LDS_ROW + cc * 16 + 8) = (uint4_t){o[4], o[5], o[6], o[7]};
-      } else {
-        const int r = c >> 1, cc = c & 1;
-        const half2_t s2 = {rs[i], rs[i]};
-        const half2_t z2 = ASYM ? (half2_t){rz[i], rz[i]} : (half2_t){};
-        uint32_t o[16];
-        dq4_word<ASYM>(rb[i].x, s2, z2, o + 0);
-        dq4_word<ASYM>(rb[i].y, s2, z2, o + 4);
-        dq4_word<ASYM>(rb[i].z, s2, z2, o + 8);
-        dq4_word<ASYM>(rb[i].w, s2, z2, o + 12);
+      if (NCB % 256 == 0 || c < NCB) {
+        if (FMT == HXA_W_F16) {
+          const int r = c >> 3, cc = c & 7;
+          *(uint4_t *)(Bs + r * LDS_ROW + cc * 8) = rb[i];
+        } else if (FMT == HXA_W_Q8) {
+          const int r = c >> 2, cc = c & 3;
+          const half2_t s2 = {rs[i], rs[i]};
+          uint32_t o[8];
+          dq8_word(rb[i].x, s2, o[0], o[1]);
+          dq8_word(rb[i].y, s2, o[2], o[3]);
+          dq8_word(rb[i].z, s2, o[4], o[5]);
+          dq8_word(rb[i].w, s2, o[6], o[7]);
+          *(uint4_t *)(Bs + r * LDS_ROW + cc * 16) = (uint4_t){o[0], o[1], o[2], o[3]};
+          *(uint4_t *)(Bs + r * LDS_ROW + cc * 16 + 8) = (uint4_t){o[4], o[5], o[6], o[7]};
+        } else {
+          const int r = c >> 1, cc = c & 1;
+          const half2_t s2 = {rs[i], rs[i]};
+          const half2_t z2 = ASYM ? (half2_t){rz[i], rz[i]} : (half2_t){};
+          uint32_t o[16];
+          dq4_word<ASYM>(rb[i].x, s2, z2, o + 0);
+          dq4_word<ASYM>(rb[i].y, s2, z2, o + 4);
+          dq4_word<ASYM>(rb[i].z, s2, z2, o + 8);
+          dq4_word<ASYM>(rb[i].w, s2, z2, o + 12);
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-          *(uint4_t *)(Bs + r * LDS_ROW + cc * 32 + q * 8) = (uint4_t){o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+          for (int q = 0; q < 4; q++)
+            *(uint4_t *)(Bs + r * LDS_ROW + cc * 32 + q * 8) = (uint4_t){o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+        }
       }
     }
   };
@@ -195,9 +205,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < NI; j++) b[j] = *(const half8_t *)(Bs + (wn * WTN + j * 32 + (lane & 31)) * LDS_ROW + col);
 #pragma unroll
-      for (int i = 0; i < MI; i++)
+      for (int j = 0; j < NI; j++)
 #pragma unroll
-        for (int j = 0; j < NI; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < MI; i++) acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[j][i], 0, 0, 0);
     }
   };
 
@@ -213,73 +223,96 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     __syncthreads();
   }
 
-  // ---- epilogue: lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + (r%4) of each 32x32 block ----
-  const int rbase = m0 + wm * WTM + 4 * (lane >> 5);
-  const int cbase = n0 + wn * WTN + (lane & 31);
-  if (p.epi == HXA_EPI_SITU) {
-    // wave columns [n0 + wn*WTN, +WTN) hold NI/2 (up, gate) block pairs
-    const int pair0 = (n0 + wn * WTN) / 64;
+  // ---- epilogue. Stage f16(acc) through LDS as a row-major [BM][CROW] tile: lane holds, for block (j, i),
+  // row i*32 + (lane & 31) and columns j*32 + 8q + 4*(lane/32) + 0..3 (q = 0..3) -> one 8-byte write each.
+  hxa_h *Cs = lds;
+  {
+    const int ml = wm * WTM + (lane & 31), nl = wn * WTN + 4 * (lane >> 5);
 #pragma unroll
-    for (int i = 0; i < MI; i++)
+    for (int j = 0; j < NI; j++)
 #pragma unroll
-      for (int jp = 0; jp < NI / 2; jp++)
+      for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int row = rbase + i * 32 + 8 * (r >> 2) + (r & 3);
-          const int col = (pair0 + jp) * 32 + (lane & 31);
-          if (row < p.M && col * 2 < p.N) {
-            const float u = (float)(hxa_h)acc[i][2 * jp][r], g = (float)(hxa_h)acc[i][2 * jp + 1][r];
-            p.out[(long)row * p.ldo + col] = (hxa_h)situ_f(u, g);
-          }
+        for (int q = 0; q < 4; q++) {
+          const half4_t v = {(hxa_h)acc[j][i][4 * q], (hxa_h)acc[j][i][4 * q + 1], (hxa_h)acc[j][i][4 * q + 2],
+                             (hxa_h)acc[j][i][4 * q + 3]};
+          *(half4_t *)(Cs + (ml + i * 32) * CROW + nl + j * 32 + 8 * q) = v;
         }
+  }
+  __syncthreads();
+  // Cooperative pass over 8-column chunks: coalesced 16-byte loads / stores.
+  constexpr int C8 = BN / 8;
+  if (p.epi == HXA_EPI_SITU) {
+    // columns interleaved per 32 (up_j, gate_j): output column (n0/2) + p*32 + c
+    for (int c = tid; c < BM * (C8 / 2); c += 256) {
+      const int ml = c / (C8 / 2), oc = (c % (C8 / 2)) * 8;
+      const int m = m0 + ml, on = n0 / 2 + oc;
+      if (m >= p.M || on * 2 >= p.N) continue;
+      const int pr = oc / 32, cc = oc % 32;
+      const half8_t u = *(const half8_t *)(Cs + ml * CROW + pr * 64 + cc);
+      const half8_t g = *(const half8_t *)(Cs + ml * CROW + pr * 64 + 32 + cc);
+      half8_t o;
+#pragma unroll
+      for (int e = 0; e < 8; e++) o[e] = (hxa_h)situ_f((float)u[e], (float)g[e]);
+      *(half8_t *)(p.out + (long)m * p.ldo + on) = o;
+    }
     return;
   }
+  // local columns [0, nsplit) row-major, [nsplit, BN) transposed into out_t
+  const int nsplit = p.out_t == nullptr ? BN : min(max(p.split_col - n0, 0), BN);
+  for (int c = tid; c < BM * (nsplit / 8); c += 256) {
+    const int ml = c / (nsplit / 8), nl = (c % (nsplit / 8)) * 8;
+    const int m = m0 + ml, n = n0 + nl;
+    if (m >= p.M || n >= p.N) continue;
+    half8_t v = *(const half8_t *)(Cs + ml * CROW + nl);
+    const long o = (long)m * p.ldo + n;
+    if (p.epi == HXA_EPI_RESADD) {
+      float4_t *xp = (float4_t *)(p.x + (long)m * p.ldx + n);
+      const float4_t g0 = *(const float4_t *)(p.gate + n), g1 = *(const float4_t *)(p.gate + n + 4);
+      float4_t x0 = xp[0], x1 = xp[1];
 #pragma unroll
-  for (int i = 0; i < MI; i++)
-#pragma unroll
-    for (int j = 0; j < NI; j++) {
-      const int col = cbase + j * 32;
-      if (col >= p.N) continue;
-      if (p.out_t != nullptr && col >= p.split_col) {
-#pragma unroll
-        for (int r4 = 0; r4 < 4; r4++) {
-          const int row = rbase + i * 32 + 8 * r4;
-          hxa_h *dst = p.out_t + (long)(col - p.split_col) * p.ldo_t + row;
-          if (row + 3 < p.M) {
-            const half4_t v = {(hxa_h)acc[i][j][4 * r4], (hxa_h)acc[i][j][4 * r4 + 1], (hxa_h)acc[i][j][4 * r4 + 2], (hxa_h)acc[i][j][4 * r4 + 3]};
-            *(half4_t *)dst = v;
-          } else {
-            for (int e = 0; e < 4; e++)
-              if (row + e < p.M) dst[e] = (hxa_h)acc[i][j][4 * r4 + e];
-          }
-        }
-        continue;
+      for (int e = 0; e < 4; e++) {
+        x0[e] = fmaf(g0[e], (float)v[e], x0[e]);
+        x1[e] = fmaf(g1[e], (float)v[e + 4], x1[e]);
       }
-      const float g = p.epi == HXA_EPI_RESADD ? p.gate[col] : 0.0f;
+      xp[0] = x0;
+      xp[1] = x1;
+    } else if (p.epi == HXA_EPI_PARTIAL) {
+      *(half8_t *)(p.out + (long)z * p.out_zstride + o) = v;
+    } else {
+      if (p.epi == HXA_EPI_GELU_TANH) {
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = rbase + i * 32 + 8 * (r >> 2) + (r & 3);
-        if (row >= p.M) continue;
-        const hxa_h t = (hxa_h)acc[i][j][r];
-        switch (p.epi) {
-          case HXA_EPI_STORE: p.out[(long)row * p.ldo + col] = t; break;
-          case HXA_EPI_GELU_TANH: p.out[(long)row * p.ldo + col] = (hxa_h)gelu_tanh_f((float)t); break;
-          case HXA_EPI_GELU_ERF: p.out[(long)row * p.ldo + col] = (hxa_h)gelu_erf_f((float)t); break;
-          case HXA_EPI_RESADD: {
-            float *xp = p.x + (long)row * p.ldx + col;
-            *xp = fmaf(g, (float)t, *xp);
-          } break;
-          case HXA_EPI_PARTIAL: p.out[(long)z * p.out_zstride + (long)row * p.ldo + col] = t; break;
-          default: break;
-        }
+        for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_tanh_f((float)v[e]);
+      } else if (p.epi == HXA_EPI_GELU_ERF) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_erf_f((float)v[e]);
+      }
+      *(half8_t *)(p.out + o) = v;
+    }
+  }
+  if (nsplit < BN) {  // transposed columns: chunk = (column, 8 consecutive rows)
+    const int ncol = BN - nsplit;
+    for (int c = tid; c < ncol * (BM / 8); c += 256) {
+      const int nl = nsplit + c / (BM / 8), ml = (c % (BM / 8)) * 8;
+      const int n = n0 + nl, m = m0 + ml;
+      if (n >= p.N || m >= p.M) continue;
+      half8_t v;
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = Cs[(ml + e) * CROW + nl];
+      hxa_h *dst = p.out_t + (long)(n - p.split_col) * p.ldo_t + m;
+      if (m + 7 < p.M) {
+        *(half8_t *)dst = v;
+      } else {
+        for (int e = 0; e < 8 && m + e < p.M; e++) dst[e] = v[e];
       }
     }
+  }
 }
 
 struct TileCfg {
   int bm, bn;
 };
-constexpr TileCfg kCfgs[] = {{256, 128}, {128, 256}, {128, 128}, {64, 128}, {128, 64}};
+constexpr TileCfg kCfgs[] = {{192, 256}, {192, 192}, {192, 128}, {256, 128}, {128, 256}, {128, 128}, {64, 128}, {128, 64}};
 
 template <int BM, int BN, int FMT, bool ASYM>
 hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
@@ -298,6 +331,9 @@ hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
 
 template <int FMT, bool ASYM>
 hipError_t launch_fmt(int bm, int bn, const GemmParams &p, int ksplit, hipStream_t st) {
+  if (bm == 192 && bn == 256) return launch_t<192, 256, FMT, ASYM>(p, ksplit, st);
+  if (bm == 192 && bn == 192) return launch_t<192, 192, FMT, ASYM>(p, ksplit, st);
+  if (bm == 192 && bn == 128) return launch_t<192, 128, FMT, ASYM>(p, ksplit, st);
   if (bm == 256 && bn == 128) return launch_t<256, 128, FMT, ASYM>(p, ksplit, st);
   if (bm == 128 && bn == 256) return launch_t<128, 256, FMT, ASYM>(p, ksplit, st);
   if (bm == 128 && bn == 128) return launch_t<128, 128, FMT, ASYM>(p, ksplit, st);
@@ -323,7 +359,7 @@ static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int *bm, int *
   double best = -1.0;
   for (const TileCfg &c : kCfgs) {
     if (fmt == HXA_W_Q4 && c.bn < 128) continue;
-    if (epi == HXA_EPI_SITU && c.bn < 128) continue;
+    if (epi == HXA_EPI_SITU && c.bn % 128 != 0) continue;  // each wave needs whole (up, gate) block pairs
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ksplit;
     const long waves = (tiles + g_num_cu - 1) / g_num_cu;
     const double useful = (double)M * N / ((double)((M + c.bm - 1) / c.bm) * c.bm * ((N + c.bn - 1) / c.bn) * c.bn);
@@ -343,6 +379,10 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   if (w.fmt != HXA_W_F16 && w.s == nullptr) return HXA_E_ARG;
   if (g.epi == HXA_EPI_SITU && (w.N % 64) != 0) return HXA_E_ARG;
   if ((g.lda % 8) != 0 || ((uintptr_t)g.A % 16) != 0 || ((uintptr_t)w.w % 16) != 0) return HXA_E_ARG;
+  if (w.N % 8 != 0) return HXA_E_ARG;  // 16-byte epilogue chunks
+  if (g.epi == HXA_EPI_RESADD ? ((g.ldx % 8) != 0 || ((uintptr_t)g.x % 32) != 0 || ((uintptr_t)g.gate % 32) != 0)
+                              : ((g.ldo % 8) != 0 || ((uintptr_t)g.out % 16) != 0))
+    return HXA_E_ARG;
   GemmParams p{};
   if (g.epi == HXA_EPI_STORE_T) {  // all columns transposed
     p.out_t = g.out;
@@ -354,7 +394,7 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
     p.ldo_t = g.ldo_t;
     p.split_col = g.split_col;
   }
-  if (p.out_t != nullptr && ((p.ldo_t % 4) != 0 || ((uintptr_t)p.out_t % 8) != 0)) return HXA_E_ARG;
+  if (p.out_t != nullptr && ((p.ldo_t % 8) != 0 || ((uintptr_t)p.out_t % 16) != 0)) return HXA_E_ARG;
   p.A = g.A;
   p.lda = g.lda;
   p.W = w.w;
@@ -377,7 +417,7 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   if (g.force_bm) {
     bm = g.force_bm;
     bn = g.force_bn;
-    if ((g.epi == HXA_EPI_SITU || w.fmt == HXA_W_Q4) && bn < 128) return HXA_E_ARG;  // needs >= 2 column blocks per wave
+    if ((g.epi == HXA_EPI_SITU && bn % 128 != 0) || (w.fmt == HXA_W_Q4 && bn < 128)) return HXA_E_ARG;
   }
   p.tiles_m = (g.M + bm - 1) / bm;
   p.tiles_n = (w.N + bn - 1) / bn;

@@ -93,3 +93,24 @@ def oracle_anima_velocity(lat, ctx16, sigma, blocks, modws, glue, *, D, H, F, C4
         xn = hxo.final_norm(x, fm[:D], fm[D:])
         out[b] = hxo.unpatchify(hxo.linear_f32(xn, Wfin), Cc, Hl, Wl)
     return out
+
+
+def gemm_bound(A16, W16):
+    """Per-element bound on |f16(fp32-accumulated A.W^T) - f16(exact)|: one fp16 ulp of the result plus the fp32
+    accumulation-order error 4 sqrt(K) 2^-24 sum_k |a_k w_k| (probabilistic form of the gamma_K bound)."""
+    K = A16.shape[1]
+    absdot = hxo.gemm(np.abs(np.asarray(A16, np.float16)), np.abs(np.asarray(W16, np.float16))).astype(np.float64)
+    return absdot * 4.0 * np.sqrt(K) * 2.0 ** -24
+
+
+def assert_gemm_close(got16, ref32, A16, W16, ident=0.98):
+    """GEMM parity: |got - f16(ref)| <= ulp(|ref|) + accumulation bound, and >= ident of the outputs bit-identical."""
+    g = np.asarray(got16, np.float16).astype(np.float64)
+    r16 = np.asarray(ref32, np.float32).astype(np.float16)
+    r = r16.astype(np.float64)
+    ulp = np.spacing(np.maximum(np.abs(r), 2.0 ** -14).astype(np.float16)).astype(np.float64)
+    tol = ulp + gemm_bound(A16, W16)
+    err = np.abs(g - r)
+    assert np.all(err <= tol), f"max excess {np.max(err - tol):.3e}"
+    same = np.mean(np.asarray(got16, np.float16).view(np.uint16) == r16.view(np.uint16))
+    assert same >= ident, f"only {same:.4f} bit-identical"

@@ -1,14 +1,15 @@
 """GPU parity of the individual HIP kernels against the CPU oracle, through the C-ABI (hexanima_amd/hip.py).
 
-Tolerances (fp16 storage): GEMM / norm outputs may differ from the oracle's correctly rounded value by the fp32
-accumulation order only -> at most 1 fp16 ulp, almost all bit-identical. Attention uses an fp32 online softmax,
+Tolerances (fp16 storage): a GEMM output may differ from the oracle's correctly rounded value by one fp16 ulp plus
+the fp32 accumulation-order error 4 sqrt(K) 2^-24 sum|a w| (tests/_helpers.assert_gemm_close), and >= 98% of the
+outputs must be bit-identical; norm outputs by at most 1 ulp. Attention uses an fp32 online softmax,
 so it is compared with the oracle's exact-softmax mode (max abs 4e-3, rel-l2 2e-3) and with the reference-rounding
 mode (rel-l2 1e-2, the reference's own fp16 S/P rounding noise)."""
 import numpy as np
 import pytest
 
 from oracle import hxo
-from tests._helpers import f16, rel, ulp_diff
+from tests._helpers import assert_gemm_close, f16, rel, ulp_diff
 
 pytestmark = pytest.mark.gpu
 
@@ -52,7 +53,7 @@ def _run_gemm(hip, A, fmt, w, s, N, K, epi=0, ksplit=1, tile=None, x=None, gate=
     return dx.numpy() if epi == hip.EPI_RESADD else out.numpy()
 
 
-@pytest.mark.parametrize("tile", [None, (256, 128), (128, 256), (128, 128), (64, 128), (128, 64)])
+@pytest.mark.parametrize("tile", [None, (192, 256), (192, 192), (192, 128), (256, 128), (128, 256), (128, 128), (64, 128), (128, 64)])
 def test_gemm_f16_tiles(tile):
     hip = _hip()
     say(f"gemm f16 tile={tile}")
@@ -61,9 +62,7 @@ def test_gemm_f16_tiles(tile):
     A = rng.standard_normal((M, K))
     W = f16(rng.standard_normal((N, K)) * 0.05)
     got = _run_gemm(hip, A, 0, W, None, N, K, tile=tile)
-    ref = f16(hxo.gemm(f16(A), W))
-    assert ulp_diff(got, ref).max() <= 1
-    assert np.mean(got.view(np.uint16) == ref.view(np.uint16)) > 0.98
+    assert_gemm_close(got, hxo.gemm(f16(A), W), f16(A), W)
 
 
 @pytest.mark.parametrize("N,K", [(6144, 2048), (2048, 2048), (8192, 2048), (2048, 8192)])
@@ -89,10 +88,7 @@ def test_gemm_w8a16_w4a16_config1(N, K, fmt):
         wdq = hxo.q4_dequant(q, s)
         assert np.array_equal(wdq.view(np.float16).astype(np.float32), (qv * np.float32(np.float16(0.02 / 127))).astype(np.float16).astype(np.float32))
     got = _run_gemm(hip, A, fmt, q, s, N, K)
-    ref = f16(hxo.gemm(A, wdq))
-    d = ulp_diff(got, ref)
-    assert d.max() <= 1, d.max()
-    assert np.mean(d == 0) > 0.98
+    assert_gemm_close(got, hxo.gemm(A, wdq), A, wdq.view(np.float16))
 
 
 def test_gemm_epilogues():
@@ -103,13 +99,14 @@ def test_gemm_epilogues():
     W = f16(rng.standard_normal((N, K)) * 0.1)
     t = f16(hxo.gemm(A, W))
     say("gemm epi gelu tanh / erf")
+    t_gpu = _run_gemm(hip, A, 0, W, None, N, K)  # the GPU's own f16(acc), then the activation on the same values
     for epi, mode in ((1, 1), (2, 0)):
         got = _run_gemm(hip, A, 0, W, None, N, K, epi=epi)
-        ref = hxo.gelu(t, mode).view(np.float16)
+        ref = hxo.gelu(t_gpu, mode).view(np.float16)
         assert ulp_diff(got, ref).max() <= 2
     say("gemm epi store_t")
     got = _run_gemm(hip, A, 0, W, None, N, K, epi=4)
-    assert ulp_diff(got.T, t).max() <= 1
+    assert_gemm_close(np.ascontiguousarray(got.T), hxo.gemm(A, W), A, W)
     say("gemm epi resadd")
     x = rng.standard_normal((M, N)).astype(np.float32)
     g = rng.standard_normal(N).astype(np.float32)
@@ -118,15 +115,17 @@ def test_gemm_epilogues():
     assert np.allclose(got, hxo.resadd(x, t, g), atol=np.abs(g).max() * 2e-3 * np.abs(t.astype(np.float32)).max())
     say("gemm epi partial (split-K 2)")
     got = _run_gemm(hip, A, 0, W, None, N, K, epi=6, ksplit=2)
-    r0 = f16(hxo.gemm(np.ascontiguousarray(A[:, :K // 2]), np.ascontiguousarray(W[:, :K // 2])))
-    r1 = f16(hxo.gemm(np.ascontiguousarray(A[:, K // 2:]), np.ascontiguousarray(W[:, K // 2:])))
-    assert ulp_diff(got[0], r0).max() <= 1 and ulp_diff(got[1], r1).max() <= 1
+    for z, sl in ((0, slice(0, K // 2)), (1, slice(K // 2, K))):
+        Az, Wz = np.ascontiguousarray(A[:, sl]), np.ascontiguousarray(W[:, sl])
+        assert_gemm_close(got[z], hxo.gemm(Az, Wz), Az, Wz)
     say("gemm epi situ (interleaved up/gate)")
     F = N // 2
     up = np.ascontiguousarray(W.reshape(F // 32, 2, 32, K)[:, 0].reshape(F, K))
     gt = np.ascontiguousarray(W.reshape(F // 32, 2, 32, K)[:, 1].reshape(F, K))
     got = _run_gemm(hip, A, 0, W, None, N, K, epi=5)
-    ref = hxo.situ(f16(hxo.gemm(A, up)), f16(hxo.gemm(A, gt))).view(np.float16)
+    tu = np.ascontiguousarray(t_gpu.reshape(M, F // 32, 2, 32)[:, :, 0].reshape(M, F))
+    tg = np.ascontiguousarray(t_gpu.reshape(M, F // 32, 2, 32)[:, :, 1].reshape(M, F))
+    ref = hxo.situ(tu, tg).view(np.float16)
     assert ulp_diff(got, ref).max() <= 2
 
 
@@ -143,9 +142,10 @@ def test_gemm_fused_qkv_split_transposed():
     hip.check(hip.lib().hxa_gemm(dA.ptr, D, M, 0, dW.ptr, None, None, 3 * D, D, 1, 0, qk.ptr, 2 * D, 0, None, 0, None,
                                  vt.ptr, M, 2 * D, None), "qkv")
     hip.sync()
-    ref = f16(hxo.gemm(A, W))
-    assert ulp_diff(qk.numpy(), ref[:, :2 * D]).max() <= 1
-    assert ulp_diff(vt.numpy().T, ref[:, 2 * D:]).max() <= 1
+    ref = hxo.gemm(A, W)
+    Wq, Wv = np.ascontiguousarray(W[:2 * D]), np.ascontiguousarray(W[2 * D:])
+    assert_gemm_close(qk.numpy(), ref[:, :2 * D], A, Wq)
+    assert_gemm_close(np.ascontiguousarray(vt.numpy().T), ref[:, 2 * D:], A, Wv)
 
 
 def test_gemm_rejects_bad_shapes():
