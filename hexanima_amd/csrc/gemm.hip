@@ -7,20 +7,21 @@
 // Design (CDNA4, 64-wide waves):
 //  * 256 threads = 4 waves in a 2x2 grid; each wave owns a (BM/2)x(BN/2) sub-tile computed with
 //    v_mfma_f32_32x32x16_f16 (fp32 accumulate).
-//  * K is consumed in BK=64 steps; A and W tiles are staged in LDS (double buffered, rows padded to 144 B so the
-//    16-byte fragment reads of 32 consecutive rows fall in distinct banks). Global loads for step k+1 are issued
-//    before the MFMAs of step k.
-//  * int8 / int4 weights are dequantised on their way into LDS with the fp16 exponent-bias trick: a byte u placed
-//    under the exponent 0x64 is the fp16 value 1024+u, so (1024+u) - 1152 = q exactly, then one fp16 multiply by
-//    the group scale gives f16(q*s) -- the reference's exact dequantised value (gemm2.c:19-22).
+//  * K is consumed in steps of 32 (one quantisation group). A and W k-tiles go from global memory straight into a
+//    4-stage LDS ring (global_load_lds_dwordx4, no VGPR staging), 3 steps ahead of the MFMAs; one s_barrier per
+//    step, with explicit vmcnt waits so the prefetches stay in flight. 16-byte LDS chunks are XOR-swizzled per row
+//    so the fragment reads of 32 consecutive rows hit distinct banks.
+//  * int8 / int4 weights stay raw in LDS and are dequantised into the B fragments in registers with the fp16
+//    exponent-bias trick: a byte u placed under the exponent 0x64 is the fp16 value 1024+u, so (1024+u) - 1152 = q
+//    exactly, then one fp16 multiply by the group scale gives f16(q*s) -- the reference's exact dequantised value
+//    (gemm2.c:19-22).
+//  * The fp16-rounded output tile is staged through LDS for a coalesced epilogue (16-byte loads / stores).
 //  * The block index is remapped so each of the 8 XCDs (own L2) works on a contiguous range of output tiles.
 #include "hxa_common.h"
 #include "kernels.h"
 
 namespace {
 
-constexpr int BK = 64;
-constexpr int LDS_ROW = BK + 8;  // halves
 
 struct GemmParams {
   const hxa_h *A;
@@ -88,19 +89,66 @@ HXA_DEV float situ_f(float u, float g) {
   return tu * gs;
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void gmem_void_t;
+
+// s_waitcnt vmcnt(N) only (expcnt / lgkmcnt left at their maxima); encoding of gfx9: vmcnt[3:0] | vmcnt_hi[15:14]
+template <int N>
+HXA_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+// 16 bytes per lane from global memory straight into LDS: lane l writes lds_base + 16 l
+HXA_DEV void g2l16(const void *g, void *lds_base) {
+  __builtin_amdgcn_global_load_lds((gmem_void_t *)g, (lds_void_t *)lds_base, 16, 0, 0);
+}
+
+template <int BM, int BN, int FMT>
+struct GemmGeo {
+  static constexpr int BK = 32;                                      // k per stage (one quantisation group)
+  static constexpr int NS = 4, PD = 3;                               // LDS ring stages, prefetch distance
+  static constexpr int RB = FMT == HXA_W_F16 ? 64 : FMT == HXA_W_Q8 ? 32 : 16;  // W bytes per row per stage
+  static constexpr int A_BYTES = BM * 64;
+  static constexpr int W_BYTES = BN * RB;
+  static constexpr int S_BYTES = FMT == HXA_W_F16 ? 0 : (BN * 2 + 15) / 16 * 16;
+  static constexpr int STAGE = A_BYTES + W_BYTES + 2 * S_BYTES;     // scale + optional offset vectors
+  static constexpr int CROW = BN + 8;
+  static constexpr int C_BYTES = BM * CROW * 2;
+  static constexpr int LDS = NS * STAGE > C_BYTES ? NS * STAGE : C_BYTES;
+  static constexpr int NA = BM / 64;                                 // A load instructions per wave per stage
+  static constexpr int TW = (W_BYTES / 16 + 63) / 64;                // W load instructions per stage (all waves)
+};
+
+// Per-wave number of direct-to-LDS instructions issued for one stage.
+template <int BM, int BN, int FMT, bool ASYM>
+HXA_DEV constexpr int loads_per_stage(int wave) {
+  using G = GemmGeo<BM, BN, FMT>;
+  return G::NA + (G::TW / 4 + (wave < G::TW % 4 ? 1 : 0)) + (FMT != HXA_W_F16 && wave == 0 ? (ASYM ? 2 : 1) : 0);
+}
+// wait until at most `later` further stages of loads are outstanding for this wave
+template <int BM, int BN, int FMT, bool ASYM, int WAVE>
+HXA_DEV void wait_stage_w(int later) {
+  constexpr int n = loads_per_stage<BM, BN, FMT, ASYM>(WAVE);
+  if (later >= 2) wait_vm<2 * n>();
+  else if (later == 1) wait_vm<n>();
+  else wait_vm<0>();
+}
+template <int BM, int BN, int FMT, bool ASYM>
+HXA_DEV void wait_stage(int wave, int later) {
+  static_assert(GemmGeo<BM, BN, FMT>::PD == 3, "wait_stage handles up to two later stages");
+  if (wave == 0) wait_stage_w<BM, BN, FMT, ASYM, 0>(later);
+  else if (wave == 1) wait_stage_w<BM, BN, FMT, ASYM, 1>(later);
+  else if (wave == 2) wait_stage_w<BM, BN, FMT, ASYM, 2>(later);
+  else wait_stage_w<BM, BN, FMT, ASYM, 3>(later);
+}
+
 template <int BM, int BN, int FMT, bool ASYM>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
+  using G = GemmGeo<BM, BN, FMT>;
   constexpr int WTM = BM / 2, WTN = BN / 2, MI = WTM / 32, NI = WTN / 32;
-  constexpr int CA = BM * 8 / 256;                                   // 16-byte A chunks per thread per stage
-  constexpr int CPR = FMT == HXA_W_F16 ? 8 : FMT == HXA_W_Q8 ? 4 : 2;  // 16-byte W chunks per row per stage
-  constexpr int NCB = BN * CPR;                                      // W chunks per stage
-  constexpr int CB = (NCB + 255) / 256;
-  constexpr int STAGE = (BM + BN) * LDS_ROW;
-  constexpr int CROW = BN + 8;                                       // epilogue C tile row (halves)
-  static_assert(BM * 8 % 256 == 0, "A tile must split evenly over 256 threads");
-  static_assert(BM * CROW <= 2 * STAGE, "C tile must fit in the main-loop LDS");
-  extern __shared__ __attribute__((aligned(16))) hxa_h lds[];
-  hxa_h *const As0 = lds, *const Bs0 = lds + BM * LDS_ROW;
+  constexpr int BK = G::BK, NS = G::NS, PD = G::PD;
+  static_assert(BM % 64 == 0 && BN % 64 == 0, "tile shape");
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
 
   const int ntiles = p.tiles_m * p.tiles_n;
   const int bid = blockIdx.x;
@@ -109,101 +157,90 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   const int m0 = tm * BM, n0 = tn * BN;
   const int z = blockIdx.z;
   const int kbase = z * p.Kslice;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
 
-  // acc[j][i]: 32x32 block of output columns j (A operand of the MFMA = W rows) and rows i (B operand = A rows)
+  // ---- loader: stage s <- k tile kt. A and fp16 W rows are 64 B (4 chunks of 16 B) stored with the chunk swizzle
+  // c ^ ((row >> 2) & 3); q8 rows are 32 B with chunk swizzle c ^ ((row >> 3) & 1); q4 rows are 16 B.
+  auto issue = [&](int s, int kt) {
+    uint8_t *st = lds8 + s * G::STAGE;
+    const int k0 = kbase + kt * BK;
+#pragma unroll
+    for (int i = 0; i < G::NA; i++) {
+      const int r0 = (wave * G::NA + i) * 16, row = r0 + (lane >> 2);
+      const int cl = (lane & 3) ^ ((row >> 2) & 3);
+      const int m = min(m0 + row, p.M - 1);
+      g2l16(p.A + (long)m * p.lda + k0 + cl * 8, st + r0 * 64);
+    }
+    uint8_t *ws = st + G::A_BYTES;
+#pragma unroll
+    for (int t0 = 0; t0 < G::TW; t0 += 4) {
+      const int t = t0 + wave;
+      if (t < G::TW) {
+        const int chunk = t * 64 + lane;
+        if (chunk < G::W_BYTES / 16) {
+          if (FMT == HXA_W_F16) {
+            const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3), n = min(n0 + row, p.N - 1);
+            g2l16((const hxa_h *)p.W + (long)n * p.ldw + k0 + cl * 8, ws + t * 1024);
+          } else if (FMT == HXA_W_Q8) {
+            const int row = chunk >> 1, cl = (chunk & 1) ^ ((row >> 3) & 1), n = min(n0 + row, p.N - 1);
+            g2l16((const int8_t *)p.W + (long)n * p.ldw + k0 + cl * 16, ws + t * 1024);
+          } else {
+            const int row = chunk, n = min(n0 + row, p.N - 1);
+            g2l16((const uint8_t *)p.W + (long)n * p.ldw + (k0 >> 1), ws + t * 1024);
+          }
+        }
+      }
+    }
+    if (FMT != HXA_W_F16 && wave == 0) {
+      const int g = k0 >> 5;
+      const int nn = min(n0 + lane * 8, p.N - 8);
+      if (lane < BN / 8) g2l16(p.S + (long)g * p.N + nn, ws + G::W_BYTES);
+      if (ASYM && lane < BN / 8) g2l16(p.Z + (long)g * p.N + nn, ws + G::W_BYTES + G::S_BYTES);
+    }
+  };
+
   float16_t acc[NI][MI];
 #pragma unroll
   for (int j = 0; j < NI; j++)
 #pragma unroll
     for (int i = 0; i < MI; i++) acc[j][i] = (float16_t){};
 
-  uint4_t ra[CA];
-  uint4_t rb[CB];
-  hxa_h rs[CB], rz[CB];
-
-  auto load = [&](int kt) {
-    const int k0 = kbase + kt * BK;
-#pragma unroll
-    for (int i = 0; i < CA; i++) {
-      const int c = tid + i * 256, r = c >> 3, cc = c & 7;
-      const int m = m0 + r;
-      ra[i] = m < p.M ? *(const uint4_t *)(p.A + (long)m * p.lda + k0 + cc * 8) : (uint4_t){0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int i = 0; i < CB; i++) {
-      const int c = tid + i * 256;
-      if (NCB % 256 == 0 || c < NCB) {
-        if (FMT == HXA_W_F16) {
-          const int r = c >> 3, cc = c & 7, n = n0 + r;
-          rb[i] = n < p.N ? *(const uint4_t *)((const hxa_h *)p.W + (long)n * p.ldw + k0 + cc * 8) : (uint4_t){0, 0, 0, 0};
-        } else if (FMT == HXA_W_Q8) {
-          const int r = c >> 2, cc = c & 3, n = n0 + r;
-          const int kk = k0 + cc * 16;
-          rb[i] = n < p.N ? *(const uint4_t *)((const int8_t *)p.W + (long)n * p.ldw + kk) : (uint4_t){0, 0, 0, 0};
-          rs[i] = n < p.N ? p.S[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
-        } else {
-          const int r = c >> 1, cc = c & 1, n = n0 + r;
-          const int kk = k0 + cc * 32;
-          rb[i] = n < p.N ? *(const uint4_t *)((const uint8_t *)p.W + (long)n * p.ldw + (kk >> 1)) : (uint4_t){0, 0, 0, 0};
-          rs[i] = n < p.N ? p.S[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
-          if (ASYM) rz[i] = n < p.N ? p.Z[(long)(kk >> 5) * p.N + n] : (hxa_h)0.0f;
-        }
-      }
-    }
-  };
-  auto store = [&](int buf) {
-    hxa_h *As = As0 + buf * STAGE, *Bs = Bs0 + buf * STAGE;
-#pragma unroll
-    for (int i = 0; i < CA; i++) {
-      const int c = tid + i * 256, r = c >> 3, cc = c & 7;
-      *(uint4_t *)(As + r * LDS_ROW + cc * 8) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < CB; i++) {
-      const int c = tid + i * 256;
-      if (NCB % 256 == 0 || c < NCB) {
-        if (FMT == HXA_W_F16) {
-          const int r = c >> 3, cc = c & 7;
-          *(uint4_t *)(Bs + r * LDS_ROW + cc * 8) = rb[i];
-        } else if (FMT == HXA_W_Q8) {
-          const int r = c >> 2, cc = c & 3;
-          const half2_t s2 = {rs[i], rs[i]};
-          uint32_t o[8];
-          dq8_word(rb[i].x, s2, o[0], o[1]);
-          dq8_word(rb[i].y, s2, o[2], o[3]);
-          dq8_word(rb[i].z, s2, o[4], o[5]);
-          dq8_word(rb[i].w, s2, o[6], o[7]);
-          *(uint4_t *)(Bs + r * LDS_ROW + cc * 16) = (uint4_t){o[0], o[1], o[2], o[3]};
-          *(uint4_t *)(Bs + r * LDS_ROW + cc * 16 + 8) = (uint4_t){o[4], o[5], o[6], o[7]};
-        } else {
-          const int r = c >> 1, cc = c & 1;
-          const half2_t s2 = {rs[i], rs[i]};
-          const half2_t z2 = ASYM ? (half2_t){rz[i], rz[i]} : (half2_t){};
-          uint32_t o[16];
-          dq4_word<ASYM>(rb[i].x, s2, z2, o + 0);
-          dq4_word<ASYM>(rb[i].y, s2, z2, o + 4);
-          dq4_word<ASYM>(rb[i].z, s2, z2, o + 8);
-          dq4_word<ASYM>(rb[i].w, s2, z2, o + 12);
-#pragma unroll
-          for (int q = 0; q < 4; q++)
-            *(uint4_t *)(Bs + r * LDS_ROW + cc * 32 + q * 8) = (uint4_t){o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
-        }
-      }
-    }
-  };
-  auto compute = [&](int buf) {
-    const hxa_h *As = As0 + buf * STAGE, *Bs = Bs0 + buf * STAGE;
+  auto compute = [&](int s) {
+    const uint8_t *st = lds8 + s * G::STAGE;
+    const uint8_t *ws = st + G::A_BYTES;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ks++) {
+      const int cl = ks * 2 + (lane >> 5);
       half8_t a[MI], b[NI];
-      const int col = ks * 16 + (lane >> 5) * 8;
 #pragma unroll
-      for (int i = 0; i < MI; i++) a[i] = *(const half8_t *)(As + (wm * WTM + i * 32 + (lane & 31)) * LDS_ROW + col);
+      for (int i = 0; i < MI; i++) {
+        const int row = wm * WTM + i * 32 + (lane & 31);
+        a[i] = *(const half8_t *)(st + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
+      }
 #pragma unroll
-      for (int j = 0; j < NI; j++) b[j] = *(const half8_t *)(Bs + (wn * WTN + j * 32 + (lane & 31)) * LDS_ROW + col);
+      for (int j = 0; j < NI; j++) {
+        const int row = wn * WTN + j * 32 + (lane & 31);
+        if (FMT == HXA_W_F16) {
+          b[j] = *(const half8_t *)(ws + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
+        } else {
+          const hxa_h sc = *(const hxa_h *)(ws + G::W_BYTES + row * 2);
+          const half2_t s2 = {sc, sc};
+          uint32_t o[4];
+          if (FMT == HXA_W_Q8) {  // 8-byte slot cl of the row: chunk cl >> 1 (swizzled), half cl & 1
+            const uint2_t q = *(const uint2_t *)(ws + row * 32 + (((cl >> 1) ^ ((row >> 3) & 1)) << 4) + ((cl & 1) << 3));
+            dq8_word(q.x, s2, o[0], o[1]);
+            dq8_word(q.y, s2, o[2], o[3]);
+          } else {  // 4-byte slot cl: 8 consecutive k
+            const uint32_t q = *(const uint32_t *)(ws + row * 16 + (cl << 2));
+            const half2_t z2 = ASYM ? (half2_t){*(const hxa_h *)(ws + G::W_BYTES + G::S_BYTES + row * 2),
+                                                *(const hxa_h *)(ws + G::W_BYTES + G::S_BYTES + row * 2)}
+                                    : (half2_t){};
+            dq4_word<ASYM>(q, s2, z2, o);
+          }
+          b[j] = __builtin_bit_cast(half8_t, (uint4_t){o[0], o[1], o[2], o[3]});
+        }
+      }
 #pragma unroll
       for (int j = 0; j < NI; j++)
 #pragma unroll
@@ -212,20 +249,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   };
 
   const int nk = p.Kslice / BK;
-  load(0);
-  store(0);
-  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < PD; s++)
+    if (s < nk) issue(s, s);
   for (int kt = 0; kt < nk; kt++) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) load(kt + 1);
-    compute(cur);
-    if (kt + 1 < nk) store(cur ^ 1);
-    __syncthreads();
+    const int later = min(PD - 1, nk - 1 - kt);  // stages issued after kt that may stay in flight
+    wait_stage<BM, BN, FMT, ASYM>(wave, later);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // tile kt visible to all waves; stage (kt-1) % NS no longer read
+    asm volatile("" ::: "memory");
+    if (kt + PD < nk) issue((kt + PD) % NS, kt + PD);
+    compute(kt % NS);
   }
+  __syncthreads();
 
   // ---- epilogue. Stage f16(acc) through LDS as a row-major [BM][CROW] tile: lane holds, for block (j, i),
   // row i*32 + (lane & 31) and columns j*32 + 8q + 4*(lane/32) + 0..3 (q = 0..3) -> one 8-byte write each.
-  hxa_h *Cs = lds;
+  constexpr int CROW = G::CROW;
+  hxa_h *Cs = (hxa_h *)lds8;
   {
     const int ml = wm * WTM + (lane & 31), nl = wn * WTN + 4 * (lane >> 5);
 #pragma unroll
@@ -317,7 +358,7 @@ constexpr TileCfg kCfgs[] = {{192, 256}, {192, 192}, {192, 128}, {256, 128}, {12
 template <int BM, int BN, int FMT, bool ASYM>
 hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
   auto kern = gemm_kernel<BM, BN, FMT, ASYM>;
-  const int lds = 2 * (BM + BN) * LDS_ROW * (int)sizeof(hxa_h);
+  const int lds = GemmGeo<BM, BN, FMT>::LDS;
   static bool attr = false;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -375,7 +416,7 @@ static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int *bm, int *
 int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   const HxaWeight &w = *g.w;
   if (g.M <= 0 || w.N <= 0 || w.K <= 0 || g.ksplit < 1) return HXA_E_ARG;
-  if (w.K % (BK * g.ksplit) != 0) return HXA_E_ARG;
+  if (w.K % (32 * g.ksplit) != 0) return HXA_E_ARG;
   if (w.fmt != HXA_W_F16 && w.s == nullptr) return HXA_E_ARG;
   if (g.epi == HXA_EPI_SITU && (w.N % 64) != 0) return HXA_E_ARG;
   if ((g.lda % 8) != 0 || ((uintptr_t)g.A % 16) != 0 || ((uintptr_t)w.w % 16) != 0) return HXA_E_ARG;
