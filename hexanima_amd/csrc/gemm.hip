@@ -17,6 +17,8 @@
 //    (gemm2.c:19-22).
 //  * The fp16-rounded output tile is staged through LDS for a coalesced epilogue (16-byte loads / stores).
 //  * The block index is remapped so each of the 8 XCDs (own L2) works on a contiguous range of output tiles.
+#include <type_traits>
+
 #include "hxa_common.h"
 #include "kernels.h"
 
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   // c ^ ((row >> 2) & 3); q8 rows are 32 B with chunk swizzle c ^ ((row >> 3) & 1); q4 rows are 16 B.
   auto issue = [&](int s, int kt) {
     uint8_t *st = lds8 + s * G::STAGE;
-    const int k0 = kbase + kt * BK;
+    const int k0 = kbase + min(kt, p.Kslice / BK - 1) * BK;  // tiles past the end reload the last one (never read)
 #pragma unroll
     for (int i = 0; i < G::NA; i++) {
       const int r0 = (wave * G::NA + i) * 16, row = r0 + (lane >> 2);
@@ -176,9 +178,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int t0 = 0; t0 < G::TW; t0 += 4) {
       const int t = t0 + wave;
-      if (t < G::TW) {
+      if (G::TW % 4 == 0 || t < G::TW) {
         const int chunk = t * 64 + lane;
-        if (chunk < G::W_BYTES / 16) {
+        if ((G::W_BYTES / 16) % 64 == 0 || chunk < G::W_BYTES / 16) {
           if (FMT == HXA_W_F16) {
             const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3), n = min(n0 + row, p.N - 1);
             g2l16((const hxa_h *)p.W + (long)n * p.ldw + k0 + cl * 8, ws + t * 1024);
@@ -206,60 +208,120 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < MI; i++) acc[j][i] = (float16_t){};
 
-  auto compute = [&](int s) {
+  // Fragments of one stage: A rows fa[ks][i]; W rows fb[ks][j]. fp16 W fragments are read directly; quantised W
+  // is read raw (wq, scale ws_, offset wz) and dequantised by dequant(ks) right before the MFMAs that need it, so the
+  // LDS latency of the raw reads is covered by the preceding MFMAs.
+  typedef typename std::conditional<FMT == HXA_W_Q8, uint2_t, uint32_t>::type raw_t;
+  raw_t wq0[2][NI], wq1[2][NI];
+  hxa_h sc0[NI], sc1[NI], zc0[NI], zc1[NI];
+  auto read_frags = [&](int s, half8_t (&fa)[2][MI], half8_t (&fb)[2][NI], raw_t (&wq)[2][NI], hxa_h (&sc)[NI],
+                        hxa_h (&zc)[NI]) {
     const uint8_t *st = lds8 + s * G::STAGE;
     const uint8_t *ws = st + G::A_BYTES;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ks++) {
       const int cl = ks * 2 + (lane >> 5);
-      half8_t a[MI], b[NI];
 #pragma unroll
       for (int i = 0; i < MI; i++) {
         const int row = wm * WTM + i * 32 + (lane & 31);
-        a[i] = *(const half8_t *)(st + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
+        fa[ks][i] = *(const half8_t *)(st + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
       }
 #pragma unroll
       for (int j = 0; j < NI; j++) {
         const int row = wn * WTN + j * 32 + (lane & 31);
-        if (FMT == HXA_W_F16) {
-          b[j] = *(const half8_t *)(ws + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
-        } else {
-          const hxa_h sc = *(const hxa_h *)(ws + G::W_BYTES + row * 2);
-          const half2_t s2 = {sc, sc};
-          uint32_t o[4];
-          if (FMT == HXA_W_Q8) {  // 8-byte slot cl of the row: chunk cl >> 1 (swizzled), half cl & 1
-            const uint2_t q = *(const uint2_t *)(ws + row * 32 + (((cl >> 1) ^ ((row >> 3) & 1)) << 4) + ((cl & 1) << 3));
-            dq8_word(q.x, s2, o[0], o[1]);
-            dq8_word(q.y, s2, o[2], o[3]);
-          } else {  // 4-byte slot cl: 8 consecutive k
-            const uint32_t q = *(const uint32_t *)(ws + row * 16 + (cl << 2));
-            const half2_t z2 = ASYM ? (half2_t){*(const hxa_h *)(ws + G::W_BYTES + G::S_BYTES + row * 2),
-                                                *(const hxa_h *)(ws + G::W_BYTES + G::S_BYTES + row * 2)}
-                                    : (half2_t){};
-            dq4_word<ASYM>(q, s2, z2, o);
-          }
-          b[j] = __builtin_bit_cast(half8_t, (uint4_t){o[0], o[1], o[2], o[3]});
+        if constexpr (FMT == HXA_W_F16) {
+          fb[ks][j] = *(const half8_t *)(ws + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
+        } else if constexpr (FMT == HXA_W_Q8) {  // 8-byte slot cl of the row: chunk cl >> 1 (swizzled), half cl & 1
+          wq[ks][j] = *(const uint2_t *)(ws + row * 32 + (((cl >> 1) ^ ((row >> 3) & 1)) << 4) + ((cl & 1) << 3));
+        } else {  // 4-byte slot cl: 8 consecutive k
+          wq[ks][j] = *(const uint32_t *)(ws + row * 16 + (cl << 2));
         }
       }
+    }
+    if constexpr (FMT != HXA_W_F16) {
 #pragma unroll
-      for (int j = 0; j < NI; j++)
-#pragma unroll
-        for (int i = 0; i < MI; i++) acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[j][i], 0, 0, 0);
+      for (int j = 0; j < NI; j++) {
+        const int row = wn * WTN + j * 32 + (lane & 31);
+        sc[j] = *(const hxa_h *)(ws + G::W_BYTES + row * 2);
+        zc[j] = ASYM ? *(const hxa_h *)(ws + G::W_BYTES + G::S_BYTES + row * 2) : (hxa_h)0.0f;
+      }
     }
   };
-
-  const int nk = p.Kslice / BK;
+  auto dequant = [&](int ks, half8_t (&fb)[2][NI], const raw_t (&wq)[2][NI], const hxa_h (&sc)[NI], const hxa_h (&zc)[NI]) {
+    if constexpr (FMT != HXA_W_F16) {
 #pragma unroll
-  for (int s = 0; s < PD; s++)
-    if (s < nk) issue(s, s);
-  for (int kt = 0; kt < nk; kt++) {
-    const int later = min(PD - 1, nk - 1 - kt);  // stages issued after kt that may stay in flight
-    wait_stage<BM, BN, FMT, ASYM>(wave, later);
+      for (int j = 0; j < NI; j++) {
+        const half2_t s2 = {sc[j], sc[j]};
+        uint32_t o[4];
+        if constexpr (FMT == HXA_W_Q8) {
+          dq8_word(wq[ks][j].x, s2, o[0], o[1]);
+          dq8_word(wq[ks][j].y, s2, o[2], o[3]);
+        } else {
+          const half2_t z2 = {zc[j], zc[j]};
+          dq4_word<ASYM>(wq[ks][j], s2, z2, o);
+        }
+        fb[ks][j] = __builtin_bit_cast(half8_t, (uint4_t){o[0], o[1], o[2], o[3]});
+      }
+    }
+  };
+  auto mfma_range = [&](const half8_t (&fa)[MI], const half8_t (&fb)[NI], int from, int to) {
+#pragma unroll
+    for (int q = 0; q < NI * MI; q++) {
+      if (q >= from && q < to) {
+        const int j = q / MI, i = q % MI;
+        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[j], fa[i], acc[j][i], 0, 0, 0);
+      }
+    }
+  };
+  constexpr int NMF = NI * MI;  // MFMAs per 16-k slice
+  const int nk = p.Kslice / BK;
+  // One k step with register-double-buffered fragments. After the first two MFMAs of stage kt this wave waits for
+  // stage kt+1, passes the barrier, then interleaves the remaining MFMAs of stage kt one-to-one with the prefetch of
+  // tile kt+NS (into stage kt's LDS, whose fragments are already in registers) and the fragment reads of stage kt+1.
+  // Every load is unconditional (past the end: clamped dummy loads), so the vmcnt accounting is constant.
+  auto step = [&](int kt, half8_t (&ca)[2][MI], half8_t (&cb)[2][NI], half8_t (&na)[2][MI], half8_t (&nb)[2][NI],
+                  raw_t (&cq)[2][NI], hxa_h (&cs)[NI], hxa_h (&cz)[NI], raw_t (&nq)[2][NI], hxa_h (&ns)[NI],
+                  hxa_h (&nz)[NI]) {
+    dequant(0, cb, cq, cs, cz);
+    mfma_range(ca[0], cb[0], 0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_stage<BM, BN, FMT, ASYM>(wave, 2);  // tile kt+1 complete; tiles kt+2, kt+3 may still fly
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();  // tile kt visible to all waves; stage (kt-1) % NS no longer read
+    __builtin_amdgcn_s_barrier();             // stage kt+1 visible; every wave holds its stage kt fragments
     asm volatile("" ::: "memory");
-    if (kt + PD < nk) issue((kt + PD) % NS, kt + PD);
-    compute(kt % NS);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(kt % NS, kt + NS);
+    mfma_range(ca[0], cb[0], 2, NMF);
+    dequant(1, cb, cq, cs, cz);
+    read_frags((kt + 1) % NS, na, nb, nq, ns, nz);
+    mfma_range(ca[1], cb[1], 0, NMF);
+    constexpr int NV = G::NA + (G::TW + 3) / 4 + 2;  // upper bound of the VMEM loads of this wave
+#pragma unroll
+    for (int q = 0; q < NV; q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one VMEM (direct-to-LDS) load
+    }
+#pragma unroll
+    for (int q = 0; q < 2 * (MI + NI); q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // prologue: fill all NS stages (tiles 0..NS-1); step kt then refills stage kt % NS with tile kt + NS
+  static_assert(NS == PD + 1, "ring of PD + 1 stages");
+  half8_t fa0[2][MI], fb0[2][NI], fa1[2][MI], fb1[2][NI];
+#pragma unroll
+  for (int s = 0; s < NS; s++) issue(s, s);
+  wait_stage<BM, BN, FMT, ASYM>(wave, 2);  // tiles 0 and 1 complete
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  read_frags(0, fa0, fb0, wq0, sc0, zc0);
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, fa0, fb0, fa1, fb1, wq0, sc0, zc0, wq1, sc1, zc1);
+    if (kt + 1 < nk) step(kt + 1, fa1, fb1, fa0, fb0, wq1, sc1, zc1, wq0, sc0, zc0);
   }
   __syncthreads();
 

@@ -154,8 +154,10 @@ def test_gemm_rejects_bad_shapes():
     dA = hip.DeviceArray((64, 96), np.float16, zero=True)
     dW = hip.DeviceArray((64, 96), np.float16, zero=True)
     out = hip.DeviceArray((64, 64), np.float16)
-    rc = hip.lib().hxa_gemm(dA.ptr, 96, 64, 0, dW.ptr, None, None, 64, 96, 1, 0, out.ptr, 64, 0, None, 0, None, None, 0, 0, None)
-    assert rc == -12  # K % 64 != 0
+    rc = hip.lib().hxa_gemm(dA.ptr, 96, 64, 0, dW.ptr, None, None, 64, 80, 1, 0, out.ptr, 64, 0, None, 0, None, None, 0, 0, None)
+    assert rc == -12  # K % 32 != 0
+    rc = hip.lib().hxa_gemm(dA.ptr, 96, 64, 0, dW.ptr, None, None, 64, 96, 2, 6, out.ptr, 64, 0, None, 0, None, None, 0, 0, None)
+    assert rc == -12  # K / ksplit % 32 != 0
     rc = hip.lib().hxa_gemm(dA.ptr, 96, 64, 1, dW.ptr, None, None, 64, 64, 1, 0, out.ptr, 64, 0, None, 0, None, None, 0, 0, None)
     assert rc == -12  # q8 without scales
 
