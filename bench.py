@@ -99,6 +99,33 @@ def gpu_run(steps, warmup):
     return info, ms_step, up_ms
 
 
+def kernel_probe(reps):
+    """Launches only the dominant kernel (MLP-up GEMM, `reps` times) and a 256 MiB device-to-device copy (3 times,
+    the byte-count calibration of the FETCH_SIZE / WRITE_SIZE counters), for `rocprofv3 --pmc` passes."""
+    from hexanima_amd import hip
+    hip.init(0)
+    L = hip.lib()
+    s = C.c_void_p()
+    hip.check(L.hxa_stream_create(C.byref(s)), "stream")
+    A = hip.DeviceArray((T, D), np.float16)
+    W = hip.DeviceArray((F, D), np.float16)
+    O = hip.DeviceArray((T, F), np.float16)
+    hip.check(L.hxa_fill_normal(A.ptr, 1, T * D, 11, 0.0, 1.0, s), "fill")
+    hip.check(L.hxa_fill_normal(W.ptr, 1, F * D, 12, 0.0, 0.02, s), "fill")
+    for _ in range(reps):
+        hip.check(L.hxa_gemm(A.ptr, D, T, hip.W_F16, W.ptr, None, None, F, D, 1, hip.EPI_GELU_TANH, O.ptr, F, 0, None, 0,
+                             None, None, 0, 0, s), "gemm")
+    nb = 256 << 20
+    src = hip.DeviceArray((nb,), np.uint8)
+    dst = hip.DeviceArray((nb,), np.uint8)
+    hip.check(L.hxa_stream_sync(s), "sync")
+    hip.check(L.hxa_memset(src.ptr, 1, nb), "memset")
+    for _ in range(3):
+        hip.check(L.hxa_d2d(dst.ptr, src.ptr, nb), "copy")
+    hip.check(L.hxa_stream_sync(s), "sync")
+    print(f"kernel probe: {reps} x gemm {T}x{D}x{F} GELU, 3 x copy {nb} B", flush=True)
+
+
 def cpu_baseline():
     """The oracle (C port of the reference block, OpenMP) on one 1536-token block, scaled to a 28-block step."""
     from oracle import hxo
@@ -126,15 +153,22 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-probe", type=int, default=0, metavar="REPS",
+                    help="only launch the dominant kernel REPS times plus a copy calibration (for rocprofv3 --pmc)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build targets a single MI355X (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
+    if a.kernel_probe:
+        kernel_probe(a.kernel_probe)
+        return
     info, ms_step, up_ms = gpu_run(a.steps, a.warmup)
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic_gemm_mlp_up_1536x2048x8192.json")
-    if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
+    tpath = os.path.join(ROOT, "profiles", "traffic_gemm_mlp_up_1536x2048x8192.txt")
+    if os.path.exists(tpath):  # rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated (see that file)
+        for line in open(tpath):
+            if line.startswith("hbm_bytes_per_launch:"):
+                traffic = int(line.split(":")[1])
     up_tf = UP_FLOPS / (up_ms * 1e-3)
     res = {
         "metric": "DiT denoise steps/s at 1536 tok (2B fp16, 2.9B q8); GEMM+attn % MFMA peak",
