@@ -26,6 +26,7 @@ struct Dit {
   hipStream_t st = nullptr;
   std::vector<void *> packs;
   long pack_bytes = 0;
+  hxa_h *modw_all = nullptr;  // one allocation: every block's modulation weights, stacked
   std::vector<hxa_h *> modw;  // Anima: per block [6D][D]; MOSS: one shared [6D][D]
   hxa_h *glue = nullptr;      // x_embed [D][4C] | t_embed [D][temb] | final_mod [2D][D] | final_lin [4C][D] | text_proj
   long glue_elems = 0;
@@ -156,13 +157,13 @@ int record_step(Dit &d, int mode) {
   // timestep embedding and modulation
   DTRY(hxa_sinusoid_launch(d.sig, 1, temb, d.sinus, st));
   DTRY(hxa_linear_f32_launch(d.sinus, temb, 1, temb, d.L1, D, d.cvec, D, 0, nullptr, 0, 0, st));
-  if (b.kind == 0) {
-    for (int k = 0; k < nb; k++)  // rows 0-2 -> site 0, rows 3-5 -> site 2 (site 1 keeps identity modulation)
-      DTRY(hxa_linear_f32_launch(d.cvec, D, 1, D, d.modw[k], 6 * D, d.mods + (long)k * 9 * D, 0, 1, nullptr, 3 * D, 3 * D, st));
-  } else {
-    DTRY(hxa_linear_f32_launch(d.cvec, D, 1, D, d.modw[0], 6 * D, d.mods, 0, 1, nullptr, 0, 0, st));
-  }
-  DTRY(hxa_linear_f32_launch(d.cvec, D, 1, D, d.Lf, 2 * D, d.fmod, 0, 1, nullptr, 0, 0, st));
+  // every block's modulation in one launch over the stacked [nb][6D][D] weights: rows 0-2 -> site 0, rows 3-5 ->
+  // site 2 of that block's [9][D] (site 1 keeps the identity modulation); MOSS: one shared [6D][D]
+  if (b.kind == 0)
+    DTRY(hxa_modgemv_launch(d.cvec, D, d.modw_all, (long)nb * 6 * D, d.mods, 6 * D, 9L * D, 3 * D, 3 * D, 1, st));
+  else
+    DTRY(hxa_modgemv_launch(d.cvec, D, d.modw_all, 6L * D, d.mods, 6 * D, 0, 6 * D, 0, 1, st));
+  DTRY(hxa_modgemv_launch(d.cvec, D, d.Lf, 2L * D, d.fmod, 2 * D, 0, 2 * D, 0, 1, st));
   // patch embed (+ MOSS text tokens)
   DTRY(hxa_patchify_launch(d.lat, B, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w, d.tok, st));
   for (int i = 0; i < B; i++) {
@@ -249,7 +250,8 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   d.packs.assign(cfg->nblocks, nullptr);
   for (auto &p : d.packs) M(&p, d.pack_bytes);
   d.modw.assign(b.kind == 0 ? cfg->nblocks : 1, nullptr);
-  for (auto &p : d.modw) M((void **)&p, 2L * 6 * D * D);
+  M((void **)&d.modw_all, 2L * 6 * D * D * (long)d.modw.size());
+  for (size_t k = 0; k < d.modw.size() && d.modw_all; k++) d.modw[k] = d.modw_all + (long)k * 6 * D * D;
   d.glue_elems = (long)D * C4 + (long)D * cfg->temb + 2L * D * D + (long)C4 * D + (b.kind == 1 ? (long)D * cfg->ntxt_in : 0);
   M((void **)&d.glue, 2 * d.glue_elems);
   const long latn = (long)B * cfg->lat_c * cfg->lat_h * cfg->lat_w;
@@ -324,7 +326,7 @@ extern "C" int hxa_dit_destroy(void *p) {
   if (d->exec) (void)hipGraphExecDestroy(d->exec);
   if (d->graph) (void)hipGraphDestroy(d->graph);
   for (void *q : d->packs) if (q) (void)hipFree(q);
-  for (void *q : d->modw) if (q) (void)hipFree(q);
+  if (d->modw_all) (void)hipFree(d->modw_all);
   void *bufs[] = {d->glue, d->lat, d->vel, d->tok, d->x, d->sinus, d->cvec, d->mods, d->fmod, d->sig, d->cosT, d->sinT, d->ones, d->ctx16, d->ws};
   for (void *q : bufs) if (q) (void)hipFree(q);
   if (d->st) (void)hipStreamDestroy(d->st);

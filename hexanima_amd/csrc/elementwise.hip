@@ -4,6 +4,8 @@
 //
 // Row kernels use one 64-lane wave per row with 16-byte vector loads (fully coalesced); reductions stay inside
 // the wave (no LDS, no barriers).
+#include <type_traits>
+
 #include "hxa_common.h"
 #include "kernels.h"
 
@@ -225,6 +227,59 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float *__restrict__ x, 
     if (m < M) {
       const float v = wave_sum(accm[m]);
       if (lane == 0) y[(long)m * ldy + n + (n >= split ? gap : 0)] = v + (bias ? bias[n] : 0.0f);
+    }
+  }
+}
+
+// Modulation GEMV over stacked weight matrices (megarun.cpp:156-171 role: every block's adaLN rows from one
+// embedding vector). Row n of W [N][K] gives y[(n / per) * ostride + r + (r >= split ? gap : 0)], r = n % per, with
+// y = sum_k act(x[k]) W[n][k]. act(x) is applied once per lane when x is loaded (1: SiLU). K = KC chunks of 64*EPL;
+// each lane keeps its EPL*KC inputs in registers (k = c*64*EPL + EPL*lane + e); a wave streams RPW rows with
+// EPL*2-byte weight loads, two rows in flight.
+template <int KC, int EPL>
+__global__ __launch_bounds__(256) void modgemv_kernel(const float *__restrict__ x, const hxa_h *__restrict__ W, long N,
+                                                      float *__restrict__ y, int per, long ostride, int split, int gap,
+                                                      int act, int rpw) {
+  constexpr int CH = 64 * EPL, K = KC * CH;
+  using wvec = std::conditional_t<EPL == 8, half8_t, half4_t>;
+  const int lane = threadIdx.x & 63;
+  const long row0 = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw;
+  float xr[KC][EPL];
+#pragma unroll
+  for (int c = 0; c < KC; c++)
+#pragma unroll
+    for (int e4 = 0; e4 < EPL; e4 += 4) {
+      const float4_t a = *(const float4_t *)(x + c * CH + lane * EPL + e4);
+#pragma unroll
+      for (int e = 0; e < 4; e++) xr[c][e4 + e] = act == 1 ? a[e] / (1.0f + __expf(-a[e])) : a[e];
+    }
+  for (int i = 0; i < rpw; i += 2) {
+    const long n0 = row0 + i;
+    if (n0 >= N) break;
+    const bool two = n0 + 1 < N && i + 1 < rpw;
+    wvec w0[KC], w1[KC];
+#pragma unroll
+    for (int c = 0; c < KC; c++) w0[c] = *(const wvec *)(W + n0 * K + c * CH + lane * EPL);
+    if (two) {
+#pragma unroll
+      for (int c = 0; c < KC; c++) w1[c] = *(const wvec *)(W + (n0 + 1) * K + c * CH + lane * EPL);
+    }
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < KC; c++)
+#pragma unroll
+      for (int e = 0; e < EPL; e++) {
+        a0 = fmaf(xr[c][e], (float)w0[c][e], a0);
+        if (two) a1 = fmaf(xr[c][e], (float)w1[c][e], a1);
+      }
+    a0 = wave_sum(a0);
+    if (two) a1 = wave_sum(a1);
+    if (lane == 0) {
+      for (int j = 0; j < (two ? 2 : 1); j++) {
+        const long n = n0 + j;
+        const int r = (int)(n % per);
+        y[(n / per) * ostride + r + (r >= split ? gap : 0)] = j ? a1 : a0;
+      }
     }
   }
 }
@@ -465,6 +520,39 @@ int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W
     if (K > 64 || act != 0 || bias != nullptr || split > 0) return HXA_E_ARG;
     hipLaunchKernelGGL(linear_smallk_kernel, dim3(nblk(N, 64), nblk(M, 64)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy);
   }
+  return LAUNCH_OK();
+}
+
+int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, int per, long ostride, int split, int gap,
+                       int act, hipStream_t st) {
+  if (N <= 0 || per <= 0 || K % 256 || K < 256 || K > 4096 || split < 0 || gap < 0) return HXA_E_ARG;
+  if ((uintptr_t)x % 16 || (uintptr_t)W % 16) return HXA_E_ARG;
+  constexpr int RPW = 8;
+  const dim3 grid((unsigned)((N + 4 * RPW - 1) / (4 * RPW)));
+#define HXA_MODGEMV(KC, EPL)                                                                                       \
+  hipLaunchKernelGGL((modgemv_kernel<KC, EPL>), grid, dim3(256), 0, st, x, W, N, y, per, ostride, split, gap, act, RPW)
+  if (K % 512) {
+    switch (K / 256) {
+      case 1: HXA_MODGEMV(1, 4); break;
+      case 3: HXA_MODGEMV(3, 4); break;
+      case 5: HXA_MODGEMV(5, 4); break;
+      case 7: HXA_MODGEMV(7, 4); break;
+      default: return HXA_E_ARG;
+    }
+  } else {
+    switch (K / 512) {
+      case 1: HXA_MODGEMV(1, 8); break;
+      case 2: HXA_MODGEMV(2, 8); break;
+      case 3: HXA_MODGEMV(3, 8); break;
+      case 4: HXA_MODGEMV(4, 8); break;
+      case 5: HXA_MODGEMV(5, 8); break;
+      case 6: HXA_MODGEMV(6, 8); break;
+      case 7: HXA_MODGEMV(7, 8); break;
+      case 8: HXA_MODGEMV(8, 8); break;
+      default: return HXA_E_ARG;
+    }
+  }
+#undef HXA_MODGEMV
   return LAUNCH_OK();
 }
 

@@ -76,7 +76,7 @@ HXA_DEV void dq4_word(uint32_t d, half2_t s2, half2_t z2, uint32_t *o) {
 HXA_DEV float gelu_tanh_f(float t) {
   // 0.5 t (1 + tanh u) written as t / (1 + exp(-2u)) (kern.c:116-132): no cancellation for negative t
   const float u = 0.7978845608028654f * (t + 0.044715f * t * t * t);
-  return t / (1.0f + __expf(-2.0f * u));
+  return t * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * u));  // v_rcp_f32 (1 ulp): far below the fp16 rounding
 }
 HXA_DEV float gelu_erf_f(float t) {
   // kern.c:248-260: f16(max(t,0) - T2(|t|)), T2 = f16(|t| * 0.5 * erfc(|t|/sqrt 2))
@@ -361,10 +361,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     }
     return;
   }
-  // local columns [0, nsplit) row-major, [nsplit, BN) transposed into out_t
+  // local columns [0, nsplit) row-major, [nsplit, BN) transposed into out_t. Without out_t the chunk count per row
+  // is the compile-time BN / 8 (no runtime division in the loop).
   const int nsplit = p.out_t == nullptr ? BN : min(max(p.split_col - n0, 0), BN);
-  for (int c = tid; c < BM * (nsplit / 8); c += 256) {
-    const int ml = c / (nsplit / 8), nl = (c % (nsplit / 8)) * 8;
+  auto rows_pass = [&](auto ncols_c) {
+  const int nc8 = ncols_c / 8;
+  for (int c = tid; c < BM * nc8; c += 256) {
+    const int ml = c / nc8, nl = (c % nc8) * 8;
     const int m = m0 + ml, n = n0 + nl;
     if (m >= p.M || n >= p.N) continue;
     half8_t v = *(const half8_t *)(Cs + ml * CROW + nl);
@@ -393,6 +396,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
       *(half8_t *)(p.out + o) = v;
     }
   }
+  };
+  if (p.out_t == nullptr)
+    rows_pass(std::integral_constant<int, BN>{});
+  else
+    rows_pass(nsplit);
   if (nsplit < BN) {  // transposed columns: chunk = (column, 8 consecutive rows)
     const int ncol = BN - nsplit;
     for (int c = tid; c < ncol * (BM / 8); c += 256) {

@@ -57,6 +57,10 @@ int hxa_fill_const_launch(void *dst, int dtype, size_t n, float v, hipStream_t s
 // caller-side glue (phone/animad.cpp)
 int hxa_patchify_launch(const float *lat, int B, int Cc, int H, int W, float *tok, hipStream_t st);
 // M <= 8: GEMV (one wave per output; output index n -> n + gap for n >= split); M > 8: K <= 64 (patch embed)
+// stacked GEMV: y[(n / per) * ostride + r + (r >= split ? gap : 0)] = sum_k act(x[k]) W[n][k], r = n % per;
+// K % 256 == 0, K <= 4096; act 1 = SiLU on the input
+int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, int per, long ostride, int split, int gap,
+                       int act, hipStream_t st);
 int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W, int N, float *y, long ldy, int act,
                           const float *bias, int split, int gap, hipStream_t st);
 // final layer over B images of T image tokens (image b's rows start at b*xrows); dtp == NULL: lat = v,
