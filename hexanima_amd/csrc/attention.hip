@@ -5,156 +5,214 @@
 // (moss/hexagon/mega/blk.c:56-58). No 1/sqrt(d) is applied: it is folded into the q RMSNorm gain
 // (export_all.py:31-32). Keys >= nvalid get probability 0.
 //
-// Each wave owns 32 queries of one head. It computes S^T = K . Q^T with v_mfma_f32_32x32x16_f16, so every lane
-// holds 16 scores of ONE query (its partner lane l^32 holds the other 16 of the 32-key block): the row max and
-// row sum need only one cross-lane exchange, and the fp16 probabilities already sit in the B-operand layout of
-// O^T += V^T . P^T. V is consumed transposed (V^T [H*128][keys]), which the V projection writes directly.
-// K / V^T tiles of 64 keys are staged in LDS (double buffered) and shared by the 4 waves of a workgroup.
+// Work split: a workgroup of 8 waves owns 128 queries of one head. Waves 0-3 take the first half of the key tiles,
+// waves 4-7 the second half (two waves per SIMD, so one wave's softmax overlaps the other's MFMAs); the halves are
+// merged through LDS at the end. Each wave owns 32 queries and keeps Q in registers.
+//
+// Per 64-key tile a wave computes S^T = K . Q^T (v_mfma_f32_32x32x16_f16), so a lane holds 16 scores of ONE query
+// and the row max needs a single shfl_xor(32). K rows are stored in LDS with rows 4-7 and 8-11 of every 16 swapped,
+// which makes the scores of lane l (keys 8*(l/32)+0..7 of each 16-key slice) exactly the B operand of
+// O^T += V^T . P^T: P goes from the accumulator to the PV MFMA with one fp16 conversion, and each V^T fragment is one
+// 16-byte LDS read. K and V^T tiles move global -> LDS directly (global_load_lds_dwordx4), XOR-swizzled so the
+// fragment reads are bank-conflict free, double buffered, one barrier per tile. The QK MFMAs of tile j+1 are issued
+// before the softmax of tile j so the exponentials overlap them. exp(s - m) is exp2(s*log2e - m*log2e) (one FMA +
+// v_exp_f32). O and the row sum are rescaled only when the running max grows by more than 5.5 (P <= e^5.5 in fp16
+// otherwise), which keeps the result exact up to rounding while skipping most rescales.
 #include "hxa_common.h"
 #include "kernels.h"
 
 namespace {
 
-constexpr int KT = 64;          // keys per tile
-constexpr int KROW = 128 + 8;   // K tile row (halves)
-constexpr int VROW = KT + 8;    // V^T tile row (halves)
-constexpr int NW = 4;           // waves per workgroup
-constexpr int NT = NW * 64;
-constexpr int K_STAGE = KT * KROW, V_STAGE = 128 * VROW;
-constexpr int LDS_BYTES = 2 * (K_STAGE + V_STAGE) * (int)sizeof(hxa_h);
-constexpr int KCH = KT * 16 / NT;   // 16-byte K chunks per thread
-constexpr int VCH = 128 * 8 / NT;   // 16-byte V^T chunks per thread
+constexpr int KT = 64;                        // keys per tile
+constexpr int NWH = 4;                        // waves per key half
+constexpr int NT = 2 * NWH * 64;              // 512 threads
+constexpr int QB = NWH * 32;                  // queries per workgroup
+constexpr int TILE_BYTES = KT * 128 * 2;      // K tile [64 keys][128] = V^T tile [128][64 keys] = 16 KB
+constexpr int HALF_BYTES = 4 * TILE_BYTES;    // K[2] | V[2]
+constexpr int LDS_BYTES = 2 * HALF_BYTES;     // 128 KB
+constexpr float L2E = 1.4426950408889634f;
+constexpr float RESCALE_TH = 5.5f;
 
-__global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p) {
-  extern __shared__ __attribute__((aligned(16))) hxa_h lds[];
-  hxa_h *const Ks0 = lds, *const Vs0 = lds + 2 * K_STAGE;
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, ql = lane & 31;
+// key (within the tile) held by LDS row i of a K tile: rows 4-7 and 8-11 of each 16-row group are swapped
+HXA_DEV int krow_key(int i) {
+  const int b = i & 15, q4 = b >> 2;
+  return (i & ~15) + (q4 == 1 ? b + 4 : q4 == 2 ? b - 4 : b);
+}
+
+HXA_DEV float16_t mfma(half8_t a, half8_t b, float16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+
+__global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = wave >> 2, wq = wave & 3, g = lane >> 5, ql = lane & 31;
+  // XCD-aware order: the query blocks of one head run on one XCD (its L2 keeps that head's K / V^T)
+  const int ntot = nqb * p.H, bid = blockIdx.x;
+  const int tile = (ntot % 8 == 0) ? (bid % 8) * (ntot / 8) + bid / 8 : bid;
+  const int h = tile / nqb, qb = tile % nqb, b = blockIdx.y;
   const hxa_h *q = p.q + (long)b * p.q_bstride + h * 128;
   const hxa_h *k = p.k + (long)b * p.k_bstride + h * 128;
   const hxa_h *vt = p.vt + (long)b * p.vt_bstride + (long)h * 128 * p.ldvt;
   hxa_h *o = p.o + (long)b * p.o_bstride + h * 128;
 
-  const int qrow = blockIdx.x * (NW * 32) + wave * 32 + ql;
+  const int qrow = qb * QB + wq * 32 + ql;
   const bool qok = qrow < p.T;
   half8_t qf[8];
 #pragma unroll
-  for (int s = 0; s < 8; s++)
-    qf[s] = qok ? *(const half8_t *)(q + (long)qrow * p.ldq + s * 16 + 8 * g) : (half8_t){};
+  for (int s = 0; s < 8; s++) qf[s] = qok ? *(const half8_t *)(q + (long)qrow * p.ldq + s * 16 + 8 * g) : (half8_t){};
+
+  // key tiles covering [0, nvalid); half 0 takes [0, nh), half 1 takes [nh, ntiles)
+  const int ntiles = (p.nvalid + KT - 1) / KT, nh = (ntiles + 1) / 2;
+  const int t0 = half * nh, nmine = min(nh, ntiles - t0);
+  uint8_t *const hb = lds + half * HALF_BYTES;
+  auto kbuf = [&](int i) { return hb + (i & 1) * TILE_BYTES; };
+  auto vbuf = [&](int i) { return hb + (2 + (i & 1)) * TILE_BYTES; };
+
+  // local tile i -> LDS: 16 KB of K (rows of 256 B, 16 chunks, chunk c at c ^ (row & 15)) and 16 KB of V^T (rows of
+  // 128 B, 8 chunks, chunk c at c ^ ((row >> 1) & 7)); each wave moves 4 + 4 blocks of 1 KB. Keys past NKV read a valid
+  // row (their probability is 0).
+  auto load_kv = [&](int i, bool with_k, bool with_v) {
+    const int key0 = (t0 + i) * KT;
+    if (with_k) {
+      uint8_t *dst = kbuf(i);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int blk = j * NWH + wq, row = 4 * blk + (lane >> 4), c = (lane & 15) ^ (row & 15);
+        const int key = min(key0 + krow_key(row), p.NKV - 1);
+        g2l16(k + (long)key * p.ldk + c * 8, dst + blk * 1024);
+      }
+    }
+    if (with_v) {
+      uint8_t *dst = vbuf(i);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int blk = j * NWH + wq, d = 8 * blk + (lane >> 3), c = (lane & 7) ^ ((d >> 1) & 7);
+        int key = key0 + c * 8;
+        if (key >= p.NKV) key = 0;
+        g2l16(vt + (long)d * p.ldvt + key, dst + blk * 1024);
+      }
+    }
+  };
 
   float16_t acc[4];
 #pragma unroll
   for (int d = 0; d < 4; d++) acc[d] = (float16_t){};
   float mrun = -INFINITY, lsum = 0.0f;
 
-  uint4_t rk[KCH], rv[VCH];
-  auto load = [&](int t) {
-    const int key0 = t * KT;
+  auto qk = [&](int i, float16_t(&S)[2]) {
+    const uint8_t *kb = kbuf(i);
+    S[0] = (float16_t){};
+    S[1] = (float16_t){};
 #pragma unroll
-    for (int i = 0; i < KCH; i++) {
-      const int c = tid + i * NT, r = c >> 4, cc = c & 15, key = key0 + r;
-      rk[i] = key < p.NKV ? *(const uint4_t *)(k + (long)key * p.ldk + cc * 8) : (uint4_t){0, 0, 0, 0};
-    }
+    for (int ds = 0; ds < 8; ds++)
 #pragma unroll
-    for (int i = 0; i < VCH; i++) {
-      const int c = tid + i * NT, r = c >> 3, cc = c & 7, key = key0 + cc * 8;
-      rv[i] = key < p.NKV ? *(const uint4_t *)(vt + (long)r * p.ldvt + key) : (uint4_t){0, 0, 0, 0};
-    }
-  };
-  auto store = [&](int buf) {
-    hxa_h *Ks = Ks0 + buf * K_STAGE, *Vs = Vs0 + buf * V_STAGE;
-#pragma unroll
-    for (int i = 0; i < KCH; i++) {
-      const int c = tid + i * NT, r = c >> 4, cc = c & 15;
-      *(uint4_t *)(Ks + r * KROW + cc * 8) = rk[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; i++) {
-      const int c = tid + i * NT, r = c >> 3, cc = c & 7;
-      *(uint4_t *)(Vs + r * VROW + cc * 8) = rv[i];
-    }
-  };
-
-  const int ntiles = (p.NKV + KT - 1) / KT;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int t = 0; t < ntiles; t++) {
-    const int cur = t & 1;
-    if (t + 1 < ntiles) load(t + 1);
-    const hxa_h *Ks = Ks0 + cur * K_STAGE, *Vs = Vs0 + cur * V_STAGE;
-
-    // S^T for two 32-key blocks: lane holds keys 8*(r/4) + 4*g + (r%4) of query ql
-    float16_t sc[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; kb++) {
-      sc[kb] = (float16_t){};
-#pragma unroll
-      for (int ds = 0; ds < 8; ds++) {
-        const half8_t kf = *(const half8_t *)(Ks + (kb * 32 + ql) * KROW + ds * 16 + 8 * g);
-        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ds], sc[kb], 0, 0, 0);
+      for (int kb2 = 0; kb2 < 2; kb2++) {
+        const int row = kb2 * 32 + ql, c = 2 * ds + g;
+        const half8_t kf = *(const half8_t *)(kb + row * 256 + ((c ^ (row & 15)) << 4));
+        S[kb2] = mfma(kf, qf[ds], S[kb2]);
       }
+  };
+
+  // one key tile: (mask, max, rescale) of tile i, then QK of tile i+1 overlapped with the exponentials of tile i,
+  // then O^T += V^T P^T for tile i
+  auto step = [&](int i, float16_t(&Sc)[2], float16_t(&Sn)[2]) {
+    wait_vm<0>();
+    __builtin_amdgcn_s_barrier();  // tile i V^T and tile i+1 K landed; every wave is done with tiles i-1 / i reads
+    if (i + 2 < nmine) load_kv(i + 2, true, false);
+    if (i + 1 < nmine) load_kv(i + 1, false, true);
+    const bool cur = i < nmine, nxt = i + 1 < nmine;
+    if (!cur) return;
+    const int key0 = (t0 + i) * KT;
+    if (key0 + KT > p.nvalid) {
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          if (key0 + kb2 * 32 + 16 * (r >> 3) + 8 * g + (r & 7) >= p.nvalid) Sc[kb2][r] = -INFINITY;
     }
-    // mask keys >= nvalid and take the tile max
     float mt = -INFINITY;
-    const int key0 = t * KT;
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++)
+    for (int kb2 = 0; kb2 < 2; kb2++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int key = key0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (key >= p.nvalid) sc[kb][r] = -INFINITY;
-        mt = fmaxf(mt, sc[kb][r]);
-      }
+      for (int r = 0; r < 16; r++) mt = fmaxf(mt, Sc[kb2][r]);
     mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float mnew = fmaxf(mrun, mt);
-    const float alpha = mnew == -INFINITY ? 1.0f : __expf(mrun - mnew);
-    const float mref = mnew == -INFINITY ? 0.0f : mnew;
-    mrun = mnew;
-    lsum *= alpha;
+    const bool need = mt > mrun + RESCALE_TH;  // also when mrun is still -inf
+    if (__any(need)) {
+      const float alpha = need ? __builtin_amdgcn_exp2f((mrun - mt) * L2E) : 1.0f;
+      if (need) mrun = mt;
+      lsum *= alpha;
 #pragma unroll
-    for (int d = 0; d < 4; d++) acc[d] *= alpha;
-
+      for (int d = 0; d < 4; d++) acc[d] *= alpha;
+    }
+    const float mb = (mrun == -INFINITY ? 0.0f : mrun) * L2E;
+    if (nxt) qk(i + 1, Sn);
     half8_t pf[2][2];
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++)
+    for (int kb2 = 0; kb2 < 2; kb2++)
 #pragma unroll
       for (int ks = 0; ks < 2; ks++)
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-          const hxa_h ph = (hxa_h)__expf(sc[kb][8 * ks + e] - mref);
-          pf[kb][ks][e] = ph;
-          lsum += (float)ph;
+          const float pv = __builtin_amdgcn_exp2f(fmaf(Sc[kb2][8 * ks + e], L2E, -mb));
+          lsum += pv;
+          pf[kb2][ks][e] = (hxa_h)pv;
         }
-    // O^T += V^T . P^T ; B operand keys of slice ks: {16ks + 4g + 0..3, 16ks + 8 + 4g + 0..3}
+    const uint8_t *vb = vbuf(i);
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++)
+    for (int kb2 = 0; kb2 < 2; kb2++)
 #pragma unroll
       for (int ks = 0; ks < 2; ks++)
 #pragma unroll
-        for (int d = 0; d < 4; d++) {
-          const hxa_h *vr = Vs + (d * 32 + ql) * VROW + kb * 32 + ks * 16 + 4 * g;
-          const half4_t v0 = *(const half4_t *)vr, v1 = *(const half4_t *)(vr + 8);
-          const half8_t va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-          acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf[kb][ks], acc[d], 0, 0, 0);
+        for (int dblk = 0; dblk < 4; dblk++) {
+          const int d = dblk * 32 + ql, c = 4 * kb2 + 2 * ks + g;
+          const half8_t va = *(const half8_t *)(vb + d * 128 + ((c ^ ((d >> 1) & 7)) << 4));
+          acc[dblk] = mfma(va, pf[kb2][ks], acc[dblk]);
         }
-    if (t + 1 < ntiles) store(cur ^ 1);
-    __syncthreads();
+  };
+
+  if (nmine > 0) load_kv(0, true, true);
+  if (nmine > 1) load_kv(1, true, false);
+  wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+  float16_t Sa[2], Sb[2];
+  if (nmine > 0) qk(0, Sa);
+  for (int i = 0; i < nh; i += 2) {
+    step(i, Sa, Sb);
+    if (i + 1 < nh) step(i + 1, Sb, Sa);
   }
 
-  const float ltot = lsum + __shfl_xor(lsum, 32);
-  const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
-  if (qok) {
+  // merge the two key halves: half 1 publishes (m, l, O) per lane, half 0 combines and stores
+  __syncthreads();
+  float *xch = (float *)lds + wq * 66 * 64;
+  if (half == 1) {
+    xch[lane] = mrun;
+    xch[64 + lane] = lsum;
 #pragma unroll
     for (int d = 0; d < 4; d++)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; r4++) {
-        const int dim = d * 32 + 8 * r4 + 4 * g;
-        const half4_t v = {(hxa_h)(acc[d][4 * r4] * inv), (hxa_h)(acc[d][4 * r4 + 1] * inv), (hxa_h)(acc[d][4 * r4 + 2] * inv),
-                           (hxa_h)(acc[d][4 * r4 + 3] * inv)};
-        *(half4_t *)(o + (long)qrow * p.ldo + dim) = v;
-      }
+      for (int r = 0; r < 16; r++) xch[(2 + d * 16 + r) * 64 + lane] = acc[d][r];
   }
+  __syncthreads();
+  if (half == 1 || !qok) return;
+  const float m2 = xch[lane], l2 = xch[64 + lane];
+  const float m = fmaxf(mrun, m2);
+  const float a1 = mrun == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((mrun - m) * L2E);
+  const float a2 = m2 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m2 - m) * L2E);
+  const float lp = lsum * a1 + l2 * a2;
+  const float ltot = lp + __shfl_xor(lp, 32);
+  const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+#pragma unroll
+  for (int d = 0; d < 4; d++)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; r4++) {
+      half4_t v;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int r = 4 * r4 + e;
+        v[e] = (hxa_h)((acc[d][r] * a1 + xch[(2 + d * 16 + r) * 64 + lane] * a2) * inv);
+      }
+      *(half4_t *)(o + (long)qrow * p.ldo + d * 32 + 8 * r4 + 4 * g) = v;
+    }
 }
 
 }  // namespace
@@ -164,13 +222,15 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   if (p.nvalid < 1 || p.nvalid > p.NKV) return HXA_E_ARG;
   if ((p.NKV % 8) || (p.ldq % 8) || (p.ldk % 8) || (p.ldvt % 8) || (p.ldo % 4) || p.ldvt < p.NKV) return HXA_E_ARG;
   if (((uintptr_t)p.q | (uintptr_t)p.k | (uintptr_t)p.vt) % 16 || (uintptr_t)p.o % 8) return HXA_E_ARG;
+  if (p.q_bstride % 8 || p.k_bstride % 8 || p.vt_bstride % 8 || p.o_bstride % 4) return HXA_E_ARG;
   static bool attr = false;
   if (!attr) {
     if (hipFuncSetAttribute((const void *)attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES) != hipSuccess)
       return HXA_E_HIP;
     attr = true;
   }
-  dim3 grid((p.T + NW * 32 - 1) / (NW * 32), p.H, p.batch);
-  hipLaunchKernelGGL(attn_kernel, grid, dim3(NT), LDS_BYTES, st, p);
+  const int nqb = (p.T + QB - 1) / QB;
+  dim3 grid(nqb * p.H, p.batch);
+  hipLaunchKernelGGL(attn_kernel, grid, dim3(NT), LDS_BYTES, st, p, nqb);
   return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
 }

@@ -25,6 +25,21 @@ struct HxaWeight {
   const hxa_h *z;     // [K/32][N] q4 offsets (optional)
 };
 
+// ---- direct-to-LDS loads and VMEM waits (gfx950) ----
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void gmem_void_t;
+
+// s_waitcnt vmcnt(N) only (expcnt / lgkmcnt left at their maxima); encoding of gfx9: vmcnt[3:0] | vmcnt_hi[15:14]
+template <int N>
+HXA_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+// 16 bytes per lane from global memory straight into LDS: lane l writes lds_base + 16 l
+HXA_DEV void g2l16(const void *g, void *lds_base) {
+  __builtin_amdgcn_global_load_lds((gmem_void_t *)g, (lds_void_t *)lds_base, 16, 0, 0);
+}
+
 #define HXA_CHECK(x)                                  \
   do {                                                \
     hipError_t e_ = (x);                              \
