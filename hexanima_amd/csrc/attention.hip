@@ -39,6 +39,16 @@ HXA_DEV int krow_key(int i) {
   return (i & ~15) + (q4 == 1 ? b + 4 : q4 == 2 ? b - 4 : b);
 }
 
+// global_load_lds_dwordx4 issued from inline asm: lane l's 16 bytes land at LDS byte address lds_addr + 16 l (M0).
+// The compiler does not see this as an LDS write, so it keeps exact lgkmcnt waits for the fragment reads around it
+// (it falls back to lgkmcnt(0) while a visible LDS DMA is in flight). Completion is awaited explicitly (vmcnt(0) and
+// a barrier) before any wave reads the tile; LDS reads complete in order, so these loads can only lengthen an
+// lgkmcnt wait, never satisfy one early.
+HXA_DEV void g2l16_asm(const void *g, const void *lds_ptr) {
+  const uint32_t la = (uint32_t)(uintptr_t)(lds_void_t *)lds_ptr;
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
+}
+
 HXA_DEV float16_t mfma(half8_t a, half8_t b, float16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
 
 __global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
@@ -79,7 +89,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
       for (int j = 0; j < 4; j++) {
         const int blk = j * NWH + wq, row = 4 * blk + (lane >> 4), c = (lane & 15) ^ (row & 15);
         const int key = min(key0 + krow_key(row), p.NKV - 1);
-        g2l16(k + (long)key * p.ldk + c * 8, dst + blk * 1024);
+        g2l16_asm(k + (long)key * p.ldk + c * 8, dst + blk * 1024);
       }
     }
     if (with_v) {
@@ -89,7 +99,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
         const int blk = j * NWH + wq, d = 8 * blk + (lane >> 3), c = (lane & 7) ^ ((d >> 1) & 7);
         int key = key0 + c * 8;
         if (key >= p.NKV) key = 0;
-        g2l16(vt + (long)d * p.ldvt + key, dst + blk * 1024);
+        g2l16_asm(vt + (long)d * p.ldvt + key, dst + blk * 1024);
       }
     }
   };
@@ -118,6 +128,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
   auto step = [&](int i, float16_t(&Sc)[2], float16_t(&Sn)[2]) {
     wait_vm<0>();
     __builtin_amdgcn_s_barrier();  // tile i V^T and tile i+1 K landed; every wave is done with tiles i-1 / i reads
+    asm volatile("" ::: "memory");
     if (i + 2 < nmine) load_kv(i + 2, true, false);
     if (i + 1 < nmine) load_kv(i + 1, false, true);
     const bool cur = i < nmine, nxt = i + 1 < nmine;
@@ -145,35 +156,64 @@ __global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
       for (int d = 0; d < 4; d++) acc[d] *= alpha;
     }
     const float mb = (mrun == -INFINITY ? 0.0f : mrun) * L2E;
-    if (nxt) qk(i + 1, Sn);
-    half8_t pf[2][2];
-#pragma unroll
-    for (int kb2 = 0; kb2 < 2; kb2++)
-#pragma unroll
-      for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(Sc[kb2][8 * ks + e], L2E, -mb));
-          lsum += pv;
-          pf[kb2][ks][e] = (hxa_h)pv;
-        }
+    // One straight-line block: QK of tile i+1 (clamped: the last tile recomputes its own, unused scores) with the
+    // K fragments read one step ahead, the exponentials of tile i between its MFMAs, then PV of tile i.
+    const uint8_t *kb = kbuf(nxt ? i + 1 : i);
     const uint8_t *vb = vbuf(i);
+    auto kfrag = [&](int ds, int kb2) {
+      const int row = kb2 * 32 + ql, c = 2 * ds + g;
+      return *(const half8_t *)(kb + row * 256 + ((c ^ (row & 15)) << 4));
+    };
+    auto vfrag = [&](int j) {  // j = (kb2 * 2 + ks) * 4 + dblk
+      const int dblk = j & 3, kk = j >> 2, d = dblk * 32 + ql, c = 2 * kk + g;
+      return *(const half8_t *)(vb + d * 128 + ((c ^ ((d >> 1) & 7)) << 4));
+    };
+    Sn[0] = (float16_t){};
+    Sn[1] = (float16_t){};
+    half8_t pf[2][2];
+    float ls[2] = {0.0f, 0.0f};
+    // sched_barrier(0) fences keep each fragment read one stage ahead of the MFMA that consumes it (the scheduler
+    // would otherwise sink the reads next to their uses under this register pressure)
+    half8_t kf[2][2];
+    kf[0][0] = kfrag(0, 0);
+    kf[0][1] = kfrag(0, 1);
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; kb2++)
+    for (int ds = 0; ds < 8; ds++) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (ds + 1 < 8) {
+        kf[(ds + 1) & 1][0] = kfrag(ds + 1, 0);
+        kf[(ds + 1) & 1][1] = kfrag(ds + 1, 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      Sn[0] = mfma(kf[ds & 1][0], qf[ds], Sn[0]);
+      Sn[1] = mfma(kf[ds & 1][1], qf[ds], Sn[1]);
 #pragma unroll
-      for (int ks = 0; ks < 2; ks++)
+      for (int u = 0; u < 4; u++) {
+        const int idx = ds * 4 + u, kb2 = idx >> 4, r = idx & 15;
+        const float pv = __builtin_amdgcn_exp2f(fmaf(Sc[kb2][r], L2E, -mb));
+        ls[u & 1] += pv;
+        pf[kb2][r >> 3][r & 7] = (hxa_h)pv;
+      }
+    }
+    lsum += ls[0] + ls[1];
+    half8_t va[2];
+    __builtin_amdgcn_sched_barrier(0);
+    va[0] = vfrag(0);
 #pragma unroll
-        for (int dblk = 0; dblk < 4; dblk++) {
-          const int d = dblk * 32 + ql, c = 4 * kb2 + 2 * ks + g;
-          const half8_t va = *(const half8_t *)(vb + d * 128 + ((c ^ ((d >> 1) & 7)) << 4));
-          acc[dblk] = mfma(va, pf[kb2][ks], acc[dblk]);
-        }
+    for (int j = 0; j < 16; j++) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (j + 1 < 16) va[(j + 1) & 1] = vfrag(j + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      acc[j & 3] = mfma(va[j & 1], pf[j >> 3][(j >> 2) & 1], acc[j & 3]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   if (nmine > 0) load_kv(0, true, true);
   if (nmine > 1) load_kv(1, true, false);
   wait_vm<0>();
   __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
   float16_t Sa[2], Sb[2];
   if (nmine > 0) qk(0, Sa);
   for (int i = 0; i < nh; i += 2) {
