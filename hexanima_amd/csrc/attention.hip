@@ -39,16 +39,6 @@ HXA_DEV int krow_key(int i) {
   return (i & ~15) + (q4 == 1 ? b + 4 : q4 == 2 ? b - 4 : b);
 }
 
-// global_load_lds_dwordx4 issued from inline asm: lane l's 16 bytes land at LDS byte address lds_addr + 16 l (M0).
-// The compiler does not see this as an LDS write, so it keeps exact lgkmcnt waits for the fragment reads around it
-// (it falls back to lgkmcnt(0) while a visible LDS DMA is in flight). Completion is awaited explicitly (vmcnt(0) and
-// a barrier) before any wave reads the tile; LDS reads complete in order, so these loads can only lengthen an
-// lgkmcnt wait, never satisfy one early.
-HXA_DEV void g2l16_asm(const void *g, const void *lds_ptr) {
-  const uint32_t la = (uint32_t)(uintptr_t)(lds_void_t *)lds_ptr;
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
-}
-
 HXA_DEV float16_t mfma(half8_t a, half8_t b, float16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
 
 __global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
@@ -89,7 +79,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
       for (int j = 0; j < 4; j++) {
         const int blk = j * NWH + wq, row = 4 * blk + (lane >> 4), c = (lane & 15) ^ (row & 15);
         const int key = min(key0 + krow_key(row), p.NKV - 1);
-        g2l16_asm(k + (long)key * p.ldk + c * 8, dst + blk * 1024);
+        g2l16_opaque(k + (long)key * p.ldk + c * 8, dst + blk * 1024);
       }
     }
     if (with_v) {
@@ -99,7 +89,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
         const int blk = j * NWH + wq, d = 8 * blk + (lane >> 3), c = (lane & 7) ^ ((d >> 1) & 7);
         int key = key0 + c * 8;
         if (key >= p.NKV) key = 0;
-        g2l16_asm(vt + (long)d * p.ldvt + key, dst + blk * 1024);
+        g2l16_opaque(vt + (long)d * p.ldvt + key, dst + blk * 1024);
       }
     }
   };
@@ -222,6 +212,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
   }
 
   // merge the two key halves: half 1 publishes (m, l, O) per lane, half 0 combines and stores
+  wait_vm<0>();  // no tile load may still be writing the LDS reused below
   __syncthreads();
   float *xch = (float *)lds + wq * 66 * 64;
   if (half == 1) {

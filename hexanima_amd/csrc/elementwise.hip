@@ -61,32 +61,52 @@ __global__ __launch_bounds__(256) void normmod_kernel(const float *__restrict__ 
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// per-head RMSNorm * gain + split-half RoPE (kern.c:163-197); one wave per (token, head): lane l owns d = l, l+64
+// per-head RMSNorm * gain + split-half RoPE (kern.c:163-197). 16 lanes per (token, head), lane j owns the 8
+// consecutive dims [8j, 8j+8) (one 16-byte load / store); the RoPE partner of dim d < 64 is d + 64, held by lane j ^ 8.
 // ---------------------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void rmsrope_kernel(hxa_h *q0, hxa_h *q1, const float *g0, const float *g1, long ldq,
                                                       int T, int H, const float *__restrict__ cosT,
                                                       const float *__restrict__ sinT, int ttab) {
-  const long wid = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (wid >= (long)T * H) return;
-  const int t = (int)(wid / H), hd = (int)(wid % H);
+  const long gid = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int j = threadIdx.x & 15;
+  if (gid >= (long)T * H) return;  // whole 16-lane groups leave together; shuffles stay inside a group
+  const int t = (int)(gid / H), hd = (int)(gid % H);
   hxa_h *q = blockIdx.y ? q1 : q0;
   const float *g = blockIdx.y ? g1 : g0;
-  hxa_h *p = q + (long)t * ldq + hd * 128;
-  float a = (float)p[lane], b = (float)p[lane + 64];
-  const float ss = wave_sum(a * a + b * b);
-  const float r = rsqrtf(ss * (1.0f / 128.0f) + 1e-6f);
-  a = a * r * g[lane];
-  b = b * r * g[lane + 64];
-  if (cosT != nullptr) {
-    const int tt = t % ttab;
-    const float c = cosT[(long)tt * 64 + lane], s = sinT[(long)tt * 64 + lane];
-    const float na = a * c - b * s, nb = a * s + b * c;
-    a = na;
-    b = nb;
+  hxa_h *p = q + (long)t * ldq + hd * 128 + 8 * j;
+  const half8_t v = *(const half8_t *)p;
+  float a[8], ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    a[e] = (float)v[e];
+    ss += a[e] * a[e];
   }
-  p[lane] = (hxa_h)a;
-  p[lane + 64] = (hxa_h)b;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);
+  const float r = rsqrtf(ss * (1.0f / 128.0f) + 1e-6f);
+  const float4_t ga = *(const float4_t *)(g + 8 * j), gb = *(const float4_t *)(g + 8 * j + 4);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    a[e] = a[e] * r * ga[e];
+    a[e + 4] = a[e + 4] * r * gb[e];
+  }
+  if (cosT != nullptr) {
+    const int tt = t % ttab, d0 = 8 * (j & 7);
+    const float4_t c0 = *(const float4_t *)(cosT + (long)tt * 64 + d0), c1 = *(const float4_t *)(cosT + (long)tt * 64 + d0 + 4);
+    const float4_t s0 = *(const float4_t *)(sinT + (long)tt * 64 + d0), s1 = *(const float4_t *)(sinT + (long)tt * 64 + d0 + 4);
+    const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+    const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float partner = __shfl_xor(a[e], 8);
+      // d < 64: y[d] = x[d] c - x[d+64] s;  d >= 64: y[d] = x[d-64] s + x[d] c
+      a[e] = j < 8 ? a[e] * cs[e] - partner * sn[e] : partner * sn[e] + a[e] * cs[e];
+    }
+  }
+  half8_t o;
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = (hxa_h)a[e];
+  *(half8_t *)p = o;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -447,8 +467,8 @@ int hxa_norm_mod_launch(const float *x, long ldx, int T, int D, const float *shi
 
 int hxa_rmsrope_launch(hxa_h *q0, hxa_h *q1, const float *g0, const float *g1, long ldq, int T, int H, const float *cosT,
                        const float *sinT, int ttab, hipStream_t st) {
-  if (T <= 0 || H <= 0 || (cosT && ttab <= 0)) return HXA_E_ARG;
-  dim3 g(nblk((long)T * H, 4), q1 ? 2 : 1);
+  if (T <= 0 || H <= 0 || (cosT && ttab <= 0) || ldq % 8 || (uintptr_t)q0 % 16 || (uintptr_t)q1 % 16) return HXA_E_ARG;
+  dim3 g(nblk((long)T * H, 16), q1 ? 2 : 1);
   hipLaunchKernelGGL(rmsrope_kernel, g, dim3(256), 0, st, q0, q1, g0, g1, ldq, T, H, cosT, sinT, ttab > 0 ? ttab : 1);
   return LAUNCH_OK();
 }

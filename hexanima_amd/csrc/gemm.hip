@@ -94,8 +94,8 @@ HXA_DEV float situ_f(float u, float g) {
 template <int BM, int BN, int FMT>
 struct GemmGeo {
   static constexpr int BK = 32;                                      // k per stage (one quantisation group)
-  static constexpr int NS = 4, PD = 3;                               // LDS ring stages, prefetch distance
   static constexpr int RB = FMT == HXA_W_F16 ? 64 : FMT == HXA_W_Q8 ? 32 : 16;  // W bytes per row per stage
+  static constexpr int NS = 4, PD = NS - 1;  // LDS ring stages, prefetch distance
   static constexpr int A_BYTES = BM * 64;
   static constexpr int W_BYTES = BN * RB;
   static constexpr int S_BYTES = FMT == HXA_W_F16 ? 0 : (BN * 2 + 15) / 16 * 16;
@@ -113,24 +113,24 @@ HXA_DEV constexpr int loads_per_stage(int wave) {
   using G = GemmGeo<BM, BN, FMT>;
   return G::NA + (G::TW / 4 + (wave < G::TW % 4 ? 1 : 0)) + (FMT != HXA_W_F16 && wave == 0 ? (ASYM ? 2 : 1) : 0);
 }
-// wait until at most `later` further stages of loads are outstanding for this wave
-template <int BM, int BN, int FMT, bool ASYM, int WAVE>
-HXA_DEV void wait_stage_w(int later) {
+// wait until at most LATER further stages of loads are outstanding for this wave
+template <int BM, int BN, int FMT, bool ASYM, int WAVE, int LATER>
+HXA_DEV void wait_stage_w() {
   constexpr int n = loads_per_stage<BM, BN, FMT, ASYM>(WAVE);
-  if (later >= 2) wait_vm<2 * n>();
-  else if (later == 1) wait_vm<n>();
-  else wait_vm<0>();
+  wait_vm<LATER * n>();
 }
-template <int BM, int BN, int FMT, bool ASYM>
-HXA_DEV void wait_stage(int wave, int later) {
-  static_assert(GemmGeo<BM, BN, FMT>::PD == 3, "wait_stage handles up to two later stages");
-  if (wave == 0) wait_stage_w<BM, BN, FMT, ASYM, 0>(later);
-  else if (wave == 1) wait_stage_w<BM, BN, FMT, ASYM, 1>(later);
-  else if (wave == 2) wait_stage_w<BM, BN, FMT, ASYM, 2>(later);
-  else wait_stage_w<BM, BN, FMT, ASYM, 3>(later);
+template <int BM, int BN, int FMT, bool ASYM, int LATER>
+HXA_DEV void wait_stage(int wave) {
+  if (wave == 0) wait_stage_w<BM, BN, FMT, ASYM, 0, LATER>();
+  else if (wave == 1) wait_stage_w<BM, BN, FMT, ASYM, 1, LATER>();
+  else if (wave == 2) wait_stage_w<BM, BN, FMT, ASYM, 2, LATER>();
+  else wait_stage_w<BM, BN, FMT, ASYM, 3, LATER>();
 }
 
-template <int BM, int BN, int FMT, bool ASYM>
+// SPLIT2: the first and second halves of K are rounded to fp16 separately and combined in the residual epilogue,
+// x += gate * (f16(first half) + f16(second half)) (blk.c:172-174 + kern.c:330-339 in one kernel): the first half's
+// f16 accumulators are kept in registers while the second half accumulates.
+template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   using G = GemmGeo<BM, BN, FMT>;
   constexpr int WTM = BM / 2, WTN = BN / 2, MI = WTM / 32, NI = WTN / 32;
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
       const int r0 = (wave * G::NA + i) * 16, row = r0 + (lane >> 2);
       const int cl = (lane & 3) ^ ((row >> 2) & 3);
       const int m = min(m0 + row, p.M - 1);
-      g2l16(p.A + (long)m * p.lda + k0 + cl * 8, st + r0 * 64);
+      g2l16_opaque(p.A + (long)m * p.lda + k0 + cl * 8, st + r0 * 64);
     }
     uint8_t *ws = st + G::A_BYTES;
 #pragma unroll
@@ -169,13 +169,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
         if ((G::W_BYTES / 16) % 64 == 0 || chunk < G::W_BYTES / 16) {
           if (FMT == HXA_W_F16) {
             const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3), n = min(n0 + row, p.N - 1);
-            g2l16((const hxa_h *)p.W + (long)n * p.ldw + k0 + cl * 8, ws + t * 1024);
+            g2l16_opaque((const hxa_h *)p.W + (long)n * p.ldw + k0 + cl * 8, ws + t * 1024);
           } else if (FMT == HXA_W_Q8) {
             const int row = chunk >> 1, cl = (chunk & 1) ^ ((row >> 3) & 1), n = min(n0 + row, p.N - 1);
-            g2l16((const int8_t *)p.W + (long)n * p.ldw + k0 + cl * 16, ws + t * 1024);
+            g2l16_opaque((const int8_t *)p.W + (long)n * p.ldw + k0 + cl * 16, ws + t * 1024);
           } else {
             const int row = chunk, n = min(n0 + row, p.N - 1);
-            g2l16((const uint8_t *)p.W + (long)n * p.ldw + (k0 >> 1), ws + t * 1024);
+            g2l16_opaque((const uint8_t *)p.W + (long)n * p.ldw + (k0 >> 1), ws + t * 1024);
           }
         }
       }
@@ -183,8 +183,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     if (FMT != HXA_W_F16 && wave == 0) {
       const int g = k0 >> 5;
       const int nn = min(n0 + lane * 8, p.N - 8);
-      if (lane < BN / 8) g2l16(p.S + (long)g * p.N + nn, ws + G::W_BYTES);
-      if (ASYM && lane < BN / 8) g2l16(p.Z + (long)g * p.N + nn, ws + G::W_BYTES + G::S_BYTES);
+      if (lane < BN / 8) g2l16_opaque(p.S + (long)g * p.N + nn, ws + G::W_BYTES);
+      if (ASYM && lane < BN / 8) g2l16_opaque(p.Z + (long)g * p.N + nn, ws + G::W_BYTES + G::S_BYTES);
     }
   };
 
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     dequant(0, cb, cq, cs, cz);
     mfma_range(ca[0], cb[0], 0, 2);
     __builtin_amdgcn_sched_barrier(0);
-    wait_stage<BM, BN, FMT, ASYM>(wave, 2);  // tile kt+1 complete; tiles kt+2, kt+3 may still fly
+    wait_stage<BM, BN, FMT, ASYM, NS - 2>(wave);  // tile kt+1 complete; tiles kt+2 .. kt+NS-1 may still fly
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();             // stage kt+1 visible; every wave holds its stage kt fragments
     asm volatile("" ::: "memory");
@@ -300,15 +300,31 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   half8_t fa0[2][MI], fb0[2][NI], fa1[2][MI], fb1[2][NI];
 #pragma unroll
   for (int s = 0; s < NS; s++) issue(s, s);
-  wait_stage<BM, BN, FMT, ASYM>(wave, 2);  // tiles 0 and 1 complete
+  wait_stage<BM, BN, FMT, ASYM, NS - 2>(wave);  // tiles 0 and 1 complete
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   read_frags(0, fa0, fb0, wq0, sc0, zc0);
+  [[maybe_unused]] half4_t first[SPLIT2 ? NI : 1][SPLIT2 ? MI : 1][4];
   for (int kt = 0; kt < nk; kt += 2) {
     step(kt, fa0, fb0, fa1, fb1, wq0, sc0, zc0, wq1, sc1, zc1);
     if (kt + 1 < nk) step(kt + 1, fa1, fb1, fa0, fb0, wq1, sc1, zc1, wq0, sc0, zc0);
+    if constexpr (SPLIT2) {
+      if (kt + 2 == nk / 2) {  // first half of K done: keep its fp16 rounding, restart the accumulators
+#pragma unroll
+        for (int j = 0; j < NI; j++)
+#pragma unroll
+          for (int i = 0; i < MI; i++) {
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+              first[j][i][q] = (half4_t){(hxa_h)acc[j][i][4 * q], (hxa_h)acc[j][i][4 * q + 1], (hxa_h)acc[j][i][4 * q + 2],
+                                         (hxa_h)acc[j][i][4 * q + 3]};
+            acc[j][i] = (float16_t){};
+          }
+      }
+    }
   }
+  wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
   __syncthreads();
 
   // ---- epilogue. Stage f16(acc) through LDS as a row-major [BM][CROW] tile: lane holds, for block (j, i),
@@ -326,6 +342,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
           const half4_t v = {(hxa_h)acc[j][i][4 * q], (hxa_h)acc[j][i][4 * q + 1], (hxa_h)acc[j][i][4 * q + 2],
                              (hxa_h)acc[j][i][4 * q + 3]};
           *(half4_t *)(Cs + (ml + i * 32) * CROW + nl + j * 32 + 8 * q) = v;
+          if constexpr (SPLIT2) *(half4_t *)(Cs + BM * CROW + (ml + i * 32) * CROW + nl + j * 32 + 8 * q) = first[j][i][q];
         }
   }
   __syncthreads();
@@ -350,6 +367,52 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   // local columns [0, nsplit) row-major, [nsplit, BN) transposed into out_t. Without out_t the chunk count per row
   // is the compile-time BN / 8 (no runtime division in the loop).
   const int nsplit = p.out_t == nullptr ? BN : min(max(p.split_col - n0, 0), BN);
+  if (p.epi == HXA_EPI_RESADD) {
+    // x += gate * t: the x / gate loads of RB chunks are issued together before any of them is used, so a thread
+    // waits one memory latency per batch instead of one per chunk (x stores may alias later x loads otherwise)
+    constexpr int NC8 = BN / 8, ITERS = BM * NC8 / 256, RB = ITERS < 4 ? ITERS : 4;
+    static_assert(BM * NC8 % 256 == 0, "whole chunk passes");
+#pragma unroll
+    for (int b0 = 0; b0 < ITERS; b0 += RB) {
+      float4_t xv[RB][2], gv[RB][2];
+      float t[RB][8];
+      bool ok[RB];
+#pragma unroll
+      for (int u = 0; u < RB; u++) {
+        const int c = tid + (b0 + u) * 256, ml = c / NC8, nl = (c % NC8) * 8, m = m0 + ml, n = n0 + nl;
+        ok[u] = m < p.M && n < p.N;
+        if (ok[u]) {
+          const float4_t *xp = (const float4_t *)(p.x + (long)m * p.ldx + n);
+          xv[u][0] = xp[0];
+          xv[u][1] = xp[1];
+          gv[u][0] = *(const float4_t *)(p.gate + n);
+          gv[u][1] = *(const float4_t *)(p.gate + n + 4);
+          const half8_t v = *(const half8_t *)(Cs + ml * CROW + nl);
+#pragma unroll
+          for (int e = 0; e < 8; e++) t[u][e] = (float)v[e];
+          if constexpr (SPLIT2) {
+            const half8_t v1 = *(const half8_t *)(Cs + BM * CROW + ml * CROW + nl);
+#pragma unroll
+            for (int e = 0; e < 8; e++) t[u][e] = (float)v1[e] + t[u][e];
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < RB; u++) {
+        if (!ok[u]) continue;
+        const int c = tid + (b0 + u) * 256, ml = c / NC8, nl = (c % NC8) * 8;
+        float4_t *xp = (float4_t *)(p.x + (long)(m0 + ml) * p.ldx + n0 + nl);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          xv[u][0][e] = fmaf(gv[u][0][e], t[u][e], xv[u][0][e]);
+          xv[u][1][e] = fmaf(gv[u][1][e], t[u][e + 4], xv[u][1][e]);
+        }
+        xp[0] = xv[u][0];
+        xp[1] = xv[u][1];
+      }
+    }
+    return;
+  }
   auto rows_pass = [&](auto ncols_c) {
   const int nc8 = ncols_c / 8;
   for (int c = tid; c < BM * nc8; c += 256) {
@@ -358,18 +421,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     if (m >= p.M || n >= p.N) continue;
     half8_t v = *(const half8_t *)(Cs + ml * CROW + nl);
     const long o = (long)m * p.ldo + n;
-    if (p.epi == HXA_EPI_RESADD) {
-      float4_t *xp = (float4_t *)(p.x + (long)m * p.ldx + n);
-      const float4_t g0 = *(const float4_t *)(p.gate + n), g1 = *(const float4_t *)(p.gate + n + 4);
-      float4_t x0 = xp[0], x1 = xp[1];
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        x0[e] = fmaf(g0[e], (float)v[e], x0[e]);
-        x1[e] = fmaf(g1[e], (float)v[e + 4], x1[e]);
-      }
-      xp[0] = x0;
-      xp[1] = x1;
-    } else if (p.epi == HXA_EPI_PARTIAL) {
+    if (p.epi == HXA_EPI_PARTIAL) {
       *(half8_t *)(p.out + (long)z * p.out_zstride + o) = v;
     } else {
       if (p.epi == HXA_EPI_GELU_TANH) {
@@ -411,10 +463,11 @@ struct TileCfg {
 };
 constexpr TileCfg kCfgs[] = {{192, 256}, {192, 192}, {192, 128}, {256, 128}, {128, 256}, {128, 128}, {64, 128}, {128, 64}};
 
-template <int BM, int BN, int FMT, bool ASYM>
+template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false>
 hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
-  auto kern = gemm_kernel<BM, BN, FMT, ASYM>;
-  const int lds = GemmGeo<BM, BN, FMT>::LDS;
+  auto kern = gemm_kernel<BM, BN, FMT, ASYM, SPLIT2>;
+  using G = GemmGeo<BM, BN, FMT>;
+  const int lds = SPLIT2 && 2 * G::C_BYTES > G::LDS ? 2 * G::C_BYTES : G::LDS;
   static bool attr = false;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -424,6 +477,13 @@ hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
   dim3 grid(p.tiles_m * p.tiles_n, 1, ksplit);
   hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, p);
   return hipGetLastError();
+}
+
+template <int FMT, bool ASYM>
+hipError_t launch_split2(int bm, int bn, const GemmParams &p, hipStream_t st) {
+  if (bm == 128 && bn == 128) return launch_t<128, 128, FMT, ASYM, true>(p, 1, st);
+  if (bm == 64 && bn == 128) return launch_t<64, 128, FMT, ASYM, true>(p, 1, st);
+  return hipErrorInvalidValue;
 }
 
 template <int FMT, bool ASYM>
@@ -457,6 +517,7 @@ static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int *bm, int *
   for (const TileCfg &c : kCfgs) {
     if (fmt == HXA_W_Q4 && c.bn < 128) continue;
     if (epi == HXA_EPI_SITU && c.bn % 128 != 0) continue;  // each wave needs whole (up, gate) block pairs
+    if (epi == HXA_EPI_RESADD_SPLIT2 && !(c.bn == 128 && (c.bm == 128 || c.bm == 64))) continue;  // register budget
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ksplit;
     const long waves = (tiles + g_num_cu - 1) / g_num_cu;
     const double useful = (double)M * N / ((double)((M + c.bm - 1) / c.bm) * c.bm * ((N + c.bn - 1) / c.bn) * c.bn);
@@ -477,8 +538,11 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   if (g.epi == HXA_EPI_SITU && (w.N % 64) != 0) return HXA_E_ARG;
   if ((g.lda % 8) != 0 || ((uintptr_t)g.A % 16) != 0 || ((uintptr_t)w.w % 16) != 0) return HXA_E_ARG;
   if (w.N % 8 != 0) return HXA_E_ARG;  // 16-byte epilogue chunks
-  if (g.epi == HXA_EPI_RESADD ? ((g.ldx % 8) != 0 || ((uintptr_t)g.x % 32) != 0 || ((uintptr_t)g.gate % 32) != 0)
-                              : ((g.ldo % 8) != 0 || ((uintptr_t)g.out % 16) != 0))
+  const bool split2 = g.epi == HXA_EPI_RESADD_SPLIT2;
+  if (split2 && (g.ksplit != 1 || w.K % 128 != 0)) return HXA_E_ARG;  // two halves of whole k-step pairs
+  if (g.epi == HXA_EPI_RESADD || split2
+          ? ((g.ldx % 8) != 0 || ((uintptr_t)g.x % 32) != 0 || ((uintptr_t)g.gate % 32) != 0)
+          : ((g.ldo % 8) != 0 || ((uintptr_t)g.out % 16) != 0))
     return HXA_E_ARG;
   GemmParams p{};
   if (g.epi == HXA_EPI_STORE_T) {  // all columns transposed
@@ -502,7 +566,7 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   p.N = w.N;
   p.Ktot = w.K;
   p.Kslice = w.K / g.ksplit;
-  p.epi = g.epi;
+  p.epi = split2 ? HXA_EPI_RESADD : g.epi;
   p.out = g.epi == HXA_EPI_STORE_T ? nullptr : g.out;
   p.ldo = g.ldo;
   p.out_zstride = g.out_zstride;
@@ -515,10 +579,18 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
     bm = g.force_bm;
     bn = g.force_bn;
     if ((g.epi == HXA_EPI_SITU && bn % 128 != 0) || (w.fmt == HXA_W_Q4 && bn < 128)) return HXA_E_ARG;
+    if (split2 && !(bn == 128 && (bm == 128 || bm == 64))) return HXA_E_ARG;
   }
   p.tiles_m = (g.M + bm - 1) / bm;
   p.tiles_n = (w.N + bn - 1) / bn;
   hipError_t e;
+  if (split2) {
+    if (w.fmt == HXA_W_F16) e = launch_split2<HXA_W_F16, false>(bm, bn, p, st);
+    else if (w.fmt == HXA_W_Q8) e = launch_split2<HXA_W_Q8, false>(bm, bn, p, st);
+    else if (w.z) e = launch_split2<HXA_W_Q4, true>(bm, bn, p, st);
+    else e = launch_split2<HXA_W_Q4, false>(bm, bn, p, st);
+    return e == hipSuccess ? HXA_OK : HXA_E_HIP;
+  }
   if (w.fmt == HXA_W_F16) e = launch_fmt<HXA_W_F16, false>(bm, bn, p, g.ksplit, st);
   else if (w.fmt == HXA_W_Q8) e = launch_fmt<HXA_W_Q8, false>(bm, bn, p, g.ksplit, st);
   else if (w.z) e = launch_fmt<HXA_W_Q4, true>(bm, bn, p, g.ksplit, st);

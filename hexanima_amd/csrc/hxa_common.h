@@ -40,6 +40,16 @@ HXA_DEV void g2l16(const void *g, void *lds_base) {
   __builtin_amdgcn_global_load_lds((gmem_void_t *)g, (lds_void_t *)lds_base, 16, 0, 0);
 }
 
+// global_load_lds_dwordx4 issued from inline asm: lane l's 16 bytes land at LDS byte address lds_addr + 16 l (M0).
+// The compiler does not see this as an LDS write, so it keeps exact lgkmcnt waits for the fragment reads around it
+// (it falls back to lgkmcnt(0) while a visible LDS DMA is in flight). Completion is awaited explicitly (vmcnt(0) and
+// a barrier) before any wave reads the tile; LDS reads complete in order, so these loads can only lengthen an
+// lgkmcnt wait, never satisfy one early.
+HXA_DEV void g2l16_opaque(const void *g, const void *lds_ptr) {
+  const uint32_t la = (uint32_t)(uintptr_t)(lds_void_t *)lds_ptr;
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
+}
+
 #define HXA_CHECK(x)                                  \
   do {                                                \
     hipError_t e_ = (x);                              \

@@ -144,7 +144,7 @@ static int gemm_common(const void *A, long lda, int M, int fmt, const void *w, c
                        const float *gate, void *out_t, long ldo_t, int split_col, int bm, int bn, void *stream) {
   if (!A || !w) return fail(HXA_E_ARG, "gemm: null operand");
   if (fmt < HXA_W_F16 || fmt > HXA_W_Q4) return fail(HXA_E_MODE, "gemm: format %d", fmt);
-  if (epi == HXA_EPI_RESADD ? (!x || !gate) : !out) return fail(HXA_E_ARG, "gemm: null output");
+  if (epi == HXA_EPI_RESADD || epi == HXA_EPI_RESADD_SPLIT2 ? (!x || !gate) : !out) return fail(HXA_E_ARG, "gemm: null output");
   HxaWeight wt{fmt, N, K, w, (const hxa_h *)s, (const hxa_h *)z};
   HxaGemm g{};
   g.A = (const hxa_h *)A;
@@ -436,6 +436,13 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     return HXA_OK;
   };
 
+  // split-K down projection + gated residual (blk.c:172-174): two fp16 partial GEMMs over 2x the workgroups (fills
+  // the GPU at N = D) then the residual; measured faster than the single-launch HXA_EPI_RESADD_SPLIT2 form, whose
+  // 128-wide tiles leave a quarter of the CUs idle at 1536 x 2048
+  auto down_resadd = [&](const hxa_h *a, const HxaWeight &w, const float *gate) -> int {
+    TRY(gemm(a, F, BT, w, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
+    return hxa_resadd2_launch(x, D, t1, t2, D, BT, D, gate, st);
+  };
   if (d->kind == 0) {
     const float *gain = pv.vec;
     const HxaWeight &Wqkv = pv.w[0], &Wo = pv.w[1], &Wcq = pv.w[2], &Wckv = pv.w[3], &Wco = pv.w[4], &W1 = pv.w[5],
@@ -471,8 +478,7 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     STAGE_DONE();
     TRY(gemm(h, D, BT, W1, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
-    TRY(gemm(mid, F, BT, W2, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
-    TRY(hxa_resadd2_launch(x, D, t1, t2, D, BT, D, mod + 8 * D, st));
+    TRY(down_resadd(mid, W2, mod + 8 * D));
     STAGE_DONE();
   } else {
     const float *gq = pv.vec, *gk = pv.vec + 128, *n1 = pv.vec + 256, *n2 = pv.vec + 256 + D;
@@ -493,8 +499,7 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     STAGE_DONE();
     TRY(gemm(h, D, BT, Wug, HXA_EPI_SITU, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
-    TRY(gemm(mid, F, BT, Wdn, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
-    TRY(hxa_resadd2_launch(x, D, t1, t2, D, BT, D, mod + 5 * D, st));
+    TRY(down_resadd(mid, Wdn, mod + 5 * D));
     STAGE_DONE();
   }
 #undef STAGE_DONE

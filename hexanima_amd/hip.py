@@ -18,7 +18,7 @@ SZ, U64 = C.c_size_t, C.c_uint64
 
 # constants of the C-ABI
 W_F16, W_Q8, W_Q4 = 0, 1, 2
-EPI_STORE, EPI_GELU_TANH, EPI_GELU_ERF, EPI_RESADD, EPI_STORE_T, EPI_SITU, EPI_PARTIAL = range(7)
+EPI_STORE, EPI_GELU_TANH, EPI_GELU_ERF, EPI_RESADD, EPI_STORE_T, EPI_SITU, EPI_PARTIAL, EPI_RESADD_SPLIT2 = range(8)
 KIND_WEIGHTS_ANIMA, KIND_BLOB, KIND_WEIGHTS_MOSS = 0, 1, 2
 E_NAMES = {0: "OK", -1: "RESOURCE", -2: "LOCK", -5: "WEIGHTS", -6: "NOBLOB", -7: "BLOB", -10: "META", -11: "MODE",
            -12: "ARG", -13: "HIP"}

@@ -99,12 +99,15 @@ int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, char *name, 
 #define HXA_EPI_STORE_T 4
 #define HXA_EPI_SITU 5
 #define HXA_EPI_PARTIAL 6
+#define HXA_EPI_RESADD_SPLIT2 7
 
 /* out = epi(A[M][K] . W[N][K]^T); replaces gemm_run_ex / gemm_run_geo (hexagon/mega/gemm2.c:96-141).
  * STORE: out[m][n] (ldo); with out_t != NULL the columns n >= split_col go to out_t[n - split_col][m] (ldo_t).
  * STORE_T: out[n][m]. GELU_*: out = f16(gelu(f16(acc))). RESADD: x[m][n] += gate[n] f16(acc) (x fp32, ldx).
  * SITU: W rows interleaved per 32 (up_j, gate_j), out[m][j*32+c] (moss gemm2.c mode 5).
- * PARTIAL: ksplit slices, out[z*out_zstride + m*ldo + n] = f16(partial z) (blk.c:172-174). */
+ * PARTIAL: ksplit slices, out[z*out_zstride + m*ldo + n] = f16(partial z) (blk.c:172-174).
+ * RESADD_SPLIT2 (ksplit 1, K % 128 == 0): x[m][n] += gate[n] (f16(first K/2) + f16(second K/2)), the split-K
+ * down projection and its residual (blk.c:172-174, kern.c:330-339) in one launch. */
 int hxa_gemm(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
              int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
              void *out_t, long ldo_t, int split_col, void *stream);

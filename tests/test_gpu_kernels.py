@@ -30,7 +30,8 @@ def _run_gemm(hip, A, fmt, w, s, N, K, epi=0, ksplit=1, tile=None, x=None, gate=
     dA = hip.DeviceArray.from_numpy(f16(A))
     dW = hip.DeviceArray.from_numpy(w)
     dS = hip.DeviceArray.from_numpy(s) if s is not None else None
-    if epi == hip.EPI_RESADD:
+    resadd = epi in (hip.EPI_RESADD, hip.EPI_RESADD_SPLIT2)
+    if resadd:
         dx = hip.DeviceArray.from_numpy(x.astype(np.float32))
         dg = hip.DeviceArray.from_numpy(gate.astype(np.float32))
         out = None
@@ -44,13 +45,13 @@ def _run_gemm(hip, A, fmt, w, s, N, K, epi=0, ksplit=1, tile=None, x=None, gate=
         out = hip.DeviceArray((M, N), np.float16)
     ldo = {hip.EPI_STORE_T: M, hip.EPI_SITU: N // 2}.get(epi, N)
     args = (dA.ptr, K, M, fmt, dW.ptr, dS.ptr if dS else None, None, N, K, ksplit, epi, out.ptr if out else None, ldo,
-            M * N, dx.ptr if epi == hip.EPI_RESADD else None, N, dg.ptr if epi == hip.EPI_RESADD else None)
+            M * N, dx.ptr if resadd else None, N, dg.ptr if resadd else None)
     if tile:
         hip.check(hip.lib().hxa_gemm_tile(*args, tile[0], tile[1], None), "gemm_tile")
     else:
         hip.check(hip.lib().hxa_gemm(*args, None, 0, 0, None), "gemm")
     hip.sync()
-    return dx.numpy() if epi == hip.EPI_RESADD else out.numpy()
+    return dx.numpy() if resadd else out.numpy()
 
 
 @pytest.mark.parametrize("tile", [None, (192, 256), (192, 192), (192, 128), (256, 128), (128, 256), (128, 128), (64, 128), (128, 64)])
@@ -127,6 +128,46 @@ def test_gemm_epilogues():
     tg = np.ascontiguousarray(t_gpu.reshape(M, F // 32, 2, 32)[:, :, 1].reshape(M, F))
     ref = hxo.situ(tu, tg).view(np.float16)
     assert ulp_diff(got, ref).max() <= 2
+
+
+@pytest.mark.parametrize("fmt,tile", [(0, None), (0, (64, 128)), (1, None), (2, None)])
+def test_gemm_resadd_split2_matches_partial_then_resadd2(fmt, tile):
+    """The fused split-K residual (blk.c:172-174) equals the two fp16 PARTIAL halves + resadd2, bit for bit, and the
+    oracle's resadd2 on those halves."""
+    hip = _hip()
+    rng = np.random.default_rng(11)
+    M, N, K = 320, 256, 1024
+    A = f16(rng.standard_normal((M, K)))
+    if fmt == 0:
+        w, s = f16(rng.standard_normal((N, K)) * 0.05), None
+    else:
+        wf = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+        w, s = hxo.q8_quantize(wf) if fmt == 1 else hxo.q4_quantize(wf)
+    x = rng.standard_normal((M, N)).astype(np.float32)
+    g = rng.standard_normal(N).astype(np.float32)
+    say(f"gemm resadd_split2 fmt={fmt} tile={tile}")
+    got = _run_gemm(hip, A, fmt, w, s, N, K, epi=hip.EPI_RESADD_SPLIT2, x=x, gate=g, tile=tile)
+    parts = _run_gemm(hip, A, fmt, w, s, N, K, epi=hip.EPI_PARTIAL, ksplit=2)
+    ref = hxo.resadd2(x, parts[0], parts[1], g)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)) or np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+    dx = hip.DeviceArray.from_numpy(x)
+    dt = [hip.DeviceArray.from_numpy(np.ascontiguousarray(parts[z])) for z in (0, 1)]
+    dg = hip.DeviceArray.from_numpy(g)
+    hip.check(hip.lib().hxa_resadd2(dx.ptr, N, dt[0].ptr, dt[1].ptr, N, M, N, dg.ptr, None), "resadd2")
+    hip.sync()
+    assert np.array_equal(got.view(np.uint32), dx.numpy().view(np.uint32))
+    # K must split into two halves of whole 64-k step pairs; ksplit must be 1
+    bad = _run_gemm_rc(hip, A[:, :96], N, 96, hip.EPI_RESADD_SPLIT2, x, g)
+    assert bad == -12
+
+
+def _run_gemm_rc(hip, A, N, K, epi, x, g):
+    dA = hip.DeviceArray.from_numpy(f16(A))
+    dW = hip.DeviceArray((N, K), np.float16)
+    dx = hip.DeviceArray.from_numpy(x)
+    dg = hip.DeviceArray.from_numpy(g)
+    return hip.lib().hxa_gemm(dA.ptr, K, A.shape[0], 0, dW.ptr, None, None, N, K, 1, epi, None, N, 0, dx.ptr, N, dg.ptr,
+                              None, 0, 0, None)
 
 
 def test_gemm_fused_qkv_split_transposed():
