@@ -107,35 +107,39 @@ struct GemmGeo {
   static constexpr int TW = (W_BYTES / 16 + 63) / 64;                // W load instructions per stage (all waves)
 };
 
-// Per-wave number of direct-to-LDS instructions issued for one stage.
-template <int BM, int BN, int FMT, bool ASYM>
+// Per-wave number of direct-to-LDS instructions issued for one stage (A and W instructions dealt round-robin over
+// the NW waves, the scale / offset vectors by wave 0).
+template <int BM, int BN, int FMT, bool ASYM, int NW>
 HXA_DEV constexpr int loads_per_stage(int wave) {
   using G = GemmGeo<BM, BN, FMT>;
-  return G::NA + (G::TW / 4 + (wave < G::TW % 4 ? 1 : 0)) + (FMT != HXA_W_F16 && wave == 0 ? (ASYM ? 2 : 1) : 0);
+  constexpr int NA = BM / 16;
+  return NA / NW + (wave < NA % NW ? 1 : 0) + G::TW / NW + (wave < G::TW % NW ? 1 : 0) +
+         (FMT != HXA_W_F16 && wave == 0 ? (ASYM ? 2 : 1) : 0);
 }
 // wait until at most LATER further stages of loads are outstanding for this wave
-template <int BM, int BN, int FMT, bool ASYM, int WAVE, int LATER>
-HXA_DEV void wait_stage_w() {
-  constexpr int n = loads_per_stage<BM, BN, FMT, ASYM>(WAVE);
-  wait_vm<LATER * n>();
-}
-template <int BM, int BN, int FMT, bool ASYM, int LATER>
+template <int BM, int BN, int FMT, bool ASYM, int NW, int LATER, int W = 0>
 HXA_DEV void wait_stage(int wave) {
-  if (wave == 0) wait_stage_w<BM, BN, FMT, ASYM, 0, LATER>();
-  else if (wave == 1) wait_stage_w<BM, BN, FMT, ASYM, 1, LATER>();
-  else if (wave == 2) wait_stage_w<BM, BN, FMT, ASYM, 2, LATER>();
-  else wait_stage_w<BM, BN, FMT, ASYM, 3, LATER>();
+  if constexpr (W + 1 < NW) {
+    if (wave != W) {
+      wait_stage<BM, BN, FMT, ASYM, NW, LATER, W + 1>(wave);
+      return;
+    }
+  }
+  wait_vm<LATER * loads_per_stage<BM, BN, FMT, ASYM, NW>(W)>();
 }
 
 // SPLIT2: the first and second halves of K are rounded to fp16 separately and combined in the residual epilogue,
 // x += gate * (f16(first half) + f16(second half)) (blk.c:172-174 + kern.c:330-339 in one kernel): the first half's
 // f16 accumulators are kept in registers while the second half accumulates.
-template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
+// NW = 4 waves (2 x 2 grid, one wave per SIMD) or 8 waves (2 x 4 grid, two waves per SIMD: one wave's waits are
+// covered by the other's MFMAs).
+template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
   using G = GemmGeo<BM, BN, FMT>;
-  constexpr int WTM = BM / 2, WTN = BN / 2, MI = WTM / 32, NI = WTN / 32;
+  constexpr int NT = 64 * NW;
+  constexpr int WTM = BM / 2, WTN = BN / (NW / 2), MI = WTM / 32, NI = WTN / 32;
   constexpr int BK = G::BK, NS = G::NS, PD = G::PD;
-  static_assert(BM % 64 == 0 && BN % 64 == 0, "tile shape");
+  static_assert(BM % 64 == 0 && WTN % 32 == 0 && (NW == 4 || NW == 8), "tile shape");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
 
   const int ntiles = p.tiles_m * p.tiles_n;
@@ -153,18 +157,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   auto issue = [&](int s, int kt) {
     uint8_t *st = lds8 + s * G::STAGE;
     const int k0 = kbase + min(kt, p.Kslice / BK - 1) * BK;  // tiles past the end reload the last one (never read)
+    constexpr int NAI = BM / 16;  // 1 KB A instructions (16 rows) per stage
 #pragma unroll
-    for (int i = 0; i < G::NA; i++) {
-      const int r0 = (wave * G::NA + i) * 16, row = r0 + (lane >> 2);
-      const int cl = (lane & 3) ^ ((row >> 2) & 3);
-      const int m = min(m0 + row, p.M - 1);
-      g2l16_opaque(p.A + (long)m * p.lda + k0 + cl * 8, st + r0 * 64);
+    for (int a0 = 0; a0 < NAI; a0 += NW) {
+      const int a = a0 + wave;
+      if (NAI % NW == 0 || a < NAI) {
+        const int r0 = a * 16, row = r0 + (lane >> 2);
+        const int cl = (lane & 3) ^ ((row >> 2) & 3);
+        const int m = min(m0 + row, p.M - 1);
+        g2l16_opaque(p.A + (long)m * p.lda + k0 + cl * 8, st + r0 * 64);
+      }
     }
     uint8_t *ws = st + G::A_BYTES;
 #pragma unroll
-    for (int t0 = 0; t0 < G::TW; t0 += 4) {
+    for (int t0 = 0; t0 < G::TW; t0 += NW) {
       const int t = t0 + wave;
-      if (G::TW % 4 == 0 || t < G::TW) {
+      if (G::TW % NW == 0 || t < G::TW) {
         const int chunk = t * 64 + lane;
         if ((G::W_BYTES / 16) % 64 == 0 || chunk < G::W_BYTES / 16) {
           if (FMT == HXA_W_F16) {
@@ -271,7 +279,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     dequant(0, cb, cq, cs, cz);
     mfma_range(ca[0], cb[0], 0, 2);
     __builtin_amdgcn_sched_barrier(0);
-    wait_stage<BM, BN, FMT, ASYM, NS - 2>(wave);  // tile kt+1 complete; tiles kt+2 .. kt+NS-1 may still fly
+    wait_stage<BM, BN, FMT, ASYM, NW, NS - 2>(wave);  // tile kt+1 complete; tiles kt+2 .. kt+NS-1 may still fly
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();             // stage kt+1 visible; every wave holds its stage kt fragments
     asm volatile("" ::: "memory");
@@ -281,7 +289,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     dequant(1, cb, cq, cs, cz);
     read_frags((kt + 1) % NS, na, nb, nq, ns, nz);
     mfma_range(ca[1], cb[1], 0, NMF);
-    constexpr int NV = G::NA + (G::TW + 3) / 4 + 2;  // upper bound of the VMEM loads of this wave
+    constexpr int NV = (BM / 16 + NW - 1) / NW + (G::TW + NW - 1) / NW + 2;  // upper bound of this wave's VMEM loads
 #pragma unroll
     for (int q = 0; q < NV; q++) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
@@ -300,7 +308,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   half8_t fa0[2][MI], fb0[2][NI], fa1[2][MI], fb1[2][NI];
 #pragma unroll
   for (int s = 0; s < NS; s++) issue(s, s);
-  wait_stage<BM, BN, FMT, ASYM, NS - 2>(wave);  // tiles 0 and 1 complete
+  wait_stage<BM, BN, FMT, ASYM, NW, NS - 2>(wave);  // tiles 0 and 1 complete
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
@@ -350,7 +358,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   constexpr int C8 = BN / 8;
   if (p.epi == HXA_EPI_SITU) {
     // columns interleaved per 32 (up_j, gate_j): output column (n0/2) + p*32 + c
-    for (int c = tid; c < BM * (C8 / 2); c += 256) {
+    for (int c = tid; c < BM * (C8 / 2); c += NT) {
       const int ml = c / (C8 / 2), oc = (c % (C8 / 2)) * 8;
       const int m = m0 + ml, on = n0 / 2 + oc;
       if (m >= p.M || on * 2 >= p.N) continue;
@@ -370,8 +378,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   if (p.epi == HXA_EPI_RESADD) {
     // x += gate * t: the x / gate loads of RB chunks are issued together before any of them is used, so a thread
     // waits one memory latency per batch instead of one per chunk (x stores may alias later x loads otherwise)
-    constexpr int NC8 = BN / 8, ITERS = BM * NC8 / 256, RB = ITERS < 4 ? ITERS : 4;
-    static_assert(BM * NC8 % 256 == 0, "whole chunk passes");
+    constexpr int NC8 = BN / 8, ITERS = BM * NC8 / NT, RB = ITERS % 4 == 0 ? 4 : ITERS % 3 == 0 ? 3 : ITERS % 2 == 0 ? 2 : 1;
+    static_assert(BM * NC8 % NT == 0 && ITERS % RB == 0, "whole chunk passes");
 #pragma unroll
     for (int b0 = 0; b0 < ITERS; b0 += RB) {
       float4_t xv[RB][2], gv[RB][2];
@@ -379,7 +387,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
       bool ok[RB];
 #pragma unroll
       for (int u = 0; u < RB; u++) {
-        const int c = tid + (b0 + u) * 256, ml = c / NC8, nl = (c % NC8) * 8, m = m0 + ml, n = n0 + nl;
+        const int c = tid + (b0 + u) * NT, ml = c / NC8, nl = (c % NC8) * 8, m = m0 + ml, n = n0 + nl;
         ok[u] = m < p.M && n < p.N;
         if (ok[u]) {
           const float4_t *xp = (const float4_t *)(p.x + (long)m * p.ldx + n);
@@ -400,7 +408,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int u = 0; u < RB; u++) {
         if (!ok[u]) continue;
-        const int c = tid + (b0 + u) * 256, ml = c / NC8, nl = (c % NC8) * 8;
+        const int c = tid + (b0 + u) * NT, ml = c / NC8, nl = (c % NC8) * 8;
         float4_t *xp = (float4_t *)(p.x + (long)(m0 + ml) * p.ldx + n0 + nl);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -415,7 +423,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   }
   auto rows_pass = [&](auto ncols_c) {
   const int nc8 = ncols_c / 8;
-  for (int c = tid; c < BM * nc8; c += 256) {
+  for (int c = tid; c < BM * nc8; c += NT) {
     const int ml = c / nc8, nl = (c % nc8) * 8;
     const int m = m0 + ml, n = n0 + nl;
     if (m >= p.M || n >= p.N) continue;
@@ -441,7 +449,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     rows_pass(nsplit);
   if (nsplit < BN) {  // transposed columns: chunk = (column, 8 consecutive rows)
     const int ncol = BN - nsplit;
-    for (int c = tid; c < ncol * (BM / 8); c += 256) {
+    for (int c = tid; c < ncol * (BM / 8); c += NT) {
       const int nl = nsplit + c / (BM / 8), ml = (c % (BM / 8)) * 8;
       const int n = n0 + nl, m = m0 + ml;
       if (n >= p.N || m >= p.M) continue;
@@ -459,13 +467,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 }
 
 struct TileCfg {
-  int bm, bn;
+  int bm, bn, nw;
 };
-constexpr TileCfg kCfgs[] = {{192, 256}, {192, 192}, {192, 128}, {256, 128}, {128, 256}, {128, 128}, {64, 128}, {128, 64}};
+constexpr TileCfg kCfgs[] = {{192, 256, 4}, {192, 192, 4}, {192, 128, 4}, {256, 128, 4}, {128, 256, 4},
+                             {128, 128, 4}, {64, 128, 4},  {128, 64, 4},  {192, 256, 8}};
 
-template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false>
+template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false, int NW = 4>
 hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
-  auto kern = gemm_kernel<BM, BN, FMT, ASYM, SPLIT2>;
+  auto kern = gemm_kernel<BM, BN, FMT, ASYM, SPLIT2, NW>;
   using G = GemmGeo<BM, BN, FMT>;
   const int lds = SPLIT2 && 2 * G::C_BYTES > G::LDS ? 2 * G::C_BYTES : G::LDS;
   static bool attr = false;
@@ -475,7 +484,7 @@ hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
     attr = true;
   }
   dim3 grid(p.tiles_m * p.tiles_n, 1, ksplit);
-  hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, p);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, st, p);
   return hipGetLastError();
 }
 
@@ -487,7 +496,11 @@ hipError_t launch_split2(int bm, int bn, const GemmParams &p, hipStream_t st) {
 }
 
 template <int FMT, bool ASYM>
-hipError_t launch_fmt(int bm, int bn, const GemmParams &p, int ksplit, hipStream_t st) {
+hipError_t launch_fmt(int bm, int bn, int nw, const GemmParams &p, int ksplit, hipStream_t st) {
+  if (nw == 8) {
+    if (bm == 192 && bn == 256) return launch_t<192, 256, FMT, ASYM, false, 8>(p, ksplit, st);
+    return hipErrorInvalidValue;
+  }
   if (bm == 192 && bn == 256) return launch_t<192, 256, FMT, ASYM>(p, ksplit, st);
   if (bm == 192 && bn == 192) return launch_t<192, 192, FMT, ASYM>(p, ksplit, st);
   if (bm == 192 && bn == 128) return launch_t<192, 128, FMT, ASYM>(p, ksplit, st);
@@ -506,7 +519,7 @@ int g_num_cu = 0;
 }  // namespace
 
 // Choose a tile shape: best wave-quantisation efficiency over the GPU's CUs, ties to the larger tile.
-static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int *bm, int *bn) {
+static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int *bm, int *bn, int *nw) {
   if (g_num_cu == 0) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
@@ -526,6 +539,7 @@ static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int *bm, int *
       best = eff;
       *bm = c.bm;
       *bn = c.bn;
+      *nw = c.nw;
     }
   }
 }
@@ -573,11 +587,13 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   p.x = g.x;
   p.ldx = g.ldx;
   p.gate = g.gate;
-  int bm = 128, bn = 128;
-  pick_tile(g.M, w.N, g.ksplit, w.fmt, g.epi, &bm, &bn);
+  int bm = 128, bn = 128, nw = 4;
+  pick_tile(g.M, w.N, g.ksplit, w.fmt, g.epi, &bm, &bn, &nw);
   if (g.force_bm) {
     bm = g.force_bm;
     bn = g.force_bn;
+    nw = g.force_nw ? g.force_nw : 4;
+    if (nw != 4 && (nw != 8 || split2)) return HXA_E_ARG;
     if ((g.epi == HXA_EPI_SITU && bn % 128 != 0) || (w.fmt == HXA_W_Q4 && bn < 128)) return HXA_E_ARG;
     if (split2 && !(bn == 128 && (bm == 128 || bm == 64))) return HXA_E_ARG;
   }
@@ -591,9 +607,9 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
     else e = launch_split2<HXA_W_Q4, false>(bm, bn, p, st);
     return e == hipSuccess ? HXA_OK : HXA_E_HIP;
   }
-  if (w.fmt == HXA_W_F16) e = launch_fmt<HXA_W_F16, false>(bm, bn, p, g.ksplit, st);
-  else if (w.fmt == HXA_W_Q8) e = launch_fmt<HXA_W_Q8, false>(bm, bn, p, g.ksplit, st);
-  else if (w.z) e = launch_fmt<HXA_W_Q4, true>(bm, bn, p, g.ksplit, st);
-  else e = launch_fmt<HXA_W_Q4, false>(bm, bn, p, g.ksplit, st);
+  if (w.fmt == HXA_W_F16) e = launch_fmt<HXA_W_F16, false>(bm, bn, nw, p, g.ksplit, st);
+  else if (w.fmt == HXA_W_Q8) e = launch_fmt<HXA_W_Q8, false>(bm, bn, nw, p, g.ksplit, st);
+  else if (w.z) e = launch_fmt<HXA_W_Q4, true>(bm, bn, nw, p, g.ksplit, st);
+  else e = launch_fmt<HXA_W_Q4, false>(bm, bn, nw, p, g.ksplit, st);
   return e == hipSuccess ? HXA_OK : HXA_E_HIP;
 }

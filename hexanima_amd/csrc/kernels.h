@@ -18,6 +18,7 @@ struct HxaGemm {
   long ldo_t;
   int split_col;
   int force_bm, force_bn;  // 0 = automatic tile choice
+  int force_nw;            // waves per workgroup with a forced tile: 0 / 4, or 8 (192 x 256 only)
 };
 int hxa_gemm_launch(const HxaGemm &g, hipStream_t st);
 

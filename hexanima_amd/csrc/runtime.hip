@@ -141,7 +141,7 @@ extern "C" int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, c
 // ---------------------------------------------------------------------------------------------------------------
 static int gemm_common(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
                        int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx,
-                       const float *gate, void *out_t, long ldo_t, int split_col, int bm, int bn, void *stream) {
+                       const float *gate, void *out_t, long ldo_t, int split_col, int bm, int bn, int nw, void *stream) {
   if (!A || !w) return fail(HXA_E_ARG, "gemm: null operand");
   if (fmt < HXA_W_F16 || fmt > HXA_W_Q4) return fail(HXA_E_MODE, "gemm: format %d", fmt);
   if (epi == HXA_EPI_RESADD || epi == HXA_EPI_RESADD_SPLIT2 ? (!x || !gate) : !out) return fail(HXA_E_ARG, "gemm: null output");
@@ -164,6 +164,7 @@ static int gemm_common(const void *A, long lda, int M, int fmt, const void *w, c
   g.split_col = split_col;
   g.force_bm = bm;
   g.force_bn = bn;
+  g.force_nw = nw;
   const int r = hxa_gemm_launch(g, S(stream));
   if (r != HXA_OK) return fail(r, "gemm M=%d N=%d K=%d fmt=%d epi=%d ksplit=%d rejected (%d)", M, N, K, fmt, epi, ksplit, r);
   return HXA_OK;
@@ -172,13 +173,13 @@ extern "C" int hxa_gemm(const void *A, long lda, int M, int fmt, const void *w, 
                         int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
                         void *out_t, long ldo_t, int split_col, void *stream) {
   return gemm_common(A, lda, M, fmt, w, s, z, N, K, ksplit, epi, out, ldo, out_zstride, x, ldx, gate, out_t, ldo_t,
-                     split_col, 0, 0, stream);
+                     split_col, 0, 0, 0, stream);
 }
 extern "C" int hxa_gemm_tile(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N,
                              int K, int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx,
-                             const float *gate, int bm, int bn, void *stream) {
+                             const float *gate, int bm, int bn, int waves, void *stream) {
   return gemm_common(A, lda, M, fmt, w, s, z, N, K, ksplit, epi, out, ldo, out_zstride, x, ldx, gate, nullptr, 0, 0, bm,
-                     bn, stream);
+                     bn, waves, stream);
 }
 extern "C" int hxa_attention(const void *q, long ldq, const void *k, long ldk, const void *vt, long ldvt, void *o, long ldo,
                              int T, int NKV, int nvalid, int H, int batch, long qb, long kb, long vb, long ob,

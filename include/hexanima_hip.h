@@ -111,10 +111,11 @@ int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, char *name, 
 int hxa_gemm(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
              int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
              void *out_t, long ldo_t, int split_col, void *stream);
-/* same, with an explicit tile shape (tests / tuning); bm x bn in {256x128, 128x256, 128x128, 64x128, 128x64} */
+/* same, with an explicit tile shape (tests / tuning): bm x bn in {192x256, 192x192, 192x128, 256x128, 128x256,
+ * 128x128, 64x128, 128x64}; waves per workgroup 4 (0 = 4) or 8 (192x256 only) */
 int hxa_gemm_tile(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
                   int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
-                  int bm, int bn, void *stream);
+                  int bm, int bn, int waves, void *stream);
 /* attention over heads of 128 (blk.c:54-91): q [T][ldq], k [NKV][ldk], vt [H*128][ldvt] (V transposed),
  * o [T][ldo]; keys >= nvalid masked; batch images at element strides qb/kb/vb/ob. */
 int hxa_attention(const void *q, long ldq, const void *k, long ldk, const void *vt, long ldvt, void *o, long ldo, int T,

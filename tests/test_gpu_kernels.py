@@ -47,14 +47,15 @@ def _run_gemm(hip, A, fmt, w, s, N, K, epi=0, ksplit=1, tile=None, x=None, gate=
     args = (dA.ptr, K, M, fmt, dW.ptr, dS.ptr if dS else None, None, N, K, ksplit, epi, out.ptr if out else None, ldo,
             M * N, dx.ptr if resadd else None, N, dg.ptr if resadd else None)
     if tile:
-        hip.check(hip.lib().hxa_gemm_tile(*args, tile[0], tile[1], None), "gemm_tile")
+        hip.check(hip.lib().hxa_gemm_tile(*args, tile[0], tile[1], tile[2] if len(tile) > 2 else 0, None), "gemm_tile")
     else:
         hip.check(hip.lib().hxa_gemm(*args, None, 0, 0, None), "gemm")
     hip.sync()
     return dx.numpy() if resadd else out.numpy()
 
 
-@pytest.mark.parametrize("tile", [None, (192, 256), (192, 192), (192, 128), (256, 128), (128, 256), (128, 128), (64, 128), (128, 64)])
+@pytest.mark.parametrize("tile", [None, (192, 256), (192, 256, 8), (192, 192), (192, 128), (256, 128), (128, 256), (128, 128),
+                                  (64, 128), (128, 64)])
 def test_gemm_f16_tiles(tile):
     hip = _hip()
     say(f"gemm f16 tile={tile}")
