@@ -42,7 +42,49 @@ struct GemmParams {
   long ldo_t;
   int split_col;
   int tiles_m, tiles_n;
+  // head norm (STORE epilogue): columns [0, hn_cols), in whole heads of 128, get RMSNorm * gain and optional RoPE
+  int hn_cols, hn_gsplit, hn_ttab;
+  const float *hn_g0, *hn_g1, *hn_cos, *hn_sin;
 };
+
+// Per-head RMSNorm * gain + split-half RoPE of one 8-column chunk (kern.c:163-197), the same arithmetic as the
+// standalone RMS+RoPE kernel: the 16 lanes holding one head's 128 values (aligned 16-lane group, chunk j = lane & 15
+// owning dims [8j, 8j+8)) reduce with shfl_xor(1..8); the RoPE partner of dim d < 64 (d + 64) is in lane j ^ 8.
+HXA_DEV half8_t head_norm(half8_t v, int j, int m, int n, const GemmParams &p) {
+  float a[8], ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    a[e] = (float)v[e];
+    ss += a[e] * a[e];
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);
+  const float r = rsqrtf(ss * (1.0f / 128.0f) + 1e-6f);
+  const float *g = (n < p.hn_gsplit ? p.hn_g0 : p.hn_g1) + 8 * j;
+  const float4_t ga = *(const float4_t *)g, gb = *(const float4_t *)(g + 4);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    a[e] = a[e] * r * ga[e];
+    a[e + 4] = a[e + 4] * r * gb[e];
+  }
+  if (p.hn_cos != nullptr) {
+    const int tt = m % p.hn_ttab, d0 = 8 * (j & 7);
+    const float *cr = p.hn_cos + (long)tt * 64 + d0, *sr = p.hn_sin + (long)tt * 64 + d0;
+    const float4_t c0 = *(const float4_t *)cr, c1 = *(const float4_t *)(cr + 4);
+    const float4_t s0 = *(const float4_t *)sr, s1 = *(const float4_t *)(sr + 4);
+    const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+    const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float partner = __shfl_xor(a[e], 8);
+      a[e] = j < 8 ? a[e] * cs[e] - partner * sn[e] : partner * sn[e] + a[e] * cs[e];
+    }
+  }
+  half8_t o;
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = (hxa_h)a[e];
+  return o;
+}
 
 HXA_DEV half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 HXA_DEV uint32_t as_u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
@@ -432,7 +474,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
     if (p.epi == HXA_EPI_PARTIAL) {
       *(half8_t *)(p.out + (long)z * p.out_zstride + o) = v;
     } else {
-      if (p.epi == HXA_EPI_GELU_TANH) {
+      if (n < p.hn_cols) {  // whole 16-lane head groups take this branch together (n0, ncols multiples of 128)
+        v = head_norm(v, (nl >> 3) & 15, m, n, p);
+      } else if (p.epi == HXA_EPI_GELU_TANH) {
 #pragma unroll
         for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_tanh_f((float)v[e]);
       } else if (p.epi == HXA_EPI_GELU_ERF) {
@@ -519,7 +563,7 @@ int g_num_cu = 0;
 }  // namespace
 
 // Choose a tile shape: best wave-quantisation efficiency over the GPU's CUs, ties to the larger tile.
-static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int *bm, int *bn, int *nw) {
+static void pick_tile(int M, int N, int ksplit, int fmt, int epi, bool headnorm, int *bm, int *bn, int *nw) {
   if (g_num_cu == 0) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
@@ -531,6 +575,7 @@ static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int *bm, int *
     if (fmt == HXA_W_Q4 && c.bn < 128) continue;
     if (epi == HXA_EPI_SITU && c.bn % 128 != 0) continue;  // each wave needs whole (up, gate) block pairs
     if (epi == HXA_EPI_RESADD_SPLIT2 && !(c.bn == 128 && (c.bm == 128 || c.bm == 64))) continue;  // register budget
+    if (headnorm && (c.bn % 128 != 0 || c.nw != 4)) continue;  // whole heads per tile
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ksplit;
     const long waves = (tiles + g_num_cu - 1) / g_num_cu;
     const double useful = (double)M * N / ((double)((M + c.bm - 1) / c.bm) * c.bm * ((N + c.bn - 1) / c.bn) * c.bn);
@@ -587,8 +632,22 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   p.x = g.x;
   p.ldx = g.ldx;
   p.gate = g.gate;
+  const bool headnorm = g.hn_cols > 0;
+  if (headnorm) {
+    if (g.epi != HXA_EPI_STORE || g.ksplit != 1 || g.hn_cols % 128 || w.N % 128 || !g.hn_g0 || !g.hn_g1 ||
+        (g.hn_cos && (!g.hn_sin || g.hn_ttab <= 0)) || ((uintptr_t)g.hn_g0 | (uintptr_t)g.hn_g1) % 16 ||
+        (g.out_t && (g.split_col % 128 || g.split_col < g.hn_cols)))
+      return HXA_E_ARG;
+  }
+  p.hn_cols = headnorm ? min(g.hn_cols, w.N) : 0;
+  p.hn_gsplit = g.hn_gsplit;
+  p.hn_ttab = g.hn_ttab;
+  p.hn_g0 = g.hn_g0;
+  p.hn_g1 = g.hn_g1;
+  p.hn_cos = g.hn_cos;
+  p.hn_sin = g.hn_sin;
   int bm = 128, bn = 128, nw = 4;
-  pick_tile(g.M, w.N, g.ksplit, w.fmt, g.epi, &bm, &bn, &nw);
+  pick_tile(g.M, w.N, g.ksplit, w.fmt, g.epi, headnorm, &bm, &bn, &nw);
   if (g.force_bm) {
     bm = g.force_bm;
     bn = g.force_bn;
@@ -596,6 +655,7 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
     if (nw != 4 && (nw != 8 || split2)) return HXA_E_ARG;
     if ((g.epi == HXA_EPI_SITU && bn % 128 != 0) || (w.fmt == HXA_W_Q4 && bn < 128)) return HXA_E_ARG;
     if (split2 && !(bn == 128 && (bm == 128 || bm == 64))) return HXA_E_ARG;
+    if (headnorm && (bn % 128 != 0 || nw != 4)) return HXA_E_ARG;
   }
   p.tiles_m = (g.M + bm - 1) / bm;
   p.tiles_n = (w.N + bn - 1) / bn;

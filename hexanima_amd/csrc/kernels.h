@@ -19,6 +19,10 @@ struct HxaGemm {
   int split_col;
   int force_bm, force_bn;  // 0 = automatic tile choice
   int force_nw;            // waves per workgroup with a forced tile: 0 / 4, or 8 (192 x 256 only)
+  // STORE with head norm: columns [0, hn_cols) (multiple of 128) get per-head RMSNorm * gain (gain hn_g0 for columns
+  // < hn_gsplit, hn_g1 above) and, with hn_cos / hn_sin [hn_ttab][64], RoPE at token m % hn_ttab (kern.c:163-197)
+  int hn_cols, hn_gsplit, hn_ttab;
+  const float *hn_g0, *hn_g1, *hn_cos, *hn_sin;
 };
 int hxa_gemm_launch(const HxaGemm &g, hipStream_t st);
 

@@ -181,6 +181,36 @@ extern "C" int hxa_gemm_tile(const void *A, long lda, int M, int fmt, const void
   return gemm_common(A, lda, M, fmt, w, s, z, N, K, ksplit, epi, out, ldo, out_zstride, x, ldx, gate, nullptr, 0, 0, bm,
                      bn, waves, stream);
 }
+extern "C" int hxa_gemm_headnorm(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N,
+                                 int K, void *out, long ldo, void *out_t, long ldo_t, int split_col, int norm_cols,
+                                 const float *gain0, const float *gain1, int gain_split, const float *cosT,
+                                 const float *sinT, int ttab, void *stream) {
+  if (!A || !w || !out) return fail(HXA_E_ARG, "gemm_headnorm: null pointer");
+  if (fmt < HXA_W_F16 || fmt > HXA_W_Q4) return fail(HXA_E_MODE, "gemm_headnorm: format %d", fmt);
+  HxaWeight wt{fmt, N, K, w, (const hxa_h *)s, (const hxa_h *)z};
+  HxaGemm g{};
+  g.A = (const hxa_h *)A;
+  g.lda = lda;
+  g.M = M;
+  g.w = &wt;
+  g.ksplit = 1;
+  g.epi = HXA_EPI_STORE;
+  g.out = (hxa_h *)out;
+  g.ldo = ldo;
+  g.out_t = (hxa_h *)out_t;
+  g.ldo_t = ldo_t;
+  g.split_col = split_col;
+  g.hn_cols = norm_cols;
+  g.hn_g0 = gain0;
+  g.hn_g1 = gain1;
+  g.hn_gsplit = gain_split;
+  g.hn_cos = cosT;
+  g.hn_sin = sinT;
+  g.hn_ttab = ttab;
+  const int r = hxa_gemm_launch(g, S(stream));
+  if (r != HXA_OK) return fail(r, "gemm_headnorm M=%d N=%d K=%d norm_cols=%d rejected (%d)", M, N, K, norm_cols, r);
+  return HXA_OK;
+}
 extern "C" int hxa_attention(const void *q, long ldq, const void *k, long ldk, const void *vt, long ldvt, void *o, long ldo,
                              int T, int NKV, int nvalid, int H, int batch, long qb, long kb, long vb, long ob,
                              void *stream) {
@@ -407,9 +437,26 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     if (stop && ++stage >= stop) return HXA_OK;   \
     if (!stop) ++stage;                           \
   } while (0)
+  // head norm of the projection epilogue (kern.c:163-197 fused into gemm2.c's flush): hn = {cols, g0, g1, gsplit,
+  // cos, sin}; cols == 0 for a plain projection
+  struct HeadNorm {
+    int cols;
+    const float *g0, *g1;
+    int gsplit;
+    const float *cs, *sn;
+  };
+  HeadNorm hn{};
   auto gemm = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
                   const float *gate, hxa_h *out_t, long ldo_t, int split, int ksplit, long zstride) -> int {
     HxaGemm g{};
+    g.hn_cols = hn.cols;
+    g.hn_g0 = hn.g0;
+    g.hn_g1 = hn.g1;
+    g.hn_gsplit = hn.gsplit;
+    g.hn_cos = hn.cs;
+    g.hn_sin = hn.sn;
+    g.hn_ttab = T;
+    hn = HeadNorm{};  // applies to one projection
     g.A = A;
     g.lda = lda;
     g.M = M;
@@ -453,9 +500,13 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     // site 0: self-attention (blk.c:157-162)
     TRY(hxa_norm_mod_launch(x, D, BT, D, mod, mod + D, nullptr, 1e-6f, h, D, st));
     STAGE_DONE();
+    // q, k: RMSNorm * gain + RoPE (blk.c:159-160), fused into the projection's store unless a stage dump needs the
+    // un-normalised projections (M_STOP)
+    const bool fuse = stop == 0;
+    if (fuse) hn = HeadNorm{2 * D, gain, gain + 128, D, cosT, sinT};
     TRY(gemm(h, D, BT, Wqkv, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
     STAGE_DONE();
-    TRY(hxa_rmsrope_launch(qk, k, gain, gain + 128, ldqk, BT, H, cosT, sinT, T, st));
+    if (!fuse) TRY(hxa_rmsrope_launch(qk, k, gain, gain + 128, ldqk, BT, H, cosT, sinT, T, st));
     STAGE_DONE();
     TRY(attn(qk, k, ldqk, vT, BT, T, T, (long)T * ldqk, T));
     STAGE_DONE();
@@ -464,11 +515,15 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     // site 1: cross-attention (blk.c:163-169)
     TRY(hxa_norm_mod_launch(x, D, BT, D, mod + 3 * D, mod + 4 * D, nullptr, 1e-6f, h, D, st));
     STAGE_DONE();
+    if (fuse) hn = HeadNorm{D, gain + 256, gain + 256, D, nullptr, nullptr};  // cross q: RMSNorm * gain (blk.c:166)
     TRY(gemm(h, D, BT, Wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    if (fuse) hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
     TRY(gemm((const hxa_h *)ctx, d->DC, BC, Wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0));
     STAGE_DONE();
-    TRY(hxa_rmsrope_launch(qk, nullptr, gain + 256, nullptr, ldqk, BT, H, nullptr, nullptr, 0, st));
-    TRY(hxa_rmsrope_launch(ck, nullptr, gain + 384, nullptr, D, BC, H, nullptr, nullptr, 0, st));
+    if (!fuse) {
+      TRY(hxa_rmsrope_launch(qk, nullptr, gain + 256, nullptr, ldqk, BT, H, nullptr, nullptr, 0, st));
+      TRY(hxa_rmsrope_launch(ck, nullptr, gain + 384, nullptr, D, BC, H, nullptr, nullptr, 0, st));
+    }
     STAGE_DONE();
     TRY(attn(qk, ck, D, cvT, BC, d->C, d->C, (long)d->C * D, d->C));
     STAGE_DONE();
@@ -488,8 +543,8 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     TRY(hxa_norm_mod_launch(x, D, BT, D, mod, mod + D, n1, 1e-6f, h, D, st));
     STAGE_DONE();
     STAGE_DONE();  // the reference's LoRA-A GEMM stage (no LoRA)
+    hn = HeadNorm{2 * D, gq, gk, D, cosT, sinT};  // q, k: RMSNorm * gain + RoPE in the GEMM (moss blk.c:239-242, mode 3)
     TRY(gemm(h, D, BT, Wqkv, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
-    TRY(hxa_rmsrope_launch(qk, k, gq, gk, ldqk, BT, H, cosT, sinT, T, st));
     STAGE_DONE();
     TRY(attn(qk, k, ldqk, vT, BT, T, d->nvalid, (long)T * ldqk, T));
     STAGE_DONE();

@@ -66,6 +66,7 @@ _SIGS = {
     "hxa_event_elapsed_ms": (I, [P, P, C.POINTER(F)]),
     "hxa_device_info": (I, [C.POINTER(I), C.POINTER(I), C.POINTER(SZ), C.c_char_p, I]),
     "hxa_gemm": (I, [P, L, I, I, P, P, P, I, I, I, I, P, L, L, P, L, P, P, L, I, P]),
+    "hxa_gemm_headnorm": (I, [P, L, I, I, P, P, P, I, I, P, L, P, L, I, I, P, P, I, P, P, I, P]),
     "hxa_gemm_tile": (I, [P, L, I, I, P, P, P, I, I, I, I, P, L, L, P, L, P, I, I, I, P]),
     "hxa_attention": (I, [P, L, P, L, P, L, P, L, I, I, I, I, I, L, L, L, L, P]),
     "hxa_norm_mod": (I, [P, L, I, I, P, P, P, F, P, L, P]),

@@ -116,6 +116,14 @@ int hxa_gemm(const void *A, long lda, int M, int fmt, const void *w, const void 
 int hxa_gemm_tile(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
                   int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
                   int bm, int bn, int waves, void *stream);
+/* out = f16(A[M][K] . W[N][K]^T) with the per-head norm fused into the store (blk.c:158-160, :164-167,
+ * kern.c:163-197): columns [0, norm_cols) (whole heads of 128) become f16(RMSNorm(f16 value) * gain), gain0 for
+ * columns < gain_split, gain1 above; with cosT / sinT [ttab][64] also RoPE on pairs (d, d+64) at token m % ttab.
+ * Columns >= split_col go transposed to out_t[n - split_col][m] (out_t NULL: none). N, norm_cols, split_col: multiples
+ * of 128. Same values as hxa_gemm + hxa_rmsrope. */
+int hxa_gemm_headnorm(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
+                      void *out, long ldo, void *out_t, long ldo_t, int split_col, int norm_cols, const float *gain0,
+                      const float *gain1, int gain_split, const float *cosT, const float *sinT, int ttab, void *stream);
 /* attention over heads of 128 (blk.c:54-91): q [T][ldq], k [NKV][ldk], vt [H*128][ldvt] (V transposed),
  * o [T][ldo]; keys >= nvalid masked; batch images at element strides qb/kb/vb/ob. */
 int hxa_attention(const void *q, long ldq, const void *k, long ldk, const void *vt, long ldvt, void *o, long ldo, int T,

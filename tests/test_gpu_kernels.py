@@ -190,6 +190,53 @@ def test_gemm_fused_qkv_split_transposed():
     assert_gemm_close(np.ascontiguousarray(vt.numpy().T), ref[:, 2 * D:], A, Wv)
 
 
+@pytest.mark.parametrize("rope,fmt", [(True, 0), (False, 0), (True, 1)])
+def test_gemm_headnorm_equals_gemm_then_rmsrope(rope, fmt):
+    """The projection with the per-head RMSNorm (+ RoPE) fused into its store (kern.c:163-197 in the GEMM flush)
+    equals the plain projection followed by the standalone RMS+RoPE kernel, bit for bit; q and k take their own
+    gains, the v columns go transposed and un-normalised. Two images of 128 tokens share the RoPE table."""
+    hip = _hip()
+    say(f"gemm headnorm rope={rope} fmt={fmt}")
+    rng = np.random.default_rng(21)
+    T, D, B = 128, 256, 2
+    M = B * T
+    A = f16(rng.standard_normal((M, D)))
+    if fmt == 0:
+        W, S = f16(rng.standard_normal((3 * D, D)) * 0.05), None
+    else:
+        W, S = hxo.q8_quantize((rng.standard_normal((3 * D, D)) * 0.05).astype(np.float32))
+    gq = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    gk = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    cos, sin = hxo.rope_anima(8, 16)
+    dA, dW = hip.DeviceArray.from_numpy(A), hip.DeviceArray.from_numpy(W)
+    dS = hip.DeviceArray.from_numpy(S) if S is not None else None
+    dq, dk = hip.DeviceArray.from_numpy(gq), hip.DeviceArray.from_numpy(gk)
+    dc, ds = hip.DeviceArray.from_numpy(cos), hip.DeviceArray.from_numpy(sin)
+    qk = hip.DeviceArray((M, 2 * D), np.float16)
+    vt = hip.DeviceArray((D, M), np.float16)
+    hip.check(hip.lib().hxa_gemm_headnorm(dA.ptr, D, M, fmt, dW.ptr, dS.ptr if dS else None, None, 3 * D, D, qk.ptr, 2 * D,
+                                          vt.ptr, M, 2 * D, 2 * D, dq.ptr, dk.ptr, D, dc.ptr if rope else None,
+                                          ds.ptr if rope else None, T, None), "gemm_headnorm")
+    qk2 = hip.DeviceArray((M, 2 * D), np.float16)
+    vt2 = hip.DeviceArray((D, M), np.float16)
+    hip.check(hip.lib().hxa_gemm(dA.ptr, D, M, fmt, dW.ptr, dS.ptr if dS else None, None, 3 * D, D, 1, 0, qk2.ptr, 2 * D, 0,
+                                 None, 0, None, vt2.ptr, M, 2 * D, None), "gemm")
+    hip.sync()
+    plain = qk2.numpy()  # the projection before the head norm
+    hip.check(hip.lib().hxa_rmsrope(qk2.ptr, qk2.ptr + 2 * D, dq.ptr, dk.ptr, 2 * D, M, D // 128, dc.ptr if rope else None,
+                                    ds.ptr if rope else None, T, None), "rmsrope")
+    hip.sync()
+    assert np.array_equal(qk.numpy().view(np.uint16), qk2.numpy().view(np.uint16))
+    assert np.array_equal(vt.numpy().view(np.uint16), vt2.numpy().view(np.uint16))
+    # and against the oracle's RMS+RoPE of the GPU's own projection
+    ref = plain
+    for part, g in ((slice(0, D), gq), (slice(D, 2 * D), gk)):
+        for b in range(B):
+            rows = slice(b * T, (b + 1) * T)
+            o = hxo.rmsrope(np.ascontiguousarray(ref[rows, part]), g, cos if rope else None, sin if rope else None)
+            assert ulp_diff(qk.numpy()[rows, part], o.view(np.float16)).max() <= 1
+
+
 def test_gemm_rejects_bad_shapes():
     hip = _hip()
     say("gemm argument checks")
