@@ -50,7 +50,8 @@ struct GemmParams {
 // Per-head RMSNorm * gain + split-half RoPE of one 8-column chunk (kern.c:163-197), the same arithmetic as the
 // standalone RMS+RoPE kernel: the 16 lanes holding one head's 128 values (aligned 16-lane group, chunk j = lane & 15
 // owning dims [8j, 8j+8)) reduce with shfl_xor(1..8); the RoPE partner of dim d < 64 (d + 64) is in lane j ^ 8.
-HXA_DEV half8_t head_norm(half8_t v, int j, int m, int n, const GemmParams &p) {
+// g: the chunk's 8 gains; cs / sn: cos / sin of dims 8 (j & 7) .. +8 at the row's token (rope only).
+HXA_DEV half8_t head_norm(half8_t v, int j, const float (&g)[8], bool rope, const float (&cs)[8], const float (&sn)[8]) {
   float a[8], ss = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; e++) {
@@ -60,20 +61,9 @@ HXA_DEV half8_t head_norm(half8_t v, int j, int m, int n, const GemmParams &p) {
 #pragma unroll
   for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);
   const float r = rsqrtf(ss * (1.0f / 128.0f) + 1e-6f);
-  const float *g = (n < p.hn_gsplit ? p.hn_g0 : p.hn_g1) + 8 * j;
-  const float4_t ga = *(const float4_t *)g, gb = *(const float4_t *)(g + 4);
 #pragma unroll
-  for (int e = 0; e < 4; e++) {
-    a[e] = a[e] * r * ga[e];
-    a[e + 4] = a[e + 4] * r * gb[e];
-  }
-  if (p.hn_cos != nullptr) {
-    const int tt = m % p.hn_ttab, d0 = 8 * (j & 7);
-    const float *cr = p.hn_cos + (long)tt * 64 + d0, *sr = p.hn_sin + (long)tt * 64 + d0;
-    const float4_t c0 = *(const float4_t *)cr, c1 = *(const float4_t *)(cr + 4);
-    const float4_t s0 = *(const float4_t *)sr, s1 = *(const float4_t *)(sr + 4);
-    const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-    const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  for (int e = 0; e < 8; e++) a[e] = a[e] * r * g[e];
+  if (rope) {
 #pragma unroll
     for (int e = 0; e < 8; e++) {
       const float partner = __shfl_xor(a[e], 8);
@@ -84,6 +74,28 @@ HXA_DEV half8_t head_norm(half8_t v, int j, int m, int n, const GemmParams &p) {
 #pragma unroll
   for (int e = 0; e < 8; e++) o[e] = (hxa_h)a[e];
   return o;
+}
+// the chunk's gains (columns n .. n+7 of head-normed output) and a row's RoPE coefficients
+HXA_DEV void hn_gains(const GemmParams &p, int n, float (&g)[8]) {
+  const float *gp = (n < p.hn_gsplit ? p.hn_g0 : p.hn_g1) + (n & 127);
+  const float4_t a = *(const float4_t *)gp, b = *(const float4_t *)(gp + 4);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    g[e] = a[e];
+    g[e + 4] = b[e];
+  }
+}
+HXA_DEV void hn_rope(const GemmParams &p, int m, int n, float (&cs)[8], float (&sn)[8]) {
+  const long o = (long)(m % p.hn_ttab) * 64 + (n & 63);
+  const float4_t c0 = *(const float4_t *)(p.hn_cos + o), c1 = *(const float4_t *)(p.hn_cos + o + 4);
+  const float4_t s0 = *(const float4_t *)(p.hn_sin + o), s1 = *(const float4_t *)(p.hn_sin + o + 4);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    cs[e] = c0[e];
+    cs[e + 4] = c1[e];
+    sn[e] = s0[e];
+    sn[e + 4] = s1[e];
+  }
 }
 
 HXA_DEV half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
@@ -463,6 +475,36 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
     }
     return;
   }
+  if constexpr (BN % 128 == 0 && (64 * NW) % (BN / 8) == 0) {
+  if (p.hn_cols > 0 && n0 + BN <= p.hn_cols) {
+    // every column of this tile is head-normed: a thread's chunk position (column) is the same in every pass, so its
+    // gains are loaded once; the next row's RoPE coefficients are fetched one pass ahead
+    constexpr int NC8 = BN / 8, ITERS = BM * NC8 / NT;
+    static_assert(NT % NC8 == 0 && NC8 % 16 == 0, "head groups aligned to 16 lanes");
+    const int nl = (tid % NC8) * 8, n = n0 + nl, j = (nl >> 3) & 15;
+    const bool rope = p.hn_cos != nullptr;
+    float g[8], cs[8] = {}, sn[8] = {}, csn[8] = {}, snn[8] = {};
+    hn_gains(p, n, g);
+    if (rope) hn_rope(p, min(m0 + tid / NC8, p.M - 1), n, cs, sn);
+#pragma unroll 2
+    for (int it = 0; it < ITERS; it++) {
+      const int ml = (tid + it * NT) / NC8, m = m0 + ml;
+      if (rope && it + 1 < ITERS) hn_rope(p, min(m + NT / NC8, p.M - 1), n, csn, snn);
+      if (m < p.M) {
+        const half8_t v = *(const half8_t *)(Cs + ml * CROW + nl);
+        *(half8_t *)(p.out + (long)m * p.ldo + n) = head_norm(v, j, g, rope, cs, sn);
+      }
+      if (rope) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          cs[e] = csn[e];
+          sn[e] = snn[e];
+        }
+      }
+    }
+    return;
+  }
+  }
   auto rows_pass = [&](auto ncols_c) {
   const int nc8 = ncols_c / 8;
   for (int c = tid; c < BM * nc8; c += NT) {
@@ -475,7 +517,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
       *(half8_t *)(p.out + (long)z * p.out_zstride + o) = v;
     } else {
       if (n < p.hn_cols) {  // whole 16-lane head groups take this branch together (n0, ncols multiples of 128)
-        v = head_norm(v, (nl >> 3) & 15, m, n, p);
+        float g[8], cs[8] = {}, sn[8] = {};
+        hn_gains(p, n, g);
+        if (p.hn_cos) hn_rope(p, m, n, cs, sn);
+        v = head_norm(v, (nl >> 3) & 15, g, p.hn_cos != nullptr, cs, sn);
       } else if (p.epi == HXA_EPI_GELU_TANH) {
 #pragma unroll
         for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_tanh_f((float)v[e]);
