@@ -1,0 +1,80 @@
+"""Full-size DiT parity: the 2B-class fp16 DiT (28 Anima-structure blocks, hidden 2048, 16 heads, MLP 8192, 256 text
+tokens of width 1024) at 1536 image tokens runs a 4-step Euler denoise (sigmas 1, .75, .5, .25 -> 0) on the GPU and
+on the CPU oracle (the reference block's rounding points, blk.c:149-176, composed with the caller-side glue of
+phone/animad.cpp:424-492), with the same weights (exported from the GPU runner) and inputs.
+
+Tolerance: the reference's own block metric (cmp_block.py:5-6) on the whole denoise, rel err on the latent change
+< 5e-3 and cosine > 0.99999 (measured on MI355X: 5.3e-4 and 0.9999999; the reference device reaches 6.9e-4 on ONE
+block, docs/PITFALLS.md:154). The GPU softmax is exact fp32 with fp16 probabilities where the reference rounds S,
+S-m, P and the row sum to fp16, and the GPU GEMMs accumulate in fp32 where the oracle uses double; these are the
+differences that compound over the 112 block evaluations. The oracle needs about a minute on 16 host threads;
+progress is printed after every step. Collected after the other GPU tests."""
+import time
+
+import numpy as np
+import pytest
+
+from oracle import hxo
+from tests._helpers import delta_metrics, f16, oracle_anima_velocity, unpack_weights
+
+pytestmark = pytest.mark.gpu
+
+D, H, F, C, DC, NB = 2048, 16, 8192, 256, 1024, 28
+LAT = (16, 96, 64)
+
+
+def test_dit_2b_fp16_1536tok_4step_denoise_vs_oracle():
+    from hexanima_amd import hip
+    import ctypes as C_
+
+    hip.init(0)
+    lib = hip.lib()
+    hxo.set_threads(0)
+    print("[case] 2B fp16 DiT, 28 blocks, 1536 tokens, 4-step denoise vs oracle", flush=True)
+    bd = hip.BlockDims(0, D, H, F, C, DC, 0, 1, 0, hip.W_F16, hip.W_F16, 1)
+    cfg = hip.DitCfg(bd, NB, LAT[0], LAT[1], LAT[2], 256, 0)
+    p = C_.c_void_p()
+    hip.check(lib.hxa_dit_create(C_.byref(cfg), 77, C_.byref(p)), "dit_create")
+    try:
+        rng = np.random.default_rng(9)
+        lat = rng.standard_normal((1,) + LAT).astype(np.float32)
+        ctx = rng.standard_normal((1, C, DC)).astype(np.float32)
+        hip.check(lib.hxa_dit_set_inputs(p, lat.ctypes.data, ctx.ctypes.data), "set_inputs")
+
+        def export(which):
+            n = lib.hxa_dit_export(p, which, None, 0)
+            buf = np.zeros(n, np.uint8)
+            assert lib.hxa_dit_export(p, which, buf.ctypes.data, n) == n
+            return buf
+
+        t0 = time.time()
+        layout = hip.pack_layout(0, D, F, DC, 0, 0)
+        blocks = [unpack_weights(export(k), 0, D, F, DC, 0, 0, layout) for k in range(NB)]
+        modws = [export(NB + k).view(np.uint16).reshape(6 * D, D) for k in range(NB)]
+        g = export(2 * NB).view(np.uint16)
+        C4 = 4 * LAT[0]
+        glue, o = [], 0
+        for (n, k) in ((D, C4), (D, 256), (2 * D, D), (C4, D)):
+            glue.append(g[o:o + n * k].reshape(n, k))
+            o += n * k
+        print(f"weights exported in {time.time() - t0:.1f} s", flush=True)
+
+        sig = [1.0, 0.75, 0.5, 0.25, 0.0]
+        for i in range(4):
+            hip.check(lib.hxa_dit_step(p, sig[i], sig[i + 1], 1), "step")
+        got = np.zeros_like(lat)
+        hip.check(lib.hxa_dit_get_latent(p, got.ctypes.data), "get_latent")
+
+        ctx16 = f16(ctx)
+        ref = lat.copy()
+        for i in range(4):
+            t1 = time.time()
+            v = oracle_anima_velocity(ref, ctx16, sig[i], blocks, modws, glue, D=D, H=H, F=F, C4=C4, temb=256)
+            ref = ref + (sig[i + 1] - sig[i]) * v
+            print(f"oracle step {i + 1}/4 done in {time.time() - t1:.1f} s", flush=True)
+        r, c = delta_metrics(got, ref, lat)
+        print(f"2B DiT 4-step denoise: rel err on latent change {r:.3e}, cosine {c:.7f}", flush=True)
+        assert np.isfinite(got).all()
+        assert r < 5e-3 and c > 0.99999
+    finally:
+        lib.hxa_dit_destroy(p)
