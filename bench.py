@@ -99,6 +99,47 @@ def gpu_run(steps, warmup):
     return info, ms_step, up_ms
 
 
+def q8_dit_run(steps=10, warmup=2):
+    """The 2.9B-class q8 DiT step (28 blocks, hidden 2560, 20 heads, MLP 10240, every block linear int8 with fp16
+    group-32 scales; norms and modulation fp16), same latent / text shapes: ms per graph-replayed Euler step."""
+    from hexanima_amd import hip
+    L = hip.lib()
+    Dq, Hq, Fq = 2560, 20, 10240
+    bd = hip.BlockDims(0, Dq, Hq, Fq, C_TXT, DC, 0, 1, 0, hip.W_Q8, hip.W_Q8, 1)
+    cfg = hip.DitCfg(bd, NBLK, LAT[0], LAT[1], LAT[2], 256, 0)
+    dit = C.c_void_p()
+    hip.check(L.hxa_dit_create(C.byref(cfg), 2025, C.byref(dit)), "dit_create q8")
+    rng = np.random.default_rng(2)
+    lat = rng.standard_normal((1,) + LAT).astype(np.float32)
+    ctx = rng.standard_normal((1, C_TXT, DC)).astype(np.float32)
+    hip.check(L.hxa_dit_set_inputs(dit, lat.ctypes.data, ctx.ctypes.data), "set_inputs q8")
+    st = L.hxa_dit_stream(dit)
+    sig = [1.0, 0.75, 0.5, 0.25, 0.0]
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    hip.check(L.hxa_event_create(C.byref(e0)), "event")
+    hip.check(L.hxa_event_create(C.byref(e1)), "event")
+    for i in range(warmup):
+        hip.check(L.hxa_dit_step(dit, sig[i % 4], sig[i % 4 + 1], 1), "step q8")
+    hip.check(L.hxa_event_record(e0, st), "rec")
+    for i in range(steps):
+        hip.check(L.hxa_dit_step(dit, sig[i % 4], sig[i % 4 + 1], 1), "step q8")
+    hip.check(L.hxa_event_record(e1, st), "rec")
+    hip.check(L.hxa_stream_sync(st), "sync")
+    ms = C.c_float()
+    hip.check(L.hxa_event_elapsed_ms(e0, e1, C.byref(ms)), "elapsed")
+    out = np.zeros_like(lat)
+    hip.check(L.hxa_dit_get_latent(dit, out.ctypes.data), "latent q8")
+    L.hxa_dit_destroy(dit)
+    if not np.isfinite(out).all():
+        raise RuntimeError("non-finite q8 latent")
+    blk = 2 * T * Dq * (3 * Dq) + 3 * 2 * T * Dq * Dq + 2 * C_TXT * DC * 2 * Dq + 2 * 2 * T * Dq * Fq \
+        + 4 * T * T * Dq + 4 * T * C_TXT * Dq
+    ms_step = ms.value / steps
+    return {"steps_per_s": round(1000.0 / ms_step, 3), "ms_per_step": round(ms_step, 4),
+            "step_tflops": round(NBLK * blk / (ms_step * 1e-3) / 1e12, 1),
+            "config": "28 blocks, hidden 2560, 20 heads, MLP 10240, int8 g32 block linears, 1536 image + 256 text tokens"}
+
+
 def kernel_probe(reps):
     """Launches only the dominant kernel (MLP-up GEMM, `reps` times) and a 256 MiB device-to-device copy (3 times,
     the byte-count calibration of the FETCH_SIZE / WRITE_SIZE counters), for `rocprofv3 --pmc` passes."""
@@ -196,6 +237,7 @@ def main():
                      "frac": round(up_tf / PEAK_FP16, 4), "traffic": traffic, "avg_launch_us": round(up_ms * 1e3, 2)},
         "device": info.get("name"),
     }
+    res["q8_2p9b_dit"] = q8_dit_run()
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)
