@@ -95,6 +95,35 @@ def oracle_anima_velocity(lat, ctx16, sigma, blocks, modws, glue, *, D, H, F, C4
     return out
 
 
+def oracle_moss_velocity(lat, txt16, sigma, blocks, modw, glue, *, D, H, F, C4, temb, ntxt, Ttot, attn_mode=0):
+    """v(x, sigma) of the MOSS-class DiT (moss_ref.py:56-67 blocks with one shared modulation, joint image + text
+    attention over nvalid = image + text tokens, padded to Ttot), image by image, from the oracle primitives.
+    glue = (Wemb [D][C4], L1 [D][temb], Lf [2D][D], Wfin [C4][D], Wtxt [D][ntxt_in]) fp16; modw [6D][D] fp16.
+    The text rows are f16(text . Wtxt^T) (the projection written into zeroed rows, moss blk.c MODE 2)."""
+    Wemb, L1, Lf, Wfin, Wtxt = glue
+    B, Cc, Hl, Wl = lat.shape
+    s = hxo.sinusoid(sigma, temb)
+    sc = silu(hxo.linear_f32(s[None, :], L1))
+    mod6 = hxo.linear_f32(sc, modw)[0].reshape(6, D)
+    fm = hxo.linear_f32(sc, Lf)[0]
+    bands = (1.0 / 10000.0 ** (np.arange(16) / 16.0)).astype(np.float32)
+    c, sn = hxo.rope_moss(Hl // 2, Wl // 2, ntxt, bands)
+    cos = np.ones((Ttot, 64), np.float32)
+    sin = np.zeros((Ttot, 64), np.float32)
+    cos[:c.shape[0]], sin[:c.shape[0]] = c, sn
+    timg = (Hl // 2) * (Wl // 2)
+    out = np.zeros_like(lat)
+    for b in range(B):
+        x = np.zeros((Ttot, D), np.float32)
+        x[:timg] = hxo.linear_f32(hxo.patchify(lat[b]), Wemb)
+        x[timg:timg + ntxt] = f16(hxo.gemm(txt16[b], Wtxt)).astype(np.float32)
+        for w in blocks:
+            x, _, _ = hxo.moss_block(x, mod6, cos, sin, w, H=H, F=F, nvalid=timg + ntxt, attn_mode=attn_mode)
+        xn = hxo.final_norm(x[:timg], fm[:D], fm[D:])
+        out[b] = hxo.unpatchify(hxo.linear_f32(xn, Wfin), Cc, Hl, Wl)
+    return out
+
+
 def gemm_bound(A16, W16):
     """Per-element bound on |f16(fp32-accumulated A.W^T) - f16(exact)|: one fp16 ulp of the result plus the fp32
     accumulation-order error 4 sqrt(K) 2^-24 sum_k |a_k w_k| (probabilistic form of the gamma_K bound)."""

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from oracle import hxo
-from tests._helpers import delta_metrics, f16, oracle_anima_velocity, rel, unpack_weights
+from tests._helpers import delta_metrics, f16, oracle_anima_velocity, oracle_moss_velocity, rel, unpack_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -317,6 +317,50 @@ def test_dit_small_denoise_vs_oracle():
         hip.check(lib.hxa_dit_get_latent(p, got.ctypes.data), "get_latent")
         r, c = delta_metrics(got, ref, lat)
         print(f"denoise rel err on delta {r:.2e} cos {c:.7f}", flush=True)
+        assert r < 5e-3 and c > 0.99999
+    finally:
+        lib.hxa_dit_destroy(p)
+
+
+def test_dit_moss_small_denoise_vs_oracle():
+    """MOSS-class DiT (shared modulation, joint image + text attention with padded keys masked, SiTU FFN, text
+    projection into the joint token layout), 2 blocks, batch 2, q8 attention / q4 FFN weights: 4-step Euler denoise
+    against the oracle DiT. With N(0, 0.02) modulation weights the block gates are small, so this pins mostly the
+    caller-side glue around the blocks; the blocks themselves are pinned by test_moss_block_joint_attention_q8_q4."""
+    hip = _hip()
+    say("dit moss small 2 blocks batch 2 q8/q4 4-step denoise")
+    lib = hip.lib()
+    D, H, F, ntxt, tin, nb = 256, 2, 512, 20, 128, 2
+    bd = hip.BlockDims(1, D, H, F, ntxt, 0, 0, 2, 0, hip.W_Q8, hip.W_Q4, 1)
+    cfg = hip.DitCfg(bd, nb, 16, 16, 16, 256, tin)
+    p = C.c_void_p()
+    hip.check(lib.hxa_dit_create(C.byref(cfg), 4321, C.byref(p)), "dit_create")
+    try:
+        rng = np.random.default_rng(8)
+        lat = rng.standard_normal((2, 16, 16, 16)).astype(np.float32)
+        txt = rng.standard_normal((2, ntxt, tin)).astype(np.float32)
+        hip.check(lib.hxa_dit_set_inputs(p, lat.ctypes.data, txt.ctypes.data), "set_inputs")
+        C4, timg = 64, 64
+        Ttot = (timg + ntxt + 31) // 32 * 32
+        layout = hip.pack_layout(1, D, F, 0, hip.W_Q8, hip.W_Q4)
+        blocks = [unpack_weights(_export(hip, p, k), 1, D, F, 0, hip.W_Q8, hip.W_Q4, layout) for k in range(nb)]
+        modw = _export(hip, p, nb).view(np.uint16).reshape(6 * D, D)
+        g = _export(hip, p, 2 * nb).view(np.uint16)
+        glue, o = [], 0
+        for (n, k) in ((D, C4), (D, 256), (2 * D, D), (C4, D), (D, tin)):
+            glue.append(g[o:o + n * k].reshape(n, k))
+            o += n * k
+        kw = dict(D=D, H=H, F=F, C4=C4, temb=256, ntxt=ntxt, Ttot=Ttot)
+        txt16 = f16(txt)
+        sig = [1.0, 0.75, 0.5, 0.25, 0.0]
+        ref = lat.copy()
+        for i in range(4):
+            hip.check(lib.hxa_dit_step(p, sig[i], sig[i + 1], 1), "step")
+            ref = ref + (sig[i + 1] - sig[i]) * oracle_moss_velocity(ref, txt16, sig[i], blocks, modw, glue, **kw)
+        got = np.zeros_like(lat)
+        hip.check(lib.hxa_dit_get_latent(p, got.ctypes.data), "get_latent")
+        r, c = delta_metrics(got, ref, lat)
+        print(f"moss denoise rel err on delta {r:.2e} cos {c:.7f}", flush=True)
         assert r < 5e-3 and c > 0.99999
     finally:
         lib.hxa_dit_destroy(p)
