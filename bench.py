@@ -27,6 +27,7 @@ PEAK_HBM = 8.0e12      # bytes/s
 D, H, F, C_TXT, DC, NBLK = 2048, 16, 8192, 256, 1024, 28
 LAT = (16, 96, 64)
 T = (LAT[1] // 2) * (LAT[2] // 2)
+WFMT = 0 | 16  # fp16 weights, k-tiled: the block-pack layout of the DiT's matrices
 BLOCK_FLOPS = 2 * T * D * (3 * D) + 2 * T * D * D + 2 * T * D * D + 2 * C_TXT * DC * (2 * D) + 2 * T * D * D \
     + 2 * T * D * F * 2 + 4 * T * T * D + 4 * T * C_TXT * D
 STEP_FLOPS = NBLK * BLOCK_FLOPS + 2 * T * 64 * D + 2 * T * D * 64
@@ -84,7 +85,7 @@ def gpu_run(steps, warmup):
     hip.check(L.hxa_fill_normal(W.ptr, 1, F * D, 12, 0.0, 0.02, s), "fill")
 
     def up():
-        hip.check(L.hxa_gemm(A.ptr, D, T, hip.W_F16, W.ptr, None, None, F, D, 1, hip.EPI_GELU_TANH, O.ptr, F, 0, None, 0,
+        hip.check(L.hxa_gemm(A.ptr, D, T, WFMT, W.ptr, None, None, F, D, 1, hip.EPI_GELU_TANH, O.ptr, F, 0, None, 0,
                              None, None, 0, 0, s), "gemm")
     for _ in range(5):
         up()
@@ -154,7 +155,7 @@ def kernel_probe(reps):
     hip.check(L.hxa_fill_normal(A.ptr, 1, T * D, 11, 0.0, 1.0, s), "fill")
     hip.check(L.hxa_fill_normal(W.ptr, 1, F * D, 12, 0.0, 0.02, s), "fill")
     for _ in range(reps):
-        hip.check(L.hxa_gemm(A.ptr, D, T, hip.W_F16, W.ptr, None, None, F, D, 1, hip.EPI_GELU_TANH, O.ptr, F, 0, None, 0,
+        hip.check(L.hxa_gemm(A.ptr, D, T, WFMT, W.ptr, None, None, F, D, 1, hip.EPI_GELU_TANH, O.ptr, F, 0, None, 0,
                              None, None, 0, 0, s), "gemm")
     nb = 256 << 20
     src = hip.DeviceArray((nb,), np.uint8)
@@ -232,7 +233,7 @@ def main():
                    "seq_len": T, "parallelism": "single GPU"},
         "step_tflops": round(STEP_FLOPS / (ms_step * 1e-3) / 1e12, 1),
         "step_frac_of_fp16_peak": round(STEP_FLOPS / (ms_step * 1e-3) / PEAK_FP16, 4),
-        "roofline": {"kernel": "gemm_kernel (fp16, GELU epilogue) MLP up 1536x2048x8192", "bound": "mfma",
+        "roofline": {"kernel": "gemm_kernel (fp16 k-tiled W, GELU epilogue) MLP up 1536x2048x8192", "bound": "mfma",
                      "achieved": round(up_tf / 1e12, 1), "peak": PEAK_FP16 / 1e12, "unit": "TFLOP/s",
                      "frac": round(up_tf / PEAK_FP16, 4), "traffic": traffic, "avg_launch_us": round(up_ms * 1e3, 2)},
         "device": info.get("name"),

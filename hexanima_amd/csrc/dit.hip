@@ -131,7 +131,9 @@ int init_pack(Dit &d, void *pack, uint64_t seed, float *tmp32) {
       DTRY(hxa_fill_normal_launch(base + offs[3 * i], 1, elems, seed * 131 + i, 0.0f, 0.02f, d.st));
     } else {
       DTRY(hxa_fill_normal_launch(tmp32, 0, elems, seed * 131 + i, 0.0f, 0.02f, d.st));
-      DTRY(hxa_quantize_launch(tmp32, N[i], K[i], fmt[i], base + offs[3 * i], (hxa_h *)(base + offs[3 * i + 1]), d.st));
+      // packs hold k-tiled matrices; the i.i.d. fp16 fill above needs no layout
+      DTRY(hxa_quantize_launch(tmp32, N[i], K[i], fmt[i] | HXA_W_KTILED, base + offs[3 * i],
+                               (hxa_h *)(base + offs[3 * i + 1]), d.st));
     }
   }
   float *vec = (float *)(base + offs[3 * n]);

@@ -20,19 +20,35 @@ HXA_DEV float wave_sum(float v) {
 // ---------------------------------------------------------------------------------------------------------------
 // modulated norm (kern.c:31-65 LN-mod; moss kern.c:345-375 RMS-mod)
 // ---------------------------------------------------------------------------------------------------------------
+// With t != NULL the pending gated residual of the previous site is applied first, x += gate * t (kern.c:320-328,
+// the same fma as the GEMM residual epilogue), x is written back, and the norm is taken of the updated row.
 template <int VPL>
-__global__ __launch_bounds__(256) void normmod_kernel(const float *__restrict__ x, long ldx, int T, int D,
+__global__ __launch_bounds__(256) void normmod_kernel(float *__restrict__ x, long ldx, int T, int D,
+                                                      const hxa_h *__restrict__ t, long ldt, const float *__restrict__ gate,
                                                       const float *__restrict__ shift, const float *__restrict__ scale,
                                                       const float *__restrict__ w, float eps, hxa_h *__restrict__ h,
                                                       long ldh) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= T) return;
-  const float4_t *xr = (const float4_t *)(x + (long)row * ldx);
+  float4_t *xr = (float4_t *)(x + (long)row * ldx);
   float4_t v[VPL];
   float s = 0.0f, q = 0.0f;
 #pragma unroll
+  for (int i = 0; i < VPL; i++) v[i] = xr[lane + 64 * i];
+  if (t != nullptr) {
+    half4_t tv[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; i++) tv[i] = *(const half4_t *)(t + (long)row * ldt + (lane + 64 * i) * 4);
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+      const float4_t g = *(const float4_t *)(gate + (lane + 64 * i) * 4);
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[i][e] = fmaf(g[e], (float)tv[i][e], v[i][e]);
+      xr[lane + 64 * i] = v[i];
+    }
+  }
+#pragma unroll
   for (int i = 0; i < VPL; i++) {
-    v[i] = xr[lane + 64 * i];
     s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
     q += (v[i][0] * v[i][0] + v[i][1] * v[i][1]) + (v[i][2] * v[i][2] + v[i][3] * v[i][3]);
   }
@@ -404,7 +420,7 @@ __global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ x,
 
 // q8 / q4 quantisation of W[N][K] fp32, one thread per (column n, 32-group g): amax of the fp16-rounded weights,
 // s = f16(max(amax / qmax, 6.2e-5)), q = clip(rint(f16(w) / s)) (export_all.py:10-18, moss/export_all_q8.py:13)
-__global__ void quantize_kernel(const float *W, int N, int K, int fmt, void *q, hxa_h *s) {
+__global__ void quantize_kernel(const float *W, int N, int K, int fmt, int kt, void *q, hxa_h *s) {
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   const int G = K / 32;
   if (i >= (long)N * G) return;
@@ -423,11 +439,11 @@ __global__ void quantize_kernel(const float *W, int N, int K, int fmt, void *q, 
   const float sf = (float)sh;
   s[(long)g * N + n] = sh;
   if (fmt == HXA_W_Q8) {
-    int8_t *qr = (int8_t *)q + (long)n * K + g * 32;
+    int8_t *qr = (int8_t *)q + (kt ? ((long)g * N + n) * 32 : (long)n * K + g * 32);
 #pragma unroll
     for (int j = 0; j < 32; j++) qr[j] = (int8_t)fminf(fmaxf(rintf(a[j] / sf), qmin), qmax);
   } else {
-    uint32_t *qw = (uint32_t *)((uint8_t *)q + (long)n * (K / 2) + g * 16);
+    uint32_t *qw = (uint32_t *)((uint8_t *)q + (kt ? ((long)g * N + n) * 16 : (long)n * (K / 2) + g * 16));
 #pragma unroll
     for (int w8 = 0; w8 < 4; w8++) {
       uint32_t word = 0;
@@ -447,22 +463,26 @@ inline unsigned nblk(long n, int per = 256) { return (unsigned)((n + per - 1) / 
 
 #define LAUNCH_OK() (hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP)
 
-int hxa_norm_mod_launch(const float *x, long ldx, int T, int D, const float *shift, const float *scale, const float *w,
-                        float eps, hxa_h *h, long ldh, hipStream_t st) {
-  if (T <= 0 || D % 256 != 0 || ldx % 4 || ldh % 4) return HXA_E_ARG;
+int hxa_resid_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, long ldt, const float *gate,
+                              const float *shift, const float *scale, const float *w, float eps, hxa_h *h, long ldh,
+                              hipStream_t st) {
+  if (T <= 0 || D % 256 != 0 || ldx % 4 || ldh % 4 || (t && (ldt % 4 || !gate))) return HXA_E_ARG;
   const int vpl = D / 256;
   dim3 g(nblk(T, 4)), b(256);
   switch (vpl) {
-    case 1: hipLaunchKernelGGL(normmod_kernel<1>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
-    case 2: hipLaunchKernelGGL(normmod_kernel<2>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
-    case 4: hipLaunchKernelGGL(normmod_kernel<4>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
-    case 8: hipLaunchKernelGGL(normmod_kernel<8>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
-    case 10: hipLaunchKernelGGL(normmod_kernel<10>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
-    case 12: hipLaunchKernelGGL(normmod_kernel<12>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
-    case 16: hipLaunchKernelGGL(normmod_kernel<16>, g, b, 0, st, x, ldx, T, D, shift, scale, w, eps, h, ldh); break;
-    default: return HXA_E_ARG;
+#define HXA_NORMMOD(V) \
+  case V: hipLaunchKernelGGL(normmod_kernel<V>, g, b, 0, st, x, ldx, T, D, t, ldt, gate, shift, scale, w, eps, h, ldh); break;
+    HXA_NORMMOD(1) HXA_NORMMOD(2) HXA_NORMMOD(4) HXA_NORMMOD(8) HXA_NORMMOD(10) HXA_NORMMOD(12) HXA_NORMMOD(16)
+#undef HXA_NORMMOD
+    default:
+      return HXA_E_ARG;
   }
   return LAUNCH_OK();
+}
+
+int hxa_norm_mod_launch(const float *x, long ldx, int T, int D, const float *shift, const float *scale, const float *w,
+                        float eps, hxa_h *h, long ldh, hipStream_t st) {
+  return hxa_resid_norm_mod_launch((float *)x, ldx, T, D, nullptr, 0, nullptr, shift, scale, w, eps, h, ldh, st);
 }
 
 int hxa_rmsrope_launch(hxa_h *q0, hxa_h *q1, const float *g0, const float *g1, long ldq, int T, int H, const float *cosT,
@@ -576,6 +596,7 @@ int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, 
   return LAUNCH_OK();
 }
 
+
 int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale,
                      const hxa_h *Wf, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st) {
   const int NO = 4 * Cc;
@@ -592,7 +613,9 @@ int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t 
   return LAUNCH_OK();
 }
 int hxa_quantize_launch(const float *W, int N, int K, int fmt, void *q, hxa_h *s, hipStream_t st) {
+  const int kt = (fmt & HXA_W_KTILED) ? 1 : 0;
+  fmt &= ~HXA_W_KTILED;
   if (K % 32 || (fmt != HXA_W_Q8 && fmt != HXA_W_Q4)) return HXA_E_ARG;
-  hipLaunchKernelGGL(quantize_kernel, dim3(nblk((long)N * (K / 32))), dim3(256), 0, st, W, N, K, fmt, q, s);
+  hipLaunchKernelGGL(quantize_kernel, dim3(nblk((long)N * (K / 32))), dim3(256), 0, st, W, N, K, fmt, kt, q, s);
   return LAUNCH_OK();
 }

@@ -30,7 +30,8 @@ struct GemmParams {
   long lda;
   const void *W;
   const hxa_h *S, *Z;
-  long ldw;  // elements per W row (fp16/int8: K; int4: bytes per row = K/2)
+  long ldw;  // elements per W row (fp16/int8: K; int4: bytes per row = K/2); row-major layout only
+  int wkt;   // 1: W k-tiled, [K/32][N][32 elements] (q4: [K/32][N][16 bytes])
   int M, N, Kslice, Ktot;
   int epi;
   hxa_h *out;
@@ -229,15 +230,20 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
       if (G::TW % NW == 0 || t < G::TW) {
         const int chunk = t * 64 + lane;
         if ((G::W_BYTES / 16) % 64 == 0 || chunk < G::W_BYTES / 16) {
+          // W row n, k tile k0: row-major [N][K] (n ldw + k0), or k-tiled [K/32][N][32] (k0 N + 32 n: one step's
+          // slice of the whole matrix is contiguous)
           if (FMT == HXA_W_F16) {
             const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3), n = min(n0 + row, p.N - 1);
-            g2l16_opaque((const hxa_h *)p.W + (long)n * p.ldw + k0 + cl * 8, ws + t * 1024);
+            const long o = p.wkt ? (long)k0 * p.N + n * 32L : (long)n * p.ldw + k0;
+            g2l16_opaque((const hxa_h *)p.W + o + cl * 8, ws + t * 1024);
           } else if (FMT == HXA_W_Q8) {
             const int row = chunk >> 1, cl = (chunk & 1) ^ ((row >> 3) & 1), n = min(n0 + row, p.N - 1);
-            g2l16_opaque((const int8_t *)p.W + (long)n * p.ldw + k0 + cl * 16, ws + t * 1024);
+            const long o = p.wkt ? (long)k0 * p.N + n * 32L : (long)n * p.ldw + k0;
+            g2l16_opaque((const int8_t *)p.W + o + cl * 16, ws + t * 1024);
           } else {
             const int row = chunk, n = min(n0 + row, p.N - 1);
-            g2l16_opaque((const uint8_t *)p.W + (long)n * p.ldw + (k0 >> 1), ws + t * 1024);
+            const long o = p.wkt ? (long)(k0 >> 1) * p.N + n * 16L : (long)n * p.ldw + (k0 >> 1);
+            g2l16_opaque((const uint8_t *)p.W + o, ws + t * 1024);
           }
         }
       }
@@ -635,7 +641,9 @@ static void pick_tile(int M, int N, int ksplit, int fmt, int epi, bool headnorm,
 }
 
 int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
-  const HxaWeight &w = *g.w;
+  HxaWeight w = *g.w;
+  const int wkt = (w.fmt & HXA_W_KTILED) ? 1 : 0;
+  w.fmt &= ~HXA_W_KTILED;
   if (g.M <= 0 || w.N <= 0 || w.K <= 0 || g.ksplit < 1) return HXA_E_ARG;
   if (w.K % (32 * g.ksplit) != 0) return HXA_E_ARG;
   if (w.fmt != HXA_W_F16 && w.s == nullptr) return HXA_E_ARG;
@@ -666,6 +674,7 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   p.S = w.s;
   p.Z = w.z;
   p.ldw = w.fmt == HXA_W_Q4 ? w.K / 2 : w.K;
+  p.wkt = wkt;
   p.M = g.M;
   p.N = w.N;
   p.Ktot = w.K;

@@ -38,6 +38,10 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st);
 
 // h[t][:] = f16(norm(x[t][:]) * mul + add); LN: (x-mu)*rsqrt(E[x^2]-mu^2+eps), RMS (w != NULL): x*rsqrt(E[x^2]+eps)
 // with mul = (1 + scale) (LN) or (1 + scale) * w (RMS), add = shift.
+// the same with the previous site's gated residual applied first: x += gate * t (fp16 t [T][ldt]), x written back
+int hxa_resid_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, long ldt, const float *gate,
+                              const float *shift, const float *scale, const float *w, float eps, hxa_h *h, long ldh,
+                              hipStream_t st);
 int hxa_norm_mod_launch(const float *x, long ldx, int T, int D, const float *shift, const float *scale, const float *w,
                         float eps, hxa_h *h, long ldh, hipStream_t st);
 // per-head RMSNorm * gain (+ RoPE on pairs (d, d+64)) in place for ntens tensors sharing a layout
@@ -77,3 +81,6 @@ int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t 
 
 // matrix shapes of a GPU block pack (see hxa_pack_layout); returns the matrix count
 int hxa_pack_mats(int kind, int D, int F, int DC, int fa, int fm, int *N, int *K, int *fmt);
+
+// read-only pass over [p, p + bytes): one 16-byte word every `stride` bytes, nblocks workgroups (warms the memory-side
+// cache with stride 16, only address translation with a page stride)

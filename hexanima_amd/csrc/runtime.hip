@@ -119,6 +119,10 @@ extern "C" int hxa_event_record(void *ev, void *stream) {
   HIPC(hipEventRecord((hipEvent_t)ev, S(stream)));
   return HXA_OK;
 }
+extern "C" int hxa_stream_wait_event(void *stream, void *ev) {
+  HIPC(hipStreamWaitEvent(S(stream), (hipEvent_t)ev, 0));
+  return HXA_OK;
+}
 extern "C" int hxa_event_elapsed_ms(void *a, void *b, float *ms) {
   HIPC(hipEventSynchronize((hipEvent_t)b));
   HIPC(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
@@ -143,7 +147,7 @@ static int gemm_common(const void *A, long lda, int M, int fmt, const void *w, c
                        int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx,
                        const float *gate, void *out_t, long ldo_t, int split_col, int bm, int bn, int nw, void *stream) {
   if (!A || !w) return fail(HXA_E_ARG, "gemm: null operand");
-  if (fmt < HXA_W_F16 || fmt > HXA_W_Q4) return fail(HXA_E_MODE, "gemm: format %d", fmt);
+  if ((fmt & ~HXA_W_KTILED) > HXA_W_Q4 || fmt < 0) return fail(HXA_E_MODE, "gemm: format %d", fmt);
   if (epi == HXA_EPI_RESADD || epi == HXA_EPI_RESADD_SPLIT2 ? (!x || !gate) : !out) return fail(HXA_E_ARG, "gemm: null output");
   HxaWeight wt{fmt, N, K, w, (const hxa_h *)s, (const hxa_h *)z};
   HxaGemm g{};
@@ -186,7 +190,7 @@ extern "C" int hxa_gemm_headnorm(const void *A, long lda, int M, int fmt, const 
                                  const float *gain0, const float *gain1, int gain_split, const float *cosT,
                                  const float *sinT, int ttab, void *stream) {
   if (!A || !w || !out) return fail(HXA_E_ARG, "gemm_headnorm: null pointer");
-  if (fmt < HXA_W_F16 || fmt > HXA_W_Q4) return fail(HXA_E_MODE, "gemm_headnorm: format %d", fmt);
+  if ((fmt & ~HXA_W_KTILED) > HXA_W_Q4 || fmt < 0) return fail(HXA_E_MODE, "gemm_headnorm: format %d", fmt);
   HxaWeight wt{fmt, N, K, w, (const hxa_h *)s, (const hxa_h *)z};
   HxaGemm g{};
   g.A = (const hxa_h *)A;
@@ -224,6 +228,14 @@ extern "C" int hxa_norm_mod(const float *x, long ldx, int T, int D, const float 
                             const float *w, float eps, void *h, long ldh, void *stream) {
   const int r = hxa_norm_mod_launch(x, ldx, T, D, shift, scale, w, eps, (hxa_h *)h, ldh, S(stream));
   if (r != HXA_OK) return fail(r, "norm_mod T=%d D=%d rejected", T, D);
+  return HXA_OK;
+}
+extern "C" int hxa_resadd_norm_mod(float *x, long ldx, int T, int D, const void *t, long ldt, const float *gate,
+                                   const float *shift, const float *scale, const float *w, float eps, void *h, long ldh,
+                                   void *stream) {
+  const int r = hxa_resid_norm_mod_launch(x, ldx, T, D, (const hxa_h *)t, ldt, gate, shift, scale, w, eps, (hxa_h *)h,
+                                          ldh, S(stream));
+  if (r != HXA_OK) return fail(r, "resadd_norm_mod T=%d D=%d rejected", T, D);
   return HXA_OK;
 }
 extern "C" int hxa_rmsrope(void *q0, void *q1, const float *g0, const float *g1, long ldq, int T, int H,
@@ -307,6 +319,28 @@ extern "C" long hxa_pack_layout(int kind, int D, int F, int DC, int fa, int fm, 
   off += al256(kind == 0 ? 4L * 4 * 128 : 4L * (256 + 2 * D));
   return off;
 }
+// Block packs store every matrix k-tiled (HXA_W_KTILED): the chunk of row n and k group g (64 bytes fp16, 32 q8,
+// 16 q4) moves from n * G * cb + g * cb to g * N * cb + n * cb, so each 32-deep k step of the matrix is contiguous.
+static int chunk_bytes(int fmt) { return fmt == HXA_W_F16 ? 64 : fmt == HXA_W_Q8 ? 32 : 16; }
+static void tile_matrix_host(const uint8_t *rm, uint8_t *kt, int N, int K, int fmt) {
+  const int cb = chunk_bytes(fmt), G = K / 32;
+  for (int n = 0; n < N; n++)
+    for (int g = 0; g < G; g++) memcpy(kt + ((size_t)g * N + n) * cb, rm + ((size_t)n * G + g) * cb, cb);
+}
+// host image of a pack whose matrices were written row-major -> the k-tiled pack (scales / vectors unchanged)
+static void tile_pack_host(std::vector<uint8_t> &host, int kind, int D, int F, int DC, int fa, int fm) {
+  int N[8], K[8], f[8];
+  const int n = hxa_pack_mats(kind, D, F, DC, fa, fm, N, K, f);
+  long offs[32];
+  hxa_pack_layout(kind, D, F, DC, fa, fm, offs, 32);
+  std::vector<uint8_t> tmp;
+  for (int i = 0; i < n; i++) {
+    const size_t bytes = (size_t)N[i] * K[i] / 32 * chunk_bytes(f[i]);
+    tmp.assign(host.begin() + offs[3 * i], host.begin() + offs[3 * i] + bytes);
+    tile_matrix_host(tmp.data(), host.data() + offs[3 * i], N[i], K[i], f[i]);
+  }
+}
+
 struct PackView {
   HxaWeight w[7];
   int nmat;
@@ -321,7 +355,7 @@ static PackView pack_view(const hxa_block_dims *d, const void *pack) {
   v.nmat = (int)mats.size();
   const char *b = (const char *)pack;
   for (int i = 0; i < v.nmat; i++) {
-    v.w[i] = HxaWeight{mats[i].fmt, mats[i].N, mats[i].K, b + offs[3 * i],
+    v.w[i] = HxaWeight{mats[i].fmt | HXA_W_KTILED, mats[i].N, mats[i].K, b + offs[3 * i],
                        offs[3 * i + 1] >= 0 ? (const hxa_h *)(b + offs[3 * i + 1]) : nullptr, nullptr};
   }
   v.vec = (const float *)(b + offs[3 * v.nmat]);
@@ -510,10 +544,14 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     STAGE_DONE();
     TRY(attn(qk, k, ldqk, vT, BT, T, T, (long)T * ldqk, T));
     STAGE_DONE();
-    TRY(gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
+    // gated residual x += gate * f16(o Wo) (blk.c:162): without a stage dump it is applied by the next site's LN
+    // kernel, which reads x anyway (same fma, so the same x); the projection is then a plain store into t1
+    TRY(fuse ? gemm(o, D, BT, Wo, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0)
+             : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 1: cross-attention (blk.c:163-169)
-    TRY(hxa_norm_mod_launch(x, D, BT, D, mod + 3 * D, mod + 4 * D, nullptr, 1e-6f, h, D, st));
+    TRY(hxa_resid_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, D, mod + 2 * D, mod + 3 * D, mod + 4 * D, nullptr,
+                                  1e-6f, h, D, st));
     STAGE_DONE();
     if (fuse) hn = HeadNorm{D, gain + 256, gain + 256, D, nullptr, nullptr};  // cross q: RMSNorm * gain (blk.c:166)
     TRY(gemm(h, D, BT, Wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0));
@@ -527,10 +565,12 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     STAGE_DONE();
     TRY(attn(qk, ck, D, cvT, BC, d->C, d->C, (long)d->C * D, d->C));
     STAGE_DONE();
-    TRY(gemm(o, D, BT, Wco, HXA_EPI_RESADD, nullptr, 0, x, mod + 5 * D, nullptr, 0, 0, 1, 0));
+    TRY(fuse ? gemm(o, D, BT, Wco, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0)
+             : gemm(o, D, BT, Wco, HXA_EPI_RESADD, nullptr, 0, x, mod + 5 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 2: MLP (blk.c:170-174)
-    TRY(hxa_norm_mod_launch(x, D, BT, D, mod + 6 * D, mod + 7 * D, nullptr, 1e-6f, h, D, st));
+    TRY(hxa_resid_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, D, mod + 5 * D, mod + 6 * D, mod + 7 * D, nullptr,
+                                  1e-6f, h, D, st));
     STAGE_DONE();
     TRY(gemm(h, D, BT, W1, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
@@ -548,10 +588,13 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     STAGE_DONE();
     TRY(attn(qk, k, ldqk, vT, BT, T, d->nvalid, (long)T * ldqk, T));
     STAGE_DONE();
-    TRY(gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
+    const bool fuse = stop == 0;  // residual deferred into the FFN's RMS-mod kernel (same fma) unless dumping stages
+    TRY(fuse ? gemm(o, D, BT, Wo, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0)
+             : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // FFN half (moss blk.c:248-259)
-    TRY(hxa_norm_mod_launch(x, D, BT, D, mod + 3 * D, mod + 4 * D, n2, 1e-6f, h, D, st));
+    TRY(hxa_resid_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, D, mod + 2 * D, mod + 3 * D, mod + 4 * D, n2, 1e-6f,
+                                  h, D, st));
     STAGE_DONE();
     TRY(gemm(h, D, BT, Wug, HXA_EPI_SITU, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
@@ -663,6 +706,7 @@ int build_anima_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
   }
   if (meta[M_GAIN] < 0 || (size_t)meta[M_GAIN] + 2048 > hb.bytes) return fail(HXA_E_WEIGHTS, "gain offset out of range");
   memcpy(host.data() + offs[21], (const uint8_t *)hb.ptr + meta[M_GAIN], 2048);
+  tile_pack_host(host, 0, D, F, DC, fmt, fmt);
   void *dev = nullptr;
   HIPC(hipMalloc(&dev, bytes));
   HIPC(hipMemcpy(dev, host.data(), bytes, hipMemcpyHostToDevice));
@@ -695,6 +739,7 @@ int build_moss_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
   q8rec_to_native(b + W_DN, D, F, F / 32 + 4, host.data() + offs[9], (uint16_t *)(host.data() + offs[10]), D);
   // gains: q/sqrt(128) [128], k [128], norm1 [3072], norm2 [3072] (export_moss.py gain vector)
   memcpy(host.data() + offs[12], b + W_GAIN, 4L * (256 + 2 * D));
+  tile_pack_host(host, 1, D, F, 0, fmt, fmt);
   void *dev = nullptr;
   HIPC(hipMalloc(&dev, bytes));
   HIPC(hipMemcpy(dev, host.data(), bytes, hipMemcpyHostToDevice));

@@ -18,6 +18,7 @@ SZ, U64 = C.c_size_t, C.c_uint64
 
 # constants of the C-ABI
 W_F16, W_Q8, W_Q4 = 0, 1, 2
+W_KTILED = 16  # OR'ed into a format: matrix stored k-tiled, [K/32][N][chunk]
 EPI_STORE, EPI_GELU_TANH, EPI_GELU_ERF, EPI_RESADD, EPI_STORE_T, EPI_SITU, EPI_PARTIAL, EPI_RESADD_SPLIT2 = range(8)
 KIND_WEIGHTS_ANIMA, KIND_BLOB, KIND_WEIGHTS_MOSS = 0, 1, 2
 E_NAMES = {0: "OK", -1: "RESOURCE", -2: "LOCK", -5: "WEIGHTS", -6: "NOBLOB", -7: "BLOB", -10: "META", -11: "MODE",
@@ -63,9 +64,11 @@ _SIGS = {
     "hxa_event_create": (I, [C.POINTER(P)]),
     "hxa_event_destroy": (I, [P]),
     "hxa_event_record": (I, [P, P]),
+    "hxa_stream_wait_event": (I, [P, P]),
     "hxa_event_elapsed_ms": (I, [P, P, C.POINTER(F)]),
     "hxa_device_info": (I, [C.POINTER(I), C.POINTER(I), C.POINTER(SZ), C.c_char_p, I]),
     "hxa_gemm": (I, [P, L, I, I, P, P, P, I, I, I, I, P, L, L, P, L, P, P, L, I, P]),
+    "hxa_resadd_norm_mod": (I, [P, L, I, I, P, L, P, P, P, P, F, P, L, P]),
     "hxa_gemm_headnorm": (I, [P, L, I, I, P, P, P, I, I, P, L, P, L, I, I, P, P, I, P, P, I, P]),
     "hxa_gemm_tile": (I, [P, L, I, I, P, P, P, I, I, I, I, P, L, L, P, L, P, I, I, I, P]),
     "hxa_attention": (I, [P, L, P, L, P, L, P, L, I, I, I, I, I, L, L, L, L, P]),
@@ -208,9 +211,21 @@ def pack_shapes(kind: int, D: int, F: int, DC: int):
     return [(3 * D, D), (D, D), (2 * F, D), (D, F)]
 
 
+def ktile(rows: np.ndarray, N: int, K: int) -> np.ndarray:
+    """Bytes of a row-major weight matrix with N rows of 32-deep k groups -> the k-tiled order
+    [K/32][N][chunk] (chunk = 64 bytes fp16, 32 q8, 16 q4)."""
+    return np.ascontiguousarray(rows.reshape(N, K // 32, -1).transpose(1, 0, 2)).reshape(-1)
+
+
+def unktile(tiled: np.ndarray, N: int, K: int) -> np.ndarray:
+    """Inverse of ktile: k-tiled bytes -> row-major bytes [N][...]."""
+    return np.ascontiguousarray(tiled.reshape(K // 32, N, -1).transpose(1, 0, 2)).reshape(-1)
+
+
 def build_pack(kind: int, D: int, F: int, DC: int, fmt_attn: int, fmt_mlp: int, mats, vec: np.ndarray) -> np.ndarray:
     """Host image of a GPU block pack. mats: per matrix either an fp16 [N][K] array (F16) or a (q, s) pair
-    (q8: int8 [N][K]; q4: uint8 [N][K/2]; s: fp16 bits [K/32][N]). vec: the fp32 vector section."""
+    (q8: int8 [N][K]; q4: uint8 [N][K/2]; s: fp16 bits [K/32][N]). vec: the fp32 vector section. The matrices
+    are stored k-tiled, the pack layout the block runner reads."""
     total, offs, voff = pack_layout(kind, D, F, DC, fmt_attn, fmt_mlp)
     buf = np.zeros(total, np.uint8)
     shapes = pack_shapes(kind, D, F, DC)
@@ -220,13 +235,13 @@ def build_pack(kind: int, D: int, F: int, DC: int, fmt_attn: int, fmt_mlp: int, 
         if fmt == W_F16:
             a = np.ascontiguousarray(m).view(np.uint8).reshape(-1)
             assert a.size == N * K * 2
-            buf[woff:woff + a.size] = a
+            buf[woff:woff + a.size] = ktile(a, N, K)
         else:
             q, s = m
             qa = np.ascontiguousarray(q).view(np.uint8).reshape(-1)
             sa = np.ascontiguousarray(s).view(np.uint8).reshape(-1)
             assert qa.size == (N * K if fmt == W_Q8 else N * K // 2) and sa.size == (K // 32) * N * 2
-            buf[woff:woff + qa.size] = qa
+            buf[woff:woff + qa.size] = ktile(qa, N, K)
             buf[soff:soff + sa.size] = sa
     v = np.ascontiguousarray(vec, np.float32).view(np.uint8).reshape(-1)
     buf[voff:voff + v.size] = v

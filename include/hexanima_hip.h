@@ -82,6 +82,7 @@ int hxa_stream_sync(void *stream);
 int hxa_event_create(void **ev);
 int hxa_event_destroy(void *ev);
 int hxa_event_record(void *ev, void *stream);
+int hxa_stream_wait_event(void *stream, void *ev); /* later work on stream waits for ev */
 int hxa_event_elapsed_ms(void *start, void *stop, float *ms);
 int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, char *name, int name_len);
 
@@ -90,6 +91,8 @@ int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, char *name, 
  * ============================================================================================================ */
 #define HXA_W_F16 0 /* w [N][K] fp16 */
 #define HXA_W_Q8 1  /* q [N][K] int8, s [K/32][N] fp16; value f16(q*s) */
+#define HXA_W_KTILED 16 /* OR'ed into a format: weights stored k-tiled, [K/32][N][32 values] (q4: 16 bytes per row and
+                           tile); each 32-deep k step of the whole matrix is contiguous in memory (scales unchanged) */
 #define HXA_W_Q4 2  /* q [N][K/2] (k0+2j at bits 4j, k0+2j+1 at bits 16+4j of each 32-bit word; nibble = q+8),
                        s [K/32][N] fp16, optional z [K/32][N]: value f16(nibble*s + z), z NULL: f16((nibble-8)*s) */
 #define HXA_EPI_STORE 0
@@ -131,6 +134,10 @@ int hxa_attention(const void *q, long ldq, const void *k, long ldk, const void *
 /* h = f16(norm(x) * (1 + scale) [* w] + shift); LN when w == NULL (kern.c:38-65), RMS otherwise (moss kern.c:353) */
 int hxa_norm_mod(const float *x, long ldx, int T, int D, const float *shift, const float *scale, const float *w,
                  float eps, void *h, long ldh, void *stream);
+/* the same after applying the previous site's gated residual, x += gate * t (kern.c:320-328; t fp16 [T][ldt]),
+ * with x written back: one pass over x for the residual and the next site's norm */
+int hxa_resadd_norm_mod(float *x, long ldx, int T, int D, const void *t, long ldt, const float *gate, const float *shift,
+                        const float *scale, const float *w, float eps, void *h, long ldh, void *stream);
 /* per-head RMSNorm * gain (+ RoPE when cosT != NULL) in place on q0 (and q1 when not NULL) (kern.c:163-197);
  * cos/sin [ttab][64], row t % ttab */
 int hxa_rmsrope(void *q0, void *q1, const float *g0, const float *g1, long ldq, int T, int H, const float *cosT,
@@ -142,7 +149,8 @@ int hxa_resadd2(float *x, long ldx, const void *t1, const void *t2, long ldt, in
 int hxa_fill_normal(void *dst, int dtype, size_t n, uint64_t seed, float mean, float std, void *stream);
 int hxa_fill_uniform_int(void *dst, int bits, size_t n, uint64_t seed, int lo, int hi, void *stream);
 int hxa_fill_const(void *dst, int dtype, size_t n, float v, void *stream);
-/* q8 / q4 quantisation of fp32 W[N][K] (export_all.py:10-18 semantics, group 32, fp16 scales) */
+/* q8 / q4 quantisation of fp32 W[N][K] (export_all.py:10-18 semantics, group 32, fp16 scales); fmt may carry
+ * HXA_W_KTILED to write q k-tiled */
 int hxa_quantize(const float *W, int N, int K, int fmt, void *q, void *s, void *stream);
 /* crouton <-> row-major conversions (kern.h:5-8) */
 int hxa_x32_to_rows(const float *tiles, float *x, int R, int C, void *stream);
@@ -152,7 +160,8 @@ int hxa_rows_to_x32(const float *x, float *tiles, int R, int C, void *stream);
  * 4. GPU block packs and the device-level block (weights resident in HBM)
  * ============================================================================================================ */
 /* A pack is one device allocation holding every weight of one block in the GPU layouts above, at offsets
- * given by hxa_pack_layout (each matrix: w, then s, then z, 256-byte aligned).
+ * given by hxa_pack_layout (each matrix: w, then s, then z, 256-byte aligned). Every matrix w of a pack is stored
+ * k-tiled (HXA_W_KTILED): [K/32][N][32 values] (q4: [K/32][N][16 bytes]).
  * kind 0 (Anima structure): matrices qkv [3D][D], o [D][D], cq [D][D], ckv [2D][DC], co [D][D], w1 [F][D],
  *   w2 [D][F], then gain fp32 [4][128] (q/sqrt(128), k, cross q/sqrt(128), cross k).
  * kind 1 (MOSS structure): qkv [3D][D], o [D][D], ug [2F][D] (rows interleaved per 32: up_j, gate_j),

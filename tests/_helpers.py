@@ -4,6 +4,7 @@ and an oracle-composed DiT step (the caller-side glue of phone/animad.cpp:424-49
 import numpy as np
 
 from oracle import hxo
+from hexanima_amd import hip
 
 
 def f16(a):
@@ -36,7 +37,8 @@ def ulp_diff(a16, b16):
 
 
 def unpack_weights(pack: np.ndarray, kind: int, D: int, F: int, DC: int, fmt_attn: int, fmt_mlp: int, layout):
-    """GPU pack image -> dict of fp16 (uint16) W[N][K] matrices (dequantised) and the fp32 vector section."""
+    """GPU pack image (k-tiled matrices) -> dict of fp16 (uint16) W[N][K] matrices (dequantised) and the fp32
+    vector section."""
     total, offs, voff = layout
     shapes = ([(3 * D, D), (D, D), (D, D), (2 * D, DC), (D, D), (F, D), (D, F)] if kind == 0
               else [(3 * D, D), (D, D), (2 * F, D), (D, F)])
@@ -44,14 +46,14 @@ def unpack_weights(pack: np.ndarray, kind: int, D: int, F: int, DC: int, fmt_att
     for i, ((N, K), (wo, so)) in enumerate(zip(shapes, offs)):
         fmt = fmt_attn if i < (5 if kind == 0 else 2) else fmt_mlp
         if fmt == 0:
-            mats.append(pack[wo:wo + N * K * 2].view(np.uint16).reshape(N, K).copy())
+            mats.append(hip.unktile(pack[wo:wo + N * K * 2], N, K).view(np.uint16).reshape(N, K).copy())
         else:
             s = pack[so:so + (K // 32) * N * 2].view(np.uint16).reshape(K // 32, N).copy()
             if fmt == 1:
-                q = pack[wo:wo + N * K].view(np.int8).reshape(N, K).copy()
+                q = hip.unktile(pack[wo:wo + N * K], N, K).view(np.int8).reshape(N, K).copy()
                 mats.append(hxo.q8_dequant(q, s))
             else:
-                q = pack[wo:wo + N * K // 2].reshape(N, K // 2).copy()
+                q = hip.unktile(pack[wo:wo + N * K // 2], N, K).reshape(N, K // 2).copy()
                 mats.append(hxo.q4_dequant(q, s))
     if kind == 0:
         qkv, wo_, wcq, ckv, wco, w1, w2 = mats

@@ -49,6 +49,19 @@ def test_pack_layout_matches_reference_matrix_bytes(hip):
     assert all(s >= 0 for _, s in m4)
 
 
+@pytest.mark.parametrize("cb", [64, 32, 16])
+def test_ktile_places_each_row_chunk_at_its_k_step(hip, cb):
+    """The block-pack matrix order: the chunk of row n and k group g (64 B fp16, 32 B q8, 16 B q4) sits at
+    (g * N + n) * chunk, so one 32-deep k step of all N rows is one contiguous slice; unktile inverts it."""
+    N, K = 40, 96
+    rm = np.random.default_rng(2).integers(0, 256, N * (K // 32) * cb, dtype=np.uint8)
+    kt = hip.ktile(rm, N, K)
+    for n in (0, 7, N - 1):
+        for g in range(K // 32):
+            assert np.array_equal(kt[(g * N + n) * cb:(g * N + n + 1) * cb], rm[(n * (K // 32) + g) * cb:][:cb])
+    assert np.array_equal(hip.unktile(kt, N, K), rm)
+
+
 def test_ws_bytes_and_init_without_gpu(hip):
     d = hip.BlockDims(0, 2048, 16, 8192, 256, 1024, 1536, 1, 1536, 0, 0, 1)
     # h, q|k, v^T, o, two split-K partials (fp16, 7 x [T][D] in total) + the MLP hidden [T][F] + cross k / v^T

@@ -162,6 +162,32 @@ def test_gemm_resadd_split2_matches_partial_then_resadd2(fmt, tile):
     assert bad == -12
 
 
+@pytest.mark.parametrize("fmt,tile,epi,ksplit", [(0, None, 0, 1), (0, (192, 256, 8), 0, 1), (0, (64, 128), 0, 1),
+                                                (0, None, 6, 2), (1, None, 0, 1), (1, (128, 64), 0, 1), (2, None, 0, 1),
+                                                (2, None, 6, 2), (0, None, 7, 1), (1, None, 3, 1)])
+def test_gemm_ktiled_weights_equal_row_major(fmt, tile, epi, ksplit):
+    """W stored k-tiled ([K/32][N][chunk], the block-pack layout) gives the same bits as W row-major, for every
+    format, tile family and split-K form; N is ragged against the 256-wide tiles."""
+    hip = _hip()
+    say(f"gemm k-tiled fmt={fmt} tile={tile} epi={epi} ksplit={ksplit}")
+    rng = np.random.default_rng(31)
+    M, N, K = 320, 416, 1024
+    A = f16(rng.standard_normal((M, K)))
+    if fmt == 0:
+        w, s = f16(rng.standard_normal((N, K)) * 0.05), None
+    else:
+        wf = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+        w, s = hxo.q8_quantize(wf) if fmt == 1 else hxo.q4_quantize(wf)
+    wt = hip.ktile(np.ascontiguousarray(w).view(np.uint8).reshape(-1), N, K)
+    assert np.array_equal(hip.unktile(wt, N, K), np.ascontiguousarray(w).view(np.uint8).reshape(-1))
+    x = rng.standard_normal((M, N)).astype(np.float32)
+    g = rng.standard_normal(N).astype(np.float32)
+    kw = dict(epi=epi, ksplit=ksplit, tile=tile, x=x, gate=g)
+    ref = _run_gemm(hip, A, fmt, w, s, N, K, **kw)
+    got = _run_gemm(hip, A, fmt | hip.W_KTILED, wt, s, N, K, **kw)
+    assert np.array_equal(got.view(np.uint8), ref.view(np.uint8))
+
+
 def _run_gemm_rc(hip, A, N, K, epi, x, g):
     dA = hip.DeviceArray.from_numpy(f16(A))
     dW = hip.DeviceArray((N, K), np.float16)
@@ -335,6 +361,33 @@ def test_rmsrope(rope):
     assert ulp_diff(dq.numpy(), ref).max() <= 1
 
 
+@pytest.mark.parametrize("rms", [False, True])
+def test_resadd_norm_mod_equals_resadd_then_norm(rms):
+    """The previous site's gated residual applied inside the next site's norm kernel equals the residual update
+    followed by the norm, bit for bit (x and h)."""
+    hip = _hip()
+    say(f"resadd + norm_mod rms={rms}")
+    rng = np.random.default_rng(13)
+    T, D = 96, 2048
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    t = f16(rng.standard_normal((T, D)))
+    g, sh, sc = (rng.standard_normal(D).astype(np.float32) * 0.5 for _ in range(3))
+    w = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    dx1, dx2 = hip.DeviceArray.from_numpy(x), hip.DeviceArray.from_numpy(x)
+    dt, dz = hip.DeviceArray.from_numpy(t), hip.DeviceArray((T, D), np.float16, zero=True)
+    dg, dsh, dsc, dw = (hip.DeviceArray.from_numpy(a) for a in (g, sh, sc, w))
+    h1, h2 = hip.DeviceArray((T, D), np.float16), hip.DeviceArray((T, D), np.float16)
+    wp = dw.ptr if rms else None
+    hip.check(hip.lib().hxa_resadd_norm_mod(dx1.ptr, D, T, D, dt.ptr, D, dg.ptr, dsh.ptr, dsc.ptr, wp, 1e-6, h1.ptr, D, None),
+              "resadd_norm_mod")
+    hip.check(hip.lib().hxa_resadd2(dx2.ptr, D, dt.ptr, dz.ptr, D, T, D, dg.ptr, None), "resadd2")
+    hip.check(hip.lib().hxa_norm_mod(dx2.ptr, D, T, D, dsh.ptr, dsc.ptr, wp, 1e-6, h2.ptr, D, None), "norm_mod")
+    hip.sync()
+    assert np.array_equal(dx1.numpy().view(np.uint32), dx2.numpy().view(np.uint32))
+    assert np.array_equal(h1.numpy().view(np.uint16), h2.numpy().view(np.uint16))
+    assert np.array_equal(dx1.numpy(), hxo.resadd(x, t, g))
+
+
 def test_resadd2_and_tile_conversions():
     hip = _hip()
     say("resadd2 + x32 conversions")
@@ -371,3 +424,8 @@ def test_quantize_matches_oracle():
         hip.check(hip.lib().hxa_quantize(dW.ptr, N, K, fmt, q.ptr, s.ptr, None), "quantize")
         hip.sync()
         assert np.array_equal(s.numpy(), so) and np.array_equal(q.numpy(), qo)
+        # k-tiled output: the same bytes in [K/32][N][chunk] order, scales unchanged
+        hip.check(hip.lib().hxa_quantize(dW.ptr, N, K, fmt | hip.W_KTILED, q.ptr, s.ptr, None), "quantize k-tiled")
+        hip.sync()
+        assert np.array_equal(s.numpy(), so)
+        assert np.array_equal(q.numpy().view(np.uint8).reshape(-1), hip.ktile(qo.view(np.uint8).reshape(-1), N, K))
