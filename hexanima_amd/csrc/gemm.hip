@@ -30,8 +30,9 @@ struct GemmParams {
   long lda;
   const void *W;
   const hxa_h *S, *Z;
-  long ldw;  // elements per W row (fp16/int8: K; int4: bytes per row = K/2); row-major layout only
-  int wkt;   // 1: W k-tiled, [K/32][N][32 elements] (q4: [K/32][N][16 bytes])
+  // W element (fp16 / int8; q4: byte) offset of row n, k group g: n * w_rs + g * w_gs. Row-major [N][K]: w_rs = K
+  // (q4: K/2), w_gs = 32 (16); k-tiled [K/32][N][32] (q4: [K/32][N][16 bytes]): w_rs = 32 (16), w_gs = 32 N (16 N)
+  long w_rs, w_gs;
   int M, N, Kslice, Ktot;
   int epi;
   hxa_h *out;
@@ -230,20 +231,17 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
       if (G::TW % NW == 0 || t < G::TW) {
         const int chunk = t * 64 + lane;
         if ((G::W_BYTES / 16) % 64 == 0 || chunk < G::W_BYTES / 16) {
-          // W row n, k tile k0: row-major [N][K] (n ldw + k0), or k-tiled [K/32][N][32] (k0 N + 32 n: one step's
-          // slice of the whole matrix is contiguous)
+          // W row n, k group k0/32: one strided address form covers both layouts (no branch in the loop)
+          const long og = (long)(k0 >> 5) * p.w_gs;
           if (FMT == HXA_W_F16) {
             const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3), n = min(n0 + row, p.N - 1);
-            const long o = p.wkt ? (long)k0 * p.N + n * 32L : (long)n * p.ldw + k0;
-            g2l16_opaque((const hxa_h *)p.W + o + cl * 8, ws + t * 1024);
+            g2l16_opaque((const hxa_h *)p.W + n * p.w_rs + og + cl * 8, ws + t * 1024);
           } else if (FMT == HXA_W_Q8) {
             const int row = chunk >> 1, cl = (chunk & 1) ^ ((row >> 3) & 1), n = min(n0 + row, p.N - 1);
-            const long o = p.wkt ? (long)k0 * p.N + n * 32L : (long)n * p.ldw + k0;
-            g2l16_opaque((const int8_t *)p.W + o + cl * 16, ws + t * 1024);
+            g2l16_opaque((const int8_t *)p.W + n * p.w_rs + og + cl * 16, ws + t * 1024);
           } else {
             const int row = chunk, n = min(n0 + row, p.N - 1);
-            const long o = p.wkt ? (long)(k0 >> 1) * p.N + n * 16L : (long)n * p.ldw + (k0 >> 1);
-            g2l16_opaque((const uint8_t *)p.W + o, ws + t * 1024);
+            g2l16_opaque((const uint8_t *)p.W + n * p.w_rs + og, ws + t * 1024);
           }
         }
       }
@@ -673,8 +671,11 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   p.W = w.w;
   p.S = w.s;
   p.Z = w.z;
-  p.ldw = w.fmt == HXA_W_Q4 ? w.K / 2 : w.K;
-  p.wkt = wkt;
+  {
+    const long cb = w.fmt == HXA_W_Q4 ? 16 : 32;  // elements (q4: bytes) of one row's k group
+    p.w_rs = wkt ? cb : (long)w.K / 32 * cb;
+    p.w_gs = wkt ? cb * w.N : cb;
+  }
   p.M = g.M;
   p.N = w.N;
   p.Ktot = w.K;
