@@ -34,46 +34,59 @@ STEP_FLOPS = NBLK * BLOCK_FLOPS + 2 * T * 64 * D + 2 * T * D * 64
 UP_FLOPS = 2 * T * D * F
 
 
+def _event(L, hip):
+    p = C.c_void_p()
+    hip.check(L.hxa_event_create(C.byref(p)), "event")
+    return p
+
+
+def dit_ms(bd, nblk, lat_shape, ctx_shape, tin, steps, warmup, seed, wall_check=False):
+    """ms per graph-replayed Euler step of a DiT (hxa_dit_*), sigma schedule 1.0, 0.75, 0.5, 0.25 -> 0 cycled.
+    lat_shape = (batch, C, H, W); ctx_shape = (batch, tokens, width). The latent must stay finite."""
+    from hexanima_amd import hip
+    L = hip.lib()
+    cfg = hip.DitCfg(bd, nblk, lat_shape[1], lat_shape[2], lat_shape[3], 256, tin)
+    dit = C.c_void_p()
+    hip.check(L.hxa_dit_create(C.byref(cfg), seed, C.byref(dit)), "dit_create")
+    try:
+        rng = np.random.default_rng(seed)
+        lat = rng.standard_normal(lat_shape).astype(np.float32)
+        ctx = rng.standard_normal(ctx_shape).astype(np.float32)
+        hip.check(L.hxa_dit_set_inputs(dit, lat.ctypes.data, ctx.ctypes.data), "set_inputs")
+        st = L.hxa_dit_stream(dit)
+        sig = [1.0, 0.75, 0.5, 0.25, 0.0]
+        e0, e1 = _event(L, hip), _event(L, hip)
+        for i in range(warmup):
+            hip.check(L.hxa_dit_step(dit, sig[i % 4], sig[i % 4 + 1], 1), "step")
+        hip.check(L.hxa_stream_sync(st), "sync")
+        t0 = time.perf_counter()
+        hip.check(L.hxa_event_record(e0, st), "rec")
+        for i in range(steps):
+            hip.check(L.hxa_dit_step(dit, sig[i % 4], sig[i % 4 + 1], 1), "step")
+        hip.check(L.hxa_event_record(e1, st), "rec")
+        hip.check(L.hxa_stream_sync(st), "sync")
+        wall = time.perf_counter() - t0
+        ms = C.c_float()
+        hip.check(L.hxa_event_elapsed_ms(e0, e1, C.byref(ms)), "elapsed")
+        out = np.zeros_like(lat)
+        hip.check(L.hxa_dit_get_latent(dit, out.ctypes.data), "latent")
+        if not np.isfinite(out).all():
+            raise RuntimeError("non-finite latent")
+        for e in (e0, e1):
+            L.hxa_event_destroy(e)
+    finally:
+        L.hxa_dit_destroy(dit)
+    # the event interval, or the host wall clock when that is longer (nothing hidden outside the events)
+    return (max(ms.value, wall * 1e3) if wall_check else ms.value) / steps
+
+
 def gpu_run(steps, warmup):
     from hexanima_amd import hip
     hip.init(0)
     L = hip.lib()
     info = hip.device_info()
     bd = hip.BlockDims(0, D, H, F, C_TXT, DC, 0, 1, 0, hip.W_F16, hip.W_F16, 1)
-    cfg = hip.DitCfg(bd, NBLK, LAT[0], LAT[1], LAT[2], 256, 0)
-    dit = C.c_void_p()
-    hip.check(L.hxa_dit_create(C.byref(cfg), 2024, C.byref(dit)), "dit_create")
-    rng = np.random.default_rng(1)
-    lat = rng.standard_normal((1,) + LAT).astype(np.float32)
-    ctx = rng.standard_normal((1, C_TXT, DC)).astype(np.float32)
-    hip.check(L.hxa_dit_set_inputs(dit, lat.ctypes.data, ctx.ctypes.data), "set_inputs")
-    st = L.hxa_dit_stream(dit)
-    sig = [1.0, 0.75, 0.5, 0.25, 0.0]
-
-    def ev():
-        p = C.c_void_p()
-        hip.check(L.hxa_event_create(C.byref(p)), "event")
-        return p
-
-    e0, e1 = ev(), ev()
-    for i in range(warmup):
-        hip.check(L.hxa_dit_step(dit, sig[i % 4], sig[i % 4 + 1], 1), "step")
-    hip.check(L.hxa_stream_sync(st), "sync")
-    t0 = time.perf_counter()
-    hip.check(L.hxa_event_record(e0, st), "rec")
-    for i in range(steps):
-        hip.check(L.hxa_dit_step(dit, sig[i % 4], sig[i % 4 + 1], 1), "step")
-    hip.check(L.hxa_event_record(e1, st), "rec")
-    hip.check(L.hxa_stream_sync(st), "sync")
-    wall = time.perf_counter() - t0
-    ms = C.c_float()
-    hip.check(L.hxa_event_elapsed_ms(e0, e1, C.byref(ms)), "elapsed")
-    ms_step = max(ms.value, wall * 1e3) / steps
-    out = np.zeros_like(lat)
-    hip.check(L.hxa_dit_get_latent(dit, out.ctypes.data), "latent")
-    if not np.isfinite(out).all():
-        raise RuntimeError("non-finite latent")
-    L.hxa_dit_destroy(dit)
+    ms_step = dit_ms(bd, NBLK, (1,) + LAT, (1, C_TXT, DC), 0, steps, warmup, 2024, wall_check=True)
 
     # dominant kernel: MLP up-projection GEMM with the GELU epilogue (one launch per block per step)
     s = C.c_void_p()
@@ -87,58 +100,146 @@ def gpu_run(steps, warmup):
     def up():
         hip.check(L.hxa_gemm(A.ptr, D, T, WFMT, W.ptr, None, None, F, D, 1, hip.EPI_GELU_TANH, O.ptr, F, 0, None, 0,
                              None, None, 0, 0, s), "gemm")
-    for _ in range(5):
-        up()
-    reps = 50
-    hip.check(L.hxa_event_record(e0, s), "rec")
-    for _ in range(reps):
-        up()
-    hip.check(L.hxa_event_record(e1, s), "rec")
-    hip.check(L.hxa_event_elapsed_ms(e0, e1, C.byref(ms)), "elapsed")
-    up_ms = ms.value / reps
+    up_ms = _time_launches(L, hip, up, s, reps=50)
     L.hxa_stream_destroy(s)
     return info, ms_step, up_ms
 
 
-def q8_dit_run(steps=10, warmup=2):
-    """The 2.9B-class q8 DiT step (28 blocks, hidden 2560, 20 heads, MLP 10240, every block linear int8 with fp16
-    group-32 scales; norms and modulation fp16), same latent / text shapes: ms per graph-replayed Euler step."""
-    from hexanima_amd import hip
-    L = hip.lib()
-    Dq, Hq, Fq = 2560, 20, 10240
-    bd = hip.BlockDims(0, Dq, Hq, Fq, C_TXT, DC, 0, 1, 0, hip.W_Q8, hip.W_Q8, 1)
-    cfg = hip.DitCfg(bd, NBLK, LAT[0], LAT[1], LAT[2], 256, 0)
-    dit = C.c_void_p()
-    hip.check(L.hxa_dit_create(C.byref(cfg), 2025, C.byref(dit)), "dit_create q8")
-    rng = np.random.default_rng(2)
-    lat = rng.standard_normal((1,) + LAT).astype(np.float32)
-    ctx = rng.standard_normal((1, C_TXT, DC)).astype(np.float32)
-    hip.check(L.hxa_dit_set_inputs(dit, lat.ctypes.data, ctx.ctypes.data), "set_inputs q8")
-    st = L.hxa_dit_stream(dit)
-    sig = [1.0, 0.75, 0.5, 0.25, 0.0]
-    e0, e1 = C.c_void_p(), C.c_void_p()
-    hip.check(L.hxa_event_create(C.byref(e0)), "event")
-    hip.check(L.hxa_event_create(C.byref(e1)), "event")
-    for i in range(warmup):
-        hip.check(L.hxa_dit_step(dit, sig[i % 4], sig[i % 4 + 1], 1), "step q8")
-    hip.check(L.hxa_event_record(e0, st), "rec")
-    for i in range(steps):
-        hip.check(L.hxa_dit_step(dit, sig[i % 4], sig[i % 4 + 1], 1), "step q8")
-    hip.check(L.hxa_event_record(e1, st), "rec")
-    hip.check(L.hxa_stream_sync(st), "sync")
+def _time_launches(L, hip, fn, s, reps=20, warm=5):
+    """average ms per call of fn (launches on stream s), HIP events on s"""
+    e0, e1 = _event(L, hip), _event(L, hip)
+    for _ in range(warm):
+        fn()
+    hip.check(L.hxa_event_record(e0, s), "rec")
+    for _ in range(reps):
+        fn()
+    hip.check(L.hxa_event_record(e1, s), "rec")
+    hip.check(L.hxa_stream_sync(s), "sync")
     ms = C.c_float()
     hip.check(L.hxa_event_elapsed_ms(e0, e1, C.byref(ms)), "elapsed")
-    out = np.zeros_like(lat)
-    hip.check(L.hxa_dit_get_latent(dit, out.ctypes.data), "latent q8")
-    L.hxa_dit_destroy(dit)
-    if not np.isfinite(out).all():
-        raise RuntimeError("non-finite q8 latent")
+    for e in (e0, e1):
+        L.hxa_event_destroy(e)
+    return ms.value / reps
+
+
+def _rate(flops, ms):
+    tf = flops / (ms * 1e-3)
+    return {"us": round(ms * 1e3, 2), "tflops": round(tf / 1e12, 1), "frac_of_fp16_peak": round(tf / PEAK_FP16, 4)}
+
+
+def extra_dits():
+    """The other DiT workloads: the 2B fp16 DiT at batch 4, the 2.9B-class q8 DiT and the MOSS-class q8/q4 DiT
+    (36 blocks, hidden 3072, 24 heads, MLP 12288 SiTU-gated, int8 attention / int4 MLP weights, joint attention
+    over 6144 image + 512 text tokens of width 4096 projected to 3072), each as ms per graph-replayed Euler step."""
+    from hexanima_amd import hip
+    out = {}
+    # 2B fp16, batch 4 (the flops scale with the batch)
+    bd = hip.BlockDims(0, D, H, F, C_TXT, DC, 0, 4, 0, hip.W_F16, hip.W_F16, 1)
+    ms = dit_ms(bd, NBLK, (4,) + LAT, (4, C_TXT, DC), 0, 6, 1, 2026)
+    out["fp16_2b_dit_batch4"] = {"images_per_s": round(4000.0 / ms, 2), "ms_per_step": round(ms, 3),
+                                 "step_tflops": round(4 * STEP_FLOPS / (ms * 1e-3) / 1e12, 1),
+                                 "config": "28 blocks, hidden 2048, batch 4 x 1536 tokens, fp16"}
+    # 2.9B-class q8
+    Dq, Hq, Fq = 2560, 20, 10240
+    bd = hip.BlockDims(0, Dq, Hq, Fq, C_TXT, DC, 0, 1, 0, hip.W_Q8, hip.W_Q8, 1)
+    ms = dit_ms(bd, NBLK, (1,) + LAT, (1, C_TXT, DC), 0, 10, 2, 2025)
     blk = 2 * T * Dq * (3 * Dq) + 3 * 2 * T * Dq * Dq + 2 * C_TXT * DC * 2 * Dq + 2 * 2 * T * Dq * Fq \
         + 4 * T * T * Dq + 4 * T * C_TXT * Dq
-    ms_step = ms.value / steps
-    return {"steps_per_s": round(1000.0 / ms_step, 3), "ms_per_step": round(ms_step, 4),
-            "step_tflops": round(NBLK * blk / (ms_step * 1e-3) / 1e12, 1),
-            "config": "28 blocks, hidden 2560, 20 heads, MLP 10240, int8 g32 block linears, 1536 image + 256 text tokens"}
+    out["q8_2p9b_dit"] = {"steps_per_s": round(1000.0 / ms, 3), "ms_per_step": round(ms, 4),
+                          "step_tflops": round(NBLK * blk / (ms * 1e-3) / 1e12, 1),
+                          "config": "28 blocks, hidden 2560, 20 heads, MLP 10240, int8 g32 block linears, "
+                                    "1536 image + 256 text tokens"}
+    # MOSS-class: latent 32 x 128 x 192 -> 64 x 96 patch grid = 6144 image tokens, + 512 text tokens
+    Dm, Hm, Fm, NBm, NTXT, TIN = 3072, 24, 12288, 36, 512, 4096
+    bd = hip.BlockDims(1, Dm, Hm, Fm, NTXT, 0, 0, 1, 0, hip.W_Q8, hip.W_Q4, 1)
+    ms = dit_ms(bd, NBm, (1, 32, 128, 192), (1, NTXT, TIN), TIN, 3, 1, 2027)
+    Tm = 6144 + NTXT
+    blk = 2 * Tm * Dm * 4 * Dm + 2 * Tm * Dm * 2 * Fm + 2 * Tm * Fm * Dm + 4 * Tm * Tm * Dm
+    out["moss_5b_dit"] = {"steps_per_s": round(1000.0 / ms, 3), "ms_per_step": round(ms, 2),
+                          "step_tflops": round(NBm * blk / (ms * 1e-3) / 1e12, 1),
+                          "step_frac_of_fp16_peak": round(NBm * blk / (ms * 1e-3) / PEAK_FP16, 4),
+                          "config": "36 blocks, hidden 3072, 24 heads, MLP 12288 SiTU, int8 attention / int4 MLP "
+                                    "g32, joint attention 6144 image + 512 text tokens"}
+    return out
+
+
+def microbench():
+    """Kernel-level figures on the benchmark shapes (HIP events, inputs resident in HBM):
+    - W8A16 / W4A16 linears at M = 1536 (K x N = 2048 x 6144, 2048 x 2048, 2048 x 8192, 8192 x 2048; int8 uniform in
+      [-127, 127] / int4 uniform in [-8, 7], group-32 fp16 scales 0.02/127, pack layout), beside fp16 weights;
+    - attention: the 2B block's self (1536 x 1536, 16 heads) and cross (1536 x 256) attention, and the MOSS-class
+      joint attention (6656 x 6656, 24 heads);
+    - one 2B fp16 block (hxa_block_run, 1536 tokens), the block latency."""
+    from hexanima_amd import hip
+    L = hip.lib()
+    s = C.c_void_p()
+    hip.check(L.hxa_stream_create(C.byref(s)), "stream")
+    res = {"linear_m1536": {}, "attention": {}}
+    M = T
+    A = hip.DeviceArray((M, 8192), np.float16)
+    hip.check(L.hxa_fill_normal(A.ptr, 1, M * 8192, 21, 0.0, 1.0, s), "fill")
+    Wb = hip.DeviceArray((8192 * 8192 * 2,), np.uint8)
+    Sb = hip.DeviceArray((256 * 8192,), np.float16)
+    O = hip.DeviceArray((M, 8192), np.float16)
+    hip.check(L.hxa_fill_const(Sb.ptr, 1, 256 * 8192, 0.02 / 127, s), "fill")
+    for name, fmt in (("fp16", hip.W_F16), ("q8", hip.W_Q8), ("q4", hip.W_Q4)):
+        row = {}
+        for K, N in ((2048, 6144), (2048, 2048), (2048, 8192), (8192, 2048)):
+            if fmt == hip.W_F16:
+                hip.check(L.hxa_fill_normal(Wb.ptr, 1, N * K, 22, 0.0, 0.02, s), "fill")
+            elif fmt == hip.W_Q8:
+                hip.check(L.hxa_fill_uniform_int(Wb.ptr, 8, N * K, 23, -127, 127, s), "fill")
+            else:
+                hip.check(L.hxa_fill_uniform_int(Wb.ptr, 4, N * K // 2, 24, -8, 7, s), "fill")
+            sp = None if fmt == hip.W_F16 else Sb.ptr
+
+            def run(K=K, N=N, fmt=fmt, sp=sp):
+                hip.check(L.hxa_gemm(A.ptr, K, M, fmt | hip.W_KTILED, Wb.ptr, sp, None, N, K, 1, hip.EPI_STORE, O.ptr,
+                                     N, 0, None, 0, None, None, 0, 0, s), "gemm")
+            row[f"{K}x{N}"] = _rate(2.0 * M * N * K, _time_launches(L, hip, run, s))
+        res["linear_m1536"][name] = row
+    # attention (q, k, v^T resident; random fp16)
+    for name, Tq, NKV, Hh in (("self_1536x1536_h16", T, T, H), ("cross_1536x256_h16", T, C_TXT, H),
+                              ("joint_6656x6656_h24", 6656, 6656, 24)):
+        Dd = Hh * 128
+        q = hip.DeviceArray((Tq, Dd), np.float16)
+        k = hip.DeviceArray((NKV, Dd), np.float16)
+        vt = hip.DeviceArray((Dd, NKV), np.float16)
+        o = hip.DeviceArray((Tq, Dd), np.float16)
+        for i, t in enumerate((q, k, vt)):
+            hip.check(L.hxa_fill_normal(t.ptr, 1, t.nbytes // 2, 30 + i, 0.0, 1.0, s), "fill")
+
+        def att(q=q, k=k, vt=vt, o=o, Tq=Tq, NKV=NKV, Dd=Dd, Hh=Hh):
+            hip.check(L.hxa_attention(q.ptr, Dd, k.ptr, Dd, vt.ptr, NKV, o.ptr, Dd, Tq, NKV, NKV, Hh, 1, 0, 0, 0, 0, s),
+                      "attention")
+        res["attention"][name] = _rate(4.0 * Tq * NKV * Dd, _time_launches(L, hip, att, s))
+        del q, k, vt, o
+    # one 2B fp16 block
+    bd = hip.BlockDims(0, D, H, F, C_TXT, DC, T, 1, T, hip.W_F16, hip.W_F16, 1)
+    total, mats, voff = hip.pack_layout(0, D, F, DC, hip.W_F16, hip.W_F16)
+    pack = hip.DeviceArray((total,), np.uint8)
+    for i, ((n, kk), (wo, _)) in enumerate(zip(hip.pack_shapes(0, D, F, DC), mats)):
+        hip.check(L.hxa_fill_normal(C.c_void_p(pack.ptr + wo), 1, n * kk, 40 + i, 0.0, 0.02, s), "fill")
+    gain = np.concatenate([np.full(128, 128 ** -0.5), np.ones(128), np.full(128, 128 ** -0.5), np.ones(128)])
+    hip.check(L.hxa_h2d(C.c_void_p(pack.ptr + voff), gain.astype(np.float32).ctypes.data, 4 * 512), "gain")
+    x = hip.DeviceArray((T, D), np.float32)
+    ctx = hip.DeviceArray((C_TXT, DC), np.float16)
+    mod = hip.DeviceArray((9, D), np.float32)
+    hip.check(L.hxa_fill_normal(x.ptr, 0, T * D, 50, 0.0, 1.0, s), "fill")
+    hip.check(L.hxa_fill_normal(ctx.ptr, 1, C_TXT * DC, 51, 0.0, 1.0, s), "fill")
+    hip.check(L.hxa_fill_normal(mod.ptr, 0, 9 * D, 52, 0.0, 0.02, s), "fill")
+    cos, sin = hip.DeviceArray((T, 64), np.float32), hip.DeviceArray((T, 64), np.float32)
+    hip.check(L.hxa_fill_const(cos.ptr, 0, T * 64, 1.0, s), "fill")
+    hip.check(L.hxa_fill_const(sin.ptr, 0, T * 64, 0.0, s), "fill")
+    ws = hip.block_ws(bd)
+
+    def blk():
+        hip.check(L.hxa_block_run(C.byref(bd), pack.ptr, x.ptr, ctx.ptr, mod.ptr, cos.ptr, sin.ptr, ws.ptr, 0, None, 0,
+                                  s), "block")
+    res["block_2b_fp16_1536tok"] = _rate(BLOCK_FLOPS, _time_launches(L, hip, blk, s, reps=10, warm=2))
+    hip.check(L.hxa_stream_sync(s), "sync")
+    L.hxa_stream_destroy(s)
+    return res
 
 
 def kernel_probe(reps):
@@ -238,7 +339,8 @@ def main():
                      "frac": round(up_tf / PEAK_FP16, 4), "traffic": traffic, "avg_launch_us": round(up_ms * 1e3, 2)},
         "device": info.get("name"),
     }
-    res["q8_2p9b_dit"] = q8_dit_run()
+    res.update(extra_dits())
+    res["microbench"] = microbench()
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)

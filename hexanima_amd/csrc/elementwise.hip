@@ -320,7 +320,7 @@ __global__ __launch_bounds__(256) void modgemv_kernel(const float *__restrict__ 
   }
 }
 
-// x[m][n] = sum_k tok[m][k] * W[n][k], K <= 256 (patch embed). A 64-row x 64-col tile per workgroup; tok rows and
+// x[m][n] = sum_k tok[m][k] * W[n][k], small K (patch embed: 4 x latent channels), in k chunks of 64. A 64-row x 64-col tile per workgroup; tok rows and
 // the weight tile are staged in LDS as fp32.
 __global__ __launch_bounds__(256) void linear_smallk_kernel(const float *__restrict__ x, long ldx, int M, int K,
                                                             const hxa_h *__restrict__ W, int N, float *__restrict__ y,
@@ -328,24 +328,28 @@ __global__ __launch_bounds__(256) void linear_smallk_kernel(const float *__restr
   __shared__ float xs[64][65];
   __shared__ float ws[64][65];
   const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64, tid = threadIdx.x;
-  for (int i = tid; i < 64 * K; i += 256) {
-    const int r = i / K, k = i % K;
-    xs[r][k] = m0 + r < M ? x[(long)(m0 + r) * ldx + k] : 0.0f;
-    ws[r][k] = n0 + r < N ? (float)W[(long)(n0 + r) * K + k] : 0.0f;
-  }
-  __syncthreads();
   const int tr = tid / 16, tc = tid % 16;  // 4x4 outputs per thread
   float acc[4][4] = {};
-  for (int k = 0; k < K; k++) {
-    float a[4], b[4];
+  for (int k0 = 0; k0 < K; k0 += 64) {  // k chunks of 64, accumulated in k order
+    const int kc = min(64, K - k0);
+    __syncthreads();
+    for (int i = tid; i < 64 * kc; i += 256) {
+      const int r = i / kc, k = i % kc;
+      xs[r][k] = m0 + r < M ? x[(long)(m0 + r) * ldx + k0 + k] : 0.0f;
+      ws[r][k] = n0 + r < N ? (float)W[(long)(n0 + r) * K + k0 + k] : 0.0f;
+    }
+    __syncthreads();
+    for (int k = 0; k < kc; k++) {
+      float a[4], b[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) a[i] = xs[tr * 4 + i][k];
+      for (int i = 0; i < 4; i++) a[i] = xs[tr * 4 + i][k];
 #pragma unroll
-    for (int j = 0; j < 4; j++) b[j] = ws[tc + 16 * j][k];
+      for (int j = 0; j < 4; j++) b[j] = ws[tc + 16 * j][k];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+      for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < 4; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
   }
 #pragma unroll
   for (int i = 0; i < 4; i++)
@@ -557,7 +561,7 @@ int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W
     hipLaunchKernelGGL(gemv_kernel, dim3(nblk(N, 4)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy, act, bias,
                        split > 0 ? split : N, gap);
   } else {
-    if (K > 64 || act != 0 || bias != nullptr || split > 0) return HXA_E_ARG;
+    if (act != 0 || bias != nullptr || split > 0) return HXA_E_ARG;
     hipLaunchKernelGGL(linear_smallk_kernel, dim3(nblk(N, 64), nblk(M, 64)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy);
   }
   return LAUNCH_OK();

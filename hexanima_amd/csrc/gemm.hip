@@ -562,8 +562,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
 struct TileCfg {
   int bm, bn, nw;
 };
+// fp16 weights take the 4-wave tiles; int8 / int4 weights the 8-wave ones (two waves per SIMD: the dequantisation
+// registers of a 4-wave tile crowd out the fragment double-buffering, measured 13-18% slower at M = 1536)
 constexpr TileCfg kCfgs[] = {{192, 256, 4}, {192, 192, 4}, {192, 128, 4}, {256, 128, 4}, {128, 256, 4},
-                             {128, 128, 4}, {64, 128, 4},  {128, 64, 4},  {192, 256, 8}};
+                             {128, 128, 4}, {64, 128, 4},  {128, 64, 4},  {192, 256, 8}, {128, 256, 8},
+                             {192, 128, 8}, {128, 128, 8}};
 
 template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false, int NW = 4>
 hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
@@ -592,7 +595,10 @@ template <int FMT, bool ASYM>
 hipError_t launch_fmt(int bm, int bn, int nw, const GemmParams &p, int ksplit, hipStream_t st) {
   if (nw == 8) {
     if (bm == 192 && bn == 256) return launch_t<192, 256, FMT, ASYM, false, 8>(p, ksplit, st);
-    return hipErrorInvalidValue;
+    if (bm == 192 && bn == 128) return launch_t<192, 128, FMT, ASYM, false, 8>(p, ksplit, st);
+    if (bm == 128 && bn == 256) return launch_t<128, 256, FMT, ASYM, false, 8>(p, ksplit, st);
+    if (bm == 128 && bn == 128) return launch_t<128, 128, FMT, ASYM, false, 8>(p, ksplit, st);
+    return hipErrorInvalidValue;  // (kCfgs lists the shapes instantiated here)
   }
   if (bm == 192 && bn == 256) return launch_t<192, 256, FMT, ASYM>(p, ksplit, st);
   if (bm == 192 && bn == 192) return launch_t<192, 192, FMT, ASYM>(p, ksplit, st);
@@ -623,8 +629,12 @@ static void pick_tile(int M, int N, int ksplit, int fmt, int epi, bool headnorm,
   for (const TileCfg &c : kCfgs) {
     if (fmt == HXA_W_Q4 && c.bn < 128) continue;
     if (epi == HXA_EPI_SITU && c.bn % 128 != 0) continue;  // each wave needs whole (up, gate) block pairs
-    if (epi == HXA_EPI_RESADD_SPLIT2 && !(c.bn == 128 && (c.bm == 128 || c.bm == 64))) continue;  // register budget
-    if (headnorm && (c.bn % 128 != 0 || c.nw != 4)) continue;  // whole heads per tile
+    if (epi == HXA_EPI_RESADD_SPLIT2) {
+      if (!(c.bn == 128 && (c.bm == 128 || c.bm == 64) && c.nw == 4)) continue;  // register budget
+    } else if ((c.nw == 8) != (fmt != HXA_W_F16)) {
+      continue;
+    }
+    if (headnorm && c.bn % 128 != 0) continue;  // whole heads per tile
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ksplit;
     const long waves = (tiles + g_num_cu - 1) / g_num_cu;
     const double useful = (double)M * N / ((double)((M + c.bm - 1) / c.bm) * c.bm * ((N + c.bn - 1) / c.bn) * c.bn);
@@ -710,7 +720,7 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
     if (nw != 4 && (nw != 8 || split2)) return HXA_E_ARG;
     if ((g.epi == HXA_EPI_SITU && bn % 128 != 0) || (w.fmt == HXA_W_Q4 && bn < 128)) return HXA_E_ARG;
     if (split2 && !(bn == 128 && (bm == 128 || bm == 64))) return HXA_E_ARG;
-    if (headnorm && (bn % 128 != 0 || nw != 4)) return HXA_E_ARG;
+    if (headnorm && bn % 128 != 0) return HXA_E_ARG;
   }
   p.tiles_m = (g.M + bm - 1) / bm;
   p.tiles_n = (w.N + bn - 1) / bn;

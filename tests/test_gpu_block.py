@@ -332,15 +332,15 @@ def test_dit_moss_small_denoise_vs_oracle():
     lib = hip.lib()
     D, H, F, ntxt, tin, nb = 256, 2, 512, 20, 128, 2
     bd = hip.BlockDims(1, D, H, F, ntxt, 0, 0, 2, 0, hip.W_Q8, hip.W_Q4, 1)
-    cfg = hip.DitCfg(bd, nb, 16, 16, 16, 256, tin)
+    cfg = hip.DitCfg(bd, nb, 32, 16, 16, 256, tin)  # 32 latent channels: patch-embed K = 128 (two k chunks)
     p = C.c_void_p()
     hip.check(lib.hxa_dit_create(C.byref(cfg), 4321, C.byref(p)), "dit_create")
     try:
         rng = np.random.default_rng(8)
-        lat = rng.standard_normal((2, 16, 16, 16)).astype(np.float32)
+        lat = rng.standard_normal((2, 32, 16, 16)).astype(np.float32)
         txt = rng.standard_normal((2, ntxt, tin)).astype(np.float32)
         hip.check(lib.hxa_dit_set_inputs(p, lat.ctypes.data, txt.ctypes.data), "set_inputs")
-        C4, timg = 64, 64
+        C4, timg = 128, 64
         Ttot = (timg + ntxt + 31) // 32 * 32
         layout = hip.pack_layout(1, D, F, 0, hip.W_Q8, hip.W_Q4)
         blocks = [unpack_weights(_export(hip, p, k), 1, D, F, 0, hip.W_Q8, hip.W_Q4, layout) for k in range(nb)]

@@ -93,6 +93,23 @@ def test_gemm_w8a16_w4a16_config1(N, K, fmt):
     assert_gemm_close(got, hxo.gemm(A, wdq), A, wdq.view(np.float16))
 
 
+@pytest.mark.parametrize("tile", [(192, 256, 8), (128, 256, 8), (192, 128, 8), (128, 128, 8), (128, 128, 4)])
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_gemm_quant_tiles(fmt, tile):
+    """int8 / int4 weights on every 8-wave tile (and a 4-wave one), ragged in M and N: dequantised-fp16 GEMM is the
+    reference."""
+    hip = _hip()
+    say(f"gemm fmt={fmt} tile={tile}")
+    rng = np.random.default_rng(40 + fmt)
+    M, N, K = 320, 384, 512
+    A = f16(rng.standard_normal((M, K)))
+    wf = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    q, s = hxo.q8_quantize(wf) if fmt == 1 else hxo.q4_quantize(wf)
+    wdq = hxo.q8_dequant(q, s) if fmt == 1 else hxo.q4_dequant(q, s)
+    got = _run_gemm(hip, A, fmt, q, s, N, K, tile=tile)
+    assert_gemm_close(got, hxo.gemm(A, wdq), A, wdq.view(np.float16))
+
+
 def test_gemm_epilogues():
     hip = _hip()
     rng = np.random.default_rng(3)
