@@ -77,52 +77,47 @@ __global__ __launch_bounds__(256) void normmod_kernel(float *__restrict__ x, lon
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// per-head RMSNorm * gain + split-half RoPE (kern.c:163-197). 16 lanes per (token, head), lane j owns the 8
-// consecutive dims [8j, 8j+8) (one 16-byte load / store); the RoPE partner of dim d < 64 is d + 64, held by lane j ^ 8.
+// per-head RMSNorm * gain + split-half RoPE (kern.c:163-197). 8 lanes per (token, head); lane jj owns dims
+// [8jj, 8jj+8) and [64+8jj, 64+8jj+8) (two 16-byte loads / stores), see head_norm2.
 // ---------------------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void rmsrope_kernel(hxa_h *q0, hxa_h *q1, const float *g0, const float *g1, long ldq,
                                                       int T, int H, const float *__restrict__ cosT,
                                                       const float *__restrict__ sinT, int ttab) {
-  const long gid = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int j = threadIdx.x & 15;
-  if (gid >= (long)T * H) return;  // whole 16-lane groups leave together; shuffles stay inside a group
+  const long gid = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int jj = threadIdx.x & 7;
+  if (gid >= (long)T * H) return;  // whole 8-lane groups leave together; the cross-lane sum stays inside a group
   const int t = (int)(gid / H), hd = (int)(gid % H);
   hxa_h *q = blockIdx.y ? q1 : q0;
   const float *g = blockIdx.y ? g1 : g0;
-  hxa_h *p = q + (long)t * ldq + hd * 128 + 8 * j;
-  const half8_t v = *(const half8_t *)p;
-  float a[8], ss = 0.0f;
+  hxa_h *p = q + (long)t * ldq + hd * 128 + 8 * jj;
+  half8_t lo = *(const half8_t *)p, hi = *(const half8_t *)(p + 64);
+  float glo[8], ghi[8], cs[8] = {}, sn[8] = {};
+  {
+    const float4_t a0 = *(const float4_t *)(g + 8 * jj), a1 = *(const float4_t *)(g + 8 * jj + 4);
+    const float4_t b0 = *(const float4_t *)(g + 64 + 8 * jj), b1 = *(const float4_t *)(g + 64 + 8 * jj + 4);
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    a[e] = (float)v[e];
-    ss += a[e] * a[e];
-  }
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);
-  const float r = rsqrtf(ss * (1.0f / 128.0f) + 1e-6f);
-  const float4_t ga = *(const float4_t *)(g + 8 * j), gb = *(const float4_t *)(g + 8 * j + 4);
-#pragma unroll
-  for (int e = 0; e < 4; e++) {
-    a[e] = a[e] * r * ga[e];
-    a[e + 4] = a[e + 4] * r * gb[e];
-  }
-  if (cosT != nullptr) {
-    const int tt = t % ttab, d0 = 8 * (j & 7);
-    const float4_t c0 = *(const float4_t *)(cosT + (long)tt * 64 + d0), c1 = *(const float4_t *)(cosT + (long)tt * 64 + d0 + 4);
-    const float4_t s0 = *(const float4_t *)(sinT + (long)tt * 64 + d0), s1 = *(const float4_t *)(sinT + (long)tt * 64 + d0 + 4);
-    const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-    const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const float partner = __shfl_xor(a[e], 8);
-      // d < 64: y[d] = x[d] c - x[d+64] s;  d >= 64: y[d] = x[d-64] s + x[d] c
-      a[e] = j < 8 ? a[e] * cs[e] - partner * sn[e] : partner * sn[e] + a[e] * cs[e];
+    for (int e = 0; e < 4; e++) {
+      glo[e] = a0[e];
+      glo[e + 4] = a1[e];
+      ghi[e] = b0[e];
+      ghi[e + 4] = b1[e];
     }
   }
-  half8_t o;
+  if (cosT != nullptr) {
+    const long o = (long)(t % ttab) * 64 + 8 * jj;
+    const float4_t c0 = *(const float4_t *)(cosT + o), c1 = *(const float4_t *)(cosT + o + 4);
+    const float4_t s0 = *(const float4_t *)(sinT + o), s1 = *(const float4_t *)(sinT + o + 4);
 #pragma unroll
-  for (int e = 0; e < 8; e++) o[e] = (hxa_h)a[e];
-  *(half8_t *)p = o;
+    for (int e = 0; e < 4; e++) {
+      cs[e] = c0[e];
+      cs[e + 4] = c1[e];
+      sn[e] = s0[e];
+      sn[e + 4] = s1[e];
+    }
+  }
+  head_norm2(lo, hi, glo, ghi, cosT != nullptr, cs, sn);
+  *(half8_t *)p = lo;
+  *(half8_t *)(p + 64) = hi;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -492,7 +487,7 @@ int hxa_norm_mod_launch(const float *x, long ldx, int T, int D, const float *shi
 int hxa_rmsrope_launch(hxa_h *q0, hxa_h *q1, const float *g0, const float *g1, long ldq, int T, int H, const float *cosT,
                        const float *sinT, int ttab, hipStream_t st) {
   if (T <= 0 || H <= 0 || (cosT && ttab <= 0) || ldq % 8 || (uintptr_t)q0 % 16 || (uintptr_t)q1 % 16) return HXA_E_ARG;
-  dim3 g(nblk((long)T * H, 16), q1 ? 2 : 1);
+  dim3 g(nblk((long)T * H, 32), q1 ? 2 : 1);
   hipLaunchKernelGGL(rmsrope_kernel, g, dim3(256), 0, st, q0, q1, g0, g1, ldq, T, H, cosT, sinT, ttab > 0 ? ttab : 1);
   return LAUNCH_OK();
 }

@@ -49,35 +49,7 @@ struct GemmParams {
   const float *hn_g0, *hn_g1, *hn_cos, *hn_sin;
 };
 
-// Per-head RMSNorm * gain + split-half RoPE of one 8-column chunk (kern.c:163-197), the same arithmetic as the
-// standalone RMS+RoPE kernel: the 16 lanes holding one head's 128 values (aligned 16-lane group, chunk j = lane & 15
-// owning dims [8j, 8j+8)) reduce with shfl_xor(1..8); the RoPE partner of dim d < 64 (d + 64) is in lane j ^ 8.
-// g: the chunk's 8 gains; cs / sn: cos / sin of dims 8 (j & 7) .. +8 at the row's token (rope only).
-HXA_DEV half8_t head_norm(half8_t v, int j, const float (&g)[8], bool rope, const float (&cs)[8], const float (&sn)[8]) {
-  float a[8], ss = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    a[e] = (float)v[e];
-    ss += a[e] * a[e];
-  }
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);
-  const float r = rsqrtf(ss * (1.0f / 128.0f) + 1e-6f);
-#pragma unroll
-  for (int e = 0; e < 8; e++) a[e] = a[e] * r * g[e];
-  if (rope) {
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const float partner = __shfl_xor(a[e], 8);
-      a[e] = j < 8 ? a[e] * cs[e] - partner * sn[e] : partner * sn[e] + a[e] * cs[e];
-    }
-  }
-  half8_t o;
-#pragma unroll
-  for (int e = 0; e < 8; e++) o[e] = (hxa_h)a[e];
-  return o;
-}
-// the chunk's gains (columns n .. n+7 of head-normed output) and a row's RoPE coefficients
+// the gains of head-normed columns n .. n+7 and a row's RoPE coefficients of dims (n & 63) .. +7
 HXA_DEV void hn_gains(const GemmParams &p, int n, float (&g)[8]) {
   const float *gp = (n < p.hn_gsplit ? p.hn_g0 : p.hn_g1) + (n & 127);
   const float4_t a = *(const float4_t *)gp, b = *(const float4_t *)(gp + 4);
@@ -87,8 +59,8 @@ HXA_DEV void hn_gains(const GemmParams &p, int n, float (&g)[8]) {
     g[e + 4] = b[e];
   }
 }
-HXA_DEV void hn_rope(const GemmParams &p, int m, int n, float (&cs)[8], float (&sn)[8]) {
-  const long o = (long)(m % p.hn_ttab) * 64 + (n & 63);
+HXA_DEV void hn_rope_t(const GemmParams &p, int tt, int n, float (&cs)[8], float (&sn)[8]) {
+  const long o = (long)tt * 64 + (n & 63);
   const float4_t c0 = *(const float4_t *)(p.hn_cos + o), c1 = *(const float4_t *)(p.hn_cos + o + 4);
   const float4_t s0 = *(const float4_t *)(p.hn_sin + o), s1 = *(const float4_t *)(p.hn_sin + o + 4);
 #pragma unroll
@@ -479,24 +451,43 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
     }
     return;
   }
-  if constexpr (BN % 128 == 0 && (64 * NW) % (BN / 8) == 0) {
-  if (p.hn_cols > 0 && n0 + BN <= p.hn_cols) {
-    // every column of this tile is head-normed: a thread's chunk position (column) is the same in every pass, so its
-    // gains are loaded once; the next row's RoPE coefficients are fetched one pass ahead
-    constexpr int NC8 = BN / 8, ITERS = BM * NC8 / NT;
-    static_assert(NT % NC8 == 0 && NC8 % 16 == 0, "head groups aligned to 16 lanes");
-    const int nl = (tid % NC8) * 8, n = n0 + nl, j = (nl >> 3) & 15;
+  if constexpr (BN % 128 == 0) {
+  if (p.hn_cols > 0 && (n0 + BN <= p.hn_cols || p.hn_cols >= p.N)) {
+    // every (valid) column of this tile is head-normed. Thread (row group r0, jj) owns dims [8jj, 8jj+8) and
+    // [64+8jj, 64+8jj+8) of every head of the tile on its rows: the gains are loaded once, the RoPE coefficients once
+    // per row for all heads (fetched one pass ahead), and the rotation partners sit in the same thread.
+    constexpr int HT = BN / 128, RP = NT / 8;  // heads per tile, rows per pass
+    static_assert(BM % RP == 0, "whole passes");
+    const int jj = tid & 7, r0 = tid >> 3;
     const bool rope = p.hn_cos != nullptr;
-    float g[8], cs[8] = {}, sn[8] = {}, csn[8] = {}, snn[8] = {};
-    hn_gains(p, n, g);
-    if (rope) hn_rope(p, min(m0 + tid / NC8, p.M - 1), n, cs, sn);
-#pragma unroll 2
-    for (int it = 0; it < ITERS; it++) {
-      const int ml = (tid + it * NT) / NC8, m = m0 + ml;
-      if (rope && it + 1 < ITERS) hn_rope(p, min(m + NT / NC8, p.M - 1), n, csn, snn);
-      if (m < p.M) {
-        const half8_t v = *(const half8_t *)(Cs + ml * CROW + nl);
-        *(half8_t *)(p.out + (long)m * p.ldo + n) = head_norm(v, j, g, rope, cs, sn);
+    float glo[HT][8], ghi[HT][8], cs[8] = {}, sn[8] = {}, csn[8] = {}, snn[8] = {};
+#pragma unroll
+    for (int hh = 0; hh < HT; hh++) {
+      hn_gains(p, n0 + hh * 128 + 8 * jj, glo[hh]);
+      hn_gains(p, n0 + hh * 128 + 64 + 8 * jj, ghi[hh]);
+    }
+    // RoPE table row of the next pass's row, stepped by RP rows without a division (rows past M are not stored)
+    int tt = rope ? min(m0 + r0, p.M - 1) % p.hn_ttab : 0;
+    if (rope) hn_rope_t(p, tt, 8 * jj, cs, sn);
+    for (int it = 0; it < BM / RP; it++) {
+      const int ml = r0 + it * RP, m = m0 + ml;
+      if (rope && it + 1 < BM / RP) {
+        if (m + RP < p.M) {
+          tt += RP;
+          while (tt >= p.hn_ttab) tt -= p.hn_ttab;
+        }
+        hn_rope_t(p, tt, 8 * jj, csn, snn);
+      }
+      if (m < p.M) {  // whole 8-lane groups share m
+#pragma unroll
+        for (int hh = 0; hh < HT; hh++) {
+          const int nl = hh * 128 + 8 * jj;
+          if (n0 + nl >= p.N) break;
+          half8_t lo = *(const half8_t *)(Cs + ml * CROW + nl), hi = *(const half8_t *)(Cs + ml * CROW + nl + 64);
+          head_norm2(lo, hi, glo[hh], ghi[hh], rope, cs, sn);
+          *(half8_t *)(p.out + (long)m * p.ldo + n0 + nl) = lo;
+          *(half8_t *)(p.out + (long)m * p.ldo + n0 + nl + 64) = hi;
+        }
       }
       if (rope) {
 #pragma unroll
@@ -520,12 +511,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
     if (p.epi == HXA_EPI_PARTIAL) {
       *(half8_t *)(p.out + (long)z * p.out_zstride + o) = v;
     } else {
-      if (n < p.hn_cols) {  // whole 16-lane head groups take this branch together (n0, ncols multiples of 128)
-        float g[8], cs[8] = {}, sn[8] = {};
-        hn_gains(p, n, g);
-        if (p.hn_cos) hn_rope(p, m, n, cs, sn);
-        v = head_norm(v, (nl >> 3) & 15, g, p.hn_cos != nullptr, cs, sn);
-      } else if (p.epi == HXA_EPI_GELU_TANH) {
+      if (p.epi == HXA_EPI_GELU_TANH) {  // (head-normed tiles never get here: whole tiles take the path above)
 #pragma unroll
         for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_tanh_f((float)v[e]);
       } else if (p.epi == HXA_EPI_GELU_ERF) {
@@ -540,20 +526,35 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
     rows_pass(std::integral_constant<int, BN>{});
   else
     rows_pass(nsplit);
-  if (nsplit < BN) {  // transposed columns: chunk = (column, 8 consecutive rows)
-    const int ncol = BN - nsplit;
-    for (int c = tid; c < ncol * (BM / 8); c += NT) {
-      const int nl = nsplit + c / (BM / 8), ml = (c % (BM / 8)) * 8;
-      const int n = n0 + nl, m = m0 + ml;
-      if (n >= p.N || m >= p.M) continue;
-      half8_t v;
+  if (nsplit < BN) {
+    // transposed columns (a multiple of 32: split_col % 32 == 0): a thread takes 4 adjacent columns x 8 rows, read as
+    // 8-byte LDS words (consecutive threads -> consecutive words: no bank conflicts) and written as four 16-byte
+    // runs of 8 rows, one per output row n of out_t
+    const int ngrp = (BN - nsplit) / 4;
+    for (int c = tid; c < ngrp * (BM / 8); c += NT) {
+      const int nl = nsplit + (c % ngrp) * 4, ml = (c / ngrp) * 8;
+      const int m = m0 + ml;
+      if (m >= p.M) continue;
+      uint2_t w[8];
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = Cs[(ml + e) * CROW + nl];
-      hxa_h *dst = p.out_t + (long)(n - p.split_col) * p.ldo_t + m;
-      if (m + 7 < p.M) {
-        *(half8_t *)dst = v;
-      } else {
-        for (int e = 0; e < 8 && m + e < p.M; e++) dst[e] = v[e];
+      for (int e = 0; e < 8; e++) w[e] = *(const uint2_t *)(Cs + (ml + e) * CROW + nl);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int n = n0 + nl + q;
+        if (n >= p.N) break;
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {  // rows 2k, 2k+1 of column q: halves (q & 1) of word (q >> 1)
+          const uint32_t a = (q >> 1) ? w[2 * k].y : w[2 * k].x, b = (q >> 1) ? w[2 * k + 1].y : w[2 * k + 1].x;
+          o[k] = __builtin_amdgcn_perm(b, a, (q & 1) ? 0x07060302u : 0x05040100u);
+        }
+        hxa_h *dst = p.out_t + (long)(n - p.split_col) * p.ldo_t + m;
+        if (m + 7 < p.M) {
+          *(uint4_t *)dst = (uint4_t){o[0], o[1], o[2], o[3]};
+        } else {
+          const half8_t v = __builtin_bit_cast(half8_t, (uint4_t){o[0], o[1], o[2], o[3]});
+          for (int e = 0; e < 8 && m + e < p.M; e++) dst[e] = v[e];
+        }
       }
     }
   }
@@ -618,7 +619,8 @@ int g_num_cu = 0;
 }  // namespace
 
 // Choose a tile shape: best wave-quantisation efficiency over the GPU's CUs, ties to the larger tile.
-static void pick_tile(int M, int N, int ksplit, int fmt, int epi, bool headnorm, int *bm, int *bn, int *nw) {
+static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int hn_cols, int *bm, int *bn, int *nw) {
+  const bool headnorm = hn_cols > 0;
   if (g_num_cu == 0) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
@@ -634,7 +636,7 @@ static void pick_tile(int M, int N, int ksplit, int fmt, int epi, bool headnorm,
     } else if ((c.nw == 8) != (fmt != HXA_W_F16)) {
       continue;
     }
-    if (headnorm && c.bn % 128 != 0) continue;  // whole heads per tile
+    if (headnorm && (c.bn % 128 != 0 || (hn_cols % c.bn != 0 && hn_cols < N))) continue;  // whole head-normed tiles
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ksplit;
     const long waves = (tiles + g_num_cu - 1) / g_num_cu;
     const double useful = (double)M * N / ((double)((M + c.bm - 1) / c.bm) * c.bm * ((N + c.bn - 1) / c.bn) * c.bn);
@@ -712,7 +714,7 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   p.hn_cos = g.hn_cos;
   p.hn_sin = g.hn_sin;
   int bm = 128, bn = 128, nw = 4;
-  pick_tile(g.M, w.N, g.ksplit, w.fmt, g.epi, headnorm, &bm, &bn, &nw);
+  pick_tile(g.M, w.N, g.ksplit, w.fmt, g.epi, headnorm ? min(g.hn_cols, w.N) : 0, &bm, &bn, &nw);
   if (g.force_bm) {
     bm = g.force_bm;
     bn = g.force_bn;
@@ -720,7 +722,7 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
     if (nw != 4 && (nw != 8 || split2)) return HXA_E_ARG;
     if ((g.epi == HXA_EPI_SITU && bn % 128 != 0) || (w.fmt == HXA_W_Q4 && bn < 128)) return HXA_E_ARG;
     if (split2 && !(bn == 128 && (bm == 128 || bm == 64))) return HXA_E_ARG;
-    if (headnorm && bn % 128 != 0) return HXA_E_ARG;
+    if (headnorm && (bn % 128 != 0 || (p.hn_cols % bn != 0 && p.hn_cols < w.N))) return HXA_E_ARG;
   }
   p.tiles_m = (g.M + bm - 1) / bm;
   p.tiles_n = (w.N + bn - 1) / bn;

@@ -50,6 +50,59 @@ HXA_DEV void g2l16_opaque(const void *g, const void *lds_ptr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
 }
 
+// Cross-lane moves inside a 16-lane DPP row (VALU, no LDS round trip).
+template <int CTRL>
+HXA_DEV float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over the aligned 8-lane group (pairs i^1, i^2 within quads, then quad with quad by the half-row mirror
+// i^7): every lane of the group gets the bit-identical total.
+HXA_DEV float sum8(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  return v;
+}
+
+// Per-head RMSNorm * gain + split-half RoPE (kern.c:163-197) on the 8 lanes holding one head of 128: lane jj owns
+// dims [8jj, 8jj+8) (lo) and their RoPE partners [64+8jj, 64+8jj+8) (hi), so the rotation needs no exchange:
+//   y[d] = x[d] c_d - x[d+64] s_d,  y[d+64] = x[d] s_d + x[d+64] c_d  (d < 64).
+// Shared by the GEMM's head-norm epilogue and the standalone kernel, which therefore give the same bits.
+HXA_DEV void head_norm2(half8_t &lo, half8_t &hi, const float (&glo)[8], const float (&ghi)[8], bool rope,
+                        const float (&cs)[8], const float (&sn)[8]) {
+  float a[8], b[8], ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    a[e] = (float)lo[e];
+    ss = fmaf(a[e], a[e], ss);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    b[e] = (float)hi[e];
+    ss = fmaf(b[e], b[e], ss);
+  }
+  ss = sum8(ss);
+  const float r = rsqrtf(fmaf(ss, 1.0f / 128.0f, 1e-6f));
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    a[e] = a[e] * r * glo[e];
+    b[e] = b[e] * r * ghi[e];
+  }
+  if (rope) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float x = a[e], y = b[e];
+      a[e] = fmaf(x, cs[e], -(y * sn[e]));
+      b[e] = fmaf(x, sn[e], y * cs[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    lo[e] = (hxa_h)a[e];
+    hi[e] = (hxa_h)b[e];
+  }
+}
+
 #define HXA_CHECK(x)                                  \
   do {                                                \
     hipError_t e_ = (x);                              \

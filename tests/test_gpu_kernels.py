@@ -214,23 +214,29 @@ def _run_gemm_rc(hip, A, N, K, epi, x, g):
                               None, 0, 0, None)
 
 
-def test_gemm_fused_qkv_split_transposed():
+@pytest.mark.parametrize("M", [256, 300])
+def test_gemm_fused_qkv_split_transposed(M):
+    """q|k row-major and v transposed from one projection; M = 300 leaves a partial 8-row run in the transposed
+    store (rows past M are not written)."""
     hip = _hip()
-    say("gemm fused qkv with transposed v")
+    say(f"gemm fused qkv with transposed v M={M}")
     rng = np.random.default_rng(4)
-    M, D = 256, 256
+    D = 256
+    ldt = (M + 7) // 8 * 8
     A = f16(rng.standard_normal((M, D)))
     W = f16(rng.standard_normal((3 * D, D)) * 0.05)
     dA, dW = hip.DeviceArray.from_numpy(A), hip.DeviceArray.from_numpy(W)
     qk = hip.DeviceArray((M, 2 * D), np.float16)
-    vt = hip.DeviceArray((D, M), np.float16)
+    vt = hip.DeviceArray.from_numpy(np.full((D, ldt), 7.0, np.float16))
     hip.check(hip.lib().hxa_gemm(dA.ptr, D, M, 0, dW.ptr, None, None, 3 * D, D, 1, 0, qk.ptr, 2 * D, 0, None, 0, None,
-                                 vt.ptr, M, 2 * D, None), "qkv")
+                                 vt.ptr, ldt, 2 * D, None), "qkv")
     hip.sync()
     ref = hxo.gemm(A, W)
     Wq, Wv = np.ascontiguousarray(W[:2 * D]), np.ascontiguousarray(W[2 * D:])
     assert_gemm_close(qk.numpy(), ref[:, :2 * D], A, Wq)
-    assert_gemm_close(np.ascontiguousarray(vt.numpy().T), ref[:, 2 * D:], A, Wv)
+    got_t = vt.numpy()
+    assert_gemm_close(np.ascontiguousarray(got_t[:, :M].T), ref[:, 2 * D:], A, Wv)
+    assert (got_t[:, M:] == 7.0).all()
 
 
 @pytest.mark.parametrize("rope,fmt", [(True, 0), (False, 0), (True, 1)])
