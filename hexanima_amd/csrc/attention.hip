@@ -5,9 +5,10 @@
 // (moss/hexagon/mega/blk.c:56-58). No 1/sqrt(d) is applied: it is folded into the q RMSNorm gain
 // (export_all.py:31-32). Keys >= nvalid get probability 0.
 //
-// Work split: a workgroup of 8 waves owns 128 queries of one head. Waves 0-3 take the first half of the key tiles,
-// waves 4-7 the second half (two waves per SIMD, so one wave's softmax overlaps the other's MFMAs); the halves are
-// merged through LDS at the end. Each wave owns 32 queries and keeps Q in registers.
+// Work split: a workgroup of 2 x NWH waves owns 32 NWH queries of one head (NWH = 4: 128 queries, or 3: 96 queries
+// when that fills the CUs better). Waves [0, NWH) take the first half of the key tiles, the others the second half
+// (up to two waves per SIMD, so one wave's softmax overlaps another's MFMAs); the halves are merged through LDS at
+// the end. Each wave owns 32 queries and keeps Q in registers.
 //
 // Per 64-key tile a wave computes S^T = K . Q^T (v_mfma_f32_32x32x16_f16), so a lane holds 16 scores of ONE query
 // and the row max needs a single shfl_xor(32). K rows are stored in LDS with rows 4-7 and 8-11 of every 16 swapped,
@@ -24,9 +25,6 @@
 namespace {
 
 constexpr int KT = 64;                        // keys per tile
-constexpr int NWH = 4;                        // waves per key half
-constexpr int NT = 2 * NWH * 64;              // 512 threads
-constexpr int QB = NWH * 32;                  // queries per workgroup
 constexpr int TILE_BYTES = KT * 128 * 2;      // K tile [64 keys][128] = V^T tile [128][64 keys] = 16 KB
 constexpr int HALF_BYTES = 4 * TILE_BYTES;    // K[2] | V[2]
 constexpr int LDS_BYTES = 2 * HALF_BYTES;     // 128 KB
@@ -41,11 +39,15 @@ HXA_DEV int krow_key(int i) {
 
 HXA_DEV float16_t mfma(half8_t a, half8_t b, float16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
 
-__global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
+// NWH waves per key half (4: 128 queries per workgroup, 8 waves; 3: 96 queries, 6 waves -- chosen per launch so
+// that the grid fills the CUs)
+template <int NWH>
+__global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) {
+  constexpr int QB = NWH * 32;  // queries per workgroup
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = wave >> 2, wq = wave & 3, g = lane >> 5, ql = lane & 31;
+  const int half = wave / NWH, wq = wave % NWH, g = lane >> 5, ql = lane & 31;
   // XCD-aware order: the query blocks of one head run on one XCD (its L2 keeps that head's K / V^T)
   const int ntot = nqb * p.H, bid = blockIdx.x;
   const int tile = (ntot % 8 == 0) ? (bid % 8) * (ntot / 8) + bid / 8 : bid;
@@ -69,27 +71,33 @@ __global__ __launch_bounds__(NT) void attn_kernel(HxaAttn p, int nqb) {
   auto vbuf = [&](int i) { return hb + (2 + (i & 1)) * TILE_BYTES; };
 
   // local tile i -> LDS: 16 KB of K (rows of 256 B, 16 chunks, chunk c at c ^ (row & 15)) and 16 KB of V^T (rows of
-  // 128 B, 8 chunks, chunk c at c ^ ((row >> 1) & 7)); each wave moves 4 + 4 blocks of 1 KB. Keys past NKV read a valid
-  // row (their probability is 0).
+  // 128 B, 8 chunks, chunk c at c ^ ((row >> 1) & 7)); the 16 + 16 blocks of 1 KB are dealt round-robin over the NWH
+  // waves of the half. Keys past NKV read a valid row (their probability is 0).
   auto load_kv = [&](int i, bool with_k, bool with_v) {
     const int key0 = (t0 + i) * KT;
     if (with_k) {
       uint8_t *dst = kbuf(i);
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int blk = j * NWH + wq, row = 4 * blk + (lane >> 4), c = (lane & 15) ^ (row & 15);
-        const int key = min(key0 + krow_key(row), p.NKV - 1);
-        g2l16_opaque(k + (long)key * p.ldk + c * 8, dst + blk * 1024);
+      for (int j = 0; j < (16 + NWH - 1) / NWH; j++) {
+        const int blk = j * NWH + wq;
+        if (16 % NWH == 0 || blk < 16) {
+          const int row = 4 * blk + (lane >> 4), c = (lane & 15) ^ (row & 15);
+          const int key = min(key0 + krow_key(row), p.NKV - 1);
+          g2l16_opaque(k + (long)key * p.ldk + c * 8, dst + blk * 1024);
+        }
       }
     }
     if (with_v) {
       uint8_t *dst = vbuf(i);
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int blk = j * NWH + wq, d = 8 * blk + (lane >> 3), c = (lane & 7) ^ ((d >> 1) & 7);
-        int key = key0 + c * 8;
-        if (key >= p.NKV) key = 0;
-        g2l16_opaque(vt + (long)d * p.ldvt + key, dst + blk * 1024);
+      for (int j = 0; j < (16 + NWH - 1) / NWH; j++) {
+        const int blk = j * NWH + wq;
+        if (16 % NWH == 0 || blk < 16) {
+          const int d = 8 * blk + (lane >> 3), c = (lane & 7) ^ ((d >> 1) & 7);
+          int key = key0 + c * 8;
+          if (key >= p.NKV) key = 0;
+          g2l16_opaque(vt + (long)d * p.ldvt + key, dst + blk * 1024);
+        }
       }
     }
   };
@@ -255,13 +263,29 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   if (((uintptr_t)p.q | (uintptr_t)p.k | (uintptr_t)p.vt) % 16 || (uintptr_t)p.o % 8) return HXA_E_ARG;
   if (p.q_bstride % 8 || p.k_bstride % 8 || p.vt_bstride % 8 || p.o_bstride % 4) return HXA_E_ARG;
   static bool attr = false;
+  static int num_cu = 0;
   if (!attr) {
-    if (hipFuncSetAttribute((const void *)attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES) != hipSuccess)
+    if (hipFuncSetAttribute((const void *)attn_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES) !=
+            hipSuccess ||
+        hipFuncSetAttribute((const void *)attn_kernel<3>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES) !=
+            hipSuccess)
       return HXA_E_HIP;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                  hipSuccess)
+      num_cu = 256;
     attr = true;
   }
-  const int nqb = (p.T + QB - 1) / QB;
+  // one workgroup per CU at a time (128 KB of LDS): take the query-block size whose grid wastes the least of the
+  // last round (ties: 128 queries)
+  auto fill = [&](int qb) {
+    const long wgs = (long)((p.T + qb - 1) / qb) * p.H * p.batch, rounds = (wgs + num_cu - 1) / num_cu;
+    return (double)wgs / (double)(rounds * num_cu);
+  };
+  const bool small = fill(96) > fill(128) + 1e-9;
+  const int QB = small ? 96 : 128, nqb = (p.T + QB - 1) / QB;
   dim3 grid(nqb * p.H, p.batch);
-  hipLaunchKernelGGL(attn_kernel, grid, dim3(NT), LDS_BYTES, st, p, nqb);
+  if (small) hipLaunchKernelGGL(attn_kernel<3>, grid, dim3(384), LDS_BYTES, st, p, nqb);
+  else hipLaunchKernelGGL(attn_kernel<4>, grid, dim3(512), LDS_BYTES, st, p, nqb);
   return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
 }

@@ -11,10 +11,14 @@
 
 namespace {
 
+// sum over the 64 lanes, all in VALU cross-lane moves: the 16-lane row sums (sum8 + row mirror), then row 0 -> 1
+// and row 2 -> 3 (row_bcast:15), rows 0+1 -> 3 (row_bcast:31); lane 63 holds the total, read into a scalar
 HXA_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v = sum8(v);
+  v += dpp_f<0x140>(v);  // row_mirror: every lane of a row holds the row sum
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -368,52 +372,94 @@ __global__ void sinusoid_kernel(const float *t, int n, int dim, float *out) {
 
 // final layer (animad.cpp:474-492): per token LN (eps 1e-6, two-pass) * (1 + scale) + shift, linear D -> 4C,
 // unpatchify (ph, pw, c) into lat; when dt != 0 the Euler update lat += dt * v is applied instead of storing v.
+// FT tokens per workgroup: each wave normalises FT/4 tokens into LDS, then thread (output o, part) accumulates its
+// quarter-interleaved share of the D products for all FT tokens (the weights are read once per workgroup), and the
+// `per` parts of an output (adjacent lanes) are summed with DPP.
+constexpr int FT = 8;
 __global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ x, int T, int xrows, int D,
                                                     const float *__restrict__ shift, const float *__restrict__ scale,
                                                     const hxa_h *__restrict__ Wf, int Cc, int H, int W, float *lat,
-                                                    const float *__restrict__ dtp) {
-  extern __shared__ float xn[];  // D floats + 256 scratch
-  float *red = xn + D;
-  const long tok = blockIdx.x;
-  const int b = (int)(tok / T), tk = (int)(tok % T), tid = threadIdx.x;
-  const float *xr = x + ((long)b * xrows + tk) * D;
-  float s = 0.0f;
-  for (int c = tid; c < D; c += 256) s += xr[c];
-  s = wave_sum(s);
-  if ((tid & 63) == 0) red[tid >> 6] = s;
-  __syncthreads();
-  const float mu = (red[0] + red[1] + red[2] + red[3]) / (float)D;
-  __syncthreads();
-  float q = 0.0f;
-  for (int c = tid; c < D; c += 256) {
-    const float d = xr[c] - mu;
-    q += d * d;
+                                                    const float *__restrict__ dtp, int ntok) {
+  extern __shared__ float xn[];  // [FT][D]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tok0 = blockIdx.x * FT;
+  for (int u = 0; u < FT / 4; u++) {
+    const int tl = wave * (FT / 4) + u, tok = tok0 + tl;
+    float *dst = xn + tl * D;
+    if (tok >= ntok) {
+      for (int c = lane; c < D; c += 64) dst[c] = 0.0f;
+      continue;
+    }
+    const int b = tok / T, tk = tok % T;
+    const float4_t *xr = (const float4_t *)(x + ((long)b * xrows + tk) * D);
+    const int nv = D / 256;  // float4 per lane (D % 256 == 0, D <= 4096)
+    float4_t v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      if (i < nv) v[i] = xr[lane + 64 * i];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      if (i < nv) s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+    const float mu = wave_sum(s) / (float)D;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      if (i < nv) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float d = v[i][e] - mu;
+          q = fmaf(d, d, q);
+        }
+      }
+    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      if (i < nv) {
+        const int c = (lane + 64 * i) * 4;
+        const float4_t sc = *(const float4_t *)(scale + c), sh = *(const float4_t *)(shift + c);
+        float4_t o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] = (v[i][e] - mu) * rs * (1.0f + sc[e]) + sh[e];
+        *(float4_t *)(dst + c) = o;
+      }
   }
-  q = wave_sum(q);
-  if ((tid & 63) == 0) red[tid >> 6] = q;
   __syncthreads();
-  const float rs = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)D + 1e-6f);
-  for (int c = tid; c < D; c += 256) xn[c] = (xr[c] - mu) * rs * (1.0f + scale[c]) + shift[c];
-  __syncthreads();
-  // 4C outputs, 256/(4C) threads each
   const int NO = 4 * Cc, per = 256 / NO;
   const int o = tid / per, part = tid % per;
-  float acc = 0.0f;
-  if (o < NO) {
-    const hxa_h *wr = Wf + (long)o * D;
-    for (int c = part; c < D; c += per) acc = fmaf(xn[c], (float)wr[c], acc);
+  float acc[FT];
+#pragma unroll
+  for (int t = 0; t < FT; t++) acc[t] = 0.0f;
+  const hxa_h *wr = Wf + (long)o * D;
+  for (int c0 = 4 * part; c0 < D; c0 += 32 * per) {  // 8 weight loads in flight per round (D % 128 == 0)
+    half4_t w4[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) w4[u] = *(const half4_t *)(wr + c0 + u * 4 * per);
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int c = c0 + u * 4 * per;
+      const float w0 = (float)w4[u][0], w1 = (float)w4[u][1], w2 = (float)w4[u][2], w3 = (float)w4[u][3];
+#pragma unroll
+      for (int t = 0; t < FT; t++) {
+        const float4_t v = *(const float4_t *)(xn + t * D + c);
+        acc[t] = fmaf(v[0], w0, fmaf(v[1], w1, fmaf(v[2], w2, fmaf(v[3], w3, acc[t]))));
+      }
+    }
   }
-  __syncthreads();
-  red[tid] = acc;
-  __syncthreads();
-  if (tid < NO) {
-    float v = 0.0f;
-    for (int j = 0; j < per; j++) v += red[tid * per + j];
-    const int gw = W / 2, gy = tk / gw, gx = tk % gw;
-    const int ab = tid / Cc, c = tid % Cc, a = ab >> 1, bb = ab & 1;
-    float *dst = lat + (((long)b * Cc + c) * H + gy * 2 + a) * W + gx * 2 + bb;
-    if (dtp != nullptr) *dst += *dtp * v;
-    else *dst = v;
+  const int gw = W / 2;
+#pragma unroll
+  for (int t = 0; t < FT; t++) {
+    float v = acc[t];
+    if (per >= 2) v += dpp_f<0xB1>(v);  // lanes i^1
+    if (per >= 4) v += dpp_f<0x4E>(v);  // lanes i^2
+    const int tok = tok0 + t;
+    if (part == 0 && tok < ntok) {
+      const int b = tok / T, tk = tok % T, gy = tk / gw, gx = tk % gw;
+      const int ab = o / Cc, c = o % Cc, a = ab >> 1, bb = ab & 1;
+      float *dst = lat + (((long)b * Cc + c) * H + gy * 2 + a) * W + gx * 2 + bb;
+      if (dtp != nullptr) *dst += *dtp * v;
+      else *dst = v;
+    }
   }
 }
 
@@ -599,9 +645,19 @@ int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, 
 int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale,
                      const hxa_h *Wf, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st) {
   const int NO = 4 * Cc;
-  if (NO > 256 || 256 % NO || (H / 2) * (W / 2) != T || xrows < T) return HXA_E_ARG;
-  const size_t lds = sizeof(float) * (size_t)(D + 256);
-  hipLaunchKernelGGL(final_kernel, dim3(B * T), dim3(256), lds, st, x, T, xrows, D, shift, scale, Wf, Cc, H, W, lat, dtp);
+  if (NO > 256 || 256 % NO || 256 / NO > 4 || (H / 2) * (W / 2) != T || xrows < T || D % 256 || D > 4096)
+    return HXA_E_ARG;
+  const size_t lds = sizeof(float) * (size_t)FT * D;
+  if (lds > 160 * 1024) return HXA_E_ARG;
+  static size_t lds_set = 0;
+  if (lds > lds_set) {
+    if (hipFuncSetAttribute((const void *)final_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+      return HXA_E_HIP;
+    lds_set = lds;
+  }
+  const int ntok = B * T;
+  hipLaunchKernelGGL(final_kernel, dim3((ntok + FT - 1) / FT), dim3(256), lds, st, x, T, xrows, D, shift, scale, Wf, Cc,
+                     H, W, lat, dtp, ntok);
   return LAUNCH_OK();
 }
 
