@@ -299,6 +299,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="leave out the other DiT workloads and the kernel microbenchmarks (for a kernel trace of the step)")
     ap.add_argument("--kernel-probe", type=int, default=0, metavar="REPS",
                     help="only launch the dominant kernel REPS times plus a copy calibration (for rocprofv3 --pmc)")
     a = ap.parse_args()
@@ -339,8 +341,9 @@ def main():
                      "frac": round(up_tf / PEAK_FP16, 4), "traffic": traffic, "avg_launch_us": round(up_ms * 1e3, 2)},
         "device": info.get("name"),
     }
-    res.update(extra_dits())
-    res["microbench"] = microbench()
+    if not a.no_extras:
+        res.update(extra_dits())
+        res["microbench"] = microbench()
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)
