@@ -156,6 +156,186 @@ HXA_DEV void wait_stage(int wave) {
   wait_vm<LATER * loads_per_stage<BM, BN, FMT, ASYM, NW>(W)>();
 }
 
+// ---- epilogue after f16(acc) is staged in LDS as a row-major [BM][BN + 8] tile (and, for SPLIT2, the first K
+// half's tile after it): cooperative passes over 8-column chunks, coalesced 16-byte loads / stores.
+template <int BM, int BN, int NT, bool SPLIT2>
+HXA_DEV void gemm_epilogue(const GemmParams &p, const hxa_h *Cs, int m0, int n0, int tid, int z) {
+  constexpr int CROW = BN + 8;
+  constexpr int C8 = BN / 8;
+  if (p.epi == HXA_EPI_SITU) {
+    // columns interleaved per 32 (up_j, gate_j): output column (n0/2) + p*32 + c
+    for (int c = tid; c < BM * (C8 / 2); c += NT) {
+      const int ml = c / (C8 / 2), oc = (c % (C8 / 2)) * 8;
+      const int m = m0 + ml, on = n0 / 2 + oc;
+      if (m >= p.M || on * 2 >= p.N) continue;
+      const int pr = oc / 32, cc = oc % 32;
+      const half8_t u = *(const half8_t *)(Cs + ml * CROW + pr * 64 + cc);
+      const half8_t g = *(const half8_t *)(Cs + ml * CROW + pr * 64 + 32 + cc);
+      half8_t o;
+#pragma unroll
+      for (int e = 0; e < 8; e++) o[e] = (hxa_h)situ_f((float)u[e], (float)g[e]);
+      *(half8_t *)(p.out + (long)m * p.ldo + on) = o;
+    }
+    return;
+  }
+  // local columns [0, nsplit) row-major, [nsplit, BN) transposed into out_t. Without out_t the chunk count per row
+  // is the compile-time BN / 8 (no runtime division in the loop).
+  const int nsplit = p.out_t == nullptr ? BN : min(max(p.split_col - n0, 0), BN);
+  if (p.epi == HXA_EPI_RESADD) {
+    // x += gate * t: the x / gate loads of RB chunks are issued together before any of them is used, so a thread
+    // waits one memory latency per batch instead of one per chunk (x stores may alias later x loads otherwise)
+    constexpr int NC8 = BN / 8, ITERS = BM * NC8 / NT, RB = ITERS % 4 == 0 ? 4 : ITERS % 3 == 0 ? 3 : ITERS % 2 == 0 ? 2 : 1;
+    static_assert(BM * NC8 % NT == 0 && ITERS % RB == 0, "whole chunk passes");
+#pragma unroll
+    for (int b0 = 0; b0 < ITERS; b0 += RB) {
+      float4_t xv[RB][2], gv[RB][2];
+      float t[RB][8];
+      bool ok[RB];
+#pragma unroll
+      for (int u = 0; u < RB; u++) {
+        const int c = tid + (b0 + u) * NT, ml = c / NC8, nl = (c % NC8) * 8, m = m0 + ml, n = n0 + nl;
+        ok[u] = m < p.M && n < p.N;
+        if (ok[u]) {
+          const float4_t *xp = (const float4_t *)(p.x + (long)m * p.ldx + n);
+          xv[u][0] = xp[0];
+          xv[u][1] = xp[1];
+          gv[u][0] = *(const float4_t *)(p.gate + n);
+          gv[u][1] = *(const float4_t *)(p.gate + n + 4);
+          const half8_t v = *(const half8_t *)(Cs + ml * CROW + nl);
+#pragma unroll
+          for (int e = 0; e < 8; e++) t[u][e] = (float)v[e];
+          if constexpr (SPLIT2) {
+            const half8_t v1 = *(const half8_t *)(Cs + BM * CROW + ml * CROW + nl);
+#pragma unroll
+            for (int e = 0; e < 8; e++) t[u][e] = (float)v1[e] + t[u][e];
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < RB; u++) {
+        if (!ok[u]) continue;
+        const int c = tid + (b0 + u) * NT, ml = c / NC8, nl = (c % NC8) * 8;
+        float4_t *xp = (float4_t *)(p.x + (long)(m0 + ml) * p.ldx + n0 + nl);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          xv[u][0][e] = fmaf(gv[u][0][e], t[u][e], xv[u][0][e]);
+          xv[u][1][e] = fmaf(gv[u][1][e], t[u][e + 4], xv[u][1][e]);
+        }
+        xp[0] = xv[u][0];
+        xp[1] = xv[u][1];
+      }
+    }
+    return;
+  }
+  if constexpr (BN % 128 == 0) {
+  if (p.hn_cols > 0 && (n0 + BN <= p.hn_cols || p.hn_cols >= p.N)) {
+    // every (valid) column of this tile is head-normed. Thread (row group r0, jj) owns dims [8jj, 8jj+8) and
+    // [64+8jj, 64+8jj+8) of every head of the tile on its rows: the gains are loaded once, the RoPE coefficients once
+    // per row for all heads (fetched one pass ahead), and the rotation partners sit in the same thread.
+    constexpr int HT = BN / 128, RP = NT / 8;  // heads per tile, rows per pass
+    static_assert(BM % RP == 0, "whole passes");
+    const int jj = tid & 7, r0 = tid >> 3;
+    const bool rope = p.hn_cos != nullptr;
+    float glo[HT][8], ghi[HT][8], cs[8] = {}, sn[8] = {}, csn[8] = {}, snn[8] = {};
+#pragma unroll
+    for (int hh = 0; hh < HT; hh++) {
+      hn_gains(p, n0 + hh * 128 + 8 * jj, glo[hh]);
+      hn_gains(p, n0 + hh * 128 + 64 + 8 * jj, ghi[hh]);
+    }
+    // RoPE table row of the next pass's row, stepped by RP rows without a division (rows past M are not stored)
+    int tt = rope ? min(m0 + r0, p.M - 1) % p.hn_ttab : 0;
+    if (rope) hn_rope_t(p, tt, 8 * jj, cs, sn);
+    for (int it = 0; it < BM / RP; it++) {
+      const int ml = r0 + it * RP, m = m0 + ml;
+      if (rope && it + 1 < BM / RP) {
+        if (m + RP < p.M) {
+          tt += RP;
+          while (tt >= p.hn_ttab) tt -= p.hn_ttab;
+        }
+        hn_rope_t(p, tt, 8 * jj, csn, snn);
+      }
+      if (m < p.M) {  // whole 8-lane groups share m
+#pragma unroll
+        for (int hh = 0; hh < HT; hh++) {
+          const int nl = hh * 128 + 8 * jj;
+          if (n0 + nl >= p.N) break;
+          half8_t lo = *(const half8_t *)(Cs + ml * CROW + nl), hi = *(const half8_t *)(Cs + ml * CROW + nl + 64);
+          head_norm2(lo, hi, glo[hh], ghi[hh], rope, cs, sn);
+          *(half8_t *)(p.out + (long)m * p.ldo + n0 + nl) = lo;
+          *(half8_t *)(p.out + (long)m * p.ldo + n0 + nl + 64) = hi;
+        }
+      }
+      if (rope) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          cs[e] = csn[e];
+          sn[e] = snn[e];
+        }
+      }
+    }
+    return;
+  }
+  }
+  auto rows_pass = [&](auto ncols_c) {
+  const int nc8 = ncols_c / 8;
+  for (int c = tid; c < BM * nc8; c += NT) {
+    const int ml = c / nc8, nl = (c % nc8) * 8;
+    const int m = m0 + ml, n = n0 + nl;
+    if (m >= p.M || n >= p.N) continue;
+    half8_t v = *(const half8_t *)(Cs + ml * CROW + nl);
+    const long o = (long)m * p.ldo + n;
+    if (p.epi == HXA_EPI_PARTIAL) {
+      *(half8_t *)(p.out + (long)z * p.out_zstride + o) = v;
+    } else {
+      if (p.epi == HXA_EPI_GELU_TANH) {  // (head-normed tiles never get here: whole tiles take the path above)
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_tanh_f((float)v[e]);
+      } else if (p.epi == HXA_EPI_GELU_ERF) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_erf_f((float)v[e]);
+      }
+      *(half8_t *)(p.out + o) = v;
+    }
+  }
+  };
+  if (p.out_t == nullptr)
+    rows_pass(std::integral_constant<int, BN>{});
+  else
+    rows_pass(nsplit);
+  if (nsplit < BN) {
+    // transposed columns (a multiple of 32: split_col % 32 == 0): a thread takes 4 adjacent columns x 8 rows, read as
+    // 8-byte LDS words (consecutive threads -> consecutive words: no bank conflicts) and written as four 16-byte
+    // runs of 8 rows, one per output row n of out_t
+    const int ngrp = (BN - nsplit) / 4;
+    for (int c = tid; c < ngrp * (BM / 8); c += NT) {
+      const int nl = nsplit + (c % ngrp) * 4, ml = (c / ngrp) * 8;
+      const int m = m0 + ml;
+      if (m >= p.M) continue;
+      uint2_t w[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) w[e] = *(const uint2_t *)(Cs + (ml + e) * CROW + nl);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int n = n0 + nl + q;
+        if (n >= p.N) break;
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {  // rows 2k, 2k+1 of column q: halves (q & 1) of word (q >> 1)
+          const uint32_t a = (q >> 1) ? w[2 * k].y : w[2 * k].x, b = (q >> 1) ? w[2 * k + 1].y : w[2 * k + 1].x;
+          o[k] = __builtin_amdgcn_perm(b, a, (q & 1) ? 0x07060302u : 0x05040100u);
+        }
+        hxa_h *dst = p.out_t + (long)(n - p.split_col) * p.ldo_t + m;
+        if (m + 7 < p.M) {
+          *(uint4_t *)dst = (uint4_t){o[0], o[1], o[2], o[3]};
+        } else {
+          const half8_t v = __builtin_bit_cast(half8_t, (uint4_t){o[0], o[1], o[2], o[3]});
+          for (int e = 0; e < 8 && m + e < p.M; e++) dst[e] = v[e];
+        }
+      }
+    }
+  }
+}
+
 // SPLIT2: the first and second halves of K are rounded to fp16 separately and combined in the residual epilogue,
 // x += gate * (f16(first half) + f16(second half)) (blk.c:172-174 + kern.c:330-339 in one kernel): the first half's
 // f16 accumulators are kept in registers while the second half accumulates.
@@ -384,180 +564,156 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
         }
   }
   __syncthreads();
-  // Cooperative pass over 8-column chunks: coalesced 16-byte loads / stores.
-  constexpr int C8 = BN / 8;
-  if (p.epi == HXA_EPI_SITU) {
-    // columns interleaved per 32 (up_j, gate_j): output column (n0/2) + p*32 + c
-    for (int c = tid; c < BM * (C8 / 2); c += NT) {
-      const int ml = c / (C8 / 2), oc = (c % (C8 / 2)) * 8;
-      const int m = m0 + ml, on = n0 / 2 + oc;
-      if (m >= p.M || on * 2 >= p.N) continue;
-      const int pr = oc / 32, cc = oc % 32;
-      const half8_t u = *(const half8_t *)(Cs + ml * CROW + pr * 64 + cc);
-      const half8_t g = *(const half8_t *)(Cs + ml * CROW + pr * 64 + 32 + cc);
-      half8_t o;
+  gemm_epilogue<BM, BN, NT, SPLIT2>(p, Cs, m0, n0, tid, z);
+}
+
+// Ping-pong GEMM, fp16 weights, 8 waves: two groups of 4 (one wave of each per SIMD). Group g owns columns
+// [g BN/2, (g+1) BN/2) of the tile, its waves split them 2 x 2 (wave tile BM/2 x BN/4). The main loop runs in
+// phases separated by one s_barrier: in each phase one group issues the MFMAs of a stage on fragments already in
+// registers (s_setprio 1) while the other group reads the next stage's fragments from LDS -- group 1 also issues
+// the global -> LDS loads, three stages ahead -- so one wave per SIMD keeps the matrix core fed while its partner
+// waits on memory. Stage j: group 1 reads it in phase 2j and computes it in 2j+1; group 0 reads it in 2j+1 and
+// computes it in 2j+2. The LDS ring, stage layout and epilogue are those of gemm_kernel.
+template <int BM, int BN>
+__global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
+  using G = GemmGeo<BM, BN, HXA_W_F16>;
+  constexpr int NT = 512, NWG = 4;  // threads, waves per group
+  constexpr int WTM = BM / 2, WTN = BN / 4, MI = WTM / 32, NI = WTN / 32;
+  constexpr int BK = G::BK, NS = G::NS;
+  constexpr int NAI = BM / 16, TW = G::W_BYTES / 1024;       // 1 KB load instructions per stage (A, W)
+  constexpr int LPS = (NAI + TW + NWG - 1) / NWG;           // per group-1 wave and stage
+  static_assert(BM % 64 == 0 && WTN % 32 == 0 && NS == 4 && (NAI + TW) % NWG == 0 && NAI % NWG == 0, "tile shape");
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int bid = blockIdx.x;
+  const int tile = (ntiles % 8 == 0) ? (bid % 8) * (ntiles / 8) + bid / 8 : bid;
+  const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int z = blockIdx.z;
+  const int kbase = z * p.Kslice;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wl = wave & 3, wm = wl & 1, wn = wl >> 1;
+  const int nk = p.Kslice / BK;
+
+  // group 1: stage s <- k tile kt (clamped past the end: dummy reloads keep the vmcnt accounting constant)
+  auto issue = [&](int s, int kt) {
+    uint8_t *st = lds8 + s * G::STAGE;
+    const int k0 = kbase + min(kt, nk - 1) * BK;
+    const long og = (long)(k0 >> 5) * p.w_gs;
 #pragma unroll
-      for (int e = 0; e < 8; e++) o[e] = (hxa_h)situ_f((float)u[e], (float)g[e]);
-      *(half8_t *)(p.out + (long)m * p.ldo + on) = o;
-    }
-    return;
-  }
-  // local columns [0, nsplit) row-major, [nsplit, BN) transposed into out_t. Without out_t the chunk count per row
-  // is the compile-time BN / 8 (no runtime division in the loop).
-  const int nsplit = p.out_t == nullptr ? BN : min(max(p.split_col - n0, 0), BN);
-  if (p.epi == HXA_EPI_RESADD) {
-    // x += gate * t: the x / gate loads of RB chunks are issued together before any of them is used, so a thread
-    // waits one memory latency per batch instead of one per chunk (x stores may alias later x loads otherwise)
-    constexpr int NC8 = BN / 8, ITERS = BM * NC8 / NT, RB = ITERS % 4 == 0 ? 4 : ITERS % 3 == 0 ? 3 : ITERS % 2 == 0 ? 2 : 1;
-    static_assert(BM * NC8 % NT == 0 && ITERS % RB == 0, "whole chunk passes");
-#pragma unroll
-    for (int b0 = 0; b0 < ITERS; b0 += RB) {
-      float4_t xv[RB][2], gv[RB][2];
-      float t[RB][8];
-      bool ok[RB];
-#pragma unroll
-      for (int u = 0; u < RB; u++) {
-        const int c = tid + (b0 + u) * NT, ml = c / NC8, nl = (c % NC8) * 8, m = m0 + ml, n = n0 + nl;
-        ok[u] = m < p.M && n < p.N;
-        if (ok[u]) {
-          const float4_t *xp = (const float4_t *)(p.x + (long)m * p.ldx + n);
-          xv[u][0] = xp[0];
-          xv[u][1] = xp[1];
-          gv[u][0] = *(const float4_t *)(p.gate + n);
-          gv[u][1] = *(const float4_t *)(p.gate + n + 4);
-          const half8_t v = *(const half8_t *)(Cs + ml * CROW + nl);
-#pragma unroll
-          for (int e = 0; e < 8; e++) t[u][e] = (float)v[e];
-          if constexpr (SPLIT2) {
-            const half8_t v1 = *(const half8_t *)(Cs + BM * CROW + ml * CROW + nl);
-#pragma unroll
-            for (int e = 0; e < 8; e++) t[u][e] = (float)v1[e] + t[u][e];
-          }
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < RB; u++) {
-        if (!ok[u]) continue;
-        const int c = tid + (b0 + u) * NT, ml = c / NC8, nl = (c % NC8) * 8;
-        float4_t *xp = (float4_t *)(p.x + (long)(m0 + ml) * p.ldx + n0 + nl);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          xv[u][0][e] = fmaf(gv[u][0][e], t[u][e], xv[u][0][e]);
-          xv[u][1][e] = fmaf(gv[u][1][e], t[u][e + 4], xv[u][1][e]);
-        }
-        xp[0] = xv[u][0];
-        xp[1] = xv[u][1];
+    for (int t0 = 0; t0 < NAI + TW; t0 += NWG) {
+      const int t = t0 + wl;
+      if (t < NAI) {
+        const int r0 = t * 16, row = r0 + (lane >> 2);
+        const int cl = (lane & 3) ^ ((row >> 2) & 3);
+        const int m = min(m0 + row, p.M - 1);
+        g2l16_opaque(p.A + (long)m * p.lda + k0 + cl * 8, st + r0 * 64);
+      } else {
+        const int tw = t - NAI, chunk = tw * 64 + lane;
+        const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3), n = min(n0 + row, p.N - 1);
+        g2l16_opaque((const hxa_h *)p.W + n * p.w_rs + og + cl * 8, st + G::A_BYTES + tw * 1024);
       }
     }
-    return;
-  }
-  if constexpr (BN % 128 == 0) {
-  if (p.hn_cols > 0 && (n0 + BN <= p.hn_cols || p.hn_cols >= p.N)) {
-    // every (valid) column of this tile is head-normed. Thread (row group r0, jj) owns dims [8jj, 8jj+8) and
-    // [64+8jj, 64+8jj+8) of every head of the tile on its rows: the gains are loaded once, the RoPE coefficients once
-    // per row for all heads (fetched one pass ahead), and the rotation partners sit in the same thread.
-    constexpr int HT = BN / 128, RP = NT / 8;  // heads per tile, rows per pass
-    static_assert(BM % RP == 0, "whole passes");
-    const int jj = tid & 7, r0 = tid >> 3;
-    const bool rope = p.hn_cos != nullptr;
-    float glo[HT][8], ghi[HT][8], cs[8] = {}, sn[8] = {}, csn[8] = {}, snn[8] = {};
-#pragma unroll
-    for (int hh = 0; hh < HT; hh++) {
-      hn_gains(p, n0 + hh * 128 + 8 * jj, glo[hh]);
-      hn_gains(p, n0 + hh * 128 + 64 + 8 * jj, ghi[hh]);
-    }
-    // RoPE table row of the next pass's row, stepped by RP rows without a division (rows past M are not stored)
-    int tt = rope ? min(m0 + r0, p.M - 1) % p.hn_ttab : 0;
-    if (rope) hn_rope_t(p, tt, 8 * jj, cs, sn);
-    for (int it = 0; it < BM / RP; it++) {
-      const int ml = r0 + it * RP, m = m0 + ml;
-      if (rope && it + 1 < BM / RP) {
-        if (m + RP < p.M) {
-          tt += RP;
-          while (tt >= p.hn_ttab) tt -= p.hn_ttab;
-        }
-        hn_rope_t(p, tt, 8 * jj, csn, snn);
-      }
-      if (m < p.M) {  // whole 8-lane groups share m
-#pragma unroll
-        for (int hh = 0; hh < HT; hh++) {
-          const int nl = hh * 128 + 8 * jj;
-          if (n0 + nl >= p.N) break;
-          half8_t lo = *(const half8_t *)(Cs + ml * CROW + nl), hi = *(const half8_t *)(Cs + ml * CROW + nl + 64);
-          head_norm2(lo, hi, glo[hh], ghi[hh], rope, cs, sn);
-          *(half8_t *)(p.out + (long)m * p.ldo + n0 + nl) = lo;
-          *(half8_t *)(p.out + (long)m * p.ldo + n0 + nl + 64) = hi;
-        }
-      }
-      if (rope) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          cs[e] = csn[e];
-          sn[e] = snn[e];
-        }
-      }
-    }
-    return;
-  }
-  }
-  auto rows_pass = [&](auto ncols_c) {
-  const int nc8 = ncols_c / 8;
-  for (int c = tid; c < BM * nc8; c += NT) {
-    const int ml = c / nc8, nl = (c % nc8) * 8;
-    const int m = m0 + ml, n = n0 + nl;
-    if (m >= p.M || n >= p.N) continue;
-    half8_t v = *(const half8_t *)(Cs + ml * CROW + nl);
-    const long o = (long)m * p.ldo + n;
-    if (p.epi == HXA_EPI_PARTIAL) {
-      *(half8_t *)(p.out + (long)z * p.out_zstride + o) = v;
-    } else {
-      if (p.epi == HXA_EPI_GELU_TANH) {  // (head-normed tiles never get here: whole tiles take the path above)
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_tanh_f((float)v[e]);
-      } else if (p.epi == HXA_EPI_GELU_ERF) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_erf_f((float)v[e]);
-      }
-      *(half8_t *)(p.out + o) = v;
-    }
-  }
   };
-  if (p.out_t == nullptr)
-    rows_pass(std::integral_constant<int, BN>{});
-  else
-    rows_pass(nsplit);
-  if (nsplit < BN) {
-    // transposed columns (a multiple of 32: split_col % 32 == 0): a thread takes 4 adjacent columns x 8 rows, read as
-    // 8-byte LDS words (consecutive threads -> consecutive words: no bank conflicts) and written as four 16-byte
-    // runs of 8 rows, one per output row n of out_t
-    const int ngrp = (BN - nsplit) / 4;
-    for (int c = tid; c < ngrp * (BM / 8); c += NT) {
-      const int nl = nsplit + (c % ngrp) * 4, ml = (c / ngrp) * 8;
-      const int m = m0 + ml;
-      if (m >= p.M) continue;
-      uint2_t w[8];
+  auto read_frags = [&](int s, half8_t (&fa)[2][MI], half8_t (&fb)[2][NI]) {
+    const uint8_t *st = lds8 + s * G::STAGE;
+    const uint8_t *ws = st + G::A_BYTES;
 #pragma unroll
-      for (int e = 0; e < 8; e++) w[e] = *(const uint2_t *)(Cs + (ml + e) * CROW + nl);
+    for (int ks = 0; ks < 2; ks++) {
+      const int cl = ks * 2 + (lane >> 5);
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int n = n0 + nl + q;
-        if (n >= p.N) break;
-        uint32_t o[4];
+      for (int i = 0; i < MI; i++) {
+        const int row = wm * WTM + i * 32 + (lane & 31);
+        fa[ks][i] = *(const half8_t *)(st + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
+      }
 #pragma unroll
-        for (int k = 0; k < 4; k++) {  // rows 2k, 2k+1 of column q: halves (q & 1) of word (q >> 1)
-          const uint32_t a = (q >> 1) ? w[2 * k].y : w[2 * k].x, b = (q >> 1) ? w[2 * k + 1].y : w[2 * k + 1].x;
-          o[k] = __builtin_amdgcn_perm(b, a, (q & 1) ? 0x07060302u : 0x05040100u);
-        }
-        hxa_h *dst = p.out_t + (long)(n - p.split_col) * p.ldo_t + m;
-        if (m + 7 < p.M) {
-          *(uint4_t *)dst = (uint4_t){o[0], o[1], o[2], o[3]};
-        } else {
-          const half8_t v = __builtin_bit_cast(half8_t, (uint4_t){o[0], o[1], o[2], o[3]});
-          for (int e = 0; e < 8 && m + e < p.M; e++) dst[e] = v[e];
-        }
+      for (int j = 0; j < NI; j++) {
+        const int row = grp * (BN / 2) + wn * WTN + j * 32 + (lane & 31);
+        fb[ks][j] = *(const half8_t *)(ws + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
       }
     }
+  };
+  float16_t acc[NI][MI];
+#pragma unroll
+  for (int j = 0; j < NI; j++)
+#pragma unroll
+    for (int i = 0; i < MI; i++) acc[j][i] = (float16_t){};
+  auto mfmas = [&](const half8_t (&fa)[2][MI], const half8_t (&fb)[2][NI]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+      for (int j = 0; j < NI; j++)
+#pragma unroll
+        for (int i = 0; i < MI; i++) acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[ks][j], fa[ks][i], acc[j][i], 0, 0, 0);
+  };
+  auto bar = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // each group runs its own loop (one fragment buffer: read in one phase, consumed in the next); both loops pass
+  // the same barriers, two per stage
+  half8_t fa[2][MI], fb[2][NI];
+  if (grp == 1) {
+#pragma unroll
+    for (int s = 0; s < NS; s++) issue(s, s);
+    wait_vm<(NS - 1) * LPS>();  // stage 0 landed
+    bar();
+    for (int j = 0; j < nk; j++) {
+      // phase 2j: read stage j, load stage j+3 into the buffer of stage j-1 (read by both groups by now)
+      read_frags(j % NS, fa, fb);
+      if (j >= 1) issue((j + NS - 1) % NS, j + NS - 1);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the fragments are in registers
+      bar();
+      // phase 2j+1: compute stage j, then wait for stage j+1 (stages j+2, j+3 may still fly)
+      __builtin_amdgcn_s_setprio(1);
+      mfmas(fa, fb);
+      __builtin_amdgcn_s_setprio(0);
+      wait_vm<2 * LPS>();
+      bar();
+    }
+  } else {
+    bar();
+    for (int j = 0; j < nk; j++) {
+      // phase 2j: compute stage j-1
+      if (j >= 1) {
+        __builtin_amdgcn_s_setprio(1);
+        mfmas(fa, fb);
+        __builtin_amdgcn_s_setprio(0);
+      }
+      bar();
+      // phase 2j+1: read stage j
+      read_frags(j % NS, fa, fb);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      bar();
+    }
+    // phase 2 nk: compute stage nk-1
+    mfmas(fa, fb);
   }
+  wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
+  __syncthreads();
+
+  constexpr int CROW = G::CROW;
+  hxa_h *Cs = (hxa_h *)lds8;
+  {
+    const int ml = wm * WTM + (lane & 31), nl = grp * (BN / 2) + wn * WTN + 4 * (lane >> 5);
+#pragma unroll
+    for (int j = 0; j < NI; j++)
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const half4_t v = {(hxa_h)acc[j][i][4 * q], (hxa_h)acc[j][i][4 * q + 1], (hxa_h)acc[j][i][4 * q + 2],
+                             (hxa_h)acc[j][i][4 * q + 3]};
+          *(half4_t *)(Cs + (ml + i * 32) * CROW + nl + j * 32 + 8 * q) = v;
+        }
+  }
+  __syncthreads();
+  gemm_epilogue<BM, BN, NT, false>(p, Cs, m0, n0, tid, z);
 }
 
 struct TileCfg {
@@ -565,9 +721,17 @@ struct TileCfg {
 };
 // fp16 weights take the 4-wave tiles; int8 / int4 weights the 8-wave ones (two waves per SIMD: the dequantisation
 // registers of a 4-wave tile crowd out the fragment double-buffering, measured 13-18% slower at M = 1536)
+// fp16 weights with M >= 4096 and N >= 8192 take the 256x256 ping-pong tile (nw 9; 13% faster on the MLP-up at
+// 6144 tokens, no faster elsewhere).
 constexpr TileCfg kCfgs[] = {{192, 256, 4}, {192, 192, 4}, {192, 128, 4}, {256, 128, 4}, {128, 256, 4},
                              {128, 128, 4}, {64, 128, 4},  {128, 64, 4},  {192, 256, 8}, {128, 256, 8},
                              {192, 128, 8}, {128, 128, 8}};
+// relative MFMA efficiency of a full grid of each tile (LDS traffic per MFMA grows as the tile shrinks): ranks tiles
+// whose CU fill is (nearly) the same
+static double tile_eff(int bm, int bn) {
+  const int a = bm * bn;
+  return a >= 192 * 256 ? 1.0 : a >= 128 * 256 ? 0.97 : a >= 192 * 128 ? 0.95 : a >= 128 * 128 ? 0.92 : 0.75;
+}
 
 template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false, int NW = 4>
 hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
@@ -592,8 +756,32 @@ hipError_t launch_split2(int bm, int bn, const GemmParams &p, hipStream_t st) {
   return hipErrorInvalidValue;
 }
 
+template <int BM, int BN>
+hipError_t launch_pp(const GemmParams &p, int ksplit, hipStream_t st) {
+  auto kern = gemm_pp_kernel<BM, BN>;
+  using G = GemmGeo<BM, BN, HXA_W_F16>;
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  dim3 grid(p.tiles_m * p.tiles_n, 1, ksplit);
+  hipLaunchKernelGGL(kern, grid, dim3(512), G::LDS, st, p);
+  return hipGetLastError();
+}
+
 template <int FMT, bool ASYM>
 hipError_t launch_fmt(int bm, int bn, int nw, const GemmParams &p, int ksplit, hipStream_t st) {
+  if (nw == 9) {  // ping-pong 8 waves (fp16 weights)
+    if constexpr (FMT == HXA_W_F16) {
+      if (bm == 192 && bn == 256) return launch_pp<192, 256>(p, ksplit, st);
+      if (bm == 256 && bn == 256) return launch_pp<256, 256>(p, ksplit, st);
+      if (bm == 128 && bn == 256) return launch_pp<128, 256>(p, ksplit, st);
+      if (bm == 128 && bn == 128) return launch_pp<128, 128>(p, ksplit, st);
+    }
+    return hipErrorInvalidValue;
+  }
   if (nw == 8) {
     if (bm == 192 && bn == 256) return launch_t<192, 256, FMT, ASYM, false, 8>(p, ksplit, st);
     if (bm == 192 && bn == 128) return launch_t<192, 128, FMT, ASYM, false, 8>(p, ksplit, st);
@@ -640,13 +828,19 @@ static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int hn_cols, i
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ksplit;
     const long waves = (tiles + g_num_cu - 1) / g_num_cu;
     const double useful = (double)M * N / ((double)((M + c.bm - 1) / c.bm) * c.bm * ((N + c.bn - 1) / c.bn) * c.bn);
-    const double eff = useful * (double)tiles / (double)(waves * g_num_cu) * (c.bm * c.bn >= 128 * 128 ? 1.0 : 0.8);
+    const double eff = useful * (double)tiles / (double)(waves * g_num_cu) * tile_eff(c.bm, c.bn);
     if (eff > best + 1e-9) {
       best = eff;
       *bm = c.bm;
       *bn = c.bn;
       *nw = c.nw;
     }
+  }
+  if (fmt == HXA_W_F16 && M >= 4096 && N >= 8192 && ksplit == 1 && !headnorm &&
+      (epi == HXA_EPI_STORE || epi == HXA_EPI_GELU_TANH || epi == HXA_EPI_GELU_ERF || epi == HXA_EPI_SITU)) {
+    *bm = 256;
+    *bn = 256;
+    *nw = 9;
   }
 }
 
@@ -719,7 +913,7 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
     bm = g.force_bm;
     bn = g.force_bn;
     nw = g.force_nw ? g.force_nw : 4;
-    if (nw != 4 && (nw != 8 || split2)) return HXA_E_ARG;
+    if (nw != 4 && ((nw != 8 && nw != 9) || split2)) return HXA_E_ARG;
     if ((g.epi == HXA_EPI_SITU && bn % 128 != 0) || (w.fmt == HXA_W_Q4 && bn < 128)) return HXA_E_ARG;
     if (split2 && !(bn == 128 && (bm == 128 || bm == 64))) return HXA_E_ARG;
     if (headnorm && (bn % 128 != 0 || (p.hn_cols % bn != 0 && p.hn_cols < w.N))) return HXA_E_ARG;

@@ -54,8 +54,9 @@ def _run_gemm(hip, A, fmt, w, s, N, K, epi=0, ksplit=1, tile=None, x=None, gate=
     return dx.numpy() if resadd else out.numpy()
 
 
+# waves 9: the ping-pong 8-wave kernel
 @pytest.mark.parametrize("tile", [None, (192, 256), (192, 256, 8), (192, 192), (192, 128), (256, 128), (128, 256), (128, 128),
-                                  (64, 128), (128, 64)])
+                                  (64, 128), (128, 64), (192, 256, 9), (256, 256, 9), (128, 256, 9), (128, 128, 9)])
 def test_gemm_f16_tiles(tile):
     hip = _hip()
     say(f"gemm f16 tile={tile}")
@@ -181,7 +182,8 @@ def test_gemm_resadd_split2_matches_partial_then_resadd2(fmt, tile):
 
 @pytest.mark.parametrize("fmt,tile,epi,ksplit", [(0, None, 0, 1), (0, (192, 256, 8), 0, 1), (0, (64, 128), 0, 1),
                                                 (0, None, 6, 2), (1, None, 0, 1), (1, (128, 64), 0, 1), (2, None, 0, 1),
-                                                (2, None, 6, 2), (0, None, 7, 1), (1, None, 3, 1)])
+                                                (2, None, 6, 2), (0, None, 7, 1), (1, None, 3, 1), (0, (192, 256, 9), 1, 1),
+                                                (0, (192, 256, 9), 6, 2), (0, (128, 128, 9), 3, 1), (0, (256, 256, 9), 0, 1)])
 def test_gemm_ktiled_weights_equal_row_major(fmt, tile, epi, ksplit):
     """W stored k-tiled ([K/32][N][chunk], the block-pack layout) gives the same bits as W row-major, for every
     format, tile family and split-K form; N is ragged against the 256-wide tiles."""
