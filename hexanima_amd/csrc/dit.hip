@@ -188,10 +188,18 @@ int record_step(Dit &d, int mode) {
       DTRY(hxa_gemm_launch(g, st));
     }
   }
-  // blocks
+  // blocks, chained: each block's MLP residual (x += gate * (t1 + t2), blk.c:172-174) is applied by the next
+  // block's first norm, which reads x anyway; the last one is applied here
+  auto mlp_gate = [&](int k) { return b.kind == 0 ? d.mods + (long)k * 9 * D + 8L * D : d.mods + 5L * D; };
   for (int k = 0; k < nb; k++) {
     const float *mod = b.kind == 0 ? d.mods + (long)k * 9 * D : d.mods;
-    DTRY(hxa_block_run(&d.bd, d.packs[k], d.x, b.kind == 0 ? d.ctx16 : nullptr, mod, d.cosT, d.sinT, d.ws, 0, nullptr, 0, st));
+    DTRY(hxa_block_run_chained(&d.bd, d.packs[k], d.x, b.kind == 0 ? d.ctx16 : nullptr, mod, d.cosT, d.sinT, d.ws, 0,
+                               nullptr, 0, st, k > 0 ? mlp_gate(k - 1) : nullptr, 1));
+  }
+  {
+    long ld = 0;
+    const hxa_h *t1 = (const hxa_h *)hxa_block_ws_buf(&d.bd, d.ws, 5, &ld), *t2 = (const hxa_h *)hxa_block_ws_buf(&d.bd, d.ws, 9, &ld);
+    DTRY(hxa_resadd2_launch(d.x, D, t1, t2, ld, B * d.Ttot, D, mlp_gate(nb - 1), st));
   }
   // final layer (+ Euler update)
   DTRY(hxa_final_launch(d.x, B, d.Timg, d.Ttot, D, d.fmod, d.fmod + D, d.Wfin, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w,

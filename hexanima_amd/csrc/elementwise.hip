@@ -25,29 +25,53 @@ HXA_DEV float wave_sum(float v) {
 // modulated norm (kern.c:31-65 LN-mod; moss kern.c:345-375 RMS-mod)
 // ---------------------------------------------------------------------------------------------------------------
 // With t != NULL the pending gated residual of the previous site is applied first, x += gate * t (kern.c:320-328,
-// the same fma as the GEMM residual epilogue), x is written back, and the norm is taken of the updated row.
+// the same fma as the GEMM residual epilogue), or with t2 as well x += gate * (t + t2) (kern.c:330-339, the same
+// fma as resadd2_kernel); x is written back, and the norm is taken of the updated row.
 template <int VPL>
 __global__ __launch_bounds__(256) void normmod_kernel(float *__restrict__ x, long ldx, int T, int D,
-                                                      const hxa_h *__restrict__ t, long ldt, const float *__restrict__ gate,
+                                                      const hxa_h *__restrict__ t, const hxa_h *__restrict__ t2,
+                                                      long ldt, const float *__restrict__ gate,
                                                       const float *__restrict__ shift, const float *__restrict__ scale,
                                                       const float *__restrict__ w, float eps, hxa_h *__restrict__ h,
                                                       long ldh) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= T) return;
   float4_t *xr = (float4_t *)(x + (long)row * ldx);
-  float4_t v[VPL];
+  float4_t v[VPL], mul[VPL], sh[VPL];
   float s = 0.0f, q = 0.0f;
+  // every load is issued up front (row, residual, per-column vectors): one memory latency per row
 #pragma unroll
   for (int i = 0; i < VPL; i++) v[i] = xr[lane + 64 * i];
+  half4_t tv[VPL], tv2[VPL];
+  float4_t gv[VPL];
   if (t != nullptr) {
-    half4_t tv[VPL];
-#pragma unroll
-    for (int i = 0; i < VPL; i++) tv[i] = *(const half4_t *)(t + (long)row * ldt + (lane + 64 * i) * 4);
 #pragma unroll
     for (int i = 0; i < VPL; i++) {
-      const float4_t g = *(const float4_t *)(gate + (lane + 64 * i) * 4);
+      tv[i] = *(const half4_t *)(t + (long)row * ldt + (lane + 64 * i) * 4);
+      gv[i] = *(const float4_t *)(gate + (lane + 64 * i) * 4);
+    }
+    if (t2 != nullptr) {
 #pragma unroll
-      for (int e = 0; e < 4; e++) v[i][e] = fmaf(g[e], (float)tv[i][e], v[i][e]);
+      for (int i = 0; i < VPL; i++) tv2[i] = *(const half4_t *)(t2 + (long)row * ldt + (lane + 64 * i) * 4);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; i++) {
+    const int c = (lane + 64 * i) * 4;
+    mul[i] = *(const float4_t *)(scale + c) + 1.0f;
+    sh[i] = *(const float4_t *)(shift + c);
+    if (w != nullptr) mul[i] *= *(const float4_t *)(w + c);  // k_rms_prep: M = (1 + scale) * w
+  }
+  if (t != nullptr) {
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+      if (t2 != nullptr) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[i][e] = fmaf(gv[i][e], (float)tv[i][e] + (float)tv2[i][e], v[i][e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[i][e] = fmaf(gv[i][e], (float)tv[i][e], v[i][e]);
+      }
       xr[lane + 64 * i] = v[i];
     }
   }
@@ -70,12 +94,9 @@ __global__ __launch_bounds__(256) void normmod_kernel(float *__restrict__ x, lon
 #pragma unroll
   for (int i = 0; i < VPL; i++) {
     const int c = (lane + 64 * i) * 4;
-    const float4_t sc = *(const float4_t *)(scale + c), sh = *(const float4_t *)(shift + c);
-    float4_t mul = sc + 1.0f;
-    if (w != nullptr) mul *= *(const float4_t *)(w + c);  // k_rms_prep: M = (1 + scale) * w
     half4_t o;
 #pragma unroll
-    for (int e = 0; e < 4; e++) o[e] = (hxa_h)((v[i][e] - mu) * r * mul[e] + sh[e]);
+    for (int e = 0; e < 4; e++) o[e] = (hxa_h)((v[i][e] - mu) * r * mul[i][e] + sh[i][e]);
     *(half4_t *)(h + (long)row * ldh + c) = o;
   }
 }
@@ -511,12 +532,17 @@ inline unsigned nblk(long n, int per = 256) { return (unsigned)((n + per - 1) / 
 int hxa_resid_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, long ldt, const float *gate,
                               const float *shift, const float *scale, const float *w, float eps, hxa_h *h, long ldh,
                               hipStream_t st) {
-  if (T <= 0 || D % 256 != 0 || ldx % 4 || ldh % 4 || (t && (ldt % 4 || !gate))) return HXA_E_ARG;
+  return hxa_resid2_norm_mod_launch(x, ldx, T, D, t, nullptr, ldt, gate, shift, scale, w, eps, h, ldh, st);
+}
+int hxa_resid2_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, const hxa_h *t2, long ldt,
+                               const float *gate, const float *shift, const float *scale, const float *w, float eps,
+                               hxa_h *h, long ldh, hipStream_t st) {
+  if (T <= 0 || D % 256 != 0 || ldx % 4 || ldh % 4 || (t && (ldt % 4 || !gate)) || (t2 && !t)) return HXA_E_ARG;
   const int vpl = D / 256;
   dim3 g(nblk(T, 4)), b(256);
   switch (vpl) {
 #define HXA_NORMMOD(V) \
-  case V: hipLaunchKernelGGL(normmod_kernel<V>, g, b, 0, st, x, ldx, T, D, t, ldt, gate, shift, scale, w, eps, h, ldh); break;
+  case V: hipLaunchKernelGGL(normmod_kernel<V>, g, b, 0, st, x, ldx, T, D, t, t2, ldt, gate, shift, scale, w, eps, h, ldh); break;
     HXA_NORMMOD(1) HXA_NORMMOD(2) HXA_NORMMOD(4) HXA_NORMMOD(8) HXA_NORMMOD(10) HXA_NORMMOD(12) HXA_NORMMOD(16)
 #undef HXA_NORMMOD
     default:

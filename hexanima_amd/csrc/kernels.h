@@ -42,6 +42,10 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st);
 int hxa_resid_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, long ldt, const float *gate,
                               const float *shift, const float *scale, const float *w, float eps, hxa_h *h, long ldh,
                               hipStream_t st);
+// the same with two pending fp16 terms: x += gate * (t + t2) (t2 NULL: the single-term form)
+int hxa_resid2_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, const hxa_h *t2, long ldt,
+                               const float *gate, const float *shift, const float *scale, const float *w, float eps,
+                               hxa_h *h, long ldh, hipStream_t st);
 int hxa_norm_mod_launch(const float *x, long ldx, int T, int D, const float *shift, const float *scale, const float *w,
                         float eps, hxa_h *h, long ldh, hipStream_t st);
 // per-head RMSNorm * gain (+ RoPE on pairs (d, d+64)) in place for ntens tensors sharing a layout
@@ -65,7 +69,7 @@ int hxa_fill_const_launch(void *dst, int dtype, size_t n, float v, hipStream_t s
 
 // caller-side glue (phone/animad.cpp)
 int hxa_patchify_launch(const float *lat, int B, int Cc, int H, int W, float *tok, hipStream_t st);
-// M <= 8: GEMV (one wave per output; output index n -> n + gap for n >= split); M > 8: K <= 64 (patch embed)
+// M <= 8: GEMV (one wave per output; output index n -> n + gap for n >= split); M > 8: small-K tiles (patch embed)
 // stacked GEMV: y[(n / per) * ostride + r + (r >= split ? gap : 0)] = sum_k act(x[k]) W[n][k], r = n % per;
 // K % 256 == 0, K <= 4096; act 1 = SiLU on the input
 int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, int per, long ostride, int split, int gap,
@@ -82,5 +86,9 @@ int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t 
 // matrix shapes of a GPU block pack (see hxa_pack_layout); returns the matrix count
 int hxa_pack_mats(int kind, int D, int F, int DC, int fa, int fm, int *N, int *K, int *fmt);
 
-// read-only pass over [p, p + bytes): one 16-byte word every `stride` bytes, nblocks workgroups (warms the memory-side
-// cache with stride 16, only address translation with a page stride)
+// hxa_block_run for a chain of blocks: pend_gate != NULL applies the previous block's pending MLP residual
+// (x += pend_gate * (t1 + t2) from the workspace) in the first norm; defer != 0 leaves this block's MLP residual
+// pending in t1 / t2
+int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
+                          const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
+                          void *stream, const float *pend_gate, int defer);

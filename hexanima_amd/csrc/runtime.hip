@@ -450,7 +450,18 @@ struct StageTimer {
 extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
                              const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
                              void *stream) {
+  return hxa_block_run_chained(d, pack, x, ctx, mod, cosT, sinT, ws, stop, stage_us, nstage, stream, nullptr, 0);
+}
+
+// pend_gate != NULL: the previous block of a chain left its MLP residual pending (its two fp16 down-projection
+// halves in this workspace's t1 / t2); the first norm applies x += pend_gate * (t1 + t2), resadd2's fma, before
+// normalising. defer != 0: this block leaves its own MLP residual pending the same way (the caller applies it to
+// the last block of the chain). Without a stage stop only.
+int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
+                          const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
+                          void *stream, const float *pend_gate, int defer) {
   g_err[0] = 0;
+  if ((pend_gate || defer) && stop) return fail(HXA_E_ARG, "block: chained residuals need stop == 0");
   TRY(check_dims(d));
   if (!pack || !x || !mod || !ws || (d->kind == 0 && !ctx)) return fail(HXA_E_ARG, "block: null pointer");
   hipStream_t st = S(stream);
@@ -523,7 +534,7 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
   // 128-wide tiles leave a quarter of the CUs idle at 1536 x 2048
   auto down_resadd = [&](const hxa_h *a, const HxaWeight &w, const float *gate) -> int {
     TRY(gemm(a, F, BT, w, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
-    return hxa_resadd2_launch(x, D, t1, t2, D, BT, D, gate, st);
+    return defer ? HXA_OK : hxa_resadd2_launch(x, D, t1, t2, D, BT, D, gate, st);
   };
   if (d->kind == 0) {
     const float *gain = pv.vec;
@@ -532,7 +543,8 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     const int BC = B * d->C;
     hxa_h *ck = (hxa_h *)(w8 + L.off[WS_CK]), *cvT = (hxa_h *)(w8 + L.off[WS_CVT]);
     // site 0: self-attention (blk.c:157-162)
-    TRY(hxa_norm_mod_launch(x, D, BT, D, mod, mod + D, nullptr, 1e-6f, h, D, st));
+    TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, pend_gate ? t1 : nullptr, pend_gate ? t2 : nullptr, D, pend_gate, mod,
+                                   mod + D, nullptr, 1e-6f, h, D, st));
     STAGE_DONE();
     // q, k: RMSNorm * gain + RoPE (blk.c:159-160), fused into the projection's store unless a stage dump needs the
     // un-normalised projections (M_STOP)
@@ -580,7 +592,8 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
     const float *gq = pv.vec, *gk = pv.vec + 128, *n1 = pv.vec + 256, *n2 = pv.vec + 256 + D;
     const HxaWeight &Wqkv = pv.w[0], &Wo = pv.w[1], &Wug = pv.w[2], &Wdn = pv.w[3];
     // attention half (moss blk.c:234-247)
-    TRY(hxa_norm_mod_launch(x, D, BT, D, mod, mod + D, n1, 1e-6f, h, D, st));
+    TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, pend_gate ? t1 : nullptr, pend_gate ? t2 : nullptr, D, pend_gate, mod,
+                                   mod + D, n1, 1e-6f, h, D, st));
     STAGE_DONE();
     STAGE_DONE();  // the reference's LoRA-A GEMM stage (no LoRA)
     hn = HeadNorm{2 * D, gq, gk, D, cosT, sinT};  // q, k: RMSNorm * gain + RoPE in the GEMM (moss blk.c:239-242, mode 3)
