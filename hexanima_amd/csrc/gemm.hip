@@ -341,8 +341,8 @@ HXA_DEV void gemm_epilogue(const GemmParams &p, const hxa_h *Cs, int m0, int n0,
 // f16 accumulators are kept in registers while the second half accumulates.
 // NW = 4 waves (2 x 2 grid, one wave per SIMD) or 8 waves (2 x 4 grid, two waves per SIMD: one wave's waits are
 // covered by the other's MFMAs).
-template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false, int NW = 4>
-__global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
+template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2, int NW>
+HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   using G = GemmGeo<BM, BN, FMT>;
   constexpr int NT = 64 * NW;
   constexpr int WTM = BM / 2, WTN = BN / (NW / 2), MI = WTM / 32, NI = WTN / 32;
@@ -351,11 +351,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
 
   const int ntiles = p.tiles_m * p.tiles_n;
-  const int bid = blockIdx.x;
   const int tile = (ntiles % 8 == 0) ? (bid % 8) * (ntiles / 8) + bid / 8 : bid;
   const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int z = blockIdx.z;
   const int kbase = z * p.Kslice;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
@@ -565,6 +563,18 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
   }
   __syncthreads();
   gemm_epilogue<BM, BN, NT, SPLIT2>(p, Cs, m0, n0, tid, z);
+}
+
+template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
+  gemm_body<BM, BN, FMT, ASYM, SPLIT2, NW>(p, blockIdx.x, blockIdx.z);
+}
+// two independent GEMMs of the same tile shape and weight format in one launch: workgroups [0, nwg0) run p0,
+// the rest p1 (nwg0 a multiple of 8 keeps each GEMM's XCD placement)
+template <int BM, int BN, int FMT, bool ASYM, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void gemm_pair_kernel(GemmParams p0, GemmParams p1, int nwg0) {
+  if ((int)blockIdx.x < nwg0) gemm_body<BM, BN, FMT, ASYM, false, NW>(p0, blockIdx.x, 0);
+  else gemm_body<BM, BN, FMT, ASYM, false, NW>(p1, blockIdx.x - nwg0, 0);
 }
 
 // Ping-pong GEMM, fp16 weights, 8 waves: two groups of 4 (one wave of each per SIMD). Group g owns columns
@@ -844,8 +854,9 @@ static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int hn_cols, i
   }
 }
 
-int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
-  HxaWeight w = *g.w;
+// validate a GEMM description, fill its kernel parameters and choose (or take the forced) tile
+static int gemm_prepare(const HxaGemm &g, GemmParams &p, int &bm, int &bn, int &nw, HxaWeight &w, bool &split2) {
+  w = *g.w;
   const int wkt = (w.fmt & HXA_W_KTILED) ? 1 : 0;
   w.fmt &= ~HXA_W_KTILED;
   if (g.M <= 0 || w.N <= 0 || w.K <= 0 || g.ksplit < 1) return HXA_E_ARG;
@@ -854,13 +865,13 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   if (g.epi == HXA_EPI_SITU && (w.N % 64) != 0) return HXA_E_ARG;
   if ((g.lda % 8) != 0 || ((uintptr_t)g.A % 16) != 0 || ((uintptr_t)w.w % 16) != 0) return HXA_E_ARG;
   if (w.N % 8 != 0) return HXA_E_ARG;  // 16-byte epilogue chunks
-  const bool split2 = g.epi == HXA_EPI_RESADD_SPLIT2;
+  split2 = g.epi == HXA_EPI_RESADD_SPLIT2;
   if (split2 && (g.ksplit != 1 || w.K % 128 != 0)) return HXA_E_ARG;  // two halves of whole k-step pairs
   if (g.epi == HXA_EPI_RESADD || split2
           ? ((g.ldx % 8) != 0 || ((uintptr_t)g.x % 32) != 0 || ((uintptr_t)g.gate % 32) != 0)
           : ((g.ldo % 8) != 0 || ((uintptr_t)g.out % 16) != 0))
     return HXA_E_ARG;
-  GemmParams p{};
+  p = GemmParams{};
   if (g.epi == HXA_EPI_STORE_T) {  // all columns transposed
     p.out_t = g.out;
     p.ldo_t = g.ldo;
@@ -907,7 +918,9 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   p.hn_g1 = g.hn_g1;
   p.hn_cos = g.hn_cos;
   p.hn_sin = g.hn_sin;
-  int bm = 128, bn = 128, nw = 4;
+  bm = 128;
+  bn = 128;
+  nw = 4;
   pick_tile(g.M, w.N, g.ksplit, w.fmt, g.epi, headnorm ? min(g.hn_cols, w.N) : 0, &bm, &bn, &nw);
   if (g.force_bm) {
     bm = g.force_bm;
@@ -920,6 +933,16 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   }
   p.tiles_m = (g.M + bm - 1) / bm;
   p.tiles_n = (w.N + bn - 1) / bn;
+  return HXA_OK;
+}
+
+int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
+  GemmParams p;
+  int bm, bn, nw;
+  HxaWeight w;
+  bool split2;
+  const int r = gemm_prepare(g, p, bm, bn, nw, w, split2);
+  if (r != HXA_OK) return r;
   hipError_t e;
   if (split2) {
     if (w.fmt == HXA_W_F16) e = launch_split2<HXA_W_F16, false>(bm, bn, p, st);
@@ -932,5 +955,56 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   else if (w.fmt == HXA_W_Q8) e = launch_fmt<HXA_W_Q8, false>(bm, bn, nw, p, g.ksplit, st);
   else if (w.z) e = launch_fmt<HXA_W_Q4, true>(bm, bn, nw, p, g.ksplit, st);
   else e = launch_fmt<HXA_W_Q4, false>(bm, bn, nw, p, g.ksplit, st);
+  return e == hipSuccess ? HXA_OK : HXA_E_HIP;
+}
+
+template <int BM, int BN, int FMT, bool ASYM, int NW>
+hipError_t launch_pair_t(const GemmParams &p0, const GemmParams &p1, hipStream_t st) {
+  auto kern = gemm_pair_kernel<BM, BN, FMT, ASYM, NW>;
+  using G = GemmGeo<BM, BN, FMT>;
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  const int n0 = p0.tiles_m * p0.tiles_n;
+  hipLaunchKernelGGL(kern, dim3(n0 + p1.tiles_m * p1.tiles_n), dim3(64 * NW), G::LDS, st, p0, p1, n0);
+  return hipGetLastError();
+}
+template <int FMT, bool ASYM>
+hipError_t launch_pair_fmt(int bm, int bn, int nw, const GemmParams &p0, const GemmParams &p1, hipStream_t st) {
+  if (bm == 128 && bn == 128 && nw == 4) return launch_pair_t<128, 128, FMT, ASYM, 4>(p0, p1, st);
+  if (bm == 128 && bn == 128 && nw == 8) return launch_pair_t<128, 128, FMT, ASYM, 8>(p0, p1, st);
+  return hipErrorInvalidValue;
+}
+
+int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st) {
+  GemmParams p0, p1;
+  int bm, bn, nw, bm1, bn1, nw1;
+  HxaWeight w0, w1;
+  bool s0, s1;
+  int r = gemm_prepare(g0, p0, bm, bn, nw, w0, s0);
+  if (r != HXA_OK) return r;
+  // the second GEMM takes the first one's tile
+  HxaGemm g1f = g1;
+  g1f.force_bm = bm;
+  g1f.force_bn = bn;
+  g1f.force_nw = nw;
+  r = gemm_prepare(g1f, p1, bm1, bn1, nw1, w1, s1);
+  if (r != HXA_OK) return r;
+  const bool same = w0.fmt == w1.fmt && (w0.z != nullptr) == (w1.z != nullptr) && !s0 && !s1 && g0.ksplit == 1 &&
+                    g1.ksplit == 1 && (p0.tiles_m * p0.tiles_n) % 8 == 0;
+  hipError_t e = hipErrorInvalidValue;
+  if (same) {
+    if (w0.fmt == HXA_W_F16) e = launch_pair_fmt<HXA_W_F16, false>(bm, bn, nw, p0, p1, st);
+    else if (w0.fmt == HXA_W_Q8) e = launch_pair_fmt<HXA_W_Q8, false>(bm, bn, nw, p0, p1, st);
+    else if (w0.z) e = launch_pair_fmt<HXA_W_Q4, true>(bm, bn, nw, p0, p1, st);
+    else e = launch_pair_fmt<HXA_W_Q4, false>(bm, bn, nw, p0, p1, st);
+  }
+  if (e == hipErrorInvalidValue) {  // no paired instantiation for this tile: two launches
+    r = hxa_gemm_launch(g0, st);
+    return r != HXA_OK ? r : hxa_gemm_launch(g1, st);
+  }
   return e == hipSuccess ? HXA_OK : HXA_E_HIP;
 }

@@ -25,6 +25,9 @@ struct HxaGemm {
   const float *hn_g0, *hn_g1, *hn_cos, *hn_sin;
 };
 int hxa_gemm_launch(const HxaGemm &g, hipStream_t st);
+// two independent GEMMs in one launch (the second takes the first one's tile; same weight format, no split-K);
+// falls back to two launches when the tile has no paired kernel
+int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st);
 
 struct HxaAttn {
   const hxa_h *q, *k, *vt;  // q [T][ldq], k [NKV][ldk] (head h at column h*128); vt [H*128][ldvt] (keys contiguous)

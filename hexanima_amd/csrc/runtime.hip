@@ -491,8 +491,8 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     const float *cs, *sn;
   };
   HeadNorm hn{};
-  auto gemm = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
-                  const float *gate, hxa_h *out_t, long ldo_t, int split, int ksplit, long zstride) -> int {
+  auto make = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
+                  const float *gate, hxa_h *out_t, long ldo_t, int split, int ksplit, long zstride) -> HxaGemm {
     HxaGemm g{};
     g.hn_cols = hn.cols;
     g.hn_g0 = hn.g0;
@@ -517,7 +517,11 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     g.out_t = out_t;
     g.ldo_t = ldo_t;
     g.split_col = split;
-    const int r = hxa_gemm_launch(g, st);
+    return g;
+  };
+  auto gemm = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
+                  const float *gate, hxa_h *out_t, long ldo_t, int split, int ksplit, long zstride) -> int {
+    const int r = hxa_gemm_launch(make(A, lda, M, w, epi, out, ldo, xx, gate, out_t, ldo_t, split, ksplit, zstride), st);
     if (r != HXA_OK) return fail(r, "block gemm N=%d K=%d epi=%d rejected", w.N, w.K, epi);
     return HXA_OK;
   };
@@ -565,10 +569,16 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     TRY(hxa_resid_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, D, mod + 2 * D, mod + 3 * D, mod + 4 * D, nullptr,
                                   1e-6f, h, D, st));
     STAGE_DONE();
+    // cross q from h and the text k / v from ctx are independent: one launch, the text tiles filling the CUs the
+    // 1536-token projection leaves idle
     if (fuse) hn = HeadNorm{D, gain + 256, gain + 256, D, nullptr, nullptr};  // cross q: RMSNorm * gain (blk.c:166)
-    TRY(gemm(h, D, BT, Wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    const HxaGemm gq = make(h, D, BT, Wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
     if (fuse) hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
-    TRY(gemm((const hxa_h *)ctx, d->DC, BC, Wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0));
+    const HxaGemm gkv = make((const hxa_h *)ctx, d->DC, BC, Wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0);
+    {
+      const int r = hxa_gemm_pair_launch(gq, gkv, st);
+      if (r != HXA_OK) return fail(r, "block cross q / text k v gemms rejected");
+    }
     STAGE_DONE();
     if (!fuse) {
       TRY(hxa_rmsrope_launch(qk, nullptr, gain + 256, nullptr, ldqk, BT, H, nullptr, nullptr, 0, st));
