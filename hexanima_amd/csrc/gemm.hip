@@ -584,15 +584,20 @@ __global__ __launch_bounds__(64 * NW) void gemm_pair_kernel(GemmParams p0, GemmP
 // the global -> LDS loads, three stages ahead -- so one wave per SIMD keeps the matrix core fed while its partner
 // waits on memory. Stage j: group 1 reads it in phase 2j and computes it in 2j+1; group 0 reads it in 2j+1 and
 // computes it in 2j+2. The LDS ring, stage layout and epilogue are those of gemm_kernel.
-template <int BM, int BN>
+// int8 / int4 weights: the memory phase also reads the raw weights and their scales (and offsets) and dequantises
+// them into the fp16 fragments, so the compute phase is MFMAs only.
+template <int BM, int BN, int FMT = HXA_W_F16, bool ASYM = false>
 __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
-  using G = GemmGeo<BM, BN, HXA_W_F16>;
+  using G = GemmGeo<BM, BN, FMT>;
   constexpr int NT = 512, NWG = 4;  // threads, waves per group
   constexpr int WTM = BM / 2, WTN = BN / 4, MI = WTM / 32, NI = WTN / 32;
   constexpr int BK = G::BK, NS = G::NS;
   constexpr int NAI = BM / 16, TW = G::W_BYTES / 1024;       // 1 KB load instructions per stage (A, W)
-  constexpr int LPS = (NAI + TW + NWG - 1) / NWG;           // per group-1 wave and stage
-  static_assert(BM % 64 == 0 && WTN % 32 == 0 && NS == 4 && (NAI + TW) % NWG == 0 && NAI % NWG == 0, "tile shape");
+  constexpr int LPS = (NAI + TW) / NWG;                     // per group-1 wave and stage (+ the vectors for wave 0)
+  constexpr int NVEC = FMT == HXA_W_F16 ? 0 : (ASYM ? 2 : 1);
+  static_assert(BM % 64 == 0 && WTN % 32 == 0 && NS == 4 && (NAI + TW) % NWG == 0 && NAI % NWG == 0 &&
+                    G::W_BYTES % 1024 == 0 && BN / 8 <= 64,
+                "tile shape");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
 
   const int ntiles = p.tiles_m * p.tiles_n;
@@ -621,9 +626,35 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
         g2l16_opaque(p.A + (long)m * p.lda + k0 + cl * 8, st + r0 * 64);
       } else {
         const int tw = t - NAI, chunk = tw * 64 + lane;
-        const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3), n = min(n0 + row, p.N - 1);
-        g2l16_opaque((const hxa_h *)p.W + n * p.w_rs + og + cl * 8, st + G::A_BYTES + tw * 1024);
+        if constexpr (FMT == HXA_W_F16) {
+          const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3), n = min(n0 + row, p.N - 1);
+          g2l16_opaque((const hxa_h *)p.W + n * p.w_rs + og + cl * 8, st + G::A_BYTES + tw * 1024);
+        } else if constexpr (FMT == HXA_W_Q8) {
+          const int row = chunk >> 1, cl = (chunk & 1) ^ ((row >> 3) & 1), n = min(n0 + row, p.N - 1);
+          g2l16_opaque((const int8_t *)p.W + n * p.w_rs + og + cl * 16, st + G::A_BYTES + tw * 1024);
+        } else {
+          const int row = chunk, n = min(n0 + row, p.N - 1);
+          g2l16_opaque((const uint8_t *)p.W + n * p.w_rs + og, st + G::A_BYTES + tw * 1024);
+        }
       }
+    }
+    if constexpr (NVEC > 0) {  // scale (and offset) vector of the stage's k group: wave 0 of the group
+      if (wl == 0) {
+        const int g = k0 >> 5, nn = min(n0 + lane * 8, p.N - 8);
+        uint8_t *ws = st + G::A_BYTES;
+        if (lane < BN / 8) g2l16_opaque(p.S + (long)g * p.N + nn, ws + G::W_BYTES);
+        if (ASYM && lane < BN / 8) g2l16_opaque(p.Z + (long)g * p.N + nn, ws + G::W_BYTES + G::S_BYTES);
+      }
+    }
+  };
+  // wait until at most `later` further stages of this group-1 wave's loads are in flight
+  auto wait_later = [&](auto later_c) {
+    constexpr int L = decltype(later_c)::value;
+    if constexpr (NVEC == 0) {
+      wait_vm<L * LPS>();
+    } else {
+      if (wl == 0) wait_vm<L * (LPS + NVEC)>();
+      else wait_vm<L * LPS>();
     }
   };
   auto read_frags = [&](int s, half8_t (&fa)[2][MI], half8_t (&fb)[2][NI]) {
@@ -640,7 +671,23 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < NI; j++) {
         const int row = grp * (BN / 2) + wn * WTN + j * 32 + (lane & 31);
-        fb[ks][j] = *(const half8_t *)(ws + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
+        if constexpr (FMT == HXA_W_F16) {
+          fb[ks][j] = *(const half8_t *)(ws + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
+        } else {
+          const hxa_h sc = *(const hxa_h *)(ws + G::W_BYTES + row * 2);
+          const hxa_h zc = ASYM ? *(const hxa_h *)(ws + G::W_BYTES + G::S_BYTES + row * 2) : (hxa_h)0.0f;
+          const half2_t s2 = {sc, sc};
+          uint32_t o[4];
+          if constexpr (FMT == HXA_W_Q8) {  // 8-byte slot cl of the row: chunk cl >> 1 (swizzled), half cl & 1
+            const uint2_t q = *(const uint2_t *)(ws + row * 32 + (((cl >> 1) ^ ((row >> 3) & 1)) << 4) + ((cl & 1) << 3));
+            dq8_word(q.x, s2, o[0], o[1]);
+            dq8_word(q.y, s2, o[2], o[3]);
+          } else {  // 4-byte slot cl: 8 consecutive k
+            const half2_t z2 = {zc, zc};
+            dq4_word<ASYM>(*(const uint32_t *)(ws + row * 16 + (cl << 2)), s2, z2, o);
+          }
+          fb[ks][j] = __builtin_bit_cast(half8_t, (uint4_t){o[0], o[1], o[2], o[3]});
+        }
       }
     }
   };
@@ -671,7 +718,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
   if (grp == 1) {
 #pragma unroll
     for (int s = 0; s < NS; s++) issue(s, s);
-    wait_vm<(NS - 1) * LPS>();  // stage 0 landed
+    wait_later(std::integral_constant<int, NS - 1>{});  // stage 0 landed
     bar();
     for (int j = 0; j < nk; j++) {
       // phase 2j: read stage j, load stage j+3 into the buffer of stage j-1 (read by both groups by now)
@@ -683,7 +730,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
       __builtin_amdgcn_s_setprio(1);
       mfmas(fa, fb);
       __builtin_amdgcn_s_setprio(0);
-      wait_vm<2 * LPS>();
+      wait_later(std::integral_constant<int, 2>{});
       bar();
     }
   } else {
@@ -731,8 +778,7 @@ struct TileCfg {
 };
 // fp16 weights take the 4-wave tiles; int8 / int4 weights the 8-wave ones (two waves per SIMD: the dequantisation
 // registers of a 4-wave tile crowd out the fragment double-buffering, measured 13-18% slower at M = 1536)
-// fp16 weights with M >= 4096 and N >= 8192 take the 256x256 ping-pong tile (nw 9; 13% faster on the MLP-up at
-// 6144 tokens, no faster elsewhere).
+// nw 9: the ping-pong kernel (see pick_tile for where it is chosen).
 constexpr TileCfg kCfgs[] = {{192, 256, 4}, {192, 192, 4}, {192, 128, 4}, {256, 128, 4}, {128, 256, 4},
                              {128, 128, 4}, {64, 128, 4},  {128, 64, 4},  {192, 256, 8}, {128, 256, 8},
                              {192, 128, 8}, {128, 128, 8}};
@@ -766,10 +812,10 @@ hipError_t launch_split2(int bm, int bn, const GemmParams &p, hipStream_t st) {
   return hipErrorInvalidValue;
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int FMT, bool ASYM>
 hipError_t launch_pp(const GemmParams &p, int ksplit, hipStream_t st) {
-  auto kern = gemm_pp_kernel<BM, BN>;
-  using G = GemmGeo<BM, BN, HXA_W_F16>;
+  auto kern = gemm_pp_kernel<BM, BN, FMT, ASYM>;
+  using G = GemmGeo<BM, BN, FMT>;
   static bool attr = false;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
@@ -783,12 +829,12 @@ hipError_t launch_pp(const GemmParams &p, int ksplit, hipStream_t st) {
 
 template <int FMT, bool ASYM>
 hipError_t launch_fmt(int bm, int bn, int nw, const GemmParams &p, int ksplit, hipStream_t st) {
-  if (nw == 9) {  // ping-pong 8 waves (fp16 weights)
-    if constexpr (FMT == HXA_W_F16) {
-      if (bm == 192 && bn == 256) return launch_pp<192, 256>(p, ksplit, st);
-      if (bm == 256 && bn == 256) return launch_pp<256, 256>(p, ksplit, st);
-      if (bm == 128 && bn == 256) return launch_pp<128, 256>(p, ksplit, st);
-      if (bm == 128 && bn == 128) return launch_pp<128, 128>(p, ksplit, st);
+  if (nw == 9) {  // ping-pong 8 waves
+    if (bm == 192 && bn == 256) return launch_pp<192, 256, FMT, ASYM>(p, ksplit, st);
+    if (bm == 256 && bn == 256) return launch_pp<256, 256, FMT, ASYM>(p, ksplit, st);
+    if (bm == 128 && bn == 256) return launch_pp<128, 256, FMT, ASYM>(p, ksplit, st);
+    if constexpr (FMT != HXA_W_Q4) {
+      if (bm == 128 && bn == 128) return launch_pp<128, 128, FMT, ASYM>(p, ksplit, st);
     }
     return hipErrorInvalidValue;
   }
@@ -846,8 +892,15 @@ static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int hn_cols, i
       *nw = c.nw;
     }
   }
-  if (fmt == HXA_W_F16 && M >= 4096 && N >= 8192 && ksplit == 1 && !headnorm &&
-      (epi == HXA_EPI_STORE || epi == HXA_EPI_GELU_TANH || epi == HXA_EPI_GELU_ERF || epi == HXA_EPI_SITU)) {
+  // the 256x256 ping-pong tile at large M: fp16 weights only for the wide MLP-up (13% faster at 6144 tokens, slower
+  // elsewhere than the 4-wave kernel); int8 / int4 weights for every projection of N >= 3072 (14-28% faster than the
+  // 8-wave tiles at 6656 tokens)
+  const bool quant = fmt != HXA_W_F16;
+  const bool pp_epi = epi != HXA_EPI_RESADD_SPLIT2 && (!headnorm || hn_cols % 256 == 0 || hn_cols >= N);
+  if (M >= 4096 && pp_epi &&
+      (quant ? N >= 3072
+             : N >= 8192 && ksplit == 1 && !headnorm &&
+                   (epi == HXA_EPI_STORE || epi == HXA_EPI_GELU_TANH || epi == HXA_EPI_GELU_ERF || epi == HXA_EPI_SITU))) {
     *bm = 256;
     *bn = 256;
     *nw = 9;

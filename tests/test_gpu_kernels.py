@@ -94,7 +94,8 @@ def test_gemm_w8a16_w4a16_config1(N, K, fmt):
     assert_gemm_close(got, hxo.gemm(A, wdq), A, wdq.view(np.float16))
 
 
-@pytest.mark.parametrize("tile", [(192, 256, 8), (128, 256, 8), (192, 128, 8), (128, 128, 8), (128, 128, 4)])
+@pytest.mark.parametrize("tile", [(192, 256, 8), (128, 256, 8), (192, 128, 8), (128, 128, 8), (128, 128, 4), (192, 256, 9),
+                                  (256, 256, 9), (128, 256, 9)])
 @pytest.mark.parametrize("fmt", [1, 2])
 def test_gemm_quant_tiles(fmt, tile):
     """int8 / int4 weights on every 8-wave tile (and a 4-wave one), ragged in M and N: dequantised-fp16 GEMM is the
