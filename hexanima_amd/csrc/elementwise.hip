@@ -27,61 +27,57 @@ HXA_DEV float wave_sum(float v) {
 // With t != NULL the pending gated residual of the previous site is applied first, x += gate * t (kern.c:320-328,
 // the same fma as the GEMM residual epilogue), or with t2 as well x += gate * (t + t2) (kern.c:330-339, the same
 // fma as resadd2_kernel); x is written back, and the norm is taken of the updated row.
-template <int VPL>
-__global__ __launch_bounds__(256) void normmod_kernel(float *__restrict__ x, long ldx, int T, int D,
-                                                      const hxa_h *__restrict__ t, const hxa_h *__restrict__ t2,
-                                                      long ldt, const float *__restrict__ gate,
+// One 256-thread workgroup per row (a float4 of every 1024 columns per thread): short per-thread register arrays
+// keep many rows in flight. The row sums are wave DPP sums combined through LDS in a fixed order.
+template <int NV>
+__global__ __launch_bounds__(256) void normrow_kernel(float *__restrict__ x, long ldx, int D, const hxa_h *__restrict__ t,
+                                                      const hxa_h *__restrict__ t2, long ldt, const float *__restrict__ gate,
                                                       const float *__restrict__ shift, const float *__restrict__ scale,
                                                       const float *__restrict__ w, float eps, hxa_h *__restrict__ h,
                                                       long ldh) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= T) return;
+  __shared__ float red[8];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float4_t *xr = (float4_t *)(x + (long)row * ldx);
-  float4_t v[VPL], mul[VPL], sh[VPL];
-  float s = 0.0f, q = 0.0f;
-  // every load is issued up front (row, residual, per-column vectors): one memory latency per row
+  float4_t v[NV];
 #pragma unroll
-  for (int i = 0; i < VPL; i++) v[i] = xr[lane + 64 * i];
-  half4_t tv[VPL], tv2[VPL];
-  float4_t gv[VPL];
-  if (t != nullptr) {
-#pragma unroll
-    for (int i = 0; i < VPL; i++) {
-      tv[i] = *(const half4_t *)(t + (long)row * ldt + (lane + 64 * i) * 4);
-      gv[i] = *(const float4_t *)(gate + (lane + 64 * i) * 4);
-    }
-    if (t2 != nullptr) {
-#pragma unroll
-      for (int i = 0; i < VPL; i++) tv2[i] = *(const half4_t *)(t2 + (long)row * ldt + (lane + 64 * i) * 4);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < VPL; i++) {
-    const int c = (lane + 64 * i) * 4;
-    mul[i] = *(const float4_t *)(scale + c) + 1.0f;
-    sh[i] = *(const float4_t *)(shift + c);
-    if (w != nullptr) mul[i] *= *(const float4_t *)(w + c);  // k_rms_prep: M = (1 + scale) * w
+  for (int k = 0; k < NV; k++) {
+    const int c = (tid + 256 * k) * 4;
+    v[k] = c < D ? xr[tid + 256 * k] : (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
   }
   if (t != nullptr) {
 #pragma unroll
-    for (int i = 0; i < VPL; i++) {
-      if (t2 != nullptr) {
+    for (int k = 0; k < NV; k++) {
+      const int c = (tid + 256 * k) * 4;
+      if (c < D) {
+        const half4_t a = *(const half4_t *)(t + (long)row * ldt + c);
+        const float4_t g = *(const float4_t *)(gate + c);
+        if (t2 != nullptr) {
+          const half4_t b = *(const half4_t *)(t2 + (long)row * ldt + c);
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[i][e] = fmaf(gv[i][e], (float)tv[i][e] + (float)tv2[i][e], v[i][e]);
-      } else {
+          for (int e = 0; e < 4; e++) v[k][e] = fmaf(g[e], (float)a[e] + (float)b[e], v[k][e]);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[i][e] = fmaf(gv[i][e], (float)tv[i][e], v[i][e]);
+          for (int e = 0; e < 4; e++) v[k][e] = fmaf(g[e], (float)a[e], v[k][e]);
+        }
+        xr[tid + 256 * k] = v[k];
       }
-      xr[lane + 64 * i] = v[i];
     }
   }
+  float s = 0.0f, q = 0.0f;
 #pragma unroll
-  for (int i = 0; i < VPL; i++) {
-    s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
-    q += (v[i][0] * v[i][0] + v[i][1] * v[i][1]) + (v[i][2] * v[i][2] + v[i][3] * v[i][3]);
+  for (int k = 0; k < NV; k++) {
+    s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
+    q += (v[k][0] * v[k][0] + v[k][1] * v[k][1]) + (v[k][2] * v[k][2] + v[k][3] * v[k][3]);
   }
   s = wave_sum(s);
   q = wave_sum(q);
+  if (lane == 0) {
+    red[2 * wave] = s;
+    red[2 * wave + 1] = q;
+  }
+  __syncthreads();
+  s = (red[0] + red[2]) + (red[4] + red[6]);
+  q = (red[1] + red[3]) + (red[5] + red[7]);
   const float inv = 1.0f / (float)D;
   float mu, r;
   if (w == nullptr) {
@@ -92,12 +88,17 @@ __global__ __launch_bounds__(256) void normmod_kernel(float *__restrict__ x, lon
     r = rsqrtf(q * inv + eps);
   }
 #pragma unroll
-  for (int i = 0; i < VPL; i++) {
-    const int c = (lane + 64 * i) * 4;
-    half4_t o;
+  for (int k = 0; k < NV; k++) {
+    const int c = (tid + 256 * k) * 4;
+    if (c < D) {
+      float4_t mul = *(const float4_t *)(scale + c) + 1.0f;
+      if (w != nullptr) mul *= *(const float4_t *)(w + c);  // k_rms_prep: M = (1 + scale) * w
+      const float4_t sh = *(const float4_t *)(shift + c);
+      half4_t o;
 #pragma unroll
-    for (int e = 0; e < 4; e++) o[e] = (hxa_h)((v[i][e] - mu) * r * mul[i][e] + sh[i][e]);
-    *(half4_t *)(h + (long)row * ldh + c) = o;
+      for (int e = 0; e < 4; e++) o[e] = (hxa_h)((v[k][e] - mu) * r * mul[e] + sh[e]);
+      *(half4_t *)(h + (long)row * ldh + c) = o;
+    }
   }
 }
 
@@ -538,13 +539,15 @@ int hxa_resid2_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t,
                                const float *gate, const float *shift, const float *scale, const float *w, float eps,
                                hxa_h *h, long ldh, hipStream_t st) {
   if (T <= 0 || D % 256 != 0 || ldx % 4 || ldh % 4 || (t && (ldt % 4 || !gate)) || (t2 && !t)) return HXA_E_ARG;
-  const int vpl = D / 256;
-  dim3 g(nblk(T, 4)), b(256);
-  switch (vpl) {
-#define HXA_NORMMOD(V) \
-  case V: hipLaunchKernelGGL(normmod_kernel<V>, g, b, 0, st, x, ldx, T, D, t, t2, ldt, gate, shift, scale, w, eps, h, ldh); break;
-    HXA_NORMMOD(1) HXA_NORMMOD(2) HXA_NORMMOD(4) HXA_NORMMOD(8) HXA_NORMMOD(10) HXA_NORMMOD(12) HXA_NORMMOD(16)
-#undef HXA_NORMMOD
+  if (D > 4096) return HXA_E_ARG;
+  switch ((D + 1023) / 1024) {
+#define HXA_NORMROW(V)                                                                                            \
+  case V:                                                                                                          \
+    hipLaunchKernelGGL(normrow_kernel<V>, dim3(T), dim3(256), 0, st, x, ldx, D, t, t2, ldt, gate, shift, scale, w, eps, \
+                       h, ldh);                                                                                    \
+    break;
+    HXA_NORMROW(1) HXA_NORMROW(2) HXA_NORMROW(3) HXA_NORMROW(4)
+#undef HXA_NORMROW
     default:
       return HXA_E_ARG;
   }
