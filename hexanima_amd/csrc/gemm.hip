@@ -44,10 +44,28 @@ struct GemmParams {
   long ldo_t;
   int split_col;
   int tiles_m, tiles_n;
+  // XCD placement: workgroup b runs on XCD b % 8. xcd_gm > 0: the tile grid is cut into 8 equal rectangles, xcd_gm
+  // along M, and XCD x takes rectangle x (M-fastest inside); 0: XCD x takes the x-th eighth of the M-fastest order
+  int xcd_gm;
   // head norm (STORE epilogue): columns [0, hn_cols), in whole heads of 128, get RMSNorm * gain and optional RoPE
   int hn_cols, hn_gsplit, hn_ttab;
   const float *hn_g0, *hn_g1, *hn_cos, *hn_sin;
 };
+
+// tile (tm, tn) of workgroup bid
+HXA_DEV void tile_coords(const GemmParams &p, int bid, int &tm, int &tn) {
+  const int ntiles = p.tiles_m * p.tiles_n;
+  if (p.xcd_gm > 0) {
+    const int x = bid & 7, i = bid >> 3;
+    const int xm = p.tiles_m / p.xcd_gm, xn = p.tiles_n * p.xcd_gm / 8;
+    tm = (x % p.xcd_gm) * xm + i % xm;
+    tn = (x / p.xcd_gm) * xn + i / xm;
+    return;
+  }
+  const int tile = (ntiles % 8 == 0) ? (bid % 8) * (ntiles / 8) + bid / 8 : bid;
+  tm = tile % p.tiles_m;
+  tn = tile / p.tiles_m;
+}
 
 // the gains of head-normed columns n .. n+7 and a row's RoPE coefficients of dims (n & 63) .. +7
 HXA_DEV void hn_gains(const GemmParams &p, int n, float (&g)[8]) {
@@ -350,9 +368,8 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   static_assert(BM % 64 == 0 && WTN % 32 == 0 && (NW == 4 || NW == 8), "tile shape");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
 
-  const int ntiles = p.tiles_m * p.tiles_n;
-  const int tile = (ntiles % 8 == 0) ? (bid % 8) * (ntiles / 8) + bid / 8 : bid;
-  const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
+  int tm, tn;
+  tile_coords(p, bid, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int kbase = z * p.Kslice;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -600,10 +617,8 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
                 "tile shape");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
 
-  const int ntiles = p.tiles_m * p.tiles_n;
-  const int bid = blockIdx.x;
-  const int tile = (ntiles % 8 == 0) ? (bid % 8) * (ntiles / 8) + bid / 8 : bid;
-  const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
+  int tm, tn;
+  tile_coords(p, blockIdx.x, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int z = blockIdx.z;
   const int kbase = z * p.Kslice;
@@ -986,6 +1001,20 @@ static int gemm_prepare(const HxaGemm &g, GemmParams &p, int &bm, int &bn, int &
   }
   p.tiles_m = (g.M + bm - 1) / bm;
   p.tiles_n = (w.N + bn - 1) / bn;
+  // 8 XCD rectangles of the fewest A + W bytes per k step (each XCD's L2 then serves its CUs' shared rows)
+  p.xcd_gm = 0;
+  {
+    const long wrow = w.fmt == HXA_W_F16 ? 64 : (w.fmt == HXA_W_Q8 ? 32 : 16);
+    long best = -1;
+    for (int gm = 1; gm <= 8; gm *= 2) {
+      if (p.tiles_m % gm || p.tiles_n % (8 / gm)) continue;
+      const long bytes = (long)(p.tiles_m / gm) * bm * 64 + (long)(p.tiles_n / (8 / gm)) * bn * wrow;
+      if (best < 0 || bytes < best) {
+        best = bytes;
+        p.xcd_gm = gm;
+      }
+    }
+  }
   return HXA_OK;
 }
 
