@@ -788,21 +788,34 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
   gemm_epilogue<BM, BN, NT, false>(p, Cs, m0, n0, tid, z);
 }
 
-struct TileCfg {
+// Tile cost model, per weight format (fp16, int8, int4): a launch of `waves` rounds of workgroups over the CUs takes
+// about waves * (a * BM * BN * Kslice / 1e6 + b) microseconds. a and b were fitted by least squares (b >= 0) to
+// every tile timed on 18 projection shapes of 256-6656 rows (hidden 2048-3072, MLP 8192-24576, split-K 1-2) on a
+// 256-CU MI355X; a = 0 marks a tile that format does not use. nw 4: one wave per SIMD; nw 8: two (int8 / int4
+// dequantisation overlaps the other wave's MFMAs); nw 9: the ping-pong kernel. The 4-wave tiles lose 13-25% to the
+// 8-wave ones and the ping-pong kernel on quantised weights, except the small tiles of short-M projections.
+struct TileCost {
   int bm, bn, nw;
+  float a[3], b[3];
 };
-// fp16 weights take the 4-wave tiles; int8 / int4 weights the 8-wave ones (two waves per SIMD: the dequantisation
-// registers of a 4-wave tile crowd out the fragment double-buffering, measured 13-18% slower at M = 1536)
-// nw 9: the ping-pong kernel (see pick_tile for where it is chosen).
-constexpr TileCfg kCfgs[] = {{192, 256, 4}, {192, 192, 4}, {192, 128, 4}, {256, 128, 4}, {128, 256, 4},
-                             {128, 128, 4}, {64, 128, 4},  {128, 64, 4},  {192, 256, 8}, {128, 256, 8},
-                             {192, 128, 8}, {128, 128, 8}};
-// relative MFMA efficiency of a full grid of each tile (LDS traffic per MFMA grows as the tile shrinks): ranks tiles
-// whose CU fill is (nearly) the same
-static double tile_eff(int bm, int bn) {
-  const int a = bm * bn;
-  return a >= 192 * 256 ? 1.0 : a >= 128 * 256 ? 0.97 : a >= 192 * 128 ? 0.95 : a >= 128 * 128 ? 0.92 : 0.75;
-}
+constexpr TileCost kTiles[] = {
+    {192, 256, 4, {0.4384f, 0.0f, 0.0f}, {2.40f, 0.0f, 0.0f}},
+    {192, 192, 4, {0.4607f, 0.0f, 0.0f}, {2.21f, 0.0f, 0.0f}},
+    {256, 128, 4, {0.5216f, 0.0f, 0.0f}, {0.00f, 0.0f, 0.0f}},
+    {128, 256, 4, {0.4833f, 0.0f, 0.0f}, {1.14f, 0.0f, 0.0f}},
+    {192, 128, 4, {0.5076f, 0.0f, 0.0f}, {1.90f, 0.0f, 0.0f}},
+    {128, 128, 4, {0.5077f, 0.0f, 0.0f}, {3.26f, 0.0f, 0.0f}},
+    {128, 64, 4, {0.7260f, 0.5797f, 0.0f}, {2.46f, 5.95f, 0.0f}},
+    {64, 128, 4, {0.5808f, 0.5976f, 0.6163f}, {3.38f, 7.19f, 7.20f}},
+    {192, 256, 8, {0.5071f, 0.5792f, 0.5675f}, {0.33f, 1.53f, 3.47f}},
+    {128, 256, 8, {0.5004f, 0.6363f, 0.5286f}, {0.00f, 1.84f, 4.99f}},
+    {192, 128, 8, {0.6810f, 0.7205f, 0.7193f}, {1.31f, 2.55f, 3.09f}},
+    {128, 128, 8, {0.5529f, 0.5801f, 0.5555f}, {2.44f, 6.01f, 6.46f}},
+    {256, 256, 9, {0.4230f, 0.4486f, 0.4598f}, {0.00f, 1.51f, 2.49f}},
+    {192, 256, 9, {0.4566f, 0.5385f, 0.5270f}, {0.00f, 2.91f, 3.90f}},
+    {128, 256, 9, {0.4991f, 0.5582f, 0.5452f}, {0.00f, 4.29f, 5.67f}},
+    {128, 128, 9, {0.5282f, 0.5643f, 0.0f}, {3.54f, 6.21f, 0.0f}},
+};
 
 template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false, int NW = 4>
 hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
@@ -858,7 +871,7 @@ hipError_t launch_fmt(int bm, int bn, int nw, const GemmParams &p, int ksplit, h
     if (bm == 192 && bn == 128) return launch_t<192, 128, FMT, ASYM, false, 8>(p, ksplit, st);
     if (bm == 128 && bn == 256) return launch_t<128, 256, FMT, ASYM, false, 8>(p, ksplit, st);
     if (bm == 128 && bn == 128) return launch_t<128, 128, FMT, ASYM, false, 8>(p, ksplit, st);
-    return hipErrorInvalidValue;  // (kCfgs lists the shapes instantiated here)
+    return hipErrorInvalidValue;  // (kTiles lists the shapes instantiated here)
   }
   if (bm == 192 && bn == 256) return launch_t<192, 256, FMT, ASYM>(p, ksplit, st);
   if (bm == 192 && bn == 192) return launch_t<192, 192, FMT, ASYM>(p, ksplit, st);
@@ -877,48 +890,34 @@ int g_num_cu = 0;
 
 }  // namespace
 
-// Choose a tile shape: best wave-quantisation efficiency over the GPU's CUs, ties to the larger tile.
-static void pick_tile(int M, int N, int ksplit, int fmt, int epi, int hn_cols, int *bm, int *bn, int *nw) {
+// Choose the tile of least modelled time (kTiles). HXA_EPI_RESADD_SPLIT2 keeps both K halves' accumulators in
+// registers and runs on the 4-wave 128x128 / 64x128 tiles only (ranked with the fp16 costs).
+static void pick_tile(int M, int N, int K, int ksplit, int fmt, int epi, int hn_cols, int *bm, int *bn, int *nw) {
   const bool headnorm = hn_cols > 0;
+  const bool split2 = epi == HXA_EPI_RESADD_SPLIT2;
   if (g_num_cu == 0) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
     hipDeviceProp_t prop;
     g_num_cu = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 256;
   }
+  const int f = split2 ? 0 : fmt;
   double best = -1.0;
-  for (const TileCfg &c : kCfgs) {
+  for (const TileCost &c : kTiles) {
+    if (c.a[f] == 0.0f) continue;
+    if (split2 && !(c.bn == 128 && (c.bm == 128 || c.bm == 64) && c.nw == 4)) continue;  // register budget
     if (fmt == HXA_W_Q4 && c.bn < 128) continue;
     if (epi == HXA_EPI_SITU && c.bn % 128 != 0) continue;  // each wave needs whole (up, gate) block pairs
-    if (epi == HXA_EPI_RESADD_SPLIT2) {
-      if (!(c.bn == 128 && (c.bm == 128 || c.bm == 64) && c.nw == 4)) continue;  // register budget
-    } else if ((c.nw == 8) != (fmt != HXA_W_F16)) {
-      continue;
-    }
     if (headnorm && (c.bn % 128 != 0 || (hn_cols % c.bn != 0 && hn_cols < N))) continue;  // whole head-normed tiles
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ksplit;
     const long waves = (tiles + g_num_cu - 1) / g_num_cu;
-    const double useful = (double)M * N / ((double)((M + c.bm - 1) / c.bm) * c.bm * ((N + c.bn - 1) / c.bn) * c.bn);
-    const double eff = useful * (double)tiles / (double)(waves * g_num_cu) * tile_eff(c.bm, c.bn);
-    if (eff > best + 1e-9) {
-      best = eff;
+    const double t = (double)waves * (c.a[f] * 1e-6 * c.bm * c.bn * (double)(K / ksplit) + c.b[f]);
+    if (best < 0.0 || t < best - 1e-9) {
+      best = t;
       *bm = c.bm;
       *bn = c.bn;
       *nw = c.nw;
     }
-  }
-  // the 256x256 ping-pong tile at large M: fp16 weights only for the wide MLP-up (13% faster at 6144 tokens, slower
-  // elsewhere than the 4-wave kernel); int8 / int4 weights for every projection of N >= 3072 (14-28% faster than the
-  // 8-wave tiles at 6656 tokens)
-  const bool quant = fmt != HXA_W_F16;
-  const bool pp_epi = epi != HXA_EPI_RESADD_SPLIT2 && (!headnorm || hn_cols % 256 == 0 || hn_cols >= N);
-  if (M >= 4096 && pp_epi &&
-      (quant ? N >= 3072
-             : N >= 8192 && ksplit == 1 && !headnorm &&
-                   (epi == HXA_EPI_STORE || epi == HXA_EPI_GELU_TANH || epi == HXA_EPI_GELU_ERF || epi == HXA_EPI_SITU))) {
-    *bm = 256;
-    *bn = 256;
-    *nw = 9;
   }
 }
 
@@ -989,7 +988,7 @@ static int gemm_prepare(const HxaGemm &g, GemmParams &p, int &bm, int &bn, int &
   bm = 128;
   bn = 128;
   nw = 4;
-  pick_tile(g.M, w.N, g.ksplit, w.fmt, g.epi, headnorm ? min(g.hn_cols, w.N) : 0, &bm, &bn, &nw);
+  pick_tile(g.M, w.N, w.K, g.ksplit, w.fmt, g.epi, headnorm ? min(g.hn_cols, w.N) : 0, &bm, &bn, &nw);
   if (g.force_bm) {
     bm = g.force_bm;
     bn = g.force_bn;
@@ -1061,6 +1060,18 @@ hipError_t launch_pair_fmt(int bm, int bn, int nw, const GemmParams &p0, const G
   return hipErrorInvalidValue;
 }
 
+int hxa_gemm_plan(const HxaGemm &g, int *bm, int *bn, int *rounds) {
+  GemmParams p;
+  int nw;
+  HxaWeight w;
+  bool split2;
+  const int r = gemm_prepare(g, p, *bm, *bn, nw, w, split2);
+  if (r != HXA_OK) return r;
+  const long n = (long)p.tiles_m * p.tiles_n * g.ksplit;
+  *rounds = (int)((n + g_num_cu - 1) / g_num_cu);
+  return HXA_OK;
+}
+
 int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st) {
   GemmParams p0, p1;
   int bm, bn, nw, bm1, bn1, nw1;
@@ -1068,23 +1079,24 @@ int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st) {
   bool s0, s1;
   int r = gemm_prepare(g0, p0, bm, bn, nw, w0, s0);
   if (r != HXA_OK) return r;
-  // the second GEMM takes the first one's tile
-  HxaGemm g1f = g1;
-  g1f.force_bm = bm;
-  g1f.force_bn = bn;
-  g1f.force_nw = nw;
-  r = gemm_prepare(g1f, p1, bm1, bn1, nw1, w1, s1);
-  if (r != HXA_OK) return r;
-  const bool same = w0.fmt == w1.fmt && (w0.z != nullptr) == (w1.z != nullptr) && !s0 && !s1 && g0.ksplit == 1 &&
-                    g1.ksplit == 1 && (p0.tiles_m * p0.tiles_n) % 8 == 0;
   hipError_t e = hipErrorInvalidValue;
-  if (same) {
-    if (w0.fmt == HXA_W_F16) e = launch_pair_fmt<HXA_W_F16, false>(bm, bn, nw, p0, p1, st);
-    else if (w0.fmt == HXA_W_Q8) e = launch_pair_fmt<HXA_W_Q8, false>(bm, bn, nw, p0, p1, st);
-    else if (w0.z) e = launch_pair_fmt<HXA_W_Q4, true>(bm, bn, nw, p0, p1, st);
-    else e = launch_pair_fmt<HXA_W_Q4, false>(bm, bn, nw, p0, p1, st);
+  // paired only on the 128x128 4- / 8-wave tiles; the second GEMM then takes the first one's tile
+  if (bm == 128 && bn == 128 && nw != 9 && !s0 && g0.ksplit == 1 && g1.ksplit == 1 &&
+      (p0.tiles_m * p0.tiles_n) % 8 == 0) {
+    HxaGemm g1f = g1;
+    g1f.force_bm = bm;
+    g1f.force_bn = bn;
+    g1f.force_nw = nw;
+    r = gemm_prepare(g1f, p1, bm1, bn1, nw1, w1, s1);
+    if (r != HXA_OK) return r;
+    if (w0.fmt == w1.fmt && (w0.z != nullptr) == (w1.z != nullptr) && !s1) {
+      if (w0.fmt == HXA_W_F16) e = launch_pair_fmt<HXA_W_F16, false>(bm, bn, nw, p0, p1, st);
+      else if (w0.fmt == HXA_W_Q8) e = launch_pair_fmt<HXA_W_Q8, false>(bm, bn, nw, p0, p1, st);
+      else if (w0.z) e = launch_pair_fmt<HXA_W_Q4, true>(bm, bn, nw, p0, p1, st);
+      else e = launch_pair_fmt<HXA_W_Q4, false>(bm, bn, nw, p0, p1, st);
+    }
   }
-  if (e == hipErrorInvalidValue) {  // no paired instantiation for this tile: two launches
+  if (e == hipErrorInvalidValue) {  // not pairable: two launches, each on its own tile
     r = hxa_gemm_launch(g0, st);
     return r != HXA_OK ? r : hxa_gemm_launch(g1, st);
   }

@@ -18,13 +18,16 @@ struct HxaGemm {
   long ldo_t;
   int split_col;
   int force_bm, force_bn;  // 0 = automatic tile choice
-  int force_nw;            // waves per workgroup with a forced tile: 0 / 4, or 8 (192 x 256 only)
+  int force_nw;            // waves per workgroup with a forced tile: 0 / 4, 8, or 9 (the ping-pong kernel)
   // STORE with head norm: columns [0, hn_cols) (multiple of 128) get per-head RMSNorm * gain (gain hn_g0 for columns
   // < hn_gsplit, hn_g1 above) and, with hn_cos / hn_sin [hn_ttab][64], RoPE at token m % hn_ttab (kern.c:163-197)
   int hn_cols, hn_gsplit, hn_ttab;
   const float *hn_g0, *hn_g1, *hn_cos, *hn_sin;
 };
 int hxa_gemm_launch(const HxaGemm &g, hipStream_t st);
+// the tile hxa_gemm_launch would run g on and the rounds of workgroups over the CUs it would take (tile grid x
+// ksplit / CUs, rounded up); HXA_OK, or the error hxa_gemm_launch would return
+int hxa_gemm_plan(const HxaGemm &g, int *bm, int *bn, int *rounds);
 // two independent GEMMs in one launch (the second takes the first one's tile; same weight format, no split-K);
 // falls back to two launches when the tile has no paired kernel
 int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st);

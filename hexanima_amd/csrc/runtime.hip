@@ -540,6 +540,22 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     TRY(gemm(a, F, BT, w, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
     return defer ? HXA_OK : hxa_resadd2_launch(x, D, t1, t2, D, BT, D, gate, st);
   };
+  // the attention output projection whose gated residual the next norm applies (no stage dump): one K pass into
+  // t1, or -- when that runs as a single round of 128x128 (or smaller) tiles, whose short k loops leave the fixed
+  // prologue and epilogue a large share -- two fp16 K-half partials into t1 and t2 on twice the workgroups, which
+  // the norm adds (1536 tokens: 4% faster for fp16, 9-21% for int8 / int4 weights; slower on a grid of 192x256 or
+  // 256x256 tiles or of several rounds). split_o says which, for that norm's t2.
+  bool split_o = false;
+  auto deferred_proj = [&](const HxaWeight &w) -> int {
+    const HxaGemm g1 = make(o, D, BT, w, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0);
+    int bm = 0, bn = 0, rounds = 0;
+    split_o = w.K % 64 == 0 && hxa_gemm_plan(g1, &bm, &bn, &rounds) == HXA_OK && rounds == 1 && bm * bn <= 128 * 128;
+    if (!split_o) {
+      const int r = hxa_gemm_launch(g1, st);
+      return r == HXA_OK ? HXA_OK : fail(r, "block gemm N=%d K=%d rejected", w.N, w.K);
+    }
+    return gemm(o, D, BT, w, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D);
+  };
   if (d->kind == 0) {
     const float *gain = pv.vec;
     const HxaWeight &Wqkv = pv.w[0], &Wo = pv.w[1], &Wcq = pv.w[2], &Wckv = pv.w[3], &Wco = pv.w[4], &W1 = pv.w[5],
@@ -562,12 +578,11 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     // gated residual x += gate * f16(o Wo) (blk.c:162): without a stage dump it is applied by the next site's LN
     // kernel, which reads x anyway (same fma, so the same x); the projection is then a plain store into t1
-    TRY(fuse ? gemm(o, D, BT, Wo, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0)
-             : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
+    TRY(fuse ? deferred_proj(Wo) : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 1: cross-attention (blk.c:163-169)
-    TRY(hxa_resid_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, D, mod + 2 * D, mod + 3 * D, mod + 4 * D, nullptr,
-                                  1e-6f, h, D, st));
+    TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 2 * D,
+                                   mod + 3 * D, mod + 4 * D, nullptr, 1e-6f, h, D, st));
     STAGE_DONE();
     // cross q from h and the text k / v from ctx are independent: one launch, the text tiles filling the CUs the
     // 1536-token projection leaves idle
@@ -587,12 +602,11 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     TRY(attn(qk, ck, D, cvT, BC, d->C, d->C, (long)d->C * D, d->C));
     STAGE_DONE();
-    TRY(fuse ? gemm(o, D, BT, Wco, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0)
-             : gemm(o, D, BT, Wco, HXA_EPI_RESADD, nullptr, 0, x, mod + 5 * D, nullptr, 0, 0, 1, 0));
+    TRY(fuse ? deferred_proj(Wco) : gemm(o, D, BT, Wco, HXA_EPI_RESADD, nullptr, 0, x, mod + 5 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 2: MLP (blk.c:170-174)
-    TRY(hxa_resid_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, D, mod + 5 * D, mod + 6 * D, mod + 7 * D, nullptr,
-                                  1e-6f, h, D, st));
+    TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 5 * D,
+                                   mod + 6 * D, mod + 7 * D, nullptr, 1e-6f, h, D, st));
     STAGE_DONE();
     TRY(gemm(h, D, BT, W1, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
@@ -612,12 +626,11 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     TRY(attn(qk, k, ldqk, vT, BT, T, d->nvalid, (long)T * ldqk, T));
     STAGE_DONE();
     const bool fuse = stop == 0;  // residual deferred into the FFN's RMS-mod kernel (same fma) unless dumping stages
-    TRY(fuse ? gemm(o, D, BT, Wo, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0)
-             : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
+    TRY(fuse ? deferred_proj(Wo) : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // FFN half (moss blk.c:248-259)
-    TRY(hxa_resid_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, D, mod + 2 * D, mod + 3 * D, mod + 4 * D, n2, 1e-6f,
-                                  h, D, st));
+    TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 2 * D,
+                                   mod + 3 * D, mod + 4 * D, n2, 1e-6f, h, D, st));
     STAGE_DONE();
     TRY(gemm(h, D, BT, Wug, HXA_EPI_SITU, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     STAGE_DONE();

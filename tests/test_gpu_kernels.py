@@ -150,6 +150,32 @@ def test_gemm_epilogues():
     assert ulp_diff(got, ref).max() <= 2
 
 
+@pytest.mark.parametrize("fmt,tile", [(f, t) for f in (0, 1, 2)
+                                      for t in ((256, 256, 9), (192, 256, 9), (128, 256, 9), (128, 128, 9), (192, 128, 8),
+                                                (192, 128, 4))
+                                      if not (f == 2 and t == (128, 128, 9))])
+def test_gemm_partial_split_k_tiles(fmt, tile):
+    """Split-K into two fp16 partials (the K halves of the MLP-down and of the deferred attention-output projection)
+    on the ping-pong, 8-wave and 4-wave tiles for each weight format: each half is the oracle GEMM of its K half;
+    M and N ragged against the tiles."""
+    hip = _hip()
+    say(f"gemm partial ksplit=2 fmt={fmt} tile={tile}")
+    rng = np.random.default_rng(60 + fmt)
+    M, N, K = 320, 416, 1024
+    A = f16(rng.standard_normal((M, K)))
+    if fmt == 0:
+        w, s = f16(rng.standard_normal((N, K)) * 0.05), None
+        wd = w.view(np.uint16)
+    else:
+        wf = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+        w, s = hxo.q8_quantize(wf) if fmt == 1 else hxo.q4_quantize(wf)
+        wd = hxo.q8_dequant(w, s) if fmt == 1 else hxo.q4_dequant(w, s)
+    got = _run_gemm(hip, A, fmt, w, s, N, K, epi=hip.EPI_PARTIAL, ksplit=2, tile=tile)
+    for z, sl in ((0, slice(0, K // 2)), (1, slice(K // 2, K))):
+        Az, Wz = np.ascontiguousarray(A[:, sl]), np.ascontiguousarray(wd[:, sl])
+        assert_gemm_close(got[z], hxo.gemm(Az, Wz), Az, Wz.view(np.float16))
+
+
 @pytest.mark.parametrize("fmt,tile", [(0, None), (0, (64, 128)), (1, None), (2, None)])
 def test_gemm_resadd_split2_matches_partial_then_resadd2(fmt, tile):
     """The fused split-K residual (blk.c:172-174) equals the two fp16 PARTIAL halves + resadd2, bit for bit, and the
