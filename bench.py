@@ -102,6 +102,9 @@ def gpu_run(steps, warmup):
                              None, None, 0, 0, s), "gemm")
     up_ms = _time_launches(L, hip, up, s, reps=50)
     L.hxa_stream_destroy(s)
+    pk = hip.gemm_pick(T, F, D, WFMT, 1, hip.EPI_GELU_TANH)
+    info["up_kernel"] = (f"{'gemm_pp_kernel' if pk['waves'] == 9 else 'gemm_kernel'} {pk['bm']}x{pk['bn']}"
+                         f" ({8 if pk['waves'] == 9 else pk['waves']} waves)")
     return info, ms_step, up_ms
 
 
@@ -127,40 +130,53 @@ def _rate(flops, ms):
     return {"us": round(ms * 1e3, 2), "tflops": round(tf / 1e12, 1), "frac_of_fp16_peak": round(tf / PEAK_FP16, 4)}
 
 
-def extra_dits():
-    """The other DiT workloads: the 2B fp16 DiT at batch 4, the 2.9B-class q8 DiT and the MOSS-class q8/q4 DiT
-    (36 blocks, hidden 3072, 24 heads, MLP 12288 SiTU-gated, int8 attention / int4 MLP weights, joint attention
-    over 6144 image + 512 text tokens of width 4096 projected to 3072), each as ms per graph-replayed Euler step."""
+def dit_fp16_2b_batch4():
+    """the 2B fp16 DiT at batch 4 (the flops scale with the batch)"""
     from hexanima_amd import hip
-    out = {}
-    # 2B fp16, batch 4 (the flops scale with the batch)
     bd = hip.BlockDims(0, D, H, F, C_TXT, DC, 0, 4, 0, hip.W_F16, hip.W_F16, 1)
     ms = dit_ms(bd, NBLK, (4,) + LAT, (4, C_TXT, DC), 0, 6, 1, 2026)
-    out["fp16_2b_dit_batch4"] = {"images_per_s": round(4000.0 / ms, 2), "ms_per_step": round(ms, 3),
-                                 "step_tflops": round(4 * STEP_FLOPS / (ms * 1e-3) / 1e12, 1),
-                                 "config": "28 blocks, hidden 2048, batch 4 x 1536 tokens, fp16"}
-    # 2.9B-class q8
+    return {"images_per_s": round(4000.0 / ms, 2), "ms_per_step": round(ms, 3),
+            "step_tflops": round(4 * STEP_FLOPS / (ms * 1e-3) / 1e12, 1),
+            "config": "28 blocks, hidden 2048, batch 4 x 1536 tokens, fp16"}
+
+
+def dit_q8_2p9b():
+    """the 2.9B-class DiT with int8 group-32 block linears"""
+    from hexanima_amd import hip
     Dq, Hq, Fq = 2560, 20, 10240
     bd = hip.BlockDims(0, Dq, Hq, Fq, C_TXT, DC, 0, 1, 0, hip.W_Q8, hip.W_Q8, 1)
     ms = dit_ms(bd, NBLK, (1,) + LAT, (1, C_TXT, DC), 0, 10, 2, 2025)
     blk = 2 * T * Dq * (3 * Dq) + 3 * 2 * T * Dq * Dq + 2 * C_TXT * DC * 2 * Dq + 2 * 2 * T * Dq * Fq \
         + 4 * T * T * Dq + 4 * T * C_TXT * Dq
-    out["q8_2p9b_dit"] = {"steps_per_s": round(1000.0 / ms, 3), "ms_per_step": round(ms, 4),
-                          "step_tflops": round(NBLK * blk / (ms * 1e-3) / 1e12, 1),
-                          "config": "28 blocks, hidden 2560, 20 heads, MLP 10240, int8 g32 block linears, "
-                                    "1536 image + 256 text tokens"}
-    # MOSS-class: latent 32 x 128 x 192 -> 64 x 96 patch grid = 6144 image tokens, + 512 text tokens
+    return {"steps_per_s": round(1000.0 / ms, 3), "ms_per_step": round(ms, 4),
+            "step_tflops": round(NBLK * blk / (ms * 1e-3) / 1e12, 1),
+            "config": "28 blocks, hidden 2560, 20 heads, MLP 10240, int8 g32 block linears, "
+                      "1536 image + 256 text tokens"}
+
+
+def dit_moss():
+    """the MOSS-class DiT: 36 blocks, hidden 3072, 24 heads, MLP 12288 SiTU-gated, int8 attention / int4 MLP
+    weights, joint attention over 6144 image + 512 text tokens of width 4096 projected to 3072 (latent 32 x 128 x
+    192 -> 64 x 96 patch grid)"""
+    from hexanima_amd import hip
     Dm, Hm, Fm, NBm, NTXT, TIN = 3072, 24, 12288, 36, 512, 4096
     bd = hip.BlockDims(1, Dm, Hm, Fm, NTXT, 0, 0, 1, 0, hip.W_Q8, hip.W_Q4, 1)
     ms = dit_ms(bd, NBm, (1, 32, 128, 192), (1, NTXT, TIN), TIN, 3, 1, 2027)
     Tm = 6144 + NTXT
     blk = 2 * Tm * Dm * 4 * Dm + 2 * Tm * Dm * 2 * Fm + 2 * Tm * Fm * Dm + 4 * Tm * Tm * Dm
-    out["moss_5b_dit"] = {"steps_per_s": round(1000.0 / ms, 3), "ms_per_step": round(ms, 2),
-                          "step_tflops": round(NBm * blk / (ms * 1e-3) / 1e12, 1),
-                          "step_frac_of_fp16_peak": round(NBm * blk / (ms * 1e-3) / PEAK_FP16, 4),
-                          "config": "36 blocks, hidden 3072, 24 heads, MLP 12288 SiTU, int8 attention / int4 MLP "
-                                    "g32, joint attention 6144 image + 512 text tokens"}
-    return out
+    return {"steps_per_s": round(1000.0 / ms, 3), "ms_per_step": round(ms, 2),
+            "step_tflops": round(NBm * blk / (ms * 1e-3) / 1e12, 1),
+            "step_frac_of_fp16_peak": round(NBm * blk / (ms * 1e-3) / PEAK_FP16, 4),
+            "config": "36 blocks, hidden 3072, 24 heads, MLP 12288 SiTU, int8 attention / int4 MLP "
+                      "g32, joint attention 6144 image + 512 text tokens"}
+
+
+EXTRA_DITS = {"fp16_2b_dit_batch4": dit_fp16_2b_batch4, "q8_2p9b_dit": dit_q8_2p9b, "moss_5b_dit": dit_moss}
+
+
+def extra_dits():
+    """The other DiT workloads, each as ms per graph-replayed Euler step."""
+    return {k: f() for k, f in EXTRA_DITS.items()}
 
 
 def microbench():
@@ -174,30 +190,36 @@ def microbench():
     L = hip.lib()
     s = C.c_void_p()
     hip.check(L.hxa_stream_create(C.byref(s)), "stream")
-    res = {"linear_m1536": {}, "attention": {}}
+    res = {"linear_m1536": {}, "linear_m1536_2p9b": {}, "attention": {}}
     M = T
-    A = hip.DeviceArray((M, 8192), np.float16)
-    hip.check(L.hxa_fill_normal(A.ptr, 1, M * 8192, 21, 0.0, 1.0, s), "fill")
-    Wb = hip.DeviceArray((8192 * 8192 * 2,), np.uint8)
-    Sb = hip.DeviceArray((256 * 8192,), np.float16)
-    O = hip.DeviceArray((M, 8192), np.float16)
-    hip.check(L.hxa_fill_const(Sb.ptr, 1, 256 * 8192, 0.02 / 127, s), "fill")
-    for name, fmt in (("fp16", hip.W_F16), ("q8", hip.W_Q8), ("q4", hip.W_Q4)):
-        row = {}
-        for K, N in ((2048, 6144), (2048, 2048), (2048, 8192), (8192, 2048)):
-            if fmt == hip.W_F16:
-                hip.check(L.hxa_fill_normal(Wb.ptr, 1, N * K, 22, 0.0, 0.02, s), "fill")
-            elif fmt == hip.W_Q8:
-                hip.check(L.hxa_fill_uniform_int(Wb.ptr, 8, N * K, 23, -127, 127, s), "fill")
-            else:
-                hip.check(L.hxa_fill_uniform_int(Wb.ptr, 4, N * K // 2, 24, -8, 7, s), "fill")
-            sp = None if fmt == hip.W_F16 else Sb.ptr
+    A = hip.DeviceArray((M, 10240), np.float16)
+    hip.check(L.hxa_fill_normal(A.ptr, 1, M * 10240, 21, 0.0, 1.0, s), "fill")
+    Wb = hip.DeviceArray((10240 * 2560 * 2,), np.uint8)
+    Sb = hip.DeviceArray((320 * 10240,), np.float16)
+    O = hip.DeviceArray((M, 10240), np.float16)
+    hip.check(L.hxa_fill_const(Sb.ptr, 1, 320 * 10240, 0.02 / 127, s), "fill")
+    # the 2B block's projections in each format, and the 2.9B-class block's (hidden 2560, MLP 10240) in fp16 / int8
+    for key, shapes, fmts in (("linear_m1536", ((2048, 6144), (2048, 2048), (2048, 8192), (8192, 2048)),
+                               (("fp16", hip.W_F16), ("q8", hip.W_Q8), ("q4", hip.W_Q4))),
+                              ("linear_m1536_2p9b", ((2560, 7680), (2560, 2560), (2560, 10240), (10240, 2560)),
+                               (("fp16", hip.W_F16), ("q8", hip.W_Q8)))):
+        for name, fmt in fmts:
+            row = {}
+            for K, N in shapes:
+                assert N * K <= 10240 * 2560 and K <= 10240 and N <= 10240
+                if fmt == hip.W_F16:
+                    hip.check(L.hxa_fill_normal(Wb.ptr, 1, N * K, 22, 0.0, 0.02, s), "fill")
+                elif fmt == hip.W_Q8:
+                    hip.check(L.hxa_fill_uniform_int(Wb.ptr, 8, N * K, 23, -127, 127, s), "fill")
+                else:
+                    hip.check(L.hxa_fill_uniform_int(Wb.ptr, 4, N * K // 2, 24, -8, 7, s), "fill")
+                sp = None if fmt == hip.W_F16 else Sb.ptr
 
-            def run(K=K, N=N, fmt=fmt, sp=sp):
-                hip.check(L.hxa_gemm(A.ptr, K, M, fmt | hip.W_KTILED, Wb.ptr, sp, None, N, K, 1, hip.EPI_STORE, O.ptr,
-                                     N, 0, None, 0, None, None, 0, 0, s), "gemm")
-            row[f"{K}x{N}"] = _rate(2.0 * M * N * K, _time_launches(L, hip, run, s))
-        res["linear_m1536"][name] = row
+                def run(K=K, N=N, fmt=fmt, sp=sp):
+                    hip.check(L.hxa_gemm(A.ptr, K, M, fmt | hip.W_KTILED, Wb.ptr, sp, None, N, K, 1, hip.EPI_STORE, O.ptr,
+                                         N, 0, None, 0, None, None, 0, 0, s), "gemm")
+                row[f"{K}x{N}"] = _rate(2.0 * M * N * K, _time_launches(L, hip, run, s))
+            res[key][name] = row
     # attention (q, k, v^T resident; random fp16)
     for name, Tq, NKV, Hh in (("self_1536x1536_h16", T, T, H), ("cross_1536x256_h16", T, C_TXT, H),
                               ("joint_6656x6656_h24", 6656, 6656, 24)):
@@ -301,6 +323,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="leave out the other DiT workloads and the kernel microbenchmarks (for a kernel trace of the step)")
+    ap.add_argument("--workload", choices=sorted(EXTRA_DITS), default=None,
+                    help="time only this other DiT workload and print its JSON (for a kernel trace of it)")
     ap.add_argument("--kernel-probe", type=int, default=0, metavar="REPS",
                     help="only launch the dominant kernel REPS times plus a copy calibration (for rocprofv3 --pmc)")
     a = ap.parse_args()
@@ -309,6 +333,11 @@ def main():
         sys.exit(2)
     if a.kernel_probe:
         kernel_probe(a.kernel_probe)
+        return
+    if a.workload:
+        from hexanima_amd import hip
+        hip.init(0)
+        print(json.dumps({a.workload: EXTRA_DITS[a.workload]()}), flush=True)
         return
     info, ms_step, up_ms = gpu_run(a.steps, a.warmup)
     traffic = None
@@ -336,7 +365,7 @@ def main():
                    "seq_len": T, "parallelism": "single GPU"},
         "step_tflops": round(STEP_FLOPS / (ms_step * 1e-3) / 1e12, 1),
         "step_frac_of_fp16_peak": round(STEP_FLOPS / (ms_step * 1e-3) / PEAK_FP16, 4),
-        "roofline": {"kernel": "gemm_kernel (fp16 k-tiled W, GELU epilogue) MLP up 1536x2048x8192", "bound": "mfma",
+        "roofline": {"kernel": f"{info['up_kernel']}, fp16 k-tiled W, GELU epilogue: MLP up {T}x{D}x{F}", "bound": "mfma",
                      "achieved": round(up_tf / 1e12, 1), "peak": PEAK_FP16 / 1e12, "unit": "TFLOP/s",
                      "frac": round(up_tf / PEAK_FP16, 4), "traffic": traffic, "avg_launch_us": round(up_ms * 1e3, 2)},
         "device": info.get("name"),

@@ -1060,12 +1060,11 @@ hipError_t launch_pair_fmt(int bm, int bn, int nw, const GemmParams &p0, const G
   return hipErrorInvalidValue;
 }
 
-int hxa_gemm_plan(const HxaGemm &g, int *bm, int *bn, int *rounds) {
+int hxa_gemm_plan(const HxaGemm &g, int *bm, int *bn, int *nw, int *rounds) {
   GemmParams p;
-  int nw;
   HxaWeight w;
   bool split2;
-  const int r = gemm_prepare(g, p, *bm, *bn, nw, w, split2);
+  const int r = gemm_prepare(g, p, *bm, *bn, *nw, w, split2);
   if (r != HXA_OK) return r;
   const long n = (long)p.tiles_m * p.tiles_n * g.ksplit;
   *rounds = (int)((n + g_num_cu - 1) / g_num_cu);

@@ -25,9 +25,10 @@ struct HxaGemm {
   const float *hn_g0, *hn_g1, *hn_cos, *hn_sin;
 };
 int hxa_gemm_launch(const HxaGemm &g, hipStream_t st);
-// the tile hxa_gemm_launch would run g on and the rounds of workgroups over the CUs it would take (tile grid x
-// ksplit / CUs, rounded up); HXA_OK, or the error hxa_gemm_launch would return
-int hxa_gemm_plan(const HxaGemm &g, int *bm, int *bn, int *rounds);
+// the tile hxa_gemm_launch would run g on (bm x bn, nw waves per workgroup, 9 = the ping-pong kernel) and the
+// rounds of workgroups over the CUs it would take (tile grid x ksplit / CUs, rounded up); HXA_OK, or the error
+// hxa_gemm_launch would return
+int hxa_gemm_plan(const HxaGemm &g, int *bm, int *bn, int *nw, int *rounds);
 // two independent GEMMs in one launch (the second takes the first one's tile; same weight format, no split-K);
 // falls back to two launches when the tile has no paired kernel
 int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st);

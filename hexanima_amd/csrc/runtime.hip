@@ -185,6 +185,33 @@ extern "C" int hxa_gemm_tile(const void *A, long lda, int M, int fmt, const void
   return gemm_common(A, lda, M, fmt, w, s, z, N, K, ksplit, epi, out, ldo, out_zstride, x, ldx, gate, nullptr, 0, 0, bm,
                      bn, waves, stream);
 }
+extern "C" int hxa_gemm_pick(int M, int N, int K, int fmt, int ksplit, int epi, int norm_cols, int *bm, int *bn,
+                             int *waves, int *rounds) {
+  if (!bm || !bn || !waves || !rounds) return fail(HXA_E_ARG, "gemm_pick: null output");
+  // nothing is launched: aligned stand-in addresses satisfy the operand checks
+  const uintptr_t any = 256;
+  HxaWeight wt{fmt, N, K, (const void *)any, (const hxa_h *)any, nullptr};
+  HxaGemm g{};
+  g.A = (const hxa_h *)any;
+  g.lda = K;
+  g.M = M;
+  g.w = &wt;
+  g.ksplit = ksplit < 1 ? 1 : ksplit;
+  g.epi = epi;
+  g.out = (hxa_h *)any;
+  g.ldo = N;
+  g.x = (float *)any;
+  g.ldx = N;
+  g.gate = (const float *)any;
+  if (norm_cols > 0) {
+    g.hn_cols = norm_cols;
+    g.hn_g0 = g.hn_g1 = (const float *)any;
+    g.hn_gsplit = norm_cols;
+  }
+  const int r = hxa_gemm_plan(g, bm, bn, waves, rounds);
+  if (r != HXA_OK) return fail(r, "gemm_pick M=%d N=%d K=%d fmt=%d epi=%d ksplit=%d rejected (%d)", M, N, K, fmt, epi, ksplit, r);
+  return HXA_OK;
+}
 extern "C" int hxa_gemm_headnorm(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N,
                                  int K, void *out, long ldo, void *out_t, long ldo_t, int split_col, int norm_cols,
                                  const float *gain0, const float *gain1, int gain_split, const float *cosT,
@@ -548,8 +575,8 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   bool split_o = false;
   auto deferred_proj = [&](const HxaWeight &w) -> int {
     const HxaGemm g1 = make(o, D, BT, w, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0);
-    int bm = 0, bn = 0, rounds = 0;
-    split_o = w.K % 64 == 0 && hxa_gemm_plan(g1, &bm, &bn, &rounds) == HXA_OK && rounds == 1 && bm * bn <= 128 * 128;
+    int bm = 0, bn = 0, nw = 0, rounds = 0;
+    split_o = w.K % 64 == 0 && hxa_gemm_plan(g1, &bm, &bn, &nw, &rounds) == HXA_OK && rounds == 1 && bm * bn <= 128 * 128;
     if (!split_o) {
       const int r = hxa_gemm_launch(g1, st);
       return r == HXA_OK ? HXA_OK : fail(r, "block gemm N=%d K=%d rejected", w.N, w.K);

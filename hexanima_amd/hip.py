@@ -71,6 +71,7 @@ _SIGS = {
     "hxa_resadd_norm_mod": (I, [P, L, I, I, P, L, P, P, P, P, F, P, L, P]),
     "hxa_gemm_headnorm": (I, [P, L, I, I, P, P, P, I, I, P, L, P, L, I, I, P, P, I, P, P, I, P]),
     "hxa_gemm_tile": (I, [P, L, I, I, P, P, P, I, I, I, I, P, L, L, P, L, P, I, I, I, P]),
+    "hxa_gemm_pick": (I, [I, I, I, I, I, I, I, P, P, P, P]),
     "hxa_attention": (I, [P, L, P, L, P, L, P, L, I, I, I, I, I, L, L, L, L, P]),
     "hxa_norm_mod": (I, [P, L, I, I, P, P, P, F, P, L, P]),
     "hxa_rmsrope": (I, [P, P, P, P, L, I, I, P, P, I, P]),
@@ -142,6 +143,15 @@ def device_info():
     name = C.create_string_buffer(256)
     check(lib().hxa_device_info(C.byref(cu), C.byref(clk), C.byref(mem), name, 256), "device_info")
     return {"num_cu": cu.value, "clock_khz": clk.value, "mem_bytes": mem.value, "name": name.value.decode()}
+
+
+def gemm_pick(M, N, K, fmt, ksplit=1, epi=0, norm_cols=0):
+    """the tile hxa_gemm chooses: {'bm', 'bn', 'waves' (9 = ping-pong kernel), 'rounds'}"""
+    init()
+    bm, bn, w, r = I(), I(), I(), I()
+    check(lib().hxa_gemm_pick(M, N, K, fmt, ksplit, epi, norm_cols, C.byref(bm), C.byref(bn), C.byref(w), C.byref(r)),
+          "gemm_pick")
+    return {"bm": bm.value, "bn": bn.value, "waves": w.value, "rounds": r.value}
 
 
 class DeviceArray:

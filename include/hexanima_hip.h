@@ -114,11 +114,18 @@ int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, char *name, 
 int hxa_gemm(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
              int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
              void *out_t, long ldo_t, int split_col, void *stream);
-/* same, with an explicit tile shape (tests / tuning): bm x bn in {192x256, 192x192, 192x128, 256x128, 128x256,
- * 128x128, 64x128, 128x64}; waves per workgroup 4 (0 = 4) or 8 (192x256 only) */
+/* same, with an explicit tile shape (tests / tuning). waves per workgroup 4 (0 = 4): bm x bn in {192x256, 192x192,
+ * 192x128, 256x128, 128x256, 128x128, 64x128, 128x64}; 8: {192x256, 192x128, 128x256, 128x128}; 9, the ping-pong
+ * kernel: {256x256, 192x256, 128x256, 128x128 (not int4)}. int4 weights need bn >= 128, SiTU bn % 128 == 0. */
 int hxa_gemm_tile(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
                   int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
                   int bm, int bn, int waves, void *stream);
+/* The tile hxa_gemm chooses for these sizes, weight format (HXA_W_*, KTILED ignored), split and epilogue
+ * (norm_cols > 0: hxa_gemm_headnorm's head-normed columns): *bm x *bn with *waves per workgroup (9: the ping-pong
+ * kernel) and *rounds of workgroups over the GPU's CUs. Returns 0, or the error hxa_gemm would return for these
+ * sizes. No counterpart in the reference (its GEMM has one tile); for tuning and benchmarks. */
+int hxa_gemm_pick(int M, int N, int K, int fmt, int ksplit, int epi, int norm_cols, int *bm, int *bn, int *waves,
+                  int *rounds);
 /* out = f16(A[M][K] . W[N][K]^T) with the per-head norm fused into the store (blk.c:158-160, :164-167,
  * kern.c:163-197): columns [0, norm_cols) (whole heads of 128) become f16(RMSNorm(f16 value) * gain), gain0 for
  * columns < gain_split, gain1 above; with cosT / sinT [ttab][64] also RoPE on pairs (d, d+64) at token m % ttab.

@@ -483,3 +483,36 @@ def test_quantize_matches_oracle():
         hip.sync()
         assert np.array_equal(s.numpy(), so)
         assert np.array_equal(q.numpy().view(np.uint8).reshape(-1), hip.ktile(qo.view(np.uint8).reshape(-1), N, K))
+
+
+@pytest.mark.parametrize("M,N,K,fmt,ksplit,epi,norm", [(1536, 8192, 2048, 0, 1, 1, 0), (1536, 6144, 2048, 0, 1, 0, 4096),
+                                                       (1536, 10240, 2560, 1, 1, 1, 0), (320, 384, 512, 2, 2, 6, 0),
+                                                       (256, 4096, 1024, 1, 1, 0, 0)])
+def test_gemm_pick_names_the_tile_hxa_gemm_runs(M, N, K, fmt, ksplit, epi, norm):
+    """hxa_gemm_pick reports the tile hxa_gemm runs: forcing that tile gives the same bits as the automatic choice;
+    the pick respects head-norm (whole heads per tile) and int4 (bn >= 128) limits; bad sizes give hxa_gemm's error."""
+    hip = _hip()
+    say(f"gemm_pick M={M} N={N} K={K} fmt={fmt} ksplit={ksplit} epi={epi} norm={norm}")
+    pk = hip.gemm_pick(M, N, K, fmt, ksplit, epi, norm)
+    assert pk["waves"] in (4, 8, 9) and pk["rounds"] >= 1
+    assert pk["rounds"] == -(-(-(-M // pk["bm"]) * -(-N // pk["bn"]) * ksplit) // hip.device_info()["num_cu"])
+    if norm:
+        assert pk["bn"] % 128 == 0 and norm % pk["bn"] == 0
+    if fmt == 2:
+        assert pk["bn"] >= 128
+    if norm:
+        return  # hxa_gemm_headnorm's pick; the plain-store comparison below does not apply
+    rng = np.random.default_rng(70)
+    Mt = min(M, 512)
+    A = f16(rng.standard_normal((Mt, K)))
+    if fmt == 0:
+        w, s = f16(rng.standard_normal((N, K)) * 0.05), None
+    else:
+        wf = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+        w, s = hxo.q8_quantize(wf) if fmt == 1 else hxo.q4_quantize(wf)
+    pk_t = hip.gemm_pick(Mt, N, K, fmt, ksplit, epi, 0)
+    auto = _run_gemm(hip, A, fmt, w, s, N, K, epi=epi, ksplit=ksplit)
+    forced = _run_gemm(hip, A, fmt, w, s, N, K, epi=epi, ksplit=ksplit, tile=(pk_t["bm"], pk_t["bn"], pk_t["waves"]))
+    assert np.array_equal(auto.view(np.uint16), forced.view(np.uint16))
+    with pytest.raises(RuntimeError):
+        hip.gemm_pick(M, N, K + 16, fmt, ksplit, epi, 0)
