@@ -322,11 +322,15 @@ HXA_DEV void gemm_epilogue(const GemmParams &p, const hxa_h *Cs, int m0, int n0,
     rows_pass(nsplit);
   if (nsplit < BN) {
     // transposed columns (a multiple of 32: split_col % 32 == 0): a thread takes 4 adjacent columns x 8 rows, read as
-    // 8-byte LDS words (consecutive threads -> consecutive words: no bank conflicts) and written as four 16-byte
-    // runs of 8 rows, one per output row n of out_t
+    // 8-byte LDS words, and writes four 16-byte runs of 8 rows, one per output row n of out_t. Four consecutive
+    // threads take consecutive 8-row chunks of the same columns, so each store instruction writes 64-byte runs
+    // (16 rows of out_t per wave) rather than 64 scattered 16-byte pieces; the LDS reads of those four threads are 8
+    // rows apart (two-way bank conflicts).
+    static_assert(BM % 32 == 0, "8-row chunks in fours");
     const int ngrp = (BN - nsplit) / 4;
     for (int c = tid; c < ngrp * (BM / 8); c += NT) {
-      const int nl = nsplit + (c % ngrp) * 4, ml = (c / ngrp) * 8;
+      const int rest = c >> 2;
+      const int nl = nsplit + (rest % ngrp) * 4, ml = ((rest / ngrp) * 4 + (c & 3)) * 8;
       const int m = m0 + ml;
       if (m >= p.M) continue;
       uint2_t w[8];
