@@ -925,6 +925,18 @@ static void pick_tile(int M, int N, int K, int ksplit, int fmt, int epi, int hn_
   }
 }
 
+// the tiles launch_fmt has kernels for (split2: launch_split2's)
+static bool tile_built(int bm, int bn, int nw, int fmt, bool split2) {
+  if (split2) return nw == 4 && bn == 128 && (bm == 128 || bm == 64);
+  const bool q4 = fmt == HXA_W_Q4;
+  if (nw == 9) return (bn == 256 && (bm == 256 || bm == 192 || bm == 128)) || (bm == 128 && bn == 128 && !q4);
+  if (nw == 8) return (bm == 192 || bm == 128) && (bn == 256 || bn == 128);
+  if (nw != 4) return false;
+  if (bm == 128 && bn == 64) return !q4;
+  return (bm == 192 && (bn == 256 || bn == 192 || bn == 128)) || (bm == 256 && bn == 128) ||
+         (bm == 128 && (bn == 256 || bn == 128)) || (bm == 64 && bn == 128);
+}
+
 // validate a GEMM description, fill its kernel parameters and choose (or take the forced) tile
 static int gemm_prepare(const HxaGemm &g, GemmParams &p, int &bm, int &bn, int &nw, HxaWeight &w, bool &split2) {
   w = *g.w;
@@ -997,9 +1009,8 @@ static int gemm_prepare(const HxaGemm &g, GemmParams &p, int &bm, int &bn, int &
     bm = g.force_bm;
     bn = g.force_bn;
     nw = g.force_nw ? g.force_nw : 4;
-    if (nw != 4 && ((nw != 8 && nw != 9) || split2)) return HXA_E_ARG;
+    if (!tile_built(bm, bn, nw, w.fmt, split2)) return HXA_E_ARG;
     if ((g.epi == HXA_EPI_SITU && bn % 128 != 0) || (w.fmt == HXA_W_Q4 && bn < 128)) return HXA_E_ARG;
-    if (split2 && !(bn == 128 && (bm == 128 || bm == 64))) return HXA_E_ARG;
     if (headnorm && (bn % 128 != 0 || (p.hn_cols % bn != 0 && p.hn_cols < w.N))) return HXA_E_ARG;
   }
   p.tiles_m = (g.M + bm - 1) / bm;

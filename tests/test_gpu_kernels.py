@@ -517,3 +517,20 @@ def test_gemm_pick_names_the_tile_hxa_gemm_runs(M, N, K, fmt, ksplit, epi, norm)
     assert np.array_equal(auto.view(np.uint16), forced.view(np.uint16))
     with pytest.raises(RuntimeError):
         hip.gemm_pick(M, N, K + 16, fmt, ksplit, epi, 0)
+
+
+@pytest.mark.parametrize("fmt,tile", [(2, (128, 128, 9)), (0, (96, 128, 4)), (0, (192, 256, 5)), (1, (256, 128, 8)),
+                                      (2, (128, 64, 4)), (0, (256, 256, 4))])
+def test_gemm_forced_tile_without_kernel_is_an_argument_error(fmt, tile):
+    """A forced tile with no kernel for that shape / wave count / format is rejected with HXA_E_ARG (-12) before
+    anything is launched."""
+    hip = _hip()
+    say(f"gemm forced tile {tile} fmt={fmt}")
+    M, N, K = 256, 256, 256
+    dA = hip.DeviceArray((M, K), np.float16, zero=True)
+    dW = hip.DeviceArray((N * K,), np.float16, zero=True)
+    dS = hip.DeviceArray((K // 32 * N,), np.float16, zero=True)
+    out = hip.DeviceArray((M, N), np.float16)
+    rc = hip.lib().hxa_gemm_tile(dA.ptr, K, M, fmt, dW.ptr, dS.ptr if fmt else None, None, N, K, 1, 0, out.ptr, N, 0,
+                                 None, 0, None, tile[0], tile[1], tile[2], None)
+    assert rc == -12
