@@ -50,7 +50,23 @@ struct GemmParams {
   // head norm (STORE epilogue): columns [0, hn_cols), in whole heads of 128, get RMSNorm * gain and optional RoPE
   int hn_cols, hn_gsplit, hn_ttab;
   const float *hn_g0, *hn_g1, *hn_cos, *hn_sin;
+  const uint8_t *pf;  // bytes to touch after the main loop (HxaGemm::pf)
+  long pf_bytes;
 };
+
+// Touch this workgroup's share of [p.pf, p.pf + p.pf_bytes), one 4-byte load per 128-byte line: the lines come into
+// L2 / MALL for the next kernel while this one runs its epilogue. The loaded values are not used; the caller waits
+// (vmcnt 0) before the workgroup ends.
+HXA_DEV void prefetch_share(const GemmParams &p, int wg, int nwg, int tid, int nt) {
+  const long lines = (p.pf_bytes + 127) >> 7;
+  const long per = (lines + nwg - 1) / nwg;
+  const long l0 = (long)wg * per, l1 = min(lines, l0 + per);
+  for (long l = l0 + tid; l < l1; l += nt) {
+    const uint8_t *a = p.pf + min(l << 7, p.pf_bytes - 4);  // pf_bytes >= 4 (checked on the host)
+    uint32_t v;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(a) : "memory");
+  }
+}
 
 // tile (tm, tn) of workgroup bid
 HXA_DEV void tile_coords(const GemmParams &p, int bid, int &tm, int &tn) {
@@ -563,6 +579,7 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   }
   wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
   __syncthreads();
+  if (p.pf_bytes > 0) prefetch_share(p, bid + z * p.tiles_m * p.tiles_n, p.tiles_m * p.tiles_n * (int)gridDim.z, tid, NT);
 
   // ---- epilogue. Stage f16(acc) through LDS as a row-major [BM][CROW] tile: lane holds, for block (j, i),
   // row i*32 + (lane & 31) and columns j*32 + 8q + 4*(lane/32) + 0..3 (q = 0..3) -> one 8-byte write each.
@@ -584,6 +601,7 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   }
   __syncthreads();
   gemm_epilogue<BM, BN, NT, SPLIT2>(p, Cs, m0, n0, tid, z);
+  if (p.pf_bytes > 0) wait_vm<0>();
 }
 
 template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false, int NW = 4>
@@ -772,6 +790,8 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
   }
   wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
   __syncthreads();
+  if (p.pf_bytes > 0)
+    prefetch_share(p, blockIdx.x + z * p.tiles_m * p.tiles_n, p.tiles_m * p.tiles_n * (int)gridDim.z, tid, NT);
 
   constexpr int CROW = G::CROW;
   hxa_h *Cs = (hxa_h *)lds8;
@@ -790,6 +810,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
   }
   __syncthreads();
   gemm_epilogue<BM, BN, NT, false>(p, Cs, m0, n0, tid, z);
+  if (p.pf_bytes > 0) wait_vm<0>();
 }
 
 // Tile cost model, per weight format (fp16, int8, int4): a launch of `waves` rounds of workgroups over the CUs takes
@@ -1001,6 +1022,9 @@ static int gemm_prepare(const HxaGemm &g, GemmParams &p, int &bm, int &bn, int &
   p.hn_g1 = g.hn_g1;
   p.hn_cos = g.hn_cos;
   p.hn_sin = g.hn_sin;
+  if (g.pf_bytes > 0 && (g.pf == nullptr || g.pf_bytes < 4 || ((uintptr_t)g.pf & 3))) return HXA_E_ARG;
+  p.pf = (const uint8_t *)g.pf;
+  p.pf_bytes = g.pf_bytes > 0 ? g.pf_bytes : 0;
   bm = 128;
   bn = 128;
   nw = 4;

@@ -546,6 +546,19 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     g.split_col = split;
     return g;
   };
+  // with fp16 weights the MLP up-projection brings the down-projection's weights into L2 / MALL under its
+  // epilogue: the down GEMM's short k steps leave its loads too little lookahead for weights arriving cold from HBM
+  // (1536 tokens: 62 us warm, 75 us cold; 2B step 9.52 -> 9.40 ms). With int8 / int4 weights (half or a quarter of
+  // the bytes) it measured 1% slower on the 2.9B-class step and neutral on the MOSS-class one, so it is not used.
+  auto up_with_prefetch = [&](const hxa_h *A, const HxaWeight &w, int epi, const HxaWeight &next) -> int {
+    HxaGemm g = make(A, D, BT, w, epi, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0);
+    if ((next.fmt & ~HXA_W_KTILED) == HXA_W_F16) {
+      g.pf = next.w;
+      g.pf_bytes = (long)next.N * next.K * 2;
+    }
+    const int r = hxa_gemm_launch(g, st);
+    return r == HXA_OK ? HXA_OK : fail(r, "block gemm N=%d K=%d epi=%d rejected", w.N, w.K, epi);
+  };
   auto gemm = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
                   const float *gate, hxa_h *out_t, long ldo_t, int split, int ksplit, long zstride) -> int {
     const int r = hxa_gemm_launch(make(A, lda, M, w, epi, out, ldo, xx, gate, out_t, ldo_t, split, ksplit, zstride), st);
@@ -635,7 +648,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 5 * D,
                                    mod + 6 * D, mod + 7 * D, nullptr, 1e-6f, h, D, st));
     STAGE_DONE();
-    TRY(gemm(h, D, BT, W1, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    TRY(up_with_prefetch(h, W1, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, W2));
     STAGE_DONE();
     TRY(down_resadd(mid, W2, mod + 8 * D));
     STAGE_DONE();
@@ -659,7 +672,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 2 * D,
                                    mod + 3 * D, mod + 4 * D, n2, 1e-6f, h, D, st));
     STAGE_DONE();
-    TRY(gemm(h, D, BT, Wug, HXA_EPI_SITU, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    TRY(up_with_prefetch(h, Wug, HXA_EPI_SITU, Wdn));
     STAGE_DONE();
     TRY(down_resadd(mid, Wdn, mod + 5 * D));
     STAGE_DONE();
