@@ -55,16 +55,17 @@ struct GemmParams {
 };
 
 // Touch this workgroup's share of [p.pf, p.pf + p.pf_bytes), one 4-byte load per 128-byte line: the lines come into
-// L2 / MALL for the next kernel while this one runs its epilogue. The loaded values are not used; the caller waits
-// (vmcnt 0) before the workgroup ends.
-HXA_DEV void prefetch_share(const GemmParams &p, int wg, int nwg, int tid, int nt) {
+// L2 / MALL for the next kernel while this one runs its epilogue. The loads go straight to LDS (no register is
+// written behind the compiler's back) into `sink`, PF_LDS bytes past everything the kernel uses, whose contents are
+// never read; the workgroup drains them (vmcnt 0) before it ends, as every LDS DMA must.
+HXA_DEV void prefetch_share(const GemmParams &p, int wg, int nwg, int tid, int nt, const uint8_t *sink) {
   const long lines = (p.pf_bytes + 127) >> 7;
   const long per = (lines + nwg - 1) / nwg;
   const long l0 = (long)wg * per, l1 = min(lines, l0 + per);
+  const uint32_t la = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t *)sink);
   for (long l = l0 + tid; l < l1; l += nt) {
     const uint8_t *a = p.pf + min(l << 7, p.pf_bytes - 4);  // pf_bytes >= 4 (checked on the host)
-    uint32_t v;
-    asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(a) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(a), "s"(la) : "memory", "m0");
   }
 }
 
@@ -164,7 +165,8 @@ struct GemmGeo {
   static constexpr int STAGE = A_BYTES + W_BYTES + 2 * S_BYTES;     // scale + optional offset vectors
   static constexpr int CROW = BN + 8;
   static constexpr int C_BYTES = BM * CROW * 2;
-  static constexpr int LDS = NS * STAGE > C_BYTES ? NS * STAGE : C_BYTES;
+  static constexpr int PF_LDS = 256;                                 // prefetch_share's sink (64 lanes x 4 B)
+  static constexpr int LDS = (NS * STAGE > C_BYTES ? NS * STAGE : C_BYTES) + PF_LDS;
   static constexpr int NA = BM / 64;                                 // A load instructions per wave per stage
   static constexpr int TW = (W_BYTES / 16 + 63) / 64;                // W load instructions per stage (all waves)
 };
@@ -579,7 +581,9 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   }
   wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
   __syncthreads();
-  if (p.pf_bytes > 0) prefetch_share(p, bid + z * p.tiles_m * p.tiles_n, p.tiles_m * p.tiles_n * (int)gridDim.z, tid, NT);
+  if (p.pf_bytes > 0)
+    prefetch_share(p, bid + z * p.tiles_m * p.tiles_n, p.tiles_m * p.tiles_n * (int)gridDim.z, tid, NT,
+                   lds8 + G::LDS - G::PF_LDS);
 
   // ---- epilogue. Stage f16(acc) through LDS as a row-major [BM][CROW] tile: lane holds, for block (j, i),
   // row i*32 + (lane & 31) and columns j*32 + 8q + 4*(lane/32) + 0..3 (q = 0..3) -> one 8-byte write each.
@@ -791,7 +795,8 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
   wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
   __syncthreads();
   if (p.pf_bytes > 0)
-    prefetch_share(p, blockIdx.x + z * p.tiles_m * p.tiles_n, p.tiles_m * p.tiles_n * (int)gridDim.z, tid, NT);
+    prefetch_share(p, blockIdx.x + z * p.tiles_m * p.tiles_n, p.tiles_m * p.tiles_n * (int)gridDim.z, tid, NT,
+                   lds8 + G::LDS - G::PF_LDS);
 
   constexpr int CROW = G::CROW;
   hxa_h *Cs = (hxa_h *)lds8;
@@ -1022,7 +1027,10 @@ static int gemm_prepare(const HxaGemm &g, GemmParams &p, int &bm, int &bn, int &
   p.hn_g1 = g.hn_g1;
   p.hn_cos = g.hn_cos;
   p.hn_sin = g.hn_sin;
-  if (g.pf_bytes > 0 && (g.pf == nullptr || g.pf_bytes < 4 || ((uintptr_t)g.pf & 3))) return HXA_E_ARG;
+  // the prefetch rides on epilogues that issue no loads of their own (their waits would wait for it too)
+  if (g.pf_bytes > 0 && (g.pf == nullptr || g.pf_bytes < 4 || ((uintptr_t)g.pf & 3) || headnorm ||
+                         g.epi == HXA_EPI_RESADD || split2))
+    return HXA_E_ARG;
   p.pf = (const uint8_t *)g.pf;
   p.pf_bytes = g.pf_bytes > 0 ? g.pf_bytes : 0;
   bm = 128;

@@ -15,7 +15,8 @@ struct HxaGemm {
   long ldx;
   const float *gate;  // RESADD: gate[N]
   // [pf, pf + pf_bytes): memory the next kernel reads (its weights), touched once per 128-byte line after this
-  // GEMM's main loop so that it streams in from HBM under the epilogue; 0 bytes: none
+  // GEMM's main loop so that it streams in from HBM under the epilogue; 0 bytes: none.
+  // Not with RESADD / RESADD_SPLIT2 or a head norm (their epilogues load, and would wait for the prefetch).
   const void *pf;
   long pf_bytes;
   hxa_h *out_t;       // QKV/KV split: columns >= split_col are written transposed to out_t[n - split_col][m]

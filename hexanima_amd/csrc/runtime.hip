@@ -518,9 +518,23 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     const float *cs, *sn;
   };
   HeadNorm hn{};
+  // the weights of the projection(s) after the next one (pf0 .. pf1, adjacent in the pack), which the next
+  // projection brings into L2 / MALL after its main loop when both are fp16: the following GEMM then starts on warm
+  // weights (cold, they cost the MLP-down 62 -> 75 us at 1536 tokens, the others 1-3 us; with int8 / int4 weights the
+  // touch measured neutral to 1% slower and is not made). Applies to one projection, like hn.
+  const HxaWeight *pf0 = nullptr, *pf1 = nullptr;
   auto make = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
                   const float *gate, hxa_h *out_t, long ldo_t, int split, int ksplit, long zstride) -> HxaGemm {
     HxaGemm g{};
+    if (pf0 != nullptr) {
+      const HxaWeight *last = pf1 != nullptr ? pf1 : pf0;
+      if (((pf0->fmt | last->fmt | w.fmt) & ~HXA_W_KTILED) == HXA_W_F16 && hn.cols == 0 && epi != HXA_EPI_RESADD) {
+        const uint8_t *b0 = (const uint8_t *)pf0->w, *b1 = (const uint8_t *)last->w + (long)last->N * last->K * 2;
+        g.pf = b0;
+        g.pf_bytes = b1 - b0;
+      }
+      pf0 = pf1 = nullptr;
+    }
     g.hn_cols = hn.cols;
     g.hn_g0 = hn.g0;
     g.hn_g1 = hn.g1;
@@ -545,19 +559,6 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     g.ldo_t = ldo_t;
     g.split_col = split;
     return g;
-  };
-  // with fp16 weights the MLP up-projection brings the down-projection's weights into L2 / MALL under its
-  // epilogue: the down GEMM's short k steps leave its loads too little lookahead for weights arriving cold from HBM
-  // (1536 tokens: 62 us warm, 75 us cold; 2B step 9.52 -> 9.40 ms). With int8 / int4 weights (half or a quarter of
-  // the bytes) it measured 1% slower on the 2.9B-class step and neutral on the MOSS-class one, so it is not used.
-  auto up_with_prefetch = [&](const hxa_h *A, const HxaWeight &w, int epi, const HxaWeight &next) -> int {
-    HxaGemm g = make(A, D, BT, w, epi, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0);
-    if ((next.fmt & ~HXA_W_KTILED) == HXA_W_F16) {
-      g.pf = next.w;
-      g.pf_bytes = (long)next.N * next.K * 2;
-    }
-    const int r = hxa_gemm_launch(g, st);
-    return r == HXA_OK ? HXA_OK : fail(r, "block gemm N=%d K=%d epi=%d rejected", w.N, w.K, epi);
   };
   auto gemm = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
                   const float *gate, hxa_h *out_t, long ldo_t, int split, int ksplit, long zstride) -> int {
@@ -590,11 +591,14 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     const HxaGemm g1 = make(o, D, BT, w, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0);
     int bm = 0, bn = 0, nw = 0, rounds = 0;
     split_o = w.K % 64 == 0 && hxa_gemm_plan(g1, &bm, &bn, &nw, &rounds) == HXA_OK && rounds == 1 && bm * bn <= 128 * 128;
-    if (!split_o) {
-      const int r = hxa_gemm_launch(g1, st);
-      return r == HXA_OK ? HXA_OK : fail(r, "block gemm N=%d K=%d rejected", w.N, w.K);
+    HxaGemm g = g1;
+    if (split_o) {
+      g.epi = HXA_EPI_PARTIAL;
+      g.ksplit = 2;
+      g.out_zstride = (long)BT * D;
     }
-    return gemm(o, D, BT, w, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D);
+    const int r = hxa_gemm_launch(g, st);
+    return r == HXA_OK ? HXA_OK : fail(r, "block gemm N=%d K=%d rejected", w.N, w.K);
   };
   if (d->kind == 0) {
     const float *gain = pv.vec;
@@ -610,6 +614,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     // un-normalised projections (M_STOP)
     const bool fuse = stop == 0;
     if (fuse) hn = HeadNorm{2 * D, gain, gain + 128, D, cosT, sinT};
+    pf0 = &Wo;
     TRY(gemm(h, D, BT, Wqkv, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
     STAGE_DONE();
     if (!fuse) TRY(hxa_rmsrope_launch(qk, k, gain, gain + 128, ldqk, BT, H, cosT, sinT, T, st));
@@ -618,6 +623,8 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     // gated residual x += gate * f16(o Wo) (blk.c:162): without a stage dump it is applied by the next site's LN
     // kernel, which reads x anyway (same fma, so the same x); the projection is then a plain store into t1
+    pf0 = &Wcq;
+    pf1 = &Wckv;
     TRY(fuse ? deferred_proj(Wo) : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 1: cross-attention (blk.c:163-169)
@@ -627,6 +634,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     // cross q from h and the text k / v from ctx are independent: one launch, the text tiles filling the CUs the
     // 1536-token projection leaves idle
     if (fuse) hn = HeadNorm{D, gain + 256, gain + 256, D, nullptr, nullptr};  // cross q: RMSNorm * gain (blk.c:166)
+    pf0 = &Wco;
     const HxaGemm gq = make(h, D, BT, Wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
     if (fuse) hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
     const HxaGemm gkv = make((const hxa_h *)ctx, d->DC, BC, Wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0);
@@ -642,13 +650,15 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     TRY(attn(qk, ck, D, cvT, BC, d->C, d->C, (long)d->C * D, d->C));
     STAGE_DONE();
+    pf0 = &W1;
     TRY(fuse ? deferred_proj(Wco) : gemm(o, D, BT, Wco, HXA_EPI_RESADD, nullptr, 0, x, mod + 5 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 2: MLP (blk.c:170-174)
     TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 5 * D,
                                    mod + 6 * D, mod + 7 * D, nullptr, 1e-6f, h, D, st));
     STAGE_DONE();
-    TRY(up_with_prefetch(h, W1, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, W2));
+    pf0 = &W2;
+    TRY(gemm(h, D, BT, W1, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     TRY(down_resadd(mid, W2, mod + 8 * D));
     STAGE_DONE();
@@ -661,18 +671,21 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     STAGE_DONE();  // the reference's LoRA-A GEMM stage (no LoRA)
     hn = HeadNorm{2 * D, gq, gk, D, cosT, sinT};  // q, k: RMSNorm * gain + RoPE in the GEMM (moss blk.c:239-242, mode 3)
+    pf0 = &Wo;
     TRY(gemm(h, D, BT, Wqkv, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
     STAGE_DONE();
     TRY(attn(qk, k, ldqk, vT, BT, T, d->nvalid, (long)T * ldqk, T));
     STAGE_DONE();
     const bool fuse = stop == 0;  // residual deferred into the FFN's RMS-mod kernel (same fma) unless dumping stages
+    pf0 = &Wug;
     TRY(fuse ? deferred_proj(Wo) : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // FFN half (moss blk.c:248-259)
     TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 2 * D,
                                    mod + 3 * D, mod + 4 * D, n2, 1e-6f, h, D, st));
     STAGE_DONE();
-    TRY(up_with_prefetch(h, Wug, HXA_EPI_SITU, Wdn));
+    pf0 = &Wdn;
+    TRY(gemm(h, D, BT, Wug, HXA_EPI_SITU, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     TRY(down_resadd(mid, Wdn, mod + 5 * D));
     STAGE_DONE();
