@@ -518,10 +518,12 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     const float *cs, *sn;
   };
   HeadNorm hn{};
-  // the weights of the projection(s) after the next one (pf0 .. pf1, adjacent in the pack), which the next
-  // projection brings into L2 / MALL after its main loop when both are fp16: the following GEMM then starts on warm
-  // weights (cold, they cost the MLP-down 62 -> 75 us at 1536 tokens, the others 1-3 us; with int8 / int4 weights the
-  // touch measured neutral to 1% slower and is not made). Applies to one projection, like hn.
+  // the weights (pf0 .. pf1, adjacent in the pack) that the next projection brings into L2 / MALL after its main
+  // loop when both are fp16, so that the GEMM after it starts on warm weights. Used for the MLP-up -> MLP-down pair:
+  // the down GEMM's short k steps leave its lookahead too short for weights arriving cold from HBM (62 us warm,
+  // 75 us cold at 1536 tokens). The other projections lose 1-3 us cold, less than a touch adds to the short store
+  // epilogues before them; with int8 / int4 weights the touch measured neutral to 1% slower and is not made.
+  // Applies to one projection, like hn.
   const HxaWeight *pf0 = nullptr, *pf1 = nullptr;
   auto make = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
                   const float *gate, hxa_h *out_t, long ldo_t, int split, int ksplit, long zstride) -> HxaGemm {
@@ -614,7 +616,6 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     // un-normalised projections (M_STOP)
     const bool fuse = stop == 0;
     if (fuse) hn = HeadNorm{2 * D, gain, gain + 128, D, cosT, sinT};
-    pf0 = &Wo;
     TRY(gemm(h, D, BT, Wqkv, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
     STAGE_DONE();
     if (!fuse) TRY(hxa_rmsrope_launch(qk, k, gain, gain + 128, ldqk, BT, H, cosT, sinT, T, st));
@@ -623,8 +624,6 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     // gated residual x += gate * f16(o Wo) (blk.c:162): without a stage dump it is applied by the next site's LN
     // kernel, which reads x anyway (same fma, so the same x); the projection is then a plain store into t1
-    pf0 = &Wcq;
-    pf1 = &Wckv;
     TRY(fuse ? deferred_proj(Wo) : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 1: cross-attention (blk.c:163-169)
@@ -634,7 +633,6 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     // cross q from h and the text k / v from ctx are independent: one launch, the text tiles filling the CUs the
     // 1536-token projection leaves idle
     if (fuse) hn = HeadNorm{D, gain + 256, gain + 256, D, nullptr, nullptr};  // cross q: RMSNorm * gain (blk.c:166)
-    pf0 = &Wco;
     const HxaGemm gq = make(h, D, BT, Wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
     if (fuse) hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
     const HxaGemm gkv = make((const hxa_h *)ctx, d->DC, BC, Wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0);
@@ -650,7 +648,6 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     TRY(attn(qk, ck, D, cvT, BC, d->C, d->C, (long)d->C * D, d->C));
     STAGE_DONE();
-    pf0 = &W1;
     TRY(fuse ? deferred_proj(Wco) : gemm(o, D, BT, Wco, HXA_EPI_RESADD, nullptr, 0, x, mod + 5 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 2: MLP (blk.c:170-174)
@@ -671,13 +668,11 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     STAGE_DONE();  // the reference's LoRA-A GEMM stage (no LoRA)
     hn = HeadNorm{2 * D, gq, gk, D, cosT, sinT};  // q, k: RMSNorm * gain + RoPE in the GEMM (moss blk.c:239-242, mode 3)
-    pf0 = &Wo;
     TRY(gemm(h, D, BT, Wqkv, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
     STAGE_DONE();
     TRY(attn(qk, k, ldqk, vT, BT, T, d->nvalid, (long)T * ldqk, T));
     STAGE_DONE();
     const bool fuse = stop == 0;  // residual deferred into the FFN's RMS-mod kernel (same fma) unless dumping stages
-    pf0 = &Wug;
     TRY(fuse ? deferred_proj(Wo) : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // FFN half (moss blk.c:248-259)
