@@ -11,7 +11,7 @@
 // the end. Each wave owns 32 queries and keeps Q in registers.
 //
 // Per 64-key tile a wave computes S^T = K . Q^T (v_mfma_f32_32x32x16_f16), so a lane holds 16 scores of ONE query
-// and the row max needs a single shfl_xor(32). K rows are stored in LDS with rows 4-7 and 8-11 of every 16 swapped,
+// and the row max needs a single exchange between the wave's two halves (v_permlane32_swap). K rows are stored in LDS with rows 4-7 and 8-11 of every 16 swapped,
 // which makes the scores of lane l (keys 8*(l/32)+0..7 of each 16-key slice) exactly the B operand of
 // O^T += V^T . P^T: P goes from the accumulator to the PV MFMA with one fp16 conversion, and each V^T fragment is one
 // 16-byte LDS read. K and V^T tiles move global -> LDS directly (global_load_lds_dwordx4), XOR-swizzled so the
@@ -38,6 +38,15 @@ HXA_DEV int krow_key(int i) {
 }
 
 HXA_DEV float16_t mfma(half8_t a, half8_t b, float16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+
+// every lane l gets the values of lanes l % 32 (lo) and l % 32 + 32 (hi): one v_permlane32_swap, no LDS round trip.
+// Combining lo and hi gives lanes l and l ^ 32 bit-identical results.
+HXA_DEV void halves(float v, float &lo, float &hi) {
+  const int x = __builtin_bit_cast(int, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  lo = __builtin_bit_cast(float, (int)r[0]);
+  hi = __builtin_bit_cast(float, (int)r[1]);
+}
 
 // NWH waves per key half (4: 128 queries per workgroup, 8 waves; 3: 96 queries, 6 waves -- chosen per launch so
 // that the grid fills the CUs)
@@ -144,7 +153,11 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
     for (int kb2 = 0; kb2 < 2; kb2++)
 #pragma unroll
       for (int r = 0; r < 16; r++) mt = fmaxf(mt, Sc[kb2][r]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    {
+      float lo, hi;
+      halves(mt, lo, hi);
+      mt = fmaxf(lo, hi);
+    }
     const bool need = mt > mrun + RESCALE_TH;  // also when mrun is still -inf
     if (__any(need)) {
       const float alpha = need ? __builtin_amdgcn_exp2f((mrun - mt) * L2E) : 1.0f;
@@ -238,7 +251,9 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   const float a1 = mrun == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((mrun - m) * L2E);
   const float a2 = m2 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m2 - m) * L2E);
   const float lp = lsum * a1 + l2 * a2;
-  const float ltot = lp + __shfl_xor(lp, 32);
+  float llo, lhi;
+  halves(lp, llo, lhi);
+  const float ltot = llo + lhi;
   const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
 #pragma unroll
   for (int d = 0; d < 4; d++)
