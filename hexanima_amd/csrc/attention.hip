@@ -136,10 +136,12 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
     wait_vm<0>();
     __builtin_amdgcn_s_barrier();  // tile i V^T and tile i+1 K landed; every wave is done with tiles i-1 / i reads
     asm volatile("" ::: "memory");
-    if (i + 2 < nmine) load_kv(i + 2, true, false);
-    if (i + 1 < nmine) load_kv(i + 1, false, true);
     const bool cur = i < nmine, nxt = i + 1 < nmine;
-    if (!cur) return;
+    if (!cur) {
+      if (i + 2 < nmine) load_kv(i + 2, true, false);
+      if (i + 1 < nmine) load_kv(i + 1, false, true);
+      return;
+    }
     const int key0 = (t0 + i) * KT;
     if (key0 + KT > p.nvalid) {
 #pragma unroll
@@ -207,6 +209,9 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
       }
     }
     lsum += ls[0] + ls[1];
+    // the next tiles' loads after the QK / exponential block, not ahead of it (their issue would delay the softmax)
+    if (i + 2 < nmine) load_kv(i + 2, true, false);
+    if (i + 1 < nmine) load_kv(i + 1, false, true);
     half8_t va[2];
     __builtin_amdgcn_sched_barrier(0);
     va[0] = vfrag(0);
