@@ -82,8 +82,39 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   // local tile i -> LDS: 16 KB of K (rows of 256 B, 16 chunks, chunk c at c ^ (row & 15)) and 16 KB of V^T (rows of
   // 128 B, 8 chunks, chunk c at c ^ ((row >> 1) & 7)); the 16 + 16 blocks of 1 KB are dealt round-robin over the NWH
   // waves of the half. Keys past NKV read a valid row (their probability is 0).
+  // A tile that lies wholly below NKV moves only a wave-uniform base: each lane's byte offsets within the tile are
+  // fixed (koff / voff, computed once), so those loads take the scalar-base form with no per-lane address math.
+  constexpr int NLD = (16 + NWH - 1) / NWH;
+  uint32_t koff[NLD], voff[NLD];
+#pragma unroll
+  for (int j = 0; j < NLD; j++) {
+    const int blk = min(j * NWH + wq, 15);
+    const int row = 4 * blk + (lane >> 4), c = (lane & 15) ^ (row & 15);
+    koff[j] = ((uint32_t)krow_key(row) * (uint32_t)p.ldk + c * 8) * 2u;
+    const int d = 8 * blk + (lane >> 3), cv = (lane & 7) ^ ((d >> 1) & 7);
+    voff[j] = ((uint32_t)d * (uint32_t)p.ldvt + cv * 8) * 2u;
+  }
   auto load_kv = [&](int i, bool with_k, bool with_v) {
     const int key0 = (t0 + i) * KT;
+    if (key0 + KT <= p.NKV) {
+      if (with_k) {
+        const hxa_h *kt = k + (long)key0 * p.ldk;
+#pragma unroll
+        for (int j = 0; j < NLD; j++) {
+          const int blk = j * NWH + wq;
+          if (16 % NWH == 0 || blk < 16) g2l16_sbase(kt, koff[j], kbuf(i) + blk * 1024);
+        }
+      }
+      if (with_v) {
+        const hxa_h *vtt = vt + key0;
+#pragma unroll
+        for (int j = 0; j < NLD; j++) {
+          const int blk = j * NWH + wq;
+          if (16 % NWH == 0 || blk < 16) g2l16_sbase(vtt, voff[j], vbuf(i) + blk * 1024);
+        }
+      }
+      return;
+    }
     if (with_k) {
       uint8_t *dst = kbuf(i);
 #pragma unroll
@@ -280,6 +311,8 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   if (p.T <= 0 || p.NKV <= 0 || p.H <= 0 || p.batch <= 0) return HXA_E_ARG;
   if (p.nvalid < 1 || p.nvalid > p.NKV) return HXA_E_ARG;
   if ((p.NKV % 8) || (p.ldq % 8) || (p.ldk % 8) || (p.ldvt % 8) || (p.ldo % 4) || p.ldvt < p.NKV) return HXA_E_ARG;
+  // per-lane byte offsets within a K / V^T tile are 32-bit: 64 key rows of K and 128 rows of V^T stay below 2^31
+  if (p.ldk >= (1 << 24) || p.ldvt >= (1 << 23)) return HXA_E_ARG;
   if (((uintptr_t)p.q | (uintptr_t)p.k | (uintptr_t)p.vt) % 16 || (uintptr_t)p.o % 8) return HXA_E_ARG;
   if (p.q_bstride % 8 || p.k_bstride % 8 || p.vt_bstride % 8 || p.o_bstride % 4) return HXA_E_ARG;
   static bool attr = false;

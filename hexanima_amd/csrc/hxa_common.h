@@ -50,6 +50,13 @@ HXA_DEV void g2l16_opaque(const void *g, const void *lds_ptr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
 }
 
+// The same load in the scalar-base form: a wave-uniform 64-bit base in SGPRs plus a 32-bit per-lane byte offset
+// (unsigned; keep it below 2^31), so a loop that moves only the base does no per-lane 64-bit address arithmetic.
+HXA_DEV void g2l16_sbase(const void *sbase, uint32_t off, const void *lds_ptr) {
+  const uint32_t la = (uint32_t)(uintptr_t)(lds_void_t *)lds_ptr;
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(sbase), "s"(la) : "memory", "m0");
+}
+
 // Cross-lane moves inside a 16-lane DPP row (VALU, no LDS round trip).
 template <int CTRL>
 HXA_DEV float dpp_f(float v) {

@@ -135,7 +135,7 @@ int hxa_gemm_headnorm(const void *A, long lda, int M, int fmt, const void *w, co
                       void *out, long ldo, void *out_t, long ldo_t, int split_col, int norm_cols, const float *gain0,
                       const float *gain1, int gain_split, const float *cosT, const float *sinT, int ttab, void *stream);
 /* attention over heads of 128 (blk.c:54-91): q [T][ldq], k [NKV][ldk], vt [H*128][ldvt] (V transposed),
- * o [T][ldo]; keys >= nvalid masked; batch images at element strides qb/kb/vb/ob. */
+ * o [T][ldo]; keys >= nvalid masked; batch images at element strides qb/kb/vb/ob; ldk < 2^24, ldvt < 2^23. */
 int hxa_attention(const void *q, long ldq, const void *k, long ldk, const void *vt, long ldvt, void *o, long ldo, int T,
                   int NKV, int nvalid, int H, int batch, long qb, long kb, long vb, long ob, void *stream);
 /* h = f16(norm(x) * (1 + scale) [* w] + shift); LN when w == NULL (kern.c:38-65), RMS otherwise (moss kern.c:353) */

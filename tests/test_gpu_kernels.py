@@ -330,6 +330,18 @@ def test_gemm_rejects_bad_shapes():
 
 
 # ------------------------------------------------------------------------------------------------ attention
+def test_attention_rejects_bad_strides():
+    """Row pitches whose per-lane tile offsets would not fit 31 bits, and NKV not a multiple of 8, are argument errors
+    (-12) reported before any launch."""
+    hip = _hip()
+    say("attention argument checks")
+    d = hip.DeviceArray((64, 128), np.float16, zero=True)
+    L = hip.lib()
+    assert L.hxa_attention(d.ptr, 128, d.ptr, 1 << 24, d.ptr, 64, d.ptr, 128, 64, 64, 64, 1, 1, 0, 0, 0, 0, None) == -12
+    assert L.hxa_attention(d.ptr, 128, d.ptr, 128, d.ptr, 1 << 23, d.ptr, 128, 64, 64, 64, 1, 1, 0, 0, 0, 0, None) == -12
+    assert L.hxa_attention(d.ptr, 128, d.ptr, 128, d.ptr, 64, d.ptr, 128, 64, 60, 60, 1, 1, 0, 0, 0, 0, None) == -12
+
+
 def _attn(hip, q, k, v, nvalid=None, batch=1):
     T, D = q.shape[0] // batch, q.shape[1]
     NKV = k.shape[0] // batch
