@@ -70,6 +70,37 @@ HXA_DEV void prefetch_share(const GemmParams &p, int wg, int nwg, int tid, int n
 }
 
 // tile (tm, tn) of workgroup bid
+// Byte offsets of one lane's 16-byte load chunks from the tile corner (row m0 of A / row n0 of W, k group 0). They
+// are the same for every k tile, so the loaders compute them once and then issue each load as a wave-uniform base
+// (moved per k tile, in SGPRs) plus this offset: no per-lane 64-bit address arithmetic in the k loop. Rows past
+// the end are clamped to the last row. A chunk: 16 rows x 64 B per 1 KB block, swizzle c ^ ((row >> 2) & 3).
+HXA_DEV uint32_t a_lane_off(const GemmParams &p, int blk, int lane, int m0) {
+  const int row = blk * 16 + (lane >> 2), cl = (lane & 3) ^ ((row >> 2) & 3);
+  return ((uint32_t)(min(m0 + row, p.M - 1) - m0) * (uint32_t)p.lda + cl * 8) * 2u;
+}
+// W chunk c of a stage: fp16 rows of 64 B (4 chunks), q8 rows of 32 B (2 chunks), q4 rows of 16 B (1 chunk)
+template <int FMT>
+HXA_DEV uint32_t w_lane_off(const GemmParams &p, int chunk, int n0) {
+  if constexpr (FMT == HXA_W_F16) {
+    const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3);
+    return ((uint32_t)(min(n0 + row, p.N - 1) - n0) * (uint32_t)p.w_rs + cl * 8) * 2u;
+  } else if constexpr (FMT == HXA_W_Q8) {
+    const int row = chunk >> 1, cl = (chunk & 1) ^ ((row >> 3) & 1);
+    return (uint32_t)(min(n0 + row, p.N - 1) - n0) * (uint32_t)p.w_rs + cl * 16;
+  } else {
+    return (uint32_t)(min(n0 + chunk, p.N - 1) - n0) * (uint32_t)p.w_rs;
+  }
+}
+// the k tile's A / W corners: A row m0, column k0; W row n0, k group k0 / 32
+HXA_DEV const uint8_t *a_tile_base(const GemmParams &p, int m0, int k0) {
+  return (const uint8_t *)(p.A + (long)m0 * p.lda + k0);
+}
+template <int FMT>
+HXA_DEV const uint8_t *w_tile_base(const GemmParams &p, int n0, int k0) {
+  constexpr long ES = FMT == HXA_W_F16 ? 2 : 1;
+  return (const uint8_t *)p.W + ((long)n0 * p.w_rs + (long)(k0 >> 5) * p.w_gs) * ES;
+}
+
 HXA_DEV void tile_coords(const GemmParams &p, int bid, int &tm, int &tn) {
   const int ntiles = p.tiles_m * p.tiles_n;
   if (p.xcd_gm > 0) {
@@ -399,41 +430,36 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
 
   // ---- loader: stage s <- k tile kt. A and fp16 W rows are 64 B (4 chunks of 16 B) stored with the chunk swizzle
   // c ^ ((row >> 2) & 3); q8 rows are 32 B with chunk swizzle c ^ ((row >> 3) & 1); q4 rows are 16 B.
-  auto issue = [&](int s, int kt) {
+  constexpr int NAI = BM / 16;  // 1 KB A instructions (16 rows) per stage
+  constexpr int NAL = (NAI + NW - 1) / NW, NWL = (G::TW + NW - 1) / NW;  // this wave's A / W loads per stage
+  uint32_t aoff[NAL], woff[NWL];
+#pragma unroll
+  for (int a = 0; a < NAL; a++) aoff[a] = a_lane_off(p, min(a * NW + wave, NAI - 1), lane, m0);
+#pragma unroll
+  for (int t = 0; t < NWL; t++) woff[t] = w_lane_off<FMT>(p, min((t * NW + wave) * 64 + lane, G::W_BYTES / 16 - 1), n0);
+  // between(q) runs before load slot q (q < NAL + NWL) in a region of its own: the scheduler does not see these asm
+  // loads as memory instructions, so only such fences keep them spread over the MFMAs instead of in one burst
+  auto issue = [&](int s, int kt, auto between) {
     uint8_t *st = lds8 + s * G::STAGE;
     const int k0 = kbase + min(kt, p.Kslice / BK - 1) * BK;  // tiles past the end reload the last one (never read)
-    constexpr int NAI = BM / 16;  // 1 KB A instructions (16 rows) per stage
+    const uint8_t *ab = a_tile_base(p, m0, k0), *wb = w_tile_base<FMT>(p, n0, k0);
 #pragma unroll
     for (int a0 = 0; a0 < NAI; a0 += NW) {
       const int a = a0 + wave;
-      if (NAI % NW == 0 || a < NAI) {
-        const int r0 = a * 16, row = r0 + (lane >> 2);
-        const int cl = (lane & 3) ^ ((row >> 2) & 3);
-        const int m = min(m0 + row, p.M - 1);
-        g2l16_opaque(p.A + (long)m * p.lda + k0 + cl * 8, st + r0 * 64);
-      }
+      between(a0 / NW);
+      if (NAI % NW == 0 || a < NAI) g2l16_sbase(ab, aoff[a0 / NW], st + a * 1024);
+      __builtin_amdgcn_sched_barrier(0);
     }
     uint8_t *ws = st + G::A_BYTES;
 #pragma unroll
     for (int t0 = 0; t0 < G::TW; t0 += NW) {
       const int t = t0 + wave;
+      between(NAL + t0 / NW);
       if (G::TW % NW == 0 || t < G::TW) {
         const int chunk = t * 64 + lane;
-        if ((G::W_BYTES / 16) % 64 == 0 || chunk < G::W_BYTES / 16) {
-          // W row n, k group k0/32: one strided address form covers both layouts (no branch in the loop)
-          const long og = (long)(k0 >> 5) * p.w_gs;
-          if (FMT == HXA_W_F16) {
-            const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3), n = min(n0 + row, p.N - 1);
-            g2l16_opaque((const hxa_h *)p.W + n * p.w_rs + og + cl * 8, ws + t * 1024);
-          } else if (FMT == HXA_W_Q8) {
-            const int row = chunk >> 1, cl = (chunk & 1) ^ ((row >> 3) & 1), n = min(n0 + row, p.N - 1);
-            g2l16_opaque((const int8_t *)p.W + n * p.w_rs + og + cl * 16, ws + t * 1024);
-          } else {
-            const int row = chunk, n = min(n0 + row, p.N - 1);
-            g2l16_opaque((const uint8_t *)p.W + n * p.w_rs + og, ws + t * 1024);
-          }
-        }
+        if ((G::W_BYTES / 16) % 64 == 0 || chunk < G::W_BYTES / 16) g2l16_sbase(wb, woff[t0 / NW], ws + t * 1024);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (FMT != HXA_W_F16 && wave == 0) {
       const int g = k0 >> 5;
@@ -531,17 +557,12 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
     __builtin_amdgcn_s_barrier();             // stage kt+1 visible; every wave holds its stage kt fragments
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    issue(kt % NS, kt + NS);
-    mfma_range(ca[0], cb[0], 2, NMF);
+    // the remaining slice-0 MFMAs one per load slot, then the rest with the fragment reads of stage kt+1
+    issue(kt % NS, kt + NS, [&](int q) { mfma_range(ca[0], cb[0], 2 + q, 3 + q); });
+    mfma_range(ca[0], cb[0], 2 + NAL + NWL, NMF);
     dequant(1, cb, cq, cs, cz);
     read_frags((kt + 1) % NS, na, nb, nq, ns, nz);
     mfma_range(ca[1], cb[1], 0, NMF);
-    constexpr int NV = (BM / 16 + NW - 1) / NW + (G::TW + NW - 1) / NW + 2;  // upper bound of this wave's VMEM loads
-#pragma unroll
-    for (int q = 0; q < NV; q++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one VMEM (direct-to-LDS) load
-    }
 #pragma unroll
     for (int q = 0; q < 2 * (MI + NI); q++) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
@@ -554,7 +575,7 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   static_assert(NS == PD + 1, "ring of PD + 1 stages");
   half8_t fa0[2][MI], fb0[2][NI], fa1[2][MI], fb1[2][NI];
 #pragma unroll
-  for (int s = 0; s < NS; s++) issue(s, s);
+  for (int s = 0; s < NS; s++) issue(s, s, [](int) {});
   wait_stage<BM, BN, FMT, ASYM, NW, NS - 2>(wave);  // tiles 0 and 1 complete
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
@@ -653,31 +674,23 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
   const int nk = p.Kslice / BK;
 
   // group 1: stage s <- k tile kt (clamped past the end: dummy reloads keep the vmcnt accounting constant)
+  // per-lane offsets from the tile corner, fixed over the k loop (only group 1 issues loads)
+  constexpr int NLP = (NAI + TW) / NWG;
+  uint32_t loff[NLP];
+#pragma unroll
+  for (int j = 0; j < NLP; j++) {
+    const int t = j * NWG + wl;
+    loff[j] = t < NAI ? a_lane_off(p, t, lane, m0) : w_lane_off<FMT>(p, (t - NAI) * 64 + lane, n0);
+  }
   auto issue = [&](int s, int kt) {
     uint8_t *st = lds8 + s * G::STAGE;
     const int k0 = kbase + min(kt, nk - 1) * BK;
-    const long og = (long)(k0 >> 5) * p.w_gs;
+    const uint8_t *ab = a_tile_base(p, m0, k0), *wb = w_tile_base<FMT>(p, n0, k0);
 #pragma unroll
     for (int t0 = 0; t0 < NAI + TW; t0 += NWG) {
       const int t = t0 + wl;
-      if (t < NAI) {
-        const int r0 = t * 16, row = r0 + (lane >> 2);
-        const int cl = (lane & 3) ^ ((row >> 2) & 3);
-        const int m = min(m0 + row, p.M - 1);
-        g2l16_opaque(p.A + (long)m * p.lda + k0 + cl * 8, st + r0 * 64);
-      } else {
-        const int tw = t - NAI, chunk = tw * 64 + lane;
-        if constexpr (FMT == HXA_W_F16) {
-          const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3), n = min(n0 + row, p.N - 1);
-          g2l16_opaque((const hxa_h *)p.W + n * p.w_rs + og + cl * 8, st + G::A_BYTES + tw * 1024);
-        } else if constexpr (FMT == HXA_W_Q8) {
-          const int row = chunk >> 1, cl = (chunk & 1) ^ ((row >> 3) & 1), n = min(n0 + row, p.N - 1);
-          g2l16_opaque((const int8_t *)p.W + n * p.w_rs + og + cl * 16, st + G::A_BYTES + tw * 1024);
-        } else {
-          const int row = chunk, n = min(n0 + row, p.N - 1);
-          g2l16_opaque((const uint8_t *)p.W + n * p.w_rs + og, st + G::A_BYTES + tw * 1024);
-        }
-      }
+      if (t < NAI) g2l16_sbase(ab, loff[t0 / NWG], st + t * 1024);
+      else g2l16_sbase(wb, loff[t0 / NWG], st + G::A_BYTES + (t - NAI) * 1024);
     }
     if constexpr (NVEC > 0) {  // scale (and offset) vector of the stage's k group: wave 0 of the group
       if (wl == 0) {
@@ -1002,6 +1015,8 @@ static int gemm_prepare(const HxaGemm &g, GemmParams &p, int &bm, int &bn, int &
     p.w_rs = wkt ? cb : (long)w.K / 32 * cb;
     p.w_gs = wkt ? cb * w.N : cb;
   }
+  // the loaders' per-lane offsets within a tile (up to 256 rows) are 32-bit: keep them below 2^31
+  if (g.lda >= (1L << 22) || p.w_rs * (w.fmt == HXA_W_F16 ? 2 : 1) >= (1L << 23)) return HXA_E_ARG;
   p.M = g.M;
   p.N = w.N;
   p.Ktot = w.K;
