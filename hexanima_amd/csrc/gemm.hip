@@ -1163,3 +1163,57 @@ int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st) {
   }
   return e == hipSuccess ? HXA_OK : HXA_E_HIP;
 }
+
+// ---- int8 / int4 weights -> fp16, k-tiled [K/32][N][32] (the layout the fp16 kernels read) ----
+// One 8-k slot of one row per thread (the 16-byte fragment unit of the main loops), dequantised with their own
+// dq8_word / dq4_word, so the values are the same f16(q * s) (+ z) bits the fused path feeds its MFMAs. Reads
+// w.w / w.s / w.z once, writes 2 N K bytes.
+namespace {
+template <int FMT, bool ASYM>
+__global__ __launch_bounds__(256) void dequant_kernel(GemmParams p, hxa_h *out) {
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;  // 8-k slot c = t % 4 of group i = t / 4 (g = i / N, n = i % N)
+  const long i = t >> 2;
+  const int c = (int)(t & 3);
+  if (i >= (long)(p.Ktot / 32) * p.N) return;
+  const long g = i / p.N, n = i % p.N;
+  const hxa_h s = p.S[i];
+  const half2_t s2 = {s, s};
+  const hxa_h z = ASYM ? p.Z[i] : (hxa_h)0.0f;
+  const half2_t z2 = {z, z};
+  const uint8_t *src = (const uint8_t *)p.W + n * p.w_rs + g * p.w_gs;
+  uint32_t o[4];
+  if constexpr (FMT == HXA_W_Q8) {
+    const uint2_t v = *(const uint2_t *)(src + 8 * c);
+    dq8_word(v.x, s2, o[0], o[1]);
+    dq8_word(v.y, s2, o[2], o[3]);
+  } else {
+    dq4_word<ASYM>(*(const uint32_t *)(src + 4 * c), s2, z2, o);
+  }
+  // lanes write consecutive 16-byte chunks: 1 KB per wave store
+  *(uint4_t *)(out + i * 32 + c * 8) = (uint4_t){o[0], o[1], o[2], o[3]};
+}
+}  // namespace
+
+int hxa_dequant_launch(const HxaWeight &w0, hxa_h *out, hipStream_t st) {
+  HxaWeight w = w0;
+  const int wkt = (w.fmt & HXA_W_KTILED) ? 1 : 0;
+  w.fmt &= ~HXA_W_KTILED;
+  if ((w.fmt != HXA_W_Q8 && w.fmt != HXA_W_Q4) || w.s == nullptr || w.N <= 0 || w.K <= 0 || w.K % 32 != 0)
+    return HXA_E_ARG;
+  if (((uintptr_t)w.w % 16) != 0 || ((uintptr_t)out % 16) != 0) return HXA_E_ARG;
+  GemmParams p{};
+  p.W = w.w;
+  p.S = w.s;
+  p.Z = w.z;
+  p.N = w.N;
+  p.Ktot = w.K;
+  const long cb = w.fmt == HXA_W_Q4 ? 16 : 32;
+  p.w_rs = wkt ? cb : (long)w.K / 32 * cb;
+  p.w_gs = wkt ? cb * w.N : cb;
+  const long slots = (long)(w.K / 32) * w.N * 4;
+  const dim3 grid((unsigned)((slots + 255) / 256));
+  if (w.fmt == HXA_W_Q8) hipLaunchKernelGGL((dequant_kernel<HXA_W_Q8, false>), grid, dim3(256), 0, st, p, out);
+  else if (w.z) hipLaunchKernelGGL((dequant_kernel<HXA_W_Q4, true>), grid, dim3(256), 0, st, p, out);
+  else hipLaunchKernelGGL((dequant_kernel<HXA_W_Q4, false>), grid, dim3(256), 0, st, p, out);
+  return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
+}

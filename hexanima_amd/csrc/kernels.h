@@ -37,6 +37,8 @@ int hxa_gemm_plan(const HxaGemm &g, int *bm, int *bn, int *nw, int *rounds);
 // two independent GEMMs in one launch (the second takes the first one's tile; same weight format, no split-K);
 // falls back to two launches when the tile has no paired kernel
 int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st);
+// int8 / int4 weight -> fp16 k-tiled [K/32][N][32] at out (2 N K bytes): the same values the GEMM main loops use
+int hxa_dequant_launch(const HxaWeight &w, hxa_h *out, hipStream_t st);
 
 struct HxaAttn {
   const hxa_h *q, *k, *vt;  // q [T][ldq], k [NKV][ldk] (head h at column h*128); vt [H*128][ldvt] (keys contiguous)

@@ -392,12 +392,18 @@ static PackView pack_view(const hxa_block_dims *d, const void *pack) {
 // ---------------------------------------------------------------------------------------------------------------
 // block workspace + orchestrator
 // ---------------------------------------------------------------------------------------------------------------
-enum { WS_H, WS_Q, WS_K, WS_VT, WS_O, WS_T1, WS_MID, WS_CK, WS_CVT, WS_T2, WS_N };
+enum { WS_H, WS_Q, WS_K, WS_VT, WS_O, WS_T1, WS_MID, WS_CK, WS_CVT, WS_T2, WS_DQ, WS_N };
 struct WsLayout {
   long off[WS_N];
   long ld[WS_N];
   long total;
+  long dq_bytes;  // size of WS_DQ (0: no quantised projection is dequantised first)
 };
+// Quantised attention-output and MLP-down projections (N <= K) at this many rows or more run as one dequantisation
+// pass into fp16 (WS_DQ) and the fp16 kernels: at 1536 tokens the main loops' per-MFMA dequantisation costs those
+// shapes 11-18% more than the pass. Wider projections (qkv, MLP up) keep the fused form, and so does the cross q,
+// whose launch is paired with the text k / v projection of the same weight format.
+constexpr long DQ_MIN_ROWS = 1024;
 static WsLayout ws_layout(const hxa_block_dims *d) {
   const long BT = (long)d->batch * d->T, BC = (long)d->batch * d->C, D = d->D;
   WsLayout L{};
@@ -424,6 +430,11 @@ static WsLayout ws_layout(const hxa_block_dims *d) {
     L.off[WS_CK] = L.off[WS_CVT] = 0;
     L.ld[WS_CK] = L.ld[WS_CVT] = 0;
   }
+  // fp16 copy of one int8 / int4 o-class (D x D) or MLP-down (D x F) weight (dq_rows)
+  const bool qa = d->fmt_attn != HXA_W_F16, qm = d->fmt_mlp != HXA_W_F16;
+  const long dq = BT >= DQ_MIN_ROWS ? std::max(qa ? 2 * D * D : 0L, qm ? 2 * D * (long)d->F : 0L) : 0;
+  put(WS_DQ, dq, d->F);
+  L.dq_bytes = dq;
   L.total = off;
   return L;
 }
@@ -562,6 +573,20 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     g.split_col = split;
     return g;
   };
+  // the weight a projection runs on: w itself, or (int8 / int4, N <= K, WS_DQ sized) its fp16 k-tiled copy made
+  // now in WS_DQ. One copy at a time: each is consumed by the launch that follows it on this stream.
+  HxaWeight wdq{};
+  auto prep = [&](const HxaWeight &w, const HxaWeight *&wp) -> int {
+    wp = &w;
+    const int f = w.fmt & ~HXA_W_KTILED;
+    if (f == HXA_W_F16 || w.N > w.K || BT < DQ_MIN_ROWS || 2L * w.N * w.K > L.dq_bytes) return HXA_OK;
+    hxa_h *buf = (hxa_h *)(w8 + L.off[WS_DQ]);
+    const int r = hxa_dequant_launch(w, buf, st);
+    if (r != HXA_OK) return fail(r, "block dequant N=%d K=%d rejected", w.N, w.K);
+    wdq = HxaWeight{HXA_W_F16 | HXA_W_KTILED, w.N, w.K, buf, nullptr, nullptr};
+    wp = &wdq;
+    return HXA_OK;
+  };
   auto gemm = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
                   const float *gate, hxa_h *out_t, long ldo_t, int split, int ksplit, long zstride) -> int {
     const int r = hxa_gemm_launch(make(A, lda, M, w, epi, out, ldo, xx, gate, out_t, ldo_t, split, ksplit, zstride), st);
@@ -580,7 +605,9 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   // the GPU at N = D) then the residual; measured faster than the single-launch HXA_EPI_RESADD_SPLIT2 form, whose
   // 128-wide tiles leave a quarter of the CUs idle at 1536 x 2048
   auto down_resadd = [&](const hxa_h *a, const HxaWeight &w, const float *gate) -> int {
-    TRY(gemm(a, F, BT, w, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
+    const HxaWeight *wp;
+    TRY(prep(w, wp));
+    TRY(gemm(a, F, BT, *wp, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
     return defer ? HXA_OK : hxa_resadd2_launch(x, D, t1, t2, D, BT, D, gate, st);
   };
   // the attention output projection whose gated residual the next norm applies (no stage dump): one K pass into
@@ -590,7 +617,9 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   // 256x256 tiles or of several rounds). split_o says which, for that norm's t2.
   bool split_o = false;
   auto deferred_proj = [&](const HxaWeight &w) -> int {
-    const HxaGemm g1 = make(o, D, BT, w, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0);
+    const HxaWeight *wp;
+    TRY(prep(w, wp));
+    const HxaGemm g1 = make(o, D, BT, *wp, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0);
     int bm = 0, bn = 0, nw = 0, rounds = 0;
     split_o = w.K % 64 == 0 && hxa_gemm_plan(g1, &bm, &bn, &nw, &rounds) == HXA_OK && rounds == 1 && bm * bn <= 128 * 128;
     HxaGemm g = g1;

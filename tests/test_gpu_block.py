@@ -120,12 +120,14 @@ def test_anima_block_stages_and_batch():
                 assert rel(g.astype(np.float32), buf[k].view(np.float16).astype(np.float32)) < tol, (stop, k)
 
 
-def test_moss_block_joint_attention_q8_q4():
-    """MOSS-class block (joint attention with a key mask, RMS-mod, SiTU, int8 attention / int4 MLP weights)."""
+@pytest.mark.parametrize("T,nv,gh,gw", [(544, 520, 20, 24), (1088, 1060, 30, 34)])
+def test_moss_block_joint_attention_q8_q4(T, nv, gh, gw):
+    """MOSS-class block (joint attention with a key mask, RMS-mod, SiTU, int8 attention / int4 MLP weights). At
+    1088 rows the int8 o projection and the int4 MLP-down run through the fp16 dequantisation pass."""
     hip = _hip()
-    say("moss block T=544 nvalid=520 D=3072 F=4096 q8/q4")
+    say(f"moss block T={T} nvalid={nv} D=3072 F=4096 q8/q4")
     rng = np.random.default_rng(11)
-    D, F, T, nv = 3072, 4096, 544, 520
+    D, F = 3072, 4096
     H = D // 128
     shapes = hip.pack_shapes(1, D, F, 0)
     mats = []
@@ -139,7 +141,7 @@ def test_moss_block_joint_attention_q8_q4():
     x[nv:] = 0
     mod6 = (rng.standard_normal((6, D)) * 0.2).astype(np.float32)
     bands = (1.0 / 10000.0 ** (np.arange(16) / 16)).astype(np.float32)
-    cs, sn = hxo.rope_moss(20, 24, 40, bands)  # 480 image + 40 text tokens
+    cs, sn = hxo.rope_moss(gh, gw, 40, bands)  # gh * gw image + 40 text tokens
     cos = np.concatenate([cs, np.ones((T - nv, 64), np.float32)])
     sin = np.concatenate([sn, np.zeros((T - nv, 64), np.float32)])
     d = hip.BlockDims(1, D, H, F, 0, 0, T, 1, nv, 1, 2, 0)
