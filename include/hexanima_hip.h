@@ -186,7 +186,8 @@ typedef struct {
   int fmt_attn, fmt_mlp;
   int gelu;      /* Anima MLP activation: 0 erf (reference block), 1 tanh */
 } hxa_block_dims;
-/* bytes of the activation workspace of hxa_block_run */
+/* bytes of the activation workspace of hxa_block_run (with int8 / int4 weights and batch*T >= 1024 it includes one
+ * fp16 copy of the largest o-class or MLP-down weight, which those projections run from) */
 long hxa_block_ws_bytes(const hxa_block_dims *d);
 /* One block, everything on the device:
  *   x    [batch*T][D] fp32 residual stream, updated in place
@@ -197,7 +198,8 @@ long hxa_block_ws_bytes(const hxa_block_dims *d);
  *   stop: stop after this many stages (0 = all); stage_us: per-stage microseconds (NULL: not timed). */
 int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod, const float *cosT,
                   const float *sinT, void *ws, int stop, int *stage_us, int nstage, void *stream);
-/* stage buffers of the workspace: which 0 h, 1 q, 2 k, 3 vT ([D][batch*T]), 4 o, 5 t1, 6 mid, 7 ck, 8 cvT, 9 t2;
+/* stage buffers of the workspace: which 0 h, 1 q, 2 k, 3 vT ([D][batch*T]), 4 o, 5 t1, 6 mid, 7 ck, 8 cvT, 9 t2,
+ * 10 the fp16 weight copy;
  * returns the device pointer and its row stride in elements */
 void *hxa_block_ws_buf(const hxa_block_dims *d, void *ws, int which, long *ld);
 
