@@ -404,6 +404,8 @@ struct WsLayout {
 // shapes 11-18% more than the pass. Wider projections (qkv, MLP up) keep the fused form, and so does the cross q,
 // whose launch is paired with the text k / v projection of the same weight format.
 constexpr long DQ_MIN_ROWS = 1024;
+// from this many rows on the pass also pays for the wide projections (qkv, MLP up / up-gate)
+constexpr long DQ_WIDE_ROWS = 4096;
 static WsLayout ws_layout(const hxa_block_dims *d) {
   const long BT = (long)d->batch * d->T, BC = (long)d->batch * d->C, D = d->D;
   WsLayout L{};
@@ -432,7 +434,10 @@ static WsLayout ws_layout(const hxa_block_dims *d) {
   }
   // fp16 copy of one int8 / int4 o-class (D x D) or MLP-down (D x F) weight (dq_rows)
   const bool qa = d->fmt_attn != HXA_W_F16, qm = d->fmt_mlp != HXA_W_F16;
-  const long dq = BT >= DQ_MIN_ROWS ? std::max(qa ? 2 * D * D : 0L, qm ? 2 * D * (long)d->F : 0L) : 0;
+  const long F = d->F, FU = d->kind == 1 ? 2 * F : F;  // MLP up rows (MOSS: up | gate)
+  long dq = 0;
+  if (BT >= DQ_WIDE_ROWS) dq = std::max(qa ? 2 * 3 * D * D : 0L, qm ? 2 * std::max(FU, F) * D : 0L);
+  else if (BT >= DQ_MIN_ROWS) dq = std::max(qa ? 2 * D * D : 0L, qm ? 2 * D * F : 0L);
   put(WS_DQ, dq, d->F);
   L.dq_bytes = dq;
   L.total = off;
@@ -579,7 +584,8 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   auto prep = [&](const HxaWeight &w, const HxaWeight *&wp) -> int {
     wp = &w;
     const int f = w.fmt & ~HXA_W_KTILED;
-    if (f == HXA_W_F16 || w.N > w.K || BT < DQ_MIN_ROWS || 2L * w.N * w.K > L.dq_bytes) return HXA_OK;
+    if (f == HXA_W_F16 || (w.N > w.K && BT < DQ_WIDE_ROWS) || BT < DQ_MIN_ROWS || 2L * w.N * w.K > L.dq_bytes)
+      return HXA_OK;
     hxa_h *buf = (hxa_h *)(w8 + L.off[WS_DQ]);
     const int r = hxa_dequant_launch(w, buf, st);
     if (r != HXA_OK) return fail(r, "block dequant N=%d K=%d rejected", w.N, w.K);
@@ -645,7 +651,11 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     // un-normalised projections (M_STOP)
     const bool fuse = stop == 0;
     if (fuse) hn = HeadNorm{2 * D, gain, gain + 128, D, cosT, sinT};
-    TRY(gemm(h, D, BT, Wqkv, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
+    {
+      const HxaWeight *wp;
+      TRY(prep(Wqkv, wp));
+      TRY(gemm(h, D, BT, *wp, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
+    }
     STAGE_DONE();
     if (!fuse) TRY(hxa_rmsrope_launch(qk, k, gain, gain + 128, ldqk, BT, H, cosT, sinT, T, st));
     STAGE_DONE();
@@ -684,7 +694,11 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
                                    mod + 6 * D, mod + 7 * D, nullptr, 1e-6f, h, D, st));
     STAGE_DONE();
     pf0 = &W2;
-    TRY(gemm(h, D, BT, W1, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    {
+      const HxaWeight *wp;
+      TRY(prep(W1, wp));
+      TRY(gemm(h, D, BT, *wp, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    }
     STAGE_DONE();
     TRY(down_resadd(mid, W2, mod + 8 * D));
     STAGE_DONE();
@@ -697,7 +711,11 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     STAGE_DONE();  // the reference's LoRA-A GEMM stage (no LoRA)
     hn = HeadNorm{2 * D, gq, gk, D, cosT, sinT};  // q, k: RMSNorm * gain + RoPE in the GEMM (moss blk.c:239-242, mode 3)
-    TRY(gemm(h, D, BT, Wqkv, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
+    {
+      const HxaWeight *wp;
+      TRY(prep(Wqkv, wp));
+      TRY(gemm(h, D, BT, *wp, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
+    }
     STAGE_DONE();
     TRY(attn(qk, k, ldqk, vT, BT, T, d->nvalid, (long)T * ldqk, T));
     STAGE_DONE();
@@ -709,7 +727,11 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
                                    mod + 3 * D, mod + 4 * D, n2, 1e-6f, h, D, st));
     STAGE_DONE();
     pf0 = &Wdn;
-    TRY(gemm(h, D, BT, Wug, HXA_EPI_SITU, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    {
+      const HxaWeight *wp;
+      TRY(prep(Wug, wp));
+      TRY(gemm(h, D, BT, *wp, HXA_EPI_SITU, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    }
     STAGE_DONE();
     TRY(down_resadd(mid, Wdn, mod + 5 * D));
     STAGE_DONE();

@@ -120,10 +120,11 @@ def test_anima_block_stages_and_batch():
                 assert rel(g.astype(np.float32), buf[k].view(np.float16).astype(np.float32)) < tol, (stop, k)
 
 
-@pytest.mark.parametrize("T,nv,gh,gw", [(544, 520, 20, 24), (1088, 1060, 30, 34)])
+@pytest.mark.parametrize("T,nv,gh,gw", [(544, 520, 20, 24), (1088, 1060, 30, 34), (4128, 4100, 58, 70)])
 def test_moss_block_joint_attention_q8_q4(T, nv, gh, gw):
     """MOSS-class block (joint attention with a key mask, RMS-mod, SiTU, int8 attention / int4 MLP weights). At
-    1088 rows the int8 o projection and the int4 MLP-down run through the fp16 dequantisation pass."""
+    1088 rows the int8 o projection and the int4 MLP-down run through the fp16 dequantisation pass, at 4128 rows
+    every projection does."""
     hip = _hip()
     say(f"moss block T={T} nvalid={nv} D=3072 F=4096 q8/q4")
     rng = np.random.default_rng(11)
