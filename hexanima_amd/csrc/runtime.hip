@@ -399,10 +399,9 @@ struct WsLayout {
   long total;
   long dq_bytes;  // size of WS_DQ (0: no quantised projection is dequantised first)
 };
-// Quantised attention-output and MLP-down projections (N <= K) at this many rows or more run as one dequantisation
-// pass into fp16 (WS_DQ) and the fp16 kernels: at 1536 tokens the main loops' per-MFMA dequantisation costs those
-// shapes 11-18% more than the pass. Wider projections (qkv, MLP up) keep the fused form, and so does the cross q,
-// whose launch is paired with the text k / v projection of the same weight format.
+// Quantised attention-output, cross-q and MLP-down projections (N <= K) at this many rows or more run as one
+// dequantisation pass into fp16 (WS_DQ) and the fp16 kernels: at 1536 tokens the main loops' per-MFMA
+// dequantisation costs those shapes 11-18% more than the pass. Wider projections (qkv, MLP up) keep the fused form.
 constexpr long DQ_MIN_ROWS = 1024;
 // from this many rows on the pass also pays for the wide projections (qkv, MLP up / up-gate)
 constexpr long DQ_WIDE_ROWS = 4096;
@@ -672,7 +671,9 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     // cross q from h and the text k / v from ctx are independent: one launch, the text tiles filling the CUs the
     // 1536-token projection leaves idle
     if (fuse) hn = HeadNorm{D, gain + 256, gain + 256, D, nullptr, nullptr};  // cross q: RMSNorm * gain (blk.c:166)
-    const HxaGemm gq = make(h, D, BT, Wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
+    const HxaWeight *wcq;
+    TRY(prep(Wcq, wcq));
+    const HxaGemm gq = make(h, D, BT, *wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
     if (fuse) hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
     const HxaGemm gkv = make((const hxa_h *)ctx, d->DC, BC, Wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0);
     {
