@@ -397,7 +397,8 @@ struct WsLayout {
   long off[WS_N];
   long ld[WS_N];
   long total;
-  long dq_bytes;  // size of WS_DQ (0: no quantised projection is dequantised first)
+  long dq_bytes;            // size of WS_DQ's first slot (0: no quantised projection is dequantised first)
+  long dq2_off, dq2_bytes;  // its second slot (text k / v weight)
 };
 // Quantised attention-output, cross-q and MLP-down projections (N <= K) at this many rows or more run as one
 // dequantisation pass into fp16 (WS_DQ) and the fp16 kernels: at 1536 tokens the main loops' per-MFMA
@@ -437,8 +438,12 @@ static WsLayout ws_layout(const hxa_block_dims *d) {
   long dq = 0;
   if (BT >= DQ_WIDE_ROWS) dq = std::max(qa ? 2 * 3 * D * D : 0L, qm ? 2 * std::max(FU, F) * D : 0L);
   else if (BT >= DQ_MIN_ROWS) dq = std::max(qa ? 2 * D * D : 0L, qm ? 2 * D * F : 0L);
-  put(WS_DQ, dq, d->F);
+  // a second slot for the text k / v weight (2D x DC), so that it and the cross q run as one paired fp16 launch
+  const long dq2 = d->kind == 0 && qa && BT >= DQ_MIN_ROWS ? al256(2 * 2 * D * (long)d->DC) : 0;
+  put(WS_DQ, al256(dq) + dq2, d->F);
   L.dq_bytes = dq;
+  L.dq2_off = al256(dq);
+  L.dq2_bytes = dq2;
   L.total = off;
   return L;
 }
@@ -580,16 +585,19 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   // the weight a projection runs on: w itself, or (int8 / int4, N <= K, WS_DQ sized) its fp16 k-tiled copy made
   // now in WS_DQ. One copy at a time: each is consumed by the launch that follows it on this stream.
   HxaWeight wdq{};
-  auto prep = [&](const HxaWeight &w, const HxaWeight *&wp) -> int {
+  HxaWeight wdq2{};
+  auto prep = [&](const HxaWeight &w, const HxaWeight *&wp, int slot = 0) -> int {
     wp = &w;
     const int f = w.fmt & ~HXA_W_KTILED;
-    if (f == HXA_W_F16 || (w.N > w.K && BT < DQ_WIDE_ROWS) || BT < DQ_MIN_ROWS || 2L * w.N * w.K > L.dq_bytes)
-      return HXA_OK;
-    hxa_h *buf = (hxa_h *)(w8 + L.off[WS_DQ]);
+    if (f == HXA_W_F16 || BT < DQ_MIN_ROWS) return HXA_OK;
+    if (slot == 0 && ((w.N > w.K && BT < DQ_WIDE_ROWS) || 2L * w.N * w.K > L.dq_bytes)) return HXA_OK;
+    if (slot == 1 && 2L * w.N * w.K > L.dq2_bytes) return HXA_OK;
+    hxa_h *buf = (hxa_h *)(w8 + L.off[WS_DQ] + (slot ? L.dq2_off : 0));
     const int r = hxa_dequant_launch(w, buf, st);
     if (r != HXA_OK) return fail(r, "block dequant N=%d K=%d rejected", w.N, w.K);
-    wdq = HxaWeight{HXA_W_F16 | HXA_W_KTILED, w.N, w.K, buf, nullptr, nullptr};
-    wp = &wdq;
+    HxaWeight &dst = slot ? wdq2 : wdq;
+    dst = HxaWeight{HXA_W_F16 | HXA_W_KTILED, w.N, w.K, buf, nullptr, nullptr};
+    wp = &dst;
     return HXA_OK;
   };
   auto gemm = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
@@ -675,7 +683,9 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     TRY(prep(Wcq, wcq));
     const HxaGemm gq = make(h, D, BT, *wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
     if (fuse) hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
-    const HxaGemm gkv = make((const hxa_h *)ctx, d->DC, BC, Wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0);
+    const HxaWeight *wckv;
+    TRY(prep(Wckv, wckv, 1));
+    const HxaGemm gkv = make((const hxa_h *)ctx, d->DC, BC, *wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0);
     {
       const int r = hxa_gemm_pair_launch(gq, gkv, st);
       if (r != HXA_OK) return fail(r, "block cross q / text k v gemms rejected");
