@@ -242,8 +242,8 @@ def microbench():
     pack = hip.DeviceArray((total,), np.uint8)
     for i, ((n, kk), (wo, _)) in enumerate(zip(hip.pack_shapes(0, D, F, DC), mats)):
         hip.check(L.hxa_fill_normal(C.c_void_p(pack.ptr + wo), 1, n * kk, 40 + i, 0.0, 0.02, s), "fill")
-    gain = np.concatenate([np.full(128, 128 ** -0.5), np.ones(128), np.full(128, 128 ** -0.5), np.ones(128)])
-    hip.check(L.hxa_h2d(C.c_void_p(pack.ptr + voff), gain.astype(np.float32).ctypes.data, 4 * 512), "gain")
+    gain = np.concatenate([np.full(128, 128 ** -0.5), np.ones(128), np.full(128, 128 ** -0.5), np.ones(128)]).astype(np.float32)
+    hip.check(L.hxa_h2d(C.c_void_p(pack.ptr + voff), gain.ctypes.data, 4 * 512), "gain")
     x = hip.DeviceArray((T, D), np.float32)
     ctx = hip.DeviceArray((C_TXT, DC), np.float16)
     mod = hip.DeviceArray((9, D), np.float32)

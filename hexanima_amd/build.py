@@ -34,11 +34,23 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source and link the shared library; returns its path."""
+def _stale(src: str) -> bool:
+    obj = os.path.join(OBJ, src.replace(".hip", ".o"))
+    if not os.path.exists(obj):
+        return True
+    deps = [os.path.join(CSRC, src)] + [os.path.join(CSRC, h) for h in os.listdir(CSRC) if h.endswith(".h")]
+    deps.append(os.path.join(os.path.dirname(HERE), "include", "hexanima_hip.h"))
+    return max(os.path.getmtime(d) for d in deps) > os.path.getmtime(obj)
+
+
+def build(verbose: bool = False, incremental: bool = False) -> str:
+    """Compile every HIP source (incremental: only those newer than their object) and link the shared library;
+    returns its path."""
     os.makedirs(OBJ, exist_ok=True)
+    todo = [s for s in SOURCES if _stale(s)] if incremental else SOURCES
     with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        list(ex.map(_compile, todo))
+    objs = [os.path.join(OBJ, s.replace(".hip", ".o")) for s in SOURCES]
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -51,5 +63,5 @@ def build(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv)
     sys.exit(0)

@@ -37,7 +37,9 @@ struct Dit {
   void *ws = nullptr;
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
-  float *sig_host = nullptr;  // pinned
+  float *sig_host = nullptr;   // pinned source of the per-step sigma upload
+  hipEvent_t sig_ev = nullptr;  // recorded after that upload: sig_host is rewritten only once it has completed
+  bool sig_pending = false;
 };
 
 thread_local char g_derr[256];
@@ -207,9 +209,18 @@ int record_step(Dit &d, int mode) {
   return HXA_OK;
 }
 
+// sigma, sigma_next and their difference into device memory, where the (captured) step reads them. The copy source
+// is pinned memory owned by the runner: an asynchronous copy may read its source after the call has returned, so
+// the source must outlive it, and it is rewritten only after the previous upload has completed.
 int set_sigma(Dit &d, float s0, float s1) {
-  float h[4] = {s0, s1, s1 - s0, 0.0f};  // pageable source: staged before the call returns
-  DHIP(hipMemcpyAsync(d.sig, h, sizeof h, hipMemcpyHostToDevice, d.st));
+  if (d.sig_pending) DHIP(hipEventSynchronize(d.sig_ev));
+  d.sig_host[0] = s0;
+  d.sig_host[1] = s1;
+  d.sig_host[2] = s1 - s0;
+  d.sig_host[3] = 0.0f;
+  DHIP(hipMemcpyAsync(d.sig, d.sig_host, 4 * sizeof(float), hipMemcpyHostToDevice, d.st));
+  DHIP(hipEventRecord(d.sig_ev, d.st));
+  d.sig_pending = true;
   return HXA_OK;
 }
 
@@ -255,6 +266,11 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   if (hipStreamCreateWithFlags(&d.st, hipStreamNonBlocking) != hipSuccess) {
     delete dp;
     return dfail(HXA_E_RESOURCE, "dit: stream");
+  }
+  if (hipHostMalloc((void **)&d.sig_host, 4 * sizeof(float), hipHostMallocDefault) != hipSuccess ||
+      hipEventCreateWithFlags(&d.sig_ev, hipEventDisableTiming) != hipSuccess) {
+    hxa_dit_destroy(dp);
+    return dfail(HXA_E_RESOURCE, "dit: pinned sigma buffer");
   }
   d.pack_bytes = hxa_pack_layout(b.kind, D, b.F, b.DC, b.fmt_attn, b.fmt_mlp, nullptr, 0);
   d.packs.assign(cfg->nblocks, nullptr);
@@ -339,6 +355,8 @@ extern "C" int hxa_dit_destroy(void *p) {
   if (d->modw_all) (void)hipFree(d->modw_all);
   void *bufs[] = {d->glue, d->lat, d->vel, d->tok, d->x, d->sinus, d->cvec, d->mods, d->fmod, d->sig, d->cosT, d->sinT, d->ones, d->ctx16, d->ws};
   for (void *q : bufs) if (q) (void)hipFree(q);
+  if (d->sig_ev) (void)hipEventDestroy(d->sig_ev);
+  if (d->sig_host) (void)hipHostFree(d->sig_host);
   if (d->st) (void)hipStreamDestroy(d->st);
   delete d;
   return HXA_OK;

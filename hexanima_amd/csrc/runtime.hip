@@ -277,6 +277,16 @@ extern "C" int hxa_resadd2(float *x, long ldx, const void *t1, const void *t2, l
   if (r != HXA_OK) return fail(r, "resadd2 rejected");
   return HXA_OK;
 }
+extern "C" int hxa_dequant(int fmt, const void *w, const void *s, const void *z, int N, int K, void *out, void *stream) {
+  if (!w || !s || !out) return fail(HXA_E_ARG, "dequant: null pointer");
+  const int f = fmt & ~HXA_W_KTILED;
+  if (f != HXA_W_Q8 && f != HXA_W_Q4) return fail(HXA_E_MODE, "dequant: format %d", fmt);
+  if (z && f != HXA_W_Q4) return fail(HXA_E_ARG, "dequant: mins only with int4 weights");
+  const HxaWeight wt{fmt, N, K, w, (const hxa_h *)s, (const hxa_h *)z};
+  const int r = hxa_dequant_launch(wt, (hxa_h *)out, S(stream));
+  if (r != HXA_OK) return fail(r, "dequant N=%d K=%d fmt=%d rejected", N, K, fmt);
+  return HXA_OK;
+}
 extern "C" int hxa_fill_normal(void *dst, int dtype, size_t n, uint64_t seed, float mean, float std, void *stream) {
   return hxa_fill_normal_launch(dst, dtype, n, seed, mean, std, S(stream));
 }

@@ -76,6 +76,7 @@ _SIGS = {
     "hxa_norm_mod": (I, [P, L, I, I, P, P, P, F, P, L, P]),
     "hxa_rmsrope": (I, [P, P, P, P, L, I, I, P, P, I, P]),
     "hxa_resadd2": (I, [P, L, P, P, L, I, I, P, P]),
+    "hxa_dequant": (I, [I, P, P, P, I, I, P, P]),
     "hxa_fill_normal": (I, [P, I, SZ, U64, F, F, P]),
     "hxa_fill_uniform_int": (I, [P, I, SZ, U64, I, I, P]),
     "hxa_fill_const": (I, [P, I, SZ, F, P]),

@@ -152,6 +152,11 @@ int hxa_rmsrope(void *q0, void *q1, const float *g0, const float *g1, long ldq, 
 /* x += gate * (t1 + t2) (kern.c:330-339) */
 int hxa_resadd2(float *x, long ldx, const void *t1, const void *t2, long ldt, int T, int D, const float *gate,
                 void *stream);
+/* int8 / int4 weight w [N][K] (scales s [K/32][N], q4 mins z or NULL) -> fp16 k-tiled out [K/32][N][32]: the values
+ * f16(q*s) (q4: f16(nibble*s + z), or f16((nibble-8)*s) without z) that hxa_gemm's main loops feed their MFMAs,
+ * written once to memory (the block runner's dequantisation pass; gemm2.c:19-35 dq_tile, moss gemm2.c:39-56
+ * dq4_tile). fmt may carry HXA_W_KTILED for a k-tiled source. out: 2 N K bytes, 16-byte aligned. */
+int hxa_dequant(int fmt, const void *w, const void *s, const void *z, int N, int K, void *out, void *stream);
 /* synthetic data: dtype 0 fp32, 1 fp16 */
 int hxa_fill_normal(void *dst, int dtype, size_t n, uint64_t seed, float mean, float std, void *stream);
 int hxa_fill_uniform_int(void *dst, int bits, size_t n, uint64_t seed, int lo, int hi, void *stream);

@@ -1,11 +1,13 @@
 """GPU parity of whole blocks, the reference block ABI (mega_block) and the DiT runner against the CPU oracle.
 
 Metrics are the reference's own (hexagon/mega/cmp_block.py:5-6 rel err on the block delta + cosine;
-moss/cmp_blk.py:9 per-stage rel err). Tolerances, stated per test: block delta rel err <= 5e-3 and cosine
->= 0.99999 against the oracle in reference-rounding mode; per-stage fp16 buffers rel err <= 2e-3 before
-attention and <= 1e-2 after it (the oracle keeps the reference's fp16 S/P/rowsum rounding, the GPU an fp32 online
-softmax)."""
+moss/cmp_blk.py:9 per-stage rel err) plus the max abs difference of the fp32 output. Tolerances are stated per
+test, at about 3x the error measured on MI355X (the measured value is quoted beside each), so a regression of a
+few x fails. Cosine thresholds are 1 - R^2 for the rel tolerance R (the two are tied: 1 - cos ~ rel^2 / 2). The
+oracle keeps the reference's fp16 S / P / rowsum rounding in attention, the GPU an fp32 online softmax with fp16
+probabilities, and the GPU GEMMs accumulate in fp32 where the oracle uses double: these set the achieved error."""
 import ctypes as C
+import time
 
 import numpy as np
 import pytest
@@ -63,28 +65,47 @@ def run_block_gpu(hip, d, img, x, ctx, mod, cos, sin, stop=0):
     return dx.numpy(), ws, list(us)
 
 
-@pytest.mark.parametrize("fmt,D,F,label", [(0, 2048, 8192, "cfg0 2B fp16 block"), (1, 2560, 10240, "cfg3 2.9B q8 block")])
-def test_anima_block_full_size(fmt, D, F, label):
-    """Config 0 (and the config-3 q8 block): 1536 image tokens, 256 text tokens of width 1024, tanh GELU."""
+def metrics_line(got, ref, x0):
+    """rel err on the delta, cosine of the deltas (cmp_block.py:5-6) and max |got - ref| on the fp32 output."""
+    r, c = delta_metrics(got, ref, x0)
+    mx = float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))))
+    return r, c, mx
+
+
+# tolerances (rel err on delta, max abs): measured 5.1e-4 / 8.0e-4 (cfg0), 1.1e-3 / 6.5e-3 (cfg3), 5.0e-4 / 7.9e-4
+# (int4), 5.0e-4 / 1.0e-3 (batch 4, both formats)
+@pytest.mark.parametrize("fmt,D,F,batch,tol,label", [
+    (0, 2048, 8192, 1, (1.5e-3, 2.5e-3), "cfg0 2B fp16 block"),
+    (1, 2560, 10240, 1, (3.3e-3, 2e-2), "cfg3 2.9B q8 block"),
+    (2, 2048, 8192, 1, (1.5e-3, 2.5e-3), "2B int4 block"),
+    (0, 2048, 8192, 4, (1.5e-3, 3.2e-3), "cfg2 2B fp16 block, batch 4"),
+    (1, 2048, 8192, 4, (1.5e-3, 3.2e-3), "2B q8 block, batch 4 (6144 rows: every projection through the dequantisation pass)")])
+def test_anima_block_full_size(fmt, D, F, batch, tol, label):
+    """Config 0 (and the config-3 q8 block, int4 weights, and the config-2 batch of 4 images): 1536 image tokens per
+    image, 256 text tokens of width 1024, tanh GELU; every image against the oracle."""
     hip = _hip()
-    say(f"{label}: T=1536 D={D} F={F} fmt={fmt}")
-    rng = np.random.default_rng(100 + fmt)
+    say(f"{label}: T=1536 D={D} F={F} fmt={fmt} batch={batch}")
+    rng = np.random.default_rng(100 + fmt + 10 * batch)
     T, C_, DC = 1536, 256, 1024
     img, w, H = make_anima_pack(hip, rng, D, F, DC, fmt)
-    x = rng.standard_normal((T, D)).astype(np.float32)
-    ctx = f16(rng.standard_normal((C_, DC)))
+    x = rng.standard_normal((batch * T, D)).astype(np.float32)
+    ctx = f16(rng.standard_normal((batch * C_, DC)))
     mod9 = cfg0_mod9(D, rng)
     cos, sin = hxo.rope_anima(48, 32)
-    d = hip.BlockDims(0, D, H, F, C_, DC, T, 1, T, fmt, fmt, 1)
+    d = hip.BlockDims(0, D, H, F, C_, DC, T, batch, T, fmt, fmt, 1)
     got, ws, us = run_block_gpu(hip, d, img, x, ctx, mod9, cos, sin)
     print("stage us:", us[:13], flush=True)
-    ref, buf, n = hxo.anima_block(x, ctx, mod9, cos, sin, w, H=H, F=F, gelu=1, attn_mode=0)
-    r, c = delta_metrics(got, ref, x)
-    print(f"rel err on delta {r:.2e} cos {c:.7f}", flush=True)
-    assert r < 5e-3 and c > 0.99999
-    # per-stage (cmp_blk.py style) from the last site's buffers: MLP hidden
-    mid = hip.read_ws(d, ws, hip.WS_MID, T, F)
-    assert rel(mid.astype(np.float32), buf["mid"].view(np.float16).astype(np.float32)) < 1e-2
+    for b in range(batch):
+        sl = slice(b * T, (b + 1) * T)
+        ref, buf, n = hxo.anima_block(x[sl], ctx[b * C_:(b + 1) * C_], mod9, cos, sin, w, H=H, F=F, gelu=1, attn_mode=0)
+        r, c, mx = metrics_line(got[sl], ref, x[sl])
+        print(f"image {b}: rel err on delta {r:.2e} cos {c:.8f} max abs {mx:.2e}", flush=True)
+        assert r < tol[0] and c > 1 - tol[0] ** 2 and mx < tol[1]
+        # per-stage (cmp_blk.py style) from the last site's buffers: MLP hidden (measured 3.0e-4 - 3.6e-4)
+        mid = hip.read_ws(d, ws, hip.WS_MID, batch * T, F)[sl]
+        rm = rel(mid.astype(np.float32), buf["mid"].view(np.float16).astype(np.float32))
+        print(f"image {b}: MLP hidden rel err {rm:.2e}", flush=True)
+        assert rm < 1.1e-3
 
 
 def test_anima_block_stages_and_batch():
@@ -109,31 +130,39 @@ def test_anima_block_stages_and_batch():
                 assert np.array_equal(gx, x[b * T:(b + 1) * T])
             else:
                 r, c = delta_metrics(gx, ref, x[b * T:(b + 1) * T])
-                assert r < 5e-3 and c > 0.99999
+                print(f"stop {stop} image {b}: rel err on delta {r:.2e}", flush=True)
+                assert r < 2e-3 and c > 1 - 2e-3 ** 2  # measured 6.6e-4
             for k in keys:
                 which = {"h": hip.WS_H, "q": hip.WS_Q, "k": hip.WS_K, "v": hip.WS_VT, "o": hip.WS_O}[k]
                 if k == "v":
                     g = hip.read_ws(d, ws, which, D, 2 * T)[:, b * T:(b + 1) * T].T
                 else:
                     g = hip.read_ws(d, ws, which, 2 * T, D)[b * T:(b + 1) * T]
-                tol = 1e-2 if k == "o" else 2e-3
-                assert rel(g.astype(np.float32), buf[k].view(np.float16).astype(np.float32)) < tol, (stop, k)
+                # measured: h 7.6e-6, q / k / v 2.8e-5 (raw) and 3.7e-5 (normalised), o 6.2e-4
+                tol = {"h": 2.3e-5, "o": 1.9e-3}.get(k, 1.1e-4)
+                e = rel(g.astype(np.float32), buf[k].view(np.float16).astype(np.float32))
+                print(f"stop {stop} image {b}: {k} rel err {e:.2e}", flush=True)
+                assert e < tol, (stop, k)
 
 
-@pytest.mark.parametrize("T,nv,gh,gw", [(544, 520, 20, 24), (1088, 1060, 30, 34), (4128, 4100, 58, 70)])
-def test_moss_block_joint_attention_q8_q4(T, nv, gh, gw):
+# measured rel err on delta 3.7e-4 - 3.9e-4, max abs 1.4e-3 / 1.6e-3 / 1.9e-3 / 3.1e-3
+@pytest.mark.parametrize("T,nv,gh,gw,F,ntxt,maxabs", [(544, 520, 20, 24, 4096, 40, 4.5e-3), (1088, 1060, 30, 34, 4096, 40, 5e-3),
+                                                      (4128, 4100, 58, 70, 4096, 40, 6e-3),
+                                                      (6656, 6656, 64, 96, 12288, 512, 1e-2)])
+def test_moss_block_joint_attention_q8_q4(T, nv, gh, gw, F, ntxt, maxabs):
     """MOSS-class block (joint attention with a key mask, RMS-mod, SiTU, int8 attention / int4 MLP weights). At
     1088 rows the int8 o projection and the int4 MLP-down run through the fp16 dequantisation pass, at 4128 rows
-    every projection does."""
+    every projection does. The last case is config 4's own block: 6144 image tokens (64 x 96) + 512 text tokens,
+    D 3072, 24 heads, SiTU FFN 12288 (up-gate N = 24576)."""
     hip = _hip()
-    say(f"moss block T={T} nvalid={nv} D=3072 F=4096 q8/q4")
+    say(f"moss block T={T} nvalid={nv} D=3072 F={F} q8/q4")
     rng = np.random.default_rng(11)
-    D, F = 3072, 4096
+    D = 3072
     H = D // 128
     shapes = hip.pack_shapes(1, D, F, 0)
     mats = []
     for i, (N, K) in enumerate(shapes):
-        W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        W = (rng.standard_normal((N, K), dtype=np.float32) * 0.02).astype(np.float32)
         mats.append(hxo.q8_quantize(W) if i < 2 else hxo.q4_quantize(W))
     vec = np.concatenate([np.full(128, 1 / np.sqrt(128)), np.ones(128), rng.uniform(0.5, 1.5, 2 * D)]).astype(np.float32)
     img = hip.build_pack(1, D, F, 0, 1, 2, mats, vec)
@@ -142,15 +171,17 @@ def test_moss_block_joint_attention_q8_q4(T, nv, gh, gw):
     x[nv:] = 0
     mod6 = (rng.standard_normal((6, D)) * 0.2).astype(np.float32)
     bands = (1.0 / 10000.0 ** (np.arange(16) / 16)).astype(np.float32)
-    cs, sn = hxo.rope_moss(gh, gw, 40, bands)  # gh * gw image + 40 text tokens
+    cs, sn = hxo.rope_moss(gh, gw, ntxt, bands)  # gh * gw image + ntxt text tokens
     cos = np.concatenate([cs, np.ones((T - nv, 64), np.float32)])
     sin = np.concatenate([sn, np.zeros((T - nv, 64), np.float32)])
     d = hip.BlockDims(1, D, H, F, 0, 0, T, 1, nv, 1, 2, 0)
     got, ws, us = run_block_gpu(hip, d, img, x, None, mod6, cos, sin)
+    print("stage us:", us[:8], flush=True)
+    t0 = time.time()
     ref, buf, n = hxo.moss_block(x, mod6, cos, sin, w, H=H, F=F, nvalid=nv)
-    r, c = delta_metrics(got[:nv], ref[:nv], x[:nv])
-    print(f"moss rel err on delta {r:.2e} cos {c:.7f}", flush=True)
-    assert r < 5e-3 and c > 0.99999
+    r, c, mx = metrics_line(got[:nv], ref[:nv], x[:nv])
+    print(f"moss rel err on delta {r:.2e} cos {c:.8f} max abs {mx:.2e} (oracle {time.time() - t0:.1f} s)", flush=True)
+    assert r < 1.2e-3 and c > 1 - 1.2e-3 ** 2 and mx < maxabs
 
 
 # ------------------------------------------------------------------------------------------------ reference ABI
@@ -204,15 +235,9 @@ def _blk_file(rng, q8):
     return buf, ow
 
 
-@pytest.mark.parametrize("q8", [False, True])
-def test_mega_block_reference_abi(q8):
-    """Two blocks through mega_block exactly as megarun drives them (FIRST on the first, REL on the last)."""
-    hip = _hip()
-    say(f"mega_block ABI q8={q8}")
-    lib = hip.lib()
-    rng = np.random.default_rng(21 + q8)
-    D, T, NCTX = 2048, 256, 256
-    gh, gw = 16, 16
+def _abi_blob(rng, T, NCTX, gh, gw):
+    """megarun's activation blob (megarun.cpp:42-57, :150-153): x32 tiles of x, ctx16 tiles, cos / sin tiles."""
+    D = 2048
     offs, total = _megarun_layout(T, NCTX)
     blob = np.zeros(total, np.uint8)
     x = rng.standard_normal((T, D)).astype(np.float32)
@@ -223,6 +248,29 @@ def test_mega_block_reference_abi(q8):
     for nm, tab in (("COS", cos), ("SIN", sin)):  # [slab][j][32][32], angle index d = 32 j + col
         t = np.ascontiguousarray(tab.reshape(T // 32, 32, 2, 32).transpose(0, 2, 1, 3)).astype(np.float32)
         blob[offs[nm]:offs[nm] + t.nbytes] = t.view(np.uint8).reshape(-1)
+    return offs, blob, x, ctx, cos, sin
+
+
+def _abi_meta(offs, T, NCTX, q8):
+    meta = np.zeros(32, np.int32)
+    for k, v in offs.items():
+        meta[META.index(k)] = v
+    for k, v in W_OFFS.items():
+        meta[META.index(k)] = v if not q8 else v // 2048 * 1152
+    meta[META.index("NTOK")], meta[META.index("NCTX")], meta[META.index("Q8")] = T, NCTX, int(q8)
+    return meta
+
+
+@pytest.mark.parametrize("q8", [False, True])
+def test_mega_block_reference_abi(q8):
+    """Two blocks through mega_block exactly as megarun drives them (FIRST on the first, REL on the last) at
+    megarun's default 1536 tokens (gh 48, gw 32) and 256 context tokens; times[] filled per stage."""
+    hip = _hip()
+    say(f"mega_block ABI q8={q8} T=1536")
+    lib = hip.lib()
+    rng = np.random.default_rng(21 + q8)
+    D, T, NCTX = 2048, 1536, 256
+    offs, blob, x, ctx, cos, sin = _abi_blob(rng, T, NCTX, 48, 32)
     blocks = [_blk_file(rng, q8) for _ in range(2)]
     mods = [cfg0_mod9(D, rng) for _ in range(2)]
     h = C.c_uint64()
@@ -231,29 +279,30 @@ def test_mega_block_reference_abi(q8):
         hip.check(lib.hxa_register(h, 100, blob.ctypes.data, blob.nbytes, hip.KIND_BLOB), "register blob")
         for i, (wb, _) in enumerate(blocks):
             hip.check(lib.hxa_register(h, 200 + i, wb.ctypes.data, wb.nbytes, hip.KIND_WEIGHTS_ANIMA), "register w")
-        meta = np.zeros(32, np.int32)
-        for k, v in offs.items():
-            meta[META.index(k)] = v
-        for k, v in W_OFFS.items():
-            meta[META.index(k)] = v if not q8 else v // 2048 * 1152
-        meta[META.index("NTOK")], meta[META.index("NCTX")], meta[META.index("Q8")] = T, NCTX, int(q8)
-        times = np.zeros(32, np.int32)
+        meta = _abi_meta(offs, T, NCTX, q8)
         rc = C.c_int(0)
         for i in range(2):
+            times = np.full(32, -1, np.int32)
             meta[META.index("FIRST")], meta[META.index("REL")] = int(i == 0), int(i == 1)
+            t0 = time.time()
             r = lib.mega_block(h, meta.ctypes.data, 32, 200 + i, 100, mods[i].ctypes.data, mods[i].nbytes,
                                times.ctypes.data, 32, C.byref(rc))
+            wall_us = (time.time() - t0) * 1e6
             assert r == 0 and rc.value == 0, hip.last_error()
+            print(f"block {i}: times (us) {times[:13].tolist()} attn {times[17:23].tolist()} entry {times[24]}, "
+                  f"call {wall_us:.0f} us", flush=True)
+            # times[]: the 13 TICK stages of blk.c:136-175 in order, attention sub-stages at 17.., entry overhead at 24
+            assert (times[:13] >= 0).all() and (times[13:17] == 0).all() and times[24] >= 0
+            assert 0 < times[:13].sum() <= wall_us
             if i == 0:  # x stays on the device until REL
                 assert np.array_equal(blob[offs["X"]:offs["X"] + T * D * 4].view(np.float32), hxo.x32_tile(x))
-        print("times (us):", times[:13].tolist(), flush=True)
         got = hxo.x32_untile(blob[offs["X"]:offs["X"] + T * D * 4].view(np.float32).copy(), T, D)
         ref = x
         for (wb, ow), m in zip(blocks, mods):
             ref, _, _ = hxo.anima_block(ref, ctx, m, cos, sin, ow, H=16, F=8192, gelu=0)
-        r, c = delta_metrics(got, ref, x)
-        print(f"ABI rel err on delta {r:.2e} cos {c:.7f}", flush=True)
-        assert r < 5e-3 and c > 0.99999
+        r, c, mx = metrics_line(got, ref, x)
+        print(f"ABI rel err on delta {r:.2e} cos {c:.8f} max abs {mx:.2e}", flush=True)
+        assert r < 1.6e-3 and c > 1 - 1.6e-3 ** 2 and mx < 3e-3  # measured 5.3e-4, 1.0e-3
         # error paths (blk.c:110-127, :188 codes)
         r = lib.mega_block(h, meta.ctypes.data, 32, 200, 999, mods[0].ctypes.data, mods[0].nbytes, None, 0, C.byref(rc))
         assert r == 0 and rc.value == -7
@@ -263,6 +312,67 @@ def test_mega_block_reference_abi(q8):
         bad[META.index("NTOK")] = 250
         r = lib.mega_block(h, bad.ctypes.data, 32, 200, 100, mods[0].ctypes.data, mods[0].nbytes, None, 0, C.byref(rc))
         assert r == 0 and rc.value == -10
+    finally:
+        lib.mega_close(h)
+
+
+# blk.c:150-175 TICK stages, the blob buffers each one leaves to check (the reference's in-place buffers: q / k
+# after stage 3 are the normalised ones; site 1 reuses h, q, o; t holds the first MLP-down partial at 13) and the
+# rel-err tolerance of each, about 3x the value measured on MI355X; x (from stage 5 on) is checked against XTOL
+STOP_CHECKS = [(1, {"H": 1.6e-5}), (2, {"Q": 9e-5, "K": 9e-5, "V": 9e-5}), (3, {"Q": 1.2e-4, "K": 1.2e-4}),
+               (4, {"O": 1.5e-3}), (5, {}), (6, {"H": 1.2e-4}), (7, {"Q": 4e-4, "CK": 3e-5, "CV": 3.2e-5}),
+               (8, {"Q": 5e-4, "CK": 4.5e-5}), (9, {"O": 2.1e-3}), (11, {"H": 4.2e-4}), (12, {"MID": 9e-4}),
+               (13, {"T": 1.2e-3})]
+XTOL = {5: 1.7e-3, 6: 1.7e-3, 7: 1.7e-3, 8: 1.7e-3, 9: 1.7e-3, 11: 2.3e-3, 12: 2.3e-3, 13: 1.6e-3}
+
+
+def test_mega_block_stage_dumps_1536():
+    """meta[M_STOP] = n stops after n stages (blk.c:136) and leaves the stage buffers in the blob as h16 tiles, the
+    way cmp_block.py reads them: each one against the oracle's buffer at the same stage, x (written back with REL)
+    against the oracle's x, times[] filled for the n stages run and 0 after."""
+    hip = _hip()
+    say("mega_block M_STOP stage dumps T=1536")
+    lib = hip.lib()
+    rng = np.random.default_rng(31)
+    D, T, NCTX, F = 2048, 1536, 256, 8192
+    offs, blob, x, ctx, cos, sin = _abi_blob(rng, T, NCTX, 48, 32)
+    x_tiles = blob[offs["X"]:offs["X"] + T * D * 4].copy()
+    wb, ow = _blk_file(rng, False)
+    mod = cfg0_mod9(D, rng)
+    h = C.c_uint64()
+    hip.check(lib.mega_open(b"", C.byref(h)), "mega_open")
+    try:
+        hip.check(lib.hxa_register(h, 100, blob.ctypes.data, blob.nbytes, hip.KIND_BLOB), "register blob")
+        hip.check(lib.hxa_register(h, 200, wb.ctypes.data, wb.nbytes, hip.KIND_WEIGHTS_ANIMA), "register w")
+        meta = _abi_meta(offs, T, NCTX, False)
+        meta[META.index("FIRST")], meta[META.index("REL")] = 1, 1
+        rc = C.c_int(0)
+        rows = {"H": T, "Q": T, "K": T, "V": T, "O": T, "T": T, "MID": T, "CK": NCTX, "CV": NCTX}
+        cols = {"MID": F}
+        for stop, keys in STOP_CHECKS:
+            blob[offs["X"]:offs["X"] + T * D * 4] = x_tiles
+            meta[META.index("STOP")] = stop
+            times = np.full(32, -1, np.int32)
+            r = lib.mega_block(h, meta.ctypes.data, 32, 200, 100, mod.ctypes.data, mod.nbytes, times.ctypes.data, 32,
+                               C.byref(rc))
+            assert r == 0 and rc.value == 0, hip.last_error()
+            assert (times[:stop] >= 0).all() and (times[stop:17] == 0).all(), (stop, times[:17].tolist())
+            ref, buf, n = hxo.anima_block(x, ctx, mod, cos, sin, ow, H=16, F=F, gelu=0, stop=stop)
+            assert n == stop
+            gx = hxo.x32_untile(blob[offs["X"]:offs["X"] + T * D * 4].view(np.float32).copy(), T, D)
+            if stop < 5:
+                assert np.array_equal(gx, x)
+            else:
+                rx, cx_, mx = metrics_line(gx, ref, x)
+                print(f"stop {stop}: x rel err on delta {rx:.2e} cos {cx_:.8f}", flush=True)
+                assert rx < XTOL[stop] and cx_ > 1 - XTOL[stop] ** 2
+            for k, tol in keys.items():
+                R, Cc = rows[k], cols.get(k, D)
+                tiles = blob[offs[k]:offs[k] + R * Cc * 2].view(np.uint16)
+                g = hxo.h16_untile(tiles, R, Cc).view(np.float16).astype(np.float32)
+                e = rel(g, buf[k.lower()].view(np.float16).astype(np.float32))
+                print(f"stop {stop}: {k} rel err {e:.2e}", flush=True)
+                assert e < tol, (stop, k)
     finally:
         lib.mega_close(h)
 
@@ -310,7 +420,7 @@ def test_dit_small_denoise_vs_oracle():
         hip.check(lib.hxa_dit_velocity(p, 1.0, v_gpu.ctypes.data), "velocity")
         v_ref = oracle_anima_velocity(lat, ctx16, 1.0, blocks, modws, glue, D=D, H=2, F=1024, C4=C4, temb=256)
         print("velocity rel err", rel(v_gpu, v_ref), flush=True)
-        assert rel(v_gpu, v_ref) < 5e-3
+        assert rel(v_gpu, v_ref) < 4e-4  # measured 1.2e-4
         ref = lat.copy()
         for i in range(4):
             hip.check(lib.hxa_dit_step(p, sig[i], sig[i + 1], 1), "step")
@@ -319,8 +429,8 @@ def test_dit_small_denoise_vs_oracle():
         got = np.zeros_like(lat)
         hip.check(lib.hxa_dit_get_latent(p, got.ctypes.data), "get_latent")
         r, c = delta_metrics(got, ref, lat)
-        print(f"denoise rel err on delta {r:.2e} cos {c:.7f}", flush=True)
-        assert r < 5e-3 and c > 0.99999
+        print(f"denoise rel err on delta {r:.2e} cos {c:.9f}", flush=True)
+        assert r < 2e-4 and c > 1 - 2e-4 ** 2  # measured 6.0e-5
     finally:
         lib.hxa_dit_destroy(p)
 
@@ -363,8 +473,8 @@ def test_dit_moss_small_denoise_vs_oracle():
         got = np.zeros_like(lat)
         hip.check(lib.hxa_dit_get_latent(p, got.ctypes.data), "get_latent")
         r, c = delta_metrics(got, ref, lat)
-        print(f"moss denoise rel err on delta {r:.2e} cos {c:.7f}", flush=True)
-        assert r < 5e-3 and c > 0.99999
+        print(f"moss denoise rel err on delta {r:.2e} cos {c:.9f}", flush=True)
+        assert r < 6e-6 and c > 1 - 6e-6 ** 2  # measured 1.7e-6 (small gates: mostly the glue around the blocks)
     finally:
         lib.hxa_dit_destroy(p)
 

@@ -3,8 +3,8 @@
 Tolerances (fp16 storage): a GEMM output may differ from the oracle's correctly rounded value by one fp16 ulp plus
 the fp32 accumulation-order error 4 sqrt(K) 2^-24 sum|a w| (tests/_helpers.assert_gemm_close), and >= 98% of the
 outputs must be bit-identical; norm outputs by at most 1 ulp. Attention uses an fp32 online softmax,
-so it is compared with the oracle's exact-softmax mode (max abs 4e-3, rel-l2 2e-3) and with the reference-rounding
-mode (rel-l2 1e-2, the reference's own fp16 S/P rounding noise)."""
+so it is compared with the oracle's exact-softmax mode (max abs 4e-3, rel-l2 1e-3) and with the reference-rounding
+mode (rel-l2 4.7e-3, the reference's own fp16 S/P rounding noise), about 3x the measured errors."""
 import numpy as np
 import pytest
 
@@ -25,11 +25,12 @@ def say(msg):
 
 
 # ------------------------------------------------------------------------------------------------ GEMM
-def _run_gemm(hip, A, fmt, w, s, N, K, epi=0, ksplit=1, tile=None, x=None, gate=None):
+def _run_gemm(hip, A, fmt, w, s, N, K, epi=0, ksplit=1, tile=None, x=None, gate=None, z=None):
     M = A.shape[0]
     dA = hip.DeviceArray.from_numpy(f16(A))
     dW = hip.DeviceArray.from_numpy(w)
     dS = hip.DeviceArray.from_numpy(s) if s is not None else None
+    dZ = hip.DeviceArray.from_numpy(z) if z is not None else None
     resadd = epi in (hip.EPI_RESADD, hip.EPI_RESADD_SPLIT2)
     if resadd:
         dx = hip.DeviceArray.from_numpy(x.astype(np.float32))
@@ -44,7 +45,8 @@ def _run_gemm(hip, A, fmt, w, s, N, K, epi=0, ksplit=1, tile=None, x=None, gate=
     else:
         out = hip.DeviceArray((M, N), np.float16)
     ldo = {hip.EPI_STORE_T: M, hip.EPI_SITU: N // 2}.get(epi, N)
-    args = (dA.ptr, K, M, fmt, dW.ptr, dS.ptr if dS else None, None, N, K, ksplit, epi, out.ptr if out else None, ldo,
+    args = (dA.ptr, K, M, fmt, dW.ptr, dS.ptr if dS else None, dZ.ptr if dZ else None, N, K, ksplit, epi,
+            out.ptr if out else None, ldo,
             M * N, dx.ptr if resadd else None, N, dg.ptr if resadd else None)
     if tile:
         hip.check(hip.lib().hxa_gemm_tile(*args, tile[0], tile[1], tile[2] if len(tile) > 2 else 0, None), "gemm_tile")
@@ -110,6 +112,74 @@ def test_gemm_quant_tiles(fmt, tile):
     wdq = hxo.q8_dequant(q, s) if fmt == 1 else hxo.q4_dequant(q, s)
     got = _run_gemm(hip, A, fmt, q, s, N, K, tile=tile)
     assert_gemm_close(got, hxo.gemm(A, wdq), A, wdq.view(np.float16))
+
+
+def _q4a_weights(rng, N, K):
+    """Asymmetric int4 (q4a, moss/export_te.py:1-3, dequantised as moss/hexagon/mega/gemm2.c:39-56): nibble in
+    [0, 15] with a per-(32-row group, column) fp16 scale s and min z, value f16(nibble * s + z). Packed in the GPU
+    order (k0+2j at bits 4j, k0+2j+1 at bits 16+4j of each 32-bit word)."""
+    nib = rng.integers(0, 16, (N, K))
+    q = np.zeros((N, K // 8), np.uint32)
+    for j in range(8):
+        sh = 16 + 4 * (j // 2) if j % 2 else 4 * (j // 2)
+        q |= nib[:, j::8].astype(np.uint32) << sh
+    s = f16(rng.uniform(0.002, 0.01, (K // 32, N)))
+    z = f16(-8.0 * s.astype(np.float32) + rng.uniform(-0.01, 0.01, (K // 32, N)))
+    return q.view(np.uint8).reshape(N, K // 2), s.view(np.uint16), z.view(np.uint16)
+
+
+@pytest.mark.parametrize("tile", [None, (128, 128, 4), (192, 256, 4), (128, 256, 8), (192, 256, 9), (128, 256, 9)])
+def test_gemm_q4_asymmetric(tile):
+    """q4a weights (a scale and a min per group) through hxa_gemm with z != NULL, ragged in M: the dequantised-fp16
+    GEMM is the reference."""
+    hip = _hip()
+    say(f"gemm q4a tile={tile}")
+    rng = np.random.default_rng(77)
+    M, N, K = 320, 384, 512
+    A = f16(rng.standard_normal((M, K)))
+    q, s, z = _q4a_weights(rng, N, K)
+    wdq = hxo.q4_dequant(q, s, z)
+    got = _run_gemm(hip, A, 2, q, s, N, K, tile=tile, z=z)
+    assert_gemm_close(got, hxo.gemm(A, wdq), A, wdq.view(np.float16))
+
+
+@pytest.mark.parametrize("fmt,asym,ktiled", [(1, False, False), (1, False, True), (2, False, True), (2, True, False),
+                                             (2, True, True)])
+def test_dequant_pass_equals_oracle_and_fused_gemm(fmt, asym, ktiled):
+    """The block runner's dequantisation pass (hxa_dequant): its fp16 output is bit-identical to the oracle's
+    f16(q*s) / f16(nibble*s + z) (gemm2.c:19-35, moss gemm2.c:39-56), and an fp16 GEMM on it gives the same bits as
+    the fused int8 / int4 GEMM on the same tile (both feed the MFMAs the same values in the same k order)."""
+    hip = _hip()
+    say(f"dequant pass fmt={fmt} asym={asym} ktiled={ktiled}")
+    rng = np.random.default_rng(90 + fmt + 2 * asym)
+    M, N, K = 320, 384, 512
+    A = f16(rng.standard_normal((M, K)))
+    z = None
+    if fmt == 1:
+        q, s = hxo.q8_quantize((rng.standard_normal((N, K)) * 0.05).astype(np.float32))
+        wdq = hxo.q8_dequant(q, s)
+    elif asym:
+        q, s, z = _q4a_weights(rng, N, K)
+        wdq = hxo.q4_dequant(q, s, z)
+    else:
+        q, s = hxo.q4_quantize((rng.standard_normal((N, K)) * 0.05).astype(np.float32))
+        wdq = hxo.q4_dequant(q, s)
+    qb = np.ascontiguousarray(q).view(np.uint8).reshape(-1)
+    src = hip.ktile(qb, N, K) if ktiled else qb
+    fl = fmt | (hip.W_KTILED if ktiled else 0)
+    dq_, ds = hip.DeviceArray.from_numpy(src), hip.DeviceArray.from_numpy(s)
+    dz = hip.DeviceArray.from_numpy(z) if z is not None else None
+    out = hip.DeviceArray((K // 32, N, 32), np.float16)
+    hip.check(hip.lib().hxa_dequant(fl, dq_.ptr, ds.ptr, dz.ptr if dz else None, N, K, out.ptr, None), "dequant")
+    hip.sync()
+    w16 = hip.unktile(out.numpy().view(np.uint8).reshape(-1), N, K).view(np.uint16).reshape(N, K)
+    assert np.array_equal(w16, wdq)
+    kt16 = out.numpy().reshape(-1)
+    for tile in ((128, 128, 4), (192, 256, 8) if fmt == 1 else (128, 256, 8), (192, 256, 9)):
+        via_pass = _run_gemm(hip, A, hip.W_F16 | hip.W_KTILED, kt16, None, N, K, tile=tile)
+        fused = _run_gemm(hip, A, fl, src, s, N, K, tile=tile, z=z)
+        assert np.array_equal(via_pass.view(np.uint16), fused.view(np.uint16)), tile
+    assert_gemm_close(via_pass, hxo.gemm(A, wdq), A, wdq.view(np.float16))
 
 
 def test_gemm_epilogues():
@@ -358,8 +428,11 @@ def _attn(hip, q, k, v, nvalid=None, batch=1):
 
 # on 256 CUs the 1024 x 32-head case takes the 128-query workgroups (8 waves), the others the 96-query ones; odd tile
 # counts (448 keys: 7, 520 valid of 576: 9) leave the second key half one tile short
+# the last case is the MOSS-class joint attention at its own shape (6144 image + 512 text tokens, 24 heads); the
+# oracle (rows are independent) is evaluated on a sample of 416 query rows spread over all key tiles' range
 @pytest.mark.parametrize("T,NKV,nvalid,H", [(1536, 1536, 1536, 16), (1536, 256, 256, 16), (448, 448, 430, 4), (96, 64, 64, 2),
-                                            (1024, 1024, 1000, 32), (300, 512, 500, 3), (200, 576, 520, 2)])
+                                            (1024, 1024, 1000, 32), (300, 512, 500, 3), (200, 576, 520, 2),
+                                            (6656, 6656, 6656, 24)])
 def test_attention_vs_oracle(T, NKV, nvalid, H):
     hip = _hip()
     say(f"attention T={T} NKV={NKV} nvalid={nvalid} H={H}")
@@ -370,11 +443,16 @@ def test_attention_vs_oracle(T, NKV, nvalid, H):
     k = f16(rng.standard_normal((NKV, D)))
     v = f16(rng.standard_normal((NKV, D)))
     got = _attn(hip, q, k, v, nvalid).astype(np.float64)
-    exact = hxo.attention(q, k, v, nvalid, mode=1).view(np.float16).astype(np.float64)
-    refr = hxo.attention(q, k, v, nvalid, mode=0).view(np.float16).astype(np.float64)
-    assert np.max(np.abs(got - exact)) < 4e-3
-    assert rel(got, exact) < 2e-3
-    assert rel(got, refr) < 1e-2
+    rows = np.arange(T) if T * NKV * H <= 64 << 20 else np.unique(np.r_[np.arange(0, T, 16), T - 1])
+    got = got[rows]
+    exact = hxo.attention(q[rows], k, v, nvalid, mode=1).view(np.float16).astype(np.float64)
+    refr = hxo.attention(q[rows], k, v, nvalid, mode=0).view(np.float16).astype(np.float64)
+    mx, r1, r0 = np.max(np.abs(got - exact)), rel(got, exact), rel(got, refr)
+    print(f"attention rows={rows.size}: max abs {mx:.2e}, rel vs exact {r1:.2e}, rel vs reference rounding {r0:.2e}",
+          flush=True)
+    assert mx < 4e-3  # measured 9.8e-4 - 2.0e-3 (one or two fp16 ulps of outputs near 1)
+    assert r1 < 1e-3  # measured 2.1e-4 - 3.2e-4
+    assert r0 < 4.7e-3  # measured 8.2e-4 - 1.6e-3
 
 
 def test_attention_batched_images_are_independent():

@@ -4,8 +4,8 @@ on the CPU oracle (the reference block's rounding points, blk.c:149-176, compose
 phone/animad.cpp:424-492), with the same weights (exported from the GPU runner) and inputs.
 
 Tolerance: the reference's own block metric (cmp_block.py:5-6) on the whole denoise, rel err on the latent change
-< 5e-3 and cosine > 0.99999 (measured on MI355X: 5.3e-4 and 0.9999999; the reference device reaches 6.9e-4 on ONE
-block, docs/PITFALLS.md:154). The GPU softmax is exact fp32 with fp16 probabilities where the reference rounds S,
+< 1.6e-3 (cosine > 1 - 1.6e-3^2) and max abs < 7e-3 (measured on MI355X: 5.3e-4 and 2.4e-3; the reference device
+reaches 6.9e-4 on ONE block, docs/PITFALLS.md:154). The GPU softmax is exact fp32 with fp16 probabilities where the reference rounds S,
 S-m, P and the row sum to fp16, and the GPU GEMMs accumulate in fp32 where the oracle uses double; these are the
 differences that compound over the 112 block evaluations. The oracle needs about a minute on 16 host threads;
 progress is printed after every step. Collected after the other GPU tests."""
@@ -73,8 +73,54 @@ def test_dit_2b_fp16_1536tok_4step_denoise_vs_oracle():
             ref = ref + (sig[i + 1] - sig[i]) * v
             print(f"oracle step {i + 1}/4 done in {time.time() - t1:.1f} s", flush=True)
         r, c = delta_metrics(got, ref, lat)
-        print(f"2B DiT 4-step denoise: rel err on latent change {r:.3e}, cosine {c:.7f}", flush=True)
+        mx = float(np.max(np.abs(got - ref)))
+        print(f"2B DiT 4-step denoise: rel err on latent change {r:.3e}, cosine {c:.8f}, max abs {mx:.3e}", flush=True)
         assert np.isfinite(got).all()
-        assert r < 5e-3 and c > 0.99999
+        assert r < 1.6e-3 and c > 1 - 1.6e-3 ** 2 and mx < 7e-3
     finally:
         lib.hxa_dit_destroy(p)
+
+
+def test_dit_2b_fp16_batch4_images_match_batch1():
+    """Config 2 at batch 4: the full-size 28-block DiT run on 4 images at once gives each image the velocity the
+    same DiT (same seed, so the same weights) gives it alone at batch 1, which the test above pins to the oracle.
+    The batch changes only the GEMM row count (6144 vs 1536 rows), hence the tiles and K splits the projections run
+    on, so the two agree to fp16 rounding, not bit for bit."""
+    from hexanima_amd import hip
+    import ctypes as C_
+
+    hip.init(0)
+    lib = hip.lib()
+    print("[case] 2B fp16 DiT, 28 blocks, batch 4 vs batch 1", flush=True)
+    dits = []
+    try:
+        for batch in (4, 1):
+            bd = hip.BlockDims(0, D, H, F, C, DC, 0, batch, 0, hip.W_F16, hip.W_F16, 1)
+            cfg = hip.DitCfg(bd, NB, LAT[0], LAT[1], LAT[2], 256, 0)
+            p = C_.c_void_p()
+            hip.check(lib.hxa_dit_create(C_.byref(cfg), 77, C_.byref(p)), "dit_create")
+            dits.append(p)
+        # same seed, same weights: compare one block pack and the glue of the two runners
+        for which in (NB - 1, 2 * NB):
+            a = [np.zeros(lib.hxa_dit_export(p, which, None, 0), np.uint8) for p in dits]
+            for p, buf in zip(dits, a):
+                assert lib.hxa_dit_export(p, which, buf.ctypes.data, buf.nbytes) == buf.nbytes
+            assert np.array_equal(a[0], a[1])
+        rng = np.random.default_rng(19)
+        lat = rng.standard_normal((4,) + LAT).astype(np.float32)
+        ctx = rng.standard_normal((4, C, DC)).astype(np.float32)
+        hip.check(lib.hxa_dit_set_inputs(dits[0], lat.ctypes.data, ctx.ctypes.data), "set_inputs")
+        v4 = np.zeros_like(lat)
+        hip.check(lib.hxa_dit_velocity(dits[0], 0.75, v4.ctypes.data), "velocity b4")
+        for b in range(4):
+            lb, cb = np.ascontiguousarray(lat[b:b + 1]), np.ascontiguousarray(ctx[b:b + 1])  # kept alive for the call
+            hip.check(lib.hxa_dit_set_inputs(dits[1], lb.ctypes.data, cb.ctypes.data), "set_inputs b1")
+            v1 = np.zeros_like(lat[b:b + 1])
+            hip.check(lib.hxa_dit_velocity(dits[1], 0.75, v1.ctypes.data), "velocity b1")
+            r = float(np.linalg.norm(v4[b] - v1[0]) / np.linalg.norm(v1[0]))
+            mx = float(np.max(np.abs(v4[b] - v1[0])))
+            print(f"image {b}: batch-4 vs batch-1 velocity rel {r:.2e} max abs {mx:.2e}", flush=True)
+            assert np.isfinite(v4[b]).all() and r < 2.7e-3 and mx < 1.2e-2  # measured 8.4e-4 - 8.9e-4, 3.8e-3
+    finally:
+        for p in dits:
+            lib.hxa_dit_destroy(p)
