@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libhexanima_hip.so")
-SOURCES = ["gemm.hip", "attention.hip", "elementwise.hip", "runtime.hip", "dit.hip"]
+SOURCES = ["gemm.hip", "attention.hip", "elementwise.hip", "runtime.hip", "dit.hip", "noalloc.hip"]
 
 ARCH = os.environ.get("HXA_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")

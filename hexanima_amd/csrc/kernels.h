@@ -100,6 +100,11 @@ int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t 
 // matrix shapes of a GPU block pack (see hxa_pack_layout); returns the matrix count
 int hxa_pack_mats(int kind, int D, int F, int DC, int fa, int fm, int *N, int *K, int *fmt);
 
+// the library's error record (hxa_last_error): sets it and returns code
+int hxa_set_error(int code, const char *fmt, ...);
+// device address of hxa_block_run_noalloc's static workspace on the current device (resolved once per device)
+int hxa_noalloc_setup(void **out);
+
 // hxa_block_run for a chain of blocks: pend_gate != NULL applies the previous block's pending MLP residual
 // (x += pend_gate * (t1 + t2) from the workspace) in the first norm; defer != 0 leaves this block's MLP residual
 // pending in t1 / t2

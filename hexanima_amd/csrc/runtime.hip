@@ -29,6 +29,13 @@ static int fail(int code, const char *fmt, ...) {
   va_end(ap);
   return code;
 }
+int hxa_set_error(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
 #define HIPC(x)                                                                                  \
   do {                                                                                           \
     hipError_t e__ = (x);                                                                        \
@@ -314,34 +321,37 @@ extern "C" int hxa_rows_to_x32(const float *x, float *tiles, int R, int C, void 
 struct MatSpec {
   int N, K, fmt;
 };
-static void pack_mats(int kind, int D, int F, int DC, int fa, int fm, std::vector<MatSpec> &m) {
-  m.clear();
-  if (kind == 0) m = {{3 * D, D, fa}, {D, D, fa}, {D, D, fa}, {2 * D, DC, fa}, {D, D, fa}, {F, D, fm}, {D, F, fm}};
-  else m = {{3 * D, D, fa}, {D, D, fa}, {2 * F, D, fm}, {D, F, fm}};
+// the matrices of a pack, in pack order (fixed storage: the block call path allocates nothing)
+struct MatList {
+  MatSpec m[8];
+  int n;
+};
+static MatList pack_mats(int kind, int D, int F, int DC, int fa, int fm) {
+  if (kind == 0) return MatList{{{3 * D, D, fa}, {D, D, fa}, {D, D, fa}, {2 * D, DC, fa}, {D, D, fa}, {F, D, fm}, {D, F, fm}}, 7};
+  return MatList{{{3 * D, D, fa}, {D, D, fa}, {2 * F, D, fm}, {D, F, fm}}, 4};
 }
 int hxa_pack_mats(int kind, int D, int F, int DC, int fa, int fm, int *N, int *K, int *fmt) {
-  std::vector<MatSpec> m;
-  pack_mats(kind, D, F, DC, fa, fm, m);
-  for (size_t i = 0; i < m.size(); i++) {
-    N[i] = m[i].N;
-    K[i] = m[i].K;
-    fmt[i] = m[i].fmt;
+  const MatList m = pack_mats(kind, D, F, DC, fa, fm);
+  for (int i = 0; i < m.n; i++) {
+    N[i] = m.m[i].N;
+    K[i] = m.m[i].K;
+    fmt[i] = m.m[i].fmt;
   }
-  return (int)m.size();
+  return m.n;
 }
 static long wbytes(const MatSpec &m) {
   return m.fmt == HXA_W_F16 ? 2L * m.N * m.K : m.fmt == HXA_W_Q8 ? (long)m.N * m.K : (long)m.N * m.K / 2;
 }
 extern "C" long hxa_pack_layout(int kind, int D, int F, int DC, int fa, int fm, long *offs, int noffs) {
-  std::vector<MatSpec> mats;
-  pack_mats(kind, D, F, DC, fa, fm, mats);
+  const MatList mats = pack_mats(kind, D, F, DC, fa, fm);
   long off = 0;
   int o = 0;
   auto put = [&](long v) {
     if (offs && o < noffs) offs[o] = v;
     o++;
   };
-  for (const MatSpec &m : mats) {
+  for (int i = 0; i < mats.n; i++) {
+    const MatSpec &m = mats.m[i];
     put(off);
     off += al256(wbytes(m));
     if (m.fmt != HXA_W_F16) {
@@ -384,15 +394,14 @@ struct PackView {
   const float *vec;
 };
 static PackView pack_view(const hxa_block_dims *d, const void *pack) {
-  std::vector<MatSpec> mats;
-  pack_mats(d->kind, d->D, d->F, d->DC, d->fmt_attn, d->fmt_mlp, mats);
+  const MatList mats = pack_mats(d->kind, d->D, d->F, d->DC, d->fmt_attn, d->fmt_mlp);
   long offs[32];
   hxa_pack_layout(d->kind, d->D, d->F, d->DC, d->fmt_attn, d->fmt_mlp, offs, 32);
   PackView v{};
-  v.nmat = (int)mats.size();
+  v.nmat = mats.n;
   const char *b = (const char *)pack;
   for (int i = 0; i < v.nmat; i++) {
-    v.w[i] = HxaWeight{mats[i].fmt | HXA_W_KTILED, mats[i].N, mats[i].K, b + offs[3 * i],
+    v.w[i] = HxaWeight{mats.m[i].fmt | HXA_W_KTILED, mats.m[i].N, mats.m[i].K, b + offs[3 * i],
                        offs[3 * i + 1] >= 0 ? (const hxa_h *)(b + offs[3 * i + 1]) : nullptr, nullptr};
   }
   v.vec = (const float *)(b + offs[3 * v.nmat]);

@@ -87,6 +87,7 @@ _SIGS = {
     "hxa_block_ws_bytes": (L, [C.POINTER(BlockDims)]),
     "hxa_block_run": (I, [C.POINTER(BlockDims), P, P, P, P, P, P, P, I, C.POINTER(I), I, P]),
     "hxa_block_ws_buf": (P, [C.POINTER(BlockDims), P, I, C.POINTER(L)]),
+    "hxa_block_run_noalloc": (I, [C.POINTER(BlockDims), P, P, P, P, P, P, I, P]),
     "hxa_dit_create": (I, [C.POINTER(DitCfg), U64, C.POINTER(P)]),
     "hxa_dit_destroy": (I, [P]),
     "hxa_dit_set_inputs": (I, [P, P, P]),

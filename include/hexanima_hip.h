@@ -203,6 +203,15 @@ long hxa_block_ws_bytes(const hxa_block_dims *d);
  *   stop: stop after this many stages (0 = all); stage_us: per-stage microseconds (NULL: not timed). */
 int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod, const float *cosT,
                   const float *sinT, void *ws, int stop, int *stage_us, int nstage, void *stream);
+/* hxa_block_run without a workspace argument and without any allocation: the workspace is a static device array of
+ * HXA_NOALLOC_WS_MAX bytes held by each GPU the library runs on until the process ends (one 1536-token image of the
+ * 2B fp16 / q8 and 2.9B-class q8 blocks fits; hxa_block_ws_bytes larger than that is HXA_E_ARG, nothing launched).
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc). All calls on one GPU share the array, so calls that overlap on
+ * one GPU race; no stage timing. Otherwise as hxa_block_run (same kernels, same results). */
+#define HXA_NOALLOC_WS_MAX (160L << 20)
+int hxa_block_run_noalloc(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
+                          const float *cosT, const float *sinT, int stop, void *stream);
 /* stage buffers of the workspace: which 0 h, 1 q, 2 k, 3 vT ([D][batch*T]), 4 o, 5 t1, 6 mid, 7 ck, 8 cvT, 9 t2,
  * 10 the fp16 weight copy;
  * returns the device pointer and its row stride in elements */
