@@ -15,6 +15,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libhexanima_hip.so")
+# the MOSS build of the block interface: exports the reference's mega_block name with the MOSS semantics
+MOSS_LIB = os.path.join(HERE, "libhexanima_moss.so")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 SOURCES = ["gemm.hip", "attention.hip", "elementwise.hip", "runtime.hip", "dit.hip", "noalloc.hip"]
 
 ARCH = os.environ.get("HXA_ARCH", "gfx950")
@@ -52,11 +55,20 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
         list(ex.map(_compile, todo))
     objs = [os.path.join(OBJ, s.replace(".hip", ".o")) for s in SOURCES]
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    # -Bsymbolic-functions: the library's own calls bind to its own definitions, also when libhexanima_moss.so's
+    # mega_block is loaded first in a process
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-Bsymbolic-functions", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    tmp = MOSS_LIB + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-I", INCLUDE, "-o", tmp,
+           os.path.join(CSRC, "moss_abi.cpp"), "-L", HERE, "-lhexanima_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"libhexanima_moss.so failed:\n{r.stderr}")
+    os.replace(tmp, MOSS_LIB)
     if verbose:
         print("built", LIB)
     return LIB

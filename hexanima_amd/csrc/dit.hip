@@ -235,6 +235,10 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   d.bd = cfg->blk;
   hxa_block_dims &b = d.bd;
   const int D = b.D, B = b.batch, C4 = 4 * cfg->lat_c;
+  if (b.kind != 0 && b.kind != 1) {  // the synthetic DiT builds Anima- or MOSS-structure packs without LoRA
+    delete dp;
+    return dfail(HXA_E_MODE, "dit: block kind");
+  }
   if (cfg->lat_h % 2 || cfg->lat_w % 2 || C4 > 256 || 256 % C4 || cfg->temb % 2 || cfg->nblocks < 1) {
     delete dp;
     return dfail(HXA_E_ARG, "dit: latent / embedding shape");

@@ -12,6 +12,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/hexanima_hip.h"
@@ -52,6 +53,20 @@ int hxa_set_error(int code, const char *fmt, ...) {
 
 static inline hipStream_t S(void *s) { return (hipStream_t)s; }
 static inline long al256(long x) { return (x + 255) & ~255L; }
+
+// host-side weight conversions split their outer loop over up to 16 threads
+template <class Fn>
+void par_for(int n, Fn fn) {
+  const int nt = std::max(1, std::min({n, 16, (int)std::thread::hardware_concurrency()}));
+  std::vector<std::thread> th;
+  for (int t = 1; t < nt; t++)
+    th.emplace_back([&, t] {
+      for (int i = t; i < n; i += nt) fn(i);
+    });
+  for (int i = 0; i < n; i += nt) fn(i);
+  for (auto &x : th) x.join();
+}
+
 
 extern "C" const char *hxa_last_error(void) { return g_err; }
 extern "C" const char *hxa_version(void) { return "hexanima_hip 0.1 gfx950"; }
@@ -326,8 +341,17 @@ struct MatList {
   MatSpec m[8];
   int n;
 };
+// kind 2 (MOSS with the rapid-moss LoRA, moss/export_moss.py:14-47): every projection carries its R scaled LoRA-B
+// columns after K; the q, k and v parts sit block-diagonally in the fused qkv matrix (q rows use columns [D, D+R),
+// k rows [D+R, D+2R), v rows [D+2R, D+3R), zeros elsewhere), so one launch on [h | L_q | L_k | L_v] gives all
+// three. Then the four LoRA-A matrices as W[N][K]: A_qkv [3R][D], A_o [R][D], A_ug [R][D], A_dn [R][F].
+constexpr int LORA_R = 128;
 static MatList pack_mats(int kind, int D, int F, int DC, int fa, int fm) {
   if (kind == 0) return MatList{{{3 * D, D, fa}, {D, D, fa}, {D, D, fa}, {2 * D, DC, fa}, {D, D, fa}, {F, D, fm}, {D, F, fm}}, 7};
+  if (kind == 2)
+    return MatList{{{3 * D, D + 3 * LORA_R, fa}, {D, D + LORA_R, fa}, {2 * F, D + LORA_R, fm}, {D, F + LORA_R, fm},
+                    {3 * LORA_R, D, fa}, {LORA_R, D, fa}, {LORA_R, D, fm}, {LORA_R, F, fm}},
+                   8};
   return MatList{{{3 * D, D, fa}, {D, D, fa}, {2 * F, D, fm}, {D, F, fm}}, 4};
 }
 int hxa_pack_mats(int kind, int D, int F, int DC, int fa, int fm, int *N, int *K, int *fmt) {
@@ -371,8 +395,9 @@ extern "C" long hxa_pack_layout(int kind, int D, int F, int DC, int fa, int fm, 
 static int chunk_bytes(int fmt) { return fmt == HXA_W_F16 ? 64 : fmt == HXA_W_Q8 ? 32 : 16; }
 static void tile_matrix_host(const uint8_t *rm, uint8_t *kt, int N, int K, int fmt) {
   const int cb = chunk_bytes(fmt), G = K / 32;
-  for (int n = 0; n < N; n++)
-    for (int g = 0; g < G; g++) memcpy(kt + ((size_t)g * N + n) * cb, rm + ((size_t)n * G + g) * cb, cb);
+  par_for(G, [&](int g) {
+    for (int n = 0; n < N; n++) memcpy(kt + ((size_t)g * N + n) * cb, rm + ((size_t)n * G + g) * cb, cb);
+  });
 }
 // host image of a pack whose matrices were written row-major -> the k-tiled pack (scales / vectors unchanged)
 static void tile_pack_host(std::vector<uint8_t> &host, int kind, int D, int F, int DC, int fa, int fm) {
@@ -389,7 +414,7 @@ static void tile_pack_host(std::vector<uint8_t> &host, int kind, int D, int F, i
 }
 
 struct PackView {
-  HxaWeight w[7];
+  HxaWeight w[8];
   int nmat;
   const float *vec;
 };
@@ -427,6 +452,9 @@ constexpr long DQ_MIN_ROWS = 1024;
 constexpr long DQ_WIDE_ROWS = 4096;
 static WsLayout ws_layout(const hxa_block_dims *d) {
   const long BT = (long)d->batch * d->T, BC = (long)d->batch * d->C, D = d->D;
+  // with the LoRA (kind 2) the rows of h, o and mid carry the L columns of the projection that reads them:
+  // h | L_q L_k L_v (later h | L_ug), o | L_o, mid | L_dn
+  const long R = d->kind == 2 ? LORA_R : 0, LDH = D + 3 * R, LDO = D + R, LDM = (long)d->F + R;
   WsLayout L{};
   long off = 0;
   auto put = [&](int id, long bytes, long ld) {
@@ -434,16 +462,16 @@ static WsLayout ws_layout(const hxa_block_dims *d) {
     L.ld[id] = ld;
     off += al256(bytes);
   };
-  put(WS_H, 2 * BT * D, D);
+  put(WS_H, 2 * BT * LDH, LDH);
   put(WS_Q, 2 * BT * 2 * D, 2 * D);  // q | k interleaved per row
   L.off[WS_K] = L.off[WS_Q] + 2 * D;  // byte offset of k inside the q|k rows
   L.ld[WS_K] = 2 * D;
   put(WS_VT, 2 * D * BT, BT);
-  put(WS_O, 2 * BT * D, D);
+  put(WS_O, 2 * BT * LDO, LDO);
   put(WS_T1, 2 * 2 * BT * D, D);  // two split-K partials
   L.off[WS_T2] = L.off[WS_T1] + 2 * BT * D;
   L.ld[WS_T2] = D;
-  put(WS_MID, 2 * BT * (long)d->F, d->F);
+  put(WS_MID, 2 * BT * LDM, LDM);
   if (d->kind == 0) {
     put(WS_CK, 2 * BC * D, D);
     put(WS_CVT, 2 * D * BC, BC);
@@ -451,14 +479,18 @@ static WsLayout ws_layout(const hxa_block_dims *d) {
     L.off[WS_CK] = L.off[WS_CVT] = 0;
     L.ld[WS_CK] = L.ld[WS_CVT] = 0;
   }
-  // fp16 copy of one int8 / int4 o-class (D x D) or MLP-down (D x F) weight (dq_rows)
-  const bool qa = d->fmt_attn != HXA_W_F16, qm = d->fmt_mlp != HXA_W_F16;
-  const long F = d->F, FU = d->kind == 1 ? 2 * F : F;  // MLP up rows (MOSS: up | gate)
+  // fp16 copy of the largest int8 / int4 projection weight that runs through the dequantisation pass: from
+  // DQ_MIN_ROWS rows those with N <= K (attention output, cross q, MLP down), from DQ_WIDE_ROWS rows all of them
+  const MatList mats = pack_mats(d->kind, d->D, d->F, d->DC, d->fmt_attn, d->fmt_mlp);
+  const int nproj = d->kind == 0 ? 7 : 4;  // the LoRA-A matrices run fused
   long dq = 0;
-  if (BT >= DQ_WIDE_ROWS) dq = std::max(qa ? 2 * 3 * D * D : 0L, qm ? 2 * std::max(FU, F) * D : 0L);
-  else if (BT >= DQ_MIN_ROWS) dq = std::max(qa ? 2 * D * D : 0L, qm ? 2 * D * F : 0L);
+  for (int i = 0; i < nproj && BT >= DQ_MIN_ROWS; i++) {
+    const MatSpec &m = mats.m[i];
+    if (m.fmt == HXA_W_F16 || (d->kind == 0 && i == 3)) continue;  // the text k / v weight has its own slot
+    if (BT >= DQ_WIDE_ROWS || m.N <= m.K) dq = std::max(dq, 2L * m.N * m.K);
+  }
   // a second slot for the text k / v weight (2D x DC), so that it and the cross q run as one paired fp16 launch
-  const long dq2 = d->kind == 0 && qa && BT >= DQ_MIN_ROWS ? al256(2 * 2 * D * (long)d->DC) : 0;
+  const long dq2 = d->kind == 0 && d->fmt_attn != HXA_W_F16 && BT >= DQ_MIN_ROWS ? al256(2 * 2 * D * (long)d->DC) : 0;
   put(WS_DQ, al256(dq) + dq2, d->F);
   L.dq_bytes = dq;
   L.dq2_off = al256(dq);
@@ -470,16 +502,17 @@ extern "C" long hxa_block_ws_bytes(const hxa_block_dims *d) { return ws_layout(d
 extern "C" void *hxa_block_ws_buf(const hxa_block_dims *d, void *ws, int which, long *ld) {
   if (which < 0 || which >= WS_N) return nullptr;
   const WsLayout L = ws_layout(d);
-  if (ld) *ld = L.ld[which];
+  if (ld) *ld = which == WS_DQ ? 0 : L.ld[which];
   return (char *)ws + L.off[which];
 }
 
 static int check_dims(const hxa_block_dims *d) {
-  if (d->kind != 0 && d->kind != 1) return fail(HXA_E_MODE, "block kind %d", d->kind);
+  if (d->kind < 0 || d->kind > 2) return fail(HXA_E_MODE, "block kind %d", d->kind);
   if (d->D % 256 || d->H * 128 != d->D || d->T <= 0 || d->T % 32 || d->batch < 1 || d->F % 128)
     return fail(HXA_E_ARG, "block dims D=%d H=%d F=%d T=%d batch=%d", d->D, d->H, d->F, d->T, d->batch);
   if (d->kind == 0 && (d->C <= 0 || d->C % 32 || d->DC % 64)) return fail(HXA_E_ARG, "context C=%d DC=%d", d->C, d->DC);
-  if (d->kind == 1 && (d->nvalid < 1 || d->nvalid > d->T)) return fail(HXA_E_ARG, "nvalid %d", d->nvalid);
+  if (d->kind != 0 && (d->nvalid < 1 || d->nvalid > d->T)) return fail(HXA_E_ARG, "nvalid %d", d->nvalid);
+  if (d->kind == 2 && (d->F % 64 || (d->F / 2) % 32)) return fail(HXA_E_ARG, "LoRA block F=%d", d->F);
   return HXA_OK;
 }
 
@@ -540,6 +573,8 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   const int D = d->D, H = d->H, T = d->T, B = d->batch, F = d->F;
   const int BT = B * T;
   const long ldqk = 2L * D;
+  const long ldh = L.ld[WS_H], ldo = L.ld[WS_O], ldmid = L.ld[WS_MID];  // D, D, F; wider with the LoRA columns
+  const bool lora = d->kind == 2;
   StageTimer tm(stage_us, nstage, st);
   int stage = 0;
 #define STAGE_DONE()                              \
@@ -627,19 +662,39 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   };
   auto attn = [&](const hxa_h *q, const hxa_h *kk, long ldk, const hxa_h *vt, long ldvt, int NKV, int nvalid, long kb,
                   long vb) -> int {
-    HxaAttn p{q, kk, vt, ldqk, ldk, ldvt, o, D, T, NKV, nvalid, H, B, (long)T * ldqk, kb, vb, (long)T * D};
+    HxaAttn p{q, kk, vt, ldqk, ldk, ldvt, o, ldo, T, NKV, nvalid, H, B, (long)T * ldqk, kb, vb, (long)T * ldo};
     const int r = hxa_attn_launch(p, st);
     if (r != HXA_OK) return fail(r, "block attention rejected");
     return HXA_OK;
   };
+  // LoRA-A GEMM (moss blk.c:238, :244, :251, :255): L = f16(a[:, :K] . A^T) into the columns of the same rows right
+  // after the K activations (a[:, K:K+N]), where the projection that follows reads it as its last k steps
+  auto lora_a = [&](hxa_h *a, long lda, const HxaWeight &A) -> int {
+    return gemm(a, lda, BT, A, HXA_EPI_STORE, a + A.K, lda, nullptr, nullptr, nullptr, 0, 0, 1, 0);
+  };
+  // k groups [g0, g0 + ng) of a k-tiled weight: another k-tiled weight (groups are contiguous slices)
+  auto ksub = [](const HxaWeight &w, int g0, int ng) -> HxaWeight {
+    const int f = w.fmt & ~HXA_W_KTILED;
+    const long cb = f == HXA_W_F16 ? 64 : f == HXA_W_Q8 ? 32 : 16;
+    return HxaWeight{w.fmt, w.N, 32 * ng, (const uint8_t *)w.w + (long)g0 * w.N * cb,
+                     w.s ? w.s + (long)g0 * w.N : nullptr, w.z ? w.z + (long)g0 * w.N : nullptr};
+  };
 
   // split-K down projection + gated residual (blk.c:172-174): two fp16 partial GEMMs over 2x the workgroups (fills
   // the GPU at N = D) then the residual; measured faster than the single-launch HXA_EPI_RESADD_SPLIT2 form, whose
-  // 128-wide tiles leave a quarter of the CUs idle at 1536 x 2048
+  // 128-wide tiles leave a quarter of the CUs idle at 1536 x 2048. With the LoRA the halves are [0, F/2) and
+  // [F/2, F) + the LoRA columns (moss blk.c:256-259): two launches.
   auto down_resadd = [&](const hxa_h *a, const HxaWeight &w, const float *gate) -> int {
     const HxaWeight *wp;
     TRY(prep(w, wp));
-    TRY(gemm(a, F, BT, *wp, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
+    if (!lora) {
+      TRY(gemm(a, ldmid, BT, *wp, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
+    } else {
+      const int G = F / 64;  // k groups of one half
+      const HxaWeight w0 = ksub(*wp, 0, G), w1 = ksub(*wp, G, G + LORA_R / 32);
+      TRY(gemm(a, ldmid, BT, w0, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+      TRY(gemm(a + F / 2, ldmid, BT, w1, HXA_EPI_STORE, t2, D, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+    }
     return defer ? HXA_OK : hxa_resadd2_launch(x, D, t1, t2, D, BT, D, gate, st);
   };
   // the attention output projection whose gated residual the next norm applies (no stage dump): one K pass into
@@ -651,9 +706,10 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   auto deferred_proj = [&](const HxaWeight &w) -> int {
     const HxaWeight *wp;
     TRY(prep(w, wp));
-    const HxaGemm g1 = make(o, D, BT, *wp, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0);
+    const HxaGemm g1 = make(o, ldo, BT, *wp, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0);
     int bm = 0, bn = 0, nw = 0, rounds = 0;
-    split_o = w.K % 64 == 0 && hxa_gemm_plan(g1, &bm, &bn, &nw, &rounds) == HXA_OK && rounds == 1 && bm * bn <= 128 * 128;
+    split_o = !lora && w.K % 64 == 0 && hxa_gemm_plan(g1, &bm, &bn, &nw, &rounds) == HXA_OK && rounds == 1 &&
+              bm * bn <= 128 * 128;
     HxaGemm g = g1;
     if (split_o) {
       g.epi = HXA_EPI_PARTIAL;
@@ -671,7 +727,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     hxa_h *ck = (hxa_h *)(w8 + L.off[WS_CK]), *cvT = (hxa_h *)(w8 + L.off[WS_CVT]);
     // site 0: self-attention (blk.c:157-162)
     TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, pend_gate ? t1 : nullptr, pend_gate ? t2 : nullptr, D, pend_gate, mod,
-                                   mod + D, nullptr, 1e-6f, h, D, st));
+                                   mod + D, nullptr, 1e-6f, h, ldh, st));
     STAGE_DONE();
     // q, k: RMSNorm * gain + RoPE (blk.c:159-160), fused into the projection's store unless a stage dump needs the
     // un-normalised projections (M_STOP)
@@ -680,7 +736,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     {
       const HxaWeight *wp;
       TRY(prep(Wqkv, wp));
-      TRY(gemm(h, D, BT, *wp, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
+      TRY(gemm(h, ldh, BT, *wp, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
     }
     STAGE_DONE();
     if (!fuse) TRY(hxa_rmsrope_launch(qk, k, gain, gain + 128, ldqk, BT, H, cosT, sinT, T, st));
@@ -689,18 +745,18 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     // gated residual x += gate * f16(o Wo) (blk.c:162): without a stage dump it is applied by the next site's LN
     // kernel, which reads x anyway (same fma, so the same x); the projection is then a plain store into t1
-    TRY(fuse ? deferred_proj(Wo) : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
+    TRY(fuse ? deferred_proj(Wo) : gemm(o, ldo, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 1: cross-attention (blk.c:163-169)
     TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 2 * D,
-                                   mod + 3 * D, mod + 4 * D, nullptr, 1e-6f, h, D, st));
+                                   mod + 3 * D, mod + 4 * D, nullptr, 1e-6f, h, ldh, st));
     STAGE_DONE();
     // cross q from h and the text k / v from ctx are independent: one launch, the text tiles filling the CUs the
     // 1536-token projection leaves idle
     if (fuse) hn = HeadNorm{D, gain + 256, gain + 256, D, nullptr, nullptr};  // cross q: RMSNorm * gain (blk.c:166)
     const HxaWeight *wcq;
     TRY(prep(Wcq, wcq));
-    const HxaGemm gq = make(h, D, BT, *wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
+    const HxaGemm gq = make(h, ldh, BT, *wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
     if (fuse) hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
     const HxaWeight *wckv;
     TRY(prep(Wckv, wckv, 1));
@@ -717,17 +773,17 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     TRY(attn(qk, ck, D, cvT, BC, d->C, d->C, (long)d->C * D, d->C));
     STAGE_DONE();
-    TRY(fuse ? deferred_proj(Wco) : gemm(o, D, BT, Wco, HXA_EPI_RESADD, nullptr, 0, x, mod + 5 * D, nullptr, 0, 0, 1, 0));
+    TRY(fuse ? deferred_proj(Wco) : gemm(o, ldo, BT, Wco, HXA_EPI_RESADD, nullptr, 0, x, mod + 5 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 2: MLP (blk.c:170-174)
     TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 5 * D,
-                                   mod + 6 * D, mod + 7 * D, nullptr, 1e-6f, h, D, st));
+                                   mod + 6 * D, mod + 7 * D, nullptr, 1e-6f, h, ldh, st));
     STAGE_DONE();
     pf0 = &W2;
     {
       const HxaWeight *wp;
       TRY(prep(W1, wp));
-      TRY(gemm(h, D, BT, *wp, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+      TRY(gemm(h, ldh, BT, *wp, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, mid, ldmid, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     }
     STAGE_DONE();
     TRY(down_resadd(mid, W2, mod + 8 * D));
@@ -737,32 +793,36 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     const HxaWeight &Wqkv = pv.w[0], &Wo = pv.w[1], &Wug = pv.w[2], &Wdn = pv.w[3];
     // attention half (moss blk.c:234-247)
     TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, pend_gate ? t1 : nullptr, pend_gate ? t2 : nullptr, D, pend_gate, mod,
-                                   mod + D, n1, 1e-6f, h, D, st));
+                                   mod + D, n1, 1e-6f, h, ldh, st));
     STAGE_DONE();
-    STAGE_DONE();  // the reference's LoRA-A GEMM stage (no LoRA)
+    if (lora) TRY(lora_a(h, ldh, pv.w[4]));  // L_q | L_k | L_v (blk.c:238)
+    STAGE_DONE();
     hn = HeadNorm{2 * D, gq, gk, D, cosT, sinT};  // q, k: RMSNorm * gain + RoPE in the GEMM (moss blk.c:239-242, mode 3)
     {
       const HxaWeight *wp;
       TRY(prep(Wqkv, wp));
-      TRY(gemm(h, D, BT, *wp, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
+      TRY(gemm(h, ldh, BT, *wp, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
     }
     STAGE_DONE();
     TRY(attn(qk, k, ldqk, vT, BT, T, d->nvalid, (long)T * ldqk, T));
     STAGE_DONE();
+    if (lora) TRY(lora_a(o, ldo, pv.w[5]));  // L_o (blk.c:244)
     const bool fuse = stop == 0;  // residual deferred into the FFN's RMS-mod kernel (same fma) unless dumping stages
-    TRY(fuse ? deferred_proj(Wo) : gemm(o, D, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
+    TRY(fuse ? deferred_proj(Wo) : gemm(o, ldo, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // FFN half (moss blk.c:248-259)
     TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 2 * D,
-                                   mod + 3 * D, mod + 4 * D, n2, 1e-6f, h, D, st));
+                                   mod + 3 * D, mod + 4 * D, n2, 1e-6f, h, ldh, st));
     STAGE_DONE();
+    if (lora) TRY(lora_a(h, ldh, pv.w[6]));  // L_ug (blk.c:251)
     pf0 = &Wdn;
     {
       const HxaWeight *wp;
       TRY(prep(Wug, wp));
-      TRY(gemm(h, D, BT, *wp, HXA_EPI_SITU, mid, F, nullptr, nullptr, nullptr, 0, 0, 1, 0));
+      TRY(gemm(h, ldh, BT, *wp, HXA_EPI_SITU, mid, ldmid, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     }
     STAGE_DONE();
+    if (lora) TRY(lora_a(mid, ldmid, pv.w[7]));  // L_dn (blk.c:255)
     TRY(down_resadd(mid, Wdn, mod + 5 * D));
     STAGE_DONE();
   }
@@ -818,25 +878,31 @@ int ensure(void **p, size_t *have, size_t need) {
 // fp16 crouton weight tiles of matrix [K][N] ([nb][kb], tile rows = k) -> W[N][K] (export_all.py:7-8)
 void crouton_to_nk(const uint16_t *tiles, int N, int K, uint16_t *w) {
   const int kb = K / 32;
-  for (int n = 0; n < N; n++)
-    for (int k = 0; k < K; k++) {
-      const int r = k & 31, c = n & 31;
-      w[(size_t)n * K + k] = tiles[((size_t)(n >> 5) * kb + (k >> 5)) * 1024 + (r >> 1) * 64 + c * 2 + (r & 1)];
-    }
+  par_for(N / 32, [&](int nb) {
+    for (int n = nb * 32; n < nb * 32 + 32; n++)
+      for (int k = 0; k < K; k++) {
+        const int r = k & 31, c = n & 31;
+        w[(size_t)n * K + k] = tiles[((size_t)(n >> 5) * kb + (k >> 5)) * 1024 + (r >> 1) * 64 + c * 2 + (r & 1)];
+      }
+  });
 }
-// q8 records (export_all.py:10-18) -> int8 q[N][K] + s[K/32][N]; rows kofs.. of a record matrix with kbt k-blocks
-void q8rec_to_native(const uint8_t *rec, int N, int K, int kbt, uint8_t *q, uint16_t *s, int ncol_stride) {
-  const int kb = K / 32;
-  for (int jb = 0; jb < N / 32; jb++)
-    for (int ib = 0; ib < kb; ib++) {
+// q8 records (export_all.py:10-18) of a matrix [K][N] stored [N/32][kbt] -> int8 q[n][col] (row stride ldq) + fp16
+// scales s[col/32][n] (row stride lds). Record k-block ib < nkb_main lands at column 32 ib, the LoRA-B blocks after it
+// (ib >= nkb_main, moss/export_moss.py:40-46) at column lora_col + 32 (ib - nkb_main).
+void q8rec_to_native(const uint8_t *rec, int N, int nkb, int kbt, uint8_t *q, long ldq, uint16_t *s, long lds,
+                     int nkb_main, int lora_col) {
+  par_for(N / 32, [&](int jb) {
+    for (int ib = 0; ib < nkb; ib++) {
       const uint8_t *R = rec + ((size_t)jb * kbt + ib) * 1152;
       const uint16_t *sv = (const uint16_t *)R;
+      const long col = ib < nkb_main ? 32L * ib : lora_col + 32L * (ib - nkb_main);
       for (int c = 0; c < 32; c++) {
         const int n = jb * 32 + c;
-        s[(size_t)ib * ncol_stride + n] = sv[2 * c];
-        for (int r = 0; r < 32; r++) q[(size_t)n * K + ib * 32 + r] = (uint8_t)(R[128 + (r >> 1) * 64 + c * 2 + (r & 1)] ^ 0x80);
+        s[(col / 32) * lds + n] = sv[2 * c];
+        for (int r = 0; r < 32; r++) q[(size_t)n * ldq + col + r] = (uint8_t)(R[128 + (r >> 1) * 64 + c * 2 + (r & 1)] ^ 0x80);
       }
     }
+  });
 }
 
 // Convert one registered Anima blkNN.bin (fixed D=2048 layout, blk_wlayout.h) into a GPU pack.
@@ -865,8 +931,8 @@ int build_anima_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
     if (!q8) {
       crouton_to_nk((const uint16_t *)src, s.N, s.K, (uint16_t *)wdst + (size_t)s.row0 * s.K);
     } else {
-      q8rec_to_native(src, s.N, s.K, s.K / 32, wdst + (size_t)s.row0 * s.K, (uint16_t *)(host.data() + offs[3 * s.mat + 1]) + s.row0,
-                      matN[s.mat]);
+      q8rec_to_native(src, s.N, s.K / 32, s.K / 32, wdst + (size_t)s.row0 * s.K, s.K,
+                      (uint16_t *)(host.data() + offs[3 * s.mat + 1]) + s.row0, matN[s.mat], s.K / 32, 0);
     }
   }
   if (meta[M_GAIN] < 0 || (size_t)meta[M_GAIN] + 2048 > hb.bytes) return fail(HXA_E_WEIGHTS, "gain offset out of range");
@@ -880,31 +946,43 @@ int build_anima_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
   return HXA_OK;
 }
 
-// MOSS blkNN.bin (moss/export_moss.py:14-41, offsets moss blk_meta.h:6-17): q,k,v,o [3072+128][3072], up_gate
-// [3072+128][16384] (32-column blocks interleaved up/gate), down [8192+128][3072], LoRA A matrices, gains.
-// The LoRA rows are dropped (a pack without LoRA); gains: gq, gk, n1, n2.
+// MOSS blkNN.bin (moss/export_moss.py:14-58, offsets moss blk_meta.h:6-17), all q8 records: q, k, v, o
+// [3072 + 128][3072], up_gate [3072 + 128][16384] (32-column blocks interleaved up / gate), down [8192 + 128][3072]
+// -- the 128 extra K rows are the rapid-moss LoRA's scaled B -- then the LoRA A matrices A_qkv [3072][384],
+// A_o / A_up_gate [3072][128], A_down [8192][128], and the fp32 gains q/sqrt(128), k, norm1, norm2.
+// -> a kind-2 GPU pack (the B rows kept as 4 extra k groups, q / k / v block-diagonal in the fused qkv matrix).
 int build_moss_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
-  const int D = meta[MM_NCB] ? meta[MM_NCB] * 32 : 3072, F = 8192, fmt = HXA_W_Q8;
+  const int D = meta[MM_NCB] ? meta[MM_NCB] * 32 : 3072, F = 8192, fmt = HXA_W_Q8, R = LORA_R;
   if (D != 3072) return fail(HXA_E_MODE, "moss pack: only the 3072-wide layout is defined");
   const size_t W_Q = 0, W_K = 11059200, W_V = 22118400, W_O = 33177600, W_UG = 44236800, W_DN = 103219200,
-               W_GAIN = 135364608, W_TOTAL = 135397376;
+               W_AQKV = 131973120, W_AO = 133300224, W_AUG = 133742592, W_ADN = 134184960, W_GAIN = 135364608,
+               W_TOTAL = 135397376;
   const size_t base = (size_t)meta[MM_WOFF];
-  if (base + W_TOTAL > hb.bytes) return fail(HXA_E_WEIGHTS, "moss weights shorter than a block pack");
+  if (meta[MM_WOFF] < 0 || base + W_TOTAL > hb.bytes) return fail(HXA_E_WEIGHTS, "moss weights shorter than a block pack");
   const uint8_t *b = (const uint8_t *)hb.ptr + base;
-  db.dims = hxa_block_dims{1, D, D / 128, F, 0, 0, 0, 1, 0, fmt, fmt, 0};
+  db.dims = hxa_block_dims{2, D, D / 128, F, 0, 0, 0, 1, 0, fmt, fmt, 0};
   long offs[32];
-  const long bytes = hxa_pack_layout(1, D, F, 0, fmt, fmt, offs, 32);
+  const long bytes = hxa_pack_layout(2, D, F, 0, fmt, fmt, offs, 32);
   std::vector<uint8_t> host(bytes, 0);
-  const int kbt = D / 32 + 4;  // LoRA B rows appended as 4 extra k blocks
-  q8rec_to_native(b + W_Q, D, D, kbt, host.data() + offs[0], (uint16_t *)(host.data() + offs[1]), 3 * D);
-  q8rec_to_native(b + W_K, D, D, kbt, host.data() + offs[0] + (size_t)D * D, (uint16_t *)(host.data() + offs[1]) + D, 3 * D);
-  q8rec_to_native(b + W_V, D, D, kbt, host.data() + offs[0] + (size_t)2 * D * D, (uint16_t *)(host.data() + offs[1]) + 2 * D, 3 * D);
-  q8rec_to_native(b + W_O, D, D, kbt, host.data() + offs[3], (uint16_t *)(host.data() + offs[4]), D);
-  q8rec_to_native(b + W_UG, 2 * F, D, kbt, host.data() + offs[6], (uint16_t *)(host.data() + offs[7]), 2 * F);
-  q8rec_to_native(b + W_DN, D, F, F / 32 + 4, host.data() + offs[9], (uint16_t *)(host.data() + offs[10]), D);
-  // gains: q/sqrt(128) [128], k [128], norm1 [3072], norm2 [3072] (export_moss.py gain vector)
-  memcpy(host.data() + offs[12], b + W_GAIN, 4L * (256 + 2 * D));
-  tile_pack_host(host, 1, D, F, 0, fmt, fmt);
+  uint8_t *h8 = host.data();
+  auto q_of = [&](int m) { return h8 + offs[3 * m]; };
+  auto s_of = [&](int m) { return (uint16_t *)(h8 + offs[3 * m + 1]); };
+  const int kb = D / 32, kbt = kb + R / 32, LDQKV = D + 3 * R;
+  // q / k / v: rows p D .. (p + 1) D of qkv, their LoRA blocks at columns D + p R (the others stay zero)
+  const size_t srcs[3] = {W_Q, W_K, W_V};
+  for (int p = 0; p < 3; p++)
+    q8rec_to_native(b + srcs[p], D, kbt, kbt, q_of(0) + (size_t)p * D * LDQKV, LDQKV, s_of(0) + (size_t)p * D, 3 * D, kb,
+                    D + p * R);
+  q8rec_to_native(b + W_O, D, kbt, kbt, q_of(1), D + R, s_of(1), D, kb, D);
+  q8rec_to_native(b + W_UG, 2 * F, kbt, kbt, q_of(2), D + R, s_of(2), 2 * F, kb, D);
+  q8rec_to_native(b + W_DN, D, F / 32 + R / 32, F / 32 + R / 32, q_of(3), F + R, s_of(3), D, F / 32, F);
+  q8rec_to_native(b + W_AQKV, 3 * R, kb, kb, q_of(4), D, s_of(4), 3 * R, kb, 0);
+  q8rec_to_native(b + W_AO, R, kb, kb, q_of(5), D, s_of(5), R, kb, 0);
+  q8rec_to_native(b + W_AUG, R, kb, kb, q_of(6), D, s_of(6), R, kb, 0);
+  q8rec_to_native(b + W_ADN, R, F / 32, F / 32, q_of(7), F, s_of(7), R, F / 32, 0);
+  // gains: q/sqrt(128) [128], k [128], norm1 [3072], norm2 [3072] (export_moss.py:59-60)
+  memcpy(h8 + offs[24], b + W_GAIN, 4L * (256 + 2 * D));
+  tile_pack_host(host, 2, D, F, 0, fmt, fmt);
   void *dev = nullptr;
   HIPC(hipMalloc(&dev, bytes));
   HIPC(hipMemcpy(dev, host.data(), bytes, hipMemcpyHostToDevice));
@@ -1028,7 +1106,7 @@ int run_ref_block(Ctx *c, const BlockCall &bc, const DevBlock &db, const HostBuf
     const int which[9] = {WS_H, WS_Q, WS_K, WS_VT, WS_O, WS_T1, WS_MID, WS_CK, WS_CVT};
     for (int i = 0; i < 9; i++) {
       if (bc.off_stage[i] < 0) continue;
-      if (d.kind == 1 && i >= 7) continue;
+      if (d.kind != 0 && i >= 7) continue;
       const int R = i >= 7 ? bc.C : bc.T, Cc = i == 6 ? d.F : D;
       const size_t bytes = (size_t)R * Cc * 2;
       if (!blob_range(blob, bc.off_stage[i], bytes)) continue;
@@ -1096,6 +1174,8 @@ extern "C" int mega_moss_block(remote_handle64 h, const int *meta, int nmeta, in
   auto wit = c->bufs.find(wfd);
   if (wit == c->bufs.end() || wit->second.kind != HXA_KIND_WEIGHTS_MOSS) { *rc = HXA_E_WEIGHTS; fail(*rc, "weight fd %d not registered", wfd); return 0; }
   if (!meta || nmeta < MM_NMETA || !mod) { *rc = HXA_E_META; fail(*rc, "meta too short"); return 0; }
+  // MODE 0 is the DiT block with its LoRA (moss blk.c:234-259); 1 / 2 (text refiner, text projection) and the
+  // text-encoder modes 10 / 11 / 20 / 21 / 30 belong to the text side and are not built here
   if (meta[MM_MODE] != 0) { *rc = HXA_E_MODE; fail(*rc, "moss mode %d (only the DiT block, mode 0)", meta[MM_MODE]); return 0; }
   const int T = meta[MM_NTOK], nv = meta[MM_NVALID] ? meta[MM_NVALID] : T;
   if (T <= 0 || T % 32 || T > 8192 || nv < 1 || nv > T) { *rc = HXA_E_META; fail(*rc, "ntok %d nvalid %d", T, nv); return 0; }

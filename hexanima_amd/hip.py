@@ -209,18 +209,36 @@ def sync():
 
 
 # ------------------------------------------------------------------------------------------------ packs
+LORA_R = 128  # rank of the rapid-moss LoRA of a kind-2 (MOSS + LoRA) pack
+
+
 def pack_layout(kind: int, D: int, F: int, DC: int, fmt_attn: int, fmt_mlp: int):
     offs = (L * 32)()
     total = lib().hxa_pack_layout(kind, D, F, DC, fmt_attn, fmt_mlp, offs, 32)
-    nmat = 7 if kind == 0 else 4
+    nmat = len(pack_shapes(kind, D, F, DC))
     mats = [(offs[3 * i], offs[3 * i + 1]) for i in range(nmat)]
     return total, mats, offs[3 * nmat]
 
 
 def pack_shapes(kind: int, D: int, F: int, DC: int):
+    """(N, K) of each pack matrix in pack order (kind 0 Anima, 1 MOSS, 2 MOSS with the LoRA columns after K, then
+    the four LoRA-A matrices)."""
     if kind == 0:
         return [(3 * D, D), (D, D), (D, D), (2 * D, DC), (D, D), (F, D), (D, F)]
+    if kind == 2:
+        R = LORA_R
+        return [(3 * D, D + 3 * R), (D, D + R), (2 * F, D + R), (D, F + R), (3 * R, D), (R, D), (R, D), (R, F)]
     return [(3 * D, D), (D, D), (2 * F, D), (D, F)]
+
+
+def pack_fmts(kind: int, fmt_attn: int, fmt_mlp: int):
+    """weight format of each pack matrix: attention matrices fmt_attn, MLP ones fmt_mlp"""
+    attn = {0: 5, 1: 2, 2: 2}[kind]
+    n = len(pack_shapes(kind, 256, 256, 256))
+    f = [fmt_attn if i < attn else fmt_mlp for i in range(n)]
+    if kind == 2:  # the LoRA-A matrices follow their projections' formats
+        f[4], f[5], f[6], f[7] = fmt_attn, fmt_attn, fmt_mlp, fmt_mlp
+    return f
 
 
 def ktile(rows: np.ndarray, N: int, K: int) -> np.ndarray:
@@ -241,8 +259,10 @@ def build_pack(kind: int, D: int, F: int, DC: int, fmt_attn: int, fmt_mlp: int, 
     total, offs, voff = pack_layout(kind, D, F, DC, fmt_attn, fmt_mlp)
     buf = np.zeros(total, np.uint8)
     shapes = pack_shapes(kind, D, F, DC)
+    fmts = pack_fmts(kind, fmt_attn, fmt_mlp)
+    assert len(mats) == len(shapes)
     for i, (m, (woff, soff)) in enumerate(zip(mats, offs)):
-        fmt = fmt_attn if (i < (5 if kind == 0 else 2)) else fmt_mlp
+        fmt = fmts[i]
         N, K = shapes[i]
         if fmt == W_F16:
             a = np.ascontiguousarray(m).view(np.uint8).reshape(-1)

@@ -43,15 +43,19 @@ int mega_close(remote_handle64 h);
  *   meta[]   : the reference enum of blk_meta.h:3-4 (byte offsets into the blob / weight buffer + params)
  *   wfd, bfd : keys of buffers registered with hxa_register (the reference's rpcmem fds)
  *   mod      : 9 x 2048 fp32 (shift, scale, gate per site), modlen = 73728
- *   times    : per-stage microseconds (TICK order of blk.c:136), times[24] = entry overhead
+ *   times    : per-stage microseconds (TICK order of blk.c:136), times[24] = entry overhead; times[17..22], the
+ *              reference's attention sub-phases (K^T / V setup, QK, PV, row scale, softmax wait, flush: g_acc of
+ *              blk.c:178), are 0: attention is one fused kernel here, timed whole in its stage slot
  *   *rc      : 0 or a status code; the return value is 0 as in the reference.
  * meta[M_FIRST] uploads x / ctx / cos / sin from the blob to device-resident copies; meta[M_REL] writes x back
  * to the blob (x32 tiles). Weights are converted to the GPU layout and uploaded on first use, then stay resident.
  * meta[M_STOP] = n stops after n stages and writes the stage buffers (h,q,k,v,o,t,mid,ck,cv) back to the blob. */
 int mega_block(remote_handle64 h, const int *meta, int nmeta, int wfd, int bfd, const uint8_t *mod, int modlen, int *times,
                int ntimes, int *rc);
-/* the MOSS build of the same entry (moss/hexagon/mega/blk.c:262-274) with the MOSS meta enum
- * (moss/hexagon/mega/blk_meta.h:3-4); MODE 0 (DiT block) only; mod = 6 x DIM fp32. */
+/* the MOSS build of the same entry (moss/hexagon/mega/blk.c:269-281) with the MOSS meta enum
+ * (moss/hexagon/mega/blk_meta.h:3-4): MODE 0, the DiT block with its rapid-moss LoRA (blk.c:234-259); the text side's
+ * modes (1, 2, 10, 11, 20, 21, 30) return *rc = HXA_E_MODE. mod = 6 x 3072 fp32. libhexanima_moss.so exports it under
+ * the reference's own name, mega_block (include/hexanima_moss.h). */
 int mega_moss_block(remote_handle64 h, const int *meta, int nmeta, int wfd, int bfd, const uint8_t *mod, int modlen,
                     int *times, int ntimes, int *rc);
 
@@ -59,7 +63,8 @@ int mega_moss_block(remote_handle64 h, const int *meta, int nmeta, int wfd, int 
  * kind: HXA_KIND_* below. The host memory must stay valid until hxa_unregister / mega_close. */
 #define HXA_KIND_WEIGHTS_ANIMA 0 /* blkNN.bin of hexagon/mega/export_all.py (fp16 crouton or q8 records) */
 #define HXA_KIND_BLOB 1          /* activation blob (offsets in meta[]) */
-#define HXA_KIND_WEIGHTS_MOSS 2  /* blkNN.bin of moss/export_moss.py (q8 records, LoRA rows appended) */
+#define HXA_KIND_WEIGHTS_MOSS 2  /* blkNN.bin of moss/export_moss.py (q8 records, LoRA-B rows appended, LoRA-A
+                                    matrices): converted to a kind-2 pack */
 int hxa_register(remote_handle64 h, int fd, void *host_ptr, size_t bytes, int kind);
 int hxa_unregister(remote_handle64 h, int fd);
 
@@ -178,12 +183,16 @@ int hxa_rows_to_x32(const float *x, float *tiles, int R, int C, void *stream);
  *   w2 [D][F], then gain fp32 [4][128] (q/sqrt(128), k, cross q/sqrt(128), cross k).
  * kind 1 (MOSS structure): qkv [3D][D], o [D][D], ug [2F][D] (rows interleaved per 32: up_j, gate_j),
  *   down [D][F], then fp32 gq[128], gk[128], n1[D], n2[D].
+ * kind 2 (MOSS + LoRA, moss/export_moss.py:34-58): as kind 1 with each projection's 128 scaled LoRA-B columns after
+ *   K -- qkv [3D][D + 384] (q rows use columns [D, D+128), k rows [D+128, D+256), v rows [D+256, D+384), zero
+ *   elsewhere), o [D][D + 128], ug [2F][D + 128], down [D][F + 128] -- then the LoRA-A matrices A_qkv [384][D],
+ *   A_o [128][D] (fmt_attn), A_ug [128][D], A_dn [128][F] (fmt_mlp); the same vectors as kind 1.
  * fmt_attn applies to the attention matrices, fmt_mlp to the MLP ones (asym q4 not used in packs).
  * offs receives 3 offsets (w, s, z; -1 when absent) per matrix followed by the vector offset; returns bytes. */
 long hxa_pack_layout(int kind, int D, int F, int DC, int fmt_attn, int fmt_mlp, long *offs, int noffs);
 
 typedef struct {
-  int kind;      /* 0 Anima, 1 MOSS */
+  int kind;      /* 0 Anima, 1 MOSS, 2 MOSS with the rapid-moss LoRA (rank 128, moss/hexagon/mega/blk.c:238-259) */
   int D, H, F;   /* width, heads (x128), MLP width (MOSS: up and gate each F) */
   int C, DC;     /* context tokens per image and context width (Anima) */
   int T, batch;  /* tokens per image (padded to 32), images */
@@ -191,8 +200,10 @@ typedef struct {
   int fmt_attn, fmt_mlp;
   int gelu;      /* Anima MLP activation: 0 erf (reference block), 1 tanh */
 } hxa_block_dims;
-/* bytes of the activation workspace of hxa_block_run (with int8 / int4 weights and batch*T >= 1024 it includes one
- * fp16 copy of the largest o-class or MLP-down weight, which those projections run from) */
+/* bytes of the activation workspace of hxa_block_run. With int8 / int4 weights it includes the dequantisation slot:
+ * one fp16 copy of the largest quantised projection that runs from fp16 -- from batch*T >= 1024 rows those with
+ * N <= K (attention output, cross q, MLP down), from 4096 rows all of them -- and for Anima blocks a second slot for
+ * the text k / v weight. */
 long hxa_block_ws_bytes(const hxa_block_dims *d);
 /* One block, everything on the device:
  *   x    [batch*T][D] fp32 residual stream, updated in place
@@ -213,8 +224,9 @@ int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x, const voi
 int hxa_block_run_noalloc(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
                           const float *cosT, const float *sinT, int stop, void *stream);
 /* stage buffers of the workspace: which 0 h, 1 q, 2 k, 3 vT ([D][batch*T]), 4 o, 5 t1, 6 mid, 7 ck, 8 cvT, 9 t2,
- * 10 the fp16 weight copy;
- * returns the device pointer and its row stride in elements */
+ * 10 the dequantisation slot (k-tiled [K/32][N][32] fp16 copies; *ld = 0: no row stride);
+ * returns the device pointer and its row stride in elements (kind 2: h, o and mid rows carry the LoRA L columns
+ * after their D / D / F activations, so their strides are D + 384, D + 128, F + 128) */
 void *hxa_block_ws_buf(const hxa_block_dims *d, void *ws, int which, long *ld);
 
 /* ============================================================================================================

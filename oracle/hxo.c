@@ -492,6 +492,7 @@ void hxo_wt16_unpack(const uint16_t *tiles, int N, int K, uint16_t *wNK) {
 }
 void hxo_q8rec_pack(const uint16_t *wNK, int N, int K, uint8_t *rec, int floor_mode) {
   const int kb = K / 32, nb = N / 32;
+#pragma omp parallel for schedule(static)
   for (int jb = 0; jb < nb; jb++)
     for (int ib = 0; ib < kb; ib++) {
       uint8_t *R = rec + ((size_t)jb * kb + ib) * 1152;
@@ -515,6 +516,7 @@ void hxo_q8rec_pack(const uint16_t *wNK, int N, int K, uint8_t *rec, int floor_m
 }
 void hxo_q8rec_unpack(const uint8_t *rec, int N, int K, uint16_t *wNK) {
   const int kb = K / 32, nb = N / 32;
+#pragma omp parallel for schedule(static)
   for (int jb = 0; jb < nb; jb++)
     for (int ib = 0; ib < kb; ib++) {
       const uint8_t *R = rec + ((size_t)jb * kb + ib) * 1152;
@@ -630,42 +632,66 @@ done:
   return stage;
 }
 
+#define LORA_R 128
+/* C[T][N] = [a | l] . W^T with a [T][Ka] (row stride lda), the LoRA columns l [T][r] (ldl; NULL: none) and
+   W[N][Ka + r] (ldw): the K range of the reference's gemm_geo_t A2 tiles (moss/hexagon/mega/gemm2.c:125-133) */
+static void gemm_cat(const uint16_t *a, long lda, int Ka, const uint16_t *l, long ldl, int r, const uint16_t *W, long ldw,
+                     float *C, int T, int N, uint16_t *cat) {
+  if (!l) { hxo_gemm(a, lda, W, ldw, C, N, T, N, Ka); return; }
+#pragma omp parallel for schedule(static)
+  for (int t = 0; t < T; t++) {
+    memcpy(cat + (size_t)t * (Ka + r), a + (size_t)t * lda, sizeof(uint16_t) * Ka);
+    memcpy(cat + (size_t)t * (Ka + r) + Ka, l + (size_t)t * ldl, sizeof(uint16_t) * r);
+  }
+  hxo_gemm(cat, Ka + r, W, ldw, C, N, T, N, Ka + r);
+}
+
 int hxo_moss_block(const hxo_moss_cfg *cfg, const hxo_moss_w *w, float *x, const float *mod6, const float *cosT,
                    const float *sinT, hxo_moss_buf *b) {
   const int T = cfg->T, D = cfg->D, H = cfg->H, F = cfg->F;
+  const int lora = w->aqkv != NULL, R = lora ? LORA_R : 0;
   const float *sha = mod6, *sca = mod6 + D, *ga = mod6 + 2 * D, *shf = mod6 + 3 * D, *scf = mod6 + 4 * D, *gf = mod6 + 5 * D;
   float *tmp = (float *)malloc(sizeof(float) * (size_t)T * (F > D ? F : D));
   uint16_t *t2 = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * D);
+  uint16_t *cat = lora ? (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * ((F / 2 > D ? F / 2 : D) + R)) : NULL;
   int stage = 0;
   hxo_rmsmod(x, T, D, w->n1, sha, sca, 1e-6f, b->h);
   TICK();
-  TICK(); /* LoRA-A GEMM stage of the reference (no LoRA here) */
-  hxo_gemm(b->h, D, w->wq, D, tmp, D, T, D, D); f2h_rows(tmp, D, b->q, D, T, D);
-  hxo_gemm(b->h, D, w->wk, D, tmp, D, T, D, D); f2h_rows(tmp, D, b->k, D, T, D);
-  hxo_gemm(b->h, D, w->wv, D, tmp, D, T, D, D); f2h_rows(tmp, D, b->v, D, T, D);
+  if (lora) { /* L = f16(h . A_qkv) (blk.c:238) */
+    hxo_gemm(b->h, D, w->aqkv, D, tmp, 3 * R, T, 3 * R, D); f2h_rows(tmp, 3 * R, b->lqkv, 3 * R, T, 3 * R);
+  }
+  TICK(); /* the LoRA-A GEMM stage (blk.c:238) */
+  gemm_cat(b->h, D, D, lora ? b->lqkv : NULL, 3 * R, R, w->wq, D + R, tmp, T, D, cat); f2h_rows(tmp, D, b->q, D, T, D);
+  gemm_cat(b->h, D, D, lora ? b->lqkv + R : NULL, 3 * R, R, w->wk, D + R, tmp, T, D, cat); f2h_rows(tmp, D, b->k, D, T, D);
+  gemm_cat(b->h, D, D, lora ? b->lqkv + 2 * R : NULL, 3 * R, R, w->wv, D + R, tmp, T, D, cat); f2h_rows(tmp, D, b->v, D, T, D);
   hxo_rmsrope(b->q, T, D, H, w->gq, cosT, sinT, 1);
   hxo_rmsrope(b->k, T, D, H, w->gk, cosT, sinT, 1);
   TICK();
   hxo_attention(b->q, D, b->k, D, b->v, D, b->o, D, T, T, cfg->nvalid, H, cfg->attn_mode);
   TICK();
-  hxo_gemm(b->o, D, w->wo, D, tmp, D, T, D, D); f2h_rows(tmp, D, b->t, D, T, D);
+  if (lora) { hxo_gemm(b->o, D, w->ao, D, tmp, R, T, R, D); f2h_rows(tmp, R, b->lo, R, T, R); } /* blk.c:244 */
+  gemm_cat(b->o, D, D, lora ? b->lo : NULL, R, R, w->wo, D + R, tmp, T, D, cat); f2h_rows(tmp, D, b->t, D, T, D);
   hxo_resadd(x, T, D, b->t, ga);
   TICK();
   hxo_rmsmod(x, T, D, w->n2, shf, scf, 1e-6f, b->h);
   TICK();
-  hxo_gemm(b->h, D, w->wup, D, tmp, F, T, F, D); f2h_rows(tmp, F, b->up, F, T, F);
-  hxo_gemm(b->h, D, w->wgate, D, tmp, F, T, F, D); f2h_rows(tmp, F, b->gate, F, T, F);
+  if (lora) { hxo_gemm(b->h, D, w->aug, D, tmp, R, T, R, D); f2h_rows(tmp, R, b->lu, R, T, R); } /* blk.c:251 */
+  gemm_cat(b->h, D, D, lora ? b->lu : NULL, R, R, w->wup, D + R, tmp, T, F, cat); f2h_rows(tmp, F, b->up, F, T, F);
+  gemm_cat(b->h, D, D, lora ? b->lu : NULL, R, R, w->wgate, D + R, tmp, T, F, cat); f2h_rows(tmp, F, b->gate, F, T, F);
   hxo_situ_n(b->up, b->gate, b->mid, (size_t)T * F);
   TICK();
   {
     const int F2 = F / 2;
-    hxo_gemm(b->mid, F, w->wdown, F, tmp, D, T, D, F2); f2h_rows(tmp, D, b->t, D, T, D);
-    hxo_gemm(b->mid + F2, F, w->wdown + F2, F, tmp, D, T, D, F2); f2h_rows(tmp, D, t2, D, T, D);
+    if (lora) { hxo_gemm(b->mid, F, w->adn, F, tmp, R, T, R, F); f2h_rows(tmp, R, b->ld, R, T, R); } /* blk.c:255 */
+    /* first K half without, second K half with the LoRA columns (blk.c:256-259) */
+    hxo_gemm(b->mid, F, w->wdown, F + R, tmp, D, T, D, F2); f2h_rows(tmp, D, b->t, D, T, D);
+    gemm_cat(b->mid + F2, F, F2, lora ? b->ld : NULL, R, R, w->wdown + F2, F + R, tmp, T, D, cat);
+    f2h_rows(tmp, D, t2, D, T, D);
     hxo_resadd2(x, T, D, b->t, t2, gf);
   }
   TICK();
 done:
-  free(tmp); free(t2);
+  free(tmp); free(t2); free(cat);
   return stage;
 }
 

@@ -128,16 +128,23 @@ typedef struct {
   int T, nvalid, D, H, F; /* padded tokens, valid tokens, width, heads, FFN width (up and gate each F) */
   int stop, attn_mode;
 } hxo_moss_cfg;
+/* rapid-moss LoRA (moss/hexagon/mega/blk.c:238-259, packed by moss/export_moss.py:34-47): with aqkv != NULL every
+   projection runs on [x | L] . [W ; s B] where L = f16(x . A) is rank r = 128 and the scaled B rows are appended
+   along K. The matrices are then W[N][K + r]: wq / wk / wv / wo / wup / wgate [.][D + r], wdown [D][F + r]; the
+   A matrices (as W[N][K]): aqkv [3r][D] (q, k, v parts), ao [r][D], aug [r][D], adn [r][F]. The down projection's
+   two K halves are [0, F/2) and [F/2, F) + the r LoRA columns (blk.c:256-259). */
 typedef struct {
-  const uint16_t *wq, *wk, *wv, *wo; /* [D][D] */
-  const uint16_t *wup, *wgate;       /* [F][D] */
-  const uint16_t *wdown;             /* [D][F] */
+  const uint16_t *wq, *wk, *wv, *wo; /* [D][D] ([D][D + r] with LoRA) */
+  const uint16_t *wup, *wgate;       /* [F][D] ([F][D + r]) */
+  const uint16_t *wdown;             /* [D][F] ([D][F + r]) */
   const float *gq, *gk;              /* [128]; gq pre-scaled by 1/sqrt(128) */
   const float *n1, *n2;              /* [D] RMSNorm weights */
+  const uint16_t *aqkv, *ao, *aug, *adn; /* LoRA A matrices (NULL: no LoRA) */
 } hxo_moss_w;
 typedef struct {
   uint16_t *h, *q, *k, *v, *o, *t; /* [T][D] */
   uint16_t *up, *gate, *mid;       /* [T][F] */
+  uint16_t *lqkv, *lo, *lu, *ld;   /* LoRA L buffers [T][3r], [T][r] x 3 (NULL / unused without LoRA) */
 } hxo_moss_buf;
 int hxo_moss_block(const hxo_moss_cfg *cfg, const hxo_moss_w *w, float *x, const float *mod6, const float *cosT,
                    const float *sinT, hxo_moss_buf *b);

@@ -46,11 +46,12 @@ class _MCfg(C.Structure):
 
 
 class _MW(C.Structure):
-    _fields_ = [(n, P) for n in ("wq", "wk", "wv", "wo", "wup", "wgate", "wdown", "gq", "gk", "n1", "n2")]
+    _fields_ = [(n, P) for n in ("wq", "wk", "wv", "wo", "wup", "wgate", "wdown", "gq", "gk", "n1", "n2", "aqkv", "ao",
+                                 "aug", "adn")]
 
 
 class _MB(C.Structure):
-    _fields_ = [(n, P) for n in ("h", "q", "k", "v", "o", "t", "up", "gate", "mid")]
+    _fields_ = [(n, P) for n in ("h", "q", "k", "v", "o", "t", "up", "gate", "mid", "lqkv", "lo", "lu", "ld")]
 
 
 def lib():
@@ -411,19 +412,35 @@ def anima_block(x, ctx, mod9, cos, sin, w: dict, *, H, F, gelu=1, stop=0, attn_m
 
 
 MOSS_W = ("wq", "wk", "wv", "wo", "wup", "wgate", "wdown")
+MOSS_A = ("aqkv", "ao", "aug", "adn")
+LORA_R = 128
 
 
 def moss_block(x, mod6, cos, sin, w: dict, *, H, F, nvalid=None, stop=0, attn_mode=0):
+    """One MOSS-class block. w: fp16 W[N][K] matrices wq, wk, wv, wo, wup, wgate, wdown, the fp32 vectors gq, gk,
+    n1, n2 and, for the rapid-moss LoRA (moss/hexagon/mega/blk.c:238-259), the A matrices aqkv [384][D], ao [128][D],
+    aug [128][D], adn [128][F] with every W then carrying its 128 scaled B columns after K ([N][K + 128]).
+    Returns (x_out, stage buffers dict, number of stages run)."""
     x = _f32(x).copy()
     T, D = x.shape
+    lora = w.get("aqkv") is not None
+    R = LORA_R if lora else 0
     ws = {k: _u16(w[k]) for k in MOSS_W}
+    for k in ("wq", "wk", "wv", "wo"):
+        assert ws[k].shape == (D, D + R), (k, ws[k].shape)
+    assert ws["wup"].shape == (F, D + R) and ws["wgate"].shape == (F, D + R) and ws["wdown"].shape == (D, F + R)
+    aw = {k: _u16(w[k]) for k in MOSS_A} if lora else {}
     vec = {k: _f32(w[k]) for k in ("gq", "gk", "n1", "n2")}
     buf = {k: np.zeros((T, D), np.uint16) for k in ("h", "q", "k", "v", "o", "t")}
     for k in ("up", "gate", "mid"):
         buf[k] = np.zeros((T, F), np.uint16)
+    buf["lqkv"] = np.zeros((T, 3 * max(R, 1)), np.uint16)
+    for k in ("lo", "lu", "ld"):
+        buf[k] = np.zeros((T, max(R, 1)), np.uint16)
     cfg = _MCfg(T, T if nvalid is None else nvalid, D, H, F, stop, attn_mode)
-    mw = _MW(*[_p(ws[k]) for k in MOSS_W], *[_p(vec[k]) for k in ("gq", "gk", "n1", "n2")])
-    mb = _MB(*[_p(buf[k]) for k in ("h", "q", "k", "v", "o", "t", "up", "gate", "mid")])
+    mw = _MW(*[_p(ws[k]) for k in MOSS_W], *[_p(vec[k]) for k in ("gq", "gk", "n1", "n2")],
+             *[_p(aw[k]) if lora else None for k in MOSS_A])
+    mb = _MB(*[_p(buf[k]) for k in ("h", "q", "k", "v", "o", "t", "up", "gate", "mid", "lqkv", "lo", "lu", "ld")])
     mod6 = _f32(mod6)
     cos, sin = _f32(cos), _f32(sin)
     n = lib().hxo_moss_block(C.byref(cfg), C.byref(mw), _p(x), _p(mod6), _p(cos), _p(sin), C.byref(mb))

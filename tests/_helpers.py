@@ -40,11 +40,11 @@ def unpack_weights(pack: np.ndarray, kind: int, D: int, F: int, DC: int, fmt_att
     """GPU pack image (k-tiled matrices) -> dict of fp16 (uint16) W[N][K] matrices (dequantised) and the fp32
     vector section."""
     total, offs, voff = layout
-    shapes = ([(3 * D, D), (D, D), (D, D), (2 * D, DC), (D, D), (F, D), (D, F)] if kind == 0
-              else [(3 * D, D), (D, D), (2 * F, D), (D, F)])
+    shapes = hip.pack_shapes(kind, D, F, DC)
+    fmts = hip.pack_fmts(kind, fmt_attn, fmt_mlp)
     mats = []
     for i, ((N, K), (wo, so)) in enumerate(zip(shapes, offs)):
-        fmt = fmt_attn if i < (5 if kind == 0 else 2) else fmt_mlp
+        fmt = fmts[i]
         if fmt == 0:
             mats.append(hip.unktile(pack[wo:wo + N * K * 2], N, K).view(np.uint16).reshape(N, K).copy())
         else:
@@ -60,12 +60,22 @@ def unpack_weights(pack: np.ndarray, kind: int, D: int, F: int, DC: int, fmt_att
         vec = pack[voff:voff + 4 * 512].view(np.float32).copy()
         return {"wq": qkv[:D], "wk": qkv[D:2 * D], "wv": qkv[2 * D:], "wo": wo_, "wcq": wcq, "wck": ckv[:D],
                 "wcv": ckv[D:], "wco": wco, "w1": w1, "w2": w2, "gain": vec}
-    qkv, wo_, ug, dn = mats
+    qkv, wo_, ug, dn = mats[:4]
     vec = pack[voff:voff + 4 * (256 + 2 * D)].view(np.float32).copy()
-    ugr = ug.reshape(F // 32, 2, 32, D)
-    return {"wq": qkv[:D], "wk": qkv[D:2 * D], "wv": qkv[2 * D:], "wo": wo_,
-            "wup": np.ascontiguousarray(ugr[:, 0].reshape(F, D)), "wgate": np.ascontiguousarray(ugr[:, 1].reshape(F, D)),
-            "wdown": dn, "gq": vec[:128], "gk": vec[128:256], "n1": vec[256:256 + D], "n2": vec[256 + D:]}
+    K1 = ug.shape[1]
+    ugr = ug.reshape(F // 32, 2, 32, K1)
+    out = {"wo": wo_, "wup": np.ascontiguousarray(ugr[:, 0].reshape(F, K1)),
+           "wgate": np.ascontiguousarray(ugr[:, 1].reshape(F, K1)), "wdown": dn, "gq": vec[:128], "gk": vec[128:256],
+           "n1": vec[256:256 + D], "n2": vec[256 + D:]}
+    if kind == 1:
+        out.update({"wq": qkv[:D], "wk": qkv[D:2 * D], "wv": qkv[2 * D:]})
+    else:  # block-diagonal LoRA columns of the fused qkv -> [W | s B] per projection (the oracle's form)
+        R = hip.LORA_R
+        for p, n in enumerate(("wq", "wk", "wv")):
+            rows = qkv[p * D:(p + 1) * D]
+            out[n] = np.ascontiguousarray(np.concatenate([rows[:, :D], rows[:, D + p * R:D + (p + 1) * R]], 1))
+        out.update({"aqkv": mats[4], "ao": mats[5], "aug": mats[6], "adn": mats[7]})
+    return out
 
 
 def silu(v):

@@ -12,8 +12,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "hexanima_hip.h")
 
 
-def _declared():
-    src = open(HEADER).read()
+MOSS_HEADER = os.path.join(ROOT, "include", "hexanima_moss.h")
+
+
+def _declared(header=HEADER):
+    src = open(header).read()
     return set(re.findall(r"^\s*(?:int|long|void\s*\*|const char\s*\*)\s*\**\s*(\w+)\s*\(", src, re.M))
 
 
@@ -34,6 +37,18 @@ def test_library_exports_every_declared_symbol(hip):
     assert {"mega_open", "mega_block", "mega_close"} <= syms
     # and the Python binding covers exactly the declared set
     assert set(hip.exported_symbols()) == decl
+
+
+def test_moss_library_exports_the_reference_mega_block(hip):
+    """libhexanima_moss.so exports mega_block (moss/hexagon/mega/blk.c:269, called mossrun.cpp:185) and nothing that
+    would shadow libhexanima_hip.so's other entry points; it resolves mega_moss_block from libhexanima_hip.so."""
+    path = os.path.join(os.path.dirname(hip.LIB_PATH), "libhexanima_moss.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    syms = {l.split()[-1] for l in out.splitlines() if l.strip()} - {"_init", "_fini"}
+    assert _declared(MOSS_HEADER) == {"mega_block"} and syms == {"mega_block"}, syms
+    und = subprocess.run(["nm", "-D", "--undefined-only", path], capture_output=True, text=True, check=True).stdout
+    assert "mega_moss_block" in und
+    C.CDLL(path).mega_block  # loads, with libhexanima_hip.so found next to it
 
 
 def test_pack_layout_matches_reference_matrix_bytes(hip):

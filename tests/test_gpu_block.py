@@ -184,6 +184,63 @@ def test_moss_block_joint_attention_q8_q4(T, nv, gh, gw, F, ntxt, maxabs):
     assert r < 1.2e-3 and c > 1 - 1.2e-3 ** 2 and mx < maxabs
 
 
+def lora_pack_mats(rng, D, F, fmt_attn, fmt_mlp):
+    """Random MOSS weights with the rapid-moss LoRA in the kind-2 pack order (hip.pack_shapes(2, ...)): the fp32
+    projections with their scaled LoRA-B columns after K (q / k / v block-diagonal in the fused qkv), then the LoRA-A
+    matrices, each quantised to its format."""
+    R = 128
+    nrm = lambda *sh: (rng.standard_normal(sh, dtype=np.float32) * 0.02).astype(np.float32)
+    qkv = np.zeros((3 * D, D + 3 * R), np.float32)
+    for p in range(3):
+        qkv[p * D:(p + 1) * D, :D] = nrm(D, D)
+        qkv[p * D:(p + 1) * D, D + p * R:D + (p + 1) * R] = nrm(D, R) * 2
+    o = np.concatenate([nrm(D, D), nrm(D, R) * 2], 1)
+    ug = np.concatenate([nrm(2 * F, D), nrm(2 * F, R) * 2], 1)  # rows interleaved per 32 (up_j, gate_j) as packed
+    dn = np.concatenate([nrm(D, F), nrm(D, R) * 2], 1)
+    A = [nrm(3 * R, D) * 2, nrm(R, D) * 2, nrm(R, D) * 2, nrm(R, F) * 2]
+    q = lambda W, f: hxo.q8_quantize(W) if f == 1 else hxo.q4_quantize(W)
+    return [q(qkv, fmt_attn), q(o, fmt_attn), q(ug, fmt_mlp), q(dn, fmt_mlp), q(A[0], fmt_attn), q(A[1], fmt_attn),
+            q(A[2], fmt_mlp), q(A[3], fmt_mlp)]
+
+
+@pytest.mark.parametrize("T,nv,gh,gw", [(544, 520, 20, 24), (1088, 1060, 30, 34), (4128, 4100, 58, 70)])
+def test_moss_lora_block_q8_q4(T, nv, gh, gw):
+    """MOSS-class block with the rapid-moss LoRA (kind-2 pack: moss/hexagon/mega/blk.c:238-259): four LoRA-A GEMMs
+    write L next to the activations they read, and every projection runs on [x | L] . [W ; s B] with the B rows as 4
+    extra k groups; the down projection's second K half carries them. int8 attention / int4 MLP weights; at 1088
+    rows the o and down projections, at 4128 rows all of them, run through the dequantisation pass."""
+    hip = _hip()
+    say(f"moss LoRA block T={T} nvalid={nv} D=3072 F=4096 q8/q4")
+    rng = np.random.default_rng(13)
+    D, F = 3072, 4096
+    H = D // 128
+    mats = lora_pack_mats(rng, D, F, 1, 2)
+    vec = np.concatenate([np.full(128, 1 / np.sqrt(128)), np.ones(128), rng.uniform(0.5, 1.5, 2 * D)]).astype(np.float32)
+    img = hip.build_pack(2, D, F, 0, 1, 2, mats, vec)
+    w = unpack_weights(img, 2, D, F, 0, 1, 2, hip.pack_layout(2, D, F, 0, 1, 2))
+    x = (rng.standard_normal((T, D)) * 2).astype(np.float32)
+    x[nv:] = 0
+    mod6 = (rng.standard_normal((6, D)) * 0.2).astype(np.float32)
+    bands = (1.0 / 10000.0 ** (np.arange(16) / 16)).astype(np.float32)
+    cs, sn = hxo.rope_moss(gh, gw, 40, bands)
+    cos = np.concatenate([cs, np.ones((T - nv, 64), np.float32)])
+    sin = np.concatenate([sn, np.zeros((T - nv, 64), np.float32)])
+    d = hip.BlockDims(2, D, H, F, 0, 0, T, 1, nv, 1, 2, 0)
+    got, ws, us = run_block_gpu(hip, d, img, x, None, mod6, cos, sin)
+    print("stage us:", us[:8], flush=True)
+    ref, buf, n = hxo.moss_block(x, mod6, cos, sin, w, H=H, F=F, nvalid=nv)
+    r, c, mx = metrics_line(got[:nv], ref[:nv], x[:nv])
+    plain = {k: v for k, v in w.items() if k not in ("aqkv", "ao", "aug", "adn")}
+    for k in ("wq", "wk", "wv", "wo", "wup", "wgate"):
+        plain[k] = np.ascontiguousarray(w[k][:, :D])
+    plain["wdown"] = np.ascontiguousarray(w["wdown"][:, :F])
+    nolora, _, _ = hxo.moss_block(x, mod6, cos, sin, plain, H=H, F=F, nvalid=nv)
+    r0, _, _ = metrics_line(nolora[:nv], ref[:nv], x[:nv])
+    print(f"moss LoRA rel err on delta {r:.2e} cos {c:.8f} max abs {mx:.2e} (the LoRA term itself: {r0:.2e})", flush=True)
+    assert r0 > 30 * r  # the LoRA term is far above the tolerance: dropping it would fail
+    assert r < 1.6e-3 and c > 1 - 1.6e-3 ** 2 and mx < 1.6e-2  # measured 5.3e-4 - 5.4e-4, 4.4e-3 - 5.2e-3
+
+
 # ------------------------------------------------------------------------------------------------ reference ABI
 def _megarun_layout(T, nctx):
     """megarun.cpp:42-57 layout(): blob offsets (4 KiB aligned) of x, ctx, mod, cos, sin, h, q, k, v, o, t, mid, ck, cv."""
@@ -373,6 +430,135 @@ def test_mega_block_stage_dumps_1536():
                 e = rel(g, buf[k.lower()].view(np.float16).astype(np.float32))
                 print(f"stop {stop}: {k} rel err {e:.2e}", flush=True)
                 assert e < tol, (stop, k)
+    finally:
+        lib.mega_close(h)
+
+
+# moss/hexagon/mega/blk_meta.h:3-4
+MOSS_META = ["X", "COS", "SIN", "H", "Q", "K", "V", "O", "T", "MID", "LQ", "LO", "LU", "LD", "NTOK", "NVALID", "STOP", "NW",
+             "REL", "FIRST", "MODE", "NCB", "FMT", "ROWS", "CS", "WOFF"]
+
+
+def _mossrun_layout(ntok, hid=3072, midcols=8192):
+    """mossrun.cpp:117-126 make_layout(ntok, 3072, 8192, rows=false): 4 KiB aligned blob offsets."""
+    ns = ntok // 32
+    up = lambda v: (v + 4095) & ~4095
+    ent = [("X", ntok * hid * 4), ("COS", ns * 8192), ("SIN", ns * 8192), ("H", ntok * max(hid, 4096) * 2)]
+    ent += [(k, ntok * hid * 2) for k in ("Q", "K", "V", "O", "T")]
+    ent += [("MID", ntok * midcols * 2), ("ROWS", 4096), ("CS", ntok * 64 * 4), ("LQ", ns * 12 * 2048),
+            ("LO", ns * 4 * 2048), ("LU", ns * 4 * 2048), ("LD", ns * 4 * 2048)]
+    offs, off = {}, 0
+    for k, b in ent:
+        offs[k] = off
+        off += up(b)
+    return offs, off
+
+
+def _moss_blk_file(rng):
+    """A synthetic blkNN.bin in the moss/export_moss.py:49-61 (pack_layer) layout, 135397376 bytes: q, k, v, o,
+    up_gate, down as q8 records of [K + 128][N] with the scaled LoRA-B rows after K (mat(), :34-47; up_gate's
+    32-column blocks interleaved up / gate), then A_qkv = cat(A_q, A_k, A_v), A_o, A_up_gate, A_down, and the gains
+    (q/sqrt(128), k, norm1, norm2, padded to 8192 floats). Returns the file and the oracle's weights (the records
+    dequantised, in the [W | s B] form)."""
+    D, F, R = 3072, 8192, 128
+    nrm = lambda *sh: rng.standard_normal(sh, dtype=np.float32) * 0.02
+    ext = lambda W, n_out: np.concatenate([W, nrm(n_out, R) * 2], 1)  # [W | s B]
+    wq, wk, wv, wo = (ext(nrm(D, D), D) for _ in range(4))
+    up, gate = ext(nrm(F, D), F), ext(nrm(F, D), F)
+    ug = np.stack([up.reshape(F // 32, 32, D + R), gate.reshape(F // 32, 32, D + R)], 1).reshape(2 * F, D + R)
+    dn = ext(nrm(D, F), D)
+    A = [nrm(3 * R, D) * 2, nrm(R, D) * 2, nrm(R, D) * 2, nrm(R, F) * 2]
+    parts, w = [], {}
+    for name, W in (("wq", wq), ("wk", wk), ("wv", wv), ("wo", wo), ("ug", ug), ("wdown", dn), ("aqkv", A[0]),
+                    ("ao", A[1]), ("aug", A[2]), ("adn", A[3])):
+        rec = hxo.q8rec_pack(f16(W), floor_mode=1)
+        parts.append(rec)
+        w[name] = hxo.q8rec_unpack(rec, W.shape[0], W.shape[1])
+    ugd = w.pop("ug").reshape(F // 32, 2, 32, D + R)
+    w["wup"], w["wgate"] = (np.ascontiguousarray(ugd[:, i].reshape(F, D + R)) for i in (0, 1))
+    gain = np.concatenate([rng.uniform(0.5, 1.5, 128) / np.sqrt(128), rng.uniform(0.5, 1.5, 128),
+                           rng.uniform(0.5, 1.5, 2 * D)]).astype(np.float32)
+    w["gq"], w["gk"], w["n1"], w["n2"] = gain[:128], gain[128:256], gain[256:256 + D], gain[256 + D:]
+    parts.append(np.concatenate([gain, np.zeros(8192 - gain.size, np.float32)]).view(np.uint8))
+    blob = np.concatenate([p.reshape(-1).view(np.uint8) for p in parts])
+    assert blob.size == 135397376
+    offs = np.cumsum([0] + [p.size for p in parts])  # moss blk_meta.h:6-17 offsets
+    assert list(offs[:11]) == [0, 11059200, 22118400, 33177600, 44236800, 103219200, 131973120, 133300224, 133742592,
+                               134184960, 135364608]
+    return blob, w
+
+
+def test_mega_block_moss_abi_with_lora():
+    """One MOSS-class DiT block through libhexanima_moss.so's mega_block -- the reference's own symbol, as mossrun
+    calls it (mossrun.cpp:182-188, MODE 0) -- on a synthetic export_moss.py pack with the rapid-moss LoRA: 544 tokens,
+    520 valid (480 image + 40 text), against the oracle with the LoRA term; M_STOP stage dumps of h and o; the text
+    side's modes (1, 2, 10, 20, ...) are refused with -11."""
+    import os
+    hip = _hip()
+    say("MOSS mega_block ABI with LoRA, T=544 nvalid=520")
+    lib = hip.lib()
+    moss = C.CDLL(os.path.join(os.path.dirname(hip.LIB_PATH), "libhexanima_moss.so"))
+    moss.mega_block.restype = C.c_int
+    moss.mega_block.argtypes = [C.c_uint64, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
+                                C.c_int, C.c_void_p]
+    rng = np.random.default_rng(55)
+    D, F, T, NV, gh, gw, ntxt = 3072, 8192, 544, 520, 20, 24, 40
+    wfile, w = _moss_blk_file(rng)
+    offs, total = _mossrun_layout(T)
+    blob = np.zeros(total, np.uint8)
+    x = np.zeros((T, D), np.float32)
+    x[:NV] = rng.standard_normal((NV, D)) * 2
+    bands = (1.0 / 10000.0 ** (np.arange(16) / 16)).astype(np.float32)
+    cs, sn = hxo.rope_moss(gh, gw, ntxt, bands)
+    cos, sin = np.zeros((T, 64), np.float32), np.zeros((T, 64), np.float32)  # mossrun.cpp:192 zero-fills the padding
+    cos[:NV], sin[:NV] = cs, sn
+    x_tiles = hxo.x32_tile(x).view(np.uint8)
+    blob[offs["X"]:offs["X"] + x_tiles.size] = x_tiles
+    for nm, tab in (("COS", cos), ("SIN", sin)):  # [slab][j][32][32], angle index d = 32 j + col (mossrun.cpp:197)
+        t = np.ascontiguousarray(tab.reshape(T // 32, 32, 2, 32).transpose(0, 2, 1, 3)).astype(np.float32)
+        blob[offs[nm]:offs[nm] + t.nbytes] = t.view(np.uint8).reshape(-1)
+    mod6 = (rng.standard_normal((6, D)) * 0.2).astype(np.float32)
+    meta = np.zeros(len(MOSS_META), np.int32)
+    for k, v in offs.items():
+        meta[MOSS_META.index(k)] = v
+    for k, v in (("NTOK", T), ("NVALID", NV), ("NW", 3), ("REL", 1), ("FIRST", 1), ("MODE", 0), ("NCB", 96), ("WOFF", 0)):
+        meta[MOSS_META.index(k)] = v
+    h = C.c_uint64()
+    hip.check(lib.mega_open(b"", C.byref(h)), "mega_open")
+    try:
+        hip.check(lib.hxa_register(h, 100, blob.ctypes.data, blob.nbytes, hip.KIND_BLOB), "register blob")
+        hip.check(lib.hxa_register(h, 300, wfile.ctypes.data, wfile.nbytes, hip.KIND_WEIGHTS_MOSS), "register w")
+        rc = C.c_int(0)
+        times = np.full(32, -1, np.int32)
+        t0 = time.time()
+        r = moss.mega_block(h.value, meta.ctypes.data, len(MOSS_META), 300, 100, mod6.ctypes.data, mod6.nbytes,
+                            times.ctypes.data, 32, C.byref(rc))
+        assert r == 0 and rc.value == 0, hip.last_error()
+        print(f"times (us) {times[:8].tolist()} entry {times[24]}, call {1e3 * (time.time() - t0):.0f} ms", flush=True)
+        assert (times[:8] >= 0).all() and (times[8:17] == 0).all() and times[24] >= 0
+        got = hxo.x32_untile(blob[offs["X"]:offs["X"] + T * D * 4].view(np.float32).copy(), T, D)
+        ref, buf, n = hxo.moss_block(x, mod6, cos, sin, w, H=24, F=F, nvalid=NV)
+        r_, c, mx = metrics_line(got[:NV], ref[:NV], x[:NV])
+        print(f"MOSS ABI rel err on delta {r_:.2e} cos {c:.8f} max abs {mx:.2e}", flush=True)
+        assert r_ < 1.6e-3 and c > 1 - 1.6e-3 ** 2 and mx < 1.9e-2  # measured 5.4e-4, 6.4e-3
+        # M_STOP: stop after n stages, the stage buffers left in the blob as h16 tiles
+        for stop, key in ((1, "H"), (4, "O")):
+            blob[offs["X"]:offs["X"] + x_tiles.size] = x_tiles
+            meta[MOSS_META.index("STOP")] = stop
+            r = moss.mega_block(h.value, meta.ctypes.data, len(MOSS_META), 300, 100, mod6.ctypes.data, mod6.nbytes,
+                                None, 0, C.byref(rc))
+            assert r == 0 and rc.value == 0, hip.last_error()
+            _, sbuf, _ = hxo.moss_block(x, mod6, cos, sin, w, H=24, F=F, nvalid=NV, stop=stop)
+            g = hxo.h16_untile(blob[offs[key]:offs[key] + T * D * 2].view(np.uint16), T, D).view(np.float16)[:NV]
+            e = rel(g.astype(np.float32), sbuf[key.lower()].view(np.float16)[:NV].astype(np.float32))
+            print(f"stop {stop}: {key} rel err {e:.2e}", flush=True)
+            assert e < (1e-4 if key == "H" else 2e-3)
+        meta[MOSS_META.index("STOP")] = 0
+        for mode in (1, 2, 10, 20, 30):
+            meta[MOSS_META.index("MODE")] = mode
+            r = moss.mega_block(h.value, meta.ctypes.data, len(MOSS_META), 300, 100, mod6.ctypes.data, mod6.nbytes,
+                                None, 0, C.byref(rc))
+            assert r == 0 and rc.value == -11
     finally:
         lib.mega_close(h)
 

@@ -189,3 +189,67 @@ def test_moss_stop(stop):
         assert np.array_equal(out, x)
     else:
         assert not np.array_equal(out, x)
+
+
+def make_moss_lora(T=160, nvalid=150, D=256, F=512, seed=5, scale=0.75, bzero=False):
+    """A MOSS block with the rapid-moss LoRA in the reference's torch form (moss_ref.py:44-50 `lin`: per projection
+    A [r][in], B [out][r], scale s) and in the packed form the oracle / GPU take (moss/export_moss.py:34-47 `mat`:
+    the rows of f16(s B) appended after K, A_qkv = cat(A_q, A_k, A_v))."""
+    x, mod6, cos, sin, w = make_moss(T, nvalid, D, F, seed)
+    rng = np.random.default_rng(seed + 100)
+    R = hxo.LORA_R
+    ins = {"q": D, "k": D, "v": D, "o": D, "up": D, "gate": D, "down": F}
+    A = {n: f16(rng.standard_normal((R, k)) * 0.05) for n, k in ins.items()}
+    A["gate"] = A["up"]  # one LoRA on the fused up_gate projection (moss_ref.py:64)
+    B = {n: f16(rng.standard_normal((w["w" + n].shape[0], R)) * (0.0 if bzero else 0.05)) for n in ins}
+    Bs = {n: f16(scale * B[n].astype(np.float32)) for n in ins}  # s B rounded to the pack's storage
+    wl = dict(w)
+    for n in ins:
+        wl["w" + n] = np.ascontiguousarray(np.concatenate([w["w" + n], Bs[n]], 1))
+    wl["aqkv"] = np.ascontiguousarray(np.concatenate([A["q"], A["k"], A["v"]], 0))
+    wl["ao"], wl["aug"], wl["adn"] = A["o"], A["up"], A["down"]
+    return x, mod6, cos, sin, w, wl, A, Bs
+
+
+def moss_block_lora_f64(x, mod6, cos, sin, w, A, Bs, nvalid):
+    """float64 restatement of moss_ref.py:56-67 `block` with `lin(x, W, lora=(A, B, s))` = x W^T + s (x A^T) B^T."""
+    d = lambda a: np.asarray(a).astype(np.float64)
+    lin = lambda y, n: y @ d(w["w" + n]).T + (y @ d(A[n]).T) @ d(Bs[n]).T
+    T, D = x.shape
+    H = D // 128
+    sa, ca, ga, sf, cf, gf = mod6.astype(np.float64).reshape(6, D)
+    x = x.astype(np.float64).copy()
+    y = _rms(x, w["n1"]) * (1 + ca) + sa
+    q = _rope(_rms(lin(y, "q").reshape(T, H, 128), w["gq"]), cos, sin).reshape(T, D)
+    k = _rope(_rms(lin(y, "k").reshape(T, H, 128), w["gk"]), cos, sin).reshape(T, D)
+    v = lin(y, "v")
+    x = x + lin(_attn(q, k, v, nvalid), "o") * ga
+    y = _rms(x, w["n2"]) * (1 + cf) + sf
+    up, gt = lin(y, "up"), lin(y, "gate")
+    mid = (4.0 * np.tanh(gt / 4.0) / (1 + np.exp(-gt))) * (25.0 * np.tanh(up / 25.0))
+    return x + lin(mid, "down") * gf
+
+
+def test_moss_lora_block_vs_float64_restatement():
+    """The oracle's [x | L] . [W ; s B] form (moss/hexagon/mega/blk.c:238-259) against the torch reference's
+    x W^T + s (x A^T) B^T: the q / k / v parts of L feed their own projections, the down projection's LoRA rides on
+    its second K half. The LoRA term is large enough here that a dropped or misrouted part fails the bound."""
+    x, mod6, cos, sin, w, wl, A, Bs = make_moss_lora()
+    nv = 150
+    ref = moss_block_lora_f64(x, mod6, cos, sin, w, A, Bs, nv)
+    out, buf, n = hxo.moss_block(x, mod6, cos, sin, wl, H=2, F=512, nvalid=nv)
+    assert n == 8
+    dl = (ref - x)[:nv]
+    rel = np.linalg.norm((out - ref)[:nv]) / np.linalg.norm(dl)
+    assert rel < 6e-3, rel
+    nolora = moss_block_f64(x, mod6, cos, sin, w, nv)
+    assert np.linalg.norm((nolora - ref)[:nv]) / np.linalg.norm(dl) > 20 * rel  # the LoRA term is not negligible
+
+
+def test_moss_lora_with_zero_b_is_the_plain_block():
+    """B = 0: [x | L] . [W ; 0] accumulates exact zeros after the W part, so the block is bit-identical to the
+    block without LoRA."""
+    x, mod6, cos, sin, w, wl, A, Bs = make_moss_lora(bzero=True)
+    out, _, _ = hxo.moss_block(x, mod6, cos, sin, wl, H=2, F=512, nvalid=150)
+    plain, _, _ = hxo.moss_block(x, mod6, cos, sin, w, H=2, F=512, nvalid=150)
+    assert np.array_equal(out, plain)
