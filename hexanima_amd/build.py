@@ -18,6 +18,7 @@ LIB = os.path.join(HERE, "libhexanima_hip.so")
 # the MOSS build of the block interface: exports the reference's mega_block name with the MOSS semantics
 MOSS_LIB = os.path.join(HERE, "libhexanima_moss.so")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+PROGRAMS = ["hxa_run", "hxa_blk"]
 SOURCES = ["gemm.hip", "attention.hip", "elementwise.hip", "runtime.hip", "dit.hip", "noalloc.hip"]
 
 ARCH = os.environ.get("HXA_ARCH", "gfx950")
@@ -69,6 +70,15 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"libhexanima_moss.so failed:\n{r.stderr}")
     os.replace(tmp, MOSS_LIB)
+    # the host programs above the block interface: the megarun-protocol runner and the blk_main-style harness
+    for prog in PROGRAMS:
+        out = os.path.join(HERE, prog)
+        cmd = ["g++", "-O2", "-std=c++17", "-Wall", "-I", INCLUDE, "-o", out + ".tmp", os.path.join(CSRC, prog + ".cpp"),
+               "-L", HERE, "-lhexanima_hip", "-Wl,-rpath,$ORIGIN"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"{prog} failed:\n{r.stderr}")
+        os.replace(out + ".tmp", out)
     if verbose:
         print("built", LIB)
     return LIB

@@ -852,10 +852,21 @@ struct DevBlock {  // a registered block's weights converted to a GPU pack
   hxa_block_dims dims{};
   std::vector<int> key;  // meta offsets used for the conversion
 };
+// the adaLN modulation weights of a registered Anima blkNN.bin (blk_wlayout.h:14-15, export_all.py:59-61), resident:
+// A [3 sites x 256][2048] then B [3 sites][6144][256], fp16
+struct DevModw {
+  hxa_h *w = nullptr;
+};
+constexpr long MODW_A = 256L * 2048, MODW_B = 6144L * 256;  // elements of one site's A and B
+constexpr size_t W_MODW_F16 = 125833216, W_TOTAL_F16 = 138416128;  // blk_wlayout.h:14-15
+constexpr size_t W_MODW_Q8 = 125829120 / 2048 * 1152 + 4096, W_TOTAL_Q8 = W_MODW_Q8 + (W_TOTAL_F16 - W_MODW_F16);
 struct Ctx {
   hipStream_t st = nullptr;
   std::map<int, HostBuf> bufs;
   std::map<int, DevBlock> blocks;
+  std::map<int, DevModw> modws;
+  float *mod_dev = nullptr, *emb_dev = nullptr, *h1_dev = nullptr;
+  size_t mod_dev_bytes = 0, emb_dev_bytes = 0, h1_dev_bytes = 0;
   // device-resident activations of the current run of blocks
   float *x = nullptr, *cosr = nullptr, *sinr = nullptr, *mod = nullptr, *stage = nullptr;
   hxa_h *ctx = nullptr;
@@ -1014,7 +1025,9 @@ extern "C" int mega_close(remote_handle64 h) {
   if (!c) return HXA_OK;
   (void)hipStreamSynchronize(c->st);
   for (auto &kv : c->blocks) (void)hipFree(kv.second.pack);
-  for (void *p : {(void *)c->x, (void *)c->cosr, (void *)c->sinr, (void *)c->mod, (void *)c->ctx, c->ws, (void *)c->stage})
+  for (auto &kv : c->modws) (void)hipFree(kv.second.w);
+  for (void *p : {(void *)c->x, (void *)c->cosr, (void *)c->sinr, (void *)c->mod, (void *)c->ctx, c->ws, (void *)c->stage,
+                  (void *)c->mod_dev, (void *)c->emb_dev, (void *)c->h1_dev})
     if (p) (void)hipFree(p);
   (void)hipStreamDestroy(c->st);
   delete c;
@@ -1025,10 +1038,16 @@ extern "C" int hxa_register(remote_handle64 h, int fd, void *host_ptr, size_t by
   Ctx *c = ctx_of(h);
   if (!c || !host_ptr || bytes == 0) return fail(HXA_E_ARG, "hxa_register: bad arguments");
   if (kind < 0 || kind > 2) return fail(HXA_E_MODE, "hxa_register: kind %d", kind);
+  (void)hipStreamSynchronize(c->st);
   auto it = c->blocks.find(fd);
-  if (it != c->blocks.end()) {  // re-registration invalidates the converted copy
+  if (it != c->blocks.end()) {  // re-registration invalidates the converted copies
     (void)hipFree(it->second.pack);
     c->blocks.erase(it);
+  }
+  auto mt = c->modws.find(fd);
+  if (mt != c->modws.end()) {
+    (void)hipFree(mt->second.w);
+    c->modws.erase(mt);
   }
   c->bufs[fd] = HostBuf{host_ptr, bytes, kind};
   return HXA_OK;
@@ -1041,6 +1060,11 @@ extern "C" int hxa_unregister(remote_handle64 h, int fd) {
   if (it != c->blocks.end()) {
     (void)hipFree(it->second.pack);
     c->blocks.erase(it);
+  }
+  auto mt = c->modws.find(fd);
+  if (mt != c->modws.end()) {
+    (void)hipFree(mt->second.w);
+    c->modws.erase(mt);
   }
   c->bufs.erase(fd);
   return HXA_OK;
@@ -1130,6 +1154,66 @@ int run_ref_block(Ctx *c, const BlockCall &bc, const DevBlock &db, const HostBuf
   return HXA_OK;
 }
 }  // namespace
+
+namespace {
+// The modulation weights of a registered Anima weight buffer, uploaded on first use: A_site [256][2048] and
+// B_site [6144][256] per site at W_MODW of an fp16 file or WQ_MODW of a q8 file, told apart by size like megarun
+// (megarun.cpp:97-98, blk_wlayout.h:14-20); repacked as all sites' A rows, then all sites' B.
+int modw_of(Ctx *c, int fd, const hxa_h **out) {
+  auto mt = c->modws.find(fd);
+  if (mt != c->modws.end()) {
+    *out = mt->second.w;
+    return HXA_OK;
+  }
+  auto bit = c->bufs.find(fd);
+  if (bit == c->bufs.end() || bit->second.kind != HXA_KIND_WEIGHTS_ANIMA)
+    return fail(HXA_E_WEIGHTS, "modulation: weight fd %d not registered", fd);
+  const size_t n = bit->second.bytes;
+  const size_t off = n >= W_TOTAL_F16 ? W_MODW_F16 : n >= W_TOTAL_Q8 ? W_MODW_Q8 : 0;
+  if (off == 0) return fail(HXA_E_WEIGHTS, "modulation: weight fd %d (%zu bytes) holds no modulation weights", fd, n);
+  const uint16_t *src = (const uint16_t *)((const uint8_t *)bit->second.ptr + off);
+  std::vector<uint16_t> host(3 * (MODW_A + MODW_B));
+  for (int site = 0; site < 3; site++) {
+    const uint16_t *a = src + site * (MODW_A + MODW_B), *b = a + MODW_A;
+    memcpy(host.data() + site * MODW_A, a, 2 * MODW_A);
+    memcpy(host.data() + 3 * MODW_A + site * MODW_B, b, 2 * MODW_B);
+  }
+  DevModw m;
+  HIPC(hipMalloc((void **)&m.w, 2 * host.size()));
+  HIPC(hipMemcpy(m.w, host.data(), 2 * host.size(), hipMemcpyHostToDevice));
+  c->modws[fd] = m;
+  *out = m.w;
+  return HXA_OK;
+}
+}  // namespace
+
+extern "C" int hxa_anima_modulation(remote_handle64 h, const int *wfds, int count, const float *emb, const float *lora,
+                                    float *mod) {
+  g_err[0] = 0;
+  Ctx *c = ctx_of(h);
+  if (!c || !wfds || count <= 0 || !emb || !lora || !mod) return fail(HXA_E_ARG, "modulation: bad arguments");
+  hipStream_t st = c->st;
+  const int D = ANIMA_D;
+  TRY(ensure((void **)&c->emb_dev, &c->emb_dev_bytes, 4 * (D + 6144)));
+  TRY(ensure((void **)&c->h1_dev, &c->h1_dev_bytes, 4 * 3 * 256));
+  TRY(ensure((void **)&c->mod_dev, &c->mod_dev_bytes, (size_t)count * 9 * D * 4));
+  float *emb_d = c->emb_dev, *lora_d = c->emb_dev + D;
+  HIPC(hipMemcpyAsync(emb_d, emb, 4 * D, hipMemcpyHostToDevice, st));
+  HIPC(hipMemcpyAsync(lora_d, lora, 4 * 6144, hipMemcpyHostToDevice, st));
+  for (int k = 0; k < count; k++) {
+    const hxa_h *w = nullptr;
+    TRY(modw_of(c, wfds[k], &w));
+    // h1 = A silu(emb) for the three sites at once (megarun.cpp:160, :165)
+    TRY(hxa_linear_f32_launch(emb_d, D, 1, D, w, 3 * 256, c->h1_dev, 3 * 256, 1, nullptr, 0, 0, st));
+    // mod rows 3 site .. 3 site + 2 = lora + B_site h1_site (megarun.cpp:166-167)
+    for (int site = 0; site < 3; site++)
+      TRY(hxa_linear_f32_launch(c->h1_dev + 256 * site, 256, 1, 256, w + 3 * MODW_A + site * MODW_B, 6144,
+                                c->mod_dev + ((size_t)k * 9 + 3 * site) * D, 6144, 0, lora_d, 0, 0, st));
+  }
+  HIPC(hipMemcpyAsync(mod, c->mod_dev, (size_t)count * 9 * D * 4, hipMemcpyDeviceToHost, st));
+  HIPC(hipStreamSynchronize(st));
+  return HXA_OK;
+}
 
 extern "C" int mega_block(remote_handle64 h, const int *meta, int nmeta, int wfd, int bfd, const uint8_t *mod, int modlen,
                           int *times, int ntimes, int *rc) {

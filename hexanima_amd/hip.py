@@ -48,6 +48,7 @@ _SIGS = {
     "mega_moss_block": (I, [U64, P, I, I, I, P, I, P, I, P]),
     "hxa_register": (I, [U64, I, P, SZ, I]),
     "hxa_unregister": (I, [U64, I]),
+    "hxa_anima_modulation": (I, [U64, P, I, P, P, P]),
     "hxa_last_error": (C.c_char_p, []),
     "hxa_version": (C.c_char_p, []),
     "hxa_init": (I, [I]),

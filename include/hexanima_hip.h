@@ -67,6 +67,13 @@ int mega_moss_block(remote_handle64 h, const int *meta, int nmeta, int wfd, int 
                                     matrices): converted to a kind-2 pack */
 int hxa_register(remote_handle64 h, int fd, void *host_ptr, size_t bytes, int kind);
 int hxa_unregister(remote_handle64 h, int fd);
+/* replaces megarun's modulation thread (megarun.cpp:156-171) with GPU GEMVs: for the Anima weight buffers registered
+ * under wfds[0..count), s = silu(emb) and per site (self-attn, cross-attn, MLP) mod[k][3 site .. 3 site + 2] =
+ * lora + B_site (A_site s), from the modulation weights of each blkNN.bin (A [256][2048], B [6144][256] fp16 per site
+ * at W_MODW, or WQ_MODW for a q8 file, told apart by the file size as megarun.cpp:97 does; blk_wlayout.h:14-20),
+ * uploaded on first use and then resident. emb [2048], lora [6144] fp32 host; mod [count][9][2048] fp32 host, ready
+ * to pass to mega_block block by block. */
+int hxa_anima_modulation(remote_handle64 h, const int *wfds, int count, const float *emb, const float *lora, float *mod);
 
 /* ============================================================================================================
  * 2. Device runtime

@@ -155,3 +155,18 @@ def assert_gemm_close(got16, ref32, A16, W16, ident=0.98):
     assert np.all(err <= tol), f"max excess {np.max(err - tol):.3e}"
     same = np.mean(np.asarray(got16, np.float16).view(np.uint16) == r16.view(np.uint16))
     assert same >= ident, f"only {same:.4f} bit-identical"
+
+
+def oracle_anima_modulation(modw16, emb, lora):
+    """megarun.cpp:156-171: s = silu(emb); per site: h1 = A_site s, mod rows 3 site .. 3 site + 2 = lora + B_site h1
+    (fp32 activations, fp16 weights). modw16: the W_MODW section of a blkNN.bin as uint16, per site A [256][2048]
+    then B [6144][256] (export_all.py:59-61). Returns [9][2048] fp32."""
+    out = []
+    s = silu(np.asarray(emb, np.float32))[None, :]
+    step = 256 * 2048 + 6144 * 256
+    for site in range(3):
+        a = modw16[site * step:site * step + 256 * 2048].reshape(256, 2048)
+        b = modw16[site * step + 256 * 2048:(site + 1) * step].reshape(6144, 256)
+        h1 = hxo.linear_f32(s, a)
+        out.append(np.asarray(lora, np.float32) + hxo.linear_f32(h1, b)[0])
+    return np.concatenate(out).reshape(9, 2048).astype(np.float32)

@@ -93,3 +93,19 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(h, "_lib", None)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         h.lib()
+
+
+def test_host_programs_reject_bad_arguments_before_any_device_call(hip, tmp_path):
+    """hxa_run (megarun protocol) and hxa_blk (blk_main harness) are built beside the library and fail cleanly on
+    missing inputs; the GPU runs of both are in tests/test_gpu_runners.py."""
+    d = os.path.dirname(hip.LIB_PATH)
+    run, blk = os.path.join(d, "hxa_run"), os.path.join(d, "hxa_blk")
+    r = subprocess.run([run], capture_output=True, text=True)
+    assert r.returncode == 1 and "usage" in r.stderr
+    r = subprocess.run([run, str(tmp_path), "0", "2"], capture_output=True, text=True)
+    assert r.returncode == 1 and "cannot load" in r.stderr
+    (tmp_path / "blk00.bin").write_bytes(b"\0" * 4096)
+    r = subprocess.run([run, str(tmp_path), "0", "1"], capture_output=True, text=True)
+    assert r.returncode == 1 and "not a block file" in r.stderr
+    r = subprocess.run([blk, str(tmp_path)], capture_output=True, text=True)
+    assert r.returncode == 1 and "missing" in r.stdout

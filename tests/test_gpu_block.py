@@ -265,8 +265,12 @@ W_OFFS = {"WSQ": 0, "WSK": 8388608, "WSV": 16777216, "WSO": 25165824, "WCQ": 335
           "WCV": 46137344, "WCO": 50331648, "WM1": 58720256, "WM2": 92274688, "GAIN": 125829120}  # blk_wlayout.h
 
 
-def _blk_file(rng, q8):
-    """A synthetic blkNN.bin (export_all.py:29-36): 10 matrices as fp16 crouton tiles or q8 records, gains."""
+W_MODW, W_TOTAL = 125833216, 138416128  # blk_wlayout.h:14-15
+
+
+def _blk_file(rng, q8, modw=False):
+    """A synthetic blkNN.bin (export_all.py:29-36): 10 matrices as fp16 crouton tiles or q8 records, gains and, with
+    modw, random adaLN modulation weights (per site A [256][2048], B [6144][256] fp16; zeros otherwise)."""
     D, F, DC = 2048, 8192, 1024
     mats = {"WSQ": (D, D), "WSK": (D, D), "WSV": (D, D), "WSO": (D, D), "WCQ": (D, D), "WCK": (D, DC), "WCV": (D, DC),
             "WCO": (D, D), "WM1": (F, D), "WM2": (D, F)}
@@ -287,6 +291,10 @@ def _blk_file(rng, q8):
     gain = np.concatenate([np.full(128, 1 / np.sqrt(128)), np.ones(128), np.full(128, 1 / np.sqrt(128)), np.ones(128)]).astype(np.float32)
     goff = W_OFFS["GAIN"] if not q8 else W_OFFS["GAIN"] // 2048 * 1152
     buf[goff:goff + 2048] = gain.view(np.uint8)
+    if modw:
+        mw = f16(rng.standard_normal((W_TOTAL - W_MODW) // 2, dtype=np.float32) * 0.02).view(np.uint16)
+        moff = W_MODW if not q8 else 125829120 // 2048 * 1152 + 4096
+        buf[moff:moff + mw.nbytes] = mw.view(np.uint8)
     ow = {"wq": w["WSQ"], "wk": w["WSK"], "wv": w["WSV"], "wo": w["WSO"], "wcq": w["WCQ"], "wck": w["WCK"],
           "wcv": w["WCV"], "wco": w["WCO"], "w1": w["WM1"], "w2": w["WM2"], "gain": gain}
     return buf, ow
