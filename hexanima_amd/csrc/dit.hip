@@ -6,6 +6,12 @@
 //   final adaLN + linear + unpatchify (animad.cpp:474-492) fused with the Euler update x += (s' - s) v
 // A step is captured once into a HIP graph and replayed; sigma values are read from device memory so one graph
 // serves every step.
+// Two forms of the glue around the blocks (hxa_dit_cfg.form): 0, the benchmark configurations' (a 256-wide sinusoid,
+// Linear . SiLU . Linear to dense per-block modulation, LN final layer); 1, the reference's own -- Anima: the
+// RMSNorm'd 2048-wide sinusoid and its LoRA MLP (animad.cpp:424-431), low-rank per-block modulation
+// (megarun.cpp:156-171) and final adaLN (animad.cpp:475-479); MOSS: the time MLP with biases, shared block and head
+// modulation (mossrun.cpp:255-264), the rapid-moss sampler's latent mix and video embedding, the RMS head and
+// x0 = z - v (mossrun.cpp:307-334), BN denorm + unpatchify of the result (mossrun.cpp:339-343).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -37,6 +43,16 @@ struct Dit {
   void *ws = nullptr;
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
+  // form 1 (the reference's glue): fp16 matrices inside `glue`, fp32 vectors in `vec`, per-step vectors below
+  int form = 0;
+  hxa_h *Wl2 = nullptr, *F1 = nullptr, *F2 = nullptr, *tnorm = nullptr, *T2 = nullptr, *Wh = nullptr;
+  float *vec = nullptr;  // MOSS: b_video [D] | b_t0 [D] | b_t2 [D] | b_smod [6D] | b_hmod [2D] | final_norm [D] | Q [4C][4C] | bn mean, var [4C]
+  long vec_elems = 0;
+  float *bve = nullptr, *b0 = nullptr, *b2 = nullptr, *bm = nullptr, *bh = nullptr, *nfin = nullptr, *Q = nullptr;
+  float *bnm = nullptr, *bnv = nullptr;
+  float *emb = nullptr, *a1 = nullptr, *lora = nullptr, *h1 = nullptr;  // t-embedding work vectors
+  float *zrows = nullptr, *x0rows = nullptr;  // rapid-moss state: noise z and clean estimate x0, token rows [B*T][4C]
+  long modw_block = 0;                        // elements of one block's modulation weights
   float *sig_host = nullptr;   // pinned source of the per-step sigma upload
   hipEvent_t sig_ev = nullptr;  // recorded after that upload: sig_host is rewritten only once it has completed
   bool sig_pending = false;
@@ -154,10 +170,43 @@ int init_pack(Dit &d, void *pack, uint64_t seed, float *tmp32) {
 
 enum { MODE_EULER = 0, MODE_VELOCITY = 1 };
 
+// form 1, Anima (animad.cpp:424-431, megarun.cpp:156-171, animad.cpp:475-479): tp = sinusoid_D(t), emb = RMSNorm(tp)
+// * w, lora = L2 silu(L1 tp); per block and site mod = lora + B (A silu(emb)); final (shift, scale) =
+// F2 (F1 silu(emb)) + lora[0 : 2D]
+int record_prelude_anima_ref(Dit &d) {
+  const int D = d.bd.D, nb = d.cfg.nblocks;
+  hipStream_t st = d.st;
+  DTRY(hxa_sinusoid_launch(d.sig, 1, D, d.sinus, st));
+  DTRY(hxa_rmsvec_launch(d.sinus, D, d.tnorm, 1e-6f, d.emb, st));
+  DTRY(hxa_linear_f32_launch(d.sinus, D, 1, D, d.L1, D, d.a1, D, 0, nullptr, 0, 0, st));
+  DTRY(hxa_linear_f32_launch(d.a1, D, 1, D, d.Wl2, 3 * D, d.lora, 3 * D, 1, nullptr, 0, 0, st));
+  // all blocks' A (s = silu(emb)) in one launch, then all blocks' and sites' B with their own h1 in one launch
+  DTRY(hxa_linear_f32_launch(d.emb, D, 1, D, d.modw_all, nb * 768, d.h1, nb * 768, 1, nullptr, 0, 0, st));
+  DTRY(hxa_grouped_gemv_launch(d.h1, 256, d.modw_all + (long)nb * 768 * D, nb * 3, 3 * D, 256, d.lora, d.mods, 3L * D, st));
+  DTRY(hxa_linear_f32_launch(d.emb, D, 1, D, d.F1, 256, d.h1 + (long)nb * 768, 256, 1, nullptr, 0, 0, st));
+  DTRY(hxa_linear_f32_launch(d.h1 + (long)nb * 768, 256, 1, 256, d.F2, 2 * D, d.fmod, 2 * D, 0, d.lora, 0, 0, st));
+  return HXA_OK;
+}
+// form 1, MOSS (mossrun.cpp:255-264): e = sinusoid_256(code), a = T0 e + b0, b = T2 silu(a) + b2; shared block
+// modulation Wm b + bm [6D], head modulation Wh b + bh [2D]
+int record_prelude_moss_ref(Dit &d) {
+  const int D = d.bd.D, temb = d.cfg.temb;
+  hipStream_t st = d.st;
+  DTRY(hxa_sinusoid_launch(d.sig, 1, temb, d.sinus, st));
+  DTRY(hxa_linear_f32_launch(d.sinus, temb, 1, temb, d.L1, D, d.a1, D, 0, d.b0, 0, 0, st));
+  DTRY(hxa_linear_f32_launch(d.a1, D, 1, D, d.T2, D, d.emb, D, 1, d.b2, 0, 0, st));
+  DTRY(hxa_linear_f32_launch(d.emb, D, 1, D, d.modw_all, 6 * D, d.mods, 6 * D, 0, d.bm, 0, 0, st));
+  DTRY(hxa_linear_f32_launch(d.emb, D, 1, D, d.Wh, 2 * D, d.fmod, 2 * D, 0, d.bh, 0, 0, st));
+  return HXA_OK;
+}
+
 int record_step(Dit &d, int mode) {
   const hxa_block_dims &b = d.bd;
   const int B = b.batch, D = b.D, C4 = 4 * d.cfg.lat_c, temb = d.cfg.temb, nb = d.cfg.nblocks;
   hipStream_t st = d.st;
+  const bool moss_ref = d.form == 1 && b.kind == 1;
+  if (d.form == 1) DTRY(b.kind == 0 ? record_prelude_anima_ref(d) : record_prelude_moss_ref(d));
+  if (d.form == 0) {
   // timestep embedding and modulation
   DTRY(hxa_sinusoid_launch(d.sig, 1, temb, d.sinus, st));
   DTRY(hxa_linear_f32_launch(d.sinus, temb, 1, temb, d.L1, D, d.cvec, D, 0, nullptr, 0, 0, st));
@@ -168,11 +217,16 @@ int record_step(Dit &d, int mode) {
   else
     DTRY(hxa_modgemv_launch(d.cvec, D, d.modw_all, 6L * D, d.mods, 6 * D, 0, 6 * D, 0, 1, st));
   DTRY(hxa_modgemv_launch(d.cvec, D, d.Lf, 2L * D, d.fmod, 2 * D, 0, 2 * D, 0, 1, st));
-  // patch embed (+ MOSS text tokens)
-  DTRY(hxa_patchify_launch(d.lat, B, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w, d.tok, st));
+  }
+  // patch embed (rapid-moss: latent mix + video embedding of the token rows) (+ MOSS text tokens)
+  if (moss_ref)
+    DTRY(hxa_moss_embed_launch(d.zrows, d.x0rows, d.Q, d.Wemb, d.bve, d.x, B, d.Timg, d.Ttot, D, C4, st));
+  else
+    DTRY(hxa_patchify_launch(d.lat, B, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w, d.tok, st));
   for (int i = 0; i < B; i++) {
-    DTRY(hxa_linear_f32_launch(d.tok + (long)i * d.Timg * C4, C4, d.Timg, C4, d.Wemb, D, d.x + (long)i * d.Ttot * D, D, 0,
-                               nullptr, 0, 0, st));
+    if (!moss_ref)
+      DTRY(hxa_linear_f32_launch(d.tok + (long)i * d.Timg * C4, C4, d.Timg, C4, d.Wemb, D, d.x + (long)i * d.Ttot * D, D,
+                                 0, nullptr, 0, 0, st));
     if (b.kind == 1) {
       float *xt = d.x + ((long)i * d.Ttot + d.Timg) * D;
       DTRY(hxa_fill_const_launch(xt, 0, (size_t)(d.Ttot - d.Timg) * D, 0.0f, st));
@@ -203,9 +257,13 @@ int record_step(Dit &d, int mode) {
     const hxa_h *t1 = (const hxa_h *)hxa_block_ws_buf(&d.bd, d.ws, 5, &ld), *t2 = (const hxa_h *)hxa_block_ws_buf(&d.bd, d.ws, 9, &ld);
     DTRY(hxa_resadd2_launch(d.x, D, t1, t2, ld, B * d.Ttot, D, mlp_gate(nb - 1), st));
   }
-  // final layer (+ Euler update)
-  DTRY(hxa_final_launch(d.x, B, d.Timg, d.Ttot, D, d.fmod, d.fmod + D, d.Wfin, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w,
-                        mode == MODE_EULER ? d.lat : d.vel, mode == MODE_EULER ? d.sig + 2 : nullptr, st));
+  // final layer (+ Euler update); rapid-moss: RMS head and x0 = z - v
+  if (moss_ref)
+    DTRY(hxa_final_launch(d.x, B, d.Timg, d.Ttot, D, d.fmod, d.fmod + D, d.Wfin, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w,
+                          d.vel, nullptr, st, d.nfin, d.x0rows, d.zrows));
+  else
+    DTRY(hxa_final_launch(d.x, B, d.Timg, d.Ttot, D, d.fmod, d.fmod + D, d.Wfin, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w,
+                          mode == MODE_EULER ? d.lat : d.vel, mode == MODE_EULER ? d.sig + 2 : nullptr, st));
   return HXA_OK;
 }
 
@@ -243,6 +301,16 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
     delete dp;
     return dfail(HXA_E_ARG, "dit: latent / embedding shape");
   }
+  d.form = cfg->form;
+  if (d.form != 0 && d.form != 1) {
+    delete dp;
+    return dfail(HXA_E_MODE, "dit: form");
+  }
+  // the reference's Anima t-embedding is a D-wide sinusoid (animad.cpp:425), the MOSS one 256-wide (mossrun.cpp:256)
+  if (d.form == 1 && (b.kind == 0 ? cfg->temb != D : cfg->temb != 256)) {
+    delete dp;
+    return dfail(HXA_E_ARG, "dit: the reference form's sinusoid width");
+  }
   d.Timg = (cfg->lat_h / 2) * (cfg->lat_w / 2);
   if (b.kind == 0) {
     b.T = d.Ttot = d.Timg;
@@ -279,11 +347,36 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   d.pack_bytes = hxa_pack_layout(b.kind, D, b.F, b.DC, b.fmt_attn, b.fmt_mlp, nullptr, 0);
   d.packs.assign(cfg->nblocks, nullptr);
   for (auto &p : d.packs) M(&p, d.pack_bytes);
+  // modulation weights: per block [6D][D] (config form), per block A [3 x 256][D] + B [3][3D][256] (reference form;
+  // stored all blocks' A first, then all B), or one shared [6D][D] (MOSS)
+  const bool anima_ref = d.form == 1 && b.kind == 0;
   d.modw.assign(b.kind == 0 ? cfg->nblocks : 1, nullptr);
-  M((void **)&d.modw_all, 2L * 6 * D * D * (long)d.modw.size());
-  for (size_t k = 0; k < d.modw.size() && d.modw_all; k++) d.modw[k] = d.modw_all + (long)k * 6 * D * D;
-  d.glue_elems = (long)D * C4 + (long)D * cfg->temb + 2L * D * D + (long)C4 * D + (b.kind == 1 ? (long)D * cfg->ntxt_in : 0);
+  d.modw_block = anima_ref ? 768L * D + 3L * 3 * D * 256 : 6L * D * D;
+  M((void **)&d.modw_all, 2L * d.modw_block * (long)d.modw.size());
+  for (size_t k = 0; k < d.modw.size() && d.modw_all; k++) d.modw[k] = d.modw_all + (anima_ref ? 768L * D : d.modw_block) * (long)k;
+  // fp16 glue. config form: x_embed [D][4C] | t_embed [D][temb] | final_mod [2D][D] | final_lin [4C][D] | MOSS
+  // text_proj [D][ntxt_in]. Reference form, Anima: x_embed | t_l1 [D][D] | t_l2 [3D][D] | f1 [256][D] | f2 [2D][256]
+  // | final_lin | t_norm [D]; MOSS: video_embed [D][4C] | t0 [D][256] | t2 [D][D] | head_mod [2D][D] | final_lin |
+  // text_proj
+  if (d.form == 0)
+    d.glue_elems = (long)D * C4 + (long)D * cfg->temb + 2L * D * D + (long)C4 * D + (b.kind == 1 ? (long)D * cfg->ntxt_in : 0);
+  else if (b.kind == 0)
+    d.glue_elems = (long)D * C4 + (long)D * D + 3L * D * D + 256L * D + 2L * D * 256 + (long)C4 * D + D;
+  else
+    d.glue_elems = (long)D * C4 + (long)D * 256 + (long)D * D + 2L * D * D + (long)C4 * D + (long)D * cfg->ntxt_in;
   M((void **)&d.glue, 2 * d.glue_elems);
+  if (d.form == 1) {
+    d.vec_elems = b.kind == 0 ? 0 : 3L * D + 6L * D + 2L * D + D + (long)C4 * C4 + 2L * C4;
+    if (d.vec_elems) M((void **)&d.vec, 4 * d.vec_elems);
+    M((void **)&d.emb, 4L * D);
+    M((void **)&d.a1, 4L * D);
+    M((void **)&d.lora, 4L * 3 * D);
+    M((void **)&d.h1, 4L * ((long)cfg->nblocks * 768 + 256));
+    if (b.kind == 1) {
+      M((void **)&d.zrows, 4L * B * d.Timg * C4);
+      M((void **)&d.x0rows, 4L * B * d.Timg * C4);
+    }
+  }
   const long latn = (long)B * cfg->lat_c * cfg->lat_h * cfg->lat_w;
   M((void **)&d.lat, 4 * latn);
   M((void **)&d.vel, 4 * latn);
@@ -313,14 +406,45 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   float *tmp = nullptr;
   if (b.fmt_attn != HXA_W_F16 || b.fmt_mlp != HXA_W_F16) M((void **)&tmp, 4 * maxmat);
   for (int k = 0; k < cfg->nblocks && rc == HXA_OK; k++) rc = init_pack(d, d.packs[k], seed * 1000003ull + k, tmp);
-  for (size_t k = 0; k < d.modw.size() && rc == HXA_OK; k++)
-    rc = hxa_fill_normal_launch(d.modw[k], 1, 6L * D * D, seed * 7919ull + 100000 + k, 0.0f, 0.02f, d.st);
+  if (rc == HXA_OK)
+    rc = hxa_fill_normal_launch(d.modw_all, 1, d.modw_block * (long)d.modw.size(), seed * 7919ull + 100000, 0.0f, 0.02f, d.st);
   if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.glue, 1, d.glue_elems, seed * 7919ull + 99999, 0.0f, 0.02f, d.st);
   d.Wemb = d.glue;
   d.L1 = d.Wemb + (long)D * C4;
-  d.Lf = d.L1 + (long)D * cfg->temb;
-  d.Wfin = d.Lf + 2L * D * D;
-  d.Wtxt = b.kind == 1 ? d.Wfin + (long)C4 * D : nullptr;
+  if (d.form == 0) {
+    d.Lf = d.L1 + (long)D * cfg->temb;
+    d.Wfin = d.Lf + 2L * D * D;
+    d.Wtxt = b.kind == 1 ? d.Wfin + (long)C4 * D : nullptr;
+  } else if (b.kind == 0) {
+    d.Wl2 = d.L1 + (long)D * D;
+    d.F1 = d.Wl2 + 3L * D * D;
+    d.F2 = d.F1 + 256L * D;
+    d.Wfin = d.F2 + 2L * D * 256;
+    d.tnorm = d.Wfin + (long)C4 * D;  // RMSNorm weight of the t-embedding, fp16 like the reference's tensors
+    if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.tnorm, 1, D, seed * 7919ull + 99998, 1.0f, 0.1f, d.st);
+  } else {
+    d.T2 = d.L1 + 256L * D;
+    d.Wh = d.T2 + (long)D * D;
+    d.Wfin = d.Wh + 2L * D * D;
+    d.Wtxt = d.Wfin + (long)C4 * D;
+    d.bve = d.vec;
+    d.b0 = d.bve + D;
+    d.b2 = d.b0 + D;
+    d.bm = d.b2 + D;
+    d.bh = d.bm + 6L * D;
+    d.nfin = d.bh + 2L * D;
+    d.Q = d.nfin + D;
+    d.bnm = d.Q + (long)C4 * C4;
+    d.bnv = d.bnm + C4;
+    // biases and the latent mix N(0, 0.02); the head's RMSNorm weight and the BN variance around 1, the BN mean
+    // around 0 (N(0, 0.1))
+    const uint64_t vs = seed * 7919ull + 99997;
+    if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.bve, 0, 11L * D, vs, 0.0f, 0.02f, d.st);  // bve, b0, b2, bm, bh
+    if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.Q, 0, (long)C4 * C4, vs + 4, 0.0f, 0.02f, d.st);
+    if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.nfin, 0, D, vs + 1, 1.0f, 0.1f, d.st);
+    if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.bnm, 0, C4, vs + 2, 0.0f, 0.1f, d.st);
+    if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.bnv, 0, C4, vs + 3, 1.0f, 0.1f, d.st);
+  }
   if (rc == HXA_OK) rc = hxa_fill_const_launch(d.ones, 0, D, 1.0f, d.st);
   if (rc == HXA_OK && b.kind == 0) {  // site-1 rows of every block: shift 0, scale 0, gate 1
     for (int k = 0; k < cfg->nblocks && rc == HXA_OK; k++) {
@@ -357,7 +481,8 @@ extern "C" int hxa_dit_destroy(void *p) {
   if (d->graph) (void)hipGraphDestroy(d->graph);
   for (void *q : d->packs) if (q) (void)hipFree(q);
   if (d->modw_all) (void)hipFree(d->modw_all);
-  void *bufs[] = {d->glue, d->lat, d->vel, d->tok, d->x, d->sinus, d->cvec, d->mods, d->fmod, d->sig, d->cosT, d->sinT, d->ones, d->ctx16, d->ws};
+  void *bufs[] = {d->glue, d->lat, d->vel, d->tok, d->x, d->sinus, d->cvec, d->mods, d->fmod, d->sig, d->cosT, d->sinT,
+                  d->ones, d->ctx16, d->ws, d->vec, d->emb, d->a1, d->lora, d->h1, d->zrows, d->x0rows};
   for (void *q : bufs) if (q) (void)hipFree(q);
   if (d->sig_ev) (void)hipEventDestroy(d->sig_ev);
   if (d->sig_host) (void)hipHostFree(d->sig_host);
@@ -371,6 +496,10 @@ extern "C" int hxa_dit_set_inputs(void *p, const float *lat, const float *ctx) {
   const hxa_block_dims &b = d.bd;
   const long latn = (long)b.batch * d.cfg.lat_c * d.cfg.lat_h * d.cfg.lat_w;
   if (lat) DHIP(hipMemcpyAsync(d.lat, lat, 4 * latn, hipMemcpyHostToDevice, d.st));
+  if (lat && d.zrows) {  // rapid-moss: the latent is the noise z (token rows), the clean estimate starts at 0
+    DTRY(hxa_patchify_launch(d.lat, b.batch, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w, d.zrows, d.st));
+    DTRY(hxa_fill_const_launch(d.x0rows, 0, (size_t)latn, 0.0f, d.st));
+  }
   if (ctx) {
     const long n = b.kind == 0 ? (long)b.batch * b.C * b.DC : (long)b.batch * d.ntxt * d.cfg.ntxt_in;
     std::vector<uint16_t> h(n);
@@ -384,14 +513,19 @@ extern "C" int hxa_dit_set_inputs(void *p, const float *lat, const float *ctx) {
 extern "C" int hxa_dit_get_latent(void *p, float *lat) {
   Dit &d = *(Dit *)p;
   const long latn = (long)d.bd.batch * d.cfg.lat_c * d.cfg.lat_h * d.cfg.lat_w;
+  if (d.x0rows) {  // rapid-moss: the BN-denormalised, unpatchified clean estimate (mossrun.cpp:339-343)
+    DTRY(hxa_bn_unpatchify_launch(d.x0rows, d.bnm, d.bnv, d.bd.batch, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w, d.vel, d.st));
+    DHIP(hipMemcpyAsync(lat, d.vel, 4 * latn, hipMemcpyDeviceToHost, d.st));
+    DHIP(hipStreamSynchronize(d.st));
+    return HXA_OK;
+  }
   DHIP(hipMemcpyAsync(lat, d.lat, 4 * latn, hipMemcpyDeviceToHost, d.st));
   DHIP(hipStreamSynchronize(d.st));
   return HXA_OK;
 }
 
-extern "C" int hxa_dit_step(void *p, float sigma, float sigma_next, int use_graph) {
-  Dit &d = *(Dit *)p;
-  DTRY(set_sigma(d, sigma, sigma_next));
+namespace {
+int run_step(Dit &d, int use_graph) {
   if (!use_graph) return record_step(d, MODE_EULER);
   if (!d.exec) {
     DHIP(hipStreamBeginCapture(d.st, hipStreamCaptureModeRelaxed));
@@ -409,9 +543,25 @@ extern "C" int hxa_dit_step(void *p, float sigma, float sigma_next, int use_grap
   DHIP(hipGraphLaunch(d.exec, d.st));
   return HXA_OK;
 }
+}  // namespace
+
+extern "C" int hxa_dit_step(void *p, float sigma, float sigma_next, int use_graph) {
+  Dit &d = *(Dit *)p;
+  if (d.x0rows) return dfail(HXA_E_MODE, "dit: the rapid-moss form steps with hxa_dit_moss_step");
+  DTRY(set_sigma(d, sigma, sigma_next));
+  return run_step(d, use_graph);
+}
+
+extern "C" int hxa_dit_moss_step(void *p, float code, int use_graph) {
+  Dit &d = *(Dit *)p;
+  if (!d.x0rows) return dfail(HXA_E_MODE, "dit: hxa_dit_moss_step needs the MOSS reference form");
+  DTRY(set_sigma(d, code, code));
+  return run_step(d, use_graph);
+}
 
 extern "C" int hxa_dit_velocity(void *p, float sigma, float *v) {
   Dit &d = *(Dit *)p;
+  if (d.x0rows) return dfail(HXA_E_MODE, "dit: the rapid-moss form has no velocity output");
   DTRY(set_sigma(d, sigma, sigma));
   DTRY(record_step(d, MODE_VELOCITY));
   const long latn = (long)d.bd.batch * d.cfg.lat_c * d.cfg.lat_h * d.cfg.lat_w;
@@ -422,25 +572,37 @@ extern "C" int hxa_dit_velocity(void *p, float sigma, float *v) {
 
 extern "C" long hxa_dit_export(void *p, int which, void *host, size_t bytes) {
   Dit &d = *(Dit *)p;
-  const int nb = d.cfg.nblocks;
-  const void *src = nullptr;
-  long n = 0;
+  const int nb = d.cfg.nblocks, D = d.bd.D;
+  struct Part {
+    const void *src;
+    long n;
+  } parts[2] = {{nullptr, 0}, {nullptr, 0}};
   if (which >= 0 && which < nb) {
-    src = d.packs[which];
-    n = d.pack_bytes;
+    parts[0] = {d.packs[which], d.pack_bytes};
   } else if (which >= nb && which < nb + (int)d.modw.size()) {
-    src = d.modw[which - nb];
-    n = 2L * 6 * d.bd.D * d.bd.D;
+    const int k = which - nb;
+    if (d.form == 1 && d.bd.kind == 0) {  // this block's A rows, then its B
+      parts[0] = {d.modw_all + 768L * D * k, 2 * 768L * D};
+      parts[1] = {d.modw_all + 768L * D * nb + 3L * 3 * D * 256 * k, 2 * 3L * 3 * D * 256};
+    } else {
+      parts[0] = {d.modw[k], 2 * d.modw_block};
+    }
   } else if (which == 2 * nb) {
-    src = d.glue;
-    n = 2 * d.glue_elems;
+    parts[0] = {d.glue, 2 * d.glue_elems};
+  } else if (which == 2 * nb + 1 && d.vec) {
+    parts[0] = {d.vec, 4 * d.vec_elems};
   } else {
     return dfail(HXA_E_ARG, "dit export index");
   }
+  const long n = parts[0].n + parts[1].n;
   if (!host) return n;
   if ((long)bytes < n) return dfail(HXA_E_ARG, "dit export buffer too small");
-  if (hipStreamSynchronize(d.st) != hipSuccess || hipMemcpy(host, src, n, hipMemcpyDeviceToHost) != hipSuccess)
-    return dfail(HXA_E_HIP, "dit export copy");
+  if (hipStreamSynchronize(d.st) != hipSuccess) return dfail(HXA_E_HIP, "dit export sync");
+  char *out = (char *)host;
+  for (const Part &q : parts) {
+    if (q.n && hipMemcpy(out, q.src, q.n, hipMemcpyDeviceToHost) != hipSuccess) return dfail(HXA_E_HIP, "dit export copy");
+    out += q.n;
+  }
   return n;
 }
 

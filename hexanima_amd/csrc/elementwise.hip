@@ -394,6 +394,8 @@ __global__ void sinusoid_kernel(const float *t, int n, int dim, float *out) {
 
 // final layer (animad.cpp:474-492): per token LN (eps 1e-6, two-pass) * (1 + scale) + shift, linear D -> 4C,
 // unpatchify (ph, pw, c) into lat; when dt != 0 the Euler update lat += dt * v is applied instead of storing v.
+// With normw the norm is the MOSS head's RMSNorm * normw (mossrun.cpp:331-332), and with x0rows the 4C outputs v of
+// token t go to x0rows[t][o] = zrows[t][o] - v, the rapid-moss estimate x0 = z - v (mossrun.cpp:333-334).
 // FT tokens per workgroup: each wave normalises FT/4 tokens into LDS, then thread (output o, part) accumulates its
 // quarter-interleaved share of the D products for all FT tokens (the weights are read once per workgroup), and the
 // `per` parts of an output (adjacent lanes) are summed with DPP.
@@ -401,7 +403,8 @@ constexpr int FT = 8;
 __global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ x, int T, int xrows, int D,
                                                     const float *__restrict__ shift, const float *__restrict__ scale,
                                                     const hxa_h *__restrict__ Wf, int Cc, int H, int W, float *lat,
-                                                    const float *__restrict__ dtp, int ntok) {
+                                                    const float *__restrict__ dtp, int ntok, const float *__restrict__ normw,
+                                                    float *__restrict__ x0rows, const float *__restrict__ zrows) {
   extern __shared__ float xn[];  // [FT][D]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tok0 = blockIdx.x * FT;
@@ -420,10 +423,12 @@ __global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ x,
     for (int i = 0; i < 16; i++)
       if (i < nv) v[i] = xr[lane + 64 * i];
     float s = 0.0f;
+    if (normw == nullptr) {
 #pragma unroll
-    for (int i = 0; i < 16; i++)
-      if (i < nv) s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
-    const float mu = wave_sum(s) / (float)D;
+      for (int i = 0; i < 16; i++)
+        if (i < nv) s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+    }
+    const float mu = normw == nullptr ? wave_sum(s) / (float)D : 0.0f;  // RMS: no centring
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; i++)
@@ -440,9 +445,11 @@ __global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ x,
       if (i < nv) {
         const int c = (lane + 64 * i) * 4;
         const float4_t sc = *(const float4_t *)(scale + c), sh = *(const float4_t *)(shift + c);
+        float4_t nw = {1.0f, 1.0f, 1.0f, 1.0f};
+        if (normw != nullptr) nw = *(const float4_t *)(normw + c);
         float4_t o;
 #pragma unroll
-        for (int e = 0; e < 4; e++) o[e] = (v[i][e] - mu) * rs * (1.0f + sc[e]) + sh[e];
+        for (int e = 0; e < 4; e++) o[e] = (v[i][e] - mu) * rs * nw[e] * (1.0f + sc[e]) + sh[e];
         *(float4_t *)(dst + c) = o;
       }
   }
@@ -475,7 +482,9 @@ __global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ x,
     if (per >= 2) v += dpp_f<0xB1>(v);  // lanes i^1
     if (per >= 4) v += dpp_f<0x4E>(v);  // lanes i^2
     const int tok = tok0 + t;
-    if (part == 0 && tok < ntok) {
+    if (part == 0 && tok < ntok && x0rows != nullptr) {
+      x0rows[(long)tok * NO + o] = zrows[(long)tok * NO + o] - v;
+    } else if (part == 0 && tok < ntok) {
       const int b = tok / T, tk = tok % T, gy = tk / gw, gx = tk % gw;
       const int ab = o / Cc, c = o % Cc, a = ab >> 1, bb = ab & 1;
       float *dst = lat + (((long)b * Cc + c) * H + gy * 2 + a) * W + gx * 2 + bb;
@@ -672,7 +681,9 @@ int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, 
 
 
 int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale,
-                     const hxa_h *Wf, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st) {
+                     const hxa_h *Wf, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st,
+                     const float *normw, float *x0rows, const float *zrows) {
+  if ((x0rows == nullptr) != (zrows == nullptr) || (normw && (uintptr_t)normw % 16)) return HXA_E_ARG;
   const int NO = 4 * Cc;
   if (NO > 256 || 256 % NO || 256 / NO > 4 || (H / 2) * (W / 2) != T || xrows < T || D % 256 || D > 4096)
     return HXA_E_ARG;
@@ -686,11 +697,117 @@ int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float
   }
   const int ntok = B * T;
   hipLaunchKernelGGL(final_kernel, dim3((ntok + FT - 1) / FT), dim3(256), lds, st, x, T, xrows, D, shift, scale, Wf, Cc,
-                     H, W, lat, dtp, ntok);
+                     H, W, lat, dtp, ntok, normw, x0rows, zrows);
   return LAUNCH_OK();
 }
 
 
+
+// ---- the reference's own DiT glue (phone/animad.cpp:424-492, moss/mossrun/mossrun.cpp:255-343) ----
+// y = x * rsqrt(mean(x^2) + eps) * w, one vector of n <= 4096 (animad.cpp:115-123 rms_rows on the t-embedding)
+__global__ __launch_bounds__(256) void rmsvec_kernel(const float *__restrict__ x, int n, const hxa_h *__restrict__ w,
+                                                     float eps, float *__restrict__ y) {
+  __shared__ float part[4];
+  float q = 0.0f;
+  for (int i = threadIdx.x; i < n; i += 256) q = fmaf(x[i], x[i], q);
+  q = wave_sum(q);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = q;
+  __syncthreads();
+  const float r = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)n + eps);
+  for (int i = threadIdx.x; i < n; i += 256) y[i] = x[i] * r * (float)w[i];
+}
+// G independent GEMVs in one launch: y[g * ldy + n] = bias[n] + sum_k W[g][n][k] x[g * ldx + k] (W fp16
+// [G][N][K]); one wave per output row. The per-block, per-site B matrices of the Anima modulation (megarun.cpp:166-167)
+__global__ __launch_bounds__(256) void grouped_gemv_kernel(const float *__restrict__ x, long ldx, const hxa_h *__restrict__ W,
+                                                           int N, int K, const float *__restrict__ bias, float *__restrict__ y,
+                                                           long ldy) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63, g = blockIdx.y;
+  if (n >= N) return;
+  const hxa_h *wr = W + ((long)g * N + n) * K;
+  const float *xg = x + (long)g * ldx;
+  float acc = 0.0f;
+  for (int k = lane * 2; k < K; k += 128) {
+    const half2_t wv = *(const half2_t *)(wr + k);
+    acc = fmaf(xg[k], (float)wv[0], fmaf(xg[k + 1], (float)wv[1], acc));
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) y[(long)g * ldy + n] = acc + (bias ? bias[n] : 0.0f);
+}
+// rapid-moss input (mossrun.cpp:316-320): per image token t, xin = z_t + Q x0_t (Q fp32 [C4][C4]) and the token's
+// row x = Wv xin + bv (Wv fp16 [D][C4]); FT tokens per workgroup, their xin in LDS, each weight row read once
+__global__ __launch_bounds__(256) void moss_embed_kernel(const float *__restrict__ z, const float *__restrict__ x0,
+                                                         const float *__restrict__ Q, const hxa_h *__restrict__ Wv,
+                                                         const float *__restrict__ bv, float *__restrict__ x, int T,
+                                                         int xrows, int D, int C4, int ntok) {
+  extern __shared__ float xin[];  // [FT][C4]
+  const int tok0 = blockIdx.x * FT;
+  for (int i = threadIdx.x; i < FT * C4; i += 256) {
+    const int tl = i / C4, o = i % C4, tok = tok0 + tl;
+    float a = 0.0f;
+    if (tok < ntok) {
+      a = z[(long)tok * C4 + o];
+      const float *xr = x0 + (long)tok * C4;
+      for (int c = 0; c < C4; c++) a = fmaf(Q[o * C4 + c], xr[c], a);
+    }
+    xin[i] = a;
+  }
+  __syncthreads();
+  for (int n = threadIdx.x; n < D; n += 256) {
+    float acc[FT];
+#pragma unroll
+    for (int t = 0; t < FT; t++) acc[t] = bv[n];
+    const hxa_h *wr = Wv + (long)n * C4;
+    for (int c = 0; c < C4; c += 2) {
+      const half2_t wv = *(const half2_t *)(wr + c);
+#pragma unroll
+      for (int t = 0; t < FT; t++) acc[t] = fmaf(xin[t * C4 + c], (float)wv[0], fmaf(xin[t * C4 + c + 1], (float)wv[1], acc[t]));
+    }
+#pragma unroll
+    for (int t = 0; t < FT; t++) {
+      const int tok = tok0 + t;
+      if (tok < ntok) x[((long)(tok / T) * xrows + tok % T) * D + n] = acc[t];
+    }
+  }
+}
+// BN denorm + unpatchify (mossrun.cpp:339-343): x0 token rows [B*T][4C] (feature c*4 + ph*2 + pw) ->
+// lat [B][C][H][W] = x0 * sqrt(var + 1e-4) + mean, per feature
+__global__ void bn_unpatchify_kernel(const float *__restrict__ x0, const float *__restrict__ mean,
+                                     const float *__restrict__ var, int B, int Cc, int H, int W, float *__restrict__ lat) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const int C4 = 4 * Cc, gh = H / 2, gw = W / 2;
+  if (i >= (long)B * gh * gw * C4) return;
+  const int f = (int)(i % C4);
+  const long tb = i / C4;
+  const int tk = (int)(tb % (gh * gw)), b = (int)(tb / (gh * gw));
+  const int gy = tk / gw, gx = tk % gw, c = f / 4, ph = (f / 2) & 1, pw = f & 1;
+  lat[(((long)b * Cc + c) * H + 2 * gy + ph) * W + 2 * gx + pw] = x0[i] * sqrtf(var[f] + 1e-4f) + mean[f];
+}
+
+int hxa_rmsvec_launch(const float *x, int n, const hxa_h *w, float eps, float *y, hipStream_t st) {
+  if (n <= 0 || n > 4096) return HXA_E_ARG;
+  hipLaunchKernelGGL(rmsvec_kernel, dim3(1), dim3(256), 0, st, x, n, w, eps, y);
+  return LAUNCH_OK();
+}
+int hxa_grouped_gemv_launch(const float *x, long ldx, const hxa_h *W, int G, int N, int K, const float *bias, float *y,
+                            long ldy, hipStream_t st) {
+  if (G <= 0 || N <= 0 || K <= 0 || K % 2 || G > 65535) return HXA_E_ARG;
+  hipLaunchKernelGGL(grouped_gemv_kernel, dim3(nblk(N, 4), G), dim3(256), 0, st, x, ldx, W, N, K, bias, y, ldy);
+  return LAUNCH_OK();
+}
+int hxa_moss_embed_launch(const float *z, const float *x0, const float *Q, const hxa_h *Wv, const float *bv, float *x, int B,
+                          int T, int xrows, int D, int C4, hipStream_t st) {
+  if (C4 % 2 || C4 > 512 || B <= 0 || T <= 0 || xrows < T) return HXA_E_ARG;
+  const int ntok = B * T;
+  hipLaunchKernelGGL(moss_embed_kernel, dim3((ntok + FT - 1) / FT), dim3(256), sizeof(float) * FT * C4, st, z, x0, Q, Wv,
+                     bv, x, T, xrows, D, C4, ntok);
+  return LAUNCH_OK();
+}
+int hxa_bn_unpatchify_launch(const float *x0, const float *mean, const float *var, int B, int Cc, int H, int W, float *lat,
+                             hipStream_t st) {
+  hipLaunchKernelGGL(bn_unpatchify_kernel, dim3(nblk((long)B * Cc * H * W)), dim3(256), 0, st, x0, mean, var, B, Cc, H, W,
+                     lat);
+  return LAUNCH_OK();
+}
 
 int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t st) {
   hipLaunchKernelGGL(sinusoid_kernel, dim3(nblk((long)n * dim / 2)), dim3(256), 0, st, t, n, dim, out);

@@ -92,8 +92,20 @@ int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W
                           const float *bias, int split, int gap, hipStream_t st);
 // final layer over B images of T image tokens (image b's rows start at b*xrows); dtp == NULL: lat = v,
 // else lat += (*dtp) * v (Euler step)
+// normw != NULL: RMSNorm * normw instead of LN (the MOSS head); x0rows / zrows != NULL: write the token rows
+// x0rows[t][o] = zrows[t][o] - v (rapid-moss) instead of the latent
 int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale,
-                     const hxa_h *Wf, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st);
+                     const hxa_h *Wf, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st,
+                     const float *normw = nullptr, float *x0rows = nullptr, const float *zrows = nullptr);
+// the reference's own DiT glue: vector RMSNorm * w (fp16 w), G GEMVs with their own inputs, the rapid-moss latent mix +
+// video embedding, and BN denorm + unpatchify of the x0 token rows
+int hxa_rmsvec_launch(const float *x, int n, const hxa_h *w, float eps, float *y, hipStream_t st);
+int hxa_grouped_gemv_launch(const float *x, long ldx, const hxa_h *W, int G, int N, int K, const float *bias, float *y,
+                            long ldy, hipStream_t st);
+int hxa_moss_embed_launch(const float *z, const float *x0, const float *Q, const hxa_h *Wv, const float *bv, float *x, int B,
+                          int T, int xrows, int D, int C4, hipStream_t st);
+int hxa_bn_unpatchify_launch(const float *x0, const float *mean, const float *var, int B, int Cc, int H, int W, float *lat,
+                             hipStream_t st);
 int hxa_quantize_launch(const float *W, int N, int K, int fmt, void *q, hxa_h *s, hipStream_t st);
 int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t st);
 

@@ -38,7 +38,7 @@ class BlockDims(C.Structure):
 
 class DitCfg(C.Structure):
     _fields_ = [("blk", BlockDims), ("nblocks", I), ("lat_c", I), ("lat_h", I), ("lat_w", I), ("temb", I),
-                ("ntxt_in", I)]
+                ("ntxt_in", I), ("form", I)]
 
 
 _SIGS = {
@@ -95,6 +95,7 @@ _SIGS = {
     "hxa_dit_get_latent": (I, [P, P]),
     "hxa_dit_step": (I, [P, F, F, I]),
     "hxa_dit_velocity": (I, [P, F, P]),
+    "hxa_dit_moss_step": (I, [P, F, I]),
     "hxa_dit_export": (L, [P, I, P, SZ]),
     "hxa_dit_stream": (P, [P]),
 }

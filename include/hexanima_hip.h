@@ -243,8 +243,17 @@ typedef struct {
   hxa_block_dims blk;   /* per-block shape (T = gh*gw tokens per image) */
   int nblocks;
   int lat_c, lat_h, lat_w; /* latent [C][H][W]; patch 2 */
-  int temb;             /* sinusoid width of the timestep embedding (256) */
+  int temb;             /* sinusoid width of the timestep embedding (form 0: 256; form 1: D for Anima, 256 for MOSS) */
   int ntxt_in;          /* MOSS: text width before projection (0 = none) */
+  int form;             /* glue around the blocks. 0: the benchmark configurations' (Linear . SiLU . Linear of the
+                           sinusoid to dense per-block [6D][D] modulation, LN final layer, Euler steps).
+                           1: the reference's own. Anima (phone/animad.cpp:424-492, megarun.cpp:156-171): emb =
+                           RMSNorm(sinusoid_D(t)) * w, lora = L2 silu(L1 sinusoid_D(t)) [3D], per block and site
+                           mod = lora + B (A silu(emb)) with A [256][D], B [3D][256], final (shift, scale) =
+                           F2 (F1 silu(emb)) + lora[0 : 2D]. MOSS, the rapid-moss sampler (mossrun.cpp:255-343):
+                           time MLP with biases, shared block modulation and head modulation, per step x_in = z + Q x0
+                           per token, video embedding with bias, the blocks, RMS head, x0 = z - v
+                           (hxa_dit_moss_step); hxa_dit_get_latent returns the BN-denormalised x0. */
 } hxa_dit_cfg;
 int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **dit);
 int hxa_dit_destroy(void *dit);
@@ -255,12 +264,21 @@ int hxa_dit_get_latent(void *dit, float *lat);
 int hxa_dit_step(void *dit, float sigma, float sigma_next, int use_graph);
 /* the velocity v(x, sigma) of the current latent into v [batch][C][H][W] (host), without updating x */
 int hxa_dit_velocity(void *dit, float sigma, float *v);
+/* one step of the rapid-moss sampler (moss/mossrun/mossrun.cpp:307-334) for a MOSS DiT in form 1, with the step's
+ * time code: x_in = z + Q x0, v = head(blocks(embed(x_in), text)), x0 = z - v; the latent set by hxa_dit_set_inputs
+ * is the noise z, and x0 starts at 0 */
+int hxa_dit_moss_step(void *dit, float code, int use_graph);
 /* copies of the device weights for checking (host may be NULL to query the size; returns bytes):
  *   which in [0, nblocks): block pack `which`
  *   which in [nblocks, 2 nblocks): modulation weights of block which-nblocks, fp16 [6D][D]
- *     (MOSS: one shared [6D][D] matrix, which == nblocks)
+ *     (form 1 Anima: A [3 x 256][D] then B [3][3D][256]; MOSS: one shared [6D][D] matrix, which == nblocks)
  *   which == 2 nblocks: glue, fp16, concatenated: x_embed [D][4C], t_embed [D][temb], final_mod [2D][D],
- *     final_linear [4C][D], then (MOSS only) text_proj [D][ntxt_in] */
+ *     final_linear [4C][D], then (MOSS only) text_proj [D][ntxt_in].
+ *     Form 1 Anima: x_embed [D][4C], t_l1 [D][D], t_l2 [3D][D], f1 [256][D], f2 [2D][256], final_linear [4C][D],
+ *     t_norm [D]; form 1 MOSS: video_embed [D][4C], t0 [D][256], t2 [D][D], head_mod [2D][D], final_linear [4C][D],
+ *     text_proj [D][ntxt_in]
+ *   which == 2 nblocks + 1 (form 1 MOSS): fp32 b_video [D], b_t0 [D], b_t2 [D], b_smod [6D], b_hmod [2D],
+ *     final_norm [D], latent_mix Q [4C][4C], bn_mean [4C], bn_var [4C] */
 long hxa_dit_export(void *dit, int which, void *host, size_t bytes);
 void *hxa_dit_stream(void *dit);
 

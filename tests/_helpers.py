@@ -170,3 +170,88 @@ def oracle_anima_modulation(modw16, emb, lora):
         h1 = hxo.linear_f32(s, a)
         out.append(np.asarray(lora, np.float32) + hxo.linear_f32(h1, b)[0])
     return np.concatenate(out).reshape(9, 2048).astype(np.float32)
+
+
+def rms_vec(x, w16, eps=1e-6):
+    """animad.cpp:115-123 rms_rows on one vector: x * 1 / sqrt(sum(x^2) / n + eps) (sum in double) * w (fp16)."""
+    x = np.asarray(x, np.float32)
+    s = float(np.sum(x.astype(np.float64) ** 2))
+    k = np.float32(1.0) / np.sqrt(np.float32(s / x.size) + np.float32(eps))
+    return (x * k * np.asarray(w16).view(np.float16).astype(np.float32)).astype(np.float32)
+
+
+def oracle_anima_ref_velocity(lat, ctx16, sigma, blocks, modws, glue, *, D, H, F, C4, gelu=1, attn_mode=0):
+    """v(x, sigma) of the Anima DiT with the reference's own glue, image by image:
+    t-embedding (animad.cpp:424-431): tp = sinusoid_D(t), emb = RMSNorm(tp) * t_norm, lora = L2 silu(L1 tp);
+    per block and site (megarun.cpp:159-167): mod = lora + B (A silu(emb)); final (animad.cpp:475-492): (shift, scale) =
+    F2 (F1 silu(emb)) + lora[:2D], LN(x) (1 + scale) + shift, linear, unpatchify.
+    glue = (Wemb [D][C4], L1 [D][D], L2 [3D][D], F1 [256][D], F2 [2D][256], Wfin [C4][D], t_norm [D]) fp16;
+    modws[k] = (A [3*256][D], B [3][3D][256]) fp16."""
+    Wemb, L1, L2, F1, F2, Wfin, tnorm = glue
+    B_, Cc, Hl, Wl = lat.shape
+    tp = hxo.sinusoid(sigma, D)
+    emb = rms_vec(tp, tnorm)
+    lora = hxo.linear_f32(silu(hxo.linear_f32(tp[None, :], L1)), L2)[0]
+    se = silu(emb)[None, :]
+    mods = []
+    for A, Bm in modws:
+        rows = []
+        for site in range(3):
+            h1 = hxo.linear_f32(se, A[site * 256:(site + 1) * 256])
+            rows.append(lora + hxo.linear_f32(h1, np.ascontiguousarray(Bm[site]))[0])
+        mods.append(np.concatenate(rows).reshape(9, D).astype(np.float32))
+    fm = hxo.linear_f32(hxo.linear_f32(se, F1), F2)[0] + lora[:2 * D]
+    cos, sin = hxo.rope_anima(Hl // 2, Wl // 2)
+    out = np.zeros_like(lat)
+    for b in range(B_):
+        x = hxo.linear_f32(hxo.patchify(lat[b]), Wemb)
+        for w, m9 in zip(blocks, mods):
+            x, _, _ = hxo.anima_block(x, ctx16[b], m9, cos, sin, w, H=H, F=F, gelu=gelu, attn_mode=attn_mode)
+        xn = hxo.final_norm(x, fm[:D], fm[D:])
+        out[b] = hxo.unpatchify(hxo.linear_f32(xn, Wfin), Cc, Hl, Wl)
+    return out
+
+
+def oracle_moss_rapid_step(z, x0, txt16, code, blocks, modw, glue, vec, *, D, H, F, C4, ntxt, Ttot, gh, gw,
+                           attn_mode=0):
+    """One rapid-moss step (mossrun.cpp:307-334) with the reference's glue, image by image. z, x0: token rows
+    [B][T][C4] (feature c*4 + ph*2 + pw); returns the new x0.
+    time_vecs (mossrun.cpp:255-264): e = sinusoid_256(code), a = T0 e + b0, b = T2 silu(a) + b2, block modulation
+    Wm b + bm [6][D], head modulation Wh b + bh; x_in = z + x0 Q^T per token; rows = Wv x_in + bv, then the text rows
+    f16(text Wt^T) (the text projection into zeroed rows); blocks; head RMS(x) nfin (1 + head[D:]) + head[:D],
+    v = Wfin r, x0 = z - v.
+    glue = (Wv [D][C4], T0 [D][256], T2 [D][D], Wh [2D][D], Wfin [C4][D], Wt [D][ntxt_in]) fp16, modw [6D][D] fp16,
+    vec = (bv, b0, b2, bm, bh, nfin, Q [C4][C4], bn_mean, bn_var) fp32."""
+    Wv, T0, T2, Wh, Wfin, Wt = glue
+    bv, b0, b2, bm, bh, nfin, Q = vec[:7]
+    e = hxo.sinusoid(code, 256)[None, :]
+    a = hxo.linear_f32(e, T0) + b0
+    bt = hxo.linear_f32(silu(a), T2) + b2
+    mod6 = (hxo.linear_f32(bt, modw)[0] + bm).reshape(6, D).astype(np.float32)
+    head = (hxo.linear_f32(bt, Wh)[0] + bh).astype(np.float32)
+    bands = (1.0 / 10000.0 ** (np.arange(16) / 16.0)).astype(np.float32)
+    c, sn = hxo.rope_moss(gh, gw, ntxt, bands)
+    cos = np.ones((Ttot, 64), np.float32)
+    sin = np.zeros((Ttot, 64), np.float32)
+    cos[:c.shape[0]], sin[:c.shape[0]] = c, sn
+    timg = gh * gw
+    out = np.zeros_like(x0)
+    for b in range(z.shape[0]):
+        xin = (z[b].astype(np.float64) + x0[b].astype(np.float64) @ Q.astype(np.float64).T).astype(np.float32)
+        x = np.zeros((Ttot, D), np.float32)
+        x[:timg] = hxo.linear_f32(xin, Wv) + bv
+        x[timg:timg + ntxt] = f16(hxo.gemm(txt16[b], Wt)).astype(np.float32)
+        for w in blocks:
+            x, _, _ = hxo.moss_block(x, mod6, cos, sin, w, H=H, F=F, nvalid=timg + ntxt, attn_mode=attn_mode)
+        xi = x[:timg].astype(np.float64)
+        rs = 1.0 / np.sqrt((xi * xi).mean(-1, keepdims=True) + 1e-6)
+        r = (xi * rs * nfin * (1.0 + head[D:]) + head[:D]).astype(np.float32)
+        out[b] = z[b] - hxo.linear_f32(r, Wfin)
+    return out
+
+
+def bn_unpatchify(x0, mean, var, Cc, H, W):
+    """mossrun.cpp:339-343: x0 token rows [T][4C] (feature c*4 + ph*2 + pw) -> [C][H][W] * sqrt(var + 1e-4) + mean."""
+    y = (x0.astype(np.float64) * np.sqrt(var.astype(np.float64) + 1e-4) + mean).astype(np.float32)
+    gh, gw = H // 2, W // 2
+    return np.ascontiguousarray(y.reshape(gh, gw, Cc, 2, 2).transpose(2, 0, 3, 1, 4).reshape(Cc, H, W))

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 from oracle import hxo
-from tests._helpers import delta_metrics, f16, oracle_anima_velocity, oracle_moss_velocity, rel, unpack_weights
+from tests._helpers import (bn_unpatchify, delta_metrics, f16, oracle_anima_ref_velocity, oracle_anima_velocity,
+                            oracle_moss_rapid_step, oracle_moss_velocity, rel, unpack_weights)
 
 pytestmark = pytest.mark.gpu
 
@@ -698,3 +699,115 @@ def test_dit_graph_replay_matches_eager():
             lib.hxa_dit_destroy(p)
     for a, b in zip(*outs):
         assert np.array_equal(a, b)
+
+
+def _split(buf, shapes):
+    out, o = [], 0
+    for sh in shapes:
+        n = int(np.prod(sh))
+        out.append(buf[o:o + n].reshape(sh))
+        o += n
+    assert o == buf.size
+    return out
+
+
+def _anima_ref_weights(hip, p, nb, D, F, DC, C4):
+    layout = hip.pack_layout(0, D, F, DC, 0, 0)
+    blocks = [unpack_weights(_export(hip, p, k), 0, D, F, DC, 0, 0, layout) for k in range(nb)]
+    modws = []
+    for k in range(nb):
+        A, Bm = _split(_export(hip, p, nb + k).view(np.uint16), [(768, D), (3, 3 * D, 256)])
+        modws.append((A, Bm))
+    glue = _split(_export(hip, p, 2 * nb).view(np.uint16),
+                  [(D, C4), (D, D), (3 * D, D), (256, D), (2 * D, 256), (C4, D), (D,)])
+    return blocks, modws, glue
+
+
+@pytest.mark.parametrize("D,H,F,C_,DC,nb,lat_hw,batch", [(256, 2, 1024, 32, 128, 2, 16, 2), (2048, 16, 8192, 256, 1024, 2, (96, 64), 1)])
+def test_dit_anima_reference_form(D, H, F, C_, DC, nb, lat_hw, batch):
+    """The Anima DiT with the reference's own glue (hxa_dit_cfg.form 1): the RMSNorm'd D-wide sinusoid and its LoRA MLP
+    (animad.cpp:424-431), per-block low-rank modulation (megarun.cpp:156-171, every block's A in one GEMV and every
+    block's and site's B in one grouped GEMV), the low-rank final adaLN (animad.cpp:475-479). The small DiT runs a
+    4-step Euler denoise at batch 2, the 2B-width one (1536 tokens, 2 blocks) a velocity check."""
+    hip = _hip()
+    lh, lw = (lat_hw, lat_hw) if isinstance(lat_hw, int) else lat_hw
+    say(f"dit anima reference form D={D} blocks={nb} latent 16x{lh}x{lw} batch {batch}")
+    lib = hip.lib()
+    bd = hip.BlockDims(0, D, H, F, C_, DC, 0, batch, 0, 0, 0, 1)
+    cfg = hip.DitCfg(bd, nb, 16, lh, lw, D, 0, 1)
+    p = C.c_void_p()
+    hip.check(lib.hxa_dit_create(C.byref(cfg), 555, C.byref(p)), "dit_create")
+    try:
+        rng = np.random.default_rng(15)
+        lat = rng.standard_normal((batch, 16, lh, lw)).astype(np.float32)
+        ctx = rng.standard_normal((batch, C_, DC)).astype(np.float32)
+        hip.check(lib.hxa_dit_set_inputs(p, lat.ctypes.data, ctx.ctypes.data), "set_inputs")
+        blocks, modws, glue = _anima_ref_weights(hip, p, nb, D, F, DC, 64)
+        kw = dict(D=D, H=H, F=F, C4=64)
+        ctx16 = f16(ctx)
+        v_gpu = np.zeros_like(lat)
+        hip.check(lib.hxa_dit_velocity(p, 0.75, v_gpu.ctypes.data), "velocity")
+        v_ref = oracle_anima_ref_velocity(lat, ctx16, 0.75, blocks, modws, glue, **kw)
+        rv = rel(v_gpu, v_ref)
+        print(f"velocity rel err {rv:.2e} max abs {np.max(np.abs(v_gpu - v_ref)):.2e}", flush=True)
+        assert rv < (1.1e-4 if D == 256 else 1.8e-3)  # measured 3.5e-5 (D 256), 6.1e-4 (D 2048, 1536 tokens)
+        if D > 256:
+            return
+        sig = [1.0, 0.75, 0.5, 0.25, 0.0]
+        ref = lat.copy()
+        for i in range(4):
+            hip.check(lib.hxa_dit_step(p, sig[i], sig[i + 1], 1), "step")
+            ref = ref + (sig[i + 1] - sig[i]) * oracle_anima_ref_velocity(ref, ctx16, sig[i], blocks, modws, glue, **kw)
+        got = np.zeros_like(lat)
+        hip.check(lib.hxa_dit_get_latent(p, got.ctypes.data), "get_latent")
+        r, c, mx = metrics_line(got, ref, lat)
+        print(f"reference-form denoise rel err on delta {r:.2e} cos {c:.9f} max abs {mx:.2e}", flush=True)
+        assert r < 6e-5 and c > 1 - 6e-5 ** 2 and mx < 7e-5  # measured 1.7e-5, 2.3e-5
+    finally:
+        lib.hxa_dit_destroy(p)
+
+
+def test_dit_moss_rapid_sampler():
+    """The MOSS DiT with the reference's own glue and sampler (hxa_dit_cfg.form 1, mossrun.cpp:255-343): time MLP with
+    biases, shared block modulation and head modulation; per step x_in = z + Q x0 per token, video embedding with bias,
+    the blocks over image + text tokens, RMS head, x0 = z - v; 4 steps at batch 2 with int8 attention / int4 SiTU
+    weights, then the BN-denormalised, unpatchified x0 against the oracle's."""
+    hip = _hip()
+    say("dit moss rapid-moss sampler, 2 blocks, batch 2, 4 steps")
+    lib = hip.lib()
+    D, H, F, ntxt, tin, nb, B = 256, 2, 512, 20, 128, 2, 2
+    bd = hip.BlockDims(1, D, H, F, ntxt, 0, 0, B, 0, hip.W_Q8, hip.W_Q4, 1)
+    cfg = hip.DitCfg(bd, nb, 32, 16, 16, 256, tin, 1)
+    p = C.c_void_p()
+    hip.check(lib.hxa_dit_create(C.byref(cfg), 777, C.byref(p)), "dit_create")
+    try:
+        rng = np.random.default_rng(17)
+        z = rng.standard_normal((B, 32, 16, 16)).astype(np.float32)
+        txt = rng.standard_normal((B, ntxt, tin)).astype(np.float32)
+        hip.check(lib.hxa_dit_set_inputs(p, z.ctypes.data, txt.ctypes.data), "set_inputs")
+        C4, timg = 128, 64
+        Ttot = (timg + ntxt + 31) // 32 * 32
+        layout = hip.pack_layout(1, D, F, 0, hip.W_Q8, hip.W_Q4)
+        blocks = [unpack_weights(_export(hip, p, k), 1, D, F, 0, hip.W_Q8, hip.W_Q4, layout) for k in range(nb)]
+        modw = _export(hip, p, nb).view(np.uint16).reshape(6 * D, D)
+        glue = _split(_export(hip, p, 2 * nb).view(np.uint16),
+                      [(D, C4), (D, 256), (D, D), (2 * D, D), (C4, D), (D, tin)])
+        vec = _split(_export(hip, p, 2 * nb + 1).view(np.float32),
+                     [(D,), (D,), (D,), (6 * D,), (2 * D,), (D,), (C4, C4), (C4,), (C4,)])
+        codes = [0.999, 0.75, 0.5, 0.25]
+        zr = np.stack([hxo.patchify(z[b]) for b in range(B)])
+        x0 = np.zeros_like(zr)
+        txt16 = f16(txt)
+        for code in codes:
+            hip.check(lib.hxa_dit_moss_step(p, code, 1), "moss_step")
+            x0 = oracle_moss_rapid_step(zr, x0, txt16, code, blocks, modw, glue, vec, D=D, H=H, F=F, C4=C4, ntxt=ntxt,
+                                        Ttot=Ttot, gh=8, gw=8)
+        got = np.zeros_like(z)
+        hip.check(lib.hxa_dit_get_latent(p, got.ctypes.data), "get_latent")
+        ref = np.stack([bn_unpatchify(x0[b], vec[7], vec[8], 32, 16, 16) for b in range(B)])
+        r, mx = rel(got, ref), float(np.max(np.abs(got - ref)))
+        print(f"rapid-moss output rel err {r:.2e} max abs {mx:.2e}", flush=True)
+        assert r < 2e-6 and mx < 1.2e-5  # measured 6.3e-7, 3.8e-6 (small gates: mostly the glue around the blocks)
+        assert lib.hxa_dit_step(p, 1.0, 0.5, 0) == -11  # the Euler step is not this form's
+    finally:
+        lib.hxa_dit_destroy(p)

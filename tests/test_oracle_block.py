@@ -253,3 +253,26 @@ def test_moss_lora_with_zero_b_is_the_plain_block():
     out, _, _ = hxo.moss_block(x, mod6, cos, sin, wl, H=2, F=512, nvalid=150)
     plain, _, _ = hxo.moss_block(x, mod6, cos, sin, w, H=2, F=512, nvalid=150)
     assert np.array_equal(out, plain)
+
+
+def test_glue_oracle_bn_unpatchify_and_rms_vec():
+    """The rapid-moss output step (mossrun.cpp:339-343) restated by loops on a tiny case: zo[c/4][2h + (c/2)%2]
+    [2w + c%2] = x0[c][h][w] sqrt(var[c] + 1e-4) + mean[c]; and the t-embedding RMSNorm (animad.cpp:115-123)
+    against float64 with a one-hot input (the norm of a one-hot vector of value a is sqrt(n) sign(a) w)."""
+    from tests._helpers import bn_unpatchify, rms_vec
+    rng = np.random.default_rng(3)
+    Cc, H, W = 2, 4, 6
+    x0 = rng.standard_normal((H // 2 * W // 2, 4 * Cc)).astype(np.float32)  # token rows [T][128-channel]
+    mean, var = rng.standard_normal(4 * Cc).astype(np.float32), rng.uniform(0.5, 2, 4 * Cc).astype(np.float32)
+    want = np.zeros((Cc, H, W), np.float64)
+    for c in range(4 * Cc):
+        for h in range(H // 2):
+            for w in range(W // 2):
+                want[c // 4, 2 * h + (c // 2) % 2, 2 * w + c % 2] = x0[h * (W // 2) + w, c] * np.sqrt(var[c] + 1e-4) + mean[c]
+    assert np.allclose(bn_unpatchify(x0, mean, var, Cc, H, W), want, rtol=1e-6, atol=1e-6)
+    n = 64
+    wv = f16(rng.uniform(0.5, 1.5, n))
+    e = np.zeros(n, np.float32)
+    e[5] = -3.0
+    y = rms_vec(e, wv.view(np.uint16))
+    assert abs(y[5] - (-np.sqrt(n) * float(wv[5]))) < 1e-4 and np.count_nonzero(y) == 1
