@@ -6,9 +6,12 @@ random N(0, 0.02) weights, N(0, 1) latent and text. One step = one flow-matching
 28 x modulation, patch embed, 28 blocks, final layer, update), replayed from a captured HIP graph with the sigma
 schedule 1.0, 0.75, 0.5, 0.25 -> 0 cycled.
 
-Prints one JSON line. `roofline` is for the dominant kernel (the MLP up-projection GEMM with GELU epilogue,
-1536 x 2048 x 8192, the largest launch of the step), timed with HIP events on the stream it is launched on.
-`cpu_baseline` times the CPU oracle (a port of the reference block) on one block and scales to a step.
+Prints one JSON line. `kernels` splits the block's time over its kernel families (HIP events between the block's
+stages on its stream); `roofline` is for the family with the largest share -- the 192 x 128 split-K GEMM of the
+o, cross-o and MLP-down projections -- timed with HIP events on the stream it is launched on, at the launch shapes
+of the step. `abi_chain` runs the 28 blocks through mega_block the way megarun drives them (hxa_run, a child
+process). `cpu_baseline` times the CPU oracle (a port of the reference block, built -march=native with OpenMP)
+on whole blocks and one GEMM, scaled to a step.
 """
 import argparse
 import ctypes as C
@@ -31,7 +34,6 @@ WFMT = 0 | 16  # fp16 weights, k-tiled: the block-pack layout of the DiT's matri
 BLOCK_FLOPS = 2 * T * D * (3 * D) + 2 * T * D * D + 2 * T * D * D + 2 * C_TXT * DC * (2 * D) + 2 * T * D * D \
     + 2 * T * D * F * 2 + 4 * T * T * D + 4 * T * C_TXT * D
 STEP_FLOPS = NBLK * BLOCK_FLOPS + 2 * T * 64 * D + 2 * T * D * 64
-UP_FLOPS = 2 * T * D * F
 
 
 def _event(L, hip):
@@ -83,29 +85,10 @@ def dit_ms(bd, nblk, lat_shape, ctx_shape, tin, steps, warmup, seed, wall_check=
 def gpu_run(steps, warmup):
     from hexanima_amd import hip
     hip.init(0)
-    L = hip.lib()
     info = hip.device_info()
     bd = hip.BlockDims(0, D, H, F, C_TXT, DC, 0, 1, 0, hip.W_F16, hip.W_F16, 1)
     ms_step = dit_ms(bd, NBLK, (1,) + LAT, (1, C_TXT, DC), 0, steps, warmup, 2024, wall_check=True)
-
-    # dominant kernel: MLP up-projection GEMM with the GELU epilogue (one launch per block per step)
-    s = C.c_void_p()
-    hip.check(L.hxa_stream_create(C.byref(s)), "stream")
-    A = hip.DeviceArray((T, D), np.float16)
-    W = hip.DeviceArray((F, D), np.float16)
-    O = hip.DeviceArray((T, F), np.float16)
-    hip.check(L.hxa_fill_normal(A.ptr, 1, T * D, 11, 0.0, 1.0, s), "fill")
-    hip.check(L.hxa_fill_normal(W.ptr, 1, F * D, 12, 0.0, 0.02, s), "fill")
-
-    def up():
-        hip.check(L.hxa_gemm(A.ptr, D, T, WFMT, W.ptr, None, None, F, D, 1, hip.EPI_GELU_TANH, O.ptr, F, 0, None, 0,
-                             None, None, 0, 0, s), "gemm")
-    up_ms = _time_launches(L, hip, up, s, reps=50)
-    L.hxa_stream_destroy(s)
-    pk = hip.gemm_pick(T, F, D, WFMT, 1, hip.EPI_GELU_TANH)
-    info["up_kernel"] = (f"{'gemm_pp_kernel' if pk['waves'] == 9 else 'gemm_kernel'} {pk['bm']}x{pk['bn']}"
-                         f" ({8 if pk['waves'] == 9 else pk['waves']} waves)")
-    return info, ms_step, up_ms
+    return info, ms_step
 
 
 def _time_launches(L, hip, fn, s, reps=20, warm=5):
@@ -237,6 +220,16 @@ def microbench():
         res["attention"][name] = _rate(4.0 * Tq * NKV * Dd, _time_launches(L, hip, att, s))
         del q, k, vt, o
     # one 2B fp16 block
+    blk, _keep = _block_setup(L, hip, s)
+    res["block_2b_fp16_1536tok"] = _rate(BLOCK_FLOPS, _time_launches(L, hip, blk, s, reps=10, warm=2))
+    hip.check(L.hxa_stream_sync(s), "sync")
+    L.hxa_stream_destroy(s)
+    return res
+
+
+def _block_setup(L, hip, s):
+    """The 2B fp16 block on resident synthetic data (weights N(0, 0.02), x N(0, 1), text N(0, 1), modulation
+    N(0, 0.02), identity RoPE); returns blk(stage_us=None), one hxa_block_run on stream s, and the buffers it uses."""
     bd = hip.BlockDims(0, D, H, F, C_TXT, DC, T, 1, T, hip.W_F16, hip.W_F16, 1)
     total, mats, voff = hip.pack_layout(0, D, F, DC, hip.W_F16, hip.W_F16)
     pack = hip.DeviceArray((total,), np.uint8)
@@ -255,31 +248,149 @@ def microbench():
     hip.check(L.hxa_fill_const(sin.ptr, 0, T * 64, 0.0, s), "fill")
     ws = hip.block_ws(bd)
 
-    def blk():
-        hip.check(L.hxa_block_run(C.byref(bd), pack.ptr, x.ptr, ctx.ptr, mod.ptr, cos.ptr, sin.ptr, ws.ptr, 0, None, 0,
-                                  s), "block")
-    res["block_2b_fp16_1536tok"] = _rate(BLOCK_FLOPS, _time_launches(L, hip, blk, s, reps=10, warm=2))
+    def blk(stage_us=None):
+        hip.check(L.hxa_block_run(C.byref(bd), pack.ptr, x.ptr, ctx.ptr, mod.ptr, cos.ptr, sin.ptr, ws.ptr, 0, stage_us,
+                                  24 if stage_us is not None else 0, s), "block")
+    return blk, (bd, pack, x, ctx, mod, cos, sin, ws)
+
+
+# The Anima block's 13 stages (blk.c:136 TICK order) and the kernel family each one launches.
+STAGES = ("LN-mod self", "qkv + head RMSNorm + RoPE", "(RoPE: fused)", "self attention", "o projection",
+          "LN-mod cross", "cross q + text k/v", "(RMSNorm: fused)", "cross attention", "cross-o projection",
+          "LN-mod MLP", "MLP up + GELU", "MLP down")
+FAMILIES = {  # family -> the stages whose launches it is
+    "gemm_splitk": (4, 9, 12),
+    "gemm_pp_mlp_up": (11,),
+    "gemm_pp_qkv_headnorm": (1,),
+    "attention": (3, 8),
+    "normrow": (0, 5, 10),
+    "gemm_pair_crossq_textkv": (6,),
+}
+
+
+def _kname(pk):
+    return (f"{'gemm_pp_kernel' if pk['waves'] == 9 else 'gemm_kernel'} {pk['bm']}x{pk['bn']}"
+            f" ({8 if pk['waves'] == 9 else pk['waves']} waves)")
+
+
+def family_launchers(L, hip, s):
+    """The launches of the GEMM and attention families at their in-step shapes (batch 1, 1536 tokens, 256 text
+    tokens), on resident synthetic fp16 data: family -> (fn launching the family's launches of one block once,
+    launches, algorithmic FLOP of those launches, algorithmic HBM bytes of those launches (operands read once,
+    results written once), kernel name), plus the buffers to keep alive."""
+    keep = []
+
+    def arr(shape, seed, std=1.0):
+        a = hip.DeviceArray(shape, np.float16)
+        hip.check(L.hxa_fill_normal(a.ptr, 1, int(np.prod(shape)), seed, 0.0, std, s), "fill")
+        keep.append(a)
+        return a
+    h, mid, o = arr((T, D), 61), arr((T, F), 62), arr((T, D), 63)
+    Wo, Wco, W1, W2, Wqkv = arr((D, D), 64, 0.02), arr((D, D), 65, 0.02), arr((F, D), 66, 0.02), arr((D, F), 67, 0.02), \
+        arr((3 * D, D), 68, 0.02)
+    part, up, qk, vt = arr((2, T, D), 69), arr((T, F), 70), arr((T, 2 * D), 71), arr((D, T), 72)
+    k, ck, cvt = arr((T, D), 73), arr((C_TXT, D), 74), arr((D, C_TXT), 75)
+    gain = hip.DeviceArray((512,), np.float32)
+    cs, sn = hip.DeviceArray((T, 64), np.float32), hip.DeviceArray((T, 64), np.float32)
+    keep += [gain, cs, sn]
+    hip.check(L.hxa_fill_const(gain.ptr, 0, 512, 128 ** -0.5, s), "fill")
+    hip.check(L.hxa_fill_const(cs.ptr, 0, T * 64, 1.0, s), "fill")
+    hip.check(L.hxa_fill_const(sn.ptr, 0, T * 64, 0.0, s), "fill")
+    P = hip.EPI_PARTIAL
+
+    def splitk():  # o, cross-o (K = D) and MLP down (K = F): two fp16 K-half partials each
+        for A, lda, W, K in ((o, D, Wo, D), (o, D, Wco, D), (mid, F, W2, F)):
+            hip.check(L.hxa_gemm(A.ptr, lda, T, WFMT, W.ptr, None, None, D, K, 2, P, part.ptr, D, T * D, None, 0, None,
+                                 None, 0, 0, s), "gemm")
+
+    def mlp_up():
+        hip.check(L.hxa_gemm(h.ptr, D, T, WFMT, W1.ptr, None, None, F, D, 1, hip.EPI_GELU_TANH, up.ptr, F, 0, None, 0,
+                             None, None, 0, 0, s), "gemm")
+
+    def qkv():
+        hip.check(L.hxa_gemm_headnorm(h.ptr, D, T, WFMT, Wqkv.ptr, None, None, 3 * D, D, qk.ptr, 2 * D, vt.ptr, T, 2 * D,
+                                      2 * D, gain.ptr, gain.ptr, D, cs.ptr, sn.ptr, T, s), "gemm_headnorm")
+
+    def attention():
+        hip.check(L.hxa_attention(qk.ptr, 2 * D, k.ptr, D, vt.ptr, T, o.ptr, D, T, T, T, H, 1, 0, 0, 0, 0, s), "attn")
+        hip.check(L.hxa_attention(qk.ptr, 2 * D, ck.ptr, D, cvt.ptr, C_TXT, o.ptr, D, T, C_TXT, C_TXT, H, 1, 0, 0, 0, 0,
+                                  s), "attn")
+    f16 = 2
+    fam = {
+        "gemm_splitk": (splitk, 3, 2 * T * D * D * 2 + 2 * T * F * D,
+                        f16 * (2 * (T * D + D * D + 2 * T * D) + (T * F + D * F + 2 * T * D)),
+                        _kname(hip.gemm_pick(T, D, F, WFMT, 2, P)) + " split-K 2, fp16 partials"),
+        "gemm_pp_mlp_up": (mlp_up, 1, 2 * T * D * F, f16 * (T * D + F * D + T * F),
+                           _kname(hip.gemm_pick(T, F, D, WFMT, 1, hip.EPI_GELU_TANH)) + ", GELU epilogue"),
+        "gemm_pp_qkv_headnorm": (qkv, 1, 2 * T * D * 3 * D, f16 * (T * D + 3 * D * D + 3 * T * D),
+                                 _kname(hip.gemm_pick(T, 3 * D, D, WFMT, 1, 0, 2 * D)) + ", head RMSNorm + RoPE epilogue"),
+        "attention": (attention, 2, 4 * T * T * D + 4 * T * C_TXT * D,
+                      f16 * (4 * T * D + 2 * T * D + 2 * C_TXT * D + T * D), "attn_kernel (96-query workgroups)"),
+    }
+    return fam, keep
+
+
+def kernel_breakdown(L, hip, reps=10):
+    """Per-stage microseconds of the 2B fp16 block (HIP events between its stages, `reps` blocks after 2 warm-up),
+    grouped into kernel families, each family's launches timed alone at the step's shapes, and the roofline of the
+    family with the largest share of the block."""
+    s = C.c_void_p()
+    hip.check(L.hxa_stream_create(C.byref(s)), "stream")
+    blk, keep = _block_setup(L, hip, s)
+    acc = np.zeros(len(STAGES))
+    st = (C.c_int * 24)()
+    for r in range(reps + 2):
+        blk(st)
+        if r >= 2:
+            acc += np.array(st[:len(STAGES)], dtype=np.float64)
+    us = acc / reps
+    block_us = float(us.sum())
+    fam, keep2 = family_launchers(L, hip, s)
+    table = {}
+    for name, stages in FAMILIES.items():
+        row = {"stages": [STAGES[i] for i in stages], "block_us": round(float(us[list(stages)].sum()), 1),
+               "share_of_block": round(float(us[list(stages)].sum()) / block_us, 4)}
+        if name in fam:
+            fn, n, flops, nbytes, kname = fam[name]
+            ms = _time_launches(L, hip, fn, s, reps=30, warm=5)
+            row.update({"kernel": kname, "launches": n, "avg_launch_us": round(ms * 1e3 / n, 2),
+                        "gflop_per_launch": round(flops / n / 1e9, 3), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                        "frac_of_fp16_peak": round(flops / (ms * 1e-3) / PEAK_FP16, 4),
+                        "alg_mb_per_launch": round(nbytes / n / 1e6, 2)})
+        table[name] = row
+    dom = max(fam, key=lambda k: table[k]["block_us"])
+    fn, n, flops, nbytes, kname = fam[dom]
+    ms = _time_launches(L, hip, fn, s, reps=50, warm=5)
     hip.check(L.hxa_stream_sync(s), "sync")
     L.hxa_stream_destroy(s)
-    return res
+    del keep, keep2
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{dom}_1536tok.txt")
+    if os.path.exists(tpath):  # rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, copy-calibrated (see that file)
+        for line in open(tpath):
+            if line.startswith("hbm_bytes_per_launch:"):
+                traffic = int(line.split(":")[1])
+    tf = flops / (ms * 1e-3)
+    roof = {"kernel": f"{kname}: {dom} ({', '.join(table[dom]['stages'])}), {n} launches per block",
+            "bound": "mfma", "achieved": round(tf / 1e12, 1), "peak": PEAK_FP16 / 1e12, "unit": "TFLOP/s",
+            "frac": round(tf / PEAK_FP16, 4), "traffic": traffic, "avg_launch_us": round(ms * 1e3 / n, 2),
+            "gflop_per_launch": round(flops / n / 1e9, 3), "alg_bytes_per_launch": int(nbytes // n),
+            "share_of_block": table[dom]["share_of_block"]}
+    return {"block_us_staged": round(block_us, 1), "families": table}, roof
 
 
-def kernel_probe(reps):
-    """Launches only the dominant kernel (MLP-up GEMM, `reps` times) and a 256 MiB device-to-device copy (3 times,
+def kernel_probe(reps, family):
+    """Launches only one kernel family's in-step launches (`reps` times) and a 256 MiB device-to-device copy (3 times,
     the byte-count calibration of the FETCH_SIZE / WRITE_SIZE counters), for `rocprofv3 --pmc` passes."""
     from hexanima_amd import hip
     hip.init(0)
     L = hip.lib()
     s = C.c_void_p()
     hip.check(L.hxa_stream_create(C.byref(s)), "stream")
-    A = hip.DeviceArray((T, D), np.float16)
-    W = hip.DeviceArray((F, D), np.float16)
-    O = hip.DeviceArray((T, F), np.float16)
-    hip.check(L.hxa_fill_normal(A.ptr, 1, T * D, 11, 0.0, 1.0, s), "fill")
-    hip.check(L.hxa_fill_normal(W.ptr, 1, F * D, 12, 0.0, 0.02, s), "fill")
+    fam, keep = family_launchers(L, hip, s)
+    fn, n, flops, nbytes, kname = fam[family]
     for _ in range(reps):
-        hip.check(L.hxa_gemm(A.ptr, D, T, WFMT, W.ptr, None, None, F, D, 1, hip.EPI_GELU_TANH, O.ptr, F, 0, None, 0,
-                             None, None, 0, 0, s), "gemm")
+        fn()
     nb = 256 << 20
     src = hip.DeviceArray((nb,), np.uint8)
     dst = hip.DeviceArray((nb,), np.uint8)
@@ -288,12 +399,76 @@ def kernel_probe(reps):
     for _ in range(3):
         hip.check(L.hxa_d2d(dst.ptr, src.ptr, nb), "copy")
     hip.check(L.hxa_stream_sync(s), "sync")
-    print(f"kernel probe: {reps} x gemm {T}x{D}x{F} GELU, 3 x copy {nb} B", flush=True)
+    print(f"kernel probe: {reps} x {family} ({n} launches, {kname}, {nbytes / n:.0f} algorithmic bytes per launch),"
+          f" 3 x copy {nb} B", flush=True)
+
+
+BLK_W_END, BLK_GAIN, BLK_MODW, BLK_TOTAL = 125829120, 125829120, 125833216, 138416128  # blk_wlayout.h:3-20
+
+
+def abi_chain(runs=3):
+    """The 28 blocks through the reference ABI the way megarun drives them (megarun.cpp:132-195): hxa_run, the
+    megarun protocol on mega_open / mega_block, as a child process holding 28 registered fp16 blkNN.bin buffers
+    (one synthetic file: N(0, 0.02) fp16 weights and modulation weights, q/k gains 1/sqrt(128)), 1536 tokens
+    (48 x 32 grid) and 512 context tokens. Per `run`: GPU modulation of the 28 blocks, then 28 mega_block calls,
+    FIRST on the first (x uploaded) and REL on the last (x downloaded). One warm-up run converts the weights."""
+    import subprocess
+    import tempfile
+    exe = os.path.join(ROOT, "hexanima_amd", "hxa_run")
+    if not os.access(exe, os.X_OK):
+        raise RuntimeError(f"{exe} is not built")
+    rng = np.random.default_rng(77)
+    buf = np.zeros(BLK_TOTAL, np.uint8)
+    buf[:BLK_W_END] = (rng.standard_normal(BLK_W_END // 2, dtype=np.float32) * 0.02).astype(np.float16).view(np.uint8)
+    gain = np.concatenate([np.full(128, 128 ** -0.5), np.ones(128), np.full(128, 128 ** -0.5), np.ones(128)])
+    buf[BLK_GAIN:BLK_GAIN + 2048] = gain.astype(np.float32).view(np.uint8)
+    buf[BLK_MODW:] = (rng.standard_normal((BLK_TOTAL - BLK_MODW) // 2, dtype=np.float32) * 0.02).astype(np.float16).view(np.uint8)
+    gh, gw, nctx = 48, 32, 512
+    with tempfile.TemporaryDirectory() as td:
+        buf.tofile(os.path.join(td, "blk00.bin"))
+        del buf
+        for i in range(1, NBLK):
+            os.symlink("blk00.bin", os.path.join(td, f"blk{i:02d}.bin"))
+        rng.standard_normal((D, gh * gw), dtype=np.float32).tofile(os.path.join(td, "x.raw"))
+        rng.standard_normal(D, dtype=np.float32).tofile(os.path.join(td, "emb.raw"))
+        (rng.standard_normal(6144, dtype=np.float32) * 0.1).tofile(os.path.join(td, "lora.raw"))
+        rng.standard_normal((1024, nctx), dtype=np.float32).tofile(os.path.join(td, "ctx.raw"))
+        cmd = f"run {td}/x.raw {td}/emb.raw {td}/lora.raw {td}/ctx.raw {td}/out.raw {gh} {gw}\n"
+        env = dict(os.environ, HXA_RUN_DBG="1")
+        t0 = time.perf_counter()
+        r = subprocess.run([exe, td, "0", str(NBLK)], input=cmd * (runs + 1) + "quit\n", capture_output=True, text=True,
+                           timeout=900, env=env)
+        wall = time.perf_counter() - t0
+        done = [ln for ln in r.stdout.splitlines() if ln.startswith("done ")]
+        if r.returncode != 0 or len(done) != runs + 1:
+            raise RuntimeError(f"hxa_run failed ({r.returncode}): {r.stdout[-500:]} {r.stderr[-2000:]}")
+        split = [ln for ln in r.stderr.splitlines() if ln.startswith("run: ")]
+        blocks_ms = [float(ln.split("modulation+blocks ")[1].split(" ms")[0]) for ln in split][1:]
+        out = np.fromfile(os.path.join(td, "out.raw"), np.float32)
+        if out.size != D * gh * gw or not np.isfinite(out).all():
+            raise RuntimeError("hxa_run output missing or non-finite")
+    ms = float(np.median(blocks_ms))
+    return {"modulation_plus_28_blocks_ms": round(ms, 2), "per_block_ms": round(ms / NBLK, 3),
+            "run_ms_incl_file_io": [int(ln.split()[1]) for ln in done[1:]],
+            "first_run_ms_incl_weight_conversion": int(done[0].split()[1]), "process_wall_s": round(wall, 1),
+            "config": "hxa_run (megarun protocol), 28 fp16 blkNN.bin, 1536 tokens, 512 context tokens, mod on GPU"}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline():
-    """The oracle (C port of the reference block, OpenMP) on one 1536-token block, scaled to a 28-block step."""
+    """The oracle (C port of the reference block, built for this host with -march=native and OpenMP) on whole
+    1536-token blocks, scaled to the 28-block step, and on one 1536 x 2048 x 8192 fp16 GEMM (double accumulation)."""
     from oracle import hxo
+    flags = hxo.use_native()
     threads = hxo.set_threads(0)
     rng = np.random.default_rng(3)
     w = {}
@@ -305,14 +480,30 @@ def cpu_baseline():
     ctx = rng.standard_normal((C_TXT, DC), dtype=np.float32).astype(np.float16)
     mod9 = (rng.standard_normal((9, D), dtype=np.float32) * 0.2)
     cos, sin = hxo.rope_anima(LAT[1] // 2, LAT[2] // 2)
-    # bounded sample: whole 1536-token blocks (each feeding the next, as in a step) until ~10 s of CPU work
+    # bounded sample: whole 1536-token blocks (each feeding the next, as in a step) until ~12 s of CPU work
     nblk, t0 = 0, time.perf_counter()
-    while nblk < NBLK and (nblk == 0 or time.perf_counter() - t0 < 10.0):
+    while nblk < NBLK and (nblk == 0 or time.perf_counter() - t0 < 12.0):
         x, _, _ = hxo.anima_block(x, ctx, mod9, cos, sin, w, H=H, F=F, gelu=1)
         nblk += 1
     tb = (time.perf_counter() - t0) / nblk
+    A = rng.standard_normal((T, D), dtype=np.float32).astype(np.float16)
+    hxo.gemm(A[:64], w["w1"])
+    t0 = time.perf_counter()
+    for _ in range(2):
+        hxo.gemm(A, w["w1"])
+    tg = (time.perf_counter() - t0) / 2
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count()
     return {"value": round(1.0 / (NBLK * tb), 5), "unit": "steps/s", "cores": threads, "kind": "port",
-            "sample": f"{nblk} chained 1536-token blocks on the C oracle ({tb:.2f} s each), scaled to the 28-block step"}
+            "sample": f"{nblk} chained 1536-token blocks on the C oracle ({tb:.2f} s each), scaled to the 28-block "
+                      f"step; 2 GEMMs 1536x2048x8192",
+            "block_ms": round(tb * 1e3, 1), "steps_per_s_batch4": round(1.0 / (4 * NBLK * tb), 6),
+            "steps_per_s_batch4_basis": "4 x the batch-1 block time (the oracle block runs one image; the work is 4x)",
+            "gemm_1536x2048x8192_gflops": round(2 * T * D * F / tg / 1e9, 1),
+            "nproc": aff, "cpu_model": _cpu_model(), "threads": threads, "compiler": flags,
+            "label": "baseline only"}
 
 
 def main():
@@ -322,31 +513,33 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
-                    help="leave out the other DiT workloads and the kernel microbenchmarks (for a kernel trace of the step)")
+                    help="leave out the other DiT workloads, the kernel microbenchmarks and the ABI chain (for a "
+                         "kernel trace of the step)")
     ap.add_argument("--workload", choices=sorted(EXTRA_DITS), default=None,
                     help="time only this other DiT workload and print its JSON (for a kernel trace of it)")
     ap.add_argument("--kernel-probe", type=int, default=0, metavar="REPS",
-                    help="only launch the dominant kernel REPS times plus a copy calibration (for rocprofv3 --pmc)")
+                    help="only launch one kernel family REPS times plus a copy calibration (for rocprofv3 --pmc)")
+    ap.add_argument("--probe-family", default="gemm_splitk",
+                    choices=["gemm_splitk", "gemm_pp_mlp_up", "gemm_pp_qkv_headnorm", "attention"])
+    ap.add_argument("--abi-chain", action="store_true", help="only time the 28-block mega_block chain (hxa_run)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build targets a single MI355X (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     if a.kernel_probe:
-        kernel_probe(a.kernel_probe)
+        kernel_probe(a.kernel_probe, a.probe_family)
+        return
+    if a.abi_chain:
+        print(json.dumps({"abi_chain": abi_chain()}), flush=True)
         return
     if a.workload:
         from hexanima_amd import hip
         hip.init(0)
         print(json.dumps({a.workload: EXTRA_DITS[a.workload]()}), flush=True)
         return
-    info, ms_step, up_ms = gpu_run(a.steps, a.warmup)
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic_gemm_mlp_up_1536x2048x8192.txt")
-    if os.path.exists(tpath):  # rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated (see that file)
-        for line in open(tpath):
-            if line.startswith("hbm_bytes_per_launch:"):
-                traffic = int(line.split(":")[1])
-    up_tf = UP_FLOPS / (up_ms * 1e-3)
+    info, ms_step = gpu_run(a.steps, a.warmup)
+    from hexanima_amd import hip
+    kernels, roof = kernel_breakdown(hip.lib(), hip)
     res = {
         "metric": "DiT denoise steps/s at 1536 tok (2B fp16, 2.9B q8); GEMM+attn % MFMA peak",
         "value": round(1000.0 / ms_step, 3),
@@ -365,14 +558,16 @@ def main():
                    "seq_len": T, "parallelism": "single GPU"},
         "step_tflops": round(STEP_FLOPS / (ms_step * 1e-3) / 1e12, 1),
         "step_frac_of_fp16_peak": round(STEP_FLOPS / (ms_step * 1e-3) / PEAK_FP16, 4),
-        "roofline": {"kernel": f"{info['up_kernel']}, fp16 k-tiled W, GELU epilogue: MLP up {T}x{D}x{F}", "bound": "mfma",
-                     "achieved": round(up_tf / 1e12, 1), "peak": PEAK_FP16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(up_tf / PEAK_FP16, 4), "traffic": traffic, "avg_launch_us": round(up_ms * 1e3, 2)},
+        "roofline": roof,
+        "kernels": kernels,
         "device": info.get("name"),
     }
+    print(json.dumps({"progress": "step, kernels done"}), file=sys.stderr, flush=True)
     if not a.no_extras:
         res.update(extra_dits())
         res["microbench"] = microbench()
+        res["abi_chain"] = abi_chain()
+        res["abi_chain"]["graph_step_ms_for_comparison"] = round(ms_step, 3)
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)

@@ -338,7 +338,7 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   const bool small = fill(96) > fill(128) + 1e-9;
   const int QB = small ? 96 : 128, nqb = (p.T + QB - 1) / QB;
   dim3 grid(nqb * p.H, p.batch);
-  if (small) hipLaunchKernelGGL(attn_kernel<3>, grid, dim3(384), LDS_BYTES, st, p, nqb);
-  else hipLaunchKernelGGL(attn_kernel<4>, grid, dim3(512), LDS_BYTES, st, p, nqb);
+  if (small) hxa_launch(attn_kernel<3>, grid, dim3(384), LDS_BYTES, st, p, nqb);
+  else hxa_launch(attn_kernel<4>, grid, dim3(512), LDS_BYTES, st, p, nqb);
   return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
 }

@@ -552,7 +552,7 @@ int hxa_resid2_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t,
   switch ((D + 1023) / 1024) {
 #define HXA_NORMROW(V)                                                                                            \
   case V:                                                                                                          \
-    hipLaunchKernelGGL(normrow_kernel<V>, dim3(T), dim3(256), 0, st, x, ldx, D, t, t2, ldt, gate, shift, scale, w, eps, \
+    hxa_launch(normrow_kernel<V>, dim3(T), dim3(256), 0, st, x, ldx, D, t, t2, ldt, gate, shift, scale, w, eps, \
                        h, ldh);                                                                                    \
     break;
     HXA_NORMROW(1) HXA_NORMROW(2) HXA_NORMROW(3) HXA_NORMROW(4)
@@ -572,63 +572,63 @@ int hxa_rmsrope_launch(hxa_h *q0, hxa_h *q1, const float *g0, const float *g1, l
                        const float *sinT, int ttab, hipStream_t st) {
   if (T <= 0 || H <= 0 || (cosT && ttab <= 0) || ldq % 8 || (uintptr_t)q0 % 16 || (uintptr_t)q1 % 16) return HXA_E_ARG;
   dim3 g(nblk((long)T * H, 32), q1 ? 2 : 1);
-  hipLaunchKernelGGL(rmsrope_kernel, g, dim3(256), 0, st, q0, q1, g0, g1, ldq, T, H, cosT, sinT, ttab > 0 ? ttab : 1);
+  hxa_launch(rmsrope_kernel, g, dim3(256), 0, st, q0, q1, g0, g1, ldq, T, H, cosT, sinT, ttab > 0 ? ttab : 1);
   return LAUNCH_OK();
 }
 
 int hxa_resadd2_launch(float *x, long ldx, const hxa_h *t1, const hxa_h *t2, long ldt, int T, int D, const float *gate,
                        hipStream_t st) {
   if (D % 4 || ldx % 4 || ldt % 4) return HXA_E_ARG;
-  hipLaunchKernelGGL(resadd2_kernel, dim3(nblk((long)T * D / 4)), dim3(256), 0, st, x, ldx, t1, t2, ldt, T, D, gate);
+  hxa_launch(resadd2_kernel, dim3(nblk((long)T * D / 4)), dim3(256), 0, st, x, ldx, t1, t2, ldt, T, D, gate);
   return LAUNCH_OK();
 }
 
 int hxa_x32_to_rows_launch(const float *tiles, float *x, int R, int C, hipStream_t st) {
   if (R % 32 || C % 32) return HXA_E_ARG;
-  hipLaunchKernelGGL(x32_to_rows_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, tiles, x, R, C);
+  hxa_launch(x32_to_rows_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, tiles, x, R, C);
   return LAUNCH_OK();
 }
 int hxa_rows_to_x32_launch(const float *x, float *tiles, int R, int C, hipStream_t st) {
   if (R % 32 || C % 32) return HXA_E_ARG;
-  hipLaunchKernelGGL(rows_to_x32_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, x, tiles, R, C);
+  hxa_launch(rows_to_x32_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, x, tiles, R, C);
   return LAUNCH_OK();
 }
 int hxa_h16_to_rows_launch(const hxa_h *tiles, hxa_h *a, long lda, int R, int C, hipStream_t st) {
   if (R % 32 || C % 32) return HXA_E_ARG;
-  hipLaunchKernelGGL(h16_to_rows_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, tiles, a, lda, R, C);
+  hxa_launch(h16_to_rows_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, tiles, a, lda, R, C);
   return LAUNCH_OK();
 }
 int hxa_rows_to_h16_launch(const hxa_h *a, long lda, hxa_h *tiles, int R, int C, int transposed, hipStream_t st) {
   if (R % 32 || C % 32) return HXA_E_ARG;
-  hipLaunchKernelGGL(rows_to_h16_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, a, lda, tiles, R, C, transposed);
+  hxa_launch(rows_to_h16_kernel, dim3(nblk((long)R * C)), dim3(256), 0, st, a, lda, tiles, R, C, transposed);
   return LAUNCH_OK();
 }
 int hxa_cs_to_rows_launch(const float *tiles, float *rows, int T, hipStream_t st) {
   if (T % 32) return HXA_E_ARG;
-  hipLaunchKernelGGL(cs_to_rows_kernel, dim3(nblk((long)T * 64)), dim3(256), 0, st, tiles, rows, T);
+  hxa_launch(cs_to_rows_kernel, dim3(nblk((long)T * 64)), dim3(256), 0, st, tiles, rows, T);
   return LAUNCH_OK();
 }
 
 int hxa_fill_normal_launch(void *dst, int dtype, size_t n, uint64_t seed, float mean, float std, hipStream_t st) {
   if (n == 0) return HXA_OK;
-  hipLaunchKernelGGL(fill_normal_kernel, dim3(nblk((long)n)), dim3(256), 0, st, dst, dtype, n, seed, mean, std);
+  hxa_launch(fill_normal_kernel, dim3(nblk((long)n)), dim3(256), 0, st, dst, dtype, n, seed, mean, std);
   return LAUNCH_OK();
 }
 int hxa_fill_uniform_int_launch(void *dst, int bits, size_t n, uint64_t seed, int lo, int hi, hipStream_t st) {
   if (n == 0) return HXA_OK;
   if (hi < lo || (bits != 8 && bits != 4)) return HXA_E_ARG;
-  hipLaunchKernelGGL(fill_uniform_int_kernel, dim3(nblk((long)n)), dim3(256), 0, st, dst, bits, n, seed, lo, hi);
+  hxa_launch(fill_uniform_int_kernel, dim3(nblk((long)n)), dim3(256), 0, st, dst, bits, n, seed, lo, hi);
   return LAUNCH_OK();
 }
 int hxa_fill_const_launch(void *dst, int dtype, size_t n, float v, hipStream_t st) {
   if (n == 0) return HXA_OK;
-  hipLaunchKernelGGL(fill_const_kernel, dim3(nblk((long)n)), dim3(256), 0, st, dst, dtype, n, v);
+  hxa_launch(fill_const_kernel, dim3(nblk((long)n)), dim3(256), 0, st, dst, dtype, n, v);
   return LAUNCH_OK();
 }
 
 int hxa_patchify_launch(const float *lat, int B, int Cc, int H, int W, float *tok, hipStream_t st) {
   if (H % 2 || W % 2) return HXA_E_ARG;
-  hipLaunchKernelGGL(patchify_kernel, dim3(nblk((long)B * Cc * H * W)), dim3(256), 0, st, lat, B, Cc, H, W, tok);
+  hxa_launch(patchify_kernel, dim3(nblk((long)B * Cc * H * W)), dim3(256), 0, st, lat, B, Cc, H, W, tok);
   return LAUNCH_OK();
 }
 
@@ -637,11 +637,11 @@ int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W
   if (M <= 0 || K <= 0 || N <= 0) return HXA_E_ARG;
   if (M <= 8) {
     if (K % 2) return HXA_E_ARG;
-    hipLaunchKernelGGL(gemv_kernel, dim3(nblk(N, 4)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy, act, bias,
+    hxa_launch(gemv_kernel, dim3(nblk(N, 4)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy, act, bias,
                        split > 0 ? split : N, gap);
   } else {
     if (act != 0 || bias != nullptr || split > 0) return HXA_E_ARG;
-    hipLaunchKernelGGL(linear_smallk_kernel, dim3(nblk(N, 64), nblk(M, 64)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy);
+    hxa_launch(linear_smallk_kernel, dim3(nblk(N, 64), nblk(M, 64)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy);
   }
   return LAUNCH_OK();
 }
@@ -653,7 +653,7 @@ int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, 
   constexpr int RPW = 8;
   const dim3 grid((unsigned)((N + 4 * RPW - 1) / (4 * RPW)));
 #define HXA_MODGEMV(KC, EPL)                                                                                       \
-  hipLaunchKernelGGL((modgemv_kernel<KC, EPL>), grid, dim3(256), 0, st, x, W, N, y, per, ostride, split, gap, act, RPW)
+  hxa_launch((modgemv_kernel<KC, EPL>), grid, dim3(256), 0, st, x, W, N, y, per, ostride, split, gap, act, RPW)
   if (K % 512) {
     switch (K / 256) {
       case 1: HXA_MODGEMV(1, 4); break;
@@ -696,7 +696,7 @@ int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float
     lds_set = lds;
   }
   const int ntok = B * T;
-  hipLaunchKernelGGL(final_kernel, dim3((ntok + FT - 1) / FT), dim3(256), lds, st, x, T, xrows, D, shift, scale, Wf, Cc,
+  hxa_launch(final_kernel, dim3((ntok + FT - 1) / FT), dim3(256), lds, st, x, T, xrows, D, shift, scale, Wf, Cc,
                      H, W, lat, dtp, ntok, normw, x0rows, zrows);
   return LAUNCH_OK();
 }
@@ -732,6 +732,30 @@ __global__ __launch_bounds__(256) void grouped_gemv_kernel(const float *__restri
   }
   acc = wave_sum(acc);
   if (lane == 0) y[(long)g * ldy + n] = acc + (bias ? bias[n] : 0.0f);
+}
+// Groups of GEMV rows whose weights sit in separate allocations: group g reads x + g * x_gs (SiLU applied on load
+// when act == 1), weight rows Wp[g / gpp] + w_off + (g % gpp) * w_gs ([N][K] fp16) and writes y + g * y_gs [N],
+// plus bias. Same per-lane order of the products as gemv_kernel, so the same sums.
+__global__ __launch_bounds__(256) void ptr_gemv_kernel(const float *__restrict__ x, long x_gs, int act,
+                                                       const hxa_h *const *__restrict__ Wp, int gpp, long w_off, long w_gs,
+                                                       int N, int K, const float *__restrict__ bias, float *__restrict__ y,
+                                                       long y_gs) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63, g = blockIdx.y;
+  if (n >= N) return;
+  const hxa_h *wr = Wp[g / gpp] + w_off + (long)(g % gpp) * w_gs + (long)n * K;
+  const float *xg = x + (long)g * x_gs;
+  float acc = 0.0f;
+  for (int k = lane * 2; k < K; k += 128) {
+    const half2_t wv = *(const half2_t *)(wr + k);
+    float x0 = xg[k], x1 = xg[k + 1];
+    if (act == 1) {
+      x0 = x0 / (1.0f + __expf(-x0));
+      x1 = x1 / (1.0f + __expf(-x1));
+    }
+    acc = fmaf(x0, (float)wv[0], fmaf(x1, (float)wv[1], acc));
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) y[(long)g * y_gs + n] = acc + (bias ? bias[n] : 0.0f);
 }
 // rapid-moss input (mossrun.cpp:316-320): per image token t, xin = z_t + Q x0_t (Q fp32 [C4][C4]) and the token's
 // row x = Wv xin + bv (Wv fp16 [D][C4]); FT tokens per workgroup, their xin in LDS, each weight row read once
@@ -785,38 +809,45 @@ __global__ void bn_unpatchify_kernel(const float *__restrict__ x0, const float *
 
 int hxa_rmsvec_launch(const float *x, int n, const hxa_h *w, float eps, float *y, hipStream_t st) {
   if (n <= 0 || n > 4096) return HXA_E_ARG;
-  hipLaunchKernelGGL(rmsvec_kernel, dim3(1), dim3(256), 0, st, x, n, w, eps, y);
+  hxa_launch(rmsvec_kernel, dim3(1), dim3(256), 0, st, x, n, w, eps, y);
   return LAUNCH_OK();
 }
 int hxa_grouped_gemv_launch(const float *x, long ldx, const hxa_h *W, int G, int N, int K, const float *bias, float *y,
                             long ldy, hipStream_t st) {
   if (G <= 0 || N <= 0 || K <= 0 || K % 2 || G > 65535) return HXA_E_ARG;
-  hipLaunchKernelGGL(grouped_gemv_kernel, dim3(nblk(N, 4), G), dim3(256), 0, st, x, ldx, W, N, K, bias, y, ldy);
+  hxa_launch(grouped_gemv_kernel, dim3(nblk(N, 4), G), dim3(256), 0, st, x, ldx, W, N, K, bias, y, ldy);
+  return LAUNCH_OK();
+}
+int hxa_ptr_gemv_launch(const float *x, long x_gs, int act, const hxa_h *const *Wp, int G, int gpp, long w_off, long w_gs,
+                        int N, int K, const float *bias, float *y, long y_gs, hipStream_t st) {
+  if (G <= 0 || gpp <= 0 || N <= 0 || K <= 0 || K % 2 || G > 65535 || !Wp) return HXA_E_ARG;
+  hxa_launch(ptr_gemv_kernel, dim3(nblk(N, 4), G), dim3(256), 0, st, x, x_gs, act, Wp, gpp, w_off, w_gs, N, K, bias, y,
+             y_gs);
   return LAUNCH_OK();
 }
 int hxa_moss_embed_launch(const float *z, const float *x0, const float *Q, const hxa_h *Wv, const float *bv, float *x, int B,
                           int T, int xrows, int D, int C4, hipStream_t st) {
   if (C4 % 2 || C4 > 512 || B <= 0 || T <= 0 || xrows < T) return HXA_E_ARG;
   const int ntok = B * T;
-  hipLaunchKernelGGL(moss_embed_kernel, dim3((ntok + FT - 1) / FT), dim3(256), sizeof(float) * FT * C4, st, z, x0, Q, Wv,
+  hxa_launch(moss_embed_kernel, dim3((ntok + FT - 1) / FT), dim3(256), sizeof(float) * FT * C4, st, z, x0, Q, Wv,
                      bv, x, T, xrows, D, C4, ntok);
   return LAUNCH_OK();
 }
 int hxa_bn_unpatchify_launch(const float *x0, const float *mean, const float *var, int B, int Cc, int H, int W, float *lat,
                              hipStream_t st) {
-  hipLaunchKernelGGL(bn_unpatchify_kernel, dim3(nblk((long)B * Cc * H * W)), dim3(256), 0, st, x0, mean, var, B, Cc, H, W,
+  hxa_launch(bn_unpatchify_kernel, dim3(nblk((long)B * Cc * H * W)), dim3(256), 0, st, x0, mean, var, B, Cc, H, W,
                      lat);
   return LAUNCH_OK();
 }
 
 int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t st) {
-  hipLaunchKernelGGL(sinusoid_kernel, dim3(nblk((long)n * dim / 2)), dim3(256), 0, st, t, n, dim, out);
+  hxa_launch(sinusoid_kernel, dim3(nblk((long)n * dim / 2)), dim3(256), 0, st, t, n, dim, out);
   return LAUNCH_OK();
 }
 int hxa_quantize_launch(const float *W, int N, int K, int fmt, void *q, hxa_h *s, hipStream_t st) {
   const int kt = (fmt & HXA_W_KTILED) ? 1 : 0;
   fmt &= ~HXA_W_KTILED;
   if (K % 32 || (fmt != HXA_W_Q8 && fmt != HXA_W_Q4)) return HXA_E_ARG;
-  hipLaunchKernelGGL(quantize_kernel, dim3(nblk((long)N * (K / 32))), dim3(256), 0, st, W, N, K, fmt, kt, q, s);
+  hxa_launch(quantize_kernel, dim3(nblk((long)N * (K / 32))), dim3(256), 0, st, W, N, K, fmt, kt, q, s);
   return LAUNCH_OK();
 }

@@ -872,7 +872,7 @@ hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
     attr = true;
   }
   dim3 grid(p.tiles_m * p.tiles_n, 1, ksplit);
-  hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, st, p);
+  hxa_launch(kern, grid, dim3(64 * NW), lds, st, p);
   return hipGetLastError();
 }
 
@@ -894,7 +894,7 @@ hipError_t launch_pp(const GemmParams &p, int ksplit, hipStream_t st) {
     attr = true;
   }
   dim3 grid(p.tiles_m * p.tiles_n, 1, ksplit);
-  hipLaunchKernelGGL(kern, grid, dim3(512), G::LDS, st, p);
+  hxa_launch(kern, grid, dim3(512), G::LDS, st, p);
   return hipGetLastError();
 }
 
@@ -1112,7 +1112,7 @@ hipError_t launch_pair_t(const GemmParams &p0, const GemmParams &p1, hipStream_t
     attr = true;
   }
   const int n0 = p0.tiles_m * p0.tiles_n;
-  hipLaunchKernelGGL(kern, dim3(n0 + p1.tiles_m * p1.tiles_n), dim3(64 * NW), G::LDS, st, p0, p1, n0);
+  hxa_launch(kern, dim3(n0 + p1.tiles_m * p1.tiles_n), dim3(64 * NW), G::LDS, st, p0, p1, n0);
   return hipGetLastError();
 }
 template <int FMT, bool ASYM>
@@ -1212,8 +1212,8 @@ int hxa_dequant_launch(const HxaWeight &w0, hxa_h *out, hipStream_t st) {
   p.w_gs = wkt ? cb * w.N : cb;
   const long slots = (long)(w.K / 32) * w.N * 4;
   const dim3 grid((unsigned)((slots + 255) / 256));
-  if (w.fmt == HXA_W_Q8) hipLaunchKernelGGL((dequant_kernel<HXA_W_Q8, false>), grid, dim3(256), 0, st, p, out);
-  else if (w.z) hipLaunchKernelGGL((dequant_kernel<HXA_W_Q4, true>), grid, dim3(256), 0, st, p, out);
-  else hipLaunchKernelGGL((dequant_kernel<HXA_W_Q4, false>), grid, dim3(256), 0, st, p, out);
+  if (w.fmt == HXA_W_Q8) hxa_launch((dequant_kernel<HXA_W_Q8, false>), grid, dim3(256), 0, st, p, out);
+  else if (w.z) hxa_launch((dequant_kernel<HXA_W_Q4, true>), grid, dim3(256), 0, st, p, out);
+  else hxa_launch((dequant_kernel<HXA_W_Q4, false>), grid, dim3(256), 0, st, p, out);
   return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
 }

@@ -1,6 +1,7 @@
 // Shared definitions for the MI355X (gfx950) kernels of the DiT block runner.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 typedef _Float16 hxa_h;
@@ -13,6 +14,24 @@ typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
 
 #define HXA_DEV __device__ __forceinline__
+
+// Stage timing of a block run (host side, per thread): while hxa_t_stage_event is set, every launch binds it as
+// its stop event (hipExtLaunchKernel), so the event completes with the last kernel of the stage and no marker packet
+// sits between the kernels. hxa_t_stage_launches counts the launches since the event was set.
+extern thread_local hipEvent_t hxa_t_stage_event;
+extern thread_local int hxa_t_stage_launches;
+template <typename F, typename... Args>
+inline void hxa_launch(F kernel, const dim3 &grid, const dim3 &block, uint32_t shmem, hipStream_t st, Args... args) {
+  if (hxa_t_stage_event != nullptr) {
+    ++hxa_t_stage_launches;
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, st, nullptr, hxa_t_stage_event, 0, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shmem, st, args...);
+  }
+}
+
+// devices with per-device host-side state (the no-allocation scratch address, the stage-timing events)
+constexpr int HXA_MAX_DEVICES = 64;
 
 // status codes, weight formats (HXA_W_*) and GEMM epilogues (HXA_EPI_*) are those of the public C-ABI
 #include "../../include/hexanima_hip.h"

@@ -100,6 +100,9 @@ int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float
 // the reference's own DiT glue: vector RMSNorm * w (fp16 w), G GEMVs with their own inputs, the rapid-moss latent mix +
 // video embedding, and BN denorm + unpatchify of the x0 token rows
 int hxa_rmsvec_launch(const float *x, int n, const hxa_h *w, float eps, float *y, hipStream_t st);
+// group g of G: y + g*y_gs = act(x + g*x_gs) . (Wp[g / gpp] + w_off + (g % gpp)*w_gs)^T (+ bias); act 1 = SiLU
+int hxa_ptr_gemv_launch(const float *x, long x_gs, int act, const hxa_h *const *Wp, int G, int gpp, long w_off, long w_gs,
+                        int N, int K, const float *bias, float *y, long y_gs, hipStream_t st);
 int hxa_grouped_gemv_launch(const float *x, long ldx, const hxa_h *W, int G, int N, int K, const float *bias, float *y,
                             long ldy, hipStream_t st);
 int hxa_moss_embed_launch(const float *z, const float *x0, const float *Q, const hxa_h *Wv, const float *bv, float *x, int B,

@@ -18,15 +18,14 @@
 namespace {
 static __device__ __align__(256) uint8_t scratch[HXA_NOALLOC_WS_MAX];
 
-constexpr int MAX_DEVICES = 64;
-void *g_scratch[MAX_DEVICES];  // device address of `scratch` on each device (the host name is only a stand-in)
+void *g_scratch[HXA_MAX_DEVICES];  // device address of `scratch` on each device (the host name is only a stand-in)
 std::mutex g_scratch_mu;
 }  // namespace
 
 // Resolves the device address of `scratch` on the current device, once per device.
 int hxa_noalloc_setup(void **out) {
   int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= HXA_MAX_DEVICES)
     return hxa_set_error(HXA_E_RESOURCE, "noalloc: no current HIP device");
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (g_scratch[dev] == nullptr) {

@@ -516,32 +516,70 @@ static int check_dims(const hxa_block_dims *d) {
   return HXA_OK;
 }
 
+// The stage events of one thread, created on first use on a device and kept: a timed block records up to 25 of
+// them, and creating and destroying that many per call costs more host time than a block's launches (the reference
+// ABI asks for stage times on every call). One set per thread and device; a StageTimer uses it from construction
+// until its destructor has read the times, and block calls on one thread do not nest. The events are never
+// destroyed (a thread-exit destructor could run after the HIP runtime has shut down); they end with the process.
+struct ThreadEvents {
+  std::vector<hipEvent_t> ev[HXA_MAX_DEVICES];
+};
+static thread_local ThreadEvents t_events;
+
+thread_local hipEvent_t hxa_t_stage_event = nullptr;
+thread_local int hxa_t_stage_launches = 0;
+
+// Stage i's time is the interval from event i to event i+1: event 0 is recorded before the first stage, event i+1
+// completes with the last kernel stage i launched (bound to its launches through hxa_t_stage_event), or is recorded
+// as a marker when the stage launched nothing.
 struct StageTimer {
   int *us;
   int n;
   hipStream_t st;
-  std::vector<hipEvent_t> ev;
+  hipEvent_t *ev = nullptr;
   int count = 0;
   StageTimer(int *u, int nn, hipStream_t s) : us(u), n(nn), st(s) {
-    if (us) {
-      ev.resize(n + 1);
-      for (auto &e : ev) (void)hipEventCreate(&e);
-      (void)hipEventRecord(ev[0], st);
+    if (!us) return;
+    if (n < 1) {
+      us = nullptr;
+      return;
     }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= HXA_MAX_DEVICES) {
+      us = nullptr;  // no timing: the stages report 0
+      return;
+    }
+    std::vector<hipEvent_t> &pool = t_events.ev[dev];
+    while ((int)pool.size() < n + 1) {
+      hipEvent_t e;
+      if (hipEventCreate(&e) != hipSuccess) break;
+      pool.push_back(e);
+    }
+    if ((int)pool.size() < n + 1) {
+      us = nullptr;
+      return;
+    }
+    ev = pool.data();
+    (void)hipEventRecord(ev[0], st);
+    hxa_t_stage_event = ev[1];
+    hxa_t_stage_launches = 0;
   }
   void tick() {
     count++;
-    if (us && count <= n) (void)hipEventRecord(ev[count], st);
+    if (!us || count > n) return;
+    if (hxa_t_stage_launches == 0) (void)hipEventRecord(ev[count], st);
+    hxa_t_stage_event = count < n ? ev[count + 1] : nullptr;
+    hxa_t_stage_launches = 0;
   }
   ~StageTimer() {
     if (!us) return;
+    hxa_t_stage_event = nullptr;
     (void)hipStreamSynchronize(st);
     for (int i = 0; i < n; i++) {
       float ms = 0.0f;
       if (i < count && hipEventElapsedTime(&ms, ev[i], ev[i + 1]) == hipSuccess) us[i] = (int)lrintf(ms * 1000.0f);
       else us[i] = 0;
     }
-    for (auto &e : ev) (void)hipEventDestroy(e);
   }
 };
 
@@ -866,6 +904,9 @@ struct Ctx {
   std::map<int, DevBlock> blocks;
   std::map<int, DevModw> modws;
   float *mod_dev = nullptr, *emb_dev = nullptr, *h1_dev = nullptr;
+  const hxa_h **modw_ptrs = nullptr;  // device table of the modulation weights of one hxa_anima_modulation call
+  size_t modw_ptrs_bytes = 0;
+  float *mod_pin = nullptr;  // pinned staging of mega_block's modulation vectors (9 x 3072 fp32 at most)
   size_t mod_dev_bytes = 0, emb_dev_bytes = 0, h1_dev_bytes = 0;
   // device-resident activations of the current run of blocks
   float *x = nullptr, *cosr = nullptr, *sinr = nullptr, *mod = nullptr, *stage = nullptr;
@@ -1027,8 +1068,9 @@ extern "C" int mega_close(remote_handle64 h) {
   for (auto &kv : c->blocks) (void)hipFree(kv.second.pack);
   for (auto &kv : c->modws) (void)hipFree(kv.second.w);
   for (void *p : {(void *)c->x, (void *)c->cosr, (void *)c->sinr, (void *)c->mod, (void *)c->ctx, c->ws, (void *)c->stage,
-                  (void *)c->mod_dev, (void *)c->emb_dev, (void *)c->h1_dev})
+                  (void *)c->mod_dev, (void *)c->emb_dev, (void *)c->h1_dev, (void *)c->modw_ptrs})
     if (p) (void)hipFree(p);
+  if (c->mod_pin) (void)hipHostFree(c->mod_pin);
   (void)hipStreamDestroy(c->st);
   delete c;
   return HXA_OK;
@@ -1120,7 +1162,13 @@ int run_ref_block(Ctx *c, const BlockCall &bc, const DevBlock &db, const HostBuf
     c->cur_T = bc.T;
     c->cur_C = bc.C;
   }
-  HIPC(hipMemcpyAsync(c->mod, modh, (size_t)(d.kind == 0 ? 9 : 6) * D * 4, hipMemcpyHostToDevice, st));
+  // the modulation through pinned memory: an asynchronous DMA instead of a staged pageable copy. The previous
+  // call's copy from mod_pin has completed (every call ends with a stream synchronisation).
+  const size_t modb = (size_t)(d.kind == 0 ? 9 : 6) * D * 4;
+  if (!c->mod_pin) HIPC(hipHostMalloc((void **)&c->mod_pin, (size_t)9 * 3072 * 4, hipHostMallocDefault));
+  if (modb > (size_t)9 * 3072 * 4) return fail(HXA_E_META, "modulation of %zu bytes", modb);
+  memcpy(c->mod_pin, modh, modb);
+  HIPC(hipMemcpyAsync(c->mod, c->mod_pin, modb, hipMemcpyHostToDevice, st));
   int us[16] = {0};
   const int nst = d.kind == 0 ? 13 : 8;
   const auto t_work = std::chrono::steady_clock::now();
@@ -1195,21 +1243,20 @@ extern "C" int hxa_anima_modulation(remote_handle64 h, const int *wfds, int coun
   hipStream_t st = c->st;
   const int D = ANIMA_D;
   TRY(ensure((void **)&c->emb_dev, &c->emb_dev_bytes, 4 * (D + 6144)));
-  TRY(ensure((void **)&c->h1_dev, &c->h1_dev_bytes, 4 * 3 * 256));
+  TRY(ensure((void **)&c->h1_dev, &c->h1_dev_bytes, 4 * 3 * 256 * (size_t)count));
   TRY(ensure((void **)&c->mod_dev, &c->mod_dev_bytes, (size_t)count * 9 * D * 4));
+  TRY(ensure((void **)&c->modw_ptrs, &c->modw_ptrs_bytes, sizeof(void *) * (size_t)count));
   float *emb_d = c->emb_dev, *lora_d = c->emb_dev + D;
+  std::vector<const hxa_h *> wp(count);
+  for (int k = 0; k < count; k++) TRY(modw_of(c, wfds[k], &wp[k]));
   HIPC(hipMemcpyAsync(emb_d, emb, 4 * D, hipMemcpyHostToDevice, st));
   HIPC(hipMemcpyAsync(lora_d, lora, 4 * 6144, hipMemcpyHostToDevice, st));
-  for (int k = 0; k < count; k++) {
-    const hxa_h *w = nullptr;
-    TRY(modw_of(c, wfds[k], &w));
-    // h1 = A silu(emb) for the three sites at once (megarun.cpp:160, :165)
-    TRY(hxa_linear_f32_launch(emb_d, D, 1, D, w, 3 * 256, c->h1_dev, 3 * 256, 1, nullptr, 0, 0, st));
-    // mod rows 3 site .. 3 site + 2 = lora + B_site h1_site (megarun.cpp:166-167)
-    for (int site = 0; site < 3; site++)
-      TRY(hxa_linear_f32_launch(c->h1_dev + 256 * site, 256, 1, 256, w + 3 * MODW_A + site * MODW_B, 6144,
-                                c->mod_dev + ((size_t)k * 9 + 3 * site) * D, 6144, 0, lora_d, 0, 0, st));
-  }
+  HIPC(hipMemcpyAsync(c->modw_ptrs, wp.data(), sizeof(void *) * (size_t)count, hipMemcpyHostToDevice, st));
+  // every block in two launches: h1_k = A_k silu(emb) for the three sites at once (megarun.cpp:160, :165), then
+  // mod rows 3 site .. 3 site + 2 of block k = lora + B_k,site h1_k,site (megarun.cpp:166-167)
+  TRY(hxa_ptr_gemv_launch(emb_d, 0, 1, c->modw_ptrs, count, 1, 0, 0, 3 * 256, D, nullptr, c->h1_dev, 3 * 256, st));
+  TRY(hxa_ptr_gemv_launch(c->h1_dev, 256, 0, c->modw_ptrs, 3 * count, 3, 3 * MODW_A, MODW_B, 6144, 256, lora_d,
+                          c->mod_dev, 3L * D, st));
   HIPC(hipMemcpyAsync(mod, c->mod_dev, (size_t)count * 9 * D * 4, hipMemcpyDeviceToHost, st));
   HIPC(hipStreamSynchronize(st));
   return HXA_OK;

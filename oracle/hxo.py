@@ -29,6 +29,18 @@ def build(force: bool = False) -> str:
     return _LIB_PATH
 
 
+def use_native() -> str:
+    """Build the oracle for this host's CPU (-march=native) and load that copy instead of the portable one; must be
+    called before the first oracle call. Returns the compiler command line used."""
+    global _LIB_PATH
+    if _lib is not None:
+        raise RuntimeError("the oracle is already loaded")
+    subprocess.run(["make", "-s", "-B", "-C", _HERE, "native"], check=True)
+    _LIB_PATH = os.path.join(_HERE, "_build", "libhxo_native.so")
+    return subprocess.run(["make", "-s", "-C", _HERE, "native-flags"], check=True, capture_output=True,
+                          text=True).stdout.strip()
+
+
 class _Cfg(C.Structure):
     _fields_ = [("T", I), ("D", I), ("H", I), ("C", I), ("DC", I), ("F", I), ("gelu", I), ("stop", I), ("attn_mode", I)]
 
@@ -57,7 +69,8 @@ class _MB(C.Structure):
 def lib():
     global _lib
     if _lib is None:
-        build()
+        if not _LIB_PATH.endswith("libhxo_native.so"):
+            build()
         lb = C.CDLL(_LIB_PATH)
         sig = {
             "hxo_f2h": (C.c_uint16, [C.c_float]),
