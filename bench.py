@@ -298,21 +298,31 @@ def family_launchers(L, hip, s):
     hip.check(L.hxa_fill_const(sn.ptr, 0, T * 64, 0.0, s), "fill")
     P = hip.EPI_PARTIAL
 
-    def splitk():  # o, cross-o (K = D) and MLP down (K = F): two fp16 K-half partials each
-        for A, lda, W, K in ((o, D, Wo, D), (o, D, Wco, D), (mid, F, W2, F)):
+    def splitk(hook=None):  # o, cross-o (K = D) and MLP down (K = F): two fp16 K-half partials each
+        for i, (A, lda, W, K) in enumerate(((o, D, Wo, D), (o, D, Wco, D), (mid, F, W2, F))):
+            if hook:
+                hook(i)
             hip.check(L.hxa_gemm(A.ptr, lda, T, WFMT, W.ptr, None, None, D, K, 2, P, part.ptr, D, T * D, None, 0, None,
                                  None, 0, 0, s), "gemm")
 
-    def mlp_up():
+    def mlp_up(hook=None):
+        if hook:
+            hook(0)
         hip.check(L.hxa_gemm(h.ptr, D, T, WFMT, W1.ptr, None, None, F, D, 1, hip.EPI_GELU_TANH, up.ptr, F, 0, None, 0,
                              None, None, 0, 0, s), "gemm")
 
-    def qkv():
+    def qkv(hook=None):
+        if hook:
+            hook(0)
         hip.check(L.hxa_gemm_headnorm(h.ptr, D, T, WFMT, Wqkv.ptr, None, None, 3 * D, D, qk.ptr, 2 * D, vt.ptr, T, 2 * D,
                                       2 * D, gain.ptr, gain.ptr, D, cs.ptr, sn.ptr, T, s), "gemm_headnorm")
 
-    def attention():
+    def attention(hook=None):
+        if hook:
+            hook(0)
         hip.check(L.hxa_attention(qk.ptr, 2 * D, k.ptr, D, vt.ptr, T, o.ptr, D, T, T, T, H, 1, 0, 0, 0, 0, s), "attn")
+        if hook:
+            hook(1)
         hip.check(L.hxa_attention(qk.ptr, 2 * D, ck.ptr, D, cvt.ptr, C_TXT, o.ptr, D, T, C_TXT, C_TXT, H, 1, 0, 0, 0, 0,
                                   s), "attn")
     f16 = 2
@@ -361,6 +371,7 @@ def kernel_breakdown(L, hip, reps=10):
     dom = max(fam, key=lambda k: table[k]["block_us"])
     fn, n, flops, nbytes, kname = fam[dom]
     ms = _time_launches(L, hip, fn, s, reps=50, warm=5)
+    clocks = _family_clocks(L, hip, fn, n, s, kind=1 if dom == "attention" else 0)
     hip.check(L.hxa_stream_sync(s), "sync")
     L.hxa_stream_destroy(s)
     del keep, keep2
@@ -371,12 +382,105 @@ def kernel_breakdown(L, hip, reps=10):
             if line.startswith("hbm_bytes_per_launch:"):
                 traffic = int(line.split(":")[1])
     tf = flops / (ms * 1e-3)
+    ghz = float(np.mean([c["ghz"] for c in clocks]))
+    peak_clk = CLK_FLOPS_PER_CYCLE * ghz * 1e9
     roof = {"kernel": f"{kname}: {dom} ({', '.join(table[dom]['stages'])}), {n} launches per block",
             "bound": "mfma", "achieved": round(tf / 1e12, 1), "peak": PEAK_FP16 / 1e12, "unit": "TFLOP/s",
             "frac": round(tf / PEAK_FP16, 4), "traffic": traffic, "avg_launch_us": round(ms * 1e3 / n, 2),
             "gflop_per_launch": round(flops / n / 1e9, 3), "alg_bytes_per_launch": int(nbytes // n),
-            "share_of_block": table[dom]["share_of_block"]}
+            "share_of_block": table[dom]["share_of_block"],
+            "clock_ghz": round(ghz, 3), "peak_at_clock": round(peak_clk / 1e12, 1),
+            "frac_at_clock": round(tf / peak_clk, 4), "clock_by_launch": clocks}
     return {"block_us_staged": round(block_us, 1), "families": table}, roof
+
+
+CLK_FLOPS_PER_CYCLE = 256 * 4 * 1024  # 256 CUs x 4 SIMDs x 1024 fp16 MFMA flops per SIMD per cycle (2.5 PF at 2.4 GHz)
+
+
+def _records(L, hip, rec, nwg):
+    """(clock GHz, main-loop cycles) per workgroup from a shader-clock record (hxa_clock_record)"""
+    buf = np.zeros(nwg * 4, np.uint64)
+    hip.check(L.hxa_d2h(buf.ctypes.data, rec.ptr, buf.nbytes), "d2h")
+    b = buf.reshape(nwg, 4).astype(np.float64)
+    ok = b[:, 3] > b[:, 1]
+    cyc, real = b[ok, 2] - b[ok, 0], b[ok, 3] - b[ok, 1]
+    return cyc / real * 0.1, cyc, int(ok.sum())
+
+
+def _family_clocks(L, hip, fn, n, s, kind=0, reps=50, maxwg=4096):
+    """The shader clock of each launch of a kernel family (kind 0: GEMM, 1: attention), run back to back `reps` times
+    with a clock record per launch (the records keep the last repetition): per launch the mean clock over its
+    workgroups and its main-loop cycles."""
+    recs = [hip.DeviceArray((maxwg * 4,), np.uint64) for _ in range(n)]
+    for r in recs:
+        hip.check(L.hxa_memset(r.ptr, 0, r.nbytes), "memset")
+    for _ in range(reps):
+        fn(lambda i: hip.check(L.hxa_clock_record(kind, recs[i].ptr, maxwg), "clock_record"))
+    hip.check(L.hxa_clock_record(kind, None, 0), "clock_record")
+    hip.check(L.hxa_stream_sync(s), "sync")
+    out = []
+    for r in recs:
+        ghz, cyc, nwg = _records(L, hip, r, maxwg)
+        out.append({"ghz": round(float(ghz.mean()), 3), "loop_cycles": round(float(cyc.mean())), "workgroups": nwg})
+    return out
+
+
+def clock_probe():
+    """Shader clock and main-loop cycles of the MLP-up GEMM (1536 x 8192, K 2048, fp16 k-tiled weights, the tile
+    hxa_gemm picks) launched 40 times back to back: with N(0, 1) activations and N(0, 0.02) weights, with both zero,
+    and on one workgroup (M x N = one tile) with random data; then the clock of the 2B DiT step's GEMM and attention
+    launches (the last launch of each, graph-replayed steps). One JSON line."""
+    from hexanima_amd import hip
+    hip.init(0)
+    L = hip.lib()
+    s = C.c_void_p()
+    hip.check(L.hxa_stream_create(C.byref(s)), "stream")
+    K, N = D, F
+    pk = hip.gemm_pick(T, N, K, WFMT, 1, 0)
+    bm, bn = pk["bm"], pk["bn"]
+    A = hip.DeviceArray((T, K), np.float16)
+    W = hip.DeviceArray((N, K), np.float16)
+    O = hip.DeviceArray((T, N), np.float16)
+    rec = hip.DeviceArray((4096 * 4,), np.uint64)
+    res = {"gemm": f"{T}x{N}x{K} fp16, {_kname(pk)}", "cases": []}
+    for name, M_, N_, astd, wstd in (("full chip, random data", T, N, 1.0, 0.02), ("full chip, zero data", T, N, 0.0, 0.0),
+                                     ("one workgroup, random data", bm, bn, 1.0, 0.02)):
+        hip.check(L.hxa_fill_normal(A.ptr, 1, T * K, 81, 0.0, astd, s), "fill")
+        hip.check(L.hxa_fill_normal(W.ptr, 1, N * K, 82, 0.0, wstd, s), "fill")
+        hip.check(L.hxa_memset(rec.ptr, 0, rec.nbytes), "memset")
+
+        def run(M_=M_, N_=N_):  # the tile picked for the full shape, also on one workgroup
+            hip.check(L.hxa_gemm_tile(A.ptr, K, M_, WFMT, W.ptr, None, None, N_, K, 1, 0, O.ptr, N_, 0, None, 0, None, bm, bn,
+                                      pk["waves"], s), "gemm")
+        ms = _time_launches(L, hip, run, s, reps=40, warm=10)
+        hip.check(L.hxa_clock_record(0, rec.ptr, 4096), "clock_record")
+        for _ in range(40):
+            run()
+        hip.check(L.hxa_clock_record(0, None, 0), "clock_record")
+        hip.check(L.hxa_stream_sync(s), "sync")
+        ghz, cyc, nwg = _records(L, hip, rec, 4096)
+        flops = 2.0 * M_ * N_ * K
+        res["cases"].append({"case": name, "launch_us": round(ms * 1e3, 2), "workgroups": nwg,
+                             "clock_ghz": round(float(ghz.mean()), 3), "clock_min_max": [round(float(ghz.min()), 3),
+                                                                                        round(float(ghz.max()), 3)],
+                             "loop_cycles": round(float(cyc.mean())), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)})
+    del A, W, O
+    # the DiT step: records on while the graph is captured (the step's launches carry them), last launch kept
+    recs = [hip.DeviceArray((4096 * 4,), np.uint64) for _ in range(2)]
+    for k, r in enumerate(recs):
+        hip.check(L.hxa_memset(r.ptr, 0, r.nbytes), "memset")
+        hip.check(L.hxa_clock_record(k, r.ptr, 4096), "clock_record")
+    bd = hip.BlockDims(0, D, H, F, C_TXT, DC, 0, 1, 0, hip.W_F16, hip.W_F16, 1)
+    ms = dit_ms(bd, NBLK, (1,) + LAT, (1, C_TXT, DC), 0, 20, 3, 2024)
+    for k in range(2):
+        hip.check(L.hxa_clock_record(k, None, 0), "clock_record")
+    step = {"ms_per_step": round(ms, 3)}
+    for k, name in enumerate(("last_gemm", "last_attention")):
+        ghz, cyc, nwg = _records(L, hip, recs[k], 4096)
+        step[name] = {"clock_ghz": round(float(ghz.mean()), 3), "workgroups": nwg}
+    res["dit_step_2b"] = step
+    L.hxa_stream_destroy(s)
+    print(json.dumps(res), flush=True)
 
 
 def kernel_probe(reps, family):
@@ -522,12 +626,18 @@ def main():
     ap.add_argument("--probe-family", default="gemm_splitk",
                     choices=["gemm_splitk", "gemm_pp_mlp_up", "gemm_pp_qkv_headnorm", "attention"])
     ap.add_argument("--abi-chain", action="store_true", help="only time the 28-block mega_block chain (hxa_run)")
+    ap.add_argument("--clock-probe", action="store_true",
+                    help="only measure the shader clock of the MLP-up GEMM (random / zero data, one workgroup) and of "
+                         "the DiT step's kernels")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build targets a single MI355X (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     if a.kernel_probe:
         kernel_probe(a.kernel_probe, a.probe_family)
+        return
+    if a.clock_probe:
+        clock_probe()
         return
     if a.abi_chain:
         print(json.dumps({"abi_chain": abi_chain()}), flush=True)

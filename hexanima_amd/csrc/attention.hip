@@ -65,6 +65,7 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   const hxa_h *k = p.k + (long)b * p.k_bstride + h * 128;
   const hxa_h *vt = p.vt + (long)b * p.vt_bstride + (long)h * 128 * p.ldvt;
   hxa_h *o = p.o + (long)b * p.o_bstride + h * 128;
+  const HxaClkMark clk0 = clk_mark(p.clk);
 
   const int qrow = qb * QB + wq * 32 + ql;
   const bool qok = qrow < p.T;
@@ -269,6 +270,7 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   }
 
   // merge the two key halves: half 1 publishes (m, l, O) per lane, half 0 combines and stores
+  clk_store(p.clk, (int)(blockIdx.x + blockIdx.y * gridDim.x), tid, clk0);
   wait_vm<0>();  // no tile load may still be writing the LDS reused below
   __syncthreads();
   float *xch = (float *)lds + wq * 66 * 64;
@@ -338,7 +340,9 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   const bool small = fill(96) > fill(128) + 1e-9;
   const int QB = small ? 96 : 128, nqb = (p.T + QB - 1) / QB;
   dim3 grid(nqb * p.H, p.batch);
-  if (small) hxa_launch(attn_kernel<3>, grid, dim3(384), LDS_BYTES, st, p, nqb);
-  else hxa_launch(attn_kernel<4>, grid, dim3(512), LDS_BYTES, st, p, nqb);
+  HxaAttn pk = p;
+  pk.clk = g_hxa_clk_attn;
+  if (small) hxa_launch(attn_kernel<3>, grid, dim3(384), LDS_BYTES, st, pk, nqb);
+  else hxa_launch(attn_kernel<4>, grid, dim3(512), LDS_BYTES, st, pk, nqb);
   return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
 }

@@ -52,6 +52,7 @@ struct GemmParams {
   const float *hn_g0, *hn_g1, *hn_cos, *hn_sin;
   const uint8_t *pf;  // bytes to touch after the main loop (HxaGemm::pf)
   long pf_bytes;
+  HxaClk clk;  // shader-clock record (hxa_clock_record), indexed by the launch's flat workgroup id
 };
 
 // Touch this workgroup's share of [p.pf, p.pf + p.pf_bytes), one 4-byte load per 128-byte line: the lines come into
@@ -427,6 +428,7 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   const int kbase = z * p.Kslice;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
+  const HxaClkMark clk0 = clk_mark(p.clk);
 
   // ---- loader: stage s <- k tile kt. A and fp16 W rows are 64 B (4 chunks of 16 B) stored with the chunk swizzle
   // c ^ ((row >> 2) & 3); q8 rows are 32 B with chunk swizzle c ^ ((row >> 3) & 1); q4 rows are 16 B.
@@ -600,6 +602,7 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
       }
     }
   }
+  clk_store(p.clk, (int)(blockIdx.x + blockIdx.z * gridDim.x), tid, clk0);
   wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
   __syncthreads();
   if (p.pf_bytes > 0)
@@ -672,6 +675,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = wave >> 2, wl = wave & 3, wm = wl & 1, wn = wl >> 1;
   const int nk = p.Kslice / BK;
+  const HxaClkMark clk0 = clk_mark(p.clk);
 
   // group 1: stage s <- k tile kt (clamped past the end: dummy reloads keep the vmcnt accounting constant)
   // per-lane offsets from the tile corner, fixed over the k loop (only group 1 issues loads)
@@ -805,6 +809,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
     // phase 2 nk: compute stage nk-1
     mfmas(fa, fb);
   }
+  clk_store(p.clk, (int)(blockIdx.x + blockIdx.z * gridDim.x), tid, clk0);
   wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
   __syncthreads();
   if (p.pf_bytes > 0)
@@ -1048,6 +1053,7 @@ static int gemm_prepare(const HxaGemm &g, GemmParams &p, int &bm, int &bn, int &
     return HXA_E_ARG;
   p.pf = (const uint8_t *)g.pf;
   p.pf_bytes = g.pf_bytes > 0 ? g.pf_bytes : 0;
+  p.clk = g_hxa_clk_gemm;
   bm = 128;
   bn = 128;
   nw = 4;

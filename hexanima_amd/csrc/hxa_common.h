@@ -44,6 +44,31 @@ struct HxaWeight {
   const hxa_h *z;     // [K/32][N] q4 offsets (optional)
 };
 
+// ---- shader-clock record (hxa_clock_record) ----
+// A kernel given a record writes, per workgroup w < n, four 64-bit counters at rec[4 w .. 4 w + 3]: s_memtime and
+// s_memrealtime when its work starts, and both again when its main loop ends. s_memtime counts shader-clock cycles,
+// s_memrealtime a constant 100 MHz clock, so (c1 - c0) / (r1 - r0) * 100 MHz is the clock the workgroup ran at and
+// c1 - c0 its main loop's length in cycles. rec == nullptr: nothing is read or written.
+struct HxaClk {
+  unsigned long long *rec;
+  int n;
+};
+// the record the GEMM and attention launches copy into their parameters (set by hxa_clock_record; host side)
+extern HxaClk g_hxa_clk_gemm, g_hxa_clk_attn;
+struct HxaClkMark {
+  unsigned long long c, r;
+};
+HXA_DEV HxaClkMark clk_mark(const HxaClk &k) {
+  if (k.rec == nullptr) return {0, 0};
+  return {__builtin_amdgcn_s_memtime(), __builtin_amdgcn_s_memrealtime()};
+}
+// lanes 0-3 of the calling threads write the record (a per-lane address: vector stores)
+HXA_DEV void clk_store(const HxaClk &k, int wg, int tid, HxaClkMark s) {
+  if (k.rec == nullptr) return;
+  const HxaClkMark e = clk_mark(k);
+  if (tid < 4 && wg < k.n) k.rec[4L * wg + tid] = tid == 0 ? s.c : tid == 1 ? s.r : tid == 2 ? e.c : e.r;
+}
+
 // ---- direct-to-LDS loads and VMEM waits (gfx950) ----
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) const void gmem_void_t;

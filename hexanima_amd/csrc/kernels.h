@@ -47,6 +47,7 @@ struct HxaAttn {
   long ldo;
   int T, NKV, nvalid, H, batch;
   long q_bstride, k_bstride, vt_bstride, o_bstride;  // per-image offsets (elements)
+  HxaClk clk;  // shader-clock record: set by hxa_attn_launch from the current one (callers leave it empty)
 };
 int hxa_attn_launch(const HxaAttn &p, hipStream_t st);
 

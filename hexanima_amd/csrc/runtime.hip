@@ -162,6 +162,16 @@ extern "C" int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, c
   return HXA_OK;
 }
 
+HxaClk g_hxa_clk_gemm{nullptr, 0}, g_hxa_clk_attn{nullptr, 0};
+extern "C" int hxa_clock_record(int kind, void *rec, long nrec) {
+  if (kind != 0 && kind != 1) return fail(HXA_E_ARG, "clock_record: kind %d", kind);
+  if (rec != nullptr && (nrec <= 0 || (uintptr_t)rec % 8)) return fail(HXA_E_ARG, "clock_record: buffer");
+  HxaClk &k = kind == 0 ? g_hxa_clk_gemm : g_hxa_clk_attn;
+  k.rec = (unsigned long long *)rec;
+  k.n = rec == nullptr ? 0 : (int)(nrec < (1L << 30) ? nrec : (1L << 30));
+  return HXA_OK;
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // kernel entry points
 // ---------------------------------------------------------------------------------------------------------------

@@ -68,6 +68,7 @@ _SIGS = {
     "hxa_stream_wait_event": (I, [P, P]),
     "hxa_event_elapsed_ms": (I, [P, P, C.POINTER(F)]),
     "hxa_device_info": (I, [C.POINTER(I), C.POINTER(I), C.POINTER(SZ), C.c_char_p, I]),
+    "hxa_clock_record": (I, [I, P, L]),
     "hxa_gemm": (I, [P, L, I, I, P, P, P, I, I, I, I, P, L, L, P, L, P, P, L, I, P]),
     "hxa_resadd_norm_mod": (I, [P, L, I, I, P, L, P, P, P, P, F, P, L, P]),
     "hxa_gemm_headnorm": (I, [P, L, I, I, P, P, P, I, I, P, L, P, L, I, I, P, P, I, P, P, I, P]),

@@ -97,6 +97,13 @@ int hxa_event_record(void *ev, void *stream);
 int hxa_stream_wait_event(void *stream, void *ev); /* later work on stream waits for ev */
 int hxa_event_elapsed_ms(void *start, void *stop, float *ms);
 int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, char *name, int name_len);
+/* Shader-clock record, for measurement; no counterpart in the reference. kind 0: every GEMM launched after this call
+ * (hxa_gemm*, the block runner's and DiT's projections, graphs captured after it) writes, per workgroup w < nrec,
+ * four uint64 at rec[4w .. 4w+3] (device memory): s_memtime and s_memrealtime when the workgroup starts, both again
+ * when its main loop ends; kind 1: the same for attention launches. s_memtime counts shader-clock cycles and
+ * s_memrealtime a constant 100 MHz clock, so (c1-c0)/(r1-r0) x 100 MHz is the clock the workgroup ran at. Each launch
+ * overwrites the records of its workgroup ids (the launch's flat workgroup index). rec NULL: off (the default). */
+int hxa_clock_record(int kind, void *rec, long nrec);
 
 /* ============================================================================================================
  * 3. Kernels (device pointers; stream NULL = the null stream)

@@ -455,6 +455,45 @@ def test_attention_vs_oracle(T, NKV, nvalid, H):
     assert r0 < 4.7e-3  # measured 8.2e-4 - 1.6e-3
 
 
+def test_clock_record_gemm_and_attention():
+    """hxa_clock_record: one record per workgroup with a plausible shader clock, results unchanged, and nothing
+    written once it is switched off."""
+    hip = _hip()
+    say("clock record: 1536 x 2048 x 2048 GEMM (128 workgroups or more), 1536 x 1536 attention, 16 heads")
+    L = hip.lib()
+    rng = np.random.default_rng(5)
+    A = f16(rng.standard_normal((1536, 2048)))
+    W = f16(rng.standard_normal((2048, 2048)) * 0.02)
+    plain = _run_gemm(hip, A, 0, W, None, 2048, 2048)
+    recs = [hip.DeviceArray((4096 * 4,), np.uint64, zero=True) for _ in range(2)]
+    for kind, r in enumerate(recs):
+        hip.check(L.hxa_clock_record(kind, r.ptr, 4096), "clock_record")
+    try:
+        timed = _run_gemm(hip, A, 0, W, None, 2048, 2048)
+        q = f16(rng.standard_normal((1536, 2048)) / np.sqrt(128))
+        k, v = f16(rng.standard_normal((1536, 2048))), f16(rng.standard_normal((1536, 2048)))
+        _attn(hip, q, k, v)
+    finally:
+        for kind in range(2):
+            hip.check(L.hxa_clock_record(kind, None, 0), "clock_record")
+    assert np.array_equal(plain.view(np.uint16), timed.view(np.uint16))
+    pk = hip.gemm_pick(1536, 2048, 2048, 0)
+    nwg_gemm = -(-1536 // pk["bm"]) * -(-2048 // pk["bn"])
+    for r, nwg in ((recs[0], nwg_gemm), (recs[1], None)):
+        b = r.numpy().reshape(4096, 4).astype(np.float64)
+        ok = b[:, 3] > b[:, 1]
+        if nwg is not None:
+            assert ok[:nwg].all() and not ok[nwg:].any()
+        assert ok.sum() >= 128
+        ghz = (b[ok, 2] - b[ok, 0]) / (b[ok, 3] - b[ok, 1]) * 0.1
+        print(f"clock record: {ok.sum()} workgroups, {ghz.min():.2f} - {ghz.max():.2f} GHz", flush=True)
+        assert (ghz > 0.3).all() and (ghz < 3.5).all()
+    # switched off: a further launch leaves the (cleared) records alone
+    hip.check(L.hxa_memset(recs[0].ptr, 0, recs[0].nbytes), "memset")
+    _run_gemm(hip, A, 0, W, None, 2048, 2048)
+    assert not recs[0].numpy().any()
+
+
 def test_attention_batched_images_are_independent():
     hip = _hip()
     say("attention batch=3")
