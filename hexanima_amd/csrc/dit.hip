@@ -56,6 +56,17 @@ struct Dit {
   float *sig_host = nullptr;   // pinned source of the per-step sigma upload
   hipEvent_t sig_ev = nullptr;  // recorded after that upload: sig_host is rewritten only once it has completed
   bool sig_pending = false;
+  // low-res first steps (animad.cpp:392-503; mossrun.cpp:288-313), allocated at the first such step.
+  // Anima: the noise of the first step and the last clean estimate [B][C][H][W], the low-res latent and velocity
+  // [B][C][H/f][W/f]; MOSS: the low-res noise and clean estimate, token rows [B][(gh/2)*(gw/2)][4C].
+  float *nfull = nullptr, *dhat = nullptr, *xlow = nullptr, *vlow = nullptr, *zl = nullptr, *x0l = nullptr;
+  bool low_init = false;      // the low-res state holds this input's noise (reset by hxa_dit_set_inputs)
+  bool moss_low_live = false; // MOSS: the last step was low-res, so a full step first upsamples its clean estimate
+  static constexpr int MAXF = 8;
+  float *cosL[MAXF + 1] = {}, *sinL[MAXF + 1] = {};  // RoPE tables of the 1/f grid
+  double ropeL_scale = 0.0;                          // MOSS: the position scale cosL[2] / sinL[2] were built with
+  hipGraphExec_t execL[MAXF + 1] = {};
+  hipGraph_t graphL[MAXF + 1] = {};
 };
 
 thread_local char g_derr[256];
@@ -93,7 +104,8 @@ void rope_anima(int gh, int gw, std::vector<float> &c, std::vector<float> &s) {
 }
 // moss_ref.py:27-35: 4 axes x 16 bands; image (0, ntxt, h-(H-1)/2, w-(W-1)/2), text (0, i, 0, 0);
 // synthetic bands 10000^(-i/16); padding rows get the identity rotation
-void rope_moss(int H, int W, int ntxt, int Ttot, std::vector<float> &c, std::vector<float> &s) {
+// image positions times `scale`: 1 on the full grid, MOSS_LOWSCALE (2) on the low-res steps' (mossrun.cpp:190-201, :313)
+void rope_moss(int H, int W, int ntxt, int Ttot, std::vector<float> &c, std::vector<float> &s, double scale = 1.0) {
   c.assign((size_t)Ttot * 64, 1.0f);
   s.assign((size_t)Ttot * 64, 0.0f);
   const int nimg = H * W;
@@ -102,8 +114,8 @@ void rope_moss(int H, int W, int ntxt, int Ttot, std::vector<float> &c, std::vec
     if (tk < nimg) {
       pos[0] = 0;
       pos[1] = ntxt;
-      pos[2] = (tk / W) - (H - 1) / 2.0;
-      pos[3] = (tk % W) - (W - 1) / 2.0;
+      pos[2] = ((tk / W) - (H - 1) / 2.0) * scale;
+      pos[3] = ((tk % W) - (W - 1) / 2.0) * scale;
     } else {
       pos[0] = 0;
       pos[1] = tk - nimg;
@@ -200,8 +212,37 @@ int record_prelude_moss_ref(Dit &d) {
   return HXA_OK;
 }
 
-int record_step(Dit &d, int mode) {
-  const hxa_block_dims &b = d.bd;
+// One pass of the blocks over a latent grid: the full one, or a low-res step's 1/f grid.
+struct Pass {
+  int lat_h = 0, lat_w = 0;        // latent height and width of this pass
+  int Timg = 0, Ttot = 0;          // image tokens; rows per image in x (MOSS: image + text, padded to 32)
+  hxa_block_dims bd{};             // the blocks' shape (T = Ttot)
+  const float *cosT = nullptr, *sinT = nullptr;
+  const float *lat_in = nullptr;   // the latent the patch embedding reads
+  float *lat_out = nullptr;        // the final layer's output: the Euler-updated latent (dtp) or the velocity
+  const float *dtp = nullptr;      // device pointer to tn - t for the Euler update; nullptr: lat_out = v
+  float *zrows = nullptr, *x0rows = nullptr;  // rapid-moss: noise and clean estimate of this grid (token rows)
+};
+
+Pass full_pass(Dit &d, int mode) {
+  Pass q;
+  q.lat_h = d.cfg.lat_h;
+  q.lat_w = d.cfg.lat_w;
+  q.Timg = d.Timg;
+  q.Ttot = d.Ttot;
+  q.bd = d.bd;
+  q.cosT = d.cosT;
+  q.sinT = d.sinT;
+  q.lat_in = d.lat;
+  q.lat_out = mode == MODE_EULER ? d.lat : d.vel;
+  q.dtp = mode == MODE_EULER ? d.sig + 2 : nullptr;
+  q.zrows = d.zrows;
+  q.x0rows = d.x0rows;
+  return q;
+}
+
+int record_step(Dit &d, const Pass &ps) {
+  const hxa_block_dims &b = ps.bd;
   const int B = b.batch, D = b.D, C4 = 4 * d.cfg.lat_c, temb = d.cfg.temb, nb = d.cfg.nblocks;
   hipStream_t st = d.st;
   const bool moss_ref = d.form == 1 && b.kind == 1;
@@ -220,16 +261,16 @@ int record_step(Dit &d, int mode) {
   }
   // patch embed (rapid-moss: latent mix + video embedding of the token rows) (+ MOSS text tokens)
   if (moss_ref)
-    DTRY(hxa_moss_embed_launch(d.zrows, d.x0rows, d.Q, d.Wemb, d.bve, d.x, B, d.Timg, d.Ttot, D, C4, st));
+    DTRY(hxa_moss_embed_launch(ps.zrows, ps.x0rows, d.Q, d.Wemb, d.bve, d.x, B, ps.Timg, ps.Ttot, D, C4, st));
   else
-    DTRY(hxa_patchify_launch(d.lat, B, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w, d.tok, st));
+    DTRY(hxa_patchify_launch(ps.lat_in, B, d.cfg.lat_c, ps.lat_h, ps.lat_w, d.tok, st));
   for (int i = 0; i < B; i++) {
     if (!moss_ref)
-      DTRY(hxa_linear_f32_launch(d.tok + (long)i * d.Timg * C4, C4, d.Timg, C4, d.Wemb, D, d.x + (long)i * d.Ttot * D, D,
-                                 0, nullptr, 0, 0, st));
+      DTRY(hxa_linear_f32_launch(d.tok + (long)i * ps.Timg * C4, C4, ps.Timg, C4, d.Wemb, D, d.x + (long)i * ps.Ttot * D,
+                                 D, 0, nullptr, 0, 0, st));
     if (b.kind == 1) {
-      float *xt = d.x + ((long)i * d.Ttot + d.Timg) * D;
-      DTRY(hxa_fill_const_launch(xt, 0, (size_t)(d.Ttot - d.Timg) * D, 0.0f, st));
+      float *xt = d.x + ((long)i * ps.Ttot + ps.Timg) * D;
+      DTRY(hxa_fill_const_launch(xt, 0, (size_t)(ps.Ttot - ps.Timg) * D, 0.0f, st));
       HxaWeight wt{HXA_W_F16, D, d.cfg.ntxt_in, d.Wtxt, nullptr, nullptr};
       HxaGemm g{};
       g.A = d.ctx16 + (long)i * d.ntxt * d.cfg.ntxt_in;
@@ -249,21 +290,21 @@ int record_step(Dit &d, int mode) {
   auto mlp_gate = [&](int k) { return b.kind == 0 ? d.mods + (long)k * 9 * D + 8L * D : d.mods + 5L * D; };
   for (int k = 0; k < nb; k++) {
     const float *mod = b.kind == 0 ? d.mods + (long)k * 9 * D : d.mods;
-    DTRY(hxa_block_run_chained(&d.bd, d.packs[k], d.x, b.kind == 0 ? d.ctx16 : nullptr, mod, d.cosT, d.sinT, d.ws, 0,
+    DTRY(hxa_block_run_chained(&b, d.packs[k], d.x, b.kind == 0 ? d.ctx16 : nullptr, mod, ps.cosT, ps.sinT, d.ws, 0,
                                nullptr, 0, st, k > 0 ? mlp_gate(k - 1) : nullptr, 1));
   }
   {
     long ld = 0;
-    const hxa_h *t1 = (const hxa_h *)hxa_block_ws_buf(&d.bd, d.ws, 5, &ld), *t2 = (const hxa_h *)hxa_block_ws_buf(&d.bd, d.ws, 9, &ld);
-    DTRY(hxa_resadd2_launch(d.x, D, t1, t2, ld, B * d.Ttot, D, mlp_gate(nb - 1), st));
+    const hxa_h *t1 = (const hxa_h *)hxa_block_ws_buf(&b, d.ws, 5, &ld), *t2 = (const hxa_h *)hxa_block_ws_buf(&b, d.ws, 9, &ld);
+    DTRY(hxa_resadd2_launch(d.x, D, t1, t2, ld, B * ps.Ttot, D, mlp_gate(nb - 1), st));
   }
   // final layer (+ Euler update); rapid-moss: RMS head and x0 = z - v
   if (moss_ref)
-    DTRY(hxa_final_launch(d.x, B, d.Timg, d.Ttot, D, d.fmod, d.fmod + D, d.Wfin, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w,
-                          d.vel, nullptr, st, d.nfin, d.x0rows, d.zrows));
+    DTRY(hxa_final_launch(d.x, B, ps.Timg, ps.Ttot, D, d.fmod, d.fmod + D, d.Wfin, d.cfg.lat_c, ps.lat_h, ps.lat_w,
+                          d.vel, nullptr, st, d.nfin, ps.x0rows, ps.zrows));
   else
-    DTRY(hxa_final_launch(d.x, B, d.Timg, d.Ttot, D, d.fmod, d.fmod + D, d.Wfin, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w,
-                          mode == MODE_EULER ? d.lat : d.vel, mode == MODE_EULER ? d.sig + 2 : nullptr, st));
+    DTRY(hxa_final_launch(d.x, B, ps.Timg, ps.Ttot, D, d.fmod, d.fmod + D, d.Wfin, d.cfg.lat_c, ps.lat_h, ps.lat_w,
+                          ps.lat_out, ps.dtp, st));
   return HXA_OK;
 }
 
@@ -479,6 +520,13 @@ extern "C" int hxa_dit_destroy(void *p) {
   if (d->st) (void)hipStreamSynchronize(d->st);
   if (d->exec) (void)hipGraphExecDestroy(d->exec);
   if (d->graph) (void)hipGraphDestroy(d->graph);
+  for (int f = 0; f <= Dit::MAXF; f++) {
+    if (d->execL[f]) (void)hipGraphExecDestroy(d->execL[f]);
+    if (d->graphL[f]) (void)hipGraphDestroy(d->graphL[f]);
+    if (d->cosL[f]) (void)hipFree(d->cosL[f]);
+    if (d->sinL[f]) (void)hipFree(d->sinL[f]);
+  }
+  for (float *q : {d->nfull, d->dhat, d->xlow, d->vlow, d->zl, d->x0l}) if (q) (void)hipFree(q);
   for (void *q : d->packs) if (q) (void)hipFree(q);
   if (d->modw_all) (void)hipFree(d->modw_all);
   void *bufs[] = {d->glue, d->lat, d->vel, d->tok, d->x, d->sinus, d->cvec, d->mods, d->fmod, d->sig, d->cosT, d->sinT,
@@ -496,6 +544,10 @@ extern "C" int hxa_dit_set_inputs(void *p, const float *lat, const float *ctx) {
   const hxa_block_dims &b = d.bd;
   const long latn = (long)b.batch * d.cfg.lat_c * d.cfg.lat_h * d.cfg.lat_w;
   if (lat) DHIP(hipMemcpyAsync(d.lat, lat, 4 * latn, hipMemcpyHostToDevice, d.st));
+  if (lat) {  // new noise: the low-res steps start over from it
+    d.low_init = false;
+    d.moss_low_live = false;
+  }
   if (lat && d.zrows) {  // rapid-moss: the latent is the noise z (token rows), the clean estimate starts at 0
     DTRY(hxa_patchify_launch(d.lat, b.batch, d.cfg.lat_c, d.cfg.lat_h, d.cfg.lat_w, d.zrows, d.st));
     DTRY(hxa_fill_const_launch(d.x0rows, 0, (size_t)latn, 0.0f, d.st));
@@ -525,11 +577,13 @@ extern "C" int hxa_dit_get_latent(void *p, float *lat) {
 }
 
 namespace {
-int run_step(Dit &d, int use_graph) {
-  if (!use_graph) return record_step(d, MODE_EULER);
-  if (!d.exec) {
+// record (use_graph 0) or replay the graph in (graph, exec) of `rec`, capturing it on first use
+template <class Rec>
+int run_graph(Dit &d, int use_graph, hipGraph_t &graph, hipGraphExec_t &exec, Rec rec) {
+  if (!use_graph) return rec();
+  if (!exec) {
     DHIP(hipStreamBeginCapture(d.st, hipStreamCaptureModeRelaxed));
-    const int r = record_step(d, MODE_EULER);
+    const int r = rec();
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(d.st, &g);
     if (r != HXA_OK) {
@@ -537,11 +591,24 @@ int run_step(Dit &d, int use_graph) {
       return r;
     }
     if (e != hipSuccess) return dfail(HXA_E_HIP, "graph capture");
-    d.graph = g;
-    DHIP(hipGraphInstantiate(&d.exec, d.graph, nullptr, nullptr, 0));
+    graph = g;
+    DHIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
   }
-  DHIP(hipGraphLaunch(d.exec, d.st));
+  DHIP(hipGraphLaunch(exec, d.st));
   return HXA_OK;
+}
+// a MOSS full step after low-res ones starts from their clean estimate, upsampled (mossrun.cpp:311)
+int moss_leave_low(Dit &d) {
+  if (!d.moss_low_live) return HXA_OK;
+  const int gh = d.cfg.lat_h / 2, gw = d.cfg.lat_w / 2;
+  DTRY(hxa_upsample2_rows_launch(d.x0l, d.bd.batch, gh / 2, gw / 2, 4 * d.cfg.lat_c, d.x0rows, d.st));
+  d.moss_low_live = false;
+  return HXA_OK;
+}
+int run_step(Dit &d, int use_graph) {
+  if (d.x0rows) DTRY(moss_leave_low(d));
+  const Pass ps = full_pass(d, MODE_EULER);
+  return run_graph(d, use_graph, d.graph, d.exec, [&]() { return record_step(d, ps); });
 }
 }  // namespace
 
@@ -559,11 +626,104 @@ extern "C" int hxa_dit_moss_step(void *p, float code, int use_graph) {
   return run_step(d, use_graph);
 }
 
+namespace {
+// the RoPE tables of the 1/f grid (MOSS: image positions times `scale`), built on first use (and again when the MOSS
+// scale changes); the upload completes before the call returns
+int low_rope(Dit &d, int f, double scale) {
+  const bool moss = d.bd.kind == 1;
+  if (d.cosL[f] && (!moss || d.ropeL_scale == scale)) return HXA_OK;
+  const int gh = d.cfg.lat_h / 2 / f, gw = d.cfg.lat_w / 2 / f;
+  const int Ttot = moss ? (gh * gw + d.ntxt + 31) / 32 * 32 : gh * gw;
+  std::vector<float> c, sn;
+  if (moss) rope_moss(gh, gw, d.ntxt, Ttot, c, sn, scale);
+  else rope_anima(gh, gw, c, sn);
+  if (!d.cosL[f]) {
+    DHIP(hipMalloc((void **)&d.cosL[f], 4L * Ttot * 64));
+    DHIP(hipMalloc((void **)&d.sinL[f], 4L * Ttot * 64));
+  }
+  DHIP(hipMemcpyAsync(d.cosL[f], c.data(), 4 * c.size(), hipMemcpyHostToDevice, d.st));
+  DHIP(hipMemcpyAsync(d.sinL[f], sn.data(), 4 * sn.size(), hipMemcpyHostToDevice, d.st));
+  DHIP(hipStreamSynchronize(d.st));
+  d.ropeL_scale = scale;
+  return HXA_OK;
+}
+int ensure(float *&p, long floats) {
+  if (!p && hipMalloc((void **)&p, 4 * floats) != hipSuccess) return dfail(HXA_E_RESOURCE, "dit: out of device memory");
+  return HXA_OK;
+}
+// the pass over the 1/f grid
+Pass low_pass(Dit &d, int f) {
+  Pass q;
+  q.lat_h = d.cfg.lat_h / f;
+  q.lat_w = d.cfg.lat_w / f;
+  q.Timg = (q.lat_h / 2) * (q.lat_w / 2);
+  q.Ttot = d.bd.kind == 1 ? (q.Timg + d.ntxt + 31) / 32 * 32 : q.Timg;
+  q.bd = d.bd;
+  q.bd.T = q.Ttot;
+  q.bd.nvalid = d.bd.kind == 1 ? q.Timg + d.ntxt : q.Timg;
+  q.cosT = d.cosL[f];
+  q.sinT = d.sinL[f];
+  return q;
+}
+}  // namespace
+
+extern "C" int hxa_dit_step_lowres(void *p, float sigma, float sigma_next, int factor, int use_graph) {
+  Dit &d = *(Dit *)p;
+  if (d.x0rows) return dfail(HXA_E_MODE, "dit: the rapid-moss form steps with hxa_dit_moss_step_lowres");
+  const int H = d.cfg.lat_h, W = d.cfg.lat_w;
+  // animad.cpp:407: a factor the latent does not divide into whole patches, or whose token count is not a multiple
+  // of 32, runs the step at full resolution
+  if (factor < 2 || factor > Dit::MAXF || H % (2 * factor) || W % (2 * factor) || ((H / 2 / factor) * (W / 2 / factor)) % 32)
+    return hxa_dit_step(p, sigma, sigma_next, use_graph);
+  const long BC = (long)d.bd.batch * d.cfg.lat_c, full = BC * H * W;
+  DTRY(ensure(d.nfull, full));
+  DTRY(ensure(d.dhat, full));
+  DTRY(ensure(d.xlow, full / 4));  // the largest low grid (factor 2)
+  DTRY(ensure(d.vlow, full / 4));
+  DTRY(low_rope(d, factor, 1.0));
+  DTRY(set_sigma(d, sigma, sigma_next));
+  if (!d.low_init) {  // the first low-res step: its latent is the noise, no clean estimate yet (animad.cpp:430)
+    DHIP(hipMemcpyAsync(d.nfull, d.lat, 4 * full, hipMemcpyDeviceToDevice, d.st));
+    DTRY(hxa_fill_const_launch(d.dhat, 0, (size_t)full, 0.0f, d.st));
+    d.low_init = true;
+  }
+  Pass ps = low_pass(d, factor);
+  ps.lat_in = d.xlow;
+  ps.lat_out = d.vlow;
+  return run_graph(d, use_graph, d.graphL[factor], d.execL[factor], [&]() {
+    DTRY(hxa_lowres_pool_launch(d.nfull, d.dhat, BC, H, W, factor, d.sig, d.xlow, d.st));
+    DTRY(record_step(d, ps));
+    return hxa_lowres_velocity_launch(d.xlow, d.vlow, d.lat, d.nfull, d.dhat, BC, H, W, factor, d.sig, d.st);
+  });
+}
+
+extern "C" int hxa_dit_moss_step_lowres(void *p, float code, float rope_scale, int use_graph) {
+  Dit &d = *(Dit *)p;
+  if (!d.x0rows) return dfail(HXA_E_MODE, "dit: hxa_dit_moss_step_lowres needs the MOSS reference form");
+  const int gh = d.cfg.lat_h / 2, gw = d.cfg.lat_w / 2, C4 = 4 * d.cfg.lat_c, B = d.bd.batch;
+  if (gh % 2 || gw % 2) return hxa_dit_moss_step(p, code, use_graph);  // mossrun.cpp:289: an even grid only
+  const long low = (long)B * (gh / 2) * (gw / 2) * C4;
+  DTRY(ensure(d.zl, low));
+  DTRY(ensure(d.x0l, low));
+  DTRY(low_rope(d, 2, rope_scale));
+  DTRY(set_sigma(d, code, code));
+  if (!d.low_init) {  // mossrun.cpp:290-291: the low-res noise, and a clean estimate of 0
+    DTRY(hxa_moss_pool2_launch(d.zrows, B, gh, gw, C4, d.zl, d.st));
+    DTRY(hxa_fill_const_launch(d.x0l, 0, (size_t)low, 0.0f, d.st));
+    d.low_init = true;
+  }
+  d.moss_low_live = true;
+  Pass ps = low_pass(d, 2);
+  ps.zrows = d.zl;
+  ps.x0rows = d.x0l;
+  return run_graph(d, use_graph, d.graphL[2], d.execL[2], [&]() { return record_step(d, ps); });
+}
+
 extern "C" int hxa_dit_velocity(void *p, float sigma, float *v) {
   Dit &d = *(Dit *)p;
   if (d.x0rows) return dfail(HXA_E_MODE, "dit: the rapid-moss form has no velocity output");
   DTRY(set_sigma(d, sigma, sigma));
-  DTRY(record_step(d, MODE_VELOCITY));
+  DTRY(record_step(d, full_pass(d, MODE_VELOCITY)));
   const long latn = (long)d.bd.batch * d.cfg.lat_c * d.cfg.lat_h * d.cfg.lat_w;
   DHIP(hipMemcpyAsync(v, d.vel, 4 * latn, hipMemcpyDeviceToHost, d.st));
   DHIP(hipStreamSynchronize(d.st));

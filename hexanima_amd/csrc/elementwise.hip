@@ -38,7 +38,9 @@ __global__ __launch_bounds__(256) void normrow_kernel(float *__restrict__ x, lon
   __shared__ float red[8];
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float4_t *xr = (float4_t *)(x + (long)row * ldx);
-  float4_t v[NV];
+  // every load of the row is issued up front (x, the pending terms and the column vectors), so the row costs one
+  // memory latency; the vectors' multiplier (1 + scale) [* w] and shift are formed while x is in flight
+  float4_t v[NV], mul[NV], sh[NV];
 #pragma unroll
   for (int k = 0; k < NV; k++) {
     const int c = (tid + 256 * k) * 4;
@@ -59,9 +61,22 @@ __global__ __launch_bounds__(256) void normrow_kernel(float *__restrict__ x, lon
 #pragma unroll
           for (int e = 0; e < 4; e++) v[k][e] = fmaf(g[e], (float)a[e], v[k][e]);
         }
-        xr[tid + 256 * k] = v[k];
       }
     }
+  }
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    const int c = (tid + 256 * k) * 4;
+    if (c < D) {
+      mul[k] = *(const float4_t *)(scale + c) + 1.0f;
+      if (w != nullptr) mul[k] *= *(const float4_t *)(w + c);  // k_rms_prep: M = (1 + scale) * w
+      sh[k] = *(const float4_t *)(shift + c);
+    }
+  }
+  if (t != nullptr) {
+#pragma unroll
+    for (int k = 0; k < NV; k++)
+      if ((tid + 256 * k) * 4 < D) xr[tid + 256 * k] = v[k];
   }
   float s = 0.0f, q = 0.0f;
 #pragma unroll
@@ -91,12 +106,9 @@ __global__ __launch_bounds__(256) void normrow_kernel(float *__restrict__ x, lon
   for (int k = 0; k < NV; k++) {
     const int c = (tid + 256 * k) * 4;
     if (c < D) {
-      float4_t mul = *(const float4_t *)(scale + c) + 1.0f;
-      if (w != nullptr) mul *= *(const float4_t *)(w + c);  // k_rms_prep: M = (1 + scale) * w
-      const float4_t sh = *(const float4_t *)(shift + c);
       half4_t o;
 #pragma unroll
-      for (int e = 0; e < 4; e++) o[e] = (hxa_h)((v[k][e] - mu) * r * mul[e] + sh[e]);
+      for (int e = 0; e < 4; e++) o[e] = (hxa_h)((v[k][e] - mu) * r * mul[k][e] + sh[k][e]);
       *(half4_t *)(h + (long)row * ldh + c) = o;
     }
   }
@@ -807,6 +819,99 @@ __global__ void bn_unpatchify_kernel(const float *__restrict__ x0, const float *
   lat[(((long)b * Cc + c) * H + 2 * gy + ph) * W + 2 * gx + pw] = x0[i] * sqrtf(var[f] + 1e-4f) + mean[f];
 }
 
+// ---- low-res first steps (phone/animad.cpp:392-503, moss/mossrun/mossrun.cpp:278-313). Round-to-nearest
+// operations in the reference's order, no contraction: the results are the reference's fp32 / double values.
+// t = sig[0], tn = sig[1], sig[2] = tn - t (the runner's sigma vector in device memory).
+// x_low [BC][H/f][W/f] = (1 - t) mean_fxf(dhat) + t sum_fxf(noise) / f, the sums in double (animad.cpp:429-437)
+__global__ void lowres_pool_kernel(const float *__restrict__ nfull, const float *__restrict__ dhat, long BC, int H, int W,
+                                   int f, const float *__restrict__ sig, float *__restrict__ xlow) {
+  const int Hl = H / f, Wl = W / f;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= BC * Hl * Wl) return;
+  const int x = (int)(i % Wl), y = (int)((i / Wl) % Hl);
+  const long c = i / ((long)Wl * Hl);
+  double sn = 0.0, sd = 0.0;
+  for (int a = 0; a < f; a++)
+    for (int b = 0; b < f; b++) {
+      const long j = (c * H + (long)y * f + a) * W + (long)x * f + b;
+      sn = __dadd_rn(sn, (double)nfull[j]);
+      sd = __dadd_rn(sd, (double)dhat[j]);
+    }
+  const float t = sig[0];  // (1 - t) is a float expression in the reference, the rest double
+  xlow[i] = (float)__dadd_rn(__ddiv_rn(__dmul_rn((double)__fsub_rn(1.0f, t), sd), (double)(f * f)),
+                             __ddiv_rn(__dmul_rn((double)t, sn), (double)f));
+}
+// dl = x_low - t v_low bilinearly upsampled (half-pixel centres, clamped) into dhat; x_next = (1 - tn) dhat + tn noise;
+// v = (x - x_next) / (t - tn) (0 when t - tn <= 1e-6); then the Euler step x += (tn - t) v in place (animad.cpp:486-503
+// and the sampler's update)
+__global__ void lowres_velocity_kernel(const float *__restrict__ xlow, const float *__restrict__ vlow, float *__restrict__ lat,
+                                       const float *__restrict__ nfull, float *__restrict__ dhat, long BC, int H, int W,
+                                       int f, const float *__restrict__ sig) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= BC * H * W) return;
+  const int Hl = H / f, Wl = W / f;
+  const int x = (int)(i % W), y = (int)((i / W) % H);
+  const long c = i / ((long)W * H);
+  const float t = sig[0];
+  const double tn = (double)sig[1], dt = __dsub_rn((double)t, tn);
+  const float fy = __fsub_rn(__fdiv_rn(__fadd_rn((float)y, 0.5f), (float)f), 0.5f);
+  const float fx = __fsub_rn(__fdiv_rn(__fadd_rn((float)x, 0.5f), (float)f), 0.5f);
+  int y0 = (int)floorf(fy), x0 = (int)floorf(fx);
+  const float wy = __fsub_rn(fy, (float)y0), wx = __fsub_rn(fx, (float)x0);
+  const int y1 = min(max(y0 + 1, 0), Hl - 1), x1 = min(max(x0 + 1, 0), Wl - 1);
+  y0 = min(max(y0, 0), Hl - 1);
+  x0 = min(max(x0, 0), Wl - 1);
+  const long base = c * Hl * Wl;
+  auto dl = [&](int yy, int xx) {
+    const long j = base + (long)yy * Wl + xx;
+    return __fsub_rn(xlow[j], __fmul_rn(t, vlow[j]));
+  };
+  const float owy = __fsub_rn(1.0f, wy), owx = __fsub_rn(1.0f, wx);
+  const float top = __fadd_rn(__fmul_rn(owx, dl(y0, x0)), __fmul_rn(wx, dl(y0, x1)));
+  const float bot = __fadd_rn(__fmul_rn(owx, dl(y1, x0)), __fmul_rn(wx, dl(y1, x1)));
+  const float up = __fadd_rn(__fmul_rn(owy, top), __fmul_rn(wy, bot));
+  dhat[i] = up;
+  const float xnext = __fadd_rn(__fmul_rn((float)__dsub_rn(1.0, tn), up), __fmul_rn((float)tn, nfull[i]));
+  const float xf = lat[i];
+  const float v = dt > 1e-6 ? __fdiv_rn(__fsub_rn(xf, xnext), (float)dt) : 0.0f;
+  lat[i] = __fadd_rn(xf, __fmul_rn(sig[2], v));
+}
+// token rows [B][H*W][C4] -> 2 x the 2x2 mean, [B][(H/2)*(W/2)][C4] (mossrun.cpp:291)
+__global__ void moss_pool2_kernel(const float *__restrict__ z, int B, int H, int W, int C4, float *__restrict__ zl) {
+  const int Wl = W / 2, Tl = (H / 2) * Wl;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)B * Tl * C4) return;
+  const int cc = (int)(i % C4), tk = (int)((i / C4) % Tl);
+  const long b = i / ((long)C4 * Tl);
+  const int ii = tk / Wl, jj = tk % Wl;
+  const float *zb = z + b * H * W * C4;
+  auto at = [&](int r, int q) { return zb[((long)r * W + q) * C4 + cc]; };
+  const float sum = __fadd_rn(__fadd_rn(__fadd_rn(at(2 * ii, 2 * jj), at(2 * ii, 2 * jj + 1)), at(2 * ii + 1, 2 * jj)),
+                              at(2 * ii + 1, 2 * jj + 1));
+  zl[i] = __fmul_rn(0.5f, sum);
+}
+// token rows [B][h*w][C4] -> bilinear 2x with half-pixel centres, clamped, [B][(2h)*(2w)][C4] (mossrun.cpp:278-282)
+__global__ void upsample2_rows_kernel(const float *__restrict__ src, int B, int h, int w, int C4, float *__restrict__ dst) {
+  const int Tn = 4 * h * w;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)B * Tn * C4) return;
+  const int cc = (int)(i % C4), tk = (int)((i / C4) % Tn);
+  const long b = i / ((long)C4 * Tn);
+  const int y = tk / (2 * w), x = tk % (2 * w);
+  const float fy = __fsub_rn(__fdiv_rn(__fadd_rn((float)y, 0.5f), 2.0f), 0.5f);
+  const float fx = __fsub_rn(__fdiv_rn(__fadd_rn((float)x, 0.5f), 2.0f), 0.5f);
+  const int y0 = (int)floorf(fy), x0 = (int)floorf(fx);
+  const float ty = __fsub_rn(fy, (float)y0), tx = __fsub_rn(fx, (float)x0);
+  const int ya = min(max(y0, 0), h - 1), yb = min(max(y0 + 1, 0), h - 1);
+  const int xa = min(max(x0, 0), w - 1), xb = min(max(x0 + 1, 0), w - 1);
+  const float *sb = src + b * h * w * C4;
+  auto at = [&](int r, int q) { return sb[((long)r * w + q) * C4 + cc]; };
+  const float otx = __fsub_rn(1.0f, tx), oty = __fsub_rn(1.0f, ty);
+  const float top = __fadd_rn(__fmul_rn(otx, at(ya, xa)), __fmul_rn(tx, at(ya, xb)));
+  const float bot = __fadd_rn(__fmul_rn(otx, at(yb, xa)), __fmul_rn(tx, at(yb, xb)));
+  dst[i] = __fadd_rn(__fmul_rn(oty, top), __fmul_rn(ty, bot));
+}
+
 int hxa_rmsvec_launch(const float *x, int n, const hxa_h *w, float eps, float *y, hipStream_t st) {
   if (n <= 0 || n > 4096) return HXA_E_ARG;
   hxa_launch(rmsvec_kernel, dim3(1), dim3(256), 0, st, x, n, w, eps, y);
@@ -837,6 +942,30 @@ int hxa_bn_unpatchify_launch(const float *x0, const float *mean, const float *va
                              hipStream_t st) {
   hxa_launch(bn_unpatchify_kernel, dim3(nblk((long)B * Cc * H * W)), dim3(256), 0, st, x0, mean, var, B, Cc, H, W,
                      lat);
+  return LAUNCH_OK();
+}
+
+int hxa_lowres_pool_launch(const float *nfull, const float *dhat, long BC, int H, int W, int f, const float *sig,
+                           float *xlow, hipStream_t st) {
+  if (f < 2 || H % f || W % f || BC <= 0) return HXA_E_ARG;
+  hxa_launch(lowres_pool_kernel, dim3(nblk(BC * (H / f) * (W / f))), dim3(256), 0, st, nfull, dhat, BC, H, W, f, sig, xlow);
+  return LAUNCH_OK();
+}
+int hxa_lowres_velocity_launch(const float *xlow, const float *vlow, float *lat, const float *nfull, float *dhat, long BC,
+                               int H, int W, int f, const float *sig, hipStream_t st) {
+  if (f < 2 || H % f || W % f || BC <= 0) return HXA_E_ARG;
+  hxa_launch(lowres_velocity_kernel, dim3(nblk(BC * H * W)), dim3(256), 0, st, xlow, vlow, lat, nfull, dhat, BC, H, W, f,
+             sig);
+  return LAUNCH_OK();
+}
+int hxa_moss_pool2_launch(const float *z, int B, int H, int W, int C4, float *zl, hipStream_t st) {
+  if (H % 2 || W % 2 || B <= 0 || C4 <= 0) return HXA_E_ARG;
+  hxa_launch(moss_pool2_kernel, dim3(nblk((long)B * (H / 2) * (W / 2) * C4)), dim3(256), 0, st, z, B, H, W, C4, zl);
+  return LAUNCH_OK();
+}
+int hxa_upsample2_rows_launch(const float *src, int B, int h, int w, int C4, float *dst, hipStream_t st) {
+  if (h <= 0 || w <= 0 || B <= 0 || C4 <= 0) return HXA_E_ARG;
+  hxa_launch(upsample2_rows_kernel, dim3(nblk((long)B * 4 * h * w * C4)), dim3(256), 0, st, src, B, h, w, C4, dst);
   return LAUNCH_OK();
 }
 

@@ -112,6 +112,17 @@ int hxa_bn_unpatchify_launch(const float *x0, const float *mean, const float *va
                              hipStream_t st);
 int hxa_quantize_launch(const float *W, int N, int K, int fmt, void *q, hxa_h *s, hipStream_t st);
 int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t st);
+// low-res first steps (phone/animad.cpp:392-503, moss/mossrun/mossrun.cpp:278-313); sig: t, tn, tn - t on the device.
+// x_low [BC][H/f][W/f] from the full-res noise and clean estimate [BC][H][W]
+int hxa_lowres_pool_launch(const float *nfull, const float *dhat, long BC, int H, int W, int f, const float *sig,
+                           float *xlow, hipStream_t st);
+// the low-res velocity -> dhat (upsampled clean estimate) and the Euler step lat += (tn - t) v of the velocity that lands
+// it on (1 - tn) dhat + tn noise
+int hxa_lowres_velocity_launch(const float *xlow, const float *vlow, float *lat, const float *nfull, float *dhat, long BC,
+                               int H, int W, int f, const float *sig, hipStream_t st);
+// MOSS: token rows [B][H*W][C4] -> 2 x 2x2 mean [B][(H/2)*(W/2)][C4]; bilinear 2x of token rows [B][h*w][C4]
+int hxa_moss_pool2_launch(const float *z, int B, int H, int W, int C4, float *zl, hipStream_t st);
+int hxa_upsample2_rows_launch(const float *src, int B, int h, int w, int C4, float *dst, hipStream_t st);
 
 // matrix shapes of a GPU block pack (see hxa_pack_layout); returns the matrix count
 int hxa_pack_mats(int kind, int D, int F, int DC, int fa, int fm, int *N, int *K, int *fmt);

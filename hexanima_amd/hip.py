@@ -97,6 +97,8 @@ _SIGS = {
     "hxa_dit_step": (I, [P, F, F, I]),
     "hxa_dit_velocity": (I, [P, F, P]),
     "hxa_dit_moss_step": (I, [P, F, I]),
+    "hxa_dit_step_lowres": (I, [P, F, F, I, I]),
+    "hxa_dit_moss_step_lowres": (I, [P, F, F, I]),
     "hxa_dit_export": (L, [P, I, P, SZ]),
     "hxa_dit_stream": (P, [P]),
 }

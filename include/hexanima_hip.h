@@ -275,6 +275,20 @@ int hxa_dit_velocity(void *dit, float sigma, float *v);
  * time code: x_in = z + Q x0, v = head(blocks(embed(x_in), text)), x0 = z - v; the latent set by hxa_dit_set_inputs
  * is the noise z, and x0 starts at 0 */
 int hxa_dit_moss_step(void *dit, float code, int use_graph);
+/* Low-res first steps (phone/animad.cpp:392-503). One Euler step from sigma to sigma_next whose velocity comes from the
+ * DiT run on a latent downsampled by `factor` (a quarter of the tokens at 2): with the latent of the first low-res step
+ * after hxa_dit_set_inputs taken as the noise n and dhat the last clean estimate (0 at first),
+ * x_low = (1 - sigma) mean_fxf(dhat) + sigma sum_fxf(n) / factor; v_low = DiT(x_low, sigma);
+ * dhat = bilinear_up(x_low - sigma v_low) (half-pixel centres); the latent becomes x + (sigma_next - sigma) v with
+ * v = (x - ((1 - sigma_next) dhat + sigma_next n)) / (sigma - sigma_next), i.e. (1 - sigma_next) dhat + sigma_next n.
+ * Low-res steps come first. A factor the latent does not divide into 2x2 patches, or whose token count is not a
+ * multiple of 32, runs a full-resolution step instead, as the reference does. Anima-structure DiTs (either form). */
+int hxa_dit_step_lowres(void *dit, float sigma, float sigma_next, int factor, int use_graph);
+/* MOSS low-res first steps (moss/mossrun/mossrun.cpp:288-313): a rapid-moss step on the half-size token grid, from the
+ * noise pooled 2x2 (2 x the mean) and its own clean estimate (0 at first), image RoPE positions times rope_scale
+ * (MOSS_LOWSCALE, 2 in the reference); the first hxa_dit_moss_step after them starts from that clean estimate
+ * upsampled 2x (bilinear, half-pixel centres). An odd token grid runs a full-resolution step instead. */
+int hxa_dit_moss_step_lowres(void *dit, float code, float rope_scale, int use_graph);
 /* copies of the device weights for checking (host may be NULL to query the size; returns bytes):
  *   which in [0, nblocks): block pack `which`
  *   which in [nblocks, 2 nblocks): modulation weights of block which-nblocks, fp16 [6D][D]

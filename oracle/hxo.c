@@ -561,15 +561,115 @@ void hxo_rope_anima(int gh, int gw, float *cosT, float *sinT) {
   }
 }
 void hxo_rope_moss(int H, int W, int ntxt, const float *bands16, float *cosT, float *sinT) {
+  hxo_rope_moss_scaled(H, W, ntxt, bands16, 1.0, cosT, sinT);
+}
+/* moss/mossrun/mossrun.cpp:190-201 with its position scale: image positions (row, column) times `scale` (the
+ * low-res steps' MOSS_LOWSCALE, 2 by default: mossrun.cpp:288, :313) */
+void hxo_rope_moss_scaled(int H, int W, int ntxt, const float *bands16, double scale, float *cosT, float *sinT) {
   const int nimg = H * W;
   for (int tk = 0; tk < nimg + ntxt; tk++) {
     double pos[4];
-    if (tk < nimg) { pos[0] = 0; pos[1] = ntxt; pos[2] = (tk / W) - (H - 1) / 2.0; pos[3] = (tk % W) - (W - 1) / 2.0; }
+    if (tk < nimg) {
+      pos[0] = 0; pos[1] = ntxt; pos[2] = ((tk / W) - (H - 1) / 2.0) * scale; pos[3] = ((tk % W) - (W - 1) / 2.0) * scale;
+    }
     else { pos[0] = 0; pos[1] = tk - nimg; pos[2] = 0; pos[3] = 0; }
     for (int d = 0; d < 64; d++) {
       const double ph = pos[d / 16] * (double)bands16[d % 16];
       cosT[(size_t)tk * 64 + d] = (float)cos(ph);
       sinT[(size_t)tk * 64 + d] = (float)sin(ph);
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------------------------------ */
+/* low-res first steps (no fp contraction: the expressions are rounded as written)                  */
+/* ------------------------------------------------------------------------------------------------ */
+/* phone/animad.cpp:429-437: the latent of a step run at 1/f resolution, [C][H/f][W/f] from the full-res noise of the
+ * first step and the previous full-res clean estimate: x_low = (1 - t) mean_fxf(dhat) + t sum_fxf(noise) / f (the
+ * noise mean times f keeps unit variance), both sums in double in (a, b) order */
+__attribute__((optimize("fp-contract=off")))
+void hxo_lowres_pool(const float *nfull, const float *dhat, int C, int H, int W, int f, float t, float *xlow) {
+  const int Hl = H / f, Wl = W / f;
+  for (int c = 0; c < C; c++)
+    for (int y = 0; y < Hl; y++)
+      for (int x = 0; x < Wl; x++) {
+        double sn = 0, sd = 0;
+        for (int a = 0; a < f; a++)
+          for (int b = 0; b < f; b++) {
+            const size_t i = ((size_t)c * H + y * f + a) * W + x * f + b;
+            sn += nfull[i];
+            sd += dhat[i];
+          }
+        xlow[((size_t)c * Hl + y) * Wl + x] = (float)((1 - t) * sd / (f * f) + t * sn / f);  /* 1 - t in float */
+      }
+}
+/* phone/animad.cpp:486-503: from the low-res velocity, the low-res clean estimate dl = x_low - t v_low, bilinearly
+ * upsampled with half-pixel centres (clamped at the edges) into dhat, the full-res state it implies at tn,
+ * x_next = (1 - tn) dhat + tn noise, and the velocity that lands sd.cpp's Euler step there, (x_full - x_next) / (t - tn)
+ * (0 when t - tn <= 1e-6). tn and t - tn in double as in the reference. */
+__attribute__((optimize("fp-contract=off")))
+void hxo_lowres_velocity(const float *xlow, const float *vlow, const float *xfull, const float *nfull, int C, int H, int W,
+                         int f, float t, double tn, float *dhat, float *vf) {
+  const int Hl = H / f, Wl = W / f;
+  const double dt = t - tn;
+  float *dl = (float *)malloc(sizeof(float) * (size_t)C * Hl * Wl);
+  for (size_t i = 0; i < (size_t)C * Hl * Wl; i++) dl[i] = xlow[i] - t * vlow[i];
+  for (int c = 0; c < C; c++)
+    for (int y = 0; y < H; y++) {
+      const float fy = (y + 0.5f) / f - 0.5f;
+      int y0 = (int)floorf(fy);
+      const float wy = fy - y0;
+      const int y1 = y0 + 1 < 0 ? 0 : (y0 + 1 > Hl - 1 ? Hl - 1 : y0 + 1);
+      y0 = y0 < 0 ? 0 : (y0 > Hl - 1 ? Hl - 1 : y0);
+      for (int x = 0; x < W; x++) {
+        const float fx = (x + 0.5f) / f - 0.5f;
+        int x0 = (int)floorf(fx);
+        const float wx = fx - x0;
+        const int x1 = x0 + 1 < 0 ? 0 : (x0 + 1 > Wl - 1 ? Wl - 1 : x0 + 1);
+        x0 = x0 < 0 ? 0 : (x0 > Wl - 1 ? Wl - 1 : x0);
+        const float *b = dl + (size_t)c * Hl * Wl;
+        const float up = (1 - wy) * ((1 - wx) * b[y0 * Wl + x0] + wx * b[y0 * Wl + x1]) +
+                         wy * ((1 - wx) * b[y1 * Wl + x0] + wx * b[y1 * Wl + x1]);
+        const size_t i = ((size_t)c * H + y) * W + x;
+        dhat[i] = up;
+        const float xnext = (float)(1 - tn) * up + (float)tn * nfull[i];
+        vf[i] = dt > 1e-6 ? (xfull[i] - xnext) / (float)dt : 0.f;
+      }
+    }
+  free(dl);
+}
+/* moss/mossrun/mossrun.cpp:291: the low-res noise of the MOSS steps, 2 x the mean of each 2x2 block of the token grid
+ * (unit variance), on token rows: z [H*W][C4] -> zl [(H/2)*(W/2)][C4] */
+__attribute__((optimize("fp-contract=off")))
+void hxo_moss_pool2(const float *z, int H, int W, int C4, float *zl) {
+  const int Wl = W / 2;
+  for (int i = 0; i < H / 2; i++)
+    for (int j = 0; j < Wl; j++)
+      for (int c = 0; c < C4; c++) {
+        const float p0 = z[((size_t)(2 * i) * W + 2 * j) * C4 + c], p1 = z[((size_t)(2 * i) * W + 2 * j + 1) * C4 + c];
+        const float p2 = z[((size_t)(2 * i + 1) * W + 2 * j) * C4 + c], p3 = z[((size_t)(2 * i + 1) * W + 2 * j + 1) * C4 + c];
+        zl[((size_t)i * Wl + j) * C4 + c] = 0.5f * (p0 + p1 + p2 + p3);
+      }
+}
+/* moss/mossrun/mossrun.cpp:278-282 upsample2: bilinear 2x with half-pixel centres, clamped, on token rows
+ * [h*w][C4] -> [(2h)*(2w)][C4] (the low-res clean estimate seeding the first full-res step, :311) */
+__attribute__((optimize("fp-contract=off")))
+void hxo_upsample2_rows(const float *src, int h, int w, int C4, float *dst) {
+  for (int y = 0; y < 2 * h; y++) {
+    const float fy = (y + 0.5f) / 2 - 0.5f;
+    const int y0 = (int)floorf(fy);
+    const float ty = fy - y0;
+    const int ya = y0 < 0 ? 0 : (y0 > h - 1 ? h - 1 : y0), yb = y0 + 1 < 0 ? 0 : (y0 + 1 > h - 1 ? h - 1 : y0 + 1);
+    for (int x = 0; x < 2 * w; x++) {
+      const float fx = (x + 0.5f) / 2 - 0.5f;
+      const int x0 = (int)floorf(fx);
+      const float tx = fx - x0;
+      const int xa = x0 < 0 ? 0 : (x0 > w - 1 ? w - 1 : x0), xb = x0 + 1 < 0 ? 0 : (x0 + 1 > w - 1 ? w - 1 : x0 + 1);
+      for (int c = 0; c < C4; c++) {
+        const float a = src[((size_t)ya * w + xa) * C4 + c], b = src[((size_t)ya * w + xb) * C4 + c];
+        const float cc = src[((size_t)yb * w + xa) * C4 + c], d = src[((size_t)yb * w + xb) * C4 + c];
+        dst[((size_t)y * 2 * w + x) * C4 + c] = (1 - ty) * ((1 - tx) * a + tx * b) + ty * ((1 - tx) * cc + tx * d);
+      }
     }
   }
 }

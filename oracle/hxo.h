@@ -103,6 +103,13 @@ void hxo_q4arec_unpack(const uint8_t *rec, int N, int K, uint16_t *wNK);
    moss:  moss_ref.py:27-35 (4 axes x 16 bands; image tokens (0, ntxt, h-(H-1)/2, w-(W-1)/2), text (0, i, 0, 0)) */
 void hxo_rope_anima(int gh, int gw, float *cosT, float *sinT);
 void hxo_rope_moss(int H, int W, int ntxt, const float *bands16, float *cosT, float *sinT);
+void hxo_rope_moss_scaled(int H, int W, int ntxt, const float *bands16, double scale, float *cosT, float *sinT);
+/* low-res first steps: phone/animad.cpp:429-437, :486-503; moss/mossrun/mossrun.cpp:278-282, :291 */
+void hxo_lowres_pool(const float *nfull, const float *dhat, int C, int H, int W, int f, float t, float *xlow);
+void hxo_lowres_velocity(const float *xlow, const float *vlow, const float *xfull, const float *nfull, int C, int H, int W,
+                         int f, float t, double tn, float *dhat, float *vf);
+void hxo_moss_pool2(const float *z, int H, int W, int C4, float *zl);
+void hxo_upsample2_rows(const float *src, int h, int w, int C4, float *dst);
 
 /* ---- one Anima-structure DiT block (blk.c:149-176; appendix semantics in the header comment of hxo.c) ---- */
 typedef struct {

@@ -107,6 +107,11 @@ def lib():
             "hxo_q4arec_unpack": (None, [P, I, I, P]),
             "hxo_rope_anima": (None, [I, I, P, P]),
             "hxo_rope_moss": (None, [I, I, I, P, P, P]),
+            "hxo_rope_moss_scaled": (None, [I, I, I, P, C.c_double, P, P]),
+            "hxo_lowres_pool": (None, [P, P, I, I, I, I, C.c_float, P]),
+            "hxo_lowres_velocity": (None, [P, P, P, P, I, I, I, I, C.c_float, C.c_double, P, P]),
+            "hxo_moss_pool2": (None, [P, I, I, I, P]),
+            "hxo_upsample2_rows": (None, [P, I, I, I, P]),
             "hxo_anima_block": (I, [C.POINTER(_Cfg), C.POINTER(_AW), P, P, P, P, P, C.POINTER(_AB)]),
             "hxo_moss_block": (I, [C.POINTER(_MCfg), C.POINTER(_MW), P, P, P, P, C.POINTER(_MB)]),
             "hxo_sinusoid": (None, [C.c_float, I, P]),
@@ -367,6 +372,52 @@ def rope_moss(H, W, ntxt, bands16):
     bands16 = _f32(bands16)
     lib().hxo_rope_moss(H, W, ntxt, _p(bands16), _p(c), _p(s))
     return c, s
+
+
+def rope_moss_scaled(H, W, ntxt, bands16, scale):
+    """moss/mossrun/mossrun.cpp:190-201 with image positions times `scale` (the low-res steps, :313)"""
+    T = H * W + ntxt
+    c = np.empty((T, 64), np.float32)
+    s = np.empty((T, 64), np.float32)
+    bands16 = _f32(bands16)
+    lib().hxo_rope_moss_scaled(H, W, ntxt, _p(bands16), float(scale), _p(c), _p(s))
+    return c, s
+
+
+def lowres_pool(nfull, dhat, f, t):
+    """phone/animad.cpp:429-437: [C][H][W] noise and clean estimate -> the [C][H/f][W/f] latent of a 1/f step"""
+    nfull, dhat = _f32(nfull), _f32(dhat)
+    Cc, H, W = nfull.shape
+    out = np.empty((Cc, H // f, W // f), np.float32)
+    lib().hxo_lowres_pool(_p(nfull), _p(dhat), Cc, H, W, f, float(t), _p(out))
+    return out
+
+
+def lowres_velocity(xlow, vlow, xfull, nfull, f, t, tn):
+    """phone/animad.cpp:486-503: (dhat, v) -- the upsampled clean estimate and the full-res velocity that lands the
+    Euler step from t to tn on (1 - tn) dhat + tn noise"""
+    xlow, vlow, xfull, nfull = _f32(xlow), _f32(vlow), _f32(xfull), _f32(nfull)
+    Cc, H, W = xfull.shape
+    dhat = np.empty_like(xfull)
+    vf = np.empty_like(xfull)
+    lib().hxo_lowres_velocity(_p(xlow), _p(vlow), _p(xfull), _p(nfull), Cc, H, W, f, float(t), float(tn), _p(dhat), _p(vf))
+    return dhat, vf
+
+
+def moss_pool2(z, H, W):
+    """moss/mossrun/mossrun.cpp:291: token rows [H*W][C4] -> 2 x the 2x2 mean, [(H/2)*(W/2)][C4]"""
+    z = _f32(z)
+    out = np.empty(((H // 2) * (W // 2), z.shape[1]), np.float32)
+    lib().hxo_moss_pool2(_p(z), H, W, z.shape[1], _p(out))
+    return out
+
+
+def upsample2_rows(src, h, w):
+    """moss/mossrun/mossrun.cpp:278-282: token rows [h*w][C4] -> bilinear 2x, [(2h)*(2w)][C4]"""
+    src = _f32(src)
+    out = np.empty((4 * h * w, src.shape[1]), np.float32)
+    lib().hxo_upsample2_rows(_p(src), h, w, src.shape[1], _p(out))
+    return out
 
 
 def sinusoid(t, dim):

@@ -213,9 +213,10 @@ def oracle_anima_ref_velocity(lat, ctx16, sigma, blocks, modws, glue, *, D, H, F
 
 
 def oracle_moss_rapid_step(z, x0, txt16, code, blocks, modw, glue, vec, *, D, H, F, C4, ntxt, Ttot, gh, gw,
-                           attn_mode=0):
+                           attn_mode=0, rope_scale=1.0):
     """One rapid-moss step (mossrun.cpp:307-334) with the reference's glue, image by image. z, x0: token rows
-    [B][T][C4] (feature c*4 + ph*2 + pw); returns the new x0.
+    [B][T][C4] (feature c*4 + ph*2 + pw) of a gh x gw grid; returns the new x0. rope_scale: the low-res steps' image
+    position scale (mossrun.cpp:313).
     time_vecs (mossrun.cpp:255-264): e = sinusoid_256(code), a = T0 e + b0, b = T2 silu(a) + b2, block modulation
     Wm b + bm [6][D], head modulation Wh b + bh; x_in = z + x0 Q^T per token; rows = Wv x_in + bv, then the text rows
     f16(text Wt^T) (the text projection into zeroed rows); blocks; head RMS(x) nfin (1 + head[D:]) + head[:D],
@@ -230,7 +231,7 @@ def oracle_moss_rapid_step(z, x0, txt16, code, blocks, modw, glue, vec, *, D, H,
     mod6 = (hxo.linear_f32(bt, modw)[0] + bm).reshape(6, D).astype(np.float32)
     head = (hxo.linear_f32(bt, Wh)[0] + bh).astype(np.float32)
     bands = (1.0 / 10000.0 ** (np.arange(16) / 16.0)).astype(np.float32)
-    c, sn = hxo.rope_moss(gh, gw, ntxt, bands)
+    c, sn = hxo.rope_moss_scaled(gh, gw, ntxt, bands, rope_scale)  # image positions x rope_scale (low-res steps)
     cos = np.ones((Ttot, 64), np.float32)
     sin = np.zeros((Ttot, 64), np.float32)
     cos[:c.shape[0]], sin[:c.shape[0]] = c, sn
