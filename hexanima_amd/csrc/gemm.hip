@@ -715,6 +715,12 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
       else wait_vm<L * LPS>();
     }
   };
+  // Quantised W is read raw in the memory phase (wq, scale sc, offset zc) and dequantised in the compute phase, where
+  // its VALU work issues under the MFMAs (the memory phase stays a phase of LDS reads and loads only): the
+  // dequantisation of the second 16-deep slice overlaps the first slice's MFMAs.
+  typedef typename std::conditional<FMT == HXA_W_Q8, uint2_t, uint32_t>::type raw_t;
+  [[maybe_unused]] raw_t wq[2][NI];
+  [[maybe_unused]] hxa_h sc[NI], zc[NI];
   auto read_frags = [&](int s, half8_t (&fa)[2][MI], half8_t (&fb)[2][NI]) {
     const uint8_t *st = lds8 + s * G::STAGE;
     const uint8_t *ws = st + G::A_BYTES;
@@ -731,22 +737,34 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
         const int row = grp * (BN / 2) + wn * WTN + j * 32 + (lane & 31);
         if constexpr (FMT == HXA_W_F16) {
           fb[ks][j] = *(const half8_t *)(ws + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
-        } else {
-          const hxa_h sc = *(const hxa_h *)(ws + G::W_BYTES + row * 2);
-          const hxa_h zc = ASYM ? *(const hxa_h *)(ws + G::W_BYTES + G::S_BYTES + row * 2) : (hxa_h)0.0f;
-          const half2_t s2 = {sc, sc};
-          uint32_t o[4];
-          if constexpr (FMT == HXA_W_Q8) {  // 8-byte slot cl of the row: chunk cl >> 1 (swizzled), half cl & 1
-            const uint2_t q = *(const uint2_t *)(ws + row * 32 + (((cl >> 1) ^ ((row >> 3) & 1)) << 4) + ((cl & 1) << 3));
-            dq8_word(q.x, s2, o[0], o[1]);
-            dq8_word(q.y, s2, o[2], o[3]);
-          } else {  // 4-byte slot cl: 8 consecutive k
-            const half2_t z2 = {zc, zc};
-            dq4_word<ASYM>(*(const uint32_t *)(ws + row * 16 + (cl << 2)), s2, z2, o);
-          }
-          fb[ks][j] = __builtin_bit_cast(half8_t, (uint4_t){o[0], o[1], o[2], o[3]});
+        } else if constexpr (FMT == HXA_W_Q8) {  // 8-byte slot cl of the row: chunk cl >> 1 (swizzled), half cl & 1
+          wq[ks][j] = *(const uint2_t *)(ws + row * 32 + (((cl >> 1) ^ ((row >> 3) & 1)) << 4) + ((cl & 1) << 3));
+        } else {  // 4-byte slot cl: 8 consecutive k
+          wq[ks][j] = *(const uint32_t *)(ws + row * 16 + (cl << 2));
         }
       }
+    }
+    if constexpr (FMT != HXA_W_F16) {
+#pragma unroll
+      for (int j = 0; j < NI; j++) {
+        const int row = grp * (BN / 2) + wn * WTN + j * 32 + (lane & 31);
+        sc[j] = *(const hxa_h *)(ws + G::W_BYTES + row * 2);
+        zc[j] = ASYM ? *(const hxa_h *)(ws + G::W_BYTES + G::S_BYTES + row * 2) : (hxa_h)0.0f;
+      }
+    }
+  };
+  auto dequant = [&](int ks, int j, half8_t (&fb)[2][NI]) {
+    if constexpr (FMT != HXA_W_F16) {
+      const half2_t s2 = {sc[j], sc[j]};
+      uint32_t o[4];
+      if constexpr (FMT == HXA_W_Q8) {
+        dq8_word(wq[ks][j].x, s2, o[0], o[1]);
+        dq8_word(wq[ks][j].y, s2, o[2], o[3]);
+      } else {
+        const half2_t z2 = {zc[j], zc[j]};
+        dq4_word<ASYM>(wq[ks][j], s2, z2, o);
+      }
+      fb[ks][j] = __builtin_bit_cast(half8_t, (uint4_t){o[0], o[1], o[2], o[3]});
     }
   };
   float16_t acc[NI][MI];
@@ -754,13 +772,19 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
   for (int j = 0; j < NI; j++)
 #pragma unroll
     for (int i = 0; i < MI; i++) acc[j][i] = (float16_t){};
-  auto mfmas = [&](const half8_t (&fa)[2][MI], const half8_t (&fb)[2][NI]) {
+  auto mfmas = [&](const half8_t (&fa)[2][MI], half8_t (&fb)[2][NI]) {
+    if constexpr (FMT != HXA_W_F16) {
+#pragma unroll
+      for (int j = 0; j < NI; j++) dequant(0, j, fb);
+    }
 #pragma unroll
     for (int ks = 0; ks < 2; ks++)
 #pragma unroll
-      for (int j = 0; j < NI; j++)
+      for (int j = 0; j < NI; j++) {
+        if (ks == 0) dequant(1, j, fb);  // slice 1's fragment j, under slice 0's MFMAs
 #pragma unroll
         for (int i = 0; i < MI; i++) acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[ks][j], fa[ks][i], acc[j][i], 0, 0, 0);
+      }
   };
   auto bar = [&]() {
     __builtin_amdgcn_sched_barrier(0);
