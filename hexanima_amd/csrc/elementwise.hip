@@ -912,6 +912,33 @@ __global__ void upsample2_rows_kernel(const float *__restrict__ src, int B, int 
   dst[i] = __fadd_rn(__fmul_rn(oty, top), __fmul_rn(ty, bot));
 }
 
+// ---- weight-file import: the reference's on-disk tiles (already in device memory) -> k-tiled pack matrices.
+// fp16 crouton tiles of a [K][N] matrix, [N/32][K/32] tiles of 1024 halves with k pairs interleaved (export_all.py:7-8)
+// -> rows row0 .. row0 + N of a k-tiled [K/32][ldn][32] fp16 matrix; one thread per output element, k fastest
+__global__ void crouton_to_ktiled_kernel(const uint16_t *__restrict__ src, int N, int K, uint16_t *__restrict__ dst,
+                                         int row0, int ldn) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)N * K) return;
+  const int r = (int)(i & 31), n = (int)((i >> 5) % N);
+  const long g = (i >> 5) / N;
+  dst[(g * ldn + row0 + n) * 32 + r] = src[((long)(n >> 5) * (K / 32) + g) * 1024 + (r >> 1) * 64 + (n & 31) * 2 + (r & 1)];
+}
+// q8 records of a [K][N] matrix, [N/32][kbt] records of 1152 bytes: 64 fp16 scales (each stored twice) and 1024
+// offset-binary bytes u = q + 128 with k pairs interleaved (export_all.py:10-18) -> int8 rows row0 .. row0 + N of a
+// k-tiled [Kt/32][ldn][32] matrix and scales s[Kt/32][ldn]. Record k-block ib < nkb_main is k group ib, the others
+// (the rapid-moss LoRA's B rows, moss/export_moss.py:40-46) group lora_g + ib - nkb_main.
+__global__ void q8rec_to_ktiled_kernel(const uint8_t *__restrict__ rec, int N, int nkb, int kbt, uint8_t *__restrict__ q,
+                                       uint16_t *__restrict__ s, int row0, int ldn, int nkb_main, int lora_g) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)N * nkb * 32) return;
+  const int r = (int)(i & 31), n = (int)((i >> 5) % N), ib = (int)((i >> 5) / N);
+  const int c = n & 31;
+  const uint8_t *R = rec + ((long)(n >> 5) * kbt + ib) * 1152;
+  const long g = ib < nkb_main ? ib : lora_g + (ib - nkb_main);
+  q[(g * ldn + row0 + n) * 32 + r] = (uint8_t)(R[128 + (r >> 1) * 64 + c * 2 + (r & 1)] ^ 0x80);
+  if (r == 0) s[g * ldn + row0 + n] = ((const uint16_t *)R)[2 * c];
+}
+
 int hxa_rmsvec_launch(const float *x, int n, const hxa_h *w, float eps, float *y, hipStream_t st) {
   if (n <= 0 || n > 4096) return HXA_E_ARG;
   hxa_launch(rmsvec_kernel, dim3(1), dim3(256), 0, st, x, n, w, eps, y);
@@ -966,6 +993,20 @@ int hxa_moss_pool2_launch(const float *z, int B, int H, int W, int C4, float *zl
 int hxa_upsample2_rows_launch(const float *src, int B, int h, int w, int C4, float *dst, hipStream_t st) {
   if (h <= 0 || w <= 0 || B <= 0 || C4 <= 0) return HXA_E_ARG;
   hxa_launch(upsample2_rows_kernel, dim3(nblk((long)B * 4 * h * w * C4)), dim3(256), 0, st, src, B, h, w, C4, dst);
+  return LAUNCH_OK();
+}
+
+int hxa_crouton_to_ktiled_launch(const void *src, int N, int K, void *dst, int row0, int ldn, hipStream_t st) {
+  if (N % 32 || K % 32 || row0 < 0 || row0 + N > ldn) return HXA_E_ARG;
+  hxa_launch(crouton_to_ktiled_kernel, dim3(nblk((long)N * K)), dim3(256), 0, st, (const uint16_t *)src, N, K,
+             (uint16_t *)dst, row0, ldn);
+  return LAUNCH_OK();
+}
+int hxa_q8rec_to_ktiled_launch(const void *rec, int N, int nkb, int kbt, void *q, void *s, int row0, int ldn, int nkb_main,
+                               int lora_g, hipStream_t st) {
+  if (N % 32 || nkb <= 0 || nkb > kbt || row0 < 0 || row0 + N > ldn) return HXA_E_ARG;
+  hxa_launch(q8rec_to_ktiled_kernel, dim3(nblk((long)N * nkb * 32)), dim3(256), 0, st, (const uint8_t *)rec, N, nkb, kbt,
+             (uint8_t *)q, (uint16_t *)s, row0, ldn, nkb_main, lora_g);
   return LAUNCH_OK();
 }
 

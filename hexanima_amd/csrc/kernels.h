@@ -124,6 +124,12 @@ int hxa_lowres_velocity_launch(const float *xlow, const float *vlow, float *lat,
 int hxa_moss_pool2_launch(const float *z, int B, int H, int W, int C4, float *zl, hipStream_t st);
 int hxa_upsample2_rows_launch(const float *src, int B, int h, int w, int C4, float *dst, hipStream_t st);
 
+// weight-file import (device memory in and out): fp16 crouton tiles of a [K][N] matrix (export_all.py:7-8), or q8
+// records (export_all.py:10-18; record k-blocks >= nkb_main to k group lora_g + ...), -> rows row0.. of a k-tiled
+// [K/32][ldn][32] pack matrix (+ the q8 scales [K/32][ldn])
+int hxa_crouton_to_ktiled_launch(const void *src, int N, int K, void *dst, int row0, int ldn, hipStream_t st);
+int hxa_q8rec_to_ktiled_launch(const void *rec, int N, int nkb, int kbt, void *q, void *s, int row0, int ldn, int nkb_main,
+                               int lora_g, hipStream_t st);
 // matrix shapes of a GPU block pack (see hxa_pack_layout); returns the matrix count
 int hxa_pack_mats(int kind, int D, int F, int DC, int fa, int fm, int *N, int *K, int *fmt);
 

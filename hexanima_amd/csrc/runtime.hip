@@ -401,28 +401,7 @@ extern "C" long hxa_pack_layout(int kind, int D, int F, int DC, int fa, int fm, 
   return off;
 }
 // Block packs store every matrix k-tiled (HXA_W_KTILED): the chunk of row n and k group g (64 bytes fp16, 32 q8,
-// 16 q4) moves from n * G * cb + g * cb to g * N * cb + n * cb, so each 32-deep k step of the matrix is contiguous.
-static int chunk_bytes(int fmt) { return fmt == HXA_W_F16 ? 64 : fmt == HXA_W_Q8 ? 32 : 16; }
-static void tile_matrix_host(const uint8_t *rm, uint8_t *kt, int N, int K, int fmt) {
-  const int cb = chunk_bytes(fmt), G = K / 32;
-  par_for(G, [&](int g) {
-    for (int n = 0; n < N; n++) memcpy(kt + ((size_t)g * N + n) * cb, rm + ((size_t)n * G + g) * cb, cb);
-  });
-}
-// host image of a pack whose matrices were written row-major -> the k-tiled pack (scales / vectors unchanged)
-static void tile_pack_host(std::vector<uint8_t> &host, int kind, int D, int F, int DC, int fa, int fm) {
-  int N[8], K[8], f[8];
-  const int n = hxa_pack_mats(kind, D, F, DC, fa, fm, N, K, f);
-  long offs[32];
-  hxa_pack_layout(kind, D, F, DC, fa, fm, offs, 32);
-  std::vector<uint8_t> tmp;
-  for (int i = 0; i < n; i++) {
-    const size_t bytes = (size_t)N[i] * K[i] / 32 * chunk_bytes(f[i]);
-    tmp.assign(host.begin() + offs[3 * i], host.begin() + offs[3 * i] + bytes);
-    tile_matrix_host(tmp.data(), host.data() + offs[3 * i], N[i], K[i], f[i]);
-  }
-}
-
+// 16 q4) sits at g * N * cb + n * cb, so each 32-deep k step of the matrix is contiguous.
 struct PackView {
   HxaWeight w[8];
   int nmat;
@@ -924,6 +903,8 @@ struct Ctx {
   void *ws = nullptr;
   size_t x_bytes = 0, ctx_bytes = 0, cs_bytes = 0, sn_bytes = 0, mod_bytes = 0, ws_bytes = 0, stage_bytes = 0;
   int cur_T = 0, cur_C = 0;
+  void *wstage = nullptr;  // a registered weight file's bytes in device memory while it is converted into a pack
+  size_t wstage_bytes = 0;
 };
 std::mutex g_ctx_mu;
 
@@ -937,34 +918,25 @@ int ensure(void **p, size_t *have, size_t need) {
   return HXA_OK;
 }
 
-// fp16 crouton weight tiles of matrix [K][N] ([nb][kb], tile rows = k) -> W[N][K] (export_all.py:7-8)
-void crouton_to_nk(const uint16_t *tiles, int N, int K, uint16_t *w) {
-  const int kb = K / 32;
-  par_for(N / 32, [&](int nb) {
-    for (int n = nb * 32; n < nb * 32 + 32; n++)
-      for (int k = 0; k < K; k++) {
-        const int r = k & 31, c = n & 31;
-        w[(size_t)n * K + k] = tiles[((size_t)(n >> 5) * kb + (k >> 5)) * 1024 + (r >> 1) * 64 + c * 2 + (r & 1)];
-      }
-  });
+// A registered weight file is converted on the GPU: its bytes [off, off + bytes) are copied once into the import
+// staging buffer, then one gather kernel per matrix writes the k-tiled pack matrix (and the q8 scales) straight from
+// the reference's tiles.
+int stage_weights(Ctx &c, const HostBuf &hb, size_t off, size_t bytes, const uint8_t **dev) {
+  if (ensure(&c.wstage, &c.wstage_bytes, bytes) != HXA_OK) return fail(HXA_E_RESOURCE, "weight staging: out of device memory");
+  HIPC(hipMemcpyAsync(c.wstage, (const uint8_t *)hb.ptr + off, bytes, hipMemcpyHostToDevice, c.st));
+  *dev = (const uint8_t *)c.wstage;
+  return HXA_OK;
 }
-// q8 records (export_all.py:10-18) of a matrix [K][N] stored [N/32][kbt] -> int8 q[n][col] (row stride ldq) + fp16
-// scales s[col/32][n] (row stride lds). Record k-block ib < nkb_main lands at column 32 ib, the LoRA-B blocks after it
-// (ib >= nkb_main, moss/export_moss.py:40-46) at column lora_col + 32 (ib - nkb_main).
-void q8rec_to_native(const uint8_t *rec, int N, int nkb, int kbt, uint8_t *q, long ldq, uint16_t *s, long lds,
-                     int nkb_main, int lora_col) {
-  par_for(N / 32, [&](int jb) {
-    for (int ib = 0; ib < nkb; ib++) {
-      const uint8_t *R = rec + ((size_t)jb * kbt + ib) * 1152;
-      const uint16_t *sv = (const uint16_t *)R;
-      const long col = ib < nkb_main ? 32L * ib : lora_col + 32L * (ib - nkb_main);
-      for (int c = 0; c < 32; c++) {
-        const int n = jb * 32 + c;
-        s[(col / 32) * lds + n] = sv[2 * c];
-        for (int r = 0; r < 32; r++) q[(size_t)n * ldq + col + r] = (uint8_t)(R[128 + (r >> 1) * 64 + c * 2 + (r & 1)] ^ 0x80);
-      }
-    }
-  });
+// a new zeroed pack of `bytes` (the conversion writes every matrix; zeros stay where a matrix has no data, such as the
+// off-diagonal LoRA blocks of the MOSS qkv matrix)
+int new_pack(Ctx &c, long bytes, void **dev) {
+  HIPC(hipMalloc(dev, bytes));
+  if (hipMemsetAsync(*dev, 0, bytes, c.st) != hipSuccess) {
+    (void)hipFree(*dev);
+    *dev = nullptr;
+    return fail(HXA_E_HIP, "pack memset");
+  }
+  return HXA_OK;
 }
 
 // Convert one registered Anima blkNN.bin (fixed D=2048 layout, blk_wlayout.h) into a GPU pack.
@@ -975,7 +947,6 @@ int build_anima_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
   db.dims = hxa_block_dims{0, D, D / 128, F, 0, DC, 0, 1, 0, fmt, fmt, 0};
   long offs[32];
   const long bytes = hxa_pack_layout(0, D, F, DC, fmt, fmt, offs, 32);
-  std::vector<uint8_t> host(bytes, 0);
   // pack matrix order: qkv (q,k,v rows), o, cq, ckv (k,v rows), co, w1, w2
   struct Src {
     int meta_id, N, K, mat, row0;
@@ -988,23 +959,28 @@ int build_anima_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
     const size_t elems = (size_t)s.N * s.K;
     const size_t need = q8 ? elems / 1024 * 1152 : elems * 2;
     if (meta[s.meta_id] < 0 || (size_t)meta[s.meta_id] + need > hb.bytes) return fail(HXA_E_WEIGHTS, "weight offset out of range");
-    const uint8_t *src = (const uint8_t *)hb.ptr + meta[s.meta_id];
-    uint8_t *wdst = host.data() + offs[3 * s.mat];
-    if (!q8) {
-      crouton_to_nk((const uint16_t *)src, s.N, s.K, (uint16_t *)wdst + (size_t)s.row0 * s.K);
-    } else {
-      q8rec_to_native(src, s.N, s.K / 32, s.K / 32, wdst + (size_t)s.row0 * s.K, s.K,
-                      (uint16_t *)(host.data() + offs[3 * s.mat + 1]) + s.row0, matN[s.mat], s.K / 32, 0);
-    }
   }
   if (meta[M_GAIN] < 0 || (size_t)meta[M_GAIN] + 2048 > hb.bytes) return fail(HXA_E_WEIGHTS, "gain offset out of range");
-  memcpy(host.data() + offs[21], (const uint8_t *)hb.ptr + meta[M_GAIN], 2048);
-  tile_pack_host(host, 0, D, F, DC, fmt, fmt);
+  const uint8_t *dsrc = nullptr;
   void *dev = nullptr;
-  HIPC(hipMalloc(&dev, bytes));
-  HIPC(hipMemcpy(dev, host.data(), bytes, hipMemcpyHostToDevice));
+  int rc = stage_weights(c, hb, 0, hb.bytes, &dsrc);
+  if (rc == HXA_OK) rc = new_pack(c, bytes, &dev);
+  uint8_t *d8 = (uint8_t *)dev;
+  for (const Src &s : srcs) {
+    if (rc != HXA_OK) break;
+    const uint8_t *src = dsrc + meta[s.meta_id];
+    rc = q8 ? hxa_q8rec_to_ktiled_launch(src, s.N, s.K / 32, s.K / 32, d8 + offs[3 * s.mat], d8 + offs[3 * s.mat + 1], s.row0,
+                                         matN[s.mat], s.K / 32, 0, c.st)
+            : hxa_crouton_to_ktiled_launch(src, s.N, s.K, d8 + offs[3 * s.mat], s.row0, matN[s.mat], c.st);
+  }
+  if (rc == HXA_OK && hipMemcpyAsync(d8 + offs[21], dsrc + meta[M_GAIN], 2048, hipMemcpyDeviceToDevice, c.st) != hipSuccess)
+    rc = fail(HXA_E_HIP, "gain copy");
+  if (rc == HXA_OK && hipStreamSynchronize(c.st) != hipSuccess) rc = fail(HXA_E_HIP, "pack conversion");
+  if (rc != HXA_OK) {
+    if (dev) (void)hipFree(dev);
+    return rc;
+  }
   db.pack = dev;
-  (void)c;
   return HXA_OK;
 }
 
@@ -1021,35 +997,49 @@ int build_moss_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
                W_TOTAL = 135397376;
   const size_t base = (size_t)meta[MM_WOFF];
   if (meta[MM_WOFF] < 0 || base + W_TOTAL > hb.bytes) return fail(HXA_E_WEIGHTS, "moss weights shorter than a block pack");
-  const uint8_t *b = (const uint8_t *)hb.ptr + base;
   db.dims = hxa_block_dims{2, D, D / 128, F, 0, 0, 0, 1, 0, fmt, fmt, 0};
   long offs[32];
   const long bytes = hxa_pack_layout(2, D, F, 0, fmt, fmt, offs, 32);
-  std::vector<uint8_t> host(bytes, 0);
-  uint8_t *h8 = host.data();
-  auto q_of = [&](int m) { return h8 + offs[3 * m]; };
-  auto s_of = [&](int m) { return (uint16_t *)(h8 + offs[3 * m + 1]); };
-  const int kb = D / 32, kbt = kb + R / 32, LDQKV = D + 3 * R;
-  // q / k / v: rows p D .. (p + 1) D of qkv, their LoRA blocks at columns D + p R (the others stay zero)
-  const size_t srcs[3] = {W_Q, W_K, W_V};
-  for (int p = 0; p < 3; p++)
-    q8rec_to_native(b + srcs[p], D, kbt, kbt, q_of(0) + (size_t)p * D * LDQKV, LDQKV, s_of(0) + (size_t)p * D, 3 * D, kb,
-                    D + p * R);
-  q8rec_to_native(b + W_O, D, kbt, kbt, q_of(1), D + R, s_of(1), D, kb, D);
-  q8rec_to_native(b + W_UG, 2 * F, kbt, kbt, q_of(2), D + R, s_of(2), 2 * F, kb, D);
-  q8rec_to_native(b + W_DN, D, F / 32 + R / 32, F / 32 + R / 32, q_of(3), F + R, s_of(3), D, F / 32, F);
-  q8rec_to_native(b + W_AQKV, 3 * R, kb, kb, q_of(4), D, s_of(4), 3 * R, kb, 0);
-  q8rec_to_native(b + W_AO, R, kb, kb, q_of(5), D, s_of(5), R, kb, 0);
-  q8rec_to_native(b + W_AUG, R, kb, kb, q_of(6), D, s_of(6), R, kb, 0);
-  q8rec_to_native(b + W_ADN, R, F / 32, F / 32, q_of(7), F, s_of(7), R, F / 32, 0);
-  // gains: q/sqrt(128) [128], k [128], norm1 [3072], norm2 [3072] (export_moss.py:59-60)
-  memcpy(h8 + offs[24], b + W_GAIN, 4L * (256 + 2 * D));
-  tile_pack_host(host, 2, D, F, 0, fmt, fmt);
+  const uint8_t *b = nullptr;
   void *dev = nullptr;
-  HIPC(hipMalloc(&dev, bytes));
-  HIPC(hipMemcpy(dev, host.data(), bytes, hipMemcpyHostToDevice));
+  int rc = stage_weights(c, hb, base, W_TOTAL, &b);
+  if (rc == HXA_OK) rc = new_pack(c, bytes, &dev);
+  uint8_t *d8 = (uint8_t *)dev;
+  auto q_of = [&](int m) { return d8 + offs[3 * m]; };
+  auto s_of = [&](int m) { return d8 + offs[3 * m + 1]; };
+  const int kb = D / 32, kbt = kb + R / 32;
+  // (source, rows N, record k-blocks, records per row block, pack matrix, row0, matrix rows, main k-blocks, LoRA group)
+  struct Rec {
+    size_t off;
+    int N, nkb, kbt, mat, row0, ldn, nkb_main, lora_g;
+  };
+  const Rec recs[] = {
+      // q / k / v: rows p D .. (p + 1) D of qkv, their LoRA blocks at columns D + p R (the others stay zero)
+      {W_Q, D, kbt, kbt, 0, 0, 3 * D, kb, (D + 0 * R) / 32},
+      {W_K, D, kbt, kbt, 0, D, 3 * D, kb, (D + 1 * R) / 32},
+      {W_V, D, kbt, kbt, 0, 2 * D, 3 * D, kb, (D + 2 * R) / 32},
+      {W_O, D, kbt, kbt, 1, 0, D, kb, D / 32},
+      {W_UG, 2 * F, kbt, kbt, 2, 0, 2 * F, kb, D / 32},
+      {W_DN, D, F / 32 + R / 32, F / 32 + R / 32, 3, 0, D, F / 32, F / 32},
+      {W_AQKV, 3 * R, kb, kb, 4, 0, 3 * R, kb, 0},
+      {W_AO, R, kb, kb, 5, 0, R, kb, 0},
+      {W_AUG, R, kb, kb, 6, 0, R, kb, 0},
+      {W_ADN, R, F / 32, F / 32, 7, 0, R, F / 32, 0},
+  };
+  for (const Rec &r : recs) {
+    if (rc != HXA_OK) break;
+    rc = hxa_q8rec_to_ktiled_launch(b + r.off, r.N, r.nkb, r.kbt, q_of(r.mat), s_of(r.mat), r.row0, r.ldn, r.nkb_main,
+                                    r.lora_g, c.st);
+  }
+  // gains: q/sqrt(128) [128], k [128], norm1 [3072], norm2 [3072] (export_moss.py:59-60)
+  if (rc == HXA_OK && hipMemcpyAsync(d8 + offs[24], b + W_GAIN, 4L * (256 + 2 * D), hipMemcpyDeviceToDevice, c.st) != hipSuccess)
+    rc = fail(HXA_E_HIP, "gain copy");
+  if (rc == HXA_OK && hipStreamSynchronize(c.st) != hipSuccess) rc = fail(HXA_E_HIP, "pack conversion");
+  if (rc != HXA_OK) {
+    if (dev) (void)hipFree(dev);
+    return rc;
+  }
   db.pack = dev;
-  (void)c;
   return HXA_OK;
 }
 
@@ -1078,7 +1068,7 @@ extern "C" int mega_close(remote_handle64 h) {
   for (auto &kv : c->blocks) (void)hipFree(kv.second.pack);
   for (auto &kv : c->modws) (void)hipFree(kv.second.w);
   for (void *p : {(void *)c->x, (void *)c->cosr, (void *)c->sinr, (void *)c->mod, (void *)c->ctx, c->ws, (void *)c->stage,
-                  (void *)c->mod_dev, (void *)c->emb_dev, (void *)c->h1_dev, (void *)c->modw_ptrs})
+                  (void *)c->mod_dev, (void *)c->emb_dev, (void *)c->h1_dev, (void *)c->modw_ptrs, c->wstage})
     if (p) (void)hipFree(p);
   if (c->mod_pin) (void)hipHostFree(c->mod_pin);
   (void)hipStreamDestroy(c->st);
