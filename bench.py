@@ -255,16 +255,18 @@ def _block_setup(L, hip, s):
 
 
 # The Anima block's 13 stages (blk.c:136 TICK order) and the kernel family each one launches.
-STAGES = ("LN-mod self", "qkv + head RMSNorm + RoPE", "(RoPE: fused)", "self attention", "o projection",
-          "LN-mod cross", "cross q + text k/v", "(RMSNorm: fused)", "cross attention", "cross-o projection",
-          "LN-mod MLP", "MLP up + GELU", "MLP down")
+# At 1536 tokens the text k / v projection runs in the qkv launch (its tiles on the CUs the qkv grid leaves idle)
+# and the cross q projection is fused with the cross attention, so stages 2, 7 and 8 launch nothing.
+STAGES = ("LN-mod self", "qkv + head RMSNorm + RoPE (+ text k/v tiles)", "(RoPE: fused)", "self attention",
+          "o projection", "LN-mod cross", "cross q + RMSNorm + cross attention (fused)", "(RMSNorm: fused)",
+          "(cross attention: fused)", "cross-o projection", "LN-mod MLP", "MLP up + GELU", "MLP down")
 FAMILIES = {  # family -> the stages whose launches it is
     "gemm_splitk": (4, 9, 12),
     "gemm_pp_mlp_up": (11,),
     "gemm_pp_qkv_headnorm": (1,),
-    "attention": (3, 8),
+    "attention": (3,),
+    "gemm_xattn_cross": (6,),
     "normrow": (0, 5, 10),
-    "gemm_pair_crossq_textkv": (6,),
 }
 
 
@@ -321,10 +323,12 @@ def family_launchers(L, hip, s):
         if hook:
             hook(0)
         hip.check(L.hxa_attention(qk.ptr, 2 * D, k.ptr, D, vt.ptr, T, o.ptr, D, T, T, T, H, 1, 0, 0, 0, 0, s), "attn")
+
+    def xattn(hook=None):
         if hook:
-            hook(1)
-        hip.check(L.hxa_attention(qk.ptr, 2 * D, ck.ptr, D, cvt.ptr, C_TXT, o.ptr, D, T, C_TXT, C_TXT, H, 1, 0, 0, 0, 0,
-                                  s), "attn")
+            hook(0)
+        hip.check(L.hxa_cross_attention_fused(h.ptr, D, T, T, WFMT, Wco.ptr, D, D, gain.ptr, ck.ptr, D, cvt.ptr, C_TXT,
+                                              C_TXT, C_TXT, 0, 0, o.ptr, D, s), "cross_attention_fused")
     f16 = 2
     fam = {
         "gemm_splitk": (splitk, 3, 2 * T * D * D * 2 + 2 * T * F * D,
@@ -333,9 +337,11 @@ def family_launchers(L, hip, s):
         "gemm_pp_mlp_up": (mlp_up, 1, 2 * T * D * F, f16 * (T * D + F * D + T * F),
                            _kname(hip.gemm_pick(T, F, D, WFMT, 1, hip.EPI_GELU_TANH)) + ", GELU epilogue"),
         "gemm_pp_qkv_headnorm": (qkv, 1, 2 * T * D * 3 * D, f16 * (T * D + 3 * D * D + 3 * T * D),
-                                 _kname(hip.gemm_pick(T, 3 * D, D, WFMT, 1, 0, 2 * D)) + ", head RMSNorm + RoPE epilogue"),
-        "attention": (attention, 2, 4 * T * T * D + 4 * T * C_TXT * D,
-                      f16 * (4 * T * D + 2 * T * D + 2 * C_TXT * D + T * D), "attn_kernel (96-query workgroups)"),
+                                 _kname(hip.gemm_pick(T, 3 * D, D, WFMT, 1, 0, 2 * D)) + ", head RMSNorm + RoPE epilogue"
+                                 " (timed without the text k/v tiles the step's launch adds)"),
+        "attention": (attention, 1, 4 * T * T * D, f16 * (4 * T * D), "attn_kernel (96-query workgroups)"),
+        "gemm_xattn_cross": (xattn, 1, 2 * T * D * D + 4 * T * C_TXT * D, f16 * (T * D + D * D + 2 * C_TXT * D + T * D),
+                             "gemm_xattn_kernel 128x128 (4 waves): cross q + head RMSNorm, attention over the text keys"),
     }
     return fam, keep
 

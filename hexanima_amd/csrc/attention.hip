@@ -31,22 +31,7 @@ constexpr int LDS_BYTES = 2 * HALF_BYTES;     // 128 KB
 constexpr float L2E = 1.4426950408889634f;
 constexpr float RESCALE_TH = 5.5f;
 
-// key (within the tile) held by LDS row i of a K tile: rows 4-7 and 8-11 of each 16-row group are swapped
-HXA_DEV int krow_key(int i) {
-  const int b = i & 15, q4 = b >> 2;
-  return (i & ~15) + (q4 == 1 ? b + 4 : q4 == 2 ? b - 4 : b);
-}
-
 HXA_DEV float16_t mfma(half8_t a, half8_t b, float16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
-
-// every lane l gets the values of lanes l % 32 (lo) and l % 32 + 32 (hi): one v_permlane32_swap, no LDS round trip.
-// Combining lo and hi gives lanes l and l ^ 32 bit-identical results.
-HXA_DEV void halves(float v, float &lo, float &hi) {
-  const int x = __builtin_bit_cast(int, v);
-  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-  lo = __builtin_bit_cast(float, (int)r[0]);
-  hi = __builtin_bit_cast(float, (int)r[1]);
-}
 
 // NWH waves per key half (4: 128 queries per workgroup, 8 waves; 3: 96 queries, 6 waves -- chosen per launch so
 // that the grid fills the CUs)

@@ -53,6 +53,12 @@ struct GemmParams {
   const uint8_t *pf;  // bytes to touch after the main loop (HxaGemm::pf)
   long pf_bytes;
   HxaClk clk;  // shader-clock record (hxa_clock_record), indexed by the launch's flat workgroup id
+  // fused cross attention (gemm_xattn_kernel): the tile's queries attend to image (m0 / xa_T)'s keys
+  // xa_k [NKV][xa_ldk] (+ image * xa_kb), V^T xa_vt [D][xa_ldvt] (+ image * xa_vb); O to xa_o [M][xa_ldo]
+  const hxa_h *xa_k, *xa_vt;
+  hxa_h *xa_o;
+  long xa_ldk, xa_ldvt, xa_ldo, xa_kb, xa_vb;
+  int xa_nkv, xa_nvalid, xa_T;
 };
 
 // Touch this workgroup's share of [p.pf, p.pf + p.pf_bytes), one 4-byte load per 128-byte line: the lines come into
@@ -408,12 +414,192 @@ HXA_DEV void gemm_epilogue(const GemmParams &p, const hxa_h *Cs, int m0, int n0,
   }
 }
 
+// ---- fused cross attention (blk.c:163-169 in one kernel) ----
+// After the main loop of a 128 x 128 fp16 tile of the cross-q projection (one head: the tile's 128 columns), the
+// tile becomes that head's 128 queries: f16(acc) is staged in LDS and RMSNorm * gain is applied in place (kern.c:163-197,
+// the head-norm epilogue's arithmetic), each of the 4 waves takes 32 queries as MFMA fragments, and the head's text
+// keys are swept in 64-key tiles of K and V^T, double-buffered in LDS behind the query tile (the attention kernel's
+// layouts: K rows in krow_key order, chunks XOR-swizzled), with the exact online softmax in fp32; O = f16(P V / l).
+// LDS: the GEMM's ring (64 KB, then the query tile [128][136] fp16 in its place), then K, K, V^T, V^T (64 KB): the
+// first two key tiles are loaded when the workgroup starts and arrive during the main loop.
+constexpr int XA_KV_OFF = 4 * 16384 + 256;
+constexpr int XA_LDS = XA_KV_OFF + 4 * 16384;
+// key tile i of the tile's head into LDS buffer i & 1: 16 KB of K (rows in krow_key order, 256 B each, chunk c at
+// c ^ (row & 15)) and 16 KB of V^T (128 rows of 64 keys, chunk c at c ^ ((d >> 1) & 7)); keys past NKV read a valid
+// row (probability 0). 8 loads per wave of the 4.
+HXA_DEV void xattn_load_kv(const GemmParams &p, int m0, int n0, int i, int wave, int lane, uint8_t *lds8) {
+  const int img = m0 / p.xa_T, h = n0 >> 7, key0 = i * 64, NKV = p.xa_nkv;
+  const hxa_h *kh = p.xa_k + (long)img * p.xa_kb + h * 128;
+  const hxa_h *vh = p.xa_vt + (long)img * p.xa_vb + (long)h * 128 * p.xa_ldvt;
+  uint8_t *kb = lds8 + XA_KV_OFF + (i & 1) * 16384, *vb = lds8 + XA_KV_OFF + (2 + (i & 1)) * 16384;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int blk = j * 4 + wave;
+    const int row = 4 * blk + (lane >> 4), c = (lane & 15) ^ (row & 15);
+    const int key = min(key0 + krow_key(row), NKV - 1);
+    g2l16_opaque(kh + (long)key * p.xa_ldk + c * 8, kb + blk * 1024);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int blk = j * 4 + wave;
+    const int d = 8 * blk + (lane >> 3), c = (lane & 7) ^ ((d >> 1) & 7);
+    int key = key0 + c * 8;
+    if (key >= NKV) key = 0;
+    g2l16_opaque(vh + (long)d * p.xa_ldvt + key, vb + blk * 1024);
+  }
+}
+template <int MI, int NI, int WTM, int WTN>
+HXA_DEV void xattn_tail(const GemmParams &p, float16_t (&acc)[NI][MI], int m0, int n0, int tid, int lane, int wave, int wm,
+                        int wn, uint8_t *lds8) {
+  constexpr float L2E = 1.4426950408889634f, RESCALE_TH = 5.5f;
+  constexpr int CROW = 136;
+  const int g = lane >> 5, ql = lane & 31;
+  const int h = n0 >> 7, ntiles = (p.xa_nvalid + 63) / 64;
+  auto kbuf = [&](int i) { return lds8 + XA_KV_OFF + (i & 1) * 16384; };
+  auto vbuf = [&](int i) { return lds8 + XA_KV_OFF + (2 + (i & 1)) * 16384; };
+  // the head's gains (key tiles 0 and 1 were loaded when the workgroup started and have landed: the main loop's
+  // waits covered every older load)
+  const int jj = tid & 7, r0 = tid >> 3;
+  float glo[8], ghi[8];
+  hn_gains(p, n0 + 8 * jj, glo);
+  hn_gains(p, n0 + 64 + 8 * jj, ghi);
+  wait_vm<0>();  // (and the main loop's trailing loads must land before its LDS ring is reused)
+  __syncthreads();
+  // stage f16(acc) as the row-major query tile
+  hxa_h *Cs = (hxa_h *)lds8;
+  {
+    const int ml = wm * WTM + (lane & 31), nl = wn * WTN + 4 * (lane >> 5);
+#pragma unroll
+    for (int j = 0; j < NI; j++)
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const half4_t v = {(hxa_h)acc[j][i][4 * q], (hxa_h)acc[j][i][4 * q + 1], (hxa_h)acc[j][i][4 * q + 2],
+                             (hxa_h)acc[j][i][4 * q + 3]};
+          *(half4_t *)(Cs + (ml + i * 32) * CROW + nl + j * 32 + 8 * q) = v;
+        }
+  }
+  __syncthreads();
+  // RMSNorm * gain per query row, in place: 8 lanes per row (lane jj owns dims [8jj, 8jj+8) and [64+8jj, 64+8jj+8))
+  {
+    const float z8[8] = {};
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+      hxa_h *row = Cs + (r0 + it * 32) * CROW;
+      half8_t lo = *(const half8_t *)(row + 8 * jj), hi = *(const half8_t *)(row + 64 + 8 * jj);
+      head_norm2(lo, hi, glo, ghi, false, z8, z8);
+      *(half8_t *)(row + 8 * jj) = lo;
+      *(half8_t *)(row + 64 + 8 * jj) = hi;
+    }
+  }
+  __syncthreads();
+  half8_t qf[8];
+#pragma unroll
+  for (int sd = 0; sd < 8; sd++) qf[sd] = *(const half8_t *)(Cs + (wave * 32 + ql) * CROW + sd * 16 + 8 * g);
+  float16_t o[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) o[d] = (float16_t){};
+  float mrun = -INFINITY, lsum = 0.0f;
+  for (int i = 0; i < ntiles; i++) {
+    if (i + 1 < ntiles) wait_vm<8>();  // tile i landed (tile i + 1 may still fly)
+    else wait_vm<0>();
+    // a plain barrier (no fence): tile i + 1's loads stay in flight
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const uint8_t *kb = kbuf(i), *vb = vbuf(i);
+    // every K fragment of the tile, then the V^T fragments, read ahead of the MFMAs that use them (the V^T reads
+    // land during the QK MFMAs and the softmax)
+    half8_t kf[8][2], vf[16];
+#pragma unroll
+    for (int ds = 0; ds < 8; ds++)
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; kb2++) {
+        const int row = kb2 * 32 + ql, c = 2 * ds + g;
+        kf[ds][kb2] = *(const half8_t *)(kb + row * 256 + ((c ^ (row & 15)) << 4));
+      }
+#pragma unroll
+    for (int j = 0; j < 16; j++) {  // j = (kb2 * 2 + ks) * 4 + dblk
+      const int dblk = j & 3, kk = j >> 2, d = dblk * 32 + ql, c = 2 * kk + g;
+      vf[j] = *(const half8_t *)(vb + d * 128 + ((c ^ ((d >> 1) & 7)) << 4));
+    }
+    float16_t S[2];
+    S[0] = (float16_t){};
+    S[1] = (float16_t){};
+#pragma unroll
+    for (int ds = 0; ds < 8; ds++)
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; kb2++) S[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ds][kb2], qf[ds], S[kb2], 0, 0, 0);
+    const int key0 = i * 64;
+    if (key0 + 64 > p.xa_nvalid) {
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          if (key0 + kb2 * 32 + 16 * (r >> 3) + 8 * g + (r & 7) >= p.xa_nvalid) S[kb2][r] = -INFINITY;
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) mt = fmaxf(mt, S[kb2][r]);
+    {
+      float lo, hi;
+      halves(mt, lo, hi);
+      mt = fmaxf(lo, hi);
+    }
+    const bool need = mt > mrun + RESCALE_TH;  // also while mrun is -inf
+    if (__any(need)) {
+      const float alpha = need ? __builtin_amdgcn_exp2f((mrun - mt) * L2E) : 1.0f;
+      if (need) mrun = mt;
+      lsum *= alpha;
+#pragma unroll
+      for (int d = 0; d < 4; d++) o[d] *= alpha;
+    }
+    const float mb = (mrun == -INFINITY ? 0.0f : mrun) * L2E;
+    half8_t pf[2][2];
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(S[kb2][r], L2E, -mb));
+        lsum += pv;
+        pf[kb2][r >> 3][r & 7] = (hxa_h)pv;
+      }
+#pragma unroll
+    for (int j = 0; j < 16; j++)
+      o[j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[j], pf[j >> 3][(j >> 2) & 1], o[j & 3], 0, 0, 0);
+    if (i + 2 < ntiles) {
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();  // every wave's reads of buffer i & 1 are in registers (the MFMAs used them)
+      asm volatile("" ::: "memory");
+      xattn_load_kv(p, m0, n0, i + 2, wave, lane, lds8);
+    }
+  }
+  float llo, lhi;
+  halves(lsum, llo, lhi);
+  const float ltot = llo + lhi;
+  const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+  const int qrow = m0 + wave * 32 + ql;
+  hxa_h *orow = p.xa_o + (long)qrow * p.xa_ldo + h * 128;
+#pragma unroll
+  for (int d = 0; d < 4; d++)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; r4++) {
+      half4_t v;
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[e] = (hxa_h)(o[d][4 * r4 + e] * inv);
+      *(half4_t *)(orow + d * 32 + 8 * r4 + 4 * g) = v;
+    }
+}
+
 // SPLIT2: the first and second halves of K are rounded to fp16 separately and combined in the residual epilogue,
 // x += gate * (f16(first half) + f16(second half)) (blk.c:172-174 + kern.c:330-339 in one kernel): the first half's
 // f16 accumulators are kept in registers while the second half accumulates.
 // NW = 4 waves (2 x 2 grid, one wave per SIMD) or 8 waves (2 x 4 grid, two waves per SIMD: one wave's waits are
 // covered by the other's MFMAs).
-template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2, int NW>
+template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2, int NW, bool XATTN = false>
 HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   using G = GemmGeo<BM, BN, FMT>;
   constexpr int NT = 64 * NW;
@@ -429,6 +615,10 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
   const HxaClkMark clk0 = clk_mark(p.clk);
+  if constexpr (XATTN) {  // the first two key tiles of the fused attention, into LDS past the ring
+    xattn_load_kv(p, m0, n0, 0, wave, lane, lds8);
+    if (p.xa_nvalid > 64) xattn_load_kv(p, m0, n0, 1, wave, lane, lds8);
+  }
 
   // ---- loader: stage s <- k tile kt. A and fp16 W rows are 64 B (4 chunks of 16 B) stored with the chunk swizzle
   // c ^ ((row >> 2) & 3); q8 rows are 32 B with chunk swizzle c ^ ((row >> 3) & 1); q4 rows are 16 B.
@@ -603,6 +793,10 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
     }
   }
   clk_store(p.clk, (int)(blockIdx.x + blockIdx.z * gridDim.x), tid, clk0);
+  if constexpr (XATTN) {
+    xattn_tail<MI, NI, WTM, WTN>(p, acc, m0, n0, tid, lane, wave, wm, wn, lds8);
+    return;
+  }
   wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
   __syncthreads();
   if (p.pf_bytes > 0)
@@ -636,6 +830,10 @@ template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false, int NW = 4>
 __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
   gemm_body<BM, BN, FMT, ASYM, SPLIT2, NW>(p, blockIdx.x, blockIdx.z);
 }
+// the cross-q projection with its attention (xattn_tail): 128 x 128 fp16 tiles, 4 waves
+__global__ __launch_bounds__(256) void gemm_xattn_kernel(GemmParams p) {
+  gemm_body<128, 128, HXA_W_F16, false, false, 4, true>(p, blockIdx.x, 0);
+}
 // two independent GEMMs of the same tile shape and weight format in one launch: workgroups [0, nwg0) run p0,
 // the rest p1 (nwg0 a multiple of 8 keeps each GEMM's XCD placement)
 template <int BM, int BN, int FMT, bool ASYM, int NW = 4>
@@ -653,8 +851,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_pair_kernel(GemmParams p0, GemmP
 // computes it in 2j+2. The LDS ring, stage layout and epilogue are those of gemm_kernel.
 // int8 / int4 weights: the memory phase also reads the raw weights and their scales (and offsets) and dequantises
 // them into the fp16 fragments, so the compute phase is MFMAs only.
-template <int BM, int BN, int FMT = HXA_W_F16, bool ASYM = false>
-__global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
+// PAIRED: the workgroup index within its GEMM is `bid` (the pair kernel); otherwise blockIdx.x (bid unused)
+template <int BM, int BN, int FMT, bool ASYM, bool PAIRED>
+HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
+  const int bid = PAIRED ? bid_arg : (int)blockIdx.x;
   using G = GemmGeo<BM, BN, FMT>;
   constexpr int NT = 512, NWG = 4;  // threads, waves per group
   constexpr int WTM = BM / 2, WTN = BN / 4, MI = WTM / 32, NI = WTN / 32;
@@ -668,7 +868,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
 
   int tm, tn;
-  tile_coords(p, blockIdx.x, tm, tn);
+  tile_coords(p, bid, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int z = blockIdx.z;
   const int kbase = z * p.Kslice;
@@ -837,7 +1037,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
   wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
   __syncthreads();
   if (p.pf_bytes > 0)
-    prefetch_share(p, blockIdx.x + z * p.tiles_m * p.tiles_n, p.tiles_m * p.tiles_n * (int)gridDim.z, tid, NT,
+    prefetch_share(p, bid + z * p.tiles_m * p.tiles_n, p.tiles_m * p.tiles_n * (int)gridDim.z, tid, NT,
                    lds8 + G::LDS - G::PF_LDS);
 
   constexpr int CROW = G::CROW;
@@ -858,6 +1058,16 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
   __syncthreads();
   gemm_epilogue<BM, BN, NT, false>(p, Cs, m0, n0, tid, z);
   if (p.pf_bytes > 0) wait_vm<0>();
+}
+template <int BM, int BN, int FMT = HXA_W_F16, bool ASYM = false>
+__global__ __launch_bounds__(512) void gemm_pp_kernel(GemmParams p) {
+  gemm_pp_body<BM, BN, FMT, ASYM, false>(p, 0);
+}
+// two independent GEMMs on the ping-pong kernel in one grid: workgroups [0, nwg0) run p0, the rest p1
+template <int BM, int BN, int FMT, bool ASYM>
+__global__ __launch_bounds__(512) void gemm_pp_pair_kernel(GemmParams p0, GemmParams p1, int nwg0) {
+  if ((int)blockIdx.x < nwg0) gemm_pp_body<BM, BN, FMT, ASYM, true>(p0, blockIdx.x);
+  else gemm_pp_body<BM, BN, FMT, ASYM, true>(p1, blockIdx.x - nwg0);
 }
 
 // Tile cost model, per weight format (fp16, int8, int4): a launch of `waves` rounds of workgroups over the CUs takes
@@ -960,6 +1170,17 @@ hipError_t launch_fmt(int bm, int bn, int nw, const GemmParams &p, int ksplit, h
 
 int g_num_cu = 0;
 
+// CUs of the current device (read once)
+int num_cu() {
+  if (g_num_cu == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    hipDeviceProp_t prop;
+    g_num_cu = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 256;
+  }
+  return g_num_cu;
+}
+
 }  // namespace
 
 // Choose the tile of least modelled time (kTiles). HXA_EPI_RESADD_SPLIT2 keeps both K halves' accumulators in
@@ -967,12 +1188,7 @@ int g_num_cu = 0;
 static void pick_tile(int M, int N, int K, int ksplit, int fmt, int epi, int hn_cols, int *bm, int *bn, int *nw) {
   const bool headnorm = hn_cols > 0;
   const bool split2 = epi == HXA_EPI_RESADD_SPLIT2;
-  if (g_num_cu == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    hipDeviceProp_t prop;
-    g_num_cu = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 256;
-  }
+  const int ncu = num_cu();
   const int f = split2 ? 0 : fmt;
   double best = -1.0;
   for (const TileCost &c : kTiles) {
@@ -982,7 +1198,7 @@ static void pick_tile(int M, int N, int K, int ksplit, int fmt, int epi, int hn_
     if (epi == HXA_EPI_SITU && c.bn % 128 != 0) continue;  // each wave needs whole (up, gate) block pairs
     if (headnorm && (c.bn % 128 != 0 || (hn_cols % c.bn != 0 && hn_cols < N))) continue;  // whole head-normed tiles
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ksplit;
-    const long waves = (tiles + g_num_cu - 1) / g_num_cu;
+    const long waves = (tiles + ncu - 1) / ncu;
     const double t = (double)waves * (c.a[f] * 1e-6 * c.bm * c.bn * (double)(K / ksplit) + c.b[f]);
     if (best < 0.0 || t < best - 1e-9) {
       best = t;
@@ -1145,11 +1361,92 @@ hipError_t launch_pair_t(const GemmParams &p0, const GemmParams &p1, hipStream_t
   hxa_launch(kern, dim3(n0 + p1.tiles_m * p1.tiles_n), dim3(64 * NW), G::LDS, st, p0, p1, n0);
   return hipGetLastError();
 }
+template <int BM, int BN, int FMT, bool ASYM>
+hipError_t launch_pp_pair_t(const GemmParams &p0, const GemmParams &p1, hipStream_t st) {
+  auto kern = gemm_pp_pair_kernel<BM, BN, FMT, ASYM>;
+  using G = GemmGeo<BM, BN, FMT>;
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  const int n0 = p0.tiles_m * p0.tiles_n;
+  hxa_launch(kern, dim3(n0 + p1.tiles_m * p1.tiles_n), dim3(512), G::LDS, st, p0, p1, n0);
+  return hipGetLastError();
+}
 template <int FMT, bool ASYM>
 hipError_t launch_pair_fmt(int bm, int bn, int nw, const GemmParams &p0, const GemmParams &p1, hipStream_t st) {
   if (bm == 128 && bn == 128 && nw == 4) return launch_pair_t<128, 128, FMT, ASYM, 4>(p0, p1, st);
   if (bm == 128 && bn == 128 && nw == 8) return launch_pair_t<128, 128, FMT, ASYM, 8>(p0, p1, st);
+  if (bm == 192 && bn == 256 && nw == 9) return launch_pp_pair_t<192, 256, FMT, ASYM>(p0, p1, st);
   return hipErrorInvalidValue;
+}
+
+bool hxa_gemm_pair_fits(const HxaGemm &g0, const HxaGemm &g1) {
+  GemmParams p0, p1;
+  int bm, bn, nw, bm1, bn1, nw1;
+  HxaWeight w0, w1;
+  bool s0, s1;
+  if (gemm_prepare(g0, p0, bm, bn, nw, w0, s0) != HXA_OK || s0 || g0.ksplit != 1 || g1.ksplit != 1) return false;
+  if (!((bm == 128 && bn == 128 && nw != 9) || (bm == 192 && bn == 256 && nw == 9)) || (p0.tiles_m * p0.tiles_n) % 8)
+    return false;
+  HxaGemm g1f = g1;
+  g1f.force_bm = bm;
+  g1f.force_bn = bn;
+  g1f.force_nw = nw;
+  if (gemm_prepare(g1f, p1, bm1, bn1, nw1, w1, s1) != HXA_OK || s1 || w0.fmt != w1.fmt || (w0.z != nullptr) != (w1.z != nullptr))
+    return false;
+  const long n0 = (long)p0.tiles_m * p0.tiles_n, n1 = (long)p1.tiles_m * p1.tiles_n;
+  const long c = num_cu();
+  return (n0 + n1 + c - 1) / c == (n0 + c - 1) / c;
+}
+
+bool hxa_gemm_xattn_fits(int M, int N) {
+  return (long)((M + 127) / 128) * ((N + 127) / 128) <= num_cu();
+}
+
+int hxa_gemm_xattn_launch(const HxaGemm &g, const HxaXAttn &a, hipStream_t st) {
+  if (g.w == nullptr || (g.w->fmt & ~HXA_W_KTILED) != HXA_W_F16 || g.epi != HXA_EPI_STORE || g.ksplit != 1 ||
+      g.hn_cols < g.w->N || g.hn_cos != nullptr || g.out_t != nullptr || g.pf_bytes > 0)
+    return HXA_E_ARG;
+  // (NKV % 8: a V^T chunk of 8 keys that starts below NKV ends within it)
+  if (a.T <= 0 || a.T % 128 || g.M % a.T || g.w->N % 128 || a.NKV < 1 || a.NKV % 8 || a.nvalid < 1 || a.nvalid > a.NKV ||
+      !a.k || !a.vt || !a.o)
+    return HXA_E_ARG;
+  if ((a.ldk % 8) || (a.ldvt % 8) || (a.ldo % 4) || a.ldvt < a.NKV || (((uintptr_t)a.k | (uintptr_t)a.vt) % 16) ||
+      ((uintptr_t)a.o % 8) || (a.kb % 8) || (a.vb % 8) || a.ldk >= (1L << 24) || a.ldvt >= (1L << 23))
+    return HXA_E_ARG;
+  HxaGemm gf = g;
+  gf.force_bm = 128;
+  gf.force_bn = 128;
+  gf.force_nw = 4;
+  GemmParams p;
+  int bm, bn, nw;
+  HxaWeight w;
+  bool split2;
+  const int r = gemm_prepare(gf, p, bm, bn, nw, w, split2);
+  if (r != HXA_OK) return r;
+  p.xa_k = a.k;
+  p.xa_vt = a.vt;
+  p.xa_o = a.o;
+  p.xa_ldk = a.ldk;
+  p.xa_ldvt = a.ldvt;
+  p.xa_ldo = a.ldo;
+  p.xa_kb = a.kb;
+  p.xa_vb = a.vb;
+  p.xa_nkv = a.NKV;
+  p.xa_nvalid = a.nvalid;
+  p.xa_T = a.T;
+  constexpr int LDS = GemmGeo<128, 128, HXA_W_F16>::LDS > XA_LDS ? GemmGeo<128, 128, HXA_W_F16>::LDS : XA_LDS;
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute((const void *)gemm_xattn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, LDS) != hipSuccess)
+      return HXA_E_HIP;
+    attr = true;
+  }
+  hxa_launch(gemm_xattn_kernel, dim3(p.tiles_m * p.tiles_n), dim3(256), LDS, st, p);
+  return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
 }
 
 int hxa_gemm_plan(const HxaGemm &g, int *bm, int *bn, int *nw, int *rounds) {
@@ -1159,7 +1456,7 @@ int hxa_gemm_plan(const HxaGemm &g, int *bm, int *bn, int *nw, int *rounds) {
   const int r = gemm_prepare(g, p, *bm, *bn, *nw, w, split2);
   if (r != HXA_OK) return r;
   const long n = (long)p.tiles_m * p.tiles_n * g.ksplit;
-  *rounds = (int)((n + g_num_cu - 1) / g_num_cu);
+  *rounds = (int)((n + num_cu() - 1) / num_cu());
   return HXA_OK;
 }
 
@@ -1171,16 +1468,22 @@ int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st) {
   int r = gemm_prepare(g0, p0, bm, bn, nw, w0, s0);
   if (r != HXA_OK) return r;
   hipError_t e = hipErrorInvalidValue;
-  // paired only on the 128x128 4- / 8-wave tiles; the second GEMM then takes the first one's tile
-  if (bm == 128 && bn == 128 && nw != 9 && !s0 && g0.ksplit == 1 && g1.ksplit == 1 &&
-      (p0.tiles_m * p0.tiles_n) % 8 == 0) {
+  // paired on the 128x128 4- / 8-wave tiles and the 192x256 ping-pong tile; the second GEMM then takes the first
+  // one's tile. The ping-pong pair only where the second GEMM's tiles fit in the CUs the first leaves idle: a
+  // further round of 192x256 tiles is slower than the second GEMM's own launch (6144 x 2048 cross q + 512-row text
+  // k / v: 79 us paired, 70 us as two launches)
+  if (((bm == 128 && bn == 128 && nw != 9) || (bm == 192 && bn == 256 && nw == 9)) && !s0 && g0.ksplit == 1 &&
+      g1.ksplit == 1 && (p0.tiles_m * p0.tiles_n) % 8 == 0) {
     HxaGemm g1f = g1;
     g1f.force_bm = bm;
     g1f.force_bn = bn;
     g1f.force_nw = nw;
     r = gemm_prepare(g1f, p1, bm1, bn1, nw1, w1, s1);
     if (r != HXA_OK) return r;
-    if (w0.fmt == w1.fmt && (w0.z != nullptr) == (w1.z != nullptr) && !s1) {
+    const long n0 = (long)p0.tiles_m * p0.tiles_n, n1 = (long)p1.tiles_m * p1.tiles_n;
+    const long c = num_cu();
+    const bool extra_round = (n0 + n1 + c - 1) / c > (n0 + c - 1) / c;
+    if (w0.fmt == w1.fmt && (w0.z != nullptr) == (w1.z != nullptr) && !s1 && !(nw == 9 && extra_round)) {
       if (w0.fmt == HXA_W_F16) e = launch_pair_fmt<HXA_W_F16, false>(bm, bn, nw, p0, p1, st);
       else if (w0.fmt == HXA_W_Q8) e = launch_pair_fmt<HXA_W_Q8, false>(bm, bn, nw, p0, p1, st);
       else if (w0.z) e = launch_pair_fmt<HXA_W_Q4, true>(bm, bn, nw, p0, p1, st);

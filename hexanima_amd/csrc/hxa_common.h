@@ -69,6 +69,22 @@ HXA_DEV void clk_store(const HxaClk &k, int wg, int tid, HxaClkMark s) {
   if (tid < 4 && wg < k.n) k.rec[4L * wg + tid] = tid == 0 ? s.c : tid == 1 ? s.r : tid == 2 ? e.c : e.r;
 }
 
+// ---- attention tile layout (shared by the attention kernel and the fused cross-attention tail) ----
+// key (within a 64-key tile) held by LDS row i of a K tile: rows 4-7 and 8-11 of each 16-row group are swapped, which
+// makes the S^T = K Q^T scores of a lane exactly the B operand of O^T += V^T P^T
+HXA_DEV int krow_key(int i) {
+  const int b = i & 15, q4 = b >> 2;
+  return (i & ~15) + (q4 == 1 ? b + 4 : q4 == 2 ? b - 4 : b);
+}
+// every lane l gets the values of lanes l % 32 (lo) and l % 32 + 32 (hi): one v_permlane32_swap, no LDS round trip.
+// Combining lo and hi gives lanes l and l ^ 32 bit-identical results.
+HXA_DEV void halves(float v, float &lo, float &hi) {
+  const int x = __builtin_bit_cast(int, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  lo = __builtin_bit_cast(float, (int)r[0]);
+  hi = __builtin_bit_cast(float, (int)r[1]);
+}
+
 // ---- direct-to-LDS loads and VMEM waits (gfx950) ----
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) const void gmem_void_t;

@@ -37,6 +37,24 @@ int hxa_gemm_plan(const HxaGemm &g, int *bm, int *bn, int *nw, int *rounds);
 // two independent GEMMs in one launch (the second takes the first one's tile; same weight format, no split-K);
 // falls back to two launches when the tile has no paired kernel
 int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st);
+// The cross-attention site's q projection fused with its attention (blk.c:163-169): g is the cross-q GEMM (fp16
+// weights, HXA_EPI_STORE, a head norm on every column, no RoPE); each 128 x 128 tile's queries (one head) attend to
+// their image's keys. Returns HXA_E_ARG when the shapes do not fit the fused kernel (T % 128, N % 128, weight format,
+// strides); the caller then runs the projection and hxa_attn_launch.
+struct HxaXAttn {
+  const hxa_h *k, *vt;  // k [NKV][ldk] (head h at column 128 h), vt [D][ldvt] (keys contiguous)
+  hxa_h *o;             // [M][ldo]
+  long ldk, ldvt, ldo;
+  long kb, vb;          // per-image offsets: k elements, vt columns
+  int NKV, nvalid, T;   // keys, valid keys, query rows per image
+};
+int hxa_gemm_xattn_launch(const HxaGemm &g, const HxaXAttn &a, hipStream_t st);
+// whether the fused kernel's 128 x 128 tiles of an M x N projection fit in one round over the CUs (beyond one round
+// the projection's own tile pick plus the attention kernel is faster)
+bool hxa_gemm_xattn_fits(int M, int N);
+// whether hxa_gemm_pair_launch(g0, g1) would be one launch that takes no more rounds of workgroups over the CUs than
+// g0 alone (g1 only fills CUs g0 leaves idle)
+bool hxa_gemm_pair_fits(const HxaGemm &g0, const HxaGemm &g1);
 // int8 / int4 weight -> fp16 k-tiled [K/32][N][32] at out (2 N K bytes): the same values the GEMM main loops use
 int hxa_dequant_launch(const HxaWeight &w, hxa_h *out, hipStream_t st);
 

@@ -283,6 +283,30 @@ extern "C" int hxa_attention(const void *q, long ldq, const void *k, long ldk, c
   if (r != HXA_OK) return fail(r, "attention T=%d NKV=%d nvalid=%d H=%d rejected", T, NKV, nvalid, H);
   return HXA_OK;
 }
+
+extern "C" int hxa_cross_attention_fused(const void *h, long ldh, int M, int T, int fmt, const void *w, int N, int K,
+                                         const float *gain, const void *k, long ldk, const void *vt, long ldvt, int NKV,
+                                         int nvalid, long kb, long vb, void *o, long ldo, void *stream) {
+  if (!h || !w || !gain || !k || !vt || !o) return fail(HXA_E_ARG, "cross_attention_fused: null pointer");
+  HxaWeight wt{fmt, N, K, w, nullptr, nullptr};
+  HxaGemm g{};
+  g.A = (const hxa_h *)h;
+  g.lda = ldh;
+  g.M = M;
+  g.w = &wt;
+  g.ksplit = 1;
+  g.epi = HXA_EPI_STORE;
+  g.ldo = N;
+  g.hn_cols = N;
+  g.hn_g0 = gain;
+  g.hn_g1 = gain;
+  g.hn_gsplit = N;
+  g.hn_ttab = 1;
+  const HxaXAttn a{(const hxa_h *)k, (const hxa_h *)vt, (hxa_h *)o, ldk, ldvt, ldo, kb, vb, NKV, nvalid, T};
+  const int r = hxa_gemm_xattn_launch(g, a, S(stream));
+  if (r != HXA_OK) return fail(r, "cross_attention_fused M=%d T=%d N=%d K=%d NKV=%d rejected", M, T, N, K, NKV);
+  return HXA_OK;
+}
 extern "C" int hxa_norm_mod(const float *x, long ldx, int T, int D, const float *shift, const float *scale,
                             const float *w, float eps, void *h, long ldh, void *stream) {
   const int r = hxa_norm_mod_launch(x, ldx, T, D, shift, scale, w, eps, (hxa_h *)h, ldh, S(stream));
@@ -759,8 +783,31 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     // q, k: RMSNorm * gain + RoPE (blk.c:159-160), fused into the projection's store unless a stage dump needs the
     // un-normalised projections (M_STOP)
     const bool fuse = stop == 0;
+    bool fuse_x = false;  // the text k / v ran with qkv; the cross site fuses cross q with its attention
     if (fuse) hn = HeadNorm{2 * D, gain, gain + 128, D, cosT, sinT};
-    {
+    if (fuse) {
+      // When the text k / v projection (ctx only) fits in the qkv launch without a further round of workgroups, it
+      // runs there, filling CUs the qkv grid leaves idle, and the cross-attention site fuses the cross-q projection
+      // with its attention (fuse_x). Both projections in one weight format: int8 / int4 text k / v weights take the
+      // fp16 copy when the qkv projection does.
+      const HxaWeight *wp, *wkv = &Wckv;
+      TRY(prep(Wqkv, wp));
+      const HxaGemm gqkv = make(h, ldh, BT, *wp, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0);
+      const bool kv16 = (wp->fmt & ~HXA_W_KTILED) == HXA_W_F16 && (Wckv.fmt & ~HXA_W_KTILED) != HXA_W_F16;
+      const HxaWeight kvshape{kv16 ? (HXA_W_F16 | HXA_W_KTILED) : Wckv.fmt, Wckv.N, Wckv.K, Wckv.w, Wckv.s, Wckv.z};
+      hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
+      HxaGemm gkv = make((const hxa_h *)ctx, d->DC, BC, kvshape, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0);
+      fuse_x = T % 128 == 0 && d->C % 8 == 0 && hxa_gemm_xattn_fits(BT, Wcq.N) && hxa_gemm_pair_fits(gqkv, gkv);
+      if (fuse_x) {
+        if (kv16) TRY(prep(Wckv, wkv, 1));
+        gkv.w = wkv;
+        const int r = hxa_gemm_pair_launch(gqkv, gkv, st);
+        if (r != HXA_OK) return fail(r, "block qkv / text k v gemms rejected");
+      } else {
+        const int r = hxa_gemm_launch(gqkv, st);
+        if (r != HXA_OK) return fail(r, "block qkv gemm rejected");
+      }
+    } else {
       const HxaWeight *wp;
       TRY(prep(Wqkv, wp));
       TRY(gemm(h, ldh, BT, *wp, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
@@ -778,28 +825,48 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 2 * D,
                                    mod + 3 * D, mod + 4 * D, nullptr, 1e-6f, h, ldh, st));
     STAGE_DONE();
-    // cross q from h and the text k / v from ctx are independent: one launch, the text tiles filling the CUs the
-    // 1536-token projection leaves idle
-    if (fuse) hn = HeadNorm{D, gain + 256, gain + 256, D, nullptr, nullptr};  // cross q: RMSNorm * gain (blk.c:166)
-    const HxaWeight *wcq;
-    TRY(prep(Wcq, wcq));
-    const HxaGemm gq = make(h, ldh, BT, *wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
-    if (fuse) hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
-    const HxaWeight *wckv;
-    TRY(prep(Wckv, wckv, 1));
-    const HxaGemm gkv = make((const hxa_h *)ctx, d->DC, BC, *wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0);
-    {
-      const int r = hxa_gemm_pair_launch(gq, gkv, st);
-      if (r != HXA_OK) return fail(r, "block cross q / text k v gemms rejected");
+    if (fuse_x) {
+      // cross q (RMSNorm * gain, blk.c:166) and the cross attention in one kernel: each 128 x 128 tile of the
+      // projection is one head's 128 queries, which attend to their image's text keys from LDS
+      hn = HeadNorm{D, gain + 256, gain + 256, D, nullptr, nullptr};
+      const HxaWeight *wcq;
+      TRY(prep(Wcq, wcq));
+      const HxaGemm gq = make(h, ldh, BT, *wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
+      const HxaXAttn xa{ck, cvT, o, D, BC, ldo, (long)d->C * D, d->C, d->C, d->C, T};
+      int r = hxa_gemm_xattn_launch(gq, xa, st);
+      if (r == HXA_E_ARG) {  // shapes the fused kernel does not take: the projection, then the attention kernel
+        r = hxa_gemm_launch(gq, st);
+        if (r == HXA_OK) r = hxa_attn_launch(HxaAttn{qk, ck, cvT, ldqk, D, BC, o, ldo, T, d->C, d->C, H, B, (long)T * ldqk,
+                                                     (long)d->C * D, d->C, (long)T * ldo}, st);
+      }
+      if (r != HXA_OK) return fail(r, "block cross q / cross attention rejected");
+      STAGE_DONE();
+      STAGE_DONE();
+      STAGE_DONE();
+    } else {
+      // cross q from h and the text k / v from ctx are independent: one launch, the text tiles filling the CUs the
+      // 1536-token projection leaves idle
+      if (fuse) hn = HeadNorm{D, gain + 256, gain + 256, D, nullptr, nullptr};  // cross q: RMSNorm * gain (blk.c:166)
+      const HxaWeight *wcq;
+      TRY(prep(Wcq, wcq));
+      const HxaGemm gq = make(h, ldh, BT, *wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
+      if (fuse) hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
+      const HxaWeight *wckv;
+      TRY(prep(Wckv, wckv, 1));
+      const HxaGemm gkv = make((const hxa_h *)ctx, d->DC, BC, *wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0);
+      {
+        const int r = hxa_gemm_pair_launch(gq, gkv, st);
+        if (r != HXA_OK) return fail(r, "block cross q / text k v gemms rejected");
+      }
+      STAGE_DONE();
+      if (!fuse) {
+        TRY(hxa_rmsrope_launch(qk, nullptr, gain + 256, nullptr, ldqk, BT, H, nullptr, nullptr, 0, st));
+        TRY(hxa_rmsrope_launch(ck, nullptr, gain + 384, nullptr, D, BC, H, nullptr, nullptr, 0, st));
+      }
+      STAGE_DONE();
+      TRY(attn(qk, ck, D, cvT, BC, d->C, d->C, (long)d->C * D, d->C));
+      STAGE_DONE();
     }
-    STAGE_DONE();
-    if (!fuse) {
-      TRY(hxa_rmsrope_launch(qk, nullptr, gain + 256, nullptr, ldqk, BT, H, nullptr, nullptr, 0, st));
-      TRY(hxa_rmsrope_launch(ck, nullptr, gain + 384, nullptr, D, BC, H, nullptr, nullptr, 0, st));
-    }
-    STAGE_DONE();
-    TRY(attn(qk, ck, D, cvT, BC, d->C, d->C, (long)d->C * D, d->C));
-    STAGE_DONE();
     TRY(fuse ? deferred_proj(Wco) : gemm(o, ldo, BT, Wco, HXA_EPI_RESADD, nullptr, 0, x, mod + 5 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 2: MLP (blk.c:170-174)

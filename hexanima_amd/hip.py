@@ -76,6 +76,7 @@ _SIGS = {
     "hxa_gemm_pick": (I, [I, I, I, I, I, I, I, P, P, P, P]),
     "hxa_attention": (I, [P, L, P, L, P, L, P, L, I, I, I, I, I, L, L, L, L, P]),
     "hxa_norm_mod": (I, [P, L, I, I, P, P, P, F, P, L, P]),
+    "hxa_cross_attention_fused": (I, [P, L, I, I, I, P, I, I, P, P, L, P, L, I, I, L, L, P, L, P]),
     "hxa_rmsrope": (I, [P, P, P, P, L, I, I, P, P, I, P]),
     "hxa_resadd2": (I, [P, L, P, P, L, I, I, P, P]),
     "hxa_dequant": (I, [I, P, P, P, I, I, P, P]),

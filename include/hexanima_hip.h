@@ -157,6 +157,15 @@ int hxa_gemm_headnorm(const void *A, long lda, int M, int fmt, const void *w, co
  * o [T][ldo]; keys >= nvalid masked; batch images at element strides qb/kb/vb/ob; ldk < 2^24, ldvt < 2^23. */
 int hxa_attention(const void *q, long ldq, const void *k, long ldk, const void *vt, long ldvt, void *o, long ldo, int T,
                   int NKV, int nvalid, int H, int batch, long qb, long kb, long vb, long ob, void *stream);
+/* The cross-attention site's q projection fused with its attention (blk.c:163-169): q = f16(RMSNorm(f16(h W^T)) * gain)
+ * per head of 128 (gain [128] fp32 with 1/sqrt(128) folded in, no RoPE; kern.c:163-197), then per head
+ * o = attention(q, k, v) over the nvalid of NKV keys of the query row's image (rows [b T, (b+1) T) are image b):
+ * k [NKV][ldk] at element offset b*kb, vt [N][ldvt] (V transposed) at column offset b*vb, o [M][ldo]. fp16 weights
+ * (fmt HXA_W_F16, optionally | HXA_W_KTILED); T % 128 == 0, N % 128 == 0. The same values as hxa_gemm_headnorm
+ * followed by hxa_attention, up to the softmax's summation order. The reference runs it as two stages. */
+int hxa_cross_attention_fused(const void *h, long ldh, int M, int T, int fmt, const void *w, int N, int K,
+                              const float *gain, const void *k, long ldk, const void *vt, long ldvt, int NKV, int nvalid,
+                              long kb, long vb, void *o, long ldo, void *stream);
 /* h = f16(norm(x) * (1 + scale) [* w] + shift); LN when w == NULL (kern.c:38-65), RMS otherwise (moss kern.c:353) */
 int hxa_norm_mod(const float *x, long ldx, int T, int D, const float *shift, const float *scale, const float *w,
                  float eps, void *h, long ldh, void *stream);

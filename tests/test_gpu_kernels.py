@@ -455,6 +455,62 @@ def test_attention_vs_oracle(T, NKV, nvalid, H):
     assert r0 < 4.7e-3  # measured 8.2e-4 - 1.6e-3
 
 
+# (M, T, NKV, nvalid): the 2B block's cross site (1536 tokens, 256 text tokens); batch 2 of 256 tokens over 77 of 80
+# text keys (ragged, the last tile masked); megarun's 512 context tokens
+@pytest.mark.parametrize("M,T,NKV,nvalid", [(1536, 1536, 256, 256), (512, 256, 80, 77), (384, 384, 512, 512)])
+def test_cross_attention_fused_vs_oracle(M, T, NKV, nvalid):
+    """hxa_cross_attention_fused: the cross-q projection with its per-head RMSNorm * gain and the attention of every
+    head over its image's text keys in one kernel, against the oracle's GEMM (fp16 store), rmsrope (no RoPE) and
+    exact-softmax attention, image by image; and against the unfused GPU path (head-norm GEMM, attention kernel)."""
+    hip = _hip()
+    say(f"fused cross attention M={M} T={T} NKV={NKV} nvalid={nvalid}")
+    L = hip.lib()
+    rng = np.random.default_rng(M + NKV)
+    D, H = 2048, 16
+    B = M // T
+    h = f16(rng.standard_normal((M, D)))
+    W = f16(rng.standard_normal((D, D)) * 0.02)
+    gain = (np.full(128, 128 ** -0.5) * rng.uniform(0.8, 1.2, 128)).astype(np.float32)
+    k = f16(rng.standard_normal((B * NKV, D)))
+    v = f16(rng.standard_normal((B * NKV, D)))
+    dh, dW, dg, dk = (hip.DeviceArray.from_numpy(a) for a in (h, W, gain, k))
+    dvt = hip.DeviceArray.from_numpy(np.ascontiguousarray(v.T))  # [D][B * NKV]
+    do = hip.DeviceArray((M, D), np.float16)
+    hip.check(L.hxa_cross_attention_fused(dh.ptr, D, M, T, 0, dW.ptr, D, D, dg.ptr, dk.ptr, D, dvt.ptr, B * NKV, NKV, nvalid,
+                                          NKV * D, NKV, do.ptr, D, None), "cross_attention_fused")
+    hip.sync()
+    got = do.numpy().astype(np.float64)
+    # q = f16(RMSNorm(f16(h W^T)) * gain) per head (the projection's fp16 store, then the head norm)
+    q16 = hxo.rmsrope(f16(hxo.gemm(h, W)).view(np.uint16), gain).view(np.float16)
+    ref = np.concatenate([hxo.attention(q16[b * T:(b + 1) * T], k[b * NKV:(b + 1) * NKV], v[b * NKV:(b + 1) * NKV], nvalid,
+                                        mode=1).view(np.float16) for b in range(B)]).astype(np.float64)
+    mx, r = float(np.max(np.abs(got - ref))), rel(got, ref)
+    # the unfused GPU path: hxa_gemm_headnorm (no RoPE) into q, then hxa_attention
+    dq = hip.DeviceArray((M, D), np.float16)
+    hip.check(L.hxa_gemm_headnorm(dh.ptr, D, M, 0, dW.ptr, None, None, D, D, dq.ptr, D, None, 0, D, D, dg.ptr, dg.ptr, D,
+                                  None, None, 0, None), "gemm_headnorm")
+    du = hip.DeviceArray((M, D), np.float16)
+    hip.check(L.hxa_attention(dq.ptr, D, dk.ptr, D, dvt.ptr, B * NKV, du.ptr, D, T, NKV, nvalid, H, B, T * D, NKV * D, NKV,
+                              T * D, None), "attention")
+    hip.sync()
+    mu = float(np.max(np.abs(got - du.numpy().astype(np.float64))))
+    print(f"fused cross attention: max abs {mx:.2e}, rel vs exact {r:.2e}; max abs vs unfused GPU path {mu:.2e}", flush=True)
+    assert mx < 4e-3 and r < 1e-3  # the attention kernel's bounds (test_attention_vs_oracle)
+    assert mu < 2e-3
+
+
+def test_cross_attention_fused_rejects_unfit_shapes():
+    hip = _hip()
+    L = hip.lib()
+    buf = hip.DeviceArray((4 << 20,), np.uint8)
+    g = hip.DeviceArray((128,), np.float32)
+    # T not a multiple of 128, int8 weights: argument errors, nothing launched
+    assert L.hxa_cross_attention_fused(buf.ptr, 2048, 320, 160, 0, buf.ptr, 2048, 2048, g.ptr, buf.ptr, 2048, buf.ptr, 256,
+                                       256, 256, 0, 0, buf.ptr, 2048, None) == -12
+    assert L.hxa_cross_attention_fused(buf.ptr, 2048, 256, 256, 1, buf.ptr, 2048, 2048, g.ptr, buf.ptr, 2048, buf.ptr, 256,
+                                       256, 256, 0, 0, buf.ptr, 2048, None) == -12
+
+
 def test_clock_record_gemm_and_attention():
     """hxa_clock_record: one record per workgroup with a plausible shader clock, results unchanged, and nothing
     written once it is switched off."""
