@@ -4,6 +4,7 @@
 //
 // Row kernels use one 64-lane wave per row with 16-byte vector loads (fully coalesced); reductions stay inside
 // the wave (no LDS, no barriers).
+#include <algorithm>
 #include <type_traits>
 
 #include "hxa_common.h"
@@ -27,89 +28,103 @@ HXA_DEV float wave_sum(float v) {
 // With t != NULL the pending gated residual of the previous site is applied first, x += gate * t (kern.c:320-328,
 // the same fma as the GEMM residual epilogue), or with t2 as well x += gate * (t + t2) (kern.c:330-339, the same
 // fma as resadd2_kernel); x is written back, and the norm is taken of the updated row.
-// One 256-thread workgroup per row (a float4 of every 1024 columns per thread): short per-thread register arrays
-// keep many rows in flight. The row sums are wave DPP sums combined through LDS in a fixed order.
+// A 256-thread workgroup per group of rows (row = blockIdx.x + j gridDim.x; a float4 of every 1024 columns per
+// thread). The column vectors (gate, 1 + scale [* w], shift) are read once per workgroup, and the next row's x and
+// pending terms are loaded while the current row is reduced and stored, so loads and stores of the grid overlap.
+// The row sums are wave DPP sums combined through LDS in a fixed order (the same bits for any grid).
 template <int NV>
-__global__ __launch_bounds__(256) void normrow_kernel(float *__restrict__ x, long ldx, int D, const hxa_h *__restrict__ t,
-                                                      const hxa_h *__restrict__ t2, long ldt, const float *__restrict__ gate,
-                                                      const float *__restrict__ shift, const float *__restrict__ scale,
-                                                      const float *__restrict__ w, float eps, hxa_h *__restrict__ h,
-                                                      long ldh) {
-  __shared__ float red[8];
-  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float4_t *xr = (float4_t *)(x + (long)row * ldx);
-  // every load of the row is issued up front (x, the pending terms and the column vectors), so the row costs one
-  // memory latency; the vectors' multiplier (1 + scale) [* w] and shift are formed while x is in flight
-  float4_t v[NV], mul[NV], sh[NV];
+__global__ __launch_bounds__(256) void normrow_kernel(float *__restrict__ x, long ldx, int D, int T,
+                                                      const hxa_h *__restrict__ t, const hxa_h *__restrict__ t2, long ldt,
+                                                      const float *__restrict__ gate, const float *__restrict__ shift,
+                                                      const float *__restrict__ scale, const float *__restrict__ w,
+                                                      float eps, hxa_h *__restrict__ h, long ldh) {
+  __shared__ float red[2][8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int row = blockIdx.x;
+  float4_t xv[NV];
+  half4_t ta[NV], tb[NV];
+  auto load = [&](int r) {
+    const float4_t *xr = (const float4_t *)(x + (long)r * ldx);
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+      const int c = (tid + 256 * k) * 4;
+      xv[k] = c < D ? xr[tid + 256 * k] : (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+      if (t != nullptr && c < D) {
+        ta[k] = *(const half4_t *)(t + (long)r * ldt + c);
+        if (t2 != nullptr) tb[k] = *(const half4_t *)(t2 + (long)r * ldt + c);
+      }
+    }
+  };
+  load(row);
+  // the column vectors, formed while the first row is in flight: multiplier (1 + scale) [* w] (k_rms_prep), shift
+  float4_t g[NV], mul[NV], sh[NV];
 #pragma unroll
   for (int k = 0; k < NV; k++) {
     const int c = (tid + 256 * k) * 4;
-    v[k] = c < D ? xr[tid + 256 * k] : (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+    if (c < D) {
+      if (t != nullptr) g[k] = *(const float4_t *)(gate + c);
+      mul[k] = *(const float4_t *)(scale + c) + 1.0f;
+      if (w != nullptr) mul[k] *= *(const float4_t *)(w + c);
+      sh[k] = *(const float4_t *)(shift + c);
+    }
   }
-  if (t != nullptr) {
+  const float inv = 1.0f / (float)D;
+  for (int par = 0; row < T; row += gridDim.x, par ^= 1) {
+    float4_t v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+      v[k] = xv[k];
+      if (t != nullptr && (tid + 256 * k) * 4 < D) {
+        if (t2 != nullptr) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[k][e] = fmaf(g[k][e], (float)ta[k][e] + (float)tb[k][e], v[k][e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[k][e] = fmaf(g[k][e], (float)ta[k][e], v[k][e]);
+        }
+      }
+    }
+    if (row + (int)gridDim.x < T) load(row + gridDim.x);  // in flight during this row's reduction and stores
+    float4_t *xr = (float4_t *)(x + (long)row * ldx);
+    if (t != nullptr) {
+#pragma unroll
+      for (int k = 0; k < NV; k++)
+        if ((tid + 256 * k) * 4 < D) xr[tid + 256 * k] = v[k];
+    }
+    float s = 0.0f, q = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+      s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
+      q += (v[k][0] * v[k][0] + v[k][1] * v[k][1]) + (v[k][2] * v[k][2] + v[k][3] * v[k][3]);
+    }
+    s = wave_sum(s);
+    q = wave_sum(q);
+    // red[par]: the previous row's values (red[par ^ 1]) may still be read by a slower wave; the row before that is
+    // past everyone's barrier of the previous row
+    if (lane == 0) {
+      red[par][2 * wave] = s;
+      red[par][2 * wave + 1] = q;
+    }
+    __syncthreads();
+    s = (red[par][0] + red[par][2]) + (red[par][4] + red[par][6]);
+    q = (red[par][1] + red[par][3]) + (red[par][5] + red[par][7]);
+    float mu, r;
+    if (w == nullptr) {
+      mu = s * inv;
+      r = rsqrtf(q * inv - mu * mu + eps);  // var = E[x^2] - mu^2 (kern.c:52-53)
+    } else {
+      mu = 0.0f;
+      r = rsqrtf(q * inv + eps);
+    }
 #pragma unroll
     for (int k = 0; k < NV; k++) {
       const int c = (tid + 256 * k) * 4;
       if (c < D) {
-        const half4_t a = *(const half4_t *)(t + (long)row * ldt + c);
-        const float4_t g = *(const float4_t *)(gate + c);
-        if (t2 != nullptr) {
-          const half4_t b = *(const half4_t *)(t2 + (long)row * ldt + c);
+        half4_t o;
 #pragma unroll
-          for (int e = 0; e < 4; e++) v[k][e] = fmaf(g[e], (float)a[e] + (float)b[e], v[k][e]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; e++) v[k][e] = fmaf(g[e], (float)a[e], v[k][e]);
-        }
+        for (int e = 0; e < 4; e++) o[e] = (hxa_h)((v[k][e] - mu) * r * mul[k][e] + sh[k][e]);
+        *(half4_t *)(h + (long)row * ldh + c) = o;
       }
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < NV; k++) {
-    const int c = (tid + 256 * k) * 4;
-    if (c < D) {
-      mul[k] = *(const float4_t *)(scale + c) + 1.0f;
-      if (w != nullptr) mul[k] *= *(const float4_t *)(w + c);  // k_rms_prep: M = (1 + scale) * w
-      sh[k] = *(const float4_t *)(shift + c);
-    }
-  }
-  if (t != nullptr) {
-#pragma unroll
-    for (int k = 0; k < NV; k++)
-      if ((tid + 256 * k) * 4 < D) xr[tid + 256 * k] = v[k];
-  }
-  float s = 0.0f, q = 0.0f;
-#pragma unroll
-  for (int k = 0; k < NV; k++) {
-    s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
-    q += (v[k][0] * v[k][0] + v[k][1] * v[k][1]) + (v[k][2] * v[k][2] + v[k][3] * v[k][3]);
-  }
-  s = wave_sum(s);
-  q = wave_sum(q);
-  if (lane == 0) {
-    red[2 * wave] = s;
-    red[2 * wave + 1] = q;
-  }
-  __syncthreads();
-  s = (red[0] + red[2]) + (red[4] + red[6]);
-  q = (red[1] + red[3]) + (red[5] + red[7]);
-  const float inv = 1.0f / (float)D;
-  float mu, r;
-  if (w == nullptr) {
-    mu = s * inv;
-    r = rsqrtf(q * inv - mu * mu + eps);  // var = E[x^2] - mu^2 (kern.c:52-53)
-  } else {
-    mu = 0.0f;
-    r = rsqrtf(q * inv + eps);
-  }
-#pragma unroll
-  for (int k = 0; k < NV; k++) {
-    const int c = (tid + 256 * k) * 4;
-    if (c < D) {
-      half4_t o;
-#pragma unroll
-      for (int e = 0; e < 4; e++) o[e] = (hxa_h)((v[k][e] - mu) * r * mul[k][e] + sh[k][e]);
-      *(half4_t *)(h + (long)row * ldh + c) = o;
     }
   }
 }
@@ -545,6 +560,10 @@ __global__ void quantize_kernel(const float *W, int N, int K, int fmt, int kt, v
   }
 }
 
+#ifndef HXA_NORM_WPC
+#define HXA_NORM_WPC 4
+#endif
+
 inline unsigned nblk(long n, int per = 256) { return (unsigned)((n + per - 1) / per); }
 
 }  // namespace
@@ -561,11 +580,20 @@ int hxa_resid2_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t,
                                hxa_h *h, long ldh, hipStream_t st) {
   if (T <= 0 || D % 256 != 0 || ldx % 4 || ldh % 4 || (t && (ldt % 4 || !gate)) || (t2 && !t)) return HXA_E_ARG;
   if (D > 4096) return HXA_E_ARG;
+  // HXA_NORM_WPC workgroups per CU, each taking every grid-th row
+  static int num_cu = 0;
+  if (num_cu == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                  hipSuccess)
+      num_cu = 256;
+  }
+  const int grid = (int)std::min<long>(T, (long)HXA_NORM_WPC * num_cu);
   switch ((D + 1023) / 1024) {
 #define HXA_NORMROW(V)                                                                                            \
   case V:                                                                                                          \
-    hxa_launch(normrow_kernel<V>, dim3(T), dim3(256), 0, st, x, ldx, D, t, t2, ldt, gate, shift, scale, w, eps, \
-                       h, ldh);                                                                                    \
+    hxa_launch(normrow_kernel<V>, dim3(grid), dim3(256), 0, st, x, ldx, D, T, t, t2, ldt, gate, shift, scale, w, \
+               eps, h, ldh);                                                                                       \
     break;
     HXA_NORMROW(1) HXA_NORMROW(2) HXA_NORMROW(3) HXA_NORMROW(4)
 #undef HXA_NORMROW

@@ -422,18 +422,28 @@ HXA_DEV void gemm_epilogue(const GemmParams &p, const hxa_h *Cs, int m0, int n0,
 // layouts: K rows in krow_key order, chunks XOR-swizzled), with the exact online softmax in fp32; O = f16(P V / l).
 // LDS: the GEMM's ring (64 KB, then the query tile [128][136] fp16 in its place), then K, K, V^T, V^T (64 KB): the
 // first two key tiles are loaded when the workgroup starts and arrive during the main loop.
-constexpr int XA_KV_OFF = 4 * 16384 + 256;
-constexpr int XA_LDS = XA_KV_OFF + 4 * 16384;
+// LDS of the fused kernel: the 128x128 fp16 ring [0, 64 KB) (later the query staging and the V^T tiles 2, 3 of the
+// two-pass form), K / V^T tiles 0, 1 at XA_KV_OFF, K tiles 2, 3 at XA_K23_OFF: 160 KB. The ring's prefetch sink is
+// not needed (the fused kernel prefetches nothing).
+constexpr int XA_KV_OFF = 4 * 16384;
+constexpr int XA_K23_OFF = XA_KV_OFF + 4 * 16384;
+constexpr int XA_LDS = XA_K23_OFF + 2 * 16384;
+static_assert(XA_KV_OFF >= GemmGeo<128, 128, HXA_W_F16>::NS * GemmGeo<128, 128, HXA_W_F16>::STAGE &&
+                  XA_KV_OFF >= GemmGeo<128, 128, HXA_W_F16>::C_BYTES && XA_LDS <= 160 * 1024,
+              "fused cross-attention LDS layout");
 // key tile i of the tile's head into LDS buffer i & 1: 16 KB of K (rows in krow_key order, 256 B each, chunk c at
 // c ^ (row & 15)) and 16 KB of V^T (128 rows of 64 keys, chunk c at c ^ ((d >> 1) & 7)); keys past NKV read a valid
 // row (probability 0). 8 loads per wave of the 4.
-HXA_DEV void xattn_load_kv(const GemmParams &p, int m0, int n0, int i, int wave, int lane, uint8_t *lds8) {
+// key tile i of the workgroup's head and image -> K tile at kb, V^T tile at vb (16 KB each, the attention kernel's
+// swizzled layout); keys past NKV read a valid row
+HXA_DEV void xattn_load_tile(const GemmParams &p, int m0, int n0, int i, int wave, int lane, uint8_t *kb, uint8_t *vb,
+                             bool with_k = true, bool with_v = true) {
   const int img = m0 / p.xa_T, h = n0 >> 7, key0 = i * 64, NKV = p.xa_nkv;
   const hxa_h *kh = p.xa_k + (long)img * p.xa_kb + h * 128;
   const hxa_h *vh = p.xa_vt + (long)img * p.xa_vb + (long)h * 128 * p.xa_ldvt;
-  uint8_t *kb = lds8 + XA_KV_OFF + (i & 1) * 16384, *vb = lds8 + XA_KV_OFF + (2 + (i & 1)) * 16384;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
+    if (!with_k) break;
     const int blk = j * 4 + wave;
     const int row = 4 * blk + (lane >> 4), c = (lane & 15) ^ (row & 15);
     const int key = min(key0 + krow_key(row), NKV - 1);
@@ -441,12 +451,17 @@ HXA_DEV void xattn_load_kv(const GemmParams &p, int m0, int n0, int i, int wave,
   }
 #pragma unroll
   for (int j = 0; j < 4; j++) {
+    if (!with_v) break;
     const int blk = j * 4 + wave;
     const int d = 8 * blk + (lane >> 3), c = (lane & 7) ^ ((d >> 1) & 7);
     int key = key0 + c * 8;
     if (key >= NKV) key = 0;
     g2l16_opaque(vh + (long)d * p.xa_ldvt + key, vb + blk * 1024);
   }
+}
+// tiles 0 and 1 (and, for the online form, every later tile in turn) at the K / V^T buffers past the GEMM's ring
+HXA_DEV void xattn_load_kv(const GemmParams &p, int m0, int n0, int i, int wave, int lane, uint8_t *lds8) {
+  xattn_load_tile(p, m0, n0, i, wave, lane, lds8 + XA_KV_OFF + (i & 1) * 16384, lds8 + XA_KV_OFF + (2 + (i & 1)) * 16384);
 }
 template <int MI, int NI, int WTM, int WTN>
 HXA_DEV void xattn_tail(const GemmParams &p, float16_t (&acc)[NI][MI], int m0, int n0, int tid, int lane, int wave, int wm,
@@ -501,6 +516,118 @@ HXA_DEV void xattn_tail(const GemmParams &p, float16_t (&acc)[NI][MI], int m0, i
 #pragma unroll
   for (int d = 0; d < 4; d++) o[d] = (float16_t){};
   float mrun = -INFINITY, lsum = 0.0f;
+  if (ntiles <= 4) {
+    // Up to 256 keys: every tile stays in LDS (tiles 2 and 3 in the staging region, free once every wave holds its
+    // q fragments), so the scores of all tiles are formed first and the row max is exact: no running rescale, and
+    // the exponentials of tile t + 1 run between the P V MFMAs of tile t.
+    // (K of tiles 2 and 3 was loaded with tiles 0 and 1 and has landed; their V^T goes to the staging region)
+    __syncthreads();
+    auto kt = [&](int t) -> const uint8_t * {
+      return t < 2 ? lds8 + XA_KV_OFF + t * 16384 : lds8 + XA_K23_OFF + (t - 2) * 16384;
+    };
+    auto vt = [&](int t) -> const uint8_t * {
+      return t < 2 ? lds8 + XA_KV_OFF + (2 + t) * 16384 : lds8 + (t - 2) * 16384;
+    };
+    if (ntiles > 2) xattn_load_tile(p, m0, n0, 2, wave, lane, nullptr, lds8, false, true);
+    if (ntiles > 3) xattn_load_tile(p, m0, n0, 3, wave, lane, nullptr, lds8 + 16384, false, true);
+    // S^T = K Q^T of all four tiles as one stream of 64 MFMAs, each K fragment read 8 MFMAs ahead (one wave per
+    // SIMD here: nothing else covers the LDS latency). Absent tiles (t >= ntiles) read unused LDS and are masked.
+    float16_t S[4][2];
+#pragma unroll
+    for (int t = 0; t < 4; t++) S[t][0] = S[t][1] = (float16_t){};
+    auto kfrag = [&](int i) {  // i = (t * 8 + ds) * 2 + kb2
+      const int t = i >> 4, ds = (i >> 1) & 7, kb2 = i & 1, row = kb2 * 32 + ql, c = 2 * ds + g;
+      return *(const half8_t *)(kt(t) + row * 256 + ((c ^ (row & 15)) << 4));
+    };
+    constexpr int KA = 8;
+    half8_t kr[KA];
+#pragma unroll
+    for (int i = 0; i < KA; i++) kr[i] = kfrag(i);
+#pragma unroll
+    for (int i = 0; i < 64; i++) {
+      __builtin_amdgcn_sched_barrier(0);
+      const half8_t cur = kr[i % KA];
+      if (i + KA < 64) kr[i % KA] = kfrag(i + KA);
+      __builtin_amdgcn_sched_barrier(0);
+      S[i >> 4][i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur, qf[(i >> 1) & 7], S[i >> 4][i & 1], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+      if (t >= ntiles) {
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) S[t][kb2][r] = -INFINITY;
+      }
+    // keys past nvalid in the last tile
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+      if (t == ntiles - 1 && t * 64 + 64 > p.xa_nvalid) {
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            if (t * 64 + kb2 * 32 + 16 * (r >> 3) + 8 * g + (r & 7) >= p.xa_nvalid) S[t][kb2][r] = -INFINITY;
+      }
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) m = fmaxf(m, S[t][kb2][r]);
+    {
+      float lo, hi;
+      halves(m, lo, hi);
+      m = fmaxf(lo, hi);  // finite: nvalid >= 1
+    }
+    const float mb = m * L2E;
+    float ls[2] = {0.0f, 0.0f};
+    half8_t pf[2][2][2];
+    auto expo = [&](int t, int idx) {  // probability of score idx of tile t (0 for masked keys and absent tiles)
+      const int kb2 = idx >> 4, r = idx & 15;
+      const float pv = __builtin_amdgcn_exp2f(fmaf(S[t][kb2][r], L2E, -mb));
+      ls[idx & 1] += pv;
+      pf[t & 1][kb2][r >> 3][r & 7] = (hxa_h)pv;
+    };
+#pragma unroll
+    for (int idx = 0; idx < 32; idx++) expo(0, idx);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      if (t == 2 && ntiles > 2) {  // V^T of tiles 2 and 3 landed
+        wait_vm<0>();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
+      if (t < ntiles) {
+        const uint8_t *vb = vt(t);
+        auto vfrag = [&](int j) {  // j = (kb2 * 2 + ks) * 4 + dblk
+          const int dblk = j & 3, kk = j >> 2, d = dblk * 32 + ql, c = 2 * kk + g;
+          return *(const half8_t *)(vb + d * 128 + ((c ^ ((d >> 1) & 7)) << 4));
+        };
+        constexpr int VA = 4;  // V^T fragments read 4 MFMAs ahead
+        half8_t vr[VA];
+#pragma unroll
+        for (int j = 0; j < VA; j++) vr[j] = vfrag(j);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          __builtin_amdgcn_sched_barrier(0);
+          const half8_t cur = vr[j % VA];
+          if (j + VA < 16) vr[j % VA] = vfrag(j + VA);
+          __builtin_amdgcn_sched_barrier(0);
+          o[j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur, pf[t & 1][j >> 3][(j >> 2) & 1], o[j & 3], 0, 0, 0);
+          if (t + 1 < 4) {
+            expo(t + 1, 2 * j);
+            expo(t + 1, 2 * j + 1);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    lsum = ls[0] + ls[1];
+  } else {
   for (int i = 0; i < ntiles; i++) {
     if (i + 1 < ntiles) wait_vm<8>();  // tile i landed (tile i + 1 may still fly)
     else wait_vm<0>();
@@ -577,6 +704,7 @@ HXA_DEV void xattn_tail(const GemmParams &p, float16_t (&acc)[NI][MI], int m0, i
       xattn_load_kv(p, m0, n0, i + 2, wave, lane, lds8);
     }
   }
+  }
   float llo, lhi;
   halves(lsum, llo, lhi);
   const float ltot = llo + lhi;
@@ -618,6 +746,10 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   if constexpr (XATTN) {  // the first two key tiles of the fused attention, into LDS past the ring
     xattn_load_kv(p, m0, n0, 0, wave, lane, lds8);
     if (p.xa_nvalid > 64) xattn_load_kv(p, m0, n0, 1, wave, lane, lds8);
+    if (p.xa_nvalid > 128 && p.xa_nvalid <= 256) {  // the two-pass form: K of tiles 2 and 3 as well
+      xattn_load_tile(p, m0, n0, 2, wave, lane, lds8 + XA_K23_OFF, nullptr, true, false);
+      if (p.xa_nvalid > 192) xattn_load_tile(p, m0, n0, 3, wave, lane, lds8 + XA_K23_OFF + 16384, nullptr, true, false);
+    }
   }
 
   // ---- loader: stage s <- k tile kt. A and fp16 W rows are 64 B (4 chunks of 16 B) stored with the chunk swizzle
