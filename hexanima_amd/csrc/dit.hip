@@ -41,6 +41,7 @@ struct Dit {
   float *mods = nullptr, *fmod = nullptr, *sig = nullptr, *cosT = nullptr, *sinT = nullptr, *ones = nullptr;
   hxa_h *ctx16 = nullptr;  // Anima: [B*C][DC]; MOSS: text [B*ntxt][ntxt_in]
   void *ws = nullptr;
+  long ws_bytes = 0;  // the block workspace, sized for the full-resolution pass
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
   // form 1 (the reference's glue): fp16 matrices inside `glue`, fp32 vectors in `vec`, per-step vectors below
@@ -246,6 +247,7 @@ int record_step(Dit &d, const Pass &ps) {
   const int B = b.batch, D = b.D, C4 = 4 * d.cfg.lat_c, temb = d.cfg.temb, nb = d.cfg.nblocks;
   hipStream_t st = d.st;
   const bool moss_ref = d.form == 1 && b.kind == 1;
+  if (hxa_block_ws_bytes(&b) > d.ws_bytes) return HXA_E_ARG;  // a low-res pass needs no more than the full one
   if (d.form == 1) DTRY(b.kind == 0 ? record_prelude_anima_ref(d) : record_prelude_moss_ref(d));
   if (d.form == 0) {
   // timestep embedding and modulation
@@ -285,8 +287,8 @@ int record_step(Dit &d, const Pass &ps) {
       DTRY(hxa_gemm_launch(g, st));
     }
   }
-  // blocks, chained: each block's MLP residual (x += gate * (t1 + t2), blk.c:172-174) is applied by the next
-  // block's first norm, which reads x anyway; the last one is applied here
+  // blocks, chained: each block's MLP residual (x += gate * (sum of its split-K partials), blk.c:172-174) is applied
+  // by the next block's first norm, which reads x anyway; the last one is applied here
   auto mlp_gate = [&](int k) { return b.kind == 0 ? d.mods + (long)k * 9 * D + 8L * D : d.mods + 5L * D; };
   for (int k = 0; k < nb; k++) {
     const float *mod = b.kind == 0 ? d.mods + (long)k * 9 * D : d.mods;
@@ -295,8 +297,9 @@ int record_step(Dit &d, const Pass &ps) {
   }
   {
     long ld = 0;
-    const hxa_h *t1 = (const hxa_h *)hxa_block_ws_buf(&b, d.ws, 5, &ld), *t2 = (const hxa_h *)hxa_block_ws_buf(&b, d.ws, 9, &ld);
-    DTRY(hxa_resadd2_launch(d.x, D, t1, t2, ld, B * ps.Ttot, D, mlp_gate(nb - 1), st));
+    const hxa_h *t1 = (const hxa_h *)hxa_block_ws_buf(&b, d.ws, 5, &ld);
+    DTRY(hxa_resaddn_launch(d.x, D, t1, hxa_block_down_parts(&b), (long)B * ps.Ttot * D, ld, B * ps.Ttot, D,
+                            mlp_gate(nb - 1), st));
   }
   // final layer (+ Euler update); rapid-moss: RMS head and x0 = z - v
   if (moss_ref)
@@ -432,7 +435,8 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   M((void **)&d.sinT, 4L * d.Ttot * 64);
   M((void **)&d.ones, 4L * D);
   M((void **)&d.ctx16, b.kind == 0 ? 2L * B * b.C * b.DC : 2L * B * d.ntxt * cfg->ntxt_in);
-  M(&d.ws, hxa_block_ws_bytes(&b));
+  d.ws_bytes = hxa_block_ws_bytes(&b);
+  M(&d.ws, d.ws_bytes);
   if (rc != HXA_OK) {
     hxa_dit_destroy(dp);
     return rc;

@@ -32,26 +32,28 @@ HXA_DEV float wave_sum(float v) {
 // thread). The column vectors (gate, 1 + scale [* w], shift) are read once per workgroup, and the next row's x and
 // pending terms are loaded while the current row is reduced and stored, so loads and stores of the grid overlap.
 // The row sums are wave DPP sums combined through LDS in a fixed order (the same bits for any grid).
-template <int NV>
+// NP pending fp16 terms (0, 1, 2 or 4; term j at t + j tz) are summed in a fixed order, ((t0 + t1) + (t2 + t3)).
+template <int NV, int NP>
 __global__ __launch_bounds__(256) void normrow_kernel(float *__restrict__ x, long ldx, int D, int T,
-                                                      const hxa_h *__restrict__ t, const hxa_h *__restrict__ t2, long ldt,
+                                                      const hxa_h *__restrict__ t, long tz, long ldt,
                                                       const float *__restrict__ gate, const float *__restrict__ shift,
                                                       const float *__restrict__ scale, const float *__restrict__ w,
                                                       float eps, hxa_h *__restrict__ h, long ldh) {
+  constexpr int NT = NP > 0 ? NP : 1;
   __shared__ float red[2][8];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int row = blockIdx.x;
   float4_t xv[NV];
-  half4_t ta[NV], tb[NV];
+  half4_t ta[NT][NV];
   auto load = [&](int r) {
     const float4_t *xr = (const float4_t *)(x + (long)r * ldx);
 #pragma unroll
     for (int k = 0; k < NV; k++) {
       const int c = (tid + 256 * k) * 4;
       xv[k] = c < D ? xr[tid + 256 * k] : (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
-      if (t != nullptr && c < D) {
-        ta[k] = *(const half4_t *)(t + (long)r * ldt + c);
-        if (t2 != nullptr) tb[k] = *(const half4_t *)(t2 + (long)r * ldt + c);
+      if (NP > 0 && c < D) {
+#pragma unroll
+        for (int j = 0; j < NP; j++) ta[j][k] = *(const half4_t *)(t + j * tz + (long)r * ldt + c);
       }
     }
   };
@@ -62,7 +64,7 @@ __global__ __launch_bounds__(256) void normrow_kernel(float *__restrict__ x, lon
   for (int k = 0; k < NV; k++) {
     const int c = (tid + 256 * k) * 4;
     if (c < D) {
-      if (t != nullptr) g[k] = *(const float4_t *)(gate + c);
+      if (NP > 0) g[k] = *(const float4_t *)(gate + c);
       mul[k] = *(const float4_t *)(scale + c) + 1.0f;
       if (w != nullptr) mul[k] *= *(const float4_t *)(w + c);
       sh[k] = *(const float4_t *)(shift + c);
@@ -74,19 +76,20 @@ __global__ __launch_bounds__(256) void normrow_kernel(float *__restrict__ x, lon
 #pragma unroll
     for (int k = 0; k < NV; k++) {
       v[k] = xv[k];
-      if (t != nullptr && (tid + 256 * k) * 4 < D) {
-        if (t2 != nullptr) {
+      if (NP > 0 && (tid + 256 * k) * 4 < D) {
 #pragma unroll
-          for (int e = 0; e < 4; e++) v[k][e] = fmaf(g[k][e], (float)ta[k][e] + (float)tb[k][e], v[k][e]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; e++) v[k][e] = fmaf(g[k][e], (float)ta[k][e], v[k][e]);
+        for (int e = 0; e < 4; e++) {
+          float sum = (float)ta[0][k][e];
+          if (NP == 2) sum += (float)ta[NT > 1 ? 1 : 0][k][e];
+          if (NP == 4)
+            sum = (sum + (float)ta[NT > 1 ? 1 : 0][k][e]) + ((float)ta[NT > 2 ? 2 : 0][k][e] + (float)ta[NT > 3 ? 3 : 0][k][e]);
+          v[k][e] = fmaf(g[k][e], sum, v[k][e]);
         }
       }
     }
     if (row + (int)gridDim.x < T) load(row + gridDim.x);  // in flight during this row's reduction and stores
     float4_t *xr = (float4_t *)(x + (long)row * ldx);
-    if (t != nullptr) {
+    if (NP > 0) {
 #pragma unroll
       for (int k = 0; k < NV; k++)
         if ((tid + 256 * k) * 4 < D) xr[tid + 256 * k] = v[k];
@@ -174,21 +177,29 @@ __global__ __launch_bounds__(256) void rmsrope_kernel(hxa_h *q0, hxa_h *q1, cons
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// x += gate * (t1 + t2)   (kern.c:330-339, split-K down projection)
+// x += gate * (t1 + t2)   (kern.c:330-339, split-K down projection); NP = 4: x += gate * ((t1 + t2) + (t3 + t4)),
+// term j at t + j tz
 // ---------------------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void resadd2_kernel(float *x, long ldx, const hxa_h *__restrict__ t1,
-                                                      const hxa_h *__restrict__ t2, long ldt, int T, int D,
-                                                      const float *__restrict__ gate) {
+template <int NP>
+__global__ __launch_bounds__(256) void resaddn_kernel(float *x, long ldx, const hxa_h *__restrict__ t, long tz, long ldt,
+                                                      int T, int D, const float *__restrict__ gate) {
   const long i4 = (long)blockIdx.x * 256 + threadIdx.x;
   const int per_row = D / 4;
   if (i4 >= (long)T * per_row) return;
   const int row = (int)(i4 / per_row), c = (int)(i4 % per_row) * 4;
   float4_t *xp = (float4_t *)(x + (long)row * ldx + c);
-  const half4_t a = *(const half4_t *)(t1 + (long)row * ldt + c), b = *(const half4_t *)(t2 + (long)row * ldt + c);
+  half4_t a[NP];
+#pragma unroll
+  for (int j = 0; j < NP; j++) a[j] = *(const half4_t *)(t + j * tz + (long)row * ldt + c);
   const float4_t g = *(const float4_t *)(gate + c);
   float4_t xv = *xp;
 #pragma unroll
-  for (int e = 0; e < 4; e++) xv[e] = fmaf(g[e], (float)a[e] + (float)b[e], xv[e]);
+  for (int e = 0; e < 4; e++) {
+    const float sum = NP == 2 ? (float)a[0][e] + (float)a[NP > 1 ? 1 : 0][e]
+                              : ((float)a[0][e] + (float)a[NP > 1 ? 1 : 0][e]) +
+                                    ((float)a[NP > 2 ? 2 : 0][e] + (float)a[NP > 3 ? 3 : 0][e]);
+    xv[e] = fmaf(g[e], sum, xv[e]);
+  }
   *xp = xv;
 }
 
@@ -573,13 +584,20 @@ inline unsigned nblk(long n, int per = 256) { return (unsigned)((n + per - 1) / 
 int hxa_resid_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, long ldt, const float *gate,
                               const float *shift, const float *scale, const float *w, float eps, hxa_h *h, long ldh,
                               hipStream_t st) {
-  return hxa_resid2_norm_mod_launch(x, ldx, T, D, t, nullptr, ldt, gate, shift, scale, w, eps, h, ldh, st);
+  return hxa_residn_norm_mod_launch(x, ldx, T, D, t, t ? 1 : 0, 0, ldt, gate, shift, scale, w, eps, h, ldh, st);
 }
 int hxa_resid2_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, const hxa_h *t2, long ldt,
                                const float *gate, const float *shift, const float *scale, const float *w, float eps,
                                hxa_h *h, long ldh, hipStream_t st) {
-  if (T <= 0 || D % 256 != 0 || ldx % 4 || ldh % 4 || (t && (ldt % 4 || !gate)) || (t2 && !t)) return HXA_E_ARG;
-  if (D > 4096) return HXA_E_ARG;
+  if (t2 && !t) return HXA_E_ARG;
+  return hxa_residn_norm_mod_launch(x, ldx, T, D, t, t2 ? 2 : t ? 1 : 0, t2 ? (long)(t2 - t) : 0, ldt, gate, shift,
+                                    scale, w, eps, h, ldh, st);
+}
+int hxa_residn_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, int np, long tz, long ldt,
+                               const float *gate, const float *shift, const float *scale, const float *w, float eps,
+                               hxa_h *h, long ldh, hipStream_t st) {
+  if (T <= 0 || D % 256 != 0 || ldx % 4 || ldh % 4 || (np > 0 && (!t || ldt % 4 || tz % 4 || !gate))) return HXA_E_ARG;
+  if (D > 4096 || !(np == 0 || np == 1 || np == 2 || np == 4)) return HXA_E_ARG;
   // HXA_NORM_WPC workgroups per CU, each taking every grid-th row
   static int num_cu = 0;
   if (num_cu == 0) {
@@ -589,17 +607,15 @@ int hxa_resid2_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t,
       num_cu = 256;
   }
   const int grid = (int)std::min<long>(T, (long)HXA_NORM_WPC * num_cu);
-  switch ((D + 1023) / 1024) {
-#define HXA_NORMROW(V)                                                                                            \
-  case V:                                                                                                          \
-    hxa_launch(normrow_kernel<V>, dim3(grid), dim3(256), 0, st, x, ldx, D, T, t, t2, ldt, gate, shift, scale, w, \
-               eps, h, ldh);                                                                                       \
-    break;
-    HXA_NORMROW(1) HXA_NORMROW(2) HXA_NORMROW(3) HXA_NORMROW(4)
+  const int nv = (D + 1023) / 1024;
+#define HXA_NORMROW(V, P)                                                                                         \
+  if (nv == V && np == P)                                                                                          \
+    hxa_launch(normrow_kernel<V, P>, dim3(grid), dim3(256), 0, st, x, ldx, D, T, t, tz, ldt, gate, shift, scale, w, \
+               eps, h, ldh);
+#define HXA_NORMROW_P(V) HXA_NORMROW(V, 0) HXA_NORMROW(V, 1) HXA_NORMROW(V, 2) HXA_NORMROW(V, 4)
+  HXA_NORMROW_P(1) HXA_NORMROW_P(2) HXA_NORMROW_P(3) HXA_NORMROW_P(4)
+#undef HXA_NORMROW_P
 #undef HXA_NORMROW
-    default:
-      return HXA_E_ARG;
-  }
   return LAUNCH_OK();
 }
 
@@ -618,8 +634,15 @@ int hxa_rmsrope_launch(hxa_h *q0, hxa_h *q1, const float *g0, const float *g1, l
 
 int hxa_resadd2_launch(float *x, long ldx, const hxa_h *t1, const hxa_h *t2, long ldt, int T, int D, const float *gate,
                        hipStream_t st) {
-  if (D % 4 || ldx % 4 || ldt % 4) return HXA_E_ARG;
-  hxa_launch(resadd2_kernel, dim3(nblk((long)T * D / 4)), dim3(256), 0, st, x, ldx, t1, t2, ldt, T, D, gate);
+  return hxa_resaddn_launch(x, ldx, t1, 2, (long)(t2 - t1), ldt, T, D, gate, st);
+}
+int hxa_resaddn_launch(float *x, long ldx, const hxa_h *t, int np, long tz, long ldt, int T, int D, const float *gate,
+                       hipStream_t st) {
+  if (D % 4 || ldx % 4 || ldt % 4 || tz % 4 || !(np == 2 || np == 4)) return HXA_E_ARG;
+  if (np == 2)
+    hxa_launch(resaddn_kernel<2>, dim3(nblk((long)T * D / 4)), dim3(256), 0, st, x, ldx, t, tz, ldt, T, D, gate);
+  else
+    hxa_launch(resaddn_kernel<4>, dim3(nblk((long)T * D / 4)), dim3(256), 0, st, x, ldx, t, tz, ldt, T, D, gate);
   return LAUNCH_OK();
 }
 

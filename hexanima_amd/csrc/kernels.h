@@ -79,6 +79,10 @@ int hxa_resid_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, 
 int hxa_resid2_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, const hxa_h *t2, long ldt,
                                const float *gate, const float *shift, const float *scale, const float *w, float eps,
                                hxa_h *h, long ldh, hipStream_t st);
+// the same with np (0, 1, 2 or 4) pending fp16 terms, term j at t + j tz: x += gate * ((t0 + t1) + (t2 + t3))
+int hxa_residn_norm_mod_launch(float *x, long ldx, int T, int D, const hxa_h *t, int np, long tz, long ldt,
+                               const float *gate, const float *shift, const float *scale, const float *w, float eps,
+                               hxa_h *h, long ldh, hipStream_t st);
 int hxa_norm_mod_launch(const float *x, long ldx, int T, int D, const float *shift, const float *scale, const float *w,
                         float eps, hxa_h *h, long ldh, hipStream_t st);
 // per-head RMSNorm * gain (+ RoPE on pairs (d, d+64)) in place for ntens tensors sharing a layout
@@ -86,6 +90,9 @@ int hxa_rmsrope_launch(hxa_h *q0, hxa_h *q1, const float *g0, const float *g1, l
                        const float *sinT, int ttab, hipStream_t st);
 // x[t][c] += gate[c] * (t1 + t2)
 int hxa_resadd2_launch(float *x, long ldx, const hxa_h *t1, const hxa_h *t2, long ldt, int T, int D, const float *gate,
+                       hipStream_t st);
+// x[t][c] += gate[c] * (sum of np = 2 or 4 fp16 terms, term j at t + j tz, summed ((t0 + t1) + (t2 + t3)))
+int hxa_resaddn_launch(float *x, long ldx, const hxa_h *t, int np, long tz, long ldt, int T, int D, const float *gate,
                        hipStream_t st);
 
 // layout conversions between the reference's crouton tiles and row-major device buffers
@@ -159,6 +166,8 @@ int hxa_noalloc_setup(void **out);
 // hxa_block_run for a chain of blocks: pend_gate != NULL applies the previous block's pending MLP residual
 // (x += pend_gate * (t1 + t2) from the workspace) in the first norm; defer != 0 leaves this block's MLP residual
 // pending in t1 / t2
+// fp16 partials of the MLP-down that a chained block leaves pending (t1 .. t1 + (n-1) BT D in its workspace)
+int hxa_block_down_parts(const hxa_block_dims *d);
 int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
                           const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
                           void *stream, const float *pend_gate, int defer);

@@ -457,12 +457,22 @@ struct WsLayout {
   long dq_bytes;            // size of WS_DQ's first slot (0: no quantised projection is dequantised first)
   long dq2_off, dq2_bytes;  // its second slot (text k / v weight)
 };
-// Quantised attention-output, cross-q and MLP-down projections (N <= K) at this many rows or more run as one
-// dequantisation pass into fp16 (WS_DQ) and the fp16 kernels: at 1536 tokens the main loops' per-MFMA
-// dequantisation costs those shapes 11-18% more than the pass. Wider projections (qkv, MLP up) keep the fused form.
+// Quantised cross-q projections (and, from DQ_WIDE_ROWS rows, every quantised projection) at this many rows or more
+// run as one dequantisation pass into fp16 (WS_DQ) and the fp16 kernels; below DQ_WIDE_ROWS the attention-output and
+// MLP-down projections run fused split-K 4 (q_split4), the wider ones (qkv, MLP up) fused on their own tiles.
 constexpr long DQ_MIN_ROWS = 1024;
 // from this many rows on the pass also pays for the wide projections (qkv, MLP up / up-gate)
 constexpr long DQ_WIDE_ROWS = 4096;
+// int8 / int4 attention-output and MLP-down projections at DQ_MIN_ROWS .. DQ_WIDE_ROWS rows (no LoRA) run fused,
+// split-K 4 on the ping-pong tiles, into four fp16 partials that the next norm adds: those tiles hide the
+// dequantisation under their MFMAs, and no fp16 copy of the weight goes through memory (1536 tokens, 2.9B-class
+// MLP-down 10240 -> 2560: 80 us fused against 15.5 us of dequantisation + 84.5 us of fp16 GEMM in the step).
+static bool q_split4(const hxa_block_dims *d, int fmt, int K) {
+  const long BT = (long)d->batch * d->T;
+  return d->kind != 2 && (fmt & ~HXA_W_KTILED) != HXA_W_F16 && BT >= DQ_MIN_ROWS && BT < DQ_WIDE_ROWS && K % 128 == 0;
+}
+// fp16 partials the MLP-down leaves (pending across a chain of blocks): 4 in the fused split-K 4 form, else 2
+int hxa_block_down_parts(const hxa_block_dims *d) { return q_split4(d, d->fmt_mlp, d->F) ? 4 : 2; }
 static WsLayout ws_layout(const hxa_block_dims *d) {
   const long BT = (long)d->batch * d->T, BC = (long)d->batch * d->C, D = d->D;
   // with the LoRA (kind 2) the rows of h, o and mid carry the L columns of the projection that reads them:
@@ -481,7 +491,8 @@ static WsLayout ws_layout(const hxa_block_dims *d) {
   L.ld[WS_K] = 2 * D;
   put(WS_VT, 2 * D * BT, BT);
   put(WS_O, 2 * BT * LDO, LDO);
-  put(WS_T1, 2 * 2 * BT * D, D);  // two split-K partials
+  const long nparts = q_split4(d, d->fmt_attn, d->D) || hxa_block_down_parts(d) == 4 ? 4 : 2;
+  put(WS_T1, 2 * nparts * BT * D, D);  // split-K partials, BT x D apart
   L.off[WS_T2] = L.off[WS_T1] + 2 * BT * D;
   L.ld[WS_T2] = D;
   put(WS_MID, 2 * BT * LDM, LDM);
@@ -500,6 +511,8 @@ static WsLayout ws_layout(const hxa_block_dims *d) {
   for (int i = 0; i < nproj && BT >= DQ_MIN_ROWS; i++) {
     const MatSpec &m = mats.m[i];
     if (m.fmt == HXA_W_F16 || (d->kind == 0 && i == 3)) continue;  // the text k / v weight has its own slot
+    const bool o_like = i == 1 || (d->kind == 0 && i == 4), down = i == (d->kind == 0 ? 6 : 3);
+    if ((o_like && q_split4(d, m.fmt, m.K)) || (down && q_split4(d, m.fmt, m.K))) continue;  // fused split-K 4
     if (BT >= DQ_WIDE_ROWS || m.N <= m.K) dq = std::max(dq, 2L * m.N * m.K);
   }
   // a second slot for the text k / v weight (2D x DC), so that it and the cross q run as one paired fp16 launch
@@ -735,26 +748,37 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   // the GPU at N = D) then the residual; measured faster than the single-launch HXA_EPI_RESADD_SPLIT2 form, whose
   // 128-wide tiles leave a quarter of the CUs idle at 1536 x 2048. With the LoRA the halves are [0, F/2) and
   // [F/2, F) + the LoRA columns (moss blk.c:256-259): two launches.
+  const int down_np = hxa_block_down_parts(d);
   auto down_resadd = [&](const hxa_h *a, const HxaWeight &w, const float *gate) -> int {
-    const HxaWeight *wp;
-    TRY(prep(w, wp));
-    if (!lora) {
+    const HxaWeight *wp = &w;
+    if (down_np == 4) {
+      TRY(gemm(a, ldmid, BT, w, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 4, (long)BT * D));
+    } else if (!lora) {
+      TRY(prep(w, wp));
       TRY(gemm(a, ldmid, BT, *wp, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 2, (long)BT * D));
     } else {
+      TRY(prep(w, wp));
       const int G = F / 64;  // k groups of one half
       const HxaWeight w0 = ksub(*wp, 0, G), w1 = ksub(*wp, G, G + LORA_R / 32);
       TRY(gemm(a, ldmid, BT, w0, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0));
       TRY(gemm(a + F / 2, ldmid, BT, w1, HXA_EPI_STORE, t2, D, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     }
-    return defer ? HXA_OK : hxa_resadd2_launch(x, D, t1, t2, D, BT, D, gate, st);
+    return defer ? HXA_OK : hxa_resaddn_launch(x, D, t1, down_np, (long)BT * D, D, BT, D, gate, st);
   };
   // the attention output projection whose gated residual the next norm applies (no stage dump): one K pass into
   // t1, or -- when that runs as a single round of 128x128 (or smaller) tiles, whose short k loops leave the fixed
   // prologue and epilogue a large share -- two fp16 K-half partials into t1 and t2 on twice the workgroups, which
   // the norm adds (1536 tokens: 4% faster for fp16, 9-21% for int8 / int4 weights; slower on a grid of 192x256 or
-  // 256x256 tiles or of several rounds). split_o says which, for that norm's t2.
+  // 256x256 tiles or of several rounds). split_o says which.
+  // int8 / int4 weights at 1024 .. 4095 rows: the fused split-K 4 form (q_split4), four partials. o_np: the partials
+  // the next norm adds.
   bool split_o = false;
+  int o_np = 1;
   auto deferred_proj = [&](const HxaWeight &w) -> int {
+    if (q_split4(d, w.fmt, w.K)) {
+      o_np = 4;
+      return gemm(o, ldo, BT, w, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 4, (long)BT * D);
+    }
     const HxaWeight *wp;
     TRY(prep(w, wp));
     const HxaGemm g1 = make(o, ldo, BT, *wp, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0);
@@ -762,6 +786,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     split_o = !lora && w.K % 64 == 0 && hxa_gemm_plan(g1, &bm, &bn, &nw, &rounds) == HXA_OK && rounds == 1 &&
               bm * bn <= 128 * 128;
     HxaGemm g = g1;
+    o_np = split_o ? 2 : 1;
     if (split_o) {
       g.epi = HXA_EPI_PARTIAL;
       g.ksplit = 2;
@@ -777,7 +802,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     const int BC = B * d->C;
     hxa_h *ck = (hxa_h *)(w8 + L.off[WS_CK]), *cvT = (hxa_h *)(w8 + L.off[WS_CVT]);
     // site 0: self-attention (blk.c:157-162)
-    TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, pend_gate ? t1 : nullptr, pend_gate ? t2 : nullptr, D, pend_gate, mod,
+    TRY(hxa_residn_norm_mod_launch(x, D, BT, D, pend_gate ? t1 : nullptr, pend_gate ? down_np : 0, (long)BT * D, D, pend_gate, mod,
                                    mod + D, nullptr, 1e-6f, h, ldh, st));
     STAGE_DONE();
     // q, k: RMSNorm * gain + RoPE (blk.c:159-160), fused into the projection's store unless a stage dump needs the
@@ -822,7 +847,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     TRY(fuse ? deferred_proj(Wo) : gemm(o, ldo, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 1: cross-attention (blk.c:163-169)
-    TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 2 * D,
+    TRY(hxa_residn_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse ? o_np : 0, (long)BT * D, D, mod + 2 * D,
                                    mod + 3 * D, mod + 4 * D, nullptr, 1e-6f, h, ldh, st));
     STAGE_DONE();
     if (fuse_x) {
@@ -870,7 +895,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     TRY(fuse ? deferred_proj(Wco) : gemm(o, ldo, BT, Wco, HXA_EPI_RESADD, nullptr, 0, x, mod + 5 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // site 2: MLP (blk.c:170-174)
-    TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 5 * D,
+    TRY(hxa_residn_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse ? o_np : 0, (long)BT * D, D, mod + 5 * D,
                                    mod + 6 * D, mod + 7 * D, nullptr, 1e-6f, h, ldh, st));
     STAGE_DONE();
     pf0 = &W2;
@@ -886,7 +911,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     const float *gq = pv.vec, *gk = pv.vec + 128, *n1 = pv.vec + 256, *n2 = pv.vec + 256 + D;
     const HxaWeight &Wqkv = pv.w[0], &Wo = pv.w[1], &Wug = pv.w[2], &Wdn = pv.w[3];
     // attention half (moss blk.c:234-247)
-    TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, pend_gate ? t1 : nullptr, pend_gate ? t2 : nullptr, D, pend_gate, mod,
+    TRY(hxa_residn_norm_mod_launch(x, D, BT, D, pend_gate ? t1 : nullptr, pend_gate ? down_np : 0, (long)BT * D, D, pend_gate, mod,
                                    mod + D, n1, 1e-6f, h, ldh, st));
     STAGE_DONE();
     if (lora) TRY(lora_a(h, ldh, pv.w[4]));  // L_q | L_k | L_v (blk.c:238)
@@ -905,7 +930,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     TRY(fuse ? deferred_proj(Wo) : gemm(o, ldo, BT, Wo, HXA_EPI_RESADD, nullptr, 0, x, mod + 2 * D, nullptr, 0, 0, 1, 0));
     STAGE_DONE();
     // FFN half (moss blk.c:248-259)
-    TRY(hxa_resid2_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse && split_o ? t2 : nullptr, D, mod + 2 * D,
+    TRY(hxa_residn_norm_mod_launch(x, D, BT, D, fuse ? t1 : nullptr, fuse ? o_np : 0, (long)BT * D, D, mod + 2 * D,
                                    mod + 3 * D, mod + 4 * D, n2, 1e-6f, h, ldh, st));
     STAGE_DONE();
     if (lora) TRY(lora_a(h, ldh, pv.w[6]));  // L_ug (blk.c:251)

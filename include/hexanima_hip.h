@@ -224,9 +224,9 @@ typedef struct {
   int gelu;      /* Anima MLP activation: 0 erf (reference block), 1 tanh */
 } hxa_block_dims;
 /* bytes of the activation workspace of hxa_block_run. With int8 / int4 weights it includes the dequantisation slot:
- * one fp16 copy of the largest quantised projection that runs from fp16 -- from batch*T >= 1024 rows those with
- * N <= K (attention output, cross q, MLP down), from 4096 rows all of them -- and for Anima blocks a second slot for
- * the text k / v weight. */
+ * one fp16 copy of the largest quantised projection that runs from fp16 -- at 1024 .. 4095 rows (batch*T) the cross
+ * q, from 4096 rows all of them -- and for Anima blocks a second slot for the text k / v weight; at 1024 .. 4095 rows
+ * the int8 / int4 attention-output and MLP-down projections run fused into four fp16 split-K partials instead. */
 long hxa_block_ws_bytes(const hxa_block_dims *d);
 /* One block, everything on the device:
  *   x    [batch*T][D] fp32 residual stream, updated in place
