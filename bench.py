@@ -165,7 +165,9 @@ def extra_dits():
 def microbench():
     """Kernel-level figures on the benchmark shapes (HIP events, inputs resident in HBM):
     - W8A16 / W4A16 linears at M = 1536 (K x N = 2048 x 6144, 2048 x 2048, 2048 x 8192, 8192 x 2048; int8 uniform in
-      [-127, 127] / int4 uniform in [-8, 7], group-32 fp16 scales 0.02/127, pack layout), beside fp16 weights;
+      [-127, 127] / int4 uniform in [-8, 7], group-32 fp16 scales 0.02/127, pack layout), beside fp16 weights, as one
+      pass storing fp16; and the N <= K shapes in the form the block runs them with int8 / int4 weights (fused,
+      split-K 4 into fp16 partials);
     - attention: the 2B block's self (1536 x 1536, 16 heads) and cross (1536 x 256) attention, and the MOSS-class
       joint attention (6656 x 6656, 24 heads);
     - one 2B fp16 block (hxa_block_run, 1536 tokens), the block latency."""
@@ -203,6 +205,28 @@ def microbench():
                                          N, 0, None, 0, None, None, 0, 0, s), "gemm")
                 row[f"{K}x{N}"] = _rate(2.0 * M * N * K, _time_launches(L, hip, run, s))
             res[key][name] = row
+    # the N <= K projections as the block runs them with int8 / int4 weights at 1536 tokens: fused, split-K 4 into
+    # four fp16 partials (the next norm adds them); fp16 in the same form for comparison
+    res["linear_m1536_splitk4"] = {}
+    for name, fmt, shapes in (("fp16", hip.W_F16, ((2048, 2048), (8192, 2048), (2560, 2560), (10240, 2560))),
+                              ("q8", hip.W_Q8, ((2048, 2048), (8192, 2048), (2560, 2560), (10240, 2560))),
+                              ("q4", hip.W_Q4, ((2048, 2048), (8192, 2048)))):
+        row = {}
+        for K, N in shapes:
+            assert 4 * N <= 10240
+            if fmt == hip.W_F16:
+                hip.check(L.hxa_fill_normal(Wb.ptr, 1, N * K, 22, 0.0, 0.02, s), "fill")
+            elif fmt == hip.W_Q8:
+                hip.check(L.hxa_fill_uniform_int(Wb.ptr, 8, N * K, 23, -127, 127, s), "fill")
+            else:
+                hip.check(L.hxa_fill_uniform_int(Wb.ptr, 4, N * K // 2, 24, -8, 7, s), "fill")
+            sp = None if fmt == hip.W_F16 else Sb.ptr
+
+            def run4(K=K, N=N, fmt=fmt, sp=sp):
+                hip.check(L.hxa_gemm(A.ptr, K, M, fmt | hip.W_KTILED, Wb.ptr, sp, None, N, K, 4, hip.EPI_PARTIAL, O.ptr,
+                                     N, M * N, None, 0, None, None, 0, 0, s), "gemm")
+            row[f"{K}x{N}"] = _rate(2.0 * M * N * K, _time_launches(L, hip, run4, s))
+        res["linear_m1536_splitk4"][name] = row
     # attention (q, k, v^T resident; random fp16)
     for name, Tq, NKV, Hh in (("self_1536x1536_h16", T, T, H), ("cross_1536x256_h16", T, C_TXT, H),
                               ("joint_6656x6656_h24", 6656, 6656, 24)):
