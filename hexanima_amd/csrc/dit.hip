@@ -31,6 +31,11 @@ struct Dit {
   int Timg = 0, Ttot = 0, ntxt = 0;
   hipStream_t st = nullptr;
   std::vector<void *> packs;
+  // Anima blocks whose text k / v the chain computes up front (hxa_block_textkv_plan): block k's ck [B C][D] at
+  // tkv + 2 B C D k, its cvt [D][B C] right after; the grouped launch's parameters on the device
+  hxa_h *tkv = nullptr;
+  void *tkv_par = nullptr;
+  int tkv_tiles = 0, tkv_fmt = 0;
   long pack_bytes = 0;
   hxa_h *modw_all = nullptr;  // one allocation: every block's modulation weights, stacked
   std::vector<hxa_h *> modw;  // Anima: per block [6D][D]; MOSS: one shared [6D][D]
@@ -290,10 +295,13 @@ int record_step(Dit &d, const Pass &ps) {
   // blocks, chained: each block's MLP residual (x += gate * (sum of its split-K partials), blk.c:172-174) is applied
   // by the next block's first norm, which reads x anyway; the last one is applied here
   auto mlp_gate = [&](int k) { return b.kind == 0 ? d.mods + (long)k * 9 * D + 8L * D : d.mods + 5L * D; };
+  if (d.tkv_par) DTRY(hxa_gemm_group_launch(d.tkv_par, nb, d.tkv_tiles, d.tkv_fmt, st));  // every block's text k / v
+  const long tkv_per = 2L * B * b.C * D;
   for (int k = 0; k < nb; k++) {
     const float *mod = b.kind == 0 ? d.mods + (long)k * 9 * D : d.mods;
+    const hxa_h *ck = d.tkv ? d.tkv + tkv_per * k : nullptr, *cvt = d.tkv ? d.tkv + tkv_per * k + tkv_per / 2 : nullptr;
     DTRY(hxa_block_run_chained(&b, d.packs[k], d.x, b.kind == 0 ? d.ctx16 : nullptr, mod, ps.cosT, ps.sinT, d.ws, 0,
-                               nullptr, 0, st, k > 0 ? mlp_gate(k - 1) : nullptr, 1));
+                               nullptr, 0, st, k > 0 ? mlp_gate(k - 1) : nullptr, 1, ck, cvt));
   }
   {
     long ld = 0;
@@ -510,6 +518,38 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
     rc = dfail(HXA_E_HIP, "rope upload");
   if (rc == HXA_OK && hipStreamSynchronize(d.st) != hipSuccess) rc = dfail(HXA_E_HIP, "init sync");
   if (tmp) (void)hipFree(tmp);
+  // text k / v up front: when the blocks' qkv grids cannot carry their text k / v tiles, every block's text k / v
+  // projection (ctx only) runs at the start of the step in one grouped launch, and each block fuses its cross q with
+  // the attention
+  if (rc == HXA_OK && b.kind == 0) {
+    const int nb = cfg->nblocks;
+    const long per = 2L * B * b.C * D;  // elements of one block's ck + cvt
+    std::vector<HxaGemm> gs(nb);
+    std::vector<HxaWeight> ws(nb);
+    hxa_h *probe = nullptr;  // planning needs real, aligned ck / cvt addresses: one block's worth first
+    M((void **)&probe, 2L * per);
+    bool use = rc == HXA_OK;
+    for (int k = 0; k < nb && use; k++)
+      use = hxa_block_textkv_plan(&b, d.packs[k], d.ctx16, probe, probe + per / 2, &gs[k], &ws[k]) == 1;
+    if (probe) (void)hipFree(probe);
+    if (use) {
+      M((void **)&d.tkv, 2L * per * nb);
+      for (int k = 0; k < nb && rc == HXA_OK; k++) {
+        if (hxa_block_textkv_plan(&b, d.packs[k], d.ctx16, d.tkv + per * k, d.tkv + per * k + per / 2, &gs[k], &ws[k]) != 1)
+          rc = dfail(HXA_E_ARG, "dit: text k / v plan");
+        gs[k].w = &ws[k];
+      }
+      const long pb = hxa_gemm_group_param_bytes(nb);
+      std::vector<uint8_t> par(pb);
+      if (rc == HXA_OK) {
+        const int r = hxa_gemm_group_prepare(gs.data(), nb, par.data(), &d.tkv_tiles, &d.tkv_fmt);
+        if (r != HXA_OK) rc = dfail(r, "dit: text k / v grouped launch");
+      }
+      M(&d.tkv_par, pb);
+      if (rc == HXA_OK && hipMemcpy(d.tkv_par, par.data(), pb, hipMemcpyHostToDevice) != hipSuccess)
+        rc = dfail(HXA_E_HIP, "dit: text k / v parameters");
+    }
+  }
   if (rc != HXA_OK) {
     hxa_dit_destroy(dp);
     return rc;
@@ -534,7 +574,8 @@ extern "C" int hxa_dit_destroy(void *p) {
   for (void *q : d->packs) if (q) (void)hipFree(q);
   if (d->modw_all) (void)hipFree(d->modw_all);
   void *bufs[] = {d->glue, d->lat, d->vel, d->tok, d->x, d->sinus, d->cvec, d->mods, d->fmod, d->sig, d->cosT, d->sinT,
-                  d->ones, d->ctx16, d->ws, d->vec, d->emb, d->a1, d->lora, d->h1, d->zrows, d->x0rows};
+                  d->ones, d->ctx16, d->ws, d->vec, d->emb, d->a1, d->lora, d->h1, d->zrows, d->x0rows, d->tkv,
+                  d->tkv_par};
   for (void *q : bufs) if (q) (void)hipFree(q);
   if (d->sig_ev) (void)hipEventDestroy(d->sig_ev);
   if (d->sig_host) (void)hipHostFree(d->sig_host);

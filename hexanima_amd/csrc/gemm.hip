@@ -1201,6 +1201,12 @@ __global__ __launch_bounds__(512) void gemm_pp_pair_kernel(GemmParams p0, GemmPa
   if ((int)blockIdx.x < nwg0) gemm_pp_body<BM, BN, FMT, ASYM, true>(p0, blockIdx.x);
   else gemm_pp_body<BM, BN, FMT, ASYM, true>(p1, blockIdx.x - nwg0);
 }
+// G independent GEMMs of one tile shape and weight format on the ping-pong kernel, each with its own parameters
+// (a device array): workgroup (x, y) runs tile x of GEMM y
+template <int BM, int BN, int FMT, bool ASYM>
+__global__ __launch_bounds__(512) void gemm_pp_group_kernel(const GemmParams *__restrict__ ps) {
+  gemm_pp_body<BM, BN, FMT, ASYM, true>(ps[blockIdx.y], blockIdx.x);
+}
 
 // Tile cost model, per weight format (fp16, int8, int4): a launch of `waves` rounds of workgroups over the CUs takes
 // about waves * (a * BM * BN * Kslice / 1e6 + b) microseconds. a and b were fitted by least squares (b >= 0) to
@@ -1513,6 +1519,63 @@ hipError_t launch_pair_fmt(int bm, int bn, int nw, const GemmParams &p0, const G
   if (bm == 128 && bn == 128 && nw == 8) return launch_pair_t<128, 128, FMT, ASYM, 8>(p0, p1, st);
   if (bm == 192 && bn == 256 && nw == 9) return launch_pp_pair_t<192, 256, FMT, ASYM>(p0, p1, st);
   return hipErrorInvalidValue;
+}
+
+long hxa_gemm_group_param_bytes(int G) { return (long)G * (long)sizeof(GemmParams); }
+
+int hxa_gemm_group_prepare(const HxaGemm *g, int G, void *params_host, int *tiles, int *fmt) {
+  if (G < 1 || !g || !params_host || !tiles || !fmt) return HXA_E_ARG;
+  GemmParams *ps = (GemmParams *)params_host;
+  for (int i = 0; i < G; i++) {
+    if (g[i].ksplit != 1 || g[i].pf_bytes > 0 || g[i].M != g[0].M || !g[i].w || !g[0].w || g[i].w->N != g[0].w->N ||
+        g[i].w->K != g[0].w->K || (g[i].w->fmt & ~HXA_W_KTILED) != (g[0].w->fmt & ~HXA_W_KTILED) ||
+        (g[i].w->z != nullptr) != (g[0].w->z != nullptr))
+      return HXA_E_ARG;
+    HxaGemm gf = g[i];
+    gf.force_bm = 192;
+    gf.force_bn = 256;
+    gf.force_nw = 9;
+    int bm, bn, nw;
+    HxaWeight w;
+    bool split2;
+    const int r = gemm_prepare(gf, ps[i], bm, bn, nw, w, split2);
+    if (r != HXA_OK) return r;
+    if (split2 || bm != 192 || bn != 256 || nw != 9) return HXA_E_ARG;
+    ps[i].clk = HxaClk{nullptr, 0};  // the parameters outlive any clock record
+    *fmt = w.fmt | (w.z ? 0x100 : 0);
+  }
+  *tiles = ps[0].tiles_m * ps[0].tiles_n;
+  return HXA_OK;
+}
+
+namespace {
+template <int FMT, bool ASYM>
+hipError_t launch_group_t(const GemmParams *ps, int G, int tiles, hipStream_t st) {
+  auto kern = gemm_pp_group_kernel<192, 256, FMT, ASYM>;
+  using Geo = GemmGeo<192, 256, FMT>;
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Geo::LDS);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  hxa_launch(kern, dim3(tiles, G), dim3(512), Geo::LDS, st, ps);
+  return hipGetLastError();
+}
+}  // namespace
+
+int hxa_gemm_group_launch(const void *params_dev, int G, int tiles, int fmt, hipStream_t st) {
+  if (!params_dev || G < 1 || G > 65535 || tiles < 1) return HXA_E_ARG;
+  const GemmParams *ps = (const GemmParams *)params_dev;
+  hipError_t e;
+  switch (fmt) {
+    case HXA_W_F16: e = launch_group_t<HXA_W_F16, false>(ps, G, tiles, st); break;
+    case HXA_W_Q8: e = launch_group_t<HXA_W_Q8, false>(ps, G, tiles, st); break;
+    case HXA_W_Q4: e = launch_group_t<HXA_W_Q4, false>(ps, G, tiles, st); break;
+    case HXA_W_Q4 | 0x100: e = launch_group_t<HXA_W_Q4, true>(ps, G, tiles, st); break;
+    default: return HXA_E_ARG;
+  }
+  return e == hipSuccess ? HXA_OK : HXA_E_HIP;
 }
 
 bool hxa_gemm_pair_fits(const HxaGemm &g0, const HxaGemm &g1) {

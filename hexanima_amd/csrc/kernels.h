@@ -55,6 +55,13 @@ bool hxa_gemm_xattn_fits(int M, int N);
 // whether hxa_gemm_pair_launch(g0, g1) would be one launch that takes no more rounds of workgroups over the CUs than
 // g0 alone (g1 only fills CUs g0 leaves idle)
 bool hxa_gemm_pair_fits(const HxaGemm &g0, const HxaGemm &g1);
+// G GEMMs of one shape and weight format (ksplit 1, no prefetch) in one launch on the ping-pong 192x256 tile, each
+// with its own operands and epilogue. prepare fills params_host (hxa_gemm_group_param_bytes(G) bytes, to be copied
+// to device memory as they are) and returns the tiles per GEMM and the launch format; the device copy stays valid
+// while the GEMMs' operands stay where they are.
+long hxa_gemm_group_param_bytes(int G);
+int hxa_gemm_group_prepare(const HxaGemm *g, int G, void *params_host, int *tiles, int *fmt);
+int hxa_gemm_group_launch(const void *params_dev, int G, int tiles, int fmt, hipStream_t st);
 // int8 / int4 weight -> fp16 k-tiled [K/32][N][32] at out (2 N K bytes): the same values the GEMM main loops use
 int hxa_dequant_launch(const HxaWeight &w, hxa_h *out, hipStream_t st);
 
@@ -168,6 +175,11 @@ int hxa_noalloc_setup(void **out);
 // pending in t1 / t2
 // fp16 partials of the MLP-down that a chained block leaves pending (t1 .. t1 + (n-1) BT D in its workspace)
 int hxa_block_down_parts(const hxa_block_dims *d);
+// ck_pre / cvt_pre (Anima blocks, no stage stop): the block's text k / v, computed before the chain
+// (hxa_block_textkv_plan); the block then skips that projection
 int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
                           const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
-                          void *stream, const float *pend_gate, int defer);
+                          void *stream, const float *pend_gate, int defer, const hxa_h *ck_pre = nullptr,
+                          const hxa_h *cvt_pre = nullptr);
+int hxa_block_textkv_plan(const hxa_block_dims *d, const void *pack, const void *ctx, hxa_h *ck, hxa_h *cvt,
+                          HxaGemm *g, HxaWeight *w);

@@ -609,11 +609,62 @@ struct StageTimer {
   }
 };
 
+// The text k / v projection of block `pack` (ctx [B C][DC] -> ck [B C][D] with RMSNorm * gain, cvt [D][B C]) as the
+// block runner would launch it, for a chain that computes every block's text k / v before the chain in one grouped
+// launch. Returns 1 and fills *g (its weight in *w) when that pays: the qkv grid leaves too few idle CUs to carry the
+// text k / v tiles in its own launch (so the block could not fuse its cross q with the attention) while the fused
+// cross-attention kernel fits; 0 when the block runner's own placement is kept.
+int hxa_block_textkv_plan(const hxa_block_dims *d, const void *pack, const void *ctx, hxa_h *ck, hxa_h *cvt,
+                          HxaGemm *g, HxaWeight *w) {
+  if (d->kind != 0 || check_dims(d) != HXA_OK || !pack || !ctx || !ck || !cvt || !g || !w) return 0;
+  const long BT = (long)d->batch * d->T, BC = (long)d->batch * d->C, D = d->D;
+  if (BT >= DQ_WIDE_ROWS || d->T % 128 || d->C % 8) return 0;
+  const PackView pv = pack_view(d, pack);
+  const HxaWeight &Wqkv = pv.w[0], &Wcq = pv.w[2], &Wckv = pv.w[3];
+  const float *gain = pv.vec;
+  if (!hxa_gemm_xattn_fits((int)BT, Wcq.N)) return 0;
+  *w = Wckv;
+  HxaGemm kv{};
+  kv.A = (const hxa_h *)ctx;
+  kv.lda = d->DC;
+  kv.M = (int)BC;
+  kv.w = w;
+  kv.ksplit = 1;
+  kv.epi = HXA_EPI_STORE;
+  kv.out = ck;
+  kv.ldo = D;
+  kv.out_t = cvt;
+  kv.ldo_t = BC;
+  kv.split_col = (int)D;
+  kv.hn_cols = (int)D;  // ck: RMSNorm * gain (blk.c:167)
+  kv.hn_g0 = kv.hn_g1 = gain + 384;
+  kv.hn_gsplit = (int)D;
+  kv.hn_ttab = d->T;
+  // the qkv projection as the runner launches it below DQ_WIDE_ROWS rows (its own weights, head norm + RoPE, V^T);
+  // only its shape and tile matter here
+  HxaGemm qkv = kv;
+  qkv.A = ck;
+  qkv.lda = D;
+  qkv.M = (int)BT;
+  qkv.w = &Wqkv;
+  qkv.out_t = cvt;
+  qkv.ldo_t = BT;
+  qkv.split_col = (int)(2 * D);
+  qkv.hn_cols = (int)(2 * D);
+  qkv.hn_g0 = gain;
+  qkv.hn_g1 = gain + 128;
+  qkv.hn_cos = qkv.hn_sin = gain;
+  if (hxa_gemm_pair_fits(qkv, kv)) return 0;
+  *g = kv;
+  return 1;
+}
+
 // One block; stage numbering follows the reference TICK() order (blk.c:136).
 extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
                              const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
                              void *stream) {
-  return hxa_block_run_chained(d, pack, x, ctx, mod, cosT, sinT, ws, stop, stage_us, nstage, stream, nullptr, 0);
+  return hxa_block_run_chained(d, pack, x, ctx, mod, cosT, sinT, ws, stop, stage_us, nstage, stream, nullptr, 0,
+                               nullptr, nullptr);
 }
 
 // pend_gate != NULL: the previous block of a chain left its MLP residual pending (its two fp16 down-projection
@@ -622,7 +673,7 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
 // the last block of the chain). Without a stage stop only.
 int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
                           const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
-                          void *stream, const float *pend_gate, int defer) {
+                          void *stream, const float *pend_gate, int defer, const hxa_h *ck_pre, const hxa_h *cvt_pre) {
   g_err[0] = 0;
   if ((pend_gate || defer) && stop) return fail(HXA_E_ARG, "block: chained residuals need stop == 0");
   TRY(check_dims(d));
@@ -800,7 +851,11 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     const HxaWeight &Wqkv = pv.w[0], &Wo = pv.w[1], &Wcq = pv.w[2], &Wckv = pv.w[3], &Wco = pv.w[4], &W1 = pv.w[5],
                     &W2 = pv.w[6];
     const int BC = B * d->C;
-    hxa_h *ck = (hxa_h *)(w8 + L.off[WS_CK]), *cvT = (hxa_h *)(w8 + L.off[WS_CVT]);
+    // pre: this block's text k / v were computed before the chain (hxa_block_textkv_plan), ck_pre [BC][D] and
+    // cvt_pre [D][BC] in the layout of the workspace's
+    const bool pre = ck_pre != nullptr && cvt_pre != nullptr && stop == 0;
+    hxa_h *ck = pre ? (hxa_h *)ck_pre : (hxa_h *)(w8 + L.off[WS_CK]);
+    hxa_h *cvT = pre ? (hxa_h *)cvt_pre : (hxa_h *)(w8 + L.off[WS_CVT]);
     // site 0: self-attention (blk.c:157-162)
     TRY(hxa_residn_norm_mod_launch(x, D, BT, D, pend_gate ? t1 : nullptr, pend_gate ? down_np : 0, (long)BT * D, D, pend_gate, mod,
                                    mod + D, nullptr, 1e-6f, h, ldh, st));
@@ -810,7 +865,12 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     const bool fuse = stop == 0;
     bool fuse_x = false;  // the text k / v ran with qkv; the cross site fuses cross q with its attention
     if (fuse) hn = HeadNorm{2 * D, gain, gain + 128, D, cosT, sinT};
-    if (fuse) {
+    if (pre) {
+      const HxaWeight *wp;
+      TRY(prep(Wqkv, wp));
+      TRY(gemm(h, ldh, BT, *wp, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, vT, BT, 2 * D, 1, 0));
+      fuse_x = T % 128 == 0 && d->C % 8 == 0 && hxa_gemm_xattn_fits(BT, Wcq.N);
+    } else if (fuse) {
       // When the text k / v projection (ctx only) fits in the qkv launch without a further round of workgroups, it
       // runs there, filling CUs the qkv grid leaves idle, and the cross-attention site fuses the cross-q projection
       // with its attention (fuse_x). Both projections in one weight format: int8 / int4 text k / v weights take the
@@ -875,11 +935,15 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
       const HxaWeight *wcq;
       TRY(prep(Wcq, wcq));
       const HxaGemm gq = make(h, ldh, BT, *wcq, HXA_EPI_STORE, qk, ldqk, nullptr, nullptr, nullptr, 0, 0, 1, 0);
-      if (fuse) hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
-      const HxaWeight *wckv;
-      TRY(prep(Wckv, wckv, 1));
-      const HxaGemm gkv = make((const hxa_h *)ctx, d->DC, BC, *wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0);
-      {
+      if (pre) {  // the text k / v are there already
+        const int r = hxa_gemm_launch(gq, st);
+        if (r != HXA_OK) return fail(r, "block cross q gemm rejected");
+      } else {
+        if (fuse) hn = HeadNorm{D, gain + 384, gain + 384, D, nullptr, nullptr};  // ck: RMSNorm * gain (blk.c:167)
+        const HxaWeight *wckv;
+        TRY(prep(Wckv, wckv, 1));
+        const HxaGemm gkv =
+            make((const hxa_h *)ctx, d->DC, BC, *wckv, HXA_EPI_STORE, ck, D, nullptr, nullptr, cvT, BC, D, 1, 0);
         const int r = hxa_gemm_pair_launch(gq, gkv, st);
         if (r != HXA_OK) return fail(r, "block cross q / text k v gemms rejected");
       }

@@ -1,0 +1,65 @@
+"""Parity of the int8 DiT at the 2.9B-class block shape (hidden 2560, 20 heads, MLP 10240, 256 text tokens of width
+1024, int8 g32 weights) at 1536 image tokens against the oracle: the velocity of two chained blocks with the
+caller-side glue of phone/animad.cpp:424-492 around them.
+
+At this shape the qkv grid leaves no room for the text k / v tiles in its own launch, so the runner computes every
+block's text k / v up front in one grouped launch and each block fuses its cross q with the attention; the
+attention-output and MLP-down projections run fused split-K 4 into four fp16 partials. The oracle dequantises the
+same int8 weights (f16(q s), gemm2.c:19-35) and computes in double with the reference block's rounding points.
+Tolerance about 3x the error measured on MI355X, as the other DiT tests."""
+import ctypes as C_
+
+import numpy as np
+import pytest
+
+from oracle import hxo
+from tests._helpers import f16, oracle_anima_velocity, unpack_weights
+
+pytestmark = pytest.mark.gpu
+
+D, H, F, C, DC, NB = 2560, 20, 10240, 256, 1024, 2
+LAT = (16, 96, 64)
+
+
+def test_dit_2p9b_q8_two_blocks_velocity_vs_oracle():
+    from hexanima_amd import hip
+
+    hip.init(0)
+    lib = hip.lib()
+    hxo.set_threads(0)
+    print("[case] int8 DiT, hidden 2560, 2 blocks, 1536 tokens, velocity vs oracle", flush=True)
+    bd = hip.BlockDims(0, D, H, F, C, DC, 0, 1, 0, hip.W_Q8, hip.W_Q8, 1)
+    cfg = hip.DitCfg(bd, NB, LAT[0], LAT[1], LAT[2], 256, 0)
+    p = C_.c_void_p()
+    hip.check(lib.hxa_dit_create(C_.byref(cfg), 91, C_.byref(p)), "dit_create")
+    try:
+        rng = np.random.default_rng(29)
+        lat = rng.standard_normal((1,) + LAT).astype(np.float32)
+        ctx = rng.standard_normal((1, C, DC)).astype(np.float32)
+        hip.check(lib.hxa_dit_set_inputs(p, lat.ctypes.data, ctx.ctypes.data), "set_inputs")
+        v = np.zeros_like(lat)
+        hip.check(lib.hxa_dit_velocity(p, 0.75, v.ctypes.data), "velocity")
+
+        def export(which):
+            n = lib.hxa_dit_export(p, which, None, 0)
+            buf = np.zeros(n, np.uint8)
+            assert lib.hxa_dit_export(p, which, buf.ctypes.data, n) == n
+            return buf
+
+        layout = hip.pack_layout(0, D, F, DC, hip.W_Q8, hip.W_Q8)
+        blocks = [unpack_weights(export(k), 0, D, F, DC, hip.W_Q8, hip.W_Q8, layout) for k in range(NB)]
+        modws = [export(NB + k).view(np.uint16).reshape(6 * D, D) for k in range(NB)]
+        g = export(2 * NB).view(np.uint16)
+        C4 = 4 * LAT[0]
+        glue, o = [], 0
+        for (n, k) in ((D, C4), (D, 256), (2 * D, D), (C4, D)):
+            glue.append(g[o:o + n * k].reshape(n, k))
+            o += n * k
+        ref = oracle_anima_velocity(lat, f16(ctx), 0.75, blocks, modws, glue, D=D, H=H, F=F, C4=C4, temb=256)
+        r = float(np.linalg.norm(v - ref) / np.linalg.norm(ref))
+        mx = float(np.max(np.abs(v - ref)))
+        print(f"int8 2.9B-shape DiT velocity: rel err {r:.3e}, max abs {mx:.3e}", flush=True)
+        assert np.isfinite(v).all()
+        assert r < 2e-3 and mx < 9e-3  # measured 6.3e-4, 3.0e-3
+    finally:
+        lib.hxa_dit_destroy(p)

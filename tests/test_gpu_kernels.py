@@ -456,8 +456,10 @@ def test_attention_vs_oracle(T, NKV, nvalid, H):
 
 
 # (M, T, NKV, nvalid): the 2B block's cross site (1536 tokens, 256 text tokens); batch 2 of 256 tokens over 77 of 80
-# text keys (ragged, the last tile masked); megarun's 512 context tokens
-@pytest.mark.parametrize("M,T,NKV,nvalid", [(1536, 1536, 256, 256), (512, 256, 80, 77), (384, 384, 512, 512)])
+# text keys (ragged, the last tile masked); three key tiles, the third ragged (190 of 200); megarun's 512 context
+# tokens (more than four key tiles: the online form)
+@pytest.mark.parametrize("M,T,NKV,nvalid", [(1536, 1536, 256, 256), (512, 256, 80, 77), (256, 256, 200, 190),
+                                            (384, 384, 512, 512)])
 def test_cross_attention_fused_vs_oracle(M, T, NKV, nvalid):
     """hxa_cross_attention_fused: the cross-q projection with its per-head RMSNorm * gain and the attention of every
     head over its image's text keys in one kernel, against the oracle's GEMM (fp16 store), rmsrope (no RoPE) and
