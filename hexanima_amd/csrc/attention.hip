@@ -268,7 +268,7 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
       for (int r = 0; r < 16; r++) xch[(2 + d * 16 + r) * 64 + lane] = acc[d][r];
   }
   __syncthreads();
-  if (half == 1 || !qok) return;
+  if (half == 1) return;
   const float m2 = xch[lane], l2 = xch[64 + lane];
   const float m = fmaxf(mrun, m2);
   const float a1 = mrun == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((mrun - m) * L2E);
@@ -278,18 +278,19 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   halves(lp, llo, lhi);
   const float ltot = llo + lhi;
   const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+  half4_t v[4][4];
 #pragma unroll
   for (int d = 0; d < 4; d++)
 #pragma unroll
-    for (int r4 = 0; r4 < 4; r4++) {
-      half4_t v;
+    for (int r4 = 0; r4 < 4; r4++)
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int r = 4 * r4 + e;
-        v[e] = (hxa_h)((acc[d][r] * a1 + xch[(2 + d * 16 + r) * 64 + lane] * a2) * inv);
+        v[d][r4][e] = (hxa_h)((acc[d][r] * a1 + xch[(2 + d * 16 + r) * 64 + lane] * a2) * inv);
       }
-      *(half4_t *)(o + (long)qrow * p.ldo + d * 32 + 8 * r4 + 4 * g) = v;
-    }
+  // whole output rows, staged past the exchange area (every wave is done with the K / V tiles)
+  const int row0 = qb * QB + wq * 32;
+  store_rows32(lds + NWH * 66 * 64 * 4 + wq * 8192, v, lane, o + (long)row0 * p.ldo, p.ldo, p.T - row0);
 }
 
 }  // namespace

@@ -709,17 +709,17 @@ HXA_DEV void xattn_tail(const GemmParams &p, float16_t (&acc)[NI][MI], int m0, i
   halves(lsum, llo, lhi);
   const float ltot = llo + lhi;
   const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
-  const int qrow = m0 + wave * 32 + ql;
-  hxa_h *orow = p.xa_o + (long)qrow * p.xa_ldo + h * 128;
+  half4_t v[4][4];
 #pragma unroll
   for (int d = 0; d < 4; d++)
 #pragma unroll
-    for (int r4 = 0; r4 < 4; r4++) {
-      half4_t v;
+    for (int r4 = 0; r4 < 4; r4++)
 #pragma unroll
-      for (int e = 0; e < 4; e++) v[e] = (hxa_h)(o[d][4 * r4 + e] * inv);
-      *(half4_t *)(orow + d * 32 + 8 * r4 + 4 * g) = v;
-    }
+      for (int e = 0; e < 4; e++) v[d][r4][e] = (hxa_h)(o[d][4 * r4 + e] * inv);
+  // whole output rows, staged in the K-tile 2 / 3 region: unused with at most two key tiles, and with more every
+  // wave has passed the barrier before tile 2's P V, so every QK pass is done (the online form never uses it)
+  store_rows32(lds8 + XA_K23_OFF + wave * 8192, v, lane, p.xa_o + (long)(m0 + wave * 32) * p.xa_ldo + h * 128, p.xa_ldo,
+               32);
 }
 
 // SPLIT2: the first and second halves of K are rounded to fp16 separately and combined in the residual epilogue,

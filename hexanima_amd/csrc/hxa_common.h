@@ -85,6 +85,27 @@ HXA_DEV void halves(float v, float &lo, float &hi) {
   hi = __builtin_bit_cast(float, (int)r[1]);
 }
 
+// A wave's 32 x 128 fp16 output block of attention -- lane (g = lane / 32, r = lane % 32) holds row r, columns
+// 32 d + 8 i + 4 g .. + 3 as v[d][i] -- written as whole 256-byte rows: staged through 8 KB of LDS at `stage` (row
+// r's 8-byte unit u at r * 256 + 8 (u ^ r): conflict-free both ways), then each row by 32 lanes at out + r * ldo.
+// Rows >= nrows are not written. Only this wave touches `stage`; its LDS accesses complete in order.
+HXA_DEV void store_rows32(uint8_t *stage, const half4_t (&v)[4][4], int lane, hxa_h *out, long ldo, int nrows) {
+  const int g = lane >> 5, r = lane & 31;
+#pragma unroll
+  for (int d = 0; d < 4; d++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int u = d * 8 + 2 * i + g;
+      *(half4_t *)(stage + r * 256 + ((u ^ r) << 3)) = v[d][i];
+    }
+#pragma unroll
+  for (int it = 0; it < 16; it++) {
+    const int row = 2 * it + g;
+    const half4_t x = *(const half4_t *)(stage + row * 256 + ((r ^ row) << 3));
+    if (row < nrows) *(half4_t *)(out + (long)row * ldo + 4 * r) = x;
+  }
+}
+
 // ---- direct-to-LDS loads and VMEM waits (gfx950) ----
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) const void gmem_void_t;
