@@ -64,5 +64,21 @@ def test_dit_2p9b_two_blocks_velocity_vs_oracle(fmt, tol):
         print(f"fmt {fmt} 2.9B-shape DiT velocity: rel err {r:.3e}, max abs {mx:.3e}", flush=True)
         assert np.isfinite(v).all()
         assert r < tol[0] and mx < tol[1]  # measured 6.2e-4 - 6.4e-4, 2.8e-3 - 3.0e-3
+        if fmt == 1:
+            # one low-res first step (factor 2: 384 tokens, phone/animad.cpp:429-446) through the same chain: the
+            # pooled noise, the velocity on the half grid, the landing velocity, then the Euler update
+            t, tn = 1.0, 0.75
+            hip.check(lib.hxa_dit_step_lowres(p, t, tn, 2, 1), "step_lowres")
+            got = np.zeros_like(lat)
+            hip.check(lib.hxa_dit_get_latent(p, got.ctypes.data), "get_latent")
+            xlow = hxo.lowres_pool(lat[0], np.zeros_like(lat[0]), 2, t)[None]
+            vlow = oracle_anima_velocity(xlow, f16(ctx), t, blocks, modws, glue, D=D, H=H, F=F, C4=C4, temb=256)
+            _, vl = hxo.lowres_velocity(xlow[0], vlow[0], lat[0], lat[0], 2, t, tn)
+            ref2 = lat + np.float32(tn - t) * vl[None]
+            d_got, d_ref = got - lat, ref2 - lat
+            r2 = float(np.linalg.norm(d_got - d_ref) / np.linalg.norm(d_ref))
+            mx2 = float(np.max(np.abs(got - ref2)))
+            print(f"low-res step (384 tokens): rel err on delta {r2:.3e}, max abs {mx2:.3e}", flush=True)
+            assert r2 < 1.2e-3 and mx2 < 1.7e-3  # measured 3.6e-4, 5.5e-4
     finally:
         lib.hxa_dit_destroy(p)
