@@ -293,6 +293,79 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   store_rows32(lds + NWH * 66 * 64 * 4 + wq * 8192, v, lane, o + (long)row0 * p.ldo, p.ldo, p.T - row0);
 }
 
+// ---- short key ranges (at most 256 valid keys) ----
+// A workgroup of 4 waves owns 128 queries of one head, and every wave takes all (at most 4) key tiles, resident in
+// LDS together: the two-pass form (attn_two_pass: the exact row max, no running rescale, no key-half merge). The
+// output staging (4 x 8 KB) lies past the tiles (4 x 32 KB), so a wave done early never writes where another still
+// reads K.
+constexpr int SK_LDS = 4 * 2 * TILE_BYTES + 4 * 8192;  // 160 KB
+
+__global__ __launch_bounds__(256) void attn_short_kernel(HxaAttn p, int nqb) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, ql = lane & 31;
+  // XCD-aware order: the query blocks of one head run on one XCD
+  const int ntot = nqb * p.H, bid = blockIdx.x;
+  const int tile = (ntot % 8 == 0) ? (bid % 8) * (ntot / 8) + bid / 8 : bid;
+  const int h = tile / nqb, qb = tile % nqb, b = blockIdx.y;
+  const hxa_h *q = p.q + (long)b * p.q_bstride + h * 128;
+  const hxa_h *k = p.k + (long)b * p.k_bstride + h * 128;
+  const hxa_h *vt = p.vt + (long)b * p.vt_bstride + (long)h * 128 * p.ldvt;
+  hxa_h *o = p.o + (long)b * p.o_bstride + h * 128;
+  const HxaClkMark clk0 = clk_mark(p.clk);
+
+  const int ntiles = (p.nvalid + KT - 1) / KT;  // 1 .. 4
+  // every tile: K at 32 KB t, V^T at 32 KB t + 16 KB; this wave's blocks wave, wave + 4, wave + 8, wave + 12
+  for (int t = 0; t < ntiles; t++) {
+    uint8_t *kd = lds + t * 2 * TILE_BYTES, *vd = kd + TILE_BYTES;
+    const int key0 = t * KT;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int blk = j * 4 + wave;
+      const int row = 4 * blk + (lane >> 4), c = (lane & 15) ^ (row & 15);
+      const int key = min(key0 + krow_key(row), p.NKV - 1);
+      g2l16_opaque(k + (long)key * p.ldk + c * 8, kd + blk * 1024);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int blk = j * 4 + wave;
+      const int d = 8 * blk + (lane >> 3), c = (lane & 7) ^ ((d >> 1) & 7);
+      int key = key0 + c * 8;
+      if (key >= p.NKV) key = 0;
+      g2l16_opaque(vt + (long)d * p.ldvt + key, vd + blk * 1024);
+    }
+  }
+  const int row0 = qb * 128 + wave * 32, qrow = row0 + ql;
+  half8_t qf[8];
+#pragma unroll
+  for (int s = 0; s < 8; s++)
+    qf[s] = qrow < p.T ? *(const half8_t *)(q + (long)qrow * p.ldq + s * 16 + 8 * g) : (half8_t){};
+  wait_vm<0>();
+  __syncthreads();
+
+  const uint8_t *const kts[4] = {lds, lds + 2 * TILE_BYTES, lds + 4 * TILE_BYTES, lds + 6 * TILE_BYTES};
+  const uint8_t *const vts[4] = {lds + TILE_BYTES, lds + 3 * TILE_BYTES, lds + 5 * TILE_BYTES, lds + 7 * TILE_BYTES};
+  float16_t acc[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) acc[d] = (float16_t){};
+  float lsum;
+  attn_two_pass(qf, kts, vts, ntiles, p.nvalid, false, lane, acc, lsum);
+  clk_store(p.clk, (int)(blockIdx.x + blockIdx.y * gridDim.x), tid, clk0);
+  float llo, lhi;
+  halves(lsum, llo, lhi);
+  const float ltot = llo + lhi;
+  const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+  half4_t v[4][4];
+#pragma unroll
+  for (int d = 0; d < 4; d++)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; r4++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[d][r4][e] = (hxa_h)(acc[d][4 * r4 + e] * inv);
+  store_rows32(lds + 8 * TILE_BYTES + wave * 8192, v, lane, o + (long)row0 * p.ldo, p.ldo, p.T - row0);
+}
+
 }  // namespace
 
 int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
@@ -309,6 +382,8 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
     if (hipFuncSetAttribute((const void *)attn_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES) !=
             hipSuccess ||
         hipFuncSetAttribute((const void *)attn_kernel<3>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES) !=
+            hipSuccess ||
+        hipFuncSetAttribute((const void *)attn_short_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, SK_LDS) !=
             hipSuccess)
       return HXA_E_HIP;
     int dev = 0;
@@ -323,11 +398,19 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
     const long wgs = (long)((p.T + qb - 1) / qb) * p.H * p.batch, rounds = (wgs + num_cu - 1) / num_cu;
     return (double)wgs / (double)(rounds * num_cu);
   };
+  HxaAttn pk = p;
+  pk.clk = g_hxa_clk_attn;
+#ifndef HXA_ATTN_SHORT
+#define HXA_ATTN_SHORT 1
+#endif
+  if (HXA_ATTN_SHORT && p.nvalid <= 4 * KT) {  // every key tile resident: the two-pass kernel
+    const int nqb = (p.T + 127) / 128;
+    hxa_launch(attn_short_kernel, dim3(nqb * p.H, p.batch), dim3(256), SK_LDS, st, pk, nqb);
+    return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
+  }
   const bool small = fill(96) > fill(128) + 1e-9;
   const int QB = small ? 96 : 128, nqb = (p.T + QB - 1) / QB;
   dim3 grid(nqb * p.H, p.batch);
-  HxaAttn pk = p;
-  pk.clk = g_hxa_clk_attn;
   if (small) hxa_launch(attn_kernel<3>, grid, dim3(384), LDS_BYTES, st, pk, nqb);
   else hxa_launch(attn_kernel<4>, grid, dim3(512), LDS_BYTES, st, pk, nqb);
   return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;

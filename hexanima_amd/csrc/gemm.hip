@@ -530,103 +530,8 @@ HXA_DEV void xattn_tail(const GemmParams &p, float16_t (&acc)[NI][MI], int m0, i
     };
     if (ntiles > 2) xattn_load_tile(p, m0, n0, 2, wave, lane, nullptr, lds8, false, true);
     if (ntiles > 3) xattn_load_tile(p, m0, n0, 3, wave, lane, nullptr, lds8 + 16384, false, true);
-    // S^T = K Q^T of all four tiles as one stream of 64 MFMAs, each K fragment read 8 MFMAs ahead (one wave per
-    // SIMD here: nothing else covers the LDS latency). Absent tiles (t >= ntiles) read unused LDS and are masked.
-    float16_t S[4][2];
-#pragma unroll
-    for (int t = 0; t < 4; t++) S[t][0] = S[t][1] = (float16_t){};
-    auto kfrag = [&](int i) {  // i = (t * 8 + ds) * 2 + kb2
-      const int t = i >> 4, ds = (i >> 1) & 7, kb2 = i & 1, row = kb2 * 32 + ql, c = 2 * ds + g;
-      return *(const half8_t *)(kt(t) + row * 256 + ((c ^ (row & 15)) << 4));
-    };
-    constexpr int KA = 8;
-    half8_t kr[KA];
-#pragma unroll
-    for (int i = 0; i < KA; i++) kr[i] = kfrag(i);
-#pragma unroll
-    for (int i = 0; i < 64; i++) {
-      __builtin_amdgcn_sched_barrier(0);
-      const half8_t cur = kr[i % KA];
-      if (i + KA < 64) kr[i % KA] = kfrag(i + KA);
-      __builtin_amdgcn_sched_barrier(0);
-      S[i >> 4][i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur, qf[(i >> 1) & 7], S[i >> 4][i & 1], 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-      if (t >= ntiles) {
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; kb2++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) S[t][kb2][r] = -INFINITY;
-      }
-    // keys past nvalid in the last tile
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-      if (t == ntiles - 1 && t * 64 + 64 > p.xa_nvalid) {
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; kb2++)
-#pragma unroll
-          for (int r = 0; r < 16; r++)
-            if (t * 64 + kb2 * 32 + 16 * (r >> 3) + 8 * g + (r & 7) >= p.xa_nvalid) S[t][kb2][r] = -INFINITY;
-      }
-    float m = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-#pragma unroll
-      for (int kb2 = 0; kb2 < 2; kb2++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) m = fmaxf(m, S[t][kb2][r]);
-    {
-      float lo, hi;
-      halves(m, lo, hi);
-      m = fmaxf(lo, hi);  // finite: nvalid >= 1
-    }
-    const float mb = m * L2E;
-    float ls[2] = {0.0f, 0.0f};
-    half8_t pf[2][2][2];
-    auto expo = [&](int t, int idx) {  // probability of score idx of tile t (0 for masked keys and absent tiles)
-      const int kb2 = idx >> 4, r = idx & 15;
-      const float pv = __builtin_amdgcn_exp2f(fmaf(S[t][kb2][r], L2E, -mb));
-      ls[idx & 1] += pv;
-      pf[t & 1][kb2][r >> 3][r & 7] = (hxa_h)pv;
-    };
-#pragma unroll
-    for (int idx = 0; idx < 32; idx++) expo(0, idx);
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-      if (t == 2 && ntiles > 2) {  // V^T of tiles 2 and 3 landed
-        wait_vm<0>();
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-      }
-      if (t < ntiles) {
-        const uint8_t *vb = vt(t);
-        auto vfrag = [&](int j) {  // j = (kb2 * 2 + ks) * 4 + dblk
-          const int dblk = j & 3, kk = j >> 2, d = dblk * 32 + ql, c = 2 * kk + g;
-          return *(const half8_t *)(vb + d * 128 + ((c ^ ((d >> 1) & 7)) << 4));
-        };
-        constexpr int VA = 4;  // V^T fragments read 4 MFMAs ahead
-        half8_t vr[VA];
-#pragma unroll
-        for (int j = 0; j < VA; j++) vr[j] = vfrag(j);
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-          __builtin_amdgcn_sched_barrier(0);
-          const half8_t cur = vr[j % VA];
-          if (j + VA < 16) vr[j % VA] = vfrag(j + VA);
-          __builtin_amdgcn_sched_barrier(0);
-          o[j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur, pf[t & 1][j >> 3][(j >> 2) & 1], o[j & 3], 0, 0, 0);
-          if (t + 1 < 4) {
-            expo(t + 1, 2 * j);
-            expo(t + 1, 2 * j + 1);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    lsum = ls[0] + ls[1];
+    const uint8_t *const kts[4] = {kt(0), kt(1), kt(2), kt(3)}, *const vts[4] = {vt(0), vt(1), vt(2), vt(3)};
+    attn_two_pass(qf, kts, vts, ntiles, p.xa_nvalid, true, lane, o, lsum);
   } else {
   for (int i = 0; i < ntiles; i++) {
     if (i + 1 < ntiles) wait_vm<8>();  // tile i landed (tile i + 1 may still fly)
