@@ -218,11 +218,14 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
       Sn[0] = mfma(kf[ds & 1][0], qf[ds], Sn[0]);
       Sn[1] = mfma(kf[ds & 1][1], qf[ds], Sn[1]);
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
+      for (int u = 0; u < 4; u += 2) {  // two probabilities at a time: one fp16 pair, summed by one v_dot2
         const int idx = ds * 4 + u, kb2 = idx >> 4, r = idx & 15;
-        const float pv = __builtin_amdgcn_exp2f(fmaf(Sc[kb2][r], L2E, -mb));
-        ls[u & 1] += pv;
-        pf[kb2][r >> 3][r & 7] = (hxa_h)pv;
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(Sc[kb2][r], L2E, -mb));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(Sc[kb2][r + 1], L2E, -mb));
+        const half2_t h2 = {(hxa_h)p0, (hxa_h)p1};
+        pf[kb2][r >> 3][r & 7] = h2[0];
+        pf[kb2][r >> 3][(r & 7) + 1] = h2[1];
+        ls[u >> 1] = __builtin_amdgcn_fdot2(h2, (half2_t){(hxa_h)1.0f, (hxa_h)1.0f}, ls[u >> 1], false);
       }
     }
     lsum += ls[0] + ls[1];

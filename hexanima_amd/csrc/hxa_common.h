@@ -253,14 +253,19 @@ HXA_DEV void attn_two_pass(const half8_t (&qf)[8], const uint8_t *const (&kt)[4]
   const float mb = m * L2E;
   float ls[2] = {0.0f, 0.0f};
   half8_t pf[2][2][2];
-  auto expo = [&](int t, int idx) {  // probability of score idx of tile t (0 for masked keys and absent tiles)
+  // probabilities of scores idx, idx + 1 (idx even) of tile t (0 for masked keys and absent tiles): one fp16 pair,
+  // summed by one v_dot2 (the row sum of the fp16 P the P V MFMAs use)
+  auto expo2 = [&](int t, int idx) {
     const int kb2 = idx >> 4, r = idx & 15;
-    const float pv = __builtin_amdgcn_exp2f(fmaf(S[t][kb2][r], L2E, -mb));
-    ls[idx & 1] += pv;
-    pf[t & 1][kb2][r >> 3][r & 7] = (hxa_h)pv;
+    const float p0 = __builtin_amdgcn_exp2f(fmaf(S[t][kb2][r], L2E, -mb));
+    const float p1 = __builtin_amdgcn_exp2f(fmaf(S[t][kb2][r + 1], L2E, -mb));
+    const half2_t h2 = {(hxa_h)p0, (hxa_h)p1};
+    pf[t & 1][kb2][r >> 3][r & 7] = h2[0];
+    pf[t & 1][kb2][r >> 3][(r & 7) + 1] = h2[1];
+    ls[(idx >> 1) & 1] = __builtin_amdgcn_fdot2(h2, (half2_t){(hxa_h)1.0f, (hxa_h)1.0f}, ls[(idx >> 1) & 1], false);
   };
 #pragma unroll
-  for (int idx = 0; idx < 32; idx++) expo(0, idx);
+  for (int idx = 0; idx < 32; idx += 2) expo2(0, idx);
 #pragma unroll
   for (int t = 0; t < 4; t++) {
     if (t == 2 && v2_wait && ntiles > 2) {
@@ -286,10 +291,7 @@ HXA_DEV void attn_two_pass(const half8_t (&qf)[8], const uint8_t *const (&kt)[4]
         if (j + VA < 16) vr[j % VA] = vfrag(j + VA);
         __builtin_amdgcn_sched_barrier(0);
         o[j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur, pf[t & 1][j >> 3][(j >> 2) & 1], o[j & 3], 0, 0, 0);
-        if (t + 1 < 4) {
-          expo(t + 1, 2 * j);
-          expo(t + 1, 2 * j + 1);
-        }
+        if (t + 1 < 4) expo2(t + 1, 2 * j);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
