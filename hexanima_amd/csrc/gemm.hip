@@ -591,14 +591,19 @@ HXA_DEV void xattn_tail(const GemmParams &p, float16_t (&acc)[NI][MI], int m0, i
     }
     const float mb = (mrun == -INFINITY ? 0.0f : mrun) * L2E;
     half8_t pf[2][2];
+    float ls[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; kb2++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const float pv = __builtin_amdgcn_exp2f(fmaf(S[kb2][r], L2E, -mb));
-        lsum += pv;
-        pf[kb2][r >> 3][r & 7] = (hxa_h)pv;
+      for (int r = 0; r < 16; r += 2) {  // fp16 pairs, summed by v_dot2 (the row sum of the fp16 P)
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(S[kb2][r], L2E, -mb));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(S[kb2][r + 1], L2E, -mb));
+        const half2_t h2 = {(hxa_h)p0, (hxa_h)p1};
+        pf[kb2][r >> 3][r & 7] = h2[0];
+        pf[kb2][r >> 3][(r & 7) + 1] = h2[1];
+        ls[(r >> 1) & 1] = __builtin_amdgcn_fdot2(h2, (half2_t){(hxa_h)1.0f, (hxa_h)1.0f}, ls[(r >> 1) & 1], false);
       }
+    lsum += ls[0] + ls[1];
 #pragma unroll
     for (int j = 0; j < 16; j++)
       o[j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[j], pf[j >> 3][(j >> 2) & 1], o[j & 3], 0, 0, 0);
