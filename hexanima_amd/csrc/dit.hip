@@ -90,8 +90,6 @@ int dfail(int code, const char *m) {
     if (r__ != HXA_OK) return r__;  \
   } while (0)
 
-long align256(long x) { return (x + 255) & ~255L; }
-
 // megarun.cpp:77-90: 3-axis split-half table over hd = 128 (22 zero t-angles, 21 h, 21 w; theta 10000)
 void rope_anima(int gh, int gw, std::vector<float> &c, std::vector<float> &s) {
   const int dim_h = 128 / 6 * 2, dim_t = 128 - 2 * dim_h, nt = dim_t / 2, nh = dim_h / 2;

@@ -10,7 +10,6 @@
 #include <cstring>
 #include <algorithm>
 #include <map>
-#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -1062,7 +1061,6 @@ struct Ctx {
   void *wstage = nullptr;  // a registered weight file's bytes in device memory while it is converted into a pack
   size_t wstage_bytes = 0;
 };
-std::mutex g_ctx_mu;
 
 int ensure(void **p, size_t *have, size_t need) {
   if (*have >= need && *p) return HXA_OK;
