@@ -28,6 +28,7 @@ constexpr int KT = 64;                        // keys per tile
 constexpr int TILE_BYTES = KT * 128 * 2;      // K tile [64 keys][128] = V^T tile [128][64 keys] = 16 KB
 constexpr int HALF_BYTES = 4 * TILE_BYTES;    // K[2] | V[2]
 constexpr int LDS_BYTES = 2 * HALF_BYTES;     // 128 KB
+constexpr int SINK_BYTES = 256;               // past the tiles: where the weight touch loads land (never read)
 constexpr float L2E = 1.4426950408889634f;
 constexpr float RESCALE_TH = 5.5f;
 
@@ -125,6 +126,27 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
           g2l16_opaque(vt + (long)d * p.ldvt + key, dst + blk * 1024);
         }
       }
+    }
+  };
+
+  // the weight touch: this workgroup's share of the 128-byte lines of [p.pf, p.pf + p.pf_bytes) (a whole number of
+  // lines, checked on the host), one line per thread in each of the first steps: a 4-byte direct-to-LDS load into
+  // the sink, so no register is written, and the next step's vmcnt(0) wait drains it
+  constexpr int NT = 2 * NWH * 64;
+  const uint8_t *pf_base;
+  uint32_t pf_share;  // bytes
+  {
+    const uint32_t lines = (uint32_t)(p.pf_bytes >> 7), nwg = gridDim.x * gridDim.y;
+    const uint32_t per = (lines + nwg - 1) / nwg, l0 = min((blockIdx.x + blockIdx.y * gridDim.x) * per, lines);
+    pf_base = p.pf + ((long)l0 << 7);
+    pf_share = (min(lines, l0 + per) - l0) << 7;
+  }
+  const int pf_chunks = (int)((pf_share >> 7) + NT - 1) / NT;
+  auto touch = [&](int c) {
+    const uint32_t off = (uint32_t)(c * NT + tid) << 7;
+    if (off < pf_share) {
+      const uint32_t la = (uint32_t)(uintptr_t)(lds_void_t *)(lds + LDS_BYTES);
+      asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(pf_base), "s"(la) : "memory", "m0");
     }
   };
 
@@ -232,6 +254,7 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
     // the next tiles' loads after the QK / exponential block, not ahead of it (their issue would delay the softmax)
     if (i + 2 < nmine) load_kv(i + 2, true, false);
     if (i + 1 < nmine) load_kv(i + 1, false, true);
+    if (i < pf_chunks) touch(i);
     half8_t va[2];
     __builtin_amdgcn_sched_barrier(0);
     va[0] = vfrag(0);
@@ -379,12 +402,16 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   if (p.ldk >= (1 << 24) || p.ldvt >= (1 << 23)) return HXA_E_ARG;
   if (((uintptr_t)p.q | (uintptr_t)p.k | (uintptr_t)p.vt) % 16 || (uintptr_t)p.o % 8) return HXA_E_ARG;
   if (p.q_bstride % 8 || p.k_bstride % 8 || p.vt_bstride % 8 || p.o_bstride % 4) return HXA_E_ARG;
+  // the weight touch: whole 128-byte lines, below 2 GB (the per-lane byte offsets are unsigned 32-bit)
+  if (p.pf_bytes < 0 || p.pf_bytes % 128 || p.pf_bytes >= (1L << 31) || (p.pf_bytes > 0 && (p.pf == nullptr || (uintptr_t)p.pf % 4)))
+    return HXA_E_ARG;
   static bool attr = false;
   static int num_cu = 0;
   if (!attr) {
-    if (hipFuncSetAttribute((const void *)attn_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES) !=
-            hipSuccess ||
-        hipFuncSetAttribute((const void *)attn_kernel<3>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES) !=
+    if (hipFuncSetAttribute((const void *)attn_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            LDS_BYTES + SINK_BYTES) != hipSuccess ||
+        hipFuncSetAttribute((const void *)attn_kernel<3>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            LDS_BYTES + SINK_BYTES) !=
             hipSuccess ||
         hipFuncSetAttribute((const void *)attn_short_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, SK_LDS) !=
             hipSuccess)
@@ -414,7 +441,7 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   const bool small = fill(96) > fill(128) + 1e-9;
   const int QB = small ? 96 : 128, nqb = (p.T + QB - 1) / QB;
   dim3 grid(nqb * p.H, p.batch);
-  if (small) hxa_launch(attn_kernel<3>, grid, dim3(384), LDS_BYTES, st, pk, nqb);
-  else hxa_launch(attn_kernel<4>, grid, dim3(512), LDS_BYTES, st, pk, nqb);
+  if (small) hxa_launch(attn_kernel<3>, grid, dim3(384), LDS_BYTES + SINK_BYTES, st, pk, nqb);
+  else hxa_launch(attn_kernel<4>, grid, dim3(512), LDS_BYTES + SINK_BYTES, st, pk, nqb);
   return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
 }

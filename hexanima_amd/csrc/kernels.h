@@ -73,6 +73,11 @@ struct HxaAttn {
   int T, NKV, nvalid, H, batch;
   long q_bstride, k_bstride, vt_bstride, o_bstride;  // per-image offsets (elements)
   HxaClk clk;  // shader-clock record: set by hxa_attn_launch from the current one (callers leave it empty)
+  // [pf, pf + pf_bytes): memory the kernels after this one read (the next projections' weights), touched once per
+  // 128-byte line while the key tiles run, so that it is in L2 / MALL when they start (attn_kernel only; pf_bytes a
+  // multiple of 128)
+  const uint8_t *pf = nullptr;
+  long pf_bytes = 0;
 };
 int hxa_attn_launch(const HxaAttn &p, hipStream_t st);
 

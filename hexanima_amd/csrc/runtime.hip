@@ -774,9 +774,16 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     if (r != HXA_OK) return fail(r, "block gemm N=%d K=%d epi=%d rejected", w.N, w.K, epi);
     return HXA_OK;
   };
+  // [apf0, apf1): the pack bytes of the projections after the next attention launch, which the attention kernel
+  // touches into L2 / MALL while it runs (the pack holds its matrices in order, 256-byte aligned, so the range from
+  // the attention-output weights to a later matrix covers all between). Applies to one launch.
+  const uint8_t *apf0 = nullptr, *apf1 = nullptr;
   auto attn = [&](const hxa_h *q, const hxa_h *kk, long ldk, const hxa_h *vt, long ldvt, int NKV, int nvalid, long kb,
                   long vb) -> int {
     HxaAttn p{q, kk, vt, ldqk, ldk, ldvt, o, ldo, T, NKV, nvalid, H, B, (long)T * ldqk, kb, vb, (long)T * ldo};
+    p.pf = apf0;
+    p.pf_bytes = apf0 != nullptr && apf1 > apf0 ? apf1 - apf0 : 0;
+    apf0 = apf1 = nullptr;  // one launch
     const int r = hxa_attn_launch(p, st);
     if (r != HXA_OK) return fail(r, "block attention rejected");
     return HXA_OK;
@@ -899,6 +906,13 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     if (!fuse) TRY(hxa_rmsrope_launch(qk, k, gain, gain + 128, ldqk, BT, H, cosT, sinT, T, st));
     STAGE_DONE();
+    // fp16 packs: the self attention touches the o, cross-q, text k / v and cross-o weights (2B DiT step 8.47 ->
+    // 8.41 ms); with int8 / int4 weights, or with the MLP-up weights in the range as well, it measured neutral to
+    // 1% slower
+    if ((Wo.fmt & ~HXA_W_KTILED) == HXA_W_F16) {
+      apf0 = (const uint8_t *)Wo.w;
+      apf1 = (const uint8_t *)W1.w;
+    }
     TRY(attn(qk, k, ldqk, vT, BT, T, T, (long)T * ldqk, T));
     STAGE_DONE();
     // gated residual x += gate * f16(o Wo) (blk.c:162): without a stage dump it is applied by the next site's LN
