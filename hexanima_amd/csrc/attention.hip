@@ -130,23 +130,26 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   };
 
   // the weight touch: this workgroup's share of the 128-byte lines of [p.pf, p.pf + p.pf_bytes) (a whole number of
-  // lines, checked on the host), one line per thread in each of the first steps: a 4-byte direct-to-LDS load into
-  // the sink, so no register is written, and the next step's vmcnt(0) wait drains it
+  // lines, checked on the host), spread evenly over the steps but the last, so that the touch's HBM reads stay a
+  // small fraction of the bandwidth; each line a 4-byte direct-to-LDS load into the sink (no register is written;
+  // the next step's vmcnt(0) wait drains it)
   constexpr int NT = 2 * NWH * 64;
   const uint8_t *pf_base;
-  uint32_t pf_share;  // bytes
+  uint32_t pf_lines;  // of this workgroup
   {
     const uint32_t lines = (uint32_t)(p.pf_bytes >> 7), nwg = gridDim.x * gridDim.y;
     const uint32_t per = (lines + nwg - 1) / nwg, l0 = min((blockIdx.x + blockIdx.y * gridDim.x) * per, lines);
     pf_base = p.pf + ((long)l0 << 7);
-    pf_share = (min(lines, l0 + per) - l0) << 7;
+    pf_lines = min(lines, l0 + per) - l0;
   }
-  const int pf_chunks = (int)((pf_share >> 7) + NT - 1) / NT;
-  auto touch = [&](int c) {
-    const uint32_t off = (uint32_t)(c * NT + tid) << 7;
-    if (off < pf_share) {
+  const int pf_steps = max(nh - 1, 1);
+  const uint32_t pf_per_step = (pf_lines + pf_steps - 1) / pf_steps;
+  auto touch = [&](int i) {  // one line per thread and step at most (lines past NT a step are left untouched)
+    const uint32_t line = i * pf_per_step + tid;
+    if (tid < pf_per_step && line < pf_lines) {
       const uint32_t la = (uint32_t)(uintptr_t)(lds_void_t *)(lds + LDS_BYTES);
-      asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(pf_base), "s"(la) : "memory", "m0");
+      asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(line << 7), "s"(pf_base), "s"(la)
+                   : "memory", "m0");
     }
   };
 
@@ -254,7 +257,7 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
     // the next tiles' loads after the QK / exponential block, not ahead of it (their issue would delay the softmax)
     if (i + 2 < nmine) load_kv(i + 2, true, false);
     if (i + 1 < nmine) load_kv(i + 1, false, true);
-    if (i < pf_chunks) touch(i);
+    if (i < pf_steps) touch(i);
     half8_t va[2];
     __builtin_amdgcn_sched_barrier(0);
     va[0] = vfrag(0);

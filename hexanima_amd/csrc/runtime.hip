@@ -906,10 +906,10 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     STAGE_DONE();
     if (!fuse) TRY(hxa_rmsrope_launch(qk, k, gain, gain + 128, ldqk, BT, H, cosT, sinT, T, st));
     STAGE_DONE();
-    // fp16 packs: the self attention touches the o, cross-q, text k / v and cross-o weights (2B DiT step 8.47 ->
-    // 8.41 ms); with int8 / int4 weights, or with the MLP-up weights in the range as well, it measured neutral to
-    // 1% slower
-    if ((Wo.fmt & ~HXA_W_KTILED) == HXA_W_F16) {
+    // fp16 packs below 4096 rows: the self attention touches the o, cross-q, text k / v and cross-o weights (2B DiT
+    // step 8.78 -> 8.69 ms). With int8 / int4 weights, with the MLP-up weights in the range as well, or at 6144 rows
+    // (batch 4, where the projections run several rounds of workgroups) it measured neutral to 1% slower.
+    if ((Wo.fmt & ~HXA_W_KTILED) == HXA_W_F16 && BT < 4096) {
       apf0 = (const uint8_t *)Wo.w;
       apf1 = (const uint8_t *)W1.w;
     }
