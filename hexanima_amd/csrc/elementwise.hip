@@ -330,13 +330,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float *__restrict__ x, 
 // embedding vector). Row n of W [N][K] gives y[(n / per) * ostride + r + (r >= split ? gap : 0)], r = n % per, with
 // y = sum_k act(x[k]) W[n][k]. act(x) is applied once per lane when x is loaded (1: SiLU). K = KC chunks of 64*EPL;
 // each lane keeps its EPL*KC inputs in registers (k = c*64*EPL + EPL*lane + e); a wave streams RPW rows with
-// EPL*2-byte weight loads, two rows in flight.
+// EPL*2-byte non-temporal weight loads, two rows in flight.
 template <int KC, int EPL>
 __global__ __launch_bounds__(256) void modgemv_kernel(const float *__restrict__ x, const hxa_h *__restrict__ W, long N,
                                                       float *__restrict__ y, int per, long ostride, int split, int gap,
                                                       int act, int rpw) {
   constexpr int CH = 64 * EPL, K = KC * CH;
   using wvec = std::conditional_t<EPL == 8, half8_t, half4_t>;
+  // the weights are read once per call: non-temporal loads (modulation of 28 2B blocks, 1.41 GB: 249 -> 212 us)
+  auto wload = [](const hxa_h *p) -> wvec { return __builtin_nontemporal_load((const wvec *)p); };
   const int lane = threadIdx.x & 63;
   const long row0 = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw;
   float xr[KC][EPL];
@@ -354,10 +356,10 @@ __global__ __launch_bounds__(256) void modgemv_kernel(const float *__restrict__ 
     const bool two = n0 + 1 < N && i + 1 < rpw;
     wvec w0[KC], w1[KC];
 #pragma unroll
-    for (int c = 0; c < KC; c++) w0[c] = *(const wvec *)(W + n0 * K + c * CH + lane * EPL);
+    for (int c = 0; c < KC; c++) w0[c] = wload(W + n0 * K + c * CH + lane * EPL);
     if (two) {
 #pragma unroll
-      for (int c = 0; c < KC; c++) w1[c] = *(const wvec *)(W + (n0 + 1) * K + c * CH + lane * EPL);
+      for (int c = 0; c < KC; c++) w1[c] = wload(W + (n0 + 1) * K + c * CH + lane * EPL);
     }
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
