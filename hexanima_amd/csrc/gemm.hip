@@ -1605,7 +1605,7 @@ int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st) {
 // ---- int8 / int4 weights -> fp16, k-tiled [K/32][N][32] (the layout the fp16 kernels read) ----
 // One 8-k slot of one row per thread (the 16-byte fragment unit of the main loops), dequantised with their own
 // dq8_word / dq4_word, so the values are the same f16(q * s) (+ z) bits the fused path feeds its MFMAs. Reads
-// w.w / w.s / w.z once, writes 2 N K bytes.
+// w.w / w.s / w.z once (the weights with non-temporal loads), writes 2 N K bytes.
 namespace {
 template <int FMT, bool ASYM>
 __global__ __launch_bounds__(256) void dequant_kernel(GemmParams p, hxa_h *out) {
@@ -1621,11 +1621,11 @@ __global__ __launch_bounds__(256) void dequant_kernel(GemmParams p, hxa_h *out) 
   const uint8_t *src = (const uint8_t *)p.W + n * p.w_rs + g * p.w_gs;
   uint32_t o[4];
   if constexpr (FMT == HXA_W_Q8) {
-    const uint2_t v = *(const uint2_t *)(src + 8 * c);
+    const uint2_t v = __builtin_nontemporal_load((const uint2_t *)(src + 8 * c));
     dq8_word(v.x, s2, o[0], o[1]);
     dq8_word(v.y, s2, o[2], o[3]);
   } else {
-    dq4_word<ASYM>(*(const uint32_t *)(src + 4 * c), s2, z2, o);
+    dq4_word<ASYM>(__builtin_nontemporal_load((const uint32_t *)(src + 4 * c)), s2, z2, o);
   }
   // lanes write consecutive 16-byte chunks: 1 KB per wave store
   *(uint4_t *)(out + i * 32 + c * 8) = (uint4_t){o[0], o[1], o[2], o[3]};
