@@ -25,9 +25,10 @@ HXA_DEV float wave_sum(float v) {
 // ---------------------------------------------------------------------------------------------------------------
 // modulated norm (kern.c:31-65 LN-mod; moss kern.c:345-375 RMS-mod)
 // ---------------------------------------------------------------------------------------------------------------
-// With t != NULL the pending gated residual of the previous site is applied first, x += gate * t (kern.c:320-328,
-// the same fma as the GEMM residual epilogue), or with t2 as well x += gate * (t + t2) (kern.c:330-339, the same
-// fma as resadd2_kernel); x is written back, and the norm is taken of the updated row.
+// With NP > 0 pending fp16 partials t_j = t + j tz the gated residual of the previous site is applied first:
+// x += gate * t (NP 1, kern.c:320-328, the same fma as the GEMM residual epilogue), x += gate * (t0 + t1) (NP 2,
+// kern.c:330-339) or x += gate * ((t0 + t1) + (t2 + t3)) (NP 4, the K-quarter partials), the same sums as
+// resaddn_kernel; x is written back, and the norm is taken of the updated row.
 // A 256-thread workgroup per group of rows (row = blockIdx.x + j gridDim.x; a float4 of every 1024 columns per
 // thread). The column vectors (gate, 1 + scale [* w], shift) are read once per workgroup, and the next row's x and
 // pending terms are loaded while the current row is reduced and stored, so loads and stores of the grid overlap.
