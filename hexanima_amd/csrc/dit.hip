@@ -42,6 +42,7 @@ struct Dit {
   hxa_h *glue = nullptr;      // x_embed [D][4C] | t_embed [D][temb] | final_mod [2D][D] | final_lin [4C][D] | text_proj
   long glue_elems = 0;
   hxa_h *Wemb = nullptr, *L1 = nullptr, *Lf = nullptr, *Wfin = nullptr, *Wtxt = nullptr;
+  hxa_h *Wfin4 = nullptr;  // Wfin k-tiled by 4 ([D/4][4C][4]), what the final layer's kernel reads
   float *lat = nullptr, *vel = nullptr, *tok = nullptr, *x = nullptr, *sinus = nullptr, *cvec = nullptr;
   float *mods = nullptr, *fmod = nullptr, *sig = nullptr, *cosT = nullptr, *sinT = nullptr, *ones = nullptr;
   hxa_h *ctx16 = nullptr;  // Anima: [B*C][DC]; MOSS: text [B*ntxt][ntxt_in]
@@ -309,10 +310,10 @@ int record_step(Dit &d, const Pass &ps) {
   }
   // final layer (+ Euler update); rapid-moss: RMS head and x0 = z - v
   if (moss_ref)
-    DTRY(hxa_final_launch(d.x, B, ps.Timg, ps.Ttot, D, d.fmod, d.fmod + D, d.Wfin, d.cfg.lat_c, ps.lat_h, ps.lat_w,
+    DTRY(hxa_final_launch(d.x, B, ps.Timg, ps.Ttot, D, d.fmod, d.fmod + D, d.Wfin4, d.cfg.lat_c, ps.lat_h, ps.lat_w,
                           d.vel, nullptr, st, d.nfin, ps.x0rows, ps.zrows));
   else
-    DTRY(hxa_final_launch(d.x, B, ps.Timg, ps.Ttot, D, d.fmod, d.fmod + D, d.Wfin, d.cfg.lat_c, ps.lat_h, ps.lat_w,
+    DTRY(hxa_final_launch(d.x, B, ps.Timg, ps.Ttot, D, d.fmod, d.fmod + D, d.Wfin4, d.cfg.lat_c, ps.lat_h, ps.lat_w,
                           ps.lat_out, ps.dtp, st));
   return HXA_OK;
 }
@@ -415,6 +416,7 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   else
     d.glue_elems = (long)D * C4 + (long)D * 256 + (long)D * D + 2L * D * D + (long)C4 * D + (long)D * cfg->ntxt_in;
   M((void **)&d.glue, 2 * d.glue_elems);
+  M((void **)&d.Wfin4, 2L * C4 * D);
   if (d.form == 1) {
     d.vec_elems = b.kind == 0 ? 0 : 3L * D + 6L * D + 2L * D + D + (long)C4 * C4 + 2L * C4;
     if (d.vec_elems) M((void **)&d.vec, 4 * d.vec_elems);
@@ -496,6 +498,7 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
     if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.bnm, 0, C4, vs + 2, 0.0f, 0.1f, d.st);
     if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.bnv, 0, C4, vs + 3, 1.0f, 0.1f, d.st);
   }
+  if (rc == HXA_OK) rc = hxa_ktile4_launch(d.Wfin, C4, D, d.Wfin4, d.st);
   if (rc == HXA_OK) rc = hxa_fill_const_launch(d.ones, 0, D, 1.0f, d.st);
   if (rc == HXA_OK && b.kind == 0) {  // site-1 rows of every block: shift 0, scale 0, gate 1
     for (int k = 0; k < cfg->nblocks && rc == HXA_OK; k++) {
@@ -573,7 +576,7 @@ extern "C" int hxa_dit_destroy(void *p) {
   if (d->modw_all) (void)hipFree(d->modw_all);
   void *bufs[] = {d->glue, d->lat, d->vel, d->tok, d->x, d->sinus, d->cvec, d->mods, d->fmod, d->sig, d->cosT, d->sinT,
                   d->ones, d->ctx16, d->ws, d->vec, d->emb, d->a1, d->lora, d->h1, d->zrows, d->x0rows, d->tkv,
-                  d->tkv_par};
+                  d->tkv_par, d->Wfin4};
   for (void *q : bufs) if (q) (void)hipFree(q);
   if (d->sig_ev) (void)hipEventDestroy(d->sig_ev);
   if (d->sig_host) (void)hipHostFree(d->sig_host);

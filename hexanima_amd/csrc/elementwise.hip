@@ -382,35 +382,48 @@ __global__ __launch_bounds__(256) void modgemv_kernel(const float *__restrict__ 
   }
 }
 
-// x[m][n] = sum_k tok[m][k] * W[n][k], small K (patch embed: 4 x latent channels), in k chunks of 64. A 64-row x 64-col tile per workgroup; tok rows and
-// the weight tile are staged in LDS as fp32.
+// x[m][n] = sum_k tok[m][k] * W[n][k], small K (patch embed: 4 x latent channels; K % 4 == 0): a 64-row x 64-col
+// tile per workgroup, 4 x 4 outputs per thread. K is staged in chunks of 64 in LDS as fp32 rows of float4 (one
+// float4 of x and one half4 of W per load), and read back as float4 along k; every output accumulates its products
+// in ascending k (one fma chain).
 __global__ __launch_bounds__(256) void linear_smallk_kernel(const float *__restrict__ x, long ldx, int M, int K,
                                                             const hxa_h *__restrict__ W, int N, float *__restrict__ y,
                                                             long ldy) {
-  __shared__ float xs[64][65];
-  __shared__ float ws[64][65];
+  __shared__ float4_t xs[64][17];  // [row][k / 4], one float4 of padding per row
+  __shared__ float4_t ws[64][17];
   const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64, tid = threadIdx.x;
-  const int tr = tid / 16, tc = tid % 16;  // 4x4 outputs per thread
+  const int tr = tid / 16, tc = tid % 16;  // rows tr*4 + i, columns tc + 16 j
   float acc[4][4] = {};
-  for (int k0 = 0; k0 < K; k0 += 64) {  // k chunks of 64, accumulated in k order
-    const int kc = min(64, K - k0);
+  for (int k0 = 0; k0 < K; k0 += 64) {
+    const int kc4 = min(64, K - k0) / 4;
     __syncthreads();
-    for (int i = tid; i < 64 * kc; i += 256) {
-      const int r = i / kc, k = i % kc;
-      xs[r][k] = m0 + r < M ? x[(long)(m0 + r) * ldx + k0 + k] : 0.0f;
-      ws[r][k] = n0 + r < N ? (float)W[(long)(n0 + r) * K + k0 + k] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int i = tid + 256 * u, r = i >> 4, k4 = i & 15;
+      float4_t xv = {0.0f, 0.0f, 0.0f, 0.0f}, wv = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (k4 < kc4) {
+        if (m0 + r < M) xv = *(const float4_t *)(x + (long)(m0 + r) * ldx + k0 + 4 * k4);
+        if (n0 + r < N) {
+          const half4_t h = *(const half4_t *)(W + (long)(n0 + r) * K + k0 + 4 * k4);
+          wv = (float4_t){(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+        }
+      }
+      xs[r][k4] = xv;
+      ws[r][k4] = wv;
     }
     __syncthreads();
-    for (int k = 0; k < kc; k++) {
-      float a[4], b[4];
+    for (int k4 = 0; k4 < kc4; k4++) {
+      float4_t a[4], b[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) a[i] = xs[tr * 4 + i][k];
+      for (int i = 0; i < 4; i++) a[i] = xs[tr * 4 + i][k4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) b[j] = ws[tc + 16 * j][k];
+      for (int j = 0; j < 4; j++) b[j] = ws[tc + 16 * j][k4];
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc[i][j] = fmaf(a[i][e], b[j][e], acc[i][j]);
     }
   }
 #pragma unroll
@@ -437,102 +450,158 @@ __global__ void sinusoid_kernel(const float *t, int n, int dim, float *out) {
 // unpatchify (ph, pw, c) into lat; when dt != 0 the Euler update lat += dt * v is applied instead of storing v.
 // With normw the norm is the MOSS head's RMSNorm * normw (mossrun.cpp:331-332), and with x0rows the 4C outputs v of
 // token t go to x0rows[t][o] = zrows[t][o] - v, the rapid-moss estimate x0 = z - v (mossrun.cpp:333-334).
-// FT tokens per workgroup: each wave normalises FT/4 tokens into LDS, then thread (output o, part) accumulates its
-// quarter-interleaved share of the D products for all FT tokens (the weights are read once per workgroup), and the
-// `per` parts of an output (adjacent lanes) are summed with DPP.
-constexpr int FT = 8;
-__global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ x, int T, int xrows, int D,
-                                                    const float *__restrict__ shift, const float *__restrict__ scale,
-                                                    const hxa_h *__restrict__ Wf, int Cc, int H, int W, float *lat,
-                                                    const float *__restrict__ dtp, int ntok, const float *__restrict__ normw,
-                                                    float *__restrict__ x0rows, const float *__restrict__ zrows) {
-  extern __shared__ float xn[];  // [FT][D]
+// FT = 16 tokens per workgroup of NW waves (16; 8 for 256 outputs):
+// (1) statistics: wave w takes tokens w, w + NW (all its rows in flight together) and leaves (mu, 1/sigma) in LDS;
+// (2) the linear: wave w takes the k range [w D/NW, (w+1) D/NW). Per 16-deep k step each lane normalises its 4
+//     values of the A fragment (token lane % 16, k 4 (lane / 16) .. +3; the same fp32 expression as the
+//     reference's normalised row), splits each into f16 hi = f16(a) and lo = f16(a - hi) (22 significant bits
+//     together), and v_mfma_f32_16x16x16_f16 multiplies both by the f16 weights for the NOB = 4C / 16 output blocks
+//     (the products are exact, the sums fp32). The weights come k-tiled by 4, Wf4 [D/4][4C][4], so a step reads one
+//     contiguous block; row-major weights (64 rows 4 KB apart per step) made this phase 1.7x slower;
+// (3) the NW partial sums of each output meet in LDS and are added in wave order; each thread then finishes its
+//     outputs, reading every value it updates before it writes any.
+// One wave per SIMD (96 workgroups of 4 waves at 1536 tokens) left every load and MFMA latency exposed (45 us);
+// the 16-wave workgroup overlaps them.
+constexpr int FT = 16;
+template <int NOB, int NW>
+__global__ __launch_bounds__(64 * NW) void final_kernel(const float *__restrict__ x, int T, int xrows, int D,
+                                                        const float *__restrict__ shift, const float *__restrict__ scale,
+                                                        const hxa_h *__restrict__ Wf4, int Cc, int H, int W, float *lat,
+                                                        const float *__restrict__ dtp, int ntok,
+                                                        const float *__restrict__ normw, float *__restrict__ x0rows,
+                                                        const float *__restrict__ zrows) {
+  constexpr int NO = 16 * NOB, NT = 64 * NW;
+  extern __shared__ float fsh[];  // [NW][FT][NO] partial sums, then [FT][2] statistics
+  float *stat = fsh + NW * FT * NO;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tok0 = blockIdx.x * FT;
-  for (int u = 0; u < FT / 4; u++) {
-    const int tl = wave * (FT / 4) + u, tok = tok0 + tl;
-    float *dst = xn + tl * D;
-    if (tok >= ntok) {
-      for (int c = lane; c < D; c += 64) dst[c] = 0.0f;
-      continue;
-    }
-    const int b = tok / T, tk = tok % T;
-    const float4_t *xr = (const float4_t *)(x + ((long)b * xrows + tk) * D);
-    const int nv = D / 256;  // float4 per lane (D % 256 == 0, D <= 4096)
-    float4_t v[16];
+  const int nv = D / 256;  // float4 per lane of a row (D % 256 == 0, D <= 4096)
+  {
+    constexpr int R = FT / NW;  // rows per wave: 1 or 2
+    float4_t v[R][16];
 #pragma unroll
-    for (int i = 0; i < 16; i++)
-      if (i < nv) v[i] = xr[lane + 64 * i];
-    float s = 0.0f;
-    if (normw == nullptr) {
+    for (int r = 0; r < R; r++) {
+      const int tok = min(tok0 + wave + NW * r, ntok - 1);
+      const float4_t *xr = (const float4_t *)(x + ((long)(tok / T) * xrows + tok % T) * D);
 #pragma unroll
       for (int i = 0; i < 16; i++)
-        if (i < nv) s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+        if (i < nv) v[r][i] = xr[lane + 64 * i];
     }
-    const float mu = normw == nullptr ? wave_sum(s) / (float)D : 0.0f;  // RMS: no centring
-    float q = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; i++)
-      if (i < nv) {
+    for (int r = 0; r < R; r++) {
+      float s = 0.0f;
+      if (normw == nullptr) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const float d = v[i][e] - mu;
-          q = fmaf(d, d, q);
+        for (int i = 0; i < 16; i++)
+          if (i < nv) s += (v[r][i][0] + v[r][i][1]) + (v[r][i][2] + v[r][i][3]);
+      }
+      const float mu = normw == nullptr ? wave_sum(s) / (float)D : 0.0f;  // RMS: no centring
+      float q = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; i++)
+        if (i < nv) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const float d = v[r][i][e] - mu;
+            q = fmaf(d, d, q);
+          }
         }
+      const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-6f);
+      if (lane == 0) {
+        stat[2 * (wave + NW * r)] = mu;
+        stat[2 * (wave + NW * r) + 1] = rs;
       }
-    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-6f);
-#pragma unroll
-    for (int i = 0; i < 16; i++)
-      if (i < nv) {
-        const int c = (lane + 64 * i) * 4;
-        const float4_t sc = *(const float4_t *)(scale + c), sh = *(const float4_t *)(shift + c);
-        float4_t nw = {1.0f, 1.0f, 1.0f, 1.0f};
-        if (normw != nullptr) nw = *(const float4_t *)(normw + c);
-        float4_t o;
-#pragma unroll
-        for (int e = 0; e < 4; e++) o[e] = (v[i][e] - mu) * rs * nw[e] * (1.0f + sc[e]) + sh[e];
-        *(float4_t *)(dst + c) = o;
-      }
+    }
   }
   __syncthreads();
-  const int NO = 4 * Cc, per = 256 / NO;
-  const int o = tid / per, part = tid % per;
-  float acc[FT];
+  const int row = lane & 15, kk = 4 * (lane >> 4);
+  const int tok = tok0 + row;
+  const bool ok = tok < ntok;
+  const float mu = stat[2 * row], rs = stat[2 * row + 1];
+  const float *xr = x + ((long)(min(tok, ntok - 1) / T) * xrows + min(tok, ntok - 1) % T) * D;
+  float4_t acc[NOB];
 #pragma unroll
-  for (int t = 0; t < FT; t++) acc[t] = 0.0f;
-  const hxa_h *wr = Wf + (long)o * D;
-  for (int c0 = 4 * part; c0 < D; c0 += 32 * per) {  // 8 weight loads in flight per round (D % 128 == 0)
-    half4_t w4[8];
+  for (int b = 0; b < NOB; b++) acc[b] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+  // U k steps per round, their loads issued before the first use. The range D / NW is a multiple of 16 but not
+  // always of 16 U (D 2560: 10 steps): past its end a round reloads the range's last step and skips its MFMAs.
+  constexpr int U = NOB == 16 ? 1 : 2;
+  const int kw = D / NW, kend = (wave + 1) * kw;
+  for (int k0 = wave * kw; k0 < kend; k0 += 16 * U) {
+    float4_t xv[U], sc[U], sh[U], nw[U];
+    half4_t wv[U][NOB];
 #pragma unroll
-    for (int u = 0; u < 8; u++) w4[u] = *(const half4_t *)(wr + c0 + u * 4 * per);
+    for (int u = 0; u < U; u++) {
+      const int c = min(k0 + 16 * u, kend - 16) + kk;
+      xv[u] = *(const float4_t *)(xr + c);
+      sc[u] = *(const float4_t *)(scale + c);
+      sh[u] = *(const float4_t *)(shift + c);
+      nw[u] = normw != nullptr ? *(const float4_t *)(normw + c) : (float4_t){1.0f, 1.0f, 1.0f, 1.0f};
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const int c = c0 + u * 4 * per;
-      const float w0 = (float)w4[u][0], w1 = (float)w4[u][1], w2 = (float)w4[u][2], w3 = (float)w4[u][3];
+      for (int b = 0; b < NOB; b++) wv[u][b] = *(const half4_t *)(Wf4 + ((long)(c >> 2) * NO + 16 * b + row) * 4);
+    }
 #pragma unroll
-      for (int t = 0; t < FT; t++) {
-        const float4_t v = *(const float4_t *)(xn + t * D + c);
-        acc[t] = fmaf(v[0], w0, fmaf(v[1], w1, fmaf(v[2], w2, fmaf(v[3], w3, acc[t]))));
+    for (int u = 0; u < U; u++) {
+      if (k0 + 16 * u >= kend) break;
+      half4_t hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float a = ok ? (xv[u][e] - mu) * rs * nw[u][e] * (1.0f + sc[u][e]) + sh[u][e] : 0.0f;
+        hi[e] = (hxa_h)a;
+        lo[e] = (hxa_h)(a - (float)hi[e]);
+      }
+#pragma unroll
+      for (int b = 0; b < NOB; b++) {
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(hi, wv[u][b], acc[b], 0, 0, 0);
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(lo, wv[u][b], acc[b], 0, 0, 0);
       }
     }
   }
-  const int gw = W / 2;
+  // lane holds tokens 4 (lane / 16) + i, output 16 b + lane % 16
 #pragma unroll
-  for (int t = 0; t < FT; t++) {
-    float v = acc[t];
-    if (per >= 2) v += dpp_f<0xB1>(v);  // lanes i^1
-    if (per >= 4) v += dpp_f<0x4E>(v);  // lanes i^2
-    const int tok = tok0 + t;
-    if (part == 0 && tok < ntok && x0rows != nullptr) {
-      x0rows[(long)tok * NO + o] = zrows[(long)tok * NO + o] - v;
-    } else if (part == 0 && tok < ntok) {
-      const int b = tok / T, tk = tok % T, gy = tk / gw, gx = tk % gw;
+  for (int b = 0; b < NOB; b++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) fsh[(wave * FT + 4 * (lane >> 4) + i) * NO + 16 * b + row] = acc[b][i];
+  __syncthreads();
+  constexpr int PER = FT * NO / NT;  // outputs per thread
+  const float dt = dtp != nullptr ? *dtp : 0.0f;
+  const int gw = W / 2;
+  float val[PER], cur[PER];
+  float *dst[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int idx = tid + NT * j, t = idx / NO, o = idx % NO, tk0 = tok0 + t;
+    const float *ps = fsh + t * NO + o;
+    float sum = ps[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) sum += ps[w * FT * NO];
+    val[j] = sum;
+    dst[j] = nullptr;
+    cur[j] = 0.0f;
+    if (tk0 >= ntok) continue;
+    if (x0rows != nullptr) {
+      dst[j] = x0rows + (long)tk0 * NO + o;
+      cur[j] = zrows[(long)tk0 * NO + o];
+    } else {
+      const int bi = tk0 / T, tk = tk0 % T, gy = tk / gw, gx = tk % gw;
       const int ab = o / Cc, c = o % Cc, a = ab >> 1, bb = ab & 1;
-      float *dst = lat + (((long)b * Cc + c) * H + gy * 2 + a) * W + gx * 2 + bb;
-      if (dtp != nullptr) *dst += *dtp * v;
-      else *dst = v;
+      dst[j] = lat + (((long)bi * Cc + c) * H + gy * 2 + a) * W + gx * 2 + bb;
+      if (dtp != nullptr) cur[j] = *dst[j];
     }
   }
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    if (dst[j] == nullptr) continue;
+    if (x0rows != nullptr) *dst[j] = cur[j] - val[j];
+    else *dst[j] = dtp != nullptr ? cur[j] + dt * val[j] : val[j];
+  }
+}
+
+// W [N][K] fp16 -> Wk [K/4][N][4] (k-tiled by 4: the final layer's weight layout)
+__global__ void ktile4_kernel(const hxa_h *__restrict__ W, int N, int K, hxa_h *__restrict__ Wk) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;  // one 4-k chunk of one row
+  if (i >= (long)N * (K / 4)) return;
+  const int n = (int)(i % N), g = (int)(i / N);
+  *(half4_t *)(Wk + i * 4) = *(const half4_t *)(W + (long)n * K + 4 * g);
 }
 
 // q8 / q4 quantisation of W[N][K] fp32, one thread per (column n, 32-group g): amax of the fp16-rounded weights,
@@ -707,6 +776,7 @@ int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W
                        split > 0 ? split : N, gap);
   } else {
     if (act != 0 || bias != nullptr || split > 0) return HXA_E_ARG;
+    if (K % 4 || ldx % 4 || (uintptr_t)x % 16 || (uintptr_t)W % 8) return HXA_E_ARG;  // float4 / half4 staging
     hxa_launch(linear_smallk_kernel, dim3(nblk(N, 64), nblk(M, 64)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy);
   }
   return LAUNCH_OK();
@@ -746,24 +816,44 @@ int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, 
 }
 
 
+int hxa_ktile4_launch(const hxa_h *W, int N, int K, hxa_h *Wk, hipStream_t st) {
+  if (N <= 0 || K <= 0 || K % 4 || (uintptr_t)W % 8 || (uintptr_t)Wk % 8) return HXA_E_ARG;
+  hxa_launch(ktile4_kernel, dim3(nblk((long)N * (K / 4))), dim3(256), 0, st, W, N, K, Wk);
+  return LAUNCH_OK();
+}
+
 int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale,
-                     const hxa_h *Wf, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st,
+                     const hxa_h *Wf4, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st,
                      const float *normw, float *x0rows, const float *zrows) {
   if ((x0rows == nullptr) != (zrows == nullptr) || (normw && (uintptr_t)normw % 16)) return HXA_E_ARG;
   const int NO = 4 * Cc;
-  if (NO > 256 || 256 % NO || 256 / NO > 4 || (H / 2) * (W / 2) != T || xrows < T || D % 256 || D > 4096)
+  if ((NO != 64 && NO != 128 && NO != 256) || (H / 2) * (W / 2) != T || xrows < T || D % 256 || D > 4096 || B * T < 1)
     return HXA_E_ARG;
-  const size_t lds = sizeof(float) * (size_t)FT * D;
-  if (lds > 160 * 1024) return HXA_E_ARG;
-  static size_t lds_set = 0;
-  if (lds > lds_set) {
-    if (hipFuncSetAttribute((const void *)final_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if ((uintptr_t)x % 16 || (uintptr_t)shift % 16 || (uintptr_t)scale % 16 || (uintptr_t)Wf4 % 8) return HXA_E_ARG;
+  // partial sums + statistics: 16 x 16 x 64, 16 x 16 x 128 or 8 x 16 x 256 floats (64 / 128 / 128 KB)
+  auto bytes = [](int nw, int no) { return (int)sizeof(float) * (nw * FT * no + 2 * FT); };
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute((const void *)final_kernel<4, 16>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            bytes(16, 64)) != hipSuccess ||
+        hipFuncSetAttribute((const void *)final_kernel<8, 16>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            bytes(16, 128)) != hipSuccess ||
+        hipFuncSetAttribute((const void *)final_kernel<16, 8>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            bytes(8, 256)) != hipSuccess)
       return HXA_E_HIP;
-    lds_set = lds;
+    attr = true;
   }
   const int ntok = B * T;
-  hxa_launch(final_kernel, dim3((ntok + FT - 1) / FT), dim3(256), lds, st, x, T, xrows, D, shift, scale, Wf, Cc,
-                     H, W, lat, dtp, ntok, normw, x0rows, zrows);
+  const dim3 grid((ntok + FT - 1) / FT);
+  if (NO == 64)
+    hxa_launch(final_kernel<4, 16>, grid, dim3(1024), bytes(16, 64), st, x, T, xrows, D, shift, scale, Wf4, Cc, H, W,
+               lat, dtp, ntok, normw, x0rows, zrows);
+  else if (NO == 128)
+    hxa_launch(final_kernel<8, 16>, grid, dim3(1024), bytes(16, 128), st, x, T, xrows, D, shift, scale, Wf4, Cc, H, W,
+               lat, dtp, ntok, normw, x0rows, zrows);
+  else
+    hxa_launch(final_kernel<16, 8>, grid, dim3(512), bytes(8, 256), st, x, T, xrows, D, shift, scale, Wf4, Cc, H, W,
+               lat, dtp, ntok, normw, x0rows, zrows);
   return LAUNCH_OK();
 }
 

@@ -129,12 +129,14 @@ int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, 
 int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W, int N, float *y, long ldy, int act,
                           const float *bias, int split, int gap, hipStream_t st);
 // final layer over B images of T image tokens (image b's rows start at b*xrows); dtp == NULL: lat = v,
-// else lat += (*dtp) * v (Euler step)
+// else lat += (*dtp) * v (Euler step). Wf4: the [4 Cc][D] weights k-tiled by 4, [D/4][4 Cc][4] (hxa_ktile4_launch).
 // normw != NULL: RMSNorm * normw instead of LN (the MOSS head); x0rows / zrows != NULL: write the token rows
 // x0rows[t][o] = zrows[t][o] - v (rapid-moss) instead of the latent
 int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale,
-                     const hxa_h *Wf, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st,
+                     const hxa_h *Wf4, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st,
                      const float *normw = nullptr, float *x0rows = nullptr, const float *zrows = nullptr);
+// W [N][K] fp16 -> Wk [K/4][N][4]
+int hxa_ktile4_launch(const hxa_h *W, int N, int K, hxa_h *Wk, hipStream_t st);
 // the reference's own DiT glue: vector RMSNorm * w (fp16 w), G GEMVs with their own inputs, the rapid-moss latent mix +
 // video embedding, and BN denorm + unpatchify of the x0 token rows
 int hxa_rmsvec_launch(const float *x, int n, const hxa_h *w, float eps, float *y, hipStream_t st);
