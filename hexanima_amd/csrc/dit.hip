@@ -1,7 +1,8 @@
 // DiT runner: the layer directly above the block boundary. It owns every weight of a synthetic DiT in HBM
 // (GPU block packs + glue), and runs one flow-matching Euler step entirely on the device:
 //   timestep sinusoid -> t-embedding -> per-block adaLN modulation (megarun.cpp:156-171 role; animad.cpp:424-431)
-//   patchify + x_embedder (animad.cpp:447-452) [MOSS: + text projection, joint token layout]
+//   patch embed (animad.cpp:447-452: patchify read straight from the latent by the x_embedder) [MOSS: + text
+//   projection, joint token layout]
 //   blocks 0..n-1 (hxa_block_run)
 //   final adaLN + linear + unpatchify (animad.cpp:474-492) fused with the Euler update x += (s' - s) v
 // A step is captured once into a HIP graph and replayed; sigma values are read from device memory so one graph
@@ -43,7 +44,7 @@ struct Dit {
   long glue_elems = 0;
   hxa_h *Wemb = nullptr, *L1 = nullptr, *Lf = nullptr, *Wfin = nullptr, *Wtxt = nullptr;
   hxa_h *Wfin4 = nullptr;  // Wfin k-tiled by 4 ([D/4][4C][4]), what the final layer's kernel reads
-  float *lat = nullptr, *vel = nullptr, *tok = nullptr, *x = nullptr, *sinus = nullptr, *cvec = nullptr;
+  float *lat = nullptr, *vel = nullptr, *x = nullptr, *sinus = nullptr, *cvec = nullptr;
   float *mods = nullptr, *fmod = nullptr, *sig = nullptr, *cosT = nullptr, *sinT = nullptr, *ones = nullptr;
   hxa_h *ctx16 = nullptr;  // Anima: [B*C][DC]; MOSS: text [B*ntxt][ntxt_in]
   void *ws = nullptr;
@@ -209,8 +210,7 @@ int record_prelude_anima_ref(Dit &d) {
 int record_prelude_moss_ref(Dit &d) {
   const int D = d.bd.D, temb = d.cfg.temb;
   hipStream_t st = d.st;
-  DTRY(hxa_sinusoid_launch(d.sig, 1, temb, d.sinus, st));
-  DTRY(hxa_linear_f32_launch(d.sinus, temb, 1, temb, d.L1, D, d.a1, D, 0, d.b0, 0, 0, st));
+  DTRY(hxa_linear_f32_launch(d.sig, temb, 1, temb, d.L1, D, d.a1, D, 2, d.b0, 0, 0, st));  // sinusoid in the GEMV
   DTRY(hxa_linear_f32_launch(d.a1, D, 1, D, d.T2, D, d.emb, D, 1, d.b2, 0, 0, st));
   DTRY(hxa_linear_f32_launch(d.emb, D, 1, D, d.modw_all, 6 * D, d.mods, 6 * D, 0, d.bm, 0, 0, st));
   DTRY(hxa_linear_f32_launch(d.emb, D, 1, D, d.Wh, 2 * D, d.fmod, 2 * D, 0, d.bh, 0, 0, st));
@@ -255,8 +255,7 @@ int record_step(Dit &d, const Pass &ps) {
   if (d.form == 1) DTRY(b.kind == 0 ? record_prelude_anima_ref(d) : record_prelude_moss_ref(d));
   if (d.form == 0) {
   // timestep embedding and modulation
-  DTRY(hxa_sinusoid_launch(d.sig, 1, temb, d.sinus, st));
-  DTRY(hxa_linear_f32_launch(d.sinus, temb, 1, temb, d.L1, D, d.cvec, D, 0, nullptr, 0, 0, st));
+  DTRY(hxa_linear_f32_launch(d.sig, temb, 1, temb, d.L1, D, d.cvec, D, 2, nullptr, 0, 0, st));  // sinusoid in the GEMV
   // every block's modulation in one launch over the stacked [nb][6D][D] weights: rows 0-2 -> site 0, rows 3-5 ->
   // site 2 of that block's [9][D] (site 1 keeps the identity modulation); MOSS: one shared [6D][D]
   if (b.kind == 0)
@@ -269,11 +268,8 @@ int record_step(Dit &d, const Pass &ps) {
   if (moss_ref)
     DTRY(hxa_moss_embed_launch(ps.zrows, ps.x0rows, d.Q, d.Wemb, d.bve, d.x, B, ps.Timg, ps.Ttot, D, C4, st));
   else
-    DTRY(hxa_patchify_launch(ps.lat_in, B, d.cfg.lat_c, ps.lat_h, ps.lat_w, d.tok, st));
+    DTRY(hxa_patch_embed_launch(ps.lat_in, B, d.cfg.lat_c, ps.lat_h, ps.lat_w, d.Wemb, D, d.x, ps.Ttot, st));
   for (int i = 0; i < B; i++) {
-    if (!moss_ref)
-      DTRY(hxa_linear_f32_launch(d.tok + (long)i * ps.Timg * C4, C4, ps.Timg, C4, d.Wemb, D, d.x + (long)i * ps.Ttot * D,
-                                 D, 0, nullptr, 0, 0, st));
     if (b.kind == 1) {
       float *xt = d.x + ((long)i * ps.Ttot + ps.Timg) * D;
       DTRY(hxa_fill_const_launch(xt, 0, (size_t)(ps.Ttot - ps.Timg) * D, 0.0f, st));
@@ -432,7 +428,6 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   const long latn = (long)B * cfg->lat_c * cfg->lat_h * cfg->lat_w;
   M((void **)&d.lat, 4 * latn);
   M((void **)&d.vel, 4 * latn);
-  M((void **)&d.tok, 4L * B * d.Timg * C4);
   M((void **)&d.x, 4L * B * d.Ttot * D);
   M((void **)&d.sinus, 4L * cfg->temb);
   M((void **)&d.cvec, 4L * D);
@@ -574,7 +569,7 @@ extern "C" int hxa_dit_destroy(void *p) {
   for (float *q : {d->nfull, d->dhat, d->xlow, d->vlow, d->zl, d->x0l}) if (q) (void)hipFree(q);
   for (void *q : d->packs) if (q) (void)hipFree(q);
   if (d->modw_all) (void)hipFree(d->modw_all);
-  void *bufs[] = {d->glue, d->lat, d->vel, d->tok, d->x, d->sinus, d->cvec, d->mods, d->fmod, d->sig, d->cosT, d->sinT,
+  void *bufs[] = {d->glue, d->lat, d->vel, d->x, d->sinus, d->cvec, d->mods, d->fmod, d->sig, d->cosT, d->sinT,
                   d->ones, d->ctx16, d->ws, d->vec, d->emb, d->a1, d->lora, d->h1, d->zrows, d->x0rows, d->tkv,
                   d->tkv_par, d->Wfin4};
   for (void *q : bufs) if (q) (void)hipFree(q);

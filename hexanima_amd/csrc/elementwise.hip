@@ -293,7 +293,11 @@ __global__ void patchify_kernel(const float *lat, int B, int Cc, int H, int W, f
   tok[i] = lat[(((long)b * Cc + c) * H + gy * 2 + a) * W + gx * 2 + bb];
 }
 
-// y[m][n] = act(sum_k x[m][k] * W[n][k] (+ bias[n])); act 0 none, 1 SiLU on the input (x -> x sigmoid(x)).
+// angle of frequency j of the timestep sinusoid (animad.cpp:425): t * 10000^(-j / half)
+HXA_DEV float sinusoid_angle(float t, int j, int half) { return t * expf(-logf(10000.0f) * (float)j / (float)half); }
+
+// y[m][n] = act(sum_k x[m][k] * W[n][k] (+ bias[n])); act 0 none, 1 SiLU on the input (x -> x sigmoid(x)), 2 the
+// input row is the timestep sinusoid of t = x[0] at width K (the values sinusoid_kernel stores; one row).
 // One wave per output feature n, lanes stride K (coalesced weight reads), up to 8 input rows.
 __global__ __launch_bounds__(256) void gemv_kernel(const float *__restrict__ x, long ldx, int M, int K,
                                                    const hxa_h *__restrict__ W, int N, float *__restrict__ y, long ldy,
@@ -309,7 +313,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float *__restrict__ x, 
 #pragma unroll
     for (int m = 0; m < 8; m++) {
       if (m < M) {
-        float x0 = x[(long)m * ldx + k], x1 = x[(long)m * ldx + k + 1];
+        float x0, x1;
+        if (act == 2) {  // the sinusoid of t = x[0] at width K (sinusoid_kernel's values), one row
+          const int half = K / 2, j0 = k < half ? k : k - half;  // k even, half even: k and k + 1 on one side
+          const float a0 = sinusoid_angle(x[0], j0, half), a1 = sinusoid_angle(x[0], j0 + 1, half);
+          x0 = k < half ? cosf(a0) : sinf(a0);
+          x1 = k < half ? cosf(a1) : sinf(a1);
+        } else {
+          x0 = x[(long)m * ldx + k];
+          x1 = x[(long)m * ldx + k + 1];
+        }
         if (act == 1) {
           x0 = x0 / (1.0f + __expf(-x0));
           x1 = x1 / (1.0f + __expf(-x1));
@@ -382,17 +395,20 @@ __global__ __launch_bounds__(256) void modgemv_kernel(const float *__restrict__ 
   }
 }
 
-// x[m][n] = sum_k tok[m][k] * W[n][k], small K (patch embed: 4 x latent channels; K % 4 == 0): a 64-row x 64-col
-// tile per workgroup, 4 x 4 outputs per thread. K is staged in chunks of 64 in LDS as fp32 rows of float4 (one
-// float4 of x and one half4 of W per load), and read back as float4 along k; every output accumulates its products
-// in ascending k (one fma chain).
-__global__ __launch_bounds__(256) void linear_smallk_kernel(const float *__restrict__ x, long ldx, int M, int K,
-                                                            const hxa_h *__restrict__ W, int N, float *__restrict__ y,
-                                                            long ldy) {
-  __shared__ float4_t xs[64][17];  // [row][k / 4], one float4 of padding per row
+// patch embed (animad.cpp:440-446): x[b][tk][n] = sum_f tok[b tk][f] * Wemb[n][f], f = 4 c + 2 a + bb over the
+// Cc channels and the 2 x 2 patch (a, bb) of token tk = (gy, gx), read straight from the latent lat [B][Cc][H][W]
+// (the patchified token rows are never stored). A 64-token x 64-column tile per workgroup over the B * T tokens, 4 x 4
+// outputs per thread. K = 4 Cc is staged in chunks of 64 in LDS as fp32 rows of float4 (feature float4 c = the
+// 2 x 2 patch of channel c: two float2 loads of the latent; W as one half4), read back as float4 along k; every
+// output accumulates its products in ascending k (one fma chain). Image b's rows go to x + b * xrows * D.
+__global__ __launch_bounds__(256) void patch_embed_kernel(const float *__restrict__ lat, int B, int Cc, int H, int W,
+                                                          const hxa_h *__restrict__ Wemb, int N, float *__restrict__ x,
+                                                          int xrows) {
+  __shared__ float4_t xs[64][17];  // [token][k / 4], one float4 of padding per row
   __shared__ float4_t ws[64][17];
+  const int gw = W / 2, T = (H / 2) * gw, M = B * T, K = 4 * Cc;
   const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64, tid = threadIdx.x;
-  const int tr = tid / 16, tc = tid % 16;  // rows tr*4 + i, columns tc + 16 j
+  const int tr = tid / 16, tc = tid % 16;  // tokens tr*4 + i, columns tc + 16 j
   float acc[4][4] = {};
   for (int k0 = 0; k0 < K; k0 += 64) {
     const int kc4 = min(64, K - k0) / 4;
@@ -402,9 +418,15 @@ __global__ __launch_bounds__(256) void linear_smallk_kernel(const float *__restr
       const int i = tid + 256 * u, r = i >> 4, k4 = i & 15;
       float4_t xv = {0.0f, 0.0f, 0.0f, 0.0f}, wv = {0.0f, 0.0f, 0.0f, 0.0f};
       if (k4 < kc4) {
-        if (m0 + r < M) xv = *(const float4_t *)(x + (long)(m0 + r) * ldx + k0 + 4 * k4);
+        const int m = m0 + r;
+        if (m < M) {
+          const int b = m / T, tk = m % T, gy = tk / gw, gx = tk % gw, c = k0 / 4 + k4;
+          const float *p = lat + (((long)b * Cc + c) * H + 2 * gy) * W + 2 * gx;
+          const float2_t top = *(const float2_t *)p, bot = *(const float2_t *)(p + W);
+          xv = (float4_t){top[0], top[1], bot[0], bot[1]};
+        }
         if (n0 + r < N) {
-          const half4_t h = *(const half4_t *)(W + (long)(n0 + r) * K + k0 + 4 * k4);
+          const half4_t h = *(const half4_t *)(Wemb + (long)(n0 + r) * K + k0 + 4 * k4);
           wv = (float4_t){(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
         }
       }
@@ -413,26 +435,30 @@ __global__ __launch_bounds__(256) void linear_smallk_kernel(const float *__restr
     }
     __syncthreads();
     for (int k4 = 0; k4 < kc4; k4++) {
-      float4_t a[4], b[4];
+      float4_t a[4], bq[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) a[i] = xs[tr * 4 + i][k4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) b[j] = ws[tc + 16 * j][k4];
+      for (int j = 0; j < 4; j++) bq[j] = ws[tc + 16 * j][k4];
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
 #pragma unroll
-          for (int e = 0; e < 4; e++) acc[i][j] = fmaf(a[i][e], b[j][e], acc[i][j]);
+          for (int e = 0; e < 4; e++) acc[i][j] = fmaf(a[i][e], bq[j][e], acc[i][j]);
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < 4; i++) {
+    const int m = m0 + tr * 4 + i;
+    if (m >= M) continue;
+    float *y = x + ((long)(m / T) * xrows + m % T) * N;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const int m = m0 + tr * 4 + i, n = n0 + tc + 16 * j;
-      if (m < M && n < N) y[(long)m * ldy + n] = acc[i][j];
+      const int n = n0 + tc + 16 * j;
+      if (n < N) y[n] = acc[i][j];
     }
+  }
 }
 
 // timestep sinusoid (animad.cpp:425): out[i] = cos(t w_i), out[half+i] = sin(t w_i), w_i = 10000^(-i/half)
@@ -441,7 +467,7 @@ __global__ void sinusoid_kernel(const float *t, int n, int dim, float *out) {
   const int half = dim / 2;
   if (i >= n * half) return;
   const int b = i / half, j = i % half;
-  const float a = t[b] * expf(-logf(10000.0f) * (float)j / (float)half);
+  const float a = sinusoid_angle(t[b], j, half);
   out[(long)b * dim + j] = cosf(a);
   out[(long)b * dim + half + j] = sinf(a);
 }
@@ -767,17 +793,24 @@ int hxa_patchify_launch(const float *lat, int B, int Cc, int H, int W, float *to
   return LAUNCH_OK();
 }
 
+int hxa_patch_embed_launch(const float *lat, int B, int Cc, int H, int W, const hxa_h *Wemb, int N, float *x, int xrows,
+                           hipStream_t st) {
+  if (B < 1 || Cc < 1 || H % 2 || W % 2 || H < 2 || W < 2 || N < 1 || xrows < (H / 2) * (W / 2)) return HXA_E_ARG;
+  if ((uintptr_t)lat % 8 || (uintptr_t)Wemb % 8) return HXA_E_ARG;  // float2 latent pairs (W even), half4 weights
+  const int M = B * (H / 2) * (W / 2);
+  hxa_launch(patch_embed_kernel, dim3(nblk(N, 64), nblk(M, 64)), dim3(256), 0, st, lat, B, Cc, H, W, Wemb, N, x, xrows);
+  return LAUNCH_OK();
+}
+
 int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W, int N, float *y, long ldy, int act,
                           const float *bias, int split, int gap, hipStream_t st) {
   if (M <= 0 || K <= 0 || N <= 0) return HXA_E_ARG;
   if (M <= 8) {
-    if (K % 2) return HXA_E_ARG;
+    if (K % 2 || (act == 2 && (M != 1 || K % 4))) return HXA_E_ARG;
     hxa_launch(gemv_kernel, dim3(nblk(N, 4)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy, act, bias,
                        split > 0 ? split : N, gap);
   } else {
-    if (act != 0 || bias != nullptr || split > 0) return HXA_E_ARG;
-    if (K % 4 || ldx % 4 || (uintptr_t)x % 16 || (uintptr_t)W % 8) return HXA_E_ARG;  // float4 / half4 staging
-    hxa_launch(linear_smallk_kernel, dim3(nblk(N, 64), nblk(M, 64)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy);
+    return HXA_E_ARG;  // more than 8 rows: the patch embed has its own kernel (hxa_patch_embed_launch)
   }
   return LAUNCH_OK();
 }

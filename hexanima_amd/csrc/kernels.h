@@ -121,6 +121,10 @@ int hxa_fill_const_launch(void *dst, int dtype, size_t n, float v, hipStream_t s
 
 // caller-side glue (phone/animad.cpp)
 int hxa_patchify_launch(const float *lat, int B, int Cc, int H, int W, float *tok, hipStream_t st);
+// patch embed straight from the latent: x + (b * xrows + tk) * N <- the patchified token tk of image b times Wemb^T
+// (Wemb [N][4 Cc] fp16), all B images in one launch
+int hxa_patch_embed_launch(const float *lat, int B, int Cc, int H, int W, const hxa_h *Wemb, int N, float *x, int xrows,
+                           hipStream_t st);
 // M <= 8: GEMV (one wave per output; output index n -> n + gap for n >= split); M > 8: small-K tiles (patch embed)
 // stacked GEMV: y[(n / per) * ostride + r + (r >= split ? gap : 0)] = sum_k act(x[k]) W[n][k], r = n % per;
 // K % 256 == 0, K <= 4096; act 1 = SiLU on the input
