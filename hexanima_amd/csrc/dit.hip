@@ -61,9 +61,6 @@ struct Dit {
   float *emb = nullptr, *a1 = nullptr, *lora = nullptr, *h1 = nullptr;  // t-embedding work vectors
   float *zrows = nullptr, *x0rows = nullptr;  // rapid-moss state: noise z and clean estimate x0, token rows [B*T][4C]
   long modw_block = 0;                        // elements of one block's modulation weights
-  float *sig_host = nullptr;   // pinned source of the per-step sigma upload
-  hipEvent_t sig_ev = nullptr;  // recorded after that upload: sig_host is rewritten only once it has completed
-  bool sig_pending = false;
   // low-res first steps (animad.cpp:392-503; mossrun.cpp:288-313), allocated at the first such step.
   // Anima: the noise of the first step and the last clean estimate [B][C][H][W], the low-res latent and velocity
   // [B][C][H/f][W/f]; MOSS: the low-res noise and clean estimate, token rows [B][(gh/2)*(gw/2)][4C].
@@ -314,19 +311,11 @@ int record_step(Dit &d, const Pass &ps) {
   return HXA_OK;
 }
 
-// sigma, sigma_next and their difference into device memory, where the (captured) step reads them. The copy source
-// is pinned memory owned by the runner: an asynchronous copy may read its source after the call has returned, so
-// the source must outlive it, and it is rewritten only after the previous upload has completed.
+// sigma, sigma_next and their difference into device memory, where the (captured) step reads them: a one-workgroup
+// kernel with the values as its arguments, ahead of the step on its stream (no host buffer to keep alive and no wait
+// on an earlier upload, as a copy from pinned memory would need; the step time is the same either way)
 int set_sigma(Dit &d, float s0, float s1) {
-  if (d.sig_pending) DHIP(hipEventSynchronize(d.sig_ev));
-  d.sig_host[0] = s0;
-  d.sig_host[1] = s1;
-  d.sig_host[2] = s1 - s0;
-  d.sig_host[3] = 0.0f;
-  DHIP(hipMemcpyAsync(d.sig, d.sig_host, 4 * sizeof(float), hipMemcpyHostToDevice, d.st));
-  DHIP(hipEventRecord(d.sig_ev, d.st));
-  d.sig_pending = true;
-  return HXA_OK;
+  return hxa_set_sigma_launch(d.sig, s0, s1, d.st);
 }
 
 }  // namespace
@@ -385,11 +374,6 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   if (hipStreamCreateWithFlags(&d.st, hipStreamNonBlocking) != hipSuccess) {
     delete dp;
     return dfail(HXA_E_RESOURCE, "dit: stream");
-  }
-  if (hipHostMalloc((void **)&d.sig_host, 4 * sizeof(float), hipHostMallocDefault) != hipSuccess ||
-      hipEventCreateWithFlags(&d.sig_ev, hipEventDisableTiming) != hipSuccess) {
-    hxa_dit_destroy(dp);
-    return dfail(HXA_E_RESOURCE, "dit: pinned sigma buffer");
   }
   d.pack_bytes = hxa_pack_layout(b.kind, D, b.F, b.DC, b.fmt_attn, b.fmt_mlp, nullptr, 0);
   d.packs.assign(cfg->nblocks, nullptr);
@@ -573,8 +557,6 @@ extern "C" int hxa_dit_destroy(void *p) {
                   d->ones, d->ctx16, d->ws, d->vec, d->emb, d->a1, d->lora, d->h1, d->zrows, d->x0rows, d->tkv,
                   d->tkv_par, d->Wfin4};
   for (void *q : bufs) if (q) (void)hipFree(q);
-  if (d->sig_ev) (void)hipEventDestroy(d->sig_ev);
-  if (d->sig_host) (void)hipHostFree(d->sig_host);
   if (d->st) (void)hipStreamDestroy(d->st);
   delete d;
   return HXA_OK;

@@ -1189,6 +1189,15 @@ int hxa_q8rec_to_ktiled_launch(const void *rec, int N, int nkb, int kbt, void *q
   return LAUNCH_OK();
 }
 
+// the per-step sigma values: sig[0..3] = {s0, s1, s1 - s0, 0}, one value per lane (vector stores)
+__global__ void set_sigma_kernel(float *sig, float s0, float s1) {
+  const int i = threadIdx.x;
+  if (i < 4) sig[i] = i == 0 ? s0 : i == 1 ? s1 : i == 2 ? s1 - s0 : 0.0f;
+}
+int hxa_set_sigma_launch(float *sig, float s0, float s1, hipStream_t st) {
+  hxa_launch(set_sigma_kernel, dim3(1), dim3(64), 0, st, sig, s0, s1);
+  return LAUNCH_OK();
+}
 int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t st) {
   hxa_launch(sinusoid_kernel, dim3(nblk((long)n * dim / 2)), dim3(256), 0, st, t, n, dim, out);
   return LAUNCH_OK();
