@@ -573,9 +573,9 @@ def test_mega_block_moss_abi_with_lora():
 
 
 # ------------------------------------------------------------------------------------------------ DiT runner
-def _small_dit(hip, batch=2, nblocks=2, fmt=0):
+def _small_dit(hip, batch=2, nblocks=2, fmt=0, lat_c=16):
     bd = hip.BlockDims(0, 256, 2, 1024, 32, 128, 0, batch, 0, fmt, fmt, 1)
-    cfg = hip.DitCfg(bd, nblocks, 16, 16, 16, 256, 0)
+    cfg = hip.DitCfg(bd, nblocks, lat_c, 16, 16, 256, 0)
     p = C.c_void_p()
     hip.check(hip.lib().hxa_dit_create(C.byref(cfg), 1234, C.byref(p)), "dit_create")
     return p, cfg
@@ -626,6 +626,38 @@ def test_dit_small_denoise_vs_oracle():
         r, c = delta_metrics(got, ref, lat)
         print(f"denoise rel err on delta {r:.2e} cos {c:.9f}", flush=True)
         assert r < 2e-4 and c > 1 - 2e-4 ** 2  # measured 6.0e-5
+    finally:
+        lib.hxa_dit_destroy(p)
+
+
+@pytest.mark.parametrize("lat_c", [32, 64])
+def test_dit_small_velocity_wide_latent(lat_c):
+    """Velocity of a 1-block DiT with 32 / 64 latent channels (final layer of 128 / 256 outputs, patch embed K 128 /
+    256: two and four k chunks) against the oracle DiT."""
+    hip = _hip()
+    say(f"dit small velocity, {lat_c} latent channels")
+    lib = hip.lib()
+    p, cfg = _small_dit(hip, batch=1, nblocks=1, lat_c=lat_c)
+    try:
+        rng = np.random.default_rng(6)
+        lat = rng.standard_normal((1, lat_c, 16, 16)).astype(np.float32)
+        ctx = rng.standard_normal((1, 32, 128)).astype(np.float32)
+        hip.check(lib.hxa_dit_set_inputs(p, lat.ctypes.data, ctx.ctypes.data), "set_inputs")
+        D, C4 = 256, 4 * lat_c
+        layout = hip.pack_layout(0, 256, 1024, 128, 0, 0)
+        blocks = [unpack_weights(_export(hip, p, 0), 0, 256, 1024, 128, 0, 0, layout)]
+        modws = [_export(hip, p, 1).view(np.uint16).reshape(6 * D, D)]
+        g = _export(hip, p, 2).view(np.uint16)
+        o = 0
+        glue = []
+        for (n, k) in ((D, C4), (D, 256), (2 * D, D), (C4, D)):
+            glue.append(g[o:o + n * k].reshape(n, k))
+            o += n * k
+        v_gpu = np.zeros_like(lat)
+        hip.check(lib.hxa_dit_velocity(p, 0.75, v_gpu.ctypes.data), "velocity")
+        v_ref = oracle_anima_velocity(lat, f16(ctx), 0.75, blocks, modws, glue, D=D, H=2, F=1024, C4=C4, temb=256)
+        print(f"velocity rel err {rel(v_gpu, v_ref):.2e}", flush=True)
+        assert rel(v_gpu, v_ref) < 4e-4  # as for 16 channels (measured 1.2e-4 there)
     finally:
         lib.hxa_dit_destroy(p)
 
