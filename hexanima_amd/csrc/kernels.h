@@ -127,11 +127,12 @@ int hxa_patchify_launch(const float *lat, int B, int Cc, int H, int W, float *to
 // (Wemb [N][4 Cc] fp16), all B images in one launch
 int hxa_patch_embed_launch(const float *lat, int B, int Cc, int H, int W, const hxa_h *Wemb, int N, float *x, int xrows,
                            hipStream_t st);
-// M <= 8: GEMV (one wave per output; output index n -> n + gap for n >= split); M > 8: small-K tiles (patch embed)
 // stacked GEMV: y[(n / per) * ostride + r + (r >= split ? gap : 0)] = sum_k act(x[k]) W[n][k], r = n % per;
 // K % 256 == 0, K <= 4096; act 1 = SiLU on the input
 int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, int per, long ostride, int split, int gap,
                        int act, hipStream_t st);
+// GEMV of M <= 8 rows (one wave per output; output index n -> n + gap for n >= split); act 0 none, 1 SiLU on the
+// input, 2 the input row is the timestep sinusoid of t = x[0] at width K (M 1); more rows: HXA_E_ARG
 int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W, int N, float *y, long ldy, int act,
                           const float *bias, int split, int gap, hipStream_t st);
 // final layer over B images of T image tokens (image b's rows start at b*xrows); dtp == NULL: lat = v,
