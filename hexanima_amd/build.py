@@ -84,6 +84,31 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
     return LIB
 
 
+SAN_DIR = os.path.join(HERE, "_san")
+
+
+def build_sanitized(verbose: bool = False) -> str:
+    """The host programs (hxa_run, hxa_blk) built with AddressSanitizer + UndefinedBehaviorSanitizer into
+    hexanima_amd/_san/, linking the ordinary libhexanima_hip.so (host code only: no device code is instrumented).
+    Run the runner tests on them with HXA_PROG_DIR=hexanima_amd/_san."""
+    os.makedirs(SAN_DIR, exist_ok=True)
+    for prog in PROGRAMS:
+        out = os.path.join(SAN_DIR, prog)
+        cmd = ["g++", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+               "-std=c++17", "-Wall", "-I", INCLUDE, "-o", out + ".tmp", os.path.join(CSRC, prog + ".cpp"), "-L", HERE,
+               "-lhexanima_hip", "-Wl,-rpath,$ORIGIN/.."]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"{prog} (sanitized) failed:\n{r.stderr}")
+        os.replace(out + ".tmp", out)
+    if verbose:
+        print("built", SAN_DIR)
+    return SAN_DIR
+
+
 if __name__ == "__main__":
-    build(verbose=True, incremental="--incremental" in sys.argv)
+    if "--sanitize" in sys.argv:
+        build_sanitized(verbose=True)
+    else:
+        build(verbose=True, incremental="--incremental" in sys.argv)
     sys.exit(0)

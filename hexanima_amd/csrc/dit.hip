@@ -789,4 +789,46 @@ extern "C" long hxa_dit_export(void *p, int which, void *host, size_t bytes) {
   return n;
 }
 
+// the inverse of hxa_dit_export: the same `which` sections, the same byte images (host bytes must equal the export's
+// size); the device copy is complete when the call returns. The step graphs hold pointers, not values, so the next
+// step (replayed or recorded) runs on the imported weights.
+extern "C" int hxa_dit_import(void *p, int which, const void *host, size_t bytes) {
+  if (!p || !host) return dfail(HXA_E_ARG, "dit import: null");
+  Dit &d = *(Dit *)p;
+  const int nb = d.cfg.nblocks, D = d.bd.D;
+  struct Part {
+    void *dst;
+    long n;
+  } parts[2] = {{nullptr, 0}, {nullptr, 0}};
+  if (which >= 0 && which < nb) {
+    parts[0] = {d.packs[which], d.pack_bytes};
+  } else if (which >= nb && which < nb + (int)d.modw.size()) {
+    const int k = which - nb;
+    if (d.form == 1 && d.bd.kind == 0) {
+      parts[0] = {d.modw_all + 768L * D * k, 2 * 768L * D};
+      parts[1] = {d.modw_all + 768L * D * nb + 3L * 3 * D * 256 * k, 2 * 3L * 3 * D * 256};
+    } else {
+      parts[0] = {d.modw[k], 2 * d.modw_block};
+    }
+  } else if (which == 2 * nb) {
+    parts[0] = {d.glue, 2 * d.glue_elems};
+  } else if (which == 2 * nb + 1 && d.vec) {
+    parts[0] = {d.vec, 4 * d.vec_elems};
+  } else {
+    return dfail(HXA_E_ARG, "dit import index");
+  }
+  if ((long)bytes != parts[0].n + parts[1].n) return dfail(HXA_E_ARG, "dit import: size differs from the section's");
+  DHIP(hipStreamSynchronize(d.st));
+  const char *in = (const char *)host;
+  for (const Part &q : parts) {
+    if (q.n) DHIP(hipMemcpy(q.dst, in, q.n, hipMemcpyHostToDevice));
+    in += q.n;
+  }
+  if (which == 2 * nb) {  // the final layer's kernel reads its weights k-tiled by 4
+    DTRY(hxa_ktile4_launch(d.Wfin, 4 * d.cfg.lat_c, D, d.Wfin4, d.st));
+    DHIP(hipStreamSynchronize(d.st));
+  }
+  return HXA_OK;
+}
+
 extern "C" void *hxa_dit_stream(void *p) { return p ? (void *)((Dit *)p)->st : nullptr; }

@@ -11,7 +11,6 @@
 #include <algorithm>
 #include <map>
 #include <string>
-#include <thread>
 #include <vector>
 
 #include "../../include/hexanima_hip.h"
@@ -53,19 +52,6 @@ int hxa_set_error(int code, const char *fmt, ...) {
 static inline hipStream_t S(void *s) { return (hipStream_t)s; }
 static inline long al256(long x) { return (x + 255) & ~255L; }
 
-// host-side weight conversions split their outer loop over up to 16 threads
-template <class Fn>
-void par_for(int n, Fn fn) {
-  const int nt = std::max(1, std::min({n, 16, (int)std::thread::hardware_concurrency()}));
-  std::vector<std::thread> th;
-  for (int t = 1; t < nt; t++)
-    th.emplace_back([&, t] {
-      for (int i = t; i < n; i += nt) fn(i);
-    });
-  for (int i = 0; i < n; i += nt) fn(i);
-  for (auto &x : th) x.join();
-}
-
 
 extern "C" const char *hxa_last_error(void) { return g_err; }
 extern "C" const char *hxa_version(void) { return "hexanima_hip 0.1 gfx950"; }
@@ -80,7 +66,9 @@ extern "C" int hxa_init(int device) {
   if (device < 0 || device >= n) return fail(HXA_E_ARG, "device %d of %d", device, n);
   HIPC(hipSetDevice(device));
   HIPC(hipFree(nullptr));
-  return HXA_OK;
+  // the static workspace of hxa_block_run_noalloc is resolved here, so that a first noalloc call made under graph
+  // capture does no symbol lookup
+  return hxa_noalloc_setup(nullptr);
 }
 extern "C" int hxa_malloc(void **p, size_t bytes) {
   *p = nullptr;
@@ -147,6 +135,32 @@ extern "C" int hxa_stream_wait_event(void *stream, void *ev) {
 extern "C" int hxa_event_elapsed_ms(void *a, void *b, float *ms) {
   HIPC(hipEventSynchronize((hipEvent_t)b));
   HIPC(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+  return HXA_OK;
+}
+extern "C" int hxa_stream_begin_capture(void *stream, int mode) {
+  if (mode < 0 || mode > 2) return fail(HXA_E_ARG, "capture mode %d", mode);
+  const hipStreamCaptureMode m[3] = {hipStreamCaptureModeGlobal, hipStreamCaptureModeThreadLocal, hipStreamCaptureModeRelaxed};
+  HIPC(hipStreamBeginCapture(S(stream), m[mode]));
+  return HXA_OK;
+}
+extern "C" int hxa_stream_end_capture(void *stream, void **exec) {
+  if (!exec) return fail(HXA_E_ARG, "end capture: null exec");
+  *exec = nullptr;
+  hipGraph_t g = nullptr;
+  HIPC(hipStreamEndCapture(S(stream), &g));
+  hipGraphExec_t e = nullptr;
+  const hipError_t r = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (r != hipSuccess) return fail(HXA_E_HIP, "graph instantiate: %s", hipGetErrorString(r));
+  *exec = e;
+  return HXA_OK;
+}
+extern "C" int hxa_graph_launch(void *exec, void *stream) {
+  HIPC(hipGraphLaunch((hipGraphExec_t)exec, S(stream)));
+  return HXA_OK;
+}
+extern "C" int hxa_graph_exec_destroy(void *exec) {
+  if (exec) HIPC(hipGraphExecDestroy((hipGraphExec_t)exec));
   return HXA_OK;
 }
 extern "C" int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, char *name, int name_len) {
@@ -466,9 +480,11 @@ constexpr long DQ_WIDE_ROWS = 4096;
 // split-K 4 on the ping-pong tiles, into four fp16 partials that the next norm adds: those tiles hide the
 // dequantisation under their MFMAs, and no fp16 copy of the weight goes through memory (1536 tokens, 2.9B-class
 // MLP-down 10240 -> 2560: 80 us fused against 15.5 us of dequantisation + 84.5 us of fp16 GEMM in the step).
+// Not with the reference's rounding points (round_ref: mega_block), which round o once and the MLP-down in two halves.
 static bool q_split4(const hxa_block_dims *d, int fmt, int K) {
   const long BT = (long)d->batch * d->T;
-  return d->kind != 2 && (fmt & ~HXA_W_KTILED) != HXA_W_F16 && BT >= DQ_MIN_ROWS && BT < DQ_WIDE_ROWS && K % 128 == 0;
+  return d->kind != 2 && !d->round_ref && (fmt & ~HXA_W_KTILED) != HXA_W_F16 && BT >= DQ_MIN_ROWS && BT < DQ_WIDE_ROWS &&
+         K % 128 == 0;
 }
 // fp16 partials the MLP-down leaves (pending across a chain of blocks): 4 in the fused split-K 4 form, else 2
 int hxa_block_down_parts(const hxa_block_dims *d) { return q_split4(d, d->fmt_mlp, d->F) ? 4 : 2; }
@@ -805,7 +821,9 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   // the GPU at N = D) then the residual; measured faster than the single-launch HXA_EPI_RESADD_SPLIT2 form, whose
   // 128-wide tiles leave a quarter of the CUs idle at 1536 x 2048. With the LoRA the halves are [0, F/2) and
   // [F/2, F) + the LoRA columns (moss blk.c:256-259): two launches.
-  const int down_np = hxa_block_down_parts(d);
+  // with a stage stop the MLP-down runs in the reference's two K halves (the dumped t holds the first half's partial,
+  // blk.c:172-173) whatever the workspace layout allows
+  const int down_np = stop ? 2 : hxa_block_down_parts(d);
   auto down_resadd = [&](const hxa_h *a, const HxaWeight &w, const float *gate) -> int {
     const HxaWeight *wp = &w;
     if (down_np == 4) {
@@ -832,7 +850,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   bool split_o = false;
   int o_np = 1;
   auto deferred_proj = [&](const HxaWeight &w) -> int {
-    if (q_split4(d, w.fmt, w.K)) {
+    if (q_split4(d, w.fmt, w.K) && !stop) {
       o_np = 4;
       return gemm(o, ldo, BT, w, HXA_EPI_PARTIAL, t1, D, nullptr, nullptr, nullptr, 0, 0, 4, (long)BT * D);
     }
@@ -840,8 +858,8 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     TRY(prep(w, wp));
     const HxaGemm g1 = make(o, ldo, BT, *wp, HXA_EPI_STORE, t1, D, nullptr, nullptr, nullptr, 0, 0, 1, 0);
     int bm = 0, bn = 0, nw = 0, rounds = 0;
-    split_o = !lora && w.K % 64 == 0 && hxa_gemm_plan(g1, &bm, &bn, &nw, &rounds) == HXA_OK && rounds == 1 &&
-              bm * bn <= 128 * 128;
+    split_o = !lora && !d->round_ref && w.K % 64 == 0 && hxa_gemm_plan(g1, &bm, &bn, &nw, &rounds) == HXA_OK &&
+              rounds == 1 && bm * bn <= 128 * 128;
     HxaGemm g = g1;
     o_np = split_o ? 2 : 1;
     if (split_o) {
@@ -1065,6 +1083,7 @@ struct Ctx {
   const hxa_h **modw_ptrs = nullptr;  // device table of the modulation weights of one hxa_anima_modulation call
   size_t modw_ptrs_bytes = 0;
   float *mod_pin = nullptr;  // pinned staging of mega_block's modulation vectors (9 x 3072 fp32 at most)
+  hipEvent_t mod_ev = nullptr;  // recorded after the copy out of mod_pin; waited for before mod_pin is rewritten
   size_t mod_dev_bytes = 0, emb_dev_bytes = 0, h1_dev_bytes = 0;
   // device-resident activations of the current run of blocks
   float *x = nullptr, *cosr = nullptr, *sinr = nullptr, *mod = nullptr, *stage = nullptr;
@@ -1112,7 +1131,7 @@ int build_anima_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
   const int D = ANIMA_D, F = ANIMA_F, DC = ANIMA_DC;
   const bool q8 = meta[M_Q8] != 0;
   const int fmt = q8 ? HXA_W_Q8 : HXA_W_F16;
-  db.dims = hxa_block_dims{0, D, D / 128, F, 0, DC, 0, 1, 0, fmt, fmt, 0};
+  db.dims = hxa_block_dims{0, D, D / 128, F, 0, DC, 0, 1, 0, fmt, fmt, 0, 1};
   long offs[32];
   const long bytes = hxa_pack_layout(0, D, F, DC, fmt, fmt, offs, 32);
   // pack matrix order: qkv (q,k,v rows), o, cq, ckv (k,v rows), co, w1, w2
@@ -1165,7 +1184,7 @@ int build_moss_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
                W_TOTAL = 135397376;
   const size_t base = (size_t)meta[MM_WOFF];
   if (meta[MM_WOFF] < 0 || base + W_TOTAL > hb.bytes) return fail(HXA_E_WEIGHTS, "moss weights shorter than a block pack");
-  db.dims = hxa_block_dims{2, D, D / 128, F, 0, 0, 0, 1, 0, fmt, fmt, 0};
+  db.dims = hxa_block_dims{2, D, D / 128, F, 0, 0, 0, 1, 0, fmt, fmt, 0, 1};
   long offs[32];
   const long bytes = hxa_pack_layout(2, D, F, 0, fmt, fmt, offs, 32);
   const uint8_t *b = nullptr;
@@ -1239,6 +1258,7 @@ extern "C" int mega_close(remote_handle64 h) {
                   (void *)c->mod_dev, (void *)c->emb_dev, (void *)c->h1_dev, (void *)c->modw_ptrs, c->wstage})
     if (p) (void)hipFree(p);
   if (c->mod_pin) (void)hipHostFree(c->mod_pin);
+  if (c->mod_ev) (void)hipEventDestroy(c->mod_ev);
   (void)hipStreamDestroy(c->st);
   delete c;
   return HXA_OK;
@@ -1331,12 +1351,16 @@ int run_ref_block(Ctx *c, const BlockCall &bc, const DevBlock &db, const HostBuf
     c->cur_C = bc.C;
   }
   // the modulation through pinned memory: an asynchronous DMA instead of a staged pageable copy. The previous
-  // call's copy from mod_pin has completed (every call ends with a stream synchronisation).
+  // call's copy out of mod_pin may still be in flight when that call returned early on an error, so its event is
+  // waited for before the buffer is rewritten.
   const size_t modb = (size_t)(d.kind == 0 ? 9 : 6) * D * 4;
   if (!c->mod_pin) HIPC(hipHostMalloc((void **)&c->mod_pin, (size_t)9 * 3072 * 4, hipHostMallocDefault));
+  if (!c->mod_ev) HIPC(hipEventCreateWithFlags(&c->mod_ev, hipEventDisableTiming));
   if (modb > (size_t)9 * 3072 * 4) return fail(HXA_E_META, "modulation of %zu bytes", modb);
+  HIPC(hipEventSynchronize(c->mod_ev));
   memcpy(c->mod_pin, modh, modb);
   HIPC(hipMemcpyAsync(c->mod, c->mod_pin, modb, hipMemcpyHostToDevice, st));
+  HIPC(hipEventRecord(c->mod_ev, st));
   int us[16] = {0};
   const int nst = d.kind == 0 ? 13 : 8;
   const auto t_work = std::chrono::steady_clock::now();

@@ -33,7 +33,7 @@ class HxaError(RuntimeError):
 
 class BlockDims(C.Structure):
     _fields_ = [("kind", I), ("D", I), ("H", I), ("F", I), ("C", I), ("DC", I), ("T", I), ("batch", I), ("nvalid", I),
-                ("fmt_attn", I), ("fmt_mlp", I), ("gelu", I)]
+                ("fmt_attn", I), ("fmt_mlp", I), ("gelu", I), ("round_ref", I)]
 
 
 class DitCfg(C.Structure):
@@ -67,6 +67,10 @@ _SIGS = {
     "hxa_event_record": (I, [P, P]),
     "hxa_stream_wait_event": (I, [P, P]),
     "hxa_event_elapsed_ms": (I, [P, P, C.POINTER(F)]),
+    "hxa_stream_begin_capture": (I, [P, I]),
+    "hxa_stream_end_capture": (I, [P, C.POINTER(P)]),
+    "hxa_graph_launch": (I, [P, P]),
+    "hxa_graph_exec_destroy": (I, [P]),
     "hxa_device_info": (I, [C.POINTER(I), C.POINTER(I), C.POINTER(SZ), C.c_char_p, I]),
     "hxa_clock_record": (I, [I, P, L]),
     "hxa_gemm": (I, [P, L, I, I, P, P, P, I, I, I, I, P, L, L, P, L, P, P, L, I, P]),
@@ -101,6 +105,7 @@ _SIGS = {
     "hxa_dit_step_lowres": (I, [P, F, F, I, I]),
     "hxa_dit_moss_step_lowres": (I, [P, F, F, I]),
     "hxa_dit_export": (L, [P, I, P, SZ]),
+    "hxa_dit_import": (I, [P, I, P, SZ]),
     "hxa_dit_stream": (P, [P]),
 }
 _lib = None

@@ -97,6 +97,13 @@ int hxa_event_record(void *ev, void *stream);
 int hxa_stream_wait_event(void *stream, void *ev); /* later work on stream waits for ev */
 int hxa_event_elapsed_ms(void *start, void *stop, float *ms);
 int hxa_device_info(int *num_cu, int *clock_khz, size_t *mem_bytes, char *name, int name_len);
+/* HIP graph capture of a stream, for callers that replay launch sequences (and the tests of the capture-safe entry
+ * points); no counterpart in the reference. mode 0 global, 1 thread-local, 2 relaxed (hipStreamCaptureMode);
+ * end_capture instantiates the captured graph into *exec, launched with hxa_graph_launch. */
+int hxa_stream_begin_capture(void *stream, int mode);
+int hxa_stream_end_capture(void *stream, void **exec);
+int hxa_graph_launch(void *exec, void *stream);
+int hxa_graph_exec_destroy(void *exec);
 /* Shader-clock record, for measurement; no counterpart in the reference. kind 0: every GEMM launched after this call
  * (hxa_gemm*, the block runner's and DiT's projections, graphs captured after it) writes, per workgroup w < nrec,
  * four uint64 at rec[4w .. 4w+3] (device memory): s_memtime and s_memrealtime when the workgroup starts, both again
@@ -222,6 +229,11 @@ typedef struct {
   int nvalid;    /* MOSS: valid tokens per image (joint attention key mask) */
   int fmt_attn, fmt_mlp;
   int gelu;      /* Anima MLP activation: 0 erf (reference block), 1 tanh */
+  int round_ref; /* 1: the reference's rounding points for the gated projections, o and cross-o rounded to fp16 once,
+                    the MLP-down in two K halves (blk.c:161-162, :168-169, :172-174). 0: the runner may split the
+                    o / cross-o projections into two fp16 K-half partials and, with int8 / int4 weights at
+                    1024 .. 4095 rows, the o / cross-o / MLP-down into four K-quarter partials (faster; each partial
+                    is rounded to fp16). mega_block / mega_moss_block always run with 1; a stage stop implies it */
 } hxa_block_dims;
 /* bytes of the activation workspace of hxa_block_run. With int8 / int4 weights it includes the dequantisation slot:
  * one fp16 copy of the largest quantised projection that runs from fp16 -- at 1024 .. 4095 rows (batch*T) the cross
@@ -310,6 +322,9 @@ int hxa_dit_moss_step_lowres(void *dit, float code, float rope_scale, int use_gr
  *   which == 2 nblocks + 1 (form 1 MOSS): fp32 b_video [D], b_t0 [D], b_t2 [D], b_smod [6D], b_hmod [2D],
  *     final_norm [D], latent_mix Q [4C][4C], bn_mean [4C], bn_var [4C] */
 long hxa_dit_export(void *dit, int which, void *host, size_t bytes);
+/* the inverse of hxa_dit_export: overwrite section `which` with host bytes of the same layout and size (bytes must be
+ * the size hxa_dit_export reports). Complete when the call returns; later steps (captured graphs included) use it. */
+int hxa_dit_import(void *dit, int which, const void *host, size_t bytes);
 void *hxa_dit_stream(void *dit);
 
 #ifdef __cplusplus

@@ -751,7 +751,9 @@ int hxo_moss_block(const hxo_moss_cfg *cfg, const hxo_moss_w *w, float *x, const
   const int T = cfg->T, D = cfg->D, H = cfg->H, F = cfg->F;
   const int lora = w->aqkv != NULL, R = lora ? LORA_R : 0;
   const float *sha = mod6, *sca = mod6 + D, *ga = mod6 + 2 * D, *shf = mod6 + 3 * D, *scf = mod6 + 4 * D, *gf = mod6 + 5 * D;
-  float *tmp = (float *)malloc(sizeof(float) * (size_t)T * (F > D ? F : D));
+  /* widest GEMM output: D, F or (with the LoRA) the 3R columns of L_qkv */
+  const int tw = F > D ? F : D;
+  float *tmp = (float *)malloc(sizeof(float) * (size_t)T * (tw > 3 * R ? tw : 3 * R));
   uint16_t *t2 = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * D);
   uint16_t *cat = lora ? (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * ((F / 2 > D ? F / 2 : D) + R)) : NULL;
   int stage = 0;

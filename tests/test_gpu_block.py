@@ -392,25 +392,28 @@ STOP_CHECKS = [(1, {"H": 1.6e-5}), (2, {"Q": 9e-5, "K": 9e-5, "V": 9e-5}), (3, {
 XTOL = {5: 1.7e-3, 6: 1.7e-3, 7: 1.7e-3, 8: 1.7e-3, 9: 1.7e-3, 11: 2.3e-3, 12: 2.3e-3, 13: 1.6e-3}
 
 
-def test_mega_block_stage_dumps_1536():
+@pytest.mark.parametrize("q8", [False, True])
+def test_mega_block_stage_dumps_1536(q8):
     """meta[M_STOP] = n stops after n stages (blk.c:136) and leaves the stage buffers in the blob as h16 tiles, the
     way cmp_block.py reads them: each one against the oracle's buffer at the same stage, x (written back with REL)
-    against the oracle's x, times[] filled for the n stages run and 0 after."""
+    against the oracle's x, times[] filled for the n stages run and 0 after. With a q8 file too: the dumped t of the
+    MLP-down stage (13) is the first K half's partial, as the reference leaves it (blk.c:172-173), whatever split the
+    runner would use without a stop."""
     hip = _hip()
-    say("mega_block M_STOP stage dumps T=1536")
+    say(f"mega_block M_STOP stage dumps T=1536 q8={q8}")
     lib = hip.lib()
     rng = np.random.default_rng(31)
     D, T, NCTX, F = 2048, 1536, 256, 8192
     offs, blob, x, ctx, cos, sin = _abi_blob(rng, T, NCTX, 48, 32)
     x_tiles = blob[offs["X"]:offs["X"] + T * D * 4].copy()
-    wb, ow = _blk_file(rng, False)
+    wb, ow = _blk_file(rng, q8)
     mod = cfg0_mod9(D, rng)
     h = C.c_uint64()
     hip.check(lib.mega_open(b"", C.byref(h)), "mega_open")
     try:
         hip.check(lib.hxa_register(h, 100, blob.ctypes.data, blob.nbytes, hip.KIND_BLOB), "register blob")
         hip.check(lib.hxa_register(h, 200, wb.ctypes.data, wb.nbytes, hip.KIND_WEIGHTS_ANIMA), "register w")
-        meta = _abi_meta(offs, T, NCTX, False)
+        meta = _abi_meta(offs, T, NCTX, q8)
         meta[META.index("FIRST")], meta[META.index("REL")] = 1, 1
         rc = C.c_int(0)
         rows = {"H": T, "Q": T, "K": T, "V": T, "O": T, "T": T, "MID": T, "CK": NCTX, "CV": NCTX}

@@ -26,7 +26,9 @@ def _hip():
 
 
 def _prog(hip, name):
-    p = os.path.join(os.path.dirname(hip.LIB_PATH), name)
+    # HXA_PROG_DIR: run other builds of the host programs, e.g. the AddressSanitizer + UBSan ones of
+    # `python -m hexanima_amd.build --sanitize` (hexanima_amd/_san)
+    p = os.path.join(os.environ.get("HXA_PROG_DIR") or os.path.dirname(hip.LIB_PATH), name)
     assert os.access(p, os.X_OK), f"{p} is not built"
     return p
 

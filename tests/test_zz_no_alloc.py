@@ -66,3 +66,18 @@ def test_block_run_noalloc_matches_block_run():
     dummy = hip.DeviceArray((256,), np.uint8, zero=True)
     rc = lib.hxa_block_run_noalloc(C.byref(d4), dummy.ptr, dummy.ptr, dummy.ptr, dummy.ptr, dummy.ptr, dummy.ptr, 0, None)
     assert rc == -12 and "static scratch" in hip.last_error()
+
+
+def test_block_run_noalloc_first_call_captured():
+    """The process's first noalloc call made under HIP graph capture (global mode), then replayed three times with
+    eager work between the replays, gives hxa_block_run's bits each time. Runs in a child process, so the captured
+    call is the first of its process whatever ran before this test (tests/_noalloc_capture.py)."""
+    import os
+    import subprocess
+    import sys
+    print("[case] noalloc first call under graph capture (child process)", flush=True)
+    child = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_noalloc_capture.py")
+    r = subprocess.run([sys.executable, "-u", child], capture_output=True, text=True, timeout=110)
+    print(r.stdout[-3000:], r.stderr[-3000:], flush=True)
+    assert r.returncode == 0
+    assert r.stdout.count("bit-identical to hxa_block_run True") == 3
