@@ -214,24 +214,26 @@ struct GemmGeo {
 };
 
 // Per-wave number of direct-to-LDS instructions issued for one stage (A and W instructions dealt round-robin over
-// the NW waves, the scale / offset vectors by wave 0).
+// the NW waves; every wave loads its share of the scale / offset vectors).
 template <int BM, int BN, int FMT, bool ASYM, int NW>
 HXA_DEV constexpr int loads_per_stage(int wave) {
   using G = GemmGeo<BM, BN, FMT>;
   constexpr int NA = BM / 16;
   return NA / NW + (wave < NA % NW ? 1 : 0) + G::TW / NW + (wave < G::TW % NW ? 1 : 0) +
-         (FMT != HXA_W_F16 && wave == 0 ? (ASYM ? 2 : 1) : 0);
+         (FMT != HXA_W_F16 ? (ASYM ? 2 : 1) : 0);
 }
-// wait until at most LATER further stages of loads are outstanding for this wave
-template <int BM, int BN, int FMT, bool ASYM, int NW, int LATER, int W = 0>
-HXA_DEV void wait_stage(int wave) {
-  if constexpr (W + 1 < NW) {
-    if (wave != W) {
-      wait_stage<BM, BN, FMT, ASYM, NW, LATER, W + 1>(wave);
-      return;
-    }
-  }
-  wait_vm<LATER * loads_per_stage<BM, BN, FMT, ASYM, NW>(W)>();
+// Wait until at most LATER further stages of this wave's loads are outstanding, with one wave-uniform count: the
+// fewest loads any wave issues per stage. A wave that issues more waits for a few of its newest loads too, never for
+// fewer than its own older stages. (A count chosen per wave branches on the wave index inside the main loop, and the
+// register allocator then copied the live accumulators between AGPRs and VGPRs around that branch every k step.)
+template <int BM, int BN, int FMT, bool ASYM, int NW, int LATER>
+HXA_DEV void wait_stage(int) {
+  constexpr int lmin = [] {
+    int m = loads_per_stage<BM, BN, FMT, ASYM, NW>(0);
+    for (int w = 1; w < NW; w++) m = loads_per_stage<BM, BN, FMT, ASYM, NW>(w) < m ? loads_per_stage<BM, BN, FMT, ASYM, NW>(w) : m;
+    return m;
+  }();
+  wait_vm<LATER * lmin>();
 }
 
 // ---- epilogue after f16(acc) is staged in LDS as a row-major [BM][BN + 8] tile (and, for SPLIT2, the first K
@@ -699,11 +701,13 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (FMT != HXA_W_F16 && wave == 0) {
-      const int g = k0 >> 5;
-      const int nn = min(n0 + lane * 8, p.N - 8);
-      if (lane < BN / 8) g2l16_opaque(p.S + (long)g * p.N + nn, ws + G::W_BYTES);
-      if (ASYM && lane < BN / 8) g2l16_opaque(p.Z + (long)g * p.N + nn, ws + G::W_BYTES + G::S_BYTES);
+    if constexpr (FMT != HXA_W_F16) {  // the stage's scale (and offset) vector, 16-byte chunks spread over the waves
+      constexpr int CPW = (BN / 8 + NW - 1) / NW;  // chunks per wave
+      const int g = k0 >> 5, c = wave * CPW + lane;
+      const int nn = min(n0 + c * 8, p.N - 8);
+      if (lane < CPW && c < BN / 8) g2l16_opaque(p.S + (long)g * p.N + nn, ws + G::W_BYTES + 16 * wave * CPW);
+      if (ASYM && lane < CPW && c < BN / 8)
+        g2l16_opaque(p.Z + (long)g * p.N + nn, ws + G::W_BYTES + G::S_BYTES + 16 * wave * CPW);
     }
   };
 
@@ -909,7 +913,7 @@ HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
   constexpr int LPS = (NAI + TW) / NWG;                     // per group-1 wave and stage (+ the vectors for wave 0)
   constexpr int NVEC = FMT == HXA_W_F16 ? 0 : (ASYM ? 2 : 1);
   static_assert(BM % 64 == 0 && WTN % 32 == 0 && NS == 4 && (NAI + TW) % NWG == 0 && NAI % NWG == 0 &&
-                    G::W_BYTES % 1024 == 0 && BN / 8 <= 64,
+                    G::W_BYTES % 1024 == 0 && (BN / 8) % NWG == 0,
                 "tile shape");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
 
@@ -942,24 +946,19 @@ HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
       if (t < NAI) g2l16_sbase(ab, loff[t0 / NWG], st + t * 1024);
       else g2l16_sbase(wb, loff[t0 / NWG], st + G::A_BYTES + (t - NAI) * 1024);
     }
-    if constexpr (NVEC > 0) {  // scale (and offset) vector of the stage's k group: wave 0 of the group
-      if (wl == 0) {
-        const int g = k0 >> 5, nn = min(n0 + lane * 8, p.N - 8);
-        uint8_t *ws = st + G::A_BYTES;
-        if (lane < BN / 8) g2l16_opaque(p.S + (long)g * p.N + nn, ws + G::W_BYTES);
-        if (ASYM && lane < BN / 8) g2l16_opaque(p.Z + (long)g * p.N + nn, ws + G::W_BYTES + G::S_BYTES);
-      }
+    if constexpr (NVEC > 0) {  // scale (and offset) vector of the stage's k group, 16-byte chunks over the 4 waves
+      constexpr int CPW = BN / 8 / NWG;
+      const int g = k0 >> 5, c = wl * CPW + lane, nn = min(n0 + c * 8, p.N - 8);
+      uint8_t *ws = st + G::A_BYTES;
+      if (lane < CPW) g2l16_opaque(p.S + (long)g * p.N + nn, ws + G::W_BYTES + 16 * wl * CPW);
+      if (ASYM && lane < CPW) g2l16_opaque(p.Z + (long)g * p.N + nn, ws + G::W_BYTES + G::S_BYTES + 16 * wl * CPW);
     }
   };
-  // wait until at most `later` further stages of this group-1 wave's loads are in flight
+  // wait until at most `later` further stages of this group-1 wave's loads are in flight (the same count in every
+  // wave: no branch on the wave index in the loop)
   auto wait_later = [&](auto later_c) {
     constexpr int L = decltype(later_c)::value;
-    if constexpr (NVEC == 0) {
-      wait_vm<L * LPS>();
-    } else {
-      if (wl == 0) wait_vm<L * (LPS + NVEC)>();
-      else wait_vm<L * LPS>();
-    }
+    wait_vm<L * (LPS + NVEC)>();
   };
   // Quantised W is read raw in the memory phase (wq, scale sc, offset zc) and dequantised in the compute phase, where
   // its VALU work issues under the MFMAs (the memory phase stays a phase of LDS reads and loads only): the

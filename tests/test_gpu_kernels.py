@@ -97,11 +97,12 @@ def test_gemm_w8a16_w4a16_config1(N, K, fmt):
 
 
 @pytest.mark.parametrize("tile", [(192, 256, 8), (128, 256, 8), (192, 128, 8), (128, 128, 8), (128, 128, 4), (192, 256, 9),
-                                  (256, 256, 9), (128, 256, 9)])
+                                  (256, 256, 9), (128, 256, 9), (192, 256, 4), (256, 128, 4), (128, 256, 4), (192, 128, 4),
+                                  (192, 192, 4), (64, 128, 4)])
 @pytest.mark.parametrize("fmt", [1, 2])
 def test_gemm_quant_tiles(fmt, tile):
-    """int8 / int4 weights on every 8-wave tile (and a 4-wave one), ragged in M and N: dequantised-fp16 GEMM is the
-    reference."""
+    """int8 / int4 weights on every 8-wave and 4-wave tile, ragged in M and N (every wave loads its share of the
+    scale vectors): dequantised-fp16 GEMM is the reference."""
     hip = _hip()
     say(f"gemm fmt={fmt} tile={tile}")
     rng = np.random.default_rng(40 + fmt)
@@ -112,6 +113,28 @@ def test_gemm_quant_tiles(fmt, tile):
     wdq = hxo.q8_dequant(q, s) if fmt == 1 else hxo.q4_dequant(q, s)
     got = _run_gemm(hip, A, fmt, q, s, N, K, tile=tile)
     assert_gemm_close(got, hxo.gemm(A, wdq), A, wdq.view(np.float16))
+
+
+@pytest.mark.parametrize("tile", [(192, 256, 9), (256, 256, 9), (128, 128, 4), (192, 256, 4), (128, 128, 8)])
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_gemm_quant_splitk4_partials(fmt, tile):
+    """int8 / int4 weights split-K 4 into fp16 partials (the block runner's attention-output / MLP-down form at
+    1024 - 4095 rows), including one k step per slice boundary case (K / 4 = 64, two k steps per slice): each partial
+    against the oracle's GEMM over its K quarter."""
+    hip = _hip()
+    say(f"gemm fmt={fmt} split-K 4 partials tile={tile}")
+    rng = np.random.default_rng(90 + fmt)
+    M, N = 320, 384
+    for K in (256, 1024):
+        A = f16(rng.standard_normal((M, K)))
+        wf = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+        q, s = hxo.q8_quantize(wf) if fmt == 1 else hxo.q4_quantize(wf)
+        wdq = hxo.q8_dequant(q, s) if fmt == 1 else hxo.q4_dequant(q, s)
+        got = _run_gemm(hip, A, fmt, q, s, N, K, epi=hip.EPI_PARTIAL, ksplit=4, tile=tile)
+        for z in range(4):
+            sl = slice(z * K // 4, (z + 1) * K // 4)
+            Az, Wz = np.ascontiguousarray(A[:, sl]), np.ascontiguousarray(wdq.view(np.float16)[:, sl])
+            assert_gemm_close(got[z], hxo.gemm(Az, Wz.view(np.uint16)), Az, Wz)
 
 
 def _q4a_weights(rng, N, K):
@@ -128,7 +151,8 @@ def _q4a_weights(rng, N, K):
     return q.view(np.uint8).reshape(N, K // 2), s.view(np.uint16), z.view(np.uint16)
 
 
-@pytest.mark.parametrize("tile", [None, (128, 128, 4), (192, 256, 4), (128, 256, 8), (192, 256, 9), (128, 256, 9)])
+@pytest.mark.parametrize("tile", [None, (128, 128, 4), (192, 256, 4), (128, 256, 8), (192, 256, 9), (128, 256, 9),
+                                  (192, 128, 8)])
 def test_gemm_q4_asymmetric(tile):
     """q4a weights (a scale and a min per group) through hxa_gemm with z != NULL, ragged in M: the dequantised-fp16
     GEMM is the reference."""
