@@ -35,8 +35,12 @@ constexpr float RESCALE_TH = 5.5f;
 HXA_DEV float16_t mfma(half8_t a, half8_t b, float16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
 
 // NWH waves per key half (4: 128 queries per workgroup, 8 waves; 3: 96 queries, 6 waves -- chosen per launch so
-// that the grid fills the CUs)
-template <int NWH>
+// that the grid fills the CUs). FULL: every key tile lies wholly below nvalid and NKV (nvalid % 64 == 0: 1536 image
+// tokens, 6144 + 512 joint tokens, 256 text tokens), so the loop carries no key masking and no clamped per-lane tile
+// addresses. PF: the launch touches weights for the next kernel (p.pf_bytes > 0). Both are compile-time so that the
+// main loop holds only the code it runs: the general form kept 44 - 62 scalar registers spilled to VGPR lanes and
+// their v_readlane / v_writelane in the loop.
+template <int NWH, bool FULL, bool PF>
 __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) {
   constexpr int QB = NWH * 32;  // queries per workgroup
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -83,7 +87,7 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   }
   auto load_kv = [&](int i, bool with_k, bool with_v) {
     const int key0 = (t0 + i) * KT;
-    if (key0 + KT <= p.NKV) {
+    if (FULL || key0 + KT <= p.NKV) {
       if (with_k) {
         const hxa_h *kt = k + (long)key0 * p.ldk;
 #pragma unroll
@@ -102,6 +106,7 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
       }
       return;
     }
+    if constexpr (FULL) return;
     if (with_k) {
       uint8_t *dst = kbuf(i);
 #pragma unroll
@@ -134,9 +139,9 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   // small fraction of the bandwidth; each line a 4-byte direct-to-LDS load into the sink (no register is written;
   // the next step's vmcnt(0) wait drains it)
   constexpr int NT = 2 * NWH * 64;
-  const uint8_t *pf_base;
-  uint32_t pf_lines;  // of this workgroup
-  {
+  const uint8_t *pf_base = nullptr;
+  uint32_t pf_lines = 0;  // of this workgroup
+  if constexpr (PF) {
     const uint32_t lines = (uint32_t)(p.pf_bytes >> 7), nwg = gridDim.x * gridDim.y;
     const uint32_t per = (lines + nwg - 1) / nwg, l0 = min((blockIdx.x + blockIdx.y * gridDim.x) * per, lines);
     pf_base = p.pf + ((long)l0 << 7);
@@ -146,7 +151,7 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   const uint32_t pf_per_step = (pf_lines + pf_steps - 1) / pf_steps;
   auto touch = [&](int i) {  // one line per thread and step at most (lines past NT a step are left untouched)
     const uint32_t line = i * pf_per_step + tid;
-    if (tid < pf_per_step && line < pf_lines) {
+    if (PF && tid < pf_per_step && line < pf_lines) {
       const uint32_t la = (uint32_t)(uintptr_t)(lds_void_t *)(lds + LDS_BYTES);
       asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(line << 7), "s"(pf_base), "s"(la)
                    : "memory", "m0");
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
       return;
     }
     const int key0 = (t0 + i) * KT;
-    if (key0 + KT > p.nvalid) {
+    if (!FULL && key0 + KT > p.nvalid) {
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; kb2++)
 #pragma unroll
@@ -257,7 +262,7 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
     // the next tiles' loads after the QK / exponential block, not ahead of it (their issue would delay the softmax)
     if (i + 2 < nmine) load_kv(i + 2, true, false);
     if (i + 1 < nmine) load_kv(i + 1, false, true);
-    if (i < pf_steps) touch(i);
+    if (PF && i < pf_steps) touch(i);
     half8_t va[2];
     __builtin_amdgcn_sched_barrier(0);
     va[0] = vfrag(0);
@@ -411,13 +416,15 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   static bool attr = false;
   static int num_cu = 0;
   if (!attr) {
-    if (hipFuncSetAttribute((const void *)attn_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            LDS_BYTES + SINK_BYTES) != hipSuccess ||
-        hipFuncSetAttribute((const void *)attn_kernel<3>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            LDS_BYTES + SINK_BYTES) !=
-            hipSuccess ||
-        hipFuncSetAttribute((const void *)attn_short_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, SK_LDS) !=
-            hipSuccess)
+    const void *kerns[] = {(const void *)attn_kernel<4, false, false>, (const void *)attn_kernel<4, false, true>,
+                           (const void *)attn_kernel<4, true, false>,  (const void *)attn_kernel<4, true, true>,
+                           (const void *)attn_kernel<3, false, false>, (const void *)attn_kernel<3, false, true>,
+                           (const void *)attn_kernel<3, true, false>,  (const void *)attn_kernel<3, true, true>};
+    for (const void *kf : kerns)
+      if (hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES + SINK_BYTES) != hipSuccess)
+        return HXA_E_HIP;
+    if (hipFuncSetAttribute((const void *)attn_short_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, SK_LDS) !=
+        hipSuccess)
       return HXA_E_HIP;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, dev) !=
@@ -443,8 +450,19 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   }
   const bool small = fill(96) > fill(128) + 1e-9;
   const int QB = small ? 96 : 128, nqb = (p.T + QB - 1) / QB;
+  const bool full = p.nvalid % KT == 0, pf = p.pf_bytes > 0;
   dim3 grid(nqb * p.H, p.batch);
-  if (small) hxa_launch(attn_kernel<3>, grid, dim3(384), LDS_BYTES + SINK_BYTES, st, pk, nqb);
-  else hxa_launch(attn_kernel<4>, grid, dim3(512), LDS_BYTES + SINK_BYTES, st, pk, nqb);
+  const int lds = LDS_BYTES + SINK_BYTES;
+  if (small) {
+    if (full) pf ? hxa_launch(attn_kernel<3, true, true>, grid, dim3(384), lds, st, pk, nqb)
+              : hxa_launch(attn_kernel<3, true, false>, grid, dim3(384), lds, st, pk, nqb);
+    else pf ? hxa_launch(attn_kernel<3, false, true>, grid, dim3(384), lds, st, pk, nqb)
+            : hxa_launch(attn_kernel<3, false, false>, grid, dim3(384), lds, st, pk, nqb);
+  } else {
+    if (full) pf ? hxa_launch(attn_kernel<4, true, true>, grid, dim3(512), lds, st, pk, nqb)
+              : hxa_launch(attn_kernel<4, true, false>, grid, dim3(512), lds, st, pk, nqb);
+    else pf ? hxa_launch(attn_kernel<4, false, true>, grid, dim3(512), lds, st, pk, nqb)
+            : hxa_launch(attn_kernel<4, false, false>, grid, dim3(512), lds, st, pk, nqb);
+  }
   return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
 }
