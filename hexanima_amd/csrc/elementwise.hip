@@ -1198,6 +1198,16 @@ int hxa_set_sigma_launch(float *sig, float s0, float s1, hipStream_t st) {
   hxa_launch(set_sigma_kernel, dim3(1), dim3(64), 0, st, sig, s0, s1);
   return LAUNCH_OK();
 }
+// n floats from host-mapped pinned memory into device memory on the compute queue (16 bytes per thread; n % 4 == 0)
+__global__ void copy_f4_kernel(const float4_t *__restrict__ src, float4_t *__restrict__ dst, int n4) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n4) dst[i] = src[i];
+}
+int hxa_copy_f32_launch(const float *src, float *dst, int n, hipStream_t st) {
+  if (n % 4) return HXA_E_ARG;
+  hxa_launch(copy_f4_kernel, dim3((n / 4 + 255) / 256), dim3(256), 0, st, (const float4_t *)src, (float4_t *)dst, n / 4);
+  return LAUNCH_OK();
+}
 int hxa_sinusoid_launch(const float *t, int n, int dim, float *out, hipStream_t st) {
   hxa_launch(sinusoid_kernel, dim3(nblk((long)n * dim / 2)), dim3(256), 0, st, t, n, dim, out);
   return LAUNCH_OK();

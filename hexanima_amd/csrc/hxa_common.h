@@ -16,16 +16,18 @@ typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
 
 #define HXA_DEV __device__ __forceinline__
 
-// Stage timing of a block run (host side, per thread): while hxa_t_stage_event is set, every launch binds it as
-// its stop event (hipExtLaunchKernel), so the event completes with the last kernel of the stage and no marker packet
-// sits between the kernels. hxa_t_stage_launches counts the launches since the event was set.
-extern thread_local hipEvent_t hxa_t_stage_event;
+// Stage timing of a block run (host side, per thread). While hxa_t_stage_event is set, every launch binds it as its
+// stop event (hipExtLaunchKernel), so the event completes with the last kernel of the stage; hxa_t_start_event, when
+// set, is bound as the start event of the next launch only (the start of the first stage). No marker packet sits
+// between the kernels. hxa_t_stage_launches counts the launches since the stage event was set.
+extern thread_local hipEvent_t hxa_t_stage_event, hxa_t_start_event;
 extern thread_local int hxa_t_stage_launches;
 template <typename F, typename... Args>
 inline void hxa_launch(F kernel, const dim3 &grid, const dim3 &block, uint32_t shmem, hipStream_t st, Args... args) {
-  if (hxa_t_stage_event != nullptr) {
+  if (hxa_t_stage_event != nullptr || hxa_t_start_event != nullptr) {
     ++hxa_t_stage_launches;
-    hipExtLaunchKernelGGL(kernel, grid, block, shmem, st, nullptr, hxa_t_stage_event, 0, args...);
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, st, hxa_t_start_event, hxa_t_stage_event, 0, args...);
+    hxa_t_start_event = nullptr;
   } else {
     hipLaunchKernelGGL(kernel, grid, block, shmem, st, args...);
   }

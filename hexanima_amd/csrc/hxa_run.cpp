@@ -215,17 +215,26 @@ int main(int argc, char **argv) {
         if (first_run < 0) first_run = k;
         last_run = k;
       }
+    // stage times are asked for where they are read: block 5 under HXA_RUN_DBG, as megarun logs them under MEGA_DBG
+    // (megarun.cpp:182); a call without times returns once its block is queued, so the chain runs back to back
     int times[32];
+    const bool dbg = getenv("HXA_RUN_DBG") != nullptr;
     for (int k = 0; k < count && ok; k++) {
       if ((skip >> (first + k)) & 1u) continue;
       blob.meta[M_FIRST] = k == first_run;
       blob.meta[M_REL] = k == last_run;
       int rc = 0;
+      const bool timed = dbg && k == 5;
+      const double tm1 = now_s();
       const int r = mega_block(h, blob.meta, M_NMETA, wfd[k], BLOB_FD, (const uint8_t *)&mod[(size_t)k * 9 * D], 9 * D * 4,
-                               times, 32, &rc);
+                               timed ? times : nullptr, timed ? 32 : 0, &rc);
       if (r || rc) {
         fprintf(stderr, "block %d failed r=%d rc=%d: %s\n", first + k, r, rc, hxa_last_error());
         ok = false;
+      } else if (timed) {
+        fprintf(stderr, "blk5 stages(us):");
+        for (int q = 0; q < 25; q++) fprintf(stderr, " %d", times[q]);
+        fprintf(stderr, " | call %.1f ms\n", (now_s() - tm1) * 1e3);
       }
     }
     const double t_blocks = now_s();

@@ -122,6 +122,7 @@ int hxa_fill_const_launch(void *dst, int dtype, size_t n, float v, hipStream_t s
 // caller-side glue (phone/animad.cpp)
 // sig[0..3] = {s0, s1, s1 - s0, 0} on the stream (the DiT step's sigma values)
 int hxa_set_sigma_launch(float *sig, float s0, float s1, hipStream_t st);
+int hxa_copy_f32_launch(const float *src, float *dst, int n, hipStream_t st);
 int hxa_patchify_launch(const float *lat, int B, int Cc, int H, int W, float *tok, hipStream_t st);
 // patch embed straight from the latent: x + (b * xrows + tk) * N <- the patchified token tk of image b times Wemb^T
 // (Wemb [N][4 Cc] fp16), all B images in one launch

@@ -567,21 +567,50 @@ struct ThreadEvents {
 };
 static thread_local ThreadEvents t_events;
 
-thread_local hipEvent_t hxa_t_stage_event = nullptr;
+thread_local hipEvent_t hxa_t_stage_event = nullptr, hxa_t_start_event = nullptr;
 thread_local int hxa_t_stage_launches = 0;
 
-// Stage i's time is the interval from event i to event i+1: event 0 is recorded before the first stage, event i+1
-// completes with the last kernel stage i launched (bound to its launches through hxa_t_stage_event), or is recorded
-// as a marker when the stage launched nothing.
+// Wait for a stream by polling it: a blocking synchronisation wakes the caller tens of microseconds after the work
+// ends, which the reference ABI's one-call-per-block protocol pays on every block.
+static hipError_t spin_wait(hipStream_t st) {
+  for (;;) {
+    const hipError_t e = hipStreamQuery(st);
+    if (e != hipErrorNotReady) return e;
+  }
+}
+
+// Stage times from events that ride on the kernel launches (no marker packets between the kernels): the pool's
+// event 0 is the start event of the block's first launch; each stage that launches kernels binds the next pool event
+// as their stop event, so stage i ends when its last kernel completes. A stage that launches nothing (its work fused
+// into another stage's kernel) is reported as 0 and the next stage is timed from the last event before it.
+// With t_stage_defer set (mega_block) the destructor neither waits nor reads: it leaves the record in t_stage_rec,
+// read with read_stages() once the caller has waited for the stream.
+struct StageRecord {
+  hipEvent_t *ev = nullptr;
+  int n = 0, count = 0;
+  int end_ev[32];
+};
+static thread_local StageRecord t_stage_rec;
+static thread_local bool t_stage_defer = false;
+static void read_stages(const StageRecord &r, int *us) {
+  for (int i = 0; i < r.n; i++) {
+    float ms = 0.0f;
+    const int a = i == 0 ? 0 : r.end_ev[i - 1], b = i < r.count ? r.end_ev[i] : a;
+    if (r.ev && a != b && hipEventElapsedTime(&ms, r.ev[a], r.ev[b]) == hipSuccess) us[i] = (int)lrintf(ms * 1000.0f);
+    else us[i] = 0;
+  }
+}
 struct StageTimer {
   int *us;
   int n;
   hipStream_t st;
+  bool defer;
   hipEvent_t *ev = nullptr;
-  int count = 0;
-  StageTimer(int *u, int nn, hipStream_t s) : us(u), n(nn), st(s) {
+  int count = 0, next = 1;
+  int end_ev[32];  // pool index of the event that ends stage k
+  StageTimer(int *u, int nn, hipStream_t s) : us(u), n(nn), st(s), defer(t_stage_defer) {
     if (!us) return;
-    if (n < 1) {
+    if (n < 1 || n > 31) {
       us = nullptr;
       return;
     }
@@ -601,26 +630,41 @@ struct StageTimer {
       return;
     }
     ev = pool.data();
-    (void)hipEventRecord(ev[0], st);
+    hxa_t_start_event = ev[0];
     hxa_t_stage_event = ev[1];
     hxa_t_stage_launches = 0;
   }
   void tick() {
     count++;
     if (!us || count > n) return;
-    if (hxa_t_stage_launches == 0) (void)hipEventRecord(ev[count], st);
-    hxa_t_stage_event = count < n ? ev[count + 1] : nullptr;
+    if (hxa_t_start_event != nullptr) {  // nothing launched yet: the start is here
+      (void)hipEventRecord(ev[0], st);
+      hxa_t_start_event = nullptr;
+    }
+    if (hxa_t_stage_launches > 0) {
+      end_ev[count - 1] = next;
+      next++;
+    } else {
+      end_ev[count - 1] = count >= 2 ? end_ev[count - 2] : 0;
+    }
+    hxa_t_stage_event = count < n ? ev[next] : nullptr;
     hxa_t_stage_launches = 0;
   }
   ~StageTimer() {
     if (!us) return;
     hxa_t_stage_event = nullptr;
-    (void)hipStreamSynchronize(st);
-    for (int i = 0; i < n; i++) {
-      float ms = 0.0f;
-      if (i < count && hipEventElapsedTime(&ms, ev[i], ev[i + 1]) == hipSuccess) us[i] = (int)lrintf(ms * 1000.0f);
-      else us[i] = 0;
+    hxa_t_start_event = nullptr;
+    StageRecord r;
+    r.ev = ev;
+    r.n = n;
+    r.count = count < n ? count : n;
+    for (int i = 0; i < r.count; i++) r.end_ev[i] = end_ev[i];
+    if (defer) {
+      t_stage_rec = r;
+      return;
     }
+    (void)hipStreamSynchronize(st);
+    read_stages(r, us);
   }
 };
 
@@ -1082,7 +1126,8 @@ struct Ctx {
   float *mod_dev = nullptr, *emb_dev = nullptr, *h1_dev = nullptr;
   const hxa_h **modw_ptrs = nullptr;  // device table of the modulation weights of one hxa_anima_modulation call
   size_t modw_ptrs_bytes = 0;
-  float *mod_pin = nullptr;  // pinned staging of mega_block's modulation vectors (9 x 3072 fp32 at most)
+  float *mod_pin = nullptr;  // pinned, device-mapped staging of mega_block's modulation vectors (9 x 3072 fp32 at most)
+  float *mod_pin_dev = nullptr;  // its device address
   hipEvent_t mod_ev = nullptr;  // recorded after the copy out of mod_pin; waited for before mod_pin is rewritten
   size_t mod_dev_bytes = 0, emb_dev_bytes = 0, h1_dev_bytes = 0;
   // device-resident activations of the current run of blocks
@@ -1311,6 +1356,7 @@ struct BlockCall {
 int run_ref_block(Ctx *c, const BlockCall &bc, const DevBlock &db, const HostBuf &blob, const float *modh, int modlen,
                   int *times, int ntimes) {
   const auto t_entry = std::chrono::steady_clock::now();
+  if (ntimes <= 0) times = nullptr;
   hipStream_t st = c->st;
   hxa_block_dims d = db.dims;
   d.T = bc.T;
@@ -1350,21 +1396,30 @@ int run_ref_block(Ctx *c, const BlockCall &bc, const DevBlock &db, const HostBuf
     c->cur_T = bc.T;
     c->cur_C = bc.C;
   }
-  // the modulation through pinned memory: an asynchronous DMA instead of a staged pageable copy. The previous
-  // call's copy out of mod_pin may still be in flight when that call returned early on an error, so its event is
-  // waited for before the buffer is rewritten.
+  // The modulation through pinned, device-mapped memory, copied to the device by a kernel on the block's own queue:
+  // the first kernel then waits for no DMA engine. The previous call's copy may still be queued (a call without
+  // times returns before its work has run), so its event is waited for before the buffer is rewritten.
   const size_t modb = (size_t)(d.kind == 0 ? 9 : 6) * D * 4;
-  if (!c->mod_pin) HIPC(hipHostMalloc((void **)&c->mod_pin, (size_t)9 * 3072 * 4, hipHostMallocDefault));
+  if (!c->mod_pin) {
+    HIPC(hipHostMalloc((void **)&c->mod_pin, (size_t)9 * 3072 * 4, hipHostMallocMapped));
+    HIPC(hipHostGetDevicePointer((void **)&c->mod_pin_dev, c->mod_pin, 0));
+  }
   if (!c->mod_ev) HIPC(hipEventCreateWithFlags(&c->mod_ev, hipEventDisableTiming));
   if (modb > (size_t)9 * 3072 * 4) return fail(HXA_E_META, "modulation of %zu bytes", modb);
   HIPC(hipEventSynchronize(c->mod_ev));
   memcpy(c->mod_pin, modh, modb);
-  HIPC(hipMemcpyAsync(c->mod, c->mod_pin, modb, hipMemcpyHostToDevice, st));
+  TRY(hxa_copy_f32_launch(c->mod_pin_dev, c->mod, (int)(modb / 4), st));
   HIPC(hipEventRecord(c->mod_ev, st));
   int us[16] = {0};
   const int nst = d.kind == 0 ? 13 : 8;
   const auto t_work = std::chrono::steady_clock::now();
-  TRY(hxa_block_run(&d, db.pack, c->x, c->ctx, c->mod, c->cosr, c->sinr, c->ws, bc.stop, times ? us : nullptr, nst, st));
+  // the stage times are read after this call's one wait below (not by the block run's own synchronisation)
+  t_stage_defer = times != nullptr;
+  t_stage_rec = StageRecord{};
+  const int brc = hxa_block_run(&d, db.pack, c->x, c->ctx, c->mod, c->cosr, c->sinr, c->ws, bc.stop, times ? us : nullptr,
+                                nst, st);
+  t_stage_defer = false;
+  TRY(brc);
   if (bc.stop) {  // stage buffers back to the blob as h16 tiles (what cmp_blk.py reads)
     const WsLayout L = ws_layout(&d);
     const int which[9] = {WS_H, WS_Q, WS_K, WS_VT, WS_O, WS_T1, WS_MID, WS_CK, WS_CVT};
@@ -1385,7 +1440,12 @@ int run_ref_block(Ctx *c, const BlockCall &bc, const DevBlock &db, const HostBuf
     TRY(hxa_rows_to_x32_launch(c->x, c->stage, bc.T, D, st));
     HIPC(hipMemcpyAsync((char *)blob.ptr + bc.off_x, c->stage, xb, hipMemcpyDeviceToHost, st));
   }
-  HIPC(hipStreamSynchronize(st));
+  // A call that neither stops nor releases and asks for no times returns once its work is queued: the next call's
+  // work follows it on the stream, and the releasing call's wait covers every block of the chain (an error of a
+  // queued block is reported by the next call that waits).
+  if (!times && !bc.stop && !bc.rel) return HXA_OK;
+  HIPC(spin_wait(st));
+  if (times) read_stages(t_stage_rec, us);
   if (times) {
     for (int i = 0; i < ntimes; i++) times[i] = 0;
     for (int i = 0; i < nst && i < ntimes && i < 17; i++) times[i] = us[i];

@@ -49,7 +49,11 @@ int mega_close(remote_handle64 h);
  *   *rc      : 0 or a status code; the return value is 0 as in the reference.
  * meta[M_FIRST] uploads x / ctx / cos / sin from the blob to device-resident copies; meta[M_REL] writes x back
  * to the blob (x32 tiles). Weights are converted to the GPU layout and uploaded on first use, then stay resident.
- * meta[M_STOP] = n stops after n stages and writes the stage buffers (h,q,k,v,o,t,mid,ck,cv) back to the blob. */
+ * meta[M_STOP] = n stops after n stages and writes the stage buffers (h,q,k,v,o,t,mid,ck,cv) back to the blob.
+ * A call with times == NULL (or ntimes <= 0) that neither stops nor releases returns once its block is queued on the
+ * handle's stream (mod has been copied by then); the next call's block follows it, and the releasing call waits for
+ * the whole chain. An execution error of a queued block is reported by the next call that waits. Calls on one handle
+ * must not overlap. */
 int mega_block(remote_handle64 h, const int *meta, int nmeta, int wfd, int bfd, const uint8_t *mod, int modlen, int *times,
                int ntimes, int *rc);
 /* the MOSS build of the same entry (moss/hexagon/mega/blk.c:269-281) with the MOSS meta enum
