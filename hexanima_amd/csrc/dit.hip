@@ -12,12 +12,20 @@
 // RMSNorm'd 2048-wide sinusoid and its LoRA MLP (animad.cpp:424-431), low-rank per-block modulation
 // (megarun.cpp:156-171) and final adaLN (animad.cpp:475-479); MOSS: the time MLP with biases, shared block and head
 // modulation (mossrun.cpp:255-264), the rapid-moss sampler's latent mix and video embedding, the RMS head and
-// x0 = z - v (mossrun.cpp:307-334), BN denorm + unpatchify of the result (mossrun.cpp:339-343).
+// x0 = z - v (mossrun.cpp:307-334), BN denorm + unpatchify of the result (mossrun.cpp:339-343). The reference form
+// keeps each glue tensor in the reference's storage type: fp16 for Anima (phone/extract_small.py) and for the MOSS
+// modulation matrices, fp32 for the MOSS time MLP, video embedding and head (moss/export_glue.py:7-12).
+// Real weights come in through hxa_dit_load_block (Anima blkNN.bin), hxa_dit_load_anima_glue (small.bin) and
+// hxa_dit_load_moss_glue (glue.bin, MGL1).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
+#include <map>
+#include <string>
 #include <vector>
 
 #include "../../include/hexanima_hip.h"
@@ -40,7 +48,7 @@ struct Dit {
   long pack_bytes = 0;
   hxa_h *modw_all = nullptr;  // one allocation: every block's modulation weights, stacked
   std::vector<hxa_h *> modw;  // Anima: per block [6D][D]; MOSS: one shared [6D][D]
-  hxa_h *glue = nullptr;      // x_embed [D][4C] | t_embed [D][temb] | final_mod [2D][D] | final_lin [4C][D] | text_proj
+  hxa_h *glue = nullptr;      // fp16 glue matrices (layout per form below)
   long glue_elems = 0;
   hxa_h *Wemb = nullptr, *L1 = nullptr, *Lf = nullptr, *Wfin = nullptr, *Wtxt = nullptr;
   hxa_h *Wfin4 = nullptr;  // Wfin k-tiled by 4 ([D/4][4C][4]), what the final layer's kernel reads
@@ -54,10 +62,15 @@ struct Dit {
   // form 1 (the reference's glue): fp16 matrices inside `glue`, fp32 vectors in `vec`, per-step vectors below
   int form = 0;
   hxa_h *Wl2 = nullptr, *F1 = nullptr, *F2 = nullptr, *tnorm = nullptr, *T2 = nullptr, *Wh = nullptr;
-  float *vec = nullptr;  // MOSS: b_video [D] | b_t0 [D] | b_t2 [D] | b_smod [6D] | b_hmod [2D] | final_norm [D] | Q [4C][4C] | bn mean, var [4C]
+  // MOSS: b_video [D] | b_t0 [D] | b_t2 [D] | b_smod [6D] | b_hmod [2D] | final_norm [D] | Q [4C][4C] | bn mean,
+  // var [4C] | video_embed [D][4C] | t0 [D][256] | t2 [D][D] | final_lin [4C][D], all fp32
+  float *vec = nullptr;
   long vec_elems = 0;
   float *bve = nullptr, *b0 = nullptr, *b2 = nullptr, *bm = nullptr, *bh = nullptr, *nfin = nullptr, *Q = nullptr;
   float *bnm = nullptr, *bnv = nullptr;
+  float *Wv32 = nullptr, *T0f = nullptr, *T2f = nullptr, *Wfin32 = nullptr;  // the fp32 matrices inside vec
+  float *Wfin4f = nullptr;                                                    // Wfin32 k-tiled by 4
+  float bands[16];  // MOSS RoPE bands (rope.bands of glue.bin); synthetic 10000^(-i/16) until one is loaded
   float *emb = nullptr, *a1 = nullptr, *lora = nullptr, *h1 = nullptr;  // t-embedding work vectors
   float *zrows = nullptr, *x0rows = nullptr;  // rapid-moss state: noise z and clean estimate x0, token rows [B*T][4C]
   long modw_block = 0;                        // elements of one block's modulation weights
@@ -106,9 +119,10 @@ void rope_anima(int gh, int gw, std::vector<float> &c, std::vector<float> &s) {
   }
 }
 // moss_ref.py:27-35: 4 axes x 16 bands; image (0, ntxt, h-(H-1)/2, w-(W-1)/2), text (0, i, 0, 0);
-// synthetic bands 10000^(-i/16); padding rows get the identity rotation
+// padding rows get the identity rotation
 // image positions times `scale`: 1 on the full grid, MOSS_LOWSCALE (2) on the low-res steps' (mossrun.cpp:190-201, :313)
-void rope_moss(int H, int W, int ntxt, int Ttot, std::vector<float> &c, std::vector<float> &s, double scale = 1.0) {
+void rope_moss(int H, int W, int ntxt, int Ttot, const float *bands, std::vector<float> &c, std::vector<float> &s,
+               double scale = 1.0) {
   c.assign((size_t)Ttot * 64, 1.0f);
   s.assign((size_t)Ttot * 64, 0.0f);
   const int nimg = H * W;
@@ -125,7 +139,7 @@ void rope_moss(int H, int W, int ntxt, int Ttot, std::vector<float> &c, std::vec
       pos[2] = pos[3] = 0;
     }
     for (int d = 0; d < 64; d++) {
-      const double band = (double)(float)(1.0 / pow(10000.0, (d % 16) / 16.0));
+      const double band = (double)bands[d % 16];
       const double ph = pos[d / 16] * band;
       c[(size_t)tk * 64 + d] = (float)cos(ph);
       s[(size_t)tk * 64 + d] = (float)sin(ph);
@@ -207,8 +221,8 @@ int record_prelude_anima_ref(Dit &d) {
 int record_prelude_moss_ref(Dit &d) {
   const int D = d.bd.D, temb = d.cfg.temb;
   hipStream_t st = d.st;
-  DTRY(hxa_linear_f32_launch(d.sig, temb, 1, temb, d.L1, D, d.a1, D, 2, d.b0, 0, 0, st));  // sinusoid in the GEMV
-  DTRY(hxa_linear_f32_launch(d.a1, D, 1, D, d.T2, D, d.emb, D, 1, d.b2, 0, 0, st));
+  DTRY(hxa_linear_w32_launch(d.sig, temb, 1, temb, d.T0f, D, d.a1, D, 2, d.b0, 0, 0, st));  // sinusoid in the GEMV
+  DTRY(hxa_linear_w32_launch(d.a1, D, 1, D, d.T2f, D, d.emb, D, 1, d.b2, 0, 0, st));
   DTRY(hxa_linear_f32_launch(d.emb, D, 1, D, d.modw_all, 6 * D, d.mods, 6 * D, 0, d.bm, 0, 0, st));
   DTRY(hxa_linear_f32_launch(d.emb, D, 1, D, d.Wh, 2 * D, d.fmod, 2 * D, 0, d.bh, 0, 0, st));
   return HXA_OK;
@@ -263,7 +277,7 @@ int record_step(Dit &d, const Pass &ps) {
   }
   // patch embed (rapid-moss: latent mix + video embedding of the token rows) (+ MOSS text tokens)
   if (moss_ref)
-    DTRY(hxa_moss_embed_launch(ps.zrows, ps.x0rows, d.Q, d.Wemb, d.bve, d.x, B, ps.Timg, ps.Ttot, D, C4, st));
+    DTRY(hxa_moss_embed_launch(ps.zrows, ps.x0rows, d.Q, d.Wv32, 1, d.bve, d.x, B, ps.Timg, ps.Ttot, D, C4, st));
   else
     DTRY(hxa_patch_embed_launch(ps.lat_in, B, d.cfg.lat_c, ps.lat_h, ps.lat_w, d.Wemb, D, d.x, ps.Ttot, st));
   for (int i = 0; i < B; i++) {
@@ -303,8 +317,8 @@ int record_step(Dit &d, const Pass &ps) {
   }
   // final layer (+ Euler update); rapid-moss: RMS head and x0 = z - v
   if (moss_ref)
-    DTRY(hxa_final_launch(d.x, B, ps.Timg, ps.Ttot, D, d.fmod, d.fmod + D, d.Wfin4, d.cfg.lat_c, ps.lat_h, ps.lat_w,
-                          d.vel, nullptr, st, d.nfin, ps.x0rows, ps.zrows));
+    DTRY(hxa_final_launch(d.x, B, ps.Timg, ps.Ttot, D, d.fmod, d.fmod + D, d.Wfin4f, d.cfg.lat_c, ps.lat_h, ps.lat_w,
+                          d.vel, nullptr, st, d.nfin, ps.x0rows, ps.zrows, 1));
   else
     DTRY(hxa_final_launch(d.x, B, ps.Timg, ps.Ttot, D, d.fmod, d.fmod + D, d.Wfin4, d.cfg.lat_c, ps.lat_h, ps.lat_w,
                           ps.lat_out, ps.dtp, st));
@@ -387,18 +401,21 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   for (size_t k = 0; k < d.modw.size() && d.modw_all; k++) d.modw[k] = d.modw_all + (anima_ref ? 768L * D : d.modw_block) * (long)k;
   // fp16 glue. config form: x_embed [D][4C] | t_embed [D][temb] | final_mod [2D][D] | final_lin [4C][D] | MOSS
   // text_proj [D][ntxt_in]. Reference form, Anima: x_embed | t_l1 [D][D] | t_l2 [3D][D] | f1 [256][D] | f2 [2D][256]
-  // | final_lin | t_norm [D]; MOSS: video_embed [D][4C] | t0 [D][256] | t2 [D][D] | head_mod [2D][D] | final_lin |
-  // text_proj
+  // | final_lin | t_norm [D]; MOSS: head_mod [2D][D] | text_proj (its other matrices are fp32, in vec)
+  const bool moss_ref = d.form == 1 && b.kind == 1;
   if (d.form == 0)
     d.glue_elems = (long)D * C4 + (long)D * cfg->temb + 2L * D * D + (long)C4 * D + (b.kind == 1 ? (long)D * cfg->ntxt_in : 0);
   else if (b.kind == 0)
     d.glue_elems = (long)D * C4 + (long)D * D + 3L * D * D + 256L * D + 2L * D * 256 + (long)C4 * D + D;
   else
-    d.glue_elems = (long)D * C4 + (long)D * 256 + (long)D * D + 2L * D * D + (long)C4 * D + (long)D * cfg->ntxt_in;
+    d.glue_elems = 2L * D * D + (long)D * cfg->ntxt_in;
   M((void **)&d.glue, 2 * d.glue_elems);
-  M((void **)&d.Wfin4, 2L * C4 * D);
+  if (moss_ref) M((void **)&d.Wfin4f, 4L * C4 * D);
+  else M((void **)&d.Wfin4, 2L * C4 * D);
+  for (int i = 0; i < 16; i++) d.bands[i] = (float)(1.0 / pow(10000.0, i / 16.0));
   if (d.form == 1) {
-    d.vec_elems = b.kind == 0 ? 0 : 3L * D + 6L * D + 2L * D + D + (long)C4 * C4 + 2L * C4;
+    d.vec_elems = b.kind == 0 ? 0 : 3L * D + 6L * D + 2L * D + D + (long)C4 * C4 + 2L * C4 + (long)D * C4 + 256L * D +
+                                        (long)D * D + (long)C4 * D;
     if (d.vec_elems) M((void **)&d.vec, 4 * d.vec_elems);
     M((void **)&d.emb, 4L * D);
     M((void **)&d.a1, 4L * D);
@@ -441,8 +458,10 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   if (rc == HXA_OK)
     rc = hxa_fill_normal_launch(d.modw_all, 1, d.modw_block * (long)d.modw.size(), seed * 7919ull + 100000, 0.0f, 0.02f, d.st);
   if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.glue, 1, d.glue_elems, seed * 7919ull + 99999, 0.0f, 0.02f, d.st);
-  d.Wemb = d.glue;
-  d.L1 = d.Wemb + (long)D * C4;
+  if (!moss_ref) {
+    d.Wemb = d.glue;
+    d.L1 = d.Wemb + (long)D * C4;
+  }
   if (d.form == 0) {
     d.Lf = d.L1 + (long)D * cfg->temb;
     d.Wfin = d.Lf + 2L * D * D;
@@ -455,10 +474,8 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
     d.tnorm = d.Wfin + (long)C4 * D;  // RMSNorm weight of the t-embedding, fp16 like the reference's tensors
     if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.tnorm, 1, D, seed * 7919ull + 99998, 1.0f, 0.1f, d.st);
   } else {
-    d.T2 = d.L1 + 256L * D;
-    d.Wh = d.T2 + (long)D * D;
-    d.Wfin = d.Wh + 2L * D * D;
-    d.Wtxt = d.Wfin + (long)C4 * D;
+    d.Wh = d.glue;
+    d.Wtxt = d.Wh + 2L * D * D;
     d.bve = d.vec;
     d.b0 = d.bve + D;
     d.b2 = d.b0 + D;
@@ -468,6 +485,10 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
     d.Q = d.nfin + D;
     d.bnm = d.Q + (long)C4 * C4;
     d.bnv = d.bnm + C4;
+    d.Wv32 = d.bnv + C4;
+    d.T0f = d.Wv32 + (long)D * C4;
+    d.T2f = d.T0f + 256L * D;
+    d.Wfin32 = d.T2f + (long)D * D;
     // biases and the latent mix N(0, 0.02); the head's RMSNorm weight and the BN variance around 1, the BN mean
     // around 0 (N(0, 0.1))
     const uint64_t vs = seed * 7919ull + 99997;
@@ -476,8 +497,11 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
     if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.nfin, 0, D, vs + 1, 1.0f, 0.1f, d.st);
     if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.bnm, 0, C4, vs + 2, 0.0f, 0.1f, d.st);
     if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.bnv, 0, C4, vs + 3, 1.0f, 0.1f, d.st);
+    // the fp32 matrices N(0, 0.02)
+    if (rc == HXA_OK)
+      rc = hxa_fill_normal_launch(d.Wv32, 0, (long)D * C4 + 256L * D + (long)D * D + (long)C4 * D, vs + 5, 0.0f, 0.02f, d.st);
   }
-  if (rc == HXA_OK) rc = hxa_ktile4_launch(d.Wfin, C4, D, d.Wfin4, d.st);
+  if (rc == HXA_OK) rc = moss_ref ? hxa_ktile4_f32_launch(d.Wfin32, C4, D, d.Wfin4f, d.st) : hxa_ktile4_launch(d.Wfin, C4, D, d.Wfin4, d.st);
   if (rc == HXA_OK) rc = hxa_fill_const_launch(d.ones, 0, D, 1.0f, d.st);
   if (rc == HXA_OK && b.kind == 0) {  // site-1 rows of every block: shift 0, scale 0, gate 1
     for (int k = 0; k < cfg->nblocks && rc == HXA_OK; k++) {
@@ -491,7 +515,7 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
     // token (gy, gx) of a gh x gw grid, gh = H/2 rows (megarun's gh, gw arguments)
     rope_anima(cfg->lat_h / 2, cfg->lat_w / 2, c, s);
   } else {
-    rope_moss(cfg->lat_h / 2, cfg->lat_w / 2, d.ntxt, d.Ttot, c, s);
+    rope_moss(cfg->lat_h / 2, cfg->lat_w / 2, d.ntxt, d.Ttot, d.bands, c, s);
   }
   if (rc == HXA_OK && (hipMemcpyAsync(d.cosT, c.data(), 4 * c.size(), hipMemcpyHostToDevice, d.st) != hipSuccess ||
                        hipMemcpyAsync(d.sinT, s.data(), 4 * s.size(), hipMemcpyHostToDevice, d.st) != hipSuccess))
@@ -555,7 +579,7 @@ extern "C" int hxa_dit_destroy(void *p) {
   if (d->modw_all) (void)hipFree(d->modw_all);
   void *bufs[] = {d->glue, d->lat, d->vel, d->x, d->sinus, d->cvec, d->mods, d->fmod, d->sig, d->cosT, d->sinT,
                   d->ones, d->ctx16, d->ws, d->vec, d->emb, d->a1, d->lora, d->h1, d->zrows, d->x0rows, d->tkv,
-                  d->tkv_par, d->Wfin4};
+                  d->tkv_par, d->Wfin4, d->Wfin4f};
   for (void *q : bufs) if (q) (void)hipFree(q);
   if (d->st) (void)hipStreamDestroy(d->st);
   delete d;
@@ -658,7 +682,7 @@ int low_rope(Dit &d, int f, double scale) {
   const int gh = d.cfg.lat_h / 2 / f, gw = d.cfg.lat_w / 2 / f;
   const int Ttot = moss ? (gh * gw + d.ntxt + 31) / 32 * 32 : gh * gw;
   std::vector<float> c, sn;
-  if (moss) rope_moss(gh, gw, d.ntxt, Ttot, c, sn, scale);
+  if (moss) rope_moss(gh, gw, d.ntxt, Ttot, d.bands, c, sn, scale);
   else rope_anima(gh, gw, c, sn);
   if (!d.cosL[f]) {
     DHIP(hipMalloc((void **)&d.cosL[f], 4L * Ttot * 64));
@@ -824,10 +848,224 @@ extern "C" int hxa_dit_import(void *p, int which, const void *host, size_t bytes
     if (q.n) DHIP(hipMemcpy(q.dst, in, q.n, hipMemcpyHostToDevice));
     in += q.n;
   }
-  if (which == 2 * nb) {  // the final layer's kernel reads its weights k-tiled by 4
-    DTRY(hxa_ktile4_launch(d.Wfin, 4 * d.cfg.lat_c, D, d.Wfin4, d.st));
-    DHIP(hipStreamSynchronize(d.st));
+  // the final layer's kernel reads its weights k-tiled by 4
+  if (which == 2 * nb && d.Wfin) DTRY(hxa_ktile4_launch(d.Wfin, 4 * d.cfg.lat_c, D, d.Wfin4, d.st));
+  if (which == 2 * nb + 1 && d.Wfin32) DTRY(hxa_ktile4_f32_launch(d.Wfin32, 4 * d.cfg.lat_c, D, d.Wfin4f, d.st));
+  DHIP(hipStreamSynchronize(d.st));
+  return HXA_OK;
+}
+
+namespace {
+// host bytes -> device, through one synchronous copy
+int upload(void *dst, const void *src, size_t bytes) {
+  if (bytes && hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) != hipSuccess) return dfail(HXA_E_HIP, "dit: weight upload");
+  return HXA_OK;
+}
+// tensors of a glue file: name -> (dtype 0 fp32 / 1 fp16, dims, data)
+struct GlueTensor {
+  int dtype = 0;
+  std::vector<long> dims;
+  const uint8_t *data = nullptr;
+  long elems() const {
+    long n = 1;
+    for (long v : dims) n *= v;
+    return n;
   }
+};
+bool shape_is(const GlueTensor &t, std::initializer_list<long> want) {
+  return t.dims.size() == want.size() && std::equal(want.begin(), want.end(), t.dims.begin());
+}
+}  // namespace
+
+// blk_wlayout.h:3-20: matrix offsets of an Anima blkNN.bin (q8 files: WQ(x) = x / 2048 * 1152), the adaLN modulation
+// weights at W_MODW / WQ_MODW: per site A [256][2048] then B [6144][256], fp16 (export_all.py:59-61)
+extern "C" int hxa_dit_load_block(void *p, int k, const void *blk, size_t bytes) {
+  if (!p || !blk) return dfail(HXA_E_ARG, "dit load block: null");
+  Dit &d = *(Dit *)p;
+  const hxa_block_dims &b = d.bd;
+  const int nb = d.cfg.nblocks, D = b.D;
+  if (k < 0 || k >= nb) return dfail(HXA_E_ARG, "dit load block: block index");
+  if (b.kind != 0 || d.form != 1 || D != 2048 || b.H != 16 || b.F != 8192 || b.DC != 1024)
+    return dfail(HXA_E_MODE, "dit load block: blkNN.bin files hold the Anima reference form's blocks (D 2048, 16 heads, "
+                             "MLP 8192, context 1024)");
+  const size_t W_GAIN = 125829120, W_MODW = 125833216, W_TOTAL = 138416128;
+  const size_t WQ_GAIN = W_GAIN / 2048 * 1152, WQ_MODW = WQ_GAIN + 4096, WQ_TOTAL = WQ_MODW + (W_TOTAL - W_MODW);
+  const bool q8 = bytes == WQ_TOTAL;
+  if (bytes != W_TOTAL && !q8) return dfail(HXA_E_WEIGHTS, "dit load block: neither an fp16 nor a q8 blkNN.bin (size)");
+  const int fmt = q8 ? HXA_W_Q8 : HXA_W_F16;
+  if (b.fmt_attn != fmt || b.fmt_mlp != fmt) return dfail(HXA_E_WEIGHTS, "dit load block: the file's format is not the DiT's");
+  const long wf16[11] = {0, 8388608, 16777216, 25165824, 33554432, 41943040, 46137344, 50331648, 58720256, 92274688,
+                         (long)W_GAIN};
+  long woff[11];
+  for (int i = 0; i < 11; i++) woff[i] = q8 ? wf16[i] / 2048 * 1152 : wf16[i];
+  uint8_t *stage = nullptr;
+  DHIP(hipStreamSynchronize(d.st));
+  DHIP(hipMalloc((void **)&stage, bytes));
+  int rc = upload(stage, blk, bytes);
+  if (rc == HXA_OK) rc = hxa_anima_file_to_pack(stage, woff, q8, d.packs[k], d.st);
+  // modulation weights: this block's A rows (3 sites x 256) and its three B matrices, where the prelude reads them
+  const long A = 256L * D, Bm = 3L * D * 256;
+  const uint8_t *mw = stage + (q8 ? WQ_MODW : W_MODW);
+  for (int site = 0; site < 3 && rc == HXA_OK; site++) {
+    const uint8_t *a = mw + 2 * site * (A + Bm);
+    if (hipMemcpyAsync(d.modw_all + 768L * D * k + site * A, a, 2 * A, hipMemcpyDeviceToDevice, d.st) != hipSuccess ||
+        hipMemcpyAsync(d.modw_all + 768L * D * nb + (3L * k + site) * Bm, a + 2 * A, 2 * Bm, hipMemcpyDeviceToDevice,
+                       d.st) != hipSuccess)
+      rc = dfail(HXA_E_HIP, "dit load block: modulation weights");
+  }
+  if (rc == HXA_OK && hipStreamSynchronize(d.st) != hipSuccess) rc = dfail(HXA_E_HIP, "dit load block: conversion");
+  (void)hipFree(stage);
+  return rc;
+}
+
+// phone/extract_small.py format (read by animad.cpp:43-70): u32 count; per tensor u32 name length, the name, u32 ndim,
+// i64 dims[ndim], fp16 data. The tensors of the reference glue (animad.cpp:424-492) are taken; others (the LLM
+// adapter's) are skipped.
+extern "C" int hxa_dit_load_anima_glue(void *p, const void *file, size_t bytes) {
+  if (!p || !file) return dfail(HXA_E_ARG, "dit load glue: null");
+  Dit &d = *(Dit *)p;
+  const int D = d.bd.D, C4 = 4 * d.cfg.lat_c;
+  if (d.form != 1 || d.bd.kind != 0) return dfail(HXA_E_MODE, "dit load glue: small.bin is the Anima reference form's");
+  const uint8_t *q = (const uint8_t *)file, *end = q + bytes;
+  auto take = [&](void *dst, size_t n) {
+    if ((size_t)(end - q) < n) return false;
+    memcpy(dst, q, n);
+    q += n;
+    return true;
+  };
+  uint32_t cnt = 0;
+  if (!take(&cnt, 4)) return dfail(HXA_E_WEIGHTS, "dit load glue: truncated");
+  std::map<std::string, GlueTensor> tens;
+  for (uint32_t i = 0; i < cnt; i++) {
+    uint32_t nl = 0, nd = 0;
+    if (!take(&nl, 4) || nl > 4096 || (size_t)(end - q) < nl) return dfail(HXA_E_WEIGHTS, "dit load glue: truncated");
+    std::string name((const char *)q, nl);
+    q += nl;
+    if (!take(&nd, 4) || nd > 8) return dfail(HXA_E_WEIGHTS, "dit load glue: bad tensor header");
+    GlueTensor t;
+    t.dtype = 1;
+    t.dims.resize(nd);
+    for (uint32_t j = 0; j < nd; j++) {
+      int64_t v = 0;
+      if (!take(&v, 8) || v < 0 || v > (1L << 32)) return dfail(HXA_E_WEIGHTS, "dit load glue: bad tensor header");
+      t.dims[j] = v;
+    }
+    const long n = t.elems();
+    if ((size_t)(end - q) < 2 * (size_t)n) return dfail(HXA_E_WEIGHTS, "dit load glue: truncated tensor data");
+    t.data = q;
+    q += 2 * (size_t)n;
+    tens[name] = t;
+  }
+  struct Want {
+    const char *name;
+    hxa_h *dst;
+    long rows, cols;
+  };
+  // x_embedder.proj.1 has 4 more columns than 4C (the zero mask channel, animad.cpp:446); they are dropped
+  const Want want[] = {{"t_embedder.1.linear_1.weight", d.L1, D, D},
+                       {"t_embedder.1.linear_2.weight", d.Wl2, 3L * D, D},
+                       {"final_layer.adaln_modulation.1.weight", d.F1, 256, D},
+                       {"final_layer.adaln_modulation.2.weight", d.F2, 2L * D, 256},
+                       {"final_layer.linear.weight", d.Wfin, C4, D}};
+  for (const Want &w : want) {
+    auto it = tens.find(w.name);
+    if (it == tens.end() || !shape_is(it->second, {w.rows, w.cols}))
+      return dfail(HXA_E_WEIGHTS, "dit load glue: a tensor is missing or not of the DiT's shape");
+  }
+  auto xe = tens.find("x_embedder.proj.1.weight");
+  auto tn = tens.find("t_embedding_norm.weight");
+  if (xe == tens.end() || xe->second.dims.size() != 2 || xe->second.dims[0] != D ||
+      (xe->second.dims[1] != C4 && xe->second.dims[1] != C4 + 4))
+    return dfail(HXA_E_WEIGHTS, "dit load glue: x_embedder.proj.1.weight missing or not [D][4C (+4)]");
+  if (tn == tens.end() || !shape_is(tn->second, {D})) return dfail(HXA_E_WEIGHTS, "dit load glue: t_embedding_norm.weight");
+  DHIP(hipStreamSynchronize(d.st));
+  for (const Want &w : want) DTRY(upload(w.dst, tens[w.name].data, 2 * (size_t)w.rows * w.cols));
+  DTRY(upload(d.tnorm, tn->second.data, 2L * D));
+  const long kx = xe->second.dims[1];
+  std::vector<uint16_t> xw((size_t)D * C4);
+  for (long r = 0; r < D; r++) memcpy(&xw[(size_t)r * C4], xe->second.data + 2 * r * kx, 2L * C4);
+  DTRY(upload(d.Wemb, xw.data(), 2 * xw.size()));
+  DTRY(hxa_ktile4_launch(d.Wfin, C4, D, d.Wfin4, d.st));
+  DHIP(hipStreamSynchronize(d.st));
+  return HXA_OK;
+}
+
+// moss/export_glue.py:1-22 (read by mossrun.cpp:129-139): "MGL1", i32 n; n entries { char name[40]; i32 dtype (0 fp32,
+// 1 fp16); i32 nd; i32 dims[3]; i64 offset (from the file start); i64 bytes }; data 128-byte aligned. Every tensor of
+// the DiT glue is taken (step_codes stays with the caller, who passes the step's code to hxa_dit_moss_step); rope.bands
+// rebuilds the RoPE tables.
+extern "C" int hxa_dit_load_moss_glue(void *p, const void *file, size_t bytes) {
+  if (!p || !file) return dfail(HXA_E_ARG, "dit load glue: null");
+  Dit &d = *(Dit *)p;
+  const int D = d.bd.D, C4 = 4 * d.cfg.lat_c;
+  if (d.form != 1 || d.bd.kind != 1) return dfail(HXA_E_MODE, "dit load glue: glue.bin is the MOSS reference form's");
+  const uint8_t *base = (const uint8_t *)file;
+  if (bytes < 8 || memcmp(base, "MGL1", 4)) return dfail(HXA_E_WEIGHTS, "dit load glue: not an MGL1 file");
+  int32_t n = 0;
+  memcpy(&n, base + 4, 4);
+  if (n < 0 || n > 4096 || 8 + 76L * n > (long)bytes) return dfail(HXA_E_WEIGHTS, "dit load glue: bad entry count");
+  std::map<std::string, GlueTensor> tens;
+  for (int i = 0; i < n; i++) {
+    const uint8_t *e = base + 8 + 76L * i;
+    char name[41] = {0};
+    memcpy(name, e, 40);
+    int32_t dt, nd, dims[3];
+    int64_t off, nbytes;
+    memcpy(&dt, e + 40, 4);
+    memcpy(&nd, e + 44, 4);
+    memcpy(dims, e + 48, 12);
+    memcpy(&off, e + 60, 8);
+    memcpy(&nbytes, e + 68, 8);
+    if ((dt != 0 && dt != 1) || nd < 1 || nd > 3 || off < 0 || nbytes < 0 || (uint64_t)off + (uint64_t)nbytes > bytes)
+      return dfail(HXA_E_WEIGHTS, "dit load glue: bad entry");
+    GlueTensor t;
+    t.dtype = dt;
+    for (int j = 0; j < nd; j++) t.dims.push_back(dims[j]);
+    if (t.elems() * (dt == 0 ? 4 : 2) != nbytes) return dfail(HXA_E_WEIGHTS, "dit load glue: entry size and shape differ");
+    t.data = base + off;
+    tens[name] = t;
+  }
+  struct Want {
+    const char *name;
+    int dtype;
+    void *dst;
+    long rows, cols;  // cols 0: a vector of `rows`
+  };
+  const Want want[] = {{"video_embedder.weight", 0, d.Wv32, D, C4},
+                       {"video_embedder.bias", 0, d.bve, D, 0},
+                       {"time_embedding.0.weight", 0, d.T0f, D, 256},
+                       {"time_embedding.0.bias", 0, d.b0, D, 0},
+                       {"time_embedding.2.weight", 0, d.T2f, D, D},
+                       {"time_embedding.2.bias", 0, d.b2, D, 0},
+                       {"shared_block_modulation.weight", 1, d.modw_all, 6L * D, D},
+                       {"shared_block_modulation.bias", 0, d.bm, 6L * D, 0},
+                       {"video_head_modulation.weight", 1, d.Wh, 2L * D, D},
+                       {"video_head_modulation.bias", 0, d.bh, 2L * D, 0},
+                       {"final_linear_video.weight", 0, d.Wfin32, C4, D},
+                       {"final_norm_video.weight", 0, d.nfin, D, 0},
+                       {"latent_mix.Q", 0, d.Q, C4, C4},
+                       {"bn.mean", 0, d.bnm, C4, 0},
+                       {"bn.var", 0, d.bnv, C4, 0},
+                       {"rope.bands", 0, nullptr, 16, 0}};
+  for (const Want &w : want) {
+    auto it = tens.find(w.name);
+    const bool ok = it != tens.end() && it->second.dtype == w.dtype &&
+                    (w.cols ? shape_is(it->second, {w.rows, w.cols}) : shape_is(it->second, {w.rows}));
+    if (!ok) return dfail(HXA_E_WEIGHTS, "dit load glue: a tensor is missing or not of the DiT's shape / type");
+  }
+  DHIP(hipStreamSynchronize(d.st));
+  for (const Want &w : want) {
+    const GlueTensor &t = tens[w.name];
+    if (w.dst) DTRY(upload(w.dst, t.data, (size_t)t.elems() * (w.dtype == 0 ? 4 : 2)));
+  }
+  memcpy(d.bands, tens["rope.bands"].data, sizeof d.bands);
+  DTRY(hxa_ktile4_f32_launch(d.Wfin32, C4, D, d.Wfin4f, d.st));
+  std::vector<float> c, sn;
+  rope_moss(d.cfg.lat_h / 2, d.cfg.lat_w / 2, d.ntxt, d.Ttot, d.bands, c, sn);
+  DTRY(upload(d.cosT, c.data(), 4 * c.size()));
+  DTRY(upload(d.sinT, sn.data(), 4 * sn.size()));
+  d.ropeL_scale = -1.0;  // the low-res tables are rebuilt with these bands at their next use
+  DHIP(hipStreamSynchronize(d.st));
   return HXA_OK;
 }
 

@@ -299,17 +299,25 @@ HXA_DEV float sinusoid_angle(float t, int j, int half) { return t * expf(-logf(1
 // y[m][n] = act(sum_k x[m][k] * W[n][k] (+ bias[n])); act 0 none, 1 SiLU on the input (x -> x sigmoid(x)), 2 the
 // input row is the timestep sinusoid of t = x[0] at width K (the values sinusoid_kernel stores; one row).
 // One wave per output feature n, lanes stride K (coalesced weight reads), up to 8 input rows.
+// two adjacent weights as fp32: fp16 storage (most glue) or fp32 storage (the MOSS time MLP, video embedding and
+// head, kept fp32 as the reference keeps them, moss/export_glue.py:7-12)
+__device__ inline float2_t wpair(const hxa_h *p) {
+  const half2_t h = *(const half2_t *)p;
+  return (float2_t){(float)h[0], (float)h[1]};
+}
+__device__ inline float2_t wpair(const float *p) { return *(const float2_t *)p; }
+template <typename WT>
 __global__ __launch_bounds__(256) void gemv_kernel(const float *__restrict__ x, long ldx, int M, int K,
-                                                   const hxa_h *__restrict__ W, int N, float *__restrict__ y, long ldy,
+                                                   const WT *__restrict__ W, int N, float *__restrict__ y, long ldy,
                                                    int act, const float *__restrict__ bias, int split, int gap) {
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (n >= N) return;
   float accm[8];
 #pragma unroll
   for (int m = 0; m < 8; m++) accm[m] = 0.0f;
-  const hxa_h *wr = W + (long)n * K;
+  const WT *wr = W + (long)n * K;
   for (int k = lane * 2; k < K; k += 128) {
-    const half2_t wv = *(const half2_t *)(wr + k);
+    const float2_t wv = wpair(wr + k);
 #pragma unroll
     for (int m = 0; m < 8; m++) {
       if (m < M) {
@@ -327,7 +335,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float *__restrict__ x, 
           x0 = x0 / (1.0f + __expf(-x0));
           x1 = x1 / (1.0f + __expf(-x1));
         }
-        accm[m] = fmaf(x0, (float)wv[0], fmaf(x1, (float)wv[1], accm[m]));
+        accm[m] = fmaf(x0, wv[0], fmaf(x1, wv[1], accm[m]));
       }
     }
   }
@@ -488,11 +496,13 @@ __global__ void sinusoid_kernel(const float *t, int n, int dim, float *out) {
 //     outputs, reading every value it updates before it writes any.
 // One wave per SIMD (96 workgroups of 4 waves at 1536 tokens) left every load and MFMA latency exposed (45 us);
 // the 16-wave workgroup overlaps them.
+// W32: fp32 weights (the MOSS head, final_linear_video, kept fp32 as the reference keeps it), Wf4 [D/4][4C][4] fp32;
+// the products then go through v_mfma_f32_16x16x4_f32, four per 16-deep k step, with the normalised value unsplit.
 constexpr int FT = 16;
-template <int NOB, int NW>
+template <int NOB, int NW, bool W32>
 __global__ __launch_bounds__(64 * NW) void final_kernel(const float *__restrict__ x, int T, int xrows, int D,
                                                         const float *__restrict__ shift, const float *__restrict__ scale,
-                                                        const hxa_h *__restrict__ Wf4, int Cc, int H, int W, float *lat,
+                                                        const void *__restrict__ Wf4, int Cc, int H, int W, float *lat,
                                                         const float *__restrict__ dtp, int ntok,
                                                         const float *__restrict__ normw, float *__restrict__ x0rows,
                                                         const float *__restrict__ zrows) {
@@ -554,7 +564,8 @@ __global__ __launch_bounds__(64 * NW) void final_kernel(const float *__restrict_
   const int kw = D / NW, kend = (wave + 1) * kw;
   for (int k0 = wave * kw; k0 < kend; k0 += 16 * U) {
     float4_t xv[U], sc[U], sh[U], nw[U];
-    half4_t wv[U][NOB];
+    half4_t wv[U][W32 ? 1 : NOB];
+    float4_t wf[U][W32 ? NOB : 1];
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int c = min(k0 + 16 * u, kend - 16) + kk;
@@ -563,22 +574,36 @@ __global__ __launch_bounds__(64 * NW) void final_kernel(const float *__restrict_
       sh[u] = *(const float4_t *)(shift + c);
       nw[u] = normw != nullptr ? *(const float4_t *)(normw + c) : (float4_t){1.0f, 1.0f, 1.0f, 1.0f};
 #pragma unroll
-      for (int b = 0; b < NOB; b++) wv[u][b] = *(const half4_t *)(Wf4 + ((long)(c >> 2) * NO + 16 * b + row) * 4);
+      for (int b = 0; b < NOB; b++) {
+        const long wi = ((long)(c >> 2) * NO + 16 * b + row) * 4;
+        if constexpr (W32) wf[u][b] = *(const float4_t *)((const float *)Wf4 + wi);
+        else wv[u][b] = *(const half4_t *)((const hxa_h *)Wf4 + wi);
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; u++) {
       if (k0 + 16 * u >= kend) break;
-      half4_t hi, lo;
+      float4_t a4;
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float a = ok ? (xv[u][e] - mu) * rs * nw[u][e] * (1.0f + sc[u][e]) + sh[u][e] : 0.0f;
-        hi[e] = (hxa_h)a;
-        lo[e] = (hxa_h)(a - (float)hi[e]);
-      }
+      for (int e = 0; e < 4; e++) a4[e] = ok ? (xv[u][e] - mu) * rs * nw[u][e] * (1.0f + sc[u][e]) + sh[u][e] : 0.0f;
+      if constexpr (W32) {
+        // instruction e takes k = 4 (lane / 16) + e of each lane's four: A[token][k] B[k][output] over the 16-deep step
 #pragma unroll
-      for (int b = 0; b < NOB; b++) {
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(hi, wv[u][b], acc[b], 0, 0, 0);
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(lo, wv[u][b], acc[b], 0, 0, 0);
+        for (int b = 0; b < NOB; b++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[e], wf[u][b][e], acc[b], 0, 0, 0);
+      } else {
+        half4_t hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          hi[e] = (hxa_h)a4[e];
+          lo[e] = (hxa_h)(a4[e] - (float)hi[e]);
+        }
+#pragma unroll
+        for (int b = 0; b < NOB; b++) {
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(hi, wv[u][b], acc[b], 0, 0, 0);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(lo, wv[u][b], acc[b], 0, 0, 0);
+        }
       }
     }
   }
@@ -622,12 +647,13 @@ __global__ __launch_bounds__(64 * NW) void final_kernel(const float *__restrict_
   }
 }
 
-// W [N][K] fp16 -> Wk [K/4][N][4] (k-tiled by 4: the final layer's weight layout)
-__global__ void ktile4_kernel(const hxa_h *__restrict__ W, int N, int K, hxa_h *__restrict__ Wk) {
+// W [N][K] fp16 or fp32 -> Wk [K/4][N][4] (k-tiled by 4: the final layer's weight layout)
+template <typename V, typename T>
+__global__ void ktile4_kernel(const T *__restrict__ W, int N, int K, T *__restrict__ Wk) {
   const long i = (long)blockIdx.x * 256 + threadIdx.x;  // one 4-k chunk of one row
   if (i >= (long)N * (K / 4)) return;
   const int n = (int)(i % N), g = (int)(i / N);
-  *(half4_t *)(Wk + i * 4) = *(const half4_t *)(W + (long)n * K + 4 * g);
+  *(V *)(Wk + i * 4) = *(const V *)(W + (long)n * K + 4 * g);
 }
 
 // q8 / q4 quantisation of W[N][K] fp32, one thread per (column n, 32-group g): amax of the fp16-rounded weights,
@@ -802,17 +828,26 @@ int hxa_patch_embed_launch(const float *lat, int B, int Cc, int H, int W, const 
   return LAUNCH_OK();
 }
 
-int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W, int N, float *y, long ldy, int act,
-                          const float *bias, int split, int gap, hipStream_t st) {
-  if (M <= 0 || K <= 0 || N <= 0) return HXA_E_ARG;
+template <typename WT>
+static int linear_launch(const float *x, long ldx, int M, int K, const WT *W, int N, float *y, long ldy, int act,
+                         const float *bias, int split, int gap, hipStream_t st) {
+  if (M <= 0 || K <= 0 || N <= 0 || (uintptr_t)W % (2 * sizeof(WT))) return HXA_E_ARG;
   if (M <= 8) {
     if (K % 2 || (act == 2 && (M != 1 || K % 4))) return HXA_E_ARG;
-    hxa_launch(gemv_kernel, dim3(nblk(N, 4)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy, act, bias,
-                       split > 0 ? split : N, gap);
+    hxa_launch(gemv_kernel<WT>, dim3(nblk(N, 4)), dim3(256), 0, st, x, ldx, M, K, W, N, y, ldy, act, bias,
+               split > 0 ? split : N, gap);
   } else {
     return HXA_E_ARG;  // more than 8 rows: the patch embed has its own kernel (hxa_patch_embed_launch)
   }
   return LAUNCH_OK();
+}
+int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W, int N, float *y, long ldy, int act,
+                          const float *bias, int split, int gap, hipStream_t st) {
+  return linear_launch(x, ldx, M, K, W, N, y, ldy, act, bias, split, gap, st);
+}
+int hxa_linear_w32_launch(const float *x, long ldx, int M, int K, const float *W, int N, float *y, long ldy, int act,
+                          const float *bias, int split, int gap, hipStream_t st) {
+  return linear_launch(x, ldx, M, K, W, N, y, ldy, act, bias, split, gap, st);
 }
 
 int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, int per, long ostride, int split, int gap,
@@ -853,27 +888,35 @@ int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, 
 
 int hxa_ktile4_launch(const hxa_h *W, int N, int K, hxa_h *Wk, hipStream_t st) {
   if (N <= 0 || K <= 0 || K % 4 || (uintptr_t)W % 8 || (uintptr_t)Wk % 8) return HXA_E_ARG;
-  hxa_launch(ktile4_kernel, dim3(nblk((long)N * (K / 4))), dim3(256), 0, st, W, N, K, Wk);
+  hxa_launch((ktile4_kernel<half4_t, hxa_h>), dim3(nblk((long)N * (K / 4))), dim3(256), 0, st, W, N, K, Wk);
+  return LAUNCH_OK();
+}
+int hxa_ktile4_f32_launch(const float *W, int N, int K, float *Wk, hipStream_t st) {
+  if (N <= 0 || K <= 0 || K % 4 || (uintptr_t)W % 16 || (uintptr_t)Wk % 16) return HXA_E_ARG;
+  hxa_launch((ktile4_kernel<float4_t, float>), dim3(nblk((long)N * (K / 4))), dim3(256), 0, st, W, N, K, Wk);
   return LAUNCH_OK();
 }
 
-int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale,
-                     const hxa_h *Wf4, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st,
-                     const float *normw, float *x0rows, const float *zrows) {
+namespace {
+template <bool W32>
+int final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale, const void *Wf4,
+                 int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st, const float *normw, float *x0rows,
+                 const float *zrows) {
   if ((x0rows == nullptr) != (zrows == nullptr) || (normw && (uintptr_t)normw % 16)) return HXA_E_ARG;
   const int NO = 4 * Cc;
   if ((NO != 64 && NO != 128 && NO != 256) || (H / 2) * (W / 2) != T || xrows < T || D % 256 || D > 4096 || B * T < 1)
     return HXA_E_ARG;
-  if ((uintptr_t)x % 16 || (uintptr_t)shift % 16 || (uintptr_t)scale % 16 || (uintptr_t)Wf4 % 8) return HXA_E_ARG;
+  if ((uintptr_t)x % 16 || (uintptr_t)shift % 16 || (uintptr_t)scale % 16 || (uintptr_t)Wf4 % (W32 ? 16 : 8))
+    return HXA_E_ARG;
   // partial sums + statistics: 16 x 16 x 64, 16 x 16 x 128 or 8 x 16 x 256 floats (64 / 128 / 128 KB)
   auto bytes = [](int nw, int no) { return (int)sizeof(float) * (nw * FT * no + 2 * FT); };
   static bool attr = false;
   if (!attr) {
-    if (hipFuncSetAttribute((const void *)final_kernel<4, 16>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    if (hipFuncSetAttribute((const void *)final_kernel<4, 16, W32>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             bytes(16, 64)) != hipSuccess ||
-        hipFuncSetAttribute((const void *)final_kernel<8, 16>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        hipFuncSetAttribute((const void *)final_kernel<8, 16, W32>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             bytes(16, 128)) != hipSuccess ||
-        hipFuncSetAttribute((const void *)final_kernel<16, 8>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        hipFuncSetAttribute((const void *)final_kernel<16, 8, W32>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             bytes(8, 256)) != hipSuccess)
       return HXA_E_HIP;
     attr = true;
@@ -881,15 +924,23 @@ int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float
   const int ntok = B * T;
   const dim3 grid((ntok + FT - 1) / FT);
   if (NO == 64)
-    hxa_launch(final_kernel<4, 16>, grid, dim3(1024), bytes(16, 64), st, x, T, xrows, D, shift, scale, Wf4, Cc, H, W,
-               lat, dtp, ntok, normw, x0rows, zrows);
+    hxa_launch(final_kernel<4, 16, W32>, grid, dim3(1024), bytes(16, 64), st, x, T, xrows, D, shift, scale, Wf4, Cc, H,
+               W, lat, dtp, ntok, normw, x0rows, zrows);
   else if (NO == 128)
-    hxa_launch(final_kernel<8, 16>, grid, dim3(1024), bytes(16, 128), st, x, T, xrows, D, shift, scale, Wf4, Cc, H, W,
-               lat, dtp, ntok, normw, x0rows, zrows);
+    hxa_launch(final_kernel<8, 16, W32>, grid, dim3(1024), bytes(16, 128), st, x, T, xrows, D, shift, scale, Wf4, Cc,
+               H, W, lat, dtp, ntok, normw, x0rows, zrows);
   else
-    hxa_launch(final_kernel<16, 8>, grid, dim3(512), bytes(8, 256), st, x, T, xrows, D, shift, scale, Wf4, Cc, H, W,
-               lat, dtp, ntok, normw, x0rows, zrows);
+    hxa_launch(final_kernel<16, 8, W32>, grid, dim3(512), bytes(8, 256), st, x, T, xrows, D, shift, scale, Wf4, Cc, H,
+               W, lat, dtp, ntok, normw, x0rows, zrows);
   return LAUNCH_OK();
+}
+}  // namespace
+
+int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale,
+                     const void *Wf4, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st,
+                     const float *normw, float *x0rows, const float *zrows, int w32) {
+  return w32 ? final_launch<true>(x, B, T, xrows, D, shift, scale, Wf4, Cc, H, W, lat, dtp, st, normw, x0rows, zrows)
+             : final_launch<false>(x, B, T, xrows, D, shift, scale, Wf4, Cc, H, W, lat, dtp, st, normw, x0rows, zrows);
 }
 
 
@@ -949,9 +1000,10 @@ __global__ __launch_bounds__(256) void ptr_gemv_kernel(const float *__restrict__
   if (lane == 0) y[(long)g * y_gs + n] = acc + (bias ? bias[n] : 0.0f);
 }
 // rapid-moss input (mossrun.cpp:316-320): per image token t, xin = z_t + Q x0_t (Q fp32 [C4][C4]) and the token's
-// row x = Wv xin + bv (Wv fp16 [D][C4]); FT tokens per workgroup, their xin in LDS, each weight row read once
+// row x = Wv xin + bv (Wv [D][C4], fp32 or fp16); FT tokens per workgroup, their xin in LDS, each weight row read once
+template <typename WT>
 __global__ __launch_bounds__(256) void moss_embed_kernel(const float *__restrict__ z, const float *__restrict__ x0,
-                                                         const float *__restrict__ Q, const hxa_h *__restrict__ Wv,
+                                                         const float *__restrict__ Q, const WT *__restrict__ Wv,
                                                          const float *__restrict__ bv, float *__restrict__ x, int T,
                                                          int xrows, int D, int C4, int ntok) {
   extern __shared__ float xin[];  // [FT][C4]
@@ -971,11 +1023,11 @@ __global__ __launch_bounds__(256) void moss_embed_kernel(const float *__restrict
     float acc[FT];
 #pragma unroll
     for (int t = 0; t < FT; t++) acc[t] = bv[n];
-    const hxa_h *wr = Wv + (long)n * C4;
+    const WT *wr = Wv + (long)n * C4;
     for (int c = 0; c < C4; c += 2) {
-      const half2_t wv = *(const half2_t *)(wr + c);
+      const float2_t wv = wpair(wr + c);
 #pragma unroll
-      for (int t = 0; t < FT; t++) acc[t] = fmaf(xin[t * C4 + c], (float)wv[0], fmaf(xin[t * C4 + c + 1], (float)wv[1], acc[t]));
+      for (int t = 0; t < FT; t++) acc[t] = fmaf(xin[t * C4 + c], wv[0], fmaf(xin[t * C4 + c + 1], wv[1], acc[t]));
     }
 #pragma unroll
     for (int t = 0; t < FT; t++) {
@@ -1136,12 +1188,16 @@ int hxa_ptr_gemv_launch(const float *x, long x_gs, int act, const hxa_h *const *
              y_gs);
   return LAUNCH_OK();
 }
-int hxa_moss_embed_launch(const float *z, const float *x0, const float *Q, const hxa_h *Wv, const float *bv, float *x, int B,
-                          int T, int xrows, int D, int C4, hipStream_t st) {
-  if (C4 % 2 || C4 > 512 || B <= 0 || T <= 0 || xrows < T) return HXA_E_ARG;
+int hxa_moss_embed_launch(const float *z, const float *x0, const float *Q, const void *Wv, int w32, const float *bv,
+                          float *x, int B, int T, int xrows, int D, int C4, hipStream_t st) {
+  if (C4 % 2 || C4 > 512 || B <= 0 || T <= 0 || xrows < T || (uintptr_t)Wv % (w32 ? 8 : 4)) return HXA_E_ARG;
   const int ntok = B * T;
-  hxa_launch(moss_embed_kernel, dim3((ntok + FT - 1) / FT), dim3(256), sizeof(float) * FT * C4, st, z, x0, Q, Wv,
-                     bv, x, T, xrows, D, C4, ntok);
+  if (w32)
+    hxa_launch(moss_embed_kernel<float>, dim3((ntok + FT - 1) / FT), dim3(256), sizeof(float) * FT * C4, st, z, x0, Q,
+               (const float *)Wv, bv, x, T, xrows, D, C4, ntok);
+  else
+    hxa_launch(moss_embed_kernel<hxa_h>, dim3((ntok + FT - 1) / FT), dim3(256), sizeof(float) * FT * C4, st, z, x0, Q,
+               (const hxa_h *)Wv, bv, x, T, xrows, D, C4, ntok);
   return LAUNCH_OK();
 }
 int hxa_bn_unpatchify_launch(const float *x0, const float *mean, const float *var, int B, int Cc, int H, int W, float *lat,

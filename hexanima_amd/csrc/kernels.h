@@ -136,15 +136,19 @@ int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, 
 // input, 2 the input row is the timestep sinusoid of t = x[0] at width K (M 1); more rows: HXA_E_ARG
 int hxa_linear_f32_launch(const float *x, long ldx, int M, int K, const hxa_h *W, int N, float *y, long ldy, int act,
                           const float *bias, int split, int gap, hipStream_t st);
+// the same with fp32 weights W [N][K] (8-byte aligned)
+int hxa_linear_w32_launch(const float *x, long ldx, int M, int K, const float *W, int N, float *y, long ldy, int act,
+                          const float *bias, int split, int gap, hipStream_t st);
 // final layer over B images of T image tokens (image b's rows start at b*xrows); dtp == NULL: lat = v,
 // else lat += (*dtp) * v (Euler step). Wf4: the [4 Cc][D] weights k-tiled by 4, [D/4][4 Cc][4] (hxa_ktile4_launch).
 // normw != NULL: RMSNorm * normw instead of LN (the MOSS head); x0rows / zrows != NULL: write the token rows
-// x0rows[t][o] = zrows[t][o] - v (rapid-moss) instead of the latent
+// x0rows[t][o] = zrows[t][o] - v (rapid-moss) instead of the latent. w32: Wf4 holds fp32 weights
 int hxa_final_launch(const float *x, int B, int T, int xrows, int D, const float *shift, const float *scale,
-                     const hxa_h *Wf4, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st,
-                     const float *normw = nullptr, float *x0rows = nullptr, const float *zrows = nullptr);
-// W [N][K] fp16 -> Wk [K/4][N][4]
+                     const void *Wf4, int Cc, int H, int W, float *lat, const float *dtp, hipStream_t st,
+                     const float *normw = nullptr, float *x0rows = nullptr, const float *zrows = nullptr, int w32 = 0);
+// W [N][K] fp16 (fp32) -> Wk [K/4][N][4]
 int hxa_ktile4_launch(const hxa_h *W, int N, int K, hxa_h *Wk, hipStream_t st);
+int hxa_ktile4_f32_launch(const float *W, int N, int K, float *Wk, hipStream_t st);
 // the reference's own DiT glue: vector RMSNorm * w (fp16 w), G GEMVs with their own inputs, the rapid-moss latent mix +
 // video embedding, and BN denorm + unpatchify of the x0 token rows
 int hxa_rmsvec_launch(const float *x, int n, const hxa_h *w, float eps, float *y, hipStream_t st);
@@ -153,8 +157,9 @@ int hxa_ptr_gemv_launch(const float *x, long x_gs, int act, const hxa_h *const *
                         int N, int K, const float *bias, float *y, long y_gs, hipStream_t st);
 int hxa_grouped_gemv_launch(const float *x, long ldx, const hxa_h *W, int G, int N, int K, const float *bias, float *y,
                             long ldy, hipStream_t st);
-int hxa_moss_embed_launch(const float *z, const float *x0, const float *Q, const hxa_h *Wv, const float *bv, float *x, int B,
-                          int T, int xrows, int D, int C4, hipStream_t st);
+// Wv [D][C4]: fp32 when w32, else fp16
+int hxa_moss_embed_launch(const float *z, const float *x0, const float *Q, const void *Wv, int w32, const float *bv,
+                          float *x, int B, int T, int xrows, int D, int C4, hipStream_t st);
 int hxa_bn_unpatchify_launch(const float *x0, const float *mean, const float *var, int B, int Cc, int H, int W, float *lat,
                              hipStream_t st);
 int hxa_quantize_launch(const float *W, int N, int K, int fmt, void *q, hxa_h *s, hipStream_t st);
@@ -177,6 +182,10 @@ int hxa_upsample2_rows_launch(const float *src, int B, int h, int w, int C4, flo
 int hxa_crouton_to_ktiled_launch(const void *src, int N, int K, void *dst, int row0, int ldn, hipStream_t st);
 int hxa_q8rec_to_ktiled_launch(const void *rec, int N, int nkb, int kbt, void *q, void *s, int row0, int ldn, int nkb_main,
                                int lora_g, hipStream_t st);
+// an Anima blkNN.bin in device memory -> a kind-0 GPU pack (D 2048, F 8192, DC 1024): woff[0..9] the byte offsets of
+// sq sk sv so cq ck cv co m1 m2 (blk_wlayout.h order), woff[10] the gains; q8: q8 records, else fp16 crouton tiles
+int hxa_anima_file_to_pack(const uint8_t *src, const long *woff, int q8, void *pack, hipStream_t st);
+size_t hxa_anima_file_mat_bytes(int i, int q8);
 // matrix shapes of a GPU block pack (see hxa_pack_layout); returns the matrix count
 int hxa_pack_mats(int kind, int D, int F, int DC, int fa, int fm, int *N, int *K, int *fmt);
 

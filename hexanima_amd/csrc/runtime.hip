@@ -1171,42 +1171,61 @@ int new_pack(Ctx &c, long bytes, void **dev) {
   return HXA_OK;
 }
 
+}  // namespace
+
+// The ten matrices and the gains of an Anima blkNN.bin already in device memory (src; byte offsets woff[0..9] in
+// blk_wlayout.h order sq sk sv so cq ck cv co m1 m2, woff[10] the gains; fp16 crouton tiles or q8 records) -> the
+// kind-0 GPU pack at D 2048 (pack matrix order: qkv (q,k,v rows), o, cq, ckv (k,v rows), co, w1, w2), queued on st.
+int hxa_anima_file_to_pack(const uint8_t *src, const long *woff, int q8, void *pack, hipStream_t st) {
+  const int D = ANIMA_D, F = ANIMA_F, DC = ANIMA_DC, fmt = q8 ? HXA_W_Q8 : HXA_W_F16;
+  long offs[32];
+  hxa_pack_layout(0, D, F, DC, fmt, fmt, offs, 32);
+  struct Src {
+    int N, K, mat, row0;
+  };
+  const Src srcs[10] = {{D, D, 0, 0}, {D, D, 0, D}, {D, D, 0, 2 * D}, {D, D, 1, 0}, {D, D, 2, 0},
+                        {D, DC, 3, 0}, {D, DC, 3, D}, {D, D, 4, 0}, {F, D, 5, 0}, {D, F, 6, 0}};
+  const int matN[7] = {3 * D, D, D, 2 * D, D, F, D};
+  uint8_t *d8 = (uint8_t *)pack;
+  for (int i = 0; i < 10; i++) {
+    const Src &s = srcs[i];
+    const uint8_t *m = src + woff[i];
+    const int rc = q8 ? hxa_q8rec_to_ktiled_launch(m, s.N, s.K / 32, s.K / 32, d8 + offs[3 * s.mat], d8 + offs[3 * s.mat + 1],
+                                                   s.row0, matN[s.mat], s.K / 32, 0, st)
+                      : hxa_crouton_to_ktiled_launch(m, s.N, s.K, d8 + offs[3 * s.mat], s.row0, matN[s.mat], st);
+    if (rc != HXA_OK) return rc;
+  }
+  HIPC(hipMemcpyAsync(d8 + offs[21], src + woff[10], 2048, hipMemcpyDeviceToDevice, st));
+  return HXA_OK;
+}
+// bytes of matrix i (blk_wlayout.h order) in an Anima blkNN.bin
+size_t hxa_anima_file_mat_bytes(int i, int q8) {
+  const size_t D = ANIMA_D, F = ANIMA_F, DC = ANIMA_DC;
+  const size_t elems = i == 5 || i == 6 ? D * DC : i >= 8 ? F * D : D * D;
+  return q8 ? elems / 1024 * 1152 : elems * 2;
+}
+
+namespace {
 // Convert one registered Anima blkNN.bin (fixed D=2048 layout, blk_wlayout.h) into a GPU pack.
 int build_anima_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
   const int D = ANIMA_D, F = ANIMA_F, DC = ANIMA_DC;
   const bool q8 = meta[M_Q8] != 0;
   const int fmt = q8 ? HXA_W_Q8 : HXA_W_F16;
   db.dims = hxa_block_dims{0, D, D / 128, F, 0, DC, 0, 1, 0, fmt, fmt, 0, 1};
-  long offs[32];
-  const long bytes = hxa_pack_layout(0, D, F, DC, fmt, fmt, offs, 32);
-  // pack matrix order: qkv (q,k,v rows), o, cq, ckv (k,v rows), co, w1, w2
-  struct Src {
-    int meta_id, N, K, mat, row0;
-  };
-  const Src srcs[] = {{M_WSQ, D, D, 0, 0},     {M_WSK, D, D, 0, D},   {M_WSV, D, D, 0, 2 * D}, {M_WSO, D, D, 1, 0},
-                      {M_WCQ, D, D, 2, 0},     {M_WCK, D, DC, 3, 0},  {M_WCV, D, DC, 3, D},    {M_WCO, D, D, 4, 0},
-                      {M_WM1, F, D, 5, 0},     {M_WM2, D, F, 6, 0}};
-  const int matN[7] = {3 * D, D, D, 2 * D, D, F, D};
-  for (const Src &s : srcs) {
-    const size_t elems = (size_t)s.N * s.K;
-    const size_t need = q8 ? elems / 1024 * 1152 : elems * 2;
-    if (meta[s.meta_id] < 0 || (size_t)meta[s.meta_id] + need > hb.bytes) return fail(HXA_E_WEIGHTS, "weight offset out of range");
+  const long bytes = hxa_pack_layout(0, D, F, DC, fmt, fmt, nullptr, 0);
+  const int ids[11] = {M_WSQ, M_WSK, M_WSV, M_WSO, M_WCQ, M_WCK, M_WCV, M_WCO, M_WM1, M_WM2, M_GAIN};
+  long woff[11];
+  for (int i = 0; i < 11; i++) {
+    woff[i] = meta[ids[i]];
+    const size_t need = i < 10 ? hxa_anima_file_mat_bytes(i, q8) : 2048;
+    if (woff[i] < 0 || (size_t)woff[i] + need > hb.bytes)
+      return fail(HXA_E_WEIGHTS, i < 10 ? "weight offset out of range" : "gain offset out of range");
   }
-  if (meta[M_GAIN] < 0 || (size_t)meta[M_GAIN] + 2048 > hb.bytes) return fail(HXA_E_WEIGHTS, "gain offset out of range");
   const uint8_t *dsrc = nullptr;
   void *dev = nullptr;
   int rc = stage_weights(c, hb, 0, hb.bytes, &dsrc);
   if (rc == HXA_OK) rc = new_pack(c, bytes, &dev);
-  uint8_t *d8 = (uint8_t *)dev;
-  for (const Src &s : srcs) {
-    if (rc != HXA_OK) break;
-    const uint8_t *src = dsrc + meta[s.meta_id];
-    rc = q8 ? hxa_q8rec_to_ktiled_launch(src, s.N, s.K / 32, s.K / 32, d8 + offs[3 * s.mat], d8 + offs[3 * s.mat + 1], s.row0,
-                                         matN[s.mat], s.K / 32, 0, c.st)
-            : hxa_crouton_to_ktiled_launch(src, s.N, s.K, d8 + offs[3 * s.mat], s.row0, matN[s.mat], c.st);
-  }
-  if (rc == HXA_OK && hipMemcpyAsync(d8 + offs[21], dsrc + meta[M_GAIN], 2048, hipMemcpyDeviceToDevice, c.st) != hipSuccess)
-    rc = fail(HXA_E_HIP, "gain copy");
+  if (rc == HXA_OK) rc = hxa_anima_file_to_pack(dsrc, woff, q8, dev, c.st);
   if (rc == HXA_OK && hipStreamSynchronize(c.st) != hipSuccess) rc = fail(HXA_E_HIP, "pack conversion");
   if (rc != HXA_OK) {
     if (dev) (void)hipFree(dev);

@@ -106,6 +106,9 @@ _SIGS = {
     "hxa_dit_moss_step_lowres": (I, [P, F, F, I]),
     "hxa_dit_export": (L, [P, I, P, SZ]),
     "hxa_dit_import": (I, [P, I, P, SZ]),
+    "hxa_dit_load_block": (I, [P, I, P, SZ]),
+    "hxa_dit_load_anima_glue": (I, [P, P, SZ]),
+    "hxa_dit_load_moss_glue": (I, [P, P, SZ]),
     "hxa_dit_stream": (P, [P]),
 }
 _lib = None

@@ -321,14 +321,31 @@ int hxa_dit_moss_step_lowres(void *dit, float code, float rope_scale, int use_gr
  *   which == 2 nblocks: glue, fp16, concatenated: x_embed [D][4C], t_embed [D][temb], final_mod [2D][D],
  *     final_linear [4C][D], then (MOSS only) text_proj [D][ntxt_in].
  *     Form 1 Anima: x_embed [D][4C], t_l1 [D][D], t_l2 [3D][D], f1 [256][D], f2 [2D][256], final_linear [4C][D],
- *     t_norm [D]; form 1 MOSS: video_embed [D][4C], t0 [D][256], t2 [D][D], head_mod [2D][D], final_linear [4C][D],
- *     text_proj [D][ntxt_in]
+ *     t_norm [D]; form 1 MOSS: head_mod [2D][D], text_proj [D][ntxt_in]
  *   which == 2 nblocks + 1 (form 1 MOSS): fp32 b_video [D], b_t0 [D], b_t2 [D], b_smod [6D], b_hmod [2D],
- *     final_norm [D], latent_mix Q [4C][4C], bn_mean [4C], bn_var [4C] */
+ *     final_norm [D], latent_mix Q [4C][4C], bn_mean [4C], bn_var [4C], video_embed [D][4C], t0 [D][256], t2 [D][D],
+ *     final_linear [4C][D] (the matrices the reference keeps fp32, moss/export_glue.py:7-12) */
 long hxa_dit_export(void *dit, int which, void *host, size_t bytes);
 /* the inverse of hxa_dit_export: overwrite section `which` with host bytes of the same layout and size (bytes must be
  * the size hxa_dit_export reports). Complete when the call returns; later steps (captured graphs included) use it. */
 int hxa_dit_import(void *dit, int which, const void *host, size_t bytes);
+/* Real weights into the reference form (form 1) of the DiT runner; each upload is complete when the call returns and
+ * later steps (captured graphs included) use it. Errors: HXA_E_MODE (another form or kind), HXA_E_WEIGHTS (a file that
+ * does not parse, or whose shapes are not the DiT's).
+ * hxa_dit_load_block: block k from the bytes of an Anima blkNN.bin -- the buffer megarun registers with fastrpc_mmap
+ *   (megarun.cpp:100-119) and this library's mega_block takes through hxa_register -- fp16 or q8 (told apart by size,
+ *   blk_wlayout.h:3-20; the DiT's fmt_attn / fmt_mlp must match), its adaLN modulation weights included. Needs the
+ *   Anima shape: D 2048, 16 heads, MLP 8192, context width 1024.
+ * hxa_dit_load_anima_glue: the caller-side glue of animad (animad.cpp:424-492) from small.bin (phone/extract_small.py:
+ *   u32 count; per tensor u32 name length, name, u32 ndim, i64 dims, fp16 data): t_embedder.1.linear_1 / _2,
+ *   t_embedding_norm, x_embedder.proj.1 (its 4 mask-channel columns dropped: they multiply zeros, animad.cpp:446),
+ *   final_layer.adaln_modulation.1 / .2 and final_layer.linear; other tensors are ignored.
+ * hxa_dit_load_moss_glue: the MOSS DiT glue from glue.bin (MGL1, moss/export_glue.py:1-22), in the file's storage types
+ *   (fp32 time MLP, video embedding, head linear and vectors; fp16 modulation matrices); rope.bands rebuilds the RoPE
+ *   tables; step_codes stays with the caller (the code argument of hxa_dit_moss_step). */
+int hxa_dit_load_block(void *dit, int k, const void *blk, size_t bytes);
+int hxa_dit_load_anima_glue(void *dit, const void *small_bin, size_t bytes);
+int hxa_dit_load_moss_glue(void *dit, const void *glue_bin, size_t bytes);
 void *hxa_dit_stream(void *dit);
 
 #ifdef __cplusplus

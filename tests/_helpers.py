@@ -212,8 +212,36 @@ def oracle_anima_ref_velocity(lat, ctx16, sigma, blocks, modws, glue, *, D, H, F
     return out
 
 
+def lin(x, W):
+    """x W^T: fp16 weights (uint16 bits) through the oracle's fp32 linear; fp32 weights (the MOSS glue's fp32
+    tensors, moss/export_glue.py:7-12) in float64, rounded once to fp32."""
+    if W.dtype == np.uint16:
+        return hxo.linear_f32(x, W)
+    return (np.asarray(x, np.float64) @ np.asarray(W, np.float64).T).astype(np.float32)
+
+
+def moss_ref_sections(glue16, vec32, D, C4, tin):
+    """The MOSS reference form's exported glue sections (hxa_dit_export 2 nb: fp16 head_mod [2D][D] | text_proj
+    [D][tin]; 2 nb + 1: fp32 vectors then video_embed [D][C4] | t0 [D][256] | t2 [D][D] | final_linear [C4][D]) ->
+    (glue, vec) as oracle_moss_rapid_step takes them."""
+    Wh, Wt = split_flat(glue16, [(2 * D, D), (D, tin)])
+    v = split_flat(vec32, [(D,), (D,), (D,), (6 * D,), (2 * D,), (D,), (C4, C4), (C4,), (C4,), (D, C4), (D, 256),
+                           (D, D), (C4, D)])
+    return (v[9], v[10], v[11], Wh, v[12], Wt), v[:9]
+
+
+def split_flat(buf, shapes):
+    out, o = [], 0
+    for sh in shapes:
+        n = int(np.prod(sh))
+        out.append(buf[o:o + n].reshape(sh))
+        o += n
+    assert o == buf.size
+    return out
+
+
 def oracle_moss_rapid_step(z, x0, txt16, code, blocks, modw, glue, vec, *, D, H, F, C4, ntxt, Ttot, gh, gw,
-                           attn_mode=0, rope_scale=1.0):
+                           attn_mode=0, rope_scale=1.0, bands=None):
     """One rapid-moss step (mossrun.cpp:307-334) with the reference's glue, image by image. z, x0: token rows
     [B][T][C4] (feature c*4 + ph*2 + pw) of a gh x gw grid; returns the new x0. rope_scale: the low-res steps' image
     position scale (mossrun.cpp:313).
@@ -221,16 +249,18 @@ def oracle_moss_rapid_step(z, x0, txt16, code, blocks, modw, glue, vec, *, D, H,
     Wm b + bm [6][D], head modulation Wh b + bh; x_in = z + x0 Q^T per token; rows = Wv x_in + bv, then the text rows
     f16(text Wt^T) (the text projection into zeroed rows); blocks; head RMS(x) nfin (1 + head[D:]) + head[:D],
     v = Wfin r, x0 = z - v.
-    glue = (Wv [D][C4], T0 [D][256], T2 [D][D], Wh [2D][D], Wfin [C4][D], Wt [D][ntxt_in]) fp16, modw [6D][D] fp16,
-    vec = (bv, b0, b2, bm, bh, nfin, Q [C4][C4], bn_mean, bn_var) fp32."""
+    glue = (Wv [D][C4], T0 [D][256], T2 [D][D], Wh [2D][D], Wfin [C4][D], Wt [D][ntxt_in]): Wh and Wt fp16, the
+    others fp32 or fp16; modw [6D][D] fp16; vec = (bv, b0, b2, bm, bh, nfin, Q [C4][C4], bn_mean, bn_var) fp32;
+    bands: the 16 RoPE bands (default 10000^(-i/16))."""
     Wv, T0, T2, Wh, Wfin, Wt = glue
     bv, b0, b2, bm, bh, nfin, Q = vec[:7]
     e = hxo.sinusoid(code, 256)[None, :]
-    a = hxo.linear_f32(e, T0) + b0
-    bt = hxo.linear_f32(silu(a), T2) + b2
+    a = lin(e, T0) + b0
+    bt = lin(silu(a), T2) + b2
     mod6 = (hxo.linear_f32(bt, modw)[0] + bm).reshape(6, D).astype(np.float32)
     head = (hxo.linear_f32(bt, Wh)[0] + bh).astype(np.float32)
-    bands = (1.0 / 10000.0 ** (np.arange(16) / 16.0)).astype(np.float32)
+    if bands is None:
+        bands = (1.0 / 10000.0 ** (np.arange(16) / 16.0)).astype(np.float32)
     c, sn = hxo.rope_moss_scaled(gh, gw, ntxt, bands, rope_scale)  # image positions x rope_scale (low-res steps)
     cos = np.ones((Ttot, 64), np.float32)
     sin = np.zeros((Ttot, 64), np.float32)
@@ -240,14 +270,14 @@ def oracle_moss_rapid_step(z, x0, txt16, code, blocks, modw, glue, vec, *, D, H,
     for b in range(z.shape[0]):
         xin = (z[b].astype(np.float64) + x0[b].astype(np.float64) @ Q.astype(np.float64).T).astype(np.float32)
         x = np.zeros((Ttot, D), np.float32)
-        x[:timg] = hxo.linear_f32(xin, Wv) + bv
+        x[:timg] = lin(xin, Wv) + bv
         x[timg:timg + ntxt] = f16(hxo.gemm(txt16[b], Wt)).astype(np.float32)
         for w in blocks:
             x, _, _ = hxo.moss_block(x, mod6, cos, sin, w, H=H, F=F, nvalid=timg + ntxt, attn_mode=attn_mode)
         xi = x[:timg].astype(np.float64)
         rs = 1.0 / np.sqrt((xi * xi).mean(-1, keepdims=True) + 1e-6)
         r = (xi * rs * nfin * (1.0 + head[D:]) + head[:D]).astype(np.float32)
-        out[b] = z[b] - hxo.linear_f32(r, Wfin)
+        out[b] = z[b] - lin(r, Wfin)
     return out
 
 

@@ -14,7 +14,8 @@ import pytest
 
 from oracle import hxo
 from tests._helpers import (bn_unpatchify, delta_metrics, f16, oracle_anima_ref_velocity, oracle_anima_velocity,
-                            oracle_moss_rapid_step, oracle_moss_velocity, rel, unpack_weights)
+                            moss_ref_sections, oracle_moss_rapid_step, oracle_moss_velocity, rel,
+                            unpack_weights)
 
 pytestmark = pytest.mark.gpu
 
@@ -825,10 +826,8 @@ def test_dit_moss_rapid_sampler():
         layout = hip.pack_layout(1, D, F, 0, hip.W_Q8, hip.W_Q4)
         blocks = [unpack_weights(_export(hip, p, k), 1, D, F, 0, hip.W_Q8, hip.W_Q4, layout) for k in range(nb)]
         modw = _export(hip, p, nb).view(np.uint16).reshape(6 * D, D)
-        glue = _split(_export(hip, p, 2 * nb).view(np.uint16),
-                      [(D, C4), (D, 256), (D, D), (2 * D, D), (C4, D), (D, tin)])
-        vec = _split(_export(hip, p, 2 * nb + 1).view(np.float32),
-                     [(D,), (D,), (D,), (6 * D,), (2 * D,), (D,), (C4, C4), (C4,), (C4,)])
+        glue, vec = moss_ref_sections(_export(hip, p, 2 * nb).view(np.uint16),
+                                      _export(hip, p, 2 * nb + 1).view(np.float32), D, C4, tin)
         codes = [0.999, 0.75, 0.5, 0.25]
         zr = np.stack([hxo.patchify(z[b]) for b in range(B)])
         x0 = np.zeros_like(zr)

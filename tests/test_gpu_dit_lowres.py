@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 
 from oracle import hxo
-from tests._helpers import (bn_unpatchify, delta_metrics, f16, oracle_anima_ref_velocity, oracle_moss_rapid_step, rel)
+from tests._helpers import (bn_unpatchify, delta_metrics, f16, oracle_anima_ref_velocity,
+                            moss_ref_sections, oracle_moss_rapid_step, rel)
 from tests.test_gpu_block import _anima_ref_weights, _export, _split, unpack_weights
 
 pytestmark = pytest.mark.gpu
@@ -130,10 +131,8 @@ def test_dit_moss_lowres_first_steps_vs_oracle():
         layout = hip.pack_layout(1, D, F, 0, hip.W_Q8, hip.W_Q4)
         blocks = [unpack_weights(_export(hip, p, k), 1, D, F, 0, hip.W_Q8, hip.W_Q4, layout) for k in range(nb)]
         modw = _export(hip, p, nb).view(np.uint16).reshape(6 * D, D)
-        glue = _split(_export(hip, p, 2 * nb).view(np.uint16),
-                      [(D, C4), (D, 256), (D, D), (2 * D, D), (C4, D), (D, tin)])
-        vec = _split(_export(hip, p, 2 * nb + 1).view(np.float32),
-                     [(D,), (D,), (D,), (6 * D,), (2 * D,), (D,), (C4, C4), (C4,), (C4,)])
+        glue, vec = moss_ref_sections(_export(hip, p, 2 * nb).view(np.uint16),
+                                      _export(hip, p, 2 * nb + 1).view(np.float32), D, C4, tin)
         codes = [0.999, 0.75, 0.5, 0.25]
         txt16 = f16(txt)
         zr = np.stack([hxo.patchify(z[b]) for b in range(B)])

@@ -22,7 +22,7 @@ import numpy as np
 import pytest
 
 from oracle import hxo
-from tests._helpers import (bn_unpatchify, f16, oracle_moss_rapid_step, oracle_moss_velocity, rel, silu,
+from tests._helpers import (bn_unpatchify, f16, moss_ref_sections, oracle_moss_rapid_step, oracle_moss_velocity, rel, silu,
                             unpack_weights)
 
 pytestmark = pytest.mark.gpu
@@ -135,10 +135,8 @@ def test_dit_moss_6656tok_rapid_steps_vs_oracle():
         got = np.zeros_like(z)
         hip.check(lib.hxa_dit_get_latent(p, got.ctypes.data), "get_latent")
         blocks = _blocks(hip, lib, p)
-        glue = _split(_export(lib, p, 2 * NB).view(np.uint16),
-                      [(D, C4), (D, 256), (D, D), (2 * D, D), (C4, D), (D, TIN)])
-        vec = _split(_export(lib, p, 2 * NB + 1).view(np.float32),
-                     [(D,), (D,), (D,), (6 * D,), (2 * D,), (D,), (C4, C4), (C4,), (C4,)])
+        glue, vec = moss_ref_sections(_export(lib, p, 2 * NB).view(np.uint16),
+                                      _export(lib, p, 2 * NB + 1).view(np.float32), D, C4, TIN)
         zr = hxo.patchify(z[0])[None]
         x0 = np.zeros_like(zr)
         txt16 = f16(txt)
