@@ -525,6 +525,9 @@ def kernel_probe(reps, family):
     fn, n, flops, nbytes, kname = fam[family]
     for _ in range(reps):
         fn()
+    # the same launches again between two HIP events (bench.py's own timing), so a kernel trace of this command holds
+    # both: its mean over the second `reps` groups and this average describe the same launches
+    ev_us = _time_launches(L, hip, fn, s, reps=reps, warm=0) * 1e3 / n
     nb = 256 << 20
     src = hip.DeviceArray((nb,), np.uint8)
     dst = hip.DeviceArray((nb,), np.uint8)
@@ -534,7 +537,7 @@ def kernel_probe(reps, family):
         hip.check(L.hxa_d2d(dst.ptr, src.ptr, nb), "copy")
     hip.check(L.hxa_stream_sync(s), "sync")
     print(f"kernel probe: {reps} x {family} ({n} launches, {kname}, {nbytes / n:.0f} algorithmic bytes per launch),"
-          f" 3 x copy {nb} B", flush=True)
+          f" then {reps} x again between HIP events: {ev_us:.2f} us per launch; 3 x copy {nb} B", flush=True)
 
 
 BLK_W_END, BLK_GAIN, BLK_MODW, BLK_TOTAL = 125829120, 125829120, 125833216, 138416128  # blk_wlayout.h:3-20
@@ -589,13 +592,23 @@ def abi_chain(runs=3):
 
 
 def _cpu_model():
+    """The first CPU's model name with its family / model / stepping numbers and microcode from /proc/cpuinfo (a
+    virtual machine may show a short model name; the numbers still identify the part), and the logical CPU count."""
+    f = {}
+    n = 0
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k == "processor":
+                n += 1
+            if k in ("model name", "cpu family", "model", "stepping", "microcode", "cpu MHz") and k not in f:
+                f[k] = v.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    return (f"{f.get('model name', 'unknown')} (family {f.get('cpu family', '?')}, model {f.get('model', '?')}, "
+            f"stepping {f.get('stepping', '?')}, microcode {f.get('microcode', '?')}, {f.get('cpu MHz', '?')} MHz; "
+            f"{n} logical CPUs in the host)")
 
 
 def cpu_baseline():
