@@ -7,8 +7,11 @@
 //
 // Work split: a workgroup of 2 x NWH waves owns 32 NWH queries of one head (NWH = 4: 128 queries, or 3: 96 queries
 // when that fills the CUs better). Waves [0, NWH) take the first half of the key tiles, the others the second half
-// (up to two waves per SIMD, so one wave's softmax overlaps another's MFMAs); the halves are merged through LDS at
-// the end. Each wave owns 32 queries and keeps Q in registers.
+// (up to two waves per SIMD, one of each half); the halves are merged through LDS at the end. Each wave owns 32
+// queries and keeps Q in registers. Two schedules of the key loop: lock-step (one barrier per tile for both halves)
+// and, for whole tiles in a multiple of 4, ping-pong (each tile split into a VALU phase, the softmax, and an MFMA
+// phase, PV with the next QK; the halves one phase apart, so the two waves of a SIMD alternate between the two
+// kinds of work: 5-6% faster at 1536 and 6656 keys on MI355X).
 //
 // Per 64-key tile a wave computes S^T = K . Q^T (v_mfma_f32_32x32x16_f16), so a lane holds 16 scores of ONE query
 // and the row max needs a single exchange between the wave's two halves (v_permlane32_swap). K rows are stored in LDS with rows 4-7 and 8-11 of every 16 swapped,
@@ -19,6 +22,9 @@
 // before the softmax of tile j so the exponentials overlap them. exp(s - m) is exp2(s*log2e - m*log2e) (one FMA +
 // v_exp_f32). O and the row sum are rescaled only when the running max grows by more than 5.5 (P <= e^5.5 in fp16
 // otherwise), which keeps the result exact up to rounding while skipping most rescales.
+#include <cstdlib>
+#include <type_traits>
+
 #include "hxa_common.h"
 #include "kernels.h"
 
@@ -40,12 +46,14 @@ HXA_DEV float16_t mfma(half8_t a, half8_t b, float16_t c) { return __builtin_amd
 // addresses. PF: the launch touches weights for the next kernel (p.pf_bytes > 0). Both are compile-time so that the
 // main loop holds only the code it runs: the general form kept 44 - 62 scalar registers spilled to VGPR lanes and
 // their v_readlane / v_writelane in the loop.
-template <int NWH, bool FULL, bool PF>
+template <int NWH, bool FULL, bool PF, bool PP = false>
 __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) {
+  static_assert(!PP || FULL, "the ping-pong form runs whole tiles only");
   constexpr int QB = NWH * 32;  // queries per workgroup
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // waves w and w + NWH share a SIMD (waves are dealt to the SIMDs round-robin): one wave of each key half
   const int half = wave / NWH, wq = wave % NWH, g = lane >> 5, ql = lane & 31;
   // XCD-aware order: the query blocks of one head run on one XCD (its L2 keeps that head's K / V^T)
   const int ntot = nqb * p.H, bid = blockIdx.x;
@@ -85,8 +93,10 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
     const int d = 8 * blk + (lane >> 3), cv = (lane & 7) ^ ((d >> 1) & 7);
     voff[j] = ((uint32_t)d * (uint32_t)p.ldvt + cv * 8) * 2u;
   }
-  auto load_kv = [&](int i, bool with_k, bool with_v) {
-    const int key0 = (t0 + i) * KT;
+  // tile i of this half into buffer (i & 1); src >= 0: the half's tile src into that buffer instead (the ping-pong
+  // form's loads past the last tile, into a buffer that is never read again)
+  auto load_kv = [&](int i, bool with_k, bool with_v, int src = -1) {
+    const int key0 = (t0 + (src >= 0 ? src : i)) * KT;
     if (FULL || key0 + KT <= p.NKV) {
       if (with_k) {
         const hxa_h *kt = k + (long)key0 * p.ldk;
@@ -177,18 +187,9 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
       }
   };
 
-  // one key tile: (mask, max, rescale) of tile i, then QK of tile i+1 overlapped with the exponentials of tile i,
-  // then O^T += V^T P^T for tile i
-  auto step = [&](int i, float16_t(&Sc)[2], float16_t(&Sn)[2]) {
-    wait_vm<0>();
-    __builtin_amdgcn_s_barrier();  // tile i V^T and tile i+1 K landed; every wave is done with tiles i-1 / i reads
-    asm volatile("" ::: "memory");
-    const bool cur = i < nmine, nxt = i + 1 < nmine;
-    if (!cur) {
-      if (i + 2 < nmine) load_kv(i + 2, true, false);
-      if (i + 1 < nmine) load_kv(i + 1, false, true);
-      return;
-    }
+  // (mask, max, rescale) of tile i, then QK of tile i+1 (Sn) overlapped with the exponentials of tile i (pf)
+  auto softmax_qk = [&](int i, float16_t(&Sc)[2], float16_t(&Sn)[2], half8_t(&pf)[2][2]) {
+    const bool nxt = i + 1 < nmine;
     const int key0 = (t0 + i) * KT;
     if (!FULL && key0 + KT > p.nvalid) {
 #pragma unroll
@@ -219,18 +220,12 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
     // One straight-line block: QK of tile i+1 (clamped: the last tile recomputes its own, unused scores) with the
     // K fragments read one step ahead, the exponentials of tile i between its MFMAs, then PV of tile i.
     const uint8_t *kb = kbuf(nxt ? i + 1 : i);
-    const uint8_t *vb = vbuf(i);
     auto kfrag = [&](int ds, int kb2) {
       const int row = kb2 * 32 + ql, c = 2 * ds + g;
       return *(const half8_t *)(kb + row * 256 + ((c ^ (row & 15)) << 4));
     };
-    auto vfrag = [&](int j) {  // j = (kb2 * 2 + ks) * 4 + dblk
-      const int dblk = j & 3, kk = j >> 2, d = dblk * 32 + ql, c = 2 * kk + g;
-      return *(const half8_t *)(vb + d * 128 + ((c ^ ((d >> 1) & 7)) << 4));
-    };
     Sn[0] = (float16_t){};
     Sn[1] = (float16_t){};
-    half8_t pf[2][2];
     float ls[2] = {0.0f, 0.0f};
     // sched_barrier(0) fences keep each fragment read one stage ahead of the MFMA that consumes it (the scheduler
     // would otherwise sink the reads next to their uses under this register pressure)
@@ -259,10 +254,14 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
       }
     }
     lsum += ls[0] + ls[1];
-    // the next tiles' loads after the QK / exponential block, not ahead of it (their issue would delay the softmax)
-    if (i + 2 < nmine) load_kv(i + 2, true, false);
-    if (i + 1 < nmine) load_kv(i + 1, false, true);
-    if (PF && i < pf_steps) touch(i);
+  };
+  // O^T += V^T P^T for tile i
+  auto pv = [&](int i, const half8_t(&pf)[2][2]) {
+    const uint8_t *vb = vbuf(i);
+    auto vfrag = [&](int j) {  // j = (kb2 * 2 + ks) * 4 + dblk
+      const int dblk = j & 3, kk = j >> 2, d = dblk * 32 + ql, c = 2 * kk + g;
+      return *(const half8_t *)(vb + d * 128 + ((c ^ ((d >> 1) & 7)) << 4));
+    };
     half8_t va[2];
     __builtin_amdgcn_sched_barrier(0);
     va[0] = vfrag(0);
@@ -275,6 +274,24 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
     }
     __builtin_amdgcn_sched_barrier(0);
   };
+  // lock-step form: one key tile per step, one barrier per step for both halves
+  auto step = [&](int i, float16_t(&Sc)[2], float16_t(&Sn)[2]) {
+    wait_vm<0>();
+    __builtin_amdgcn_s_barrier();  // tile i V^T and tile i+1 K landed; every wave is done with tiles i-1 / i reads
+    asm volatile("" ::: "memory");
+    if (i >= nmine) {
+      if (i + 2 < nmine) load_kv(i + 2, true, false);
+      if (i + 1 < nmine) load_kv(i + 1, false, true);
+      return;
+    }
+    half8_t pf[2][2];
+    softmax_qk(i, Sc, Sn, pf);
+    // the next tiles' loads after the QK / exponential block, not ahead of it (their issue would delay the softmax)
+    if (i + 2 < nmine) load_kv(i + 2, true, false);
+    if (i + 1 < nmine) load_kv(i + 1, false, true);
+    if (PF && i < pf_steps) touch(i);
+    pv(i, pf);
+  };
 
   if (nmine > 0) load_kv(0, true, true);
   if (nmine > 1) load_kv(1, true, false);
@@ -283,9 +300,115 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   asm volatile("" ::: "memory");
   float16_t Sa[2], Sb[2];
   if (nmine > 0) qk(0, Sa);
-  for (int i = 0; i < nh; i += 2) {
-    step(i, Sa, Sb);
-    if (i + 1 < nh) step(i + 1, Sb, Sa);
+  if constexpr (PP) {
+    // Ping-pong form (both halves hold nh tiles, whole tiles): each tile is two phases, V(i) = the softmax of tile i
+    // (VALU only: max, rescale, exponentials -> P(i)) and M(i) = its PV with the QK of tile i+1 (MFMA only), and
+    // half 1 runs one phase behind half 0. The waves of a SIMD belong to different halves (waves w and w + NWH), so
+    // in every phase one of them keeps the matrix core busy while the other computes exponentials. One workgroup
+    // barrier per phase (2 nh + 1 for either half).
+    //  V(i) issues V(i+1) (its buffer held V(i-1), read in M(i-1)) and, from i = 1, K(i+2) (its buffer held K(i),
+    //  read in M(i-1)); K(2) is issued in M(0), since half 0's QK of tile 0 has no barrier before V(0). Loads past
+    //  the half's last tile reload that tile into the free buffer (M of the last tile skips its QK), so every V
+    //  phase issues the same loads and M(i), i >= 1, waits until at most that many are in flight: K(i+1) and V(i),
+    //  issued one V phase earlier, have landed.
+    half8_t pf[2][2];
+    constexpr int NLDMIN = 16 / NWH;  // the fewest K (or V) tile loads a wave issues
+    auto bar = [&]() {
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+    // O^T += V^T P^T of tile i with, when qk, S = K Q^T of tile i+1: 16 + 16 MFMAs, the fragments read two ahead
+    auto mphase = [&](int i, auto qk_next) {
+      constexpr int nm = decltype(qk_next)::value ? 32 : 16;
+      const uint8_t *vb = vbuf(i), *kb = kbuf(i + 1);
+      auto frag = [&](int j) {
+        if (j < 16) {  // V^T: j = (kb2 * 2 + ks) * 4 + dblk
+          const int dblk = j & 3, kk = j >> 2, d = dblk * 32 + ql, c = 2 * kk + g;
+          return *(const half8_t *)(vb + d * 128 + ((c ^ ((d >> 1) & 7)) << 4));
+        }
+        const int q = j - 16, ds = q >> 1, kb2 = q & 1, row = kb2 * 32 + ql, c = 2 * ds + g;
+        return *(const half8_t *)(kb + row * 256 + ((c ^ (row & 15)) << 4));
+      };
+      if constexpr (nm == 32) {
+        Sa[0] = (float16_t){};
+        Sa[1] = (float16_t){};
+      }
+      half8_t fr[3];
+      fr[0] = frag(0);
+      fr[1] = frag(1);
+#pragma unroll
+      for (int j = 0; j < nm; j++) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (j + 2 < nm) fr[(j + 2) % 3] = frag(j + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        if (j < 16) {
+          acc[j & 3] = mfma(fr[j % 3], pf[j >> 3][(j >> 2) & 1], acc[j & 3]);
+        } else {
+          const int q = j - 16;
+          Sa[q & 1] = mfma(fr[j % 3], qf[q >> 1], Sa[q & 1]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // max, rescale and exponentials of tile i (scores in Sa) -> pf, row sums into lsum
+    auto vphase = [&](int i) {
+      float mt = -INFINITY;
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) mt = fmaxf(mt, Sa[kb2][r]);
+      {
+        float lo, hi;
+        halves(mt, lo, hi);
+        mt = fmaxf(lo, hi);
+      }
+      const bool need = mt > mrun + RESCALE_TH;  // also when mrun is still -inf
+      if (__any(need)) {
+        const float alpha = need ? __builtin_amdgcn_exp2f((mrun - mt) * L2E) : 1.0f;
+        if (need) mrun = mt;
+        lsum *= alpha;
+#pragma unroll
+        for (int d = 0; d < 4; d++) acc[d] *= alpha;
+      }
+      const float mb = (mrun == -INFINITY ? 0.0f : mrun) * L2E;
+      float ls[2] = {0.0f, 0.0f};
+#pragma unroll
+      for (int idx = 0; idx < 32; idx += 2) {
+        const int kb2 = idx >> 4, r = idx & 15;
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(Sa[kb2][r], L2E, -mb));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(Sa[kb2][r + 1], L2E, -mb));
+        const half2_t h2 = {(hxa_h)p0, (hxa_h)p1};
+        pf[kb2][r >> 3][r & 7] = h2[0];
+        pf[kb2][r >> 3][(r & 7) + 1] = h2[1];
+        ls[(idx >> 1) & 1] = __builtin_amdgcn_fdot2(h2, (half2_t){(hxa_h)1.0f, (hxa_h)1.0f}, ls[(idx >> 1) & 1], false);
+      }
+      lsum += ls[0] + ls[1];
+    };
+    auto vstep = [&](int i) {
+      if (i > 0) load_kv(i + 2, true, false, min(i + 2, nmine - 1));
+      load_kv(i + 1, false, true, min(i + 1, nmine - 1));
+      if (PF && i < pf_steps) touch(i);
+      vphase(i);
+      if (i > 0) wait_vm<2 * NLDMIN>();
+      bar();
+      if (i == 0) load_kv(2, true, false, min(2, nmine - 1));
+    };
+    if (half == 1) bar();  // phase 0: half 1 has done its QK of tile 0 (half 0 its QK and V(0))
+    for (int i = 0; i < nh - 1; i++) {
+      vstep(i);
+      mphase(i, std::true_type{});
+      bar();
+    }
+    vstep(nh - 1);
+    mphase(nh - 1, std::false_type{});  // the last tile: no next QK
+    bar();
+    if (half == 0) bar();  // the last phase: half 1's M(nh - 1)
+  } else {
+    for (int i = 0; i < nh; i += 2) {
+      step(i, Sa, Sb);
+      if (i + 1 < nh) step(i + 1, Sb, Sa);
+    }
   }
 
   // merge the two key halves: half 1 publishes (m, l, O) per lane, half 0 combines and stores
@@ -416,10 +539,12 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   static bool attr = false;
   static int num_cu = 0;
   if (!attr) {
-    const void *kerns[] = {(const void *)attn_kernel<4, false, false>, (const void *)attn_kernel<4, false, true>,
-                           (const void *)attn_kernel<4, true, false>,  (const void *)attn_kernel<4, true, true>,
-                           (const void *)attn_kernel<3, false, false>, (const void *)attn_kernel<3, false, true>,
-                           (const void *)attn_kernel<3, true, false>,  (const void *)attn_kernel<3, true, true>};
+    const void *kerns[] = {(const void *)attn_kernel<4, false, false>,      (const void *)attn_kernel<4, false, true>,
+                           (const void *)attn_kernel<4, true, false>,       (const void *)attn_kernel<4, true, true>,
+                           (const void *)attn_kernel<3, false, false>,      (const void *)attn_kernel<3, false, true>,
+                           (const void *)attn_kernel<3, true, false>,       (const void *)attn_kernel<3, true, true>,
+                           (const void *)attn_kernel<4, true, false, true>, (const void *)attn_kernel<4, true, true, true>,
+                           (const void *)attn_kernel<3, true, false, true>, (const void *)attn_kernel<3, true, true, true>};
     for (const void *kf : kerns)
       if (hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES + SINK_BYTES) != hipSuccess)
         return HXA_E_HIP;
@@ -453,6 +578,18 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   const bool full = p.nvalid % KT == 0, pf = p.pf_bytes > 0;
   dim3 grid(nqb * p.H, p.batch);
   const int lds = LDS_BYTES + SINK_BYTES;
+  // the ping-pong form: whole tiles, the same even number of tiles in both halves (HXA_ATTN_PP=0: lock-step form)
+  static const int pp_env = [] {
+    const char *e = getenv("HXA_ATTN_PP");
+    return e ? atoi(e) : 1;
+  }();
+  if (pp_env && full && (p.nvalid / KT) % 4 == 0) {
+    if (small) pf ? hxa_launch(attn_kernel<3, true, true, true>, grid, dim3(384), lds, st, pk, nqb)
+               : hxa_launch(attn_kernel<3, true, false, true>, grid, dim3(384), lds, st, pk, nqb);
+    else pf ? hxa_launch(attn_kernel<4, true, true, true>, grid, dim3(512), lds, st, pk, nqb)
+            : hxa_launch(attn_kernel<4, true, false, true>, grid, dim3(512), lds, st, pk, nqb);
+    return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
+  }
   if (small) {
     if (full) pf ? hxa_launch(attn_kernel<3, true, true>, grid, dim3(384), lds, st, pk, nqb)
               : hxa_launch(attn_kernel<3, true, false>, grid, dim3(384), lds, st, pk, nqb);
