@@ -960,9 +960,9 @@ HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
     constexpr int L = decltype(later_c)::value;
     wait_vm<L * (LPS + NVEC)>();
   };
-  // Quantised W is read raw in the memory phase (wq, scale sc, offset zc) and dequantised in the compute phase, where
-  // its VALU work issues under the MFMAs (the memory phase stays a phase of LDS reads and loads only): the
-  // dequantisation of the second 16-deep slice overlaps the first slice's MFMAs.
+  // Quantised W is read raw in the memory phase (wq, scale sc, offset zc). The first 16-deep slice is dequantised at
+  // the end of the memory phase, once the reads have landed (the other group's MFMAs run meanwhile), so the compute
+  // phase starts with MFMAs; the second slice's dequantisation issues under the first slice's MFMAs.
   typedef typename std::conditional<FMT == HXA_W_Q8, uint2_t, uint32_t>::type raw_t;
   [[maybe_unused]] raw_t wq[2][NI];
   [[maybe_unused]] hxa_h sc[NI], zc[NI];
@@ -1017,11 +1017,13 @@ HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
   for (int j = 0; j < NI; j++)
 #pragma unroll
     for (int i = 0; i < MI; i++) acc[j][i] = (float16_t){};
-  auto mfmas = [&](const half8_t (&fa)[2][MI], half8_t (&fb)[2][NI]) {
+  auto dequant0 = [&](half8_t (&fb)[2][NI]) {
     if constexpr (FMT != HXA_W_F16) {
 #pragma unroll
       for (int j = 0; j < NI; j++) dequant(0, j, fb);
     }
+  };
+  auto mfmas = [&](const half8_t (&fa)[2][MI], half8_t (&fb)[2][NI]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ks++)
 #pragma unroll
@@ -1052,6 +1054,7 @@ HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
       read_frags(j % NS, fa, fb);
       if (j >= 1) issue((j + NS - 1) % NS, j + NS - 1);
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the fragments are in registers
+      dequant0(fb);
       bar();
       // phase 2j+1: compute stage j, then wait for stage j+1 (stages j+2, j+3 may still fly)
       __builtin_amdgcn_s_setprio(1);
@@ -1073,6 +1076,7 @@ HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
       // phase 2j+1: read stage j
       read_frags(j % NS, fa, fb);
       __builtin_amdgcn_s_waitcnt(0xc07f);
+      dequant0(fb);
       bar();
     }
     // phase 2 nk: compute stage nk-1
