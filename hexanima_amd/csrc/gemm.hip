@@ -718,8 +718,8 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
     for (int i = 0; i < MI; i++) acc[j][i] = (float16_t){};
 
   // Fragments of one stage: A rows fa[ks][i]; W rows fb[ks][j]. fp16 W fragments are read directly; quantised W
-  // is read raw (wq, scale ws_, offset wz) and dequantised by dequant(ks) right before the MFMAs that need it, so the
-  // LDS latency of the raw reads is covered by the preceding MFMAs.
+  // is read raw (wq, scale ws_, offset wz) and dequantised ahead of the MFMAs that need it: the second slice under
+  // the first slice's MFMAs, the first slice of the next stage at the end of a step, under its last MFMAs.
   typedef typename std::conditional<FMT == HXA_W_Q8, uint2_t, uint32_t>::type raw_t;
   raw_t wq0[2][NI], wq1[2][NI];
   hxa_h sc0[NI], sc1[NI], zc0[NI], zc1[NI];
@@ -791,7 +791,6 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   auto step = [&](int kt, half8_t (&ca)[2][MI], half8_t (&cb)[2][NI], half8_t (&na)[2][MI], half8_t (&nb)[2][NI],
                   raw_t (&cq)[2][NI], hxa_h (&cs)[NI], hxa_h (&cz)[NI], raw_t (&nq)[2][NI], hxa_h (&ns)[NI],
                   hxa_h (&nz)[NI]) {
-    dequant(0, cb, cq, cs, cz);
     mfma_range(ca[0], cb[0], 0, 2);
     __builtin_amdgcn_sched_barrier(0);
     wait_stage<BM, BN, FMT, ASYM, NW, NS - 2>(wave);  // tile kt+1 complete; tiles kt+2 .. kt+NS-1 may still fly
@@ -811,6 +810,8 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
     }
     __builtin_amdgcn_sched_barrier(0);
+    // stage kt+1's first slice, under this stage's last MFMAs: the next step starts with MFMAs
+    dequant(0, nb, nq, ns, nz);
   };
 
   // prologue: fill all NS stages (tiles 0..NS-1); step kt then refills stage kt % NS with tile kt + NS
@@ -823,6 +824,7 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   read_frags(0, fa0, fb0, wq0, sc0, zc0);
+  dequant(0, fb0, wq0, sc0, zc0);
   [[maybe_unused]] half4_t first[SPLIT2 ? NI : 1][SPLIT2 ? MI : 1][4];
   for (int kt = 0; kt < nk; kt += 2) {
     step(kt, fa0, fb0, fa1, fb1, wq0, sc0, zc0, wq1, sc1, zc1);
