@@ -334,30 +334,33 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
         Sa[0] = (float16_t){};
         Sa[1] = (float16_t){};
       }
-      half8_t fr[3];
-      fr[0] = frag(0);
-      fr[1] = frag(1);
+      constexpr int AH = 2;  // fragment reads in flight ahead of the MFMA stream (4 or 6: no faster)
+      half8_t fr[AH + 1];
+#pragma unroll
+      for (int j = 0; j < AH; j++) fr[j] = frag(j);
 #pragma unroll
       for (int j = 0; j < nm; j++) {
         __builtin_amdgcn_sched_barrier(0);
-        if (j + 2 < nm) fr[(j + 2) % 3] = frag(j + 2);
+        if (j + AH < nm) fr[(j + AH) % (AH + 1)] = frag(j + AH);
         __builtin_amdgcn_sched_barrier(0);
         if (j < 16) {
-          acc[j & 3] = mfma(fr[j % 3], pf[j >> 3][(j >> 2) & 1], acc[j & 3]);
+          acc[j & 3] = mfma(fr[j % (AH + 1)], pf[j >> 3][(j >> 2) & 1], acc[j & 3]);
         } else {
           const int q = j - 16;
-          Sa[q & 1] = mfma(fr[j % 3], qf[q >> 1], Sa[q & 1]);
+          Sa[q & 1] = mfma(fr[j % (AH + 1)], qf[q >> 1], Sa[q & 1]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     };
     // max, rescale and exponentials of tile i (scores in Sa) -> pf, row sums into lsum
     auto vphase = [&](int i) {
-      float mt = -INFINITY;
+      // the row max as four independent chains (one wave issues this phase alone: latency, not throughput)
+      float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; kb2++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) mt = fmaxf(mt, Sa[kb2][r]);
+        for (int r = 0; r < 16; r++) m4[r & 3] = fmaxf(m4[r & 3], Sa[kb2][r]);
+      float mt = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
       {
         float lo, hi;
         halves(mt, lo, hi);
@@ -372,7 +375,7 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
         for (int d = 0; d < 4; d++) acc[d] *= alpha;
       }
       const float mb = (mrun == -INFINITY ? 0.0f : mrun) * L2E;
-      float ls[2] = {0.0f, 0.0f};
+      float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int idx = 0; idx < 32; idx += 2) {
         const int kb2 = idx >> 4, r = idx & 15;
@@ -381,9 +384,9 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
         const half2_t h2 = {(hxa_h)p0, (hxa_h)p1};
         pf[kb2][r >> 3][r & 7] = h2[0];
         pf[kb2][r >> 3][(r & 7) + 1] = h2[1];
-        ls[(idx >> 1) & 1] = __builtin_amdgcn_fdot2(h2, (half2_t){(hxa_h)1.0f, (hxa_h)1.0f}, ls[(idx >> 1) & 1], false);
+        ls[(idx >> 1) & 3] = __builtin_amdgcn_fdot2(h2, (half2_t){(hxa_h)1.0f, (hxa_h)1.0f}, ls[(idx >> 1) & 3], false);
       }
-      lsum += ls[0] + ls[1];
+      lsum += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     };
     auto vstep = [&](int i) {
       if (i > 0) load_kv(i + 2, true, false, min(i + 2, nmine - 1));
