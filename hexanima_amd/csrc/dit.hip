@@ -261,7 +261,7 @@ int record_step(Dit &d, const Pass &ps) {
   const hxa_block_dims &b = ps.bd;
   const int B = b.batch, D = b.D, C4 = 4 * d.cfg.lat_c, temb = d.cfg.temb, nb = d.cfg.nblocks;
   hipStream_t st = d.st;
-  const bool moss_ref = d.form == 1 && b.kind == 1;
+  const bool moss_ref = d.form == 1 && b.kind != 0;
   if (hxa_block_ws_bytes(&b) > d.ws_bytes) return HXA_E_ARG;  // a low-res pass needs no more than the full one
   if (d.form == 1) DTRY(b.kind == 0 ? record_prelude_anima_ref(d) : record_prelude_moss_ref(d));
   if (d.form == 0) {
@@ -281,7 +281,7 @@ int record_step(Dit &d, const Pass &ps) {
   else
     DTRY(hxa_patch_embed_launch(ps.lat_in, B, d.cfg.lat_c, ps.lat_h, ps.lat_w, d.Wemb, D, d.x, ps.Ttot, st));
   for (int i = 0; i < B; i++) {
-    if (b.kind == 1) {
+    if (b.kind != 0) {
       float *xt = d.x + ((long)i * ps.Ttot + ps.Timg) * D;
       DTRY(hxa_fill_const_launch(xt, 0, (size_t)(ps.Ttot - ps.Timg) * D, 0.0f, st));
       HxaWeight wt{HXA_W_F16, D, d.cfg.ntxt_in, d.Wtxt, nullptr, nullptr};
@@ -343,9 +343,17 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   d.bd = cfg->blk;
   hxa_block_dims &b = d.bd;
   const int D = b.D, B = b.batch, C4 = 4 * cfg->lat_c;
-  if (b.kind != 0 && b.kind != 1) {  // the synthetic DiT builds Anima- or MOSS-structure packs without LoRA
+  // kind 2, MOSS blocks with the rapid-moss LoRA: the reference form only, weights loaded from MOSS block files
+  // (hxa_dit_load_moss_block; the packs start at zero), the file's shape
+  if (b.kind != 0 && b.kind != 1 && b.kind != 2) {
     delete dp;
     return dfail(HXA_E_MODE, "dit: block kind");
+  }
+  if (b.kind == 2 && (cfg->form != 1 || b.D != 3072 || b.H != 24 || b.F != 8192 || b.fmt_attn != HXA_W_Q8 ||
+                      b.fmt_mlp != HXA_W_Q8)) {
+    delete dp;
+    return dfail(HXA_E_MODE, "dit: LoRA blocks run in the reference form at the MOSS block files' shape (D 3072, "
+                             "24 heads, MLP 8192, int8)");
   }
   if (cfg->lat_h % 2 || cfg->lat_w % 2 || C4 > 256 || 256 % C4 || cfg->temb % 2 || cfg->nblocks < 1) {
     delete dp;
@@ -402,9 +410,9 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   // fp16 glue. config form: x_embed [D][4C] | t_embed [D][temb] | final_mod [2D][D] | final_lin [4C][D] | MOSS
   // text_proj [D][ntxt_in]. Reference form, Anima: x_embed | t_l1 [D][D] | t_l2 [3D][D] | f1 [256][D] | f2 [2D][256]
   // | final_lin | t_norm [D]; MOSS: head_mod [2D][D] | text_proj (its other matrices are fp32, in vec)
-  const bool moss_ref = d.form == 1 && b.kind == 1;
+  const bool moss_ref = d.form == 1 && b.kind != 0;
   if (d.form == 0)
-    d.glue_elems = (long)D * C4 + (long)D * cfg->temb + 2L * D * D + (long)C4 * D + (b.kind == 1 ? (long)D * cfg->ntxt_in : 0);
+    d.glue_elems = (long)D * C4 + (long)D * cfg->temb + 2L * D * D + (long)C4 * D + (b.kind != 0 ? (long)D * cfg->ntxt_in : 0);
   else if (b.kind == 0)
     d.glue_elems = (long)D * C4 + (long)D * D + 3L * D * D + 256L * D + 2L * D * 256 + (long)C4 * D + D;
   else
@@ -421,7 +429,7 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
     M((void **)&d.a1, 4L * D);
     M((void **)&d.lora, 4L * 3 * D);
     M((void **)&d.h1, 4L * ((long)cfg->nblocks * 768 + 256));
-    if (b.kind == 1) {
+    if (b.kind != 0) {
       M((void **)&d.zrows, 4L * B * d.Timg * C4);
       M((void **)&d.x0rows, 4L * B * d.Timg * C4);
     }
@@ -453,8 +461,10 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
     for (int i = 0; i < n; i++) maxmat = std::max(maxmat, (long)N[i] * K[i]);
   }
   float *tmp = nullptr;
-  if (b.fmt_attn != HXA_W_F16 || b.fmt_mlp != HXA_W_F16) M((void **)&tmp, 4 * maxmat);
-  for (int k = 0; k < cfg->nblocks && rc == HXA_OK; k++) rc = init_pack(d, d.packs[k], seed * 1000003ull + k, tmp);
+  if (b.kind != 2 && (b.fmt_attn != HXA_W_F16 || b.fmt_mlp != HXA_W_F16)) M((void **)&tmp, 4 * maxmat);
+  for (int k = 0; k < cfg->nblocks && rc == HXA_OK; k++)
+    rc = b.kind == 2 ? (hipMemsetAsync(d.packs[k], 0, d.pack_bytes, d.st) == hipSuccess ? HXA_OK : HXA_E_HIP)
+                     : init_pack(d, d.packs[k], seed * 1000003ull + k, tmp);
   if (rc == HXA_OK)
     rc = hxa_fill_normal_launch(d.modw_all, 1, d.modw_block * (long)d.modw.size(), seed * 7919ull + 100000, 0.0f, 0.02f, d.st);
   if (rc == HXA_OK) rc = hxa_fill_normal_launch(d.glue, 1, d.glue_elems, seed * 7919ull + 99999, 0.0f, 0.02f, d.st);
@@ -465,7 +475,7 @@ extern "C" int hxa_dit_create(const hxa_dit_cfg *cfg, uint64_t seed, void **out)
   if (d.form == 0) {
     d.Lf = d.L1 + (long)D * cfg->temb;
     d.Wfin = d.Lf + 2L * D * D;
-    d.Wtxt = b.kind == 1 ? d.Wfin + (long)C4 * D : nullptr;
+    d.Wtxt = b.kind != 0 ? d.Wfin + (long)C4 * D : nullptr;
   } else if (b.kind == 0) {
     d.Wl2 = d.L1 + (long)D * D;
     d.F1 = d.Wl2 + 3L * D * D;
@@ -677,7 +687,7 @@ namespace {
 // the RoPE tables of the 1/f grid (MOSS: image positions times `scale`), built on first use (and again when the MOSS
 // scale changes); the upload completes before the call returns
 int low_rope(Dit &d, int f, double scale) {
-  const bool moss = d.bd.kind == 1;
+  const bool moss = d.bd.kind != 0;
   if (d.cosL[f] && (!moss || d.ropeL_scale == scale)) return HXA_OK;
   const int gh = d.cfg.lat_h / 2 / f, gw = d.cfg.lat_w / 2 / f;
   const int Ttot = moss ? (gh * gw + d.ntxt + 31) / 32 * 32 : gh * gw;
@@ -704,10 +714,10 @@ Pass low_pass(Dit &d, int f) {
   q.lat_h = d.cfg.lat_h / f;
   q.lat_w = d.cfg.lat_w / f;
   q.Timg = (q.lat_h / 2) * (q.lat_w / 2);
-  q.Ttot = d.bd.kind == 1 ? (q.Timg + d.ntxt + 31) / 32 * 32 : q.Timg;
+  q.Ttot = d.bd.kind != 0 ? (q.Timg + d.ntxt + 31) / 32 * 32 : q.Timg;
   q.bd = d.bd;
   q.bd.T = q.Ttot;
-  q.bd.nvalid = d.bd.kind == 1 ? q.Timg + d.ntxt : q.Timg;
+  q.bd.nvalid = d.bd.kind != 0 ? q.Timg + d.ntxt : q.Timg;
   q.cosT = d.cosL[f];
   q.sinT = d.sinL[f];
   return q;
@@ -918,6 +928,25 @@ extern "C" int hxa_dit_load_block(void *p, int k, const void *blk, size_t bytes)
   return rc;
 }
 
+// moss/export_moss.py pack_layer (offsets moss blk_meta.h:6-17): block k from the bytes of a MOSS blkNN.bin, the
+// buffer mossrun registers (mossrun.cpp:100-119), through the same conversion as mega_block's registered MOSS weights
+extern "C" int hxa_dit_load_moss_block(void *p, int k, const void *blk, size_t bytes) {
+  if (!p || !blk) return dfail(HXA_E_ARG, "dit load block: null");
+  Dit &d = *(Dit *)p;
+  if (k < 0 || k >= d.cfg.nblocks) return dfail(HXA_E_ARG, "dit load block: block index");
+  if (d.bd.kind != 2) return dfail(HXA_E_MODE, "dit load block: MOSS block files need a DiT of LoRA blocks (kind 2)");
+  if (bytes != HXA_MOSS_FILE_BYTES) return dfail(HXA_E_WEIGHTS, "dit load block: not a MOSS blkNN.bin (size)");
+  uint8_t *stage = nullptr;
+  DHIP(hipStreamSynchronize(d.st));
+  DHIP(hipMalloc((void **)&stage, bytes));
+  int rc = upload(stage, blk, bytes);
+  if (rc == HXA_OK && hipMemsetAsync(d.packs[k], 0, d.pack_bytes, d.st) != hipSuccess) rc = dfail(HXA_E_HIP, "dit load block: zero");
+  if (rc == HXA_OK) rc = hxa_moss_file_to_pack(stage, d.packs[k], d.st);
+  if (rc == HXA_OK && hipStreamSynchronize(d.st) != hipSuccess) rc = dfail(HXA_E_HIP, "dit load block: conversion");
+  (void)hipFree(stage);
+  return rc;
+}
+
 // phone/extract_small.py format (read by animad.cpp:43-70): u32 count; per tensor u32 name length, the name, u32 ndim,
 // i64 dims[ndim], fp16 data. The tensors of the reference glue (animad.cpp:424-492) are taken; others (the LLM
 // adapter's) are skipped.
@@ -998,7 +1027,7 @@ extern "C" int hxa_dit_load_moss_glue(void *p, const void *file, size_t bytes) {
   if (!p || !file) return dfail(HXA_E_ARG, "dit load glue: null");
   Dit &d = *(Dit *)p;
   const int D = d.bd.D, C4 = 4 * d.cfg.lat_c;
-  if (d.form != 1 || d.bd.kind != 1) return dfail(HXA_E_MODE, "dit load glue: glue.bin is the MOSS reference form's");
+  if (d.form != 1 || d.bd.kind == 0) return dfail(HXA_E_MODE, "dit load glue: glue.bin is the MOSS reference form's");
   const uint8_t *base = (const uint8_t *)file;
   if (bytes < 8 || memcmp(base, "MGL1", 4)) return dfail(HXA_E_WEIGHTS, "dit load glue: not an MGL1 file");
   int32_t n = 0;

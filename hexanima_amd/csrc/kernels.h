@@ -186,6 +186,10 @@ int hxa_q8rec_to_ktiled_launch(const void *rec, int N, int nkb, int kbt, void *q
 // sq sk sv so cq ck cv co m1 m2 (blk_wlayout.h order), woff[10] the gains; q8: q8 records, else fp16 crouton tiles
 int hxa_anima_file_to_pack(const uint8_t *src, const long *woff, int q8, void *pack, hipStream_t st);
 size_t hxa_anima_file_mat_bytes(int i, int q8);
+// a MOSS blkNN.bin (moss/export_moss.py, HXA_MOSS_FILE_BYTES) in device memory -> a zeroed kind-2 pack (D 3072, F 8192,
+// int8, the rapid-moss LoRA), queued on st
+constexpr size_t HXA_MOSS_FILE_BYTES = 135397376;
+int hxa_moss_file_to_pack(const uint8_t *src, void *pack, hipStream_t st);
 // matrix shapes of a GPU block pack (see hxa_pack_layout); returns the matrix count
 int hxa_pack_mats(int kind, int D, int F, int DC, int fa, int fm, int *N, int *K, int *fmt);
 

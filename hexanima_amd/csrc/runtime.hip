@@ -1235,27 +1235,21 @@ int build_anima_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
   return HXA_OK;
 }
 
+}  // namespace
+
 // MOSS blkNN.bin (moss/export_moss.py:14-58, offsets moss blk_meta.h:6-17), all q8 records: q, k, v, o
 // [3072 + 128][3072], up_gate [3072 + 128][16384] (32-column blocks interleaved up / gate), down [8192 + 128][3072]
 // -- the 128 extra K rows are the rapid-moss LoRA's scaled B -- then the LoRA A matrices A_qkv [3072][384],
 // A_o / A_up_gate [3072][128], A_down [8192][128], and the fp32 gains q/sqrt(128), k, norm1, norm2.
-// -> a kind-2 GPU pack (the B rows kept as 4 extra k groups, q / k / v block-diagonal in the fused qkv matrix).
-int build_moss_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
-  const int D = meta[MM_NCB] ? meta[MM_NCB] * 32 : 3072, F = 8192, fmt = HXA_W_Q8, R = LORA_R;
-  if (D != 3072) return fail(HXA_E_MODE, "moss pack: only the 3072-wide layout is defined");
+// -> a kind-2 GPU pack (the B rows kept as 4 extra k groups, q / k / v block-diagonal in the fused qkv matrix), queued
+// on st. The pack must be zeroed (the off-diagonal LoRA blocks of qkv stay zero).
+int hxa_moss_file_to_pack(const uint8_t *b, void *pack, hipStream_t st) {
+  const int D = 3072, F = 8192, R = LORA_R;
   const size_t W_Q = 0, W_K = 11059200, W_V = 22118400, W_O = 33177600, W_UG = 44236800, W_DN = 103219200,
-               W_AQKV = 131973120, W_AO = 133300224, W_AUG = 133742592, W_ADN = 134184960, W_GAIN = 135364608,
-               W_TOTAL = 135397376;
-  const size_t base = (size_t)meta[MM_WOFF];
-  if (meta[MM_WOFF] < 0 || base + W_TOTAL > hb.bytes) return fail(HXA_E_WEIGHTS, "moss weights shorter than a block pack");
-  db.dims = hxa_block_dims{2, D, D / 128, F, 0, 0, 0, 1, 0, fmt, fmt, 0, 1};
+               W_AQKV = 131973120, W_AO = 133300224, W_AUG = 133742592, W_ADN = 134184960, W_GAIN = 135364608;
   long offs[32];
-  const long bytes = hxa_pack_layout(2, D, F, 0, fmt, fmt, offs, 32);
-  const uint8_t *b = nullptr;
-  void *dev = nullptr;
-  int rc = stage_weights(c, hb, base, W_TOTAL, &b);
-  if (rc == HXA_OK) rc = new_pack(c, bytes, &dev);
-  uint8_t *d8 = (uint8_t *)dev;
+  hxa_pack_layout(2, D, F, 0, HXA_W_Q8, HXA_W_Q8, offs, 32);
+  uint8_t *d8 = (uint8_t *)pack;
   auto q_of = [&](int m) { return d8 + offs[3 * m]; };
   auto s_of = [&](int m) { return d8 + offs[3 * m + 1]; };
   const int kb = D / 32, kbt = kb + R / 32;
@@ -1278,13 +1272,28 @@ int build_moss_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
       {W_ADN, R, F / 32, F / 32, 7, 0, R, F / 32, 0},
   };
   for (const Rec &r : recs) {
-    if (rc != HXA_OK) break;
-    rc = hxa_q8rec_to_ktiled_launch(b + r.off, r.N, r.nkb, r.kbt, q_of(r.mat), s_of(r.mat), r.row0, r.ldn, r.nkb_main,
-                                    r.lora_g, c.st);
+    const int rc = hxa_q8rec_to_ktiled_launch(b + r.off, r.N, r.nkb, r.kbt, q_of(r.mat), s_of(r.mat), r.row0, r.ldn,
+                                              r.nkb_main, r.lora_g, st);
+    if (rc != HXA_OK) return rc;
   }
   // gains: q/sqrt(128) [128], k [128], norm1 [3072], norm2 [3072] (export_moss.py:59-60)
-  if (rc == HXA_OK && hipMemcpyAsync(d8 + offs[24], b + W_GAIN, 4L * (256 + 2 * D), hipMemcpyDeviceToDevice, c.st) != hipSuccess)
-    rc = fail(HXA_E_HIP, "gain copy");
+  HIPC(hipMemcpyAsync(d8 + offs[24], b + W_GAIN, 4L * (256 + 2 * D), hipMemcpyDeviceToDevice, st));
+  return HXA_OK;
+}
+
+namespace {
+int build_moss_pack(Ctx &c, const HostBuf &hb, const int *meta, DevBlock &db) {
+  const int D = meta[MM_NCB] ? meta[MM_NCB] * 32 : 3072, F = 8192, fmt = HXA_W_Q8;
+  if (D != 3072) return fail(HXA_E_MODE, "moss pack: only the 3072-wide layout is defined");
+  const size_t base = (size_t)meta[MM_WOFF];
+  if (meta[MM_WOFF] < 0 || base + HXA_MOSS_FILE_BYTES > hb.bytes) return fail(HXA_E_WEIGHTS, "moss weights shorter than a block pack");
+  db.dims = hxa_block_dims{2, D, D / 128, F, 0, 0, 0, 1, 0, fmt, fmt, 0, 1};
+  const long bytes = hxa_pack_layout(2, D, F, 0, fmt, fmt, nullptr, 0);
+  const uint8_t *b = nullptr;
+  void *dev = nullptr;
+  int rc = stage_weights(c, hb, base, HXA_MOSS_FILE_BYTES, &b);
+  if (rc == HXA_OK) rc = new_pack(c, bytes, &dev);
+  if (rc == HXA_OK) rc = hxa_moss_file_to_pack(b, dev, c.st);
   if (rc == HXA_OK && hipStreamSynchronize(c.st) != hipSuccess) rc = fail(HXA_E_HIP, "pack conversion");
   if (rc != HXA_OK) {
     if (dev) (void)hipFree(dev);

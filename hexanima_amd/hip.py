@@ -107,6 +107,7 @@ _SIGS = {
     "hxa_dit_export": (L, [P, I, P, SZ]),
     "hxa_dit_import": (I, [P, I, P, SZ]),
     "hxa_dit_load_block": (I, [P, I, P, SZ]),
+    "hxa_dit_load_moss_block": (I, [P, I, P, SZ]),
     "hxa_dit_load_anima_glue": (I, [P, P, SZ]),
     "hxa_dit_load_moss_glue": (I, [P, P, SZ]),
     "hxa_dit_stream": (P, [P]),

@@ -272,7 +272,9 @@ void *hxa_block_ws_buf(const hxa_block_dims *d, void *ws, int which, long *ld);
  * 5. DiT runner (the process above the boundary: patch embed, timestep modulation, blocks, final layer, Euler)
  * ============================================================================================================ */
 typedef struct {
-  hxa_block_dims blk;   /* per-block shape (T = gh*gw tokens per image) */
+  hxa_block_dims blk;   /* per-block shape (T = gh*gw tokens per image); kind 0 Anima, 1 MOSS (synthetic seeded
+                           weights), 2 MOSS with the rapid-moss LoRA (form 1 only; zero weights until
+                           hxa_dit_load_moss_block) */
   int nblocks;
   int lat_c, lat_h, lat_w; /* latent [C][H][W]; patch 2 */
   int temb;             /* sinusoid width of the timestep embedding (form 0: 256; form 1: D for Anima, 256 for MOSS) */
@@ -344,6 +346,10 @@ int hxa_dit_import(void *dit, int which, const void *host, size_t bytes);
  *   (fp32 time MLP, video embedding, head linear and vectors; fp16 modulation matrices); rope.bands rebuilds the RoPE
  *   tables; step_codes stays with the caller (the code argument of hxa_dit_moss_step). */
 int hxa_dit_load_block(void *dit, int k, const void *blk, size_t bytes);
+/* block k of a MOSS DiT of LoRA blocks (blk.kind 2, form 1, D 3072, 24 heads, MLP 8192, int8) from the bytes of a MOSS
+ * blkNN.bin (moss/export_moss.py; the buffer mossrun registers, 135397376 bytes), through the same conversion as
+ * mega_moss_block's registered weights. Such a DiT starts with zero weights in every block. */
+int hxa_dit_load_moss_block(void *dit, int k, const void *blk, size_t bytes);
 int hxa_dit_load_anima_glue(void *dit, const void *small_bin, size_t bytes);
 int hxa_dit_load_moss_glue(void *dit, const void *glue_bin, size_t bytes);
 void *hxa_dit_stream(void *dit);

@@ -190,3 +190,69 @@ def test_dit_moss_from_mgl1_glue():
         assert r < 6e-4 and mx < 2.5e-3  # measured 2.0e-4, 8.2e-4
     finally:
         lib.hxa_dit_destroy(p)
+
+
+def test_dit_moss_lora_blocks_from_files():
+    """The MOSS DiT of LoRA blocks (kind 2): two synthetic export_moss.py block files through hxa_dit_load_moss_block
+    (the conversion mega_block's MOSS path uses) and an MGL1 glue.bin at the real width (D 3072), four rapid-moss
+    steps against oracle_moss_rapid_step with the files' blocks (the LoRA term included)."""
+    from tests.test_gpu_block import _moss_blk_file
+    hip = _hip()
+    lib = hip.lib()
+    hxo.set_threads(0)
+    D, H, F, ntxt, tin, nb, B = 3072, 24, 8192, 20, 64, 2, 1
+    C4, LAT = 128, (32, 16, 16)
+    print("[case] MOSS DiT of LoRA blocks from block files + glue.bin, D 3072, 2 blocks, 4 rapid-moss steps",
+          flush=True)
+    bd = hip.BlockDims(2, D, H, F, ntxt, 0, 0, B, 0, hip.W_Q8, hip.W_Q8, 1)
+    cfg = hip.DitCfg(bd, nb, LAT[0], LAT[1], LAT[2], 256, tin, 1)
+    p = C.c_void_p()
+    hip.check(lib.hxa_dit_create(C.byref(cfg), 4444, C.byref(p)), "dit_create")
+    try:
+        rng = np.random.default_rng(97)
+        blocks = []
+        for k in range(nb):
+            wf, w = _moss_blk_file(rng)
+            hip.check(lib.hxa_dit_load_moss_block(p, k, wf.ctypes.data, wf.nbytes), "load_moss_block")
+            blocks.append(w)
+        assert lib.hxa_dit_load_moss_block(p, 0, wf.ctypes.data, wf.nbytes - 1) == -5  # HXA_E_WEIGHTS (size)
+        f32 = lambda *sh, s=0.02, m=0.0: (m + s * rng.standard_normal(sh)).astype(np.float32)
+        bands = (1.0 / 10000.0 ** (np.arange(16) / 16.0)).astype(np.float32)
+        t = [("video_embedder.weight", 0, f32(D, C4, s=0.005)), ("video_embedder.bias", 0, f32(D, s=0.005)),
+             ("time_embedding.0.weight", 0, f32(D, 256)), ("time_embedding.0.bias", 0, f32(D)),
+             ("time_embedding.2.weight", 0, f32(D, D)), ("time_embedding.2.bias", 0, f32(D)),
+             ("shared_block_modulation.weight", 1, f16(rng.standard_normal((6 * D, D)) * 0.02)),
+             ("shared_block_modulation.bias", 0, f32(6 * D)),
+             ("video_head_modulation.weight", 1, f16(rng.standard_normal((2 * D, D)) * 0.02)),
+             ("video_head_modulation.bias", 0, f32(2 * D)),
+             ("final_linear_video.weight", 0, f32(C4, D)), ("final_norm_video.weight", 0, f32(D, s=0.1, m=1.0)),
+             ("latent_mix.Q", 0, f32(C4, C4)), ("step_codes", 0, np.array([0.999, 0.75, 0.5, 0.25], np.float32)),
+             ("rope.bands", 0, bands), ("bn.mean", 0, f32(C4, s=0.1)), ("bn.var", 0, f32(C4, s=0.1, m=1.0))]
+        gb = mgl1_bin(t)
+        hip.check(lib.hxa_dit_load_moss_glue(p, gb.ctypes.data, gb.nbytes), "load_moss_glue")
+        g = {n: a for n, _, a in t}
+        glue, vec = moss_ref_sections(_export(hip, p, 2 * nb).view(np.uint16),
+                                      _export(hip, p, 2 * nb + 1).view(np.float32), D, C4, tin)
+        modw = _export(hip, p, nb).view(np.uint16).reshape(6 * D, D)
+        z = rng.standard_normal((B,) + LAT).astype(np.float32)
+        txt = rng.standard_normal((B, ntxt, tin)).astype(np.float32)
+        hip.check(lib.hxa_dit_set_inputs(p, z.ctypes.data, txt.ctypes.data), "set_inputs")
+        zr = np.stack([hxo.patchify(z[b]) for b in range(B)])
+        x0, x00 = np.zeros_like(zr), np.zeros_like(zr)
+        txt16 = f16(txt)
+        kw = dict(D=D, H=H, F=F, C4=C4, ntxt=ntxt, Ttot=96, gh=8, gw=8, bands=bands)
+        for code in g["step_codes"]:
+            hip.check(lib.hxa_dit_moss_step(p, float(code), 1), "moss_step")
+            x0 = oracle_moss_rapid_step(zr, x0, txt16, float(code), blocks, modw, glue, vec, **kw)
+            x00 = oracle_moss_rapid_step(zr, x00, txt16, float(code), [], modw, glue, vec, **kw)
+        got = np.zeros_like(z)
+        hip.check(lib.hxa_dit_get_latent(p, got.ctypes.data), "get_latent")
+        ref = np.stack([bn_unpatchify(x0[b], vec[7], vec[8], *LAT) for b in range(B)])
+        share = rel(x0, x00)
+        r, mx = rel(got, ref), float(np.max(np.abs(got - ref)))
+        print(f"MOSS LoRA DiT from files: rel err {r:.2e} max abs {mx:.2e}; the blocks change x0 by {share:.3f}",
+              flush=True)
+        assert share > 0.2
+        assert r < 3e-3 and mx < 3e-2
+    finally:
+        lib.hxa_dit_destroy(p)
