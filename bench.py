@@ -31,6 +31,7 @@ D, H, F, C_TXT, DC, NBLK = 2048, 16, 8192, 256, 1024, 28
 LAT = (16, 96, 64)
 T = (LAT[1] // 2) * (LAT[2] // 2)
 WFMT = 0 | 16  # fp16 weights, k-tiled: the block-pack layout of the DiT's matrices
+LIN_SHAPES = ((D, 3 * D), (D, D), (D, F), (F, D))  # K x N of the block's projections (qkv, o, MLP up, MLP down)
 BLOCK_FLOPS = 2 * T * D * (3 * D) + 2 * T * D * D + 2 * T * D * D + 2 * C_TXT * DC * (2 * D) + 2 * T * D * D \
     + 2 * T * D * F * 2 + 4 * T * T * D + 4 * T * C_TXT * D
 STEP_FLOPS = NBLK * BLOCK_FLOPS + 2 * T * 64 * D + 2 * T * D * 64
@@ -353,7 +354,31 @@ def family_launchers(L, hip, s):
             hook(0)
         hip.check(L.hxa_cross_attention_fused(h.ptr, D, T, T, WFMT, Wco.ptr, D, D, gain.ptr, ck.ptr, D, cvt.ptr, C_TXT,
                                               C_TXT, C_TXT, 0, 0, o.ptr, D, s), "cross_attention_fused")
+    def linears(fmt):  # the block's four projection shapes at 1536 rows, plain store, fp16 / int8 / int4 weights
+        wts = []
+
+        def run(hook=None):
+            if not wts:  # weights made on the first call
+                Wq, Sq = hip.DeviceArray((F * D * 2,), np.uint8), hip.DeviceArray((F // 32 * D,), np.float16)
+                wts.extend([Wq, Sq])
+                if fmt == 0:
+                    hip.check(L.hxa_fill_normal(Wq.ptr, 1, F * D, 81, 0.0, 0.02, s), "fill")
+                else:
+                    lo, hi = (-127, 127) if fmt == 1 else (-8, 7)
+                    hip.check(L.hxa_fill_uniform_int(Wq.ptr, 8 if fmt == 1 else 4, F * D // (1 if fmt == 1 else 2), 82,
+                                                     lo, hi, s), "fill")
+                    hip.check(L.hxa_fill_const(Sq.ptr, 1, F // 32 * D, 0.02 / hi, s), "fill")
+            Wq, Sq = wts
+            for i, (K, N) in enumerate(LIN_SHAPES):
+                if hook:
+                    hook(i)
+                hip.check(L.hxa_gemm(mid.ptr, K, T, fmt | 16, Wq.ptr, None if fmt == 0 else Sq.ptr, None, N, K, 1,
+                                     hip.EPI_STORE, up.ptr, N, 0, None, 0, None, None, 0, 0, s), "gemm")
+        return run
     f16 = 2
+    lin_flops = sum(2 * T * K * N for K, N in LIN_SHAPES)
+    lin_bytes = {f: sum(T * K * 2 + N * K * wb + T * N * 2 + (K // 32 * N * 2 if f else 0) for K, N in LIN_SHAPES)
+                 for f, wb in ((0, 2), (1, 1), (2, 0.5))}
     fam = {
         "gemm_splitk": (splitk, 3, 2 * T * D * D * 2 + 2 * T * F * D,
                         f16 * (2 * (T * D + D * D + 2 * T * D) + (T * F + D * F + 2 * T * D)),
@@ -367,6 +392,10 @@ def family_launchers(L, hip, s):
         "gemm_xattn_cross": (xattn, 1, 2 * T * D * D + 4 * T * C_TXT * D, f16 * (T * D + D * D + 2 * C_TXT * D + T * D),
                              "gemm_xattn_kernel 128x128 (4 waves): cross q + head RMSNorm, attention over the text keys"),
     }
+    for f, nm in ((0, "f16"), (1, "q8"), (2, "q4")):
+        picks = ", ".join(_kname(hip.gemm_pick(T, N, K, f, 1, 0)) for K, N in LIN_SHAPES)
+        fam["linears_" + nm] = (linears(f), len(LIN_SHAPES), lin_flops, lin_bytes[f],
+                                f"K x N {', '.join(f'{K}x{N}' for K, N in LIN_SHAPES)}: {picks}")
     return fam, keep
 
 
@@ -398,7 +427,7 @@ def kernel_breakdown(L, hip, reps=10):
                         "frac_of_fp16_peak": round(flops / (ms * 1e-3) / PEAK_FP16, 4),
                         "alg_mb_per_launch": round(nbytes / n / 1e6, 2)})
         table[name] = row
-    dom = max(fam, key=lambda k: table[k]["block_us"])
+    dom = max(table, key=lambda k: table[k]["block_us"] if k in fam else -1.0)
     fn, n, flops, nbytes, kname = fam[dom]
     ms = _time_launches(L, hip, fn, s, reps=50, warm=5)
     clocks = _family_clocks(L, hip, fn, n, s, kind=1 if dom == "attention" else 0)
@@ -667,7 +696,8 @@ def main():
     ap.add_argument("--kernel-probe", type=int, default=0, metavar="REPS",
                     help="only launch one kernel family REPS times plus a copy calibration (for rocprofv3 --pmc)")
     ap.add_argument("--probe-family", default="gemm_splitk",
-                    choices=["gemm_splitk", "gemm_pp_mlp_up", "gemm_pp_qkv_headnorm", "attention"])
+                    choices=["gemm_splitk", "gemm_pp_mlp_up", "gemm_pp_qkv_headnorm", "attention", "gemm_xattn_cross",
+                             "linears_f16", "linears_q8", "linears_q4"])
     ap.add_argument("--abi-chain", action="store_true", help="only time the 28-block mega_block chain (hxa_run)")
     ap.add_argument("--clock-probe", action="store_true",
                     help="only measure the shader clock of the MLP-up GEMM (random / zero data, one workgroup) and of "

@@ -85,6 +85,8 @@ HXA_DEV uint32_t a_lane_off(const GemmParams &p, int blk, int lane, int m0) {
   const int row = blk * 16 + (lane >> 2), cl = (lane & 3) ^ ((row >> 2) & 3);
   return ((uint32_t)(min(m0 + row, p.M - 1) - m0) * (uint32_t)p.lda + cl * 8) * 2u;
 }
+// q8 rows of a stage are 32 B: chunk c of row r sits at 16-byte unit 2 r + (c ^ q8_swz(r))
+HXA_DEV int q8_swz(int row) { return (row >> 3) & 1; }
 // W chunk c of a stage: fp16 rows of 64 B (4 chunks), q8 rows of 32 B (2 chunks), q4 rows of 16 B (1 chunk)
 template <int FMT>
 HXA_DEV uint32_t w_lane_off(const GemmParams &p, int chunk, int n0) {
@@ -92,7 +94,7 @@ HXA_DEV uint32_t w_lane_off(const GemmParams &p, int chunk, int n0) {
     const int row = chunk >> 2, cl = (chunk & 3) ^ ((row >> 2) & 3);
     return ((uint32_t)(min(n0 + row, p.N - 1) - n0) * (uint32_t)p.w_rs + cl * 8) * 2u;
   } else if constexpr (FMT == HXA_W_Q8) {
-    const int row = chunk >> 1, cl = (chunk & 1) ^ ((row >> 3) & 1);
+    const int row = chunk >> 1, cl = (chunk & 1) ^ q8_swz(row);
     return (uint32_t)(min(n0 + row, p.N - 1) - n0) * (uint32_t)p.w_rs + cl * 16;
   } else {
     return (uint32_t)(min(n0 + chunk, p.N - 1) - n0) * (uint32_t)p.w_rs;
@@ -172,6 +174,21 @@ HXA_DEV void dq4_word(uint32_t d, half2_t s2, half2_t z2, uint32_t *o) {
       o[j] = as_u((as_h2(v) - c) * s2);
     }
   }
+}
+
+// The k order of the fragments. In v_mfma_f32_32x32x16_f16 lane half h = lane >> 5 supplies the 8 k values
+// 8h .. 8h+7 of the instruction's 16 for both operands. Slice ks of a 32-deep stage gives lane half h the stage's
+// k values 16h + 8ks .. +7, the same for A and W (the sum over the stage is unchanged): fp16 16-byte chunk 2h + ks
+// of a row, bytes 8ks .. 8ks+7 of q8 chunk h, 4-byte q4 slot 2h + ks. A lane's two q8 slices then come from one
+// 16-byte chunk of the row (measured 3-4% faster on the large ping-pong tiles than slices 2ks + h). Every kernel
+// uses this order, so a product's fp32 sums are the same whatever the tile.
+HXA_DEV constexpr int kslot(int ks, int h) { return 2 * h + ks; }
+// the raw quantised W of slice ks of a row for lane half h
+HXA_DEV uint2_t read_wq8(const uint8_t *ws, int row, int h, int ks) {
+  return *(const uint2_t *)(ws + row * 32 + ((h ^ q8_swz(row)) << 4) + (ks << 3));
+}
+HXA_DEV uint32_t read_wq4(const uint8_t *ws, int row, int h, int ks) {
+  return *(const uint32_t *)(ws + row * 16 + (kslot(ks, h) << 2));
 }
 
 HXA_DEV float gelu_tanh_f(float t) {
@@ -669,7 +686,7 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   }
 
   // ---- loader: stage s <- k tile kt. A and fp16 W rows are 64 B (4 chunks of 16 B) stored with the chunk swizzle
-  // c ^ ((row >> 2) & 3); q8 rows are 32 B with chunk swizzle c ^ ((row >> 3) & 1); q4 rows are 16 B.
+  // c ^ ((row >> 2) & 3); q8 rows are 32 B with chunk swizzle c ^ q8_swz(row); q4 rows are 16 B.
   constexpr int NAI = BM / 16;  // 1 KB A instructions (16 rows) per stage
   constexpr int NAL = (NAI + NW - 1) / NW, NWL = (G::TW + NW - 1) / NW;  // this wave's A / W loads per stage
   uint32_t aoff[NAL], woff[NWL];
@@ -727,9 +744,10 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
                         hxa_h (&zc)[NI]) {
     const uint8_t *st = lds8 + s * G::STAGE;
     const uint8_t *ws = st + G::A_BYTES;
+    const int h = lane >> 5;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ks++) {
-      const int cl = ks * 2 + (lane >> 5);
+      const int cl = kslot(ks, h);
 #pragma unroll
       for (int i = 0; i < MI; i++) {
         const int row = wm * WTM + i * 32 + (lane & 31);
@@ -740,10 +758,10 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
         const int row = wn * WTN + j * 32 + (lane & 31);
         if constexpr (FMT == HXA_W_F16) {
           fb[ks][j] = *(const half8_t *)(ws + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
-        } else if constexpr (FMT == HXA_W_Q8) {  // 8-byte slot cl of the row: chunk cl >> 1 (swizzled), half cl & 1
-          wq[ks][j] = *(const uint2_t *)(ws + row * 32 + (((cl >> 1) ^ ((row >> 3) & 1)) << 4) + ((cl & 1) << 3));
-        } else {  // 4-byte slot cl: 8 consecutive k
-          wq[ks][j] = *(const uint32_t *)(ws + row * 16 + (cl << 2));
+        } else if constexpr (FMT == HXA_W_Q8) {
+          wq[ks][j] = read_wq8(ws, row, h, ks);
+        } else {
+          wq[ks][j] = read_wq4(ws, row, h, ks);
         }
       }
     }
@@ -971,23 +989,20 @@ HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
   auto read_frags = [&](int s, half8_t (&fa)[2][MI], half8_t (&fb)[2][NI]) {
     const uint8_t *st = lds8 + s * G::STAGE;
     const uint8_t *ws = st + G::A_BYTES;
+    const int h = lane >> 5;
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      const int cl = ks * 2 + (lane >> 5);
+      const int cl = kslot(ks, h);
 #pragma unroll
       for (int i = 0; i < MI; i++) {
         const int row = wm * WTM + i * 32 + (lane & 31);
         fa[ks][i] = *(const half8_t *)(st + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
       }
+      if constexpr (FMT == HXA_W_F16) {
 #pragma unroll
-      for (int j = 0; j < NI; j++) {
-        const int row = grp * (BN / 2) + wn * WTN + j * 32 + (lane & 31);
-        if constexpr (FMT == HXA_W_F16) {
+        for (int j = 0; j < NI; j++) {
+          const int row = grp * (BN / 2) + wn * WTN + j * 32 + (lane & 31);
           fb[ks][j] = *(const half8_t *)(ws + row * 64 + ((cl ^ ((row >> 2) & 3)) << 4));
-        } else if constexpr (FMT == HXA_W_Q8) {  // 8-byte slot cl of the row: chunk cl >> 1 (swizzled), half cl & 1
-          wq[ks][j] = *(const uint2_t *)(ws + row * 32 + (((cl >> 1) ^ ((row >> 3) & 1)) << 4) + ((cl & 1) << 3));
-        } else {  // 4-byte slot cl: 8 consecutive k
-          wq[ks][j] = *(const uint32_t *)(ws + row * 16 + (cl << 2));
         }
       }
     }
@@ -995,6 +1010,13 @@ HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
 #pragma unroll
       for (int j = 0; j < NI; j++) {
         const int row = grp * (BN / 2) + wn * WTN + j * 32 + (lane & 31);
+        if constexpr (FMT == HXA_W_Q8) {
+          wq[0][j] = read_wq8(ws, row, h, 0);
+          wq[1][j] = read_wq8(ws, row, h, 1);
+        } else {
+          wq[0][j] = read_wq4(ws, row, h, 0);
+          wq[1][j] = read_wq4(ws, row, h, 1);
+        }
         sc[j] = *(const hxa_h *)(ws + G::W_BYTES + row * 2);
         zc[j] = ASYM ? *(const hxa_h *)(ws + G::W_BYTES + G::S_BYTES + row * 2) : (hxa_h)0.0f;
       }

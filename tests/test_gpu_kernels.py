@@ -213,11 +213,14 @@ def test_gemm_epilogues():
     A = f16(rng.standard_normal((M, K)))
     W = f16(rng.standard_normal((N, K)) * 0.1)
     t = f16(hxo.gemm(A, W))
+
+    def t_gpu_for(epi):  # the GPU's own f16(acc) from a plain store on the tile the epilogue launch picks (kernels
+        pk = hip.gemm_pick(M, N, K, 0, 1, epi)  # differ in their k order, so f16(acc) may differ by an ulp)
+        return _run_gemm(hip, A, 0, W, None, N, K, tile=(pk["bm"], pk["bn"], pk["waves"]))
     say("gemm epi gelu tanh / erf")
-    t_gpu = _run_gemm(hip, A, 0, W, None, N, K)  # the GPU's own f16(acc), then the activation on the same values
     for epi, mode in ((1, 1), (2, 0)):
         got = _run_gemm(hip, A, 0, W, None, N, K, epi=epi)
-        ref = hxo.gelu(t_gpu, mode).view(np.float16)
+        ref = hxo.gelu(t_gpu_for(epi), mode).view(np.float16)  # the activation on the same values
         assert ulp_diff(got, ref).max() <= 2
     say("gemm epi store_t")
     got = _run_gemm(hip, A, 0, W, None, N, K, epi=4)
@@ -238,6 +241,7 @@ def test_gemm_epilogues():
     up = np.ascontiguousarray(W.reshape(F // 32, 2, 32, K)[:, 0].reshape(F, K))
     gt = np.ascontiguousarray(W.reshape(F // 32, 2, 32, K)[:, 1].reshape(F, K))
     got = _run_gemm(hip, A, 0, W, None, N, K, epi=5)
+    t_gpu = t_gpu_for(5)
     tu = np.ascontiguousarray(t_gpu.reshape(M, F // 32, 2, 32)[:, :, 0].reshape(M, F))
     tg = np.ascontiguousarray(t_gpu.reshape(M, F // 32, 2, 32)[:, :, 1].reshape(M, F))
     ref = hxo.situ(tu, tg).view(np.float16)
@@ -287,7 +291,7 @@ def test_gemm_resadd_split2_matches_partial_then_resadd2(fmt, tile):
     g = rng.standard_normal(N).astype(np.float32)
     say(f"gemm resadd_split2 fmt={fmt} tile={tile}")
     got = _run_gemm(hip, A, fmt, w, s, N, K, epi=hip.EPI_RESADD_SPLIT2, x=x, gate=g, tile=tile)
-    parts = _run_gemm(hip, A, fmt, w, s, N, K, epi=hip.EPI_PARTIAL, ksplit=2)
+    parts = _run_gemm(hip, A, fmt, w, s, N, K, epi=hip.EPI_PARTIAL, ksplit=2, tile=tile)
     ref = hxo.resadd2(x, parts[0], parts[1], g)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)) or np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
     dx = hip.DeviceArray.from_numpy(x)
