@@ -1150,32 +1150,36 @@ __global__ __launch_bounds__(512) void gemm_pp_group_kernel(const GemmParams *__
 }
 
 // Tile cost model, per weight format (fp16, int8, int4): a launch of `waves` rounds of workgroups over the CUs takes
-// about waves * (a * BM * BN * Kslice / 1e6 + b) microseconds. a and b were fitted by least squares (b >= 0) to
-// every tile timed on 18 projection shapes of 256-6656 rows (hidden 2048-3072, MLP 8192-24576, split-K 1-2) on a
-// 256-CU MI355X; a = 0 marks a tile that format does not use. nw 4: one wave per SIMD; nw 8: two (int8 / int4
-// dequantisation overlaps the other wave's MFMAs); nw 9: the ping-pong kernel. The 4-wave tiles lose 13-25% to the
-// 8-wave ones and the ping-pong kernel on quantised weights, except the small tiles of short-M projections.
+// about waves * (a * BM * BN * Kslice / 1e6 + b) + c microseconds. a, b, c >= 0 were fitted by least squares on the
+// relative error to every tile timed on 78 projection shapes on a 256-CU MI355X: the qkv, attention-output, MLP-up
+// and MLP-down projections of the 2B (hidden 2048), 2.9B-class (2560) and MOSS-class (3072, up-gate 16384) blocks
+// at 384, 512, 1536 and 6656 rows, split-K 1 and 2 (and 4 at 1536 rows); a = 0 marks a tile that format does not
+// use. nw 4: one wave per SIMD; nw 8: two (int8 / int4 dequantisation overlaps the other wave's MFMAs); nw 9: the
+// ping-pong kernel. Over those shapes the picks come within 0.3% (fp16), 0.5% (int8) and 0.6% (int4) of the fastest
+// tile's summed time.
 struct TileCost {
   int bm, bn, nw;
-  float a[3], b[3];
+  float a[3], b[3], c[3];
 };
 constexpr TileCost kTiles[] = {
-    {192, 256, 4, {0.4384f, 0.0f, 0.0f}, {2.40f, 0.0f, 0.0f}},
-    {192, 192, 4, {0.4607f, 0.0f, 0.0f}, {2.21f, 0.0f, 0.0f}},
-    {256, 128, 4, {0.5216f, 0.0f, 0.0f}, {0.00f, 0.0f, 0.0f}},
-    {128, 256, 4, {0.4833f, 0.0f, 0.0f}, {1.14f, 0.0f, 0.0f}},
-    {192, 128, 4, {0.5076f, 0.0f, 0.0f}, {1.90f, 0.0f, 0.0f}},
-    {128, 128, 4, {0.5077f, 0.0f, 0.0f}, {3.26f, 0.0f, 0.0f}},
-    {128, 64, 4, {0.7260f, 0.5797f, 0.0f}, {2.46f, 5.95f, 0.0f}},
-    {64, 128, 4, {0.5808f, 0.5976f, 0.6163f}, {3.38f, 7.19f, 7.20f}},
-    {192, 256, 8, {0.5071f, 0.5792f, 0.5675f}, {0.33f, 1.53f, 3.47f}},
-    {128, 256, 8, {0.5004f, 0.6363f, 0.5286f}, {0.00f, 1.84f, 4.99f}},
-    {192, 128, 8, {0.6810f, 0.7205f, 0.7193f}, {1.31f, 2.55f, 3.09f}},
-    {128, 128, 8, {0.5529f, 0.5801f, 0.5555f}, {2.44f, 6.01f, 6.46f}},
-    {256, 256, 9, {0.4230f, 0.4486f, 0.4598f}, {0.00f, 1.51f, 2.49f}},
-    {192, 256, 9, {0.4566f, 0.5385f, 0.5270f}, {0.00f, 2.91f, 3.90f}},
-    {128, 256, 9, {0.4991f, 0.5582f, 0.5452f}, {0.00f, 4.29f, 5.67f}},
-    {128, 128, 9, {0.5282f, 0.5643f, 0.0f}, {3.54f, 6.21f, 0.0f}},
+    {192, 256, 4, {0.2807f, 0.4725f, 0.5084f}, {11.50f, 10.83f, 10.16f}, {0.00f, 0.00f, 0.00f}},
+    {192, 192, 4, {0.3052f, 0.5077f, 0.5578f}, {10.33f, 8.85f, 8.12f}, {0.00f, 0.00f, 0.00f}},
+    {256, 128, 4, {0.3446f, 0.4439f, 0.5133f}, {8.80f, 8.45f, 7.53f}, {0.00f, 0.00f, 0.00f}},
+    {128, 256, 4, {0.3213f, 0.5315f, 0.6355f}, {8.75f, 7.92f, 7.10f}, {0.00f, 0.00f, 0.00f}},
+    {192, 128, 4, {0.3855f, 0.5336f, 0.5665f}, {7.27f, 2.45f, 0.18f}, {0.00f, 4.06f, 7.37f}},
+    {128, 128, 4, {0.4574f, 0.5958f, 0.5965f}, {2.89f, 0.00f, 0.00f}, {1.77f, 9.34f, 9.38f}},
+    {128, 64, 4, {0.7533f, 0.7707f, 0.0000f}, {0.99f, 0.00f, 0.00f}, {1.63f, 6.60f, 0.00f}},
+    {64, 128, 4, {0.6581f, 0.8466f, 0.8716f}, {0.49f, 0.00f, 0.00f}, {3.68f, 10.92f, 11.58f}},
+    {192, 256, 8, {0.3002f, 0.3773f, 0.4420f}, {9.65f, 8.92f, 8.16f}, {0.00f, 0.00f, 0.00f}},
+    {128, 256, 8, {0.3256f, 0.4574f, 0.5409f}, {7.24f, 6.43f, 5.79f}, {0.00f, 0.00f, 0.00f}},
+    {192, 128, 8, {0.4581f, 0.6220f, 0.5743f}, {6.41f, 5.54f, 1.68f}, {0.00f, 0.00f, 3.79f}},
+    {128, 128, 8, {0.4755f, 0.6311f, 0.6435f}, {2.77f, 0.81f, 0.10f}, {1.43f, 5.34f, 6.45f}},
+    {256, 256, 9, {0.2712f, 0.3157f, 0.3321f}, {10.91f, 9.85f, 9.27f}, {0.00f, 0.00f, 0.00f}},
+    {192, 256, 9, {0.3042f, 0.3781f, 0.4006f}, {8.70f, 7.83f, 7.13f}, {0.00f, 0.00f, 0.00f}},
+    {128, 256, 9, {0.3726f, 0.5011f, 0.5641f}, {6.15f, 0.66f, 0.00f}, {0.00f, 5.56f, 7.60f}},
+    {128, 128, 9, {0.5054f, 0.6590f, 0.0000f}, {1.74f, 0.00f, 0.00f}, {3.42f, 9.07f, 0.00f}},
+    {192, 128, 9, {0.4632f, 0.5685f, 0.0000f}, {5.52f, 0.82f, 0.00f}, {0.00f, 4.96f, 0.00f}},
+    {256, 128, 9, {0.3952f, 0.4634f, 0.0000f}, {6.39f, 6.27f, 0.00f}, {0.00f, 0.00f, 0.00f}},
 };
 
 template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2 = false, int NW = 4>
@@ -1224,6 +1228,8 @@ hipError_t launch_fmt(int bm, int bn, int nw, const GemmParams &p, int ksplit, h
     if (bm == 128 && bn == 256) return launch_pp<128, 256, FMT, ASYM>(p, ksplit, st);
     if constexpr (FMT != HXA_W_Q4) {
       if (bm == 128 && bn == 128) return launch_pp<128, 128, FMT, ASYM>(p, ksplit, st);
+      if (bm == 192 && bn == 128) return launch_pp<192, 128, FMT, ASYM>(p, ksplit, st);
+      if (bm == 256 && bn == 128) return launch_pp<256, 128, FMT, ASYM>(p, ksplit, st);
     }
     return hipErrorInvalidValue;
   }
@@ -1278,7 +1284,7 @@ static void pick_tile(int M, int N, int K, int ksplit, int fmt, int epi, int hn_
     if (headnorm && (c.bn % 128 != 0 || (hn_cols % c.bn != 0 && hn_cols < N))) continue;  // whole head-normed tiles
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ksplit;
     const long waves = (tiles + ncu - 1) / ncu;
-    const double t = (double)waves * (c.a[f] * 1e-6 * c.bm * c.bn * (double)(K / ksplit) + c.b[f]);
+    const double t = (double)waves * (c.a[f] * 1e-6 * c.bm * c.bn * (double)(K / ksplit) + c.b[f]) + c.c[f];
     if (best < 0.0 || t < best - 1e-9) {
       best = t;
       *bm = c.bm;
@@ -1292,7 +1298,7 @@ static void pick_tile(int M, int N, int K, int ksplit, int fmt, int epi, int hn_
 static bool tile_built(int bm, int bn, int nw, int fmt, bool split2) {
   if (split2) return nw == 4 && bn == 128 && (bm == 128 || bm == 64);
   const bool q4 = fmt == HXA_W_Q4;
-  if (nw == 9) return (bn == 256 && (bm == 256 || bm == 192 || bm == 128)) || (bm == 128 && bn == 128 && !q4);
+  if (nw == 9) return (bn == 256 && (bm == 256 || bm == 192 || bm == 128)) || ((bm == 128 || bm == 192 || bm == 256) && bn == 128 && !q4);
   if (nw == 8) return (bm == 192 || bm == 128) && (bn == 256 || bn == 128);
   if (nw != 4) return false;
   if (bm == 128 && bn == 64) return !q4;
