@@ -388,7 +388,7 @@ def family_launchers(L, hip, s):
         "gemm_pp_qkv_headnorm": (qkv, 1, 2 * T * D * 3 * D, f16 * (T * D + 3 * D * D + 3 * T * D),
                                  _kname(hip.gemm_pick(T, 3 * D, D, WFMT, 1, 0, 2 * D)) + ", head RMSNorm + RoPE epilogue"
                                  " (timed without the text k/v tiles the step's launch adds)"),
-        "attention": (attention, 1, 4 * T * T * D, f16 * (4 * T * D), "attn_kernel (96-query workgroups)"),
+        "attention": (attention, 1, 4 * T * T * D, f16 * (4 * T * D), "attn_kernel (128-query workgroups)"),
         "gemm_xattn_cross": (xattn, 1, 2 * T * D * D + 4 * T * C_TXT * D, f16 * (T * D + D * D + 2 * C_TXT * D + T * D),
                              "gemm_xattn_kernel 128x128 (4 waves): cross q + head RMSNorm, attention over the text keys"),
     }

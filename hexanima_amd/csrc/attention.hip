@@ -5,9 +5,11 @@
 // (moss/hexagon/mega/blk.c:56-58). No 1/sqrt(d) is applied: it is folded into the q RMSNorm gain
 // (export_all.py:31-32). Keys >= nvalid get probability 0.
 //
-// Work split: a workgroup of 2 x NWH waves owns 32 NWH queries of one head (NWH = 4: 128 queries, or 3: 96 queries
-// when that fills the CUs better). Waves [0, NWH) take the first half of the key tiles, the others the second half
-// (up to two waves per SIMD, one of each half); the halves are merged through LDS at the end. Each wave owns 32
+// Work split: a workgroup of 2 x NWH waves (NWH = 4: 8 waves) owns 32 NWH = 128 queries of one head. Waves [0, NWH)
+// take the first half of the key tiles, the others the second half (two waves per SIMD, one of each half); the
+// halves are merged through LDS at the end. (96 queries on 6 waves would fill 256 CUs at 1536 queries x 16 heads,
+// but waves are dealt to the SIMDs round-robin, two SIMDs then run two waves, and the workgroup takes as long as
+// the 128-query one: 29.5 against 29.0 us on MI355X.) Each wave owns 32
 // queries and keeps Q in registers. Two schedules of the key loop: lock-step (one barrier per tile for both halves)
 // and, for whole tiles in a multiple of 4, ping-pong (each tile split into a VALU phase, the softmax, and an MFMA
 // phase, PV with the next QK; the halves one phase apart, so the two waves of a SIMD alternate between the two
@@ -40,10 +42,9 @@ constexpr float RESCALE_TH = 5.5f;
 
 HXA_DEV float16_t mfma(half8_t a, half8_t b, float16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
 
-// NWH waves per key half (4: 128 queries per workgroup, 8 waves; 3: 96 queries, 6 waves -- chosen per launch so
-// that the grid fills the CUs). FULL: every key tile lies wholly below nvalid and NKV (nvalid % 64 == 0: 1536 image
-// tokens, 6144 + 512 joint tokens, 256 text tokens), so the loop carries no key masking and no clamped per-lane tile
-// addresses. PF: the launch touches weights for the next kernel (p.pf_bytes > 0). Both are compile-time so that the
+// NWH waves per key half (4: 128 queries per workgroup, 8 waves). FULL: every key tile lies wholly below nvalid and
+// NKV (nvalid % 64 == 0: 1536 image tokens, 6144 + 512 joint tokens, 256 text tokens), so the loop carries no key
+// masking and no clamped per-lane tile addresses. PF: the launch touches weights for the next kernel (p.pf_bytes > 0). Both are compile-time so that the
 // main loop holds only the code it runs: the general form kept 44 - 62 scalar registers spilled to VGPR lanes and
 // their v_readlane / v_writelane in the loop.
 template <int NWH, bool FULL, bool PF, bool PP = false>
@@ -540,32 +541,18 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   if (p.pf_bytes < 0 || p.pf_bytes % 128 || p.pf_bytes >= (1L << 31) || (p.pf_bytes > 0 && (p.pf == nullptr || (uintptr_t)p.pf % 4)))
     return HXA_E_ARG;
   static bool attr = false;
-  static int num_cu = 0;
   if (!attr) {
     const void *kerns[] = {(const void *)attn_kernel<4, false, false>,      (const void *)attn_kernel<4, false, true>,
                            (const void *)attn_kernel<4, true, false>,       (const void *)attn_kernel<4, true, true>,
-                           (const void *)attn_kernel<3, false, false>,      (const void *)attn_kernel<3, false, true>,
-                           (const void *)attn_kernel<3, true, false>,       (const void *)attn_kernel<3, true, true>,
-                           (const void *)attn_kernel<4, true, false, true>, (const void *)attn_kernel<4, true, true, true>,
-                           (const void *)attn_kernel<3, true, false, true>, (const void *)attn_kernel<3, true, true, true>};
+                           (const void *)attn_kernel<4, true, false, true>, (const void *)attn_kernel<4, true, true, true>};
     for (const void *kf : kerns)
       if (hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES + SINK_BYTES) != hipSuccess)
         return HXA_E_HIP;
     if (hipFuncSetAttribute((const void *)attn_short_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, SK_LDS) !=
         hipSuccess)
       return HXA_E_HIP;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                                  hipSuccess)
-      num_cu = 256;
     attr = true;
   }
-  // one workgroup per CU at a time (128 KB of LDS): take the query-block size whose grid wastes the least of the
-  // last round (ties: 128 queries)
-  auto fill = [&](int qb) {
-    const long wgs = (long)((p.T + qb - 1) / qb) * p.H * p.batch, rounds = (wgs + num_cu - 1) / num_cu;
-    return (double)wgs / (double)(rounds * num_cu);
-  };
   HxaAttn pk = p;
   pk.clk = g_hxa_clk_attn;
 #ifndef HXA_ATTN_SHORT
@@ -576,8 +563,7 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
     hxa_launch(attn_short_kernel, dim3(nqb * p.H, p.batch), dim3(256), SK_LDS, st, pk, nqb);
     return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
   }
-  const bool small = fill(96) > fill(128) + 1e-9;
-  const int QB = small ? 96 : 128, nqb = (p.T + QB - 1) / QB;
+  const int nqb = (p.T + 127) / 128;
   const bool full = p.nvalid % KT == 0, pf = p.pf_bytes > 0;
   dim3 grid(nqb * p.H, p.batch);
   const int lds = LDS_BYTES + SINK_BYTES;
@@ -587,22 +573,13 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
     return e ? atoi(e) : 1;
   }();
   if (pp_env && full && (p.nvalid / KT) % 4 == 0) {
-    if (small) pf ? hxa_launch(attn_kernel<3, true, true, true>, grid, dim3(384), lds, st, pk, nqb)
-               : hxa_launch(attn_kernel<3, true, false, true>, grid, dim3(384), lds, st, pk, nqb);
-    else pf ? hxa_launch(attn_kernel<4, true, true, true>, grid, dim3(512), lds, st, pk, nqb)
-            : hxa_launch(attn_kernel<4, true, false, true>, grid, dim3(512), lds, st, pk, nqb);
+    pf ? hxa_launch(attn_kernel<4, true, true, true>, grid, dim3(512), lds, st, pk, nqb)
+       : hxa_launch(attn_kernel<4, true, false, true>, grid, dim3(512), lds, st, pk, nqb);
     return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
   }
-  if (small) {
-    if (full) pf ? hxa_launch(attn_kernel<3, true, true>, grid, dim3(384), lds, st, pk, nqb)
-              : hxa_launch(attn_kernel<3, true, false>, grid, dim3(384), lds, st, pk, nqb);
-    else pf ? hxa_launch(attn_kernel<3, false, true>, grid, dim3(384), lds, st, pk, nqb)
-            : hxa_launch(attn_kernel<3, false, false>, grid, dim3(384), lds, st, pk, nqb);
-  } else {
-    if (full) pf ? hxa_launch(attn_kernel<4, true, true>, grid, dim3(512), lds, st, pk, nqb)
-              : hxa_launch(attn_kernel<4, true, false>, grid, dim3(512), lds, st, pk, nqb);
-    else pf ? hxa_launch(attn_kernel<4, false, true>, grid, dim3(512), lds, st, pk, nqb)
-            : hxa_launch(attn_kernel<4, false, false>, grid, dim3(512), lds, st, pk, nqb);
-  }
+  if (full) pf ? hxa_launch(attn_kernel<4, true, true>, grid, dim3(512), lds, st, pk, nqb)
+            : hxa_launch(attn_kernel<4, true, false>, grid, dim3(512), lds, st, pk, nqb);
+  else pf ? hxa_launch(attn_kernel<4, false, true>, grid, dim3(512), lds, st, pk, nqb)
+          : hxa_launch(attn_kernel<4, false, false>, grid, dim3(512), lds, st, pk, nqb);
   return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
 }

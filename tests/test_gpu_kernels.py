@@ -454,15 +454,16 @@ def _attn(hip, q, k, v, nvalid=None, batch=1):
     return do.numpy()
 
 
-# on 256 CUs the 1024 x 32-head case takes the 128-query workgroups (8 waves), the others the 96-query ones; odd tile
-# counts (448 keys: 7, 520 valid of 576: 9) leave the second key half one tile short
+# 128-query workgroups (8 waves); odd tile counts (448 keys: 7, 520 valid of 576: 9) leave the second key half one
+# tile short
 # the last case is the MOSS-class joint attention at its own shape (6144 image + 512 text tokens, 24 heads); the
 # oracle (rows are independent) is evaluated on a sample of 416 query rows spread over all key tiles' range.
-# Whole key tiles in a multiple of 4 (1536, 6656, and 512 over 200 ragged queries; 320 keys on 5 tiles does not
-# qualify) take the ping-pong form: the key halves one phase apart
+# Whole key tiles in a multiple of 4 (1536, 6656, 1024 over 1000 ragged queries, and 512 over 200) take the
+# ping-pong form: the key halves one phase apart; 320 keys on 5 tiles and 384 keys on 6 do not qualify
 @pytest.mark.parametrize("T,NKV,nvalid,H", [(1536, 1536, 1536, 16), (1536, 256, 256, 16), (448, 448, 430, 4), (96, 64, 64, 2),
                                             (1024, 1024, 1000, 32), (300, 512, 500, 3), (200, 576, 520, 2),
-                                            (200, 512, 512, 3), (96, 320, 320, 2), (6656, 6656, 6656, 24)])
+                                            (200, 512, 512, 3), (96, 320, 320, 2), (6656, 6656, 6656, 24),
+                                            (1000, 1024, 1024, 4), (384, 384, 384, 2)])
 def test_attention_vs_oracle(T, NKV, nvalid, H):
     hip = _hip()
     say(f"attention T={T} NKV={NKV} nvalid={nvalid} H={H}")
