@@ -17,6 +17,7 @@
 //    (gemm2.c:19-22).
 //  * The fp16-rounded output tile is staged through LDS for a coalesced epilogue (16-byte loads / stores).
 //  * The block index is remapped so each of the 8 XCDs (own L2) works on a contiguous range of output tiles.
+#include <mutex>
 #include <type_traits>
 
 #include "hxa_common.h"
@@ -53,6 +54,8 @@ struct GemmParams {
   const uint8_t *pf;  // bytes to touch after the main loop (HxaGemm::pf)
   long pf_bytes;
   HxaClk clk;  // shader-clock record (hxa_clock_record), indexed by the launch's flat workgroup id
+  const hxa_h *erf_t2;  // GELU-erf: T2 of every non-negative fp16 bit pattern (null: evaluated in the epilogue)
+  int erf_lds;          // > 0: byte offset in LDS where the epilogue copies the table's first ERF_T2_LDS_N values
   // fused cross attention (gemm_xattn_kernel): the tile's queries attend to image (m0 / xa_T)'s keys
   // xa_k [NKV][xa_ldk] (+ image * xa_kb), V^T xa_vt [D][xa_ldvt] (+ image * xa_vb); O to xa_o [M][xa_ldo]
   const hxa_h *xa_k, *xa_vt;
@@ -206,6 +209,24 @@ HXA_DEV float gelu_erf_f(float t) {
   const float t2 = (float)(hxa_h)(a * 0.5f * erfcf(a * 0.7071067811865476f));
   return fmaxf(t, 0.0f) - t2;
 }
+// T2(a) = f16(a * 0.5 * erfc(a / sqrt 2)) of gelu_erf_f for every non-negative fp16 bit pattern b (a = |t|; NaN and
+// inf patterns included): the GELU-erf epilogue looks its values up instead of evaluating erfcf per output. Filled
+// once per device by erf_t2_kernel with gelu_erf_f's own expression, so a lookup returns the same bits.
+constexpr int ERF_T2_N = 0x8000;
+// the part of the table a GELU-erf epilogue copies into LDS where its tile leaves room: |t| < 6 (bit patterns below
+// 0x4600), 35840 bytes = 35 wave-wide 16-byte copies; larger |t| (rare) is looked up in the global table
+constexpr int ERF_T2_LDS_N = 0x4600, ERF_T2_LDS_BYTES = ERF_T2_LDS_N * 2;
+__device__ __align__(16) hxa_h g_erf_t2[ERF_T2_N];
+__global__ __launch_bounds__(256) void erf_t2_kernel(hxa_h *t) {
+  const int b = blockIdx.x * 256 + threadIdx.x;
+  if (b >= ERF_T2_N) return;
+  const float a = (float)__builtin_bit_cast(hxa_h, (uint16_t)b);
+  t[b] = (hxa_h)(a * 0.5f * erfcf(a * 0.7071067811865476f));
+}
+HXA_DEV float gelu_erf_tab(float t, const hxa_h *__restrict__ t2tab) {
+  const uint32_t b = __builtin_bit_cast(uint16_t, (hxa_h)t) & 0x7fffu;
+  return fmaxf(t, 0.0f) - (float)t2tab[b];
+}
 HXA_DEV float situ_f(float u, float g) {
   // moss kern.c:376-405: f16(f16(25 tanh(u/25)) * f16(4 tanh(g/4) sigmoid(g)))
   const float tu = (float)(hxa_h)(25.0f * tanhf(u * 0.04f));
@@ -226,6 +247,8 @@ struct GemmGeo {
   static constexpr int C_BYTES = BM * CROW * 2;
   static constexpr int PF_LDS = 256;                                 // prefetch_share's sink (64 lanes x 4 B)
   static constexpr int LDS = (NS * STAGE > C_BYTES ? NS * STAGE : C_BYTES) + PF_LDS;
+  // a GELU-erf launch's LDS with the T2 table past everything above, where that fits the CU's 160 KB
+  static constexpr bool ERF_FITS = LDS + ERF_T2_LDS_BYTES <= 160 * 1024;
   static constexpr int NA = BM / 64;                                 // A load instructions per wave per stage
   static constexpr int TW = (W_BYTES / 16 + 63) / 64;                // W load instructions per stage (all waves)
 };
@@ -373,6 +396,56 @@ HXA_DEV void gemm_epilogue(const GemmParams &p, const hxa_h *Cs, int m0, int n0,
     return;
   }
   }
+  if (p.epi == HXA_EPI_GELU_ERF && p.erf_t2 != nullptr && nsplit == BN) {
+    // GELU-erf through the T2 table: the LDS reads and table lookups of RB chunks are issued together before any
+    // of them is used, so a thread waits one lookup latency per batch instead of one per chunk. With erf_lds the
+    // table's |t| < 6 part is first copied into LDS past the staged tile (LDS gathers, where global ones issue at
+    // a few lanes per clock)
+    constexpr int ITERS = BM * C8 / NT, RB = ITERS % 4 == 0 ? 4 : ITERS % 3 == 0 ? 3 : ITERS % 2 == 0 ? 2 : 1;
+    static_assert(BM * C8 % NT == 0 && ITERS % RB == 0, "whole chunk passes");
+    static_assert(ERF_T2_LDS_BYTES % 1024 == 0, "whole wave-wide copies");
+    const hxa_h *tl = nullptr;
+    if (p.erf_lds > 0) {
+      uint8_t *dst = (uint8_t *)Cs + p.erf_lds;
+      const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+      for (int c0 = wave * 64; c0 < ERF_T2_LDS_BYTES / 16; c0 += NT) {
+        const uint32_t la = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t *)(dst + c0 * 16));
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(p.erf_t2 + (c0 + lane) * 8), "s"(la)
+                     : "memory", "m0");
+      }
+      wait_vm<0>();
+      __syncthreads();
+      tl = (const hxa_h *)dst;
+    }
+#pragma unroll
+    for (int b0 = 0; b0 < ITERS; b0 += RB) {
+      half8_t v[RB];
+      hxa_h t2[RB][8];
+      bool ok[RB];
+#pragma unroll
+      for (int u = 0; u < RB; u++) {
+        const int c = tid + (b0 + u) * NT, ml = c / C8, nl = (c % C8) * 8;
+        ok[u] = m0 + ml < p.M && n0 + nl < p.N;
+        v[u] = *(const half8_t *)(Cs + ml * CROW + nl);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const hxa_h x = v[u][e];  // (a scalar copy: bit_cast of a vector element itself read element 0 only)
+          const uint32_t b = __builtin_bit_cast(uint16_t, x) & 0x7fffu;
+          t2[u][e] = tl != nullptr && b < (uint32_t)ERF_T2_LDS_N ? tl[b] : p.erf_t2[b];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < RB; u++) {
+        if (!ok[u]) continue;
+        const int c = tid + (b0 + u) * NT, ml = c / C8, nl = (c % C8) * 8;
+        half8_t o;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = (hxa_h)(fmaxf((float)v[u][e], 0.0f) - (float)t2[u][e]);
+        *(half8_t *)(p.out + (long)(m0 + ml) * p.ldo + n0 + nl) = o;
+      }
+    }
+    return;
+  }
   auto rows_pass = [&](auto ncols_c) {
   const int nc8 = ncols_c / 8;
   for (int c = tid; c < BM * nc8; c += NT) {
@@ -387,9 +460,14 @@ HXA_DEV void gemm_epilogue(const GemmParams &p, const hxa_h *Cs, int m0, int n0,
       if (p.epi == HXA_EPI_GELU_TANH) {  // (head-normed tiles never get here: whole tiles take the path above)
 #pragma unroll
         for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_tanh_f((float)v[e]);
-      } else if (p.epi == HXA_EPI_GELU_ERF) {
+      } else if (p.epi == HXA_EPI_GELU_ERF) {  // (without the T2 table, or with transposed columns)
+        if (p.erf_t2) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_erf_f((float)v[e]);
+          for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_erf_tab((float)v[e], p.erf_t2);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] = (hxa_h)gelu_erf_f((float)v[e]);
+        }
       }
       *(half8_t *)(p.out + o) = v;
     }
@@ -1187,14 +1265,22 @@ hipError_t launch_t(const GemmParams &p, int ksplit, hipStream_t st) {
   auto kern = gemm_kernel<BM, BN, FMT, ASYM, SPLIT2, NW>;
   using G = GemmGeo<BM, BN, FMT>;
   const int lds = SPLIT2 && 2 * G::C_BYTES > G::LDS ? 2 * G::C_BYTES : G::LDS;
+  constexpr bool erf_ok = !SPLIT2 && G::ERF_FITS;
   static bool attr = false;
   if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       erf_ok ? G::LDS + ERF_T2_LDS_BYTES : lds);
     if (e != hipSuccess) return e;
     attr = true;
   }
   dim3 grid(p.tiles_m * p.tiles_n, 1, ksplit);
-  hxa_launch(kern, grid, dim3(64 * NW), lds, st, p);
+  if (erf_ok && p.epi == HXA_EPI_GELU_ERF && p.erf_t2 != nullptr) {  // the T2 table past the kernel's own LDS
+    GemmParams pe = p;
+    pe.erf_lds = G::LDS;
+    hxa_launch(kern, grid, dim3(64 * NW), G::LDS + ERF_T2_LDS_BYTES, st, pe);
+  } else {
+    hxa_launch(kern, grid, dim3(64 * NW), lds, st, p);
+  }
   return hipGetLastError();
 }
 
@@ -1211,12 +1297,19 @@ hipError_t launch_pp(const GemmParams &p, int ksplit, hipStream_t st) {
   using G = GemmGeo<BM, BN, FMT>;
   static bool attr = false;
   if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       G::ERF_FITS ? G::LDS + ERF_T2_LDS_BYTES : G::LDS);
     if (e != hipSuccess) return e;
     attr = true;
   }
   dim3 grid(p.tiles_m * p.tiles_n, 1, ksplit);
-  hxa_launch(kern, grid, dim3(512), G::LDS, st, p);
+  if (G::ERF_FITS && p.epi == HXA_EPI_GELU_ERF && p.erf_t2 != nullptr) {  // the T2 table past the kernel's own LDS
+    GemmParams pe = p;
+    pe.erf_lds = G::LDS;
+    hxa_launch(kern, grid, dim3(512), G::LDS + ERF_T2_LDS_BYTES, st, pe);
+  } else {
+    hxa_launch(kern, grid, dim3(512), G::LDS, st, p);
+  }
   return hipGetLastError();
 }
 
@@ -1304,6 +1397,26 @@ static bool tile_built(int bm, int bn, int nw, int fmt, bool split2) {
   if (bm == 128 && bn == 64) return !q4;
   return (bm == 192 && (bn == 256 || bn == 192 || bn == 128)) || (bm == 256 && bn == 128) ||
          (bm == 128 && (bn == 256 || bn == 128)) || (bm == 64 && bn == 128);
+}
+
+// The device address of the GELU-erf T2 table on the current device, filled on first use there (a launch of
+// erf_t2_kernel on `st`, waited for, so the table is complete for every later launch on any stream). Under stream
+// capture an unfilled table is not filled (the epilogue then evaluates erfcf): null.
+const hxa_h *erf_table(hipStream_t st) {
+  static const hxa_h *tab[HXA_MAX_DEVICES];
+  static std::mutex mu;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= HXA_MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lk(mu);
+  if (tab[dev]) return tab[dev];
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+  void *ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_erf_t2)) != hipSuccess || ptr == nullptr) return nullptr;
+  hxa_launch(erf_t2_kernel, dim3(ERF_T2_N / 256), dim3(256), 0, st, (hxa_h *)ptr);
+  if (hipGetLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess) return nullptr;
+  tab[dev] = (const hxa_h *)ptr;
+  return tab[dev];
 }
 
 // validate a GEMM description, fill its kernel parameters and choose (or take the forced) tile
@@ -1417,6 +1530,7 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
   bool split2;
   const int r = gemm_prepare(g, p, bm, bn, nw, w, split2);
   if (r != HXA_OK) return r;
+  if (g.epi == HXA_EPI_GELU_ERF) p.erf_t2 = erf_table(st);
   hipError_t e;
   if (split2) {
     if (w.fmt == HXA_W_F16) e = launch_split2<HXA_W_F16, false>(bm, bn, p, st);
@@ -1622,6 +1736,8 @@ int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st) {
     g1f.force_nw = nw;
     r = gemm_prepare(g1f, p1, bm1, bn1, nw1, w1, s1);
     if (r != HXA_OK) return r;
+    if (g0.epi == HXA_EPI_GELU_ERF) p0.erf_t2 = erf_table(st);
+    if (g1.epi == HXA_EPI_GELU_ERF) p1.erf_t2 = erf_table(st);
     const long n0 = (long)p0.tiles_m * p0.tiles_n, n1 = (long)p1.tiles_m * p1.tiles_n;
     const long c = num_cu();
     const bool extra_round = (n0 + n1 + c - 1) / c > (n0 + c - 1) / c;

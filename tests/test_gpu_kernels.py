@@ -248,6 +248,27 @@ def test_gemm_epilogues():
     assert ulp_diff(got, ref).max() <= 2
 
 
+def test_gelu_epilogues_every_fp16_input():
+    """Both GELU epilogues over every finite fp16 value: with A the identity (K = M = 256) the GEMM's f16(acc) is W^T
+    exactly, and W holds each finite fp16 bit pattern once (inf / NaN patterns, which would turn the zero products
+    into NaN, and -0 replaced by 0). GELU-erf goes through the epilogue's T2 lookup table; both are checked against the
+    oracle's table semantics (kern.c:235-260)."""
+    hip = _hip()
+    say("gemm GELU epilogues over every finite fp16 input")
+    pat = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    pat[((pat & 0x7C00) == 0x7C00) | (pat == 0x8000)] = 0  # inf / NaN, and -0 (the zero products sum to +0)
+    W = pat.view(np.float16).reshape(256, 256)
+    A = np.eye(256, dtype=np.float16)
+    t = np.ascontiguousarray(W.T)
+    assert np.array_equal(_run_gemm(hip, A, 0, W, None, 256, 256).view(np.uint16), t.view(np.uint16))
+    for epi, mode in ((hip.EPI_GELU_ERF, 0), (hip.EPI_GELU_TANH, 1)):
+        got = _run_gemm(hip, A, 0, W, None, 256, 256, epi=epi)
+        ref = hxo.gelu(t, mode).view(np.float16)
+        d = ulp_diff(got, ref)
+        print(f"epi {epi}: max ulp {d.max()}, {int((d > 0).sum())} of {d.size} outputs differ", flush=True)
+        assert d.max() <= 2
+
+
 @pytest.mark.parametrize("fmt,tile", [(f, t) for f in (0, 1, 2)
                                       for t in ((256, 256, 9), (192, 256, 9), (128, 256, 9), (128, 128, 9), (192, 128, 8),
                                                 (192, 128, 4))
