@@ -137,6 +137,8 @@ int hxa_clock_record(int kind, void *rec, long nrec);
 /* out = epi(A[M][K] . W[N][K]^T); replaces gemm_run_ex / gemm_run_geo (hexagon/mega/gemm2.c:96-141).
  * STORE: out[m][n] (ldo); with out_t != NULL the columns n >= split_col go to out_t[n - split_col][m] (ldo_t).
  * STORE_T: out[n][m]. GELU_*: out = f16(gelu(f16(acc))). RESADD: x[m][n] += gate[n] f16(acc) (x fp32, ldx).
+ * GELU_ERF looks up a per-device table of f16(a * 0.5 * erfc(a / sqrt 2)), built by the first such launch on a
+ * device, which waits for its stream once (a launch under stream capture before then evaluates erfc instead).
  * SITU: W rows interleaved per 32 (up_j, gate_j), out[m][j*32+c] (moss gemm2.c mode 5).
  * PARTIAL: ksplit slices, out[z*out_zstride + m*ldo + n] = f16(partial z) (blk.c:172-174).
  * RESADD_SPLIT2 (ksplit 1, K % 128 == 0): x[m][n] += gate[n] (f16(first K/2) + f16(second K/2)), the split-K
