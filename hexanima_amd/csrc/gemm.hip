@@ -742,7 +742,11 @@ template <int BM, int BN, int FMT, bool ASYM, bool SPLIT2, int NW, bool XATTN = 
 HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   using G = GemmGeo<BM, BN, FMT>;
   constexpr int NT = 64 * NW;
-  constexpr int WTM = BM / 2, WTN = BN / (NW / 2), MI = WTM / 32, NI = WTN / 32;
+  // waves along M: 2 (a 2 x NW/2 wave grid), or 1 for int8 / int4 weights where BN splits into 32-column strips (a
+  // 1 x NW grid): every W fragment then belongs to one wave and is dequantised once per workgroup, at the price of
+  // each wave reading all BM rows of A
+  constexpr int WMW = (FMT != HXA_W_F16 && !XATTN && BN % (32 * NW) == 0) ? 1 : 2;
+  constexpr int WTM = BM / WMW, WTN = BN / (NW / WMW), MI = WTM / 32, NI = WTN / 32;
   constexpr int BK = G::BK, NS = G::NS, PD = G::PD;
   static_assert(BM % 64 == 0 && WTN % 32 == 0 && (NW == 4 || NW == 8), "tile shape");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
@@ -752,7 +756,7 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
   const int m0 = tm * BM, n0 = tn * BN;
   const int kbase = z * p.Kslice;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = WMW == 2 ? (wave & 1) : 0, wn = WMW == 2 ? (wave >> 1) : wave;
   const HxaClkMark clk0 = clk_mark(p.clk);
   if constexpr (XATTN) {  // the first two key tiles of the fused attention, into LDS past the ring
     xattn_load_kv(p, m0, n0, 0, wave, lane, lds8);
@@ -1005,7 +1009,10 @@ HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
   const int bid = PAIRED ? bid_arg : (int)blockIdx.x;
   using G = GemmGeo<BM, BN, FMT>;
   constexpr int NT = 512, NWG = 4;  // threads, waves per group
-  constexpr int WTM = BM / 2, WTN = BN / 4, MI = WTM / 32, NI = WTN / 32;
+  // each group's 4 waves cover its BN / 2 columns as a 2 x 2 grid, or, for int8 / int4 weights on 256-wide tiles, as
+  // 1 x 4 strips of 32 columns over all BM rows, so that no two waves of a group dequantise the same W fragment
+  constexpr int WMW = (FMT != HXA_W_F16 && BN >= 256) ? 1 : 2;
+  constexpr int WTM = BM / WMW, WTN = BN / 2 / (4 / WMW), MI = WTM / 32, NI = WTN / 32;
   constexpr int BK = G::BK, NS = G::NS;
   constexpr int NAI = BM / 16, TW = G::W_BYTES / 1024;       // 1 KB load instructions per stage (A, W)
   constexpr int LPS = (NAI + TW) / NWG;                     // per group-1 wave and stage (+ the vectors for wave 0)
@@ -1021,7 +1028,7 @@ HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
   const int z = blockIdx.z;
   const int kbase = z * p.Kslice;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = wave >> 2, wl = wave & 3, wm = wl & 1, wn = wl >> 1;
+  const int grp = wave >> 2, wl = wave & 3, wm = WMW == 2 ? (wl & 1) : 0, wn = WMW == 2 ? (wl >> 1) : wl;
   const int nk = p.Kslice / BK;
   const HxaClkMark clk0 = clk_mark(p.clk);
 
