@@ -42,6 +42,22 @@ constexpr float RESCALE_TH = 5.5f;
 
 HXA_DEV float16_t mfma(half8_t a, half8_t b, float16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
 
+// Wave gw of the nw waves in the workgroups past the attention tiles: an equal run of the side GEMV's rows, four in
+// flight (the same row values as modgemv_kernel)
+HXA_DEV void side_gemv(const HxaSideGemv &s, int gw, int nw, int lane) {
+  const long rpw = (s.N + nw - 1) / nw, n0 = (long)gw * rpw, n1 = n0 + rpw < s.N ? n0 + rpw : s.N;
+  if (n0 >= s.N) return;
+  auto run = [&](auto kc) {
+    constexpr int KC = decltype(kc)::value;
+    float xr[KC][8];
+    modgemv_x<KC, 8>(s.x, s.act, lane, xr);
+    modgemv_rows<KC, 8, 4>(xr, s.W, n0, n1, s.y, s.per, s.ostride, s.split, s.gap, lane);
+  };
+  if (s.K == 2048) run(std::integral_constant<int, 4>{});
+  else if (s.K == 2560) run(std::integral_constant<int, 5>{});
+  else if (s.K == 3072) run(std::integral_constant<int, 6>{});
+}
+
 // NWH waves per key half (4: 128 queries per workgroup, 8 waves). FULL: every key tile lies wholly below nvalid and
 // NKV (nvalid % 64 == 0: 1536 image tokens, 6144 + 512 joint tokens, 256 text tokens), so the loop carries no key
 // masking and no clamped per-lane tile addresses. PF: the launch touches weights for the next kernel (p.pf_bytes > 0). Both are compile-time so that the
@@ -58,6 +74,10 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   const int half = wave / NWH, wq = wave % NWH, g = lane >> 5, ql = lane & 31;
   // XCD-aware order: the query blocks of one head run on one XCD (its L2 keeps that head's K / V^T)
   const int ntot = nqb * p.H, bid = blockIdx.x;
+  if (bid >= ntot) {  // a workgroup past the tiles (side_wgs): GEMV rows, no LDS and no barrier
+    side_gemv(p.side, (bid - ntot) * 2 * NWH + wave, (gridDim.x - ntot) * 2 * NWH, lane);
+    return;
+  }
   const int tile = (ntot % 8 == 0) ? (bid % 8) * (ntot / 8) + bid / 8 : bid;
   const int h = tile / nqb, qb = tile % nqb, b = blockIdx.y;
   const hxa_h *q = p.q + (long)b * p.q_bstride + h * 128;
@@ -153,8 +173,8 @@ __global__ __launch_bounds__(2 * NWH * 64) void attn_kernel(HxaAttn p, int nqb) 
   const uint8_t *pf_base = nullptr;
   uint32_t pf_lines = 0;  // of this workgroup
   if constexpr (PF) {
-    const uint32_t lines = (uint32_t)(p.pf_bytes >> 7), nwg = gridDim.x * gridDim.y;
-    const uint32_t per = (lines + nwg - 1) / nwg, l0 = min((blockIdx.x + blockIdx.y * gridDim.x) * per, lines);
+    const uint32_t lines = (uint32_t)(p.pf_bytes >> 7), nwg = ntot * gridDim.y;  // the attention workgroups
+    const uint32_t per = (lines + nwg - 1) / nwg, l0 = min((blockIdx.x + blockIdx.y * ntot) * per, lines);
     pf_base = p.pf + ((long)l0 << 7);
     pf_lines = min(lines, l0 + per) - l0;
   }
@@ -540,6 +560,19 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   // the weight touch: whole 128-byte lines, below 2 GB (the per-lane byte offsets are unsigned 32-bit)
   if (p.pf_bytes < 0 || p.pf_bytes % 128 || p.pf_bytes >= (1L << 31) || (p.pf_bytes > 0 && (p.pf == nullptr || (uintptr_t)p.pf % 4)))
     return HXA_E_ARG;
+  if (p.side_wgs < 0 || p.side_wgs > 4096) return HXA_E_ARG;
+  if (p.side_wgs > 0) {
+    const HxaSideGemv &g = p.side;
+    if (p.batch != 1 || (g.K != 2048 && g.K != 2560 && g.K != 3072) || g.N <= 0 || g.per <= 0 || g.split < 0 ||
+        g.gap < 0 || !g.y || ((uintptr_t)g.x | (uintptr_t)g.W) % 16 || !g.x || !g.W)
+      return HXA_E_ARG;
+  }
+  // the side GEMV as its own launch, where the attention kernel does not host it
+  auto side_alone = [&]() -> int {
+    if (p.side_wgs == 0) return HXA_OK;
+    const HxaSideGemv &g = p.side;
+    return hxa_modgemv_launch(g.x, g.K, g.W, g.N, g.y, g.per, g.ostride, g.split, g.gap, g.act, st);
+  };
   static bool attr = false;
   if (!attr) {
     const void *kerns[] = {(const void *)attn_kernel<4, false, false>,      (const void *)attn_kernel<4, false, true>,
@@ -561,11 +594,12 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   if (HXA_ATTN_SHORT && p.nvalid <= 4 * KT) {  // every key tile resident: the two-pass kernel
     const int nqb = (p.T + 127) / 128;
     hxa_launch(attn_short_kernel, dim3(nqb * p.H, p.batch), dim3(256), SK_LDS, st, pk, nqb);
-    return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
+    if (hipGetLastError() != hipSuccess) return HXA_E_HIP;
+    return side_alone();
   }
   const int nqb = (p.T + 127) / 128;
   const bool full = p.nvalid % KT == 0, pf = p.pf_bytes > 0;
-  dim3 grid(nqb * p.H, p.batch);
+  dim3 grid(nqb * p.H + p.side_wgs, p.batch);
   const int lds = LDS_BYTES + SINK_BYTES;
   // the ping-pong form: whole tiles, the same even number of tiles in both halves (HXA_ATTN_PP=0: lock-step form)
   static const int pp_env = [] {
@@ -582,4 +616,17 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   else pf ? hxa_launch(attn_kernel<4, false, true>, grid, dim3(512), lds, st, pk, nqb)
           : hxa_launch(attn_kernel<4, false, false>, grid, dim3(512), lds, st, pk, nqb);
   return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
+}
+
+int hxa_attn_idle_wgs(int T, int H, int batch) {
+  if (batch != 1 || T <= 0 || H <= 0) return 0;
+  static int ncu = 0;
+  if (ncu == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 0;
+    ncu = n;
+  }
+  const int ntot = (T + 127) / 128 * H, rem = ntot % ncu, idle = rem == 0 ? 0 : ncu - rem;
+  return idle >= ncu / 4 ? idle : 0;
 }

@@ -12,16 +12,6 @@
 
 namespace {
 
-// sum over the 64 lanes, all in VALU cross-lane moves: the 16-lane row sums (sum8 + row mirror), then row 0 -> 1
-// and row 2 -> 3 (row_bcast:15), rows 0+1 -> 3 (row_bcast:31); lane 63 holds the total, read into a scalar
-HXA_DEV float wave_sum(float v) {
-  v = sum8(v);
-  v += dpp_f<0x140>(v);  // row_mirror: every lane of a row holds the row sum
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
 // ---------------------------------------------------------------------------------------------------------------
 // modulated norm (kern.c:31-65 LN-mod; moss kern.c:345-375 RMS-mod)
 // ---------------------------------------------------------------------------------------------------------------
@@ -349,58 +339,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float *__restrict__ x, 
 }
 
 // Modulation GEMV over stacked weight matrices (megarun.cpp:156-171 role: every block's adaLN rows from one
-// embedding vector). Row n of W [N][K] gives y[(n / per) * ostride + r + (r >= split ? gap : 0)], r = n % per, with
-// y = sum_k act(x[k]) W[n][k]. act(x) is applied once per lane when x is loaded (1: SiLU). K = KC chunks of 64*EPL;
-// each lane keeps its EPL*KC inputs in registers (k = c*64*EPL + EPL*lane + e); a wave streams RPW rows with
-// EPL*2-byte non-temporal weight loads, two rows in flight.
+// embedding vector): rows of W [N][K] as modgemv_rows (hxa_common.h) computes and places them; each wave streams
+// RPW rows, two in flight.
 template <int KC, int EPL>
 __global__ __launch_bounds__(256) void modgemv_kernel(const float *__restrict__ x, const hxa_h *__restrict__ W, long N,
                                                       float *__restrict__ y, int per, long ostride, int split, int gap,
                                                       int act, int rpw) {
-  constexpr int CH = 64 * EPL, K = KC * CH;
-  using wvec = std::conditional_t<EPL == 8, half8_t, half4_t>;
-  // the weights are read once per call: non-temporal loads (modulation of 28 2B blocks, 1.41 GB: 249 -> 212 us)
-  auto wload = [](const hxa_h *p) -> wvec { return __builtin_nontemporal_load((const wvec *)p); };
   const int lane = threadIdx.x & 63;
   const long row0 = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw;
+  if (row0 >= N) return;
   float xr[KC][EPL];
-#pragma unroll
-  for (int c = 0; c < KC; c++)
-#pragma unroll
-    for (int e4 = 0; e4 < EPL; e4 += 4) {
-      const float4_t a = *(const float4_t *)(x + c * CH + lane * EPL + e4);
-#pragma unroll
-      for (int e = 0; e < 4; e++) xr[c][e4 + e] = act == 1 ? a[e] / (1.0f + __expf(-a[e])) : a[e];
-    }
-  for (int i = 0; i < rpw; i += 2) {
-    const long n0 = row0 + i;
-    if (n0 >= N) break;
-    const bool two = n0 + 1 < N && i + 1 < rpw;
-    wvec w0[KC], w1[KC];
-#pragma unroll
-    for (int c = 0; c < KC; c++) w0[c] = wload(W + n0 * K + c * CH + lane * EPL);
-    if (two) {
-#pragma unroll
-      for (int c = 0; c < KC; c++) w1[c] = wload(W + (n0 + 1) * K + c * CH + lane * EPL);
-    }
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (int c = 0; c < KC; c++)
-#pragma unroll
-      for (int e = 0; e < EPL; e++) {
-        a0 = fmaf(xr[c][e], (float)w0[c][e], a0);
-        if (two) a1 = fmaf(xr[c][e], (float)w1[c][e], a1);
-      }
-    a0 = wave_sum(a0);
-    if (two) a1 = wave_sum(a1);
-    if (lane == 0) {
-      for (int j = 0; j < (two ? 2 : 1); j++) {
-        const long n = n0 + j;
-        const int r = (int)(n % per);
-        y[(n / per) * ostride + r + (r >= split ? gap : 0)] = j ? a1 : a0;
-      }
-    }
-  }
+  modgemv_x<KC, EPL>(x, act, lane, xr);
+  modgemv_rows<KC, EPL, 2>(xr, W, row0, row0 + rpw < N ? row0 + rpw : N, y, per, ostride, split, gap, lane);
 }
 
 // patch embed (animad.cpp:440-446): x[b][tk][n] = sum_f tok[b tk][f] * Wemb[n][f], f = 4 c + 2 a + bb over the

@@ -65,6 +65,18 @@ int hxa_gemm_group_launch(const void *params_dev, int G, int tiles, int fmt, hip
 // int8 / int4 weight -> fp16 k-tiled [K/32][N][32] at out (2 N K bytes): the same values the GEMM main loops use
 int hxa_dequant_launch(const HxaWeight &w, hxa_h *out, hipStream_t st);
 
+// A modulation GEMV (the rows hxa_modgemv_launch computes, with the same bits) that an attention launch runs in
+// extra workgroups appended to its grid, on the CUs its own tiles leave idle: y rows [0, N) of act(x) . W^T, K (= the
+// embedding width) 2048, 2560 or 3072
+struct HxaSideGemv {
+  const float *x = nullptr;
+  const hxa_h *W = nullptr;
+  long N = 0;
+  float *y = nullptr;
+  int per = 1;
+  long ostride = 0;
+  int split = 0, gap = 0, act = 0, K = 0;
+};
 struct HxaAttn {
   const hxa_h *q, *k, *vt;  // q [T][ldq], k [NKV][ldk] (head h at column h*128); vt [H*128][ldvt] (keys contiguous)
   long ldq, ldk, ldvt;
@@ -78,8 +90,16 @@ struct HxaAttn {
   // multiple of 128)
   const uint8_t *pf = nullptr;
   long pf_bytes = 0;
+  // side_wgs > 0 (batch 1): side runs in side_wgs workgroups past the attention tiles. Where the chosen kernel cannot
+  // host it (at most 256 keys: the two-pass kernel), it runs as its own hxa_modgemv_launch after the attention.
+  HxaSideGemv side{};
+  int side_wgs = 0;
 };
 int hxa_attn_launch(const HxaAttn &p, hipStream_t st);
+// workgroups an attention launch of T queries x H heads (batch 1) leaves idle on this GPU: what side_wgs may use
+// (0 when the tiles leave fewer than a quarter of the CUs idle in their last round: too few to stream a GEMV in
+// the attention's time)
+int hxa_attn_idle_wgs(int T, int H, int batch);
 
 // h[t][:] = f16(norm(x[t][:]) * mul + add); LN: (x-mu)*rsqrt(E[x^2]-mu^2+eps), RMS (w != NULL): x*rsqrt(E[x^2]+eps)
 // with mul = (1 + scale) (LN) or (1 + scale) * w (RMS), add = shift.
@@ -204,10 +224,11 @@ int hxa_noalloc_setup(void **out);
 // fp16 partials of the MLP-down that a chained block leaves pending (t1 .. t1 + (n-1) BT D in its workspace)
 int hxa_block_down_parts(const hxa_block_dims *d);
 // ck_pre / cvt_pre (Anima blocks, no stage stop): the block's text k / v, computed before the chain
-// (hxa_block_textkv_plan); the block then skips that projection
+// (hxa_block_textkv_plan); the block then skips that projection. side (side_wgs > 0, batch 1): a GEMV that the
+// block's self-attention launch runs in its idle workgroups (HxaAttn::side)
 int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
                           const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
                           void *stream, const float *pend_gate, int defer, const hxa_h *ck_pre = nullptr,
-                          const hxa_h *cvt_pre = nullptr);
+                          const hxa_h *cvt_pre = nullptr, const HxaSideGemv *side = nullptr, int side_wgs = 0);
 int hxa_block_textkv_plan(const hxa_block_dims *d, const void *pack, const void *ctx, hxa_h *ck, hxa_h *cvt,
                           HxaGemm *g, HxaWeight *w);

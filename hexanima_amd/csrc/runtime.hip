@@ -732,8 +732,10 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
 // the last block of the chain). Without a stage stop only.
 int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
                           const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
-                          void *stream, const float *pend_gate, int defer, const hxa_h *ck_pre, const hxa_h *cvt_pre) {
+                          void *stream, const float *pend_gate, int defer, const hxa_h *ck_pre, const hxa_h *cvt_pre,
+                          const HxaSideGemv *side, int side_wgs) {
   g_err[0] = 0;
+  if (side_wgs < 0 || (side_wgs > 0 && (!side || d->batch != 1))) return fail(HXA_E_ARG, "block: side GEMV needs batch 1");
   if ((pend_gate || defer) && stop) return fail(HXA_E_ARG, "block: chained residuals need stop == 0");
   TRY(check_dims(d));
   if (!pack || !x || !mod || !ws || (d->kind == 0 && !ctx)) return fail(HXA_E_ARG, "block: null pointer");
@@ -844,6 +846,11 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     p.pf = apf0;
     p.pf_bytes = apf0 != nullptr && apf1 > apf0 ? apf1 - apf0 : 0;
     apf0 = apf1 = nullptr;  // one launch
+    if (side_wgs > 0) {  // the first attention launch (self / joint) hosts the side GEMV
+      p.side = *side;
+      p.side_wgs = side_wgs;
+      side_wgs = 0;
+    }
     const int r = hxa_attn_launch(p, st);
     if (r != HXA_OK) return fail(r, "block attention rejected");
     return HXA_OK;
