@@ -22,6 +22,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <initializer_list>
 #include <map>
@@ -29,6 +30,7 @@
 #include <vector>
 
 #include "../../include/hexanima_hip.h"
+
 #include "hxa_common.h"
 #include "kernels.h"
 
@@ -267,8 +269,11 @@ int record_step(Dit &d, const Pass &ps) {
   // Anima blocks at batch 1 whose self attention leaves CUs idle (2B: 192 workgroups on 256 CUs): block k+1's
   // modulation, and in the last block the final layer's, runs in those CUs during block k's self attention (the same
   // rows, the same bits); only block 0's runs ahead on its own (2B DiT step: 28 x 7.6 us of modulation launches)
+  // (HXA_DIT_SIDE=0 when a step is recorded: every modulation in its own launches, for comparison)
   const bool side_k = D == 2048 || D == 2560 || D == 3072;  // the embedding widths the attention kernel hosts
-  const int side_wgs = d.form == 0 && b.kind == 0 && side_k ? hxa_attn_idle_wgs(b.T, b.H, b.batch) : 0;
+  const char *side_env = getenv("HXA_DIT_SIDE");
+  const bool side_on = side_k && !(side_env && atoi(side_env) == 0);
+  const int side_wgs = d.form == 0 && b.kind == 0 && side_on ? hxa_attn_idle_wgs(b.T, b.H, b.batch) : 0;
   if (d.form == 0) {
   // timestep embedding and modulation
   DTRY(hxa_linear_f32_launch(d.sig, temb, 1, temb, d.L1, D, d.cvec, D, 2, nullptr, 0, 0, st));  // sinusoid in the GEMV

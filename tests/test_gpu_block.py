@@ -737,6 +737,38 @@ def test_dit_graph_replay_matches_eager():
         assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("lat_hw", [(96, 64), (32, 24)])
+def test_dit_side_gemv_matches_separate_modulation(lat_hw, monkeypatch):
+    """2B-shaped DiT at batch 1: with the next block's modulation (and the final layer's) computed in workgroups
+    appended to each self-attention launch, the latents after four steps equal, bit for bit, those with every
+    modulation in its own launches (HXA_DIT_SIDE=0). 1536 tokens: 192 attention workgroups host the GEMV; 192
+    tokens: the attention runs the short-key kernel and the GEMV its own launch after it."""
+    hip = _hip()
+    lib = hip.lib()
+    say(f"dit side gemv lat {lat_hw}")
+    rng = np.random.default_rng(11)
+    lat = rng.standard_normal((1, 16) + lat_hw).astype(np.float32)
+    ctx = rng.standard_normal((1, 256, 1024)).astype(np.float32)
+    outs = []
+    for side in ("1", "0"):
+        monkeypatch.setenv("HXA_DIT_SIDE", side)
+        bd = hip.BlockDims(0, 2048, 16, 8192, 256, 1024, 0, 1, 0, 0, 0, 1)
+        cfg = hip.DitCfg(bd, 2, 16, lat_hw[0], lat_hw[1], 256, 0)
+        p = C.c_void_p()
+        hip.check(lib.hxa_dit_create(C.byref(cfg), 77, C.byref(p)), "dit_create")
+        try:
+            hip.check(lib.hxa_dit_set_inputs(p, lat.ctypes.data, ctx.ctypes.data), "set_inputs")
+            for s0, s1 in ((1.0, 0.75), (0.75, 0.5), (0.5, 0.25), (0.25, 0.0)):
+                hip.check(lib.hxa_dit_step(p, s0, s1, 1), "step")
+            cur = np.zeros_like(lat)
+            hip.check(lib.hxa_dit_get_latent(p, cur.ctypes.data), "get")
+            outs.append(cur)
+        finally:
+            lib.hxa_dit_destroy(p)
+    assert np.isfinite(outs[0]).all() and np.abs(outs[0] - lat).max() > 0.1  # the steps moved the latent
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 def _split(buf, shapes):
     out, o = [], 0
     for sh in shapes:
