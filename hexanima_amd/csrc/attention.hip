@@ -42,22 +42,6 @@ constexpr float RESCALE_TH = 5.5f;
 
 HXA_DEV float16_t mfma(half8_t a, half8_t b, float16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
 
-// Wave gw of the nw waves in the workgroups past the attention tiles: an equal run of the side GEMV's rows, four in
-// flight (the same row values as modgemv_kernel)
-HXA_DEV void side_gemv(const HxaSideGemv &s, int gw, int nw, int lane) {
-  const long rpw = (s.N + nw - 1) / nw, n0 = (long)gw * rpw, n1 = n0 + rpw < s.N ? n0 + rpw : s.N;
-  if (n0 >= s.N) return;
-  auto run = [&](auto kc) {
-    constexpr int KC = decltype(kc)::value;
-    float xr[KC][8];
-    modgemv_x<KC, 8>(s.x, s.act, lane, xr);
-    modgemv_rows<KC, 8, 4>(xr, s.W, n0, n1, s.y, s.per, s.ostride, s.split, s.gap, lane);
-  };
-  if (s.K == 2048) run(std::integral_constant<int, 4>{});
-  else if (s.K == 2560) run(std::integral_constant<int, 5>{});
-  else if (s.K == 3072) run(std::integral_constant<int, 6>{});
-}
-
 // NWH waves per key half (4: 128 queries per workgroup, 8 waves). FULL: every key tile lies wholly below nvalid and
 // NKV (nvalid % 64 == 0: 1536 image tokens, 6144 + 512 joint tokens, 256 text tokens), so the loop carries no key
 // masking and no clamped per-lane tile addresses. PF: the launch touches weights for the next kernel (p.pf_bytes > 0). Both are compile-time so that the
@@ -563,7 +547,7 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
   if (p.side_wgs < 0 || p.side_wgs > 4096) return HXA_E_ARG;
   if (p.side_wgs > 0) {
     const HxaSideGemv &g = p.side;
-    if (p.batch != 1 || (g.K != 2048 && g.K != 2560 && g.K != 3072) || g.N <= 0 || g.per <= 0 || g.split < 0 ||
+    if (p.batch != 1 || !hxa_side_k_ok(g.K) || g.N <= 0 || g.per <= 0 || g.split < 0 ||
         g.gap < 0 || !g.y || ((uintptr_t)g.x | (uintptr_t)g.W) % 16 || !g.x || !g.W)
       return HXA_E_ARG;
   }

@@ -266,25 +266,26 @@ int record_step(Dit &d, const Pass &ps) {
   const bool moss_ref = d.form == 1 && b.kind != 0;
   if (hxa_block_ws_bytes(&b) > d.ws_bytes) return HXA_E_ARG;  // a low-res pass needs no more than the full one
   if (d.form == 1) DTRY(b.kind == 0 ? record_prelude_anima_ref(d) : record_prelude_moss_ref(d));
-  // Anima blocks at batch 1 whose self attention leaves CUs idle (2B: 192 workgroups on 256 CUs): block k+1's
-  // modulation, and in the last block the final layer's, runs in those CUs during block k's self attention (the same
-  // rows, the same bits); only block 0's runs ahead on its own (2B DiT step: 28 x 7.6 us of modulation launches)
-  // (HXA_DIT_SIDE=0 when a step is recorded: every modulation in its own launches, for comparison)
-  const bool side_k = D == 2048 || D == 2560 || D == 3072;  // the embedding widths the attention kernel hosts
+  // Anima blocks at batch 1: block k+1's modulation, and in the last block the final layer's, runs with block k's
+  // kernels in CUs their grids leave idle (the same rows, the same bits); only block 0's runs ahead on its own.
+  // Where the self attention leaves a quarter of the CUs idle (2B: 192 workgroups on 256 CUs) it takes all of it;
+  // else (2.9B-class: every launch 240 workgroups) the qkv projection takes rows 0 .. 3D and the MLP up the rest
+  // (HxaBlockSide). HXA_DIT_SIDE=0 when a step is recorded: every modulation in its own launches, for comparison.
   const char *side_env = getenv("HXA_DIT_SIDE");
-  const bool side_on = side_k && !(side_env && atoi(side_env) == 0);
-  const int side_wgs = d.form == 0 && b.kind == 0 && side_on ? hxa_attn_idle_wgs(b.T, b.H, b.batch) : 0;
+  const bool side_on = d.form == 0 && b.kind == 0 && b.batch == 1 && hxa_side_k_ok(D) && !(side_env && atoi(side_env) == 0);
+  const int side_wgs = side_on ? hxa_attn_idle_wgs(b.T, b.H, b.batch) : 0;
+  const bool side_gemm = side_on && side_wgs == 0;
   if (d.form == 0) {
   // timestep embedding and modulation
   DTRY(hxa_linear_f32_launch(d.sig, temb, 1, temb, d.L1, D, d.cvec, D, 2, nullptr, 0, 0, st));  // sinusoid in the GEMV
   // every block's modulation in one launch over the stacked [nb][6D][D] weights: rows 0-2 -> site 0, rows 3-5 ->
   // site 2 of that block's [9][D] (site 1 keeps the identity modulation); MOSS: one shared [6D][D]
   if (b.kind == 0)
-    DTRY(hxa_modgemv_launch(d.cvec, D, d.modw_all, (long)(side_wgs ? 1 : nb) * 6 * D, d.mods, 6 * D, 9L * D, 3 * D,
+    DTRY(hxa_modgemv_launch(d.cvec, D, d.modw_all, (long)(side_on ? 1 : nb) * 6 * D, d.mods, 6 * D, 9L * D, 3 * D,
                             3 * D, 1, st));
   else
     DTRY(hxa_modgemv_launch(d.cvec, D, d.modw_all, 6L * D, d.mods, 6 * D, 0, 6 * D, 0, 1, st));
-  if (!side_wgs) DTRY(hxa_modgemv_launch(d.cvec, D, d.Lf, 2L * D, d.fmod, 2 * D, 0, 2 * D, 0, 1, st));
+  if (!side_on) DTRY(hxa_modgemv_launch(d.cvec, D, d.Lf, 2L * D, d.fmod, 2 * D, 0, 2 * D, 0, 1, st));
   }
   // patch embed (rapid-moss: latent mix + video embedding of the token rows) (+ MOSS text tokens)
   if (moss_ref)
@@ -317,15 +318,22 @@ int record_step(Dit &d, const Pass &ps) {
   for (int k = 0; k < nb; k++) {
     const float *mod = b.kind == 0 ? d.mods + (long)k * 9 * D : d.mods;
     const hxa_h *ck = d.tkv ? d.tkv + tkv_per * k : nullptr, *cvt = d.tkv ? d.tkv + tkv_per * k + tkv_per / 2 : nullptr;
-    HxaSideGemv sg{};
-    if (side_wgs && k + 1 < nb)
-      sg = {d.cvec, d.modw_all + (long)(k + 1) * 6 * D * D, 6L * D, d.mods + (long)(k + 1) * 9 * D, 6 * D, 9L * D,
-            3 * D, 3 * D, 1, D};
-    else if (side_wgs)
-      sg = {d.cvec, d.Lf, 2L * D, d.fmod, 2 * D, 0, 2 * D, 0, 1, D};
+    // block k+1's [6D][D] modulation rows: 0 .. 3D -> site 0 of its [9][D], 3D .. 6D -> site 2 (row 6D on)
+    HxaBlockSide sd{};
+    const HxaSideGemv fin{d.cvec, d.Lf, 2L * D, d.fmod, 2 * D, 0, 2 * D, 0, 1, D};
+    const hxa_h *wn = d.modw_all + (long)(k + 1) * 6 * D * D;
+    float *yn = d.mods + (long)(k + 1) * 9 * D;
+    if (side_wgs) {
+      sd.attn = k + 1 < nb ? HxaSideGemv{d.cvec, wn, 6L * D, yn, 6 * D, 9L * D, 3 * D, 3 * D, 1, D} : fin;
+      sd.attn_wgs = side_wgs;
+    } else if (side_gemm && k + 1 < nb) {
+      sd.qkv = HxaSideGemv{d.cvec, wn, 3L * D, yn, 3 * D, 0, 3 * D, 0, 1, D};
+      sd.up = HxaSideGemv{d.cvec, wn + 3L * D * D, 3L * D, yn + 6L * D, 3 * D, 0, 3 * D, 0, 1, D};
+    } else if (side_gemm) {
+      sd.qkv = fin;
+    }
     DTRY(hxa_block_run_chained(&b, d.packs[k], d.x, b.kind == 0 ? d.ctx16 : nullptr, mod, ps.cosT, ps.sinT, d.ws, 0,
-                               nullptr, 0, st, k > 0 ? mlp_gate(k - 1) : nullptr, 1, ck, cvt,
-                               side_wgs ? &sg : nullptr, side_wgs));
+                               nullptr, 0, st, k > 0 ? mlp_gate(k - 1) : nullptr, 1, ck, cvt, side_on ? &sd : nullptr));
   }
   {
     long ld = 0;

@@ -62,6 +62,9 @@ struct GemmParams {
   hxa_h *xa_o;
   long xa_ldk, xa_ldvt, xa_ldo, xa_kb, xa_vb;
   int xa_nkv, xa_nvalid, xa_T;
+  // side_wgs > 0 (ping-pong kernel, one K slice): workgroups past the tile grid run side's GEMV rows
+  HxaSideGemv side;
+  int side_wgs;
 };
 
 // Touch this workgroup's share of [p.pf, p.pf + p.pf_bytes), one 4-byte load per 128-byte line: the lines come into
@@ -1007,6 +1010,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_pair_kernel(GemmParams p0, GemmP
 template <int BM, int BN, int FMT, bool ASYM, bool PAIRED>
 HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
   const int bid = PAIRED ? bid_arg : (int)blockIdx.x;
+  if (!PAIRED && bid >= p.tiles_m * p.tiles_n) {  // an appended workgroup: side GEMV rows, no LDS and no barrier
+    side_gemv<2>(p.side, (bid - p.tiles_m * p.tiles_n) * 8 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+              p.side_wgs * 8, threadIdx.x & 63);
+    return;
+  }
   using G = GemmGeo<BM, BN, FMT>;
   constexpr int NT = 512, NWG = 4;  // threads, waves per group
   // each group's 4 waves cover its BN / 2 columns as a 2 x 2 grid, or, for int8 / int4 weights on 256-wide tiles, as
@@ -1309,7 +1317,7 @@ hipError_t launch_pp(const GemmParams &p, int ksplit, hipStream_t st) {
     if (e != hipSuccess) return e;
     attr = true;
   }
-  dim3 grid(p.tiles_m * p.tiles_n, 1, ksplit);
+  dim3 grid(p.tiles_m * p.tiles_n + (ksplit == 1 ? p.side_wgs : 0), 1, ksplit);
   if (G::ERF_FITS && p.epi == HXA_EPI_GELU_ERF && p.erf_t2 != nullptr) {  // the T2 table past the kernel's own LDS
     GemmParams pe = p;
     pe.erf_lds = G::LDS;
@@ -1546,11 +1554,32 @@ int hxa_gemm_launch(const HxaGemm &g, hipStream_t st) {
     else e = launch_split2<HXA_W_Q4, false>(bm, bn, p, st);
     return e == hipSuccess ? HXA_OK : HXA_E_HIP;
   }
+  // a side GEMV rides in the CUs the ping-pong grid leaves idle in its last round (at least 16 of them), else it
+  // runs as its own launch after the GEMM
+  bool side_after = false;
+  if (g.side != nullptr) {
+    const HxaSideGemv &sg = *g.side;
+    if (!hxa_side_k_ok(sg.K) || sg.N <= 0 || sg.per <= 0 || !sg.x || !sg.W || !sg.y ||
+        ((uintptr_t)sg.x | (uintptr_t)sg.W) % 16)
+      return HXA_E_ARG;
+    const int ncu = num_cu(), tiles = p.tiles_m * p.tiles_n, idle = (tiles + ncu - 1) / ncu * ncu - tiles;
+    if (nw == 9 && g.ksplit == 1 && idle >= 16) {
+      p.side = sg;
+      p.side_wgs = idle;
+    } else {
+      side_after = true;
+    }
+  }
   if (w.fmt == HXA_W_F16) e = launch_fmt<HXA_W_F16, false>(bm, bn, nw, p, g.ksplit, st);
   else if (w.fmt == HXA_W_Q8) e = launch_fmt<HXA_W_Q8, false>(bm, bn, nw, p, g.ksplit, st);
   else if (w.z) e = launch_fmt<HXA_W_Q4, true>(bm, bn, nw, p, g.ksplit, st);
   else e = launch_fmt<HXA_W_Q4, false>(bm, bn, nw, p, g.ksplit, st);
-  return e == hipSuccess ? HXA_OK : HXA_E_HIP;
+  if (e != hipSuccess) return HXA_E_HIP;
+  if (side_after) {
+    const HxaSideGemv &sg = *g.side;
+    return hxa_modgemv_launch(sg.x, sg.K, sg.W, sg.N, sg.y, sg.per, sg.ostride, sg.split, sg.gap, sg.act, st);
+  }
+  return HXA_OK;
 }
 
 template <int BM, int BN, int FMT, bool ASYM, int NW>
@@ -1670,6 +1699,7 @@ bool hxa_gemm_xattn_fits(int M, int N) {
 }
 
 int hxa_gemm_xattn_launch(const HxaGemm &g, const HxaXAttn &a, hipStream_t st) {
+  if (g.side != nullptr) return HXA_E_ARG;  // (no side GEMV: only hxa_gemm_launch hosts one)
   if (g.w == nullptr || (g.w->fmt & ~HXA_W_KTILED) != HXA_W_F16 || g.epi != HXA_EPI_STORE || g.ksplit != 1 ||
       g.hn_cols < g.w->N || g.hn_cos != nullptr || g.out_t != nullptr || g.pf_bytes > 0)
     return HXA_E_ARG;
@@ -1724,6 +1754,7 @@ int hxa_gemm_plan(const HxaGemm &g, int *bm, int *bn, int *nw, int *rounds) {
 }
 
 int hxa_gemm_pair_launch(const HxaGemm &g0, const HxaGemm &g1, hipStream_t st) {
+  if (g0.side != nullptr || g1.side != nullptr) return HXA_E_ARG;  // (only hxa_gemm_launch hosts a side GEMV)
   GemmParams p0, p1;
   int bm, bn, nw, bm1, bn1, nw1;
   HxaWeight w0, w1;

@@ -221,6 +221,37 @@ HXA_DEV void modgemv_rows(const float (&xr)[KC][EPL], const hxa_h *__restrict__ 
   }
 }
 
+// A modulation GEMV (the rows hxa_modgemv_launch computes, with the same bits) that a launch runs in extra
+// workgroups appended to its grid, on the CUs its own tiles leave idle: y rows [0, N) of act(x) . W^T, K (the
+// embedding width) 2048, 2560 or 3072
+struct HxaSideGemv {
+  const float *x = nullptr;
+  const hxa_h *W = nullptr;
+  long N = 0;
+  float *y = nullptr;
+  int per = 1;
+  long ostride = 0;
+  int split = 0, gap = 0, act = 0, K = 0;
+};
+// the widths the hosting kernels are built for
+inline bool hxa_side_k_ok(int K) { return K == 2048 || K == 2560 || K == 3072; }
+// Wave gw of the nw waves in the appended workgroups: an equal run of the side GEMV's rows, R in flight (R = 2 in the
+// GEMM kernels, where more would raise the kernel's register count for its tiles)
+template <int R = 4>
+HXA_DEV void side_gemv(const HxaSideGemv &s, int gw, int nw, int lane) {
+  const long rpw = (s.N + nw - 1) / nw, n0 = (long)gw * rpw, n1 = n0 + rpw < s.N ? n0 + rpw : s.N;
+  if (n0 >= s.N) return;
+  auto run = [&](auto kc) {
+    constexpr int KC = decltype(kc)::value;
+    float xr[KC][8];
+    modgemv_x<KC, 8>(s.x, s.act, lane, xr);
+    modgemv_rows<KC, 8, R>(xr, s.W, n0, n1, s.y, s.per, s.ostride, s.split, s.gap, lane);
+  };
+  if (s.K == 2048) run(std::integral_constant<int, 4>{});
+  else if (s.K == 2560) run(std::integral_constant<int, 5>{});
+  else if (s.K == 3072) run(std::integral_constant<int, 6>{});
+}
+
 // Per-head RMSNorm * gain + split-half RoPE (kern.c:163-197) on the 8 lanes holding one head of 128: lane jj owns
 // dims [8jj, 8jj+8) (lo) and their RoPE partners [64+8jj, 64+8jj+8) (hi), so the rotation needs no exchange:
 //   y[d] = x[d] c_d - x[d+64] s_d,  y[d+64] = x[d] s_d + x[d+64] c_d  (d < 64).

@@ -28,6 +28,9 @@ struct HxaGemm {
   // < hn_gsplit, hn_g1 above) and, with hn_cos / hn_sin [hn_ttab][64], RoPE at token m % hn_ttab (kern.c:163-197)
   int hn_cols, hn_gsplit, hn_ttab;
   const float *hn_g0, *hn_g1, *hn_cos, *hn_sin;
+  // a GEMV to run with this GEMM: in workgroups appended to a one-slice ping-pong grid whose last round leaves at
+  // least 16 CUs idle, else as its own launch after the GEMM (nullptr: none)
+  const HxaSideGemv *side;
 };
 int hxa_gemm_launch(const HxaGemm &g, hipStream_t st);
 // the tile hxa_gemm_launch would run g on (bm x bn, nw waves per workgroup, 9 = the ping-pong kernel) and the
@@ -65,18 +68,6 @@ int hxa_gemm_group_launch(const void *params_dev, int G, int tiles, int fmt, hip
 // int8 / int4 weight -> fp16 k-tiled [K/32][N][32] at out (2 N K bytes): the same values the GEMM main loops use
 int hxa_dequant_launch(const HxaWeight &w, hxa_h *out, hipStream_t st);
 
-// A modulation GEMV (the rows hxa_modgemv_launch computes, with the same bits) that an attention launch runs in
-// extra workgroups appended to its grid, on the CUs its own tiles leave idle: y rows [0, N) of act(x) . W^T, K (= the
-// embedding width) 2048, 2560 or 3072
-struct HxaSideGemv {
-  const float *x = nullptr;
-  const hxa_h *W = nullptr;
-  long N = 0;
-  float *y = nullptr;
-  int per = 1;
-  long ostride = 0;
-  int split = 0, gap = 0, act = 0, K = 0;
-};
 struct HxaAttn {
   const hxa_h *q, *k, *vt;  // q [T][ldq], k [NKV][ldk] (head h at column h*128); vt [H*128][ldvt] (keys contiguous)
   long ldq, ldk, ldvt;
@@ -224,11 +215,16 @@ int hxa_noalloc_setup(void **out);
 // fp16 partials of the MLP-down that a chained block leaves pending (t1 .. t1 + (n-1) BT D in its workspace)
 int hxa_block_down_parts(const hxa_block_dims *d);
 // ck_pre / cvt_pre (Anima blocks, no stage stop): the block's text k / v, computed before the chain
-// (hxa_block_textkv_plan); the block then skips that projection. side (side_wgs > 0, batch 1): a GEMV that the
-// block's self-attention launch runs in its idle workgroups (HxaAttn::side)
+// (hxa_block_textkv_plan); the block then skips that projection. side: GEMVs (a later block's modulation) run with
+// this block's kernels:
+struct HxaBlockSide {
+  HxaSideGemv attn;  // in attn_wgs workgroups appended to the self-attention launch (HxaAttn::side; batch 1)
+  int attn_wgs = 0;
+  HxaSideGemv qkv, up;  // with the qkv / MLP-up projection (HxaGemm::side; N == 0: none)
+};
 int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
                           const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
                           void *stream, const float *pend_gate, int defer, const hxa_h *ck_pre = nullptr,
-                          const hxa_h *cvt_pre = nullptr, const HxaSideGemv *side = nullptr, int side_wgs = 0);
+                          const hxa_h *cvt_pre = nullptr, const struct HxaBlockSide *side = nullptr);
 int hxa_block_textkv_plan(const hxa_block_dims *d, const void *pack, const void *ctx, hxa_h *ck, hxa_h *cvt,
                           HxaGemm *g, HxaWeight *w);

@@ -733,9 +733,12 @@ extern "C" int hxa_block_run(const hxa_block_dims *d, const void *pack, float *x
 int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, const void *ctx, const float *mod,
                           const float *cosT, const float *sinT, void *ws, int stop, int *stage_us, int nstage,
                           void *stream, const float *pend_gate, int defer, const hxa_h *ck_pre, const hxa_h *cvt_pre,
-                          const HxaSideGemv *side, int side_wgs) {
+                          const HxaBlockSide *side) {
   g_err[0] = 0;
-  if (side_wgs < 0 || (side_wgs > 0 && (!side || d->batch != 1))) return fail(HXA_E_ARG, "block: side GEMV needs batch 1");
+  int side_wgs = side ? side->attn_wgs : 0;  // (cleared once the attention launch has taken the GEMV)
+  if (side_wgs < 0 || (side_wgs > 0 && d->batch != 1)) return fail(HXA_E_ARG, "block: side GEMV in the attention needs batch 1");
+  // the side GEMV the next hxa_gemm_launch of gemm() takes (qkv, MLP up)
+  const HxaSideGemv *side_next = nullptr;
   if ((pend_gate || defer) && stop) return fail(HXA_E_ARG, "block: chained residuals need stop == 0");
   TRY(check_dims(d));
   if (!pack || !x || !mod || !ws || (d->kind == 0 && !ctx)) return fail(HXA_E_ARG, "block: null pointer");
@@ -832,7 +835,10 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
   };
   auto gemm = [&](const hxa_h *A, long lda, int M, const HxaWeight &w, int epi, hxa_h *out, long ldo, float *xx,
                   const float *gate, hxa_h *out_t, long ldo_t, int split, int ksplit, long zstride) -> int {
-    const int r = hxa_gemm_launch(make(A, lda, M, w, epi, out, ldo, xx, gate, out_t, ldo_t, split, ksplit, zstride), st);
+    HxaGemm g = make(A, lda, M, w, epi, out, ldo, xx, gate, out_t, ldo_t, split, ksplit, zstride);
+    g.side = side_next;
+    side_next = nullptr;
+    const int r = hxa_gemm_launch(g, st);
     if (r != HXA_OK) return fail(r, "block gemm N=%d K=%d epi=%d rejected", w.N, w.K, epi);
     return HXA_OK;
   };
@@ -847,7 +853,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     p.pf_bytes = apf0 != nullptr && apf1 > apf0 ? apf1 - apf0 : 0;
     apf0 = apf1 = nullptr;  // one launch
     if (side_wgs > 0) {  // the first attention launch (self / joint) hosts the side GEMV
-      p.side = *side;
+      p.side = side->attn;
       p.side_wgs = side_wgs;
       side_wgs = 0;
     }
@@ -940,6 +946,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     const bool fuse = stop == 0;
     bool fuse_x = false;  // the text k / v ran with qkv; the cross site fuses cross q with its attention
     if (fuse) hn = HeadNorm{2 * D, gain, gain + 128, D, cosT, sinT};
+    if (side && side->qkv.N > 0) side_next = &side->qkv;
     if (pre) {
       const HxaWeight *wp;
       TRY(prep(Wqkv, wp));
@@ -963,10 +970,17 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
         gkv.w = wkv;
         const int r = hxa_gemm_pair_launch(gqkv, gkv, st);
         if (r != HXA_OK) return fail(r, "block qkv / text k v gemms rejected");
+        if (side_next) {  // the paired launch hosts no side GEMV: its own launch
+          const HxaSideGemv &sg = *side_next;
+          TRY(hxa_modgemv_launch(sg.x, sg.K, sg.W, sg.N, sg.y, sg.per, sg.ostride, sg.split, sg.gap, sg.act, st));
+        }
       } else {
-        const int r = hxa_gemm_launch(gqkv, st);
+        HxaGemm g1 = gqkv;
+        g1.side = side_next;
+        const int r = hxa_gemm_launch(g1, st);
         if (r != HXA_OK) return fail(r, "block qkv gemm rejected");
       }
+      side_next = nullptr;
     } else {
       const HxaWeight *wp;
       TRY(prep(Wqkv, wp));
@@ -1048,6 +1062,7 @@ int hxa_block_run_chained(const hxa_block_dims *d, const void *pack, float *x, c
     {
       const HxaWeight *wp;
       TRY(prep(W1, wp));
+      if (side && side->up.N > 0) side_next = &side->up;
       TRY(gemm(h, ldh, BT, *wp, d->gelu ? HXA_EPI_GELU_TANH : HXA_EPI_GELU_ERF, mid, ldmid, nullptr, nullptr, nullptr, 0, 0, 1, 0));
     }
     STAGE_DONE();

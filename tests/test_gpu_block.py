@@ -737,22 +737,24 @@ def test_dit_graph_replay_matches_eager():
         assert np.array_equal(a, b)
 
 
-@pytest.mark.parametrize("lat_hw", [(96, 64), (32, 24)])
-def test_dit_side_gemv_matches_separate_modulation(lat_hw, monkeypatch):
-    """2B-shaped DiT at batch 1: with the next block's modulation (and the final layer's) computed in workgroups
-    appended to each self-attention launch, the latents after four steps equal, bit for bit, those with every
-    modulation in its own launches (HXA_DIT_SIDE=0). 1536 tokens: 192 attention workgroups host the GEMV; 192
-    tokens: the attention runs the short-key kernel and the GEMV its own launch after it."""
+@pytest.mark.parametrize("D,H,F,fmt,lat_hw", [(2048, 16, 8192, 0, (96, 64)), (2048, 16, 8192, 0, (32, 24)),
+                                               (2560, 20, 10240, 1, (96, 64))])
+def test_dit_side_gemv_matches_separate_modulation(D, H, F, fmt, lat_hw, monkeypatch):
+    """DiT at batch 1 with the next block's modulation (and the final layer's) computed alongside each block's
+    kernels: the latents after four steps equal, bit for bit, those with every modulation in its own launches
+    (HXA_DIT_SIDE=0). 2B at 1536 tokens: 192 attention workgroups host the GEMV in appended workgroups; at 192
+    tokens the attention runs the short-key kernel and the GEMV its own launch after it; 2.9B-class int8 at 1536
+    tokens: the qkv and MLP-up ping-pong grids (240 workgroups each) host half of the rows each."""
     hip = _hip()
     lib = hip.lib()
-    say(f"dit side gemv lat {lat_hw}")
+    say(f"dit side gemv D {D} fmt {fmt} lat {lat_hw}")
     rng = np.random.default_rng(11)
     lat = rng.standard_normal((1, 16) + lat_hw).astype(np.float32)
     ctx = rng.standard_normal((1, 256, 1024)).astype(np.float32)
     outs = []
     for side in ("1", "0"):
         monkeypatch.setenv("HXA_DIT_SIDE", side)
-        bd = hip.BlockDims(0, 2048, 16, 8192, 256, 1024, 0, 1, 0, 0, 0, 1)
+        bd = hip.BlockDims(0, D, H, F, 256, 1024, 0, 1, 0, fmt, fmt, 1)
         cfg = hip.DitCfg(bd, 2, 16, lat_hw[0], lat_hw[1], 256, 0)
         p = C.c_void_p()
         hip.check(lib.hxa_dit_create(C.byref(cfg), 77, C.byref(p)), "dit_create")
