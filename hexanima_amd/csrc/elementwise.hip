@@ -805,8 +805,9 @@ int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, 
   if (N <= 0 || per <= 0 || K % 256 || K < 256 || K > 4096 || split < 0 || gap < 0) return HXA_E_ARG;
   if ((uintptr_t)x % 16 || (uintptr_t)W % 16) return HXA_E_ARG;
   // rows per wave: 8 for the modulation of all blocks (344K rows at 2048), 2 for short matrices (the final layer's
-  // 4096 rows: 128 workgroups of 8 rows per wave left half the SIMDs idle, 10.6 us for 16.8 MB)
-  const int RPW = N >= 65536 ? 8 : 2;
+  // 4096 rows: 128 workgroups of 8 rows per wave left half the SIMDs idle, 10.6 us for 16.8 MB), 4 between (one
+  // block's 6D rows: every wave first loads and activates the whole input vector, which 2 rows do not amortise)
+  const int RPW = N >= 65536 ? 8 : N >= 8192 ? 4 : 2;
   const dim3 grid((unsigned)((N + 4 * RPW - 1) / (4 * RPW)));
 #define HXA_MODGEMV(KC, EPL)                                                                                       \
   hxa_launch((modgemv_kernel<KC, EPL>), grid, dim3(256), 0, st, x, W, N, y, per, ostride, split, gap, act, RPW)
