@@ -738,13 +738,15 @@ def test_dit_graph_replay_matches_eager():
 
 
 @pytest.mark.parametrize("D,H,F,fmt,lat_hw", [(2048, 16, 8192, 0, (96, 64)), (2048, 16, 8192, 0, (32, 24)),
-                                               (2560, 20, 10240, 1, (96, 64))])
+                                               (2560, 20, 10240, 1, (96, 64)), (2048, 16, 8192, 0, (128, 64))])
 def test_dit_side_gemv_matches_separate_modulation(D, H, F, fmt, lat_hw, monkeypatch):
     """DiT at batch 1 with the next block's modulation (and the final layer's) computed alongside each block's
     kernels: the latents after four steps equal, bit for bit, those with every modulation in its own launches
     (HXA_DIT_SIDE=0). 2B at 1536 tokens: 192 attention workgroups host the GEMV in appended workgroups; at 192
     tokens the attention runs the short-key kernel and the GEMV its own launch after it; 2.9B-class int8 at 1536
-    tokens: the qkv and MLP-up ping-pong grids (240 workgroups each) host half of the rows each."""
+    tokens: the qkv and MLP-up ping-pong grids (240 workgroups each) host half of the rows each; 2B at 2048 tokens:
+    the attention fills the CUs (256 workgroups), the qkv launch is paired with the text k / v (its half of the rows
+    then runs as its own launch) and the MLP-up grid hosts its half in a second, partly filled round."""
     hip = _hip()
     lib = hip.lib()
     say(f"dit side gemv D {D} fmt {fmt} lat {lat_hw}")
