@@ -280,18 +280,20 @@ int record_step(Dit &d, const Pass &ps) {
   DTRY(hxa_linear_f32_launch(d.sig, temb, 1, temb, d.L1, D, d.cvec, D, 2, nullptr, 0, 0, st));  // sinusoid in the GEMV
   // every block's modulation in one launch over the stacked [nb][6D][D] weights: rows 0-2 -> site 0, rows 3-5 ->
   // site 2 of that block's [9][D] (site 1 keeps the identity modulation); MOSS: one shared [6D][D]
-  if (b.kind == 0)
-    DTRY(hxa_modgemv_launch(d.cvec, D, d.modw_all, (long)(side_on ? 1 : nb) * 6 * D, d.mods, 6 * D, 9L * D, 3 * D,
-                            3 * D, 1, st));
-  else
+  if (b.kind == 0 && !side_on)
+    DTRY(hxa_modgemv_launch(d.cvec, D, d.modw_all, (long)nb * 6 * D, d.mods, 6 * D, 9L * D, 3 * D, 3 * D, 1, st));
+  else if (b.kind != 0)
     DTRY(hxa_modgemv_launch(d.cvec, D, d.modw_all, 6L * D, d.mods, 6 * D, 0, 6 * D, 0, 1, st));
   if (!side_on) DTRY(hxa_modgemv_launch(d.cvec, D, d.Lf, 2L * D, d.fmod, 2 * D, 0, 2 * D, 0, 1, st));
   }
   // patch embed (rapid-moss: latent mix + video embedding of the token rows) (+ MOSS text tokens)
   if (moss_ref)
     DTRY(hxa_moss_embed_launch(ps.zrows, ps.x0rows, d.Q, d.Wv32, 1, d.bve, d.x, B, ps.Timg, ps.Ttot, D, C4, st));
-  else
-    DTRY(hxa_patch_embed_launch(ps.lat_in, B, d.cfg.lat_c, ps.lat_h, ps.lat_w, d.Wemb, D, d.x, ps.Ttot, st));
+  else {  // (with side_on, block 0's modulation runs in workgroups appended to the patch embed)
+    const HxaSideGemv m0{d.cvec, d.modw_all, 6L * D, d.mods, 6 * D, 9L * D, 3 * D, 3 * D, 1, D};
+    DTRY(hxa_patch_embed_launch(ps.lat_in, B, d.cfg.lat_c, ps.lat_h, ps.lat_w, d.Wemb, D, d.x, ps.Ttot, st,
+                                side_on ? &m0 : nullptr));
+  }
   for (int i = 0; i < B; i++) {
     if (b.kind != 0) {
       float *xt = d.x + ((long)i * ps.Ttot + ps.Timg) * D;

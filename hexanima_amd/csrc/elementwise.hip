@@ -359,9 +359,16 @@ __global__ __launch_bounds__(256) void modgemv_kernel(const float *__restrict__ 
 // outputs per thread. K = 4 Cc is staged in chunks of 64 in LDS as fp32 rows of float4 (feature float4 c = the
 // 2 x 2 patch of channel c: two float2 loads of the latent; W as one half4), read back as float4 along k; every
 // output accumulates its products in ascending k (one fma chain). Image b's rows go to x + b * xrows * D.
+// Workgroups with blockIdx.x >= tiles_n (side_cols columns appended to the grid) run the side GEMV instead.
 __global__ __launch_bounds__(256) void patch_embed_kernel(const float *__restrict__ lat, int B, int Cc, int H, int W,
                                                           const hxa_h *__restrict__ Wemb, int N, float *__restrict__ x,
-                                                          int xrows) {
+                                                          int xrows, HxaSideGemv side, int tiles_n, int side_cols) {
+  if ((int)blockIdx.x >= tiles_n) {  // an appended workgroup: side GEMV rows, before any barrier
+    side_gemv<2>(side, (((int)blockIdx.x - tiles_n) * (int)gridDim.y + (int)blockIdx.y) * 4 +
+                        __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+              side_cols * (int)gridDim.y * 4, threadIdx.x & 63);
+    return;
+  }
   __shared__ float4_t xs[64][17];  // [token][k / 4], one float4 of padding per row
   __shared__ float4_t ws[64][17];
   const int gw = W / 2, T = (H / 2) * gw, M = B * T, K = 4 * Cc;
@@ -770,11 +777,18 @@ int hxa_patchify_launch(const float *lat, int B, int Cc, int H, int W, float *to
 }
 
 int hxa_patch_embed_launch(const float *lat, int B, int Cc, int H, int W, const hxa_h *Wemb, int N, float *x, int xrows,
-                           hipStream_t st) {
+                           hipStream_t st, const HxaSideGemv *side) {
   if (B < 1 || Cc < 1 || H % 2 || W % 2 || H < 2 || W < 2 || N < 1 || xrows < (H / 2) * (W / 2)) return HXA_E_ARG;
   if ((uintptr_t)lat % 8 || (uintptr_t)Wemb % 8) return HXA_E_ARG;  // float2 latent pairs (W even), half4 weights
-  const int M = B * (H / 2) * (W / 2);
-  hxa_launch(patch_embed_kernel, dim3(nblk(N, 64), nblk(M, 64)), dim3(256), 0, st, lat, B, Cc, H, W, Wemb, N, x, xrows);
+  if (side && (!hxa_side_k_ok(side->K) || side->N <= 0 || side->per <= 0 || !side->x || !side->W || !side->y ||
+               ((uintptr_t)side->x | (uintptr_t)side->W) % 16))
+    return HXA_E_ARG;
+  const int M = B * (H / 2) * (W / 2), gx = (int)nblk(N, 64), gy = (int)nblk(M, 64);
+  // the side GEMV: enough appended columns for ~16 rows per wave (the embedding itself is latency-bound, so the
+  // GEMV's weight stream runs beside it)
+  const int cols = side ? (int)std::min<long>(std::max<long>((side->N + 16 * 4 * gy - 1) / (16 * 4 * gy), 1), 64) : 0;
+  hxa_launch(patch_embed_kernel, dim3(gx + cols, gy), dim3(256), 0, st, lat, B, Cc, H, W, Wemb, N, x, xrows,
+             side ? *side : HxaSideGemv{}, gx, cols);
   return LAUNCH_OK();
 }
 

@@ -137,8 +137,9 @@ int hxa_copy_f32_launch(const float *src, float *dst, int n, hipStream_t st);
 int hxa_patchify_launch(const float *lat, int B, int Cc, int H, int W, float *tok, hipStream_t st);
 // patch embed straight from the latent: x + (b * xrows + tk) * N <- the patchified token tk of image b times Wemb^T
 // (Wemb [N][4 Cc] fp16), all B images in one launch
+// side (optional): a GEMV run in workgroups appended to the embedding's grid (the DiT step's block-0 modulation)
 int hxa_patch_embed_launch(const float *lat, int B, int Cc, int H, int W, const hxa_h *Wemb, int N, float *x, int xrows,
-                           hipStream_t st);
+                           hipStream_t st, const HxaSideGemv *side = nullptr);
 // stacked GEMV: y[(n / per) * ostride + r + (r >= split ? gap : 0)] = sum_k act(x[k]) W[n][k], r = n % per;
 // K % 256 == 0, K <= 4096; act 1 = SiLU on the input
 int hxa_modgemv_launch(const float *x, int K, const hxa_h *W, long N, float *y, int per, long ostride, int split, int gap,
