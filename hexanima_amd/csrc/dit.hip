@@ -267,7 +267,7 @@ int record_step(Dit &d, const Pass &ps) {
   if (hxa_block_ws_bytes(&b) > d.ws_bytes) return HXA_E_ARG;  // a low-res pass needs no more than the full one
   if (d.form == 1) DTRY(b.kind == 0 ? record_prelude_anima_ref(d) : record_prelude_moss_ref(d));
   // Anima blocks at batch 1: block k+1's modulation, and in the last block the final layer's, runs with block k's
-  // kernels in CUs their grids leave idle (the same rows, the same bits); only block 0's runs ahead on its own.
+  // kernels in CUs their grids leave idle (the same rows, the same bits); block 0's runs in the patch embed launch.
   // Where the self attention leaves a quarter of the CUs idle (2B: 192 workgroups on 256 CUs) it takes all of it;
   // else (2.9B-class: every launch 240 workgroups) the qkv projection takes rows 0 .. 3D and the MLP up the rest
   // (HxaBlockSide). HXA_DIT_SIDE=0 when a step is recorded: every modulation in its own launches, for comparison.
