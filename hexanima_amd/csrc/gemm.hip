@@ -1248,8 +1248,8 @@ __global__ __launch_bounds__(512) void gemm_pp_group_kernel(const GemmParams *__
 // and MLP-down projections of the 2B (hidden 2048), 2.9B-class (2560) and MOSS-class (3072, up-gate 16384) blocks
 // at 384, 512, 1536 and 6656 rows, split-K 1 and 2 (and 4 at 1536 rows); a = 0 marks a tile that format does not
 // use. nw 4: one wave per SIMD; nw 8: two (int8 / int4 dequantisation overlaps the other wave's MFMAs); nw 9: the
-// ping-pong kernel. Over those shapes the picks come within 0.3% (fp16), 0.5% (int8) and 0.6% (int4) of the fastest
-// tile's summed time.
+// ping-pong kernel. Over those shapes the picks came within 0.3% (fp16), 0.5% (int8) and 0.6% (int4) of the fastest
+// tile's summed time; with the int8 / int4 wave strips (gemm_body, gemm_pp_body) within 1.3% and 2.7%.
 struct TileCost {
   int bm, bn, nw;
   float a[3], b[3], c[3];
