@@ -604,13 +604,13 @@ int hxa_attn_launch(const HxaAttn &p, hipStream_t st) {
 
 int hxa_attn_idle_wgs(int T, int H, int batch) {
   if (batch != 1 || T <= 0 || H <= 0) return 0;
-  static int ncu = 0;
-  if (ncu == 0) {
+  static const int ncu = [] {  // CUs of the device current at the first call (0: unknown, no side GEMV)
     int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       return 0;
-    ncu = n;
-  }
+    return n > 0 ? n : 0;
+  }();
+  if (ncu == 0) return 0;
   const int ntot = (T + 127) / 128 * H, rem = ntot % ncu, idle = rem == 0 ? 0 : ncu - rem;
   return idle >= ncu / 4 ? idle : 0;
 }
