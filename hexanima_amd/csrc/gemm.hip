@@ -1361,17 +1361,14 @@ hipError_t launch_fmt(int bm, int bn, int nw, const GemmParams &p, int ksplit, h
   return hipErrorInvalidValue;
 }
 
-int g_num_cu = 0;
-
-// CUs of the current device (read once)
+// CUs of the device current at the first call (read once, thread-safe; 256 when the query fails)
 int num_cu() {
-  if (g_num_cu == 0) {
-    int dev = 0;
+  static const int n = [] {
+    int dev = 0, c = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    hipDeviceProp_t prop;
-    g_num_cu = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 256;
-  }
-  return g_num_cu;
+    return hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0 ? c : 256;
+  }();
+  return n;
 }
 
 }  // namespace
