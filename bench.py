@@ -166,9 +166,10 @@ def extra_dits():
 def microbench():
     """Kernel-level figures on the benchmark shapes (HIP events, inputs resident in HBM):
     - W8A16 / W4A16 linears at M = 1536 (K x N = 2048 x 6144, 2048 x 2048, 2048 x 8192, 8192 x 2048; int8 uniform in
-      [-127, 127] / int4 uniform in [-8, 7], group-32 fp16 scales 0.02/127, pack layout), beside fp16 weights, as one
-      pass storing fp16; and the N <= K shapes in the form the block runs them with int8 / int4 weights (fused,
-      split-K 4 into fp16 partials);
+      [-127, 127] / int4 uniform in [-8, 7], group-32 fp16 scales 0.02/127, pack layout), beside fp16 weights, through
+      hxa_linear (one launch storing fp16, or for the long-K shapes K slices into fp32 partials and their sum; the
+      one-launch time is given beside it there); and the N <= K shapes in the form the block runs them with int8 /
+      int4 weights (fused, split-K 4 into fp16 partials);
     - attention: the 2B block's self (1536 x 1536, 16 heads) and cross (1536 x 256) attention, and the MOSS-class
       joint attention (6656 x 6656, 24 heads);
     - one 2B fp16 block (hxa_block_run, 1536 tokens), the block latency."""
@@ -183,12 +184,13 @@ def microbench():
     Wb = hip.DeviceArray((10240 * 2560 * 2,), np.uint8)
     Sb = hip.DeviceArray((320 * 10240,), np.float16)
     O = hip.DeviceArray((M, 10240), np.float16)
+    WS = hip.DeviceArray((4 * M * 2560 * 4,), np.uint8)  # hxa_linear's fp32 slices (split shapes have N <= 2560)
     hip.check(L.hxa_fill_const(Sb.ptr, 1, 320 * 10240, 0.02 / 127, s), "fill")
     # the 2B block's projections in each format, and the 2.9B-class block's (hidden 2560, MLP 10240) in fp16 / int8
     for key, shapes, fmts in (("linear_m1536", ((2048, 6144), (2048, 2048), (2048, 8192), (8192, 2048)),
                                (("fp16", hip.W_F16), ("q8", hip.W_Q8), ("q4", hip.W_Q4))),
                               ("linear_m1536_2p9b", ((2560, 7680), (2560, 2560), (2560, 10240), (10240, 2560)),
-                               (("fp16", hip.W_F16), ("q8", hip.W_Q8)))):
+                               (("fp16", hip.W_F16), ("q8", hip.W_Q8), ("q4", hip.W_Q4)))):
         for name, fmt in fmts:
             row = {}
             for K, N in shapes:
@@ -204,7 +206,17 @@ def microbench():
                 def run(K=K, N=N, fmt=fmt, sp=sp):
                     hip.check(L.hxa_gemm(A.ptr, K, M, fmt | hip.W_KTILED, Wb.ptr, sp, None, N, K, 1, hip.EPI_STORE, O.ptr,
                                          N, 0, None, 0, None, None, 0, 0, s), "gemm")
-                row[f"{K}x{N}"] = _rate(2.0 * M * N * K, _time_launches(L, hip, run, s))
+
+                def lin(K=K, N=N, fmt=fmt, sp=sp):
+                    hip.check(L.hxa_linear(A.ptr, K, M, fmt | hip.W_KTILED, Wb.ptr, sp, None, N, K, O.ptr, N, WS.ptr,
+                                           WS.nbytes, s), "linear")
+                nsplit = L.hxa_linear_split_k(M, N, K, fmt)
+                assert L.hxa_linear_ws_bytes(M, N, K, fmt) <= WS.nbytes
+                r = _rate(2.0 * M * N * K, _time_launches(L, hip, lin, s))
+                r["split_k"] = nsplit
+                if nsplit > 1:
+                    r["one_launch_us"] = round(1e3 * _time_launches(L, hip, run, s), 2)
+                row[f"{K}x{N}"] = r
             res[key][name] = row
     # the N <= K projections as the block runs them with int8 / int4 weights at 1536 tokens: fused, split-K 4 into
     # four fp16 partials (the next norm adds them); fp16 in the same form for comparison

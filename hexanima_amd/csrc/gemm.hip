@@ -38,6 +38,7 @@ struct GemmParams {
   int epi;
   hxa_h *out;
   long ldo, out_zstride;
+  float *out32;  // PARTIAL_F32: slice z's fp32 sums at out32[z * out_zstride + m * ldo + n]
   float *x;
   long ldx;
   const float *gate;
@@ -281,6 +282,28 @@ HXA_DEV void wait_stage(int) {
 
 // ---- epilogue after f16(acc) is staged in LDS as a row-major [BM][BN + 8] tile (and, for SPLIT2, the first K
 // half's tile after it): cooperative passes over 8-column chunks, coalesced 16-byte loads / stores.
+// PARTIAL_F32: the K slice's fp32 sums straight from the accumulators (no fp16 rounding, no LDS staging). For block
+// (j, i) the lane holds row mrow + i*32 and columns ncol + j*32 + 8q + 0..3 (q = 0..3): one 16-byte store each, so
+// the four q stores of a wave fill 32 rows x 128 contiguous bytes. N % 8 == 0, so a chunk is inside N or past it.
+template <int MI, int NI>
+HXA_DEV void store_partial_f32(const GemmParams &p, const float16_t (&acc)[NI][MI], int mrow, int ncol, int z) {
+  float *base = p.out32 + (long)z * p.out_zstride;
+#pragma unroll
+  for (int i = 0; i < MI; i++) {
+    const int m = mrow + i * 32;
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int j = 0; j < NI; j++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int n = ncol + j * 32 + 8 * q;
+        if (n < p.N)
+          *(float4_t *)(base + (long)m * p.ldo + n) =
+              (float4_t){acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]};
+      }
+  }
+}
+
 template <int BM, int BN, int NT, bool SPLIT2>
 HXA_DEV void gemm_epilogue(const GemmParams &p, const hxa_h *Cs, int m0, int n0, int tid, int z) {
   constexpr int CROW = BN + 8;
@@ -953,6 +976,12 @@ HXA_DEV void gemm_body(const GemmParams &p, const int bid, const int z) {
     return;
   }
   wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
+  if constexpr (!SPLIT2) {
+    if (p.epi == HXA_EPI_PARTIAL_F32) {  // no LDS staging and no prefetch (gemm_prepare rejects pf with it)
+      store_partial_f32<MI, NI>(p, acc, m0 + wm * WTM + (lane & 31), n0 + wn * WTN + 4 * (lane >> 5), z);
+      return;
+    }
+  }
   __syncthreads();
   if (p.pf_bytes > 0)
     prefetch_share(p, bid + z * p.tiles_m * p.tiles_n, p.tiles_m * p.tiles_n * (int)gridDim.z, tid, NT,
@@ -1201,6 +1230,10 @@ HXA_DEV void gemm_pp_body(const GemmParams &p, const int bid_arg) {
   }
   clk_store(p.clk, (int)(blockIdx.x + blockIdx.z * gridDim.x), tid, clk0);
   wait_vm<0>();  // the trailing (dummy) tile loads must land before the epilogue reuses the LDS ring
+  if (p.epi == HXA_EPI_PARTIAL_F32) {  // no LDS staging and no prefetch (gemm_prepare rejects pf with it)
+    store_partial_f32<MI, NI>(p, acc, m0 + wm * WTM + (lane & 31), n0 + grp * (BN / 2) + wn * WTN + 4 * (lane >> 5), z);
+    return;
+  }
   __syncthreads();
   if (p.pf_bytes > 0)
     prefetch_share(p, bid + z * p.tiles_m * p.tiles_n, p.tiles_m * p.tiles_n * (int)gridDim.z, tid, NT,
@@ -1399,6 +1432,22 @@ static void pick_tile(int M, int N, int K, int ksplit, int fmt, int epi, int hn_
   }
 }
 
+// the modelled time (us) of the tile pick_tile chooses for a plain-store GEMM with ksplit slices
+static double tile_time(int M, int N, int K, int ksplit, int fmt) {
+  int bm = 128, bn = 128, nw = 4;
+  pick_tile(M, N, K, ksplit, fmt, HXA_EPI_STORE, 0, &bm, &bn, &nw);
+  const int ncu = num_cu();
+  for (const TileCost &c : kTiles) {
+    if (c.bm != bm || c.bn != bn || c.nw != nw) continue;
+    const long tiles = (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * ksplit;
+    return (double)((tiles + ncu - 1) / ncu) * (c.a[fmt] * 1e-6 * bm * bn * (double)(K / ksplit) + c.b[fmt]) + c.c[fmt];
+  }
+  return 1e30;
+}
+// split-K linear cost terms: the sum kernel's launch and kernel boundary (us), the bytes per us of the slices' round
+// trip through L2 / MALL, and the factor by which a split form must beat the one-launch model
+constexpr double kSumLaunchUs = 4.0, kSumBytesPerUs = 8.0e6, kSplitGain = 0.95;
+
 // the tiles launch_fmt has kernels for (split2: launch_split2's)
 static bool tile_built(int bm, int bn, int nw, int fmt, bool split2) {
   if (split2) return nw == 4 && bn == 128 && (bm == 128 || bm == 64);
@@ -1446,8 +1495,10 @@ static int gemm_prepare(const HxaGemm &g, GemmParams &p, int &bm, int &bn, int &
   if (split2 && (g.ksplit != 1 || w.K % 128 != 0)) return HXA_E_ARG;  // two halves of whole k-step pairs
   if (g.epi == HXA_EPI_RESADD || split2
           ? ((g.ldx % 8) != 0 || ((uintptr_t)g.x % 32) != 0 || ((uintptr_t)g.gate % 32) != 0)
-          : ((g.ldo % 8) != 0 || ((uintptr_t)g.out % 16) != 0))
+          : ((g.ldo % (g.epi == HXA_EPI_PARTIAL_F32 ? 4 : 8)) != 0 || ((uintptr_t)g.out % 16) != 0))
     return HXA_E_ARG;
+  const bool f32 = g.epi == HXA_EPI_PARTIAL_F32;
+  if (f32 && (g.out_t != nullptr || g.hn_cols > 0 || g.pf_bytes > 0 || g.side != nullptr)) return HXA_E_ARG;
   p = GemmParams{};
   if (g.epi == HXA_EPI_STORE_T) {  // all columns transposed
     p.out_t = g.out;
@@ -1477,7 +1528,8 @@ static int gemm_prepare(const HxaGemm &g, GemmParams &p, int &bm, int &bn, int &
   p.Ktot = w.K;
   p.Kslice = w.K / g.ksplit;
   p.epi = split2 ? HXA_EPI_RESADD : g.epi;
-  p.out = g.epi == HXA_EPI_STORE_T ? nullptr : g.out;
+  p.out = g.epi == HXA_EPI_STORE_T || f32 ? nullptr : g.out;
+  p.out32 = f32 ? (float *)g.out : nullptr;
   p.ldo = g.ldo;
   p.out_zstride = g.out_zstride;
   p.x = g.x;
@@ -1842,4 +1894,56 @@ int hxa_dequant_launch(const HxaWeight &w0, hxa_h *out, hipStream_t st) {
   else if (w.z) hxa_launch((dequant_kernel<HXA_W_Q4, true>), grid, dim3(256), 0, st, p, out);
   else hxa_launch((dequant_kernel<HXA_W_Q4, false>), grid, dim3(256), 0, st, p, out);
   return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
+}
+
+// ---- split-K linear: fp32 slice sums added in order and rounded once
+// out[m][n] = f16(p[0] + p[1] + ... + p[S-1]) at element (m, n) of each slice; one thread per 8 columns of a row
+__global__ __launch_bounds__(256) void sum_partials_kernel(const float *__restrict__ p, int S, long zstride, long ldp,
+                                                           int M, int N, hxa_h *__restrict__ out, long ldo) {
+  const int c8 = N / 8;
+  const long c = (long)blockIdx.x * 256 + threadIdx.x;
+  if (c >= (long)M * c8) return;
+  const int m = (int)(c / c8), n = (int)(c % c8) * 8;
+  const float *src = p + (long)m * ldp + n;
+  float4_t a0 = *(const float4_t *)src, a1 = *(const float4_t *)(src + 4);
+  for (int z = 1; z < S; z++) {
+    const float *q = src + (long)z * zstride;
+    a0 += *(const float4_t *)q;
+    a1 += *(const float4_t *)(q + 4);
+  }
+  const half8_t o = {(hxa_h)a0[0], (hxa_h)a0[1], (hxa_h)a0[2], (hxa_h)a0[3],
+                     (hxa_h)a1[0], (hxa_h)a1[1], (hxa_h)a1[2], (hxa_h)a1[3]};
+  *(half8_t *)(out + (long)m * ldo + n) = o;
+}
+
+int hxa_sum_partials_launch(const float *p, int S, long zstride, long ldp, int M, int N, hxa_h *out, long ldo,
+                            hipStream_t st) {
+  if (!p || !out || S < 1 || M <= 0 || N <= 0 || N % 8 || ldp < N || ldo < N || ldp % 4 || ldo % 8 ||
+      (S > 1 && zstride < (long)M * ldp) || zstride % 4 || ((uintptr_t)p | (uintptr_t)out) % 16)
+    return HXA_E_ARG;
+  const long chunks = (long)M * (N / 8);
+  hxa_launch(sum_partials_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st, p, S, zstride, ldp, M, N,
+             out, ldo);
+  return hipGetLastError() == hipSuccess ? HXA_OK : HXA_E_HIP;
+}
+
+// The K slices hxa_linear runs a linear in: 1 (one launch, fp16 store) or S in {2, 4} (fp32 slices, then their sum)
+// when the tile model's time for S slices plus the slices' round trip through memory is below the one-launch time.
+int hxa_linear_split(int M, int N, int K, int fmt) {
+  fmt &= ~HXA_W_KTILED;
+  if (M <= 0 || N <= 0 || K <= 0 || N % 8 || fmt < 0 || fmt > HXA_W_Q4) return 1;
+  const double t1 = tile_time(M, N, K, 1, fmt);
+  int best = 1;
+  double tb = t1;
+  for (int S = 2; S <= 4; S *= 2) {
+    if (K % (32 * S) != 0) continue;
+    // slices written by the GEMM and read back by the sum, fp16 out, and the second launch
+    const double bytes = 2.0 * S * M * (double)N * 4.0 + 2.0 * M * (double)N;
+    const double t = tile_time(M, N, K, S, fmt) + kSumLaunchUs + bytes / kSumBytesPerUs;
+    if (t < tb * kSplitGain) {
+      tb = t;
+      best = S;
+    }
+  }
+  return best;
 }

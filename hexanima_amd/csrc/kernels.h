@@ -67,6 +67,11 @@ int hxa_gemm_group_prepare(const HxaGemm *g, int G, void *params_host, int *tile
 int hxa_gemm_group_launch(const void *params_dev, int G, int tiles, int fmt, hipStream_t st);
 // int8 / int4 weight -> fp16 k-tiled [K/32][N][32] at out (2 N K bytes): the same values the GEMM main loops use
 int hxa_dequant_launch(const HxaWeight &w, hxa_h *out, hipStream_t st);
+// out[m][n] = f16(sum of the S fp32 slices p[z*zstride + m*ldp + n], added in order z = 0 .. S-1)
+int hxa_sum_partials_launch(const float *p, int S, long zstride, long ldp, int M, int N, hxa_h *out, long ldo,
+                            hipStream_t st);
+// the K slices hxa_linear runs M x N x K in (1: one launch)
+int hxa_linear_split(int M, int N, int K, int fmt);
 
 struct HxaAttn {
   const hxa_h *q, *k, *vt;  // q [T][ldq], k [NKV][ldk] (head h at column h*128); vt [H*128][ldvt] (keys contiguous)

@@ -224,6 +224,28 @@ extern "C" int hxa_gemm(const void *A, long lda, int M, int fmt, const void *w, 
   return gemm_common(A, lda, M, fmt, w, s, z, N, K, ksplit, epi, out, ldo, out_zstride, x, ldx, gate, out_t, ldo_t,
                      split_col, 0, 0, 0, stream);
 }
+extern "C" int hxa_sum_partials(const float *p, int nslice, long zstride, long ldp, int M, int N, void *out, long ldo,
+                                void *stream) {
+  const int r = hxa_sum_partials_launch(p, nslice, zstride, ldp, M, N, (hxa_h *)out, ldo, S(stream));
+  if (r != HXA_OK) return fail(r, "sum_partials S=%d M=%d N=%d ldp=%ld ldo=%ld rejected", nslice, M, N, ldp, ldo);
+  return HXA_OK;
+}
+extern "C" int hxa_linear_split_k(int M, int N, int K, int fmt) { return hxa_linear_split(M, N, K, fmt); }
+extern "C" long hxa_linear_ws_bytes(int M, int N, int K, int fmt) {
+  const int ns = hxa_linear_split(M, N, K, fmt);
+  return ns > 1 ? (long)ns * M * N * 4 : 0;
+}
+extern "C" int hxa_linear(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N,
+                          int K, void *out, long ldo, void *ws, long ws_bytes, void *stream) {
+  const int ns = hxa_linear_split(M, N, K, fmt);
+  const long need = (long)ns * M * N * 4;
+  if (ns == 1 || ws == nullptr || ws_bytes < need)  // one launch, one fp16 rounding of the whole sum
+    return gemm_common(A, lda, M, fmt, w, s, z, N, K, 1, HXA_EPI_STORE, out, ldo, 0, nullptr, 0, nullptr, nullptr, 0,
+                       0, 0, 0, 0, stream);
+  TRY(gemm_common(A, lda, M, fmt, w, s, z, N, K, ns, HXA_EPI_PARTIAL_F32, ws, N, (long)M * N, nullptr, 0, nullptr,
+                  nullptr, 0, 0, 0, 0, 0, stream));
+  return hxa_sum_partials((const float *)ws, ns, (long)M * N, N, M, N, out, ldo, stream);
+}
 extern "C" int hxa_gemm_tile(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N,
                              int K, int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx,
                              const float *gate, int bm, int bn, int waves, void *stream) {

@@ -19,7 +19,7 @@ SZ, U64 = C.c_size_t, C.c_uint64
 # constants of the C-ABI
 W_F16, W_Q8, W_Q4 = 0, 1, 2
 W_KTILED = 16  # OR'ed into a format: matrix stored k-tiled, [K/32][N][chunk]
-EPI_STORE, EPI_GELU_TANH, EPI_GELU_ERF, EPI_RESADD, EPI_STORE_T, EPI_SITU, EPI_PARTIAL, EPI_RESADD_SPLIT2 = range(8)
+EPI_STORE, EPI_GELU_TANH, EPI_GELU_ERF, EPI_RESADD, EPI_STORE_T, EPI_SITU, EPI_PARTIAL, EPI_RESADD_SPLIT2, EPI_PARTIAL_F32 = range(9)
 KIND_WEIGHTS_ANIMA, KIND_BLOB, KIND_WEIGHTS_MOSS = 0, 1, 2
 E_NAMES = {0: "OK", -1: "RESOURCE", -2: "LOCK", -5: "WEIGHTS", -6: "NOBLOB", -7: "BLOB", -10: "META", -11: "MODE",
            -12: "ARG", -13: "HIP"}
@@ -78,6 +78,10 @@ _SIGS = {
     "hxa_gemm_headnorm": (I, [P, L, I, I, P, P, P, I, I, P, L, P, L, I, I, P, P, I, P, P, I, P]),
     "hxa_gemm_tile": (I, [P, L, I, I, P, P, P, I, I, I, I, P, L, L, P, L, P, I, I, I, P]),
     "hxa_gemm_pick": (I, [I, I, I, I, I, I, I, P, P, P, P]),
+    "hxa_linear": (I, [P, L, I, I, P, P, P, I, I, P, L, P, L, P]),
+    "hxa_linear_split_k": (I, [I, I, I, I]),
+    "hxa_linear_ws_bytes": (L, [I, I, I, I]),
+    "hxa_sum_partials": (I, [P, I, L, L, I, I, P, L, P]),
     "hxa_attention": (I, [P, L, P, L, P, L, P, L, I, I, I, I, I, L, L, L, L, P]),
     "hxa_norm_mod": (I, [P, L, I, I, P, P, P, F, P, L, P]),
     "hxa_cross_attention_fused": (I, [P, L, I, I, I, P, I, I, P, P, L, P, L, I, I, L, L, P, L, P]),

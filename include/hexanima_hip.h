@@ -133,6 +133,7 @@ int hxa_clock_record(int kind, void *rec, long nrec);
 #define HXA_EPI_SITU 5
 #define HXA_EPI_PARTIAL 6
 #define HXA_EPI_RESADD_SPLIT2 7
+#define HXA_EPI_PARTIAL_F32 8
 
 /* out = epi(A[M][K] . W[N][K]^T); replaces gemm_run_ex / gemm_run_geo (hexagon/mega/gemm2.c:96-141).
  * STORE: out[m][n] (ldo); with out_t != NULL the columns n >= split_col go to out_t[n - split_col][m] (ldo_t).
@@ -141,6 +142,8 @@ int hxa_clock_record(int kind, void *rec, long nrec);
  * device, which waits for its stream once (a launch under stream capture before then evaluates erfc instead).
  * SITU: W rows interleaved per 32 (up_j, gate_j), out[m][j*32+c] (moss gemm2.c mode 5).
  * PARTIAL: ksplit slices, out[z*out_zstride + m*ldo + n] = f16(partial z) (blk.c:172-174).
+ * PARTIAL_F32: the same slices unrounded, ((float *)out)[z*out_zstride + m*ldo + n] (out 16-byte aligned, ldo % 4 == 0);
+ * hxa_sum_partials adds them (hxa_linear's split-K form).
  * RESADD_SPLIT2 (ksplit 1, K % 128 == 0): x[m][n] += gate[n] (f16(first K/2) + f16(second K/2)), the split-K
  * down projection and its residual (blk.c:172-174, kern.c:330-339) in one launch. */
 int hxa_gemm(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
@@ -152,6 +155,21 @@ int hxa_gemm(const void *A, long lda, int M, int fmt, const void *w, const void 
 int hxa_gemm_tile(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
                   int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
                   int bm, int bn, int waves, void *stream);
+/* The plain linear out = f16(A[M][K] . W[N][K]^T) [M][ldo] (gemm_run_ex with STORE, hexagon/mega/gemm2.c:96-141;
+ * the W8A16 / W4A16 linear of the microbench): one hxa_gemm launch, or, where the tile model favours it (long K,
+ * few output tiles: hxa_linear_split_k > 1), that many K slices as fp32 partials in ws (PARTIAL_F32) followed by
+ * hxa_sum_partials. The output is rounded to fp16 once either way; only the fp32 summation order differs. ws:
+ * hxa_linear_ws_bytes(M, N, K, fmt) bytes, 16-byte aligned (NULL or fewer bytes: the one-launch form). Calls that
+ * share ws must not overlap. */
+int hxa_linear(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N, int K,
+               void *out, long ldo, void *ws, long ws_bytes, void *stream);
+int hxa_linear_split_k(int M, int N, int K, int fmt); /* 1, 2 or 4 */
+long hxa_linear_ws_bytes(int M, int N, int K, int fmt);
+/* out[m][n] = f16(p[m*ldp + n] + p[zstride + m*ldp + n] + ... ) over nslice fp32 slices, added in slice order
+ * (N % 8 == 0, ldp % 4 == 0, ldo % 8 == 0, p and out 16-byte aligned). Second step of hxa_linear's split form; the
+ * reference's linears run unsplit, so it has no counterpart there. */
+int hxa_sum_partials(const float *p, int nslice, long zstride, long ldp, int M, int N, void *out, long ldo,
+                     void *stream);
 /* The tile hxa_gemm chooses for these sizes, weight format (HXA_W_*, KTILED ignored), split and epilogue
  * (norm_cols > 0: hxa_gemm_headnorm's head-normed columns): *bm x *bn with *waves per workgroup (9: the ping-pong
  * kernel) and *rounds of workgroups over the GPU's CUs. Returns 0, or the error hxa_gemm would return for these

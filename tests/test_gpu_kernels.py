@@ -773,3 +773,106 @@ def test_gemm_forced_tile_without_kernel_is_an_argument_error(fmt, tile):
     rc = hip.lib().hxa_gemm_tile(dA.ptr, K, M, fmt, dW.ptr, dS.ptr if fmt else None, None, N, K, 1, 0, out.ptr, N, 0,
                                  None, 0, None, tile[0], tile[1], tile[2], None)
     assert rc == -12
+
+
+# ------------------------------------------------------------------------------------------------ split-K linear
+def test_sum_partials_exact():
+    """hxa_sum_partials: fp32 slices added in slice order and rounded once to fp16, bit for bit with numpy's float32
+    sums; row padding (ldp > N, ldo > N) read and left alone."""
+    hip = _hip()
+    rng = np.random.default_rng(7)
+    M, N, ldp, ldo = 37, 72, 80, 88
+    for S in (1, 2, 3, 4):
+        say(f"sum_partials S={S}")
+        p = (rng.standard_normal((S, M, ldp)) * 3.0).astype(np.float32)
+        ref = p[0, :, :N].copy()
+        for z in range(1, S):
+            ref = (ref + p[z, :, :N]).astype(np.float32)
+        dp = hip.DeviceArray.from_numpy(p)
+        out0 = np.full((M, ldo), np.float16(-7.0))
+        dout = hip.DeviceArray.from_numpy(out0)
+        hip.check(hip.lib().hxa_sum_partials(dp.ptr, S, M * ldp, ldp, M, N, dout.ptr, ldo, None), "sum_partials")
+        hip.sync()
+        got = dout.numpy()
+        assert np.array_equal(got[:, :N].view(np.uint16), ref.astype(np.float16).view(np.uint16))
+        assert np.all(got[:, N:] == np.float16(-7.0))
+
+
+@pytest.mark.parametrize("tile", [None, (128, 128, 4), (192, 128, 4), (128, 256, 8), (192, 256, 9), (128, 128, 9)])
+@pytest.mark.parametrize("fmt", [0, 1, 2])
+def test_gemm_partial_f32_slices(fmt, tile):
+    """PARTIAL_F32: each of 4 K slices' fp32 sums (no fp16 rounding) against the oracle's double-accumulated GEMM
+    over that slice, within the fp32 accumulation bound 4 sqrt(K/4) 2^-24 sum|a w| + 2^-24 |ref|; ragged M and N."""
+    hip = _hip()
+    if fmt == 2 and tile is not None and tile[2] == 9 and tile[1] == 128:
+        pytest.skip("no int4 ping-pong kernel with bn 128")
+    say(f"gemm PARTIAL_F32 fmt={fmt} tile={tile}")
+    rng = np.random.default_rng(120 + fmt)
+    M, N, K, S = 320, 392, 1024, 4
+    A = f16(rng.standard_normal((M, K)))
+    wf = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    if fmt == 0:
+        q, s, wdq = f16(wf), None, f16(wf)
+    else:
+        q, s = hxo.q8_quantize(wf) if fmt == 1 else hxo.q4_quantize(wf)
+        wdq = hxo.q8_dequant(q, s) if fmt == 1 else hxo.q4_dequant(q, s)
+    dA, dW = hip.DeviceArray.from_numpy(A), hip.DeviceArray.from_numpy(q)
+    dS = hip.DeviceArray.from_numpy(s) if s is not None else None
+    out = hip.DeviceArray((S, M, N), np.float32)
+    args = (dA.ptr, K, M, fmt, dW.ptr, dS.ptr if dS else None, None, N, K, S, hip.EPI_PARTIAL_F32, out.ptr, N, M * N,
+            None, 0, None)
+    if tile:
+        hip.check(hip.lib().hxa_gemm_tile(*args, tile[0], tile[1], tile[2], None), "gemm_tile")
+    else:
+        hip.check(hip.lib().hxa_gemm(*args, None, 0, 0, None), "gemm")
+    hip.sync()
+    got = out.numpy()
+    W16 = np.asarray(wdq).view(np.float16)
+    for z in range(S):
+        sl = slice(z * K // S, (z + 1) * K // S)
+        ref = hxo.gemm(A[:, sl], wdq[:, sl]).astype(np.float64)
+        absdot = hxo.gemm(np.abs(A[:, sl]), np.abs(W16[:, sl])).astype(np.float64)
+        tol = absdot * 4.0 * np.sqrt(K / S) * 2.0 ** -24 + np.abs(ref) * 2.0 ** -24
+        err = np.abs(got[z].astype(np.float64) - ref)
+        assert np.all(err <= tol), f"slice {z}: max excess {np.max(err - tol):.3e}"
+
+
+@pytest.mark.parametrize("N,K", [(2048, 8192), (2560, 10240), (6144, 2048), (3072, 12288)])
+@pytest.mark.parametrize("fmt", [0, 1, 2])
+def test_linear_config1_shapes(N, K, fmt):
+    """hxa_linear at M = 1536 on the long-K shapes it splits (8192 x 2048, 10240 x 2560, 12288 x 3072) and one it
+    runs as one launch (2048 x 6144): against the oracle's dequantised-fp16 GEMM with the one-launch GEMM's
+    tolerance (one ulp + accumulation bound, >= 98% bit-identical), and against hxa_gemm's one-launch output (>= 98%
+    bit-identical; the outputs that differ are fp32 summation-order differences, inside the same bound, so near-zero
+    sums from cancellation may differ by many of their own small ulps)."""
+    hip = _hip()
+    L = hip.lib()
+    M = 1536
+    nsplit = L.hxa_linear_split_k(M, N, K, fmt)
+    say(f"linear fmt={fmt} M={M} N={N} K={K} split={nsplit}")
+    if K >= 4 * N:
+        assert nsplit > 1
+    rng = np.random.default_rng(N + K + 10 * fmt)
+    A = f16(rng.standard_normal((M, K)))
+    wf = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    if fmt == 0:
+        q, s, wdq = f16(wf), None, f16(wf)
+    else:
+        q, s = hxo.q8_quantize(wf) if fmt == 1 else hxo.q4_quantize(wf)
+        wdq = hxo.q8_dequant(q, s) if fmt == 1 else hxo.q4_dequant(q, s)
+    dA, dW = hip.DeviceArray.from_numpy(A), hip.DeviceArray.from_numpy(q)
+    dS = hip.DeviceArray.from_numpy(s) if s is not None else None
+    wsb = L.hxa_linear_ws_bytes(M, N, K, fmt)
+    assert wsb == (nsplit * M * N * 4 if nsplit > 1 else 0)
+    ws = hip.DeviceArray((max(wsb, 16),), np.uint8)
+    out = hip.DeviceArray((M, N), np.float16)
+    one = hip.DeviceArray((M, N), np.float16)
+    sp = dS.ptr if dS else None
+    hip.check(L.hxa_linear(dA.ptr, K, M, fmt, dW.ptr, sp, None, N, K, out.ptr, N, ws.ptr, wsb, None), "linear")
+    hip.check(L.hxa_gemm(dA.ptr, K, M, fmt, dW.ptr, sp, None, N, K, 1, hip.EPI_STORE, one.ptr, N, 0, None, 0, None,
+                         None, 0, 0, None), "gemm")
+    hip.sync()
+    got, g1 = out.numpy(), one.numpy()
+    assert_gemm_close(got, hxo.gemm(A, wdq), A, np.asarray(wdq).view(np.float16))
+    same = np.mean(got.view(np.uint16) == g1.view(np.uint16))
+    assert same >= 0.98, same
