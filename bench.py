@@ -408,6 +408,30 @@ def family_launchers(L, hip, s):
         picks = ", ".join(_kname(hip.gemm_pick(T, N, K, f, 1, 0)) for K, N in LIN_SHAPES)
         fam["linears_" + nm] = (linears(f), len(LIN_SHAPES), lin_flops, lin_bytes[f],
                                 f"K x N {', '.join(f'{K}x{N}' for K, N in LIN_SHAPES)}: {picks}")
+    # the MLP-down shape (K 8192, N 2048, 1536 rows) through hxa_linear: K slices into fp32 partials, then their sum
+    lws = hip.DeviceArray((4 * T * D * 4,), np.uint8)
+    keep.append(lws)
+    for f, nm in ((0, "f16"), (1, "q8"), (2, "q4")):
+        K, N, wb = F, D, (2.0, 1.0, 0.5)[f]
+        Wq, Sq = hip.DeviceArray((N * K * 2,), np.uint8), hip.DeviceArray((K // 32 * N,), np.float16)
+        keep += [Wq, Sq]
+        if f == 0:
+            hip.check(L.hxa_fill_normal(Wq.ptr, 1, N * K, 83, 0.0, 0.02, s), "fill")
+        else:
+            lo, hi = (-127, 127) if f == 1 else (-8, 7)
+            hip.check(L.hxa_fill_uniform_int(Wq.ptr, 8 if f == 1 else 4, N * K // (1 if f == 1 else 2), 84, lo, hi, s),
+                      "fill")
+            hip.check(L.hxa_fill_const(Sq.ptr, 1, K // 32 * N, 0.02 / hi, s), "fill")
+        S = L.hxa_linear_split_k(T, N, K, f)
+        assert 1 < S <= 4 and L.hxa_linear_ws_bytes(T, N, K, f) <= lws.nbytes
+
+        def lin_run(hook=None, f=f, Wq=Wq, Sq=Sq, K=K, N=N):
+            hip.check(L.hxa_linear(mid.ptr, K, T, f | 16, Wq.ptr, None if f == 0 else Sq.ptr, None, N, K, up.ptr, N,
+                                   lws.ptr, lws.nbytes, s), "linear")
+        fam["linear_split_" + nm] = (
+            lin_run, 2, 2 * T * K * N, T * K * 2 + N * K * wb + (K // 32 * N * 2 if f else 0) + T * N * 2,
+            f"hxa_linear K x N {K}x{N}: {_kname(hip.gemm_pick(T, N, K, f, S, hip.EPI_PARTIAL_F32))} split-K {S} "
+            f"(fp32 partials) + sum_partials_kernel")
     return fam, keep
 
 
@@ -709,7 +733,8 @@ def main():
                     help="only launch one kernel family REPS times plus a copy calibration (for rocprofv3 --pmc)")
     ap.add_argument("--probe-family", default="gemm_splitk",
                     choices=["gemm_splitk", "gemm_pp_mlp_up", "gemm_pp_qkv_headnorm", "attention", "gemm_xattn_cross",
-                             "linears_f16", "linears_q8", "linears_q4"])
+                             "linears_f16", "linears_q8", "linears_q4", "linear_split_f16", "linear_split_q8",
+                             "linear_split_q4"])
     ap.add_argument("--abi-chain", action="store_true", help="only time the 28-block mega_block chain (hxa_run)")
     ap.add_argument("--clock-probe", action="store_true",
                     help="only measure the shader clock of the MLP-up GEMM (random / zero data, one workgroup) and of "

@@ -109,3 +109,19 @@ def test_host_programs_reject_bad_arguments_before_any_device_call(hip, tmp_path
     assert r.returncode == 1 and "not a block file" in r.stderr
     r = subprocess.run([blk, str(tmp_path)], capture_output=True, text=True)
     assert r.returncode == 1 and "missing" in r.stdout
+
+
+def test_linear_split_choice_host_only(hip):
+    """hxa_linear's K-slice choice is host logic (the tile model, no launch): the long-K N <= K shapes of the
+    benchmark split (the forms measured fastest on MI355X), the wide and square ones run as one launch, and the
+    workspace size follows the choice. Without a GPU the model takes 256 CUs, the MI355X count."""
+    L = hip.lib()
+    M = 1536
+    want = {(2048, 8192, 0): 2, (2048, 8192, 1): 4, (2048, 8192, 2): 4, (2560, 10240, 1): 4, (2560, 10240, 2): 4,
+            (6144, 2048, 1): 1, (2048, 2048, 1): 1, (8192, 2048, 1): 1, (7680, 2560, 0): 1}
+    for (N, K, fmt), S in want.items():
+        assert L.hxa_linear_split_k(M, N, K, fmt) == S, (N, K, fmt)
+        assert L.hxa_linear_ws_bytes(M, N, K, fmt) == (S * M * N * 4 if S > 1 else 0)
+        assert L.hxa_linear_split_k(M, N, K, fmt | hip.W_KTILED) == S
+    assert L.hxa_linear_split_k(M, 2044, 8192, 1) == 1  # N % 8 != 0: no split form
+    assert L.hxa_linear_split_k(0, 2048, 8192, 1) == 1
