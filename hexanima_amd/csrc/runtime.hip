@@ -237,6 +237,7 @@ extern "C" long hxa_linear_ws_bytes(int M, int N, int K, int fmt) {
 }
 extern "C" int hxa_linear(const void *A, long lda, int M, int fmt, const void *w, const void *s, const void *z, int N,
                           int K, void *out, long ldo, void *ws, long ws_bytes, void *stream) {
+  if (!out || ldo < N || ldo % 8) return fail(HXA_E_ARG, "linear: output stride %ld for %d columns", ldo, N);
   const int ns = hxa_linear_split(M, N, K, fmt);
   const long need = (long)ns * M * N * 4;
   if (ns == 1 || ws == nullptr || ws_bytes < need)  // one launch, one fp16 rounding of the whole sum
