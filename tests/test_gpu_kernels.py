@@ -876,3 +876,45 @@ def test_linear_config1_shapes(N, K, fmt):
     assert_gemm_close(got, hxo.gemm(A, wdq), A, np.asarray(wdq).view(np.float16))
     same = np.mean(got.view(np.uint16) == g1.view(np.uint16))
     assert same >= 0.98, same
+
+
+@pytest.mark.parametrize("fmt,asym", [(1, False), (2, True)])
+def test_linear_split_ragged_padded_and_fallback(fmt, asym):
+    """hxa_linear's split form with ragged rows (M = 1000), a padded output (ldo = N + 64, padding untouched) and int4
+    with mins (q4a): against the oracle's dequantised-fp16 GEMM; with a workspace one byte short it runs the one-launch
+    form, bit for bit hxa_gemm's output."""
+    hip = _hip()
+    L = hip.lib()
+    M, N, K, ldo = 1000, 2048, 8192, 2048 + 64
+    nsplit = L.hxa_linear_split_k(M, N, K, fmt)
+    say(f"linear fmt={fmt} asym={asym} M={M} N={N} K={K} ldo={ldo} split={nsplit}")
+    assert nsplit > 1
+    rng = np.random.default_rng(300 + fmt)
+    A = f16(rng.standard_normal((M, K)))
+    if asym:
+        q, s, z = _q4a_weights(rng, N, K)
+        wdq = hxo.q4_dequant(q, s, z)
+    else:
+        q, s = hxo.q8_quantize((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+        z, wdq = None, hxo.q8_dequant(q, s)
+    dA, dW, dS = hip.DeviceArray.from_numpy(A), hip.DeviceArray.from_numpy(q), hip.DeviceArray.from_numpy(s)
+    dZ = hip.DeviceArray.from_numpy(z) if z is not None else None
+    zp = dZ.ptr if dZ else None
+    wsb = L.hxa_linear_ws_bytes(M, N, K, fmt)
+    ws = hip.DeviceArray((wsb,), np.uint8)
+    pad = np.full((M, ldo), np.float16(3.0))
+    outs = []
+    for nbytes in (wsb, wsb - 1):
+        out = hip.DeviceArray.from_numpy(pad)
+        hip.check(L.hxa_linear(dA.ptr, K, M, fmt, dW.ptr, dS.ptr, zp, N, K, out.ptr, ldo, ws.ptr, nbytes, None),
+                  "linear")
+        outs.append(out)
+    one = hip.DeviceArray((M, N), np.float16)
+    hip.check(L.hxa_gemm(dA.ptr, K, M, fmt, dW.ptr, dS.ptr, zp, N, K, 1, hip.EPI_STORE, one.ptr, N, 0, None, 0, None,
+                         None, 0, 0, None), "gemm")
+    hip.sync()
+    split, short = outs[0].numpy(), outs[1].numpy()
+    assert np.all(split[:, N:] == np.float16(3.0)) and np.all(short[:, N:] == np.float16(3.0))
+    assert_gemm_close(split[:, :N], hxo.gemm(A, wdq), A, np.asarray(wdq).view(np.float16))
+    assert np.array_equal(short[:, :N].view(np.uint16), one.numpy().view(np.uint16))
+    assert L.hxa_linear(dA.ptr, K, M, fmt, dW.ptr, dS.ptr, zp, N, K, one.ptr, N - 8, ws.ptr, wsb, None) != 0
