@@ -156,7 +156,7 @@ int hxa_gemm_tile(const void *A, long lda, int M, int fmt, const void *w, const 
                   int ksplit, int epi, void *out, long ldo, long out_zstride, float *x, long ldx, const float *gate,
                   int bm, int bn, int waves, void *stream);
 /* The plain linear out = f16(A[M][K] . W[N][K]^T) [M][ldo] (gemm_run_ex with STORE, hexagon/mega/gemm2.c:96-141;
- * the W8A16 / W4A16 linear of the microbench): one hxa_gemm launch, or, where the tile model favours it (long K,
+ * with int8 / int4 weights the W8A16 / W4A16 linear): one hxa_gemm launch, or, where the tile model favours it (long K,
  * few output tiles: hxa_linear_split_k > 1), that many K slices as fp32 partials in ws (PARTIAL_F32) followed by
  * hxa_sum_partials. The output is rounded to fp16 once either way; only the fp32 summation order differs. ws:
  * hxa_linear_ws_bytes(M, N, K, fmt) bytes, 16-byte aligned (NULL or fewer bytes: the one-launch form). Calls that
